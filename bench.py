@@ -1,0 +1,210 @@
+"""Benchmark of the per-edge hot path on one MI355X (the BASELINE.json metric).
+
+Workload (``--config water``, the default): the 9,000-atom liquid water box (3,000 rigid
+H2O at 1.0 g/cm^3, cubic periodic cell of 44.8 A), cutoff 5.0 A, 8 Bessel radial
+functions x polynomial envelope, real SH l <= 3 (16 components), 128 float32 channels.
+A step is one evaluation of ``ForceStressOutput(ShEdgePotential)``: edge vectors ->
+fused featurizer -> PyTorch radial linear -> fused SH message sum into (N, 128, 16) ->
+readout -> float64 energy -> backward to forces and virial stress, all on the GPU with
+inputs resident in HBM. The neighbor list is timed separately (``neighbor_list_ms``).
+
+Prints one JSON line. ``value`` = edges / (forward + force/stress backward time).
+``roofline`` is the dominant kernel's algorithmic bytes per launch divided by its mean
+launch time, measured with HIP events on its launch stream during the timed steps.
+``cpu_baseline`` times the oracle's PyTorch-CPU restatement of the same step on the
+host cores (rank 0, N = 1 only).
+"""
+from __future__ import annotations
+
+import argparse
+import copy
+import json
+import os
+import sys
+import time
+
+import numpy as np
+import torch
+
+HBM_PEAK_GBS = 8000.0
+
+
+def algorithmic_bytes(E: int, N: int, C: int, L: int = 16, K: int = 8) -> dict:
+    """Compulsory bytes per launch of each kernel (int32 indices, packed shifts, float32
+    features): the accounting of the measurement plan, per edge and per node."""
+    return {
+        "xnn_sh_message_sum": E * (8 + 4 * C) + N * (4 * C * L + 16),
+        "xnn_sh_message_sum_backward": E * (8 + 8 * C + 12) + N * (4 * C * L + 16),
+        "xnn_edge_featurize": E * (8 + 4 * K) + N * 16,
+        "xnn_edge_featurize_backward": E * (4 * K + 8 + 12),
+        "xnn_edge_force_reduce": E * (12 + 4) + N * (12 + 16),
+        "step": E * (124 + 12 * C) + N * (76 + 8 * C * L),
+    }
+
+
+def build_workload(config: str, device):
+    import xnn_amd as xa
+    from xnn_amd import synthetic
+    if config == "water":
+        s = synthetic.water_box(seed=0)
+        rc, kw = 5.0, dict(n_rbf=8, l_max=3, channels=128, radial_type="bessel",
+                           envelope="polynomial", p=6)
+        structs, workload = [s], "water_box_9000_atoms_rc5"
+    elif config == "argon":
+        s = synthetic.argon_fcc(seed=0)
+        rc, kw = 6.0, dict(n_rbf=8, l_max=3, channels=64, radial_type="bessel", envelope="cosine")
+        structs, workload = [s], "argon_fcc_4000_atoms_rc6"
+    elif config == "ragged":
+        structs = synthetic.ragged_molecules(1024, seed=0)
+        rc, kw = 5.0, dict(n_rbf=8, l_max=3, channels=64, radial_type="bessel",
+                           envelope="polynomial", p=6)
+        workload = "ragged_1024_molecules_rc5"
+    else:
+        raise SystemExit(f"unknown config {config!r}")
+    t0 = time.perf_counter()
+    if len(structs) == 1:
+        s = structs[0]
+        pos = torch.tensor(s.pos, dtype=torch.float32, device=device)
+        cell = torch.tensor(s.cell, dtype=torch.float32, device=device)
+        pbc = torch.tensor(s.pbc)
+        ei, sh = xa.build_neighbor_list(pos, rc, cell, pbc)        # warm-up build
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        reps = 5
+        for _ in range(reps):
+            ei, sh = xa.build_neighbor_list(pos, rc, cell, pbc)
+        torch.cuda.synchronize()
+        nl_ms = (time.perf_counter() - t0) / reps * 1e3
+        g = xa.AtomicGraph(pos=pos, atomic_numbers=torch.tensor(s.numbers, device=device),
+                           edge_index=ei, cell_shifts=sh,
+                           batch=torch.zeros(len(s.pos), dtype=torch.long, device=device),
+                           n_atoms=torch.tensor([len(s.pos)], device=device), cell=cell[None],
+                           pbc=pbc[None].to(device))
+    else:
+        pos = torch.tensor(np.concatenate([m.pos for m in structs]), dtype=torch.float32,
+                           device=device)
+        n_atoms = torch.tensor([len(m.pos) for m in structs], device=device)
+        ei, sh = xa.batched_neighbor_list(pos, n_atoms, rc)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        reps = 5
+        for _ in range(reps):
+            ei, sh = xa.batched_neighbor_list(pos, n_atoms, rc)
+        torch.cuda.synchronize()
+        nl_ms = (time.perf_counter() - t0) / reps * 1e3
+        z = torch.tensor(np.concatenate([m.numbers for m in structs]), device=device)
+        batch = torch.repeat_interleave(torch.arange(len(structs), device=device), n_atoms)
+        g = xa.AtomicGraph(pos=pos, atomic_numbers=z, edge_index=ei, cell_shifts=sh, batch=batch,
+                           n_atoms=n_atoms)
+    model = xa.ShEdgePotential(cutoff=rc, species=(1, 6, 7, 8, 18), seed=0, **kw).to(device)
+    return g, model, rc, kw, workload, nl_ms, structs
+
+
+def cpu_baseline(g, model, rc, kw, max_edges: int) -> dict:
+    """The oracle's PyTorch-CPU restatement of one step (float32) on a bounded sample:
+    the edges of the first receivers in CSR order, up to ``max_edges``."""
+    import oracle.reference as R
+    E = g.num_edges
+    n_sample = min(E, max_edges)
+    ei = g.edge_index[:, :n_sample].cpu()
+    sh = g.cell_shifts[:n_sample].cpu()
+    params = dict(W=model.W.detach().cpu(), U=model.U.detach().cpu(),
+                  atom_ref=model.atom_ref.detach().cpu(), l_max=kw["l_max"], n_rbf=kw["n_rbf"],
+                  cutoff=rc, radial=kw["radial_type"], envelope=kw["envelope"])
+    pos = g.pos.detach().cpu()
+    cell = None if g.cell is None else g.cell.detach().cpu()
+    args = (pos, g.atomic_numbers.cpu(), ei, sh, cell, g.batch.cpu(), g.num_graphs, params)
+    small = (pos, g.atomic_numbers.cpu(), ei[:, :2048], sh[:2048], cell, g.batch.cpu(),
+             g.num_graphs, params)
+    R.energy_forces_stress(*small, stress=cell is not None)          # warm-up
+    t0 = time.perf_counter()
+    R.energy_forces_stress(*args, stress=cell is not None)
+    dt = time.perf_counter() - t0
+    return {"value": n_sample / dt, "unit": "edges/s", "cores": torch.get_num_threads(),
+            "kind": "port", "seconds": dt,
+            "sample": f"one float32 forward + force/stress backward over the first {n_sample} "
+                      f"of {E} edges (receivers in CSR order), oracle PyTorch-CPU restatement, "
+                      f"torch threads={torch.get_num_threads()}, os.cpu_count()={os.cpu_count()}"}
+
+
+def main() -> None:
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--config", default="water", choices=["water", "argon", "ragged"])
+    ap.add_argument("--cpu-edges", type=int, default=480_000,
+                    help="edges of the CPU-baseline sample (0 skips it)")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one GPU: this build has no multi-GPU path "
+              "(collectives and sharding are out of scope); run with --gpus 1", file=sys.stderr)
+        raise SystemExit(2)
+    if not torch.cuda.is_available():
+        raise SystemExit("bench.py needs a GPU")
+    device = torch.device("cuda:0")
+    torch.cuda.set_device(device)
+    from xnn_amd import _lib
+    import xnn_amd as xa
+    _lib.load()
+
+    g, model, rc, kw, workload, nl_ms, structs = build_workload(args.config, device)
+    E, N = g.num_edges, g.num_nodes
+    C, L = kw["channels"], (kw["l_max"] + 1) ** 2
+    wrapped = xa.ForceStressOutput(model, compute_stress=g.cell is not None)
+    g.plan()                                    # edge plan: once per neighbor list
+
+    def step():
+        data = copy.copy(g)                     # ForceStressOutput rebinds pos / cell
+        return wrapped(data)
+
+    for _ in range(args.warmup):
+        out = step()
+    kernels = ["xnn_sh_message_sum", "xnn_sh_message_sum_backward", "xnn_edge_featurize",
+               "xnn_edge_featurize_backward", "xnn_edge_force_reduce"]
+    _lib.timed.clear()
+    _lib.time_launches(*kernels)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        out = step()
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    ms = elapsed / args.steps * 1e3
+    assert torch.isfinite(out["forces"]).all()
+
+    per_kernel = {}
+    for name in kernels:
+        ev = _lib.timed.get(name, [])
+        if ev:
+            per_kernel[name] = float(np.mean([s.elapsed_time(e) for s, e in ev])) * 1e3  # us
+    _lib.timed.clear()
+    ab = algorithmic_bytes(E, N, C, L, kw["n_rbf"])
+    total_us = {k: per_kernel[k] * (2 if k == "xnn_edge_featurize" else 1) for k in per_kernel}
+    dominant = max(per_kernel, key=lambda k: total_us[k])
+    achieved = ab[dominant] / (per_kernel[dominant] * 1e-6) / 1e9
+    roofline = {"bound": "hbm", "kernel": dominant, "achieved": round(achieved, 1),
+                "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                "traffic": None, "algorithmic_bytes": ab[dominant],
+                "mean_launch_us": round(per_kernel[dominant], 2)}
+    step_gbs = ab["step"] / (ms * 1e-3) / 1e9
+    result = {
+        "metric": "edges/s fwd+force-bwd and % HBM roofline, 9k-atom water box, 1 MI355X",
+        "value": E / (ms * 1e-3), "unit": "edges/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": ms, "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "f32", "data": "synthetic (seeded generator, random-init weights)",
+        "config": {"workload": workload, "atoms": N, "edges": E, "channels": C, "sh_components": L,
+                   "n_rbf": kw["n_rbf"], "cutoff": rc, "stress": g.cell is not None,
+                   "neighbor_list_ms": round(nl_ms, 3),
+                   "step_algorithmic_bytes": ab["step"],
+                   "step_hbm_fraction": round(step_gbs / HBM_PEAK_GBS, 4),
+                   "kernel_mean_us": {k: round(v, 2) for k, v in per_kernel.items()}},
+        "roofline": roofline,
+    }
+    if args.cpu_edges > 0:
+        result["cpu_baseline"] = cpu_baseline(g, model, rc, kw, args.cpu_edges)
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

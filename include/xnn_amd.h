@@ -1,0 +1,236 @@
+/*
+ * xnn_amd.h -- C ABI of the MI355X (gfx950) per-edge hot path of xnn.
+ *
+ * Every entry point takes plain device pointers, element counts and a HIP
+ * stream; nothing here knows about torch. All memory (outputs and workspace)
+ * is allocated by the caller. Calls are asynchronous on `stream` and return a
+ * status code:
+ *   XNN_OK        0  launched
+ *   XNN_EINVAL    1  bad argument (message in xnn_last_error())
+ *   XNN_ECAPACITY 2  an output capacity was too small (the needed count is written)
+ *   XNN_EHIP      3  a HIP launch/runtime error
+ *
+ * Conventions shared by all entry points (they follow the reference):
+ *   - edges are directed, `src` = sender, `dst` = receiver; the edge vector is
+ *     r_e = pos[dst] - pos[src] + shift_e @ cell            (atomic_data.py:371-418)
+ *   - `shift` is the integer image shift packed as three signed 10-bit fields
+ *     (x | y << 10 | z << 20), range [-512, 511] per axis.
+ *   - `pos` and `cell` share the geometry dtype; per-edge/per-node features use
+ *     the compute dtype. Dtype codes: XNN_F32 = 0, XNN_F64 = 1.
+ *   - CSR "plans": ptr_dst (N+1) and optional perm_dst (E) list the edges of
+ *     every receiver; ptr_src/perm_src list the edges of every sender. A NULL
+ *     perm means the edges are already in that order.
+ *   - `batch` (N,) int32 is the structure of every atom; `cell` is (B,3,3) or
+ *     NULL for molecules (then shifts are ignored).
+ */
+#ifndef XNN_AMD_H
+#define XNN_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct ihipStream_t* xnn_stream_t; /* == hipStream_t */
+
+enum { XNN_OK = 0, XNN_EINVAL = 1, XNN_ECAPACITY = 2, XNN_EHIP = 3 };
+enum { XNN_F32 = 0, XNN_F64 = 1 };
+enum { XNN_BASIS_BESSEL = 0, XNN_BASIS_GAUSSIAN = 1 };
+enum { XNN_ENV_POLYNOMIAL = 0, XNN_ENV_COSINE = 1, XNN_ENV_NONE = 2 };
+
+/* Last error message of the calling thread ("" if none). */
+const char* xnn_last_error(void);
+/* ABI version (bumped on any signature change). */
+int xnn_abi_version(void);
+
+/* ------------------------------------------------------------------------ */
+/* Radial basis x envelope and spherical harmonics of one edge.              */
+/*   basis  : BesselRBF      common/featurizers/radial.py:187-268           */
+/*            GaussianRBF    common/featurizers/radial.py:15-75             */
+/*   envelope: PolynomialCutoff common/featurizers/cutoff.py:83-125         */
+/*             CosineCutoff     common/featurizers/cutoff.py:10-41          */
+/*   sh     : e3nn SphericalHarmonics(normalize=True, "component"), y polar  */
+/*            gnn/featurizers/spherical.py:91-93, 135-138                   */
+typedef struct {
+  int32_t n_rbf;         /* K                                               */
+  int32_t basis;         /* XNN_BASIS_*                                     */
+  int32_t envelope;      /* XNN_ENV_*                                       */
+  int32_t poly_p;        /* polynomial envelope degree p                    */
+  int32_t l_max;         /* 0..3 (sh has (l_max+1)^2 columns)               */
+  int32_t sh_sign;       /* +1: Y(r_e); -1: Y(-r_e) (NequIP, nequip.py:722) */
+  double cutoff;         /* rc                                              */
+  double rbf_prefactor;  /* Bessel normalization                            */
+  double gaussian_gamma; /* Gaussian exponent                               */
+} xnn_featurize_params;
+
+/* Per-edge geometry and features, edge-parallel, in the edges' own order.
+ * Replaces AtomicGraph.edge_vectors (atomic_data.py:371-418) followed by
+ * SphericalHarmonicEdgeEmbedding.embed (gnn/featurizers/spherical.py:115-138).
+ * The edge vectors come either from `vec_in` ((E,3), compute dtype: embed(vec)) or,
+ * when vec_in is NULL, from pos/cell/src/dst/shift.
+ * rbf_table: (K,) Bessel frequencies (BesselRBF.freqs) or Gaussian centers, compute dtype.
+ * Outputs (each nullable): vec (E,3), length (E,), sh (E,(l_max+1)^2), radial (E,K). */
+int xnn_edge_featurize(int geom_dtype, int compute_dtype, const void* vec_in,
+                       const void* pos, int64_t n_nodes,
+                       const void* cell, int64_t n_graphs, const int32_t* batch,
+                       const int32_t* src, const int32_t* dst, const int32_t* shift,
+                       int64_t n_edges, const xnn_featurize_params* prm, const void* rbf_table,
+                       void* vec, void* length, void* sh, void* radial, xnn_stream_t stream);
+
+/* Chain rule of xnn_edge_featurize to the edge vectors: g_e = dL/dr_e (E,3),
+ * compute dtype. Every upstream gradient is nullable (zero):
+ *   d_vec (E,3), d_length (E,), d_sh (E,L), d_radial (E,K), g_extra (E,3) (added as is).
+ * Replaces the autograd backward of spherical.py:135-138 and radial.py/cutoff.py. */
+int xnn_edge_featurize_backward(int geom_dtype, int compute_dtype, const void* vec_in,
+                                const void* pos, int64_t n_nodes,
+                                const void* cell, int64_t n_graphs, const int32_t* batch,
+                                const int32_t* src, const int32_t* dst, const int32_t* shift,
+                                int64_t n_edges, const xnn_featurize_params* prm,
+                                const void* rbf_table, const void* d_vec, const void* d_length,
+                                const void* d_sh, const void* d_radial, const void* g_extra,
+                                void* g_edge, xnn_stream_t stream);
+
+/* Deterministic reduction of per-edge vector gradients onto atoms and cells.
+ * Replaces _EdgeVectors.backward (atomic_data.py:452-467): grad_pos[i] =
+ * sum_{dst=i} g_e - sum_{src=i} g_e (written, geometry dtype), and, when
+ * cell_partial != NULL, cell_partial[i] = sum_{dst=i} shift_e (x) g_e as
+ * (N,3,3) float64 (sum it per structure with xnn_segment_reduce_f64 to get
+ * grad_cell = shifts^T g). No float atomics: rows are walked in CSR order. */
+int xnn_edge_force_reduce(int geom_dtype, int compute_dtype, const void* g_edge, int64_t n_edges,
+                          const int32_t* ptr_dst, const int32_t* perm_dst,
+                          const int32_t* ptr_src, const int32_t* perm_src,
+                          const int32_t* shift, int64_t n_nodes,
+                          void* grad_pos, double* cell_partial, xnn_stream_t stream);
+
+/* ------------------------------------------------------------------------ */
+/* Fused SH message aggregation: out[i,c,lm] = sum_{e: dst=i} phi[e,c] * Y_lm(sign r_e)
+ * over the receiver CSR. Y is recomputed from positions in registers (never stored).
+ * This is the uvu tensor product of scalar edge weights with Y followed by
+ * scatter_sum to receivers: gnn/fast/conv.py:137-143 + common/models/ops.py:403-448.
+ * phi (E,C) f32, out (N,C,L) f32 with L=(l_max+1)^2, C <= 256. The edge vectors
+ * come from vec_in ((E,3) f32) or, when it is NULL, from pos/cell/src/shift. */
+int xnn_sh_message_sum(int geom_dtype, const float* vec_in, const void* pos, int64_t n_nodes,
+                       const void* cell, int64_t n_graphs, const int32_t* batch,
+                       const int32_t* src, const int32_t* shift, int64_t n_edges,
+                       const int32_t* ptr_dst, const int32_t* perm_dst,
+                       int32_t l_max, int32_t sh_sign, int32_t n_channels,
+                       const float* phi, float* out, xnn_stream_t stream);
+
+/* Backward of xnn_sh_message_sum: d_phi[e,c] = sum_lm d_out[dst,c,lm] Y_lm(e)
+ * and g_vec[e] = dL/dr_e through Y (nullable). d_phi (E,C) f32, g_vec (E,3) f32. */
+int xnn_sh_message_sum_backward(int geom_dtype, const float* vec_in, const void* pos,
+                                int64_t n_nodes,
+                                const void* cell, int64_t n_graphs, const int32_t* batch,
+                                const int32_t* src, const int32_t* shift, int64_t n_edges,
+                                const int32_t* ptr_dst, const int32_t* perm_dst,
+                                int32_t l_max, int32_t sh_sign, int32_t n_channels,
+                                const float* phi, const float* d_out, float* d_phi,
+                                float* g_vec, xnn_stream_t stream);
+
+/* ------------------------------------------------------------------------ */
+/* Segmented sum over a CSR: out[i,:] = sum_{k in [ptr[i],ptr[i+1])} src[perm[k],:].
+ * Replaces scatter_sum (common/models/ops.py:403-448) without atomics; its
+ * adjoint gather_rows (ops.py:494-528) is xnn_gather_rows. dtype f32/f64. */
+int xnn_segment_sum(int dtype, const void* src, int64_t n_rows, int64_t n_features,
+                    const int32_t* ptr, const int32_t* perm, int64_t n_segments,
+                    void* out, xnn_stream_t stream);
+
+/* out[e,:] = src[index[e],:] (index int32). Replaces gather_rows (ops.py:494-528). */
+int xnn_gather_rows(int dtype, const void* src, int64_t n_src_rows, int64_t n_features,
+                    const int32_t* index, int64_t n_rows, void* out, xnn_stream_t stream);
+
+/* Per-structure totals accumulated in float64 over contiguous node ranges
+ * seg_ptr (B+1): out[b,f] = sum_{i in seg b} src[i,f]. Replaces structure_sum
+ * (ops.py:531-557, fp64 accumulation) and structure_sums (ops.py:560-569). */
+int xnn_segment_reduce_f64(int dtype, const void* src, int64_t n_rows, int64_t n_features,
+                           const int64_t* seg_ptr, int64_t n_segments, double* out,
+                           xnn_stream_t stream);
+
+/* ------------------------------------------------------------------------ */
+/* Cell-list radius graph. Replaces build_neighbor_list (neighborlist.py:411-506):
+ * same edge set (dist < cutoff in the geometry dtype), same [src,dst] and negated,
+ * unwrapped shift convention; edges come grouped by receiver (CSR order).
+ *
+ * Call sequence (all device-side after the plan):
+ *   1. xnn_radius_graph_plan(...)        host: grid shape + workspace bytes
+ *   2. xnn_radius_graph_count(...)       device: per-atom neighbor counts -> row_ptr (N+1)
+ *   3. caller reads row_ptr[N] (= E) and allocates outputs
+ *   4. xnn_radius_graph_fill(...)        device: src, dst, shifts (+ int64 reference format)
+ * The grid is in fractional coordinates: bins of normal width >= cutoff along
+ * every axis (the image range of neighborlist.py:74-104 follows from it). */
+typedef struct {
+  int32_t nbins[3];       /* bins per axis                                      */
+  int32_t reach[3];       /* bins searched on each side                          */
+  int32_t periodic[3];    /* pbc flags                                           */
+  int32_t has_cell;       /* 0: molecule (Cartesian grid)                        */
+  double lo[3];           /* lower bound of the grid (fractional / Cartesian)     */
+  double width[3];        /* bin width in the same coordinates                    */
+  double inv_cell[9];     /* row-major inverse of the cell (when has_cell)        */
+  int64_t n_bins;         /* product of nbins                                     */
+  size_t workspace_bytes; /* bytes of device workspace the count/fill steps need  */
+} xnn_grid_plan;
+
+/* Host-only: derive the grid for one structure. `cell` (3x3, row-major, host,
+ * float64) may be NULL; pbc (3) host ints; lo/hi are the host-side min/max of
+ * the atoms' fractional (or Cartesian for molecules) coordinates along
+ * non-periodic axes (ignored on periodic axes). */
+int xnn_radius_graph_plan(int64_t n_nodes, const double* cell, const int32_t* pbc,
+                          double cutoff, const double* lo, const double* hi,
+                          xnn_grid_plan* plan);
+
+int xnn_radius_graph_count(int geom_dtype, const void* pos, int64_t n_nodes, const void* cell,
+                           double cutoff, int32_t self_interaction, const xnn_grid_plan* plan,
+                           void* workspace, int32_t* row_ptr, xnn_stream_t stream);
+
+/* Writes E = row_ptr[n_nodes] edges. src/dst int32 (E), shift packed int32 (E);
+ * edge_index64 (2,E) and shifts64 (E,3) int64 in the reference format are nullable.
+ * *overflow (device int32, nullable) is set non-zero when a packed shift field left
+ * [-512, 511] (the int64 shifts stay exact). */
+int xnn_radius_graph_fill(int geom_dtype, const void* pos, int64_t n_nodes, const void* cell,
+                          double cutoff, int32_t self_interaction, const xnn_grid_plan* plan,
+                          void* workspace, const int32_t* row_ptr, int64_t n_edges,
+                          int32_t* src, int32_t* dst, int32_t* shift,
+                          int64_t* edge_index64, int64_t* shifts64, int32_t* overflow,
+                          xnn_stream_t stream);
+
+/* Radius graph of a batch of small molecules (no cell): structure b owns atoms
+ * [node_ptr[b], node_ptr[b+1]); every atom tests every atom of its structure.
+ * Same two-step protocol as above (count -> row_ptr, then fill). Structures of
+ * more than 1024 atoms are rejected (use the cell list per structure). */
+/* molecules_count writes the per-atom counts to row_ptr[1..N]; follow it with
+ * xnn_scan_counts to turn them into row pointers. */
+int xnn_radius_graph_molecules_count(int geom_dtype, const void* pos, int64_t n_nodes,
+                                     const int64_t* node_ptr, const int32_t* batch,
+                                     int64_t n_graphs, double cutoff, int32_t self_interaction,
+                                     int32_t* row_ptr, xnn_stream_t stream);
+int xnn_radius_graph_molecules_fill(int geom_dtype, const void* pos, int64_t n_nodes,
+                                    const int64_t* node_ptr, const int32_t* batch,
+                                    int64_t n_graphs, double cutoff, int32_t self_interaction,
+                                    const int32_t* row_ptr, int64_t n_edges, int32_t* src,
+                                    int32_t* dst, int32_t* shift, int64_t* edge_index64,
+                                    int64_t* shifts64, xnn_stream_t stream);
+
+/* Exclusive scan helper for the two-step protocols: row_ptr[0..n] from counts
+ * already stored in row_ptr[1..n] (in place). workspace: xnn_scan_workspace_bytes(n). */
+size_t xnn_scan_workspace_bytes(int64_t n);
+int xnn_scan_counts(int32_t* row_ptr, int64_t n, void* workspace, xnn_stream_t stream);
+
+/* ------------------------------------------------------------------------ */
+/* Edge plan from an arbitrary edge list: int64 edge_index (2,E) and cell_shifts
+ * (E,3) -> int32 src, dst, packed shift; receiver CSR (ptr_dst, perm_dst) and
+ * sender CSR (ptr_src, perm_src), both stable (edge order within a row).
+ * Mirrors the orderings of common/models/csr.py:20-51. Shift fields outside
+ * [-512, 511] fail with XNN_ECAPACITY (flag written to *overflow on device). */
+size_t xnn_edge_plan_workspace_bytes(int64_t n_edges, int64_t n_nodes);
+int xnn_edge_plan(const int64_t* edge_index, const int64_t* cell_shifts, int64_t n_edges,
+                  int64_t n_nodes, int32_t* src, int32_t* dst, int32_t* shift,
+                  int32_t* ptr_dst, int32_t* perm_dst, int32_t* ptr_src, int32_t* perm_src,
+                  int32_t* overflow, void* workspace, size_t workspace_bytes,
+                  xnn_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* XNN_AMD_H */

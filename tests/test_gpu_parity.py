@@ -1,0 +1,334 @@
+"""GPU parity: every HIP entry point against the oracle on the same seeded inputs.
+
+Bars: edge sets bit-exact after canonical sort (margin-checked inputs), integer/CSR
+outputs exact, float32 energies rtol 1e-6, forces and stress atol 1e-5 (eV/A), float64
+paths 1e-10; reductions bitwise reproducible run to run; the native library must be the
+code that ran (call counters).
+"""
+import sys
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import margin_checked_seed
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda"
+
+
+def _note(msg):
+    print(f"[gpu-case] {msg}", flush=True)
+    sys.stdout.flush()
+
+
+@pytest.fixture(autouse=True)
+def _need_gpu():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    from xnn_amd import _lib
+    _lib.load()  # the native library must load on a GPU box
+
+
+def _canon_t(ei, sh):
+    from oracle.nl import canonical
+    return canonical(ei.cpu().numpy(), sh.cpu().numpy())
+
+
+# --------------------------------------------------------------------------- radius graph
+@pytest.mark.parametrize("name", ["argon", "water_small", "triclinic", "slab", "unwrapped"])
+@pytest.mark.parametrize("dtype", [np.float32, np.float64])
+def test_radius_graph_bit_exact(name, dtype):
+    import xnn_amd as xa
+    from xnn_amd import synthetic
+    from oracle.nl import canonical
+    tdt = torch.float32 if dtype == np.float32 else torch.float64
+    if name == "argon":
+        make, rc = (lambda seed: synthetic.argon_fcc(n_cells=4, seed=seed)), 6.0
+    elif name == "water_small":
+        make, rc = (lambda seed: synthetic.water_box(n_molecules=343, box=21.7, grid=7,
+                                                     seed=seed)), 5.0
+    elif name == "triclinic":
+        def make(seed):
+            rng = np.random.default_rng(seed)
+            cell = np.array([[13.1, 0.0, 0.0], [2.7, 12.8, 0.0], [1.3, -2.4, 14.4]])
+            pos = rng.uniform(0, 1, (300, 3)) @ cell
+            return synthetic.Structure(pos, np.ones(300, np.int64), cell, np.array([1, 1, 1], bool))
+        rc = 4.5
+    elif name == "slab":
+        def make(seed):
+            rng = np.random.default_rng(seed)
+            cell = np.eye(3) * 12.0
+            pos = rng.uniform(0, 12, (250, 3))
+            return synthetic.Structure(pos, np.ones(250, np.int64), cell, np.array([1, 0, 1], bool))
+        rc = 4.0
+    else:
+        def make(seed):
+            s = synthetic.argon_fcc(n_cells=3, seed=seed)
+            rng = np.random.default_rng(seed + 100)
+            s.pos = s.pos + rng.integers(-3, 4, s.pos.shape) @ s.cell
+            return s
+        rc = 6.0
+    seed, s, ei, sh = margin_checked_seed(make, rc, dtype=dtype)
+    _note(f"radius_graph {name} {dtype.__name__} seed={seed} N={len(s.pos)}")
+    pos = torch.tensor(s.pos, dtype=tdt, device=DEV)
+    e2, s2 = xa.build_neighbor_list(pos, rc, torch.tensor(s.cell, dtype=tdt, device=DEV),
+                                    torch.tensor(s.pbc))
+    assert e2.shape[1] == ei.shape[1]
+    assert np.array_equal(_canon_t(e2, s2), canonical(ei, sh))
+    # grouped by receiver: the CSR order of the kernels
+    assert bool((e2[1][1:] >= e2[1][:-1]).all())
+
+
+def test_radius_graph_full_water_box_bit_exact():
+    import xnn_amd as xa
+    from xnn_amd import synthetic
+    from oracle.nl import canonical
+    seed, s, ei, sh = margin_checked_seed(lambda sd: synthetic.water_box(seed=sd), 5.0)
+    _note(f"radius_graph water 9000 seed={seed}")
+    pos = torch.tensor(s.pos, dtype=torch.float32, device=DEV)
+    e2, s2 = xa.build_neighbor_list(pos, 5.0, torch.tensor(s.cell, dtype=torch.float32,
+                                                            device=DEV), torch.tensor(s.pbc))
+    assert e2.shape[1] == ei.shape[1] > 400_000
+    assert np.array_equal(_canon_t(e2, s2), canonical(ei, sh))
+
+
+def test_radius_graph_edge_cases():
+    import xnn_amd as xa
+    from oracle.nl import canonical, neighbor_list
+    _note("radius_graph edge cases")
+    # empty and single atom
+    e, s = xa.build_neighbor_list(torch.zeros((0, 3), device=DEV), 5.0)
+    assert e.shape == (2, 0) and s.shape == (0, 3)
+    e, s = xa.build_neighbor_list(torch.zeros((1, 3), device=DEV), 5.0)
+    assert e.shape == (2, 0)
+    # molecule, self-interaction, small cell (several images per axis)
+    rng = np.random.default_rng(0)
+    mol = rng.uniform(0, 6, (40, 3))
+    e, s = xa.build_neighbor_list(torch.tensor(mol, device=DEV, dtype=torch.float64), 3.0)
+    ei, sh, _ = neighbor_list(mol, 3.0, None, None, dtype=np.float64)
+    assert np.array_equal(_canon_t(e, s), canonical(ei, sh))
+    cell = np.eye(3) * 3.1
+    pos = rng.uniform(0, 3.1, (5, 3))
+    for si in (False, True):
+        e, s = xa.build_neighbor_list(torch.tensor(pos, device=DEV, dtype=torch.float64), 4.0,
+                                      torch.tensor(cell, device=DEV), torch.ones(3, dtype=torch.bool),
+                                      self_interaction=si)
+        ei, sh, _ = neighbor_list(pos, 4.0, cell, [True] * 3, self_interaction=si,
+                                  dtype=np.float64)
+        assert np.array_equal(_canon_t(e, s), canonical(ei, sh))
+    # non-finite positions raise before any kernel runs
+    bad = torch.tensor([[0.0, 0.0, float("nan")], [1.0, 0, 0]], device=DEV)
+    with pytest.raises(ValueError, match="finite"):
+        xa.build_neighbor_list(bad, 3.0)
+
+
+def test_batched_molecules_match_per_structure():
+    import xnn_amd as xa
+    from xnn_amd import synthetic
+    from oracle.nl import canonical, neighbor_list
+    mols = synthetic.ragged_molecules(64, seed=3)
+    _note("batched molecule radius graph, 64 ragged molecules")
+    pos = torch.tensor(np.concatenate([m.pos for m in mols]), dtype=torch.float32, device=DEV)
+    n_atoms = torch.tensor([len(m.pos) for m in mols])
+    e, s = xa.batched_neighbor_list(pos, n_atoms, 5.0)
+    parts, off = [], 0
+    for m in mols:
+        ei, sh, _ = neighbor_list(m.pos, 5.0, None, None, dtype=np.float32)
+        parts.append((ei + off, sh))
+        off += len(m.pos)
+    ei = np.concatenate([p[0] for p in parts], 1)
+    sh = np.concatenate([p[1] for p in parts], 0)
+    assert np.array_equal(_canon_t(e, s), canonical(ei, sh))
+
+
+# --------------------------------------------------------------------------- edge features
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float64])
+def test_edge_vectors_and_their_backward(dtype):
+    import oracle.reference as R
+    import xnn_amd as xa
+    from xnn_amd import synthetic
+    from xnn_amd.ops import edge_vectors
+    _note(f"edge_vectors {dtype}")
+    s = synthetic.water_box(n_molecules=343, box=21.7, grid=7, seed=1)
+    pos = torch.tensor(s.pos, dtype=dtype, device=DEV, requires_grad=True)
+    cell = torch.tensor(s.cell, dtype=dtype, device=DEV, requires_grad=True)
+    ei, sh = xa.build_neighbor_list(pos.detach(), 5.0, cell.detach(), torch.tensor(s.pbc))
+    g = xa.AtomicGraph(pos=pos, atomic_numbers=torch.tensor(s.numbers, device=DEV), edge_index=ei,
+                       cell_shifts=sh, batch=torch.zeros(len(s.pos), dtype=torch.long, device=DEV),
+                       n_atoms=torch.tensor([len(s.pos)], device=DEV), cell=cell[None],
+                       pbc=torch.tensor(s.pbc)[None])
+    vec = g.edge_vectors()
+    w = torch.randn(vec.shape, dtype=dtype, device=DEV, generator=torch.Generator(DEV).manual_seed(0))
+    gp, gc = torch.autograd.grad((vec * w).sum(), (pos, cell))
+    pos_c = pos.detach().cpu().double().requires_grad_(True)
+    cell_c = cell.detach().cpu().double().requires_grad_(True)
+    ref = R.edge_vectors(pos_c, ei.cpu(), sh.cpu(), cell_c[None])
+    rp, rcl = torch.autograd.grad((ref * w.cpu().double()).sum(), (pos_c, cell_c))
+    tol = 1e-5 if dtype == torch.float32 else 1e-12
+    np.testing.assert_allclose(vec.detach().cpu().double(), ref.detach(), atol=tol)
+    np.testing.assert_allclose(gp.cpu().double(), rp, atol=10 * tol)
+    np.testing.assert_allclose(gc.cpu().double(), rcl, rtol=tol, atol=100 * tol)
+    # bitwise reproducible
+    gp2, gc2 = torch.autograd.grad((g.edge_vectors() * w).sum(), (pos, cell))
+    assert torch.equal(gp, gp2) and torch.equal(gc, gc2)
+
+
+@pytest.mark.parametrize("radial,envelope,l_max,sign", [("bessel", "polynomial", 3, 1),
+                                                        ("bessel", "cosine", 2, -1),
+                                                        ("gaussian", "polynomial", 1, 1),
+                                                        ("gaussian", "cosine", 0, 1)])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float64])
+def test_edge_embed_and_backward(radial, envelope, l_max, sign, dtype):
+    import oracle.reference as R
+    from xnn_amd.featurizers import SphericalHarmonicEdgeEmbedding
+    _note(f"edge_embed {radial} {envelope} l={l_max} sign={sign} {dtype}")
+    gen = torch.Generator().manual_seed(4)
+    vec = (torch.randn(5000, 3, generator=gen, dtype=torch.float64) * 2.5)
+    vec[:3] = torch.tensor([[0.0, 0.0, 5.5], [1e-9, 0, 0], [0.0, 4.999, 0.0]], dtype=torch.float64)
+    old = torch.get_default_dtype()
+    torch.set_default_dtype(dtype)   # buffers (frequencies, centers) built in the run's dtype
+    try:
+        emb = SphericalHarmonicEdgeEmbedding(l_max=l_max, n_rbf=8, cutoff=5.0,
+                                             radial_type=radial, envelope=envelope).to(DEV)
+    finally:
+        torch.set_default_dtype(old)
+    emb.fast_active = True
+    v = vec.to(DEV, dtype).requires_grad_(True)
+    length, sh, rad = emb.embed(v, sh_sign=sign)
+    wl = torch.randn(length.shape, generator=gen, dtype=torch.float64)
+    ws = torch.randn(sh.shape, generator=gen, dtype=torch.float64)
+    wr = torch.randn(rad.shape, generator=gen, dtype=torch.float64)
+    loss = (length * wl.to(DEV, dtype)).sum() + (sh * ws.to(DEV, dtype)).sum() + \
+        (rad * wr.to(DEV, dtype)).sum()
+    (gv,) = torch.autograd.grad(loss, v)
+    vc = vec.clone().requires_grad_(True)
+    lr = torch.linalg.norm(vc, dim=-1)
+    shr = R.e3nn_sh(l_max, vc if sign == 1 else -vc)
+    rr = R.radial_features(lr, 8, 5.0, radial, envelope)
+    lossr = (lr * wl).sum() + (shr * ws).sum() + (rr * wr).sum()
+    (gr,) = torch.autograd.grad(lossr, vc)
+    tol = 2e-5 if dtype == torch.float32 else 1e-11
+    np.testing.assert_allclose(length.detach().cpu().double(), lr.detach(), rtol=tol, atol=tol)
+    np.testing.assert_allclose(sh.detach().cpu().double()[3:], shr.detach()[3:], atol=tol * 5)
+    np.testing.assert_allclose(rad.detach().cpu().double(), rr.detach(), atol=tol * 5)
+    np.testing.assert_allclose(gv.cpu().double()[3:], gr[3:], rtol=tol * 10, atol=tol * 20)
+
+
+# --------------------------------------------------------------------------- aggregation
+@pytest.mark.parametrize("C,l_max", [(128, 3), (64, 3), (32, 2), (96, 1), (200, 0)])
+def test_sh_message_sum_forward_backward(C, l_max):
+    import oracle.reference as R
+    import xnn_amd as xa
+    from xnn_amd import synthetic
+    from xnn_amd.ops import sh_message_sum
+    _note(f"sh_message_sum C={C} l_max={l_max}")
+    s = synthetic.water_box(n_molecules=216, box=18.6, grid=6, seed=2)
+    g = xa.structure_to_graph(s.as_dict(), 5.0, device=DEV)
+    g.pos = g.pos.float()
+    vec = g.edge_vectors().detach().requires_grad_(True)
+    gen = torch.Generator().manual_seed(C)
+    phi = torch.randn(vec.shape[0], C, generator=gen).to(DEV).requires_grad_(True)
+    A = sh_message_sum(vec, phi, g.plan(), l_max, 1)
+    dA = torch.randn(A.shape, generator=gen).to(DEV)
+    gvec, gphi = torch.autograd.grad((A * dA).sum(), (vec, phi))
+    vc = vec.detach().cpu().double().requires_grad_(True)
+    pc = phi.detach().cpu().double().requires_grad_(True)
+    Y = R.e3nn_sh(l_max, vc)
+    msg = (pc[:, :, None] * Y[:, None, :]).reshape(vc.shape[0], -1)
+    Ar = R.scatter_sum(msg, g.edge_index[1].cpu(), g.num_nodes).reshape(A.shape)
+    gv_r, gp_r = torch.autograd.grad((Ar * dA.cpu().double()).sum(), (vc, pc))
+    scale = float(Ar.abs().max())
+    np.testing.assert_allclose(A.detach().cpu().double(), Ar.detach(), atol=2e-6 * scale)
+    np.testing.assert_allclose(gphi.cpu().double(), gp_r, atol=2e-5 * float(gp_r.abs().max()))
+    np.testing.assert_allclose(gvec.cpu().double(), gv_r, atol=2e-5 * float(gv_r.abs().max()))
+    A2 = sh_message_sum(vec, phi, g.plan(), l_max, 1)
+    assert torch.equal(A, A2)
+
+
+def test_segment_gather_and_structure_sums():
+    import oracle.reference as R
+    import xnn_amd as xa
+    _note("segment_sum / gather_rows / structure_sum")
+    gen = torch.Generator().manual_seed(0)
+    for F in (1, 3, 17, 64, 130):
+        src = torch.randn(5000, F, generator=gen, dtype=torch.float64)
+        index = torch.randint(0, 300, (5000,), generator=gen)
+        got = xa.scatter_sum(src.to(DEV), index.to(DEV), 300)
+        np.testing.assert_allclose(got.cpu(), R.scatter_sum(src, index, 300), atol=1e-12)
+        # float32 summed in edge order equals the CPU index_add bit for bit
+        s32 = src.float()
+        got32 = xa.scatter_sum(s32.to(DEV), index.to(DEV), 300)
+        order = torch.argsort(index, stable=True)
+        want32 = torch.zeros(300, F).index_add_(0, index[order], s32[order])
+        assert torch.equal(got32.cpu(), want32)
+        gr = xa.gather_rows(src.to(DEV), index.to(DEV))
+        assert torch.equal(gr.cpu(), src[index])
+    vals = torch.randn(36800, generator=gen, dtype=torch.float64) * 10
+    n_atoms = torch.randint(10, 61, (1024,), generator=gen)
+    n_atoms = n_atoms[: int((n_atoms.cumsum(0) <= 36800).sum())]
+    batch = torch.repeat_interleave(torch.arange(len(n_atoms)), n_atoms)
+    vals = vals[: len(batch)]
+    got = xa.structure_sum(vals.to(DEV), batch.to(DEV), len(n_atoms))
+    np.testing.assert_allclose(got.cpu(), R.structure_sum(vals, batch, len(n_atoms)), rtol=1e-13)
+    got1 = xa.structure_sum(vals.float().to(DEV), torch.zeros(len(vals), dtype=torch.long,
+                                                              device=DEV), 1)
+    assert got1.dtype == torch.float64
+    assert abs(float(got1[0]) - float(vals.float().double().sum())) < 1e-9
+
+
+# --------------------------------------------------------------------------- full model
+@pytest.mark.parametrize("config", ["water", "argon", "ragged", "nequip_molecules"])
+def test_model_energy_forces_stress(config):
+    import oracle.reference as R
+    import xnn_amd as xa
+    from xnn_amd import _lib, synthetic
+    if config == "water":
+        s, rc = synthetic.water_box(seed=0), 5.0
+        kw = dict(n_rbf=8, l_max=3, channels=128, radial_type="bessel", envelope="polynomial")
+        structs = [s]
+    elif config == "argon":
+        s, rc = synthetic.argon_fcc(), 6.0
+        kw = dict(n_rbf=8, l_max=3, channels=64, radial_type="bessel", envelope="cosine")
+        structs = [s]
+    elif config == "ragged":
+        structs, rc = synthetic.ragged_molecules(256, seed=1), 5.0
+        kw = dict(n_rbf=8, l_max=3, channels=64, radial_type="bessel", envelope="polynomial")
+    else:
+        structs, rc = synthetic.random_molecules(32, seed=2), 5.0
+        kw = dict(n_rbf=8, l_max=2, channels=32, radial_type="bessel", envelope="polynomial",
+                  sh_sign=-1)
+    _note(f"model {config}")
+    graphs = [xa.structure_to_graph(st.as_dict(), rc, device=DEV) for st in structs]
+    g = graphs[0] if len(graphs) == 1 else xa.collate(graphs)
+    g.pos = g.pos.float()
+    if g.cell is not None:
+        g.cell = g.cell.float()
+    model = xa.ShEdgePotential(cutoff=rc, species=(1, 6, 7, 8, 18), **kw).to(DEV)
+    before = dict(_lib.calls)
+    out = xa.ForceStressOutput(model, compute_stress=g.cell is not None)(g)
+    for name in ("xnn_sh_message_sum", "xnn_sh_message_sum_backward", "xnn_edge_force_reduce",
+                 "xnn_edge_featurize", "xnn_edge_featurize_backward"):
+        assert _lib.calls.get(name, 0) > before.get(name, 0), f"{name} did not run"
+    params = dict(W=model.W.detach().cpu().double(), U=model.U.detach().cpu().double(),
+                  atom_ref=model.atom_ref.detach().cpu().double(), l_max=kw["l_max"],
+                  n_rbf=kw["n_rbf"], cutoff=rc, radial=kw["radial_type"],
+                  envelope=kw["envelope"], sh_sign=kw.get("sh_sign", 1))
+    cpu_pos = torch.tensor(np.concatenate([st.pos for st in structs]), dtype=torch.float32).double()
+    cell = None if g.cell is None else g.cell.detach().cpu().double()
+    ref = R.energy_forces_stress(cpu_pos, g.atomic_numbers.cpu(), g.edge_index.cpu(),
+                                 g.cell_shifts.cpu(), cell, g.batch.cpu(), g.num_graphs, params,
+                                 stress=cell is not None)
+    np.testing.assert_allclose(out["energy"].detach().cpu(), ref["energy"], rtol=1e-6, atol=1e-6)
+    np.testing.assert_allclose(out["forces"].detach().cpu().double(), ref["forces"], atol=1e-5)
+    if cell is not None:
+        np.testing.assert_allclose(out["stress"].detach().cpu().double(), ref["stress"], atol=1e-5)
+    # bitwise reproducible forces
+    g2 = graphs[0] if len(graphs) == 1 else xa.collate(graphs)
+    g2.pos = g2.pos.float()
+    if g2.cell is not None:
+        g2.cell = g2.cell.float()
+    out2 = xa.ForceStressOutput(model, compute_stress=g2.cell is not None)(g2)
+    assert torch.equal(out["forces"], out2["forces"])
+    assert torch.equal(out["energy"], out2["energy"])

@@ -1,0 +1,118 @@
+"""Host-side checks that need no GPU: the C ABI library loads and exports every
+entry point of include/xnn_amd.h, the binding declares exactly those, the ops refuse
+CPU tensors (no fallback), and the PyTorch formulation of the modules equals the
+oracle (so ``use_fast=False`` is the reference function)."""
+import ctypes
+import os
+import re
+
+import numpy as np
+import pytest
+import torch
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def _header_functions():
+    text = open(os.path.join(ROOT, "include", "xnn_amd.h")).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(xnn_[a-z0-9_]+)\s*\(", text)))
+
+
+@pytest.fixture(scope="module")
+def lib_path():
+    from xnn_amd import _lib
+    if not os.path.exists(_lib.LIBRARY):
+        from xnn_amd.build import build
+        build()
+    return _lib.LIBRARY
+
+
+def test_library_exports_every_header_entry_point(lib_path):
+    lib = ctypes.CDLL(lib_path)
+    names = _header_functions()
+    assert len(names) >= 15
+    missing = [n for n in names if not hasattr(lib, n)]
+    assert not missing, missing
+
+
+def test_binding_declares_the_header_entry_points(lib_path):
+    from xnn_amd import _lib
+    assert sorted(_lib.exported_symbols()) == _header_functions()
+    lib = _lib.load()
+    assert lib.xnn_abi_version() == _lib.ABI_VERSION
+
+
+def test_argument_errors_come_back_as_status_codes(lib_path):
+    """Invalid arguments are rejected on the host before any launch."""
+    from xnn_amd import _lib
+    lib = _lib.load()
+    prm = _lib.FeaturizeParams(8, 0, 0, 6, 7, 1, 5.0, 1.0, 1.0)   # l_max = 7
+    code = lib.xnn_edge_featurize(0, 0, 1, None, 0, None, 0, None, None, None, None, 10, prm,
+                                  1, None, None, None, None, None)
+    assert code == _lib.XNN_EINVAL
+    assert b"l_max" in lib.xnn_last_error()
+    plan = _lib.GridPlan()
+    pbc = (ctypes.c_int32 * 3)(1, 1, 1)
+    cell = (ctypes.c_double * 9)(1, 0, 0, 0, 1, 0, 0, 0, 1)
+    code = lib.xnn_radius_graph_plan(10, cell, pbc, 5.0, None, None, ctypes.byref(plan))
+    assert code == _lib.XNN_EINVAL and b"cutoff" in lib.xnn_last_error()
+    cell = (ctypes.c_double * 9)(20, 0, 0, 0, 20, 0, 0, 0, 20)
+    assert lib.xnn_radius_graph_plan(10, cell, pbc, 5.0, None, None, ctypes.byref(plan)) == 0
+    assert list(plan.nbins) == [3, 3, 3] and list(plan.reach) == [1, 1, 1]
+
+
+def test_ops_refuse_cpu_tensors():
+    from xnn_amd import ops
+    vec = torch.randn(5, 3)
+    with pytest.raises(RuntimeError, match="GPU only"):
+        ops.edge_embed(vec, torch.ones(8), n_rbf=8, basis="bessel", envelope="polynomial",
+                       poly_p=6, l_max=3, cutoff=5.0)
+
+
+def test_use_fast_true_on_a_cpu_raises():
+    import xnn_amd as xa
+    from xnn_amd import synthetic
+    s = synthetic.random_molecules(1, seed=0)[0]
+    g = xa.structure_to_graph(s.as_dict(), 5.0)
+    model = xa.ShEdgePotential(channels=8, use_fast=True)
+    with pytest.raises(RuntimeError, match="no HIP path"):
+        model(g)
+
+
+@pytest.mark.parametrize("radial,envelope,sign", [("bessel", "polynomial", 1),
+                                                  ("gaussian", "cosine", -1)])
+def test_reference_formulation_equals_the_oracle(radial, envelope, sign):
+    import oracle.reference as R
+    import xnn_amd as xa
+    from xnn_amd import synthetic
+    old = torch.get_default_dtype()
+    torch.set_default_dtype(torch.float64)
+    try:
+        s = synthetic.water_box(n_molecules=64, box=12.4, grid=4, seed=3)
+        g = xa.structure_to_graph(s.as_dict(), 4.5)
+        model = xa.ShEdgePotential(n_rbf=8, l_max=3, channels=8, cutoff=4.5, radial_type=radial,
+                                   envelope=envelope, sh_sign=sign)
+        out = xa.ForceStressOutput(model, compute_stress=True)(g)
+        g2 = xa.structure_to_graph(s.as_dict(), 4.5)
+        params = dict(W=model.W.detach(), U=model.U.detach(), atom_ref=model.atom_ref.detach(),
+                      l_max=3, n_rbf=8, cutoff=4.5, radial=radial, envelope=envelope,
+                      sh_sign=sign)
+        ref = R.energy_forces_stress(g2.pos, g2.atomic_numbers, g2.edge_index, g2.cell_shifts,
+                                     g2.cell, g2.batch, 1, params)
+        torch.testing.assert_close(out["energy"], ref["energy"], rtol=1e-12, atol=1e-10)
+        torch.testing.assert_close(out["forces"], ref["forces"], rtol=1e-10, atol=1e-11)
+        torch.testing.assert_close(out["stress"], ref["stress"], rtol=1e-10, atol=1e-12)
+    finally:
+        torch.set_default_dtype(old)
+
+
+def test_collate_offsets_and_batch():
+    import xnn_amd as xa
+    from xnn_amd import synthetic
+    mols = synthetic.random_molecules(3, seed=1)
+    graphs = [xa.structure_to_graph(m.as_dict(), 4.0) for m in mols]
+    b = xa.collate(graphs)
+    assert b.num_graphs == 3 and b.num_nodes == 63
+    assert b.num_edges == sum(g.num_edges for g in graphs)
+    assert int(b.edge_index.max()) < 63 and torch.equal(b.batch.bincount(), torch.tensor([21] * 3))

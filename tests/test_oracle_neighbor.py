@@ -1,0 +1,118 @@
+"""Pins the radius-graph oracle (oracle/neighbor.c) before it judges the HIP cell list.
+
+Checks: an independent enumeration of the edge definition on tiny inputs
+(|pos[dst] - pos[src] + shift @ cell| < rc over a wide image range, float64),
+the reference's own neighbor-list tests (tests/common/test_neighborlist.py:29-41,
+test_neighborlist_backends.py:42-108: lengths within the cutoff, periodic edges
+present, unwrapped positions, per-axis periodicity, self-interaction, molecular
+zero shifts), and the in-package CPU brute force (the reference formulation).
+"""
+import itertools
+
+import numpy as np
+import pytest
+import torch
+
+from oracle.nl import canonical, neighbor_list
+
+
+def _independent(pos, rc, cell, pbc, self_interaction=False, span=7):
+    """Every (src=j, dst=i, shift) with |pos_i - pos_j + shift @ cell| < rc, float64."""
+    n = len(pos)
+    rows = []
+    rng = [range(-span, span + 1) if (cell is not None and pbc[a]) else [0] for a in range(3)]
+    for S in itertools.product(*rng):
+        off = np.zeros(3) if cell is None else np.asarray(S, float) @ cell
+        for i in range(n):
+            d = pos[i] - pos + off
+            dist = np.sqrt((d * d).sum(1))
+            for j in np.nonzero(dist < rc)[0]:
+                if j == i and not any(S) and not self_interaction:
+                    continue
+                rows.append((i, j, *S))
+    rows = np.array(rows, dtype=np.int64).reshape(-1, 5)
+    return rows[np.lexsort(rows.T[::-1])]
+
+
+def _tiny(seed, periodic=True, pbc=(True, True, True)):
+    rng = np.random.default_rng(seed)
+    cell = np.array([[6.1, 0.0, 0.0], [0.7, 5.8, 0.0], [0.3, -0.4, 6.4]])
+    pos = rng.uniform(0.0, 1.0, (12, 3)) @ cell + rng.integers(-2, 3, (12, 3)) @ cell * periodic
+    return pos, (cell if periodic else None), np.array(pbc)
+
+
+@pytest.mark.parametrize("seed", [0, 1, 2])
+@pytest.mark.parametrize("pbc", [(True, True, True), (True, False, True), (False, False, False)])
+def test_oracle_equals_the_edge_definition(seed, pbc):
+    pos, cell, pbc = _tiny(seed, periodic=any(pbc), pbc=pbc)
+    if not any(pbc):
+        cell = None
+        pbc = None
+    rc = 3.7
+    ei, sh, near = neighbor_list(pos, rc, cell, pbc, dtype=np.float64, margin=1e-9)
+    assert near == 0
+    want = _independent(pos, rc, cell, pbc if pbc is not None else (False,) * 3)
+    assert np.array_equal(canonical(ei, sh), want)
+
+
+def test_self_interaction_adds_the_zero_image_self_edges():
+    pos, cell, pbc = _tiny(3)
+    a, sa, _ = neighbor_list(pos, 3.7, cell, pbc, dtype=np.float64)
+    b, sb, _ = neighbor_list(pos, 3.7, cell, pbc, self_interaction=True, dtype=np.float64)
+    assert b.shape[1] == a.shape[1] + len(pos)
+    want = _independent(pos, 3.7, cell, pbc, self_interaction=True)
+    assert np.array_equal(canonical(b, sb), want)
+
+
+def test_periodic_edge_lengths_within_cutoff_and_cross_the_boundary():
+    rng = np.random.default_rng(0)
+    L, rc = 8.0, 4.0
+    pos, cell = rng.uniform(0, L, (40, 3)), np.eye(3) * L
+    ei, sh, _ = neighbor_list(pos, rc, cell, [True] * 3, dtype=np.float64)
+    vec = pos[ei[1]] - pos[ei[0]] + sh @ cell
+    assert ei.shape[1] > 0
+    assert (np.abs(sh).sum(1) > 0).any()
+    assert np.linalg.norm(vec, axis=1).max() <= rc + 1e-8
+
+
+def test_unwrapped_positions_give_the_same_vectors():
+    rng = np.random.default_rng(5)
+    L, rc = 8.0, 4.0
+    pos, cell = rng.uniform(0, L, (40, 3)), np.eye(3) * L
+    moved = pos + rng.integers(-3, 4, (40, 3)) @ cell
+    a, sa, _ = neighbor_list(pos, rc, cell, [True] * 3, dtype=np.float64)
+    b, sb, _ = neighbor_list(moved, rc, cell, [True] * 3, dtype=np.float64)
+    va = pos[a[1]] - pos[a[0]] + sa @ cell
+    vb = moved[b[1]] - moved[b[0]] + sb @ cell
+    ka = np.lexsort(np.round(np.c_[a.T, va], 6).T[::-1])
+    kb = np.lexsort(np.round(np.c_[b.T, vb], 6).T[::-1])
+    assert np.array_equal(a[:, ka], b[:, kb])
+    np.testing.assert_allclose(va[ka], vb[kb], atol=1e-9)
+
+
+def test_molecular_shifts_are_zero():
+    rng = np.random.default_rng(1)
+    ei, sh, _ = neighbor_list(rng.uniform(0, 4, (8, 3)), 3.0, None, None, dtype=np.float64)
+    assert ei.shape[0] == 2 and (sh == 0).all()
+
+
+@pytest.mark.parametrize("dtype,tdtype", [(np.float32, torch.float32), (np.float64, torch.float64)])
+def test_oracle_matches_the_reference_formulation_in_order(dtype, tdtype):
+    """Same edges in the same (image, receiver, sender) order as the reference's
+    brute force restated with torch ops (xnn_amd.data._brute_force_cpu)."""
+    from xnn_amd import synthetic
+    from xnn_amd.data import _brute_force_cpu
+    s = synthetic.argon_fcc(n_cells=2, seed=4)
+    ei, sh, _ = neighbor_list(s.pos, 6.0, s.cell, s.pbc, dtype=dtype)
+    e2, s2 = _brute_force_cpu(torch.tensor(s.pos, dtype=tdtype), 6.0,
+                              torch.tensor(s.cell, dtype=tdtype), torch.tensor(s.pbc), False)
+    assert np.array_equal(ei, e2.numpy()) and np.array_equal(sh, s2.numpy())
+
+
+def test_full_list_is_symmetric():
+    from xnn_amd import synthetic
+    s = synthetic.water_box(n_molecules=64, box=12.4, grid=4)
+    ei, sh, _ = neighbor_list(s.pos, 5.0, s.cell, s.pbc, dtype=np.float64)
+    fwd = canonical(ei, sh)
+    rev = canonical(ei[::-1].copy(), -sh)
+    assert np.array_equal(fwd, rev)

@@ -1,0 +1,27 @@
+"""xnn_amd: the per-edge hot path of molssi-ai/xnn, MI355X-native.
+
+Positions/cell/pbc -> HIP cell-list radius graph -> fused edge featurizer
+(Bessel/Gaussian x cosine/polynomial envelope, real SH l <= 3) -> deterministic
+CSR edge -> atom sums -> forces and virial by a CSR reduction, behind the
+reference's module and function interfaces.
+"""
+from . import _lib
+from .data import (AtomicGraph, batched_neighbor_list, build_neighbor_list, collate,
+                   structure_to_graph)
+from .fast import AutoPolicy, FastPathModule, MI355X_POLICY, select, set_use_fast
+from .featurizers import (BesselRBF, CosineCutoff, GaussianRBF, PolynomialCutoff,
+                          SphericalHarmonicEdgeEmbedding, spherical_harmonics)
+from .functional import cell_volume, gather_rows, scatter_sum, structure_sum
+from .models import (InteratomicPotential, ModelConfig, ShEdgePotential, build_model,
+                     get_model_class, register_model)
+from .outputs import ForceStressOutput
+
+__all__ = [
+    "AtomicGraph", "build_neighbor_list", "batched_neighbor_list", "structure_to_graph", "collate",
+    "AutoPolicy", "FastPathModule", "MI355X_POLICY", "select", "set_use_fast",
+    "BesselRBF", "GaussianRBF", "CosineCutoff", "PolynomialCutoff",
+    "SphericalHarmonicEdgeEmbedding", "spherical_harmonics",
+    "scatter_sum", "gather_rows", "structure_sum", "cell_volume",
+    "InteratomicPotential", "ModelConfig", "ShEdgePotential", "build_model", "get_model_class",
+    "register_model", "ForceStressOutput",
+]

@@ -1,0 +1,185 @@
+"""ctypes binding of the C ABI in ``include/xnn_amd.h`` (``libxnn_amd.so``).
+
+The library is loaded once per process. Loading fails loudly: there is no
+silent fallback to another implementation when the HIP library is missing.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+from typing import Optional
+
+import torch
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIBRARY = os.path.join(HERE, "libxnn_amd.so")
+ABI_VERSION = 1
+
+XNN_OK, XNN_EINVAL, XNN_ECAPACITY, XNN_EHIP = 0, 1, 2, 3
+XNN_F32, XNN_F64 = 0, 1
+BASIS = {"bessel": 0, "gaussian": 1}
+ENVELOPE = {"polynomial": 0, "cosine": 1, "none": 2}
+
+c_i32p = ctypes.POINTER(ctypes.c_int32)
+c_i64p = ctypes.POINTER(ctypes.c_int64)
+c_f64p = ctypes.POINTER(ctypes.c_double)
+vp = ctypes.c_void_p
+i64 = ctypes.c_int64
+i32 = ctypes.c_int32
+c_int = ctypes.c_int
+dbl = ctypes.c_double
+sz = ctypes.c_size_t
+
+
+class FeaturizeParams(ctypes.Structure):
+    """``xnn_featurize_params``."""
+    _fields_ = [("n_rbf", i32), ("basis", i32), ("envelope", i32), ("poly_p", i32),
+                ("l_max", i32), ("sh_sign", i32), ("cutoff", dbl), ("rbf_prefactor", dbl),
+                ("gaussian_gamma", dbl)]
+
+
+class GridPlan(ctypes.Structure):
+    """``xnn_grid_plan``."""
+    _fields_ = [("nbins", i32 * 3), ("reach", i32 * 3), ("periodic", i32 * 3), ("has_cell", i32),
+                ("lo", dbl * 3), ("width", dbl * 3), ("inv_cell", dbl * 9), ("n_bins", i64),
+                ("workspace_bytes", sz)]
+
+
+# name -> argtypes (restype int unless listed in _RESTYPES)
+_SIGNATURES = {
+    "xnn_last_error": [],
+    "xnn_abi_version": [],
+    "xnn_edge_featurize": [c_int, c_int, vp, vp, i64, vp, i64, vp, vp, vp, vp, i64,
+                           ctypes.POINTER(FeaturizeParams), vp, vp, vp, vp, vp, vp],
+    "xnn_edge_featurize_backward": [c_int, c_int, vp, vp, i64, vp, i64, vp, vp, vp, vp, i64,
+                                    ctypes.POINTER(FeaturizeParams), vp, vp, vp, vp, vp, vp, vp,
+                                    vp],
+    "xnn_edge_force_reduce": [c_int, c_int, vp, i64, vp, vp, vp, vp, vp, i64, vp, vp, vp],
+    "xnn_sh_message_sum": [c_int, vp, vp, i64, vp, i64, vp, vp, vp, i64, vp, vp, i32, i32, i32,
+                           vp, vp, vp],
+    "xnn_sh_message_sum_backward": [c_int, vp, vp, i64, vp, i64, vp, vp, vp, i64, vp, vp, i32,
+                                    i32, i32, vp, vp, vp, vp, vp],
+    "xnn_segment_sum": [c_int, vp, i64, i64, vp, vp, i64, vp, vp],
+    "xnn_gather_rows": [c_int, vp, i64, i64, vp, i64, vp, vp],
+    "xnn_segment_reduce_f64": [c_int, vp, i64, i64, vp, i64, vp, vp],
+    "xnn_radius_graph_plan": [i64, c_f64p, c_i32p, dbl, c_f64p, c_f64p, ctypes.POINTER(GridPlan)],
+    "xnn_radius_graph_count": [c_int, vp, i64, vp, dbl, i32, ctypes.POINTER(GridPlan), vp, vp, vp],
+    "xnn_radius_graph_fill": [c_int, vp, i64, vp, dbl, i32, ctypes.POINTER(GridPlan), vp, vp, i64,
+                              vp, vp, vp, vp, vp, vp, vp],
+    "xnn_radius_graph_molecules_count": [c_int, vp, i64, vp, vp, i64, dbl, i32, vp, vp],
+    "xnn_radius_graph_molecules_fill": [c_int, vp, i64, vp, vp, i64, dbl, i32, vp, i64, vp, vp,
+                                        vp, vp, vp, vp],
+    "xnn_scan_workspace_bytes": [i64],
+    "xnn_scan_counts": [vp, i64, vp, vp],
+    "xnn_edge_plan_workspace_bytes": [i64, i64],
+    "xnn_edge_plan": [vp, vp, i64, i64, vp, vp, vp, vp, vp, vp, vp, vp, vp, sz, vp],
+}
+_RESTYPES = {"xnn_last_error": ctypes.c_char_p, "xnn_scan_workspace_bytes": sz,
+             "xnn_edge_plan_workspace_bytes": sz}
+
+_lock = threading.Lock()
+_lib: Optional[ctypes.CDLL] = None
+
+
+class XnnError(RuntimeError):
+    """A call into the HIP library failed (bad argument, capacity or HIP error)."""
+
+    def __init__(self, name: str, code: int, message: str):
+        super().__init__(f"{name} failed ({['ok', 'invalid argument', 'capacity', 'HIP error'][code] if 0 <= code < 4 else code}): {message}")
+        self.code = code
+
+
+def load() -> ctypes.CDLL:
+    """Load ``libxnn_amd.so`` (raises ``RuntimeError`` if it is not built)."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is not None:
+            return _lib
+        if not os.path.exists(LIBRARY):
+            raise RuntimeError(
+                f"{LIBRARY} is missing: build it with `python -m xnn_amd.build` "
+                "(the HIP kernels have no fallback)")
+        lib = ctypes.CDLL(LIBRARY)
+        for name, args in _SIGNATURES.items():
+            fn = getattr(lib, name)
+            fn.argtypes = args
+            fn.restype = _RESTYPES.get(name, ctypes.c_int)
+        if lib.xnn_abi_version() != ABI_VERSION:
+            raise RuntimeError(f"{LIBRARY} has ABI {lib.xnn_abi_version()}, expected {ABI_VERSION}")
+        _lib = lib
+        return lib
+
+
+def available() -> bool:
+    """Whether the library file exists (does not load it)."""
+    return os.path.exists(LIBRARY)
+
+
+def exported_symbols() -> list[str]:
+    """Names of the entry points this binding declares."""
+    return list(_SIGNATURES)
+
+
+def check(name: str, code: int) -> None:
+    """Raise :class:`XnnError` for a non-zero status of ``name``."""
+    if code != XNN_OK:
+        msg = load().xnn_last_error()
+        raise XnnError(name, code, msg.decode() if msg else "")
+
+
+#: entry point name -> list of (start, end) HIP events recorded around each launch,
+#: for the names a profiler asked for (see :func:`time_launches`)
+timed: dict = {}
+
+
+def time_launches(*names: str) -> None:
+    """Record HIP events around every later launch of ``names`` on the launch stream."""
+    for n in names:
+        timed.setdefault(n, [])
+
+
+def call(name: str, *args) -> None:
+    """Call entry point ``name`` and raise on a non-zero status."""
+    count_call(name)
+    fn = getattr(load(), name)
+    events = timed.get(name)
+    if events is None:
+        check(name, fn(*args))
+        return
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    code = fn(*args)
+    end.record()
+    events.append((start, end))
+    check(name, code)
+
+
+def ptr(t: Optional[torch.Tensor]) -> Optional[int]:
+    """Device pointer of a tensor (``None`` -> NULL)."""
+    if t is None:
+        return None
+    return t.data_ptr()
+
+
+def stream(device: torch.device) -> int:
+    """The current HIP stream of ``device`` as an integer handle."""
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def dtype_code(dtype: torch.dtype) -> int:
+    if dtype == torch.float32:
+        return XNN_F32
+    if dtype == torch.float64:
+        return XNN_F64
+    raise TypeError(f"unsupported dtype {dtype} (float32 or float64)")
+
+
+calls: dict = {}
+
+
+def count_call(name: str) -> None:
+    """Record that a HIP entry point ran (tests assert the native path was taken)."""
+    calls[name] = calls.get(name, 0) + 1

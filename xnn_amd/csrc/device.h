@@ -1,0 +1,244 @@
+// Device-side building blocks shared by the per-edge kernels (gfx950, wave64).
+//
+//  * packed integer image shifts
+//  * the edge vector r_e = pos[dst] - pos[src] + shift @ cell (atomic_data.py:371-418)
+//  * real spherical harmonics l <= 3 in the e3nn convention (component
+//    normalization, y is the polar axis; gnn/featurizers/spherical.py:91-93)
+//  * Bessel / Gaussian radial bases and polynomial / cosine envelopes with
+//    their derivatives (common/featurizers/radial.py, cutoff.py)
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "xnn_amd.h"
+
+namespace xnn {
+
+constexpr int kWave = 64;
+
+// ---------------------------------------------------------------- shifts
+__host__ __device__ inline int32_t pack_shift(int sx, int sy, int sz) {
+  return (int32_t)(((uint32_t)sx & 1023u) | (((uint32_t)sy & 1023u) << 10) |
+                   (((uint32_t)sz & 1023u) << 20));
+}
+__host__ __device__ inline void unpack_shift(int32_t p, int& sx, int& sy, int& sz) {
+  sx = (int32_t)((uint32_t)p << 22) >> 22;
+  sy = (int32_t)((uint32_t)p << 12) >> 22;
+  sz = (int32_t)((uint32_t)p << 2) >> 22;
+}
+
+// ---------------------------------------------------------------- geometry
+template <typename G>
+struct Cell {
+  G m[9];
+};
+
+// r = pos[d] - pos[s] + (sx, sy, sz) @ cell, formed in the geometry dtype in the
+// reference's order: the difference first, then the image offset.
+template <typename G>
+__device__ inline void edge_vector(const G* __restrict__ pos, int s, int d, int32_t shift,
+                                   const G* __restrict__ cell, G& x, G& y, G& z) {
+  x = pos[3 * d + 0] - pos[3 * s + 0];
+  y = pos[3 * d + 1] - pos[3 * s + 1];
+  z = pos[3 * d + 2] - pos[3 * s + 2];
+  if (cell != nullptr) {
+    int sx, sy, sz;
+    unpack_shift(shift, sx, sy, sz);
+    if ((sx | sy | sz) != 0) {
+      const G fx = (G)sx, fy = (G)sy, fz = (G)sz;
+      x += fx * cell[0] + fy * cell[3] + fz * cell[6];
+      y += fx * cell[1] + fy * cell[4] + fz * cell[7];
+      z += fx * cell[2] + fy * cell[5] + fz * cell[8];
+    }
+  }
+}
+
+// ---------------------------------------------------------------- spherical harmonics
+// Component-normalized real SH of a unit vector u = (x, y, z) in the e3nn order
+// (m = -l..l within each l). They are sqrt(2l+1) times the orthonormal real SH
+// without Condon-Shortley phase, taken with the standard polar axis on y:
+// (x_s, y_s, z_s) = (z, x, y). Homogeneous of degree l in u.
+template <int LMAX, typename T>
+__device__ inline void sh_eval(T x, T y, T z, T* __restrict__ Y) {
+  Y[0] = T(1);
+  if constexpr (LMAX >= 1) {
+    const T s3 = T(1.7320508075688772);
+    Y[1] = s3 * x;
+    Y[2] = s3 * y;
+    Y[3] = s3 * z;
+  }
+  if constexpr (LMAX >= 2) {
+    const T s15 = T(3.872983346207417);
+    const T s5 = T(2.23606797749979);
+    const T x2 = x * x, y2 = y * y, z2 = z * z;
+    Y[4] = s15 * x * z;
+    Y[5] = s15 * x * y;
+    Y[6] = s5 * (y2 - T(0.5) * (x2 + z2));
+    Y[7] = s15 * y * z;
+    Y[8] = T(0.5) * s15 * (z2 - x2);
+  }
+  if constexpr (LMAX >= 3) {
+    const T a = T(2.091650066335189);   // sqrt(35/8)
+    const T b = T(10.246950765959598);  // sqrt(105)
+    const T c = T(1.620185174601965);   // sqrt(21/8)
+    const T d = T(1.3228756555322954);  // sqrt(7)/2
+    const T e = T(5.123475382979799);   // sqrt(105)/2
+    const T x2 = x * x, y2 = y * y, z2 = z * z;
+    Y[9] = a * x * (T(3) * z2 - x2);
+    Y[10] = b * x * y * z;
+    Y[11] = c * x * (T(4) * y2 - x2 - z2);
+    Y[12] = d * y * (T(2) * y2 - T(3) * x2 - T(3) * z2);
+    Y[13] = c * z * (T(4) * y2 - x2 - z2);
+    Y[14] = e * y * (z2 - x2);
+    Y[15] = a * z * (z2 - T(3) * x2);
+  }
+}
+
+// G = sum_lm dY[lm] * grad_u Y_lm(u) (not projected onto the sphere).
+template <int LMAX, typename T>
+__device__ inline void sh_grad(T x, T y, T z, const T* __restrict__ dY, T& gx, T& gy, T& gz) {
+  gx = T(0);
+  gy = T(0);
+  gz = T(0);
+  if constexpr (LMAX >= 1) {
+    const T s3 = T(1.7320508075688772);
+    gx += s3 * dY[1];
+    gy += s3 * dY[2];
+    gz += s3 * dY[3];
+  }
+  if constexpr (LMAX >= 2) {
+    const T s15 = T(3.872983346207417);
+    const T s5 = T(2.23606797749979);
+    // Y4 = s15 xz, Y5 = s15 xy, Y6 = s5 (y2 - (x2+z2)/2), Y7 = s15 yz, Y8 = s15/2 (z2 - x2)
+    gx += s15 * (dY[4] * z + dY[5] * y - dY[8] * x) - s5 * dY[6] * x;
+    gy += s15 * (dY[5] * x + dY[7] * z) + T(2) * s5 * dY[6] * y;
+    gz += s15 * (dY[4] * x + dY[7] * y + dY[8] * z) - s5 * dY[6] * z;
+  }
+  if constexpr (LMAX >= 3) {
+    const T a = T(2.091650066335189);
+    const T b = T(10.246950765959598);
+    const T c = T(1.620185174601965);
+    const T d = T(1.3228756555322954);
+    const T e = T(5.123475382979799);
+    const T x2 = x * x, y2 = y * y, z2 = z * z;
+    // Y9  = a (3 x z2 - x3)            grad a (3 z2 - 3 x2, 0, 6 x z)
+    // Y10 = b x y z                    grad b (y z, x z, x y)
+    // Y11 = c (4 x y2 - x3 - x z2)     grad c (4 y2 - 3 x2 - z2, 8 x y, -2 x z)
+    // Y12 = d (2 y3 - 3 x2 y - 3 y z2) grad d (-6 x y, 6 y2 - 3 x2 - 3 z2, -6 y z)
+    // Y13 = c (4 y2 z - x2 z - z3)     grad c (-2 x z, 8 y z, 4 y2 - x2 - 3 z2)
+    // Y14 = e (y z2 - y x2)            grad e (-2 x y, z2 - x2, 2 y z)
+    // Y15 = a (z3 - 3 x2 z)            grad a (-6 x z, 0, 3 z2 - 3 x2)
+    gx += a * (dY[9] * (T(3) * z2 - T(3) * x2) - dY[15] * T(6) * x * z) + b * dY[10] * y * z +
+          c * (dY[11] * (T(4) * y2 - T(3) * x2 - z2) - dY[13] * T(2) * x * z) -
+          d * dY[12] * T(6) * x * y - e * dY[14] * T(2) * x * y;
+    gy += b * dY[10] * x * z + c * (dY[11] * T(8) * x * y + dY[13] * T(8) * y * z) +
+          d * dY[12] * (T(6) * y2 - T(3) * x2 - T(3) * z2) + e * dY[14] * (z2 - x2);
+    gz += a * (dY[9] * T(6) * x * z + dY[15] * (T(3) * z2 - T(3) * x2)) + b * dY[10] * x * y +
+          c * (-dY[11] * T(2) * x * z + dY[13] * (T(4) * y2 - x2 - T(3) * z2)) -
+          d * dY[12] * T(6) * y * z + e * dY[14] * T(2) * y * z;
+  }
+}
+
+// dL/dv for Y(v / |v|): the gradient G on the unit sphere projected to its
+// tangent plane and divided by |v|. Zero for |v| == 0.
+template <typename T>
+__device__ inline void sh_chain(T ux, T uy, T uz, T inv_len, T gx, T gy, T gz, T& ox, T& oy,
+                                T& oz) {
+  const T radial = ux * gx + uy * gy + uz * gz;
+  ox = (gx - radial * ux) * inv_len;
+  oy = (gy - radial * uy) * inv_len;
+  oz = (gz - radial * uz) * inv_len;
+}
+
+// ---------------------------------------------------------------- radial
+__device__ inline void dev_sincos(float a, float* s, float* c) { sincosf(a, s, c); }
+__device__ inline void dev_sincos(double a, double* s, double* c) { sincos(a, s, c); }
+__device__ inline float dev_exp(float a) { return expf(a); }
+__device__ inline double dev_exp(double a) { return exp(a); }
+__device__ inline float dev_sqrt(float a) { return sqrtf(a); }
+__device__ inline double dev_sqrt(double a) { return sqrt(a); }
+
+template <typename T>
+struct Radial {
+  int K;
+  int basis;
+  int envelope;
+  int p;
+  T rc;
+  T prefactor;
+  T gamma;
+  const T* __restrict__ table;  // Bessel frequencies or Gaussian centers
+};
+
+// envelope value and derivative at distance r
+template <typename T>
+__device__ inline void envelope_eval(const Radial<T>& R, T r, T& f, T& df) {
+  if (R.envelope == XNN_ENV_NONE) {
+    f = T(1);
+    df = T(0);
+    return;
+  }
+  if (!(r < R.rc)) {
+    f = T(0);
+    df = T(0);
+    return;
+  }
+  if (R.envelope == XNN_ENV_POLYNOMIAL) {
+    // 1 + ((-(p(p+1)/2) x + p(p+2)) x - (p+1)(p+2)/2) x^p  (cutoff.py:119-125)
+    const T x = r / R.rc;
+    const T pp = (T)R.p;
+    const T a = -(pp * (pp + T(1)) / T(2));
+    const T b = pp * (pp + T(2));
+    const T c = -(pp + T(1)) * (pp + T(2)) / T(2);
+    T xpm1 = T(1);
+    for (int k = 0; k < R.p - 1; ++k) xpm1 *= x;
+    const T xp = xpm1 * x;
+    const T tail = (a * x + b) * x + c;
+    f = T(1) + tail * xp;
+    df = ((T(2) * a * x + b) * xp + pp * tail * xpm1) / R.rc;
+  } else {
+    // 0.5 (cos(pi r / rc) + 1)  (cutoff.py:40-41)
+    const T w = T(3.141592653589793) / R.rc;
+    T s, c;
+    dev_sincos(w * r, &s, &c);
+    f = T(0.5) * (c + T(1));
+    df = T(-0.5) * w * s;
+  }
+}
+
+// radial[k] = rbf_k(r) * f(r), optional derivative d radial[k] / dr
+template <typename T, bool DERIV>
+__device__ inline void radial_eval(const Radial<T>& R, T r, T* __restrict__ u,
+                                   T* __restrict__ du) {
+  T f, df;
+  envelope_eval(R, r, f, df);
+  if (R.basis == XNN_BASIS_BESSEL) {
+    // prefactor * sin(freq * r / rc) / r with r clamped at 1e-8 (radial.py:267-268)
+    const bool clamped = r < T(1e-8);
+    const T rr = clamped ? T(1e-8) : r;
+    const T inv = T(1) / rr;
+    for (int k = 0; k < R.K; ++k) {
+      const T a = R.table[k] * rr / R.rc;
+      T s, c;
+      dev_sincos(a, &s, &c);
+      const T b = R.prefactor * s * inv;
+      u[k] = b * f;
+      if constexpr (DERIV) {
+        const T db = clamped ? T(0) : R.prefactor * (c * (R.table[k] / R.rc) - s * inv) * inv;
+        du[k] = db * f + b * df;
+      }
+    }
+  } else {
+    // exp(-gamma (r - mu_k)^2)  (radial.py:73-75)
+    for (int k = 0; k < R.K; ++k) {
+      const T dd = r - R.table[k];
+      const T b = dev_exp(-R.gamma * dd * dd);
+      u[k] = b * f;
+      if constexpr (DERIV) du[k] = T(-2) * R.gamma * dd * b * f + b * df;
+    }
+  }
+}
+
+constexpr int kMaxRbf = 32;
+
+}  // namespace xnn

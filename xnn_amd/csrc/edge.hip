@@ -1,0 +1,380 @@
+// Per-edge featurization, its backward, and the deterministic edge -> atom
+// force reduction (gfx950).
+//
+// xnn_edge_featurize           AtomicGraph.edge_vectors (atomic_data.py:371-418) +
+//                              SphericalHarmonicEdgeEmbedding.embed (spherical.py:115-138)
+// xnn_edge_featurize_backward  the autograd chain of the above back to r_e
+// xnn_edge_force_reduce        _EdgeVectors.backward (atomic_data.py:452-467) without atomics
+#include <string.h>
+
+#include "common.h"
+#include "device.h"
+
+namespace xnn {
+
+thread_local char g_error[512] = "";
+
+void set_error(const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_error, sizeof(g_error), fmt, ap);
+  va_end(ap);
+}
+
+template <typename G>
+__device__ inline const G* cell_of(const G* cell, int64_t n_graphs, const int32_t* batch,
+                                   int node) {
+  if (cell == nullptr) return nullptr;
+  if (n_graphs <= 1 || batch == nullptr) return cell;
+  return cell + 9 * (int64_t)batch[node];
+}
+
+// ---------------------------------------------------------------- featurize
+// edge vector in the compute dtype: given, or formed from positions
+template <typename G, typename T>
+__device__ inline void load_edge(const T* __restrict__ vec_in, const G* __restrict__ pos,
+                                 const G* __restrict__ cell, int64_t n_graphs,
+                                 const int32_t* __restrict__ batch, const int32_t* __restrict__ src,
+                                 const int32_t* __restrict__ dst, const int32_t* __restrict__ shift,
+                                 int64_t e, T& x, T& y, T& z) {
+  if (vec_in != nullptr) {
+    x = vec_in[3 * e + 0];
+    y = vec_in[3 * e + 1];
+    z = vec_in[3 * e + 2];
+    return;
+  }
+  const int s = src[e], d = dst[e];
+  G gx, gy, gz;
+  edge_vector(pos, s, d, shift[e], cell_of(cell, n_graphs, batch, d), gx, gy, gz);
+  x = (T)gx;
+  y = (T)gy;
+  z = (T)gz;
+}
+
+template <typename G, typename T, int LMAX>
+__global__ __launch_bounds__(256) void featurize_fwd_kernel(
+    const T* __restrict__ vec_in, const G* __restrict__ pos, const G* __restrict__ cell, int64_t n_graphs,
+    const int32_t* __restrict__ batch, const int32_t* __restrict__ src,
+    const int32_t* __restrict__ dst, const int32_t* __restrict__ shift, int64_t n_edges,
+    Radial<T> R, int sign, T* __restrict__ vec, T* __restrict__ length, T* __restrict__ sh,
+    T* __restrict__ radial) {
+  const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (e >= n_edges) return;
+  T x, y, z;
+  load_edge(vec_in, pos, cell, n_graphs, batch, src, dst, shift, e, x, y, z);
+  if (vec) {
+    vec[3 * e + 0] = x;
+    vec[3 * e + 1] = y;
+    vec[3 * e + 2] = z;
+  }
+  const T r = dev_sqrt(x * x + y * y + z * z);
+  if (length) length[e] = r;
+  if (sh) {
+    constexpr int L = (LMAX + 1) * (LMAX + 1);
+    const T inv = r > T(0) ? T(1) / r : T(0);
+    const T sg = (T)sign;
+    T Y[L];
+    sh_eval<LMAX, T>(sg * x * inv, sg * y * inv, sg * z * inv, Y);
+#pragma unroll
+    for (int k = 0; k < L; ++k) sh[e * L + k] = Y[k];
+  }
+  if (radial) {
+    T u[kMaxRbf];
+    radial_eval<T, false>(R, r, u, nullptr);
+    for (int k = 0; k < R.K; ++k) radial[e * R.K + k] = u[k];
+  }
+}
+
+template <typename G, typename T, int LMAX>
+__global__ __launch_bounds__(256) void featurize_bwd_kernel(
+    const T* __restrict__ vec_in, const G* __restrict__ pos, const G* __restrict__ cell, int64_t n_graphs,
+    const int32_t* __restrict__ batch, const int32_t* __restrict__ src,
+    const int32_t* __restrict__ dst, const int32_t* __restrict__ shift, int64_t n_edges,
+    Radial<T> R, int sign, const T* __restrict__ d_vec, const T* __restrict__ d_length,
+    const T* __restrict__ d_sh, const T* __restrict__ d_radial, const T* __restrict__ g_extra,
+    T* __restrict__ g_edge) {
+  const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (e >= n_edges) return;
+  T x, y, z;
+  load_edge(vec_in, pos, cell, n_graphs, batch, src, dst, shift, e, x, y, z);
+  const T r = dev_sqrt(x * x + y * y + z * z);
+  const T inv = r > T(0) ? T(1) / r : T(0);
+  const T ux = x * inv, uy = y * inv, uz = z * inv;
+  T ox = T(0), oy = T(0), oz = T(0);
+  if (d_vec) {
+    ox = d_vec[3 * e + 0];
+    oy = d_vec[3 * e + 1];
+    oz = d_vec[3 * e + 2];
+  }
+  if (g_extra) {
+    ox += g_extra[3 * e + 0];
+    oy += g_extra[3 * e + 1];
+    oz += g_extra[3 * e + 2];
+  }
+  T dl = d_length ? d_length[e] : T(0);
+  if (d_radial) {
+    T u[kMaxRbf], du[kMaxRbf];
+    radial_eval<T, true>(R, r, u, du);
+    for (int k = 0; k < R.K; ++k) dl += d_radial[e * R.K + k] * du[k];
+  }
+  ox += dl * ux;
+  oy += dl * uy;
+  oz += dl * uz;
+  if (d_sh && r > T(0)) {
+    constexpr int L = (LMAX + 1) * (LMAX + 1);
+    T dY[L];
+#pragma unroll
+    for (int k = 0; k < L; ++k) dY[k] = d_sh[e * L + k];
+    const T sg = (T)sign;
+    T Gx, Gy, Gz, vx, vy, vz;
+    sh_grad<LMAX, T>(sg * ux, sg * uy, sg * uz, dY, Gx, Gy, Gz);
+    sh_chain<T>(sg * ux, sg * uy, sg * uz, inv, Gx, Gy, Gz, vx, vy, vz);
+    ox += sg * vx;
+    oy += sg * vy;
+    oz += sg * vz;
+  }
+  g_edge[3 * e + 0] = ox;
+  g_edge[3 * e + 1] = oy;
+  g_edge[3 * e + 2] = oz;
+}
+
+// ---------------------------------------------------------------- force reduce
+// GROUP lanes per atom: lanes stride over the atom's receiver and sender rows,
+// then a fixed butterfly sums the lanes (bitwise reproducible).
+template <typename G, typename T, int GROUP>
+__global__ __launch_bounds__(256) void force_reduce_kernel(
+    const T* __restrict__ g_edge, const int32_t* __restrict__ ptr_dst,
+    const int32_t* __restrict__ perm_dst, const int32_t* __restrict__ ptr_src,
+    const int32_t* __restrict__ perm_src, const int32_t* __restrict__ shift, int64_t n_nodes,
+    G* __restrict__ grad_pos, double* __restrict__ cell_partial) {
+  const int lane = threadIdx.x % GROUP;
+  const int64_t i = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) / GROUP;
+  const bool live = i < n_nodes;
+  double fx = 0, fy = 0, fz = 0;
+  double c[9] = {0, 0, 0, 0, 0, 0, 0, 0, 0};
+  if (live) {
+    const int b0 = ptr_dst[i], b1 = ptr_dst[i + 1];
+    for (int k = b0 + lane; k < b1; k += GROUP) {
+      const int e = perm_dst ? perm_dst[k] : k;
+      const double x = g_edge[3 * (int64_t)e + 0], y = g_edge[3 * (int64_t)e + 1],
+                   z = g_edge[3 * (int64_t)e + 2];
+      fx += x;
+      fy += y;
+      fz += z;
+      if (cell_partial) {
+        int sx, sy, sz;
+        unpack_shift(shift[e], sx, sy, sz);
+        c[0] += sx * x; c[1] += sx * y; c[2] += sx * z;
+        c[3] += sy * x; c[4] += sy * y; c[5] += sy * z;
+        c[6] += sz * x; c[7] += sz * y; c[8] += sz * z;
+      }
+    }
+    const int s0 = ptr_src[i], s1 = ptr_src[i + 1];
+    for (int k = s0 + lane; k < s1; k += GROUP) {
+      const int e = perm_src ? perm_src[k] : k;
+      fx -= g_edge[3 * (int64_t)e + 0];
+      fy -= g_edge[3 * (int64_t)e + 1];
+      fz -= g_edge[3 * (int64_t)e + 2];
+    }
+  }
+#pragma unroll
+  for (int m = GROUP / 2; m > 0; m >>= 1) {
+    fx += __shfl_xor(fx, m, GROUP);
+    fy += __shfl_xor(fy, m, GROUP);
+    fz += __shfl_xor(fz, m, GROUP);
+    if (cell_partial) {
+#pragma unroll
+      for (int q = 0; q < 9; ++q) c[q] += __shfl_xor(c[q], m, GROUP);
+    }
+  }
+  if (live && lane == 0) {
+    grad_pos[3 * i + 0] = (G)fx;
+    grad_pos[3 * i + 1] = (G)fy;
+    grad_pos[3 * i + 2] = (G)fz;
+    if (cell_partial) {
+#pragma unroll
+      for (int q = 0; q < 9; ++q) cell_partial[9 * i + q] = c[q];
+    }
+  }
+}
+
+// ---------------------------------------------------------------- dispatch helpers
+template <typename T>
+static int make_radial(const xnn_featurize_params* prm, const void* table, Radial<T>& R) {
+  XNN_REQUIRE(prm != nullptr, "featurize params are NULL");
+  XNN_REQUIRE(prm->n_rbf >= 0 && prm->n_rbf <= kMaxRbf, "n_rbf must be in [0, %d], got %d",
+              kMaxRbf, prm->n_rbf);
+  XNN_REQUIRE(prm->n_rbf == 0 || table != nullptr, "rbf_table is NULL");
+  XNN_REQUIRE(prm->basis == XNN_BASIS_BESSEL || prm->basis == XNN_BASIS_GAUSSIAN,
+              "unknown basis %d", prm->basis);
+  XNN_REQUIRE(prm->envelope >= XNN_ENV_POLYNOMIAL && prm->envelope <= XNN_ENV_NONE,
+              "unknown envelope %d", prm->envelope);
+  XNN_REQUIRE(prm->envelope != XNN_ENV_POLYNOMIAL || (prm->poly_p >= 1 && prm->poly_p <= 64),
+              "polynomial envelope degree must be in [1, 64], got %d", prm->poly_p);
+  XNN_REQUIRE(prm->cutoff > 0, "cutoff must be positive");
+  XNN_REQUIRE(prm->l_max >= 0 && prm->l_max <= 3, "l_max must be in [0, 3], got %d",
+              prm->l_max);
+  XNN_REQUIRE(prm->sh_sign == 1 || prm->sh_sign == -1, "sh_sign must be +1 or -1");
+  R.K = prm->n_rbf;
+  R.basis = prm->basis;
+  R.envelope = prm->envelope;
+  R.p = prm->poly_p;
+  R.rc = (T)prm->cutoff;
+  R.prefactor = (T)prm->rbf_prefactor;
+  R.gamma = (T)prm->gaussian_gamma;
+  R.table = static_cast<const T*>(table);
+  return XNN_OK;
+}
+
+template <typename G, typename T>
+static int featurize_fwd(const void* vec_in, const void* pos, const void* cell, int64_t n_graphs,
+                         const int32_t* batch, const int32_t* src, const int32_t* dst,
+                         const int32_t* shift, int64_t n_edges,
+                         const xnn_featurize_params* prm, const void* table, void* vec,
+                         void* length, void* sh, void* radial, hipStream_t stream) {
+  Radial<T> R;
+  int st = make_radial<T>(prm, table, R);
+  if (st != XNN_OK) return st;
+  if (n_edges == 0) return XNN_OK;
+  const dim3 grid(grid_1d(n_edges, 256)), block(256);
+#define XNN_FWD(LM)                                                                      \
+  hipLaunchKernelGGL((featurize_fwd_kernel<G, T, LM>), grid, block, 0, stream,           \
+                     (const T*)vec_in, (const G*)pos, (const G*)cell, n_graphs, batch, src, dst, shift,    \
+                     n_edges, R, prm->sh_sign, (T*)vec, (T*)length, (T*)sh, (T*)radial)
+  switch (prm->l_max) {
+    case 0: XNN_FWD(0); break;
+    case 1: XNN_FWD(1); break;
+    case 2: XNN_FWD(2); break;
+    default: XNN_FWD(3); break;
+  }
+#undef XNN_FWD
+  XNN_LAUNCH_CHECK();
+  return XNN_OK;
+}
+
+template <typename G, typename T>
+static int featurize_bwd(const void* vec_in, const void* pos, const void* cell, int64_t n_graphs,
+                         const int32_t* batch, const int32_t* src, const int32_t* dst,
+                         const int32_t* shift, int64_t n_edges,
+                         const xnn_featurize_params* prm, const void* table, const void* d_vec,
+                         const void* d_length, const void* d_sh, const void* d_radial,
+                         const void* g_extra, void* g_edge, hipStream_t stream) {
+  Radial<T> R;
+  int st = make_radial<T>(prm, table, R);
+  if (st != XNN_OK) return st;
+  if (n_edges == 0) return XNN_OK;
+  const dim3 grid(grid_1d(n_edges, 256)), block(256);
+#define XNN_BWD(LM)                                                                       \
+  hipLaunchKernelGGL((featurize_bwd_kernel<G, T, LM>), grid, block, 0, stream,            \
+                     (const T*)vec_in, (const G*)pos, (const G*)cell, n_graphs, batch, src, dst, shift,     \
+                     n_edges, R, prm->sh_sign, (const T*)d_vec, (const T*)d_length,       \
+                     (const T*)d_sh, (const T*)d_radial, (const T*)g_extra, (T*)g_edge)
+  switch (prm->l_max) {
+    case 0: XNN_BWD(0); break;
+    case 1: XNN_BWD(1); break;
+    case 2: XNN_BWD(2); break;
+    default: XNN_BWD(3); break;
+  }
+#undef XNN_BWD
+  XNN_LAUNCH_CHECK();
+  return XNN_OK;
+}
+
+template <typename G, typename T, int GROUP>
+static void launch_force_reduce(const void* g_edge, const int32_t* ptr_dst,
+                                const int32_t* perm_dst, const int32_t* ptr_src,
+                                const int32_t* perm_src, const int32_t* shift, int64_t n_nodes,
+                                void* grad_pos, double* cell_partial, hipStream_t stream) {
+  const int64_t threads = n_nodes * GROUP;
+  hipLaunchKernelGGL((force_reduce_kernel<G, T, GROUP>), dim3(grid_1d(threads, 256)),
+                     dim3(256), 0, stream, (const T*)g_edge, ptr_dst, perm_dst, ptr_src,
+                     perm_src, shift, n_nodes, (G*)grad_pos, cell_partial);
+}
+
+template <typename G, typename T>
+static int force_reduce(const void* g_edge, int64_t n_edges, const int32_t* ptr_dst,
+                        const int32_t* perm_dst, const int32_t* ptr_src,
+                        const int32_t* perm_src, const int32_t* shift, int64_t n_nodes,
+                        void* grad_pos, double* cell_partial, hipStream_t stream) {
+  if (n_nodes == 0) return XNN_OK;
+  // lanes per atom from the mean degree (both rows are walked)
+  const double deg = n_nodes > 0 ? (double)n_edges / (double)n_nodes : 0.0;
+  if (deg > 24)
+    launch_force_reduce<G, T, 32>(g_edge, ptr_dst, perm_dst, ptr_src, perm_src, shift, n_nodes,
+                                  grad_pos, cell_partial, stream);
+  else if (deg > 6)
+    launch_force_reduce<G, T, 16>(g_edge, ptr_dst, perm_dst, ptr_src, perm_src, shift, n_nodes,
+                                  grad_pos, cell_partial, stream);
+  else
+    launch_force_reduce<G, T, 4>(g_edge, ptr_dst, perm_dst, ptr_src, perm_src, shift, n_nodes,
+                                 grad_pos, cell_partial, stream);
+  XNN_LAUNCH_CHECK();
+  return XNN_OK;
+}
+
+}  // namespace xnn
+
+using namespace xnn;
+
+#define XNN_DISPATCH_GT(geom, comp, FN, ...)                                         \
+  do {                                                                               \
+    if ((geom) == XNN_F32 && (comp) == XNN_F32) return FN<float, float>(__VA_ARGS__); \
+    if ((geom) == XNN_F64 && (comp) == XNN_F64)                                      \
+      return FN<double, double>(__VA_ARGS__);                                        \
+    if ((geom) == XNN_F64 && (comp) == XNN_F32)                                      \
+      return FN<double, float>(__VA_ARGS__);                                         \
+    set_error("unsupported dtype pair geometry=%d compute=%d", (int)(geom), (int)(comp)); \
+    return XNN_EINVAL;                                                               \
+  } while (0)
+
+extern "C" {
+
+const char* xnn_last_error(void) { return g_error; }
+int xnn_abi_version(void) { return 1; }
+
+int xnn_edge_featurize(int geom_dtype, int compute_dtype, const void* vec_in, const void* pos,
+                       int64_t n_nodes, const void* cell, int64_t n_graphs, const int32_t* batch,
+                       const int32_t* src, const int32_t* dst, const int32_t* shift,
+                       int64_t n_edges, const xnn_featurize_params* prm, const void* rbf_table,
+                       void* vec, void* length, void* sh, void* radial, xnn_stream_t stream) {
+  XNN_REQUIRE(n_edges >= 0 && n_nodes >= 0, "negative size");
+  XNN_REQUIRE(n_edges == 0 || vec_in || (pos && src && dst && shift), "NULL edge input");
+  XNN_REQUIRE(cell == nullptr || n_graphs <= 1 || batch != nullptr,
+              "several cells need the batch vector");
+  XNN_DISPATCH_GT(geom_dtype, compute_dtype, featurize_fwd, vec_in, pos, cell, n_graphs, batch, src,
+                  dst, shift, n_edges, prm, rbf_table, vec, length, sh, radial,
+                  as_hip(stream));
+}
+
+int xnn_edge_featurize_backward(int geom_dtype, int compute_dtype, const void* vec_in,
+                                const void* pos, int64_t n_nodes, const void* cell, int64_t n_graphs,
+                                const int32_t* batch, const int32_t* src, const int32_t* dst,
+                                const int32_t* shift, int64_t n_edges,
+                                const xnn_featurize_params* prm, const void* rbf_table,
+                                const void* d_vec, const void* d_length, const void* d_sh,
+                                const void* d_radial, const void* g_extra, void* g_edge,
+                                xnn_stream_t stream) {
+  XNN_REQUIRE(n_edges >= 0 && n_nodes >= 0, "negative size");
+  XNN_REQUIRE(n_edges == 0 || ((vec_in || (pos && src && dst && shift)) && g_edge),
+              "NULL edge input");
+  XNN_REQUIRE(cell == nullptr || n_graphs <= 1 || batch != nullptr,
+              "several cells need the batch vector");
+  XNN_DISPATCH_GT(geom_dtype, compute_dtype, featurize_bwd, vec_in, pos, cell, n_graphs, batch, src,
+                  dst, shift, n_edges, prm, rbf_table, d_vec, d_length, d_sh, d_radial,
+                  g_extra, g_edge, as_hip(stream));
+}
+
+int xnn_edge_force_reduce(int geom_dtype, int compute_dtype, const void* g_edge, int64_t n_edges,
+                          const int32_t* ptr_dst, const int32_t* perm_dst,
+                          const int32_t* ptr_src, const int32_t* perm_src,
+                          const int32_t* shift, int64_t n_nodes, void* grad_pos,
+                          double* cell_partial, xnn_stream_t stream) {
+  XNN_REQUIRE(n_edges >= 0 && n_nodes >= 0, "negative size");
+  XNN_REQUIRE(n_nodes == 0 || (ptr_dst && ptr_src && grad_pos), "NULL CSR or output");
+  XNN_REQUIRE(n_edges == 0 || g_edge, "NULL g_edge");
+  XNN_REQUIRE(cell_partial == nullptr || shift != nullptr, "cell_partial needs the shifts");
+  XNN_DISPATCH_GT(geom_dtype, compute_dtype, force_reduce, g_edge, n_edges, ptr_dst, perm_dst,
+                  ptr_src, perm_src, shift, n_nodes, grad_pos, cell_partial, as_hip(stream));
+}
+
+}  // extern "C"

@@ -1,0 +1,748 @@
+// Radius graph (cell list) and edge plans (receiver/sender CSR), gfx950.
+//
+// xnn_radius_graph_*          build_neighbor_list (common/data/neighborlist.py:411-506):
+//                             full directed list, dist < cutoff in the geometry dtype,
+//                             edge (src=j, dst=i), shift = -S + o_j - o_i with o the
+//                             wrap offsets (neighborlist.py:472-475, 500-505).
+// xnn_radius_graph_molecules_* the molecular branch (neighborlist.py:466-468) for a batch
+// xnn_edge_plan               compressed/orderings (common/models/csr.py:20-51)
+//
+// Cell list: atoms are binned on a grid in fractional coordinates whose bins are at
+// least `cutoff` wide along every plane normal, counting-sorted by bin (stable radix
+// sort), and every receiver bin stages the atoms of its neighbor bins in LDS. One wave
+// tests one receiver against 64 candidates at a time and compacts the hits with a
+// ballot + prefix popcount, so edges of a row land in a fixed order (neighbor bin,
+// then atom index): two identical passes (count, then fill) without atomics.
+#include <math.h>
+#include <string.h>
+
+#include <hipcub/hipcub.hpp>
+
+#include "common.h"
+#include "device.h"
+
+namespace xnn {
+
+constexpr double kBinSlack = 1e-5;       // bins are (1 + slack) * cutoff wide at least
+constexpr int64_t kMaxBins = 1 << 22;   // grid size cap (bins merge beyond it)
+constexpr int kTile = 1024;             // candidates staged in LDS per pass
+
+struct GridDev {
+  int nb[3], reach[3], periodic[3], has_cell;
+  double lo[3], width[3], inv[9];
+};
+
+static inline size_t align_up(size_t x) { return (x + 255) & ~(size_t)255; }
+
+// workspace layout of the cell list (offsets in bytes); the count step fills it
+// and the fill step reads it back, so both must get the same buffer.
+struct GridWs {
+  size_t bin_key, bin_key_sorted, atom_id, atom_sorted, wpos, offs, wpos_s, offs_s, bin_cnt,
+      bin_start, counts, overflow, cub, cub_bytes, total;
+};
+
+template <typename G>
+static GridWs grid_ws_layout(int64_t n, int64_t n_bins) {
+  GridWs w;
+  size_t at = 0;
+  w.bin_key = at; at += align_up(sizeof(int32_t) * n);
+  w.bin_key_sorted = at; at += align_up(sizeof(int32_t) * n);
+  w.atom_id = at; at += align_up(sizeof(int32_t) * n);
+  w.atom_sorted = at; at += align_up(sizeof(int32_t) * n);
+  w.wpos = at; at += align_up(sizeof(G) * 4 * n);
+  w.offs = at; at += align_up(sizeof(int32_t) * 4 * n);
+  w.wpos_s = at; at += align_up(sizeof(G) * 4 * n);
+  w.offs_s = at; at += align_up(sizeof(int32_t) * 4 * n);
+  w.bin_cnt = at; at += align_up(sizeof(int32_t) * (n_bins + 1));
+  w.bin_start = at; at += align_up(sizeof(int32_t) * (n_bins + 1));
+  w.counts = at; at += align_up(sizeof(int32_t) * (n + 1));
+  w.overflow = at; at += align_up(sizeof(int32_t) * 4);
+  size_t sort_bytes = 0, scan_bytes = 0, scan2 = 0;
+  (void)hipcub::DeviceRadixSort::SortPairs(nullptr, sort_bytes, (int32_t*)nullptr, (int32_t*)nullptr,
+                                     (int32_t*)nullptr, (int32_t*)nullptr, (int)n);
+  (void)hipcub::DeviceScan::ExclusiveSum(nullptr, scan_bytes, (int32_t*)nullptr, (int32_t*)nullptr,
+                                   (int)(n_bins + 1));
+  (void)hipcub::DeviceScan::InclusiveSum(nullptr, scan2, (int32_t*)nullptr, (int32_t*)nullptr,
+                                   (int)(n + 1));
+  w.cub = at;
+  w.cub_bytes = align_up(std::max(sort_bytes, std::max(scan_bytes, scan2)) + 256);
+  at += w.cub_bytes;
+  w.total = at;
+  return w;
+}
+
+template <typename T>
+__device__ __host__ inline T* ws_at(void* ws, size_t off) {
+  return reinterpret_cast<T*>(static_cast<char*>(ws) + off);
+}
+
+// ---------------------------------------------------------------- binning
+// frac = pos @ inv(cell); wrap offsets o = floor(frac) on periodic axes; wrapped
+// position wpos = pos - o @ cell (geometry dtype, as neighborlist.py:472-475).
+template <typename G>
+__global__ void bin_atoms_kernel(const G* __restrict__ pos, int64_t n, const G* __restrict__ cell,
+                                 GridDev g, int32_t* __restrict__ bin_key,
+                                 int32_t* __restrict__ atom_id, G* __restrict__ wpos,
+                                 int32_t* __restrict__ offs, int32_t* __restrict__ bin_count) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  const G p[3] = {pos[3 * i], pos[3 * i + 1], pos[3 * i + 2]};
+  G w[3] = {p[0], p[1], p[2]};
+  int o[3] = {0, 0, 0};
+  int b[3];
+  if (g.has_cell) {
+    G f[3];
+    for (int a = 0; a < 3; ++a)
+      f[a] = p[0] * (G)g.inv[0 * 3 + a] + p[1] * (G)g.inv[1 * 3 + a] + p[2] * (G)g.inv[2 * 3 + a];
+    for (int a = 0; a < 3; ++a)
+      if (g.periodic[a]) o[a] = (int)floor((double)f[a]);
+    if (o[0] | o[1] | o[2]) {
+      const G ox = (G)o[0], oy = (G)o[1], oz = (G)o[2];
+      for (int a = 0; a < 3; ++a) w[a] = p[a] - (ox * cell[a] + oy * cell[3 + a] + oz * cell[6 + a]);
+    }
+    for (int a = 0; a < 3; ++a) {
+      // bin from the unwrapped fractional coordinate minus the offset, in double
+      const double fa = (double)f[a] - (double)o[a];
+      int k = (int)floor((fa - g.lo[a]) / g.width[a]);
+      b[a] = min(max(k, 0), g.nb[a] - 1);
+    }
+  } else {
+    for (int a = 0; a < 3; ++a) {
+      int k = (int)floor(((double)p[a] - g.lo[a]) / g.width[a]);
+      b[a] = min(max(k, 0), g.nb[a] - 1);
+    }
+  }
+  const int key = (b[2] * g.nb[1] + b[1]) * g.nb[0] + b[0];
+  bin_key[i] = key;
+  atom_id[i] = (int32_t)i;
+  wpos[4 * i + 0] = w[0];
+  wpos[4 * i + 1] = w[1];
+  wpos[4 * i + 2] = w[2];
+  wpos[4 * i + 3] = G(0);
+  offs[4 * i + 0] = o[0];
+  offs[4 * i + 1] = o[1];
+  offs[4 * i + 2] = o[2];
+  offs[4 * i + 3] = key;
+  atomicAdd(&bin_count[key], 1);
+}
+
+// ---------------------------------------------------------------- search
+// One block per receiver bin. Neighbor slots enumerate (dz, dy, dx) in
+// [-reach, reach]; slot s has bin index nbin[s] (or -1) and image shift S[s].
+template <typename G, bool FILL>
+__global__ __launch_bounds__(256) void cell_search_kernel(
+    const G* __restrict__ wpos, const int32_t* __restrict__ offs,
+    const int32_t* __restrict__ atom_sorted, const int32_t* __restrict__ bin_start,
+    const G* __restrict__ cell, GridDev g, G cutoff, int self_interaction,
+    int32_t* __restrict__ counts, const int32_t* __restrict__ row_ptr, int32_t* __restrict__ src,
+    int32_t* __restrict__ dst, int32_t* __restrict__ shift_out, int64_t* __restrict__ ei64,
+    int64_t* __restrict__ sh64, int64_t n_edges, int32_t* __restrict__ overflow) {
+  constexpr int kMaxSlots = 343;  // reach <= 3 per axis
+  __shared__ int s_bin[kMaxSlots];
+  __shared__ int s_img[kMaxSlots][3];
+  __shared__ G s_vec[kMaxSlots][3];
+  __shared__ int s_first[kMaxSlots + 1];
+  __shared__ G t_pos[kTile][3];
+  __shared__ int t_atom[kTile];
+  __shared__ int t_slot[kTile];
+
+  const int bin = blockIdx.x;
+  const int bx = bin % g.nb[0], by = (bin / g.nb[0]) % g.nb[1], bz = bin / (g.nb[0] * g.nb[1]);
+  const int r0 = bin_start[bin], r1 = bin_start[bin + 1];
+  if (r0 == r1) return;  // uniform: no receivers
+  const int wx = 2 * g.reach[0] + 1, wy = 2 * g.reach[1] + 1, wz = 2 * g.reach[2] + 1;
+  const int n_slots = wx * wy * wz;
+
+  // neighbor slots and their image shifts
+  for (int s = threadIdx.x; s < n_slots; s += blockDim.x) {
+    const int d[3] = {s % wx - g.reach[0], (s / wx) % wy - g.reach[1], s / (wx * wy) - g.reach[2]};
+    const int c[3] = {bx, by, bz};
+    int idx[3], img[3];
+    bool ok = true;
+    for (int a = 0; a < 3; ++a) {
+      const int t = c[a] + d[a];
+      if (g.periodic[a]) {
+        const int q = (int)floor((double)t / (double)g.nb[a]);
+        img[a] = q;
+        idx[a] = t - q * g.nb[a];
+      } else {
+        img[a] = 0;
+        idx[a] = t;
+        ok = ok && t >= 0 && t < g.nb[a];
+      }
+    }
+    s_bin[s] = ok ? (idx[2] * g.nb[1] + idx[1]) * g.nb[0] + idx[0] : -1;
+    s_img[s][0] = img[0];
+    s_img[s][1] = img[1];
+    s_img[s][2] = img[2];
+    // image offset S @ cell in the geometry dtype (neighborlist.py:481-483)
+    if (cell != nullptr) {
+      const G fx = (G)img[0], fy = (G)img[1], fz = (G)img[2];
+      for (int a = 0; a < 3; ++a) s_vec[s][a] = fx * cell[a] + fy * cell[3 + a] + fz * cell[6 + a];
+    } else {
+      s_vec[s][0] = s_vec[s][1] = s_vec[s][2] = G(0);
+    }
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    int acc = 0;
+    for (int s = 0; s < n_slots; ++s) {
+      s_first[s] = acc;
+      const int b = s_bin[s];
+      if (b >= 0) acc += bin_start[b + 1] - bin_start[b];
+    }
+    s_first[n_slots] = acc;
+  }
+  __syncthreads();
+  const int n_cand = s_first[n_slots];
+
+  const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+  const int n_waves = blockDim.x / kWave;
+  const int n_recv = r1 - r0;
+
+  for (int c0 = 0; c0 < n_cand; c0 += kTile) {
+    const int c1 = min(n_cand, c0 + kTile);
+    // stage candidates [c0, c1) in LDS, in slot order then bin order
+    for (int c = c0 + threadIdx.x; c < c1; c += blockDim.x) {
+      int lo = 0, hi = n_slots - 1;  // slot with s_first[slot] <= c < s_first[slot+1]
+      while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if (s_first[mid] <= c) lo = mid; else hi = mid - 1;
+      }
+      const int s = lo;
+      const int p = bin_start[s_bin[s]] + (c - s_first[s]);
+      t_pos[c - c0][0] = wpos[4 * p + 0];
+      t_pos[c - c0][1] = wpos[4 * p + 1];
+      t_pos[c - c0][2] = wpos[4 * p + 2];
+      t_atom[c - c0] = atom_sorted[p];
+      t_slot[c - c0] = s;
+    }
+    __syncthreads();
+    for (int r = wave; r < n_recv; r += n_waves) {
+      const int pr = r0 + r;
+      const int i = atom_sorted[pr];
+      const G xi = wpos[4 * pr + 0], yi = wpos[4 * pr + 1], zi = wpos[4 * pr + 2];
+      // edges of receiver i found in earlier tiles (a receiver stays with its wave)
+      const int base = counts[i];
+      int local = 0;
+      for (int c = 0; c < c1 - c0; c += kWave) {
+        const int t = c + lane;
+        bool hit = false;
+        int j = -1, s = 0;
+        if (t < c1 - c0) {
+          j = t_atom[t];
+          s = t_slot[t];
+          // (pos_j - pos_i) + S @ cell in the geometry dtype; the squares summed in
+          // double (exact products: contraction cannot change them), the root
+          // rounded back to the geometry dtype before the strict comparison
+          const G dx = (t_pos[t][0] - xi) + s_vec[s][0];
+          const G dy = (t_pos[t][1] - yi) + s_vec[s][1];
+          const G dz = (t_pos[t][2] - zi) + s_vec[s][2];
+          const double d2 = (double)dx * (double)dx + (double)dy * (double)dy +
+                            (double)dz * (double)dz;
+          hit = (G)sqrt(d2) < cutoff;
+          if (!self_interaction && j == i && s_img[s][0] == 0 && s_img[s][1] == 0 &&
+              s_img[s][2] == 0)
+            hit = false;
+        }
+        const unsigned long long mask = __ballot(hit);
+        if (FILL && hit) {
+          const int rank = __popcll(mask & ((1ull << lane) - 1ull));
+          const int64_t e = (int64_t)row_ptr[i] + base + local + rank;
+          if (e < n_edges) {
+            const int oi0 = offs[4 * pr + 0], oi1 = offs[4 * pr + 1], oi2 = offs[4 * pr + 2];
+            // sender offsets live with the sorted copy; find j's through its own slot
+            const int pj = bin_start[s_bin[s]] + (t + c0 - s_first[s]);
+            const int sx = -s_img[s][0] + offs[4 * pj + 0] - oi0;
+            const int sy = -s_img[s][1] + offs[4 * pj + 1] - oi1;
+            const int sz = -s_img[s][2] + offs[4 * pj + 2] - oi2;
+            if (sx < -512 || sx > 511 || sy < -512 || sy > 511 || sz < -512 || sz > 511)
+              atomicOr(overflow, 1);
+            src[e] = j;
+            dst[e] = i;
+            shift_out[e] = pack_shift(sx, sy, sz);
+            if (ei64) {
+              ei64[e] = j;
+              ei64[n_edges + e] = i;
+            }
+            if (sh64) {
+              sh64[3 * e + 0] = sx;
+              sh64[3 * e + 1] = sy;
+              sh64[3 * e + 2] = sz;
+            }
+          }
+        }
+        local += __popcll(mask);
+      }
+      if (lane == 0) counts[i] = base + local;
+    }
+    __syncthreads();
+  }
+}
+
+__global__ void zero_i32_kernel(int32_t* p, int64_t n) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = 0;
+}
+
+__global__ void set_first_zero_kernel(int32_t* p) { p[0] = 0; }
+
+// ---------------------------------------------------------------- molecules
+template <typename G, bool FILL>
+__global__ __launch_bounds__(256) void molecule_search_kernel(
+    const G* __restrict__ pos, int64_t n, const int64_t* __restrict__ node_ptr,
+    const int32_t* __restrict__ batch, G cutoff, int self_interaction,
+    int32_t* __restrict__ counts, const int32_t* __restrict__ row_ptr, int32_t* __restrict__ src,
+    int32_t* __restrict__ dst, int32_t* __restrict__ shift_out, int64_t* __restrict__ ei64,
+    int64_t* __restrict__ sh64, int64_t n_edges) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  const int b = batch[i];
+  const int64_t j0 = node_ptr[b], j1 = node_ptr[b + 1];
+  const G xi = pos[3 * i], yi = pos[3 * i + 1], zi = pos[3 * i + 2];
+  int64_t k = FILL ? row_ptr[i] : 0;
+  int cnt = 0;
+  for (int64_t j = j0; j < j1; ++j) {
+    const G dx = pos[3 * j] - xi, dy = pos[3 * j + 1] - yi, dz = pos[3 * j + 2] - zi;
+    const double d2 = (double)dx * (double)dx + (double)dy * (double)dy + (double)dz * (double)dz;
+    if (!((G)sqrt(d2) < cutoff)) continue;
+    if (!self_interaction && j == i) continue;
+    if (FILL && k < n_edges) {
+      src[k] = (int32_t)j;
+      dst[k] = (int32_t)i;
+      shift_out[k] = 0;
+      if (ei64) {
+        ei64[k] = j;
+        ei64[n_edges + k] = i;
+      }
+      if (sh64) sh64[3 * k] = sh64[3 * k + 1] = sh64[3 * k + 2] = 0;
+    }
+    ++k;
+    ++cnt;
+  }
+  if (!FILL) counts[i + 1] = cnt;
+}
+
+// ---------------------------------------------------------------- edge plan
+__global__ void plan_unpack_kernel(const int64_t* __restrict__ ei, const int64_t* __restrict__ sh,
+                                   int64_t E, int64_t n, int32_t* __restrict__ src,
+                                   int32_t* __restrict__ dst, int32_t* __restrict__ shift,
+                                   int32_t* __restrict__ key_src, int32_t* __restrict__ key_dst,
+                                   int32_t* __restrict__ iota, int32_t* __restrict__ cnt_dst,
+                                   int32_t* __restrict__ cnt_src, int32_t* __restrict__ overflow) {
+  const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (e >= E) return;
+  const int64_t s = ei[e], d = ei[E + e];
+  if (s < 0 || s >= n || d < 0 || d >= n) {
+    atomicOr(overflow, 2);
+    src[e] = dst[e] = 0;
+    key_src[e] = key_dst[e] = 0;
+  } else {
+    src[e] = (int32_t)s;
+    dst[e] = (int32_t)d;
+    key_src[e] = (int32_t)s;
+    key_dst[e] = (int32_t)d;
+    atomicAdd(&cnt_dst[d + 1], 1);
+    atomicAdd(&cnt_src[s + 1], 1);
+  }
+  iota[e] = (int32_t)e;
+  int64_t x = 0, y = 0, z = 0;
+  if (sh) {
+    x = sh[3 * e];
+    y = sh[3 * e + 1];
+    z = sh[3 * e + 2];
+  }
+  if (x < -512 || x > 511 || y < -512 || y > 511 || z < -512 || z > 511) atomicOr(overflow, 1);
+  shift[e] = pack_shift((int)x, (int)y, (int)z);
+}
+
+struct PlanWs {
+  size_t key_src, key_dst, iota, keys_out, cnt, cub, cub_bytes, total;
+};
+
+static PlanWs plan_ws_layout(int64_t E, int64_t n) {
+  PlanWs w;
+  size_t at = 0;
+  w.key_src = at; at += align_up(sizeof(int32_t) * E);
+  w.key_dst = at; at += align_up(sizeof(int32_t) * E);
+  w.iota = at; at += align_up(sizeof(int32_t) * E);
+  w.keys_out = at; at += align_up(sizeof(int32_t) * E);
+  w.cnt = at; at += align_up(sizeof(int32_t) * 2 * (n + 1));
+  size_t sort_bytes = 0, scan_bytes = 0;
+  (void)hipcub::DeviceRadixSort::SortPairs(nullptr, sort_bytes, (int32_t*)nullptr, (int32_t*)nullptr,
+                                     (int32_t*)nullptr, (int32_t*)nullptr, (int)E);
+  (void)hipcub::DeviceScan::InclusiveSum(nullptr, scan_bytes, (int32_t*)nullptr, (int32_t*)nullptr,
+                                   (int)(n + 1));
+  w.cub = at;
+  w.cub_bytes = align_up(std::max(sort_bytes, scan_bytes) + 256);
+  at += w.cub_bytes;
+  w.total = at;
+  return w;
+}
+
+static int end_bit_for(int64_t n) {
+  int b = 1;
+  while ((int64_t(1) << b) < n + 1 && b < 31) ++b;
+  return b;
+}
+
+// sorted copies of the wrapped positions and offsets (candidates stream from them)
+template <typename G>
+__global__ void gather_sorted_kernel(const int32_t* __restrict__ atom_sorted, int64_t n,
+                                     const G* __restrict__ wpos, const int32_t* __restrict__ offs,
+                                     G* __restrict__ wpos_s, int32_t* __restrict__ offs_s) {
+  const int64_t p = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (p >= n) return;
+  const int64_t i = atom_sorted[p];
+  for (int k = 0; k < 4; ++k) {
+    wpos_s[4 * p + k] = wpos[4 * i + k];
+    offs_s[4 * p + k] = offs[4 * i + k];
+  }
+}
+
+static GridDev grid_dev(const xnn_grid_plan* plan) {
+  GridDev g;
+  for (int a = 0; a < 3; ++a) {
+    g.nb[a] = plan->nbins[a];
+    g.reach[a] = plan->reach[a];
+    g.periodic[a] = plan->periodic[a];
+    g.lo[a] = plan->lo[a];
+    g.width[a] = plan->width[a];
+  }
+  g.has_cell = plan->has_cell;
+  for (int k = 0; k < 9; ++k) g.inv[k] = plan->inv_cell[k];
+  return g;
+}
+
+// count step: bin, sort, search (counting), scan into row_ptr
+template <typename G>
+static int grid_count(const void* pos_v, int64_t n, const void* cell_v, double cutoff,
+                      int self_interaction, const xnn_grid_plan* plan, void* ws,
+                      int32_t* row_ptr, hipStream_t stream) {
+  const G* pos = (const G*)pos_v;
+  const G* cell = (const G*)cell_v;
+  const GridDev g = grid_dev(plan);
+  const GridWs w = grid_ws_layout<G>(n, plan->n_bins);
+  XNN_REQUIRE(w.total <= plan->workspace_bytes, "workspace smaller than the plan's");
+  int32_t* bin_key = ws_at<int32_t>(ws, w.bin_key);
+  int32_t* bin_key_sorted = ws_at<int32_t>(ws, w.bin_key_sorted);
+  int32_t* atom_id = ws_at<int32_t>(ws, w.atom_id);
+  int32_t* atom_sorted = ws_at<int32_t>(ws, w.atom_sorted);
+  G* wpos = ws_at<G>(ws, w.wpos);
+  int32_t* offs = ws_at<int32_t>(ws, w.offs);
+  G* wpos_s = ws_at<G>(ws, w.wpos_s);
+  int32_t* offs_s = ws_at<int32_t>(ws, w.offs_s);
+  int32_t* bin_cnt = ws_at<int32_t>(ws, w.bin_cnt);
+  int32_t* bin_start = ws_at<int32_t>(ws, w.bin_start);
+  int32_t* counts = ws_at<int32_t>(ws, w.counts);
+  int32_t* overflow = ws_at<int32_t>(ws, w.overflow);
+  void* cub = ws_at<char>(ws, w.cub);
+  size_t cub_bytes = w.cub_bytes;
+
+  const int64_t nb1 = plan->n_bins + 1;
+  hipLaunchKernelGGL(zero_i32_kernel, dim3(grid_1d(nb1, 256)), dim3(256), 0, stream, bin_cnt, nb1);
+  hipLaunchKernelGGL(zero_i32_kernel, dim3(grid_1d(n + 1, 256)), dim3(256), 0, stream, counts,
+                     n + 1);
+  hipLaunchKernelGGL(zero_i32_kernel, dim3(1), dim3(64), 0, stream, overflow, (int64_t)4);
+  hipLaunchKernelGGL((bin_atoms_kernel<G>), dim3(grid_1d(n, 256)), dim3(256), 0, stream, pos, n,
+                     cell, g, bin_key, atom_id, wpos, offs, bin_cnt);
+  XNN_LAUNCH_CHECK();
+  XNN_HIP_CHECK(hipcub::DeviceScan::ExclusiveSum(cub, cub_bytes, bin_cnt, bin_start, (int)nb1,
+                                                 stream));
+  // stable: atoms of one bin keep ascending index order
+  XNN_HIP_CHECK(hipcub::DeviceRadixSort::SortPairs(cub, cub_bytes, bin_key, bin_key_sorted,
+                                                   atom_id, atom_sorted, (int)n, 0,
+                                                   end_bit_for(plan->n_bins), stream));
+  hipLaunchKernelGGL((gather_sorted_kernel<G>), dim3(grid_1d(n, 256)), dim3(256), 0, stream,
+                     atom_sorted, n, wpos, offs, wpos_s, offs_s);
+  hipLaunchKernelGGL((cell_search_kernel<G, false>), dim3(plan->n_bins), dim3(256), 0, stream,
+                     wpos_s, offs_s, atom_sorted, bin_start, cell, g, (G)cutoff, self_interaction,
+                     counts, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, (int64_t)0,
+                     overflow);
+  XNN_LAUNCH_CHECK();
+  // row_ptr[1..n] = inclusive scan of the per-atom counts; row_ptr[0] = 0
+  XNN_HIP_CHECK(hipcub::DeviceScan::InclusiveSum(cub, cub_bytes, counts, row_ptr + 1, (int)n,
+                                                 stream));
+  hipLaunchKernelGGL(set_first_zero_kernel, dim3(1), dim3(1), 0, stream, row_ptr);
+  XNN_LAUNCH_CHECK();
+  return XNN_OK;
+}
+
+// fill step: the same search over the binned atoms left in the workspace
+template <typename G>
+static int grid_fill(const void* pos_v, int64_t n, const void* cell_v, double cutoff,
+                     int self_interaction, const xnn_grid_plan* plan, void* ws,
+                     const int32_t* row_ptr, int64_t n_edges, int32_t* src, int32_t* dst,
+                     int32_t* shift, int64_t* ei64, int64_t* sh64, int32_t* overflow_out,
+                     hipStream_t stream) {
+  (void)pos_v;
+  const G* cell = (const G*)cell_v;
+  const GridDev g = grid_dev(plan);
+  const GridWs w = grid_ws_layout<G>(n, plan->n_bins);
+  XNN_REQUIRE(w.total <= plan->workspace_bytes, "workspace smaller than the plan's");
+  int32_t* counts = ws_at<int32_t>(ws, w.counts);
+  int32_t* overflow = overflow_out ? overflow_out : ws_at<int32_t>(ws, w.overflow);
+  hipLaunchKernelGGL(zero_i32_kernel, dim3(grid_1d(n + 1, 256)), dim3(256), 0, stream, counts,
+                     n + 1);
+  hipLaunchKernelGGL(zero_i32_kernel, dim3(1), dim3(64), 0, stream, overflow, (int64_t)1);
+  hipLaunchKernelGGL((cell_search_kernel<G, true>), dim3(plan->n_bins), dim3(256), 0, stream,
+                     ws_at<G>(ws, w.wpos_s), ws_at<int32_t>(ws, w.offs_s),
+                     ws_at<int32_t>(ws, w.atom_sorted), ws_at<int32_t>(ws, w.bin_start), cell, g,
+                     (G)cutoff, self_interaction, counts, row_ptr, src, dst, shift, ei64, sh64,
+                     n_edges, overflow);
+  XNN_LAUNCH_CHECK();
+  return XNN_OK;
+}
+
+}  // namespace xnn
+
+using namespace xnn;
+
+extern "C" {
+
+int xnn_radius_graph_plan(int64_t n_nodes, const double* cell, const int32_t* pbc, double cutoff,
+                          const double* lo, const double* hi, xnn_grid_plan* plan) {
+  XNN_REQUIRE(plan != nullptr && pbc != nullptr, "NULL plan or pbc");
+  XNN_REQUIRE(n_nodes >= 0 && n_nodes < (int64_t(1) << 30), "atom count out of range");
+  XNN_REQUIRE(cutoff > 0 && isfinite(cutoff), "cutoff must be positive and finite");
+  memset(plan, 0, sizeof(*plan));
+  const double cut = cutoff * (1.0 + kBinSlack);
+  double spacing[3] = {1.0, 1.0, 1.0};
+  plan->has_cell = cell != nullptr;
+  if (cell != nullptr) {
+    const double* m = cell;
+    const double det = m[0] * (m[4] * m[8] - m[5] * m[7]) - m[1] * (m[3] * m[8] - m[5] * m[6]) +
+                       m[2] * (m[3] * m[7] - m[4] * m[6]);
+    XNN_REQUIRE(fabs(det) > 1e-12, "the cell is singular");
+    double* v = plan->inv_cell;
+    v[0] = (m[4] * m[8] - m[5] * m[7]) / det;
+    v[1] = (m[2] * m[7] - m[1] * m[8]) / det;
+    v[2] = (m[1] * m[5] - m[2] * m[4]) / det;
+    v[3] = (m[5] * m[6] - m[3] * m[8]) / det;
+    v[4] = (m[0] * m[8] - m[2] * m[6]) / det;
+    v[5] = (m[2] * m[3] - m[0] * m[5]) / det;
+    v[6] = (m[3] * m[7] - m[4] * m[6]) / det;
+    v[7] = (m[1] * m[6] - m[0] * m[7]) / det;
+    v[8] = (m[0] * m[4] - m[1] * m[3]) / det;
+    // interplanar spacing along axis a: 1 / |column a of inv(cell)| (neighborlist.py:96-98)
+    for (int a = 0; a < 3; ++a) {
+      const double c0 = v[a], c1 = v[3 + a], c2 = v[6 + a];
+      spacing[a] = 1.0 / sqrt(c0 * c0 + c1 * c1 + c2 * c2);
+    }
+  }
+  int64_t total = 1;
+  for (int a = 0; a < 3; ++a) {
+    const bool per = plan->has_cell && pbc[a] != 0;
+    plan->periodic[a] = per ? 1 : 0;
+    double extent;  // coordinate range covered by the grid (fractional or Cartesian)
+    if (per) {
+      plan->lo[a] = 0.0;
+      extent = 1.0;
+    } else {
+      XNN_REQUIRE(lo != nullptr && hi != nullptr, "non-periodic axes need the coordinate range");
+      XNN_REQUIRE(isfinite(lo[a]) && isfinite(hi[a]), "the positions are not finite");
+      plan->lo[a] = lo[a];
+      extent = hi[a] - lo[a];
+    }
+    const double length = extent * spacing[a];  // the range as a distance
+    double nb = floor(length / cut);
+    if (nb < 1) nb = 1;
+    if (nb > (double)kMaxBins) nb = (double)kMaxBins;
+    plan->nbins[a] = (int)nb;
+  }
+  // merge bins on the largest axes while the grid is too large
+  for (;;) {
+    total = (int64_t)plan->nbins[0] * plan->nbins[1] * plan->nbins[2];
+    if (total <= kMaxBins) break;
+    int a = 0;
+    for (int k = 1; k < 3; ++k)
+      if (plan->nbins[k] > plan->nbins[a]) a = k;
+    plan->nbins[a] = (plan->nbins[a] + 1) / 2;
+  }
+  for (int a = 0; a < 3; ++a) {
+    const double extent = plan->periodic[a] ? 1.0 : (hi[a] - lo[a]);
+    double w = extent / plan->nbins[a];
+    if (!(w > 0)) w = 1.0;  // a flat axis: one bin of any width
+    plan->width[a] = w;
+    const double wdist = w * spacing[a];
+    int reach = plan->periodic[a] ? (int)ceil(cut / wdist) : 1;
+    if (!plan->periodic[a] && plan->nbins[a] == 1) reach = 0;
+    plan->reach[a] = reach;
+    XNN_REQUIRE(reach <= 3,
+                "cutoff %.4g exceeds 3 cell spacings along axis %d (spacing %.4g): "
+                "too many periodic images for the cell list",
+                cutoff, a, spacing[a]);
+  }
+  plan->n_bins = total;
+  plan->workspace_bytes = grid_ws_layout<double>(n_nodes, total).total;
+  return XNN_OK;
+}
+
+int xnn_radius_graph_count(int geom_dtype, const void* pos, int64_t n_nodes, const void* cell,
+                           double cutoff, int32_t self_interaction, const xnn_grid_plan* plan,
+                           void* workspace, int32_t* row_ptr, xnn_stream_t stream) {
+  XNN_REQUIRE(plan && row_ptr, "NULL plan or row_ptr");
+  XNN_REQUIRE(plan->has_cell == 0 || cell != nullptr, "the plan has a cell: pass it");
+  if (n_nodes == 0) {
+    hipLaunchKernelGGL(set_first_zero_kernel, dim3(1), dim3(1), 0, as_hip(stream), row_ptr);
+    XNN_LAUNCH_CHECK();
+    return XNN_OK;
+  }
+  XNN_REQUIRE(pos && workspace, "NULL positions or workspace");
+  if (geom_dtype == XNN_F32)
+    return grid_count<float>(pos, n_nodes, cell, cutoff, self_interaction, plan, workspace,
+                             row_ptr, as_hip(stream));
+  if (geom_dtype == XNN_F64)
+    return grid_count<double>(pos, n_nodes, cell, cutoff, self_interaction, plan, workspace,
+                              row_ptr, as_hip(stream));
+  set_error("unsupported geometry dtype %d", geom_dtype);
+  return XNN_EINVAL;
+}
+
+int xnn_radius_graph_fill(int geom_dtype, const void* pos, int64_t n_nodes, const void* cell,
+                          double cutoff, int32_t self_interaction, const xnn_grid_plan* plan,
+                          void* workspace, const int32_t* row_ptr, int64_t n_edges, int32_t* src,
+                          int32_t* dst, int32_t* shift, int64_t* edge_index64, int64_t* shifts64,
+                          int32_t* overflow, xnn_stream_t stream) {
+  XNN_REQUIRE(plan && row_ptr, "NULL plan or row_ptr");
+  if (n_nodes == 0 || n_edges == 0) return XNN_OK;
+  XNN_REQUIRE(pos && workspace && src && dst && shift, "NULL input or output");
+  XNN_REQUIRE(plan->has_cell == 0 || cell != nullptr, "the plan has a cell: pass it");
+  if (geom_dtype == XNN_F32)
+    return grid_fill<float>(pos, n_nodes, cell, cutoff, self_interaction, plan, workspace, row_ptr,
+                            n_edges, src, dst, shift, edge_index64, shifts64, overflow,
+                            as_hip(stream));
+  if (geom_dtype == XNN_F64)
+    return grid_fill<double>(pos, n_nodes, cell, cutoff, self_interaction, plan, workspace,
+                             row_ptr, n_edges, src, dst, shift, edge_index64, shifts64, overflow,
+                             as_hip(stream));
+  set_error("unsupported geometry dtype %d", geom_dtype);
+  return XNN_EINVAL;
+}
+
+size_t xnn_scan_workspace_bytes(int64_t n) {
+  size_t bytes = 0;
+  (void)hipcub::DeviceScan::InclusiveSum(nullptr, bytes, (int32_t*)nullptr, (int32_t*)nullptr,
+                                   (int)(n + 1));
+  return align_up(bytes + 256) + align_up(sizeof(int32_t) * (n + 1));
+}
+
+int xnn_scan_counts(int32_t* row_ptr, int64_t n, void* workspace, xnn_stream_t stream) {
+  XNN_REQUIRE(row_ptr != nullptr, "NULL row_ptr");
+  hipStream_t s = as_hip(stream);
+  if (n > 0) {
+    XNN_REQUIRE(workspace != nullptr, "NULL workspace");
+    size_t bytes = 0;
+    (void)hipcub::DeviceScan::InclusiveSum(nullptr, bytes, (int32_t*)nullptr, (int32_t*)nullptr,
+                                     (int)(n + 1));
+    size_t cub_bytes = align_up(bytes + 256);
+    int32_t* tmp = ws_at<int32_t>(workspace, cub_bytes);
+    XNN_HIP_CHECK(hipMemcpyAsync(tmp, row_ptr + 1, sizeof(int32_t) * n, hipMemcpyDeviceToDevice, s));
+    XNN_HIP_CHECK(hipcub::DeviceScan::InclusiveSum(workspace, cub_bytes, tmp, row_ptr + 1, (int)n, s));
+  }
+  hipLaunchKernelGGL(set_first_zero_kernel, dim3(1), dim3(1), 0, s, row_ptr);
+  XNN_LAUNCH_CHECK();
+  return XNN_OK;
+}
+
+int xnn_radius_graph_molecules_count(int geom_dtype, const void* pos, int64_t n_nodes,
+                                     const int64_t* node_ptr, const int32_t* batch,
+                                     int64_t n_graphs, double cutoff, int32_t self_interaction,
+                                     int32_t* row_ptr, xnn_stream_t stream) {
+  XNN_REQUIRE(row_ptr != nullptr, "NULL row_ptr");
+  if (n_nodes == 0) {
+    hipLaunchKernelGGL(set_first_zero_kernel, dim3(1), dim3(1), 0, as_hip(stream), row_ptr);
+    XNN_LAUNCH_CHECK();
+    return XNN_OK;
+  }
+  XNN_REQUIRE(pos && node_ptr && batch, "NULL input");
+  XNN_REQUIRE(cutoff > 0, "cutoff must be positive");
+  const dim3 grid(grid_1d(n_nodes, 256)), block(256);
+  if (geom_dtype == XNN_F32)
+    hipLaunchKernelGGL((molecule_search_kernel<float, false>), grid, block, 0, as_hip(stream),
+                       (const float*)pos, n_nodes, node_ptr, batch, (float)cutoff,
+                       self_interaction, row_ptr, nullptr, nullptr, nullptr, nullptr, nullptr,
+                       nullptr, 0);
+  else if (geom_dtype == XNN_F64)
+    hipLaunchKernelGGL((molecule_search_kernel<double, false>), grid, block, 0, as_hip(stream),
+                       (const double*)pos, n_nodes, node_ptr, batch, cutoff, self_interaction,
+                       row_ptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, 0);
+  else {
+    set_error("unsupported geometry dtype %d", geom_dtype);
+    return XNN_EINVAL;
+  }
+  XNN_LAUNCH_CHECK();
+  return XNN_OK;
+}
+
+int xnn_radius_graph_molecules_fill(int geom_dtype, const void* pos, int64_t n_nodes,
+                                    const int64_t* node_ptr, const int32_t* batch,
+                                    int64_t n_graphs, double cutoff, int32_t self_interaction,
+                                    const int32_t* row_ptr, int64_t n_edges, int32_t* src,
+                                    int32_t* dst, int32_t* shift, int64_t* edge_index64,
+                                    int64_t* shifts64, xnn_stream_t stream) {
+  if (n_nodes == 0 || n_edges == 0) return XNN_OK;
+  XNN_REQUIRE(pos && node_ptr && batch && row_ptr && src && dst && shift, "NULL input");
+  const dim3 grid(grid_1d(n_nodes, 256)), block(256);
+  if (geom_dtype == XNN_F32)
+    hipLaunchKernelGGL((molecule_search_kernel<float, true>), grid, block, 0, as_hip(stream),
+                       (const float*)pos, n_nodes, node_ptr, batch, (float)cutoff,
+                       self_interaction, nullptr, row_ptr, src, dst, shift, edge_index64,
+                       shifts64, n_edges);
+  else if (geom_dtype == XNN_F64)
+    hipLaunchKernelGGL((molecule_search_kernel<double, true>), grid, block, 0, as_hip(stream),
+                       (const double*)pos, n_nodes, node_ptr, batch, cutoff, self_interaction,
+                       nullptr, row_ptr, src, dst, shift, edge_index64, shifts64, n_edges);
+  else {
+    set_error("unsupported geometry dtype %d", geom_dtype);
+    return XNN_EINVAL;
+  }
+  XNN_LAUNCH_CHECK();
+  return XNN_OK;
+}
+
+size_t xnn_edge_plan_workspace_bytes(int64_t n_edges, int64_t n_nodes) {
+  return plan_ws_layout(n_edges, n_nodes).total;
+}
+
+int xnn_edge_plan(const int64_t* edge_index, const int64_t* cell_shifts, int64_t n_edges,
+                  int64_t n_nodes, int32_t* src, int32_t* dst, int32_t* shift, int32_t* ptr_dst,
+                  int32_t* perm_dst, int32_t* ptr_src, int32_t* perm_src, int32_t* overflow,
+                  void* workspace, size_t workspace_bytes, xnn_stream_t stream) {
+  XNN_REQUIRE(n_edges >= 0 && n_nodes >= 0, "negative size");
+  XNN_REQUIRE(n_edges < (int64_t(1) << 31) && n_nodes < (int64_t(1) << 31),
+              "int32 indices: at most 2^31 - 1 edges and atoms");
+  XNN_REQUIRE(ptr_dst && ptr_src && overflow, "NULL output");
+  const PlanWs w = plan_ws_layout(n_edges, n_nodes);
+  XNN_REQUIRE(workspace_bytes >= w.total, "workspace too small: %zu < %zu", workspace_bytes,
+              w.total);
+  hipStream_t s = as_hip(stream);
+  int32_t* key_src = ws_at<int32_t>(workspace, w.key_src);
+  int32_t* key_dst = ws_at<int32_t>(workspace, w.key_dst);
+  int32_t* iota = ws_at<int32_t>(workspace, w.iota);
+  int32_t* keys_out = ws_at<int32_t>(workspace, w.keys_out);
+  int32_t* cnt = ws_at<int32_t>(workspace, w.cnt);
+  void* cub = ws_at<char>(workspace, w.cub);
+  size_t cub_bytes = w.cub_bytes;
+  hipLaunchKernelGGL(zero_i32_kernel, dim3(grid_1d(2 * (n_nodes + 1), 256)), dim3(256), 0, s,
+                     cnt, 2 * (n_nodes + 1));
+  hipLaunchKernelGGL(zero_i32_kernel, dim3(1), dim3(64), 0, s, overflow, (int64_t)1);
+  if (n_edges > 0) {
+    XNN_REQUIRE(edge_index && src && dst && shift && perm_dst && perm_src, "NULL input");
+    hipLaunchKernelGGL(plan_unpack_kernel, dim3(grid_1d(n_edges, 256)), dim3(256), 0, s,
+                       edge_index, cell_shifts, n_edges, n_nodes, src, dst, shift, key_src,
+                       key_dst, iota, cnt, cnt + (n_nodes + 1), overflow);
+    XNN_LAUNCH_CHECK();
+    const int eb = end_bit_for(n_nodes);
+    XNN_HIP_CHECK(hipcub::DeviceRadixSort::SortPairs(cub, cub_bytes, key_dst, keys_out, iota,
+                                                     perm_dst, (int)n_edges, 0, eb, s));
+    XNN_HIP_CHECK(hipcub::DeviceRadixSort::SortPairs(cub, cub_bytes, key_src, keys_out, iota,
+                                                     perm_src, (int)n_edges, 0, eb, s));
+  }
+  XNN_HIP_CHECK(hipcub::DeviceScan::InclusiveSum(cub, cub_bytes, cnt, ptr_dst, (int)(n_nodes + 1), s));
+  XNN_HIP_CHECK(hipcub::DeviceScan::InclusiveSum(cub, cub_bytes, cnt + (n_nodes + 1), ptr_src,
+                                                 (int)(n_nodes + 1), s));
+  return XNN_OK;
+}
+
+}  // extern "C"

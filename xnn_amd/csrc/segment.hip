@@ -1,0 +1,491 @@
+// Receiver-CSR segmented reductions (gfx950, wave64), all deterministic:
+// every output is summed by one wave in a fixed order, no float atomics.
+//
+// xnn_sh_message_sum(_backward)  gnn/fast/conv.py:137-143 (uvu TP of scalar weights with Y)
+//                                + scatter_sum (common/models/ops.py:403-448), fused: the
+//                                message phi[e,c] Y_lm(e) never leaves registers
+// xnn_segment_sum / gather_rows  scatter_sum / gather_rows (ops.py:403-448, 494-528)
+// xnn_segment_reduce_f64         structure_sum(s) (ops.py:531-569), fp64 accumulation
+#include "common.h"
+#include "device.h"
+
+namespace xnn {
+
+constexpr int kWavesPerBlock = 4;
+
+template <int LMAX>
+struct ShDims {
+  static constexpr int L = (LMAX + 1) * (LMAX + 1);
+  // partial sums are reduced across the wave padded to a power of two
+  static constexpr int LP = L == 1 ? 1 : (L <= 4 ? 4 : 16);
+  static constexpr int HALVINGS = L == 1 ? 0 : (L <= 4 ? 2 : 4);
+};
+
+// Per-lane geometry of one edge: unit vector of sign * r_e and 1/|r_e|; the
+// vector is given (vec) or formed from positions.
+template <typename G>
+__device__ inline void edge_unit(const float* __restrict__ vec, int64_t e,
+                                 const G* __restrict__ pos, const G* __restrict__ cell,
+                                 const int32_t* __restrict__ src, const int32_t* __restrict__ shift,
+                                 int d, float sign, float& ux, float& uy, float& uz, float& inv) {
+  float x, y, z;
+  if (vec != nullptr) {
+    x = vec[3 * e + 0];
+    y = vec[3 * e + 1];
+    z = vec[3 * e + 2];
+  } else {
+    G gx, gy, gz;
+    edge_vector(pos, src[e], d, shift[e], cell, gx, gy, gz);
+    x = (float)gx;
+    y = (float)gy;
+    z = (float)gz;
+  }
+  const float r = sqrtf(x * x + y * y + z * z);
+  inv = r > 0.f ? 1.f / r : 0.f;
+  ux = sign * x * inv;
+  uy = sign * y * inv;
+  uz = sign * z * inv;
+}
+
+// One wave per receiver row. Lane l owns channels [l*CPL, l*CPL+CPL). Edges are
+// processed in batches of 64: lane j evaluates Y for edge j of the batch and
+// parks it in LDS, then the whole wave streams phi rows (coalesced) and
+// accumulates phi[e, c] * Y[e, lm] in registers.
+template <typename G, int LMAX, int CPL>
+__global__ __launch_bounds__(256) void sh_msg_fwd_kernel(
+    const float* __restrict__ vec, const G* __restrict__ pos, const G* __restrict__ cell, int64_t n_graphs,
+    const int32_t* __restrict__ batch, const int32_t* __restrict__ src,
+    const int32_t* __restrict__ shift, const int32_t* __restrict__ ptr,
+    const int32_t* __restrict__ perm, int64_t n_nodes, int C, float sign,
+    const float* __restrict__ phi, float* __restrict__ out) {
+  constexpr int L = ShDims<LMAX>::L;
+  __shared__ float sY[kWavesPerBlock][kWave][L];
+  const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+  const int64_t row = (int64_t)blockIdx.x * kWavesPerBlock + wave;
+  if (row >= n_nodes) return;  // whole wave; no block-level barriers below
+  const G* cl = cell == nullptr ? nullptr
+                                : (n_graphs <= 1 || batch == nullptr ? cell
+                                                                     : cell + 9 * (int64_t)batch[row]);
+  const int c0 = lane * CPL;
+  const bool own = c0 < C;
+  float acc[CPL][L];
+#pragma unroll
+  for (int q = 0; q < CPL; ++q)
+#pragma unroll
+    for (int k = 0; k < L; ++k) acc[q][k] = 0.f;
+
+  const int b0 = ptr[row], b1 = ptr[row + 1];
+  for (int base = b0; base < b1; base += kWave) {
+    const int cnt = min(kWave, b1 - base);
+    if (lane < cnt) {
+      const int k = base + lane;
+      const int e = perm ? perm[k] : k;
+      float ux, uy, uz, inv;
+      edge_unit(vec, e, pos, cl, src, shift, (int)row, sign, ux, uy, uz, inv);
+      float Y[L];
+      sh_eval<LMAX, float>(ux, uy, uz, Y);
+#pragma unroll
+      for (int m = 0; m < L; ++m) sY[wave][lane][m] = Y[m];
+    }
+    wave_sync();
+    if (own) {
+      int j = 0;
+      for (; j + 2 <= cnt; j += 2) {
+        const int e0 = perm ? perm[base + j] : base + j;
+        const int e1 = perm ? perm[base + j + 1] : base + j + 1;
+        float p0[CPL], p1[CPL];
+#pragma unroll
+        for (int q = 0; q < CPL; ++q) {
+          p0[q] = (c0 + q < C) ? phi[(int64_t)e0 * C + c0 + q] : 0.f;
+          p1[q] = (c0 + q < C) ? phi[(int64_t)e1 * C + c0 + q] : 0.f;
+        }
+#pragma unroll
+        for (int m = 0; m < L; ++m) {
+          const float y0 = sY[wave][j][m], y1 = sY[wave][j + 1][m];
+#pragma unroll
+          for (int q = 0; q < CPL; ++q) acc[q][m] += p0[q] * y0 + p1[q] * y1;
+        }
+      }
+      for (; j < cnt; ++j) {
+        const int e0 = perm ? perm[base + j] : base + j;
+        float p0[CPL];
+#pragma unroll
+        for (int q = 0; q < CPL; ++q) p0[q] = (c0 + q < C) ? phi[(int64_t)e0 * C + c0 + q] : 0.f;
+#pragma unroll
+        for (int m = 0; m < L; ++m) {
+          const float y0 = sY[wave][j][m];
+#pragma unroll
+          for (int q = 0; q < CPL; ++q) acc[q][m] += p0[q] * y0;
+        }
+      }
+    }
+    wave_sync();
+  }
+  if (own) {
+#pragma unroll
+    for (int q = 0; q < CPL; ++q) {
+      if (c0 + q >= C) break;
+      float* o = out + ((int64_t)row * C + c0 + q) * L;
+#pragma unroll
+      for (int m = 0; m < L; ++m) o[m] = acc[q][m];
+    }
+  }
+}
+
+// Sum of p[0..LP) over the 64 lanes of a wave, returned so that lane l holds
+// the total of entry (l >> (6 - HALVINGS)). Each halving step trades half of
+// the live entries with the partner lane (17 shuffles for 16 entries instead
+// of 16 full reductions).
+template <int LP, int HALVINGS>
+__device__ inline float wave_transpose_reduce(float* p, int lane) {
+  int live = LP;
+#pragma unroll
+  for (int h = 0; h < HALVINGS; ++h) {
+    const int mask = 32 >> h;
+    const bool upper = (lane & mask) != 0;
+    const int half = live / 2;
+#pragma unroll
+    for (int k = 0; k < LP / 2; ++k) {
+      if (k < half) {
+        const float keep = upper ? p[k + half] : p[k];
+        const float send = upper ? p[k] : p[k + half];
+        p[k] = keep + __shfl_xor(send, mask, kWave);
+      }
+    }
+    live = half;
+  }
+#pragma unroll
+  for (int h = HALVINGS; h < 6; ++h) p[0] += __shfl_xor(p[0], 32 >> h, kWave);
+  return p[0];
+}
+
+template <typename G, int LMAX, int CPL>
+__global__ __launch_bounds__(256) void sh_msg_bwd_kernel(
+    const float* __restrict__ vec, const G* __restrict__ pos, const G* __restrict__ cell, int64_t n_graphs,
+    const int32_t* __restrict__ batch, const int32_t* __restrict__ src,
+    const int32_t* __restrict__ shift, const int32_t* __restrict__ ptr,
+    const int32_t* __restrict__ perm, int64_t n_nodes, int C, float sign,
+    const float* __restrict__ phi, const float* __restrict__ d_out, float* __restrict__ d_phi,
+    float* __restrict__ g_vec) {
+  using D = ShDims<LMAX>;
+  constexpr int L = D::L;
+  constexpr int LP = D::LP;
+  constexpr int SHIFT = 6 - D::HALVINGS;
+  __shared__ float sY[kWavesPerBlock][kWave][L];
+  __shared__ float sdY[kWavesPerBlock][kWave][LP];
+  const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+  const int64_t row = (int64_t)blockIdx.x * kWavesPerBlock + wave;
+  if (row >= n_nodes) return;
+  const G* cl = cell == nullptr ? nullptr
+                                : (n_graphs <= 1 || batch == nullptr ? cell
+                                                                     : cell + 9 * (int64_t)batch[row]);
+  const int c0 = lane * CPL;
+  const bool own = c0 < C;
+  float g[CPL][L];
+#pragma unroll
+  for (int q = 0; q < CPL; ++q)
+#pragma unroll
+    for (int m = 0; m < L; ++m)
+      g[q][m] = (own && c0 + q < C) ? d_out[((int64_t)row * C + c0 + q) * L + m] : 0.f;
+
+  const int b0 = ptr[row], b1 = ptr[row + 1];
+  for (int base = b0; base < b1; base += kWave) {
+    const int cnt = min(kWave, b1 - base);
+    float ux = 0.f, uy = 0.f, uz = 0.f, inv = 0.f;
+    int my_e = -1;
+    if (lane < cnt) {
+      const int k = base + lane;
+      my_e = perm ? perm[k] : k;
+      edge_unit(vec, my_e, pos, cl, src, shift, (int)row, sign, ux, uy, uz, inv);
+      float Y[L];
+      sh_eval<LMAX, float>(ux, uy, uz, Y);
+#pragma unroll
+      for (int m = 0; m < L; ++m) sY[wave][lane][m] = Y[m];
+    }
+    wave_sync();
+    for (int j = 0; j < cnt; ++j) {
+      const int e = perm ? perm[base + j] : base + j;
+      float p[CPL];
+#pragma unroll
+      for (int q = 0; q < CPL; ++q) p[q] = (own && c0 + q < C) ? phi[(int64_t)e * C + c0 + q] : 0.f;
+      float part[LP];
+#pragma unroll
+      for (int m = 0; m < LP; ++m) part[m] = 0.f;
+      float dp[CPL];
+#pragma unroll
+      for (int q = 0; q < CPL; ++q) dp[q] = 0.f;
+#pragma unroll
+      for (int m = 0; m < L; ++m) {
+        const float y = sY[wave][j][m];
+#pragma unroll
+        for (int q = 0; q < CPL; ++q) {
+          dp[q] += g[q][m] * y;
+          part[m] += g[q][m] * p[q];
+        }
+      }
+      if (own) {
+#pragma unroll
+        for (int q = 0; q < CPL; ++q)
+          if (c0 + q < C) d_phi[(int64_t)e * C + c0 + q] = dp[q];
+      }
+      if (g_vec) {
+        const float tot = wave_transpose_reduce<LP, D::HALVINGS>(part, lane);
+        if ((lane & ((1 << SHIFT) - 1)) == 0) sdY[wave][j][lane >> SHIFT] = tot;
+      }
+    }
+    wave_sync();
+    if (g_vec && lane < cnt) {
+      float dY[L];
+#pragma unroll
+      for (int m = 0; m < L; ++m) dY[m] = sdY[wave][lane][m];
+      float Gx, Gy, Gz, vx, vy, vz;
+      sh_grad<LMAX, float>(ux, uy, uz, dY, Gx, Gy, Gz);
+      sh_chain<float>(ux, uy, uz, inv, Gx, Gy, Gz, vx, vy, vz);
+      g_vec[3 * (int64_t)my_e + 0] = sign * vx;
+      g_vec[3 * (int64_t)my_e + 1] = sign * vy;
+      g_vec[3 * (int64_t)my_e + 2] = sign * vz;
+    }
+    wave_sync();
+  }
+}
+
+// ---------------------------------------------------------------- generic segment ops
+template <typename T, int GROUP>
+__global__ __launch_bounds__(256) void segment_sum_kernel(const T* __restrict__ src, int64_t F,
+                                                          const int32_t* __restrict__ ptr,
+                                                          const int32_t* __restrict__ perm,
+                                                          int64_t n_seg, T* __restrict__ out) {
+  const int lane = threadIdx.x % GROUP;
+  const int64_t row = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) / GROUP;
+  if (row >= n_seg) return;
+  const int b0 = ptr[row], b1 = ptr[row + 1];
+  for (int64_t f = lane; f < F; f += GROUP) {
+    T acc = T(0);
+    for (int k = b0; k < b1; ++k) {
+      const int64_t e = perm ? perm[k] : k;
+      acc += src[e * F + f];
+    }
+    out[row * F + f] = acc;
+  }
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void gather_rows_kernel(const T* __restrict__ src, int64_t F,
+                                                          const int32_t* __restrict__ index,
+                                                          int64_t n_rows, T* __restrict__ out) {
+  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= n_rows * F) return;
+  const int64_t e = t / F, f = t - e * F;
+  out[t] = src[(int64_t)index[e] * F + f];
+}
+
+// one block per segment; features in chunks of 8 held in registers
+template <typename T>
+__global__ __launch_bounds__(256) void segment_reduce_f64_kernel(const T* __restrict__ src,
+                                                                 int64_t F,
+                                                                 const int64_t* __restrict__ seg,
+                                                                 double* __restrict__ out) {
+  __shared__ double red[256][8];
+  const int64_t b = blockIdx.x;
+  const int64_t i0 = seg[b], i1 = seg[b + 1];
+  for (int64_t f0 = 0; f0 < F; f0 += 8) {
+    const int nf = (int)min<int64_t>(8, F - f0);
+    double acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    for (int64_t i = i0 + threadIdx.x; i < i1; i += blockDim.x) {
+#pragma unroll
+      for (int q = 0; q < 8; ++q)
+        if (q < nf) acc[q] += (double)src[i * F + f0 + q];
+    }
+#pragma unroll
+    for (int q = 0; q < 8; ++q) red[threadIdx.x][q] = acc[q];
+    __syncthreads();
+    for (int s = 128; s > 0; s >>= 1) {
+      if ((int)threadIdx.x < s) {
+#pragma unroll
+        for (int q = 0; q < 8; ++q) red[threadIdx.x][q] += red[threadIdx.x + s][q];
+      }
+      __syncthreads();
+    }
+    if (threadIdx.x < (unsigned)nf) out[b * F + f0 + threadIdx.x] = red[0][threadIdx.x];
+    __syncthreads();
+  }
+}
+
+template <typename G>
+static int sh_msg(bool backward, const float* vec, const void* pos, int64_t n_nodes, const void* cell,
+                  int64_t n_graphs, const int32_t* batch, const int32_t* src,
+                  const int32_t* shift, const int32_t* ptr, const int32_t* perm, int l_max,
+                  int sign, int C, const float* phi, const float* d_out, float* out_or_dphi,
+                  float* g_vec, hipStream_t stream) {
+  if (n_nodes == 0) return XNN_OK;
+  const dim3 grid(grid_1d(n_nodes, kWavesPerBlock)), block(kWavesPerBlock * kWave);
+  const float sg = (float)sign;
+  const int cpl = (C + kWave - 1) / kWave;
+#define XNN_MSG(LM, CP)                                                                       \
+  do {                                                                                        \
+    if (backward)                                                                             \
+      hipLaunchKernelGGL((sh_msg_bwd_kernel<G, LM, CP>), grid, block, 0, stream, vec, (const G*)pos, \
+                         (const G*)cell, n_graphs, batch, src, shift, ptr, perm, n_nodes, C,  \
+                         sg, phi, d_out, out_or_dphi, g_vec);                                 \
+    else                                                                                      \
+      hipLaunchKernelGGL((sh_msg_fwd_kernel<G, LM, CP>), grid, block, 0, stream, vec, (const G*)pos, \
+                         (const G*)cell, n_graphs, batch, src, shift, ptr, perm, n_nodes, C,  \
+                         sg, phi, out_or_dphi);                                               \
+  } while (0)
+#define XNN_MSG_L(CP)                    \
+  switch (l_max) {                       \
+    case 0: XNN_MSG(0, CP); break;       \
+    case 1: XNN_MSG(1, CP); break;       \
+    case 2: XNN_MSG(2, CP); break;       \
+    default: XNN_MSG(3, CP); break;      \
+  }
+  switch (cpl) {
+    case 1: XNN_MSG_L(1); break;
+    case 2: XNN_MSG_L(2); break;
+    case 3:
+    case 4: XNN_MSG_L(4); break;
+    default: set_error("n_channels must be <= 256, got %d", C); return XNN_EINVAL;
+  }
+#undef XNN_MSG_L
+#undef XNN_MSG
+  XNN_LAUNCH_CHECK();
+  return XNN_OK;
+}
+
+template <typename T>
+static int segment_sum_t(const void* src, int64_t F, const int32_t* ptr, const int32_t* perm,
+                         int64_t n_seg, void* out, hipStream_t stream) {
+  if (n_seg == 0 || F == 0) return XNN_OK;
+  int group = 1;
+  while (group < F && group < kWave) group <<= 1;
+  const int64_t threads = n_seg * group;
+  const dim3 grid(grid_1d(threads, 256)), block(256);
+  switch (group) {
+#define XNN_SEG(GR)                                                                         \
+  case GR:                                                                                  \
+    hipLaunchKernelGGL((segment_sum_kernel<T, GR>), grid, block, 0, stream, (const T*)src, F, \
+                       ptr, perm, n_seg, (T*)out);                                          \
+    break;
+    XNN_SEG(1) XNN_SEG(2) XNN_SEG(4) XNN_SEG(8) XNN_SEG(16) XNN_SEG(32) XNN_SEG(64)
+#undef XNN_SEG
+  }
+  XNN_LAUNCH_CHECK();
+  return XNN_OK;
+}
+
+}  // namespace xnn
+
+using namespace xnn;
+
+extern "C" {
+
+int xnn_sh_message_sum(int geom_dtype, const float* vec_in, const void* pos, int64_t n_nodes,
+                       const void* cell,
+                       int64_t n_graphs, const int32_t* batch, const int32_t* src,
+                       const int32_t* shift, int64_t n_edges, const int32_t* ptr_dst,
+                       const int32_t* perm_dst, int32_t l_max, int32_t sh_sign,
+                       int32_t n_channels, const float* phi, float* out, xnn_stream_t stream) {
+  XNN_REQUIRE(n_nodes >= 0 && n_edges >= 0, "negative size");
+  XNN_REQUIRE(l_max >= 0 && l_max <= 3, "l_max must be in [0, 3]");
+  XNN_REQUIRE(sh_sign == 1 || sh_sign == -1, "sh_sign must be +1 or -1");
+  XNN_REQUIRE(n_channels >= 1 && n_channels <= 256, "n_channels must be in [1, 256]");
+  XNN_REQUIRE(n_nodes == 0 || (ptr_dst && out), "NULL CSR or output");
+  XNN_REQUIRE(n_edges == 0 || ((vec_in || (pos && src && shift)) && phi), "NULL edge input");
+  XNN_REQUIRE(cell == nullptr || n_graphs <= 1 || batch != nullptr,
+              "several cells need the batch vector");
+  if (geom_dtype == XNN_F32)
+    return sh_msg<float>(false, vec_in, pos, n_nodes, cell, n_graphs, batch, src, shift, ptr_dst,
+                         perm_dst, l_max, sh_sign, n_channels, phi, nullptr, out, nullptr,
+                         as_hip(stream));
+  if (geom_dtype == XNN_F64)
+    return sh_msg<double>(false, vec_in, pos, n_nodes, cell, n_graphs, batch, src, shift, ptr_dst,
+                          perm_dst, l_max, sh_sign, n_channels, phi, nullptr, out, nullptr,
+                          as_hip(stream));
+  set_error("unsupported geometry dtype %d", geom_dtype);
+  return XNN_EINVAL;
+}
+
+int xnn_sh_message_sum_backward(int geom_dtype, const float* vec_in, const void* pos,
+                                int64_t n_nodes, const void* cell, int64_t n_graphs, const int32_t* batch,
+                                const int32_t* src, const int32_t* shift, int64_t n_edges,
+                                const int32_t* ptr_dst, const int32_t* perm_dst, int32_t l_max,
+                                int32_t sh_sign, int32_t n_channels, const float* phi,
+                                const float* d_out, float* d_phi, float* g_vec,
+                                xnn_stream_t stream) {
+  XNN_REQUIRE(n_nodes >= 0 && n_edges >= 0, "negative size");
+  XNN_REQUIRE(l_max >= 0 && l_max <= 3, "l_max must be in [0, 3]");
+  XNN_REQUIRE(sh_sign == 1 || sh_sign == -1, "sh_sign must be +1 or -1");
+  XNN_REQUIRE(n_channels >= 1 && n_channels <= 256, "n_channels must be in [1, 256]");
+  XNN_REQUIRE(n_nodes == 0 || (ptr_dst && d_out), "NULL CSR or d_out");
+  XNN_REQUIRE(n_edges == 0 || ((vec_in || (pos && src && shift)) && phi && d_phi),
+              "NULL edge input");
+  XNN_REQUIRE(cell == nullptr || n_graphs <= 1 || batch != nullptr,
+              "several cells need the batch vector");
+  if (geom_dtype == XNN_F32)
+    return sh_msg<float>(true, vec_in, pos, n_nodes, cell, n_graphs, batch, src, shift, ptr_dst,
+                         perm_dst, l_max, sh_sign, n_channels, phi, d_out, d_phi, g_vec,
+                         as_hip(stream));
+  if (geom_dtype == XNN_F64)
+    return sh_msg<double>(true, vec_in, pos, n_nodes, cell, n_graphs, batch, src, shift, ptr_dst,
+                          perm_dst, l_max, sh_sign, n_channels, phi, d_out, d_phi, g_vec,
+                          as_hip(stream));
+  set_error("unsupported geometry dtype %d", geom_dtype);
+  return XNN_EINVAL;
+}
+
+int xnn_segment_sum(int dtype, const void* src, int64_t n_rows, int64_t n_features,
+                    const int32_t* ptr, const int32_t* perm, int64_t n_segments, void* out,
+                    xnn_stream_t stream) {
+  XNN_REQUIRE(n_rows >= 0 && n_features >= 0 && n_segments >= 0, "negative size");
+  XNN_REQUIRE(n_segments == 0 || (ptr && out), "NULL CSR or output");
+  XNN_REQUIRE(n_rows == 0 || src, "NULL src");
+  if (dtype == XNN_F32)
+    return segment_sum_t<float>(src, n_features, ptr, perm, n_segments, out, as_hip(stream));
+  if (dtype == XNN_F64)
+    return segment_sum_t<double>(src, n_features, ptr, perm, n_segments, out, as_hip(stream));
+  set_error("unsupported dtype %d", dtype);
+  return XNN_EINVAL;
+}
+
+int xnn_gather_rows(int dtype, const void* src, int64_t n_src_rows, int64_t n_features,
+                    const int32_t* index, int64_t n_rows, void* out, xnn_stream_t stream) {
+  XNN_REQUIRE(n_rows >= 0 && n_features >= 0 && n_src_rows >= 0, "negative size");
+  if (n_rows == 0 || n_features == 0) return XNN_OK;
+  XNN_REQUIRE(src && index && out, "NULL pointer");
+  const int64_t total = n_rows * n_features;
+  const dim3 grid(grid_1d(total, 256)), block(256);
+  if (dtype == XNN_F32)
+    hipLaunchKernelGGL((gather_rows_kernel<float>), grid, block, 0, as_hip(stream),
+                       (const float*)src, n_features, index, n_rows, (float*)out);
+  else if (dtype == XNN_F64)
+    hipLaunchKernelGGL((gather_rows_kernel<double>), grid, block, 0, as_hip(stream),
+                       (const double*)src, n_features, index, n_rows, (double*)out);
+  else {
+    set_error("unsupported dtype %d", dtype);
+    return XNN_EINVAL;
+  }
+  XNN_LAUNCH_CHECK();
+  return XNN_OK;
+}
+
+int xnn_segment_reduce_f64(int dtype, const void* src, int64_t n_rows, int64_t n_features,
+                           const int64_t* seg_ptr, int64_t n_segments, double* out,
+                           xnn_stream_t stream) {
+  XNN_REQUIRE(n_rows >= 0 && n_features >= 0 && n_segments >= 0, "negative size");
+  if (n_segments == 0 || n_features == 0) return XNN_OK;
+  XNN_REQUIRE(seg_ptr && out && (n_rows == 0 || src), "NULL pointer");
+  if (dtype == XNN_F32)
+    hipLaunchKernelGGL((segment_reduce_f64_kernel<float>), dim3(n_segments), dim3(256), 0,
+                       as_hip(stream), (const float*)src, n_features, seg_ptr, out);
+  else if (dtype == XNN_F64)
+    hipLaunchKernelGGL((segment_reduce_f64_kernel<double>), dim3(n_segments), dim3(256), 0,
+                       as_hip(stream), (const double*)src, n_features, seg_ptr, out);
+  else {
+    set_error("unsupported dtype %d", dtype);
+    return XNN_EINVAL;
+  }
+  XNN_LAUNCH_CHECK();
+  return XNN_OK;
+}
+
+}  // extern "C"

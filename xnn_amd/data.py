@@ -1,0 +1,329 @@
+"""Atomic graphs and neighbor lists, the xnn data contract on MI355X.
+
+* :class:`AtomicGraph` -- the one data object (common/data/atomic_data.py:28-261):
+  positions, atomic numbers, ``edge_index = [src, dst]``, integer ``cell_shifts``,
+  ``batch``/``n_atoms``, optional ``cell``/``pbc``; :meth:`AtomicGraph.edge_vectors`
+  gives ``pos[dst] - pos[src] + cell_shift @ cell`` (atomic_data.py:371-418).
+* :func:`build_neighbor_list` -- the radius graph (common/data/neighborlist.py:411-506):
+  on a GPU the HIP cell list, with the reference's edge set and conventions
+  (``dst`` = receiver, negated and unwrapped shifts); edges come grouped by receiver.
+* :func:`structure_to_graph` / :func:`collate` (common/data/dataset.py:21-175, 371-577).
+
+GPU tensors always take the HIP kernels (and raise when the library is missing).
+CPU tensors take the reference formulation in PyTorch, as the reference does on a CPU.
+"""
+from __future__ import annotations
+
+import ctypes
+import itertools
+import math
+from dataclasses import dataclass, fields
+from typing import Optional, Sequence
+
+import numpy as np
+import torch
+from torch import Tensor
+
+from . import _lib
+
+
+@dataclass
+class AtomicGraph:
+    """Graph of one or a batch of atomic systems (atomic_data.py:28-261).
+
+    ``edge_index`` is ``(2, E)`` ``[src, dst]``: the energy of ``dst`` depends on
+    ``src``. ``cell`` is ``(B, 3, 3)`` (rows are lattice vectors) or ``None`` for
+    molecules; a molecule in a mixed batch has a zero cell.
+    """
+
+    pos: Tensor
+    atomic_numbers: Tensor
+    edge_index: Tensor
+    cell_shifts: Tensor
+    batch: Tensor
+    n_atoms: Tensor
+    cell: Optional[Tensor] = None
+    pbc: Optional[Tensor] = None
+    energy: Optional[Tensor] = None
+    forces: Optional[Tensor] = None
+    stress: Optional[Tensor] = None
+    total_charge: Optional[Tensor] = None
+    compute_dtype: Optional[torch.dtype] = None
+
+    @property
+    def model_dtype(self) -> torch.dtype:
+        return self.compute_dtype if self.compute_dtype is not None else self.pos.dtype
+
+    @property
+    def num_graphs(self) -> int:
+        return int(self.n_atoms.shape[0])
+
+    @property
+    def num_nodes(self) -> int:
+        return int(self.pos.shape[0])
+
+    @property
+    def num_edges(self) -> int:
+        return int(self.edge_index.shape[1])
+
+    def to(self, device) -> "AtomicGraph":
+        kwargs = {}
+        for f in fields(self):
+            v = getattr(self, f.name)
+            kwargs[f.name] = v.to(device) if isinstance(v, Tensor) else v
+        return AtomicGraph(**kwargs)
+
+    def plan(self):
+        """The cached :class:`~xnn_amd.plan.EdgePlan` of this graph (GPU only)."""
+        from .plan import plan_for
+        return plan_for(self)
+
+    def edge_vectors(self) -> Tensor:
+        """``pos[dst] - pos[src] + cell_shift @ cell`` per edge, in :attr:`model_dtype`,
+        differentiable with respect to ``pos`` and ``cell`` (atomic_data.py:371-418)."""
+        if self.pos.is_cuda:
+            from .ops import edge_vectors
+            return edge_vectors(self.pos, self.cell, self.plan(), self.model_dtype)
+        src, dst = self.edge_index[0], self.edge_index[1]
+        vec = self.pos.index_select(0, dst) - self.pos.index_select(0, src)
+        if self.cell is not None:
+            if self.cell.shape[0] == 1:
+                vec = vec + self.cell_shifts.to(vec.dtype) @ self.cell[0].to(vec.dtype)
+            else:
+                cell_per_edge = self.cell.index_select(0, self.batch.index_select(0, src))
+                vec = vec + torch.einsum("ei,eij->ej", self.cell_shifts.to(vec.dtype),
+                                         cell_per_edge.to(vec.dtype))
+        return vec.to(self.model_dtype)
+
+
+# --------------------------------------------------------------------------- neighbor lists
+def _n_repeats(cell: Tensor, cutoff: float, pbc: Tensor) -> list[int]:
+    """Image repeats per axis from the interplanar spacing (neighborlist.py:74-104)."""
+    recip = torch.linalg.inv(cell).T
+    spacing = 1.0 / torch.linalg.norm(recip, dim=1)
+    return [int(math.ceil(cutoff / float(spacing[i]))) if bool(pbc[i]) else 0 for i in range(3)]
+
+
+def _brute_force_cpu(pos: Tensor, cutoff: float, cell: Optional[Tensor], pbc: Optional[Tensor],
+                     self_interaction: bool) -> tuple[Tensor, Tensor]:
+    """The reference's brute force (neighborlist.py:462-506), chunked by receivers so
+    that no (S, N, N, 3) tensor is formed; same edges, order (s, i, j)."""
+    dtype, n = pos.dtype, pos.shape[0]
+    offsets = None
+    if cell is None or pbc is None or not bool(pbc.any()):
+        shifts = torch.zeros((1, 3), dtype=dtype)
+        shift_idx = torch.zeros((1, 3), dtype=torch.long)
+    else:
+        frac = pos @ torch.linalg.inv(cell)
+        offsets = torch.floor(frac).to(torch.long)
+        offsets[:, ~pbc.to(torch.bool)] = 0
+        pos = pos - offsets.to(dtype) @ cell
+        reps = _n_repeats(cell, cutoff, pbc)
+        combos = list(itertools.product(*[range(-r, r + 1) for r in reps]))
+        shift_idx = torch.tensor(combos, dtype=torch.long)
+        shifts = shift_idx.to(dtype) @ cell
+    zero_shift = (shift_idx == 0).all(dim=1)
+    parts = []
+    chunk = max(1, (1 << 24) // max(1, n * shifts.shape[0]))
+    for i0 in range(0, n, chunk):
+        i1 = min(n, i0 + chunk)
+        rij = (pos[None, None, :, :] - pos[None, i0:i1, None, :]) + shifts[:, None, None, :]
+        within = torch.linalg.norm(rij, dim=-1) < cutoff
+        if not self_interaction:
+            eye = torch.zeros((i1 - i0, n), dtype=torch.bool)
+            eye[torch.arange(i1 - i0), torch.arange(i0, i1)] = True
+            within = within & ~(eye[None] & zero_shift[:, None, None])
+        s, i, j = torch.nonzero(within, as_tuple=True)
+        parts.append((s, i + i0, j))
+    s = torch.cat([p[0] for p in parts])
+    i = torch.cat([p[1] for p in parts])
+    j = torch.cat([p[2] for p in parts])
+    order = torch.argsort(s * n + i, stable=True)          # the nonzero order (s, i, j)
+    s, i, j = s[order], i[order], j[order]
+    edge_index = torch.stack([j, i], dim=0)
+    cell_shifts = -shift_idx[s]
+    if offsets is not None:
+        cell_shifts = cell_shifts + offsets[j] - offsets[i]
+    return edge_index, cell_shifts
+
+
+def _check_finite(lo_hi: list) -> None:
+    if not all(math.isfinite(v) for v in lo_hi):
+        raise ValueError("the positions are not finite (an unstable simulation?)")
+
+
+def _radius_graph_cuda(pos: Tensor, cutoff: float, cell: Optional[Tensor], pbc: Optional[Tensor],
+                       self_interaction: bool) -> tuple[Tensor, Tensor]:
+    lib = _lib.load()
+    dev = pos.device
+    pos = pos.contiguous()
+    n = pos.shape[0]
+    molecular = cell is None or pbc is None or not bool(pbc.any())
+    plan = _lib.GridPlan()
+    pbc_host = (ctypes.c_int32 * 3)(*([0, 0, 0] if molecular else [int(bool(b)) for b in pbc.reshape(-1).tolist()]))
+    if n == 0:
+        return (torch.zeros((2, 0), dtype=torch.long, device=dev),
+                torch.zeros((0, 3), dtype=torch.long, device=dev))
+    if molecular:
+        lo_hi = torch.stack([pos.detach().amin(0), pos.detach().amax(0)]).double().flatten().tolist()
+        _check_finite(lo_hi)
+        cell_host, cell_dev = None, None
+    else:
+        cell_dev = cell.reshape(3, 3).to(device=dev, dtype=pos.dtype).contiguous()
+        cell64 = cell.reshape(3, 3).detach().double().cpu()
+        frac = pos.detach().double() @ torch.linalg.inv(cell64).to(dev)
+        lo_hi = torch.stack([frac.amin(0), frac.amax(0)]).flatten().tolist()
+        _check_finite(lo_hi)
+        cell_host = (_lib.dbl * 9)(*cell64.flatten().tolist())
+    lo = (_lib.dbl * 3)(*lo_hi[:3])
+    hi = (_lib.dbl * 3)(*lo_hi[3:])
+    _lib.check("xnn_radius_graph_plan",
+               lib.xnn_radius_graph_plan(n, cell_host, pbc_host, float(cutoff), lo, hi,
+                                         ctypes.byref(plan)))
+    ws = torch.empty(max(1, int(plan.workspace_bytes)), dtype=torch.uint8, device=dev)
+    row_ptr = torch.empty(n + 1, dtype=torch.int32, device=dev)
+    geom = _lib.dtype_code(pos.dtype)
+    s = _lib.stream(dev)
+    _lib.call("xnn_radius_graph_count", geom, _lib.ptr(pos), n, _lib.ptr(cell_dev), float(cutoff),
+              int(bool(self_interaction)), ctypes.byref(plan), _lib.ptr(ws), _lib.ptr(row_ptr), s)
+    n_edges = int(row_ptr[-1])
+    edge_index = torch.empty((2, n_edges), dtype=torch.long, device=dev)
+    cell_shifts = torch.empty((n_edges, 3), dtype=torch.long, device=dev)
+    src = torch.empty(n_edges, dtype=torch.int32, device=dev)
+    dst = torch.empty(n_edges, dtype=torch.int32, device=dev)
+    shift = torch.empty(n_edges, dtype=torch.int32, device=dev)
+    _lib.call("xnn_radius_graph_fill", geom, _lib.ptr(pos), n, _lib.ptr(cell_dev), float(cutoff),
+              int(bool(self_interaction)), ctypes.byref(plan), _lib.ptr(ws), _lib.ptr(row_ptr),
+              n_edges, _lib.ptr(src), _lib.ptr(dst), _lib.ptr(shift), _lib.ptr(edge_index),
+              _lib.ptr(cell_shifts), None, s)
+    return edge_index, cell_shifts
+
+
+def build_neighbor_list(pos: Tensor, cutoff: float, cell: Optional[Tensor] = None,
+                        pbc: Optional[Tensor] = None,
+                        self_interaction: bool = False) -> tuple[Tensor, Tensor]:
+    """Radius graph of one structure: ``(edge_index (2, E) [src, dst], cell_shifts (E, 3))``.
+
+    Same edge set and conventions as the reference (neighborlist.py:411-506): pairs with
+    ``dist < cutoff`` in the positions' dtype, ``dst`` = receiver, shifts negated and
+    re-expressed for unwrapped positions, self-edges only with ``self_interaction``.
+    On a GPU the edges come grouped by receiver (the order the kernels walk).
+    """
+    if pos.is_cuda:
+        return _radius_graph_cuda(pos, cutoff, cell, pbc, self_interaction)
+    return _brute_force_cpu(pos, cutoff, cell, pbc, self_interaction)
+
+
+def batched_neighbor_list(pos: Tensor, n_atoms: Tensor, cutoff: float,
+                          self_interaction: bool = False) -> tuple[Tensor, Tensor]:
+    """Radius graph of a batch of molecules (no cell) in one pass on the GPU:
+    the edges every structure's own :func:`build_neighbor_list` gives, offset by its
+    first atom, grouped by receiver (what :func:`collate` of the single graphs holds,
+    up to the edge order)."""
+    if not pos.is_cuda:
+        raise RuntimeError("batched_neighbor_list runs on the GPU")
+    dev = pos.device
+    pos = pos.contiguous()
+    n = pos.shape[0]
+    n_atoms = n_atoms.to(device=dev, dtype=torch.long)
+    if n == 0:
+        return (torch.zeros((2, 0), dtype=torch.long, device=dev),
+                torch.zeros((0, 3), dtype=torch.long, device=dev))
+    node_ptr = torch.zeros(n_atoms.shape[0] + 1, dtype=torch.long, device=dev)
+    node_ptr[1:] = torch.cumsum(n_atoms, 0)
+    batch32 = torch.repeat_interleave(torch.arange(n_atoms.shape[0], device=dev, dtype=torch.int32),
+                                      n_atoms)
+    lo_hi = torch.stack([pos.detach().amin(0), pos.detach().amax(0)]).double().flatten().tolist()
+    _check_finite(lo_hi)
+    if int(n_atoms.max()) > 1024:
+        raise ValueError("batched_neighbor_list takes molecules of at most 1024 atoms; list "
+                         "larger structures one by one with build_neighbor_list")
+    geom = _lib.dtype_code(pos.dtype)
+    s = _lib.stream(dev)
+    row_ptr = torch.empty(n + 1, dtype=torch.int32, device=dev)
+    _lib.call("xnn_radius_graph_molecules_count", geom, _lib.ptr(pos), n, _lib.ptr(node_ptr),
+              _lib.ptr(batch32), n_atoms.shape[0], float(cutoff), int(bool(self_interaction)),
+              _lib.ptr(row_ptr), s)
+    ws = torch.empty(int(_lib.load().xnn_scan_workspace_bytes(n)), dtype=torch.uint8, device=dev)
+    _lib.call("xnn_scan_counts", _lib.ptr(row_ptr), n, _lib.ptr(ws), s)
+    n_edges = int(row_ptr[-1])
+    edge_index = torch.empty((2, n_edges), dtype=torch.long, device=dev)
+    cell_shifts = torch.empty((n_edges, 3), dtype=torch.long, device=dev)
+    src = torch.empty(n_edges, dtype=torch.int32, device=dev)
+    dst = torch.empty(n_edges, dtype=torch.int32, device=dev)
+    shift = torch.empty(n_edges, dtype=torch.int32, device=dev)
+    _lib.call("xnn_radius_graph_molecules_fill", geom, _lib.ptr(pos), n, _lib.ptr(node_ptr),
+              _lib.ptr(batch32), n_atoms.shape[0], float(cutoff), int(bool(self_interaction)),
+              _lib.ptr(row_ptr), n_edges, _lib.ptr(src), _lib.ptr(dst), _lib.ptr(shift),
+              _lib.ptr(edge_index), _lib.ptr(cell_shifts), s)
+    return edge_index, cell_shifts
+
+
+# --------------------------------------------------------------------------- graphs
+def structure_to_graph(s: dict, cutoff: float, device=None) -> AtomicGraph:
+    """One structure (dict of arrays) to a graph (dataset.py:21-175): ``pos``,
+    ``atomic_numbers`` and optional ``cell``/``pbc`` (a cell without pbc is periodic on
+    every axis), ``energy``, ``forces``, ``stress``, ``total_charge``."""
+    def t(x, dtype=torch.get_default_dtype()):
+        out = x if isinstance(x, Tensor) else torch.as_tensor(np.asarray(x), dtype=dtype)
+        return out if device is None else out.to(device)
+
+    pos = t(s["pos"])
+    z = t(s["atomic_numbers"], dtype=torch.long)
+    cell = t(s["cell"]).reshape(3, 3) if s.get("cell") is not None else None
+    pbc = (torch.as_tensor(s["pbc"], dtype=torch.bool) if s.get("pbc") is not None
+           else (torch.ones(3, dtype=torch.bool) if cell is not None else None))
+    edge_index, cell_shifts = build_neighbor_list(pos, cutoff, cell, pbc)
+    n = pos.shape[0]
+    dev = pos.device
+    charge = s.get("total_charge", s.get("charge"))
+    return AtomicGraph(
+        pos=pos, atomic_numbers=z, edge_index=edge_index, cell_shifts=cell_shifts,
+        batch=torch.zeros(n, dtype=torch.long, device=dev),
+        n_atoms=torch.tensor([n], dtype=torch.long, device=dev),
+        cell=cell[None] if cell is not None else None,
+        pbc=pbc.to(dev)[None] if pbc is not None else None,
+        energy=(torch.as_tensor(s["energy"], dtype=torch.float64).reshape(1).to(dev)
+                if s.get("energy") is not None else None),
+        forces=t(s["forces"]) if s.get("forces") is not None else None,
+        stress=t(s["stress"]).reshape(1, 3, 3) if s.get("stress") is not None else None,
+        total_charge=(t([charge]).reshape(1) if charge is not None else None),
+    )
+
+
+def collate(graphs: Sequence[AtomicGraph]) -> AtomicGraph:
+    """Concatenate graphs into one batch (dataset.py:371-577): edge indices offset by
+    the running atom count, a ``batch`` vector, zero cells for molecules when any
+    structure has a cell."""
+    dtype, device = graphs[0].pos.dtype, graphs[0].pos.device
+    has_cell = any(g.cell is not None for g in graphs)
+    has_q = any(g.total_charge is not None for g in graphs)
+    pos, z, batch, n_atoms, ei, cs, cells, pbcs, qs = [], [], [], [], [], [], [], [], []
+    node_offset = graph_offset = 0
+    for g in graphs:
+        b = g.num_graphs
+        pos.append(g.pos)
+        z.append(g.atomic_numbers)
+        batch.append(g.batch + graph_offset)
+        n_atoms.append(g.n_atoms)
+        ei.append(g.edge_index + node_offset)
+        cs.append(g.cell_shifts)
+        node_offset += g.num_nodes
+        graph_offset += b
+        if has_cell:
+            if g.cell is not None:
+                cells.append(g.cell)
+                pbcs.append(g.pbc.to(device) if g.pbc is not None
+                            else torch.ones((b, 3), dtype=torch.bool, device=device))
+            else:
+                cells.append(torch.zeros((b, 3, 3), dtype=dtype, device=device))
+                pbcs.append(torch.zeros((b, 3), dtype=torch.bool, device=device))
+        if has_q:
+            qs.append(g.total_charge if g.total_charge is not None
+                      else torch.zeros(b, dtype=dtype, device=device))
+    return AtomicGraph(
+        pos=torch.cat(pos, 0), atomic_numbers=torch.cat(z, 0), edge_index=torch.cat(ei, 1),
+        cell_shifts=torch.cat(cs, 0), batch=torch.cat(batch, 0), n_atoms=torch.cat(n_atoms, 0),
+        cell=torch.cat(cells, 0) if has_cell else None,
+        pbc=torch.cat(pbcs, 0) if has_cell else None,
+        total_charge=torch.cat(qs, 0) if has_q else None)

@@ -1,0 +1,192 @@
+"""Edge featurizers with the reference's parameters and a HIP evaluation.
+
+* :class:`BesselRBF`, :class:`GaussianRBF` -- common/featurizers/radial.py:15-75, 187-268
+* :class:`CosineCutoff`, :class:`PolynomialCutoff` -- common/featurizers/cutoff.py:10-125
+* :func:`spherical_harmonics` -- e3nn ``SphericalHarmonics(normalize=True,
+  normalization="component")`` for ``l <= 3`` (gnn/featurizers/spherical.py:91-93): real
+  harmonics without Condon-Shortley phase, ``sum_m Y_lm^2 = 2l + 1``, polar axis y
+  (``Y_1 = sqrt(3) (x, y, z)``), homogeneous polynomials of the unit vector.
+* :class:`SphericalHarmonicEdgeEmbedding` -- gnn/featurizers/spherical.py:28-171, whose
+  ``embed`` runs one fused HIP kernel when ``fast_active``.
+
+The modules hold exactly the reference's parameters and buffers, so a state dict
+moves between the two.
+"""
+from __future__ import annotations
+
+import math
+from typing import Tuple
+
+import torch
+from torch import Tensor, nn
+
+from .fast import FastPathModule
+
+
+class GaussianRBF(nn.Module):
+    """``exp(-gamma (r - mu_k)^2)`` on centers ``linspace(start, cutoff, n_rbf)`` (radial.py:15-75)."""
+
+    def __init__(self, n_rbf: int = 50, cutoff: float = 5.0, gamma: float | None = None,
+                 start: float = 0.0, endpoint: bool = True):
+        super().__init__()
+        centers = (torch.linspace(start, cutoff, n_rbf) if endpoint
+                   else torch.linspace(start, cutoff, n_rbf + 1)[:n_rbf])
+        self.register_buffer("centers", centers)
+        self.width = (centers[1] - centers[0]).item() if n_rbf > 1 else 1.0
+        self.gamma = float(gamma) if gamma is not None else 0.5 / self.width ** 2
+
+    def forward(self, r: Tensor) -> Tensor:
+        diff = r[..., None] - self.centers
+        return torch.exp(-self.gamma * diff ** 2)
+
+
+class BesselRBF(nn.Module):
+    """``prefactor sin(freq_n r / rc) / r``, ``freq_n = n pi`` (radial.py:187-268)."""
+
+    def __init__(self, n_rbf: int = 8, cutoff: float = 5.0, trainable: bool = False,
+                 prefactor: float | None = None):
+        super().__init__()
+        self.cutoff = cutoff
+        freqs = math.pi * torch.arange(1, n_rbf + 1, dtype=torch.get_default_dtype())
+        if trainable:
+            self.freqs = nn.Parameter(freqs)
+        else:
+            self.register_buffer("freqs", freqs)
+        self.norm = math.sqrt(2.0 / cutoff) if prefactor is None else float(prefactor)
+
+    def forward(self, r: Tensor) -> Tensor:
+        r = r.clamp(min=1e-8)[..., None]
+        return self.norm * torch.sin(self.freqs * r / self.cutoff) / r
+
+
+class CosineCutoff(nn.Module):
+    """``0.5 (cos(pi r / rc) + 1)`` inside the cutoff, 0 beyond (cutoff.py:10-41)."""
+
+    def __init__(self, cutoff: float):
+        super().__init__()
+        self.cutoff = cutoff
+
+    def forward(self, r: Tensor) -> Tensor:
+        out = 0.5 * (torch.cos(math.pi * r / self.cutoff) + 1.0)
+        return out * (r < self.cutoff)
+
+
+class PolynomialCutoff(nn.Module):
+    """``1 - (p+1)(p+2)/2 x^p + p(p+2) x^(p+1) - p(p+1)/2 x^(p+2)``, ``x = r / rc`` (cutoff.py:83-125)."""
+
+    def __init__(self, cutoff: float, p: int = 6):
+        super().__init__()
+        self.cutoff = cutoff
+        self.p = p
+
+    def forward(self, r: Tensor) -> Tensor:
+        x = r / self.cutoff
+        p = self.p
+        tail = ((-(p * (p + 1) / 2)) * x + p * (p + 2)) * x - (p + 1) * (p + 2) / 2
+        return (1.0 + tail * x ** p) * (r < self.cutoff)
+
+
+_S3, _S5, _S15 = math.sqrt(3.0), math.sqrt(5.0), math.sqrt(15.0)
+_A, _B, _C = math.sqrt(35.0 / 8.0), math.sqrt(105.0), math.sqrt(21.0 / 8.0)
+_D, _E = math.sqrt(7.0) / 2.0, math.sqrt(105.0) / 2.0
+
+
+def spherical_harmonics(l_max: int, vec: Tensor) -> Tensor:
+    """Component-normalized real SH of ``vec / |vec|`` in the e3nn order, ``(E, (l_max+1)^2)``.
+
+    They are ``sqrt(2l+1)`` times the orthonormal real harmonics (no Condon-Shortley
+    phase) in standard form with the polar axis on y: ``(x_s, y_s, z_s) = (z, x, y)``.
+    A zero vector gives ``Y_0 = 1`` and zeros (``normalize`` maps it to zero).
+    """
+    if not 0 <= l_max <= 3:
+        raise ValueError("l_max must be in [0, 3]")
+    n = torch.linalg.norm(vec, dim=-1, keepdim=True)
+    u = vec / n.clamp(min=1e-12)
+    x, y, z = u[..., 0], u[..., 1], u[..., 2]
+    out = [torch.ones_like(x)]
+    if l_max >= 1:
+        out += [_S3 * x, _S3 * y, _S3 * z]
+    if l_max >= 2:
+        x2, y2, z2 = x * x, y * y, z * z
+        out += [_S15 * x * z, _S15 * x * y, _S5 * (y2 - 0.5 * (x2 + z2)), _S15 * y * z,
+                0.5 * _S15 * (z2 - x2)]
+    if l_max >= 3:
+        x2, y2, z2 = x * x, y * y, z * z
+        out += [_A * x * (3.0 * z2 - x2), _B * x * y * z, _C * x * (4.0 * y2 - x2 - z2),
+                _D * y * (2.0 * y2 - 3.0 * x2 - 3.0 * z2), _C * z * (4.0 * y2 - x2 - z2),
+                _E * y * (z2 - x2), _A * z * (z2 - 3.0 * x2)]
+    return torch.stack(out, dim=-1)
+
+
+class SphericalHarmonicEdgeEmbedding(nn.Module, FastPathModule):
+    """Per-edge length, SH edge attributes and enveloped radial basis
+    (gnn/featurizers/spherical.py:28-171).
+
+    Same constructor as the reference, plus ``envelope`` (``"polynomial"``, the
+    reference's, or ``"cosine"``) and ``sh_sign`` (``-1`` evaluates ``Y(-vec)``, as
+    NequIP does with ``embed(-edge_vec)``, nequip.py:722).
+    """
+
+    def __init__(self, l_max: int = 2, n_rbf: int = 8, cutoff: float = 5.0, p: int = 6,
+                 radial_type: str = "bessel", trainable_rbf: bool = False,
+                 rbf_prefactor: float | None = None, envelope: str = "polynomial"):
+        super().__init__()
+        if not 0 <= l_max <= 3:
+            raise ValueError("l_max must be in [0, 3] (the HIP harmonics stop at l = 3)")
+        self.cutoff = cutoff
+        self.l_max = l_max
+        self.n_rbf = n_rbf
+        self.radial_type = radial_type
+        if radial_type == "bessel":
+            self.rbf = BesselRBF(n_rbf, cutoff, trainable=trainable_rbf, prefactor=rbf_prefactor)
+        elif radial_type == "gaussian":
+            self.rbf = GaussianRBF(n_rbf, cutoff)
+        else:
+            raise ValueError(f"unknown radial_type {radial_type!r}")
+        if envelope == "polynomial":
+            self.envelope = PolynomialCutoff(cutoff, p=p)
+        elif envelope == "cosine":
+            self.envelope = CosineCutoff(cutoff)
+        else:
+            raise ValueError(f"unknown envelope {envelope!r}")
+        self.envelope_type = envelope
+        self.fast_active = False
+
+    @property
+    def output_dim(self) -> int:
+        return self.n_rbf
+
+    def _table(self) -> Tensor:
+        return self.rbf.freqs if self.radial_type == "bessel" else self.rbf.centers
+
+    def _embed_fast(self, vec: Tensor, sh_sign: int, want_sh: bool = True):
+        from .ops import edge_embed
+        rbf = self.rbf
+        return edge_embed(
+            vec, self._table(), n_rbf=self.n_rbf, basis=self.radial_type,
+            envelope=self.envelope_type, poly_p=getattr(self.envelope, "p", 1), l_max=self.l_max,
+            cutoff=self.cutoff, prefactor=getattr(rbf, "norm", 1.0),
+            gamma=getattr(rbf, "gamma", 1.0), sh_sign=sh_sign, want_sh=want_sh)
+
+    def embed(self, vec: Tensor, sh_sign: int = 1) -> Tuple[Tensor, Tensor, Tensor]:
+        """``(edge_length (E,), edge_sh (E, (l_max+1)^2), edge_radial (E, n_rbf))``
+        of edge vectors (spherical.py:115-138); ``Y`` is taken of ``sh_sign * vec``."""
+        if self.fast_active:
+            return self._embed_fast(vec, sh_sign)
+        length = torch.linalg.norm(vec, dim=-1)
+        edge_sh = spherical_harmonics(self.l_max, vec if sh_sign == 1 else -vec)
+        radial = self.rbf(length) * self.envelope(length)[:, None]
+        return length, edge_sh, radial
+
+    def radial(self, vec: Tensor) -> Tensor:
+        """The enveloped radial basis alone (no harmonics are evaluated)."""
+        if self.fast_active:
+            return self._embed_fast(vec, 1, want_sh=False)[2]
+        length = torch.linalg.norm(vec, dim=-1)
+        return self.rbf(length) * self.envelope(length)[:, None]
+
+    def forward(self, data) -> dict:
+        vec = data.edge_vectors()
+        length, edge_sh, radial = self.embed(vec)
+        return {"edge_vec": vec, "edge_length": length, "edge_sh": edge_sh,
+                "edge_radial": radial}

@@ -1,0 +1,77 @@
+"""The reference's aggregation functions with the same signatures
+(common/models/ops.py:403-557, 754-764), deterministic on the GPU.
+
+On GPU tensors ``scatter_sum`` / ``gather_rows`` / ``structure_sum`` run the HIP
+segmented reductions over a CSR of ``index`` (built once per index tensor and
+cached by identity, like the reference's ``orderings``, csr.py:35-51); on CPU
+tensors they are the reference's ``index_add`` formulation.
+"""
+from __future__ import annotations
+
+from typing import Tuple
+
+import torch
+from torch import Tensor
+
+from . import _lib
+
+_last = [None]
+
+
+def csr_of(index: Tensor, n: int) -> Tuple[Tensor, Tensor, object]:
+    """``(index32, ptr (n+1), perm or None)`` of a 1-D index over ``n`` buckets."""
+    hit = _last[0]
+    if hit is not None and hit[0] is index and hit[1] == n:
+        return hit[2]
+    from .plan import build_plan
+    pair = torch.stack([index, index]).to(torch.int64)
+    plan = build_plan(pair, None, n)
+    out = (plan.dst, plan.ptr_dst, plan.perm_dst)
+    _last[0] = (index, n, out)
+    return out
+
+
+def scatter_sum(src: Tensor, index: Tensor, dim_size: int) -> Tensor:
+    """``out[index[e]] += src[e]`` over dim 0 (ops.py:403-448), without atomics on a GPU."""
+    if not src.is_cuda:
+        if dim_size == 1:
+            return src.sum(0, keepdim=True)
+        out = torch.zeros([dim_size] + list(src.shape[1:]), dtype=src.dtype, device=src.device)
+        return out.index_add_(0, index, src)
+    from .ops import segment_sum_op
+    index32, ptr, perm = csr_of(index, dim_size)
+    return segment_sum_op(src.contiguous(), index32, ptr, perm)
+
+
+def gather_rows(src: Tensor, index: Tensor) -> Tensor:
+    """``src[index]`` along dim 0 (ops.py:494-528); its adjoint is :func:`scatter_sum`."""
+    if not src.is_cuda:
+        return src.index_select(0, index)
+    from .ops import gather_rows_op
+    index32, ptr, perm = csr_of(index, src.shape[0])
+    return gather_rows_op(src.contiguous(), index32, ptr, perm)
+
+
+def structure_sum(src: Tensor, index: Tensor, dim_size: int) -> Tensor:
+    """Per-structure totals accumulated in float64 (ops.py:531-557). ``index`` must be
+    grouped by structure (as :func:`~xnn_amd.data.collate` builds it)."""
+    if not src.is_cuda:
+        if dim_size == 1:
+            return src.to(torch.float64).sum(0, keepdim=True)
+        out = torch.zeros(dim_size, dtype=torch.float64, device=src.device)
+        return out.index_add(0, index, src.to(torch.float64))
+    from .ops import structure_sum_op
+    counts = torch.bincount(index, minlength=dim_size)
+    node_ptr = torch.zeros(dim_size + 1, dtype=torch.int64, device=src.device)
+    node_ptr[1:] = torch.cumsum(counts, 0)
+    return structure_sum_op(src, node_ptr, index.to(torch.int32))
+
+
+def cell_volume(cell: Tensor) -> Tensor:
+    """Volume of row-vector cells ``(..., 3, 3)`` by the triple product (ops.py:754-764)."""
+    cross = torch.linalg.cross(cell[..., 1, :], cell[..., 2, :])
+    return (cell[..., 0, :] * cross).sum(-1).abs()
+
+
+__all__ = ["scatter_sum", "gather_rows", "structure_sum", "cell_volume", "csr_of"]
+_ = _lib

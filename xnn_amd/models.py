@@ -1,0 +1,131 @@
+"""The model contract and registry (common/models/base.py:24-180, registry.py:23-111),
+and :class:`ShEdgePotential`, the edge -> atom model the hot path is measured on.
+
+Every model maps an :class:`~xnn_amd.data.AtomicGraph` to
+``{"node_energy": (N,), "energy": (B,) float64}``; forces and stress come from
+:class:`~xnn_amd.outputs.ForceStressOutput`.
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass, field
+from typing import Callable, Dict, Optional, Sequence, Type
+
+import torch
+from torch import Tensor, nn
+
+from .fast import MI355X_POLICY, UseFast, fast_modules, resolve_use_fast, select
+from .featurizers import SphericalHarmonicEdgeEmbedding
+from .functional import scatter_sum, structure_sum
+
+_MODELS: Dict[str, Type] = {}
+
+
+def register_model(name: str) -> Callable[[Type], Type]:
+    """Class decorator registering a model under ``name`` (case-insensitive; registry.py:23-71)."""
+    def deco(cls: Type) -> Type:
+        key = name.lower()
+        if key in _MODELS and _MODELS[key] is not cls:
+            raise KeyError(f"model '{name}' already registered")
+        _MODELS[key] = cls
+        return cls
+    return deco
+
+
+def get_model_class(name: str) -> Type:
+    try:
+        return _MODELS[name.lower()]
+    except KeyError:
+        raise KeyError(f"unknown model {name!r}; registered: {sorted(_MODELS)}") from None
+
+
+@dataclass
+class ModelConfig:
+    """``name`` selects the registered class; ``params`` go to its constructor
+    (the shape of config/schema.py ModelConfig for this path)."""
+    name: str
+    params: dict = field(default_factory=dict)
+
+
+def build_model(cfg: ModelConfig) -> nn.Module:
+    """Instantiate a registered model from its config (registry.py:74-111)."""
+    return get_model_class(cfg.name).from_config(cfg)
+
+
+class InteratomicPotential(nn.Module):
+    """Base class: ``forward(AtomicGraph) -> {"node_energy", "energy"}`` (base.py:24-180)."""
+
+    head_modules = ()
+
+    def forward(self, data) -> dict:
+        raise NotImplementedError
+
+    @classmethod
+    def from_config(cls, cfg: ModelConfig) -> "InteratomicPotential":
+        return cls(**cfg.params)
+
+    def aggregate_energy(self, node_energy: Tensor, data) -> Tensor:
+        """Per-structure energies in float64 (base.py:161-180)."""
+        return structure_sum(node_energy, data.batch, data.num_graphs)
+
+
+@register_model("sh_edge")
+class ShEdgePotential(InteratomicPotential):
+    """One equivariant edge -> atom interaction, the measured hot path.
+
+    Per edge ``e = (src -> dst)`` with vector ``r_e``: radial features
+    ``u_e = rbf(|r_e|) * envelope(|r_e|)`` (K), channel weights ``phi_e = u_e W`` (C,
+    a PyTorch linear), and the message ``phi_e (x) Y(r_e)`` summed onto the receiver:
+    ``A_i = sum_{dst(e)=i} phi_e (x) Y(r_e)``, ``(N, C, (l_max+1)^2)``. This is the uvu
+    tensor product of scalar weights with the edge harmonics followed by
+    ``scatter_sum`` (gnn/fast/conv.py:137-143). The readout is
+    ``E_i = sum_{c,lm} U[c, lm] A_i[c, lm] + atom_ref[Z_i]`` and ``E = sum_i E_i`` in
+    float64. On a GPU the featurizer and the fused message sum are HIP kernels (the
+    message never exists in memory); ``use_fast=False`` or a CPU evaluates the same
+    function with the PyTorch formulation.
+    """
+
+    def __init__(self, species: Sequence[int] = (1, 6, 7, 8), n_rbf: int = 8, l_max: int = 3,
+                 channels: int = 128, cutoff: float = 5.0, radial_type: str = "bessel",
+                 envelope: str = "polynomial", p: int = 6, sh_sign: int = 1,
+                 use_fast: UseFast = "auto", seed: Optional[int] = 0):
+        super().__init__()
+        self.cutoff = float(cutoff)
+        self.l_max = int(l_max)
+        self.channels = int(channels)
+        self.sh_sign = int(sh_sign)
+        self.use_fast = resolve_use_fast(use_fast)
+        self.double_backward = False
+        self.edge_feat = SphericalHarmonicEdgeEmbedding(
+            l_max=l_max, n_rbf=n_rbf, cutoff=cutoff, p=p, radial_type=radial_type,
+            envelope=envelope)
+        gen = torch.Generator().manual_seed(seed) if seed is not None else None
+        L = (l_max + 1) ** 2
+        self.W = nn.Parameter(torch.randn(n_rbf, channels, generator=gen) / n_rbf ** 0.5)
+        self.U = nn.Parameter(torch.randn(channels, L, generator=gen) / (channels * L) ** 0.5)
+        z_max = max(species) + 1
+        self.register_buffer("species", torch.tensor(list(species), dtype=torch.long))
+        self.atom_ref = nn.Parameter(0.1 * torch.randn(z_max, generator=gen))
+
+    def messages(self, data, vec: Tensor) -> Tensor:
+        """``A (N, C, L)`` from edge vectors (HIP fused sum or PyTorch scatter)."""
+        feat = self.edge_feat
+        if feat.fast_active:
+            from .ops import sh_message_sum
+            u = feat.radial(vec)
+            phi = u @ self.W.to(u.dtype)
+            return sh_message_sum(vec, phi, data.plan(), self.l_max, self.sh_sign)
+        _, sh, u = feat.embed(vec, sh_sign=self.sh_sign)
+        phi = u @ self.W.to(u.dtype)
+        msg = (phi[:, :, None] * sh[:, None, :]).reshape(vec.shape[0], -1)
+        out = scatter_sum(msg, data.edge_index[1], data.num_nodes)
+        return out.reshape(data.num_nodes, self.channels, -1)
+
+    def forward(self, data) -> dict:
+        dtype = data.model_dtype
+        select(fast_modules(self), self.use_fast, MI355X_POLICY, data.pos.device, dtype,
+               data.num_edges, double_backward=self.double_backward)
+        vec = data.edge_vectors()
+        A = self.messages(data, vec)
+        node_energy = (A.reshape(A.shape[0], -1) @ self.U.to(A.dtype).reshape(-1)
+                       + self.atom_ref.to(A.dtype)[data.atomic_numbers])
+        return {"node_energy": node_energy, "energy": self.aggregate_energy(node_energy, data)}

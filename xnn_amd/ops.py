@@ -1,0 +1,395 @@
+"""HIP-backed operators of the per-edge path, registered as ``torch.library`` custom ops.
+
+Each op is a thin call into ``libxnn_amd.so`` on the current stream, with its
+autograd formula registered next to it. The ops run on GPU tensors only; on any
+other device, or without the library, they raise (there is no fallback).
+
+Reference counterparts (file:line in molssi-ai/xnn):
+
+=====================  ==============================================================
+op                     replaces
+=====================  ==============================================================
+``edge_vectors``       ``AtomicGraph.edge_vectors`` / ``_EdgeVectors``
+                       (common/data/atomic_data.py:371-467)
+``edge_embed``         ``SphericalHarmonicEdgeEmbedding.embed``
+                       (gnn/featurizers/spherical.py:115-138) with ``BesselRBF`` /
+                       ``GaussianRBF`` (common/featurizers/radial.py:15-75, 187-268)
+                       and ``PolynomialCutoff`` / ``CosineCutoff`` (cutoff.py:10-125)
+``sh_message_sum``     ``ConvTensorProduct.conv`` reference path for scalar edge
+                       weights (gnn/fast/conv.py:137-143) + ``scatter_sum``
+``segment_sum``        ``scatter_sum`` (common/models/ops.py:403-448)
+``gather_rows``        ``gather_rows`` (common/models/ops.py:494-528)
+``structure_sum``      ``structure_sum`` (common/models/ops.py:531-557), float64 totals
+=====================  ==============================================================
+
+All reductions walk CSR rows in a fixed order (no float atomics), so every op
+is bitwise reproducible run to run. The backward passes are differentiable
+once: a double backward (force training with ``create_graph=True``) raises.
+"""
+from __future__ import annotations
+
+from typing import List, Optional, Tuple
+
+import torch
+from torch import Tensor
+
+from . import _lib
+from .plan import EdgePlan
+
+_NS = "xnn_amd"
+
+
+def _require_gpu(*tensors: Optional[Tensor]) -> torch.device:
+    dev = None
+    for t in tensors:
+        if t is None:
+            continue
+        if t.device.type != "cuda":
+            raise RuntimeError("xnn_amd ops run on the GPU only (got a tensor on "
+                               f"{t.device}); there is no CPU fallback")
+        dev = t.device
+    _lib.load()
+    return dev
+
+
+def _once_differentiable() -> None:
+    if torch.is_grad_enabled():
+        raise RuntimeError("the xnn_amd backward is differentiable once; double backward "
+                           "(create_graph=True) needs the reference path (use_fast=False)")
+
+
+def _opt(t: Optional[Tensor]) -> Optional[Tensor]:
+    return None if t is None or t.numel() == 0 else t
+
+
+# --------------------------------------------------------------------------- edge vectors
+@torch.library.custom_op(f"{_NS}::edge_vectors", mutates_args=())
+def edge_vectors_op(pos: Tensor, cell: Optional[Tensor], batch32: Tensor, src: Tensor, dst: Tensor,
+                    shift: Tensor, ptr_dst: Tensor, perm_dst: Optional[Tensor], ptr_src: Tensor,
+                    perm_src: Tensor, node_ptr: Tensor, out_dtype: int) -> Tensor:
+    """``pos[dst] - pos[src] + shift @ cell`` per edge, formed in the geometry dtype and
+    returned in ``out_dtype`` (atomic_data.py:371-418)."""
+    dev = _require_gpu(pos)
+    n_edges = src.shape[0]
+    odt = torch.float32 if out_dtype == _lib.XNN_F32 else torch.float64
+    vec = torch.empty((n_edges, 3), dtype=odt, device=dev)
+    cell = _opt(cell)
+    prm = _lib.FeaturizeParams(0, 0, 2, 1, 0, 1, 1.0, 1.0, 1.0)
+    _lib.call("xnn_edge_featurize", _lib.dtype_code(pos.dtype), out_dtype, None,
+              _lib.ptr(pos), pos.shape[0], _lib.ptr(cell),
+              0 if cell is None else cell.shape[0], _lib.ptr(batch32), _lib.ptr(src),
+              _lib.ptr(dst), _lib.ptr(shift), n_edges, prm, None, _lib.ptr(vec), None, None, None,
+              _lib.stream(dev))
+    return vec
+
+
+@edge_vectors_op.register_fake
+def _(pos, cell, batch32, src, dst, shift, ptr_dst, perm_dst, ptr_src, perm_src, node_ptr,
+      out_dtype):
+    odt = torch.float32 if out_dtype == _lib.XNN_F32 else torch.float64
+    return pos.new_empty((src.shape[0], 3), dtype=odt)
+
+
+def force_reduce(g_edge: Tensor, plan_tensors, n_nodes: int, geom_dtype: torch.dtype,
+                 want_cell: bool) -> Tuple[Tensor, Optional[Tensor]]:
+    """grad_pos = sum_{dst=i} g - sum_{src=i} g and, optionally, the per-structure
+    cell gradient shifts^T g (float64 accumulation), from per-edge ``g``."""
+    shift, ptr_dst, perm_dst, ptr_src, perm_src, node_ptr = plan_tensors
+    dev = g_edge.device
+    g_edge = g_edge.contiguous()
+    grad_pos = torch.empty((n_nodes, 3), dtype=geom_dtype, device=dev)
+    partial = torch.empty((n_nodes, 9), dtype=torch.float64, device=dev) if want_cell else None
+    s = _lib.stream(dev)
+    _lib.call("xnn_edge_force_reduce", _lib.dtype_code(geom_dtype), _lib.dtype_code(g_edge.dtype),
+              _lib.ptr(g_edge), g_edge.shape[0], _lib.ptr(ptr_dst), _lib.ptr(perm_dst),
+              _lib.ptr(ptr_src), _lib.ptr(perm_src), _lib.ptr(shift), n_nodes,
+              _lib.ptr(grad_pos), _lib.ptr(partial), s)
+    grad_cell = None
+    if want_cell:
+        n_graphs = node_ptr.shape[0] - 1
+        grad_cell = torch.empty((n_graphs, 9), dtype=torch.float64, device=dev)
+        _lib.call("xnn_segment_reduce_f64", _lib.XNN_F64, _lib.ptr(partial), n_nodes, 9,
+                  _lib.ptr(node_ptr), n_graphs, _lib.ptr(grad_cell), s)
+        grad_cell = grad_cell.view(n_graphs, 3, 3)
+    return grad_pos, grad_cell
+
+
+def _edge_vectors_setup(ctx, inputs, output):
+    (pos, cell, batch32, src, dst, shift, ptr_dst, perm_dst, ptr_src, perm_src, node_ptr,
+     out_dtype) = inputs
+    ctx.save_for_backward(shift, ptr_dst, perm_dst, ptr_src, perm_src, node_ptr)
+    ctx.n_nodes = pos.shape[0]
+    ctx.geom_dtype = pos.dtype
+    ctx.has_cell = cell is not None and cell.numel() > 0
+    ctx.cell_dtype = cell.dtype if ctx.has_cell else None
+
+
+def _edge_vectors_backward(ctx, grad):
+    _once_differentiable()
+    saved = ctx.saved_tensors
+    want_cell = ctx.has_cell and ctx.needs_input_grad[1]
+    grad_pos, grad_cell = force_reduce(grad, saved, ctx.n_nodes, ctx.geom_dtype, want_cell)
+    if grad_cell is not None:
+        grad_cell = grad_cell.to(ctx.cell_dtype)
+    return (grad_pos if ctx.needs_input_grad[0] else None, grad_cell, None, None, None, None,
+            None, None, None, None, None, None)
+
+
+edge_vectors_op.register_autograd(_edge_vectors_backward, setup_context=_edge_vectors_setup)
+
+
+def edge_vectors(pos: Tensor, cell: Optional[Tensor], plan: EdgePlan,
+                 out_dtype: Optional[torch.dtype] = None) -> Tensor:
+    """Edge vectors of a planned graph; differentiable to ``pos`` and ``cell``."""
+    out_dtype = out_dtype or pos.dtype
+    if cell is not None:
+        cell = cell.reshape(-1, 3, 3).to(pos.dtype)
+        if not cell.is_contiguous():
+            cell = cell.contiguous()
+    return edge_vectors_op(pos.contiguous(), cell, plan.batch32, plan.src, plan.dst, plan.shift,
+                           plan.ptr_dst, plan.perm_dst, plan.ptr_src, plan.perm_src,
+                           plan.node_ptr, _lib.dtype_code(out_dtype))
+
+
+# --------------------------------------------------------------------------- edge embedding
+def _params(iparams: List[int], fparams: List[float]) -> "_lib.FeaturizeParams":
+    n_rbf, basis, envelope, p, l_max, sign = iparams
+    cutoff, prefactor, gamma = fparams
+    return _lib.FeaturizeParams(n_rbf, basis, envelope, p, l_max, sign, cutoff, prefactor, gamma)
+
+
+@torch.library.custom_op(f"{_NS}::edge_embed", mutates_args=())
+def edge_embed_op(vec: Tensor, rbf_table: Tensor, iparams: List[int], fparams: List[float],
+                  want_length: bool, want_sh: bool, want_radial: bool
+                  ) -> Tuple[Tensor, Tensor, Tensor]:
+    """``(|v|, Y(sign v / |v|), rbf(|v|) * envelope(|v|))`` per edge vector
+    (spherical.py:135-138); unrequested outputs come back empty."""
+    dev = _require_gpu(vec)
+    n_edges = vec.shape[0]
+    n_rbf, l_max = iparams[0], iparams[4]
+    L = (l_max + 1) ** 2
+    length = vec.new_empty((n_edges,) if want_length else (0,))
+    sh = vec.new_empty((n_edges, L) if want_sh else (0,))
+    radial = vec.new_empty((n_edges, n_rbf) if want_radial else (0,))
+    code = _lib.dtype_code(vec.dtype)
+    _lib.call("xnn_edge_featurize", code, code, _lib.ptr(vec), None, 0, None, 0, None, None, None,
+              None, n_edges, _params(iparams, fparams), _lib.ptr(rbf_table), None,
+              _lib.ptr(length) if want_length else None, _lib.ptr(sh) if want_sh else None,
+              _lib.ptr(radial) if want_radial else None, _lib.stream(dev))
+    return length, sh, radial
+
+
+@edge_embed_op.register_fake
+def _(vec, rbf_table, iparams, fparams, want_length, want_sh, want_radial):
+    n_edges = vec.shape[0]
+    L = (iparams[4] + 1) ** 2
+    return (vec.new_empty((n_edges,) if want_length else (0,)),
+            vec.new_empty((n_edges, L) if want_sh else (0,)),
+            vec.new_empty((n_edges, iparams[0]) if want_radial else (0,)))
+
+
+def _edge_embed_setup(ctx, inputs, output):
+    vec, rbf_table, iparams, fparams, want_length, want_sh, want_radial = inputs
+    ctx.save_for_backward(vec, rbf_table)
+    ctx.iparams, ctx.fparams = list(iparams), list(fparams)
+    ctx.wants = (want_length, want_sh, want_radial)
+
+
+def _edge_embed_backward(ctx, d_length, d_sh, d_radial):
+    _once_differentiable()
+    vec, rbf_table = ctx.saved_tensors
+    if ctx.needs_input_grad[1]:
+        raise NotImplementedError("the fast edge embedding does not differentiate the radial "
+                                  "basis parameters; use use_fast=False to train them")
+    want_length, want_sh, want_radial = ctx.wants
+    d_length = d_length.contiguous() if want_length and d_length is not None else None
+    d_sh = d_sh.contiguous() if want_sh and d_sh is not None else None
+    d_radial = d_radial.contiguous() if want_radial and d_radial is not None else None
+    g = torch.empty_like(vec)
+    code = _lib.dtype_code(vec.dtype)
+    _lib.call("xnn_edge_featurize_backward", code, code, _lib.ptr(vec), None, 0, None, 0, None,
+              None, None, None, vec.shape[0], _params(ctx.iparams, ctx.fparams),
+              _lib.ptr(rbf_table), None, _lib.ptr(d_length), _lib.ptr(d_sh), _lib.ptr(d_radial),
+              None, _lib.ptr(g), _lib.stream(vec.device))
+    return g, None, None, None, None, None, None
+
+
+edge_embed_op.register_autograd(_edge_embed_backward, setup_context=_edge_embed_setup)
+
+
+def edge_embed(vec: Tensor, rbf_table: Tensor, *, n_rbf: int, basis: str, envelope: str,
+               poly_p: int, l_max: int, cutoff: float, prefactor: float = 1.0,
+               gamma: float = 1.0, sh_sign: int = 1, want_length: bool = True,
+               want_sh: bool = True, want_radial: bool = True) -> Tuple[Tensor, Tensor, Tensor]:
+    """Length, spherical harmonics and enveloped radial basis of edge vectors."""
+    iparams = [int(n_rbf), _lib.BASIS[basis], _lib.ENVELOPE[envelope], int(poly_p), int(l_max),
+               int(sh_sign)]
+    fparams = [float(cutoff), float(prefactor), float(gamma)]
+    table = rbf_table.to(device=vec.device, dtype=vec.dtype).contiguous()
+    return edge_embed_op(vec.contiguous(), table, iparams, fparams, bool(want_length),
+                         bool(want_sh), bool(want_radial))
+
+
+# --------------------------------------------------------------------------- SH message sum
+@torch.library.custom_op(f"{_NS}::sh_message_sum", mutates_args=())
+def sh_message_sum_op(vec: Tensor, phi: Tensor, ptr_dst: Tensor, perm_dst: Optional[Tensor],
+                      l_max: int, sh_sign: int) -> Tensor:
+    """``A[i, c, lm] = sum_{dst(e)=i} phi[e, c] Y_lm(sign vec_e)`` (float32)."""
+    dev = _require_gpu(vec, phi)
+    n_nodes = ptr_dst.shape[0] - 1
+    C = phi.shape[1]
+    L = (l_max + 1) ** 2
+    out = torch.empty((n_nodes, C, L), dtype=torch.float32, device=dev)
+    _lib.call("xnn_sh_message_sum", _lib.XNN_F32, _lib.ptr(vec), None, n_nodes, None, 0, None,
+              None, None, vec.shape[0], _lib.ptr(ptr_dst), _lib.ptr(perm_dst), l_max, sh_sign, C,
+              _lib.ptr(phi), _lib.ptr(out), _lib.stream(dev))
+    return out
+
+
+@sh_message_sum_op.register_fake
+def _(vec, phi, ptr_dst, perm_dst, l_max, sh_sign):
+    return phi.new_empty((ptr_dst.shape[0] - 1, phi.shape[1], (l_max + 1) ** 2))
+
+
+def _sh_msg_setup(ctx, inputs, output):
+    vec, phi, ptr_dst, perm_dst, l_max, sh_sign = inputs
+    ctx.save_for_backward(vec, phi, ptr_dst, perm_dst)
+    ctx.l_max, ctx.sh_sign = l_max, sh_sign
+
+
+def _sh_msg_backward(ctx, d_out):
+    _once_differentiable()
+    vec, phi, ptr_dst, perm_dst = ctx.saved_tensors
+    d_out = d_out.contiguous()
+    n_nodes = ptr_dst.shape[0] - 1
+    d_phi = torch.empty_like(phi)
+    g_vec = torch.empty_like(vec) if ctx.needs_input_grad[0] else None
+    _lib.call("xnn_sh_message_sum_backward", _lib.XNN_F32, _lib.ptr(vec), None, n_nodes, None, 0,
+              None, None, None, vec.shape[0], _lib.ptr(ptr_dst), _lib.ptr(perm_dst), ctx.l_max,
+              ctx.sh_sign, phi.shape[1], _lib.ptr(phi), _lib.ptr(d_out), _lib.ptr(d_phi),
+              _lib.ptr(g_vec), _lib.stream(vec.device))
+    return g_vec, d_phi, None, None, None, None
+
+
+sh_message_sum_op.register_autograd(_sh_msg_backward, setup_context=_sh_msg_setup)
+
+
+def sh_message_sum(vec: Tensor, phi: Tensor, plan: EdgePlan, l_max: int,
+                   sh_sign: int = 1) -> Tensor:
+    """Aggregate ``phi[e, c] * Y_lm(sign vec_e)`` onto receivers: ``(N, C, (l_max+1)^2)``."""
+    if vec.dtype != torch.float32 or phi.dtype != torch.float32:
+        raise TypeError("sh_message_sum computes in float32")
+    if phi.shape[0] != vec.shape[0]:
+        raise ValueError("phi and vec need one row per edge")
+    if not 1 <= phi.shape[1] <= 256:
+        raise ValueError("sh_message_sum takes 1 to 256 channels")
+    return sh_message_sum_op(vec.contiguous(), phi.contiguous(), plan.ptr_dst, plan.perm_dst,
+                             int(l_max), int(sh_sign))
+
+
+# --------------------------------------------------------------------------- segment sums
+@torch.library.custom_op(f"{_NS}::segment_sum", mutates_args=())
+def segment_sum_op(src: Tensor, index32: Tensor, ptr: Tensor, perm: Optional[Tensor]) -> Tensor:
+    """``out[i] = sum over rows e with index[e] = i of src[e]`` via the CSR ``ptr``/``perm``."""
+    dev = _require_gpu(src)
+    n_seg = ptr.shape[0] - 1
+    feat = src.shape[1:]
+    F = 1
+    for d in feat:
+        F *= int(d)
+    out = src.new_empty((n_seg, *feat))
+    _lib.call("xnn_segment_sum", _lib.dtype_code(src.dtype), _lib.ptr(src), src.shape[0], F,
+              _lib.ptr(ptr), _lib.ptr(perm), n_seg, _lib.ptr(out), _lib.stream(dev))
+    return out
+
+
+@segment_sum_op.register_fake
+def _(src, index32, ptr, perm):
+    return src.new_empty((ptr.shape[0] - 1, *src.shape[1:]))
+
+
+def _gather(src: Tensor, index32: Tensor) -> Tensor:
+    src = src.contiguous()
+    feat = src.shape[1:]
+    F = 1
+    for d in feat:
+        F *= int(d)
+    out = src.new_empty((index32.shape[0], *feat))
+    _lib.call("xnn_gather_rows", _lib.dtype_code(src.dtype), _lib.ptr(src), src.shape[0], F,
+              _lib.ptr(index32), index32.shape[0], _lib.ptr(out), _lib.stream(src.device))
+    return out
+
+
+def _segment_sum_setup(ctx, inputs, output):
+    src, index32, ptr, perm = inputs
+    ctx.save_for_backward(index32)
+
+
+def _segment_sum_backward(ctx, grad):
+    _once_differentiable()
+    (index32,) = ctx.saved_tensors
+    return _gather(grad, index32), None, None, None
+
+
+segment_sum_op.register_autograd(_segment_sum_backward, setup_context=_segment_sum_setup)
+
+
+@torch.library.custom_op(f"{_NS}::gather_rows", mutates_args=())
+def gather_rows_op(src: Tensor, index32: Tensor, ptr: Tensor, perm: Optional[Tensor]) -> Tensor:
+    """``src[index]`` along dim 0; its adjoint is the CSR segment sum."""
+    _require_gpu(src)
+    return _gather(src, index32)
+
+
+@gather_rows_op.register_fake
+def _(src, index32, ptr, perm):
+    return src.new_empty((index32.shape[0], *src.shape[1:]))
+
+
+def _gather_setup(ctx, inputs, output):
+    src, index32, ptr, perm = inputs
+    ctx.save_for_backward(index32, ptr, perm)
+
+
+def _gather_backward(ctx, grad):
+    _once_differentiable()
+    index32, ptr, perm = ctx.saved_tensors
+    return segment_sum_op(grad.contiguous(), index32, ptr, perm), None, None, None
+
+
+gather_rows_op.register_autograd(_gather_backward, setup_context=_gather_setup)
+
+
+@torch.library.custom_op(f"{_NS}::structure_sum", mutates_args=())
+def structure_sum_op(src: Tensor, node_ptr: Tensor, batch32: Tensor) -> Tensor:
+    """Per-structure totals of per-atom values, accumulated and returned in float64."""
+    dev = _require_gpu(src)
+    n_seg = node_ptr.shape[0] - 1
+    src = src.contiguous()
+    F = 1
+    for d in src.shape[1:]:
+        F *= int(d)
+    out = torch.empty((n_seg, *src.shape[1:]), dtype=torch.float64, device=dev)
+    _lib.call("xnn_segment_reduce_f64", _lib.dtype_code(src.dtype), _lib.ptr(src), src.shape[0],
+              F, _lib.ptr(node_ptr), n_seg, _lib.ptr(out), _lib.stream(dev))
+    return out
+
+
+@structure_sum_op.register_fake
+def _(src, node_ptr, batch32):
+    return src.new_empty((node_ptr.shape[0] - 1, *src.shape[1:]), dtype=torch.float64)
+
+
+def _structure_sum_setup(ctx, inputs, output):
+    src, node_ptr, batch32 = inputs
+    ctx.save_for_backward(batch32)
+    ctx.src_dtype = src.dtype
+
+
+def _structure_sum_backward(ctx, grad):
+    _once_differentiable()
+    (batch32,) = ctx.saved_tensors
+    return _gather(grad.contiguous(), batch32).to(ctx.src_dtype), None, None
+
+
+structure_sum_op.register_autograd(_structure_sum_backward, setup_context=_structure_sum_setup)

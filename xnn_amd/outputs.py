@@ -1,0 +1,77 @@
+"""Conservative forces and stress by differentiation (common/models/outputs.py:96-239).
+
+``forces = -dE/dpos``; ``stress = (1/V) dE/d(strain)`` with the symmetric-strain trick:
+positions and cell are displaced by ``sym(eps)`` at ``eps = 0`` so that autograd
+carries the virial back to ``eps``. On a GPU the backward of the edge vectors is the
+HIP CSR force reduction, so no float atomics touch the forces.
+"""
+from __future__ import annotations
+
+from typing import Optional
+
+import torch
+from torch import Tensor, nn
+
+from .functional import cell_volume
+
+
+class ForceStressOutput(nn.Module):
+    """Wrap a model to add ``forces`` (N, 3) and, for periodic structures, ``stress``
+    (B, 3, 3) (outputs.py:25-224)."""
+
+    def __init__(self, model: nn.Module, compute_forces: bool = True, compute_stress: bool = False):
+        super().__init__()
+        self.model = model
+        self.compute_forces = compute_forces
+        self.compute_stress = compute_stress
+        self.cutoff = getattr(model, "cutoff", None)
+
+    def forward(self, data) -> dict:
+        create_graph = self.training
+        strain: Optional[Tensor] = None
+        if self.compute_stress and data.cell is not None:
+            strain = torch.zeros((data.num_graphs, 3, 3), dtype=data.pos.dtype,
+                                 device=data.pos.device, requires_grad=True)
+            sym = 0.5 * (strain + strain.transpose(-1, -2))
+            if data.num_graphs == 1:
+                data.pos = data.pos + (data.pos[:, :, None] * sym[0]).sum(1)
+            else:
+                data.pos = data.pos + (data.pos[:, :, None] * sym.index_select(0, data.batch)).sum(1)
+            data.cell = data.cell + (data.cell[:, :, :, None] * sym[:, None]).sum(2)
+        if self.compute_forces:
+            data.pos.requires_grad_(True)
+        # the double-backward of a training step needs the differentiable formulation
+        if hasattr(self.model, "double_backward"):
+            self.model.double_backward = bool(create_graph)
+        out = self.model(data)
+        energy = out["energy"]
+        inputs, need = [], []
+        if self.compute_forces:
+            inputs.append(data.pos)
+            need.append("pos")
+        if strain is not None:
+            inputs.append(strain)
+            need.append("strain")
+        g = {k: None for k in need}
+        if inputs and energy.requires_grad:
+            grads = torch.autograd.grad([energy], inputs, grad_outputs=[torch.ones_like(energy)],
+                                        create_graph=create_graph, retain_graph=create_graph,
+                                        allow_unused=True)
+            g = dict(zip(need, grads))
+        if self.compute_forces:
+            out["forces"] = -g["pos"] if g.get("pos") is not None else torch.zeros_like(data.pos)
+        if strain is not None:
+            out["stress"] = (_stress(g["strain"], data) if g.get("strain") is not None
+                             else torch.zeros_like(strain))
+        return out
+
+
+def _stress(strain_gradient: Tensor, data) -> Tensor:
+    """``dE/d(strain) / V`` per structure, zero for molecules of a batch (outputs.py:227-239)."""
+    volume = cell_volume(data.cell)
+    periodic = volume > 1e-8
+    if data.pbc is not None:
+        periodic = periodic & data.pbc.any(-1).to(periodic.device)
+    safe = torch.where(periodic, volume, torch.ones_like(volume))
+    return torch.where(periodic[:, None, None], strain_gradient / safe[:, None, None],
+                       torch.zeros_like(strain_gradient))
