@@ -151,7 +151,7 @@ def main() -> None:
     g, model, rc, kw, workload, nl_ms, structs = build_workload(args.config, device)
     E, N = g.num_edges, g.num_nodes
     C, L = kw["channels"], (kw["l_max"] + 1) ** 2
-    wrapped = xa.ForceStressOutput(model, compute_stress=g.cell is not None)
+    wrapped = xa.ForceStressOutput(model, compute_stress=g.cell is not None).eval()
     g.plan()                                    # edge plan: once per neighbor list
 
     def step():

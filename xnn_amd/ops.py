@@ -23,8 +23,11 @@ op                     replaces
 =====================  ==============================================================
 
 All reductions walk CSR rows in a fixed order (no float atomics), so every op
-is bitwise reproducible run to run. The backward passes are differentiable
-once: a double backward (force training with ``create_graph=True``) raises.
+is bitwise reproducible run to run. The linear ops (edge vectors, segment sums,
+gathers, structure sums) are differentiable to any order: each backward is its
+adjoint op. The nonlinear ones (edge embedding, SH message sum) are
+differentiable once; a double backward through them (force training with
+``create_graph=True``) raises, and the modules take the PyTorch formulation there.
 """
 from __future__ import annotations
 
@@ -90,57 +93,93 @@ def _(pos, cell, batch32, src, dst, shift, ptr_dst, perm_dst, ptr_src, perm_src,
     return pos.new_empty((src.shape[0], 3), dtype=odt)
 
 
-def force_reduce(g_edge: Tensor, plan_tensors, n_nodes: int, geom_dtype: torch.dtype,
-                 want_cell: bool) -> Tuple[Tensor, Optional[Tensor]]:
-    """grad_pos = sum_{dst=i} g - sum_{src=i} g and, optionally, the per-structure
-    cell gradient shifts^T g (float64 accumulation), from per-edge ``g``."""
-    shift, ptr_dst, perm_dst, ptr_src, perm_src, node_ptr = plan_tensors
-    dev = g_edge.device
+@torch.library.custom_op(f"{_NS}::force_reduce", mutates_args=())
+def force_reduce_op(g_edge: Tensor, cell_like: Optional[Tensor], batch32: Tensor, src: Tensor,
+                    dst: Tensor, shift: Tensor, ptr_dst: Tensor, perm_dst: Optional[Tensor],
+                    ptr_src: Tensor, perm_src: Tensor, node_ptr: Tensor, n_nodes: int,
+                    geom_code: int, want_cell: bool) -> Tuple[Tensor, Tensor]:
+    """Adjoint of :func:`edge_vectors_op`: ``grad_pos[i] = sum_{dst=i} g - sum_{src=i} g``
+    and, when ``want_cell``, ``grad_cell[b] = sum_{edges of b} shift^T g`` (float64
+    accumulation, returned in the geometry dtype) (atomic_data.py:452-467)."""
+    dev = _require_gpu(g_edge)
     g_edge = g_edge.contiguous()
-    grad_pos = torch.empty((n_nodes, 3), dtype=geom_dtype, device=dev)
+    gdt = torch.float32 if geom_code == _lib.XNN_F32 else torch.float64
+    n_graphs = node_ptr.shape[0] - 1
+    grad_pos = torch.empty((n_nodes, 3), dtype=gdt, device=dev)
     partial = torch.empty((n_nodes, 9), dtype=torch.float64, device=dev) if want_cell else None
     s = _lib.stream(dev)
-    _lib.call("xnn_edge_force_reduce", _lib.dtype_code(geom_dtype), _lib.dtype_code(g_edge.dtype),
-              _lib.ptr(g_edge), g_edge.shape[0], _lib.ptr(ptr_dst), _lib.ptr(perm_dst),
-              _lib.ptr(ptr_src), _lib.ptr(perm_src), _lib.ptr(shift), n_nodes,
-              _lib.ptr(grad_pos), _lib.ptr(partial), s)
-    grad_cell = None
-    if want_cell:
-        n_graphs = node_ptr.shape[0] - 1
-        grad_cell = torch.empty((n_graphs, 9), dtype=torch.float64, device=dev)
-        _lib.call("xnn_segment_reduce_f64", _lib.XNN_F64, _lib.ptr(partial), n_nodes, 9,
-                  _lib.ptr(node_ptr), n_graphs, _lib.ptr(grad_cell), s)
-        grad_cell = grad_cell.view(n_graphs, 3, 3)
-    return grad_pos, grad_cell
+    _lib.call("xnn_edge_force_reduce", geom_code, _lib.dtype_code(g_edge.dtype), _lib.ptr(g_edge),
+              g_edge.shape[0], _lib.ptr(ptr_dst), _lib.ptr(perm_dst), _lib.ptr(ptr_src),
+              _lib.ptr(perm_src), _lib.ptr(shift), n_nodes, _lib.ptr(grad_pos),
+              _lib.ptr(partial), s)
+    if not want_cell:
+        return grad_pos, grad_pos.new_zeros((0,))
+    grad_cell = torch.empty((n_graphs, 9), dtype=torch.float64, device=dev)
+    _lib.call("xnn_segment_reduce_f64", _lib.XNN_F64, _lib.ptr(partial), n_nodes, 9,
+              _lib.ptr(node_ptr), n_graphs, _lib.ptr(grad_cell), s)
+    return grad_pos, grad_cell.view(n_graphs, 3, 3).to(gdt)
+
+
+@force_reduce_op.register_fake
+def _(g_edge, cell_like, batch32, src, dst, shift, ptr_dst, perm_dst, ptr_src, perm_src, node_ptr,
+      n_nodes, geom_code, want_cell):
+    gdt = torch.float32 if geom_code == _lib.XNN_F32 else torch.float64
+    n_graphs = node_ptr.shape[0] - 1
+    return (g_edge.new_empty((n_nodes, 3), dtype=gdt),
+            g_edge.new_empty((n_graphs, 3, 3) if want_cell else (0,), dtype=gdt))
 
 
 def _edge_vectors_setup(ctx, inputs, output):
     (pos, cell, batch32, src, dst, shift, ptr_dst, perm_dst, ptr_src, perm_src, node_ptr,
      out_dtype) = inputs
-    ctx.save_for_backward(shift, ptr_dst, perm_dst, ptr_src, perm_src, node_ptr)
+    ctx.save_for_backward(batch32, src, dst, shift, ptr_dst, perm_dst, ptr_src, perm_src, node_ptr)
     ctx.n_nodes = pos.shape[0]
-    ctx.geom_dtype = pos.dtype
+    ctx.geom_code = _lib.dtype_code(pos.dtype)
     ctx.has_cell = cell is not None and cell.numel() > 0
-    ctx.cell_dtype = cell.dtype if ctx.has_cell else None
 
 
 def _edge_vectors_backward(ctx, grad):
-    _once_differentiable()
-    saved = ctx.saved_tensors
-    want_cell = ctx.has_cell and ctx.needs_input_grad[1]
-    grad_pos, grad_cell = force_reduce(grad, saved, ctx.n_nodes, ctx.geom_dtype, want_cell)
-    if grad_cell is not None:
-        grad_cell = grad_cell.to(ctx.cell_dtype)
-    return (grad_pos if ctx.needs_input_grad[0] else None, grad_cell, None, None, None, None,
-            None, None, None, None, None, None)
+    batch32, src, dst, shift, ptr_dst, perm_dst, ptr_src, perm_src, node_ptr = ctx.saved_tensors
+    want_cell = bool(ctx.has_cell and ctx.needs_input_grad[1])
+    grad_pos, grad_cell = force_reduce_op(grad.contiguous(), None, batch32, src, dst, shift,
+                                          ptr_dst, perm_dst, ptr_src, perm_src, node_ptr,
+                                          ctx.n_nodes, ctx.geom_code, want_cell)
+    return (grad_pos if ctx.needs_input_grad[0] else None, grad_cell if want_cell else None,
+            None, None, None, None, None, None, None, None, None, None)
 
 
 edge_vectors_op.register_autograd(_edge_vectors_backward, setup_context=_edge_vectors_setup)
 
 
+def _force_reduce_setup(ctx, inputs, output):
+    (g_edge, cell_like, batch32, src, dst, shift, ptr_dst, perm_dst, ptr_src, perm_src, node_ptr,
+     n_nodes, geom_code, want_cell) = inputs
+    ctx.save_for_backward(batch32, src, dst, shift, ptr_dst, perm_dst, ptr_src, perm_src, node_ptr)
+    ctx.out_code = _lib.dtype_code(g_edge.dtype)
+    ctx.want_cell = want_cell
+
+
+def _force_reduce_backward(ctx, d_pos, d_cell):
+    # the adjoint of the reduction is the edge-vector map applied to the cotangents
+    batch32, src, dst, shift, ptr_dst, perm_dst, ptr_src, perm_src, node_ptr = ctx.saved_tensors
+    cell = d_cell.contiguous() if (ctx.want_cell and d_cell is not None) else None
+    if d_pos is None:
+        d_pos = torch.zeros((ptr_dst.shape[0] - 1, 3), dtype=cell.dtype if cell is not None
+                            else torch.float32, device=ptr_dst.device)
+    if cell is not None:
+        cell = cell.to(d_pos.dtype)
+    g = edge_vectors_op(d_pos.contiguous(), cell, batch32, src, dst, shift, ptr_dst, perm_dst,
+                        ptr_src, perm_src, node_ptr, ctx.out_code)
+    return (g, None, None, None, None, None, None, None, None, None, None, None, None, None)
+
+
+force_reduce_op.register_autograd(_force_reduce_backward, setup_context=_force_reduce_setup)
+
+
 def edge_vectors(pos: Tensor, cell: Optional[Tensor], plan: EdgePlan,
                  out_dtype: Optional[torch.dtype] = None) -> Tensor:
-    """Edge vectors of a planned graph; differentiable to ``pos`` and ``cell``."""
+    """Edge vectors of a planned graph; differentiable to ``pos`` and ``cell`` to any
+    order (the backward is the CSR force reduction, whose adjoint is this map again)."""
     out_dtype = out_dtype or pos.dtype
     if cell is not None:
         cell = cell.reshape(-1, 3, 3).to(pos.dtype)
@@ -322,13 +361,12 @@ def _gather(src: Tensor, index32: Tensor) -> Tensor:
 
 def _segment_sum_setup(ctx, inputs, output):
     src, index32, ptr, perm = inputs
-    ctx.save_for_backward(index32)
+    ctx.save_for_backward(index32, ptr, perm)
 
 
 def _segment_sum_backward(ctx, grad):
-    _once_differentiable()
-    (index32,) = ctx.saved_tensors
-    return _gather(grad, index32), None, None, None
+    index32, ptr, perm = ctx.saved_tensors
+    return gather_rows_op(grad.contiguous(), index32, ptr, perm), None, None, None
 
 
 segment_sum_op.register_autograd(_segment_sum_backward, setup_context=_segment_sum_setup)
@@ -352,7 +390,6 @@ def _gather_setup(ctx, inputs, output):
 
 
 def _gather_backward(ctx, grad):
-    _once_differentiable()
     index32, ptr, perm = ctx.saved_tensors
     return segment_sum_op(grad.contiguous(), index32, ptr, perm), None, None, None
 
@@ -382,14 +419,16 @@ def _(src, node_ptr, batch32):
 
 def _structure_sum_setup(ctx, inputs, output):
     src, node_ptr, batch32 = inputs
-    ctx.save_for_backward(batch32)
+    ctx.save_for_backward(node_ptr, batch32)
     ctx.src_dtype = src.dtype
 
 
 def _structure_sum_backward(ctx, grad):
-    _once_differentiable()
-    (batch32,) = ctx.saved_tensors
-    return _gather(grad.contiguous(), batch32).to(ctx.src_dtype), None, None
+    # broadcast of every structure's cotangent to its atoms: the gather over batch,
+    # whose own adjoint is the segment sum over node_ptr
+    node_ptr, batch32 = ctx.saved_tensors
+    g = gather_rows_op(grad.contiguous(), batch32, node_ptr.to(torch.int32), None)
+    return g.to(ctx.src_dtype), None, None
 
 
 structure_sum_op.register_autograd(_structure_sum_backward, setup_context=_structure_sum_setup)
