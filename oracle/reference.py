@@ -26,18 +26,34 @@ from torch import Tensor
 
 # --------------------------------------------------------------------------- geometry
 def edge_vectors(pos: Tensor, edge_index: Tensor, cell_shifts: Tensor,
-                 cell: Optional[Tensor], batch: Optional[Tensor] = None) -> Tensor:
-    """``pos[dst] - pos[src] + shift @ cell`` (atomic_data.py:371-418)."""
+                 cell: Optional[Tensor], batch: Optional[Tensor] = None,
+                 geometry_dtype: Optional[torch.dtype] = None) -> Tensor:
+    """``pos[dst] - pos[src] + shift @ cell`` (atomic_data.py:371-418).
+
+    With ``geometry_dtype`` (float32), the vector's value is formed in that dtype in the
+    reference's order -- the difference, then the image offset -- as a float32 geometry
+    does (atomic_data.py:406-410), while its derivative stays the exact linear map in
+    the working dtype; the rest of the evaluation then runs in the working dtype."""
     src, dst = edge_index[0], edge_index[1]
-    vec = pos.index_select(0, dst) - pos.index_select(0, src)
-    if cell is not None:
-        cell = cell.reshape(-1, 3, 3)
-        if cell.shape[0] == 1:
-            vec = vec + cell_shifts.to(vec.dtype) @ cell[0]
-        else:
-            per_edge = cell.index_select(0, batch.index_select(0, src))
-            vec = vec + torch.einsum("ei,eij->ej", cell_shifts.to(vec.dtype), per_edge)
-    return vec
+
+    def form(p, c):
+        v = p.index_select(0, dst) - p.index_select(0, src)
+        if c is not None:
+            c = c.reshape(-1, 3, 3)
+            if c.shape[0] == 1:
+                v = v + cell_shifts.to(v.dtype) @ c[0]
+            else:
+                per_edge = c.index_select(0, batch.index_select(0, src))
+                v = v + torch.einsum("ei,eij->ej", cell_shifts.to(v.dtype), per_edge)
+        return v
+
+    vec = form(pos, cell)
+    if geometry_dtype is None or geometry_dtype == pos.dtype:
+        return vec
+    with torch.no_grad():
+        rounded = form(pos.detach().to(geometry_dtype),
+                       None if cell is None else cell.detach().to(geometry_dtype)).to(pos.dtype)
+    return vec + (rounded - vec.detach())
 
 
 # --------------------------------------------------------------------------- radial
@@ -161,9 +177,10 @@ def sh_edge_node_energy(vec: Tensor, edge_index: Tensor, n_nodes: int, numbers: 
 
 def energy_forces_stress(pos: Tensor, numbers: Tensor, edge_index: Tensor, cell_shifts: Tensor,
                          cell: Optional[Tensor], batch: Tensor, n_graphs: int, model: dict,
-                         stress: bool = True):
+                         stress: bool = True, geometry_dtype: Optional[torch.dtype] = None):
     """Energy (B,) float64, forces (N, 3) and stress (B, 3, 3) by autograd through the
-    symmetric strain (outputs.py:166-239), for the sh_edge model parameters in ``model``."""
+    symmetric strain (outputs.py:166-239), for the sh_edge model parameters in ``model``;
+    ``geometry_dtype`` as in :func:`edge_vectors`."""
     strain = torch.zeros((n_graphs, 3, 3), dtype=pos.dtype, requires_grad=True)
     sym = 0.5 * (strain + strain.transpose(-1, -2))
     pos = pos.detach().clone().requires_grad_(True)
@@ -171,7 +188,7 @@ def energy_forces_stress(pos: Tensor, numbers: Tensor, edge_index: Tensor, cell_
     c2 = None
     if cell is not None:
         c2 = cell.reshape(-1, 3, 3) + (cell.reshape(-1, 3, 3)[:, :, :, None] * sym[:, None]).sum(2)
-    vec = edge_vectors(p2, edge_index, cell_shifts, c2, batch)
+    vec = edge_vectors(p2, edge_index, cell_shifts, c2, batch, geometry_dtype)
     node_e = sh_edge_node_energy(vec, edge_index, pos.shape[0], numbers, **model)
     energy = structure_sum(node_e, batch, n_graphs)
     inputs = [pos, strain] if (stress and cell is not None) else [pos]

@@ -18,7 +18,6 @@ struct ShDims {
   static constexpr int L = (LMAX + 1) * (LMAX + 1);
   // partial sums are reduced across the wave padded to a power of two
   static constexpr int LP = L == 1 ? 1 : (L <= 4 ? 4 : 16);
-  static constexpr int HALVINGS = L == 1 ? 0 : (L <= 4 ? 2 : 4);
 };
 
 // Per-lane geometry of one edge: unit vector of sign * r_e and 1/|r_e|; the
@@ -47,19 +46,50 @@ __device__ inline void edge_unit(const float* __restrict__ vec, int64_t e,
   uz = sign * z * inv;
 }
 
+// CPL consecutive channels of one phi row starting at c0 (vector loads when aligned)
+template <int CPL, bool VEC>
+__device__ inline void load_channels(const float* __restrict__ row, int c0, int C, float* p) {
+  if constexpr (VEC && CPL == 4) {
+    const float4 v = *reinterpret_cast<const float4*>(row + c0);
+    p[0] = v.x; p[1] = v.y; p[2] = v.z; p[3] = v.w;
+  } else if constexpr (VEC && CPL == 2) {
+    const float2 v = *reinterpret_cast<const float2*>(row + c0);
+    p[0] = v.x; p[1] = v.y;
+  } else {
+#pragma unroll
+    for (int q = 0; q < CPL; ++q) p[q] = (c0 + q < C) ? row[c0 + q] : 0.f;
+  }
+}
+
+template <int CPL, bool VEC>
+__device__ inline void store_channels(float* __restrict__ row, int c0, int C, const float* p) {
+  if constexpr (VEC && CPL == 4) {
+    *reinterpret_cast<float4*>(row + c0) = make_float4(p[0], p[1], p[2], p[3]);
+  } else if constexpr (VEC && CPL == 2) {
+    *reinterpret_cast<float2*>(row + c0) = make_float2(p[0], p[1]);
+  } else {
+#pragma unroll
+    for (int q = 0; q < CPL; ++q)
+      if (c0 + q < C) row[c0 + q] = p[q];
+  }
+}
+
 // One wave per receiver row. Lane l owns channels [l*CPL, l*CPL+CPL). Edges are
-// processed in batches of 64: lane j evaluates Y for edge j of the batch and
-// parks it in LDS, then the whole wave streams phi rows (coalesced) and
-// accumulates phi[e, c] * Y[e, lm] in registers.
-template <typename G, int LMAX, int CPL>
+// processed in batches of 64: lane j evaluates Y for edge j of the batch and parks it
+// in LDS (zeros past the row's end), then the whole wave streams the phi rows of the
+// batch, kUnroll edges at a time with all their loads in flight (coalesced, one
+// contiguous row segment per edge), and accumulates phi[e, c] * Y[e, lm] in registers.
+template <typename G, int LMAX, int CPL, bool VEC>
 __global__ __launch_bounds__(256) void sh_msg_fwd_kernel(
-    const float* __restrict__ vec, const G* __restrict__ pos, const G* __restrict__ cell, int64_t n_graphs,
-    const int32_t* __restrict__ batch, const int32_t* __restrict__ src,
+    const float* __restrict__ vec, const G* __restrict__ pos, const G* __restrict__ cell,
+    int64_t n_graphs, const int32_t* __restrict__ batch, const int32_t* __restrict__ src,
     const int32_t* __restrict__ shift, const int32_t* __restrict__ ptr,
     const int32_t* __restrict__ perm, int64_t n_nodes, int C, float sign,
     const float* __restrict__ phi, float* __restrict__ out) {
   constexpr int L = ShDims<LMAX>::L;
+  constexpr int kUnroll = 8;
   __shared__ float sY[kWavesPerBlock][kWave][L];
+  __shared__ int sE[kWavesPerBlock][kWave];
   const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
   const int64_t row = (int64_t)blockIdx.x * kWavesPerBlock + wave;
   if (row >= n_nodes) return;  // whole wave; no block-level barriers below
@@ -77,45 +107,43 @@ __global__ __launch_bounds__(256) void sh_msg_fwd_kernel(
   const int b0 = ptr[row], b1 = ptr[row + 1];
   for (int base = b0; base < b1; base += kWave) {
     const int cnt = min(kWave, b1 - base);
+    float Y[L];
+    int e = -1;
     if (lane < cnt) {
       const int k = base + lane;
-      const int e = perm ? perm[k] : k;
+      e = perm ? perm[k] : k;
       float ux, uy, uz, inv;
       edge_unit(vec, e, pos, cl, src, shift, (int)row, sign, ux, uy, uz, inv);
-      float Y[L];
       sh_eval<LMAX, float>(ux, uy, uz, Y);
+    } else {
 #pragma unroll
-      for (int m = 0; m < L; ++m) sY[wave][lane][m] = Y[m];
+      for (int m = 0; m < L; ++m) Y[m] = 0.f;
     }
+#pragma unroll
+    for (int m = 0; m < L; ++m) sY[wave][lane][m] = Y[m];
+    sE[wave][lane] = e;
     wave_sync();
     if (own) {
-      int j = 0;
-      for (; j + 2 <= cnt; j += 2) {
-        const int e0 = perm ? perm[base + j] : base + j;
-        const int e1 = perm ? perm[base + j + 1] : base + j + 1;
-        float p0[CPL], p1[CPL];
+      for (int j = 0; j < cnt; j += kUnroll) {
+        float p[kUnroll][CPL];
 #pragma unroll
-        for (int q = 0; q < CPL; ++q) {
-          p0[q] = (c0 + q < C) ? phi[(int64_t)e0 * C + c0 + q] : 0.f;
-          p1[q] = (c0 + q < C) ? phi[(int64_t)e1 * C + c0 + q] : 0.f;
+        for (int u = 0; u < kUnroll; ++u) {
+          const int eu = sE[wave][j + u < kWave ? j + u : kWave - 1];
+          if (j + u < cnt)
+            load_channels<CPL, VEC>(phi + (int64_t)eu * C, c0, C, p[u]);
+          else
+#pragma unroll
+            for (int q = 0; q < CPL; ++q) p[u][q] = 0.f;
         }
 #pragma unroll
-        for (int m = 0; m < L; ++m) {
-          const float y0 = sY[wave][j][m], y1 = sY[wave][j + 1][m];
+        for (int u = 0; u < kUnroll; ++u) {
+          if (j + u >= kWave) break;
 #pragma unroll
-          for (int q = 0; q < CPL; ++q) acc[q][m] += p0[q] * y0 + p1[q] * y1;
-        }
-      }
-      for (; j < cnt; ++j) {
-        const int e0 = perm ? perm[base + j] : base + j;
-        float p0[CPL];
+          for (int m = 0; m < L; ++m) {
+            const float y = sY[wave][j + u][m];
 #pragma unroll
-        for (int q = 0; q < CPL; ++q) p0[q] = (c0 + q < C) ? phi[(int64_t)e0 * C + c0 + q] : 0.f;
-#pragma unroll
-        for (int m = 0; m < L; ++m) {
-          const float y0 = sY[wave][j][m];
-#pragma unroll
-          for (int q = 0; q < CPL; ++q) acc[q][m] += p0[q] * y0;
+            for (int q = 0; q < CPL; ++q) acc[q][m] += p[u][q] * y;
+          }
         }
       }
     }
@@ -126,43 +154,49 @@ __global__ __launch_bounds__(256) void sh_msg_fwd_kernel(
     for (int q = 0; q < CPL; ++q) {
       if (c0 + q >= C) break;
       float* o = out + ((int64_t)row * C + c0 + q) * L;
+      if constexpr (L % 4 == 0) {
 #pragma unroll
-      for (int m = 0; m < L; ++m) o[m] = acc[q][m];
+        for (int m = 0; m < L; m += 4)
+          *reinterpret_cast<float4*>(o + m) =
+              make_float4(acc[q][m], acc[q][m + 1], acc[q][m + 2], acc[q][m + 3]);
+      } else {
+#pragma unroll
+        for (int m = 0; m < L; ++m) o[m] = acc[q][m];
+      }
     }
   }
 }
 
-// Sum of p[0..LP) over the 64 lanes of a wave, returned so that lane l holds
-// the total of entry (l >> (6 - HALVINGS)). Each halving step trades half of
-// the live entries with the partner lane (17 shuffles for 16 entries instead
-// of 16 full reductions).
-template <int LP, int HALVINGS>
-__device__ inline float wave_transpose_reduce(float* p, int lane) {
-  int live = LP;
+// Sum of p[0..64) over the 64 lanes of a wave; lane l returns the total of entry l.
+// Six halving steps: at step h every lane keeps the half of its live entries selected
+// by bit (5 - h) of its lane id and adds the partner's copy of that half (63 shuffles
+// for 64 totals, all independent within a step).
+__device__ inline float wave_transpose_reduce64(float* p, int lane) {
 #pragma unroll
-  for (int h = 0; h < HALVINGS; ++h) {
+  for (int h = 0; h < 6; ++h) {
     const int mask = 32 >> h;
+    const int half = 32 >> h;
     const bool upper = (lane & mask) != 0;
-    const int half = live / 2;
 #pragma unroll
-    for (int k = 0; k < LP / 2; ++k) {
-      if (k < half) {
-        const float keep = upper ? p[k + half] : p[k];
-        const float send = upper ? p[k] : p[k + half];
-        p[k] = keep + __shfl_xor(send, mask, kWave);
-      }
+    for (int k = 0; k < half; ++k) {
+      const float keep = upper ? p[k + half] : p[k];
+      const float send = upper ? p[k] : p[k + half];
+      p[k] = keep + __shfl_xor(send, mask, kWave);
     }
-    live = half;
   }
-#pragma unroll
-  for (int h = HALVINGS; h < 6; ++h) p[0] += __shfl_xor(p[0], 32 >> h, kWave);
   return p[0];
 }
 
-template <typename G, int LMAX, int CPL>
+// Backward, one wave per receiver row: d_phi[e, c] = sum_lm d_out[i, c, lm] Y_lm(e)
+// (channel-owned lanes, no reduction) and dY[e, lm] = sum_c d_out[i, c, lm] phi[e, c]
+// (a reduction over channels, i.e. across lanes). Edges go in groups of GE = 64 / LP:
+// their partial sums fill 64 registers that one transpose-reduction turns into one
+// (edge, lm) total per lane, parked in LDS; lane j then chains dY of edge j through
+// the SH Jacobian to g_vec.
+template <typename G, int LMAX, int CPL, bool VEC>
 __global__ __launch_bounds__(256) void sh_msg_bwd_kernel(
-    const float* __restrict__ vec, const G* __restrict__ pos, const G* __restrict__ cell, int64_t n_graphs,
-    const int32_t* __restrict__ batch, const int32_t* __restrict__ src,
+    const float* __restrict__ vec, const G* __restrict__ pos, const G* __restrict__ cell,
+    int64_t n_graphs, const int32_t* __restrict__ batch, const int32_t* __restrict__ src,
     const int32_t* __restrict__ shift, const int32_t* __restrict__ ptr,
     const int32_t* __restrict__ perm, int64_t n_nodes, int C, float sign,
     const float* __restrict__ phi, const float* __restrict__ d_out, float* __restrict__ d_phi,
@@ -170,9 +204,10 @@ __global__ __launch_bounds__(256) void sh_msg_bwd_kernel(
   using D = ShDims<LMAX>;
   constexpr int L = D::L;
   constexpr int LP = D::LP;
-  constexpr int SHIFT = 6 - D::HALVINGS;
+  constexpr int GE = kWave / LP;  // edges per reduction group
   __shared__ float sY[kWavesPerBlock][kWave][L];
   __shared__ float sdY[kWavesPerBlock][kWave][LP];
+  __shared__ int sE[kWavesPerBlock][kWave];
   const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
   const int64_t row = (int64_t)blockIdx.x * kWavesPerBlock + wave;
   if (row >= n_nodes) return;
@@ -193,44 +228,60 @@ __global__ __launch_bounds__(256) void sh_msg_bwd_kernel(
     const int cnt = min(kWave, b1 - base);
     float ux = 0.f, uy = 0.f, uz = 0.f, inv = 0.f;
     int my_e = -1;
+    float Y[L];
     if (lane < cnt) {
       const int k = base + lane;
       my_e = perm ? perm[k] : k;
       edge_unit(vec, my_e, pos, cl, src, shift, (int)row, sign, ux, uy, uz, inv);
-      float Y[L];
       sh_eval<LMAX, float>(ux, uy, uz, Y);
+    } else {
 #pragma unroll
-      for (int m = 0; m < L; ++m) sY[wave][lane][m] = Y[m];
+      for (int m = 0; m < L; ++m) Y[m] = 0.f;
     }
+#pragma unroll
+    for (int m = 0; m < L; ++m) sY[wave][lane][m] = Y[m];
+    sE[wave][lane] = my_e;
     wave_sync();
-    for (int j = 0; j < cnt; ++j) {
-      const int e = perm ? perm[base + j] : base + j;
-      float p[CPL];
+    for (int j = 0; j < cnt; j += GE) {
+      float part[kWave];
 #pragma unroll
-      for (int q = 0; q < CPL; ++q) p[q] = (own && c0 + q < C) ? phi[(int64_t)e * C + c0 + q] : 0.f;
-      float part[LP];
+      for (int u0 = 0; u0 < GE; u0 += 4) {
+        constexpr int kSub = GE < 4 ? GE : 4;
+        float p[kSub][CPL];
 #pragma unroll
-      for (int m = 0; m < LP; ++m) part[m] = 0.f;
-      float dp[CPL];
+        for (int u = 0; u < kSub; ++u) {
+          const int eu = sE[wave][j + u0 + u];
+          if (own && j + u0 + u < cnt)
+            load_channels<CPL, VEC>(phi + (int64_t)eu * C, c0, C, p[u]);
+          else
 #pragma unroll
-      for (int q = 0; q < CPL; ++q) dp[q] = 0.f;
+            for (int q = 0; q < CPL; ++q) p[u][q] = 0.f;
+        }
 #pragma unroll
-      for (int m = 0; m < L; ++m) {
-        const float y = sY[wave][j][m];
+        for (int u = 0; u < kSub; ++u) {
+          float dp[CPL];
 #pragma unroll
-        for (int q = 0; q < CPL; ++q) {
-          dp[q] += g[q][m] * y;
-          part[m] += g[q][m] * p[q];
+          for (int q = 0; q < CPL; ++q) dp[q] = 0.f;
+#pragma unroll
+          for (int m = 0; m < LP; ++m) {
+            float acc = 0.f;
+            if (m < L) {
+              const float y = sY[wave][j + u0 + u][m];
+#pragma unroll
+              for (int q = 0; q < CPL; ++q) {
+                dp[q] += g[q][m] * y;
+                acc += g[q][m] * p[u][q];
+              }
+            }
+            part[(u0 + u) * LP + m] = acc;
+          }
+          if (own && j + u0 + u < cnt)
+            store_channels<CPL, VEC>(d_phi + (int64_t)sE[wave][j + u0 + u] * C, c0, C, dp);
         }
       }
-      if (own) {
-#pragma unroll
-        for (int q = 0; q < CPL; ++q)
-          if (c0 + q < C) d_phi[(int64_t)e * C + c0 + q] = dp[q];
-      }
       if (g_vec) {
-        const float tot = wave_transpose_reduce<LP, D::HALVINGS>(part, lane);
-        if ((lane & ((1 << SHIFT) - 1)) == 0) sdY[wave][j][lane >> SHIFT] = tot;
+        const float tot = wave_transpose_reduce64(part, lane);
+        sdY[wave][j + lane / LP][lane % LP] = tot;
       }
     }
     wave_sync();
@@ -312,38 +363,43 @@ __global__ __launch_bounds__(256) void segment_reduce_f64_kernel(const T* __rest
 }
 
 template <typename G>
-static int sh_msg(bool backward, const float* vec, const void* pos, int64_t n_nodes, const void* cell,
-                  int64_t n_graphs, const int32_t* batch, const int32_t* src,
+static int sh_msg(bool backward, const float* vec, const void* pos, int64_t n_nodes,
+                  const void* cell, int64_t n_graphs, const int32_t* batch, const int32_t* src,
                   const int32_t* shift, const int32_t* ptr, const int32_t* perm, int l_max,
                   int sign, int C, const float* phi, const float* d_out, float* out_or_dphi,
                   float* g_vec, hipStream_t stream) {
   if (n_nodes == 0) return XNN_OK;
   const dim3 grid(grid_1d(n_nodes, kWavesPerBlock)), block(kWavesPerBlock * kWave);
   const float sg = (float)sign;
-  const int cpl = (C + kWave - 1) / kWave;
-#define XNN_MSG(LM, CP)                                                                       \
-  do {                                                                                        \
-    if (backward)                                                                             \
-      hipLaunchKernelGGL((sh_msg_bwd_kernel<G, LM, CP>), grid, block, 0, stream, vec, (const G*)pos, \
-                         (const G*)cell, n_graphs, batch, src, shift, ptr, perm, n_nodes, C,  \
-                         sg, phi, d_out, out_or_dphi, g_vec);                                 \
-    else                                                                                      \
-      hipLaunchKernelGGL((sh_msg_fwd_kernel<G, LM, CP>), grid, block, 0, stream, vec, (const G*)pos, \
-                         (const G*)cell, n_graphs, batch, src, shift, ptr, perm, n_nodes, C,  \
-                         sg, phi, out_or_dphi);                                               \
+  int cpl = (C + kWave - 1) / kWave;
+  if (cpl == 3) cpl = 4;
+  const bool vec_ok = (C % cpl) == 0;
+#define XNN_MSG(LM, CP, VE)                                                                  \
+  do {                                                                                       \
+    if (backward)                                                                            \
+      hipLaunchKernelGGL((sh_msg_bwd_kernel<G, LM, CP, VE>), grid, block, 0, stream, vec,     \
+                         (const G*)pos, (const G*)cell, n_graphs, batch, src, shift, ptr,     \
+                         perm, n_nodes, C, sg, phi, d_out, out_or_dphi, g_vec);              \
+    else                                                                                     \
+      hipLaunchKernelGGL((sh_msg_fwd_kernel<G, LM, CP, VE>), grid, block, 0, stream, vec,     \
+                         (const G*)pos, (const G*)cell, n_graphs, batch, src, shift, ptr,     \
+                         perm, n_nodes, C, sg, phi, out_or_dphi);                            \
   } while (0)
-#define XNN_MSG_L(CP)                    \
-  switch (l_max) {                       \
-    case 0: XNN_MSG(0, CP); break;       \
-    case 1: XNN_MSG(1, CP); break;       \
-    case 2: XNN_MSG(2, CP); break;       \
-    default: XNN_MSG(3, CP); break;      \
+#define XNN_MSG_L(CP, VE)                 \
+  switch (l_max) {                        \
+    case 0: XNN_MSG(0, CP, VE); break;    \
+    case 1: XNN_MSG(1, CP, VE); break;    \
+    case 2: XNN_MSG(2, CP, VE); break;    \
+    default: XNN_MSG(3, CP, VE); break;   \
   }
   switch (cpl) {
-    case 1: XNN_MSG_L(1); break;
-    case 2: XNN_MSG_L(2); break;
-    case 3:
-    case 4: XNN_MSG_L(4); break;
+    case 1: XNN_MSG_L(1, false); break;
+    case 2:
+      if (vec_ok) { XNN_MSG_L(2, true); } else { XNN_MSG_L(2, false); }
+      break;
+    case 4:
+      if (vec_ok) { XNN_MSG_L(4, true); } else { XNN_MSG_L(4, false); }
+      break;
     default: set_error("n_channels must be <= 256, got %d", C); return XNN_EINVAL;
   }
 #undef XNN_MSG_L
