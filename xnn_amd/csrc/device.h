@@ -206,36 +206,46 @@ __device__ inline void envelope_eval(const Radial<T>& R, T r, T& f, T& df) {
   }
 }
 
-// radial[k] = rbf_k(r) * f(r), optional derivative d radial[k] / dr
+// Per-edge state of the radial expansion: the envelope f(r), f'(r) and the clamped
+// radius, evaluated once; radial_k then gives rbf_k(r) f(r) and its r-derivative one
+// basis function at a time (no per-thread arrays, so nothing lands in scratch).
+template <typename T>
+struct RadialAt {
+  T r, rr, inv, f, df;
+  bool clamped;
+};
+
+template <typename T>
+__device__ inline RadialAt<T> radial_at(const Radial<T>& R, T r) {
+  RadialAt<T> a;
+  a.r = r;
+  envelope_eval(R, r, a.f, a.df);
+  // Bessel: r clamped at 1e-8 (radial.py:267-268)
+  a.clamped = r < T(1e-8);
+  a.rr = a.clamped ? T(1e-8) : r;
+  a.inv = T(1) / a.rr;
+  return a;
+}
+
 template <typename T, bool DERIV>
-__device__ inline void radial_eval(const Radial<T>& R, T r, T* __restrict__ u,
-                                   T* __restrict__ du) {
-  T f, df;
-  envelope_eval(R, r, f, df);
+__device__ inline void radial_k(const Radial<T>& R, const RadialAt<T>& a, int k, T& u, T& du) {
   if (R.basis == XNN_BASIS_BESSEL) {
-    // prefactor * sin(freq * r / rc) / r with r clamped at 1e-8 (radial.py:267-268)
-    const bool clamped = r < T(1e-8);
-    const T rr = clamped ? T(1e-8) : r;
-    const T inv = T(1) / rr;
-    for (int k = 0; k < R.K; ++k) {
-      const T a = R.table[k] * rr / R.rc;
-      T s, c;
-      dev_sincos(a, &s, &c);
-      const T b = R.prefactor * s * inv;
-      u[k] = b * f;
-      if constexpr (DERIV) {
-        const T db = clamped ? T(0) : R.prefactor * (c * (R.table[k] / R.rc) - s * inv) * inv;
-        du[k] = db * f + b * df;
-      }
+    // prefactor * sin(freq * r / rc) / r
+    const T w = R.table[k] / R.rc;
+    T s, c;
+    dev_sincos(R.table[k] * a.rr / R.rc, &s, &c);
+    const T b = R.prefactor * s * a.inv;
+    u = b * a.f;
+    if constexpr (DERIV) {
+      const T db = a.clamped ? T(0) : R.prefactor * (c * w - s * a.inv) * a.inv;
+      du = db * a.f + b * a.df;
     }
   } else {
     // exp(-gamma (r - mu_k)^2)  (radial.py:73-75)
-    for (int k = 0; k < R.K; ++k) {
-      const T dd = r - R.table[k];
-      const T b = dev_exp(-R.gamma * dd * dd);
-      u[k] = b * f;
-      if constexpr (DERIV) du[k] = T(-2) * R.gamma * dd * b * f + b * df;
-    }
+    const T dd = a.r - R.table[k];
+    const T b = dev_exp(-R.gamma * dd * dd);
+    u = b * a.f;
+    if constexpr (DERIV) du = T(-2) * R.gamma * dd * b * a.f + b * a.df;
   }
 }
 

@@ -79,9 +79,12 @@ __global__ __launch_bounds__(256) void featurize_fwd_kernel(
     for (int k = 0; k < L; ++k) sh[e * L + k] = Y[k];
   }
   if (radial) {
-    T u[kMaxRbf];
-    radial_eval<T, false>(R, r, u, nullptr);
-    for (int k = 0; k < R.K; ++k) radial[e * R.K + k] = u[k];
+    const RadialAt<T> a = radial_at(R, r);
+    for (int k = 0; k < R.K; ++k) {
+      T u, du;
+      radial_k<T, false>(R, a, k, u, du);
+      radial[e * R.K + k] = u;
+    }
   }
 }
 
@@ -113,9 +116,12 @@ __global__ __launch_bounds__(256) void featurize_bwd_kernel(
   }
   T dl = d_length ? d_length[e] : T(0);
   if (d_radial) {
-    T u[kMaxRbf], du[kMaxRbf];
-    radial_eval<T, true>(R, r, u, du);
-    for (int k = 0; k < R.K; ++k) dl += d_radial[e * R.K + k] * du[k];
+    const RadialAt<T> a = radial_at(R, r);
+    for (int k = 0; k < R.K; ++k) {
+      T u, du;
+      radial_k<T, true>(R, a, k, u, du);
+      dl += d_radial[e * R.K + k] * du;
+    }
   }
   ox += dl * ux;
   oy += dl * uy;

@@ -168,22 +168,24 @@ __global__ __launch_bounds__(256) void sh_msg_fwd_kernel(
 }
 
 // Sum of p[0..64) over the 64 lanes of a wave; lane l returns the total of entry l.
-// Six halving steps: at step h every lane keeps the half of its live entries selected
-// by bit (5 - h) of its lane id and adds the partner's copy of that half (63 shuffles
-// for 64 totals, all independent within a step).
-__device__ inline float wave_transpose_reduce64(float* p, int lane) {
+// Six halving steps: at the step of width HALF every lane keeps the half of its live
+// entries selected by lane bit HALF and adds the partner's copy of that half (63
+// shuffles for 64 totals, independent within a step). Template recursion keeps every
+// index a compile-time constant, so p stays in registers.
+template <int HALF>
+__device__ __forceinline__ void halving_step(float* p, int lane) {
+  const bool upper = (lane & HALF) != 0;
 #pragma unroll
-  for (int h = 0; h < 6; ++h) {
-    const int mask = 32 >> h;
-    const int half = 32 >> h;
-    const bool upper = (lane & mask) != 0;
-#pragma unroll
-    for (int k = 0; k < half; ++k) {
-      const float keep = upper ? p[k + half] : p[k];
-      const float send = upper ? p[k] : p[k + half];
-      p[k] = keep + __shfl_xor(send, mask, kWave);
-    }
+  for (int k = 0; k < HALF; ++k) {
+    const float keep = upper ? p[k + HALF] : p[k];
+    const float send = upper ? p[k] : p[k + HALF];
+    p[k] = keep + __shfl_xor(send, HALF, kWave);
   }
+  if constexpr (HALF > 1) halving_step<HALF / 2>(p, lane);
+}
+
+__device__ __forceinline__ float wave_transpose_reduce64(float* p, int lane) {
+  halving_step<32>(p, lane);
   return p[0];
 }
 
