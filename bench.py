@@ -133,6 +133,8 @@ def main() -> None:
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--config", default="water", choices=["water", "argon", "ragged"])
+    ap.add_argument("--graph", action=argparse.BooleanOptionalAction, default=True,
+                    help="time replays of the step captured as one HIP graph")
     ap.add_argument("--cpu-edges", type=int, default=480_000,
                     help="edges of the CPU-baseline sample (0 skips it)")
     args = ap.parse_args()
@@ -162,6 +164,7 @@ def main() -> None:
         out = step()
     kernels = ["xnn_sh_message_sum", "xnn_sh_message_sum_backward", "xnn_edge_featurize",
                "xnn_edge_featurize_backward", "xnn_edge_force_reduce"]
+    # eager pass: per-kernel HIP events on the launch stream
     _lib.timed.clear()
     _lib.time_launches(*kernels)
     torch.cuda.synchronize()
@@ -169,13 +172,45 @@ def main() -> None:
     for _ in range(args.steps):
         out = step()
     torch.cuda.synchronize()
-    elapsed = time.perf_counter() - t0
-    ms = elapsed / args.steps * 1e3
+    eager_ms = (time.perf_counter() - t0) / args.steps * 1e3
+    eager_forces = out["forces"].clone()
+    timed = {k: list(v) for k, v in _lib.timed.items()}
+    _lib.timed.clear()
     assert torch.isfinite(out["forces"]).all()
+
+    ms = eager_ms
+    graph_checked = None
+    if args.graph:
+        # the whole step (forward, forces and stress backward) as one HIP graph
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            for _ in range(3):
+                step()
+        torch.cuda.current_stream().wait_stream(side)
+        hip_graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(hip_graph):
+            static_out = step()
+        for _ in range(max(1, args.warmup)):
+            hip_graph.replay()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(args.steps):
+            hip_graph.replay()
+        torch.cuda.synchronize()
+        ms = (time.perf_counter() - t0) / args.steps * 1e3
+        # every replay must reproduce the eager forces bit for bit
+        graph_checked = bool(torch.equal(static_out["forces"], eager_forces))
+        eager_check = step()["forces"]
+        hip_graph.replay()
+        torch.cuda.synchronize()
+        graph_checked = graph_checked and bool(torch.equal(static_out["forces"], eager_check))
+        if not graph_checked:
+            raise SystemExit("graph replay differs from the eager step")
 
     per_kernel = {}
     for name in kernels:
-        ev = _lib.timed.get(name, [])
+        ev = timed.get(name, [])
         if ev:
             per_kernel[name] = float(np.mean([s.elapsed_time(e) for s, e in ev])) * 1e3  # us
     _lib.timed.clear()
@@ -196,6 +231,8 @@ def main() -> None:
         "config": {"workload": workload, "atoms": N, "edges": E, "channels": C, "sh_components": L,
                    "n_rbf": kw["n_rbf"], "cutoff": rc, "stress": g.cell is not None,
                    "neighbor_list_ms": round(nl_ms, 3),
+                   "hip_graph": bool(args.graph), "eager_ms_per_step": round(eager_ms, 4),
+                   "graph_replay_matches_eager": graph_checked,
                    "step_algorithmic_bytes": ab["step"],
                    "step_hbm_fraction": round(step_gbs / HBM_PEAK_GBS, 4),
                    "kernel_mean_us": {k: round(v, 2) for k, v in per_kernel.items()}},

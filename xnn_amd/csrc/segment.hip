@@ -332,35 +332,51 @@ __global__ __launch_bounds__(256) void gather_rows_kernel(const T* __restrict__ 
   out[t] = src[(int64_t)index[e] * F + f];
 }
 
-// one block per segment; features in chunks of 8 held in registers
-template <typename T>
-__global__ __launch_bounds__(256) void segment_reduce_f64_kernel(const T* __restrict__ src,
-                                                                 int64_t F,
-                                                                 const int64_t* __restrict__ seg,
-                                                                 double* __restrict__ out) {
-  __shared__ double red[256][8];
+// One block per segment; every thread sums a strided share of the segment's rows for
+// up to 16 features in registers, then a fixed tree (wave shuffles, then one LDS row
+// per wave) combines them: deterministic, float64 throughout.
+template <typename T, int BLOCK>
+__global__ __launch_bounds__(BLOCK) void segment_reduce_f64_kernel(const T* __restrict__ src,
+                                                                   int64_t F,
+                                                                   const int64_t* __restrict__ seg,
+                                                                   double* __restrict__ out) {
+  constexpr int kF = 16;
+  constexpr int kWaves = BLOCK / kWave;
+  __shared__ double red[kWaves][kF];
   const int64_t b = blockIdx.x;
   const int64_t i0 = seg[b], i1 = seg[b + 1];
-  for (int64_t f0 = 0; f0 < F; f0 += 8) {
-    const int nf = (int)min<int64_t>(8, F - f0);
-    double acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-    for (int64_t i = i0 + threadIdx.x; i < i1; i += blockDim.x) {
+  const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+  for (int64_t f0 = 0; f0 < F; f0 += kF) {
+    const int nf = (int)min<int64_t>(kF, F - f0);
+    double acc[kF];
 #pragma unroll
-      for (int q = 0; q < 8; ++q)
-        if (q < nf) acc[q] += (double)src[i * F + f0 + q];
+    for (int q = 0; q < kF; ++q) acc[q] = 0.0;
+    for (int64_t i = i0 + threadIdx.x; i < i1; i += BLOCK) {
+      const T* r = src + i * F + f0;
+#pragma unroll
+      for (int q = 0; q < kF; ++q)
+        if (q < nf) acc[q] += (double)r[q];
     }
 #pragma unroll
-    for (int q = 0; q < 8; ++q) red[threadIdx.x][q] = acc[q];
-    __syncthreads();
-    for (int s = 128; s > 0; s >>= 1) {
-      if ((int)threadIdx.x < s) {
+    for (int m = kWave / 2; m > 0; m >>= 1)
 #pragma unroll
-        for (int q = 0; q < 8; ++q) red[threadIdx.x][q] += red[threadIdx.x + s][q];
+      for (int q = 0; q < kF; ++q) acc[q] += __shfl_xor(acc[q], m, kWave);
+    if (kWaves > 1) {
+      if (lane == 0)
+#pragma unroll
+        for (int q = 0; q < kF; ++q) red[wave][q] = acc[q];
+      __syncthreads();
+      if (threadIdx.x < kF) {
+        double t = 0.0;
+        for (int w = 0; w < kWaves; ++w) t += red[w][threadIdx.x];
+        if ((int)threadIdx.x < nf) out[b * F + f0 + threadIdx.x] = t;
       }
       __syncthreads();
+    } else if (lane == 0) {
+#pragma unroll
+      for (int q = 0; q < kF; ++q)
+        if (q < nf) out[b * F + f0 + q] = acc[q];
     }
-    if (threadIdx.x < (unsigned)nf) out[b * F + f0 + threadIdx.x] = red[0][threadIdx.x];
-    __syncthreads();
   }
 }
 
@@ -532,16 +548,20 @@ int xnn_segment_reduce_f64(int dtype, const void* src, int64_t n_rows, int64_t n
   XNN_REQUIRE(n_rows >= 0 && n_features >= 0 && n_segments >= 0, "negative size");
   if (n_segments == 0 || n_features == 0) return XNN_OK;
   XNN_REQUIRE(seg_ptr && out && (n_rows == 0 || src), "NULL pointer");
-  if (dtype == XNN_F32)
-    hipLaunchKernelGGL((segment_reduce_f64_kernel<float>), dim3(n_segments), dim3(256), 0,
-                       as_hip(stream), (const float*)src, n_features, seg_ptr, out);
-  else if (dtype == XNN_F64)
-    hipLaunchKernelGGL((segment_reduce_f64_kernel<double>), dim3(n_segments), dim3(256), 0,
-                       as_hip(stream), (const double*)src, n_features, seg_ptr, out);
-  else {
+  // long segments (one structure of many atoms) get 1024 threads, short ones a wave
+  const bool wide = n_rows >= 1024 * n_segments;
+#define XNN_RED(T, B)                                                                          \
+  hipLaunchKernelGGL((segment_reduce_f64_kernel<T, B>), dim3(n_segments), dim3(B), 0,          \
+                     as_hip(stream), (const T*)src, n_features, seg_ptr, out)
+  if (dtype == XNN_F32) {
+    if (wide) XNN_RED(float, 1024); else XNN_RED(float, 64);
+  } else if (dtype == XNN_F64) {
+    if (wide) XNN_RED(double, 1024); else XNN_RED(double, 64);
+  } else {
     set_error("unsupported dtype %d", dtype);
     return XNN_EINVAL;
   }
+#undef XNN_RED
   XNN_LAUNCH_CHECK();
   return XNN_OK;
 }

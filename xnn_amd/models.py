@@ -64,7 +64,12 @@ class InteratomicPotential(nn.Module):
         return cls(**cfg.params)
 
     def aggregate_energy(self, node_energy: Tensor, data) -> Tensor:
-        """Per-structure energies in float64 (base.py:161-180)."""
+        """Per-structure energies in float64 (base.py:161-180); on a GPU over the
+        plan's structure ranges (no host synchronization, so it can be graph-captured)."""
+        if node_energy.is_cuda:
+            from .ops import structure_sum_op
+            plan = data.plan()
+            return structure_sum_op(node_energy, plan.node_ptr, plan.batch32)
         return structure_sum(node_energy, data.batch, data.num_graphs)
 
 
@@ -117,7 +122,12 @@ class ShEdgePotential(InteratomicPotential):
         _, sh, u = feat.embed(vec, sh_sign=self.sh_sign)
         phi = u @ self.W.to(u.dtype)
         msg = (phi[:, :, None] * sh[:, None, :]).reshape(vec.shape[0], -1)
-        out = scatter_sum(msg, data.edge_index[1], data.num_nodes)
+        if msg.is_cuda:
+            from .ops import segment_sum_op
+            plan = data.plan()
+            out = segment_sum_op(msg.contiguous(), plan.dst, plan.ptr_dst, plan.perm_dst)
+        else:
+            out = scatter_sum(msg, data.edge_index[1], data.num_nodes)
         return out.reshape(data.num_nodes, self.channels, -1)
 
     def forward(self, data) -> dict:
