@@ -143,10 +143,15 @@ int xnn_gather_rows(int dtype, const void* src, int64_t n_src_rows, int64_t n_fe
 
 /* Per-structure totals accumulated in float64 over contiguous node ranges
  * seg_ptr (B+1): out[b,f] = sum_{i in seg b} src[i,f]. Replaces structure_sum
- * (ops.py:531-557, fp64 accumulation) and structure_sums (ops.py:560-569). */
+ * (ops.py:531-557, fp64 accumulation) and structure_sums (ops.py:560-569).
+ * A single structure is reduced in two levels over many workgroups (partials in
+ * `workspace`, xnn_segment_reduce_workspace_bytes of it; NULL is allowed when that
+ * size is 0); several structures take one workgroup each. Fixed summation order. */
+size_t xnn_segment_reduce_workspace_bytes(int64_t n_rows, int64_t n_features,
+                                          int64_t n_segments);
 int xnn_segment_reduce_f64(int dtype, const void* src, int64_t n_rows, int64_t n_features,
                            const int64_t* seg_ptr, int64_t n_segments, double* out,
-                           xnn_stream_t stream);
+                           void* workspace, size_t workspace_bytes, xnn_stream_t stream);
 
 /* ------------------------------------------------------------------------ */
 /* Cell-list radius graph. Replaces build_neighbor_list (neighborlist.py:411-506):

@@ -62,7 +62,8 @@ _SIGNATURES = {
                                     i32, i32, vp, vp, vp, vp, vp],
     "xnn_segment_sum": [c_int, vp, i64, i64, vp, vp, i64, vp, vp],
     "xnn_gather_rows": [c_int, vp, i64, i64, vp, i64, vp, vp],
-    "xnn_segment_reduce_f64": [c_int, vp, i64, i64, vp, i64, vp, vp],
+    "xnn_segment_reduce_workspace_bytes": [i64, i64, i64],
+    "xnn_segment_reduce_f64": [c_int, vp, i64, i64, vp, i64, vp, vp, sz, vp],
     "xnn_radius_graph_plan": [i64, c_f64p, c_i32p, dbl, c_f64p, c_f64p, ctypes.POINTER(GridPlan)],
     "xnn_radius_graph_count": [c_int, vp, i64, vp, dbl, i32, ctypes.POINTER(GridPlan), vp, vp, vp],
     "xnn_radius_graph_fill": [c_int, vp, i64, vp, dbl, i32, ctypes.POINTER(GridPlan), vp, vp, i64,
@@ -76,7 +77,7 @@ _SIGNATURES = {
     "xnn_edge_plan": [vp, vp, i64, i64, vp, vp, vp, vp, vp, vp, vp, vp, vp, sz, vp],
 }
 _RESTYPES = {"xnn_last_error": ctypes.c_char_p, "xnn_scan_workspace_bytes": sz,
-             "xnn_edge_plan_workspace_bytes": sz}
+             "xnn_edge_plan_workspace_bytes": sz, "xnn_segment_reduce_workspace_bytes": sz}
 
 _lock = threading.Lock()
 _lib: Optional[ctypes.CDLL] = None
@@ -183,3 +184,12 @@ calls: dict = {}
 def count_call(name: str) -> None:
     """Record that a HIP entry point ran (tests assert the native path was taken)."""
     calls[name] = calls.get(name, 0) + 1
+
+
+def segment_reduce_f64(src: torch.Tensor, n_rows: int, n_features: int, seg_ptr: torch.Tensor,
+                       n_segments: int, out: torch.Tensor) -> None:
+    """``xnn_segment_reduce_f64`` with its workspace from the caching allocator."""
+    need = int(load().xnn_segment_reduce_workspace_bytes(n_rows, n_features, n_segments))
+    ws = torch.empty(max(need, 1), dtype=torch.uint8, device=out.device) if need else None
+    call("xnn_segment_reduce_f64", dtype_code(src.dtype), ptr(src), n_rows, n_features,
+         ptr(seg_ptr), n_segments, ptr(out), ptr(ws), need, stream(out.device))

@@ -168,18 +168,44 @@ __global__ __launch_bounds__(256) void sh_msg_fwd_kernel(
 }
 
 // Sum of p[0..64) over the 64 lanes of a wave; lane l returns the total of entry l.
-// Six halving steps: at the step of width HALF every lane keeps the half of its live
-// entries selected by lane bit HALF and adds the partner's copy of that half (63
-// shuffles for 64 totals, independent within a step). Template recursion keeps every
-// index a compile-time constant, so p stays in registers.
+// Six halving steps, one per lane bit from the top: at the step of width HALF every
+// lane keeps the half of its live entries selected by that bit and adds the partner's
+// copy of the same half. Cross-row steps (bits 5 and 4) use v_permlane32_swap /
+// v_permlane16_swap, which exchange the odd rows of one register with the even rows of
+// another, so keep + received is a plain sum of the two swapped registers. In-row steps
+// use DPP lane maps that flip the step's bit: row_mirror (l ^ 15), row_half_mirror
+// (l ^ 7), quad_perm xor 2 and xor 1. Together they pair every lane with every other
+// exactly once (63 exchanges for 64 totals, all independent within a step). Template
+// recursion keeps every index a compile-time constant, so p stays in registers.
 template <int HALF>
 __device__ __forceinline__ void halving_step(float* p, int lane) {
-  const bool upper = (lane & HALF) != 0;
+  if constexpr (HALF == 32 || HALF == 16) {
 #pragma unroll
-  for (int k = 0; k < HALF; ++k) {
-    const float keep = upper ? p[k + HALF] : p[k];
-    const float send = upper ? p[k] : p[k + HALF];
-    p[k] = keep + __shfl_xor(send, HALF, kWave);
+    for (int k = 0; k < HALF; ++k) {
+      const unsigned a = __float_as_uint(p[k]), b = __float_as_uint(p[k + HALF]);
+      unsigned lo, hi;
+      if constexpr (HALF == 32) {
+        const auto r = __builtin_amdgcn_permlane32_swap(a, b, false, false);
+        lo = r[0];
+        hi = r[1];
+      } else {
+        const auto r = __builtin_amdgcn_permlane16_swap(a, b, false, false);
+        lo = r[0];
+        hi = r[1];
+      }
+      p[k] = __uint_as_float(lo) + __uint_as_float(hi);
+    }
+  } else {
+    // DPP controls whose lane map flips bit HALF (and only lower bits)
+    constexpr int ctrl = HALF == 8 ? 0x140 : (HALF == 4 ? 0x141 : (HALF == 2 ? 0x4E : 0xB1));
+    const bool upper = (lane & HALF) != 0;
+#pragma unroll
+    for (int k = 0; k < HALF; ++k) {
+      const float keep = upper ? p[k + HALF] : p[k];
+      const float send = upper ? p[k] : p[k + HALF];
+      p[k] = keep + __uint_as_float(__builtin_amdgcn_update_dpp(
+                        0u, __float_as_uint(send), ctrl, 0xF, 0xF, false));
+    }
   }
   if constexpr (HALF > 1) halving_step<HALF / 2>(p, lane);
 }
@@ -334,17 +360,30 @@ __global__ __launch_bounds__(256) void gather_rows_kernel(const T* __restrict__ 
 
 // One block per segment; every thread sums a strided share of the segment's rows for
 // up to 16 features in registers, then a fixed tree (wave shuffles, then one LDS row
-// per wave) combines them: deterministic, float64 throughout.
+// per wave) combines them: deterministic, float64 throughout. With `chunks` > 1 the
+// single segment is split into that many contiguous row ranges, one per block, whose
+// totals land in `partial` for segment_finish_kernel.
 template <typename T, int BLOCK>
 __global__ __launch_bounds__(BLOCK) void segment_reduce_f64_kernel(const T* __restrict__ src,
                                                                    int64_t F,
                                                                    const int64_t* __restrict__ seg,
+                                                                   int chunks,
                                                                    double* __restrict__ out) {
   constexpr int kF = 16;
   constexpr int kWaves = BLOCK / kWave;
   __shared__ double red[kWaves][kF];
-  const int64_t b = blockIdx.x;
-  const int64_t i0 = seg[b], i1 = seg[b + 1];
+  int64_t b, i0, i1;
+  if (chunks > 1) {
+    b = blockIdx.x;
+    const int64_t s0 = seg[0], s1 = seg[1];
+    const int64_t per = (s1 - s0 + chunks - 1) / chunks;
+    i0 = min(s1, s0 + b * per);
+    i1 = min(s1, i0 + per);
+  } else {
+    b = blockIdx.x;
+    i0 = seg[b];
+    i1 = seg[b + 1];
+  }
   const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
   for (int64_t f0 = 0; f0 < F; f0 += kF) {
     const int nf = (int)min<int64_t>(kF, F - f0);
@@ -378,6 +417,25 @@ __global__ __launch_bounds__(BLOCK) void segment_reduce_f64_kernel(const T* __re
         if (q < nf) out[b * F + f0 + q] = acc[q];
     }
   }
+}
+
+// out[f] = sum over chunks k (in order) of partial[k, f]
+__global__ void segment_finish_kernel(const double* __restrict__ partial, int chunks, int64_t F,
+                                      double* __restrict__ out) {
+  for (int64_t f = threadIdx.x; f < F; f += blockDim.x) {
+    double t = 0.0;
+    for (int k = 0; k < chunks; ++k) t += partial[(int64_t)k * F + f];
+    out[f] = t;
+  }
+}
+
+constexpr int64_t kChunkRows = 2048;
+constexpr int kMaxChunks = 256;
+
+static int reduce_chunks(int64_t n_rows, int64_t n_segments) {
+  if (n_segments != 1 || n_rows < 2 * kChunkRows) return 1;
+  const int64_t c = (n_rows + kChunkRows - 1) / kChunkRows;
+  return (int)(c < kMaxChunks ? c : kMaxChunks);
 }
 
 template <typename G>
@@ -542,27 +600,43 @@ int xnn_gather_rows(int dtype, const void* src, int64_t n_src_rows, int64_t n_fe
   return XNN_OK;
 }
 
+size_t xnn_segment_reduce_workspace_bytes(int64_t n_rows, int64_t n_features,
+                                          int64_t n_segments) {
+  const int chunks = reduce_chunks(n_rows, n_segments);
+  return chunks > 1 ? sizeof(double) * (size_t)chunks * (size_t)n_features : 0;
+}
+
 int xnn_segment_reduce_f64(int dtype, const void* src, int64_t n_rows, int64_t n_features,
                            const int64_t* seg_ptr, int64_t n_segments, double* out,
-                           xnn_stream_t stream) {
+                           void* workspace, size_t workspace_bytes, xnn_stream_t stream) {
   XNN_REQUIRE(n_rows >= 0 && n_features >= 0 && n_segments >= 0, "negative size");
   if (n_segments == 0 || n_features == 0) return XNN_OK;
   XNN_REQUIRE(seg_ptr && out && (n_rows == 0 || src), "NULL pointer");
-  // long segments (one structure of many atoms) get 1024 threads, short ones a wave
-  const bool wide = n_rows >= 1024 * n_segments;
-#define XNN_RED(T, B)                                                                          \
-  hipLaunchKernelGGL((segment_reduce_f64_kernel<T, B>), dim3(n_segments), dim3(B), 0,          \
-                     as_hip(stream), (const T*)src, n_features, seg_ptr, out)
+  XNN_REQUIRE(dtype == XNN_F32 || dtype == XNN_F64, "unsupported dtype %d", dtype);
+  const int chunks = reduce_chunks(n_rows, n_segments);
+  const size_t need = xnn_segment_reduce_workspace_bytes(n_rows, n_features, n_segments);
+  XNN_REQUIRE(need == 0 || (workspace != nullptr && workspace_bytes >= need),
+              "workspace of %zu bytes needed", need);
+  hipStream_t s = as_hip(stream);
+  double* dest = chunks > 1 ? static_cast<double*>(workspace) : out;
+  const int64_t grid = chunks > 1 ? chunks : n_segments;
+  // long segments get 1024 threads, short ones (many small structures) a wave
+  const bool wide = chunks > 1 || n_rows >= 1024 * n_segments;
+#define XNN_RED(T, B)                                                                     \
+  hipLaunchKernelGGL((segment_reduce_f64_kernel<T, B>), dim3(grid), dim3(B), 0, s,         \
+                     (const T*)src, n_features, seg_ptr, chunks, dest)
   if (dtype == XNN_F32) {
-    if (wide) XNN_RED(float, 1024); else XNN_RED(float, 64);
-  } else if (dtype == XNN_F64) {
-    if (wide) XNN_RED(double, 1024); else XNN_RED(double, 64);
+    if (chunks > 1) XNN_RED(float, 256); else if (wide) XNN_RED(float, 1024); else XNN_RED(float, 64);
   } else {
-    set_error("unsupported dtype %d", dtype);
-    return XNN_EINVAL;
+    if (chunks > 1) XNN_RED(double, 256); else if (wide) XNN_RED(double, 1024); else XNN_RED(double, 64);
   }
 #undef XNN_RED
   XNN_LAUNCH_CHECK();
+  if (chunks > 1) {
+    hipLaunchKernelGGL(segment_finish_kernel, dim3(1), dim3(64), 0, s, dest, chunks, n_features,
+                       out);
+    XNN_LAUNCH_CHECK();
+  }
   return XNN_OK;
 }
 

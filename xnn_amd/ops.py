@@ -115,8 +115,7 @@ def force_reduce_op(g_edge: Tensor, cell_like: Optional[Tensor], batch32: Tensor
     if not want_cell:
         return grad_pos, grad_pos.new_zeros((0,))
     grad_cell = torch.empty((n_graphs, 9), dtype=torch.float64, device=dev)
-    _lib.call("xnn_segment_reduce_f64", _lib.XNN_F64, _lib.ptr(partial), n_nodes, 9,
-              _lib.ptr(node_ptr), n_graphs, _lib.ptr(grad_cell), s)
+    _lib.segment_reduce_f64(partial, n_nodes, 9, node_ptr, n_graphs, grad_cell)
     return grad_pos, grad_cell.view(n_graphs, 3, 3).to(gdt)
 
 
@@ -407,8 +406,7 @@ def structure_sum_op(src: Tensor, node_ptr: Tensor, batch32: Tensor) -> Tensor:
     for d in src.shape[1:]:
         F *= int(d)
     out = torch.empty((n_seg, *src.shape[1:]), dtype=torch.float64, device=dev)
-    _lib.call("xnn_segment_reduce_f64", _lib.dtype_code(src.dtype), _lib.ptr(src), src.shape[0],
-              F, _lib.ptr(node_ptr), n_seg, _lib.ptr(out), _lib.stream(dev))
+    _lib.segment_reduce_f64(src, src.shape[0], F, node_ptr, n_seg, out)
     return out
 
 
