@@ -6,6 +6,8 @@
 //                                message phi[e,c] Y_lm(e) never leaves registers
 // xnn_segment_sum / gather_rows  scatter_sum / gather_rows (ops.py:403-448, 494-528)
 // xnn_segment_reduce_f64         structure_sum(s) (ops.py:531-569), fp64 accumulation
+#include <algorithm>
+
 #include "common.h"
 #include "device.h"
 
@@ -87,81 +89,96 @@ __global__ __launch_bounds__(256) void sh_msg_fwd_kernel(
     const int32_t* __restrict__ perm, int64_t n_nodes, int C, float sign,
     const float* __restrict__ phi, float* __restrict__ out) {
   constexpr int L = ShDims<LMAX>::L;
-  constexpr int kUnroll = 8;
+  constexpr int kU = 8;  // edges per load group; two groups are in flight
   __shared__ float sY[kWavesPerBlock][kWave][L];
   __shared__ int sE[kWavesPerBlock][kWave];
   const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
-  const int64_t row = (int64_t)blockIdx.x * kWavesPerBlock + wave;
-  if (row >= n_nodes) return;  // whole wave; no block-level barriers below
-  const G* cl = cell == nullptr ? nullptr
-                                : (n_graphs <= 1 || batch == nullptr ? cell
-                                                                     : cell + 9 * (int64_t)batch[row]);
   const int c0 = lane * CPL;
   const bool own = c0 < C;
-  float acc[CPL][L];
+  const int64_t n_waves = (int64_t)gridDim.x * kWavesPerBlock;
+  // persistent waves: rows are dealt out round robin, so no wave idles at the tail
+  for (int64_t row = (int64_t)blockIdx.x * kWavesPerBlock + wave; row < n_nodes; row += n_waves) {
+    const G* cl = cell == nullptr ? nullptr
+                                  : (n_graphs <= 1 || batch == nullptr ? cell
+                                                                       : cell + 9 * (int64_t)batch[row]);
+    float acc[CPL][L];
 #pragma unroll
-  for (int q = 0; q < CPL; ++q)
+    for (int q = 0; q < CPL; ++q)
 #pragma unroll
-    for (int k = 0; k < L; ++k) acc[q][k] = 0.f;
+      for (int k = 0; k < L; ++k) acc[q][k] = 0.f;
 
-  const int b0 = ptr[row], b1 = ptr[row + 1];
-  for (int base = b0; base < b1; base += kWave) {
-    const int cnt = min(kWave, b1 - base);
-    float Y[L];
-    int e = -1;
-    if (lane < cnt) {
-      const int k = base + lane;
-      e = perm ? perm[k] : k;
-      float ux, uy, uz, inv;
-      edge_unit(vec, e, pos, cl, src, shift, (int)row, sign, ux, uy, uz, inv);
-      sh_eval<LMAX, float>(ux, uy, uz, Y);
-    } else {
+    const int b0 = ptr[row], b1 = ptr[row + 1];
+    for (int base = b0; base < b1; base += kWave) {
+      const int cnt = min(kWave, b1 - base);
+      float Y[L];
+      int e = -1;
+      if (lane < cnt) {
+        const int k = base + lane;
+        e = perm ? perm[k] : k;
+        float ux, uy, uz, inv;
+        edge_unit(vec, e, pos, cl, src, shift, (int)row, sign, ux, uy, uz, inv);
+        sh_eval<LMAX, float>(ux, uy, uz, Y);
+      } else {
 #pragma unroll
-      for (int m = 0; m < L; ++m) Y[m] = 0.f;
-    }
+        for (int m = 0; m < L; ++m) Y[m] = 0.f;
+      }
 #pragma unroll
-    for (int m = 0; m < L; ++m) sY[wave][lane][m] = Y[m];
-    sE[wave][lane] = e;
-    wave_sync();
-    if (own) {
-      for (int j = 0; j < cnt; j += kUnroll) {
-        float p[kUnroll][CPL];
+      for (int m = 0; m < L; ++m) sY[wave][lane][m] = Y[m];
+      sE[wave][lane] = e;
+      wave_sync();
+      if (own) {
+        float p[kU][CPL], pn[kU][CPL];
 #pragma unroll
-        for (int u = 0; u < kUnroll; ++u) {
-          const int eu = sE[wave][j + u < kWave ? j + u : kWave - 1];
-          if (j + u < cnt)
-            load_channels<CPL, VEC>(phi + (int64_t)eu * C, c0, C, p[u]);
+        for (int u = 0; u < kU; ++u) {
+          if (u < cnt)
+            load_channels<CPL, VEC>(phi + (int64_t)sE[wave][u] * C, c0, C, pn[u]);
           else
 #pragma unroll
-            for (int q = 0; q < CPL; ++q) p[u][q] = 0.f;
+            for (int q = 0; q < CPL; ++q) pn[u][q] = 0.f;
         }
+        for (int j = 0; j < cnt; j += kU) {
 #pragma unroll
-        for (int u = 0; u < kUnroll; ++u) {
-          if (j + u >= kWave) break;
+          for (int u = 0; u < kU; ++u)
 #pragma unroll
-          for (int m = 0; m < L; ++m) {
-            const float y = sY[wave][j + u][m];
+            for (int q = 0; q < CPL; ++q) p[u][q] = pn[u][q];
+          // the next group's loads go out before this group's arithmetic
 #pragma unroll
-            for (int q = 0; q < CPL; ++q) acc[q][m] += p[u][q] * y;
+          for (int u = 0; u < kU; ++u) {
+            const int t = j + kU + u;
+            if (t < cnt)
+              load_channels<CPL, VEC>(phi + (int64_t)sE[wave][t] * C, c0, C, pn[u]);
+            else
+#pragma unroll
+              for (int q = 0; q < CPL; ++q) pn[u][q] = 0.f;
+          }
+#pragma unroll
+          for (int u = 0; u < kU; ++u) {
+            if (j + u >= kWave) break;
+#pragma unroll
+            for (int m = 0; m < L; ++m) {
+              const float y = sY[wave][j + u][m];
+#pragma unroll
+              for (int q = 0; q < CPL; ++q) acc[q][m] += p[u][q] * y;
+            }
           }
         }
       }
+      wave_sync();
     }
-    wave_sync();
-  }
-  if (own) {
+    if (own) {
 #pragma unroll
-    for (int q = 0; q < CPL; ++q) {
-      if (c0 + q >= C) break;
-      float* o = out + ((int64_t)row * C + c0 + q) * L;
-      if constexpr (L % 4 == 0) {
+      for (int q = 0; q < CPL; ++q) {
+        if (c0 + q >= C) break;
+        float* o = out + ((int64_t)row * C + c0 + q) * L;
+        if constexpr (L % 4 == 0) {
 #pragma unroll
-        for (int m = 0; m < L; m += 4)
-          *reinterpret_cast<float4*>(o + m) =
-              make_float4(acc[q][m], acc[q][m + 1], acc[q][m + 2], acc[q][m + 3]);
-      } else {
+          for (int m = 0; m < L; m += 4)
+            *reinterpret_cast<float4*>(o + m) =
+                make_float4(acc[q][m], acc[q][m + 1], acc[q][m + 2], acc[q][m + 3]);
+        } else {
 #pragma unroll
-        for (int m = 0; m < L; ++m) o[m] = acc[q][m];
+          for (int m = 0; m < L; ++m) o[m] = acc[q][m];
+        }
       }
     }
   }
@@ -232,99 +249,114 @@ __global__ __launch_bounds__(256) void sh_msg_bwd_kernel(
   using D = ShDims<LMAX>;
   constexpr int L = D::L;
   constexpr int LP = D::LP;
-  constexpr int GE = kWave / LP;  // edges per reduction group
+  constexpr int GE = kWave / LP;            // edges per reduction group
+  constexpr int kSub = GE < 4 ? GE : 4;     // edges per load group
   __shared__ float sY[kWavesPerBlock][kWave][L];
   __shared__ float sdY[kWavesPerBlock][kWave][LP];
   __shared__ int sE[kWavesPerBlock][kWave];
   const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
-  const int64_t row = (int64_t)blockIdx.x * kWavesPerBlock + wave;
-  if (row >= n_nodes) return;
-  const G* cl = cell == nullptr ? nullptr
-                                : (n_graphs <= 1 || batch == nullptr ? cell
-                                                                     : cell + 9 * (int64_t)batch[row]);
   const int c0 = lane * CPL;
   const bool own = c0 < C;
-  float g[CPL][L];
+  const int64_t n_waves = (int64_t)gridDim.x * kWavesPerBlock;
+  for (int64_t row = (int64_t)blockIdx.x * kWavesPerBlock + wave; row < n_nodes; row += n_waves) {
+    const G* cl = cell == nullptr ? nullptr
+                                  : (n_graphs <= 1 || batch == nullptr ? cell
+                                                                       : cell + 9 * (int64_t)batch[row]);
+    float g[CPL][L];
 #pragma unroll
-  for (int q = 0; q < CPL; ++q)
+    for (int q = 0; q < CPL; ++q)
 #pragma unroll
-    for (int m = 0; m < L; ++m)
-      g[q][m] = (own && c0 + q < C) ? d_out[((int64_t)row * C + c0 + q) * L + m] : 0.f;
+      for (int m = 0; m < L; ++m)
+        g[q][m] = (own && c0 + q < C) ? d_out[((int64_t)row * C + c0 + q) * L + m] : 0.f;
 
-  const int b0 = ptr[row], b1 = ptr[row + 1];
-  for (int base = b0; base < b1; base += kWave) {
-    const int cnt = min(kWave, b1 - base);
-    float ux = 0.f, uy = 0.f, uz = 0.f, inv = 0.f;
-    int my_e = -1;
-    float Y[L];
-    if (lane < cnt) {
-      const int k = base + lane;
-      my_e = perm ? perm[k] : k;
-      edge_unit(vec, my_e, pos, cl, src, shift, (int)row, sign, ux, uy, uz, inv);
-      sh_eval<LMAX, float>(ux, uy, uz, Y);
-    } else {
+    const int b0 = ptr[row], b1 = ptr[row + 1];
+    for (int base = b0; base < b1; base += kWave) {
+      const int cnt = min(kWave, b1 - base);
+      float ux = 0.f, uy = 0.f, uz = 0.f, inv = 0.f;
+      int my_e = -1;
+      float Y[L];
+      if (lane < cnt) {
+        const int k = base + lane;
+        my_e = perm ? perm[k] : k;
+        edge_unit(vec, my_e, pos, cl, src, shift, (int)row, sign, ux, uy, uz, inv);
+        sh_eval<LMAX, float>(ux, uy, uz, Y);
+      } else {
 #pragma unroll
-      for (int m = 0; m < L; ++m) Y[m] = 0.f;
-    }
+        for (int m = 0; m < L; ++m) Y[m] = 0.f;
+      }
 #pragma unroll
-    for (int m = 0; m < L; ++m) sY[wave][lane][m] = Y[m];
-    sE[wave][lane] = my_e;
-    wave_sync();
-    for (int j = 0; j < cnt; j += GE) {
-      float part[kWave];
+      for (int m = 0; m < L; ++m) sY[wave][lane][m] = Y[m];
+      sE[wave][lane] = my_e;
+      wave_sync();
+      float pn[kSub][CPL];
 #pragma unroll
-      for (int u0 = 0; u0 < GE; u0 += 4) {
-        constexpr int kSub = GE < 4 ? GE : 4;
-        float p[kSub][CPL];
+      for (int u = 0; u < kSub; ++u) {
+        if (own && u < cnt)
+          load_channels<CPL, VEC>(phi + (int64_t)sE[wave][u] * C, c0, C, pn[u]);
+        else
 #pragma unroll
-        for (int u = 0; u < kSub; ++u) {
-          const int eu = sE[wave][j + u0 + u];
-          if (own && j + u0 + u < cnt)
-            load_channels<CPL, VEC>(phi + (int64_t)eu * C, c0, C, p[u]);
-          else
+          for (int q = 0; q < CPL; ++q) pn[u][q] = 0.f;
+      }
+      for (int j = 0; j < cnt; j += GE) {
+        float part[kWave];
 #pragma unroll
-            for (int q = 0; q < CPL; ++q) p[u][q] = 0.f;
-        }
+        for (int u0 = 0; u0 < GE; u0 += kSub) {
+          float p[kSub][CPL];
 #pragma unroll
-        for (int u = 0; u < kSub; ++u) {
-          float dp[CPL];
+          for (int u = 0; u < kSub; ++u)
 #pragma unroll
-          for (int q = 0; q < CPL; ++q) dp[q] = 0.f;
+            for (int q = 0; q < CPL; ++q) p[u][q] = pn[u][q];
+          // prefetch the next load group (in this reduction group or the next)
 #pragma unroll
-          for (int m = 0; m < LP; ++m) {
-            float acc = 0.f;
-            if (m < L) {
-              const float y = sY[wave][j + u0 + u][m];
+          for (int u = 0; u < kSub; ++u) {
+            const int t = j + u0 + kSub + u;
+            if (own && t < cnt)
+              load_channels<CPL, VEC>(phi + (int64_t)sE[wave][t] * C, c0, C, pn[u]);
+            else
 #pragma unroll
-              for (int q = 0; q < CPL; ++q) {
-                dp[q] += g[q][m] * y;
-                acc += g[q][m] * p[u][q];
-              }
-            }
-            part[(u0 + u) * LP + m] = acc;
+              for (int q = 0; q < CPL; ++q) pn[u][q] = 0.f;
           }
-          if (own && j + u0 + u < cnt)
-            store_channels<CPL, VEC>(d_phi + (int64_t)sE[wave][j + u0 + u] * C, c0, C, dp);
+#pragma unroll
+          for (int u = 0; u < kSub; ++u) {
+            float dp[CPL];
+#pragma unroll
+            for (int q = 0; q < CPL; ++q) dp[q] = 0.f;
+#pragma unroll
+            for (int m = 0; m < LP; ++m) {
+              float acc = 0.f;
+              if (m < L) {
+                const float y = sY[wave][j + u0 + u][m];
+#pragma unroll
+                for (int q = 0; q < CPL; ++q) {
+                  dp[q] += g[q][m] * y;
+                  acc += g[q][m] * p[u][q];
+                }
+              }
+              part[(u0 + u) * LP + m] = acc;
+            }
+            if (own && j + u0 + u < cnt)
+              store_channels<CPL, VEC>(d_phi + (int64_t)sE[wave][j + u0 + u] * C, c0, C, dp);
+          }
+        }
+        if (g_vec) {
+          const float tot = wave_transpose_reduce64(part, lane);
+          sdY[wave][j + lane / LP][lane % LP] = tot;
         }
       }
-      if (g_vec) {
-        const float tot = wave_transpose_reduce64(part, lane);
-        sdY[wave][j + lane / LP][lane % LP] = tot;
-      }
-    }
-    wave_sync();
-    if (g_vec && lane < cnt) {
-      float dY[L];
+      wave_sync();
+      if (g_vec && lane < cnt) {
+        float dY[L];
 #pragma unroll
-      for (int m = 0; m < L; ++m) dY[m] = sdY[wave][lane][m];
-      float Gx, Gy, Gz, vx, vy, vz;
-      sh_grad<LMAX, float>(ux, uy, uz, dY, Gx, Gy, Gz);
-      sh_chain<float>(ux, uy, uz, inv, Gx, Gy, Gz, vx, vy, vz);
-      g_vec[3 * (int64_t)my_e + 0] = sign * vx;
-      g_vec[3 * (int64_t)my_e + 1] = sign * vy;
-      g_vec[3 * (int64_t)my_e + 2] = sign * vz;
+        for (int m = 0; m < L; ++m) dY[m] = sdY[wave][lane][m];
+        float Gx, Gy, Gz, vx, vy, vz;
+        sh_grad<LMAX, float>(ux, uy, uz, dY, Gx, Gy, Gz);
+        sh_chain<float>(ux, uy, uz, inv, Gx, Gy, Gz, vx, vy, vz);
+        g_vec[3 * (int64_t)my_e + 0] = sign * vx;
+        g_vec[3 * (int64_t)my_e + 1] = sign * vy;
+        g_vec[3 * (int64_t)my_e + 2] = sign * vz;
+      }
+      wave_sync();
     }
-    wave_sync();
   }
 }
 
@@ -438,6 +470,48 @@ static int reduce_chunks(int64_t n_rows, int64_t n_segments) {
   return (int)(c < kMaxChunks ? c : kMaxChunks);
 }
 
+// compute units of the current device (cached per device id)
+static int device_cu_count();
+
+// blocks of `kernel` that stay resident on the whole device (all CUs), capped at `needed`
+static int64_t resident_blocks(const void* kernel, int block_threads, int64_t needed) {
+  // the occupancy of each kernel is queried once and kept (a handful of instantiations)
+  static const void* keys[128] = {nullptr};
+  static int values[128] = {0};
+  int per_cu = 0;
+  for (int i = 0; i < 128; ++i) {
+    if (keys[i] == kernel) {
+      per_cu = values[i];
+      break;
+    }
+    if (keys[i] == nullptr) {
+      if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, block_threads, 0) !=
+              hipSuccess ||
+          per_cu <= 0)
+        per_cu = 2;
+      keys[i] = kernel;
+      values[i] = per_cu;
+      break;
+    }
+  }
+  if (per_cu <= 0) per_cu = 2;
+  return std::max<int64_t>(1, std::min<int64_t>(needed, (int64_t)per_cu * device_cu_count()));
+}
+
+static int device_cu_count() {
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cached[dev] == 0) {
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        cus <= 0)
+      cus = 256;
+    cached[dev] = cus;
+  }
+  return cached[dev];
+}
+
 template <typename G>
 static int sh_msg(bool backward, const float* vec, const void* pos, int64_t n_nodes,
                   const void* cell, int64_t n_graphs, const int32_t* batch, const int32_t* src,
@@ -445,21 +519,28 @@ static int sh_msg(bool backward, const float* vec, const void* pos, int64_t n_no
                   int sign, int C, const float* phi, const float* d_out, float* out_or_dphi,
                   float* g_vec, hipStream_t stream) {
   if (n_nodes == 0) return XNN_OK;
-  const dim3 grid(grid_1d(n_nodes, kWavesPerBlock)), block(kWavesPerBlock * kWave);
+  const int64_t blocks_needed = grid_1d(n_nodes, kWavesPerBlock);
+  const dim3 block(kWavesPerBlock * kWave);
   const float sg = (float)sign;
   int cpl = (C + kWave - 1) / kWave;
   if (cpl == 3) cpl = 4;
   const bool vec_ok = (C % cpl) == 0;
-#define XNN_MSG(LM, CP, VE)                                                                  \
-  do {                                                                                       \
-    if (backward)                                                                            \
-      hipLaunchKernelGGL((sh_msg_bwd_kernel<G, LM, CP, VE>), grid, block, 0, stream, vec,     \
-                         (const G*)pos, (const G*)cell, n_graphs, batch, src, shift, ptr,     \
-                         perm, n_nodes, C, sg, phi, d_out, out_or_dphi, g_vec);              \
-    else                                                                                     \
-      hipLaunchKernelGGL((sh_msg_fwd_kernel<G, LM, CP, VE>), grid, block, 0, stream, vec,     \
-                         (const G*)pos, (const G*)cell, n_graphs, batch, src, shift, ptr,     \
-                         perm, n_nodes, C, sg, phi, out_or_dphi);                            \
+  // persistent waves: exactly as many blocks as stay resident, never more than rows need
+#define XNN_MSG(LM, CP, VE)                                                                    \
+  do {                                                                                         \
+    if (backward) {                                                                            \
+      auto k = sh_msg_bwd_kernel<G, LM, CP, VE>;                                               \
+      const dim3 grid((unsigned)resident_blocks((const void*)k, block.x, blocks_needed));      \
+      hipLaunchKernelGGL(k, grid, block, 0, stream, vec, (const G*)pos, (const G*)cell,        \
+                         n_graphs, batch, src, shift, ptr, perm, n_nodes, C, sg, phi, d_out,    \
+                         out_or_dphi, g_vec);                                                  \
+    } else {                                                                                   \
+      auto k = sh_msg_fwd_kernel<G, LM, CP, VE>;                                               \
+      const dim3 grid((unsigned)resident_blocks((const void*)k, block.x, blocks_needed));      \
+      hipLaunchKernelGGL(k, grid, block, 0, stream, vec, (const G*)pos, (const G*)cell,        \
+                         n_graphs, batch, src, shift, ptr, perm, n_nodes, C, sg, phi,          \
+                         out_or_dphi);                                                         \
+    }                                                                                          \
   } while (0)
 #define XNN_MSG_L(CP, VE)                 \
   switch (l_max) {                        \
