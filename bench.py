@@ -27,6 +27,32 @@ import numpy as np
 import torch
 
 HBM_PEAK_GBS = 8000.0
+ROOT = os.path.dirname(os.path.abspath(__file__))
+TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "hbm_traffic_sh_msg_water_box.md")
+
+
+def measured_traffic(kernel: str, workload: str):
+    """HBM bytes per launch of ``kernel`` from the committed counter profile (FETCH_SIZE
+    and WRITE_SIZE passes scaled by the copy calibration), for the water box only."""
+    if workload != "water_box_9000_atoms_rc5" or not os.path.exists(TRAFFIC_PROFILE):
+        return None
+    for line in open(TRAFFIC_PROFILE):
+        f = line.split()
+        if len(f) == 3 and f[0] == "traffic_bytes_per_launch" and f[1] == kernel:
+            return int(f[2])
+    return None
+
+
+def copy_calibration() -> None:
+    """A plain device copy of 256 MiB, three launches: the known-size kernel that scales
+    the FETCH_SIZE / WRITE_SIZE counters of a profile run to bytes."""
+    n = 64 * 1024 * 1024
+    a = torch.ones(n, device="cuda")
+    b = torch.empty_like(a)
+    for _ in range(3):
+        b.copy_(a)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_bytes_per_launch": 4 * n, "launches": 3}), flush=True)
 
 
 def algorithmic_bytes(E: int, N: int, C: int, L: int = 16, K: int = 8) -> dict:
@@ -137,6 +163,8 @@ def main() -> None:
                     help="time replays of the step captured as one HIP graph")
     ap.add_argument("--cpu-edges", type=int, default=480_000,
                     help="edges of the CPU-baseline sample (0 skips it)")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="only run the 256 MiB copy that calibrates the HBM byte counters")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: this build has no multi-GPU path "
@@ -144,6 +172,9 @@ def main() -> None:
         raise SystemExit(2)
     if not torch.cuda.is_available():
         raise SystemExit("bench.py needs a GPU")
+    if args.copy_calibration:
+        copy_calibration()
+        return
     device = torch.device("cuda:0")
     torch.cuda.set_device(device)
     from xnn_amd import _lib
@@ -220,7 +251,7 @@ def main() -> None:
     achieved = ab[dominant] / (per_kernel[dominant] * 1e-6) / 1e9
     roofline = {"bound": "hbm", "kernel": dominant, "achieved": round(achieved, 1),
                 "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-                "traffic": None, "algorithmic_bytes": ab[dominant],
+                "traffic": measured_traffic(dominant, workload), "algorithmic_bytes": ab[dominant],
                 "mean_launch_us": round(per_kernel[dominant], 2)}
     step_gbs = ab["step"] / (ms * 1e-3) / 1e9
     result = {
