@@ -217,13 +217,19 @@ def test_edge_embed_and_backward(radial, envelope, l_max, sign, dtype):
 
 
 # --------------------------------------------------------------------------- aggregation
-@pytest.mark.parametrize("C,l_max", [(128, 3), (64, 3), (32, 2), (96, 1), (200, 0)])
-def test_sh_message_sum_forward_backward(C, l_max):
+@pytest.mark.parametrize("C,l_max,mfma", [(128, 3, True), (128, 3, False), (64, 3, True),
+                                          (48, 3, True), (16, 3, True), (32, 2, True),
+                                          (96, 1, True), (96, 1, False), (64, 0, True),
+                                          (200, 0, True), (256, 3, True)])
+def test_sh_message_sum_forward_backward(C, l_max, mfma, monkeypatch):
+    """Matrix-core kernels (C = 16 T, T in 1..4, 6, 8) and vector-ALU kernels (the rest,
+    or XNN_AMD_MESSAGE_MFMA=0) against the materialized messages of the oracle."""
     import oracle.reference as R
     import xnn_amd as xa
     from xnn_amd import synthetic
     from xnn_amd.ops import sh_message_sum
-    _note(f"sh_message_sum C={C} l_max={l_max}")
+    monkeypatch.setenv("XNN_AMD_MESSAGE_MFMA", "1" if mfma else "0")
+    _note(f"sh_message_sum C={C} l_max={l_max} mfma={mfma}")
     s = synthetic.water_box(n_molecules=216, box=18.6, grid=6, seed=2)
     g = xa.structure_to_graph(s.as_dict(), 5.0, device=DEV)
     g.pos = g.pos.float()

@@ -7,6 +7,8 @@
 // xnn_segment_sum / gather_rows  scatter_sum / gather_rows (ops.py:403-448, 494-528)
 // xnn_segment_reduce_f64         structure_sum(s) (ops.py:531-569), fp64 accumulation
 #include <algorithm>
+#include <cstdint>
+#include <cstdlib>
 
 #include "common.h"
 #include "device.h"
@@ -360,6 +362,304 @@ __global__ __launch_bounds__(256) void sh_msg_bwd_kernel(
   }
 }
 
+// ---------------------------------------------------------------- matrix-core message kernels
+// Per receiver row both message contractions are small matrix products:
+//   forward   A_i^T (L x C)  = Y_i^T (L x E_i) . phi_i (E_i x C)
+//   backward  d_phi (E_i x C) = Y_i (E_i x L) . G_i^T (L x C),  dY (E_i x L) = phi_i . G_i
+// with G_i = d_out[i] (C x L). They run on v_mfma_f32_16x16x4_f32 (float32 inputs,
+// float32 accumulation): per 16 x 16 x 4 block, lane l supplies A[l % 16][l / 16] and
+// B[l / 16][l % 16] and receives D[4 (l / 16) + r][l % 16] in register r. The harmonic
+// dimension is padded to 16 with zeros; channel tile t of width 16 holds channels
+// c = 16-row index * T + t, which makes every lane's operand and result runs contiguous
+// in memory. C = 16 T.
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ floatx4 mfma_16x16x4(float a, float b, floatx4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
+// N consecutive floats at p (vector accesses: p is 4N-byte aligned within 16 bytes)
+template <int N>
+__device__ __forceinline__ void load_run(const float* __restrict__ p, float* v) {
+  if constexpr (N % 4 == 0) {
+#pragma unroll
+    for (int q = 0; q < N; q += 4) {
+      const float4 x = *reinterpret_cast<const float4*>(p + q);
+      v[q] = x.x; v[q + 1] = x.y; v[q + 2] = x.z; v[q + 3] = x.w;
+    }
+  } else if constexpr (N % 2 == 0) {
+#pragma unroll
+    for (int q = 0; q < N; q += 2) {
+      const float2 x = *reinterpret_cast<const float2*>(p + q);
+      v[q] = x.x; v[q + 1] = x.y;
+    }
+  } else {
+#pragma unroll
+    for (int q = 0; q < N; ++q) v[q] = p[q];
+  }
+}
+
+template <int N>
+__device__ __forceinline__ void store_run(float* __restrict__ p, const float* v) {
+  if constexpr (N % 4 == 0) {
+#pragma unroll
+    for (int q = 0; q < N; q += 4)
+      *reinterpret_cast<float4*>(p + q) = make_float4(v[q], v[q + 1], v[q + 2], v[q + 3]);
+  } else if constexpr (N % 2 == 0) {
+#pragma unroll
+    for (int q = 0; q < N; q += 2) *reinterpret_cast<float2*>(p + q) = make_float2(v[q], v[q + 1]);
+  } else {
+#pragma unroll
+    for (int q = 0; q < N; ++q) p[q] = v[q];
+  }
+}
+
+constexpr int kSY = 17;  // LDS row stride of per-edge harmonics (spreads the banks)
+
+// Lane's edge of the batch (lanes < cnt), and the harmonics of that edge into ys
+// (row `lane`, 16 entries, zeros past l_max and past the batch's end).
+template <typename G, int LMAX>
+__device__ __forceinline__ void batch_harmonics(
+    const float* __restrict__ vec, const G* __restrict__ pos, const G* __restrict__ cl,
+    const int32_t* __restrict__ src, const int32_t* __restrict__ shift, int row, float sign,
+    int lane, int cnt, int e, float* ys, float& ux, float& uy, float& uz, float& inv) {
+  constexpr int L = ShDims<LMAX>::L;
+  float Y[L];
+  if (lane < cnt) {
+    edge_unit(vec, e, pos, cl, src, shift, row, sign, ux, uy, uz, inv);
+    sh_eval<LMAX, float>(ux, uy, uz, Y);
+  } else {
+    ux = uy = uz = inv = 0.f;
+#pragma unroll
+    for (int m = 0; m < L; ++m) Y[m] = 0.f;
+  }
+#pragma unroll
+  for (int m = 0; m < 16; ++m) ys[lane * kSY + m] = m < L ? Y[m] : 0.f;
+}
+
+// phi operand of the forward for k-steps k0 .. k0+KG-1 of a batch: lane l feeds edge
+// 4 k + l / 16 with channels [(l % 16) T, (l % 16) T + T)
+template <int T, int KG>
+__device__ __forceinline__ void fwd_phi_group(const float* __restrict__ phi, int k0, int cnt,
+                                              int my_e, int lo, int hi, float (&buf)[KG][T]) {
+#pragma unroll
+  for (int g = 0; g < KG; ++g) {
+    const int j = 4 * (k0 + g) + hi;
+    const int ej = __shfl(my_e, j & (kWave - 1));
+    if (j < cnt) {
+      load_run<T>(phi + (int64_t)ej * (16 * T) + lo * T, buf[g]);
+    } else {
+#pragma unroll
+      for (int t = 0; t < T; ++t) buf[g][t] = 0.f;
+    }
+  }
+}
+
+// Forward: one wave per receiver row (persistent, rows dealt round robin). Per batch of
+// 64 edges, lane j evaluates Y of edge j into LDS; then 4 edges per k-step:
+// A = Y^T (lm = l % 16, edge l / 16), B = phi (edge l / 16, channel (l % 16) T + t) for
+// tile t, so D[lm][channel] leaves each lane 4 consecutive lm of one channel: float4
+// stores of the (C, L) row.
+template <typename G, int LMAX, int T>
+__global__ __launch_bounds__(256) void sh_msg_fwd_mfma_kernel(
+    const float* __restrict__ vec, const G* __restrict__ pos, const G* __restrict__ cell,
+    int64_t n_graphs, const int32_t* __restrict__ batch, const int32_t* __restrict__ src,
+    const int32_t* __restrict__ shift, const int32_t* __restrict__ ptr,
+    const int32_t* __restrict__ perm, int64_t n_nodes, float sign,
+    const float* __restrict__ phi, float* __restrict__ out) {
+  constexpr int L = ShDims<LMAX>::L;
+  constexpr int C = 16 * T;
+  constexpr int KG = 2;  // k-steps per load group (8 edges); the next group is in flight
+  __shared__ float sY[kWavesPerBlock][kWave * kSY];
+  const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+  const int lo = lane & 15, hi = lane >> 4;
+  float* ys = sY[wave];
+  const int64_t n_waves = (int64_t)gridDim.x * kWavesPerBlock;
+  for (int64_t row = (int64_t)blockIdx.x * kWavesPerBlock + wave; row < n_nodes; row += n_waves) {
+    const G* cl = cell == nullptr ? nullptr
+                                  : (n_graphs <= 1 || batch == nullptr ? cell
+                                                                       : cell + 9 * (int64_t)batch[row]);
+    floatx4 acc[T];
+#pragma unroll
+    for (int t = 0; t < T; ++t) acc[t] = floatx4{0.f, 0.f, 0.f, 0.f};
+    const int b0 = ptr[row], b1 = ptr[row + 1];
+    for (int base = b0; base < b1; base += kWave) {
+      const int cnt = min(kWave, b1 - base);
+      const int my_e = lane < cnt ? (perm ? perm[base + lane] : base + lane) : 0;
+      const int nk = (cnt + 3) >> 2;
+      float cur[KG][T], nxt[KG][T];
+      // the first phi loads go out before the harmonics are evaluated
+      fwd_phi_group<T, KG>(phi, 0, cnt, my_e, lo, hi, cur);
+      float ux, uy, uz, inv;
+      batch_harmonics<G, LMAX>(vec, pos, cl, src, shift, (int)row, sign, lane, cnt, my_e, ys, ux,
+                               uy, uz, inv);
+      wave_sync();
+      for (int k0 = 0; k0 < nk; k0 += KG) {
+        if (k0 + KG < nk) fwd_phi_group<T, KG>(phi, k0 + KG, cnt, my_e, lo, hi, nxt);
+#pragma unroll
+        for (int g = 0; g < KG; ++g) {
+          if (k0 + g < nk) {
+            const float a = ys[(4 * (k0 + g) + hi) * kSY + lo];
+#pragma unroll
+            for (int t = 0; t < T; ++t) acc[t] = mfma_16x16x4(a, cur[g][t], acc[t]);
+          }
+        }
+#pragma unroll
+        for (int g = 0; g < KG; ++g)
+#pragma unroll
+          for (int t = 0; t < T; ++t) cur[g][t] = nxt[g][t];
+      }
+      wave_sync();  // ys is rewritten by the next batch
+    }
+    // lane holds A[row, channel lo T + t, lm 4 hi + r]
+    float* o = out + (int64_t)row * C * L;
+#pragma unroll
+    for (int t = 0; t < T; ++t) {
+      float* oc = o + (int64_t)(lo * T + t) * L;
+      if constexpr (L % 4 == 0) {
+        if (4 * hi < L)
+          *reinterpret_cast<float4*>(oc + 4 * hi) =
+              make_float4(acc[t][0], acc[t][1], acc[t][2], acc[t][3]);
+      } else {
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          if (4 * hi + r < L) oc[4 * hi + r] = acc[t][r];
+      }
+    }
+  }
+}
+
+// Backward: one wave per receiver row. The row's G = d_out[i] is staged through LDS into
+// two register layouts: gA[t][s] = G[lo T + t][4 s + hi] (A operand of d_phi, K = lm)
+// and gB[s] = G[hi Q + s][lo] (B operand of dY, K = channels, Q = C / 4). Per tile of 16
+// edges of a 64-edge batch:
+//   dY:     A = phi[edge lo][hi Q + s], B = gB[s], Q k-steps -> lane gets
+//           dY[edge 4 hi + r][lm lo], parked in LDS for the edge's own lane;
+//   d_phi:  A = gA[t][s], B = Y[edge lo][4 s + hi], ceil(L / 4) k-steps per tile t ->
+//           lane gets d_phi[edge lo][(4 hi + r) T + t]: channels [32 hi, 32 hi + 32) of
+//           one edge when T = 8, stored as float4 runs.
+// The next tile's phi loads go out before this tile's d_phi products.
+template <typename G, int LMAX, int T>
+__global__ __launch_bounds__(256) void sh_msg_bwd_mfma_kernel(
+    const float* __restrict__ vec, const G* __restrict__ pos, const G* __restrict__ cell,
+    int64_t n_graphs, const int32_t* __restrict__ batch, const int32_t* __restrict__ src,
+    const int32_t* __restrict__ shift, const int32_t* __restrict__ ptr,
+    const int32_t* __restrict__ perm, int64_t n_nodes, float sign,
+    const float* __restrict__ phi, const float* __restrict__ d_out, float* __restrict__ d_phi,
+    float* __restrict__ g_vec) {
+  constexpr int L = ShDims<LMAX>::L;
+  constexpr int C = 16 * T;
+  constexpr int Q = C / 4;
+  constexpr int KS = (L + 3) / 4;
+  static_assert(C * L <= 2 * kWave * kSY, "the staged d_out row must fit the LDS slice");
+  __shared__ __align__(16) float sbuf[kWavesPerBlock][2 * kWave * kSY];
+  const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+  const int lo = lane & 15, hi = lane >> 4;
+  float* ys = sbuf[wave];
+  float* sdy = sbuf[wave] + kWave * kSY;
+  const bool want_vec = g_vec != nullptr;
+  const int64_t n_waves = (int64_t)gridDim.x * kWavesPerBlock;
+  for (int64_t row = (int64_t)blockIdx.x * kWavesPerBlock + wave; row < n_nodes; row += n_waves) {
+    const int b0 = ptr[row], b1 = ptr[row + 1];
+    if (b0 == b1) continue;  // no edges: nothing to write
+    const G* cl = cell == nullptr ? nullptr
+                                  : (n_graphs <= 1 || batch == nullptr ? cell
+                                                                       : cell + 9 * (int64_t)batch[row]);
+    // stage G (C x L, contiguous) through LDS: coalesced float4 loads
+    {
+      const float4* g4 = reinterpret_cast<const float4*>(d_out + (int64_t)row * C * L);
+      float4* s4 = reinterpret_cast<float4*>(sbuf[wave]);
+      for (int i = lane; i < C * L / 4; i += kWave) s4[i] = g4[i];
+    }
+    wave_sync();
+    float gA[T][KS], gB[Q];
+#pragma unroll
+    for (int t = 0; t < T; ++t)
+#pragma unroll
+      for (int s = 0; s < KS; ++s) {
+        const int lm = 4 * s + hi;
+        gA[t][s] = lm < L ? sbuf[wave][(lo * T + t) * L + lm] : 0.f;
+      }
+#pragma unroll
+    for (int s = 0; s < Q; ++s) gB[s] = lo < L ? sbuf[wave][(hi * Q + s) * L + lo] : 0.f;
+    wave_sync();  // the staging area becomes ys / sdy
+
+    for (int base = b0; base < b1; base += kWave) {
+      const int cnt = min(kWave, b1 - base);
+      const int my_e = lane < cnt ? (perm ? perm[base + lane] : base + lane) : 0;
+      const int ntile = (cnt + 15) >> 4;
+      float pc[Q];
+      if (want_vec) {
+        const int ej = __shfl(my_e, lo);
+        if (lo < cnt) {
+          load_run<Q>(phi + (int64_t)ej * C + hi * Q, pc);
+        } else {
+#pragma unroll
+          for (int s = 0; s < Q; ++s) pc[s] = 0.f;
+        }
+      }
+      float ux, uy, uz, inv;
+      batch_harmonics<G, LMAX>(vec, pos, cl, src, shift, (int)row, sign, lane, cnt, my_e, ys, ux,
+                               uy, uz, inv);
+      wave_sync();
+      for (int tau = 0; tau < ntile; ++tau) {
+        const int je = 16 * tau + lo;  // this lane's edge column within the batch
+        if (want_vec) {
+          floatx4 dy = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int s = 0; s < Q; ++s) dy = mfma_16x16x4(pc[s], gB[s], dy);
+          // lane holds dY[edge 16 tau + 4 hi + r][lm lo]
+#pragma unroll
+          for (int r = 0; r < 4; ++r) sdy[(16 * tau + 4 * hi + r) * kSY + lo] = dy[r];
+          if (tau + 1 < ntile) {
+            const int jn = je + 16;
+            const int ej = __shfl(my_e, jn & (kWave - 1));
+            if (jn < cnt) {
+              load_run<Q>(phi + (int64_t)ej * C + hi * Q, pc);
+            } else {
+#pragma unroll
+              for (int s = 0; s < Q; ++s) pc[s] = 0.f;
+            }
+          }
+        }
+        floatx4 dp[T];
+#pragma unroll
+        for (int t = 0; t < T; ++t) dp[t] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int s = 0; s < KS; ++s) {
+          const float b = ys[je * kSY + 4 * s + hi];
+#pragma unroll
+          for (int t = 0; t < T; ++t) dp[t] = mfma_16x16x4(gA[t][s], b, dp[t]);
+        }
+        const int ej = __shfl(my_e, je & (kWave - 1));
+        if (je < cnt) {
+          float* drow = d_phi + (int64_t)ej * C;
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            float v[T];
+#pragma unroll
+            for (int t = 0; t < T; ++t) v[t] = dp[t][r];
+            store_run<T>(drow + (4 * hi + r) * T, v);
+          }
+        }
+      }
+      wave_sync();
+      if (want_vec && lane < cnt) {
+        float dY[L];
+#pragma unroll
+        for (int m = 0; m < L; ++m) dY[m] = sdy[lane * kSY + m];
+        float Gx, Gy, Gz, vx, vy, vz;
+        sh_grad<LMAX, float>(ux, uy, uz, dY, Gx, Gy, Gz);
+        sh_chain<float>(ux, uy, uz, inv, Gx, Gy, Gz, vx, vy, vz);
+        g_vec[3 * (int64_t)my_e + 0] = sign * vx;
+        g_vec[3 * (int64_t)my_e + 1] = sign * vy;
+        g_vec[3 * (int64_t)my_e + 2] = sign * vz;
+      }
+      wave_sync();
+    }
+  }
+}
+
 // ---------------------------------------------------------------- generic segment ops
 template <typename T, int GROUP>
 __global__ __launch_bounds__(256) void segment_sum_kernel(const T* __restrict__ src, int64_t F,
@@ -512,6 +812,15 @@ static int device_cu_count() {
   return cached[dev];
 }
 
+static bool aligned16(const void* p) { return p == nullptr || (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
+// XNN_AMD_MESSAGE_MFMA=0 in the environment selects the vector-ALU message kernels
+// (read at every call, so a process can compare the two)
+static bool message_mfma_enabled() {
+  const char* v = std::getenv("XNN_AMD_MESSAGE_MFMA");
+  return !(v != nullptr && v[0] == '0');
+}
+
 template <typename G>
 static int sh_msg(bool backward, const float* vec, const void* pos, int64_t n_nodes,
                   const void* cell, int64_t n_graphs, const int32_t* batch, const int32_t* src,
@@ -524,7 +833,8 @@ static int sh_msg(bool backward, const float* vec, const void* pos, int64_t n_no
   const float sg = (float)sign;
   int cpl = (C + kWave - 1) / kWave;
   if (cpl == 3) cpl = 4;
-  const bool vec_ok = (C % cpl) == 0;
+  const bool vec_ok = (C % cpl) == 0 && aligned16(phi) && aligned16(out_or_dphi) &&
+                      (!backward || aligned16(d_out));
   // persistent waves: exactly as many blocks as stay resident, never more than rows need
 #define XNN_MSG(LM, CP, VE)                                                                    \
   do {                                                                                         \
@@ -548,6 +858,47 @@ static int sh_msg(bool backward, const float* vec, const void* pos, int64_t n_no
     case 1: XNN_MSG(1, CP, VE); break;    \
     case 2: XNN_MSG(2, CP, VE); break;    \
     default: XNN_MSG(3, CP, VE); break;   \
+  }
+  // matrix-core kernels: C = 16 T with the tile counts instantiated below, 16-byte
+  // aligned rows (XNN_AMD_MESSAGE_MFMA=0 selects the vector-ALU kernels instead)
+  const int T = C / 16;
+  const bool aligned = aligned16(phi) && aligned16(out_or_dphi) && (!backward || aligned16(d_out));
+  if (aligned && C % 16 == 0 && (T <= 4 || T == 6 || T == 8) && message_mfma_enabled()) {
+#define XNN_MFMA(LM, TT)                                                                       \
+  do {                                                                                         \
+    if (backward) {                                                                            \
+      auto k = sh_msg_bwd_mfma_kernel<G, LM, TT>;                                              \
+      const dim3 grid((unsigned)resident_blocks((const void*)k, block.x, blocks_needed));      \
+      hipLaunchKernelGGL(k, grid, block, 0, stream, vec, (const G*)pos, (const G*)cell,        \
+                         n_graphs, batch, src, shift, ptr, perm, n_nodes, sg, phi, d_out,       \
+                         out_or_dphi, g_vec);                                                  \
+    } else {                                                                                   \
+      auto k = sh_msg_fwd_mfma_kernel<G, LM, TT>;                                              \
+      const dim3 grid((unsigned)resident_blocks((const void*)k, block.x, blocks_needed));      \
+      hipLaunchKernelGGL(k, grid, block, 0, stream, vec, (const G*)pos, (const G*)cell,        \
+                         n_graphs, batch, src, shift, ptr, perm, n_nodes, sg, phi,              \
+                         out_or_dphi);                                                         \
+    }                                                                                          \
+  } while (0)
+#define XNN_MFMA_L(TT)                    \
+  switch (l_max) {                        \
+    case 0: XNN_MFMA(0, TT); break;       \
+    case 1: XNN_MFMA(1, TT); break;       \
+    case 2: XNN_MFMA(2, TT); break;       \
+    default: XNN_MFMA(3, TT); break;      \
+  }
+    switch (T) {
+      case 1: XNN_MFMA_L(1); break;
+      case 2: XNN_MFMA_L(2); break;
+      case 3: XNN_MFMA_L(3); break;
+      case 4: XNN_MFMA_L(4); break;
+      case 6: XNN_MFMA_L(6); break;
+      default: XNN_MFMA_L(8); break;
+    }
+#undef XNN_MFMA_L
+#undef XNN_MFMA
+    XNN_LAUNCH_CHECK();
+    return XNN_OK;
   }
   switch (cpl) {
     case 1: XNN_MSG_L(1, false); break;
