@@ -4,13 +4,15 @@ Workload (``--config water``, the default): the 9,000-atom liquid water box (3,0
 H2O at 1.0 g/cm^3, cubic periodic cell of 44.8 A), cutoff 5.0 A, 8 Bessel radial
 functions x polynomial envelope, real SH l <= 3 (16 components), 128 float32 channels.
 A step is one evaluation of ``ForceStressOutput(ShEdgePotential)``: edge vectors ->
-fused featurizer -> PyTorch radial linear -> fused SH message sum into (N, 128, 16) ->
-readout -> float64 energy -> backward to forces and virial stress, all on the GPU with
-inputs resident in HBM. The neighbor list is timed separately (``neighbor_list_ms``).
+fused featurizer -> radial linear + SH message sum into (N, 128, 16) in one kernel (the
+per-edge weights phi = u W are formed on the matrix cores and never stored) -> readout
+-> float64 energy -> backward to forces and virial stress, all on the GPU with inputs
+resident in HBM. The neighbor list is timed separately (``neighbor_list_ms``).
 
 Prints one JSON line. ``value`` = edges / (forward + force/stress backward time).
-``roofline`` is the dominant kernel's algorithmic bytes per launch divided by its mean
-launch time, measured with HIP events on its launch stream during the timed steps.
+``roofline`` is the dominant kernel's algorithmic work per launch (HBM bytes, or fp32
+matrix-core flops when those bound it) divided by its mean launch time, measured with
+HIP events on its launch stream during the timed steps.
 ``cpu_baseline`` times the oracle's PyTorch-CPU restatement of the same step on the
 host cores (rank 0, N = 1 only).
 """
@@ -55,17 +57,44 @@ def copy_calibration() -> None:
     print(json.dumps({"copy_bytes_per_launch": 4 * n, "launches": 3}), flush=True)
 
 
-def algorithmic_bytes(E: int, N: int, C: int, L: int = 16, K: int = 8) -> dict:
-    """Compulsory bytes per launch of each kernel (int32 indices, packed shifts, float32
-    features): the accounting of the measurement plan, per edge and per node."""
+MFMA_F32_PEAK_TFLOPS = 157.3
+
+
+def kernel_costs(E: int, N: int, C: int, L: int = 16, K: int = 8, grouped: bool = True) -> dict:
+    """Compulsory HBM bytes and matrix-core flops per launch of each kernel: int32
+    indices, float32 features, edge vectors given (12 B per edge), no perm when the edges
+    come grouped by receiver. Flops count the true dimensions (no padding)."""
+    perm = 0 if grouped else 4
     return {
-        "xnn_sh_message_sum": E * (8 + 4 * C) + N * (4 * C * L + 16),
-        "xnn_sh_message_sum_backward": E * (8 + 8 * C + 12) + N * (4 * C * L + 16),
-        "xnn_edge_featurize": E * (8 + 4 * K) + N * 16,
-        "xnn_edge_featurize_backward": E * (4 * K + 8 + 12),
-        "xnn_edge_force_reduce": E * (12 + 4) + N * (12 + 16),
-        "step": E * (124 + 12 * C) + N * (76 + 8 * C * L),
+        "xnn_sh_linear_message_sum": {
+            "bytes": E * (12 + 4 * K + perm) + N * (4 * C * L + 4),
+            "flops": E * 2 * C * (K + L)},                 # phi = h W, then phi (x) Y
+        "xnn_sh_linear_message_sum_backward": {
+            "bytes": E * (12 + 4 * K + perm + 4 * K + 12) + N * (4 * C * L + 4),
+            "flops": E * 2 * C * (2 * K + 2 * L)},         # phi, dY, d_phi, d_h
+        "xnn_sh_message_sum": {
+            "bytes": E * (12 + 4 * C + perm) + N * (4 * C * L + 4),
+            "flops": E * 2 * C * L},
+        "xnn_sh_message_sum_backward": {
+            "bytes": E * (12 + 4 * C + perm + 4 * C + 12) + N * (4 * C * L + 4),
+            "flops": E * 4 * C * L},
+        "xnn_edge_featurize": {"bytes": E * (12 + 4 * K + 4), "flops": 0},
+        "xnn_edge_featurize_backward": {"bytes": E * (12 + 4 * K + 4 + 12 + 12), "flops": 0},
+        "xnn_edge_force_reduce": {"bytes": E * (12 + 4) + N * (12 + 72 + 8), "flops": 0},
     }
+
+
+def step_bytes(E: int, N: int, C: int, L: int, K: int, fused: bool) -> int:
+    """Compulsory traffic of one whole step: edge vectors from positions, featurizer,
+    message sum, readout (reads A), its backward (writes d_A), message backward,
+    featurizer backward, force reduction."""
+    kc = kernel_costs(E, N, C, L, K)
+    msg = "xnn_sh_linear_message_sum" if fused else "xnn_sh_message_sum"
+    linear = 0 if fused else 2 * (E * 4 * (K + C))      # u @ W and d_phi @ W^T
+    return (E * 24 + N * 12 + kc["xnn_edge_featurize"]["bytes"] + kc[msg]["bytes"]
+            + N * 4 * C * L + N * 4 * C * L + kc[msg + "_backward"]["bytes"]
+            + kc["xnn_edge_featurize_backward"]["bytes"] + kc["xnn_edge_force_reduce"]["bytes"]
+            + linear)
 
 
 def build_workload(config: str, device):
@@ -163,6 +192,9 @@ def main() -> None:
                     help="time replays of the step captured as one HIP graph")
     ap.add_argument("--cpu-edges", type=int, default=480_000,
                     help="edges of the CPU-baseline sample (0 skips it)")
+    ap.add_argument("--fused", action=argparse.BooleanOptionalAction, default=True,
+                    help="radial linear layer inside the message kernels (ShEdgePotential "
+                         "fused_linear)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run the 256 MiB copy that calibrates the HBM byte counters")
     args = ap.parse_args()
@@ -182,6 +214,7 @@ def main() -> None:
     _lib.load()
 
     g, model, rc, kw, workload, nl_ms, structs = build_workload(args.config, device)
+    model.fused_linear = bool(args.fused)
     E, N = g.num_edges, g.num_nodes
     C, L = kw["channels"], (kw["l_max"] + 1) ** 2
     wrapped = xa.ForceStressOutput(model, compute_stress=g.cell is not None).eval()
@@ -193,8 +226,11 @@ def main() -> None:
 
     for _ in range(args.warmup):
         out = step()
-    kernels = ["xnn_sh_message_sum", "xnn_sh_message_sum_backward", "xnn_edge_featurize",
-               "xnn_edge_featurize_backward", "xnn_edge_force_reduce"]
+    fused = bool(model.fused_linear and
+                 xa.ops.linear_message_supported(kw["n_rbf"], C, kw["l_max"]))
+    msg = "xnn_sh_linear_message_sum" if fused else "xnn_sh_message_sum"
+    kernels = [msg, msg + "_backward", "xnn_edge_featurize", "xnn_edge_featurize_backward",
+               "xnn_edge_force_reduce"]
     # eager pass: per-kernel HIP events on the launch stream
     _lib.timed.clear()
     _lib.time_launches(*kernels)
@@ -245,15 +281,29 @@ def main() -> None:
         if ev:
             per_kernel[name] = float(np.mean([s.elapsed_time(e) for s, e in ev])) * 1e3  # us
     _lib.timed.clear()
-    ab = algorithmic_bytes(E, N, C, L, kw["n_rbf"])
+    kc = kernel_costs(E, N, C, L, kw["n_rbf"], grouped=g.plan().perm_dst is None)
     total_us = {k: per_kernel[k] * (2 if k == "xnn_edge_featurize" else 1) for k in per_kernel}
     dominant = max(per_kernel, key=lambda k: total_us[k])
-    achieved = ab[dominant] / (per_kernel[dominant] * 1e-6) / 1e9
-    roofline = {"bound": "hbm", "kernel": dominant, "achieved": round(achieved, 1),
-                "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-                "traffic": measured_traffic(dominant, workload), "algorithmic_bytes": ab[dominant],
-                "mean_launch_us": round(per_kernel[dominant], 2)}
-    step_gbs = ab["step"] / (ms * 1e-3) / 1e9
+    launch_s = per_kernel[dominant] * 1e-6
+    cost = kc[dominant]
+    # the bound is whichever resource the kernel's compulsory work needs longer on
+    t_hbm = cost["bytes"] / (HBM_PEAK_GBS * 1e9)
+    t_mfma = cost["flops"] / (MFMA_F32_PEAK_TFLOPS * 1e12)
+    if t_mfma > t_hbm:
+        achieved = cost["flops"] / launch_s / 1e12
+        roofline = {"bound": "mfma", "kernel": dominant, "achieved": round(achieved, 2),
+                    "peak": MFMA_F32_PEAK_TFLOPS, "unit": "TFLOP/s",
+                    "frac": round(achieved / MFMA_F32_PEAK_TFLOPS, 4)}
+    else:
+        achieved = cost["bytes"] / launch_s / 1e9
+        roofline = {"bound": "hbm", "kernel": dominant, "achieved": round(achieved, 1),
+                    "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4)}
+    roofline.update({"traffic": measured_traffic(dominant, workload),
+                     "algorithmic_bytes": cost["bytes"], "algorithmic_flops": cost["flops"],
+                     "hbm_GBs": round(cost["bytes"] / launch_s / 1e9, 1),
+                     "mean_launch_us": round(per_kernel[dominant], 2)})
+    sb = step_bytes(E, N, C, L, kw["n_rbf"], fused)
+    step_gbs = sb / (ms * 1e-3) / 1e9
     result = {
         "metric": "edges/s fwd+force-bwd and % HBM roofline, 9k-atom water box, 1 MI355X",
         "value": E / (ms * 1e-3), "unit": "edges/s", "n_gpus": 1, "steps": args.steps,
@@ -264,7 +314,8 @@ def main() -> None:
                    "neighbor_list_ms": round(nl_ms, 3),
                    "hip_graph": bool(args.graph), "eager_ms_per_step": round(eager_ms, 4),
                    "graph_replay_matches_eager": graph_checked,
-                   "step_algorithmic_bytes": ab["step"],
+                   "fused_linear": fused,
+                   "step_algorithmic_bytes": sb,
                    "step_hbm_fraction": round(step_gbs / HBM_PEAK_GBS, 4),
                    "kernel_mean_us": {k: round(v, 2) for k, v in per_kernel.items()}},
         "roofline": roofline,

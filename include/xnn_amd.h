@@ -129,6 +129,35 @@ int xnn_sh_message_sum_backward(int geom_dtype, const float* vec_in, const void*
                                 const float* phi, const float* d_out, float* d_phi,
                                 float* g_vec, xnn_stream_t stream);
 
+/* The same aggregation with the edge weights formed by a linear layer in the kernel:
+ * phi[e,c] = sum_k h[e,k] W[k,c], the last layer of the edge-weight network
+ * (gnn/fast/conv.py:137-143 takes the weights from the radial network; the product
+ * and the receiver sum as in xnn_sh_message_sum). phi is formed per 16-edge tile on
+ * the matrix cores and never stored. h (E,K) f32 with K = n_features in [1, 8],
+ * W (K,C) f32 with C = n_channels in {32, 64, 128}, l_max in [1, 3]; out (N,C,L) f32,
+ * 16-byte aligned. Other shapes return XNN_EINVAL (use xnn_sh_message_sum). */
+int xnn_sh_linear_message_sum(int geom_dtype, const float* vec_in, const void* pos,
+                              int64_t n_nodes, const void* cell, int64_t n_graphs,
+                              const int32_t* batch, const int32_t* src, const int32_t* shift,
+                              int64_t n_edges, const int32_t* ptr_dst, const int32_t* perm_dst,
+                              int32_t l_max, int32_t sh_sign, int32_t n_features,
+                              int32_t n_channels, const float* h, const float* W, float* out,
+                              xnn_stream_t stream);
+
+/* Backward of xnn_sh_linear_message_sum with respect to h and the edge vectors:
+ * d_h[e,k] = sum_c (sum_lm d_out[dst,c,lm] Y_lm(e)) W[k,c] (written) and g_vec (E,3)
+ * (nullable; h may be NULL when g_vec is). d_W is not formed here: it is
+ * h^T d_phi with d_phi from xnn_sh_message_sum_backward. d_out 16-byte aligned. */
+int xnn_sh_linear_message_sum_backward(int geom_dtype, const float* vec_in, const void* pos,
+                                       int64_t n_nodes, const void* cell, int64_t n_graphs,
+                                       const int32_t* batch, const int32_t* src,
+                                       const int32_t* shift, int64_t n_edges,
+                                       const int32_t* ptr_dst, const int32_t* perm_dst,
+                                       int32_t l_max, int32_t sh_sign, int32_t n_features,
+                                       int32_t n_channels, const float* h, const float* W,
+                                       const float* d_out, float* d_h, float* g_vec,
+                                       xnn_stream_t stream);
+
 /* ------------------------------------------------------------------------ */
 /* Segmented sum over a CSR: out[i,:] = sum_{k in [ptr[i],ptr[i+1])} src[perm[k],:].
  * Replaces scatter_sum (common/models/ops.py:403-448) without atomics; its

@@ -255,6 +255,48 @@ def test_sh_message_sum_forward_backward(C, l_max, mfma, monkeypatch):
     assert torch.equal(A, A2)
 
 
+@pytest.mark.parametrize("C,l_max,K", [(128, 3, 8), (64, 3, 8), (32, 2, 8), (64, 1, 5),
+                                        (128, 2, 3)])
+def test_sh_linear_message_sum_forward_backward(C, l_max, K):
+    """The fused linear + message kernels against the oracle's materialized messages with
+    phi = h W, for A, d_h, the edge-vector gradient and d_W (the last through the
+    unfused backward)."""
+    import oracle.reference as R
+    import xnn_amd as xa
+    from xnn_amd import synthetic
+    from xnn_amd.ops import sh_linear_message_sum
+    _note(f"sh_linear_message_sum C={C} l_max={l_max} K={K}")
+    s = synthetic.water_box(n_molecules=216, box=18.6, grid=6, seed=3)
+    g = xa.structure_to_graph(s.as_dict(), 5.0, device=DEV)
+    g.pos = g.pos.float()
+    vec = g.edge_vectors().detach().requires_grad_(True)
+    gen = torch.Generator().manual_seed(100 * C + K)
+    h = torch.randn(vec.shape[0], K, generator=gen).to(DEV).requires_grad_(True)
+    W = (torch.randn(K, C, generator=gen) / K ** 0.5).to(DEV).requires_grad_(True)
+    A = sh_linear_message_sum(vec, h, W, g.plan(), l_max, 1)
+    dA = torch.randn(A.shape, generator=gen).to(DEV)
+    gvec, gh, gW = torch.autograd.grad((A * dA).sum(), (vec, h, W))
+    vc = vec.detach().cpu().double().requires_grad_(True)
+    hc = h.detach().cpu().double().requires_grad_(True)
+    Wc = W.detach().cpu().double().requires_grad_(True)
+    Y = R.e3nn_sh(l_max, vc)
+    phi = hc @ Wc
+    msg = (phi[:, :, None] * Y[:, None, :]).reshape(vc.shape[0], -1)
+    Ar = R.scatter_sum(msg, g.edge_index[1].cpu(), g.num_nodes).reshape(A.shape)
+    gv_r, gh_r, gW_r = torch.autograd.grad((Ar * dA.cpu().double()).sum(), (vc, hc, Wc))
+    scale = float(Ar.detach().abs().max())
+    np.testing.assert_allclose(A.detach().cpu().double(), Ar.detach(), atol=2e-6 * scale)
+    np.testing.assert_allclose(gh.cpu().double(), gh_r, atol=2e-5 * float(gh_r.abs().max()))
+    np.testing.assert_allclose(gvec.cpu().double(), gv_r, atol=2e-5 * max(1.0, float(gv_r.abs().max())))
+    np.testing.assert_allclose(gW.cpu().double(), gW_r, atol=2e-5 * float(gW_r.abs().max()))
+    # without weight gradients the d_W pass is skipped; the rest is unchanged
+    gvec2, gh2 = torch.autograd.grad((sh_linear_message_sum(vec, h, W.detach(), g.plan(), l_max, 1)
+                                      * dA).sum(), (vec, h))
+    assert torch.equal(gvec2, gvec) and torch.equal(gh2, gh)
+    A2 = sh_linear_message_sum(vec, h, W, g.plan(), l_max, 1)
+    assert torch.equal(A, A2)
+
+
 def test_segment_gather_and_structure_sums():
     import oracle.reference as R
     import xnn_amd as xa
@@ -287,8 +329,10 @@ def test_segment_gather_and_structure_sums():
 
 
 # --------------------------------------------------------------------------- full model
-@pytest.mark.parametrize("config", ["water", "argon", "ragged", "nequip_molecules"])
-def test_model_energy_forces_stress(config):
+@pytest.mark.parametrize("config,fused", [("water", True), ("water", False), ("argon", True),
+                                          ("ragged", True), ("nequip_molecules", True),
+                                          ("nequip_molecules", False)])
+def test_model_energy_forces_stress(config, fused):
     import oracle.reference as R
     import xnn_amd as xa
     from xnn_amd import _lib, synthetic
@@ -307,16 +351,18 @@ def test_model_energy_forces_stress(config):
         structs, rc = synthetic.random_molecules(32, seed=2), 5.0
         kw = dict(n_rbf=8, l_max=2, channels=32, radial_type="bessel", envelope="polynomial",
                   sh_sign=-1)
-    _note(f"model {config}")
+    _note(f"model {config} fused={fused}")
     graphs = [xa.structure_to_graph(st.as_dict(), rc, device=DEV) for st in structs]
     g = graphs[0] if len(graphs) == 1 else xa.collate(graphs)
     g.pos = g.pos.float()
     if g.cell is not None:
         g.cell = g.cell.float()
-    model = xa.ShEdgePotential(cutoff=rc, species=(1, 6, 7, 8, 18), **kw).to(DEV)
+    model = xa.ShEdgePotential(cutoff=rc, species=(1, 6, 7, 8, 18), fused_linear=fused,
+                               **kw).to(DEV)
     before = dict(_lib.calls)
     out = xa.ForceStressOutput(model, compute_stress=g.cell is not None).eval()(g)
-    for name in ("xnn_sh_message_sum", "xnn_sh_message_sum_backward", "xnn_edge_force_reduce",
+    msg = "xnn_sh_linear_message_sum" if fused else "xnn_sh_message_sum"
+    for name in (msg, msg + "_backward", "xnn_edge_force_reduce",
                  "xnn_edge_featurize", "xnn_edge_featurize_backward"):
         assert _lib.calls.get(name, 0) > before.get(name, 0), f"{name} did not run"
     params = dict(W=model.W.detach().cpu().double(), U=model.U.detach().cpu().double(),

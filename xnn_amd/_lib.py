@@ -60,6 +60,10 @@ _SIGNATURES = {
                            vp, vp, vp],
     "xnn_sh_message_sum_backward": [c_int, vp, vp, i64, vp, i64, vp, vp, vp, i64, vp, vp, i32,
                                     i32, i32, vp, vp, vp, vp, vp],
+    "xnn_sh_linear_message_sum": [c_int, vp, vp, i64, vp, i64, vp, vp, vp, i64, vp, vp, i32, i32,
+                                  i32, i32, vp, vp, vp, vp],
+    "xnn_sh_linear_message_sum_backward": [c_int, vp, vp, i64, vp, i64, vp, vp, vp, i64, vp, vp,
+                                           i32, i32, i32, i32, vp, vp, vp, vp, vp, vp],
     "xnn_segment_sum": [c_int, vp, i64, i64, vp, vp, i64, vp, vp],
     "xnn_gather_rows": [c_int, vp, i64, i64, vp, i64, vp, vp],
     "xnn_segment_reduce_workspace_bytes": [i64, i64, i64],

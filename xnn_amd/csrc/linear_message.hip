@@ -1,0 +1,383 @@
+// Fused edge-weight linear layer + SH message aggregation (gfx950, wave64, fp32 MFMA).
+//
+// xnn_sh_linear_message_sum(_backward): the per-edge channel weights are the output of
+// a linear layer, phi_e = h_e W (h: (E, K) with K <= 8, W: (K, C)), as the last layer of
+// the reference's radial weight network; they feed the uvu product with the edge
+// harmonics and the receiver sum, A_i[c, lm] = sum_{dst(e)=i} phi_e[c] Y_lm(sign r_e)
+// (gnn/fast/conv.py:137-143 with per-edge weights, + scatter_sum, ops.py:403-448).
+// phi is formed per 16-edge tile on the matrix cores and consumed in registers: it is
+// never stored, and the backward returns d_h = (G_i Y_e) W^T, so d_phi is never stored
+// either. Per tile, one wave:
+//   forward:  phi (16 x C) = h W   (edges in the M rows, permuted so that result register
+//             r of lane l is edge 4 r + l / 16, i.e. exactly the B operand of the next
+//             product), then A^T += Y^T phi over 4 k-steps of 4 edges;
+//   backward: phi^T = W^T h^T, dY = phi G (K = channels), d_phi = Y G^T, d_h = d_phi W^T
+//             (K = channels); dY goes through LDS to the edge's own lane for the SH
+//             Jacobian, as in the unfused kernels.
+// Channel tile t of width 16 holds channels 16-row index * T + t (C = 16 T).
+#include <algorithm>
+#include <cstdint>
+
+#include "common.h"
+#include "device.h"
+#include "message.h"
+
+namespace xnn {
+
+constexpr int kLinKMax = 8;  // h features: two k-steps of 4
+constexpr int kLinKK = 2;
+
+template <typename G, int LMAX, int T>
+__global__ __launch_bounds__(256) void lin_msg_fwd_kernel(
+    const float* __restrict__ vec, const G* __restrict__ pos, const G* __restrict__ cell,
+    int64_t n_graphs, const int32_t* __restrict__ batch, const int32_t* __restrict__ src,
+    const int32_t* __restrict__ shift, const int32_t* __restrict__ ptr,
+    const int32_t* __restrict__ perm, int64_t n_nodes, float sign, int K,
+    const float* __restrict__ h, const float* __restrict__ W, float* __restrict__ out) {
+  constexpr int L = ShDims<LMAX>::L;
+  constexpr int C = 16 * T;
+  constexpr int KK = kLinKK;
+  __shared__ float sY[kWavesPerBlock][kWave * kSY];
+  const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+  const int lo = lane & 15, hi = lane >> 4;
+  float* ys = sY[wave];
+  // B operand of h W for channel tile t, k-step q: W[4 q + hi][lo T + t]
+  float wB[KK][T];
+#pragma unroll
+  for (int q = 0; q < KK; ++q)
+#pragma unroll
+    for (int t = 0; t < T; ++t) {
+      const int k = 4 * q + hi;
+      wB[q][t] = k < K ? W[k * C + lo * T + t] : 0.f;
+    }
+  // M row lo of h W stands for edge 4 (lo % 4) + lo / 4 of the tile
+  const int hrow = 4 * (lo & 3) + (lo >> 2);
+  const int64_t n_waves = (int64_t)gridDim.x * kWavesPerBlock;
+  for (int64_t row = (int64_t)blockIdx.x * kWavesPerBlock + wave; row < n_nodes; row += n_waves) {
+    const G* cl = cell == nullptr ? nullptr
+                                  : (n_graphs <= 1 || batch == nullptr ? cell
+                                                                       : cell + 9 * (int64_t)batch[row]);
+    floatx4 acc[T];
+#pragma unroll
+    for (int t = 0; t < T; ++t) acc[t] = floatx4{0.f, 0.f, 0.f, 0.f};
+    const int b0 = ptr[row], b1 = ptr[row + 1];
+    for (int base = b0; base < b1; base += kWave) {
+      const int cnt = min(kWave, b1 - base);
+      const int my_e = lane < cnt ? (perm ? perm[base + lane] : base + lane) : 0;
+      // A operand of h W for all four tiles of the batch, loaded before the harmonics
+      float ha[4][KK];
+#pragma unroll
+      for (int tau = 0; tau < 4; ++tau) {
+        const int j = 16 * tau + hrow;
+        const int ej = __shfl(my_e, j);
+#pragma unroll
+        for (int q = 0; q < KK; ++q) {
+          const int k = 4 * q + hi;
+          ha[tau][q] = (j < cnt && k < K) ? h[(int64_t)ej * K + k] : 0.f;
+        }
+      }
+      float ux, uy, uz, inv;
+      batch_harmonics<G, LMAX>(vec, pos, cl, src, shift, (int)row, sign, lane, cnt, my_e, ys, ux,
+                               uy, uz, inv);
+      wave_sync();
+#pragma unroll
+      for (int tau = 0; tau < 4; ++tau) {
+        if (16 * tau >= cnt) break;
+        floatx4 ph[T];
+#pragma unroll
+        for (int t = 0; t < T; ++t) {
+          ph[t] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int q = 0; q < KK; ++q) ph[t] = mfma_16x16x4(ha[tau][q], wB[q][t], ph[t]);
+        }
+        // ph[t][r] = phi[edge 16 tau + 4 r + hi][channel lo T + t]
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          if (16 * tau + 4 * r < cnt) {
+            const float a = ys[(16 * tau + 4 * r + hi) * kSY + lo];
+#pragma unroll
+            for (int t = 0; t < T; ++t) acc[t] = mfma_16x16x4(a, ph[t][r], acc[t]);
+          }
+        }
+      }
+      wave_sync();  // ys is rewritten by the next batch
+    }
+    // lane holds A[row, channel lo T + t, lm 4 hi + r]
+    float* o = out + (int64_t)row * C * L;
+#pragma unroll
+    for (int t = 0; t < T; ++t) {
+      float* oc = o + (int64_t)(lo * T + t) * L;
+      if constexpr (L % 4 == 0) {
+        if (4 * hi < L)
+          *reinterpret_cast<float4*>(oc + 4 * hi) =
+              make_float4(acc[t][0], acc[t][1], acc[t][2], acc[t][3]);
+      } else {
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          if (4 * hi + r < L) oc[4 * hi + r] = acc[t][r];
+      }
+    }
+  }
+}
+
+template <typename G, int LMAX, int T>
+__global__ __launch_bounds__(256, 2) void lin_msg_bwd_kernel(
+    const float* __restrict__ vec, const G* __restrict__ pos, const G* __restrict__ cell,
+    int64_t n_graphs, const int32_t* __restrict__ batch, const int32_t* __restrict__ src,
+    const int32_t* __restrict__ shift, const int32_t* __restrict__ ptr,
+    const int32_t* __restrict__ perm, int64_t n_nodes, float sign, int K,
+    const float* __restrict__ h, const float* __restrict__ W, const float* __restrict__ d_out,
+    float* __restrict__ d_h, float* __restrict__ g_vec) {
+  constexpr int L = ShDims<LMAX>::L;
+  constexpr int C = 16 * T;
+  constexpr int KS = (L + 3) / 4;
+  constexpr int KK = kLinKK;
+  static_assert(C * L <= 2 * kWave * kSY, "the staged d_out row must fit the LDS slice");
+  __shared__ __align__(16) float sbuf[kWavesPerBlock][2 * kWave * kSY];
+  const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+  const int lo = lane & 15, hi = lane >> 4;
+  float* ys = sbuf[wave];
+  float* sdy = sbuf[wave] + kWave * kSY;
+  const bool want_vec = g_vec != nullptr;
+  // A operand of phi^T = W^T h^T: W[4 q + hi][lo T + t]
+  float wA[KK][T];
+#pragma unroll
+  for (int q = 0; q < KK; ++q)
+#pragma unroll
+    for (int t = 0; t < T; ++t) {
+      const int k = 4 * q + hi;
+      wA[q][t] = k < K ? W[k * C + lo * T + t] : 0.f;
+    }
+  // W in LDS, zero rows past K: the B operand of d_h = d_phi W^T for k-step (t, r) is
+  // W[lo][(4 hi + r) T + t], a run of T floats per r
+  __shared__ __align__(16) float sW[16 * C];
+  for (int i = threadIdx.x; i < 16 * C; i += blockDim.x) sW[i] = i < K * C ? W[i] : 0.f;
+  __syncthreads();
+  const float* wrow = sW + lo * C;
+  const int64_t n_waves = (int64_t)gridDim.x * kWavesPerBlock;
+  for (int64_t row = (int64_t)blockIdx.x * kWavesPerBlock + wave; row < n_nodes; row += n_waves) {
+    const int b0 = ptr[row], b1 = ptr[row + 1];
+    if (b0 == b1) continue;
+    const G* cl = cell == nullptr ? nullptr
+                                  : (n_graphs <= 1 || batch == nullptr ? cell
+                                                                       : cell + 9 * (int64_t)batch[row]);
+    // stage G = d_out[row] (C x L) through LDS into the two operand layouts
+    {
+      const float4* g4 = reinterpret_cast<const float4*>(d_out + (int64_t)row * C * L);
+      float4* s4 = reinterpret_cast<float4*>(sbuf[wave]);
+      for (int i = lane; i < C * L / 4; i += kWave) s4[i] = g4[i];
+    }
+    wave_sync();
+    float gA[T][KS], gB[T][4];
+#pragma unroll
+    for (int t = 0; t < T; ++t) {
+#pragma unroll
+      for (int s = 0; s < KS; ++s) {
+        const int lm = 4 * s + hi;
+        gA[t][s] = lm < L ? sbuf[wave][(lo * T + t) * L + lm] : 0.f;  // G[lo T + t][4 s + hi]
+      }
+#pragma unroll
+      for (int r = 0; r < 4; ++r)  // G[(4 hi + r) T + t][lo]
+        gB[t][r] = lo < L ? sbuf[wave][((4 * hi + r) * T + t) * L + lo] : 0.f;
+    }
+    wave_sync();  // the staging area becomes ys / sdy
+
+    for (int base = b0; base < b1; base += kWave) {
+      const int cnt = min(kWave, b1 - base);
+      const int my_e = lane < cnt ? (perm ? perm[base + lane] : base + lane) : 0;
+      // B operand of phi^T for all four tiles: h[edge 16 tau + lo][4 q + hi]
+      float hb[4][KK];
+#pragma unroll
+      for (int tau = 0; tau < 4; ++tau) {
+        const int j = 16 * tau + lo;
+        const int ej = __shfl(my_e, j);
+#pragma unroll
+        for (int q = 0; q < KK; ++q) {
+          const int k = 4 * q + hi;
+          hb[tau][q] = (want_vec && j < cnt && k < K) ? h[(int64_t)ej * K + k] : 0.f;
+        }
+      }
+      float ux, uy, uz, inv;
+      batch_harmonics<G, LMAX>(vec, pos, cl, src, shift, (int)row, sign, lane, cnt, my_e, ys, ux,
+                               uy, uz, inv);
+      wave_sync();
+#pragma unroll
+      for (int tau = 0; tau < 4; ++tau) {
+        if (16 * tau >= cnt) break;
+        const int je = 16 * tau + lo;
+        if (want_vec) {
+          // pt[t][r] = phi[edge je][channel (4 hi + r) T + t]
+          floatx4 pt[T];
+#pragma unroll
+          for (int t = 0; t < T; ++t) {
+            pt[t] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int q = 0; q < KK; ++q) pt[t] = mfma_16x16x4(wA[q][t], hb[tau][q], pt[t]);
+          }
+          floatx4 dy = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int t = 0; t < T; ++t)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) dy = mfma_16x16x4(pt[t][r], gB[t][r], dy);
+          // dy[r] = dY[edge 16 tau + 4 hi + r][lm lo]
+#pragma unroll
+          for (int r = 0; r < 4; ++r) sdy[(16 * tau + 4 * hi + r) * kSY + lo] = dy[r];
+        }
+        // dp[t][r] = d_phi[edge je][channel (4 hi + r) T + t]
+        floatx4 dp[T];
+#pragma unroll
+        for (int t = 0; t < T; ++t) dp[t] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int s = 0; s < KS; ++s) {
+          const float b = ys[je * kSY + 4 * s + hi];
+#pragma unroll
+          for (int t = 0; t < T; ++t) dp[t] = mfma_16x16x4(gA[t][s], b, dp[t]);
+        }
+        floatx4 dh = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          float wb[T];
+          load_run<T>(wrow + (4 * hi + r) * T, wb);
+#pragma unroll
+          for (int t = 0; t < T; ++t) dh = mfma_16x16x4(dp[t][r], wb[t], dh);
+        }
+        // dh[r] = d_h[edge 16 tau + 4 hi + r][k lo]
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int j = 16 * tau + 4 * hi + r;
+          const int ej = __shfl(my_e, j);
+          if (j < cnt && lo < K) d_h[(int64_t)ej * K + lo] = dh[r];
+        }
+      }
+      wave_sync();
+      if (want_vec && lane < cnt) {
+        float dY[L];
+#pragma unroll
+        for (int m = 0; m < L; ++m) dY[m] = sdy[lane * kSY + m];
+        float Gx, Gy, Gz, vx, vy, vz;
+        sh_grad<LMAX, float>(ux, uy, uz, dY, Gx, Gy, Gz);
+        sh_chain<float>(ux, uy, uz, inv, Gx, Gy, Gz, vx, vy, vz);
+        g_vec[3 * (int64_t)my_e + 0] = sign * vx;
+        g_vec[3 * (int64_t)my_e + 1] = sign * vy;
+        g_vec[3 * (int64_t)my_e + 2] = sign * vz;
+      }
+      wave_sync();
+    }
+  }
+}
+
+template <typename G>
+static int lin_msg(bool backward, const float* vec, const void* pos, int64_t n_nodes,
+                   const void* cell, int64_t n_graphs, const int32_t* batch, const int32_t* src,
+                   const int32_t* shift, const int32_t* ptr, const int32_t* perm, int l_max,
+                   int sign, int K, int C, const float* h, const float* W, const float* d_out,
+                   float* out_or_dh, float* g_vec, hipStream_t stream) {
+  if (n_nodes == 0) return XNN_OK;
+  const int64_t blocks_needed = grid_1d(n_nodes, kWavesPerBlock);
+  const dim3 block(kWavesPerBlock * kWave);
+  const float sg = (float)sign;
+#define XNN_LIN(LM, TT)                                                                        \
+  do {                                                                                         \
+    if (backward) {                                                                            \
+      auto k = lin_msg_bwd_kernel<G, LM, TT>;                                                  \
+      const dim3 grid((unsigned)resident_blocks((const void*)k, block.x, blocks_needed));      \
+      hipLaunchKernelGGL(k, grid, block, 0, stream, vec, (const G*)pos, (const G*)cell,        \
+                         n_graphs, batch, src, shift, ptr, perm, n_nodes, sg, K, h, W, d_out,   \
+                         out_or_dh, g_vec);                                                    \
+    } else {                                                                                   \
+      auto k = lin_msg_fwd_kernel<G, LM, TT>;                                                  \
+      const dim3 grid((unsigned)resident_blocks((const void*)k, block.x, blocks_needed));      \
+      hipLaunchKernelGGL(k, grid, block, 0, stream, vec, (const G*)pos, (const G*)cell,        \
+                         n_graphs, batch, src, shift, ptr, perm, n_nodes, sg, K, h, W,          \
+                         out_or_dh);                                                           \
+    }                                                                                          \
+  } while (0)
+#define XNN_LIN_L(TT)                   \
+  switch (l_max) {                      \
+    case 1: XNN_LIN(1, TT); break;      \
+    case 2: XNN_LIN(2, TT); break;      \
+    default: XNN_LIN(3, TT); break;     \
+  }
+  switch (C) {
+    case 32: XNN_LIN_L(2); break;
+    case 64: XNN_LIN_L(4); break;
+    default: XNN_LIN_L(8); break;
+  }
+#undef XNN_LIN_L
+#undef XNN_LIN
+  XNN_LAUNCH_CHECK();
+  return XNN_OK;
+}
+
+static int lin_check(int64_t n_nodes, int64_t n_edges, int32_t l_max, int32_t sh_sign,
+                     int32_t K, int32_t C) {
+  XNN_REQUIRE(n_nodes >= 0 && n_edges >= 0, "negative size");
+  XNN_REQUIRE(l_max >= 1 && l_max <= 3, "l_max must be in [1, 3], got %d", l_max);
+  XNN_REQUIRE(sh_sign == 1 || sh_sign == -1, "sh_sign must be +1 or -1");
+  XNN_REQUIRE(K >= 1 && K <= kLinKMax, "n_features must be in [1, %d], got %d", kLinKMax, K);
+  XNN_REQUIRE(C == 32 || C == 64 || C == 128, "n_channels must be 32, 64 or 128, got %d", C);
+  return XNN_OK;
+}
+
+}  // namespace xnn
+
+using namespace xnn;
+
+extern "C" {
+
+int xnn_sh_linear_message_sum(int geom_dtype, const float* vec_in, const void* pos,
+                              int64_t n_nodes, const void* cell, int64_t n_graphs,
+                              const int32_t* batch, const int32_t* src, const int32_t* shift,
+                              int64_t n_edges, const int32_t* ptr_dst, const int32_t* perm_dst,
+                              int32_t l_max, int32_t sh_sign, int32_t n_features,
+                              int32_t n_channels, const float* h, const float* W, float* out,
+                              xnn_stream_t stream) {
+  const int st = lin_check(n_nodes, n_edges, l_max, sh_sign, n_features, n_channels);
+  if (st != XNN_OK) return st;
+  XNN_REQUIRE(n_nodes == 0 || (ptr_dst && out && W), "NULL CSR, weights or output");
+  XNN_REQUIRE(aligned16(out), "out must be 16-byte aligned");
+  XNN_REQUIRE(n_edges == 0 || ((vec_in || (pos && src && shift)) && h), "NULL edge input");
+  XNN_REQUIRE(cell == nullptr || n_graphs <= 1 || batch != nullptr,
+              "several cells need the batch vector");
+  if (geom_dtype == XNN_F32)
+    return lin_msg<float>(false, vec_in, pos, n_nodes, cell, n_graphs, batch, src, shift, ptr_dst,
+                          perm_dst, l_max, sh_sign, n_features, n_channels, h, W, nullptr, out,
+                          nullptr, as_hip(stream));
+  if (geom_dtype == XNN_F64)
+    return lin_msg<double>(false, vec_in, pos, n_nodes, cell, n_graphs, batch, src, shift,
+                           ptr_dst, perm_dst, l_max, sh_sign, n_features, n_channels, h, W,
+                           nullptr, out, nullptr, as_hip(stream));
+  set_error("unsupported geometry dtype %d", geom_dtype);
+  return XNN_EINVAL;
+}
+
+int xnn_sh_linear_message_sum_backward(int geom_dtype, const float* vec_in, const void* pos,
+                                       int64_t n_nodes, const void* cell, int64_t n_graphs,
+                                       const int32_t* batch, const int32_t* src,
+                                       const int32_t* shift, int64_t n_edges,
+                                       const int32_t* ptr_dst, const int32_t* perm_dst,
+                                       int32_t l_max, int32_t sh_sign, int32_t n_features,
+                                       int32_t n_channels, const float* h, const float* W,
+                                       const float* d_out, float* d_h, float* g_vec,
+                                       xnn_stream_t stream) {
+  const int st = lin_check(n_nodes, n_edges, l_max, sh_sign, n_features, n_channels);
+  if (st != XNN_OK) return st;
+  XNN_REQUIRE(n_nodes == 0 || (ptr_dst && d_out && W), "NULL CSR, weights or d_out");
+  XNN_REQUIRE(aligned16(d_out), "d_out must be 16-byte aligned");
+  XNN_REQUIRE(n_edges == 0 || ((vec_in || (pos && src && shift)) && d_h && (h || !g_vec)),
+              "NULL edge input or output");
+  XNN_REQUIRE(cell == nullptr || n_graphs <= 1 || batch != nullptr,
+              "several cells need the batch vector");
+  if (geom_dtype == XNN_F32)
+    return lin_msg<float>(true, vec_in, pos, n_nodes, cell, n_graphs, batch, src, shift, ptr_dst,
+                          perm_dst, l_max, sh_sign, n_features, n_channels, h, W, d_out, d_h,
+                          g_vec, as_hip(stream));
+  if (geom_dtype == XNN_F64)
+    return lin_msg<double>(true, vec_in, pos, n_nodes, cell, n_graphs, batch, src, shift,
+                           ptr_dst, perm_dst, l_max, sh_sign, n_features, n_channels, h, W,
+                           d_out, d_h, g_vec, as_hip(stream));
+  set_error("unsupported geometry dtype %d", geom_dtype);
+  return XNN_EINVAL;
+}
+
+}  // extern "C"

@@ -12,43 +12,9 @@
 
 #include "common.h"
 #include "device.h"
+#include "message.h"
 
 namespace xnn {
-
-constexpr int kWavesPerBlock = 4;
-
-template <int LMAX>
-struct ShDims {
-  static constexpr int L = (LMAX + 1) * (LMAX + 1);
-  // partial sums are reduced across the wave padded to a power of two
-  static constexpr int LP = L == 1 ? 1 : (L <= 4 ? 4 : 16);
-};
-
-// Per-lane geometry of one edge: unit vector of sign * r_e and 1/|r_e|; the
-// vector is given (vec) or formed from positions.
-template <typename G>
-__device__ inline void edge_unit(const float* __restrict__ vec, int64_t e,
-                                 const G* __restrict__ pos, const G* __restrict__ cell,
-                                 const int32_t* __restrict__ src, const int32_t* __restrict__ shift,
-                                 int d, float sign, float& ux, float& uy, float& uz, float& inv) {
-  float x, y, z;
-  if (vec != nullptr) {
-    x = vec[3 * e + 0];
-    y = vec[3 * e + 1];
-    z = vec[3 * e + 2];
-  } else {
-    G gx, gy, gz;
-    edge_vector(pos, src[e], d, shift[e], cell, gx, gy, gz);
-    x = (float)gx;
-    y = (float)gy;
-    z = (float)gz;
-  }
-  const float r = sqrtf(x * x + y * y + z * z);
-  inv = r > 0.f ? 1.f / r : 0.f;
-  ux = sign * x * inv;
-  uy = sign * y * inv;
-  uz = sign * z * inv;
-}
 
 // CPL consecutive channels of one phi row starting at c0 (vector loads when aligned)
 template <int CPL, bool VEC>
@@ -366,76 +332,9 @@ __global__ __launch_bounds__(256) void sh_msg_bwd_kernel(
 // Per receiver row both message contractions are small matrix products:
 //   forward   A_i^T (L x C)  = Y_i^T (L x E_i) . phi_i (E_i x C)
 //   backward  d_phi (E_i x C) = Y_i (E_i x L) . G_i^T (L x C),  dY (E_i x L) = phi_i . G_i
-// with G_i = d_out[i] (C x L). They run on v_mfma_f32_16x16x4_f32 (float32 inputs,
-// float32 accumulation): per 16 x 16 x 4 block, lane l supplies A[l % 16][l / 16] and
-// B[l / 16][l % 16] and receives D[4 (l / 16) + r][l % 16] in register r. The harmonic
-// dimension is padded to 16 with zeros; channel tile t of width 16 holds channels
-// c = 16-row index * T + t, which makes every lane's operand and result runs contiguous
-// in memory. C = 16 T.
-typedef float floatx4 __attribute__((ext_vector_type(4)));
-
-__device__ __forceinline__ floatx4 mfma_16x16x4(float a, float b, floatx4 c) {
-  return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
-}
-
-// N consecutive floats at p (vector accesses: p is 4N-byte aligned within 16 bytes)
-template <int N>
-__device__ __forceinline__ void load_run(const float* __restrict__ p, float* v) {
-  if constexpr (N % 4 == 0) {
-#pragma unroll
-    for (int q = 0; q < N; q += 4) {
-      const float4 x = *reinterpret_cast<const float4*>(p + q);
-      v[q] = x.x; v[q + 1] = x.y; v[q + 2] = x.z; v[q + 3] = x.w;
-    }
-  } else if constexpr (N % 2 == 0) {
-#pragma unroll
-    for (int q = 0; q < N; q += 2) {
-      const float2 x = *reinterpret_cast<const float2*>(p + q);
-      v[q] = x.x; v[q + 1] = x.y;
-    }
-  } else {
-#pragma unroll
-    for (int q = 0; q < N; ++q) v[q] = p[q];
-  }
-}
-
-template <int N>
-__device__ __forceinline__ void store_run(float* __restrict__ p, const float* v) {
-  if constexpr (N % 4 == 0) {
-#pragma unroll
-    for (int q = 0; q < N; q += 4)
-      *reinterpret_cast<float4*>(p + q) = make_float4(v[q], v[q + 1], v[q + 2], v[q + 3]);
-  } else if constexpr (N % 2 == 0) {
-#pragma unroll
-    for (int q = 0; q < N; q += 2) *reinterpret_cast<float2*>(p + q) = make_float2(v[q], v[q + 1]);
-  } else {
-#pragma unroll
-    for (int q = 0; q < N; ++q) p[q] = v[q];
-  }
-}
-
-constexpr int kSY = 17;  // LDS row stride of per-edge harmonics (spreads the banks)
-
-// Lane's edge of the batch (lanes < cnt), and the harmonics of that edge into ys
-// (row `lane`, 16 entries, zeros past l_max and past the batch's end).
-template <typename G, int LMAX>
-__device__ __forceinline__ void batch_harmonics(
-    const float* __restrict__ vec, const G* __restrict__ pos, const G* __restrict__ cl,
-    const int32_t* __restrict__ src, const int32_t* __restrict__ shift, int row, float sign,
-    int lane, int cnt, int e, float* ys, float& ux, float& uy, float& uz, float& inv) {
-  constexpr int L = ShDims<LMAX>::L;
-  float Y[L];
-  if (lane < cnt) {
-    edge_unit(vec, e, pos, cl, src, shift, row, sign, ux, uy, uz, inv);
-    sh_eval<LMAX, float>(ux, uy, uz, Y);
-  } else {
-    ux = uy = uz = inv = 0.f;
-#pragma unroll
-    for (int m = 0; m < L; ++m) Y[m] = 0.f;
-  }
-#pragma unroll
-  for (int m = 0; m < 16; ++m) ys[lane * kSY + m] = m < L ? Y[m] : 0.f;
-}
+// with G_i = d_out[i] (C x L), on v_mfma_f32_16x16x4_f32. The harmonic dimension is padded
+// to 16 with zeros; channel tile t of width 16 holds channels c = 16-row index * T + t,
+// which makes every lane's operand and result runs contiguous in memory. C = 16 T.
 
 // phi operand of the forward for k-steps k0 .. k0+KG-1 of a batch: lane l feeds edge
 // 4 k + l / 16 with channels [(l % 16) T, (l % 16) T + T)
@@ -770,11 +669,8 @@ static int reduce_chunks(int64_t n_rows, int64_t n_segments) {
   return (int)(c < kMaxChunks ? c : kMaxChunks);
 }
 
-// compute units of the current device (cached per device id)
-static int device_cu_count();
-
 // blocks of `kernel` that stay resident on the whole device (all CUs), capped at `needed`
-static int64_t resident_blocks(const void* kernel, int block_threads, int64_t needed) {
+int64_t resident_blocks(const void* kernel, int block_threads, int64_t needed) {
   // the occupancy of each kernel is queried once and kept (a handful of instantiations)
   static const void* keys[128] = {nullptr};
   static int values[128] = {0};
@@ -798,7 +694,7 @@ static int64_t resident_blocks(const void* kernel, int block_threads, int64_t ne
   return std::max<int64_t>(1, std::min<int64_t>(needed, (int64_t)per_cu * device_cu_count()));
 }
 
-static int device_cu_count() {
+int device_cu_count() {
   static int cached[64] = {0};
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
@@ -812,11 +708,11 @@ static int device_cu_count() {
   return cached[dev];
 }
 
-static bool aligned16(const void* p) { return p == nullptr || (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+bool aligned16(const void* p) { return p == nullptr || (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
 // XNN_AMD_MESSAGE_MFMA=0 in the environment selects the vector-ALU message kernels
 // (read at every call, so a process can compare the two)
-static bool message_mfma_enabled() {
+bool message_mfma_enabled() {
   const char* v = std::getenv("XNN_AMD_MESSAGE_MFMA");
   return !(v != nullptr && v[0] == '0');
 }

@@ -85,21 +85,26 @@ class ShEdgePotential(InteratomicPotential):
     ``scatter_sum`` (gnn/fast/conv.py:137-143). The readout is
     ``E_i = sum_{c,lm} U[c, lm] A_i[c, lm] + atom_ref[Z_i]`` and ``E = sum_i E_i`` in
     float64. On a GPU the featurizer and the fused message sum are HIP kernels (the
-    message never exists in memory); ``use_fast=False`` or a CPU evaluates the same
-    function with the PyTorch formulation.
+    message never exists in memory); with ``fused_linear`` (the default, for the channel
+    counts the fused kernels take) the radial linear layer runs inside the message
+    kernels too, so ``phi`` is never stored either. ``use_fast=False`` or a CPU evaluates
+    the same function with the PyTorch formulation.
     """
 
     def __init__(self, species: Sequence[int] = (1, 6, 7, 8), n_rbf: int = 8, l_max: int = 3,
                  channels: int = 128, cutoff: float = 5.0, radial_type: str = "bessel",
                  envelope: str = "polynomial", p: int = 6, sh_sign: int = 1,
-                 use_fast: UseFast = "auto", seed: Optional[int] = 0):
+                 use_fast: UseFast = "auto", seed: Optional[int] = 0, fused_linear: bool = True):
         super().__init__()
         self.cutoff = float(cutoff)
         self.l_max = int(l_max)
         self.channels = int(channels)
         self.sh_sign = int(sh_sign)
+        self.fused_linear = bool(fused_linear)
         self.use_fast = resolve_use_fast(use_fast)
         self.double_backward = False
+        # False while ForceStressOutput evaluates forces only (no parameter gradients)
+        self.param_grads = True
         self.edge_feat = SphericalHarmonicEdgeEmbedding(
             l_max=l_max, n_rbf=n_rbf, cutoff=cutoff, p=p, radial_type=radial_type,
             envelope=envelope)
@@ -115,10 +120,16 @@ class ShEdgePotential(InteratomicPotential):
         """``A (N, C, L)`` from edge vectors (HIP fused sum or PyTorch scatter)."""
         feat = self.edge_feat
         if feat.fast_active:
-            from .ops import sh_message_sum
+            from .ops import linear_message_supported, sh_linear_message_sum, sh_message_sum
             u = feat.radial(vec)
-            phi = u @ self.W.to(u.dtype)
-            return sh_message_sum(vec, phi, data.plan(), self.l_max, self.sh_sign)
+            W = self.W.to(u.dtype)
+            if not self.param_grads:
+                W = W.detach()
+            if self.fused_linear and linear_message_supported(W.shape[0], W.shape[1], self.l_max):
+                # the radial linear layer runs inside the message kernels: phi = u W is
+                # formed per edge tile in registers, never stored
+                return sh_linear_message_sum(vec, u, W, data.plan(), self.l_max, self.sh_sign)
+            return sh_message_sum(vec, u @ W, data.plan(), self.l_max, self.sh_sign)
         _, sh, u = feat.embed(vec, sh_sign=self.sh_sign)
         phi = u @ self.W.to(u.dtype)
         msg = (phi[:, :, None] * sh[:, None, :]).reshape(vec.shape[0], -1)

@@ -17,6 +17,8 @@ op                     replaces
                        and ``PolynomialCutoff`` / ``CosineCutoff`` (cutoff.py:10-125)
 ``sh_message_sum``     ``ConvTensorProduct.conv`` reference path for scalar edge
                        weights (gnn/fast/conv.py:137-143) + ``scatter_sum``
+``sh_linear_message_   the same with the edge weights formed in the kernel by the last
+sum``                  linear layer of the weight network (``h @ W``)
 ``segment_sum``        ``scatter_sum`` (common/models/ops.py:403-448)
 ``gather_rows``        ``gather_rows`` (common/models/ops.py:494-528)
 ``structure_sum``      ``structure_sum`` (common/models/ops.py:531-557), float64 totals
@@ -25,7 +27,7 @@ op                     replaces
 All reductions walk CSR rows in a fixed order (no float atomics), so every op
 is bitwise reproducible run to run. The linear ops (edge vectors, segment sums,
 gathers, structure sums) are differentiable to any order: each backward is its
-adjoint op. The nonlinear ones (edge embedding, SH message sum) are
+adjoint op. The nonlinear ones (edge embedding, SH message sums) are
 differentiable once; a double backward through them (force training with
 ``create_graph=True``) raises, and the modules take the PyTorch formulation there.
 """
@@ -323,6 +325,89 @@ def sh_message_sum(vec: Tensor, phi: Tensor, plan: EdgePlan, l_max: int,
         raise ValueError("sh_message_sum takes 1 to 256 channels")
     return sh_message_sum_op(vec.contiguous(), phi.contiguous(), plan.ptr_dst, plan.perm_dst,
                              int(l_max), int(sh_sign))
+
+
+# --------------------------------------------------------------------------- fused linear + SH message sum
+LINEAR_MESSAGE_CHANNELS = (32, 64, 128)
+LINEAR_MESSAGE_MAX_FEATURES = 8
+
+
+@torch.library.custom_op(f"{_NS}::sh_linear_message_sum", mutates_args=())
+def sh_linear_message_sum_op(vec: Tensor, h: Tensor, W: Tensor, ptr_dst: Tensor,
+                             perm_dst: Optional[Tensor], l_max: int, sh_sign: int) -> Tensor:
+    """``A[i, c, lm] = sum_{dst(e)=i} (h_e W)[c] Y_lm(sign vec_e)`` (float32); ``h W`` is
+    formed in the kernel and never stored."""
+    dev = _require_gpu(vec, h, W)
+    n_nodes = ptr_dst.shape[0] - 1
+    K, C = W.shape
+    L = (l_max + 1) ** 2
+    out = torch.empty((n_nodes, C, L), dtype=torch.float32, device=dev)
+    _lib.call("xnn_sh_linear_message_sum", _lib.XNN_F32, _lib.ptr(vec), None, n_nodes, None, 0,
+              None, None, None, vec.shape[0], _lib.ptr(ptr_dst), _lib.ptr(perm_dst), l_max,
+              sh_sign, K, C, _lib.ptr(h), _lib.ptr(W), _lib.ptr(out), _lib.stream(dev))
+    return out
+
+
+@sh_linear_message_sum_op.register_fake
+def _(vec, h, W, ptr_dst, perm_dst, l_max, sh_sign):
+    return h.new_empty((ptr_dst.shape[0] - 1, W.shape[1], (l_max + 1) ** 2))
+
+
+def _lin_msg_setup(ctx, inputs, output):
+    vec, h, W, ptr_dst, perm_dst, l_max, sh_sign = inputs
+    ctx.save_for_backward(vec, h, W, ptr_dst, perm_dst)
+    ctx.l_max, ctx.sh_sign = l_max, sh_sign
+
+
+def _lin_msg_backward(ctx, d_out):
+    _once_differentiable()
+    vec, h, W, ptr_dst, perm_dst = ctx.saved_tensors
+    d_out = d_out.contiguous()
+    n_nodes = ptr_dst.shape[0] - 1
+    K, C = W.shape
+    dev = vec.device
+    need_vec, need_h, need_W = ctx.needs_input_grad[0], ctx.needs_input_grad[1], ctx.needs_input_grad[2]
+    g_vec = torch.empty_like(vec) if need_vec else None
+    d_h = torch.empty_like(h) if (need_h or need_vec) else None
+    if need_vec or need_h:
+        _lib.call("xnn_sh_linear_message_sum_backward", _lib.XNN_F32, _lib.ptr(vec), None,
+                  n_nodes, None, 0, None, None, None, vec.shape[0], _lib.ptr(ptr_dst),
+                  _lib.ptr(perm_dst), ctx.l_max, ctx.sh_sign, K, C, _lib.ptr(h), _lib.ptr(W),
+                  _lib.ptr(d_out), _lib.ptr(d_h), _lib.ptr(g_vec), _lib.stream(dev))
+    d_W = None
+    if need_W:
+        # d_W = h^T d_phi needs d_phi itself: one pass of the unfused backward forms it
+        phi = h @ W
+        d_phi = torch.empty_like(phi)
+        _lib.call("xnn_sh_message_sum_backward", _lib.XNN_F32, _lib.ptr(vec), None, n_nodes, None,
+                  0, None, None, None, vec.shape[0], _lib.ptr(ptr_dst), _lib.ptr(perm_dst),
+                  ctx.l_max, ctx.sh_sign, C, _lib.ptr(phi), _lib.ptr(d_out), _lib.ptr(d_phi),
+                  None, _lib.stream(dev))
+        d_W = h.t() @ d_phi
+    return g_vec, (d_h if need_h else None), d_W, None, None, None, None
+
+
+sh_linear_message_sum_op.register_autograd(_lin_msg_backward, setup_context=_lin_msg_setup)
+
+
+def linear_message_supported(n_features: int, n_channels: int, l_max: int) -> bool:
+    """Shapes the fused kernels take; others use the linear layer + :func:`sh_message_sum`."""
+    return (n_channels in LINEAR_MESSAGE_CHANNELS and 1 <= n_features <= LINEAR_MESSAGE_MAX_FEATURES
+            and 1 <= l_max <= 3)
+
+
+def sh_linear_message_sum(vec: Tensor, h: Tensor, W: Tensor, plan: EdgePlan, l_max: int,
+                          sh_sign: int = 1) -> Tensor:
+    """``sh_message_sum(vec, h @ W, ...)`` with the linear layer inside the kernel."""
+    if vec.dtype != torch.float32 or h.dtype != torch.float32 or W.dtype != torch.float32:
+        raise TypeError("sh_linear_message_sum computes in float32")
+    if h.shape[0] != vec.shape[0] or h.shape[1] != W.shape[0]:
+        raise ValueError("h needs one row per edge and W one row per feature of h")
+    if not linear_message_supported(W.shape[0], W.shape[1], l_max):
+        raise ValueError(f"sh_linear_message_sum takes {LINEAR_MESSAGE_CHANNELS} channels, at "
+                         f"most {LINEAR_MESSAGE_MAX_FEATURES} features and l_max in [1, 3]")
+    return sh_linear_message_sum_op(vec.contiguous(), h.contiguous(), W.contiguous(),
+                                    plan.ptr_dst, plan.perm_dst, int(l_max), int(sh_sign))
 
 
 # --------------------------------------------------------------------------- segment sums

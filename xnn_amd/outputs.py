@@ -43,7 +43,16 @@ class ForceStressOutput(nn.Module):
         # the double-backward of a training step needs the differentiable formulation
         if hasattr(self.model, "double_backward"):
             self.model.double_backward = bool(create_graph)
-        out = self.model(data)
+        # forces and stress alone need no parameter gradients (the training step's
+        # create_graph=True keeps them)
+        had_param_grads = getattr(self.model, "param_grads", None)
+        if had_param_grads is not None:
+            self.model.param_grads = bool(create_graph)
+        try:
+            out = self.model(data)
+        finally:
+            if had_param_grads is not None:
+                self.model.param_grads = had_param_grads
         energy = out["energy"]
         inputs, need = [], []
         if self.compute_forces:
