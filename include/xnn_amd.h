@@ -97,12 +97,18 @@ int xnn_edge_featurize_backward(int geom_dtype, int compute_dtype, const void* v
  * sum_{dst=i} g_e - sum_{src=i} g_e (written, geometry dtype), and, when
  * cell_partial != NULL, cell_partial[i] = sum_{dst=i} shift_e (x) g_e as
  * (N,3,3) float64 (sum it per structure with xnn_segment_reduce_f64 to get
- * grad_cell = shifts^T g). No float atomics: rows are walked in CSR order. */
+ * grad_cell = shifts^T g). When virial_partial != NULL, virial_partial[i] =
+ * sum_{dst=i} r_e (x) g_e (N,3,3) float64 from the edge vectors vec (E,3, compute
+ * dtype): summed per structure it is M = sum_e r_e (x) dE/dr_e, and sym(M) is the
+ * strain derivative of ForceStressOutput (outputs.py:166-216) for an energy that
+ * depends on positions and cell only through the edge vectors.
+ * No float atomics: rows are walked in CSR order. */
 int xnn_edge_force_reduce(int geom_dtype, int compute_dtype, const void* g_edge, int64_t n_edges,
                           const int32_t* ptr_dst, const int32_t* perm_dst,
                           const int32_t* ptr_src, const int32_t* perm_src,
                           const int32_t* shift, int64_t n_nodes,
-                          void* grad_pos, double* cell_partial, xnn_stream_t stream);
+                          void* grad_pos, double* cell_partial, const void* vec,
+                          double* virial_partial, xnn_stream_t stream);
 
 /* ------------------------------------------------------------------------ */
 /* Fused SH message aggregation: out[i,c,lm] = sum_{e: dst=i} phi[e,c] * Y_lm(sign r_e)

@@ -5,6 +5,7 @@ outputs exact, float32 energies rtol 1e-6, forces and stress atol 1e-5 (eV/A), f
 paths 1e-10; reductions bitwise reproducible run to run; the native library must be the
 code that ran (call counters).
 """
+import copy
 import sys
 
 import numpy as np
@@ -331,7 +332,7 @@ def test_segment_gather_and_structure_sums():
 # --------------------------------------------------------------------------- full model
 @pytest.mark.parametrize("config,fused", [("water", True), ("water", False), ("argon", True),
                                           ("ragged", True), ("nequip_molecules", True),
-                                          ("nequip_molecules", False)])
+                                          ("nequip_molecules", False), ("periodic_batch", True)])
 def test_model_energy_forces_stress(config, fused):
     import oracle.reference as R
     import xnn_amd as xa
@@ -346,6 +347,12 @@ def test_model_energy_forces_stress(config, fused):
         structs = [s]
     elif config == "ragged":
         structs, rc = synthetic.ragged_molecules(256, seed=1), 5.0
+        kw = dict(n_rbf=8, l_max=3, channels=64, radial_type="bessel", envelope="polynomial")
+    elif config == "periodic_batch":
+        # three periodic cells of different sizes and kinds: per-structure virials
+        structs, rc = [synthetic.water_box(n_molecules=64, box=12.4, grid=4, seed=5),
+                       synthetic.argon_fcc(n_cells=3, seed=6),
+                       synthetic.organic_box(n_atoms=300, box=14.0, seed=7)], 5.0
         kw = dict(n_rbf=8, l_max=3, channels=64, radial_type="bessel", envelope="polynomial")
     else:
         structs, rc = synthetic.random_molecules(32, seed=2), 5.0
@@ -393,6 +400,28 @@ def test_model_energy_forces_stress(config, fused):
     assert torch.equal(out["energy"], out2["energy"])
 
 
+def test_stress_from_edge_virial_matches_deformation():
+    """The strain derivative formed by the edge-vector backward (sym sum_e r_e (x) dE/dr_e)
+    equals the one autograd carries back through deformed positions and cells."""
+    import xnn_amd as xa
+    from xnn_amd import synthetic
+    _note("edge virial vs deformation")
+    structs = [synthetic.water_box(n_molecules=64, box=12.4, grid=4, seed=8),
+               synthetic.argon_fcc(n_cells=3, seed=9)]
+    g = xa.collate([xa.structure_to_graph(st.as_dict(), 5.0, device=DEV) for st in structs])
+    g.pos, g.cell = g.pos.float(), g.cell.float()
+    model = xa.ShEdgePotential(cutoff=5.0, species=(1, 8, 18), channels=64, seed=3).to(DEV)
+    wrapped = xa.ForceStressOutput(model, compute_stress=True).eval()
+    out_probe = wrapped(copy.copy(g))
+    model.edge_virial = False              # instance override: deform pos and cell instead
+    out_deform = wrapped(copy.copy(g))
+    scale = float(out_deform["stress"].abs().max())
+    np.testing.assert_allclose(out_probe["stress"].detach().cpu().double(),
+                               out_deform["stress"].detach().cpu().double(), atol=1e-6 * scale)
+    np.testing.assert_allclose(out_probe["forces"].detach().cpu().double(),
+                               out_deform["forces"].detach().cpu().double(), atol=1e-6)
+
+
 def test_training_step_differentiates_forces_twice():
     """A force-loss training step (create_graph=True): the featurizer takes the PyTorch
     formulation, the edge vectors / sums stay on the HIP ops (differentiable to any
@@ -433,6 +462,9 @@ def test_graph_replays_match_the_eager_step():
     s = synthetic.water_box(n_molecules=216, box=18.6, grid=6, seed=4)
     g = xa.structure_to_graph(s.as_dict(), 5.0, device=DEV)
     model = xa.ShEdgePotential(n_rbf=8, l_max=3, channels=64, cutoff=5.0, seed=1).to(DEV)
+    # a captured step deforms positions and cell for the stress (the edge-virial path is
+    # off under capture); the eager steps take the same path so that they compare bitwise
+    model.edge_virial = False
     wrapped = xa.ForceStressOutput(model, compute_stress=True).eval()
     g.plan()
 

@@ -55,7 +55,7 @@ _SIGNATURES = {
     "xnn_edge_featurize_backward": [c_int, c_int, vp, vp, i64, vp, i64, vp, vp, vp, vp, i64,
                                     ctypes.POINTER(FeaturizeParams), vp, vp, vp, vp, vp, vp, vp,
                                     vp],
-    "xnn_edge_force_reduce": [c_int, c_int, vp, i64, vp, vp, vp, vp, vp, i64, vp, vp, vp],
+    "xnn_edge_force_reduce": [c_int, c_int, vp, i64, vp, vp, vp, vp, vp, i64, vp, vp, vp, vp, vp],
     "xnn_sh_message_sum": [c_int, vp, vp, i64, vp, i64, vp, vp, vp, i64, vp, vp, i32, i32, i32,
                            vp, vp, vp],
     "xnn_sh_message_sum_backward": [c_int, vp, vp, i64, vp, i64, vp, vp, vp, i64, vp, vp, i32,

@@ -152,12 +152,14 @@ __global__ __launch_bounds__(256) void force_reduce_kernel(
     const T* __restrict__ g_edge, const int32_t* __restrict__ ptr_dst,
     const int32_t* __restrict__ perm_dst, const int32_t* __restrict__ ptr_src,
     const int32_t* __restrict__ perm_src, const int32_t* __restrict__ shift, int64_t n_nodes,
-    G* __restrict__ grad_pos, double* __restrict__ cell_partial) {
+    G* __restrict__ grad_pos, double* __restrict__ cell_partial, const T* __restrict__ vec,
+    double* __restrict__ virial_partial) {
   const int lane = threadIdx.x % GROUP;
   const int64_t i = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) / GROUP;
   const bool live = i < n_nodes;
   double fx = 0, fy = 0, fz = 0;
   double c[9] = {0, 0, 0, 0, 0, 0, 0, 0, 0};
+  double v[9] = {0, 0, 0, 0, 0, 0, 0, 0, 0};
   if (live) {
     const int b0 = ptr_dst[i], b1 = ptr_dst[i + 1];
     for (int k = b0 + lane; k < b1; k += GROUP) {
@@ -173,6 +175,13 @@ __global__ __launch_bounds__(256) void force_reduce_kernel(
         c[0] += sx * x; c[1] += sx * y; c[2] += sx * z;
         c[3] += sy * x; c[4] += sy * y; c[5] += sy * z;
         c[6] += sz * x; c[7] += sz * y; c[8] += sz * z;
+      }
+      if (virial_partial) {
+        const double rx = vec[3 * (int64_t)e + 0], ry = vec[3 * (int64_t)e + 1],
+                     rz = vec[3 * (int64_t)e + 2];
+        v[0] += rx * x; v[1] += rx * y; v[2] += rx * z;
+        v[3] += ry * x; v[4] += ry * y; v[5] += ry * z;
+        v[6] += rz * x; v[7] += rz * y; v[8] += rz * z;
       }
     }
     const int s0 = ptr_src[i], s1 = ptr_src[i + 1];
@@ -192,6 +201,10 @@ __global__ __launch_bounds__(256) void force_reduce_kernel(
 #pragma unroll
       for (int q = 0; q < 9; ++q) c[q] += __shfl_xor(c[q], m, GROUP);
     }
+    if (virial_partial) {
+#pragma unroll
+      for (int q = 0; q < 9; ++q) v[q] += __shfl_xor(v[q], m, GROUP);
+    }
   }
   if (live && lane == 0) {
     grad_pos[3 * i + 0] = (G)fx;
@@ -200,6 +213,10 @@ __global__ __launch_bounds__(256) void force_reduce_kernel(
     if (cell_partial) {
 #pragma unroll
       for (int q = 0; q < 9; ++q) cell_partial[9 * i + q] = c[q];
+    }
+    if (virial_partial) {
+#pragma unroll
+      for (int q = 0; q < 9; ++q) virial_partial[9 * i + q] = v[q];
     }
   }
 }
@@ -290,30 +307,33 @@ template <typename G, typename T, int GROUP>
 static void launch_force_reduce(const void* g_edge, const int32_t* ptr_dst,
                                 const int32_t* perm_dst, const int32_t* ptr_src,
                                 const int32_t* perm_src, const int32_t* shift, int64_t n_nodes,
-                                void* grad_pos, double* cell_partial, hipStream_t stream) {
+                                void* grad_pos, double* cell_partial, const void* vec,
+                                double* virial_partial, hipStream_t stream) {
   const int64_t threads = n_nodes * GROUP;
   hipLaunchKernelGGL((force_reduce_kernel<G, T, GROUP>), dim3(grid_1d(threads, 256)),
                      dim3(256), 0, stream, (const T*)g_edge, ptr_dst, perm_dst, ptr_src,
-                     perm_src, shift, n_nodes, (G*)grad_pos, cell_partial);
+                     perm_src, shift, n_nodes, (G*)grad_pos, cell_partial, (const T*)vec,
+                     virial_partial);
 }
 
 template <typename G, typename T>
 static int force_reduce(const void* g_edge, int64_t n_edges, const int32_t* ptr_dst,
                         const int32_t* perm_dst, const int32_t* ptr_src,
                         const int32_t* perm_src, const int32_t* shift, int64_t n_nodes,
-                        void* grad_pos, double* cell_partial, hipStream_t stream) {
+                        void* grad_pos, double* cell_partial, const void* vec,
+                        double* virial_partial, hipStream_t stream) {
   if (n_nodes == 0) return XNN_OK;
   // lanes per atom from the mean degree (both rows are walked)
   const double deg = n_nodes > 0 ? (double)n_edges / (double)n_nodes : 0.0;
   if (deg > 24)
     launch_force_reduce<G, T, 32>(g_edge, ptr_dst, perm_dst, ptr_src, perm_src, shift, n_nodes,
-                                  grad_pos, cell_partial, stream);
+                                  grad_pos, cell_partial, vec, virial_partial, stream);
   else if (deg > 6)
     launch_force_reduce<G, T, 16>(g_edge, ptr_dst, perm_dst, ptr_src, perm_src, shift, n_nodes,
-                                  grad_pos, cell_partial, stream);
+                                  grad_pos, cell_partial, vec, virial_partial, stream);
   else
     launch_force_reduce<G, T, 4>(g_edge, ptr_dst, perm_dst, ptr_src, perm_src, shift, n_nodes,
-                                 grad_pos, cell_partial, stream);
+                                 grad_pos, cell_partial, vec, virial_partial, stream);
   XNN_LAUNCH_CHECK();
   return XNN_OK;
 }
@@ -374,13 +394,17 @@ int xnn_edge_force_reduce(int geom_dtype, int compute_dtype, const void* g_edge,
                           const int32_t* ptr_dst, const int32_t* perm_dst,
                           const int32_t* ptr_src, const int32_t* perm_src,
                           const int32_t* shift, int64_t n_nodes, void* grad_pos,
-                          double* cell_partial, xnn_stream_t stream) {
+                          double* cell_partial, const void* vec, double* virial_partial,
+                          xnn_stream_t stream) {
   XNN_REQUIRE(n_edges >= 0 && n_nodes >= 0, "negative size");
   XNN_REQUIRE(n_nodes == 0 || (ptr_dst && ptr_src && grad_pos), "NULL CSR or output");
   XNN_REQUIRE(n_edges == 0 || g_edge, "NULL g_edge");
   XNN_REQUIRE(cell_partial == nullptr || shift != nullptr, "cell_partial needs the shifts");
+  XNN_REQUIRE(virial_partial == nullptr || n_edges == 0 || vec != nullptr,
+              "virial_partial needs the edge vectors");
   XNN_DISPATCH_GT(geom_dtype, compute_dtype, force_reduce, g_edge, n_edges, ptr_dst, perm_dst,
-                  ptr_src, perm_src, shift, n_nodes, grad_pos, cell_partial, as_hip(stream));
+                  ptr_src, perm_src, shift, n_nodes, grad_pos, cell_partial, vec, virial_partial,
+                  as_hip(stream));
 }
 
 }  // extern "C"

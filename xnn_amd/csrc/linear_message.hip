@@ -64,31 +64,41 @@ __global__ __launch_bounds__(256) void lin_msg_fwd_kernel(
     for (int base = b0; base < b1; base += kWave) {
       const int cnt = min(kWave, b1 - base);
       const int my_e = lane < cnt ? (perm ? perm[base + lane] : base + lane) : 0;
-      // A operand of h W for all four tiles of the batch, loaded before the harmonics
-      float ha[4][KK];
-#pragma unroll
-      for (int tau = 0; tau < 4; ++tau) {
-        const int j = 16 * tau + hrow;
-        const int ej = __shfl(my_e, j);
+      // A operand of h W for tile tau (edge 16 tau + hrow); the next tile's is in flight
+      // while a tile is computed
+      float ha[KK], hn[KK];
+      {
+        const int ej = __shfl(my_e, hrow);
 #pragma unroll
         for (int q = 0; q < KK; ++q) {
           const int k = 4 * q + hi;
-          ha[tau][q] = (j < cnt && k < K) ? h[(int64_t)ej * K + k] : 0.f;
+          hn[q] = (hrow < cnt && k < K) ? h[(int64_t)ej * K + k] : 0.f;
         }
       }
       float ux, uy, uz, inv;
       batch_harmonics<G, LMAX>(vec, pos, cl, src, shift, (int)row, sign, lane, cnt, my_e, ys, ux,
                                uy, uz, inv);
       wave_sync();
+      const int ntile = (cnt + 15) >> 4;
+#pragma unroll 1
+      for (int tau = 0; tau < ntile; ++tau) {
 #pragma unroll
-      for (int tau = 0; tau < 4; ++tau) {
-        if (16 * tau >= cnt) break;
+        for (int q = 0; q < KK; ++q) ha[q] = hn[q];
+        {
+          const int jn = 16 * (tau + 1) + hrow;
+          const int ej = __shfl(my_e, jn & (kWave - 1));
+#pragma unroll
+          for (int q = 0; q < KK; ++q) {
+            const int k = 4 * q + hi;
+            hn[q] = (jn < cnt && k < K) ? h[(int64_t)ej * K + k] : 0.f;
+          }
+        }
         floatx4 ph[T];
 #pragma unroll
         for (int t = 0; t < T; ++t) {
           ph[t] = floatx4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-          for (int q = 0; q < KK; ++q) ph[t] = mfma_16x16x4(ha[tau][q], wB[q][t], ph[t]);
+          for (int q = 0; q < KK; ++q) ph[t] = mfma_16x16x4(ha[q], wB[q][t], ph[t]);
         }
         // ph[t][r] = phi[edge 16 tau + 4 r + hi][channel lo T + t]
 #pragma unroll
@@ -185,26 +195,36 @@ __global__ __launch_bounds__(256, 2) void lin_msg_bwd_kernel(
     for (int base = b0; base < b1; base += kWave) {
       const int cnt = min(kWave, b1 - base);
       const int my_e = lane < cnt ? (perm ? perm[base + lane] : base + lane) : 0;
-      // B operand of phi^T for all four tiles: h[edge 16 tau + lo][4 q + hi]
-      float hb[4][KK];
-#pragma unroll
-      for (int tau = 0; tau < 4; ++tau) {
-        const int j = 16 * tau + lo;
-        const int ej = __shfl(my_e, j);
+      // B operand of phi^T for tile tau: h[edge 16 tau + lo][4 q + hi]; the next tile's
+      // is in flight while a tile is computed
+      float hb[KK], hn[KK];
+      {
+        const int ej = __shfl(my_e, lo);
 #pragma unroll
         for (int q = 0; q < KK; ++q) {
           const int k = 4 * q + hi;
-          hb[tau][q] = (want_vec && j < cnt && k < K) ? h[(int64_t)ej * K + k] : 0.f;
+          hn[q] = (want_vec && lo < cnt && k < K) ? h[(int64_t)ej * K + k] : 0.f;
         }
       }
       float ux, uy, uz, inv;
       batch_harmonics<G, LMAX>(vec, pos, cl, src, shift, (int)row, sign, lane, cnt, my_e, ys, ux,
                                uy, uz, inv);
       wave_sync();
-#pragma unroll
-      for (int tau = 0; tau < 4; ++tau) {
-        if (16 * tau >= cnt) break;
+      const int ntile = (cnt + 15) >> 4;
+#pragma unroll 1
+      for (int tau = 0; tau < ntile; ++tau) {
         const int je = 16 * tau + lo;
+#pragma unroll
+        for (int q = 0; q < KK; ++q) hb[q] = hn[q];
+        {
+          const int jn = je + 16;
+          const int ej = __shfl(my_e, jn & (kWave - 1));
+#pragma unroll
+          for (int q = 0; q < KK; ++q) {
+            const int k = 4 * q + hi;
+            hn[q] = (want_vec && jn < cnt && k < K) ? h[(int64_t)ej * K + k] : 0.f;
+          }
+        }
         if (want_vec) {
           // pt[t][r] = phi[edge je][channel (4 hi + r) T + t]
           floatx4 pt[T];
@@ -212,7 +232,7 @@ __global__ __launch_bounds__(256, 2) void lin_msg_bwd_kernel(
           for (int t = 0; t < T; ++t) {
             pt[t] = floatx4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-            for (int q = 0; q < KK; ++q) pt[t] = mfma_16x16x4(wA[q][t], hb[tau][q], pt[t]);
+            for (int q = 0; q < KK; ++q) pt[t] = mfma_16x16x4(wA[q][t], hb[q], pt[t]);
           }
           floatx4 dy = floatx4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -223,6 +243,8 @@ __global__ __launch_bounds__(256, 2) void lin_msg_bwd_kernel(
 #pragma unroll
           for (int r = 0; r < 4; ++r) sdy[(16 * tau + 4 * hi + r) * kSY + lo] = dy[r];
         }
+        // keep phi^T and d_phi from being live together
+        __builtin_amdgcn_sched_barrier(0);
         // dp[t][r] = d_phi[edge je][channel (4 hi + r) T + t]
         floatx4 dp[T];
 #pragma unroll

@@ -49,6 +49,9 @@ class AtomicGraph:
     stress: Optional[Tensor] = None
     total_charge: Optional[Tensor] = None
     compute_dtype: Optional[torch.dtype] = None
+    # (B, 3, 3) zeros set by ForceStressOutput: the strain whose gradient the edge-vector
+    # backward forms directly (sym of sum_e r_e (x) dE/dr_e), in place of deforming pos and cell
+    strain_probe: Optional[Tensor] = None
 
     @property
     def model_dtype(self) -> torch.dtype:
@@ -83,7 +86,10 @@ class AtomicGraph:
         differentiable with respect to ``pos`` and ``cell`` (atomic_data.py:371-418)."""
         if self.pos.is_cuda:
             from .ops import edge_vectors
-            return edge_vectors(self.pos, self.cell, self.plan(), self.model_dtype)
+            return edge_vectors(self.pos, self.cell, self.plan(), self.model_dtype,
+                                strain_probe=self.strain_probe)
+        if self.strain_probe is not None:
+            raise RuntimeError("strain_probe is a GPU path; deform pos and cell on the CPU")
         src, dst = self.edge_index[0], self.edge_index[1]
         vec = self.pos.index_select(0, dst) - self.pos.index_select(0, src)
         if self.cell is not None:

@@ -55,6 +55,10 @@ class InteratomicPotential(nn.Module):
     """Base class: ``forward(AtomicGraph) -> {"node_energy", "energy"}`` (base.py:24-180)."""
 
     head_modules = ()
+    # True when the energy depends on positions and cell only through
+    # data.edge_vectors(): ForceStressOutput then takes the strain derivative from the
+    # edge-vector backward instead of deforming positions and cell
+    edge_virial = False
 
     def forward(self, data) -> dict:
         raise NotImplementedError
@@ -90,6 +94,8 @@ class ShEdgePotential(InteratomicPotential):
     kernels too, so ``phi`` is never stored either. ``use_fast=False`` or a CPU evaluates
     the same function with the PyTorch formulation.
     """
+
+    edge_virial = True
 
     def __init__(self, species: Sequence[int] = (1, 6, 7, 8), n_rbf: int = 8, l_max: int = 3,
                  channels: int = 128, cutoff: float = 5.0, radial_type: str = "bessel",

@@ -113,7 +113,7 @@ def force_reduce_op(g_edge: Tensor, cell_like: Optional[Tensor], batch32: Tensor
     _lib.call("xnn_edge_force_reduce", geom_code, _lib.dtype_code(g_edge.dtype), _lib.ptr(g_edge),
               g_edge.shape[0], _lib.ptr(ptr_dst), _lib.ptr(perm_dst), _lib.ptr(ptr_src),
               _lib.ptr(perm_src), _lib.ptr(shift), n_nodes, _lib.ptr(grad_pos),
-              _lib.ptr(partial), s)
+              _lib.ptr(partial), None, None, s)
     if not want_cell:
         return grad_pos, grad_pos.new_zeros((0,))
     grad_cell = torch.empty((n_graphs, 9), dtype=torch.float64, device=dev)
@@ -177,15 +177,90 @@ def _force_reduce_backward(ctx, d_pos, d_cell):
 force_reduce_op.register_autograd(_force_reduce_backward, setup_context=_force_reduce_setup)
 
 
+# --------------------------------------------------------------------------- strain probe
+@torch.library.custom_op(f"{_NS}::edge_vectors_strain_probe", mutates_args=())
+def edge_vectors_strain_probe_op(pos: Tensor, strain_probe: Tensor, cell: Optional[Tensor],
+                                 batch32: Tensor, src: Tensor, dst: Tensor, shift: Tensor,
+                                 ptr_dst: Tensor, perm_dst: Optional[Tensor], ptr_src: Tensor,
+                                 perm_src: Tensor, node_ptr: Tensor, out_dtype: int) -> Tensor:
+    """Edge vectors of the configuration deformed by the strain ``strain_probe`` (B, 3, 3)
+    about zero: ``r_e (I + sym(strain))`` with ``sym(s) = (s + s^T) / 2``, the deformation
+    of ForceStressOutput (outputs.py:166-180; it moves positions and cell, hence every
+    edge vector, by the same linear map). The probe is zero by contract (its value is not
+    read), so the vectors are the undeformed ones; what it carries is its gradient, which
+    the backward forms directly: ``dE/d strain = sym(sum_e r_e (x) dE/dr_e)`` per structure,
+    float64 accumulation, from the force-reduction kernel. Differentiable once."""
+    return edge_vectors_op(pos, cell, batch32, src, dst, shift, ptr_dst, perm_dst, ptr_src,
+                           perm_src, node_ptr, out_dtype)
+
+
+@edge_vectors_strain_probe_op.register_fake
+def _(pos, strain_probe, cell, batch32, src, dst, shift, ptr_dst, perm_dst, ptr_src, perm_src,
+      node_ptr, out_dtype):
+    odt = torch.float32 if out_dtype == _lib.XNN_F32 else torch.float64
+    return pos.new_empty((src.shape[0], 3), dtype=odt)
+
+
+def _probe_setup(ctx, inputs, output):
+    (pos, strain_probe, cell, batch32, src, dst, shift, ptr_dst, perm_dst, ptr_src, perm_src,
+     node_ptr, out_dtype) = inputs
+    ctx.save_for_backward(output, batch32, src, dst, shift, ptr_dst, perm_dst, ptr_src, perm_src,
+                          node_ptr)
+    ctx.n_nodes = pos.shape[0]
+    ctx.geom_code = _lib.dtype_code(pos.dtype)
+    ctx.has_cell = cell is not None and cell.numel() > 0
+    ctx.probe_dtype = strain_probe.dtype
+
+
+def _probe_backward(ctx, grad):
+    _once_differentiable()
+    vec, batch32, src, dst, shift, ptr_dst, perm_dst, ptr_src, perm_src, node_ptr = ctx.saved_tensors
+    grad = grad.contiguous()
+    dev = grad.device
+    n_nodes = ctx.n_nodes
+    n_graphs = node_ptr.shape[0] - 1
+    gdt = torch.float32 if ctx.geom_code == _lib.XNN_F32 else torch.float64
+    want_cell = bool(ctx.has_cell and ctx.needs_input_grad[2])
+    grad_pos = torch.empty((n_nodes, 3), dtype=gdt, device=dev)
+    cell_partial = torch.empty((n_nodes, 9), dtype=torch.float64, device=dev) if want_cell else None
+    virial_partial = torch.empty((n_nodes, 9), dtype=torch.float64, device=dev)
+    _lib.call("xnn_edge_force_reduce", ctx.geom_code, _lib.dtype_code(grad.dtype), _lib.ptr(grad),
+              grad.shape[0], _lib.ptr(ptr_dst), _lib.ptr(perm_dst), _lib.ptr(ptr_src),
+              _lib.ptr(perm_src), _lib.ptr(shift), n_nodes, _lib.ptr(grad_pos),
+              _lib.ptr(cell_partial), _lib.ptr(vec), _lib.ptr(virial_partial), _lib.stream(dev))
+    M = torch.empty((n_graphs, 9), dtype=torch.float64, device=dev)
+    _lib.segment_reduce_f64(virial_partial, n_nodes, 9, node_ptr, n_graphs, M)
+    M = M.view(n_graphs, 3, 3)
+    grad_probe = (0.5 * (M + M.transpose(1, 2))).to(ctx.probe_dtype)
+    grad_cell = None
+    if want_cell:
+        gc = torch.empty((n_graphs, 9), dtype=torch.float64, device=dev)
+        _lib.segment_reduce_f64(cell_partial, n_nodes, 9, node_ptr, n_graphs, gc)
+        grad_cell = gc.view(n_graphs, 3, 3).to(gdt)
+    return (grad_pos if ctx.needs_input_grad[0] else None, grad_probe, grad_cell,
+            None, None, None, None, None, None, None, None, None, None)
+
+
+edge_vectors_strain_probe_op.register_autograd(_probe_backward, setup_context=_probe_setup)
+
+
 def edge_vectors(pos: Tensor, cell: Optional[Tensor], plan: EdgePlan,
-                 out_dtype: Optional[torch.dtype] = None) -> Tensor:
+                 out_dtype: Optional[torch.dtype] = None,
+                 strain_probe: Optional[Tensor] = None) -> Tensor:
     """Edge vectors of a planned graph; differentiable to ``pos`` and ``cell`` to any
-    order (the backward is the CSR force reduction, whose adjoint is this map again)."""
+    order (the backward is the CSR force reduction, whose adjoint is this map again).
+    With ``strain_probe`` (a zero (B, 3, 3) tensor) the strain gradient comes from the
+    same backward pass (differentiable once)."""
     out_dtype = out_dtype or pos.dtype
     if cell is not None:
         cell = cell.reshape(-1, 3, 3).to(pos.dtype)
         if not cell.is_contiguous():
             cell = cell.contiguous()
+    if strain_probe is not None:
+        return edge_vectors_strain_probe_op(
+            pos.contiguous(), strain_probe, cell, plan.batch32, plan.src, plan.dst, plan.shift,
+            plan.ptr_dst, plan.perm_dst, plan.ptr_src, plan.perm_src, plan.node_ptr,
+            _lib.dtype_code(out_dtype))
     return edge_vectors_op(pos.contiguous(), cell, plan.batch32, plan.src, plan.dst, plan.shift,
                            plan.ptr_dst, plan.perm_dst, plan.ptr_src, plan.perm_src,
                            plan.node_ptr, _lib.dtype_code(out_dtype))

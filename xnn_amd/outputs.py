@@ -3,7 +3,10 @@
 ``forces = -dE/dpos``; ``stress = (1/V) dE/d(strain)`` with the symmetric-strain trick:
 positions and cell are displaced by ``sym(eps)`` at ``eps = 0`` so that autograd
 carries the virial back to ``eps``. On a GPU the backward of the edge vectors is the
-HIP CSR force reduction, so no float atomics touch the forces.
+HIP CSR force reduction, so no float atomics touch the forces; for a model whose energy
+depends on positions only through the edge vectors, that same reduction also forms
+``dE/d(eps) = sym(sum_e r_e (x) dE/dr_e)`` (the identity behind the trick), so nothing
+deforms positions or cell in the forward.
 """
 from __future__ import annotations
 
@@ -29,7 +32,22 @@ class ForceStressOutput(nn.Module):
     def forward(self, data) -> dict:
         create_graph = self.training
         strain: Optional[Tensor] = None
-        if self.compute_stress and data.cell is not None:
+        # A model whose energy depends on positions and cell only through the edge vectors
+        # (``edge_virial``) gets the strain derivative from the edge-vector backward itself,
+        # sym(sum_e r_e (x) dE/dr_e), the same derivative as deforming pos and cell by the
+        # strain; the training step (create_graph) and the CPU keep the deformation.
+        # Under HIP graph capture the deformation is kept: the capture of this path ended
+        # in a host crash in capture_end (cause not found), so it is switched off there.
+        probe = (self.compute_stress and data.cell is not None and not create_graph
+                 and data.pos.is_cuda and bool(getattr(self.model, "edge_virial", False))
+                 and not torch.cuda.is_current_stream_capturing())
+        if probe:
+            strain = torch.zeros((data.num_graphs, 3, 3), dtype=data.pos.dtype,
+                                 device=data.pos.device, requires_grad=True)
+            data.strain_probe = strain
+            if not data.pos.requires_grad:       # a fresh leaf; the caller's tensor is untouched
+                data.pos = data.pos.detach().requires_grad_(True)
+        elif self.compute_stress and data.cell is not None:
             strain = torch.zeros((data.num_graphs, 3, 3), dtype=data.pos.dtype,
                                  device=data.pos.device, requires_grad=True)
             sym = 0.5 * (strain + strain.transpose(-1, -2))
@@ -53,6 +71,8 @@ class ForceStressOutput(nn.Module):
         finally:
             if had_param_grads is not None:
                 self.model.param_grads = had_param_grads
+            if probe:
+                data.strain_probe = None
         energy = out["energy"]
         inputs, need = [], []
         if self.compute_forces:
