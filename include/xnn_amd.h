@@ -189,6 +189,76 @@ int xnn_segment_reduce_f64(int dtype, const void* src, int64_t n_rows, int64_t n
                            void* workspace, size_t workspace_bytes, xnn_stream_t stream);
 
 /* ------------------------------------------------------------------------ */
+/* D4 dispersion pair terms over lattice images, float64 (no edge list: every
+ * receiver i meets every source j of its structure and every translation
+ * n = (n0, n1, n2) with |n_a| <= images[b, a]; vectors pos_i - pos_j + n @ cell in
+ * Angstrom, lengths in bohr). Atoms of a structure are contiguous: node_ptr (B+1)
+ * int64 on the device, batch (N) int32, max_atoms = the largest structure.
+ * species (N) int32 indexes the per-species tables. cell (B,3,3) Angstrom rows or
+ * NULL (molecules). Gradients are exact derivatives of the returned sums; the cell
+ * gradient comes as per-atom partials n (x) dE/dr (N,3,3) to be summed per structure
+ * with xnn_segment_reduce_f64. All memory is the caller's; workspace:
+ * xnn_d4_workspace_bytes(n_nodes, n_graphs, max_atoms) bytes. Deterministic (per-
+ * receiver partials summed over source chunks in a fixed order). */
+typedef struct {
+  double cutoff_cn;      /* D4 CN cutoff, bohr (r <= cutoff counts)           */
+  double cutoff_eeq_cn;  /* EEQ CN cutoff, bohr                               */
+  double kcn, k4, k5, k6;
+} xnn_d4_cn_params;
+
+typedef struct {
+  double s6, s8, a1, a2; /* BJ damping parameters                             */
+  double cutoff;         /* pair cutoff, bohr (r <= cutoff counts)            */
+  double width;          /* quintic switching width, bohr (<= 0: sharp)       */
+} xnn_d4_pair_params;
+
+size_t xnn_d4_workspace_bytes(int64_t n_nodes, int64_t n_graphs, int64_t max_atoms);
+
+/* cn_d4[i] = sum_{j,n: r <= cutoff_cn} k4 exp(-(|EN_i - EN_j| + k5)^2 / k6) c(r) and
+ * cn_raw[i] = sum_{r <= cutoff_eeq_cn} c(r), c(r) = (1 + erf(-kcn (r - rc) / rc)) / 2,
+ * rc = rcov_i + rcov_j (bohr). Replaces DFTD4.coordination_numbers (d4.py:552-591;
+ * the soft cap of the EEQ CN, d4.py:589-590, is left to the caller). */
+int xnn_d4_coordination(const double* pos, int64_t n_nodes, const int32_t* species,
+                        const int32_t* batch, const int64_t* node_ptr, int64_t n_graphs,
+                        int64_t max_atoms, const double* cell, const int32_t* images,
+                        const double* rcov, const double* en, const xnn_d4_cn_params* prm,
+                        double* cn_d4, double* cn_raw, void* workspace, size_t workspace_bytes,
+                        xnn_stream_t stream);
+
+/* Gradients of sum_i (g_cn_d4[i] cn_d4[i] + g_cn_raw[i] cn_raw[i]) (either g may be
+ * NULL): grad_pos (N,3) and cell_partial (N,3,3, nullable). */
+int xnn_d4_coordination_backward(const double* pos, int64_t n_nodes, const int32_t* species,
+                                 const int32_t* batch, const int64_t* node_ptr, int64_t n_graphs,
+                                 int64_t max_atoms, const double* cell, const int32_t* images,
+                                 const double* rcov, const double* en,
+                                 const xnn_d4_cn_params* prm, const double* g_cn_d4,
+                                 const double* g_cn_raw, double* grad_pos, double* cell_partial,
+                                 void* workspace, size_t workspace_bytes, xnn_stream_t stream);
+
+/* e2[i] = sum_{j,n: r <= cutoff} -1/2 C6_ij sw(r) (s6 / (r^6 + R0^6) + s8 rr / (r^8 + R0^8)),
+ * C6_ij = (3/pi) sum_w cp_w alpha_i(w) alpha_j(w) over the 23-point Casimir-Polder grid,
+ * rr = 3 r4r2_i r4r2_j, R0 = a1 sqrt(rr) + a2 (hartree, bohr). alpha (N,23).
+ * Replaces DFTD4.two_body_energy / pair_damping / pair_c6 (d4.py:1044-1071) and the
+ * switching_function (dispersion.py:42-67). */
+int xnn_d4_two_body(const double* pos, int64_t n_nodes, const int32_t* species,
+                    const int32_t* batch, const int64_t* node_ptr, int64_t n_graphs,
+                    int64_t max_atoms, const double* cell, const int32_t* images,
+                    const double* r4r2, const double* alpha, const xnn_d4_pair_params* prm,
+                    double* e2, void* workspace, size_t workspace_bytes, xnn_stream_t stream);
+
+/* Gradients of sum_i g_e2[i] e2[i]: grad_pos (N,3), cell_partial (N,3,3, nullable) and
+ * grad_alpha (N,23, nullable): the outputs of the reference's native pair kernel
+ * (dispersion_fast/cpu.py:834-935, D4CpuFunction.backward 1356-1376) for the
+ * two-body term. */
+int xnn_d4_two_body_backward(const double* pos, int64_t n_nodes, const int32_t* species,
+                             const int32_t* batch, const int64_t* node_ptr, int64_t n_graphs,
+                             int64_t max_atoms, const double* cell, const int32_t* images,
+                             const double* r4r2, const double* alpha,
+                             const xnn_d4_pair_params* prm, const double* g_e2, double* grad_pos,
+                             double* cell_partial, double* grad_alpha, void* workspace,
+                             size_t workspace_bytes, xnn_stream_t stream);
+
+/* ------------------------------------------------------------------------ */
 /* Cell-list radius graph. Replaces build_neighbor_list (neighborlist.py:411-506):
  * same edge set (dist < cutoff in the geometry dtype), same [src,dst] and negated,
  * unwrapped shift convention; edges come grouped by receiver (CSR order).

@@ -1,0 +1,177 @@
+"""GPU parity of the D4 path: the HIP coordination-number and two-body kernels and the
+host-side D4 evaluation against the oracle (float64, brute-force pair images) and the
+dftd4 golden values (tests/common/test_d4.py:110-126, 173-185, 202-226)."""
+import math
+import os
+import sys
+
+import numpy as np
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+HERE = os.path.dirname(os.path.abspath(__file__))
+TABLES = os.path.join(HERE, "golden", "d4_tables_hcnoar.npz")
+WATER = (np.array([[0.0, 0.0, 0.119262], [0.0, 0.763239, -0.477047],
+                   [0.0, -0.763239, -0.477047]]), [8, 1, 1])
+FAST = dict(cutoff_pair=9.0, cutoff_cn=8.0, cutoff_eeq_cn=8.0)
+
+
+def _note(msg):
+    print(f"[gpu-case] {msg}", flush=True)
+    sys.stdout.flush()
+
+
+@pytest.fixture(scope="module")
+def tables():
+    return dict(np.load(TABLES, allow_pickle=False))
+
+
+def _cluster(n, seed, box=6.0):
+    rng = np.random.default_rng(seed)
+    pos = rng.uniform(0, box - 1, (n, 3))
+    return pos, ([1, 8, 6, 7] * (n // 4) + [1] * (n % 4))[:n]
+
+
+def _eval(model, pos, z, cell=None, charges=None, grad=False):
+    p = torch.tensor(pos, dtype=torch.float64, device=DEV, requires_grad=grad)
+    c = None
+    if cell is not None:
+        c = torch.tensor(cell, dtype=torch.float64, device=DEV)[None].requires_grad_(grad)
+    out = model.evaluate(torch.tensor(z, device=DEV), p, c, None if c is None else
+                         torch.ones((1, 3), dtype=torch.bool), torch.tensor([len(z)]),
+                         charges=charges)
+    return out, p, c
+
+
+def _oracle(tables, pos, z, cell, q, cutoffs, prm, width=0.0):
+    """Oracle energy and its gradients in positions and cell for given charges."""
+    import oracle.d4 as D
+    cut_pair, cut_cn, cut_eeq = cutoffs
+    dst, src, sh = D.pair_images(pos, cell, max(cutoffs))
+    pt = torch.tensor(pos, dtype=torch.float64, requires_grad=True)
+    ct = None if cell is None else torch.tensor(cell, dtype=torch.float64, requires_grad=True)
+    v = D.edge_vectors_au(pt, ct, dst, src, sh)
+    r = torch.linalg.norm(v, dim=-1)
+    zt = torch.as_tensor(z)
+    n = len(z)
+    cn, cn_eeq, raw = D.coordination_numbers(zt, dst, src, r, tables, cut_cn / D.BOHR,
+                                             cut_eeq / D.BOHR, n)
+    alpha = D.dynamic_polarizabilities(zt, cn, q, tables)
+    e2 = D.two_body(zt, dst, src, r, alpha, tables, prm, cut_pair / D.BOHR, width / D.BOHR, n)
+    grads = torch.autograd.grad(e2.sum(), [pt] + ([ct] if ct is not None else []))
+    return {"cn": cn.detach(), "raw": raw.detach(), "alpha": alpha.detach(), "e2": e2.detach(),
+            "grad_pos": grads[0], "grad_cell": grads[1] if ct is not None else None}
+
+
+def test_water_golden_values_on_the_gpu(tables):
+    import xnn_amd.dispersion as XD
+    _note("d4 water golden")
+    model = XD.DFTD4(tables).to(DEV)
+    out, _, _ = _eval(model, *WATER)
+    np.testing.assert_allclose(out["coordination_numbers"].cpu().numpy(),
+                               [1.60884227, 0.80442113, 0.80442113], atol=1e-7)
+    np.testing.assert_allclose(out["charges"].cpu().numpy(),
+                               [-0.58639069, 0.29319534, 0.29319534], atol=1e-7)
+    np.testing.assert_allclose(out["polarizabilities"].cpu().numpy(),
+                               [6.71824515, 1.35296894, 1.35296894], atol=1e-7)
+    c6 = XD.c6_matrix(out["dynamic_polarizabilities"]).cpu().numpy()
+    assert abs(c6[0, 0] - 24.68023585) < 1e-6 and abs(c6[0, 1] - 4.2011774) < 1e-6
+    # dftd4's total includes a 1.8e-11 Eh three-body part; the two-body term meets 1e-10
+    assert abs(float(out["energy"][0]) / XD.HARTREE - (-1.5761743e-04)) < 1e-10
+
+
+def test_argon_dimer_asymptote(tables):
+    import xnn_amd.dispersion as XD
+    _note("d4 argon dimer")
+    model = XD.DFTD4(tables).to(DEV)
+    r4r2 = float(tables["r4r2"][18])
+    for r in (12.0, 16.0):
+        out, _, _ = _eval(model, np.array([[0.0, 0, 0], [r, 0, 0]]), [18, 18])
+        c6 = float(XD.c6_matrix(out["dynamic_polarizabilities"])[0, 1])
+        ra = r / XD.BOHR
+        r0 = model.a1 * math.sqrt(3 * r4r2 ** 2) + model.a2
+        expected = -(c6 / (ra ** 6 + r0 ** 6) + model.s8 * 3 * r4r2 ** 2 * c6 / (ra ** 8 + r0 ** 8))
+        assert abs(float(out["energy"][0]) / XD.HARTREE - expected) < 1e-14
+
+
+@pytest.mark.parametrize("case", ["molecule", "periodic", "triclinic_switched"])
+def test_kernels_match_oracle(tables, case):
+    """CN, per-atom two-body energies, and the position and cell gradients of the
+    two-body energy, with the same charges on both sides, float64 (1e-11 relative)."""
+    import oracle.d4 as D
+    import xnn_amd.dispersion as XD
+    _note(f"d4 kernels vs oracle: {case}")
+    width = 0.0
+    if case == "molecule":
+        pos, z = _cluster(12, seed=5)
+        cell = None
+    elif case == "periodic":
+        pos, z = _cluster(16, seed=6, box=7.0)
+        cell = np.diag([7.0, 7.5, 8.0])
+    else:
+        pos, z = _cluster(10, seed=7)
+        cell = np.array([[6.0, 0, 0], [0.8, 5.7, 0], [-0.4, 0.6, 6.2]])
+        width = 2.0
+    model = XD.DFTD4(tables, switch_width_pair=width, **FAST).to(DEV)
+    q = torch.tensor(np.random.default_rng(1).normal(0, 0.2, len(z)), dtype=torch.float64)
+    out, p, c = _eval(model, pos, z, cell, charges=q.to(DEV), grad=True)
+    gp, *gc = torch.autograd.grad(out["energy"].sum(), [p] + ([c] if c is not None else []))
+    ref = _oracle(tables, pos, z, cell, q, (FAST["cutoff_pair"], FAST["cutoff_cn"],
+                                            FAST["cutoff_eeq_cn"]), D.PBE0_D4, width)
+    np.testing.assert_allclose(out["coordination_numbers"].detach().cpu(), ref["cn"], rtol=1e-12,
+                               atol=1e-13)
+    e2 = out["node_energy"].detach().cpu() / XD.HARTREE
+    scale = float(ref["e2"].abs().max())
+    np.testing.assert_allclose(e2, ref["e2"], atol=1e-11 * scale)
+    g_scale = float(ref["grad_pos"].abs().max())
+    np.testing.assert_allclose(gp.cpu() / XD.HARTREE, ref["grad_pos"], atol=1e-10 * g_scale)
+    if cell is not None:
+        np.testing.assert_allclose(gc[0][0].cpu() / XD.HARTREE, ref["grad_cell"],
+                                   atol=1e-10 * float(ref["grad_cell"].abs().max()))
+
+
+def test_full_molecule_with_eeq_matches_oracle_and_finite_differences(tables):
+    """Charges from the EEQ solve on both sides; forces against central differences of
+    the GPU energy (test_d4.py:202-215: h = 1e-4 A, 1e-7 eV/A)."""
+    import oracle.d4 as D
+    import xnn_amd.dispersion as XD
+    _note("d4 molecule full path")
+    pos, z = _cluster(8, seed=2)
+    model = XD.DFTD4(tables, **FAST).to(DEV)
+    out, p, _ = _eval(model, pos, z, grad=True)
+    (gp,) = torch.autograd.grad(out["energy"].sum(), [p])
+    ref = D.d4_molecule(pos, z, tables, prm=dict(D.PBE0_D4, s9=0.0), with_atm=False,
+                        cutoffs_au=(9.0 / D.BOHR, 7.0 / D.BOHR, 8.0 / D.BOHR, 8.0 / D.BOHR))
+    np.testing.assert_allclose(out["charges"].detach().cpu(), ref["q"], atol=1e-12)
+    assert abs(float(out["energy"][0]) / XD.HARTREE - float(ref["energy"])) < 1e-14
+    h = 1e-4
+    for i, a in [(0, 0), (3, 2), (5, 1)]:
+        pp, pm = pos.copy(), pos.copy()
+        pp[i, a] += h
+        pm[i, a] -= h
+        ep = float(_eval(model, pp, z)[0]["energy"][0])
+        em = float(_eval(model, pm, z)[0]["energy"][0])
+        assert abs(float(gp[i, a]) - (ep - em) / (2 * h)) < 1e-7
+
+
+def test_batch_equals_separate_structures(tables):
+    """Two molecules and a periodic cell in one call give each structure's own energy
+    and charges (pairs never cross structures)."""
+    import xnn_amd.dispersion as XD
+    _note("d4 batch")
+    model = XD.DFTD4(tables, **FAST).to(DEV)
+    m1, z1 = _cluster(9, seed=11)
+    m2, z2 = _cluster(5, seed=12)
+    pc, zc = _cluster(12, seed=13, box=7.0)
+    cell = np.diag([7.0, 7.0, 7.0])
+    pos = np.concatenate([m1, m2, pc])
+    z = z1 + z2 + zc
+    cells = torch.tensor(np.stack([np.zeros((3, 3)), np.zeros((3, 3)), cell]), device=DEV)
+    pbc = torch.tensor([[False] * 3, [False] * 3, [True] * 3])
+    out = model.evaluate(torch.tensor(z, device=DEV), torch.tensor(pos, device=DEV), cells, pbc,
+                         torch.tensor([9, 5, 12]))
+    e = [float(_eval(model, m1, z1)[0]["energy"][0]), float(_eval(model, m2, z2)[0]["energy"][0]),
+         float(_eval(model, pc, zc, cell)[0]["energy"][0])]
+    np.testing.assert_allclose(out["energy"].cpu().numpy(), e, rtol=1e-12)

@@ -1,0 +1,84 @@
+"""The D4 oracle pinned against the reference's golden values and closed forms
+(tests/common/test_d4.py:110-126, 173-199). CPU only."""
+import math
+import os
+
+import numpy as np
+import pytest
+import torch
+
+import oracle.d4 as D
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+TABLES = os.path.join(HERE, "golden", "d4_tables_hcnoar.npz")
+WATER = (np.array([[0.0, 0.0, 0.119262], [0.0, 0.763239, -0.477047],
+                   [0.0, -0.763239, -0.477047]]), [8, 1, 1])
+
+
+@pytest.fixture(scope="module")
+def tables():
+    return dict(np.load(TABLES, allow_pickle=False))
+
+
+def test_water_matches_dftd4_golden_values(tables):
+    """dftd4 4.2.0, PBE0-D4 (test_d4.py:110-126): energy 1e-10 Eh, CN / charges /
+    static polarizabilities 1e-7, C6 1e-6."""
+    out = D.d4_molecule(WATER[0], WATER[1], tables)
+    assert abs(float(out["energy"]) - (-1.5761743e-04)) < 1e-10
+    np.testing.assert_allclose(out["cn"].numpy(), [1.60884227, 0.80442113, 0.80442113], atol=1e-7)
+    np.testing.assert_allclose(out["q"].numpy(), [-0.58639069, 0.29319534, 0.29319534], atol=1e-7)
+    np.testing.assert_allclose(out["alpha"][:, 0].numpy(), [6.71824515, 1.35296894, 1.35296894],
+                               atol=1e-7)
+    c6 = D.c6_pairs(out["alpha"][:, None, :], out["alpha"][None, :, :])
+    assert abs(float(c6[0, 0]) - 24.68023585) < 1e-6 and abs(float(c6[0, 1]) - 4.2011774) < 1e-6
+    # the three-body part is tiny for water: the two-body term alone meets the bar too
+    assert abs(float(out["energy_2body"]) - (-1.5761743e-04)) < 1e-10
+    assert float(out["energy_2body"]) < 0 < float(out["energy_3body"])
+
+
+def test_dimer_two_body_tends_to_damped_c6_over_r6(tables):
+    """Ar2 far apart: E = -(C6 / (r^6 + R0^6) + s8 3 Q^2 C6 / (r^8 + R0^8)) (test_d4.py:173-185)."""
+    prm = dict(D.PBE0_D4, s9=0.0)
+    r4r2 = tables["r4r2"][18]
+    for r in (12.0, 16.0):
+        pos = np.array([[0.0, 0, 0], [r, 0, 0]])
+        out = D.d4_molecule(pos, [18, 18], tables, prm=prm, with_atm=False)
+        c6 = float(D.c6_pairs(out["alpha"][0], out["alpha"][1]))
+        ra = r / D.BOHR
+        r0 = prm["a1"] * math.sqrt(3 * r4r2 ** 2) + prm["a2"]
+        expected = -(c6 / (ra ** 6 + r0 ** 6) + prm["s8"] * 3 * r4r2 ** 2 * c6 / (ra ** 8 + r0 ** 8))
+        assert abs(float(out["energy"]) - expected) < 1e-14
+
+
+def test_switching_function_closed_form():
+    """Quintic window: 1 below cutoff - width, 0 above, x^3 (10 - 15 x + 6 x^2) inside,
+    zero slope at both ends; width <= 0 is the sharp cutoff (dispersion.py:42-67)."""
+    r = torch.linspace(0.0, 12.0, 241, dtype=torch.float64, requires_grad=True)
+    sw = D.switching(r, 10.0, 3.0)
+    assert bool((sw[r <= 7.0] == 1.0).all()) and bool((sw[r >= 10.0] == 0.0).all())
+    x = (10.0 - r.detach()) / 3.0
+    mid = (x > 0) & (x < 1)
+    np.testing.assert_allclose(sw.detach()[mid], (x ** 3 * (10 - 15 * x + 6 * x ** 2))[mid], rtol=1e-14)
+    (g,) = torch.autograd.grad(sw.sum(), r)
+    assert abs(float(g[r.detach() == 7.0])) < 1e-12 and abs(float(g[r.detach() == 10.0])) < 1e-12
+    assert bool((D.switching(r, 10.0, 0.0) == 1.0).all())
+
+
+def test_exact_invariances(tables):
+    """Rigid rotations and translations leave CN, charges and energy unchanged."""
+    rng = np.random.default_rng(3)
+    pos = rng.uniform(0, 5, (8, 3))
+    z = [1, 8, 6, 7, 1, 8, 6, 1]
+    a = D.d4_molecule(pos, z, tables, with_atm=False)
+    R, _ = np.linalg.qr(rng.normal(size=(3, 3)))
+    b = D.d4_molecule(pos @ R.T + 1.7, z, tables, with_atm=False)
+    for k in ("cn", "q", "e2"):
+        np.testing.assert_allclose(a[k].numpy(), b[k].numpy(), atol=1e-12)
+
+
+def test_tables_fixture_has_the_elements(tables):
+    assert list(tables["elements"]) == [1, 6, 7, 8, 18]
+    assert tables["refalpha"].shape == (23, 7, 119)
+    assert int(tables["nref"][6]) == 7 and int(tables["nref"][1]) == 2
+    assert 1.9 < float(tables["r4r2"][1]) < 2.1 and 3.0 < float(tables["r4r2"][6]) < 3.2
+    assert float(np.abs(tables["refalpha"][:, :, 2]).sum()) == 0.0     # outside the subset

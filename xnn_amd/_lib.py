@@ -46,6 +46,18 @@ class GridPlan(ctypes.Structure):
                 ("workspace_bytes", sz)]
 
 
+class D4CnParams(ctypes.Structure):
+    """``xnn_d4_cn_params``."""
+    _fields_ = [("cutoff_cn", dbl), ("cutoff_eeq_cn", dbl), ("kcn", dbl), ("k4", dbl),
+                ("k5", dbl), ("k6", dbl)]
+
+
+class D4PairParams(ctypes.Structure):
+    """``xnn_d4_pair_params``."""
+    _fields_ = [("s6", dbl), ("s8", dbl), ("a1", dbl), ("a2", dbl), ("cutoff", dbl),
+                ("width", dbl)]
+
+
 # name -> argtypes (restype int unless listed in _RESTYPES)
 _SIGNATURES = {
     "xnn_last_error": [],
@@ -64,6 +76,15 @@ _SIGNATURES = {
                                   i32, i32, vp, vp, vp, vp],
     "xnn_sh_linear_message_sum_backward": [c_int, vp, vp, i64, vp, i64, vp, vp, vp, i64, vp, vp,
                                            i32, i32, i32, i32, vp, vp, vp, vp, vp, vp],
+    "xnn_d4_workspace_bytes": [i64, i64, i64],
+    "xnn_d4_coordination": [vp, i64, vp, vp, vp, i64, i64, vp, vp, vp, vp,
+                            ctypes.POINTER(D4CnParams), vp, vp, vp, sz, vp],
+    "xnn_d4_coordination_backward": [vp, i64, vp, vp, vp, i64, i64, vp, vp, vp, vp,
+                                     ctypes.POINTER(D4CnParams), vp, vp, vp, vp, vp, sz, vp],
+    "xnn_d4_two_body": [vp, i64, vp, vp, vp, i64, i64, vp, vp, vp, vp,
+                        ctypes.POINTER(D4PairParams), vp, vp, sz, vp],
+    "xnn_d4_two_body_backward": [vp, i64, vp, vp, vp, i64, i64, vp, vp, vp, vp,
+                                 ctypes.POINTER(D4PairParams), vp, vp, vp, vp, vp, sz, vp],
     "xnn_segment_sum": [c_int, vp, i64, i64, vp, vp, i64, vp, vp],
     "xnn_gather_rows": [c_int, vp, i64, i64, vp, i64, vp, vp],
     "xnn_segment_reduce_workspace_bytes": [i64, i64, i64],
@@ -81,7 +102,8 @@ _SIGNATURES = {
     "xnn_edge_plan": [vp, vp, i64, i64, vp, vp, vp, vp, vp, vp, vp, vp, vp, sz, vp],
 }
 _RESTYPES = {"xnn_last_error": ctypes.c_char_p, "xnn_scan_workspace_bytes": sz,
-             "xnn_edge_plan_workspace_bytes": sz, "xnn_segment_reduce_workspace_bytes": sz}
+             "xnn_edge_plan_workspace_bytes": sz, "xnn_segment_reduce_workspace_bytes": sz,
+             "xnn_d4_workspace_bytes": sz}
 
 _lock = threading.Lock()
 _lib: Optional[ctypes.CDLL] = None

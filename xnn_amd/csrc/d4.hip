@@ -1,1 +1,541 @@
-// D4 kernels (added below)
+// D4 dispersion pair terms on lattice images (gfx950, wave64, float64).
+//
+// xnn_d4_coordination(_backward)  DFTD4.coordination_numbers (d4.py:552-591): the
+//                                 EN-weighted erf-count CN and the plain erf count
+//                                 of the charge model, summed to the receiver
+// xnn_d4_two_body(_backward)      DFTD4.two_body_energy / pair_damping / pair_c6
+//                                 (d4.py:1044-1071, 910-934) with the quintic
+//                                 switch (dispersion.py:42-67): -1/2 C6 f(r) to the
+//                                 receiver of every directed pair image; the backward
+//                                 gives grad_pos, the cell gradient and dE/d alpha, the
+//                                 quantities of the reference's native kernel run_d4
+//                                 (dispersion_fast/cpu.py:834-935)
+//
+// No edge list: the long pair cutoff (60 bohr by default) makes the image list dense,
+// so the kernels walk all (receiver, source, image) triples of each structure. Work
+// item = one wave: a tile of 64 consecutive receivers (one per lane) against one chunk
+// of source atoms, staged through LDS 64 at a time; images are looped in registers.
+// Every directed pair is evaluated by its receiver's lane, both directions of a pair
+// use their own weights, so forces need no scatter. Each item writes per-receiver
+// partials for its chunk; xnn_d4 reductions sum the chunks in a fixed order
+// (deterministic, no atomics). Positions and cells in Angstrom, lengths in the kernel
+// in bohr, all float64.
+#include <algorithm>
+#include <cmath>
+#include <cstdint>
+
+#include "common.h"
+#include "device.h"
+
+namespace xnn {
+
+constexpr int kD4Tile = 64;     // receivers per item (lanes of one wave)
+constexpr int kD4Sub = 64;      // sources per LDS stage
+constexpr int kD4MaxChunks = 128;
+constexpr int kNW = 23;         // Casimir-Polder frequencies
+constexpr double kBohr = 0.5291772109044924;
+constexpr double kSqrtPi = 1.7724538509055160273;
+
+struct D4Work {
+  int64_t chunk;   // source atoms per chunk (multiple of kD4Sub)
+  int64_t n_cy;    // chunk slots per tile
+  int64_t n_tiles;
+};
+
+// chunk size and slots: at most kD4MaxChunks chunks of the largest structure, and the
+// slots cover the source span of any 64-receiver tile (one structure: N atoms; a batch:
+// the tile's structures, at most 64 + 2 (max_atoms - 1) atoms)
+static D4Work d4_work(int64_t n_nodes, int64_t n_graphs, int64_t max_atoms) {
+  D4Work w;
+  const int64_t span = n_graphs <= 1 ? n_nodes : std::min<int64_t>(n_nodes, kD4Tile + 2 * max_atoms);
+  int64_t subs = (std::max<int64_t>(max_atoms, 1) + (int64_t)kD4Sub * kD4MaxChunks - 1) /
+                 ((int64_t)kD4Sub * kD4MaxChunks);
+  w.chunk = kD4Sub * std::max<int64_t>(subs, 1);
+  w.n_cy = (span + w.chunk - 1) / w.chunk + 1;
+  w.n_tiles = (n_nodes + kD4Tile - 1) / kD4Tile;
+  return w;
+}
+
+// Structure geometry of one lane: cell rows (Angstrom) and image counts per axis.
+struct Lattice {
+  double a[9];
+  int n0, n1, n2;
+};
+
+__device__ inline void load_lattice(const double* __restrict__ cell,
+                                    const int32_t* __restrict__ images, int b, Lattice& L) {
+  if (cell == nullptr) {
+#pragma unroll
+    for (int k = 0; k < 9; ++k) L.a[k] = 0.0;
+    L.n0 = L.n1 = L.n2 = 0;
+    return;
+  }
+#pragma unroll
+  for (int k = 0; k < 9; ++k) L.a[k] = cell[9 * (int64_t)b + k];
+  L.n0 = images[3 * b + 0];
+  L.n1 = images[3 * b + 1];
+  L.n2 = images[3 * b + 2];
+}
+
+// quintic switch and its r-derivative (dispersion.py:42-67); width <= 0: sharp
+__device__ inline void switch_d(double r, double cutoff, double width, double& sw, double& dsw) {
+  if (width <= 0.0) {
+    sw = 1.0;
+    dsw = 0.0;
+    return;
+  }
+  const double w = width < cutoff ? width : cutoff;
+  double x = (cutoff - r) / w;
+  if (x >= 1.0) {
+    sw = 1.0;
+    dsw = 0.0;
+  } else if (x <= 0.0) {
+    sw = 0.0;
+    dsw = 0.0;
+  } else {
+    sw = x * x * x * (10.0 + x * (6.0 * x - 15.0));
+    const double om = 1.0 - x;
+    dsw = -30.0 * x * x * om * om / w;
+  }
+}
+
+// source data staged in LDS (one stage of kD4Sub atoms)
+struct D4Stage {
+  double x[kD4Sub], y[kD4Sub], z[kD4Sub];
+  double w[kD4Sub];       // backward weight of the source (its upstream gradient)
+  double w2[kD4Sub];      // second weight (CN: EEQ-count gradient)
+  int sp[kD4Sub];         // species
+  int b[kD4Sub];          // structure
+};
+
+// ---------------------------------------------------------------- coordination numbers
+struct CnParams {
+  double cut_cn, cut_eeq, kcn, k4, k5, k6;
+};
+
+// BACKWARD = false: partial[cy][0/1][i] = (cn_d4, cn_raw) sums of this chunk.
+// BACKWARD = true:  partial[cy][0..11][i] = grad_pos (3), cell gradient n (x) g (9).
+template <bool BACKWARD>
+__global__ __launch_bounds__(64) void d4_cn_kernel(
+    const double* __restrict__ pos, int64_t n_nodes, const int32_t* __restrict__ species,
+    const int32_t* __restrict__ batch, const int64_t* __restrict__ node_ptr,
+    const double* __restrict__ cell, const int32_t* __restrict__ images,
+    const double* __restrict__ rcov, const double* __restrict__ en, CnParams prm,
+    const double* __restrict__ g_cn, const double* __restrict__ g_raw, int64_t chunk,
+    int64_t n_cy, double* __restrict__ partial) {
+  __shared__ D4Stage st;
+  const int lane = threadIdx.x;
+  const int64_t t = blockIdx.x, cy = blockIdx.y;
+  const int64_t i = t * kD4Tile + lane;
+  const bool live = i < n_nodes;
+  // source range of the tile's structures, in chunks
+  const int64_t i_first = t * kD4Tile, i_last = std::min<int64_t>(i_first + kD4Tile, n_nodes) - 1;
+  const int64_t s_lo = node_ptr[batch[i_first]], s_hi = node_ptr[batch[i_last] + 1];
+  const int64_t c = s_lo / chunk + cy;
+  const int64_t j0 = std::max<int64_t>(c * chunk, s_lo), j1 = std::min<int64_t>((c + 1) * chunk, s_hi);
+  constexpr int NP = BACKWARD ? 12 : 2;
+  double acc[NP];
+#pragma unroll
+  for (int k = 0; k < NP; ++k) acc[k] = 0.0;
+  double xi = 0, yi = 0, zi = 0, rci = 0, eni = 0, gi = 0, g2i = 0;
+  int bi = -1;
+  Lattice L;
+  if (live) {
+    xi = pos[3 * i];
+    yi = pos[3 * i + 1];
+    zi = pos[3 * i + 2];
+    const int s = species[i];
+    rci = rcov[s];
+    eni = en[s];
+    bi = batch[i];
+    if (BACKWARD) {
+      gi = g_cn ? g_cn[i] : 0.0;
+      g2i = g_raw ? g_raw[i] : 0.0;
+    }
+    load_lattice(cell, images, bi, L);
+  } else {
+    load_lattice(nullptr, nullptr, 0, L);
+  }
+  const double cmax = prm.cut_cn > prm.cut_eeq ? prm.cut_cn : prm.cut_eeq;
+  for (int64_t base = j0; base < j1; base += kD4Sub) {
+    const int cnt = (int)std::min<int64_t>(kD4Sub, j1 - base);
+    __syncthreads();
+    if (lane < cnt) {
+      const int64_t j = base + lane;
+      st.x[lane] = pos[3 * j];
+      st.y[lane] = pos[3 * j + 1];
+      st.z[lane] = pos[3 * j + 2];
+      st.sp[lane] = species[j];
+      st.b[lane] = batch[j];
+      if (BACKWARD) {
+        st.w[lane] = g_cn ? g_cn[j] : 0.0;
+        st.w2[lane] = g_raw ? g_raw[j] : 0.0;
+      }
+    }
+    __syncthreads();
+    if (!live) continue;
+    for (int jj = 0; jj < cnt; ++jj) {
+      if (st.b[jj] != bi) continue;
+      const int sj = st.sp[jj];
+      const double rc = rci + rcov[sj];
+      const double den = fabs(eni - en[sj]) + prm.k5;
+      const double enf = prm.k4 * exp(-den * den / prm.k6);
+      const double dx = xi - st.x[jj], dy = yi - st.y[jj], dz = zi - st.z[jj];
+      const double wsum = BACKWARD ? gi + st.w[jj] : 0.0;
+      const double w2sum = BACKWARD ? g2i + st.w2[jj] : 0.0;
+      for (int n0 = -L.n0; n0 <= L.n0; ++n0)
+        for (int n1 = -L.n1; n1 <= L.n1; ++n1)
+          for (int n2 = -L.n2; n2 <= L.n2; ++n2) {
+            const double vx = (dx + (n0 * L.a[0] + n1 * L.a[3] + n2 * L.a[6])) / kBohr;
+            const double vy = (dy + (n0 * L.a[1] + n1 * L.a[4] + n2 * L.a[7])) / kBohr;
+            const double vz = (dz + (n0 * L.a[2] + n1 * L.a[5] + n2 * L.a[8])) / kBohr;
+            const double r2 = vx * vx + vy * vy + vz * vz;
+            if (r2 <= 0.0 || r2 > cmax * cmax) continue;
+            const double r = sqrt(r2);
+            const bool in_cn = r <= prm.cut_cn, in_eeq = r <= prm.cut_eeq;
+            const double x = -prm.kcn * (r - rc) / rc;
+            if (!BACKWARD) {
+              const double count = 0.5 * (1.0 + erf(x));
+              if (in_cn) acc[0] += enf * count;
+              if (in_eeq) acc[1] += count;
+            } else {
+              // d count / d r = -k0 exp(-x^2) / (rc sqrt(pi))
+              const double dcount = -prm.kcn * exp(-x * x) / (rc * kSqrtPi);
+              const double both = (in_cn ? wsum * enf : 0.0) + (in_eeq ? w2sum : 0.0);
+              const double own = (in_cn ? gi * enf : 0.0) + (in_eeq ? g2i : 0.0);
+              // per Angstrom of the edge vector: d r_bohr / d v = v_bohr / (r bohr)
+              const double s = dcount / (r * kBohr);
+              acc[0] += both * s * vx;
+              acc[1] += both * s * vy;
+              acc[2] += both * s * vz;
+              const double ox = own * s * vx, oy = own * s * vy, oz = own * s * vz;
+              acc[3] += n0 * ox; acc[4] += n0 * oy; acc[5] += n0 * oz;
+              acc[6] += n1 * ox; acc[7] += n1 * oy; acc[8] += n1 * oz;
+              acc[9] += n2 * ox; acc[10] += n2 * oy; acc[11] += n2 * oz;
+            }
+          }
+    }
+  }
+  if (live) {
+#pragma unroll
+    for (int k = 0; k < NP; ++k) partial[((int64_t)cy * NP + k) * n_nodes + i] = acc[k];
+  }
+}
+
+// ---------------------------------------------------------------- two-body term
+struct PairParams {
+  double s6, s8, a1, a2, cutoff, width;  // cutoff, width in bohr
+};
+
+__constant__ double c_cp3[kNW];   // (3 / pi) * Casimir-Polder weights
+
+// BACKWARD = false: partial[cy][0][i] = sum of -1/2 C6 f(r) over this chunk.
+// BACKWARD = true:  partial[cy][0..11][i] = grad_pos (3), cell gradient (9), and
+//                   partial_alpha[cy][w][i] = dE/d alpha_i(w) (23).
+template <bool BACKWARD>
+__global__ __launch_bounds__(64) void d4_pair_kernel(
+    const double* __restrict__ pos, int64_t n_nodes, const int32_t* __restrict__ species,
+    const int32_t* __restrict__ batch, const int64_t* __restrict__ node_ptr,
+    const double* __restrict__ cell, const int32_t* __restrict__ images,
+    const double* __restrict__ r4r2, const double* __restrict__ alpha, PairParams prm,
+    const double* __restrict__ g_e2, int64_t chunk, int64_t n_cy, double* __restrict__ partial,
+    double* __restrict__ partial_alpha) {
+  __shared__ D4Stage st;
+  __shared__ double sa[kNW][kD4Sub];
+  const int lane = threadIdx.x;
+  const int64_t t = blockIdx.x, cy = blockIdx.y;
+  const int64_t i = t * kD4Tile + lane;
+  const bool live = i < n_nodes;
+  const int64_t i_first = t * kD4Tile, i_last = std::min<int64_t>(i_first + kD4Tile, n_nodes) - 1;
+  const int64_t s_lo = node_ptr[batch[i_first]], s_hi = node_ptr[batch[i_last] + 1];
+  const int64_t c = s_lo / chunk + cy;
+  const int64_t j0 = std::max<int64_t>(c * chunk, s_lo), j1 = std::min<int64_t>((c + 1) * chunk, s_hi);
+  constexpr int NP = BACKWARD ? 12 : 1;
+  double acc[NP];
+#pragma unroll
+  for (int k = 0; k < NP; ++k) acc[k] = 0.0;
+  double ai[kNW], da[kNW];
+#pragma unroll
+  for (int w = 0; w < kNW; ++w) {
+    ai[w] = 0.0;
+    da[w] = 0.0;
+  }
+  double xi = 0, yi = 0, zi = 0, qi = 0, gi = 0;
+  int bi = -1;
+  Lattice L;
+  if (live) {
+    xi = pos[3 * i];
+    yi = pos[3 * i + 1];
+    zi = pos[3 * i + 2];
+    qi = r4r2[species[i]];
+    bi = batch[i];
+    if (BACKWARD) gi = g_e2[i];
+#pragma unroll
+    for (int w = 0; w < kNW; ++w) ai[w] = alpha[(int64_t)kNW * i + w] * c_cp3[w];
+    load_lattice(cell, images, bi, L);
+  } else {
+    load_lattice(nullptr, nullptr, 0, L);
+  }
+  const double rc2 = prm.cutoff * prm.cutoff;
+  for (int64_t base = j0; base < j1; base += kD4Sub) {
+    const int cnt = (int)std::min<int64_t>(kD4Sub, j1 - base);
+    __syncthreads();
+    if (lane < cnt) {
+      const int64_t j = base + lane;
+      st.x[lane] = pos[3 * j];
+      st.y[lane] = pos[3 * j + 1];
+      st.z[lane] = pos[3 * j + 2];
+      st.sp[lane] = species[j];
+      st.b[lane] = batch[j];
+      if (BACKWARD) st.w[lane] = g_e2[j];
+#pragma unroll
+      for (int w = 0; w < kNW; ++w) sa[w][lane] = alpha[(int64_t)kNW * j + w];
+    }
+    __syncthreads();
+    if (!live) continue;
+    for (int jj = 0; jj < cnt; ++jj) {
+      if (st.b[jj] != bi) continue;
+      double c6 = 0.0;
+#pragma unroll
+      for (int w = 0; w < kNW; ++w) c6 += ai[w] * sa[w][jj];
+      const double rr = 3.0 * qi * r4r2[st.sp[jj]];
+      const double r0 = prm.a1 * sqrt(rr) + prm.a2;
+      const double r02 = r0 * r0;
+      const double r06 = r02 * r02 * r02, r08 = r06 * r02;
+      const double dx = xi - st.x[jj], dy = yi - st.y[jj], dz = zi - st.z[jj];
+      const double wsum = BACKWARD ? gi + st.w[jj] : 0.0;
+      double fsum = 0.0;  // sum over images of f(r): d E / d C6 of the pair
+      for (int n0 = -L.n0; n0 <= L.n0; ++n0)
+        for (int n1 = -L.n1; n1 <= L.n1; ++n1)
+          for (int n2 = -L.n2; n2 <= L.n2; ++n2) {
+            const double vx = (dx + (n0 * L.a[0] + n1 * L.a[3] + n2 * L.a[6])) / kBohr;
+            const double vy = (dy + (n0 * L.a[1] + n1 * L.a[4] + n2 * L.a[7])) / kBohr;
+            const double vz = (dz + (n0 * L.a[2] + n1 * L.a[5] + n2 * L.a[8])) / kBohr;
+            const double r2 = vx * vx + vy * vy + vz * vz;
+            if (r2 <= 0.0 || r2 > rc2) continue;
+            const double r = sqrt(r2);
+            double sw, dsw;
+            switch_d(r, prm.cutoff, prm.width, sw, dsw);
+            const double r6 = r2 * r2 * r2, r8 = r6 * r2;
+            const double t6 = 1.0 / (r6 + r06), t8 = 1.0 / (r8 + r08);
+            const double g = prm.s6 * t6 + prm.s8 * rr * t8;
+            const double f = sw * g;
+            if (!BACKWARD) {
+              acc[0] += -0.5 * c6 * f;
+            } else {
+              fsum += f;
+              // d f / d r
+              const double dg = -prm.s6 * 6.0 * r * r2 * r2 * t6 * t6 -
+                                prm.s8 * rr * 8.0 * r * r6 * t8 * t8;
+              const double df = dsw * g + sw * dg;
+              const double s = -0.5 * c6 * df / (r * kBohr);
+              acc[0] += wsum * s * vx;
+              acc[1] += wsum * s * vy;
+              acc[2] += wsum * s * vz;
+              const double ox = gi * s * vx, oy = gi * s * vy, oz = gi * s * vz;
+              acc[3] += n0 * ox; acc[4] += n0 * oy; acc[5] += n0 * oz;
+              acc[6] += n1 * ox; acc[7] += n1 * oy; acc[8] += n1 * oz;
+              acc[9] += n2 * ox; acc[10] += n2 * oy; acc[11] += n2 * oz;
+            }
+          }
+      if (BACKWARD && fsum != 0.0) {
+        const double k = -0.5 * wsum * fsum;
+#pragma unroll
+        for (int w = 0; w < kNW; ++w) da[w] += k * c_cp3[w] * sa[w][jj];
+      }
+    }
+  }
+  if (live) {
+#pragma unroll
+    for (int k = 0; k < NP; ++k) partial[((int64_t)cy * NP + k) * n_nodes + i] = acc[k];
+    if (BACKWARD) {
+#pragma unroll
+      for (int w = 0; w < kNW; ++w) partial_alpha[((int64_t)cy * kNW + w) * n_nodes + i] = da[w];
+    }
+  }
+}
+
+// out[i * nk + (k - k0)] = sum over chunk slots cy (in order) of partial[cy][k][i], for
+// the components k0 <= k < k0 + nk of a partial array of np components
+__global__ void d4_reduce_kernel(const double* __restrict__ partial, int64_t n_nodes, int np,
+                                 int k0, int nk, int64_t n_cy, double* __restrict__ out) {
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= n_nodes * nk) return;
+  const int64_t i = idx / nk;
+  const int k = k0 + (int)(idx - i * nk);
+  double s = 0.0;
+  for (int64_t cy = 0; cy < n_cy; ++cy) s += partial[(cy * np + k) * n_nodes + i];
+  out[idx] = s;
+}
+
+static void reduce_into(const double* partial, int64_t n_nodes, int np, int k0, int nk,
+                        int64_t n_cy, double* out, hipStream_t s) {
+  const int64_t n = n_nodes * nk;
+  if (n == 0 || out == nullptr) return;
+  hipLaunchKernelGGL(d4_reduce_kernel, dim3(grid_1d(n, 256)), dim3(256), 0, s, partial, n_nodes,
+                     np, k0, nk, n_cy, out);
+}
+
+static bool cp_ready[64] = {false};
+
+static int upload_cp(hipStream_t s) {
+  int dev = 0;
+  XNN_HIP_CHECK(hipGetDevice(&dev));
+  if (dev >= 0 && dev < 64 && cp_ready[dev]) return XNN_OK;
+  static const double freq[kNW] = {0.000001, 0.05, 0.1, 0.2, 0.3, 0.4, 0.5, 0.6, 0.7, 0.8, 0.9,
+                                   1.0, 1.2, 1.4, 1.6, 1.8, 2.0, 2.5, 3.0, 4.0, 5.0, 7.5, 10.0};
+  double cp3[kNW];
+  for (int k = 0; k < kNW; ++k) {
+    const double lo = k > 0 ? freq[k] - freq[k - 1] : 0.0;
+    const double hi = k < kNW - 1 ? freq[k + 1] - freq[k] : 0.0;
+    cp3[k] = (3.0 / M_PI) * 0.5 * (lo + hi);
+  }
+  XNN_HIP_CHECK(hipMemcpyToSymbol(HIP_SYMBOL(c_cp3), cp3, sizeof(cp3), 0, hipMemcpyHostToDevice));
+  if (dev >= 0 && dev < 64) cp_ready[dev] = true;
+  return XNN_OK;
+}
+
+static int d4_check(const double* pos, int64_t n_nodes, const int32_t* species,
+                    const int32_t* batch, const int64_t* node_ptr, int64_t n_graphs,
+                    const double* cell, const int32_t* images, int64_t max_atoms) {
+  XNN_REQUIRE(n_nodes >= 0 && n_graphs >= 1, "negative size or no structure");
+  XNN_REQUIRE(n_nodes == 0 || (pos && species && batch && node_ptr), "NULL atom input");
+  XNN_REQUIRE(cell == nullptr || images != nullptr, "a cell needs the image counts");
+  XNN_REQUIRE(max_atoms >= 1 || n_nodes == 0, "max_atoms must be >= 1");
+  return XNN_OK;
+}
+
+}  // namespace xnn
+
+using namespace xnn;
+
+extern "C" {
+
+size_t xnn_d4_workspace_bytes(int64_t n_nodes, int64_t n_graphs, int64_t max_atoms) {
+  if (n_nodes <= 0) return 0;
+  const D4Work w = d4_work(n_nodes, n_graphs, max_atoms);
+  // the largest user: the pair backward, 12 + 23 values per receiver and chunk slot
+  return (size_t)(w.n_cy * (12 + kNW) * n_nodes) * sizeof(double);
+}
+
+int xnn_d4_coordination(const double* pos, int64_t n_nodes, const int32_t* species,
+                        const int32_t* batch, const int64_t* node_ptr, int64_t n_graphs,
+                        int64_t max_atoms, const double* cell, const int32_t* images,
+                        const double* rcov, const double* en, const xnn_d4_cn_params* prm,
+                        double* cn_d4, double* cn_raw, void* workspace, size_t workspace_bytes,
+                        xnn_stream_t stream) {
+  const int st = d4_check(pos, n_nodes, species, batch, node_ptr, n_graphs, cell, images, max_atoms);
+  if (st != XNN_OK) return st;
+  XNN_REQUIRE(prm && rcov && en, "NULL tables or params");
+  XNN_REQUIRE(n_nodes == 0 || (cn_d4 && cn_raw), "NULL output");
+  if (n_nodes == 0) return XNN_OK;
+  const D4Work w = d4_work(n_nodes, n_graphs, max_atoms);
+  const size_t need = (size_t)(w.n_cy * 2 * n_nodes) * sizeof(double);
+  XNN_REQUIRE(workspace != nullptr && workspace_bytes >= need, "workspace too small (%zu < %zu)",
+              workspace_bytes, need);
+  const CnParams p{prm->cutoff_cn, prm->cutoff_eeq_cn, prm->kcn, prm->k4, prm->k5, prm->k6};
+  hipStream_t s = as_hip(stream);
+  double* part = static_cast<double*>(workspace);
+  hipLaunchKernelGGL(d4_cn_kernel<false>, dim3((unsigned)w.n_tiles, (unsigned)w.n_cy),
+                     dim3(kD4Tile), 0, s, pos, n_nodes, species, batch, node_ptr, cell, images,
+                     rcov, en, p, nullptr, nullptr, w.chunk, w.n_cy, part);
+  XNN_LAUNCH_CHECK();
+  reduce_into(part, n_nodes, 2, 0, 1, w.n_cy, cn_d4, s);
+  reduce_into(part, n_nodes, 2, 1, 1, w.n_cy, cn_raw, s);
+  XNN_LAUNCH_CHECK();
+  return XNN_OK;
+}
+
+int xnn_d4_coordination_backward(const double* pos, int64_t n_nodes, const int32_t* species,
+                                 const int32_t* batch, const int64_t* node_ptr, int64_t n_graphs,
+                                 int64_t max_atoms, const double* cell, const int32_t* images,
+                                 const double* rcov, const double* en,
+                                 const xnn_d4_cn_params* prm, const double* g_cn_d4,
+                                 const double* g_cn_raw, double* grad_pos, double* cell_partial,
+                                 void* workspace, size_t workspace_bytes, xnn_stream_t stream) {
+  const int st = d4_check(pos, n_nodes, species, batch, node_ptr, n_graphs, cell, images, max_atoms);
+  if (st != XNN_OK) return st;
+  XNN_REQUIRE(prm && rcov && en, "NULL tables or params");
+  XNN_REQUIRE(n_nodes == 0 || grad_pos, "NULL grad_pos");
+  if (n_nodes == 0) return XNN_OK;
+  const D4Work w = d4_work(n_nodes, n_graphs, max_atoms);
+  const size_t need = (size_t)(w.n_cy * 12 * n_nodes) * sizeof(double);
+  XNN_REQUIRE(workspace != nullptr && workspace_bytes >= need, "workspace too small (%zu < %zu)",
+              workspace_bytes, need);
+  const CnParams p{prm->cutoff_cn, prm->cutoff_eeq_cn, prm->kcn, prm->k4, prm->k5, prm->k6};
+  hipStream_t s = as_hip(stream);
+  double* part = static_cast<double*>(workspace);
+  hipLaunchKernelGGL(d4_cn_kernel<true>, dim3((unsigned)w.n_tiles, (unsigned)w.n_cy),
+                     dim3(kD4Tile), 0, s, pos, n_nodes, species, batch, node_ptr, cell, images,
+                     rcov, en, p, g_cn_d4, g_cn_raw, w.chunk, w.n_cy, part);
+  XNN_LAUNCH_CHECK();
+  reduce_into(part, n_nodes, 12, 0, 3, w.n_cy, grad_pos, s);
+  reduce_into(part, n_nodes, 12, 3, 9, w.n_cy, cell_partial, s);
+  XNN_LAUNCH_CHECK();
+  return XNN_OK;
+}
+
+int xnn_d4_two_body(const double* pos, int64_t n_nodes, const int32_t* species,
+                    const int32_t* batch, const int64_t* node_ptr, int64_t n_graphs,
+                    int64_t max_atoms, const double* cell, const int32_t* images,
+                    const double* r4r2, const double* alpha, const xnn_d4_pair_params* prm,
+                    double* e2, void* workspace, size_t workspace_bytes, xnn_stream_t stream) {
+  const int st = d4_check(pos, n_nodes, species, batch, node_ptr, n_graphs, cell, images, max_atoms);
+  if (st != XNN_OK) return st;
+  XNN_REQUIRE(prm && r4r2, "NULL tables or params");
+  XNN_REQUIRE(n_nodes == 0 || (alpha && e2), "NULL alpha or output");
+  XNN_REQUIRE(prm->cutoff > 0.0, "pair cutoff must be positive");
+  if (n_nodes == 0) return XNN_OK;
+  const D4Work w = d4_work(n_nodes, n_graphs, max_atoms);
+  const size_t need = (size_t)(w.n_cy * n_nodes) * sizeof(double);
+  XNN_REQUIRE(workspace != nullptr && workspace_bytes >= need, "workspace too small (%zu < %zu)",
+              workspace_bytes, need);
+  hipStream_t s = as_hip(stream);
+  const int up = upload_cp(s);
+  if (up != XNN_OK) return up;
+  const PairParams p{prm->s6, prm->s8, prm->a1, prm->a2, prm->cutoff, prm->width};
+  double* part = static_cast<double*>(workspace);
+  hipLaunchKernelGGL(d4_pair_kernel<false>, dim3((unsigned)w.n_tiles, (unsigned)w.n_cy),
+                     dim3(kD4Tile), 0, s, pos, n_nodes, species, batch, node_ptr, cell, images,
+                     r4r2, alpha, p, nullptr, w.chunk, w.n_cy, part, nullptr);
+  XNN_LAUNCH_CHECK();
+  reduce_into(part, n_nodes, 1, 0, 1, w.n_cy, e2, s);
+  XNN_LAUNCH_CHECK();
+  return XNN_OK;
+}
+
+int xnn_d4_two_body_backward(const double* pos, int64_t n_nodes, const int32_t* species,
+                             const int32_t* batch, const int64_t* node_ptr, int64_t n_graphs,
+                             int64_t max_atoms, const double* cell, const int32_t* images,
+                             const double* r4r2, const double* alpha,
+                             const xnn_d4_pair_params* prm, const double* g_e2, double* grad_pos,
+                             double* cell_partial, double* grad_alpha, void* workspace,
+                             size_t workspace_bytes, xnn_stream_t stream) {
+  const int st = d4_check(pos, n_nodes, species, batch, node_ptr, n_graphs, cell, images, max_atoms);
+  if (st != XNN_OK) return st;
+  XNN_REQUIRE(prm && r4r2, "NULL tables or params");
+  XNN_REQUIRE(n_nodes == 0 || (alpha && g_e2 && grad_pos), "NULL alpha, g_e2 or grad_pos");
+  XNN_REQUIRE(prm->cutoff > 0.0, "pair cutoff must be positive");
+  if (n_nodes == 0) return XNN_OK;
+  const D4Work w = d4_work(n_nodes, n_graphs, max_atoms);
+  const size_t need = (size_t)(w.n_cy * (12 + kNW) * n_nodes) * sizeof(double);
+  XNN_REQUIRE(workspace != nullptr && workspace_bytes >= need, "workspace too small (%zu < %zu)",
+              workspace_bytes, need);
+  hipStream_t s = as_hip(stream);
+  const int up = upload_cp(s);
+  if (up != XNN_OK) return up;
+  const PairParams p{prm->s6, prm->s8, prm->a1, prm->a2, prm->cutoff, prm->width};
+  double* part = static_cast<double*>(workspace);
+  double* part_a = part + w.n_cy * 12 * n_nodes;
+  hipLaunchKernelGGL(d4_pair_kernel<true>, dim3((unsigned)w.n_tiles, (unsigned)w.n_cy),
+                     dim3(kD4Tile), 0, s, pos, n_nodes, species, batch, node_ptr, cell, images,
+                     r4r2, alpha, p, g_e2, w.chunk, w.n_cy, part, part_a);
+  XNN_LAUNCH_CHECK();
+  reduce_into(part, n_nodes, 12, 0, 3, w.n_cy, grad_pos, s);
+  reduce_into(part, n_nodes, 12, 3, 9, w.n_cy, cell_partial, s);
+  reduce_into(part_a, n_nodes, kNW, 0, kNW, w.n_cy, grad_alpha, s);
+  XNN_LAUNCH_CHECK();
+  return XNN_OK;
+}
+
+}  // extern "C"
