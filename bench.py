@@ -182,12 +182,69 @@ def cpu_baseline(g, model, rc, kw, max_edges: int) -> dict:
                       f"torch threads={torch.get_num_threads()}, os.cpu_count()={os.cpu_count()}"}
 
 
+def bench_d4(steps: int, warmup: int) -> dict:
+    """D4 two-body energy + forces + stress of the 5,000-atom organic box (36.8 A cell,
+    upstream cutoffs 60 / 30 / 25 bohr): CN kernel, polarizabilities, pair kernel and
+    both backward kernels per step. The charges are fixed (zero): the dense periodic
+    charge solve of 5,000 atoms is not part of this path."""
+    import xnn_amd.dispersion as XD
+    from xnn_amd import synthetic
+    dev = torch.device("cuda:0")
+    s = synthetic.organic_box(seed=0)
+    tables = XD.load_d4_tables(os.path.join(ROOT, "tests", "golden", "d4_tables_hcnoar.npz"))
+    model = XD.DFTD4(tables).to(dev)
+    z = torch.tensor(s.numbers, device=dev)
+    pos0 = torch.tensor(s.pos, dtype=torch.float64, device=dev)
+    cell0 = torch.tensor(s.cell, dtype=torch.float64, device=dev)[None]
+    pbc = torch.ones((1, 3), dtype=torch.bool)
+    n_atoms = torch.tensor([len(s.numbers)])
+    q = torch.zeros(len(s.numbers), dtype=torch.float64, device=dev)
+
+    def step():
+        pos = pos0.clone().requires_grad_(True)
+        cell = cell0.clone().requires_grad_(True)
+        out = model.evaluate(z, pos, cell, pbc, n_atoms, charges=q)
+        gp, gc = torch.autograd.grad(out["energy"].sum(), [pos, cell])
+        return out["energy"], gp, gc
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        e, gp, gc = step()
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) / steps * 1e3
+    # pair-image terms within the pair cutoff (for the rate), counted image by image
+    imgs = XD.image_counts(cell0, pbc, model.cutoff_pair)[0].tolist()
+    n_terms = 0
+    with torch.no_grad():
+        d0 = pos0[:, None, :] - pos0[None, :, :]
+        rc2 = model.cutoff_pair ** 2
+        for a in range(-imgs[0], imgs[0] + 1):
+            for b in range(-imgs[1], imgs[1] + 1):
+                for c in range(-imgs[2], imgs[2] + 1):
+                    t = a * cell0[0, 0] + b * cell0[0, 1] + c * cell0[0, 2]
+                    r2 = ((d0 + t) ** 2).sum(-1)
+                    n_terms += int(((r2 <= rc2) & (r2 > 0)).sum())
+        del d0
+    return {"metric": "D4 pair-image terms/s, energy+forces+stress, 5000-atom organic box",
+            "value": n_terms / (ms * 1e-3), "unit": "terms/s", "n_gpus": 1, "steps": steps,
+            "warmup": warmup, "ms_per_step": ms, "higher_is_better": True, "scaling": "weak",
+            "vs_baseline": None, "dtype": "f64", "data": "synthetic (seeded generator)",
+            "config": {"workload": "d4_organic_box_5000_atoms", "atoms": len(s.numbers),
+                       "pair_image_terms": n_terms, "cutoff_pair_bohr": 60.0,
+                       "cutoff_cn_bohr": 30.0, "cutoff_eeq_cn_bohr": 25.0,
+                       "charges": "fixed zero (charge model not timed)",
+                       "energy_eV": float(e[0])}}
+
+
 def main() -> None:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--config", default="water", choices=["water", "argon", "ragged"])
+    ap.add_argument("--config", default="water", choices=["water", "argon", "ragged", "d4"])
     ap.add_argument("--graph", action=argparse.BooleanOptionalAction, default=True,
                     help="time replays of the step captured as one HIP graph")
     ap.add_argument("--cpu-edges", type=int, default=480_000,
@@ -206,6 +263,9 @@ def main() -> None:
         raise SystemExit("bench.py needs a GPU")
     if args.copy_calibration:
         copy_calibration()
+        return
+    if args.config == "d4":
+        print(json.dumps(bench_d4(args.steps, args.warmup)), flush=True)
         return
     device = torch.device("cuda:0")
     torch.cuda.set_device(device)

@@ -175,3 +175,37 @@ def test_batch_equals_separate_structures(tables):
     e = [float(_eval(model, m1, z1)[0]["energy"][0]), float(_eval(model, m2, z2)[0]["energy"][0]),
          float(_eval(model, pc, zc, cell)[0]["energy"][0])]
     np.testing.assert_allclose(out["energy"].cpu().numpy(), e, rtol=1e-12)
+
+
+def test_stress_matches_finite_strain(tables):
+    """ForceStressOutput(D4Dispersion): stress against central differences of the energy
+    under symmetric strain of positions and cell (test_d4.py:217-226: 1e-7)."""
+    import xnn_amd as xa
+    import xnn_amd.dispersion as XD
+    _note("d4 stress vs finite strain")
+    pos, z = _cluster(8, seed=4)
+    cell = np.array([[6.0, 0, 0], [0.8, 5.7, 0], [-0.4, 0.6, 6.2]])
+    model = xa.ForceStressOutput(XD.D4Dispersion(tables=tables, **FAST).to(DEV),
+                                 compute_stress=True).eval()
+
+    def graph(p, c):
+        return xa.AtomicGraph(pos=torch.tensor(p, device=DEV), atomic_numbers=torch.tensor(z, device=DEV),
+                              edge_index=torch.zeros((2, 0), dtype=torch.long, device=DEV),
+                              cell_shifts=torch.zeros((0, 3), dtype=torch.long, device=DEV),
+                              batch=torch.zeros(len(z), dtype=torch.long, device=DEV),
+                              n_atoms=torch.tensor([len(z)], device=DEV),
+                              cell=torch.tensor(c, device=DEV)[None],
+                              pbc=torch.ones((1, 3), dtype=torch.bool, device=DEV))
+
+    out = model(graph(pos, cell))
+    vol = abs(np.linalg.det(cell))
+    for (a, b) in [(0, 0), (1, 2), (2, 2)]:
+        eps = np.zeros((3, 3))
+        eps[a, b] = eps[b, a] = 1e-4
+        ep = float(model.model(graph(pos @ (np.eye(3) + eps), cell @ (np.eye(3) + eps)))["energy"][0])
+        em = float(model.model(graph(pos @ (np.eye(3) - eps), cell @ (np.eye(3) - eps)))["energy"][0])
+        fd = (ep - em) / 2e-4 / vol / (1 if a == b else 2)
+        assert abs(float(out["stress"][0, a, b]) - fd) < 1e-7
+    # forces too, and the wrapper's bookkeeping
+    assert out["forces"].shape == (len(z), 3)
+    assert torch.equal(out["energy_disp"], out["energy"])

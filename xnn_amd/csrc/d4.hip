@@ -56,17 +56,70 @@ static D4Work d4_work(int64_t n_nodes, int64_t n_graphs, int64_t max_atoms) {
   return w;
 }
 
-// Structure geometry of one lane: cell rows (Angstrom) and image counts per axis.
+// Structure geometry of one lane: cell rows (Angstrom), image counts per axis, and the
+// columns of the inverse cell scaled to interplanar spacings (for image pruning).
 struct Lattice {
   double a[9];
+  double inv[9];   // inverse cell, f = d @ inv
+  double sp[3];    // interplanar spacing per axis, 1 / |inv[:, axis]|
   int n0, n1, n2;
 };
+
+__device__ inline void lattice_inverse(Lattice& L) {
+  const double* a = L.a;
+  const double c00 = a[4] * a[8] - a[5] * a[7], c01 = a[2] * a[7] - a[1] * a[8],
+               c02 = a[1] * a[5] - a[2] * a[4];
+  const double det = a[0] * c00 + a[3] * c01 + a[6] * c02;
+  if (fabs(det) < 1e-300) {
+#pragma unroll
+    for (int k = 0; k < 9; ++k) L.inv[k] = 0.0;
+    L.sp[0] = L.sp[1] = L.sp[2] = 1e300;
+    return;
+  }
+  const double id = 1.0 / det;
+  L.inv[0] = c00 * id;
+  L.inv[1] = c01 * id;
+  L.inv[2] = c02 * id;
+  L.inv[3] = (a[5] * a[6] - a[3] * a[8]) * id;
+  L.inv[4] = (a[0] * a[8] - a[2] * a[6]) * id;
+  L.inv[5] = (a[2] * a[3] - a[0] * a[5]) * id;
+  L.inv[6] = (a[3] * a[7] - a[4] * a[6]) * id;
+  L.inv[7] = (a[1] * a[6] - a[0] * a[7]) * id;
+  L.inv[8] = (a[0] * a[4] - a[1] * a[3]) * id;
+#pragma unroll
+  for (int c = 0; c < 3; ++c) {
+    const double n2 = L.inv[c] * L.inv[c] + L.inv[3 + c] * L.inv[3 + c] + L.inv[6 + c] * L.inv[6 + c];
+    L.sp[c] = n2 > 0.0 ? 1.0 / sqrt(n2) : 1e300;
+  }
+}
+
+// Images n_c in [lo_c, hi_c] per axis that can lie within rc (Angstrom) of d: the
+// fractional component f_c + n_c of d + n @ cell bounds its length from below by
+// |f_c + n_c| sp_c, so other images are farther than rc (a small slack keeps the
+// bound conservative under rounding).
+__device__ inline void image_window(const Lattice& L, double dx, double dy, double dz, double rc,
+                                    int lo[3], int hi[3]) {
+  const int nmax[3] = {L.n0, L.n1, L.n2};
+#pragma unroll
+  for (int c = 0; c < 3; ++c) {
+    if (nmax[c] == 0) {
+      lo[c] = hi[c] = 0;
+      continue;
+    }
+    const double f = dx * L.inv[c] + dy * L.inv[3 + c] + dz * L.inv[6 + c];
+    const double w = rc / L.sp[c] + 1e-9;
+    const double m = (double)nmax[c];
+    lo[c] = (int)fmax(ceil(-w - f), -m);   // clamped as doubles, then converted
+    hi[c] = (int)fmin(floor(w - f), m);
+  }
+}
 
 __device__ inline void load_lattice(const double* __restrict__ cell,
                                     const int32_t* __restrict__ images, int b, Lattice& L) {
   if (cell == nullptr) {
 #pragma unroll
-    for (int k = 0; k < 9; ++k) L.a[k] = 0.0;
+    for (int k = 0; k < 9; ++k) L.a[k] = L.inv[k] = 0.0;
+    L.sp[0] = L.sp[1] = L.sp[2] = 1e300;
     L.n0 = L.n1 = L.n2 = 0;
     return;
   }
@@ -75,6 +128,7 @@ __device__ inline void load_lattice(const double* __restrict__ cell,
   L.n0 = images[3 * b + 0];
   L.n1 = images[3 * b + 1];
   L.n2 = images[3 * b + 2];
+  lattice_inverse(L);
 }
 
 // quintic switch and its r-derivative (dispersion.py:42-67); width <= 0: sharp
@@ -183,9 +237,11 @@ __global__ __launch_bounds__(64) void d4_cn_kernel(
       const double dx = xi - st.x[jj], dy = yi - st.y[jj], dz = zi - st.z[jj];
       const double wsum = BACKWARD ? gi + st.w[jj] : 0.0;
       const double w2sum = BACKWARD ? g2i + st.w2[jj] : 0.0;
-      for (int n0 = -L.n0; n0 <= L.n0; ++n0)
-        for (int n1 = -L.n1; n1 <= L.n1; ++n1)
-          for (int n2 = -L.n2; n2 <= L.n2; ++n2) {
+      int lo[3], hi[3];
+      image_window(L, dx, dy, dz, cmax * kBohr, lo, hi);
+      for (int n0 = lo[0]; n0 <= hi[0]; ++n0)
+        for (int n1 = lo[1]; n1 <= hi[1]; ++n1)
+          for (int n2 = lo[2]; n2 <= hi[2]; ++n2) {
             const double vx = (dx + (n0 * L.a[0] + n1 * L.a[3] + n2 * L.a[6])) / kBohr;
             const double vy = (dy + (n0 * L.a[1] + n1 * L.a[4] + n2 * L.a[7])) / kBohr;
             const double vz = (dz + (n0 * L.a[2] + n1 * L.a[5] + n2 * L.a[8])) / kBohr;
@@ -305,9 +361,11 @@ __global__ __launch_bounds__(64) void d4_pair_kernel(
       const double dx = xi - st.x[jj], dy = yi - st.y[jj], dz = zi - st.z[jj];
       const double wsum = BACKWARD ? gi + st.w[jj] : 0.0;
       double fsum = 0.0;  // sum over images of f(r): d E / d C6 of the pair
-      for (int n0 = -L.n0; n0 <= L.n0; ++n0)
-        for (int n1 = -L.n1; n1 <= L.n1; ++n1)
-          for (int n2 = -L.n2; n2 <= L.n2; ++n2) {
+      int lo[3], hi[3];
+      image_window(L, dx, dy, dz, prm.cutoff * kBohr, lo, hi);
+      for (int n0 = lo[0]; n0 <= hi[0]; ++n0)
+        for (int n1 = lo[1]; n1 <= hi[1]; ++n1)
+          for (int n2 = lo[2]; n2 <= hi[2]; ++n2) {
             const double vx = (dx + (n0 * L.a[0] + n1 * L.a[3] + n2 * L.a[6])) / kBohr;
             const double vy = (dy + (n0 * L.a[1] + n1 * L.a[4] + n2 * L.a[7])) / kBohr;
             const double vz = (dz + (n0 * L.a[2] + n1 * L.a[5] + n2 * L.a[8])) / kBohr;

@@ -438,3 +438,56 @@ def c6_matrix(alpha_iw: Tensor) -> Tensor:
           for k in range(23)]
     w = torch.tensor(cp, dtype=alpha_iw.dtype, device=alpha_iw.device)
     return (3.0 / math.pi) * (alpha_iw * w) @ alpha_iw.T
+
+
+# --------------------------------------------------------------------------- potentials
+class DispersionCorrection(nn.Module):
+    """A dispersion term as a potential, standalone or added to a short-range model
+    (dispersion.py:667-842): ``forward(data)`` returns the combined ``"energy"`` (B,) and
+    ``"node_energy"`` (eV) plus ``"energy_sr"``, ``"energy_disp"`` and the term's per-atom
+    quantities (``"eeq_charges"`` for the D4 charges). The HIP term needs no edges, so
+    ``cutoff`` is the wrapped model's own (0 standalone): graphs are built for the model
+    alone, and the wrapped model sees them unchanged."""
+
+    _RENAME = {"charges": "eeq_charges"}
+    edge_virial = False          # the term depends on the cell beyond the edge vectors
+
+    def __init__(self, term: nn.Module, model: Optional[nn.Module] = None):
+        super().__init__()
+        self.term = term
+        self.model = model
+        self.cutoff = float(getattr(model, "cutoff", 0.0)) if model is not None else 0.0
+
+    def forward(self, data) -> Dict[str, Tensor]:
+        disp = dict(self.term(data))
+        node_disp = disp.pop("node_energy")
+        energy_disp = disp.pop("energy")
+        if self.model is None:
+            out = {"node_energy": node_disp, "energy": energy_disp,
+                   "energy_sr": torch.zeros_like(energy_disp)}
+        else:
+            out = dict(self.model(data))
+            out["energy_sr"] = out["energy"]
+            out["energy"] = out["energy"] + energy_disp
+            out["node_energy"] = out["node_energy"] + node_disp.to(out["node_energy"].dtype)
+        out["energy_disp"] = energy_disp
+        for k, v in disp.items():
+            out[self._RENAME.get(k, k)] = v
+        return out
+
+
+class D4Dispersion(DispersionCorrection):
+    """D4 (two-body) dispersion as a potential, standalone or wrapped around a model
+    (d4.py:1321-1365). ``tables``: the per-element tables (dict or a path for
+    :func:`load_d4_tables`); ``d4_options``: keyword arguments of :class:`DFTD4`."""
+
+    def __init__(self, model: Optional[nn.Module] = None, tables=None, **d4_options):
+        if tables is None:
+            raise ValueError("D4Dispersion needs the per-element D4 tables (dict or .npz path)")
+        if isinstance(tables, str):
+            tables = load_d4_tables(tables)
+        super().__init__(DFTD4(tables, **d4_options), model)
+
+    @property
+    def d4(self) -> DFTD4:
+        return self.term
