@@ -30,7 +30,7 @@ import torch
 
 HBM_PEAK_GBS = 8000.0
 ROOT = os.path.dirname(os.path.abspath(__file__))
-TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "hbm_traffic_sh_msg_water_box.md")
+TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "hbm_traffic_message_kernels_water_box.md")
 
 
 def measured_traffic(kernel: str, workload: str):
