@@ -258,6 +258,54 @@ int xnn_d4_two_body_backward(const double* pos, int64_t n_nodes, const int32_t* 
                              double* cell_partial, double* grad_alpha, void* workspace,
                              size_t workspace_bytes, xnn_stream_t stream);
 
+/* D3 two-body dispersion on the same image walk (xnn_d4_workspace_bytes covers it).
+ * cn[i] = sum_{r <= cutoff_cn} 1 / (1 + exp(-kcn (rc / r - 1))), rc = rcov_i + rcov_j
+ * (bohr). Replaces DFTD3.coordination_numbers (d3.py:632-642). */
+int xnn_d3_coordination(const double* pos, int64_t n_nodes, const int32_t* species,
+                        const int32_t* batch, const int64_t* node_ptr, int64_t n_graphs,
+                        int64_t max_atoms, const double* cell, const int32_t* images,
+                        const double* rcov, double cutoff_cn, double kcn, double* cn,
+                        void* workspace, size_t workspace_bytes, xnn_stream_t stream);
+
+/* Gradient of sum_i g_cn[i] cn[i]: grad_pos (N,3), cell_partial (N,3,3, nullable). */
+int xnn_d3_coordination_backward(const double* pos, int64_t n_nodes, const int32_t* species,
+                                 const int32_t* batch, const int64_t* node_ptr, int64_t n_graphs,
+                                 int64_t max_atoms, const double* cell, const int32_t* images,
+                                 const double* rcov, double cutoff_cn, double kcn,
+                                 const double* g_cn, double* grad_pos, double* cell_partial,
+                                 void* workspace, size_t workspace_bytes, xnn_stream_t stream);
+
+typedef struct {
+  double s6, s8, a1, a2;   /* scalings; rational-damping radius a1 sqrt(C8/C6) + a2   */
+  double rs6, rs8, alp;    /* zero damping: radii scalings and exponent              */
+  double bet;              /* modified zero: shift; optimized power: exponent        */
+  double cutoff, width;    /* pair cutoff and switching width, bohr                  */
+  int32_t damping;         /* 0 bj, 1 zero, 2 mzero, 3 op                            */
+} xnn_d3_pair_params;
+
+/* e2[i] = sum_{j,n: r <= cutoff} -1/2 C6_ij sw(r) (s6 t6(r) + s8 rr t8(r)) with
+ * C6_ij = sum_ab W_i[a] W_j[b] c6ref[s_i][s_j][a][b] (weights (N,7), c6ref
+ * (S,S,7,7) by species), rr = 3 r4r2_i r4r2_j, and t6, t8 of the chosen damping with
+ * R0 = a1 sqrt(rr) + a2 (bj, op) or rvdw[s_i][s_j] (zero, mzero; (S,S), bohr).
+ * Replaces DFTD3.pair_c6 / pair_radius / two_body_energy (d3.py:651-722). */
+int xnn_d3_two_body(const double* pos, int64_t n_nodes, const int32_t* species,
+                    const int32_t* batch, const int64_t* node_ptr, int64_t n_graphs,
+                    int64_t max_atoms, const double* cell, const int32_t* images,
+                    const double* r4r2, const double* rvdw, const double* c6ref,
+                    int32_t n_species, const double* weights, const xnn_d3_pair_params* prm,
+                    double* e2, void* workspace, size_t workspace_bytes, xnn_stream_t stream);
+
+/* Gradients of sum_i g_e2[i] e2[i]: grad_pos (N,3), cell_partial (N,3,3, nullable),
+ * grad_weights (N,7, nullable; chained to the CN by the caller). */
+int xnn_d3_two_body_backward(const double* pos, int64_t n_nodes, const int32_t* species,
+                             const int32_t* batch, const int64_t* node_ptr, int64_t n_graphs,
+                             int64_t max_atoms, const double* cell, const int32_t* images,
+                             const double* r4r2, const double* rvdw, const double* c6ref,
+                             int32_t n_species, const double* weights,
+                             const xnn_d3_pair_params* prm, const double* g_e2, double* grad_pos,
+                             double* cell_partial, double* grad_weights, void* workspace,
+                             size_t workspace_bytes, xnn_stream_t stream);
+
 /* ------------------------------------------------------------------------ */
 /* Cell-list radius graph. Replaces build_neighbor_list (neighborlist.py:411-506):
  * same edge set (dist < cutoff in the geometry dtype), same [src,dst] and negated,

@@ -1,0 +1,121 @@
+"""GPU parity of the D3 path: the HIP coordination-number and two-body kernels against
+the oracle (float64, brute-force pair images) and the simple-dftd3 golden values
+(tests/common/test_d3.py:112-157)."""
+import os
+import sys
+
+import numpy as np
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+HERE = os.path.dirname(os.path.abspath(__file__))
+WATER = (np.array([[0.0, 0.0, 0.119262], [0.0, 0.763239, -0.477047],
+                   [0.0, -0.763239, -0.477047]]), [8, 1, 1])
+FAST = dict(cutoff_pair=9.0, cutoff_cn=8.0)
+
+
+def _note(msg):
+    print(f"[gpu-case] {msg}", flush=True)
+    sys.stdout.flush()
+
+
+@pytest.fixture(scope="module")
+def tables():
+    return dict(np.load(os.path.join(HERE, "golden", "d3_tables_hcnoar.npz"), allow_pickle=False))
+
+
+def _cluster(n, seed, box=6.0):
+    rng = np.random.default_rng(seed)
+    return rng.uniform(0, box - 1, (n, 3)), ([1, 8, 6, 7] * (n // 4) + [1] * (n % 4))[:n]
+
+
+def _eval(model, pos, z, cell=None, grad=False):
+    p = torch.tensor(pos, dtype=torch.float64, device=DEV, requires_grad=grad)
+    c = None if cell is None else torch.tensor(cell, dtype=torch.float64, device=DEV)[None].requires_grad_(grad)
+    out = model.evaluate(torch.tensor(z, device=DEV), p, c,
+                         None if c is None else torch.ones((1, 3), dtype=torch.bool),
+                         torch.tensor([len(z)]))
+    return out, p, c
+
+
+def _prm(damping):
+    import oracle.d3 as D3
+    prm = dict(D3.PBE0_D3BJ if damping in ("bj", "op") else D3.PBE0_D3ZERO)
+    if damping == "mzero":
+        prm["bet"] = 0.1
+    if damping == "op":
+        prm["bet"] = 6.0
+    return prm
+
+
+def test_water_golden_values_on_the_gpu(tables):
+    import xnn_amd.dispersion as XD
+    _note("d3 water golden")
+    bj, _, _ = _eval(XD.DFTD3(tables).to(DEV), *WATER)
+    assert abs(float(bj["energy"][0]) / XD.HARTREE - (-2.768885028766e-04)) < 1e-14
+    zero, _, _ = _eval(XD.DFTD3(tables, damping="zero").to(DEV), *WATER)
+    assert abs(float(zero["energy"][0]) / XD.HARTREE - (-4.644598055357e-06)) < 1e-16
+
+
+@pytest.mark.parametrize("damping", ["bj", "zero", "mzero", "op"])
+@pytest.mark.parametrize("case", ["molecule", "triclinic_switched"])
+def test_kernels_match_oracle(tables, damping, case):
+    """CN, per-atom energies and the position and cell gradients (through the CN-dependent
+    weights too) against autograd of the oracle, float64."""
+    import oracle.d3 as D3
+    import xnn_amd.dispersion as XD
+    from oracle.d4 import BOHR, edge_vectors_au, pair_images
+    _note(f"d3 kernels vs oracle: {damping} {case}")
+    prm = _prm(damping)
+    width, cell = 0.0, None
+    if case == "molecule":
+        pos, z = _cluster(12, seed=21)
+    else:
+        pos, z = _cluster(10, seed=22)
+        cell = np.array([[6.0, 0, 0], [0.8, 5.7, 0], [-0.4, 0.6, 6.2]])
+        width = 2.0
+    model = XD.DFTD3(tables, damping=damping, switch_width_pair=width,
+                     **{k: v for k, v in prm.items() if k in ("s6", "s8", "a1", "a2", "rs6", "rs8", "alp", "bet")},
+                     **FAST).to(DEV)
+    out, p, c = _eval(model, pos, z, cell, grad=True)
+    gp, *gc = torch.autograd.grad(out["energy"].sum(), [p] + ([c] if c is not None else []))
+    # oracle
+    s = D3.species_of(tables, z)
+    dst, src, sh = pair_images(pos, cell, max(FAST.values()))
+    pt = torch.tensor(pos, dtype=torch.float64, requires_grad=True)
+    ct = None if cell is None else torch.tensor(cell, dtype=torch.float64, requires_grad=True)
+    r = torch.linalg.norm(edge_vectors_au(pt, ct, dst, src, sh), dim=-1)
+    cn = D3.coordination_numbers(s, dst, src, r, tables, FAST["cutoff_cn"] / BOHR, len(z))
+    w = D3.weights(s, cn, tables)
+    c6 = D3.pair_c6(s, w, torch.as_tensor(dst), torch.as_tensor(src), tables)
+    e2 = D3.two_body(s, dst, src, r, c6, tables, prm, damping, FAST["cutoff_pair"] / BOHR,
+                     width / BOHR, len(z))
+    grads = torch.autograd.grad(e2.sum(), [pt] + ([ct] if ct is not None else []))
+    np.testing.assert_allclose(out["coordination_numbers"].detach().cpu(), cn.detach(),
+                               rtol=1e-12, atol=1e-13)
+    e_gpu = out["node_energy"].detach().cpu() / XD.HARTREE
+    np.testing.assert_allclose(e_gpu, e2.detach(), atol=1e-11 * float(e2.abs().max()))
+    np.testing.assert_allclose(gp.cpu() / XD.HARTREE, grads[0],
+                               atol=1e-10 * float(grads[0].abs().max()))
+    if cell is not None:
+        np.testing.assert_allclose(gc[0][0].cpu() / XD.HARTREE, grads[1],
+                                   atol=1e-10 * float(grads[1].abs().max()))
+
+
+def test_forces_match_finite_differences(tables):
+    """test_d3.py:237-256: central differences, h = 1e-4 A, 1e-7 eV/A."""
+    import xnn_amd.dispersion as XD
+    _note("d3 finite differences")
+    pos, z = _cluster(8, seed=23)
+    model = XD.DFTD3(tables, **FAST).to(DEV)
+    out, p, _ = _eval(model, pos, z, grad=True)
+    (gp,) = torch.autograd.grad(out["energy"].sum(), [p])
+    h = 1e-4
+    for i, a in [(0, 0), (3, 2), (5, 1)]:
+        pp, pm = pos.copy(), pos.copy()
+        pp[i, a] += h
+        pm[i, a] -= h
+        fd = (float(_eval(model, pp, z)[0]["energy"][0]) - float(_eval(model, pm, z)[0]["energy"][0])) / (2 * h)
+        assert abs(float(gp[i, a]) - fd) < 1e-7

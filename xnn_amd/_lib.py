@@ -58,6 +58,12 @@ class D4PairParams(ctypes.Structure):
                 ("width", dbl)]
 
 
+class D3PairParams(ctypes.Structure):
+    """``xnn_d3_pair_params``."""
+    _fields_ = [("s6", dbl), ("s8", dbl), ("a1", dbl), ("a2", dbl), ("rs6", dbl), ("rs8", dbl),
+                ("alp", dbl), ("bet", dbl), ("cutoff", dbl), ("width", dbl), ("damping", i32)]
+
+
 # name -> argtypes (restype int unless listed in _RESTYPES)
 _SIGNATURES = {
     "xnn_last_error": [],
@@ -85,6 +91,13 @@ _SIGNATURES = {
                         ctypes.POINTER(D4PairParams), vp, vp, sz, vp],
     "xnn_d4_two_body_backward": [vp, i64, vp, vp, vp, i64, i64, vp, vp, vp, vp,
                                  ctypes.POINTER(D4PairParams), vp, vp, vp, vp, vp, sz, vp],
+    "xnn_d3_coordination": [vp, i64, vp, vp, vp, i64, i64, vp, vp, vp, dbl, dbl, vp, vp, sz, vp],
+    "xnn_d3_coordination_backward": [vp, i64, vp, vp, vp, i64, i64, vp, vp, vp, dbl, dbl, vp, vp,
+                                     vp, vp, sz, vp],
+    "xnn_d3_two_body": [vp, i64, vp, vp, vp, i64, i64, vp, vp, vp, vp, vp, i32, vp,
+                        ctypes.POINTER(D3PairParams), vp, vp, sz, vp],
+    "xnn_d3_two_body_backward": [vp, i64, vp, vp, vp, i64, i64, vp, vp, vp, vp, vp, i32, vp,
+                                 ctypes.POINTER(D3PairParams), vp, vp, vp, vp, vp, sz, vp],
     "xnn_segment_sum": [c_int, vp, i64, i64, vp, vp, i64, vp, vp],
     "xnn_gather_rows": [c_int, vp, i64, i64, vp, i64, vp, vp],
     "xnn_segment_reduce_workspace_bytes": [i64, i64, i64],

@@ -1,4 +1,4 @@
-// D4 dispersion pair terms on lattice images (gfx950, wave64, float64).
+// D4 and D3 dispersion pair terms on lattice images (gfx950, wave64, float64).
 //
 // xnn_d4_coordination(_backward)  DFTD4.coordination_numbers (d4.py:552-591): the
 //                                 EN-weighted erf-count CN and the plain erf count
@@ -10,6 +10,11 @@
 //                                 gives grad_pos, the cell gradient and dE/d alpha, the
 //                                 quantities of the reference's native kernel run_d4
 //                                 (dispersion_fast/cpu.py:834-935)
+// xnn_d3_coordination(_backward)  DFTD3.coordination_numbers (d3.py:632-642), the
+//                                 exponential count
+// xnn_d3_two_body(_backward)      DFTD3.pair_c6 / two_body_energy (d3.py:651-722): C6
+//                                 from per-atom reference weights and the species-pair
+//                                 reference block, bj / zero / mzero / op damping
 //
 // No edge list: the long pair cutoff (60 bohr by default) makes the image list dense,
 // so the kernels walk all (receiver, source, image) triples of each structure. Work
@@ -169,7 +174,7 @@ struct CnParams {
 
 // BACKWARD = false: partial[cy][0/1][i] = (cn_d4, cn_raw) sums of this chunk.
 // BACKWARD = true:  partial[cy][0..11][i] = grad_pos (3), cell gradient n (x) g (9).
-template <bool BACKWARD>
+template <bool BACKWARD, bool D3 = false>
 __global__ __launch_bounds__(64) void d4_cn_kernel(
     const double* __restrict__ pos, int64_t n_nodes, const int32_t* __restrict__ species,
     const int32_t* __restrict__ batch, const int64_t* __restrict__ node_ptr,
@@ -232,8 +237,11 @@ __global__ __launch_bounds__(64) void d4_cn_kernel(
       if (st.b[jj] != bi) continue;
       const int sj = st.sp[jj];
       const double rc = rci + rcov[sj];
-      const double den = fabs(eni - en[sj]) + prm.k5;
-      const double enf = prm.k4 * exp(-den * den / prm.k6);
+      double enf = 1.0;
+      if (!D3) {
+        const double den = fabs(eni - en[sj]) + prm.k5;
+        enf = prm.k4 * exp(-den * den / prm.k6);
+      }
       const double dx = xi - st.x[jj], dy = yi - st.y[jj], dz = zi - st.z[jj];
       const double wsum = BACKWARD ? gi + st.w[jj] : 0.0;
       const double w2sum = BACKWARD ? g2i + st.w2[jj] : 0.0;
@@ -248,15 +256,23 @@ __global__ __launch_bounds__(64) void d4_cn_kernel(
             const double r2 = vx * vx + vy * vy + vz * vz;
             if (r2 <= 0.0 || r2 > cmax * cmax) continue;
             const double r = sqrt(r2);
-            const bool in_cn = r <= prm.cut_cn, in_eeq = r <= prm.cut_eeq;
-            const double x = -prm.kcn * (r - rc) / rc;
+            const bool in_cn = r <= prm.cut_cn, in_eeq = !D3 && r <= prm.cut_eeq;
+            double count, dcount;
+            if (D3) {
+              // 1 / (1 + exp(-k1 (rc / r - 1))) (d3.py:632-642); d/dr = -s (1 - s) k1 rc / r^2
+              const double sg = 1.0 / (1.0 + exp(-prm.kcn * (rc / r - 1.0)));
+              count = sg;
+              dcount = -sg * (1.0 - sg) * prm.kcn * rc / r2;
+            } else {
+              // (1 + erf(-k0 (r - rc) / rc)) / 2; d/dr = -k0 exp(-x^2) / (rc sqrt(pi))
+              const double x = -prm.kcn * (r - rc) / rc;
+              count = 0.5 * (1.0 + erf(x));
+              dcount = -prm.kcn * exp(-x * x) / (rc * kSqrtPi);
+            }
             if (!BACKWARD) {
-              const double count = 0.5 * (1.0 + erf(x));
               if (in_cn) acc[0] += enf * count;
               if (in_eeq) acc[1] += count;
             } else {
-              // d count / d r = -k0 exp(-x^2) / (rc sqrt(pi))
-              const double dcount = -prm.kcn * exp(-x * x) / (rc * kSqrtPi);
               const double both = (in_cn ? wsum * enf : 0.0) + (in_eeq ? w2sum : 0.0);
               const double own = (in_cn ? gi * enf : 0.0) + (in_eeq ? g2i : 0.0);
               // per Angstrom of the edge vector: d r_bohr / d v = v_bohr / (r bohr)
@@ -409,6 +425,191 @@ __global__ __launch_bounds__(64) void d4_pair_kernel(
     if (BACKWARD) {
 #pragma unroll
       for (int w = 0; w < kNW; ++w) partial_alpha[((int64_t)cy * kNW + w) * n_nodes + i] = da[w];
+    }
+  }
+}
+
+// ---------------------------------------------------------------- D3 two-body term
+constexpr int kNR = 7;  // D3 reference systems per element
+
+struct D3PairParams {
+  double s6, s8, a1, a2, rs6, rs8, alp, bet, cutoff, width;
+  int damping;  // 0 bj, 1 zero, 2 mzero, 3 op
+};
+
+// t6, t8 of the damping variants (d3.py:698-720) and their r-derivatives
+__device__ inline void d3_damp(const D3PairParams& p, double r, double r0, double& t6, double& t8,
+                               double& d6, double& d8) {
+  const double r2 = r * r, r6 = r2 * r2 * r2, r8 = r6 * r2;
+  if (p.damping == 0) {                       // rational (Becke-Johnson)
+    const double q2 = r0 * r0, q6 = q2 * q2 * q2, q8 = q6 * q2;
+    t6 = 1.0 / (r6 + q6);
+    t8 = 1.0 / (r8 + q8);
+    d6 = -6.0 * r * r2 * r2 * t6 * t6;
+    d8 = -8.0 * r * r6 * t8 * t8;
+  } else if (p.damping == 1 || p.damping == 2) {  // zero / modified zero
+    double a6, a8, da6, da8;
+    if (p.damping == 1) {
+      a6 = pow(p.rs6 * r0 / r, p.alp);
+      a8 = pow(p.rs8 * r0 / r, p.alp + 2.0);
+      da6 = -p.alp * a6 / r;
+      da8 = -(p.alp + 2.0) * a8 / r;
+    } else {
+      const double x6 = r / (p.rs6 * r0) + p.bet * r0, x8 = r / (p.rs8 * r0) + p.bet * r0;
+      a6 = pow(x6, -p.alp);
+      a8 = pow(x8, -(p.alp + 2.0));
+      da6 = -p.alp * a6 / x6 / (p.rs6 * r0);
+      da8 = -(p.alp + 2.0) * a8 / x8 / (p.rs8 * r0);
+    }
+    t6 = 1.0 / ((1.0 + 6.0 * a6) * r6);
+    t8 = 1.0 / ((1.0 + 6.0 * a8) * r8);
+    d6 = -t6 * (6.0 * da6 / (1.0 + 6.0 * a6) + 6.0 / r);
+    d8 = -t8 * (6.0 * da8 / (1.0 + 6.0 * a8) + 8.0 / r);
+  } else {                                    // optimized power
+    const double rb = pow(r, p.bet), ab = pow(r0, p.bet);
+    const double q2 = r0 * r0, q6 = q2 * q2 * q2, q8 = q6 * q2;
+    const double den6 = rb * r6 + ab * q6, den8 = rb * r8 + ab * q8;
+    t6 = rb / den6;
+    t8 = rb / den8;
+    // t = 1 / (r^n + c r^-bet), c = ab q^n: dt/dr = -t^2 (n r^(n-1) - bet c r^(-bet-1))
+    const double c6 = ab * q6 / rb, c8 = ab * q8 / rb;
+    d6 = -t6 * t6 * (6.0 * r * r2 * r2 - p.bet * c6 / r);
+    d8 = -t8 * t8 * (8.0 * r * r6 - p.bet * c8 / r);
+  }
+}
+
+// BACKWARD = false: partial[cy][0][i] = sum of -1/2 C6 f(r) over this chunk.
+// BACKWARD = true:  partial[cy][0..11][i] = grad_pos (3), cell gradient (9), and
+//                   partial_w[cy][a][i] = dE / dW_i[a] (7).
+// C6_ij = sum_ab W_i[a] W_j[b] C6ref[s_i][s_j][a][b] (d3.py:651-674).
+template <bool BACKWARD>
+__global__ __launch_bounds__(64) void d3_pair_kernel(
+    const double* __restrict__ pos, int64_t n_nodes, const int32_t* __restrict__ species,
+    const int32_t* __restrict__ batch, const int64_t* __restrict__ node_ptr,
+    const double* __restrict__ cell, const int32_t* __restrict__ images,
+    const double* __restrict__ r4r2, const double* __restrict__ rvdw,
+    const double* __restrict__ c6ref, int n_species, const double* __restrict__ wref,
+    D3PairParams prm, const double* __restrict__ g_e2, int64_t chunk, int64_t n_cy,
+    double* __restrict__ partial, double* __restrict__ partial_w) {
+  __shared__ D4Stage st;
+  __shared__ double sw_[kNR][kD4Sub];
+  const int lane = threadIdx.x;
+  const int64_t t = blockIdx.x, cy = blockIdx.y;
+  const int64_t i = t * kD4Tile + lane;
+  const bool live = i < n_nodes;
+  const int64_t i_first = t * kD4Tile, i_last = std::min<int64_t>(i_first + kD4Tile, n_nodes) - 1;
+  const int64_t s_lo = node_ptr[batch[i_first]], s_hi = node_ptr[batch[i_last] + 1];
+  const int64_t c = s_lo / chunk + cy;
+  const int64_t j0 = std::max<int64_t>(c * chunk, s_lo), j1 = std::min<int64_t>((c + 1) * chunk, s_hi);
+  constexpr int NP = BACKWARD ? 12 : 1;
+  double acc[NP];
+#pragma unroll
+  for (int k = 0; k < NP; ++k) acc[k] = 0.0;
+  double wi[kNR], dw[kNR];
+#pragma unroll
+  for (int a = 0; a < kNR; ++a) {
+    wi[a] = 0.0;
+    dw[a] = 0.0;
+  }
+  double xi = 0, yi = 0, zi = 0, qi = 0, gi = 0;
+  int bi = -1, si = 0;
+  Lattice L;
+  if (live) {
+    xi = pos[3 * i];
+    yi = pos[3 * i + 1];
+    zi = pos[3 * i + 2];
+    si = species[i];
+    qi = r4r2[si];
+    bi = batch[i];
+    if (BACKWARD) gi = g_e2[i];
+#pragma unroll
+    for (int a = 0; a < kNR; ++a) wi[a] = wref[(int64_t)kNR * i + a];
+    load_lattice(cell, images, bi, L);
+  } else {
+    load_lattice(nullptr, nullptr, 0, L);
+  }
+  const double rc2 = prm.cutoff * prm.cutoff;
+  for (int64_t base = j0; base < j1; base += kD4Sub) {
+    const int cnt = (int)std::min<int64_t>(kD4Sub, j1 - base);
+    __syncthreads();
+    if (lane < cnt) {
+      const int64_t j = base + lane;
+      st.x[lane] = pos[3 * j];
+      st.y[lane] = pos[3 * j + 1];
+      st.z[lane] = pos[3 * j + 2];
+      st.sp[lane] = species[j];
+      st.b[lane] = batch[j];
+      if (BACKWARD) st.w[lane] = g_e2[j];
+#pragma unroll
+      for (int a = 0; a < kNR; ++a) sw_[a][lane] = wref[(int64_t)kNR * j + a];
+    }
+    __syncthreads();
+    if (!live) continue;
+    for (int jj = 0; jj < cnt; ++jj) {
+      if (st.b[jj] != bi) continue;
+      const int sj = st.sp[jj];
+      const double* blk = c6ref + ((int64_t)si * n_species + sj) * (kNR * kNR);
+      double v[kNR];  // v[a] = sum_b C6ref[a][b] W_j[b]
+#pragma unroll
+      for (int a = 0; a < kNR; ++a) {
+        double sa = 0.0;
+#pragma unroll
+        for (int b = 0; b < kNR; ++b) sa += blk[a * kNR + b] * sw_[b][jj];
+        v[a] = sa;
+      }
+      double c6 = 0.0;
+#pragma unroll
+      for (int a = 0; a < kNR; ++a) c6 += wi[a] * v[a];
+      const double rr = 3.0 * qi * r4r2[sj];
+      const double r0 = (prm.damping == 0 || prm.damping == 3) ? prm.a1 * sqrt(rr) + prm.a2
+                                                               : rvdw[si * n_species + sj];
+      const double dx = xi - st.x[jj], dy = yi - st.y[jj], dz = zi - st.z[jj];
+      const double wsum = BACKWARD ? gi + st.w[jj] : 0.0;
+      double fsum = 0.0;
+      int lo[3], hi[3];
+      image_window(L, dx, dy, dz, prm.cutoff * kBohr, lo, hi);
+      for (int n0 = lo[0]; n0 <= hi[0]; ++n0)
+        for (int n1 = lo[1]; n1 <= hi[1]; ++n1)
+          for (int n2 = lo[2]; n2 <= hi[2]; ++n2) {
+            const double vx = (dx + (n0 * L.a[0] + n1 * L.a[3] + n2 * L.a[6])) / kBohr;
+            const double vy = (dy + (n0 * L.a[1] + n1 * L.a[4] + n2 * L.a[7])) / kBohr;
+            const double vz = (dz + (n0 * L.a[2] + n1 * L.a[5] + n2 * L.a[8])) / kBohr;
+            const double r2 = vx * vx + vy * vy + vz * vz;
+            if (r2 <= 0.0 || r2 > rc2) continue;
+            const double r = sqrt(r2);
+            double sw, dsw, t6, t8, d6, d8;
+            switch_d(r, prm.cutoff, prm.width, sw, dsw);
+            d3_damp(prm, r, r0, t6, t8, d6, d8);
+            const double g = prm.s6 * t6 + prm.s8 * rr * t8;
+            const double f = sw * g;
+            if (!BACKWARD) {
+              acc[0] += -0.5 * c6 * f;
+            } else {
+              fsum += f;
+              const double df = dsw * g + sw * (prm.s6 * d6 + prm.s8 * rr * d8);
+              const double s = -0.5 * c6 * df / (r * kBohr);
+              acc[0] += wsum * s * vx;
+              acc[1] += wsum * s * vy;
+              acc[2] += wsum * s * vz;
+              const double ox = gi * s * vx, oy = gi * s * vy, oz = gi * s * vz;
+              acc[3] += n0 * ox; acc[4] += n0 * oy; acc[5] += n0 * oz;
+              acc[6] += n1 * ox; acc[7] += n1 * oy; acc[8] += n1 * oz;
+              acc[9] += n2 * ox; acc[10] += n2 * oy; acc[11] += n2 * oz;
+            }
+          }
+      if (BACKWARD && fsum != 0.0) {
+        const double k = -0.5 * wsum * fsum;
+#pragma unroll
+        for (int a = 0; a < kNR; ++a) dw[a] += k * v[a];
+      }
+    }
+  }
+  if (live) {
+#pragma unroll
+    for (int k = 0; k < NP; ++k) partial[((int64_t)cy * NP + k) * n_nodes + i] = acc[k];
+    if (BACKWARD) {
+#pragma unroll
+      for (int a = 0; a < kNR; ++a) partial_w[((int64_t)cy * kNR + a) * n_nodes + i] = dw[a];
     }
   }
 }
@@ -592,6 +793,135 @@ int xnn_d4_two_body_backward(const double* pos, int64_t n_nodes, const int32_t* 
   reduce_into(part, n_nodes, 12, 0, 3, w.n_cy, grad_pos, s);
   reduce_into(part, n_nodes, 12, 3, 9, w.n_cy, cell_partial, s);
   reduce_into(part_a, n_nodes, kNW, 0, kNW, w.n_cy, grad_alpha, s);
+  XNN_LAUNCH_CHECK();
+  return XNN_OK;
+}
+
+int xnn_d3_coordination(const double* pos, int64_t n_nodes, const int32_t* species,
+                        const int32_t* batch, const int64_t* node_ptr, int64_t n_graphs,
+                        int64_t max_atoms, const double* cell, const int32_t* images,
+                        const double* rcov, double cutoff_cn, double kcn, double* cn,
+                        void* workspace, size_t workspace_bytes, xnn_stream_t stream) {
+  const int st = d4_check(pos, n_nodes, species, batch, node_ptr, n_graphs, cell, images, max_atoms);
+  if (st != XNN_OK) return st;
+  XNN_REQUIRE(rcov != nullptr, "NULL rcov");
+  XNN_REQUIRE(n_nodes == 0 || cn, "NULL output");
+  if (n_nodes == 0) return XNN_OK;
+  const D4Work w = d4_work(n_nodes, n_graphs, max_atoms);
+  const size_t need = (size_t)(w.n_cy * 2 * n_nodes) * sizeof(double);
+  XNN_REQUIRE(workspace != nullptr && workspace_bytes >= need, "workspace too small (%zu < %zu)",
+              workspace_bytes, need);
+  const CnParams p{cutoff_cn, 0.0, kcn, 0.0, 0.0, 1.0};
+  hipStream_t s = as_hip(stream);
+  double* part = static_cast<double*>(workspace);
+  hipLaunchKernelGGL((d4_cn_kernel<false, true>), dim3((unsigned)w.n_tiles, (unsigned)w.n_cy),
+                     dim3(kD4Tile), 0, s, pos, n_nodes, species, batch, node_ptr, cell, images,
+                     rcov, rcov, p, nullptr, nullptr, w.chunk, w.n_cy, part);
+  XNN_LAUNCH_CHECK();
+  reduce_into(part, n_nodes, 2, 0, 1, w.n_cy, cn, s);
+  XNN_LAUNCH_CHECK();
+  return XNN_OK;
+}
+
+int xnn_d3_coordination_backward(const double* pos, int64_t n_nodes, const int32_t* species,
+                                 const int32_t* batch, const int64_t* node_ptr, int64_t n_graphs,
+                                 int64_t max_atoms, const double* cell, const int32_t* images,
+                                 const double* rcov, double cutoff_cn, double kcn,
+                                 const double* g_cn, double* grad_pos, double* cell_partial,
+                                 void* workspace, size_t workspace_bytes, xnn_stream_t stream) {
+  const int st = d4_check(pos, n_nodes, species, batch, node_ptr, n_graphs, cell, images, max_atoms);
+  if (st != XNN_OK) return st;
+  XNN_REQUIRE(rcov != nullptr, "NULL rcov");
+  XNN_REQUIRE(n_nodes == 0 || (grad_pos && g_cn), "NULL g_cn or grad_pos");
+  if (n_nodes == 0) return XNN_OK;
+  const D4Work w = d4_work(n_nodes, n_graphs, max_atoms);
+  const size_t need = (size_t)(w.n_cy * 12 * n_nodes) * sizeof(double);
+  XNN_REQUIRE(workspace != nullptr && workspace_bytes >= need, "workspace too small (%zu < %zu)",
+              workspace_bytes, need);
+  const CnParams p{cutoff_cn, 0.0, kcn, 0.0, 0.0, 1.0};
+  hipStream_t s = as_hip(stream);
+  double* part = static_cast<double*>(workspace);
+  hipLaunchKernelGGL((d4_cn_kernel<true, true>), dim3((unsigned)w.n_tiles, (unsigned)w.n_cy),
+                     dim3(kD4Tile), 0, s, pos, n_nodes, species, batch, node_ptr, cell, images,
+                     rcov, rcov, p, g_cn, nullptr, w.chunk, w.n_cy, part);
+  XNN_LAUNCH_CHECK();
+  reduce_into(part, n_nodes, 12, 0, 3, w.n_cy, grad_pos, s);
+  reduce_into(part, n_nodes, 12, 3, 9, w.n_cy, cell_partial, s);
+  XNN_LAUNCH_CHECK();
+  return XNN_OK;
+}
+
+static int d3_pair_check(const xnn_d3_pair_params* prm, const double* r4r2, const double* rvdw,
+                         const double* c6ref, int n_species) {
+  XNN_REQUIRE(prm && r4r2 && rvdw && c6ref, "NULL tables or params");
+  XNN_REQUIRE(n_species >= 1, "n_species must be >= 1");
+  XNN_REQUIRE(prm->damping >= 0 && prm->damping <= 3, "damping must be 0..3 (bj, zero, mzero, op)");
+  XNN_REQUIRE(prm->cutoff > 0.0, "pair cutoff must be positive");
+  return XNN_OK;
+}
+
+static D3PairParams d3_params(const xnn_d3_pair_params* p) {
+  return D3PairParams{p->s6, p->s8, p->a1, p->a2, p->rs6, p->rs8, p->alp, p->bet, p->cutoff,
+                      p->width, p->damping};
+}
+
+int xnn_d3_two_body(const double* pos, int64_t n_nodes, const int32_t* species,
+                    const int32_t* batch, const int64_t* node_ptr, int64_t n_graphs,
+                    int64_t max_atoms, const double* cell, const int32_t* images,
+                    const double* r4r2, const double* rvdw, const double* c6ref,
+                    int32_t n_species, const double* weights, const xnn_d3_pair_params* prm,
+                    double* e2, void* workspace, size_t workspace_bytes, xnn_stream_t stream) {
+  const int st = d4_check(pos, n_nodes, species, batch, node_ptr, n_graphs, cell, images, max_atoms);
+  if (st != XNN_OK) return st;
+  const int st2 = d3_pair_check(prm, r4r2, rvdw, c6ref, n_species);
+  if (st2 != XNN_OK) return st2;
+  XNN_REQUIRE(n_nodes == 0 || (weights && e2), "NULL weights or output");
+  if (n_nodes == 0) return XNN_OK;
+  const D4Work w = d4_work(n_nodes, n_graphs, max_atoms);
+  const size_t need = (size_t)(w.n_cy * n_nodes) * sizeof(double);
+  XNN_REQUIRE(workspace != nullptr && workspace_bytes >= need, "workspace too small (%zu < %zu)",
+              workspace_bytes, need);
+  hipStream_t s = as_hip(stream);
+  double* part = static_cast<double*>(workspace);
+  hipLaunchKernelGGL(d3_pair_kernel<false>, dim3((unsigned)w.n_tiles, (unsigned)w.n_cy),
+                     dim3(kD4Tile), 0, s, pos, n_nodes, species, batch, node_ptr, cell, images,
+                     r4r2, rvdw, c6ref, n_species, weights, d3_params(prm), nullptr, w.chunk,
+                     w.n_cy, part, nullptr);
+  XNN_LAUNCH_CHECK();
+  reduce_into(part, n_nodes, 1, 0, 1, w.n_cy, e2, s);
+  XNN_LAUNCH_CHECK();
+  return XNN_OK;
+}
+
+int xnn_d3_two_body_backward(const double* pos, int64_t n_nodes, const int32_t* species,
+                             const int32_t* batch, const int64_t* node_ptr, int64_t n_graphs,
+                             int64_t max_atoms, const double* cell, const int32_t* images,
+                             const double* r4r2, const double* rvdw, const double* c6ref,
+                             int32_t n_species, const double* weights,
+                             const xnn_d3_pair_params* prm, const double* g_e2, double* grad_pos,
+                             double* cell_partial, double* grad_weights, void* workspace,
+                             size_t workspace_bytes, xnn_stream_t stream) {
+  const int st = d4_check(pos, n_nodes, species, batch, node_ptr, n_graphs, cell, images, max_atoms);
+  if (st != XNN_OK) return st;
+  const int st2 = d3_pair_check(prm, r4r2, rvdw, c6ref, n_species);
+  if (st2 != XNN_OK) return st2;
+  XNN_REQUIRE(n_nodes == 0 || (weights && g_e2 && grad_pos), "NULL weights, g_e2 or grad_pos");
+  if (n_nodes == 0) return XNN_OK;
+  const D4Work w = d4_work(n_nodes, n_graphs, max_atoms);
+  const size_t need = (size_t)(w.n_cy * (12 + kNR) * n_nodes) * sizeof(double);
+  XNN_REQUIRE(workspace != nullptr && workspace_bytes >= need, "workspace too small (%zu < %zu)",
+              workspace_bytes, need);
+  hipStream_t s = as_hip(stream);
+  double* part = static_cast<double*>(workspace);
+  double* part_w = part + w.n_cy * 12 * n_nodes;
+  hipLaunchKernelGGL(d3_pair_kernel<true>, dim3((unsigned)w.n_tiles, (unsigned)w.n_cy),
+                     dim3(kD4Tile), 0, s, pos, n_nodes, species, batch, node_ptr, cell, images,
+                     r4r2, rvdw, c6ref, n_species, weights, d3_params(prm), g_e2, w.chunk,
+                     w.n_cy, part, part_w);
+  XNN_LAUNCH_CHECK();
+  reduce_into(part, n_nodes, 12, 0, 3, w.n_cy, grad_pos, s);
+  reduce_into(part, n_nodes, 12, 3, 9, w.n_cy, cell_partial, s);
+  reduce_into(part_w, n_nodes, kNR, 0, kNR, w.n_cy, grad_weights, s);
   XNN_LAUNCH_CHECK();
   return XNN_OK;
 }

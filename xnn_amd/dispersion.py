@@ -491,3 +491,239 @@ class D4Dispersion(DispersionCorrection):
     @property
     def d4(self) -> DFTD4:
         return self.term
+
+
+# --------------------------------------------------------------------------- D3
+D3_DAMPINGS = {"bj": 0, "zero": 1, "mzero": 2, "op": 3}
+D3_KCN, D3_WF = 16.0, 4.0                                           # d3.py:464-465
+PBE0_D3BJ = {"s6": 1.0, "s8": 1.2177, "a1": 0.4145, "a2": 4.8593}   # d3.py:477-478
+PBE0_D3ZERO = {"s6": 1.0, "s8": 0.928, "rs6": 1.287, "rs8": 1.0}
+D3_TABLE_KEYS = ("z", "rcov", "r4r2", "rvdw", "nref", "refcn", "c6ref")
+
+
+def load_d3_tables(path: str) -> Dict[str, np.ndarray]:
+    """Compact per-element D3 tables: ``z`` (S,) element list, ``rcov`` (4/3-scaled,
+    bohr), ``r4r2``, ``rvdw`` (S, S, bohr), ``nref`` (S,), ``refcn`` (7, S) and ``c6ref``
+    (7, 7, S, S) [ref_i, ref_j, species_i, species_j] (d3.py:194-219, 617-628)."""
+    with np.load(path, allow_pickle=False) as f:
+        missing = [k for k in D3_TABLE_KEYS if k not in f.files]
+        if missing:
+            raise ValueError(f"{path}: missing D3 tables {missing}")
+        return {k: np.asarray(f[k]) for k in D3_TABLE_KEYS}
+
+
+@torch.library.custom_op(f"{_NS}::d3_coordination", mutates_args=())
+def d3_coordination_op(pos: Tensor, cell: Optional[Tensor], species: Tensor, batch32: Tensor,
+                       node_ptr: Tensor, images: Tensor, rcov: Tensor, cutoff_cn: float,
+                       max_atoms: int) -> Tensor:
+    """Exponential-count D3 coordination numbers within ``cutoff_cn`` bohr (d3.py:632-642)."""
+    dev = pos.device
+    n, b = pos.shape[0], node_ptr.shape[0] - 1
+    cn = torch.empty(n, dtype=torch.float64, device=dev)
+    ws, need = _workspace(n, b, max_atoms, dev)
+    _lib.call("xnn_d3_coordination", _lib.ptr(pos), n, _lib.ptr(species), _lib.ptr(batch32),
+              _lib.ptr(node_ptr), b, max_atoms, _lib.ptr(cell), _lib.ptr(images), _lib.ptr(rcov),
+              cutoff_cn, D3_KCN, _lib.ptr(cn), _lib.ptr(ws), need, _lib.stream(dev))
+    return cn
+
+
+@d3_coordination_op.register_fake
+def _(pos, cell, species, batch32, node_ptr, images, rcov, cutoff_cn, max_atoms):
+    return pos.new_empty(pos.shape[0])
+
+
+def _d3cn_setup(ctx, inputs, output):
+    pos, cell, species, batch32, node_ptr, images, rcov, cutoff_cn, max_atoms = inputs
+    ctx.save_for_backward(pos, cell, species, batch32, node_ptr, images, rcov)
+    ctx.cutoff_cn, ctx.max_atoms = cutoff_cn, max_atoms
+
+
+def _d3cn_backward(ctx, g_cn):
+    if torch.is_grad_enabled():
+        raise RuntimeError("the D3 kernels are differentiable once")
+    pos, cell, species, batch32, node_ptr, images, rcov = ctx.saved_tensors
+    dev, n, b = pos.device, pos.shape[0], node_ptr.shape[0] - 1
+    grad_pos = torch.empty((n, 3), dtype=torch.float64, device=dev)
+    want_cell = cell is not None and ctx.needs_input_grad[1]
+    part = torch.empty((n, 9), dtype=torch.float64, device=dev) if want_cell else None
+    ws, need = _workspace(n, b, ctx.max_atoms, dev)
+    _lib.call("xnn_d3_coordination_backward", _lib.ptr(pos), n, _lib.ptr(species),
+              _lib.ptr(batch32), _lib.ptr(node_ptr), b, ctx.max_atoms, _lib.ptr(cell),
+              _lib.ptr(images), _lib.ptr(rcov), ctx.cutoff_cn, D3_KCN,
+              _lib.ptr(g_cn.contiguous()), _lib.ptr(grad_pos), _lib.ptr(part), _lib.ptr(ws), need,
+              _lib.stream(dev))
+    grad_cell = _cell_grad(part, node_ptr, b) if want_cell else None
+    return grad_pos, grad_cell, None, None, None, None, None, None, None
+
+
+d3_coordination_op.register_autograd(_d3cn_backward, setup_context=_d3cn_setup)
+
+
+def _d3_params(p: List[float]) -> "_lib.D3PairParams":
+    return _lib.D3PairParams(*p[:10], int(p[10]))
+
+
+@torch.library.custom_op(f"{_NS}::d3_two_body", mutates_args=())
+def d3_two_body_op(pos: Tensor, cell: Optional[Tensor], weights: Tensor, species: Tensor,
+                   batch32: Tensor, node_ptr: Tensor, images: Tensor, r4r2: Tensor, rvdw: Tensor,
+                   c6ref: Tensor, params: List[float], max_atoms: int) -> Tensor:
+    """Per-atom D3 two-body energy (hartree); ``params = [s6, s8, a1, a2, rs6, rs8, alp,
+    bet, cutoff, width, damping]`` (bohr), ``c6ref`` (S, S, 7, 7) (d3.py:651-722)."""
+    dev = pos.device
+    n, b = pos.shape[0], node_ptr.shape[0] - 1
+    e2 = torch.empty(n, dtype=torch.float64, device=dev)
+    ws, need = _workspace(n, b, max_atoms, dev)
+    _lib.call("xnn_d3_two_body", _lib.ptr(pos), n, _lib.ptr(species), _lib.ptr(batch32),
+              _lib.ptr(node_ptr), b, max_atoms, _lib.ptr(cell), _lib.ptr(images), _lib.ptr(r4r2),
+              _lib.ptr(rvdw), _lib.ptr(c6ref), r4r2.shape[0], _lib.ptr(weights),
+              _d3_params(params), _lib.ptr(e2), _lib.ptr(ws), need, _lib.stream(dev))
+    return e2
+
+
+@d3_two_body_op.register_fake
+def _(pos, cell, weights, species, batch32, node_ptr, images, r4r2, rvdw, c6ref, params, max_atoms):
+    return pos.new_empty(pos.shape[0])
+
+
+def _d3pair_setup(ctx, inputs, output):
+    (pos, cell, weights, species, batch32, node_ptr, images, r4r2, rvdw, c6ref, params,
+     max_atoms) = inputs
+    ctx.save_for_backward(pos, cell, weights, species, batch32, node_ptr, images, r4r2, rvdw, c6ref)
+    ctx.params, ctx.max_atoms = list(params), max_atoms
+
+
+def _d3pair_backward(ctx, g_e2):
+    if torch.is_grad_enabled():
+        raise RuntimeError("the D3 kernels are differentiable once")
+    pos, cell, weights, species, batch32, node_ptr, images, r4r2, rvdw, c6ref = ctx.saved_tensors
+    dev, n, b = pos.device, pos.shape[0], node_ptr.shape[0] - 1
+    grad_pos = torch.empty((n, 3), dtype=torch.float64, device=dev)
+    want_cell = cell is not None and ctx.needs_input_grad[1]
+    part = torch.empty((n, 9), dtype=torch.float64, device=dev) if want_cell else None
+    grad_w = torch.empty_like(weights) if ctx.needs_input_grad[2] else None
+    ws, need = _workspace(n, b, ctx.max_atoms, dev)
+    _lib.call("xnn_d3_two_body_backward", _lib.ptr(pos), n, _lib.ptr(species), _lib.ptr(batch32),
+              _lib.ptr(node_ptr), b, ctx.max_atoms, _lib.ptr(cell), _lib.ptr(images),
+              _lib.ptr(r4r2), _lib.ptr(rvdw), _lib.ptr(c6ref), r4r2.shape[0], _lib.ptr(weights),
+              _d3_params(ctx.params), _lib.ptr(g_e2.contiguous()), _lib.ptr(grad_pos),
+              _lib.ptr(part), _lib.ptr(grad_w), _lib.ptr(ws), need, _lib.stream(dev))
+    grad_cell = _cell_grad(part, node_ptr, b) if want_cell else None
+    return grad_pos, grad_cell, grad_w, None, None, None, None, None, None, None, None, None
+
+
+d3_two_body_op.register_autograd(_d3pair_backward, setup_context=_d3pair_setup)
+
+
+def _batch_layout(n_atoms: Tensor, dev) -> Tuple[List[int], Tensor, Tensor]:
+    counts = [int(x) for x in n_atoms.cpu()]
+    node_ptr = torch.tensor(np.concatenate([[0], np.cumsum(counts)]), dtype=torch.int64, device=dev)
+    batch32 = torch.repeat_interleave(torch.arange(len(counts), dtype=torch.int32, device=dev),
+                                      torch.tensor(counts, device=dev))
+    return counts, node_ptr, batch32
+
+
+class DFTD3(nn.Module):
+    """Two-body D3 on the GPU (d3.py:483-960 without the ATM term): ``damping`` in
+    {"bj", "zero", "mzero", "op"}, PBE0 defaults, cutoffs in Angstrom (upstream 60 / 40
+    bohr for pairs / CN)."""
+
+    def __init__(self, tables: Dict[str, np.ndarray], damping: str = "bj", s6: float = 1.0,
+                 s8: Optional[float] = None, a1: float = 0.4145, a2: float = 4.8593,
+                 rs6: float = 1.287, rs8: float = 1.0, alp: float = 14.0, bet: float = 0.0,
+                 s9: float = 0.0, cutoff_pair: float = 60.0 * BOHR,
+                 cutoff_cn: float = 40.0 * BOHR, switch_width_pair: float = 0.0):
+        super().__init__()
+        damping = {"rational": "bj", "d3bj": "bj"}.get(damping.lower(), damping.lower())
+        if damping not in D3_DAMPINGS:
+            raise ValueError(f"damping must be one of {tuple(D3_DAMPINGS)}, got {damping!r}")
+        if s9 != 0.0:
+            raise NotImplementedError("the three-body ATM term is not part of this path; s9 = 0")
+        if s8 is None:
+            s8 = PBE0_D3BJ["s8"] if damping in ("bj", "op") else PBE0_D3ZERO["s8"]
+        self.damping = damping
+        self.s6, self.s8, self.a1, self.a2 = float(s6), float(s8), float(a1), float(a2)
+        self.rs6, self.rs8, self.alp, self.bet = float(rs6), float(rs8), float(alp), float(bet)
+        self.cutoff_pair, self.cutoff_cn = float(cutoff_pair), float(cutoff_cn)
+        self.switch_width_pair = float(switch_width_pair)
+        self.cutoff = max(self.cutoff_pair, self.cutoff_cn)
+        self.elements = [int(v) for v in tables["z"]]
+        for k in D3_TABLE_KEYS:
+            if k == "z":
+                continue
+            v = tables[k]
+            dt = torch.long if np.issubdtype(v.dtype, np.integer) else torch.float64
+            self.register_buffer(k, torch.as_tensor(v, dtype=dt), persistent=False)
+        # species-pair major layout of the reference block for the kernel
+        self.register_buffer("c6pair", torch.as_tensor(
+            np.ascontiguousarray(np.asarray(tables["c6ref"]).transpose(2, 3, 0, 1)),
+            dtype=torch.float64), persistent=False)
+
+    def species(self, z: Tensor) -> Tensor:
+        lut = torch.full((max(self.elements) + 1,), -1, dtype=torch.long)
+        lut[torch.tensor(self.elements)] = torch.arange(len(self.elements))
+        zc = z.detach().cpu().long()
+        if bool((zc > max(self.elements)).any()) or bool((lut[zc.clamp(max=max(self.elements))] < 0).any()):
+            raise ValueError(f"the D3 tables cover the elements {self.elements} only")
+        return lut[zc]
+
+    def weights(self, s: Tensor, cn: Tensor) -> Tensor:
+        """Gaussian reference weights exp(-4 (CN - CN_ref)^2), normalized, with the
+        largest-CN fallback (d3.py:644-649, dispersion.py:70-121)."""
+        refcn = self.refcn[:, s].t()
+        valid = torch.arange(refcn.shape[1], device=s.device)[None, :] < self.nref[s][:, None]
+        gw = torch.where(valid, torch.exp(-D3_WF * (cn[:, None] - refcn) ** 2), torch.zeros_like(refcn))
+        norm = gw.sum(1)
+        ok = norm > 0.0
+        w = gw / torch.where(ok, norm, torch.ones_like(norm))[:, None]
+        top = torch.where(valid, refcn, torch.full_like(refcn, -math.inf)).max(1).values
+        fb = (valid & ((refcn - top[:, None]).abs() < 1e-12)).to(cn.dtype)
+        return torch.where(ok[:, None], w, fb)
+
+    def evaluate(self, z: Tensor, pos: Tensor, cell: Optional[Tensor], pbc: Optional[Tensor],
+                 n_atoms: Tensor) -> Dict[str, Tensor]:
+        if not pos.is_cuda:
+            raise RuntimeError("xnn_amd D3 runs on the GPU (HIP kernels); there is no CPU path")
+        dev = pos.device
+        if self.refcn.device != dev:
+            raise RuntimeError("move the D3 module to the positions' device with .to(device)")
+        pos = pos.to(torch.float64)
+        counts, node_ptr, batch32 = _batch_layout(n_atoms, dev)
+        s = self.species(z).to(dev)
+        species = s.to(torch.int32).contiguous()
+        cell64 = None
+        images = torch.zeros((len(counts), 3), dtype=torch.int32, device=dev)
+        if cell is not None:
+            cell64 = cell.reshape(-1, 3, 3).to(dev, torch.float64).contiguous()
+            images = image_counts(cell64, pbc, self.cutoff).to(dev)
+        max_atoms = max(counts) if counts else 1
+        cn = d3_coordination_op(pos.contiguous(), cell64, species, batch32, node_ptr, images,
+                                self.rcov, self.cutoff_cn / BOHR, max_atoms)
+        w = self.weights(s, cn).contiguous()
+        params = [self.s6, self.s8, self.a1, self.a2, self.rs6, self.rs8, self.alp, self.bet,
+                  self.cutoff_pair / BOHR, self.switch_width_pair / BOHR,
+                  float(D3_DAMPINGS[self.damping])]
+        e2 = d3_two_body_op(pos.contiguous(), cell64, w, species, batch32, node_ptr, images,
+                            self.r4r2, self.rvdw.contiguous(), self.c6pair, params, max_atoms)
+        from .ops import structure_sum_op
+        energy = structure_sum_op(e2, node_ptr, batch32)
+        return {"node_energy": e2 * HARTREE, "energy": energy * HARTREE,
+                "energy_2body": energy * HARTREE, "coordination_numbers": cn, "weights": w}
+
+    def forward(self, data) -> Dict[str, Tensor]:
+        return self.evaluate(data.atomic_numbers, data.pos, data.cell, data.pbc, data.n_atoms)
+
+
+class D3Dispersion(DispersionCorrection):
+    """D3 (two-body) dispersion as a potential, standalone or wrapped around a model
+    (d3.py:965-1016); ``tables``: dict or path for :func:`load_d3_tables`."""
+
+    def __init__(self, model: Optional[nn.Module] = None, tables=None, **d3_options):
+        if tables is None:
+            raise ValueError("D3Dispersion needs the per-element D3 tables (dict or .npz path)")
+        if isinstance(tables, str):
+            tables = load_d3_tables(tables)
+        super().__init__(DFTD3(tables, **d3_options), model)
+
+    @property
+    def d3(self) -> DFTD3:
+        return self.term
