@@ -110,6 +110,25 @@ int xnn_edge_force_reduce(int geom_dtype, int compute_dtype, const void* g_edge,
                           void* grad_pos, double* cell_partial, const void* vec,
                           double* virial_partial, xnn_stream_t stream);
 
+/* The strain deformation of ForceStressOutput (outputs.py:166-180): with
+ * S_b = (strain_b + strain_b^T) / 2 (strain (B,3,3), geometry dtype),
+ * pos_out[i] = pos[i] (I + S_batch[i]) and cell_out[b] = cell[b] (I + S_b) (cell nullable).
+ * batch (N) int32 may be NULL for one structure. */
+int xnn_strain_apply(int geom_dtype, const void* pos, int64_t n_nodes, const int32_t* batch,
+                     const void* cell, int64_t n_graphs, const void* strain, void* pos_out,
+                     void* cell_out, xnn_stream_t stream);
+
+/* Backward of xnn_strain_apply for upstream g_pos (N,3) and g_cell (B,3,3):
+ * grad_pos = g_pos (I + S)^T, grad_cell = g_cell (I + S)^T, partial[i] = pos[i] (x) g_pos[i]
+ * (N,3,3) float64 (sum per structure with xnn_segment_reduce_f64) and
+ * cell_term[b] = cell[b]^T g_cell[b] (B,3,3) float64; the strain gradient is
+ * sym(sum_i partial_i + cell_term_b). */
+int xnn_strain_apply_backward(int geom_dtype, const void* pos, int64_t n_nodes,
+                              const int32_t* batch, const void* cell, int64_t n_graphs,
+                              const void* strain, const void* g_pos, const void* g_cell,
+                              void* grad_pos, void* grad_cell, double* partial,
+                              double* cell_term, xnn_stream_t stream);
+
 /* ------------------------------------------------------------------------ */
 /* Fused SH message aggregation: out[i,c,lm] = sum_{e: dst=i} phi[e,c] * Y_lm(sign r_e)
  * over the receiver CSR. Y is recomputed from positions in registers (never stored).

@@ -422,6 +422,41 @@ def test_stress_from_edge_virial_matches_deformation():
                                out_deform["forces"].detach().cpu().double(), atol=1e-6)
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float64])
+def test_strain_apply_matches_the_broadcast_formulation(dtype):
+    """The HIP strain deformation and its backward against the PyTorch formulation of
+    outputs.py:166-180 (batch of three cells, a nonzero strain), forward and gradients."""
+    from xnn_amd.ops import strain_apply_op
+    _note(f"strain_apply {dtype}")
+    gen = torch.Generator().manual_seed(5)
+    counts = [7, 11, 5]
+    pos = torch.randn(sum(counts), 3, generator=gen, dtype=torch.float64) * 3
+    cell = torch.randn(3, 3, 3, generator=gen, dtype=torch.float64) + 6 * torch.eye(3, dtype=torch.float64)
+    eps = torch.randn(3, 3, 3, generator=gen, dtype=torch.float64) * 0.01
+    batch = torch.repeat_interleave(torch.arange(3), torch.tensor(counts))
+    node_ptr = torch.tensor([0, 7, 18, 23])
+    gp = torch.randn(pos.shape, generator=gen, dtype=torch.float64)
+    gc = torch.randn(cell.shape, generator=gen, dtype=torch.float64)
+    # reference, in float64 on the CPU
+    e_r = eps.clone().requires_grad_(True)
+    p_r, c_r = pos.clone().requires_grad_(True), cell.clone().requires_grad_(True)
+    sym = 0.5 * (e_r + e_r.transpose(-1, -2))
+    p2 = p_r + (p_r[:, :, None] * sym.index_select(0, batch)).sum(1)
+    c2 = c_r + (c_r[:, :, :, None] * sym[:, None]).sum(2)
+    ge_r, gp_r, gc_r = torch.autograd.grad((p2 * gp).sum() + (c2 * gc).sum(), [e_r, p_r, c_r])
+    # HIP
+    e = eps.to(DEV, dtype).requires_grad_(True)
+    p = pos.to(DEV, dtype).requires_grad_(True)
+    c = cell.to(DEV, dtype).requires_grad_(True)
+    p3, c3 = strain_apply_op(p, c, e, batch.to(DEV, torch.int32), node_ptr.to(DEV))
+    ge, gpp, gcc = torch.autograd.grad((p3 * gp.to(DEV, dtype)).sum() + (c3 * gc.to(DEV, dtype)).sum(),
+                                       [e, p, c])
+    tol = 1e-12 if dtype == torch.float64 else 2e-5
+    for got, want in ((p3, p2), (c3, c2), (ge, ge_r), (gpp, gp_r), (gcc, gc_r)):
+        np.testing.assert_allclose(got.detach().cpu().double(), want.detach(),
+                                   atol=tol * max(1.0, float(want.abs().max())))
+
+
 def test_training_step_differentiates_forces_twice():
     """A force-loss training step (create_graph=True): the featurizer takes the PyTorch
     formulation, the edge vectors / sums stay on the HIP ops (differentiable to any

@@ -98,6 +98,8 @@ _SIGNATURES = {
                         ctypes.POINTER(D3PairParams), vp, vp, sz, vp],
     "xnn_d3_two_body_backward": [vp, i64, vp, vp, vp, i64, i64, vp, vp, vp, vp, vp, i32, vp,
                                  ctypes.POINTER(D3PairParams), vp, vp, vp, vp, vp, sz, vp],
+    "xnn_strain_apply": [c_int, vp, i64, vp, vp, i64, vp, vp, vp, vp],
+    "xnn_strain_apply_backward": [c_int, vp, i64, vp, vp, i64, vp, vp, vp, vp, vp, vp, vp, vp],
     "xnn_segment_sum": [c_int, vp, i64, i64, vp, vp, i64, vp, vp],
     "xnn_gather_rows": [c_int, vp, i64, i64, vp, i64, vp, vp],
     "xnn_segment_reduce_workspace_bytes": [i64, i64, i64],

@@ -7,6 +7,8 @@
 // xnn_edge_force_reduce        _EdgeVectors.backward (atomic_data.py:452-467) without atomics
 #include <string.h>
 
+#include <algorithm>
+
 #include "common.h"
 #include "device.h"
 
@@ -221,6 +223,94 @@ __global__ __launch_bounds__(256) void force_reduce_kernel(
   }
 }
 
+// ---------------------------------------------------------------- strain deformation
+// S_b = (eps_b + eps_b^T) / 2; pos'_i = pos_i (I + S_b), cell'_b = cell_b (I + S_b)
+// (outputs.py:166-180). Row vectors: (x S)_k = sum_j x_j S_jk.
+template <typename G>
+__device__ inline void sym_of(const G* __restrict__ eps, int64_t b, double S[9]) {
+  const G* e = eps + 9 * b;
+#pragma unroll
+  for (int j = 0; j < 3; ++j)
+#pragma unroll
+    for (int k = 0; k < 3; ++k) S[3 * j + k] = 0.5 * ((double)e[3 * j + k] + (double)e[3 * k + j]);
+}
+
+template <typename G>
+__global__ __launch_bounds__(256) void strain_fwd_kernel(
+    const G* __restrict__ pos, int64_t n_nodes, const int32_t* __restrict__ batch,
+    const G* __restrict__ cell, int64_t n_graphs, const G* __restrict__ eps,
+    G* __restrict__ pos_out, G* __restrict__ cell_out) {
+  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (t < n_nodes) {
+    double S[9];
+    sym_of(eps, batch ? batch[t] : 0, S);
+    const G x = pos[3 * t], y = pos[3 * t + 1], z = pos[3 * t + 2];
+#pragma unroll
+    for (int k = 0; k < 3; ++k)
+      pos_out[3 * t + k] = pos[3 * t + k] + (G)(x * S[k] + y * S[3 + k] + z * S[6 + k]);
+  }
+  if (cell != nullptr && t < 3 * n_graphs) {   // one cell row per thread
+    const int64_t b = t / 3;
+    double S[9];
+    sym_of(eps, b, S);
+    const G* r = cell + 3 * t;
+#pragma unroll
+    for (int k = 0; k < 3; ++k)
+      cell_out[3 * t + k] = r[k] + (G)(r[0] * S[k] + r[1] * S[3 + k] + r[2] * S[6 + k]);
+  }
+}
+
+// grad_pos_i = g_i (I + S_b)^T; partial_i = pos_i (x) g_i (float64, to be summed per
+// structure); grad_cell_b = g_cell_b (I + S_b)^T; cell_term_b = cell_b^T g_cell_b.
+template <typename G>
+__global__ __launch_bounds__(256) void strain_bwd_kernel(
+    const G* __restrict__ pos, int64_t n_nodes, const int32_t* __restrict__ batch,
+    const G* __restrict__ cell, int64_t n_graphs, const G* __restrict__ eps,
+    const G* __restrict__ g_pos, const G* __restrict__ g_cell, G* __restrict__ grad_pos,
+    G* __restrict__ grad_cell, double* __restrict__ partial, double* __restrict__ cell_term) {
+  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (t < n_nodes) {
+    double S[9];
+    sym_of(eps, batch ? batch[t] : 0, S);
+    const double gx = g_pos[3 * t], gy = g_pos[3 * t + 1], gz = g_pos[3 * t + 2];
+    // (g S^T)_j = sum_k g_k S_jk
+#pragma unroll
+    for (int j = 0; j < 3; ++j)
+      grad_pos[3 * t + j] = (G)((double)g_pos[3 * t + j] + gx * S[3 * j] + gy * S[3 * j + 1] +
+                                gz * S[3 * j + 2]);
+    const double x = pos[3 * t], y = pos[3 * t + 1], z = pos[3 * t + 2];
+    double* m = partial + 9 * t;
+    m[0] = x * gx; m[1] = x * gy; m[2] = x * gz;
+    m[3] = y * gx; m[4] = y * gy; m[5] = y * gz;
+    m[6] = z * gx; m[7] = z * gy; m[8] = z * gz;
+  }
+  if (cell != nullptr && t < n_graphs) {
+    double S[9];
+    sym_of(eps, t, S);
+    const G* c = cell + 9 * t;
+    const G* gc = g_cell + 9 * t;
+#pragma unroll
+    for (int a = 0; a < 3; ++a)
+#pragma unroll
+      for (int j = 0; j < 3; ++j) {
+        double v = gc[3 * a + j];
+#pragma unroll
+        for (int k = 0; k < 3; ++k) v += (double)gc[3 * a + k] * S[3 * j + k];
+        grad_cell[9 * t + 3 * a + j] = (G)v;
+      }
+    // (cell^T g)_jk = sum_a cell_aj g_ak
+#pragma unroll
+    for (int j = 0; j < 3; ++j)
+#pragma unroll
+      for (int k = 0; k < 3; ++k) {
+        double v = 0.0;
+#pragma unroll
+        for (int a = 0; a < 3; ++a) v += (double)c[3 * a + j] * (double)gc[3 * a + k];
+        cell_term[9 * t + 3 * j + k] = v;
+      }
+  }
+}
+
 // ---------------------------------------------------------------- dispatch helpers
 template <typename T>
 static int make_radial(const xnn_featurize_params* prm, const void* table, Radial<T>& R) {
@@ -405,6 +495,63 @@ int xnn_edge_force_reduce(int geom_dtype, int compute_dtype, const void* g_edge,
   XNN_DISPATCH_GT(geom_dtype, compute_dtype, force_reduce, g_edge, n_edges, ptr_dst, perm_dst,
                   ptr_src, perm_src, shift, n_nodes, grad_pos, cell_partial, vec, virial_partial,
                   as_hip(stream));
+}
+
+int xnn_strain_apply(int geom_dtype, const void* pos, int64_t n_nodes, const int32_t* batch,
+                     const void* cell, int64_t n_graphs, const void* strain, void* pos_out,
+                     void* cell_out, xnn_stream_t stream) {
+  XNN_REQUIRE(n_nodes >= 0 && n_graphs >= 1, "bad sizes");
+  XNN_REQUIRE(strain != nullptr && (n_nodes == 0 || (pos && pos_out)), "NULL input or output");
+  XNN_REQUIRE(n_graphs == 1 || batch != nullptr, "several structures need the batch vector");
+  XNN_REQUIRE(cell == nullptr || cell_out != nullptr, "NULL cell_out");
+  const int64_t n = std::max<int64_t>(n_nodes, 3 * n_graphs);
+  if (n == 0) return XNN_OK;
+  hipStream_t s = as_hip(stream);
+  if (geom_dtype == XNN_F32)
+    hipLaunchKernelGGL(strain_fwd_kernel<float>, dim3(grid_1d(n, 256)), dim3(256), 0, s,
+                       (const float*)pos, n_nodes, batch, (const float*)cell, n_graphs,
+                       (const float*)strain, (float*)pos_out, (float*)cell_out);
+  else if (geom_dtype == XNN_F64)
+    hipLaunchKernelGGL(strain_fwd_kernel<double>, dim3(grid_1d(n, 256)), dim3(256), 0, s,
+                       (const double*)pos, n_nodes, batch, (const double*)cell, n_graphs,
+                       (const double*)strain, (double*)pos_out, (double*)cell_out);
+  else {
+    set_error("unsupported geometry dtype %d", geom_dtype);
+    return XNN_EINVAL;
+  }
+  XNN_LAUNCH_CHECK();
+  return XNN_OK;
+}
+
+int xnn_strain_apply_backward(int geom_dtype, const void* pos, int64_t n_nodes,
+                              const int32_t* batch, const void* cell, int64_t n_graphs,
+                              const void* strain, const void* g_pos, const void* g_cell,
+                              void* grad_pos, void* grad_cell, double* partial,
+                              double* cell_term, xnn_stream_t stream) {
+  XNN_REQUIRE(n_nodes >= 0 && n_graphs >= 1, "bad sizes");
+  XNN_REQUIRE(strain != nullptr && (n_nodes == 0 || (pos && g_pos && grad_pos && partial)),
+              "NULL input or output");
+  XNN_REQUIRE(n_graphs == 1 || batch != nullptr, "several structures need the batch vector");
+  XNN_REQUIRE(cell == nullptr || (g_cell && grad_cell && cell_term), "NULL cell gradient");
+  const int64_t n = std::max<int64_t>(n_nodes, n_graphs);
+  if (n == 0) return XNN_OK;
+  hipStream_t s = as_hip(stream);
+  if (geom_dtype == XNN_F32)
+    hipLaunchKernelGGL(strain_bwd_kernel<float>, dim3(grid_1d(n, 256)), dim3(256), 0, s,
+                       (const float*)pos, n_nodes, batch, (const float*)cell, n_graphs,
+                       (const float*)strain, (const float*)g_pos, (const float*)g_cell,
+                       (float*)grad_pos, (float*)grad_cell, partial, cell_term);
+  else if (geom_dtype == XNN_F64)
+    hipLaunchKernelGGL(strain_bwd_kernel<double>, dim3(grid_1d(n, 256)), dim3(256), 0, s,
+                       (const double*)pos, n_nodes, batch, (const double*)cell, n_graphs,
+                       (const double*)strain, (const double*)g_pos, (const double*)g_cell,
+                       (double*)grad_pos, (double*)grad_cell, partial, cell_term);
+  else {
+    set_error("unsupported geometry dtype %d", geom_dtype);
+    return XNN_EINVAL;
+  }
+  XNN_LAUNCH_CHECK();
+  return XNN_OK;
 }
 
 }  // extern "C"

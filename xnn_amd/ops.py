@@ -266,6 +266,67 @@ def edge_vectors(pos: Tensor, cell: Optional[Tensor], plan: EdgePlan,
                            plan.node_ptr, _lib.dtype_code(out_dtype))
 
 
+# --------------------------------------------------------------------------- strain deformation
+@torch.library.custom_op(f"{_NS}::strain_apply", mutates_args=())
+def strain_apply_op(pos: Tensor, cell: Optional[Tensor], strain: Tensor, batch32: Tensor,
+                    node_ptr: Tensor) -> Tuple[Tensor, Tensor]:
+    """``pos (I + sym(strain)[batch])`` and ``cell (I + sym(strain))``, the deformation
+    of ForceStressOutput (outputs.py:166-180); an empty cell comes back empty."""
+    dev = _require_gpu(pos, strain)
+    code = _lib.dtype_code(pos.dtype)
+    cell = _opt(cell)
+    pos_out = torch.empty_like(pos)
+    cell_out = torch.empty_like(cell) if cell is not None else pos.new_zeros((0,))
+    n_graphs = node_ptr.shape[0] - 1
+    _lib.call("xnn_strain_apply", code, _lib.ptr(pos), pos.shape[0],
+              _lib.ptr(batch32) if n_graphs > 1 else None, _lib.ptr(cell), n_graphs,
+              _lib.ptr(strain), _lib.ptr(pos_out), _lib.ptr(cell_out) if cell is not None else None,
+              _lib.stream(dev))
+    return pos_out, cell_out
+
+
+@strain_apply_op.register_fake
+def _(pos, cell, strain, batch32, node_ptr):
+    return torch.empty_like(pos), (torch.empty_like(cell) if cell is not None and cell.numel()
+                                   else pos.new_zeros((0,)))
+
+
+def _strain_setup(ctx, inputs, output):
+    pos, cell, strain, batch32, node_ptr = inputs
+    ctx.save_for_backward(pos, _opt(cell), strain, batch32, node_ptr)
+
+
+def _strain_backward(ctx, g_pos, g_cell):
+    _once_differentiable()
+    pos, cell, strain, batch32, node_ptr = ctx.saved_tensors
+    dev, n = pos.device, pos.shape[0]
+    n_graphs = node_ptr.shape[0] - 1
+    code = _lib.dtype_code(pos.dtype)
+    g_pos = torch.zeros_like(pos) if g_pos is None else g_pos.contiguous()
+    grad_pos = torch.empty_like(pos)
+    partial = torch.empty((n, 9), dtype=torch.float64, device=dev)
+    grad_cell = term = None
+    if cell is not None:
+        g_cell = torch.zeros_like(cell) if (g_cell is None or g_cell.numel() == 0) else g_cell.contiguous()
+        grad_cell = torch.empty_like(cell)
+        term = torch.empty((n_graphs, 9), dtype=torch.float64, device=dev)
+    _lib.call("xnn_strain_apply_backward", code, _lib.ptr(pos), n,
+              _lib.ptr(batch32) if n_graphs > 1 else None, _lib.ptr(cell), n_graphs,
+              _lib.ptr(strain), _lib.ptr(g_pos), _lib.ptr(g_cell) if cell is not None else None,
+              _lib.ptr(grad_pos), _lib.ptr(grad_cell), _lib.ptr(partial), _lib.ptr(term),
+              _lib.stream(dev))
+    M = torch.empty((n_graphs, 9), dtype=torch.float64, device=dev)
+    _lib.segment_reduce_f64(partial, n, 9, node_ptr, n_graphs, M)
+    if term is not None:
+        M = M + term
+    M = M.view(n_graphs, 3, 3)
+    grad_strain = (0.5 * (M + M.transpose(1, 2))).to(strain.dtype)
+    return grad_pos, grad_cell, grad_strain, None, None
+
+
+strain_apply_op.register_autograd(_strain_backward, setup_context=_strain_setup)
+
+
 # --------------------------------------------------------------------------- edge embedding
 def _params(iparams: List[int], fparams: List[float]) -> "_lib.FeaturizeParams":
     n_rbf, basis, envelope, p, l_max, sign = iparams

@@ -47,6 +47,16 @@ class ForceStressOutput(nn.Module):
             data.strain_probe = strain
             if not data.pos.requires_grad:       # a fresh leaf; the caller's tensor is untouched
                 data.pos = data.pos.detach().requires_grad_(True)
+        elif self.compute_stress and data.cell is not None and data.pos.is_cuda and not create_graph:
+            # one HIP kernel each way instead of the broadcast products (differentiable once)
+            from .ops import strain_apply_op
+            strain = torch.zeros((data.num_graphs, 3, 3), dtype=data.pos.dtype,
+                                 device=data.pos.device, requires_grad=True)
+            batch32, node_ptr = _layout(data)
+            data.pos, cell = strain_apply_op(data.pos.contiguous(),
+                                             data.cell.reshape(-1, 3, 3).to(data.pos.dtype).contiguous(),
+                                             strain, batch32, node_ptr)
+            data.cell = cell.to(data.cell.dtype)
         elif self.compute_stress and data.cell is not None:
             strain = torch.zeros((data.num_graphs, 3, 3), dtype=data.pos.dtype,
                                  device=data.pos.device, requires_grad=True)
@@ -93,6 +103,17 @@ class ForceStressOutput(nn.Module):
             out["stress"] = (_stress(g["strain"], data) if g.get("strain") is not None
                              else torch.zeros_like(strain))
         return out
+
+
+def _layout(data):
+    """int32 structure index per atom and int64 structure offsets (B+1): from the edge
+    plan when the graph has one (cached), else from n_atoms."""
+    if data.num_edges > 0:
+        plan = data.plan()
+        return plan.batch32, plan.node_ptr
+    node_ptr = torch.zeros(data.num_graphs + 1, dtype=torch.int64, device=data.pos.device)
+    node_ptr[1:] = torch.cumsum(data.n_atoms.to(data.pos.device), 0)
+    return data.batch.to(torch.int32).contiguous(), node_ptr
 
 
 def _stress(strain_gradient: Tensor, data) -> Tensor:
