@@ -4,10 +4,11 @@ Workload (``--config water``, the default): the 9,000-atom liquid water box (3,0
 H2O at 1.0 g/cm^3, cubic periodic cell of 44.8 A), cutoff 5.0 A, 8 Bessel radial
 functions x polynomial envelope, real SH l <= 3 (16 components), 128 float32 channels.
 A step is one evaluation of ``ForceStressOutput(ShEdgePotential)``: edge vectors ->
-fused featurizer -> radial linear + SH message sum into (N, 128, 16) in one kernel (the
-per-edge weights phi = u W are formed on the matrix cores and never stored) -> readout
--> float64 energy -> backward to forces and virial stress, all on the GPU with inputs
-resident in HBM. The neighbor list is timed separately (``neighbor_list_ms``).
+radial basis + radial linear + SH message sum into (N, 128, 16) in one kernel (the radial
+features u are evaluated per lane and the per-edge weights phi = u W are formed on the
+matrix cores; neither is stored) -> readout -> float64 energy -> backward to forces and
+virial stress (one kernel back through message, linear layer and radial basis), all on
+the GPU with inputs resident in HBM. The neighbor list is timed separately (``neighbor_list_ms``).
 
 Prints one JSON line. ``value`` = edges / (forward + force/stress backward time).
 ``roofline`` is the dominant kernel's algorithmic work per launch (HBM bytes, or fp32
@@ -66,6 +67,12 @@ def kernel_costs(E: int, N: int, C: int, L: int = 16, K: int = 8, grouped: bool 
     come grouped by receiver. Flops count the true dimensions (no padding)."""
     perm = 0 if grouped else 4
     return {
+        "xnn_sh_radial_message_sum": {                     # radial basis evaluated in-kernel
+            "bytes": E * (12 + perm) + N * (4 * C * L + 4),
+            "flops": E * 2 * C * (K + L)},
+        "xnn_sh_radial_message_sum_backward": {
+            "bytes": E * (12 + perm + 12) + N * (4 * C * L + 4),
+            "flops": E * 2 * C * (2 * K + 2 * L)},
         "xnn_sh_linear_message_sum": {
             "bytes": E * (12 + 4 * K + perm) + N * (4 * C * L + 4),
             "flops": E * 2 * C * (K + L)},                 # phi = h W, then phi (x) Y
@@ -84,17 +91,16 @@ def kernel_costs(E: int, N: int, C: int, L: int = 16, K: int = 8, grouped: bool 
     }
 
 
-def step_bytes(E: int, N: int, C: int, L: int, K: int, fused: bool) -> int:
-    """Compulsory traffic of one whole step: edge vectors from positions, featurizer,
-    message sum, readout (reads A), its backward (writes d_A), message backward,
-    featurizer backward, force reduction."""
+def step_bytes(E: int, N: int, C: int, L: int, K: int, msg: str) -> int:
+    """Compulsory traffic of one whole step: edge vectors from positions, featurizer
+    (unless the message kernels evaluate the radial basis), message sum, readout (reads
+    A), its backward (writes d_A), message backward, featurizer backward, force reduction."""
     kc = kernel_costs(E, N, C, L, K)
-    msg = "xnn_sh_linear_message_sum" if fused else "xnn_sh_message_sum"
-    linear = 0 if fused else 2 * (E * 4 * (K + C))      # u @ W and d_phi @ W^T
-    return (E * 24 + N * 12 + kc["xnn_edge_featurize"]["bytes"] + kc[msg]["bytes"]
-            + N * 4 * C * L + N * 4 * C * L + kc[msg + "_backward"]["bytes"]
-            + kc["xnn_edge_featurize_backward"]["bytes"] + kc["xnn_edge_force_reduce"]["bytes"]
-            + linear)
+    feat = 0 if msg == "xnn_sh_radial_message_sum" else (
+        kc["xnn_edge_featurize"]["bytes"] + kc["xnn_edge_featurize_backward"]["bytes"])
+    linear = 2 * (E * 4 * (K + C)) if msg == "xnn_sh_message_sum" else 0  # u @ W, d_phi @ W^T
+    return (E * 24 + N * 12 + feat + kc[msg]["bytes"] + N * 4 * C * L + N * 4 * C * L
+            + kc[msg + "_backward"]["bytes"] + kc["xnn_edge_force_reduce"]["bytes"] + linear)
 
 
 def build_workload(config: str, device):
@@ -252,6 +258,9 @@ def main() -> None:
     ap.add_argument("--fused", action=argparse.BooleanOptionalAction, default=True,
                     help="radial linear layer inside the message kernels (ShEdgePotential "
                          "fused_linear)")
+    ap.add_argument("--fused-radial", action=argparse.BooleanOptionalAction, default=True,
+                    help="radial basis evaluated inside the message kernels (ShEdgePotential "
+                         "fused_radial)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run the 256 MiB copy that calibrates the HBM byte counters")
     args = ap.parse_args()
@@ -275,6 +284,7 @@ def main() -> None:
 
     g, model, rc, kw, workload, nl_ms, structs = build_workload(args.config, device)
     model.fused_linear = bool(args.fused)
+    model.fused_radial = bool(args.fused_radial)
     E, N = g.num_edges, g.num_nodes
     C, L = kw["channels"], (kw["l_max"] + 1) ** 2
     wrapped = xa.ForceStressOutput(model, compute_stress=g.cell is not None).eval()
@@ -284,11 +294,14 @@ def main() -> None:
         data = copy.copy(g)                     # ForceStressOutput rebinds pos / cell
         return wrapped(data)
 
+    _lib.calls.clear()
     for _ in range(args.warmup):
         out = step()
-    fused = bool(model.fused_linear and
-                 xa.ops.linear_message_supported(kw["n_rbf"], C, kw["l_max"]))
-    msg = "xnn_sh_linear_message_sum" if fused else "xnn_sh_message_sum"
+    # the message entry point the step took (radial basis in the kernel, linear layer in
+    # the kernel, or the linear layer in PyTorch)
+    msg = next(m for m in ("xnn_sh_radial_message_sum", "xnn_sh_linear_message_sum",
+                           "xnn_sh_message_sum") if _lib.calls.get(m))
+    fused = msg != "xnn_sh_message_sum"
     kernels = [msg, msg + "_backward", "xnn_edge_featurize", "xnn_edge_featurize_backward",
                "xnn_edge_force_reduce"]
     # eager pass: per-kernel HIP events on the launch stream
@@ -335,14 +348,15 @@ def main() -> None:
         if not graph_checked:
             raise SystemExit("graph replay differs from the eager step")
 
-    per_kernel = {}
+    per_kernel, total_us = {}, {}
     for name in kernels:
         ev = timed.get(name, [])
         if ev:
-            per_kernel[name] = float(np.mean([s.elapsed_time(e) for s, e in ev])) * 1e3  # us
+            d = [s.elapsed_time(e) * 1e3 for s, e in ev]          # us
+            per_kernel[name] = float(np.mean(d))
+            total_us[name] = float(np.sum(d)) / args.steps       # per step, all launches
     _lib.timed.clear()
     kc = kernel_costs(E, N, C, L, kw["n_rbf"], grouped=g.plan().perm_dst is None)
-    total_us = {k: per_kernel[k] * (2 if k == "xnn_edge_featurize" else 1) for k in per_kernel}
     dominant = max(per_kernel, key=lambda k: total_us[k])
     launch_s = per_kernel[dominant] * 1e-6
     cost = kc[dominant]
@@ -362,7 +376,7 @@ def main() -> None:
                      "algorithmic_bytes": cost["bytes"], "algorithmic_flops": cost["flops"],
                      "hbm_GBs": round(cost["bytes"] / launch_s / 1e9, 1),
                      "mean_launch_us": round(per_kernel[dominant], 2)})
-    sb = step_bytes(E, N, C, L, kw["n_rbf"], fused)
+    sb = step_bytes(E, N, C, L, kw["n_rbf"], msg)
     step_gbs = sb / (ms * 1e-3) / 1e9
     result = {
         "metric": "edges/s fwd+force-bwd and % HBM roofline, 9k-atom water box, 1 MI355X",
@@ -374,7 +388,7 @@ def main() -> None:
                    "neighbor_list_ms": round(nl_ms, 3),
                    "hip_graph": bool(args.graph), "eager_ms_per_step": round(eager_ms, 4),
                    "graph_replay_matches_eager": graph_checked,
-                   "fused_linear": fused,
+                   "fused_linear": fused, "message_kernel": msg,
                    "step_algorithmic_bytes": sb,
                    "step_hbm_fraction": round(step_gbs / HBM_PEAK_GBS, 4),
                    "kernel_mean_us": {k: round(v, 2) for k, v in per_kernel.items()}},

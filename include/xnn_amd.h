@@ -183,6 +183,52 @@ int xnn_sh_linear_message_sum_backward(int geom_dtype, const float* vec_in, cons
                                        const float* d_out, float* d_h, float* g_vec,
                                        xnn_stream_t stream);
 
+/* Featurizer, edge-weight linear layer and aggregation in one kernel: h is the
+ * enveloped radial basis of the edge length, h[e,k] = rbf_k(|r_e|) envelope(|r_e|)
+ * (SphericalHarmonicEdgeEmbedding.forward, gnn/featurizers/spherical.py:135-138, whose
+ * radial part feeds the edge-weight network), evaluated per lane in the kernel;
+ * A[i,c,lm] = sum_{dst(e)=i} (h_e W)[c] Y_lm(sh_sign r_e) as in xnn_sh_linear_message_sum.
+ * prm gives the basis, envelope, cutoff, l_max in [1, 3] and sh_sign; n_rbf = K in
+ * [1, 8]; rbf_table (K) f32 (Bessel frequencies or Gaussian centers). Neither h nor
+ * phi is stored. out (N,C,L) f32, 16-byte aligned. */
+int xnn_sh_radial_message_sum(int geom_dtype, const float* vec_in, const void* pos,
+                              int64_t n_nodes, const void* cell, int64_t n_graphs,
+                              const int32_t* batch, const int32_t* src, const int32_t* shift,
+                              int64_t n_edges, const int32_t* ptr_dst, const int32_t* perm_dst,
+                              const xnn_featurize_params* prm, const float* rbf_table,
+                              int32_t n_channels, const float* W, float* out,
+                              xnn_stream_t stream);
+
+/* Backward of xnn_sh_radial_message_sum with respect to the edge vectors, through the
+ * harmonics and the radial basis: g_vec (E,3) f32 = dL/dr_e (written, not added).
+ * Parameter gradients (W, rbf_table) are not formed: the caller uses
+ * xnn_edge_featurize + xnn_sh_linear_message_sum(_backward) when it trains them. */
+int xnn_sh_radial_message_sum_backward(int geom_dtype, const float* vec_in, const void* pos,
+                                       int64_t n_nodes, const void* cell, int64_t n_graphs,
+                                       const int32_t* batch, const int32_t* src,
+                                       const int32_t* shift, int64_t n_edges,
+                                       const int32_t* ptr_dst, const int32_t* perm_dst,
+                                       const xnn_featurize_params* prm, const float* rbf_table,
+                                       int32_t n_channels, const float* W, const float* d_out,
+                                       float* g_vec, xnn_stream_t stream);
+
+/* Finish of a per-structure virial: out[b] = sym(M[b] + term[b]) with sym(X) = (X + X^T)/2
+ * (symmetrize != 0) or M[b] + term[b], cast to dtype. M (B,3,3) float64 (from
+ * xnn_segment_reduce_f64 over the per-atom partials of xnn_edge_force_reduce or
+ * xnn_strain_apply_backward), term (B,3,3) float64 nullable. The strain gradient of
+ * ForceStressOutput (outputs.py:166-216) is this with symmetrize = 1. */
+int xnn_virial_finish(int dtype, const double* M, const double* term, int64_t n_graphs,
+                      int32_t symmetrize, void* out, xnn_stream_t stream);
+
+/* The stress of ForceStressOutput from the strain gradient (outputs.py:227-239):
+ * stress[b] = scale * strain_grad[b] / |det cell_b| for periodic structures
+ * (|det| > 1e-8 and, when pbc (B,3) bool/uint8 is given, some periodic direction),
+ * zero for the molecules of a batch. strain_grad and stress (B,3,3) of dtype;
+ * cell (B,3,3) of cell_dtype (f32/f64); scale = -1 takes the gradient of -E. */
+int xnn_stress_finish(int dtype, const void* strain_grad, int cell_dtype, const void* cell,
+                      const uint8_t* pbc, int64_t n_graphs, double scale, void* stress,
+                      xnn_stream_t stream);
+
 /* ------------------------------------------------------------------------ */
 /* Segmented sum over a CSR: out[i,:] = sum_{k in [ptr[i],ptr[i+1])} src[perm[k],:].
  * Replaces scatter_sum (common/models/ops.py:403-448) without atomics; its

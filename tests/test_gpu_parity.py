@@ -298,6 +298,59 @@ def test_sh_linear_message_sum_forward_backward(C, l_max, K):
     assert torch.equal(A, A2)
 
 
+@pytest.mark.parametrize("C,l_max,K,radial,envelope,sign",
+                         [(128, 3, 8, "bessel", "polynomial", 1),
+                          (64, 2, 8, "bessel", "cosine", -1),
+                          (32, 1, 6, "gaussian", "polynomial", 1),
+                          (128, 3, 4, "gaussian", "cosine", 1)])
+def test_sh_radial_message_sum_forward_backward(C, l_max, K, radial, envelope, sign):
+    """Radial basis, linear layer and message in one kernel each way, against the oracle's
+    radial features (radial.py / cutoff.py restated), materialized messages and float64
+    autograd; also against the two-kernel composition (edge_embed + the fused linear
+    message), which must agree to float32 rounding."""
+    import oracle.reference as R
+    import xnn_amd as xa
+    from xnn_amd import synthetic
+    from xnn_amd.featurizers import SphericalHarmonicEdgeEmbedding
+    from xnn_amd.ops import sh_linear_message_sum
+    _note(f"sh_radial_message_sum C={C} l_max={l_max} K={K} {radial} {envelope} sign={sign}")
+    s = synthetic.water_box(n_molecules=216, box=18.6, grid=6, seed=4)
+    g = xa.structure_to_graph(s.as_dict(), 5.0, device=DEV)
+    g.pos = g.pos.float()
+    vec = g.edge_vectors().detach().requires_grad_(True)
+    emb = SphericalHarmonicEdgeEmbedding(l_max=l_max, n_rbf=K, cutoff=5.0, radial_type=radial,
+                                         envelope=envelope).to(DEV)
+    emb.fast_active = True
+    gen = torch.Generator().manual_seed(7 * C + K)
+    W = (torch.randn(K, C, generator=gen) / K ** 0.5).to(DEV)
+    A = emb.radial_message_sum(vec, W, g.plan(), sign)
+    dA = torch.randn(A.shape, generator=gen).to(DEV)
+    (gvec,) = torch.autograd.grad((A * dA).sum(), (vec,))
+    # oracle, float64
+    vc = vec.detach().cpu().double().requires_grad_(True)
+    Y = R.e3nn_sh(l_max, vc if sign == 1 else -vc)
+    phi = R.radial_features(torch.linalg.norm(vc, dim=-1), K, 5.0, radial, envelope) @ W.cpu().double()
+    msg = (phi[:, :, None] * Y[:, None, :]).reshape(vc.shape[0], -1)
+    Ar = R.scatter_sum(msg, g.edge_index[1].cpu(), g.num_nodes).reshape(A.shape)
+    (gv_r,) = torch.autograd.grad((Ar * dA.cpu().double()).sum(), (vc,))
+    scale = float(Ar.detach().abs().max())
+    np.testing.assert_allclose(A.detach().cpu().double(), Ar.detach(), atol=2e-6 * scale)
+    np.testing.assert_allclose(gvec.cpu().double(), gv_r, atol=2e-5 * max(1.0, float(gv_r.abs().max())))
+    # the composition: radial features stored, then the fused linear message
+    u = emb.radial(vec)
+    A_c = sh_linear_message_sum(vec, u, W, g.plan(), l_max, sign)
+    (gvec_c,) = torch.autograd.grad((A_c * dA).sum(), (vec,))
+    np.testing.assert_allclose(A.detach().cpu(), A_c.detach().cpu(), atol=1e-6 * scale)
+    np.testing.assert_allclose(gvec.cpu(), gvec_c.cpu(), atol=1e-6 * max(1.0, float(gv_r.abs().max())))
+    # reproducible run to run
+    A2 = emb.radial_message_sum(vec, W, g.plan(), sign)
+    assert torch.equal(A, A2)
+    # parameter gradients are refused, not silently dropped
+    with pytest.raises(NotImplementedError):
+        torch.autograd.grad(emb.radial_message_sum(vec, W.clone().requires_grad_(True), g.plan(),
+                                                   sign).sum(), (vec,))
+
+
 def test_segment_gather_and_structure_sums():
     import oracle.reference as R
     import xnn_amd as xa
@@ -329,10 +382,71 @@ def test_segment_gather_and_structure_sums():
     assert abs(float(got1[0]) - float(vals.float().double().sum())) < 1e-9
 
 
+@pytest.mark.parametrize("F", [1, 3, 9, 16, 64, 65])
+def test_single_structure_reduction(F):
+    """One segment (one structure): the flat two-level kernel (F <= 64) and the row-chunked
+    one (F > 64) against float64 sums on the CPU, for the whole array and for a sub-range,
+    reproducible bit for bit."""
+    from xnn_amd import _lib
+    _note(f"single-structure reduction F={F}")
+    gen = torch.Generator().manual_seed(F)
+    for n, (s0, s1) in [(9000, (0, 9000)), (9000, (17, 8001)), (100, (0, 100)),
+                        (250_000, (0, 250_000))]:
+        for dt in (torch.float32, torch.float64):
+            src = (torch.randn(n, F, generator=gen, dtype=torch.float64) * 3).to(dt)
+            seg = torch.tensor([s0, s1], dtype=torch.int64, device=DEV)
+            out = torch.empty(1, F, dtype=torch.float64, device=DEV)
+            d = src.to(DEV)
+            _lib.segment_reduce_f64(d, n, F, seg, 1, out)
+            want = src[s0:s1].double().sum(0)
+            np.testing.assert_allclose(out[0].cpu(), want, rtol=1e-12, atol=1e-9)
+            out2 = torch.empty_like(out)
+            _lib.segment_reduce_f64(d, n, F, seg, 1, out2)
+            assert torch.equal(out, out2)
+
+
+def test_stress_and_virial_finish_kernels():
+    """sym(M + term) cast, and scale * g / |det cell| with zero stress for zero cells and
+    non-periodic structures, against the PyTorch formulation."""
+    from xnn_amd.ops import stress_finish, virial_finish
+    from xnn_amd.functional import cell_volume
+    _note("stress / virial finish")
+    gen = torch.Generator().manual_seed(11)
+    B = 5
+    M = torch.randn(B, 9, generator=gen, dtype=torch.float64)
+    term = torch.randn(B, 9, generator=gen, dtype=torch.float64)
+    for t in (None, term):
+        for dt in (torch.float32, torch.float64):
+            got = virial_finish(M.to(DEV), None if t is None else t.to(DEV), dt)
+            X = (M if t is None else M + t).view(B, 3, 3)
+            np.testing.assert_allclose(got.cpu().double(), 0.5 * (X + X.transpose(1, 2)),
+                                       rtol=1e-6 if dt == torch.float32 else 1e-15)
+    cell = torch.randn(B, 3, 3, generator=gen, dtype=torch.float64) + 4 * torch.eye(3, dtype=torch.float64)
+    cell[1] = 0.0                                  # a molecule of the batch
+    pbc = torch.ones(B, 3, dtype=torch.bool)
+    pbc[3] = False                                 # a cell that is not periodic
+    g = torch.randn(B, 3, 3, generator=gen, dtype=torch.float64)
+    vol = cell_volume(cell)
+    periodic = (vol > 1e-8) & pbc.any(-1)
+    want = torch.where(periodic[:, None, None], -g / torch.where(periodic, vol, torch.ones_like(vol))[:, None, None],
+                       torch.zeros_like(g))
+    for p in (pbc, pbc.to(DEV), None):
+        for dt in (torch.float32, torch.float64):
+            got = stress_finish(g.to(DEV, dt), cell.to(DEV, dt), p, -1.0)
+            w = want if p is not None else torch.where((vol > 1e-8)[:, None, None],
+                                                       -g / torch.where(vol > 1e-8, vol, torch.ones_like(vol))[:, None, None],
+                                                       torch.zeros_like(g))
+            np.testing.assert_allclose(got.cpu().double(), w, rtol=1e-6 if dt == torch.float32 else 1e-13,
+                                       atol=1e-7 if dt == torch.float32 else 1e-15)
+
+
 # --------------------------------------------------------------------------- full model
-@pytest.mark.parametrize("config,fused", [("water", True), ("water", False), ("argon", True),
-                                          ("ragged", True), ("nequip_molecules", True),
-                                          ("nequip_molecules", False), ("periodic_batch", True)])
+@pytest.mark.parametrize("config,fused", [("water", "radial"), ("water", "linear"),
+                                          ("water", "unfused"), ("argon", "radial"),
+                                          ("ragged", "radial"), ("ragged", "linear"),
+                                          ("nequip_molecules", "radial"),
+                                          ("nequip_molecules", "unfused"),
+                                          ("periodic_batch", "radial")])
 def test_model_energy_forces_stress(config, fused):
     import oracle.reference as R
     import xnn_amd as xa
@@ -364,13 +478,17 @@ def test_model_energy_forces_stress(config, fused):
     g.pos = g.pos.float()
     if g.cell is not None:
         g.cell = g.cell.float()
-    model = xa.ShEdgePotential(cutoff=rc, species=(1, 6, 7, 8, 18), fused_linear=fused,
+    model = xa.ShEdgePotential(cutoff=rc, species=(1, 6, 7, 8, 18),
+                               fused_linear=fused != "unfused", fused_radial=fused == "radial",
                                **kw).to(DEV)
     before = dict(_lib.calls)
     out = xa.ForceStressOutput(model, compute_stress=g.cell is not None).eval()(g)
-    msg = "xnn_sh_linear_message_sum" if fused else "xnn_sh_message_sum"
-    for name in (msg, msg + "_backward", "xnn_edge_force_reduce",
-                 "xnn_edge_featurize", "xnn_edge_featurize_backward"):
+    msg = {"radial": "xnn_sh_radial_message_sum", "linear": "xnn_sh_linear_message_sum",
+           "unfused": "xnn_sh_message_sum"}[fused]
+    ran = [msg, msg + "_backward", "xnn_edge_force_reduce", "xnn_edge_featurize"]
+    if fused != "radial":
+        ran.append("xnn_edge_featurize_backward")
+    for name in ran:
         assert _lib.calls.get(name, 0) > before.get(name, 0), f"{name} did not run"
     params = dict(W=model.W.detach().cpu().double(), U=model.U.detach().cpu().double(),
                   atom_ref=model.atom_ref.detach().cpu().double(), l_max=kw["l_max"],

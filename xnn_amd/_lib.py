@@ -82,6 +82,13 @@ _SIGNATURES = {
                                   i32, i32, vp, vp, vp, vp],
     "xnn_sh_linear_message_sum_backward": [c_int, vp, vp, i64, vp, i64, vp, vp, vp, i64, vp, vp,
                                            i32, i32, i32, i32, vp, vp, vp, vp, vp, vp],
+    "xnn_sh_radial_message_sum": [c_int, vp, vp, i64, vp, i64, vp, vp, vp, i64, vp, vp,
+                                  ctypes.POINTER(FeaturizeParams), vp, i32, vp, vp, vp],
+    "xnn_sh_radial_message_sum_backward": [c_int, vp, vp, i64, vp, i64, vp, vp, vp, i64, vp, vp,
+                                           ctypes.POINTER(FeaturizeParams), vp, i32, vp, vp, vp,
+                                           vp],
+    "xnn_stress_finish": [c_int, vp, c_int, vp, vp, i64, dbl, vp, vp],
+    "xnn_virial_finish": [c_int, vp, vp, i64, i32, vp, vp],
     "xnn_d4_workspace_bytes": [i64, i64, i64],
     "xnn_d4_coordination": [vp, i64, vp, vp, vp, i64, i64, vp, vp, vp, vp,
                             ctypes.POINTER(D4CnParams), vp, vp, vp, sz, vp],

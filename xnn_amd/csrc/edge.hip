@@ -11,6 +11,7 @@
 
 #include "common.h"
 #include "device.h"
+#include "message.h"
 
 namespace xnn {
 
@@ -311,33 +312,46 @@ __global__ __launch_bounds__(256) void strain_bwd_kernel(
   }
 }
 
-// ---------------------------------------------------------------- dispatch helpers
+// out[b] = sym(M[b] + term[b]) (or unsymmetrized), float64 in, dtype out
 template <typename T>
-static int make_radial(const xnn_featurize_params* prm, const void* table, Radial<T>& R) {
-  XNN_REQUIRE(prm != nullptr, "featurize params are NULL");
-  XNN_REQUIRE(prm->n_rbf >= 0 && prm->n_rbf <= kMaxRbf, "n_rbf must be in [0, %d], got %d",
-              kMaxRbf, prm->n_rbf);
-  XNN_REQUIRE(prm->n_rbf == 0 || table != nullptr, "rbf_table is NULL");
-  XNN_REQUIRE(prm->basis == XNN_BASIS_BESSEL || prm->basis == XNN_BASIS_GAUSSIAN,
-              "unknown basis %d", prm->basis);
-  XNN_REQUIRE(prm->envelope >= XNN_ENV_POLYNOMIAL && prm->envelope <= XNN_ENV_NONE,
-              "unknown envelope %d", prm->envelope);
-  XNN_REQUIRE(prm->envelope != XNN_ENV_POLYNOMIAL || (prm->poly_p >= 1 && prm->poly_p <= 64),
-              "polynomial envelope degree must be in [1, 64], got %d", prm->poly_p);
-  XNN_REQUIRE(prm->cutoff > 0, "cutoff must be positive");
-  XNN_REQUIRE(prm->l_max >= 0 && prm->l_max <= 3, "l_max must be in [0, 3], got %d",
-              prm->l_max);
-  XNN_REQUIRE(prm->sh_sign == 1 || prm->sh_sign == -1, "sh_sign must be +1 or -1");
-  R.K = prm->n_rbf;
-  R.basis = prm->basis;
-  R.envelope = prm->envelope;
-  R.p = prm->poly_p;
-  R.rc = (T)prm->cutoff;
-  R.prefactor = (T)prm->rbf_prefactor;
-  R.gamma = (T)prm->gaussian_gamma;
-  R.table = static_cast<const T*>(table);
-  return XNN_OK;
+__global__ __launch_bounds__(256) void virial_finish_kernel(const double* __restrict__ M,
+                                                            const double* __restrict__ term,
+                                                            int64_t n_graphs, int symmetrize,
+                                                            T* __restrict__ out) {
+  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= 9 * n_graphs) return;
+  const int64_t b = t / 9;
+  const int j = (int)(t - 9 * b), r = j / 3, c = j % 3;
+  double v = M[t] + (term ? term[t] : 0.0);
+  if (symmetrize) {
+    const int64_t u = 9 * b + 3 * c + r;
+    v = 0.5 * (v + M[u] + (term ? term[u] : 0.0));
+  }
+  out[t] = (T)v;
 }
+
+// stress[b] = scale g[b] / V_b for periodic structures, V_b = |det cell_b| > 1e-8 and (with
+// pbc) some periodic direction; zero otherwise (outputs.py:227-239). float64 inside.
+template <typename T, typename C>
+__global__ __launch_bounds__(256) void stress_finish_kernel(const T* __restrict__ g,
+                                                            const C* __restrict__ cell,
+                                                            const uint8_t* __restrict__ pbc,
+                                                            int64_t n_graphs, double scale,
+                                                            T* __restrict__ out) {
+  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= 9 * n_graphs) return;
+  const int64_t b = t / 9;
+  const C* c = cell + 9 * b;
+  const double a0 = c[0], a1 = c[1], a2 = c[2], b0 = c[3], b1 = c[4], b2 = c[5], c0 = c[6],
+               c1 = c[7], c2 = c[8];
+  // row 0 . (row 1 x row 2)
+  const double v = fabs(a0 * (b1 * c2 - b2 * c1) + a1 * (b2 * c0 - b0 * c2) + a2 * (b0 * c1 - b1 * c0));
+  bool periodic = v > 1e-8;
+  if (pbc != nullptr) periodic = periodic && (pbc[3 * b] | pbc[3 * b + 1] | pbc[3 * b + 2]);
+  out[t] = periodic ? (T)(scale * (double)g[t] / v) : T(0);
+}
+
+// ---------------------------------------------------------------- dispatch helpers
 
 template <typename G, typename T>
 static int featurize_fwd(const void* vec_in, const void* pos, const void* cell, int64_t n_graphs,
@@ -548,6 +562,51 @@ int xnn_strain_apply_backward(int geom_dtype, const void* pos, int64_t n_nodes,
                        (double*)grad_pos, (double*)grad_cell, partial, cell_term);
   else {
     set_error("unsupported geometry dtype %d", geom_dtype);
+    return XNN_EINVAL;
+  }
+  XNN_LAUNCH_CHECK();
+  return XNN_OK;
+}
+
+int xnn_stress_finish(int dtype, const void* strain_grad, int cell_dtype, const void* cell,
+                      const uint8_t* pbc, int64_t n_graphs, double scale, void* stress,
+                      xnn_stream_t stream) {
+  XNN_REQUIRE(n_graphs >= 0, "negative size");
+  if (n_graphs == 0) return XNN_OK;
+  XNN_REQUIRE(strain_grad && cell && stress, "NULL input or output");
+  hipStream_t s = as_hip(stream);
+  const dim3 grid(grid_1d(9 * n_graphs, 256)), block(256);
+#define XNN_SF(T, C)                                                                     \
+  hipLaunchKernelGGL((stress_finish_kernel<T, C>), grid, block, 0, s, (const T*)strain_grad, \
+                     (const C*)cell, pbc, n_graphs, scale, (T*)stress)
+  if (dtype == XNN_F32 && cell_dtype == XNN_F32) XNN_SF(float, float);
+  else if (dtype == XNN_F32 && cell_dtype == XNN_F64) XNN_SF(float, double);
+  else if (dtype == XNN_F64 && cell_dtype == XNN_F32) XNN_SF(double, float);
+  else if (dtype == XNN_F64 && cell_dtype == XNN_F64) XNN_SF(double, double);
+  else {
+    set_error("unsupported dtypes %d / %d", dtype, cell_dtype);
+    return XNN_EINVAL;
+  }
+#undef XNN_SF
+  XNN_LAUNCH_CHECK();
+  return XNN_OK;
+}
+
+int xnn_virial_finish(int dtype, const double* M, const double* term, int64_t n_graphs,
+                      int32_t symmetrize, void* out, xnn_stream_t stream) {
+  XNN_REQUIRE(n_graphs >= 0, "negative size");
+  if (n_graphs == 0) return XNN_OK;
+  XNN_REQUIRE(M && out, "NULL input or output");
+  hipStream_t s = as_hip(stream);
+  const dim3 grid(grid_1d(9 * n_graphs, 256)), block(256);
+  if (dtype == XNN_F32)
+    hipLaunchKernelGGL(virial_finish_kernel<float>, grid, block, 0, s, M, term, n_graphs,
+                       (int)symmetrize, (float*)out);
+  else if (dtype == XNN_F64)
+    hipLaunchKernelGGL(virial_finish_kernel<double>, grid, block, 0, s, M, term, n_graphs,
+                       (int)symmetrize, (double*)out);
+  else {
+    set_error("unsupported dtype %d", dtype);
     return XNN_EINVAL;
   }
   XNN_LAUNCH_CHECK();

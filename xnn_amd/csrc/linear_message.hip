@@ -15,6 +15,13 @@
 //             (K = channels); dY goes through LDS to the edge's own lane for the SH
 //             Jacobian, as in the unfused kernels.
 // Channel tile t of width 16 holds channels 16-row index * T + t (C = 16 T).
+//
+// xnn_sh_radial_message_sum(_backward) go one step further: h is the enveloped radial
+// basis of the edge length, h_e = rbf(|r_e|) * envelope(|r_e|) (spherical.py:135-138), and
+// each lane evaluates it for its own edge next to the harmonics, into LDS. Featurizer,
+// linear layer and message are then one kernel each way; the backward folds
+// d|r_e| = sum_k d_h[e, k] d h_k / d|r| into the edge gradient, so neither h nor d_h
+// exists in memory.
 #include <algorithm>
 #include <cstdint>
 
@@ -26,21 +33,57 @@ namespace xnn {
 
 constexpr int kLinKMax = 8;  // h features: two k-steps of 4
 constexpr int kLinKK = 2;
+constexpr int kSH = 9;       // LDS row stride of per-edge radial features
 
-template <typename G, int LMAX, int T>
+// The lane's row of radial features h_k = rbf_k(r) envelope(r), k < kLinKMax (zeros past
+// R.K, and the whole row when the lane has no edge).
+__device__ __forceinline__ void radial_row(const Radial<float>& R, bool valid, float r,
+                                           float* __restrict__ row) {
+  if (valid) {
+    const RadialAt<float> a = radial_at(R, r);
+#pragma unroll 1
+    for (int k = 0; k < kLinKMax; ++k) {
+      float u = 0.f, du;
+      if (k < R.K) radial_k<float, false>(R, a, k, u, du);
+      row[k] = u;
+    }
+  } else {
+#pragma unroll
+    for (int k = 0; k < kLinKMax; ++k) row[k] = 0.f;
+  }
+}
+
+// d E / d r through the radial features of one edge: sum_k d_h[k] d h_k / d r
+__device__ __forceinline__ float radial_dot(const Radial<float>& R, float r,
+                                            const float* __restrict__ d_h) {
+  const RadialAt<float> a = radial_at(R, r);
+  float dl = 0.f;
+#pragma unroll 1
+  for (int k = 0; k < R.K; ++k) {
+    float u, du;
+    radial_k<float, true>(R, a, k, u, du);
+    dl += d_h[k] * du;
+  }
+  return dl;
+}
+
+template <typename G, int LMAX, int T, bool RAD>
 __global__ __launch_bounds__(256) void lin_msg_fwd_kernel(
     const float* __restrict__ vec, const G* __restrict__ pos, const G* __restrict__ cell,
     int64_t n_graphs, const int32_t* __restrict__ batch, const int32_t* __restrict__ src,
     const int32_t* __restrict__ shift, const int32_t* __restrict__ ptr,
     const int32_t* __restrict__ perm, int64_t n_nodes, float sign, int K,
-    const float* __restrict__ h, const float* __restrict__ W, float* __restrict__ out) {
+    const float* __restrict__ h, Radial<float> R, const float* __restrict__ W,
+    float* __restrict__ out) {
   constexpr int L = ShDims<LMAX>::L;
   constexpr int C = 16 * T;
   constexpr int KK = kLinKK;
   __shared__ float sY[kWavesPerBlock][kWave * kSY];
+  __shared__ float sH[kWavesPerBlock][RAD ? kWave * kSH : 1];
   const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
   const int lo = lane & 15, hi = lane >> 4;
   float* ys = sY[wave];
+  float* hs = sH[wave];
   // B operand of h W for channel tile t, k-step q: W[4 q + hi][lo T + t]
   float wB[KK][T];
 #pragma unroll
@@ -64,10 +107,10 @@ __global__ __launch_bounds__(256) void lin_msg_fwd_kernel(
     for (int base = b0; base < b1; base += kWave) {
       const int cnt = min(kWave, b1 - base);
       const int my_e = lane < cnt ? (perm ? perm[base + lane] : base + lane) : 0;
-      // A operand of h W for tile tau (edge 16 tau + hrow); the next tile's is in flight
-      // while a tile is computed
+      // A operand of h W for tile tau (edge 16 tau + hrow): from global memory with the
+      // next tile's in flight while a tile is computed, or evaluated into LDS (RAD)
       float ha[KK], hn[KK];
-      {
+      if constexpr (!RAD) {
         const int ej = __shfl(my_e, hrow);
 #pragma unroll
         for (int q = 0; q < KK; ++q) {
@@ -75,16 +118,20 @@ __global__ __launch_bounds__(256) void lin_msg_fwd_kernel(
           hn[q] = (hrow < cnt && k < K) ? h[(int64_t)ej * K + k] : 0.f;
         }
       }
-      float ux, uy, uz, inv;
+      float ux, uy, uz, inv, len;
       batch_harmonics<G, LMAX>(vec, pos, cl, src, shift, (int)row, sign, lane, cnt, my_e, ys, ux,
-                               uy, uz, inv);
+                               uy, uz, inv, len);
+      if constexpr (RAD) radial_row(R, lane < cnt, len, hs + lane * kSH);
       wave_sync();
       const int ntile = (cnt + 15) >> 4;
 #pragma unroll 1
       for (int tau = 0; tau < ntile; ++tau) {
+        if constexpr (RAD) {
 #pragma unroll
-        for (int q = 0; q < KK; ++q) ha[q] = hn[q];
-        {
+          for (int q = 0; q < KK; ++q) ha[q] = hs[(16 * tau + hrow) * kSH + 4 * q + hi];
+        } else {
+#pragma unroll
+          for (int q = 0; q < KK; ++q) ha[q] = hn[q];
           const int jn = 16 * (tau + 1) + hrow;
           const int ej = __shfl(my_e, jn & (kWave - 1));
 #pragma unroll
@@ -130,14 +177,14 @@ __global__ __launch_bounds__(256) void lin_msg_fwd_kernel(
   }
 }
 
-template <typename G, int LMAX, int T>
+template <typename G, int LMAX, int T, bool RAD>
 __global__ __launch_bounds__(256, 2) void lin_msg_bwd_kernel(
     const float* __restrict__ vec, const G* __restrict__ pos, const G* __restrict__ cell,
     int64_t n_graphs, const int32_t* __restrict__ batch, const int32_t* __restrict__ src,
     const int32_t* __restrict__ shift, const int32_t* __restrict__ ptr,
     const int32_t* __restrict__ perm, int64_t n_nodes, float sign, int K,
-    const float* __restrict__ h, const float* __restrict__ W, const float* __restrict__ d_out,
-    float* __restrict__ d_h, float* __restrict__ g_vec) {
+    const float* __restrict__ h, Radial<float> R, const float* __restrict__ W,
+    const float* __restrict__ d_out, float* __restrict__ d_h, float* __restrict__ g_vec) {
   constexpr int L = ShDims<LMAX>::L;
   constexpr int C = 16 * T;
   constexpr int KS = (L + 3) / 4;
@@ -148,18 +195,13 @@ __global__ __launch_bounds__(256, 2) void lin_msg_bwd_kernel(
   const int lo = lane & 15, hi = lane >> 4;
   float* ys = sbuf[wave];
   float* sdy = sbuf[wave] + kWave * kSY;
-  const bool want_vec = g_vec != nullptr;
-  // A operand of phi^T = W^T h^T: W[4 q + hi][lo T + t]
-  float wA[KK][T];
-#pragma unroll
-  for (int q = 0; q < KK; ++q)
-#pragma unroll
-    for (int t = 0; t < T; ++t) {
-      const int k = 4 * q + hi;
-      wA[q][t] = k < K ? W[k * C + lo * T + t] : 0.f;
-    }
-  // W in LDS, zero rows past K: the B operand of d_h = d_phi W^T for k-step (t, r) is
-  // W[lo][(4 hi + r) T + t], a run of T floats per r
+  // RAD: per-edge radial features, overwritten tile by tile with d_h once read
+  __shared__ float sH[kWavesPerBlock][RAD ? kWave * kSH : 1];
+  float* hs = sH[wave];
+  const bool want_vec = RAD || g_vec != nullptr;
+  // W in LDS, zero rows past K: the A operand of phi^T = W^T h^T for k-step q is
+  // W[4 q + hi][lo T + t] and the B operand of d_h = d_phi W^T for k-step (t, r) is
+  // W[lo][(4 hi + r) T + t], runs of T floats
   __shared__ __align__(16) float sW[16 * C];
   for (int i = threadIdx.x; i < 16 * C; i += blockDim.x) sW[i] = i < K * C ? W[i] : 0.f;
   __syncthreads();
@@ -195,10 +237,10 @@ __global__ __launch_bounds__(256, 2) void lin_msg_bwd_kernel(
     for (int base = b0; base < b1; base += kWave) {
       const int cnt = min(kWave, b1 - base);
       const int my_e = lane < cnt ? (perm ? perm[base + lane] : base + lane) : 0;
-      // B operand of phi^T for tile tau: h[edge 16 tau + lo][4 q + hi]; the next tile's
-      // is in flight while a tile is computed
+      // B operand of phi^T for tile tau: h[edge 16 tau + lo][4 q + hi]; from global memory
+      // with the next tile's in flight while a tile is computed, or from LDS (RAD)
       float hb[KK], hn[KK];
-      {
+      if constexpr (!RAD) {
         const int ej = __shfl(my_e, lo);
 #pragma unroll
         for (int q = 0; q < KK; ++q) {
@@ -206,17 +248,24 @@ __global__ __launch_bounds__(256, 2) void lin_msg_bwd_kernel(
           hn[q] = (want_vec && lo < cnt && k < K) ? h[(int64_t)ej * K + k] : 0.f;
         }
       }
-      float ux, uy, uz, inv;
+      float ux, uy, uz, inv, len;
       batch_harmonics<G, LMAX>(vec, pos, cl, src, shift, (int)row, sign, lane, cnt, my_e, ys, ux,
-                               uy, uz, inv);
+                               uy, uz, inv, len);
+      if constexpr (RAD) {
+        __builtin_amdgcn_sched_barrier(0);
+        radial_row(R, lane < cnt, len, hs + lane * kSH);
+      }
       wave_sync();
       const int ntile = (cnt + 15) >> 4;
 #pragma unroll 1
       for (int tau = 0; tau < ntile; ++tau) {
         const int je = 16 * tau + lo;
+        if constexpr (RAD) {
 #pragma unroll
-        for (int q = 0; q < KK; ++q) hb[q] = hn[q];
-        {
+          for (int q = 0; q < KK; ++q) hb[q] = hs[je * kSH + 4 * q + hi];
+        } else {
+#pragma unroll
+          for (int q = 0; q < KK; ++q) hb[q] = hn[q];
           const int jn = je + 16;
           const int ej = __shfl(my_e, jn & (kWave - 1));
 #pragma unroll
@@ -229,10 +278,13 @@ __global__ __launch_bounds__(256, 2) void lin_msg_bwd_kernel(
           // pt[t][r] = phi[edge je][channel (4 hi + r) T + t]
           floatx4 pt[T];
 #pragma unroll
-          for (int t = 0; t < T; ++t) {
-            pt[t] = floatx4{0.f, 0.f, 0.f, 0.f};
+          for (int t = 0; t < T; ++t) pt[t] = floatx4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-            for (int q = 0; q < KK; ++q) pt[t] = mfma_16x16x4(wA[q][t], hb[q], pt[t]);
+          for (int q = 0; q < KK; ++q) {
+            float wa[T];
+            load_run<T>(sW + (4 * q + hi) * C + lo * T, wa);
+#pragma unroll
+            for (int t = 0; t < T; ++t) pt[t] = mfma_16x16x4(wa[t], hb[q], pt[t]);
           }
           floatx4 dy = floatx4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -264,21 +316,40 @@ __global__ __launch_bounds__(256, 2) void lin_msg_bwd_kernel(
           for (int t = 0; t < T; ++t) dh = mfma_16x16x4(dp[t][r], wb[t], dh);
         }
         // dh[r] = d_h[edge 16 tau + 4 hi + r][k lo]
+        if constexpr (RAD) {
+          // into the rows of this tile, whose h was read above
+          wave_sync();
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int j = 16 * tau + 4 * hi + r;
-          const int ej = __shfl(my_e, j);
-          if (j < cnt && lo < K) d_h[(int64_t)ej * K + lo] = dh[r];
+          for (int r = 0; r < 4; ++r)
+            if (lo < kLinKMax) hs[(16 * tau + 4 * hi + r) * kSH + lo] = dh[r];
+        } else {
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int j = 16 * tau + 4 * hi + r;
+            const int ej = __shfl(my_e, j);
+            if (j < cnt && lo < K) d_h[(int64_t)ej * K + lo] = dh[r];
+          }
         }
       }
       wave_sync();
       if (want_vec && lane < cnt) {
+        // d|r| from the radial features first, then the harmonics' share (kept apart so
+        // that their temporaries are not live together)
+        float dl = 0.f;
+        if constexpr (RAD) dl = radial_dot(R, len, hs + lane * kSH);
+        __builtin_amdgcn_sched_barrier(0);
         float dY[L];
 #pragma unroll
         for (int m = 0; m < L; ++m) dY[m] = sdy[lane * kSY + m];
         float Gx, Gy, Gz, vx, vy, vz;
         sh_grad<LMAX, float>(ux, uy, uz, dY, Gx, Gy, Gz);
         sh_chain<float>(ux, uy, uz, inv, Gx, Gy, Gz, vx, vy, vz);
+        if constexpr (RAD) {
+          // + d|r| r / |r|, with r / |r| = sign (ux, uy, uz)
+          vx += dl * ux;
+          vy += dl * uy;
+          vz += dl * uz;
+        }
         g_vec[3 * (int64_t)my_e + 0] = sign * vx;
         g_vec[3 * (int64_t)my_e + 1] = sign * vy;
         g_vec[3 * (int64_t)my_e + 2] = sign * vz;
@@ -288,29 +359,30 @@ __global__ __launch_bounds__(256, 2) void lin_msg_bwd_kernel(
   }
 }
 
-template <typename G>
-static int lin_msg(bool backward, const float* vec, const void* pos, int64_t n_nodes,
-                   const void* cell, int64_t n_graphs, const int32_t* batch, const int32_t* src,
-                   const int32_t* shift, const int32_t* ptr, const int32_t* perm, int l_max,
-                   int sign, int K, int C, const float* h, const float* W, const float* d_out,
-                   float* out_or_dh, float* g_vec, hipStream_t stream) {
-  if (n_nodes == 0) return XNN_OK;
+template <typename G, bool RAD>
+static void lin_msg_launch(bool backward, const float* vec, const void* pos, int64_t n_nodes,
+                           const void* cell, int64_t n_graphs, const int32_t* batch,
+                           const int32_t* src, const int32_t* shift, const int32_t* ptr,
+                           const int32_t* perm, int l_max, int sign, int K, int C,
+                           const float* h, const Radial<float>& R, const float* W,
+                           const float* d_out, float* out_or_dh, float* g_vec,
+                           hipStream_t stream) {
   const int64_t blocks_needed = grid_1d(n_nodes, kWavesPerBlock);
   const dim3 block(kWavesPerBlock * kWave);
   const float sg = (float)sign;
 #define XNN_LIN(LM, TT)                                                                        \
   do {                                                                                         \
     if (backward) {                                                                            \
-      auto k = lin_msg_bwd_kernel<G, LM, TT>;                                                  \
+      auto k = lin_msg_bwd_kernel<G, LM, TT, RAD>;                                             \
       const dim3 grid((unsigned)resident_blocks((const void*)k, block.x, blocks_needed));      \
       hipLaunchKernelGGL(k, grid, block, 0, stream, vec, (const G*)pos, (const G*)cell,        \
-                         n_graphs, batch, src, shift, ptr, perm, n_nodes, sg, K, h, W, d_out,   \
-                         out_or_dh, g_vec);                                                    \
+                         n_graphs, batch, src, shift, ptr, perm, n_nodes, sg, K, h, R, W,       \
+                         d_out, out_or_dh, g_vec);                                             \
     } else {                                                                                   \
-      auto k = lin_msg_fwd_kernel<G, LM, TT>;                                                  \
+      auto k = lin_msg_fwd_kernel<G, LM, TT, RAD>;                                             \
       const dim3 grid((unsigned)resident_blocks((const void*)k, block.x, blocks_needed));      \
       hipLaunchKernelGGL(k, grid, block, 0, stream, vec, (const G*)pos, (const G*)cell,        \
-                         n_graphs, batch, src, shift, ptr, perm, n_nodes, sg, K, h, W,          \
+                         n_graphs, batch, src, shift, ptr, perm, n_nodes, sg, K, h, R, W,       \
                          out_or_dh);                                                           \
     }                                                                                          \
   } while (0)
@@ -327,6 +399,25 @@ static int lin_msg(bool backward, const float* vec, const void* pos, int64_t n_n
   }
 #undef XNN_LIN_L
 #undef XNN_LIN
+}
+
+// R == nullptr: h is given (E, K); else h is evaluated in the kernels from R (K = R->K)
+template <typename G>
+static int lin_msg(bool backward, const float* vec, const void* pos, int64_t n_nodes,
+                   const void* cell, int64_t n_graphs, const int32_t* batch, const int32_t* src,
+                   const int32_t* shift, const int32_t* ptr, const int32_t* perm, int l_max,
+                   int sign, int K, int C, const float* h, const Radial<float>* R,
+                   const float* W, const float* d_out, float* out_or_dh, float* g_vec,
+                   hipStream_t stream) {
+  if (n_nodes == 0) return XNN_OK;
+  if (R != nullptr)
+    lin_msg_launch<G, true>(backward, vec, pos, n_nodes, cell, n_graphs, batch, src, shift, ptr,
+                            perm, l_max, sign, R->K, C, nullptr, *R, W, d_out, out_or_dh, g_vec,
+                            stream);
+  else
+    lin_msg_launch<G, false>(backward, vec, pos, n_nodes, cell, n_graphs, batch, src, shift,
+                             ptr, perm, l_max, sign, K, C, h, Radial<float>{}, W, d_out,
+                             out_or_dh, g_vec, stream);
   XNN_LAUNCH_CHECK();
   return XNN_OK;
 }
@@ -363,12 +454,12 @@ int xnn_sh_linear_message_sum(int geom_dtype, const float* vec_in, const void* p
               "several cells need the batch vector");
   if (geom_dtype == XNN_F32)
     return lin_msg<float>(false, vec_in, pos, n_nodes, cell, n_graphs, batch, src, shift, ptr_dst,
-                          perm_dst, l_max, sh_sign, n_features, n_channels, h, W, nullptr, out,
-                          nullptr, as_hip(stream));
+                          perm_dst, l_max, sh_sign, n_features, n_channels, h, nullptr, W, nullptr,
+                          out, nullptr, as_hip(stream));
   if (geom_dtype == XNN_F64)
     return lin_msg<double>(false, vec_in, pos, n_nodes, cell, n_graphs, batch, src, shift,
-                           ptr_dst, perm_dst, l_max, sh_sign, n_features, n_channels, h, W,
-                           nullptr, out, nullptr, as_hip(stream));
+                           ptr_dst, perm_dst, l_max, sh_sign, n_features, n_channels, h, nullptr,
+                           W, nullptr, out, nullptr, as_hip(stream));
   set_error("unsupported geometry dtype %d", geom_dtype);
   return XNN_EINVAL;
 }
@@ -392,12 +483,72 @@ int xnn_sh_linear_message_sum_backward(int geom_dtype, const float* vec_in, cons
               "several cells need the batch vector");
   if (geom_dtype == XNN_F32)
     return lin_msg<float>(true, vec_in, pos, n_nodes, cell, n_graphs, batch, src, shift, ptr_dst,
-                          perm_dst, l_max, sh_sign, n_features, n_channels, h, W, d_out, d_h,
-                          g_vec, as_hip(stream));
+                          perm_dst, l_max, sh_sign, n_features, n_channels, h, nullptr, W, d_out,
+                          d_h, g_vec, as_hip(stream));
   if (geom_dtype == XNN_F64)
     return lin_msg<double>(true, vec_in, pos, n_nodes, cell, n_graphs, batch, src, shift,
-                           ptr_dst, perm_dst, l_max, sh_sign, n_features, n_channels, h, W,
-                           d_out, d_h, g_vec, as_hip(stream));
+                           ptr_dst, perm_dst, l_max, sh_sign, n_features, n_channels, h, nullptr,
+                           W, d_out, d_h, g_vec, as_hip(stream));
+  set_error("unsupported geometry dtype %d", geom_dtype);
+  return XNN_EINVAL;
+}
+
+int xnn_sh_radial_message_sum(int geom_dtype, const float* vec_in, const void* pos,
+                              int64_t n_nodes, const void* cell, int64_t n_graphs,
+                              const int32_t* batch, const int32_t* src, const int32_t* shift,
+                              int64_t n_edges, const int32_t* ptr_dst, const int32_t* perm_dst,
+                              const xnn_featurize_params* prm, const float* rbf_table,
+                              int32_t n_channels, const float* W, float* out,
+                              xnn_stream_t stream) {
+  Radial<float> R;
+  int st = make_radial<float>(prm, rbf_table, R);
+  if (st != XNN_OK) return st;
+  st = lin_check(n_nodes, n_edges, prm->l_max, prm->sh_sign, prm->n_rbf, n_channels);
+  if (st != XNN_OK) return st;
+  XNN_REQUIRE(n_nodes == 0 || (ptr_dst && out && W), "NULL CSR, weights or output");
+  XNN_REQUIRE(aligned16(out), "out must be 16-byte aligned");
+  XNN_REQUIRE(n_edges == 0 || vec_in || (pos && src && shift), "NULL edge input");
+  XNN_REQUIRE(cell == nullptr || n_graphs <= 1 || batch != nullptr,
+              "several cells need the batch vector");
+  if (geom_dtype == XNN_F32)
+    return lin_msg<float>(false, vec_in, pos, n_nodes, cell, n_graphs, batch, src, shift, ptr_dst,
+                          perm_dst, prm->l_max, prm->sh_sign, R.K, n_channels, nullptr, &R, W,
+                          nullptr, out, nullptr, as_hip(stream));
+  if (geom_dtype == XNN_F64)
+    return lin_msg<double>(false, vec_in, pos, n_nodes, cell, n_graphs, batch, src, shift,
+                           ptr_dst, perm_dst, prm->l_max, prm->sh_sign, R.K, n_channels, nullptr,
+                           &R, W, nullptr, out, nullptr, as_hip(stream));
+  set_error("unsupported geometry dtype %d", geom_dtype);
+  return XNN_EINVAL;
+}
+
+int xnn_sh_radial_message_sum_backward(int geom_dtype, const float* vec_in, const void* pos,
+                                       int64_t n_nodes, const void* cell, int64_t n_graphs,
+                                       const int32_t* batch, const int32_t* src,
+                                       const int32_t* shift, int64_t n_edges,
+                                       const int32_t* ptr_dst, const int32_t* perm_dst,
+                                       const xnn_featurize_params* prm, const float* rbf_table,
+                                       int32_t n_channels, const float* W, const float* d_out,
+                                       float* g_vec, xnn_stream_t stream) {
+  Radial<float> R;
+  int st = make_radial<float>(prm, rbf_table, R);
+  if (st != XNN_OK) return st;
+  st = lin_check(n_nodes, n_edges, prm->l_max, prm->sh_sign, prm->n_rbf, n_channels);
+  if (st != XNN_OK) return st;
+  XNN_REQUIRE(n_nodes == 0 || (ptr_dst && d_out && W), "NULL CSR, weights or d_out");
+  XNN_REQUIRE(aligned16(d_out), "d_out must be 16-byte aligned");
+  XNN_REQUIRE(n_edges == 0 || ((vec_in || (pos && src && shift)) && g_vec),
+              "NULL edge input or output");
+  XNN_REQUIRE(cell == nullptr || n_graphs <= 1 || batch != nullptr,
+              "several cells need the batch vector");
+  if (geom_dtype == XNN_F32)
+    return lin_msg<float>(true, vec_in, pos, n_nodes, cell, n_graphs, batch, src, shift, ptr_dst,
+                          perm_dst, prm->l_max, prm->sh_sign, R.K, n_channels, nullptr, &R, W,
+                          d_out, nullptr, g_vec, as_hip(stream));
+  if (geom_dtype == XNN_F64)
+    return lin_msg<double>(true, vec_in, pos, n_nodes, cell, n_graphs, batch, src, shift,
+                           ptr_dst, perm_dst, prm->l_max, prm->sh_sign, R.K, n_channels, nullptr,
+                           &R, W, d_out, nullptr, g_vec, as_hip(stream));
   set_error("unsupported geometry dtype %d", geom_dtype);
   return XNN_EINVAL;
 }

@@ -25,13 +25,42 @@ struct ShDims {
   static constexpr int LP = L == 1 ? 1 : (L <= 4 ? 4 : 16);
 };
 
-// Per-lane geometry of one edge: unit vector of sign * r_e and 1/|r_e|; the
+// host: the device form of the edge-embedding parameters (validated)
+template <typename T>
+inline int make_radial(const xnn_featurize_params* prm, const void* table, Radial<T>& R) {
+  XNN_REQUIRE(prm != nullptr, "featurize params are NULL");
+  XNN_REQUIRE(prm->n_rbf >= 0 && prm->n_rbf <= kMaxRbf, "n_rbf must be in [0, %d], got %d",
+              kMaxRbf, prm->n_rbf);
+  XNN_REQUIRE(prm->n_rbf == 0 || table != nullptr, "rbf_table is NULL");
+  XNN_REQUIRE(prm->basis == XNN_BASIS_BESSEL || prm->basis == XNN_BASIS_GAUSSIAN,
+              "unknown basis %d", prm->basis);
+  XNN_REQUIRE(prm->envelope >= XNN_ENV_POLYNOMIAL && prm->envelope <= XNN_ENV_NONE,
+              "unknown envelope %d", prm->envelope);
+  XNN_REQUIRE(prm->envelope != XNN_ENV_POLYNOMIAL || (prm->poly_p >= 1 && prm->poly_p <= 64),
+              "polynomial envelope degree must be in [1, 64], got %d", prm->poly_p);
+  XNN_REQUIRE(prm->cutoff > 0, "cutoff must be positive");
+  XNN_REQUIRE(prm->l_max >= 0 && prm->l_max <= 3, "l_max must be in [0, 3], got %d",
+              prm->l_max);
+  XNN_REQUIRE(prm->sh_sign == 1 || prm->sh_sign == -1, "sh_sign must be +1 or -1");
+  R.K = prm->n_rbf;
+  R.basis = prm->basis;
+  R.envelope = prm->envelope;
+  R.p = prm->poly_p;
+  R.rc = (T)prm->cutoff;
+  R.prefactor = (T)prm->rbf_prefactor;
+  R.gamma = (T)prm->gaussian_gamma;
+  R.table = static_cast<const T*>(table);
+  return XNN_OK;
+}
+
+// Per-lane geometry of one edge: unit vector of sign * r_e, 1/|r_e| and |r_e|; the
 // vector is given (vec) or formed from positions.
 template <typename G>
 __device__ inline void edge_unit(const float* __restrict__ vec, int64_t e,
                                  const G* __restrict__ pos, const G* __restrict__ cell,
                                  const int32_t* __restrict__ src, const int32_t* __restrict__ shift,
-                                 int d, float sign, float& ux, float& uy, float& uz, float& inv) {
+                                 int d, float sign, float& ux, float& uy, float& uz, float& inv,
+                                 float& r) {
   float x, y, z;
   if (vec != nullptr) {
     x = vec[3 * e + 0];
@@ -44,7 +73,7 @@ __device__ inline void edge_unit(const float* __restrict__ vec, int64_t e,
     y = (float)gy;
     z = (float)gz;
   }
-  const float r = sqrtf(x * x + y * y + z * z);
+  r = sqrtf(x * x + y * y + z * z);
   inv = r > 0.f ? 1.f / r : 0.f;
   ux = sign * x * inv;
   uy = sign * y * inv;
@@ -106,14 +135,14 @@ template <typename G, int LMAX>
 __device__ __forceinline__ void batch_harmonics(
     const float* __restrict__ vec, const G* __restrict__ pos, const G* __restrict__ cl,
     const int32_t* __restrict__ src, const int32_t* __restrict__ shift, int row, float sign,
-    int lane, int cnt, int e, float* ys, float& ux, float& uy, float& uz, float& inv) {
+    int lane, int cnt, int e, float* ys, float& ux, float& uy, float& uz, float& inv, float& r) {
   constexpr int L = ShDims<LMAX>::L;
   float Y[L];
   if (lane < cnt) {
-    edge_unit(vec, e, pos, cl, src, shift, row, sign, ux, uy, uz, inv);
+    edge_unit(vec, e, pos, cl, src, shift, row, sign, ux, uy, uz, inv, r);
     sh_eval<LMAX, float>(ux, uy, uz, Y);
   } else {
-    ux = uy = uz = inv = 0.f;
+    ux = uy = uz = inv = r = 0.f;
 #pragma unroll
     for (int m = 0; m < L; ++m) Y[m] = 0.f;
   }

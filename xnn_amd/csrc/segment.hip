@@ -83,8 +83,8 @@ __global__ __launch_bounds__(256) void sh_msg_fwd_kernel(
       if (lane < cnt) {
         const int k = base + lane;
         e = perm ? perm[k] : k;
-        float ux, uy, uz, inv;
-        edge_unit(vec, e, pos, cl, src, shift, (int)row, sign, ux, uy, uz, inv);
+        float ux, uy, uz, inv, len;
+        edge_unit(vec, e, pos, cl, src, shift, (int)row, sign, ux, uy, uz, inv, len);
         sh_eval<LMAX, float>(ux, uy, uz, Y);
       } else {
 #pragma unroll
@@ -240,13 +240,13 @@ __global__ __launch_bounds__(256) void sh_msg_bwd_kernel(
     const int b0 = ptr[row], b1 = ptr[row + 1];
     for (int base = b0; base < b1; base += kWave) {
       const int cnt = min(kWave, b1 - base);
-      float ux = 0.f, uy = 0.f, uz = 0.f, inv = 0.f;
+      float ux = 0.f, uy = 0.f, uz = 0.f, inv = 0.f, len = 0.f;
       int my_e = -1;
       float Y[L];
       if (lane < cnt) {
         const int k = base + lane;
         my_e = perm ? perm[k] : k;
-        edge_unit(vec, my_e, pos, cl, src, shift, (int)row, sign, ux, uy, uz, inv);
+        edge_unit(vec, my_e, pos, cl, src, shift, (int)row, sign, ux, uy, uz, inv, len);
         sh_eval<LMAX, float>(ux, uy, uz, Y);
       } else {
 #pragma unroll
@@ -389,9 +389,9 @@ __global__ __launch_bounds__(256) void sh_msg_fwd_mfma_kernel(
       float cur[KG][T], nxt[KG][T];
       // the first phi loads go out before the harmonics are evaluated
       fwd_phi_group<T, KG>(phi, 0, cnt, my_e, lo, hi, cur);
-      float ux, uy, uz, inv;
+      float ux, uy, uz, inv, len;
       batch_harmonics<G, LMAX>(vec, pos, cl, src, shift, (int)row, sign, lane, cnt, my_e, ys, ux,
-                               uy, uz, inv);
+                               uy, uz, inv, len);
       wave_sync();
       for (int k0 = 0; k0 < nk; k0 += KG) {
         if (k0 + KG < nk) fwd_phi_group<T, KG>(phi, k0 + KG, cnt, my_e, lo, hi, nxt);
@@ -497,9 +497,9 @@ __global__ __launch_bounds__(256) void sh_msg_bwd_mfma_kernel(
           for (int s = 0; s < Q; ++s) pc[s] = 0.f;
         }
       }
-      float ux, uy, uz, inv;
+      float ux, uy, uz, inv, len;
       batch_harmonics<G, LMAX>(vec, pos, cl, src, shift, (int)row, sign, lane, cnt, my_e, ys, ux,
-                               uy, uz, inv);
+                               uy, uz, inv, len);
       wave_sync();
       for (int tau = 0; tau < ntile; ++tau) {
         const int je = 16 * tau + lo;  // this lane's edge column within the batch
@@ -650,20 +650,75 @@ __global__ __launch_bounds__(BLOCK) void segment_reduce_f64_kernel(const T* __re
   }
 }
 
-// out[f] = sum over chunks k (in order) of partial[k, f]
-__global__ void segment_finish_kernel(const double* __restrict__ partial, int chunks, int64_t F,
-                                      double* __restrict__ out) {
-  for (int64_t f = threadIdx.x; f < F; f += blockDim.x) {
+// out[f] = sum over chunks k of partial[k, f]: one wave per feature, lane l sums chunks
+// l, l + 64, ... in order, then a fixed butterfly (deterministic)
+__global__ __launch_bounds__(256) void segment_finish_kernel(const double* __restrict__ partial,
+                                                             int chunks, int64_t F,
+                                                             double* __restrict__ out) {
+  const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+  for (int64_t f = wave; f < F; f += blockDim.x / kWave) {
     double t = 0.0;
-    for (int k = 0; k < chunks; ++k) t += partial[(int64_t)k * F + f];
-    out[f] = t;
+    for (int k = lane; k < chunks; k += kWave) t += partial[(int64_t)k * F + f];
+#pragma unroll
+    for (int m = kWave / 2; m > 0; m >>= 1) t += __shfl_xor(t, m, kWave);
+    if (lane == 0) out[f] = t;
   }
+}
+
+// One segment of rows with F <= kFlatMaxF features, read as a flat array: thread t of a
+// block (t < S = F P, P the largest power of two with F P <= 256) adds elements
+// t, t + S, ... of the block's chunk, all of feature t % F (chunks start at multiples
+// of S), with coalesced loads; an LDS tree over the P threads of each feature then
+// gives the chunk's partial sums (fixed order: deterministic).
+constexpr int kFlatMaxF = 64;
+constexpr int kFlatPerThread = 4;
+
+static int flat_stride(int64_t F) {
+  int64_t S = F;
+  while (2 * S <= 256) S *= 2;
+  return (int)S;
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void flat_reduce_f64_kernel(const T* __restrict__ src,
+                                                              int64_t F, int S,
+                                                              const int64_t* __restrict__ seg,
+                                                              int chunks,
+                                                              double* __restrict__ partial) {
+  __shared__ double red[256];
+  const int t = threadIdx.x;
+  const int64_t e0 = seg[0] * F, e1 = seg[1] * F;
+  // chunk length: a multiple of S covering the segment in `chunks` pieces
+  const int64_t per_s = ((e1 - e0 + chunks - 1) / chunks + S - 1) / S;
+  const int64_t c0 = min(e1, e0 + (int64_t)blockIdx.x * per_s * S);
+  const int64_t c1 = min(e1, c0 + per_s * S);
+  double acc = 0.0;
+  if (t < S)
+    for (int64_t i = c0 + t; i < c1; i += S) acc += (double)src[i];
+  red[t] = acc;
+  __syncthreads();
+  for (int h = S / (int)F / 2; h > 0; h >>= 1) {
+    if (t < h * F) red[t] += red[t + h * F];
+    __syncthreads();
+  }
+  if (t < F) partial[(int64_t)blockIdx.x * F + t] = red[t];
 }
 
 constexpr int64_t kChunkRows = 2048;
 constexpr int kMaxChunks = 256;
 
-static int reduce_chunks(int64_t n_rows, int64_t n_segments) {
+// single segments of few features take the flat kernel
+static bool reduce_flat(int64_t n_rows, int64_t n_features, int64_t n_segments) {
+  return n_segments == 1 && n_features <= kFlatMaxF &&
+         n_rows * n_features >= 2 * (int64_t)flat_stride(n_features) * kFlatPerThread;
+}
+
+static int reduce_chunks(int64_t n_rows, int64_t n_features, int64_t n_segments) {
+  if (reduce_flat(n_rows, n_features, n_segments)) {
+    const int64_t per_chunk = (int64_t)flat_stride(n_features) * kFlatPerThread;
+    const int64_t c = (n_rows * n_features + per_chunk - 1) / per_chunk;
+    return (int)(c < kMaxChunks ? c : kMaxChunks);
+  }
   if (n_segments != 1 || n_rows < 2 * kChunkRows) return 1;
   const int64_t c = (n_rows + kChunkRows - 1) / kChunkRows;
   return (int)(c < kMaxChunks ? c : kMaxChunks);
@@ -930,7 +985,7 @@ int xnn_gather_rows(int dtype, const void* src, int64_t n_src_rows, int64_t n_fe
 
 size_t xnn_segment_reduce_workspace_bytes(int64_t n_rows, int64_t n_features,
                                           int64_t n_segments) {
-  const int chunks = reduce_chunks(n_rows, n_segments);
+  const int chunks = reduce_chunks(n_rows, n_features, n_segments);
   return chunks > 1 ? sizeof(double) * (size_t)chunks * (size_t)n_features : 0;
 }
 
@@ -941,12 +996,26 @@ int xnn_segment_reduce_f64(int dtype, const void* src, int64_t n_rows, int64_t n
   if (n_segments == 0 || n_features == 0) return XNN_OK;
   XNN_REQUIRE(seg_ptr && out && (n_rows == 0 || src), "NULL pointer");
   XNN_REQUIRE(dtype == XNN_F32 || dtype == XNN_F64, "unsupported dtype %d", dtype);
-  const int chunks = reduce_chunks(n_rows, n_segments);
+  const int chunks = reduce_chunks(n_rows, n_features, n_segments);
   const size_t need = xnn_segment_reduce_workspace_bytes(n_rows, n_features, n_segments);
   XNN_REQUIRE(need == 0 || (workspace != nullptr && workspace_bytes >= need),
               "workspace of %zu bytes needed", need);
   hipStream_t s = as_hip(stream);
   double* dest = chunks > 1 ? static_cast<double*>(workspace) : out;
+  if (reduce_flat(n_rows, n_features, n_segments)) {
+    const int S = flat_stride(n_features);
+    if (dtype == XNN_F32)
+      hipLaunchKernelGGL(flat_reduce_f64_kernel<float>, dim3(chunks), dim3(256), 0, s,
+                         (const float*)src, n_features, S, seg_ptr, chunks, dest);
+    else
+      hipLaunchKernelGGL(flat_reduce_f64_kernel<double>, dim3(chunks), dim3(256), 0, s,
+                         (const double*)src, n_features, S, seg_ptr, chunks, dest);
+    XNN_LAUNCH_CHECK();
+    hipLaunchKernelGGL(segment_finish_kernel, dim3(1), dim3(256), 0, s, dest, chunks, n_features,
+                       out);
+    XNN_LAUNCH_CHECK();
+    return XNN_OK;
+  }
   const int64_t grid = chunks > 1 ? chunks : n_segments;
   // long segments get 1024 threads, short ones (many small structures) a wave
   const bool wide = chunks > 1 || n_rows >= 1024 * n_segments;
@@ -961,7 +1030,7 @@ int xnn_segment_reduce_f64(int dtype, const void* src, int64_t n_rows, int64_t n
 #undef XNN_RED
   XNN_LAUNCH_CHECK();
   if (chunks > 1) {
-    hipLaunchKernelGGL(segment_finish_kernel, dim3(1), dim3(64), 0, s, dest, chunks, n_features,
+    hipLaunchKernelGGL(segment_finish_kernel, dim3(1), dim3(256), 0, s, dest, chunks, n_features,
                        out);
     XNN_LAUNCH_CHECK();
   }

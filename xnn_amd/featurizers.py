@@ -162,11 +162,29 @@ class SphericalHarmonicEdgeEmbedding(nn.Module, FastPathModule):
     def _embed_fast(self, vec: Tensor, sh_sign: int, want_sh: bool = True):
         from .ops import edge_embed
         rbf = self.rbf
+        # without harmonics, neither l_max nor the lengths are needed
         return edge_embed(
             vec, self._table(), n_rbf=self.n_rbf, basis=self.radial_type,
-            envelope=self.envelope_type, poly_p=getattr(self.envelope, "p", 1), l_max=self.l_max,
-            cutoff=self.cutoff, prefactor=getattr(rbf, "norm", 1.0),
-            gamma=getattr(rbf, "gamma", 1.0), sh_sign=sh_sign, want_sh=want_sh)
+            envelope=self.envelope_type, poly_p=getattr(self.envelope, "p", 1),
+            l_max=self.l_max if want_sh else 0, cutoff=self.cutoff,
+            prefactor=getattr(rbf, "norm", 1.0), gamma=getattr(rbf, "gamma", 1.0),
+            sh_sign=sh_sign, want_length=want_sh, want_sh=want_sh)
+
+    @property
+    def radial_trainable(self) -> bool:
+        return bool(self._table().requires_grad)
+
+    def radial_message_sum(self, vec: Tensor, W: Tensor, plan, sh_sign: int = 1) -> Tensor:
+        """``A_i = sum_{dst(e)=i} (radial(vec_e) W) (x) Y(sh_sign vec_e)``, ``(N, C, L)``,
+        with this embedding's radial basis evaluated inside the HIP message kernels
+        (float32, on a GPU; differentiable in ``vec`` only: forces and stress)."""
+        from .ops import sh_radial_message_sum
+        rbf = self.rbf
+        return sh_radial_message_sum(
+            vec, self._table(), W, plan, basis=self.radial_type, envelope=self.envelope_type,
+            poly_p=getattr(self.envelope, "p", 1), l_max=self.l_max, cutoff=self.cutoff,
+            prefactor=getattr(rbf, "norm", 1.0), gamma=getattr(rbf, "gamma", 1.0),
+            sh_sign=sh_sign)
 
     def embed(self, vec: Tensor, sh_sign: int = 1) -> Tuple[Tensor, Tensor, Tensor]:
         """``(edge_length (E,), edge_sh (E, (l_max+1)^2), edge_radial (E, n_rbf))``

@@ -91,7 +91,9 @@ class ShEdgePotential(InteratomicPotential):
     float64. On a GPU the featurizer and the fused message sum are HIP kernels (the
     message never exists in memory); with ``fused_linear`` (the default, for the channel
     counts the fused kernels take) the radial linear layer runs inside the message
-    kernels too, so ``phi`` is never stored either. ``use_fast=False`` or a CPU evaluates
+    kernels too, so ``phi`` is never stored either, and with ``fused_radial`` (the
+    default) forces and stress evaluate the radial basis inside those kernels as well
+    (one kernel each way; parameter gradients take the two-kernel path). ``use_fast=False`` or a CPU evaluates
     the same function with the PyTorch formulation.
     """
 
@@ -100,13 +102,15 @@ class ShEdgePotential(InteratomicPotential):
     def __init__(self, species: Sequence[int] = (1, 6, 7, 8), n_rbf: int = 8, l_max: int = 3,
                  channels: int = 128, cutoff: float = 5.0, radial_type: str = "bessel",
                  envelope: str = "polynomial", p: int = 6, sh_sign: int = 1,
-                 use_fast: UseFast = "auto", seed: Optional[int] = 0, fused_linear: bool = True):
+                 use_fast: UseFast = "auto", seed: Optional[int] = 0, fused_linear: bool = True,
+                 fused_radial: bool = True):
         super().__init__()
         self.cutoff = float(cutoff)
         self.l_max = int(l_max)
         self.channels = int(channels)
         self.sh_sign = int(sh_sign)
         self.fused_linear = bool(fused_linear)
+        self.fused_radial = bool(fused_radial)
         self.use_fast = resolve_use_fast(use_fast)
         self.double_backward = False
         # False while ForceStressOutput evaluates forces only (no parameter gradients)
@@ -127,14 +131,19 @@ class ShEdgePotential(InteratomicPotential):
         feat = self.edge_feat
         if feat.fast_active:
             from .ops import linear_message_supported, sh_linear_message_sum, sh_message_sum
-            u = feat.radial(vec)
-            W = self.W.to(u.dtype)
+            W = self.W.to(vec.dtype)
             if not self.param_grads:
                 W = W.detach()
             if self.fused_linear and linear_message_supported(W.shape[0], W.shape[1], self.l_max):
+                if self.fused_radial and not W.requires_grad and not feat.radial_trainable:
+                    # forces and stress only: radial basis, linear layer and message in one
+                    # kernel each way (neither u nor phi is stored)
+                    return feat.radial_message_sum(vec, W, data.plan(), self.sh_sign)
                 # the radial linear layer runs inside the message kernels: phi = u W is
                 # formed per edge tile in registers, never stored
+                u = feat.radial(vec)
                 return sh_linear_message_sum(vec, u, W, data.plan(), self.l_max, self.sh_sign)
+            u = feat.radial(vec)
             return sh_message_sum(vec, u @ W, data.plan(), self.l_max, self.sh_sign)
         _, sh, u = feat.embed(vec, sh_sign=self.sh_sign)
         phi = u @ self.W.to(u.dtype)

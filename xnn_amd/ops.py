@@ -19,6 +19,12 @@ op                     replaces
                        weights (gnn/fast/conv.py:137-143) + ``scatter_sum``
 ``sh_linear_message_   the same with the edge weights formed in the kernel by the last
 sum``                  linear layer of the weight network (``h @ W``)
+``sh_radial_message_   the same with ``h`` the enveloped radial basis of the edge length,
+sum``                  evaluated in the kernel (spherical.py:135-138): featurizer,
+                       linear layer and message in one launch each way
+``strain_apply``,      the strain deformation, strain gradient and stress of
+``virial_finish``,     ``ForceStressOutput`` (common/models/outputs.py:166-239)
+``stress_finish``
 ``segment_sum``        ``scatter_sum`` (common/models/ops.py:403-448)
 ``gather_rows``        ``gather_rows`` (common/models/ops.py:494-528)
 ``structure_sum``      ``structure_sum`` (common/models/ops.py:531-557), float64 totals
@@ -177,6 +183,39 @@ def _force_reduce_backward(ctx, d_pos, d_cell):
 force_reduce_op.register_autograd(_force_reduce_backward, setup_context=_force_reduce_setup)
 
 
+def virial_finish(M: Tensor, term: Optional[Tensor], dtype: torch.dtype) -> Tensor:
+    """``sym(M + term)`` per structure, (B, 3, 3) in ``dtype``, from float64 (B, 9) sums."""
+    n_graphs = M.shape[0]
+    out = torch.empty((n_graphs, 3, 3), dtype=dtype, device=M.device)
+    _lib.call("xnn_virial_finish", _lib.dtype_code(dtype), _lib.ptr(M), _lib.ptr(term), n_graphs,
+              1, _lib.ptr(out), _lib.stream(M.device))
+    return out
+
+
+def stress_finish(strain_gradient: Tensor, cell: Tensor, pbc: Optional[Tensor],
+                  scale: float = 1.0) -> Tensor:
+    """``scale * strain_gradient / V`` for periodic structures, zero for molecules
+    (outputs.py:227-239), one kernel; not differentiable (forces and stress only)."""
+    g = strain_gradient.contiguous()
+    c = cell.reshape(-1, 3, 3)
+    if c.dtype not in (torch.float32, torch.float64):
+        c = c.to(g.dtype)
+    c = c.contiguous()
+    flags = None
+    if pbc is not None:
+        if pbc.is_cuda:
+            flags = pbc.reshape(-1, 3).to(torch.bool).contiguous().view(torch.uint8)
+        elif not bool(pbc.reshape(-1, 3).any(-1).all()):
+            # some structure is non-periodic in every direction (host check: pbc is on
+            # the CPU, so this is no device sync)
+            flags = pbc.reshape(-1, 3).to(device=g.device, dtype=torch.uint8)
+    out = torch.empty_like(g)
+    _lib.call("xnn_stress_finish", _lib.dtype_code(g.dtype), _lib.ptr(g), _lib.dtype_code(c.dtype),
+              _lib.ptr(c), _lib.ptr(flags), g.shape[0], float(scale), _lib.ptr(out),
+              _lib.stream(g.device))
+    return out
+
+
 # --------------------------------------------------------------------------- strain probe
 @torch.library.custom_op(f"{_NS}::edge_vectors_strain_probe", mutates_args=())
 def edge_vectors_strain_probe_op(pos: Tensor, strain_probe: Tensor, cell: Optional[Tensor],
@@ -230,8 +269,7 @@ def _probe_backward(ctx, grad):
               _lib.ptr(cell_partial), _lib.ptr(vec), _lib.ptr(virial_partial), _lib.stream(dev))
     M = torch.empty((n_graphs, 9), dtype=torch.float64, device=dev)
     _lib.segment_reduce_f64(virial_partial, n_nodes, 9, node_ptr, n_graphs, M)
-    M = M.view(n_graphs, 3, 3)
-    grad_probe = (0.5 * (M + M.transpose(1, 2))).to(ctx.probe_dtype)
+    grad_probe = virial_finish(M, None, ctx.probe_dtype)
     grad_cell = None
     if want_cell:
         gc = torch.empty((n_graphs, 9), dtype=torch.float64, device=dev)
@@ -317,10 +355,7 @@ def _strain_backward(ctx, g_pos, g_cell):
               _lib.stream(dev))
     M = torch.empty((n_graphs, 9), dtype=torch.float64, device=dev)
     _lib.segment_reduce_f64(partial, n, 9, node_ptr, n_graphs, M)
-    if term is not None:
-        M = M + term
-    M = M.view(n_graphs, 3, 3)
-    grad_strain = (0.5 * (M + M.transpose(1, 2))).to(strain.dtype)
+    grad_strain = virial_finish(M, term, strain.dtype)
     return grad_pos, grad_cell, grad_strain, None, None
 
 
@@ -544,6 +579,76 @@ def sh_linear_message_sum(vec: Tensor, h: Tensor, W: Tensor, plan: EdgePlan, l_m
                          f"most {LINEAR_MESSAGE_MAX_FEATURES} features and l_max in [1, 3]")
     return sh_linear_message_sum_op(vec.contiguous(), h.contiguous(), W.contiguous(),
                                     plan.ptr_dst, plan.perm_dst, int(l_max), int(sh_sign))
+
+
+@torch.library.custom_op(f"{_NS}::sh_radial_message_sum", mutates_args=())
+def sh_radial_message_sum_op(vec: Tensor, rbf_table: Tensor, W: Tensor, ptr_dst: Tensor,
+                             perm_dst: Optional[Tensor], iparams: List[int],
+                             fparams: List[float]) -> Tensor:
+    """``A[i, c, lm] = sum_{dst(e)=i} (h_e W)[c] Y_lm(sign vec_e)`` with
+    ``h_e = rbf(|vec_e|) envelope(|vec_e|)`` evaluated in the kernel (float32): the
+    featurizer's radial part, the linear layer and the message in one launch."""
+    dev = _require_gpu(vec, W)
+    n_nodes = ptr_dst.shape[0] - 1
+    C = W.shape[1]
+    L = (iparams[4] + 1) ** 2
+    out = torch.empty((n_nodes, C, L), dtype=torch.float32, device=dev)
+    _lib.call("xnn_sh_radial_message_sum", _lib.XNN_F32, _lib.ptr(vec), None, n_nodes, None, 0,
+              None, None, None, vec.shape[0], _lib.ptr(ptr_dst), _lib.ptr(perm_dst),
+              _params(iparams, fparams), _lib.ptr(rbf_table), C, _lib.ptr(W), _lib.ptr(out),
+              _lib.stream(dev))
+    return out
+
+
+@sh_radial_message_sum_op.register_fake
+def _(vec, rbf_table, W, ptr_dst, perm_dst, iparams, fparams):
+    return vec.new_empty((ptr_dst.shape[0] - 1, W.shape[1], (iparams[4] + 1) ** 2))
+
+
+def _rad_msg_setup(ctx, inputs, output):
+    vec, rbf_table, W, ptr_dst, perm_dst, iparams, fparams = inputs
+    ctx.save_for_backward(vec, rbf_table, W, ptr_dst, perm_dst)
+    ctx.iparams, ctx.fparams = list(iparams), list(fparams)
+
+
+def _rad_msg_backward(ctx, d_out):
+    _once_differentiable()
+    if ctx.needs_input_grad[1] or ctx.needs_input_grad[2]:
+        raise NotImplementedError("sh_radial_message_sum differentiates the edge vectors only; "
+                                  "train W with edge_embed + sh_linear_message_sum")
+    vec, rbf_table, W, ptr_dst, perm_dst = ctx.saved_tensors
+    d_out = d_out.contiguous()
+    g_vec = torch.empty_like(vec)
+    _lib.call("xnn_sh_radial_message_sum_backward", _lib.XNN_F32, _lib.ptr(vec), None,
+              ptr_dst.shape[0] - 1, None, 0, None, None, None, vec.shape[0], _lib.ptr(ptr_dst),
+              _lib.ptr(perm_dst), _params(ctx.iparams, ctx.fparams), _lib.ptr(rbf_table),
+              W.shape[1], _lib.ptr(W), _lib.ptr(d_out), _lib.ptr(g_vec), _lib.stream(vec.device))
+    return g_vec, None, None, None, None, None, None
+
+
+sh_radial_message_sum_op.register_autograd(_rad_msg_backward, setup_context=_rad_msg_setup)
+
+
+def sh_radial_message_sum(vec: Tensor, rbf_table: Tensor, W: Tensor, plan: EdgePlan, *,
+                          basis: str, envelope: str, poly_p: int, l_max: int, cutoff: float,
+                          prefactor: float = 1.0, gamma: float = 1.0,
+                          sh_sign: int = 1) -> Tensor:
+    """``sh_linear_message_sum(vec, radial(vec), W, ...)`` with the radial basis (``W.shape[0]``
+    functions) evaluated inside the kernels; differentiable in ``vec`` only."""
+    if vec.dtype != torch.float32 or W.dtype != torch.float32:
+        raise TypeError("sh_radial_message_sum computes in float32")
+    n_rbf = W.shape[0]
+    if rbf_table.numel() != n_rbf:
+        raise ValueError("W needs one row per radial basis function")
+    if not linear_message_supported(n_rbf, W.shape[1], l_max):
+        raise ValueError(f"sh_radial_message_sum takes {LINEAR_MESSAGE_CHANNELS} channels, at "
+                         f"most {LINEAR_MESSAGE_MAX_FEATURES} basis functions and l_max in [1, 3]")
+    iparams = [int(n_rbf), _lib.BASIS[basis], _lib.ENVELOPE[envelope], int(poly_p), int(l_max),
+               int(sh_sign)]
+    fparams = [float(cutoff), float(prefactor), float(gamma)]
+    table = rbf_table.to(device=vec.device, dtype=torch.float32).contiguous()
+    return sh_radial_message_sum_op(vec.contiguous(), table, W.contiguous(), plan.ptr_dst,
+                                    plan.perm_dst, iparams, fparams)
 
 
 # --------------------------------------------------------------------------- segment sums

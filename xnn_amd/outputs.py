@@ -93,15 +93,18 @@ class ForceStressOutput(nn.Module):
             need.append("strain")
         g = {k: None for k in need}
         if inputs and energy.requires_grad:
-            grads = torch.autograd.grad([energy], inputs, grad_outputs=[torch.ones_like(energy)],
+            # the backward is seeded with -1: it returns d(-E), so the forces need no extra
+            # negation (negation is exact, the result is bitwise -dE/dpos)
+            grads = torch.autograd.grad([energy], inputs,
+                                        grad_outputs=[torch.full_like(energy, -1.0)],
                                         create_graph=create_graph, retain_graph=create_graph,
                                         allow_unused=True)
             g = dict(zip(need, grads))
         if self.compute_forces:
-            out["forces"] = -g["pos"] if g.get("pos") is not None else torch.zeros_like(data.pos)
+            out["forces"] = g["pos"] if g.get("pos") is not None else torch.zeros_like(data.pos)
         if strain is not None:
-            out["stress"] = (_stress(g["strain"], data) if g.get("strain") is not None
-                             else torch.zeros_like(strain))
+            out["stress"] = (_stress(g["strain"], data, scale=-1.0, differentiable=create_graph)
+                             if g.get("strain") is not None else torch.zeros_like(strain))
         return out
 
 
@@ -116,12 +119,18 @@ def _layout(data):
     return data.batch.to(torch.int32).contiguous(), node_ptr
 
 
-def _stress(strain_gradient: Tensor, data) -> Tensor:
-    """``dE/d(strain) / V`` per structure, zero for molecules of a batch (outputs.py:227-239)."""
+def _stress(strain_gradient: Tensor, data, scale: float = 1.0,
+            differentiable: bool = False) -> Tensor:
+    """``scale * strain_gradient / V`` per structure, zero for molecules of a batch
+    (outputs.py:227-239); ``scale = -1`` when the gradient is that of ``-E``. On a GPU
+    outside training this is one HIP kernel."""
+    if strain_gradient.is_cuda and data.cell.is_cuda and not differentiable:
+        from .ops import stress_finish
+        return stress_finish(strain_gradient, data.cell, data.pbc, scale)
     volume = cell_volume(data.cell)
     periodic = volume > 1e-8
     if data.pbc is not None:
         periodic = periodic & data.pbc.any(-1).to(periodic.device)
     safe = torch.where(periodic, volume, torch.ones_like(volume))
-    return torch.where(periodic[:, None, None], strain_gradient / safe[:, None, None],
+    return torch.where(periodic[:, None, None], (scale * strain_gradient) / safe[:, None, None],
                        torch.zeros_like(strain_gradient))
