@@ -220,6 +220,17 @@ int xnn_sh_radial_message_sum_backward(int geom_dtype, const float* vec_in, cons
 int xnn_virial_finish(int dtype, const double* M, const double* term, int64_t n_graphs,
                       int32_t symmetrize, void* out, xnn_stream_t stream);
 
+/* Per-structure virial from per-atom partials in one call: out[b] = sym(sum_{i in seg b}
+ * partial[i] + term[b]) (symmetrize != 0) or without sym, cast to dtype (B,3,3).
+ * partial (n_rows,3,3) float64 (xnn_edge_force_reduce's cell_partial / virial_partial, or
+ * xnn_strain_apply_backward's partial), seg_ptr (B+1) int64, term (B,3,3) float64 nullable.
+ * The same sums as xnn_segment_reduce_f64 followed by xnn_virial_finish (deterministic),
+ * in two launches. Workspace: xnn_virial_reduce_workspace_bytes (never 0). */
+size_t xnn_virial_reduce_workspace_bytes(int64_t n_rows, int64_t n_graphs);
+int xnn_virial_reduce(int dtype, const double* partial, int64_t n_rows, const int64_t* seg_ptr,
+                      int64_t n_graphs, const double* term, int32_t symmetrize, void* out,
+                      void* workspace, size_t workspace_bytes, xnn_stream_t stream);
+
 /* The stress of ForceStressOutput from the strain gradient (outputs.py:227-239):
  * stress[b] = scale * strain_grad[b] / |det cell_b| for periodic structures
  * (|det| > 1e-8 and, when pbc (B,3) bool/uint8 is given, some periodic direction),

@@ -301,6 +301,7 @@ def test_sh_linear_message_sum_forward_backward(C, l_max, K):
 @pytest.mark.parametrize("C,l_max,K,radial,envelope,sign",
                          [(128, 3, 8, "bessel", "polynomial", 1),
                           (64, 2, 8, "bessel", "cosine", -1),
+                          (128, 3, 8, "bessel_detuned", "polynomial", 1),
                           (32, 1, 6, "gaussian", "polynomial", 1),
                           (128, 3, 4, "gaussian", "cosine", 1)])
 def test_sh_radial_message_sum_forward_backward(C, l_max, K, radial, envelope, sign):
@@ -318,8 +319,15 @@ def test_sh_radial_message_sum_forward_backward(C, l_max, K, radial, envelope, s
     g = xa.structure_to_graph(s.as_dict(), 5.0, device=DEV)
     g.pos = g.pos.float()
     vec = g.edge_vectors().detach().requires_grad_(True)
-    emb = SphericalHarmonicEdgeEmbedding(l_max=l_max, n_rbf=K, cutoff=5.0, radial_type=radial,
+    emb = SphericalHarmonicEdgeEmbedding(l_max=l_max, n_rbf=K, cutoff=5.0,
+                                         radial_type=radial.split("_")[0],
                                          envelope=envelope).to(DEV)
+    freqs = None
+    if radial == "bessel_detuned":
+        # frequencies off the n pi progression: the kernels evaluate one sincos per
+        # function instead of the harmonic recurrence
+        freqs = emb.rbf.freqs * (1.0 + 0.01 * torch.arange(K, device=DEV))
+        emb.rbf.freqs.copy_(freqs)
     emb.fast_active = True
     gen = torch.Generator().manual_seed(7 * C + K)
     W = (torch.randn(K, C, generator=gen) / K ** 0.5).to(DEV)
@@ -329,7 +337,14 @@ def test_sh_radial_message_sum_forward_backward(C, l_max, K, radial, envelope, s
     # oracle, float64
     vc = vec.detach().cpu().double().requires_grad_(True)
     Y = R.e3nn_sh(l_max, vc if sign == 1 else -vc)
-    phi = R.radial_features(torch.linalg.norm(vc, dim=-1), K, 5.0, radial, envelope) @ W.cpu().double()
+    length = torch.linalg.norm(vc, dim=-1)
+    if freqs is None:
+        rad = R.radial_features(length, K, 5.0, radial, envelope)
+    else:
+        env = (R.polynomial_envelope(length, 5.0, 6) if envelope == "polynomial"
+               else R.cosine_envelope(length, 5.0))
+        rad = R.bessel(length, K, 5.0, freqs=freqs.cpu().double()) * env[:, None]
+    phi = rad @ W.cpu().double()
     msg = (phi[:, :, None] * Y[:, None, :]).reshape(vc.shape[0], -1)
     Ar = R.scatter_sum(msg, g.edge_index[1].cpu(), g.num_nodes).reshape(A.shape)
     (gv_r,) = torch.autograd.grad((Ar * dA.cpu().double()).sum(), (vc,))
@@ -421,6 +436,26 @@ def test_stress_and_virial_finish_kernels():
             X = (M if t is None else M + t).view(B, 3, 3)
             np.testing.assert_allclose(got.cpu().double(), 0.5 * (X + X.transpose(1, 2)),
                                        rtol=1e-6 if dt == torch.float32 else 1e-15)
+    # per-atom partials -> per-structure virial in one call: one structure of few atoms
+    # (one block), of many (chunked), several structures
+    from xnn_amd import _lib
+    for counts in ([50], [9000], [3000, 17, 4000], [100_000]):
+        n = sum(counts)
+        part = torch.randn(n, 9, generator=gen, dtype=torch.float64)
+        seg = torch.tensor([0] + list(np.cumsum(counts)), dtype=torch.int64)
+        tm = torch.randn(len(counts), 9, generator=gen, dtype=torch.float64)
+        for t, sym in ((None, False), (tm, True)):
+            got = _lib.virial_reduce(part.to(DEV), n, seg.to(DEV), len(counts),
+                                     None if t is None else t.to(DEV), sym, torch.float64)
+            X = torch.stack([part[a:b].sum(0) for a, b in zip(seg[:-1], seg[1:])])
+            if t is not None:
+                X = X + t
+            X = X.view(-1, 3, 3)
+            want = 0.5 * (X + X.transpose(1, 2)) if sym else X
+            np.testing.assert_allclose(got.cpu(), want, rtol=1e-12, atol=1e-10)
+            again = _lib.virial_reduce(part.to(DEV), n, seg.to(DEV), len(counts),
+                                       None if t is None else t.to(DEV), sym, torch.float64)
+            assert torch.equal(got, again)
     cell = torch.randn(B, 3, 3, generator=gen, dtype=torch.float64) + 4 * torch.eye(3, dtype=torch.float64)
     cell[1] = 0.0                                  # a molecule of the batch
     pbc = torch.ones(B, 3, dtype=torch.bool)

@@ -89,6 +89,8 @@ _SIGNATURES = {
                                            vp],
     "xnn_stress_finish": [c_int, vp, c_int, vp, vp, i64, dbl, vp, vp],
     "xnn_virial_finish": [c_int, vp, vp, i64, i32, vp, vp],
+    "xnn_virial_reduce_workspace_bytes": [i64, i64],
+    "xnn_virial_reduce": [c_int, vp, i64, vp, i64, vp, i32, vp, vp, sz, vp],
     "xnn_d4_workspace_bytes": [i64, i64, i64],
     "xnn_d4_coordination": [vp, i64, vp, vp, vp, i64, i64, vp, vp, vp, vp,
                             ctypes.POINTER(D4CnParams), vp, vp, vp, sz, vp],
@@ -125,7 +127,7 @@ _SIGNATURES = {
 }
 _RESTYPES = {"xnn_last_error": ctypes.c_char_p, "xnn_scan_workspace_bytes": sz,
              "xnn_edge_plan_workspace_bytes": sz, "xnn_segment_reduce_workspace_bytes": sz,
-             "xnn_d4_workspace_bytes": sz}
+             "xnn_d4_workspace_bytes": sz, "xnn_virial_reduce_workspace_bytes": sz}
 
 _lock = threading.Lock()
 _lib: Optional[ctypes.CDLL] = None
@@ -232,6 +234,18 @@ calls: dict = {}
 def count_call(name: str) -> None:
     """Record that a HIP entry point ran (tests assert the native path was taken)."""
     calls[name] = calls.get(name, 0) + 1
+
+
+def virial_reduce(partial: torch.Tensor, n_rows: int, seg_ptr: torch.Tensor, n_graphs: int,
+                  term: Optional[torch.Tensor], symmetrize: bool,
+                  dtype: torch.dtype) -> torch.Tensor:
+    """``xnn_virial_reduce``: (B, 3, 3) in ``dtype`` from float64 per-atom partials."""
+    out = torch.empty((n_graphs, 3, 3), dtype=dtype, device=partial.device)
+    need = int(load().xnn_virial_reduce_workspace_bytes(n_rows, n_graphs))
+    ws = torch.empty(max(need, 1), dtype=torch.uint8, device=partial.device)
+    call("xnn_virial_reduce", dtype_code(dtype), ptr(partial), n_rows, ptr(seg_ptr), n_graphs,
+         ptr(term), 1 if symmetrize else 0, ptr(out), ptr(ws), need, stream(partial.device))
+    return out
 
 
 def segment_reduce_f64(src: torch.Tensor, n_rows: int, n_features: int, seg_ptr: torch.Tensor,

@@ -16,6 +16,13 @@ namespace xnn {
 
 constexpr int kWave = 64;
 
+// Wave index within the block, as a wave-uniform (scalar) value: the compiler cannot
+// infer that threadIdx.x / 64 is the same on every lane, and values derived from a
+// divergent-looking index turn uniform loops and branches into vector control flow.
+__device__ __forceinline__ int wave_in_block() {
+  return __builtin_amdgcn_readfirstlane((int)(threadIdx.x / kWave));
+}
+
 // ---------------------------------------------------------------- shifts
 __host__ __device__ inline int32_t pack_shift(int sx, int sy, int sz) {
   return (int32_t)(((uint32_t)sx & 1023u) | (((uint32_t)sy & 1023u) << 10) |

@@ -196,7 +196,7 @@ __global__ __launch_bounds__(256) void cell_search_kernel(
   __syncthreads();
   const int n_cand = s_first[n_slots];
 
-  const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+  const int wave = wave_in_block(), lane = threadIdx.x % kWave;
   const int n_waves = blockDim.x / kWave;
   const int n_recv = r1 - r0;
 

@@ -35,12 +35,40 @@ constexpr int kLinKMax = 8;  // h features: two k-steps of 4
 constexpr int kLinKK = 2;
 constexpr int kSH = 9;       // LDS row stride of per-edge radial features
 
+// Bessel frequencies in harmonic progression, f_k = (k + 1) f_0 to 4e-7 (the default
+// BesselRBF frequencies n pi, radial.py:226): then sin((k + 1) theta) and its cosine
+// follow from one sincos by the Chebyshev recurrence x_{k+1} = 2 cos(theta) x_k - x_{k-1}
+// instead of one sincos per function. Wave-uniform (the table is the same for all lanes).
+__device__ __forceinline__ bool bessel_harmonic(const Radial<float>& R) {
+  if (R.basis != XNN_BASIS_BESSEL) return false;
+  const float f0 = R.table[0];
+  for (int k = 1; k < R.K; ++k) {
+    const float fk = R.table[k];
+    if (fabsf(fk - (float)(k + 1) * f0) > 4e-7f * fabsf(fk)) return false;
+  }
+  return true;
+}
+
 // The lane's row of radial features h_k = rbf_k(r) envelope(r), k < kLinKMax (zeros past
 // R.K, and the whole row when the lane has no edge).
-__device__ __forceinline__ void radial_row(const Radial<float>& R, bool valid, float r,
-                                           float* __restrict__ row) {
+__device__ __forceinline__ void radial_row(const Radial<float>& R, bool harmonic, bool valid,
+                                           float r, float* __restrict__ row) {
   if (valid) {
     const RadialAt<float> a = radial_at(R, r);
+    if (harmonic) {
+      float s1, c1;
+      dev_sincos(R.table[0] * a.rr / R.rc, &s1, &c1);
+      const float c2 = 2.f * c1, pf = R.prefactor * a.inv * a.f;
+      float sp = 0.f, sk = s1;  // sin(k theta), sin((k + 1) theta)
+#pragma unroll
+      for (int k = 0; k < kLinKMax; ++k) {
+        row[k] = k < R.K ? pf * sk : 0.f;
+        const float sn = c2 * sk - sp;
+        sp = sk;
+        sk = sn;
+      }
+      return;
+    }
 #pragma unroll 1
     for (int k = 0; k < kLinKMax; ++k) {
       float u = 0.f, du;
@@ -54,10 +82,31 @@ __device__ __forceinline__ void radial_row(const Radial<float>& R, bool valid, f
 }
 
 // d E / d r through the radial features of one edge: sum_k d_h[k] d h_k / d r
-__device__ __forceinline__ float radial_dot(const Radial<float>& R, float r,
+__device__ __forceinline__ float radial_dot(const Radial<float>& R, bool harmonic, float r,
                                             const float* __restrict__ d_h) {
   const RadialAt<float> a = radial_at(R, r);
   float dl = 0.f;
+  if (harmonic) {
+    // d/dr [p sin((k+1) w0 r) / r] = p ((k+1) w0 cos((k+1) w0 r) - sin(..) / r) / r
+    const float w0 = R.table[0] / R.rc;
+    float s1, c1;
+    dev_sincos(R.table[0] * a.rr / R.rc, &s1, &c1);
+    const float c2 = 2.f * c1;
+    float sp = 0.f, sk = s1, cp = 1.f, ck = c1;
+#pragma unroll 1
+    for (int k = 0; k < R.K; ++k) {
+      const float b = R.prefactor * sk * a.inv;
+      const float db =
+          a.clamped ? 0.f : R.prefactor * (ck * ((float)(k + 1) * w0) - sk * a.inv) * a.inv;
+      dl += d_h[k] * (db * a.f + b * a.df);
+      const float sn = c2 * sk - sp, cn = c2 * ck - cp;
+      sp = sk;
+      sk = sn;
+      cp = ck;
+      ck = cn;
+    }
+    return dl;
+  }
 #pragma unroll 1
   for (int k = 0; k < R.K; ++k) {
     float u, du;
@@ -68,7 +117,7 @@ __device__ __forceinline__ float radial_dot(const Radial<float>& R, float r,
 }
 
 template <typename G, int LMAX, int T, bool RAD>
-__global__ __launch_bounds__(256) void lin_msg_fwd_kernel(
+__global__ __launch_bounds__(256, 4) void lin_msg_fwd_kernel(
     const float* __restrict__ vec, const G* __restrict__ pos, const G* __restrict__ cell,
     int64_t n_graphs, const int32_t* __restrict__ batch, const int32_t* __restrict__ src,
     const int32_t* __restrict__ shift, const int32_t* __restrict__ ptr,
@@ -80,23 +129,26 @@ __global__ __launch_bounds__(256) void lin_msg_fwd_kernel(
   constexpr int KK = kLinKK;
   __shared__ float sY[kWavesPerBlock][kWave * kSY];
   __shared__ float sH[kWavesPerBlock][RAD ? kWave * kSH : 1];
-  const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+  const int wave = wave_in_block(), lane = threadIdx.x % kWave;
   const int lo = lane & 15, hi = lane >> 4;
   float* ys = sY[wave];
   float* hs = sH[wave];
-  // B operand of h W for channel tile t, k-step q: W[4 q + hi][lo T + t]
-  float wB[KK][T];
-#pragma unroll
-  for (int q = 0; q < KK; ++q)
-#pragma unroll
-    for (int t = 0; t < T; ++t) {
-      const int k = 4 * q + hi;
-      wB[q][t] = k < K ? W[k * C + lo * T + t] : 0.f;
-    }
+  const bool harmonic = RAD && bessel_harmonic(R);
+  // W in LDS (rows padded to C + 4 floats, zero rows past K): the B operand of h W for
+  // channel tile t, k-step q is W[4 q + hi][lo T + t], a run of T floats
+  constexpr int SWS = C + 4;
+  __shared__ __align__(16) float sW[kLinKMax * SWS];
+  for (int i = threadIdx.x; i < kLinKMax * C; i += blockDim.x)
+    sW[(i / C) * SWS + i % C] = i < K * C ? W[i] : 0.f;
+  __syncthreads();
   // M row lo of h W stands for edge 4 (lo % 4) + lo / 4 of the tile
   const int hrow = 4 * (lo & 3) + (lo >> 2);
   const int64_t n_waves = (int64_t)gridDim.x * kWavesPerBlock;
-  for (int64_t row = (int64_t)blockIdx.x * kWavesPerBlock + wave; row < n_nodes; row += n_waves) {
+  int64_t row = (int64_t)blockIdx.x * kWavesPerBlock + wave;
+  // with given edge vectors, the first batch of the wave's next row is loaded a row ahead
+  float px = 0.f, py = 0.f, pz = 0.f;
+  if (vec != nullptr && row < n_nodes) load_first_vec(vec, perm, ptr[row], ptr[row + 1], lane, px, py, pz);
+  for (; row < n_nodes; row += n_waves) {
     const G* cl = cell == nullptr ? nullptr
                                   : (n_graphs <= 1 || batch == nullptr ? cell
                                                                        : cell + 9 * (int64_t)batch[row]);
@@ -104,6 +156,9 @@ __global__ __launch_bounds__(256) void lin_msg_fwd_kernel(
 #pragma unroll
     for (int t = 0; t < T; ++t) acc[t] = floatx4{0.f, 0.f, 0.f, 0.f};
     const int b0 = ptr[row], b1 = ptr[row + 1];
+    const float cx = px, cy = py, cz = pz;
+    if (vec != nullptr && row + n_waves < n_nodes)
+      load_first_vec(vec, perm, ptr[row + n_waves], ptr[row + n_waves + 1], lane, px, py, pz);
     for (int base = b0; base < b1; base += kWave) {
       const int cnt = min(kWave, b1 - base);
       const int my_e = lane < cnt ? (perm ? perm[base + lane] : base + lane) : 0;
@@ -119,9 +174,15 @@ __global__ __launch_bounds__(256) void lin_msg_fwd_kernel(
         }
       }
       float ux, uy, uz, inv, len;
-      batch_harmonics<G, LMAX>(vec, pos, cl, src, shift, (int)row, sign, lane, cnt, my_e, ys, ux,
-                               uy, uz, inv, len);
-      if constexpr (RAD) radial_row(R, lane < cnt, len, hs + lane * kSH);
+      if (vec != nullptr && base == b0)
+        batch_harmonics_xyz<LMAX>(cx, cy, cz, sign, lane, cnt, ys, ux, uy, uz, inv, len);
+      else
+        batch_harmonics<G, LMAX>(vec, pos, cl, src, shift, (int)row, sign, lane, cnt, my_e, ys,
+                                 ux, uy, uz, inv, len);
+      if constexpr (RAD) {
+        __builtin_amdgcn_sched_barrier(0);
+        radial_row(R, harmonic, lane < cnt, len, hs + lane * kSH);
+      }
       wave_sync();
       const int ntile = (cnt + 15) >> 4;
 #pragma unroll 1
@@ -142,20 +203,24 @@ __global__ __launch_bounds__(256) void lin_msg_fwd_kernel(
         }
         floatx4 ph[T];
 #pragma unroll
-        for (int t = 0; t < T; ++t) {
-          ph[t] = floatx4{0.f, 0.f, 0.f, 0.f};
+        for (int t = 0; t < T; ++t) ph[t] = floatx4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-          for (int q = 0; q < KK; ++q) ph[t] = mfma_16x16x4(ha[q], wB[q][t], ph[t]);
+        for (int q = 0; q < KK; ++q) {
+          float wb[T];
+          load_run<T>(sW + (4 * q + hi) * SWS + lo * T, wb);
+#pragma unroll
+          for (int t = 0; t < T; ++t) ph[t] = mfma_16x16x4(ha[q], wb[t], ph[t]);
         }
-        // ph[t][r] = phi[edge 16 tau + 4 r + hi][channel lo T + t]
+        // ph[t][r] = phi[edge 16 tau + 4 r + hi][channel lo T + t]; rows past the batch's
+        // end hold zero harmonics, so the last tile runs whole, without branches that
+        // would split the accumulators' live ranges
+        float a[4];
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          if (16 * tau + 4 * r < cnt) {
-            const float a = ys[(16 * tau + 4 * r + hi) * kSY + lo];
+        for (int r = 0; r < 4; ++r) a[r] = ys[(16 * tau + 4 * r + hi) * kSY + lo];
 #pragma unroll
-            for (int t = 0; t < T; ++t) acc[t] = mfma_16x16x4(a, ph[t][r], acc[t]);
-          }
-        }
+        for (int r = 0; r < 4; ++r)
+#pragma unroll
+          for (int t = 0; t < T; ++t) acc[t] = mfma_16x16x4(a[r], ph[t][r], acc[t]);
       }
       wave_sync();  // ys is rewritten by the next batch
     }
@@ -178,7 +243,7 @@ __global__ __launch_bounds__(256) void lin_msg_fwd_kernel(
 }
 
 template <typename G, int LMAX, int T, bool RAD>
-__global__ __launch_bounds__(256, 2) void lin_msg_bwd_kernel(
+__global__ __launch_bounds__(256, 3) void lin_msg_bwd_kernel(
     const float* __restrict__ vec, const G* __restrict__ pos, const G* __restrict__ cell,
     int64_t n_graphs, const int32_t* __restrict__ batch, const int32_t* __restrict__ src,
     const int32_t* __restrict__ shift, const int32_t* __restrict__ ptr,
@@ -191,25 +256,40 @@ __global__ __launch_bounds__(256, 2) void lin_msg_bwd_kernel(
   constexpr int KK = kLinKK;
   static_assert(C * L <= 2 * kWave * kSY, "the staged d_out row must fit the LDS slice");
   __shared__ __align__(16) float sbuf[kWavesPerBlock][2 * kWave * kSY];
-  const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+  const int wave = wave_in_block(), lane = threadIdx.x % kWave;
   const int lo = lane & 15, hi = lane >> 4;
   float* ys = sbuf[wave];
   float* sdy = sbuf[wave] + kWave * kSY;
   // RAD: per-edge radial features, overwritten tile by tile with d_h once read
   __shared__ float sH[kWavesPerBlock][RAD ? kWave * kSH : 1];
   float* hs = sH[wave];
+  const bool harmonic = RAD && bessel_harmonic(R);
   const bool want_vec = RAD || g_vec != nullptr;
-  // W in LDS, zero rows past K: the A operand of phi^T = W^T h^T for k-step q is
+  // W in LDS, zero rows past K, rows padded to C + 4 floats (the d_h operand reads
+  // 16 rows at once): the A operand of phi^T = W^T h^T for k-step q is
   // W[4 q + hi][lo T + t] and the B operand of d_h = d_phi W^T for k-step (t, r) is
   // W[lo][(4 hi + r) T + t], runs of T floats
-  __shared__ __align__(16) float sW[16 * C];
-  for (int i = threadIdx.x; i < 16 * C; i += blockDim.x) sW[i] = i < K * C ? W[i] : 0.f;
+  constexpr int SWS = C + 4;
+  __shared__ __align__(16) float sW[16 * SWS];
+  for (int i = threadIdx.x; i < 16 * C; i += blockDim.x)
+    sW[(i / C) * SWS + i % C] = i < K * C ? W[i] : 0.f;
   __syncthreads();
-  const float* wrow = sW + lo * C;
+  const float* wrow = sW + lo * SWS;
+  // G rows of 16 floats are staged with their 4-float chunks permuted by channel,
+  // chunk q of channel c at q ^ ((c / T) & 3), so that the 16 channels lo T + t of one
+  // A-operand read fall into different banks
+  constexpr bool SWZ = (L == 16);
+  auto g_at = [](int c, int lm) {
+    return SWZ ? c * 16 + ((((lm >> 2) ^ (c / T)) & 3) << 2) + (lm & 3) : c * L + lm;
+  };
   const int64_t n_waves = (int64_t)gridDim.x * kWavesPerBlock;
   for (int64_t row = (int64_t)blockIdx.x * kWavesPerBlock + wave; row < n_nodes; row += n_waves) {
     const int b0 = ptr[row], b1 = ptr[row + 1];
     if (b0 == b1) continue;
+    // with given edge vectors, the first batch's are loaded before G is staged, so that
+    // the two loads' latencies overlap
+    float cx = 0.f, cy = 0.f, cz = 0.f;
+    if (vec != nullptr) load_first_vec(vec, perm, b0, b1, lane, cx, cy, cz);
     const G* cl = cell == nullptr ? nullptr
                                   : (n_graphs <= 1 || batch == nullptr ? cell
                                                                        : cell + 9 * (int64_t)batch[row]);
@@ -217,7 +297,21 @@ __global__ __launch_bounds__(256, 2) void lin_msg_bwd_kernel(
     {
       const float4* g4 = reinterpret_cast<const float4*>(d_out + (int64_t)row * C * L);
       float4* s4 = reinterpret_cast<float4*>(sbuf[wave]);
-      for (int i = lane; i < C * L / 4; i += kWave) s4[i] = g4[i];
+      for (int i = lane; i < C * L / 4; i += kWave) {
+        if constexpr (SWZ)
+          s4[(i & ~3) | (((i & 3) ^ ((i >> 2) / T)) & 3)] = g4[i];
+        else
+          s4[i] = g4[i];
+      }
+    }
+    // RAD: the first batch's vectors wait in the radial rows' LDS (free until the batch
+    // starts), not in registers through the operand loads below
+    if constexpr (RAD) {
+      if (vec != nullptr) {
+        hs[3 * lane + 0] = cx;
+        hs[3 * lane + 1] = cy;
+        hs[3 * lane + 2] = cz;
+      }
     }
     wave_sync();
     float gA[T][KS], gB[T][4];
@@ -226,11 +320,11 @@ __global__ __launch_bounds__(256, 2) void lin_msg_bwd_kernel(
 #pragma unroll
       for (int s = 0; s < KS; ++s) {
         const int lm = 4 * s + hi;
-        gA[t][s] = lm < L ? sbuf[wave][(lo * T + t) * L + lm] : 0.f;  // G[lo T + t][4 s + hi]
+        gA[t][s] = lm < L ? sbuf[wave][g_at(lo * T + t, lm)] : 0.f;  // G[lo T + t][4 s + hi]
       }
 #pragma unroll
       for (int r = 0; r < 4; ++r)  // G[(4 hi + r) T + t][lo]
-        gB[t][r] = lo < L ? sbuf[wave][((4 * hi + r) * T + t) * L + lo] : 0.f;
+        gB[t][r] = lo < L ? sbuf[wave][g_at((4 * hi + r) * T + t, lo)] : 0.f;
     }
     wave_sync();  // the staging area becomes ys / sdy
 
@@ -249,11 +343,20 @@ __global__ __launch_bounds__(256, 2) void lin_msg_bwd_kernel(
         }
       }
       float ux, uy, uz, inv, len;
-      batch_harmonics<G, LMAX>(vec, pos, cl, src, shift, (int)row, sign, lane, cnt, my_e, ys, ux,
-                               uy, uz, inv, len);
+      if (vec != nullptr && base == b0) {
+        if constexpr (RAD) {
+          cx = hs[3 * lane + 0];
+          cy = hs[3 * lane + 1];
+          cz = hs[3 * lane + 2];
+        }
+        batch_harmonics_xyz<LMAX>(cx, cy, cz, sign, lane, cnt, ys, ux, uy, uz, inv, len);
+      } else {
+        batch_harmonics<G, LMAX>(vec, pos, cl, src, shift, (int)row, sign, lane, cnt, my_e, ys,
+                                 ux, uy, uz, inv, len);
+      }
       if constexpr (RAD) {
         __builtin_amdgcn_sched_barrier(0);
-        radial_row(R, lane < cnt, len, hs + lane * kSH);
+        radial_row(R, harmonic, lane < cnt, len, hs + lane * kSH);
       }
       wave_sync();
       const int ntile = (cnt + 15) >> 4;
@@ -282,7 +385,7 @@ __global__ __launch_bounds__(256, 2) void lin_msg_bwd_kernel(
 #pragma unroll
           for (int q = 0; q < KK; ++q) {
             float wa[T];
-            load_run<T>(sW + (4 * q + hi) * C + lo * T, wa);
+            load_run<T>(sW + (4 * q + hi) * SWS + lo * T, wa);
 #pragma unroll
             for (int t = 0; t < T; ++t) pt[t] = mfma_16x16x4(wa[t], hb[q], pt[t]);
           }
@@ -336,7 +439,7 @@ __global__ __launch_bounds__(256, 2) void lin_msg_bwd_kernel(
         // d|r| from the radial features first, then the harmonics' share (kept apart so
         // that their temporaries are not live together)
         float dl = 0.f;
-        if constexpr (RAD) dl = radial_dot(R, len, hs + lane * kSH);
+        if constexpr (RAD) dl = radial_dot(R, harmonic, len, hs + lane * kSH);
         __builtin_amdgcn_sched_barrier(0);
         float dY[L];
 #pragma unroll

@@ -53,6 +53,16 @@ inline int make_radial(const xnn_featurize_params* prm, const void* table, Radia
   return XNN_OK;
 }
 
+// Unit vector of sign * (x, y, z), 1/|(x, y, z)| (0 for a zero vector) and the length
+__device__ __forceinline__ void unit_of(float x, float y, float z, float sign, float& ux,
+                                        float& uy, float& uz, float& inv, float& r) {
+  r = sqrtf(x * x + y * y + z * z);
+  inv = r > 0.f ? 1.f / r : 0.f;
+  ux = sign * x * inv;
+  uy = sign * y * inv;
+  uz = sign * z * inv;
+}
+
 // Per-lane geometry of one edge: unit vector of sign * r_e, 1/|r_e| and |r_e|; the
 // vector is given (vec) or formed from positions.
 template <typename G>
@@ -73,13 +83,23 @@ __device__ inline void edge_unit(const float* __restrict__ vec, int64_t e,
     y = (float)gy;
     z = (float)gz;
   }
-  r = sqrtf(x * x + y * y + z * z);
-  inv = r > 0.f ? 1.f / r : 0.f;
-  ux = sign * x * inv;
-  uy = sign * y * inv;
-  uz = sign * z * inv;
+  unit_of(x, y, z, sign, ux, uy, uz, inv, r);
 }
 
+// The lane's given edge vector in the first batch of a receiver row's edges [b0, b1)
+// (zeros past the batch's end): loaded a row ahead of its use, so that its latency
+// overlaps the previous row's products
+__device__ __forceinline__ void load_first_vec(const float* __restrict__ vec,
+                                               const int32_t* __restrict__ perm, int b0, int b1,
+                                               int lane, float& x, float& y, float& z) {
+  x = y = z = 0.f;
+  if (lane < min(kWave, b1 - b0)) {
+    const int64_t e = perm ? perm[b0 + lane] : b0 + lane;
+    x = vec[3 * e + 0];
+    y = vec[3 * e + 1];
+    z = vec[3 * e + 2];
+  }
+}
 
 // ---------------------------------------------------------------- matrix-core helpers
 // v_mfma_f32_16x16x4_f32 (float32 inputs, float32 accumulation), one wave: per
@@ -140,6 +160,25 @@ __device__ __forceinline__ void batch_harmonics(
   float Y[L];
   if (lane < cnt) {
     edge_unit(vec, e, pos, cl, src, shift, row, sign, ux, uy, uz, inv, r);
+    sh_eval<LMAX, float>(ux, uy, uz, Y);
+  } else {
+    ux = uy = uz = inv = r = 0.f;
+#pragma unroll
+    for (int m = 0; m < L; ++m) Y[m] = 0.f;
+  }
+#pragma unroll
+  for (int m = 0; m < 16; ++m) ys[lane * kSY + m] = m < L ? Y[m] : 0.f;
+}
+
+// batch_harmonics of an edge vector already in registers
+template <int LMAX>
+__device__ __forceinline__ void batch_harmonics_xyz(float x, float y, float z, float sign,
+                                                    int lane, int cnt, float* ys, float& ux,
+                                                    float& uy, float& uz, float& inv, float& r) {
+  constexpr int L = ShDims<LMAX>::L;
+  float Y[L];
+  if (lane < cnt) {
+    unit_of(x, y, z, sign, ux, uy, uz, inv, r);
     sh_eval<LMAX, float>(ux, uy, uz, Y);
   } else {
     ux = uy = uz = inv = r = 0.f;

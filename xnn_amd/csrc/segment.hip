@@ -60,7 +60,7 @@ __global__ __launch_bounds__(256) void sh_msg_fwd_kernel(
   constexpr int kU = 8;  // edges per load group; two groups are in flight
   __shared__ float sY[kWavesPerBlock][kWave][L];
   __shared__ int sE[kWavesPerBlock][kWave];
-  const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+  const int wave = wave_in_block(), lane = threadIdx.x % kWave;
   const int c0 = lane * CPL;
   const bool own = c0 < C;
   const int64_t n_waves = (int64_t)gridDim.x * kWavesPerBlock;
@@ -222,7 +222,7 @@ __global__ __launch_bounds__(256) void sh_msg_bwd_kernel(
   __shared__ float sY[kWavesPerBlock][kWave][L];
   __shared__ float sdY[kWavesPerBlock][kWave][LP];
   __shared__ int sE[kWavesPerBlock][kWave];
-  const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+  const int wave = wave_in_block(), lane = threadIdx.x % kWave;
   const int c0 = lane * CPL;
   const bool own = c0 < C;
   const int64_t n_waves = (int64_t)gridDim.x * kWavesPerBlock;
@@ -370,7 +370,7 @@ __global__ __launch_bounds__(256) void sh_msg_fwd_mfma_kernel(
   constexpr int C = 16 * T;
   constexpr int KG = 2;  // k-steps per load group (8 edges); the next group is in flight
   __shared__ float sY[kWavesPerBlock][kWave * kSY];
-  const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+  const int wave = wave_in_block(), lane = threadIdx.x % kWave;
   const int lo = lane & 15, hi = lane >> 4;
   float* ys = sY[wave];
   const int64_t n_waves = (int64_t)gridDim.x * kWavesPerBlock;
@@ -452,7 +452,7 @@ __global__ __launch_bounds__(256) void sh_msg_bwd_mfma_kernel(
   constexpr int KS = (L + 3) / 4;
   static_assert(C * L <= 2 * kWave * kSY, "the staged d_out row must fit the LDS slice");
   __shared__ __align__(16) float sbuf[kWavesPerBlock][2 * kWave * kSY];
-  const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+  const int wave = wave_in_block(), lane = threadIdx.x % kWave;
   const int lo = lane & 15, hi = lane >> 4;
   float* ys = sbuf[wave];
   float* sdy = sbuf[wave] + kWave * kSY;
@@ -615,7 +615,7 @@ __global__ __launch_bounds__(BLOCK) void segment_reduce_f64_kernel(const T* __re
     i0 = seg[b];
     i1 = seg[b + 1];
   }
-  const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+  const int wave = wave_in_block(), lane = threadIdx.x % kWave;
   for (int64_t f0 = 0; f0 < F; f0 += kF) {
     const int nf = (int)min<int64_t>(kF, F - f0);
     double acc[kF];
@@ -655,7 +655,7 @@ __global__ __launch_bounds__(BLOCK) void segment_reduce_f64_kernel(const T* __re
 __global__ __launch_bounds__(256) void segment_finish_kernel(const double* __restrict__ partial,
                                                              int chunks, int64_t F,
                                                              double* __restrict__ out) {
-  const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+  const int wave = wave_in_block(), lane = threadIdx.x % kWave;
   for (int64_t f = wave; f < F; f += blockDim.x / kWave) {
     double t = 0.0;
     for (int k = lane; k < chunks; k += kWave) t += partial[(int64_t)k * F + f];
@@ -672,20 +672,22 @@ __global__ __launch_bounds__(256) void segment_finish_kernel(const double* __res
 // gives the chunk's partial sums (fixed order: deterministic).
 constexpr int kFlatMaxF = 64;
 constexpr int kFlatPerThread = 4;
+// a single block of 1024 threads takes arrays up to this many elements (no second kernel)
+constexpr int64_t kFlatSingleMax = 16384;
 
-static int flat_stride(int64_t F) {
+static int flat_stride(int64_t F, int block) {
   int64_t S = F;
-  while (2 * S <= 256) S *= 2;
+  while (2 * S <= block) S *= 2;
   return (int)S;
 }
 
-template <typename T>
-__global__ __launch_bounds__(256) void flat_reduce_f64_kernel(const T* __restrict__ src,
-                                                              int64_t F, int S,
-                                                              const int64_t* __restrict__ seg,
-                                                              int chunks,
-                                                              double* __restrict__ partial) {
-  __shared__ double red[256];
+template <typename T, int BLOCK>
+__global__ __launch_bounds__(BLOCK) void flat_reduce_f64_kernel(const T* __restrict__ src,
+                                                                int64_t F, int S,
+                                                                const int64_t* __restrict__ seg,
+                                                                int chunks,
+                                                                double* __restrict__ partial) {
+  __shared__ double red[BLOCK];
   const int t = threadIdx.x;
   const int64_t e0 = seg[0] * F, e1 = seg[1] * F;
   // chunk length: a multiple of S covering the segment in `chunks` pieces
@@ -704,24 +706,76 @@ __global__ __launch_bounds__(256) void flat_reduce_f64_kernel(const T* __restric
   if (t < F) partial[(int64_t)blockIdx.x * F + t] = red[t];
 }
 
+// Totals of the 9 virial components over `chunks` partial rows (as segment_finish_kernel),
+// then out = sym(total + term) (or total + term) cast to T
+template <typename T>
+__global__ __launch_bounds__(256) void virial_chunks_finish_kernel(
+    const double* __restrict__ partial, int chunks, const double* __restrict__ term,
+    int symmetrize, T* __restrict__ out) {
+  __shared__ double tot[9];
+  const int wave = wave_in_block(), lane = threadIdx.x % kWave;
+  for (int f = wave; f < 9; f += blockDim.x / kWave) {
+    double v = 0.0;
+    for (int k = lane; k < chunks; k += kWave) v += partial[(int64_t)k * 9 + f];
+#pragma unroll
+    for (int m = kWave / 2; m > 0; m >>= 1) v += __shfl_xor(v, m, kWave);
+    if (lane == 0) tot[f] = v + (term ? term[f] : 0.0);
+  }
+  __syncthreads();
+  const int j = threadIdx.x;
+  if (j < 9) {
+    const int r = j / 3, c = j % 3;
+    out[j] = (T)(symmetrize ? 0.5 * (tot[j] + tot[3 * c + r]) : tot[j]);
+  }
+}
+
 constexpr int64_t kChunkRows = 2048;
 constexpr int kMaxChunks = 256;
 
 // single segments of few features take the flat kernel
 static bool reduce_flat(int64_t n_rows, int64_t n_features, int64_t n_segments) {
   return n_segments == 1 && n_features <= kFlatMaxF &&
-         n_rows * n_features >= 2 * (int64_t)flat_stride(n_features) * kFlatPerThread;
+         n_rows * n_features >= 2 * (int64_t)flat_stride(n_features, 256) * kFlatPerThread;
+}
+
+// one block (no partials) for small flat arrays
+static bool reduce_flat_single(int64_t n_rows, int64_t n_features, int64_t n_segments) {
+  return reduce_flat(n_rows, n_features, n_segments) && n_rows * n_features <= kFlatSingleMax;
 }
 
 static int reduce_chunks(int64_t n_rows, int64_t n_features, int64_t n_segments) {
+  if (reduce_flat_single(n_rows, n_features, n_segments)) return 1;
   if (reduce_flat(n_rows, n_features, n_segments)) {
-    const int64_t per_chunk = (int64_t)flat_stride(n_features) * kFlatPerThread;
+    const int64_t per_chunk = (int64_t)flat_stride(n_features, 256) * kFlatPerThread;
     const int64_t c = (n_rows * n_features + per_chunk - 1) / per_chunk;
     return (int)(c < kMaxChunks ? c : kMaxChunks);
   }
   if (n_segments != 1 || n_rows < 2 * kChunkRows) return 1;
   const int64_t c = (n_rows + kChunkRows - 1) / kChunkRows;
   return (int)(c < kMaxChunks ? c : kMaxChunks);
+}
+
+// the partial sums of one structure's (n_rows, F) values in `partial` (chunks x F), by the
+// flat kernel; `chunks` as reduce_chunks gives it
+static void launch_flat(int dtype, const void* src, int64_t F, const int64_t* seg, int chunks,
+                        double* partial, hipStream_t s) {
+  if (chunks == 1) {
+    const int S = flat_stride(F, 1024);
+    if (dtype == XNN_F32)
+      hipLaunchKernelGGL((flat_reduce_f64_kernel<float, 1024>), dim3(1), dim3(1024), 0, s,
+                         (const float*)src, F, S, seg, 1, partial);
+    else
+      hipLaunchKernelGGL((flat_reduce_f64_kernel<double, 1024>), dim3(1), dim3(1024), 0, s,
+                         (const double*)src, F, S, seg, 1, partial);
+    return;
+  }
+  const int S = flat_stride(F, 256);
+  if (dtype == XNN_F32)
+    hipLaunchKernelGGL((flat_reduce_f64_kernel<float, 256>), dim3(chunks), dim3(256), 0, s,
+                       (const float*)src, F, S, seg, chunks, partial);
+  else
+    hipLaunchKernelGGL((flat_reduce_f64_kernel<double, 256>), dim3(chunks), dim3(256), 0, s,
+                       (const double*)src, F, S, seg, chunks, partial);
 }
 
 // blocks of `kernel` that stay resident on the whole device (all CUs), capped at `needed`
@@ -1003,17 +1057,13 @@ int xnn_segment_reduce_f64(int dtype, const void* src, int64_t n_rows, int64_t n
   hipStream_t s = as_hip(stream);
   double* dest = chunks > 1 ? static_cast<double*>(workspace) : out;
   if (reduce_flat(n_rows, n_features, n_segments)) {
-    const int S = flat_stride(n_features);
-    if (dtype == XNN_F32)
-      hipLaunchKernelGGL(flat_reduce_f64_kernel<float>, dim3(chunks), dim3(256), 0, s,
-                         (const float*)src, n_features, S, seg_ptr, chunks, dest);
-    else
-      hipLaunchKernelGGL(flat_reduce_f64_kernel<double>, dim3(chunks), dim3(256), 0, s,
-                         (const double*)src, n_features, S, seg_ptr, chunks, dest);
+    launch_flat(dtype, src, n_features, seg_ptr, chunks, dest, s);
     XNN_LAUNCH_CHECK();
-    hipLaunchKernelGGL(segment_finish_kernel, dim3(1), dim3(256), 0, s, dest, chunks, n_features,
-                       out);
-    XNN_LAUNCH_CHECK();
+    if (chunks > 1) {
+      hipLaunchKernelGGL(segment_finish_kernel, dim3(1), dim3(256), 0, s, dest, chunks,
+                         n_features, out);
+      XNN_LAUNCH_CHECK();
+    }
     return XNN_OK;
   }
   const int64_t grid = chunks > 1 ? chunks : n_segments;
@@ -1035,6 +1085,57 @@ int xnn_segment_reduce_f64(int dtype, const void* src, int64_t n_rows, int64_t n
     XNN_LAUNCH_CHECK();
   }
   return XNN_OK;
+}
+
+size_t xnn_virial_reduce_workspace_bytes(int64_t n_rows, int64_t n_graphs) {
+  if (n_graphs == 1) {
+    const int chunks = reduce_chunks(n_rows, 9, 1);
+    return sizeof(double) * 9 * (size_t)chunks;
+  }
+  return sizeof(double) * 9 * (size_t)std::max<int64_t>(n_graphs, 0) +
+         xnn_segment_reduce_workspace_bytes(n_rows, 9, n_graphs);
+}
+
+int xnn_virial_reduce(int dtype, const double* partial, int64_t n_rows, const int64_t* seg_ptr,
+                      int64_t n_graphs, const double* term, int32_t symmetrize, void* out,
+                      void* workspace, size_t workspace_bytes, xnn_stream_t stream) {
+  XNN_REQUIRE(n_rows >= 0 && n_graphs >= 0, "negative size");
+  if (n_graphs == 0) return XNN_OK;
+  XNN_REQUIRE(seg_ptr && out && (n_rows == 0 || partial), "NULL pointer");
+  XNN_REQUIRE(dtype == XNN_F32 || dtype == XNN_F64, "unsupported dtype %d", dtype);
+  const size_t need = xnn_virial_reduce_workspace_bytes(n_rows, n_graphs);
+  XNN_REQUIRE(workspace != nullptr && workspace_bytes >= need, "workspace of %zu bytes needed",
+              need);
+  hipStream_t s = as_hip(stream);
+  double* ws = static_cast<double*>(workspace);
+  if (n_graphs == 1) {
+    const int chunks = reduce_chunks(n_rows, 9, 1);
+    if (reduce_flat(n_rows, 9, 1)) {
+      launch_flat(XNN_F64, partial, 9, seg_ptr, chunks, ws, s);
+    } else {
+      // few rows: one block sums them (the per-segment kernel), a single "chunk"
+      hipLaunchKernelGGL((segment_reduce_f64_kernel<double, 64>), dim3(1), dim3(64), 0, s,
+                         partial, (int64_t)9, seg_ptr, 1, ws);
+    }
+    XNN_LAUNCH_CHECK();
+    const int used = reduce_flat(n_rows, 9, 1) ? chunks : 1;
+    if (dtype == XNN_F32)
+      hipLaunchKernelGGL(virial_chunks_finish_kernel<float>, dim3(1), dim3(256), 0, s, ws, used,
+                         term, (int)symmetrize, (float*)out);
+    else
+      hipLaunchKernelGGL(virial_chunks_finish_kernel<double>, dim3(1), dim3(256), 0, s, ws, used,
+                         term, (int)symmetrize, (double*)out);
+    XNN_LAUNCH_CHECK();
+    return XNN_OK;
+  }
+  // several structures: per-structure sums, then the finish per structure
+  double* M = ws;
+  void* ws2 = ws + 9 * n_graphs;
+  const size_t ws2_bytes = workspace_bytes - sizeof(double) * 9 * (size_t)n_graphs;
+  int st = xnn_segment_reduce_f64(XNN_F64, partial, n_rows, 9, seg_ptr, n_graphs, M, ws2,
+                                  ws2_bytes, stream);
+  if (st != XNN_OK) return st;
+  return xnn_virial_finish(dtype, M, term, n_graphs, symmetrize, out, stream);
 }
 
 }  // extern "C"

@@ -162,6 +162,8 @@ class ShEdgePotential(InteratomicPotential):
                data.num_edges, double_backward=self.double_backward)
         vec = data.edge_vectors()
         A = self.messages(data, vec)
-        node_energy = (A.reshape(A.shape[0], -1) @ self.U.to(A.dtype).reshape(-1)
-                       + self.atom_ref.to(A.dtype)[data.atomic_numbers])
+        # readout E_i = <U, A_i> + atom_ref[Z_i], the reference energy added by the
+        # product itself (one launch)
+        node_energy = torch.addmv(self.atom_ref.to(A.dtype)[data.atomic_numbers],
+                                  A.reshape(A.shape[0], -1), self.U.to(A.dtype).reshape(-1))
         return {"node_energy": node_energy, "energy": self.aggregate_energy(node_energy, data)}

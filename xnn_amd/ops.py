@@ -122,9 +122,7 @@ def force_reduce_op(g_edge: Tensor, cell_like: Optional[Tensor], batch32: Tensor
               _lib.ptr(partial), None, None, s)
     if not want_cell:
         return grad_pos, grad_pos.new_zeros((0,))
-    grad_cell = torch.empty((n_graphs, 9), dtype=torch.float64, device=dev)
-    _lib.segment_reduce_f64(partial, n_nodes, 9, node_ptr, n_graphs, grad_cell)
-    return grad_pos, grad_cell.view(n_graphs, 3, 3).to(gdt)
+    return grad_pos, _lib.virial_reduce(partial, n_nodes, node_ptr, n_graphs, None, False, gdt)
 
 
 @force_reduce_op.register_fake
@@ -267,14 +265,11 @@ def _probe_backward(ctx, grad):
               grad.shape[0], _lib.ptr(ptr_dst), _lib.ptr(perm_dst), _lib.ptr(ptr_src),
               _lib.ptr(perm_src), _lib.ptr(shift), n_nodes, _lib.ptr(grad_pos),
               _lib.ptr(cell_partial), _lib.ptr(vec), _lib.ptr(virial_partial), _lib.stream(dev))
-    M = torch.empty((n_graphs, 9), dtype=torch.float64, device=dev)
-    _lib.segment_reduce_f64(virial_partial, n_nodes, 9, node_ptr, n_graphs, M)
-    grad_probe = virial_finish(M, None, ctx.probe_dtype)
+    grad_probe = _lib.virial_reduce(virial_partial, n_nodes, node_ptr, n_graphs, None, True,
+                                    ctx.probe_dtype)
     grad_cell = None
     if want_cell:
-        gc = torch.empty((n_graphs, 9), dtype=torch.float64, device=dev)
-        _lib.segment_reduce_f64(cell_partial, n_nodes, 9, node_ptr, n_graphs, gc)
-        grad_cell = gc.view(n_graphs, 3, 3).to(gdt)
+        grad_cell = _lib.virial_reduce(cell_partial, n_nodes, node_ptr, n_graphs, None, False, gdt)
     return (grad_pos if ctx.needs_input_grad[0] else None, grad_probe, grad_cell,
             None, None, None, None, None, None, None, None, None, None)
 
@@ -353,9 +348,7 @@ def _strain_backward(ctx, g_pos, g_cell):
               _lib.ptr(strain), _lib.ptr(g_pos), _lib.ptr(g_cell) if cell is not None else None,
               _lib.ptr(grad_pos), _lib.ptr(grad_cell), _lib.ptr(partial), _lib.ptr(term),
               _lib.stream(dev))
-    M = torch.empty((n_graphs, 9), dtype=torch.float64, device=dev)
-    _lib.segment_reduce_f64(partial, n, 9, node_ptr, n_graphs, M)
-    grad_strain = virial_finish(M, term, strain.dtype)
+    grad_strain = _lib.virial_reduce(partial, n, node_ptr, n_graphs, term, True, strain.dtype)
     return grad_pos, grad_cell, grad_strain, None, None
 
 
@@ -745,12 +738,16 @@ def _structure_sum_setup(ctx, inputs, output):
     src, node_ptr, batch32 = inputs
     ctx.save_for_backward(node_ptr, batch32)
     ctx.src_dtype = src.dtype
+    ctx.src_shape = src.shape
 
 
 def _structure_sum_backward(ctx, grad):
     # broadcast of every structure's cotangent to its atoms: the gather over batch,
-    # whose own adjoint is the segment sum over node_ptr
+    # whose own adjoint is the segment sum over node_ptr; one structure is a plain
+    # broadcast (a stride-0 view, no kernel)
     node_ptr, batch32 = ctx.saved_tensors
+    if node_ptr.shape[0] == 2:
+        return grad.to(ctx.src_dtype).expand(ctx.src_shape), None, None
     g = gather_rows_op(grad.contiguous(), batch32, node_ptr.to(torch.int32), None)
     return g.to(ctx.src_dtype), None, None
 
