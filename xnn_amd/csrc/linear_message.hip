@@ -265,16 +265,23 @@ __global__ __launch_bounds__(256, 3) void lin_msg_bwd_kernel(
   float* hs = sH[wave];
   const bool harmonic = RAD && bessel_harmonic(R);
   const bool want_vec = RAD || g_vec != nullptr;
-  // W in LDS, zero rows past K, rows padded to C + 4 floats (the d_h operand reads
-  // 16 rows at once): the A operand of phi^T = W^T h^T for k-step q is
-  // W[4 q + hi][lo T + t] and the B operand of d_h = d_phi W^T for k-step (t, r) is
-  // W[lo][(4 hi + r) T + t], runs of T floats
+  // W in LDS, zero rows past K, twice: rows padded to C + 4 floats for the A operand of
+  // phi^T = W^T h^T (k-step q: W[4 q + hi][lo T + t], a run of T floats), and permuted for
+  // the B operand of d_h = d_phi W^T on the 4 x 4 x 1 products: sWp[k][hi][t][r] =
+  // W[k][(4 hi + r) T + t], the four r of one (k, hi, t) a float4, (k, hi) rows padded to
+  // 4 T + 4 floats (spreads the 16 addresses of one read over the banks)
   constexpr int SWS = C + 4;
-  __shared__ __align__(16) float sW[16 * SWS];
-  for (int i = threadIdx.x; i < 16 * C; i += blockDim.x)
-    sW[(i / C) * SWS + i % C] = i < K * C ? W[i] : 0.f;
+  constexpr int SWP = 4 * T + 4;
+  __shared__ __align__(16) float sW[kLinKMax * SWS];
+  __shared__ __align__(16) float sWp[kLinKMax * 4 * SWP];
+  for (int i = threadIdx.x; i < kLinKMax * C; i += blockDim.x) {
+    const int k = i / C, c = i % C;
+    const float w = k < K ? W[i] : 0.f;
+    sW[k * SWS + c] = w;
+    const int hq = c / (4 * T), rr = (c / T) % 4, tt = c % T;  // c = (4 hq + rr) T + tt
+    sWp[(k * 4 + hq) * SWP + 4 * tt + rr] = w;
+  }
   __syncthreads();
-  const float* wrow = sW + lo * SWS;
   // G rows of 16 floats are staged with their 4-float chunks permuted by channel,
   // chunk q of channel c at q ^ ((c / T) & 3), so that the 16 channels lo T + t of one
   // A-operand read fall into different banks
@@ -400,37 +407,63 @@ __global__ __launch_bounds__(256, 3) void lin_msg_bwd_kernel(
         }
         // keep phi^T and d_phi from being live together
         __builtin_amdgcn_sched_barrier(0);
-        // dp[t][r] = d_phi[edge je][channel (4 hi + r) T + t]
-        floatx4 dp[T];
+        // d_phi per channel tile t, dp[r] = d_phi[edge je][channel (4 hi + r) T + t] on the
+        // 16 x 16 x 4 products, consumed at once by d_h = d_phi W^T on the 4 x 4 x 1 products
+        // (no padded output columns, unlike the 16 x 16 x 4 form whose N = 16 would hold
+        // K = 8 functions): block b = 4 hi + lo / 4 takes edges 4 (lo / 4) + i of the tile
+        // (A: the lane's own d_phi) and functions k = 4 kh + j (B: W[k][c]) over the 32
+        // channels (4 hi + r) T + t of its quarter hi; lane 4 b + j receives D[b][i][j] in
+        // register i
+        float yb[KS];
 #pragma unroll
-        for (int t = 0; t < T; ++t) dp[t] = floatx4{0.f, 0.f, 0.f, 0.f};
+        for (int s = 0; s < KS; ++s) yb[s] = ys[je * kSY + 4 * s + hi];
+        floatx4 dq0 = floatx4{0.f, 0.f, 0.f, 0.f}, dq1 = dq0;
+        const float* wp0 = sWp + ((lo & 3) * 4 + hi) * SWP;
+        const float* wp1 = wp0 + 16 * SWP;  // k + 4
 #pragma unroll
-        for (int s = 0; s < KS; ++s) {
-          const float b = ys[je * kSY + 4 * s + hi];
+        for (int t = 0; t < T; ++t) {
+          floatx4 dp = floatx4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-          for (int t = 0; t < T; ++t) dp[t] = mfma_16x16x4(gA[t][s], b, dp[t]);
+          for (int s = 0; s < KS; ++s) dp = mfma_16x16x4(gA[t][s], yb[s], dp);
+          const float4 w0 = *reinterpret_cast<const float4*>(wp0 + 4 * t);
+          const float4 w1 = *reinterpret_cast<const float4*>(wp1 + 4 * t);
+          dq0 = mfma_4x4x1(dp[0], w0.x, dq0);
+          dq1 = mfma_4x4x1(dp[0], w1.x, dq1);
+          dq0 = mfma_4x4x1(dp[1], w0.y, dq0);
+          dq1 = mfma_4x4x1(dp[1], w1.y, dq1);
+          dq0 = mfma_4x4x1(dp[2], w0.z, dq0);
+          dq1 = mfma_4x4x1(dp[2], w1.z, dq1);
+          dq0 = mfma_4x4x1(dp[3], w0.w, dq0);
+          dq1 = mfma_4x4x1(dp[3], w1.w, dq1);
         }
-        floatx4 dh = floatx4{0.f, 0.f, 0.f, 0.f};
+        // sum the four channel quarters (a fixed butterfly): dq{kh}[i] is then
+        // d_h[edge 16 tau + 4 (lo / 4) + i][k = 4 kh + lo % 4] on every hi
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          float wb[T];
-          load_run<T>(wrow + (4 * hi + r) * T, wb);
-#pragma unroll
-          for (int t = 0; t < T; ++t) dh = mfma_16x16x4(dp[t][r], wb[t], dh);
+        for (int i = 0; i < 4; ++i) {
+          dq0[i] += __shfl_xor(dq0[i], 16, kWave);
+          dq1[i] += __shfl_xor(dq1[i], 16, kWave);
+          dq0[i] += __shfl_xor(dq0[i], 32, kWave);
+          dq1[i] += __shfl_xor(dq1[i], 32, kWave);
         }
-        // dh[r] = d_h[edge 16 tau + 4 hi + r][k lo]
         if constexpr (RAD) {
-          // into the rows of this tile, whose h was read above
-          wave_sync();
+          wave_sync();  // d_h goes into the rows of this tile, whose h was read above
+          if (hi == 0) {
 #pragma unroll
-          for (int r = 0; r < 4; ++r)
-            if (lo < kLinKMax) hs[(16 * tau + 4 * hi + r) * kSH + lo] = dh[r];
+            for (int i = 0; i < 4; ++i) {
+              float* row_h = hs + (16 * tau + 4 * (lo >> 2) + i) * kSH + (lo & 3);
+              row_h[0] = dq0[i];
+              row_h[4] = dq1[i];
+            }
+          }
         } else {
 #pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const int j = 16 * tau + 4 * hi + r;
+          for (int i = 0; i < 4; ++i) {
+            const int j = 16 * tau + 4 * (lo >> 2) + i;
             const int ej = __shfl(my_e, j);
-            if (j < cnt && lo < K) d_h[(int64_t)ej * K + lo] = dh[r];
+            if (hi == 0 && j < cnt) {
+              if ((lo & 3) < K) d_h[(int64_t)ej * K + (lo & 3)] = dq0[i];
+              if (4 + (lo & 3) < K) d_h[(int64_t)ej * K + 4 + (lo & 3)] = dq1[i];
+            }
           }
         }
       }

@@ -111,6 +111,13 @@ __device__ __forceinline__ floatx4 mfma_16x16x4(float a, float b, floatx4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
 }
 
+// v_mfma_f32_4x4x1f32, 16 independent 4 x 4 x 1 blocks: lane 4 b + i supplies A[b][i],
+// lane 4 b + j supplies B[b][j], and lane 4 b + j receives D[b][i][j] in register i
+// (checked on gfx950 with a lane-index probe).
+__device__ __forceinline__ floatx4 mfma_4x4x1(float a, float b, floatx4 c) {
+  return __builtin_amdgcn_mfma_f32_4x4x1f32(a, b, c, 0, 0, 0);
+}
+
 // N consecutive floats at p (vector accesses: p is 4N-byte aligned within 16 bytes)
 template <int N>
 __device__ __forceinline__ void load_run(const float* __restrict__ p, float* v) {
