@@ -217,10 +217,13 @@ __global__ __launch_bounds__(256, 4) void lin_msg_fwd_kernel(
         float a[4];
 #pragma unroll
         for (int r = 0; r < 4; ++r) a[r] = ys[(16 * tau + 4 * r + hi) * kSY + lo];
+        // k-steps past the batch's end are skipped (wave-uniform branches)
 #pragma unroll
         for (int r = 0; r < 4; ++r)
+          if (r == 0 || 16 * tau + 4 * r < cnt) {
 #pragma unroll
-          for (int t = 0; t < T; ++t) acc[t] = mfma_16x16x4(a[r], ph[t][r], acc[t]);
+            for (int t = 0; t < T; ++t) acc[t] = mfma_16x16x4(a[r], ph[t][r], acc[t]);
+          }
       }
       wave_sync();  // ys is rewritten by the next batch
     }
