@@ -13,7 +13,7 @@ the GPU with inputs resident in HBM. The neighbor list is timed separately (``ne
 Prints one JSON line. ``value`` = edges / (forward + force/stress backward time).
 ``roofline`` is the dominant kernel's algorithmic work per launch (HBM bytes, or fp32
 matrix-core flops when those bound it) divided by its mean launch time, measured with
-HIP events on its launch stream during the timed steps.
+HIP events on its launch stream over back-to-back launches on the workload's inputs.
 ``cpu_baseline`` times the oracle's PyTorch-CPU restatement of the same step on the
 host cores (rank 0, N = 1 only).
 """
@@ -101,6 +101,66 @@ def step_bytes(E: int, N: int, C: int, L: int, K: int, msg: str) -> int:
     linear = 2 * (E * 4 * (K + C)) if msg == "xnn_sh_message_sum" else 0  # u @ W, d_phi @ W^T
     return (E * 24 + N * 12 + feat + kc[msg]["bytes"] + N * 4 * C * L + N * 4 * C * L
             + kc[msg + "_backward"]["bytes"] + kc["xnn_edge_force_reduce"]["bytes"] + linear)
+
+
+def message_launches(msg: str, g, model, kw: dict) -> dict:
+    """The C-ABI calls of the step's message kernels, forward and backward, on the
+    workload's own inputs (edge vectors, weights, a random node cotangent), as
+    ``name -> (args, keep)``: replayed back to back they time one launch without the host
+    gaps of the eager step."""
+    from xnn_amd import _lib
+    from xnn_amd.ops import _params
+    feat = model.edge_feat
+    plan = g.plan()
+    vec = g.edge_vectors().detach().float().contiguous()
+    E, N = vec.shape[0], g.num_nodes
+    C, L = kw["channels"], (kw["l_max"] + 1) ** 2
+    W = model.W.detach().float().contiguous()
+    K = W.shape[0]
+    gen = torch.Generator(device=vec.device).manual_seed(0)
+    d_out = torch.randn((N, C, L), device=vec.device, generator=gen)
+    out = torch.empty((N, C, L), device=vec.device)
+    g_vec = torch.empty_like(vec)
+    s = _lib.stream(vec.device)
+    rbf = feat.rbf
+    table = feat._table().detach().float().contiguous()
+    prm = _params([K, _lib.BASIS[feat.radial_type], _lib.ENVELOPE[feat.envelope_type],
+                   int(getattr(feat.envelope, "p", 1)), kw["l_max"], model.sh_sign],
+                  [float(feat.cutoff), float(getattr(rbf, "norm", 1.0)),
+                   float(getattr(rbf, "gamma", 1.0))])
+    head = (_lib.XNN_F32, _lib.ptr(vec), None, N, None, 0, None, None, None, E,
+            _lib.ptr(plan.ptr_dst), _lib.ptr(plan.perm_dst))
+    keep = (vec, W, d_out, out, g_vec, table, plan)
+    if msg == "xnn_sh_radial_message_sum":
+        return {msg: (head + (prm, _lib.ptr(table), C, _lib.ptr(W), _lib.ptr(out), s), keep),
+                msg + "_backward": (head + (prm, _lib.ptr(table), C, _lib.ptr(W),
+                                            _lib.ptr(d_out), _lib.ptr(g_vec), s), keep)}
+    if msg == "xnn_sh_linear_message_sum":
+        h = feat.radial(vec).detach().contiguous()
+        d_h = torch.empty_like(h)
+        keep = keep + (h, d_h)
+        tail = (kw["l_max"], model.sh_sign, K, C, _lib.ptr(h), _lib.ptr(W))
+        return {msg: (head + tail + (_lib.ptr(out), s), keep),
+                msg + "_backward": (head + tail + (_lib.ptr(d_out), _lib.ptr(d_h),
+                                                   _lib.ptr(g_vec), s), keep)}
+    return {}
+
+
+def replay_launch_us(name: str, args: tuple, reps: int = 40) -> float:
+    """Mean duration of ``reps`` back-to-back launches of a C-ABI entry point, between HIP
+    events recorded on the stream the kernels run on."""
+    from xnn_amd import _lib
+    fn = getattr(_lib.load(), name)
+    for _ in range(3):
+        _lib.check(name, fn(*args))
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    start.record()
+    for _ in range(reps):
+        fn(*args)
+    end.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / reps * 1e3
 
 
 def build_workload(config: str, device):
@@ -357,8 +417,15 @@ def main() -> None:
             total_us[name] = float(np.sum(d)) / args.steps       # per step, all launches
     _lib.timed.clear()
     kc = kernel_costs(E, N, C, L, kw["n_rbf"], grouped=g.plan().perm_dst is None)
-    dominant = max(per_kernel, key=lambda k: total_us[k])
-    launch_s = per_kernel[dominant] * 1e-6
+    # the eager step's events also hold the host's launch gaps; the message kernels are
+    # timed again back to back, the figure the roofline uses
+    replay_us = {}
+    for name, (call_args, _keep) in message_launches(msg, g, model, kw).items():
+        replay_us[name] = replay_launch_us(name, call_args)
+        total_us[name] = replay_us[name]
+    dominant = max(total_us, key=lambda k: total_us[k])
+    launch_us = replay_us.get(dominant, per_kernel.get(dominant))
+    launch_s = launch_us * 1e-6
     cost = kc[dominant]
     # the bound is whichever resource the kernel's compulsory work needs longer on
     t_hbm = cost["bytes"] / (HBM_PEAK_GBS * 1e9)
@@ -375,7 +442,9 @@ def main() -> None:
     roofline.update({"traffic": measured_traffic(dominant, workload),
                      "algorithmic_bytes": cost["bytes"], "algorithmic_flops": cost["flops"],
                      "hbm_GBs": round(cost["bytes"] / launch_s / 1e9, 1),
-                     "mean_launch_us": round(per_kernel[dominant], 2)})
+                     "mean_launch_us": round(launch_us, 2),
+                     "timing": ("back-to-back launches, HIP events on the launch stream"
+                                if dominant in replay_us else "eager step, HIP events")})
     sb = step_bytes(E, N, C, L, kw["n_rbf"], msg)
     step_gbs = sb / (ms * 1e-3) / 1e9
     result = {
@@ -391,7 +460,8 @@ def main() -> None:
                    "fused_linear": fused, "message_kernel": msg,
                    "step_algorithmic_bytes": sb,
                    "step_hbm_fraction": round(step_gbs / HBM_PEAK_GBS, 4),
-                   "kernel_mean_us": {k: round(v, 2) for k, v in per_kernel.items()}},
+                   "kernel_mean_us": {k: round(v, 2) for k, v in replay_us.items()},
+                   "eager_kernel_event_us": {k: round(v, 2) for k, v in per_kernel.items()}},
         "roofline": roofline,
     }
     if args.cpu_edges > 0:
