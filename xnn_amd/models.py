@@ -59,6 +59,9 @@ class InteratomicPotential(nn.Module):
     # data.edge_vectors(): ForceStressOutput then takes the strain derivative from the
     # edge-vector backward instead of deforming positions and cell
     edge_virial = False
+    # True when ``energy`` is exactly the structure sum of ``node_energy`` (ForceStressOutput
+    # then differentiates the node energies directly)
+    energy_is_node_sum = False
 
     def forward(self, data) -> dict:
         raise NotImplementedError
@@ -98,6 +101,8 @@ class ShEdgePotential(InteratomicPotential):
     """
 
     edge_virial = True
+    # energy = structure_sum(node_energy), nothing added at the structure level
+    energy_is_node_sum = True
 
     def __init__(self, species: Sequence[int] = (1, 6, 7, 8), n_rbf: int = 8, l_max: int = 3,
                  channels: int = 128, cutoff: float = 5.0, radial_type: str = "bessel",

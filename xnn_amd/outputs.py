@@ -29,6 +29,15 @@ class ForceStressOutput(nn.Module):
         self.compute_stress = compute_stress
         self.cutoff = getattr(model, "cutoff", None)
 
+    @staticmethod
+    def _zero_strain(data) -> Tensor:
+        # a fresh leaf per call: a leaf kept across calls would keep the gradient
+        # accumulator of the call that first used it, bound to that call's stream; a later
+        # call under stream capture would then synchronize the capturing stream with that
+        # other stream (autograd's producer/consumer stream sync), which breaks the capture
+        return torch.zeros((data.num_graphs, 3, 3), dtype=data.pos.dtype,
+                           device=data.pos.device, requires_grad=True)
+
     def forward(self, data) -> dict:
         create_graph = self.training
         strain: Optional[Tensor] = None
@@ -42,16 +51,14 @@ class ForceStressOutput(nn.Module):
                  and data.pos.is_cuda and bool(getattr(self.model, "edge_virial", False))
                  and not torch.cuda.is_current_stream_capturing())
         if probe:
-            strain = torch.zeros((data.num_graphs, 3, 3), dtype=data.pos.dtype,
-                                 device=data.pos.device, requires_grad=True)
+            strain = self._zero_strain(data)
             data.strain_probe = strain
             if not data.pos.requires_grad:       # a fresh leaf; the caller's tensor is untouched
                 data.pos = data.pos.detach().requires_grad_(True)
         elif self.compute_stress and data.cell is not None and data.pos.is_cuda and not create_graph:
             # one HIP kernel each way instead of the broadcast products (differentiable once)
             from .ops import strain_apply_op
-            strain = torch.zeros((data.num_graphs, 3, 3), dtype=data.pos.dtype,
-                                 device=data.pos.device, requires_grad=True)
+            strain = self._zero_strain(data)
             batch32, node_ptr = _layout(data)
             data.pos, cell = strain_apply_op(data.pos.contiguous(),
                                              data.cell.reshape(-1, 3, 3).to(data.pos.dtype).contiguous(),
@@ -94,9 +101,20 @@ class ForceStressOutput(nn.Module):
         g = {k: None for k in need}
         if inputs and energy.requires_grad:
             # the backward is seeded with -1: it returns d(-E), so the forces need no extra
-            # negation (negation is exact, the result is bitwise -dE/dpos)
-            grads = torch.autograd.grad([energy], inputs,
-                                        grad_outputs=[torch.full_like(energy, -1.0)],
+            # negation (negation is exact, the result is bitwise -dE/dpos). A model whose
+            # energy is exactly the structure sum of its node energies is differentiated
+            # from the node energies (dE/dE_i = 1), skipping the sum's backward.
+            target = energy
+            seed = None
+            node_energy = out.get("node_energy")
+            if (not create_graph and bool(getattr(self.model, "energy_is_node_sum", False))
+                    and node_energy is not None and node_energy.requires_grad):
+                target = node_energy
+                seed = torch.full((1,), -1.0, dtype=node_energy.dtype,
+                                  device=node_energy.device).expand(node_energy.shape)
+            else:
+                seed = torch.full_like(energy, -1.0)
+            grads = torch.autograd.grad([target], inputs, grad_outputs=[seed],
                                         create_graph=create_graph, retain_graph=create_graph,
                                         allow_unused=True)
             g = dict(zip(need, grads))
