@@ -448,7 +448,8 @@ def main() -> None:
     sb = step_bytes(E, N, C, L, kw["n_rbf"], msg)
     step_gbs = sb / (ms * 1e-3) / 1e9
     result = {
-        "metric": "edges/s fwd+force-bwd and % HBM roofline, 9k-atom water box, 1 MI355X",
+        "metric": ("edges/s fwd+force-bwd and % HBM roofline, 9k-atom water box, 1 MI355X"
+                   if args.config == "water" else f"edges/s fwd+force-bwd, {workload}, 1 MI355X"),
         "value": E / (ms * 1e-3), "unit": "edges/s", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": ms, "higher_is_better": True, "scaling": "weak",
         "vs_baseline": None, "dtype": "f32", "data": "synthetic (seeded generator, random-init weights)",

@@ -640,19 +640,19 @@ def test_training_step_differentiates_forces_twice():
         np.testing.assert_allclose(a, b, rtol=1e-9, atol=1e-9)
 
 
-def test_graph_replays_match_the_eager_step():
+@pytest.mark.parametrize("edge_virial", [False, True])
+def test_graph_replays_match_the_eager_step(edge_virial):
     """The whole step captured as one HIP graph: every replay, with eager work and
-    synchronizations between replays, reproduces the eager forces, stress and energy."""
+    synchronizations between replays, reproduces the eager forces, stress and energy; with
+    the strain deformation and with the edge-virial form of the stress."""
     import copy
     import xnn_amd as xa
     from xnn_amd import synthetic
-    _note("HIP graph replay")
+    _note(f"HIP graph replay edge_virial={edge_virial}")
     s = synthetic.water_box(n_molecules=216, box=18.6, grid=6, seed=4)
     g = xa.structure_to_graph(s.as_dict(), 5.0, device=DEV)
     model = xa.ShEdgePotential(n_rbf=8, l_max=3, channels=64, cutoff=5.0, seed=1).to(DEV)
-    # a captured step deforms positions and cell for the stress (the edge-virial path is
-    # off under capture); the eager steps take the same path so that they compare bitwise
-    model.edge_virial = False
+    model.edge_virial = edge_virial
     wrapped = xa.ForceStressOutput(model, compute_stress=True).eval()
     g.plan()
 

@@ -107,6 +107,25 @@ def test_reference_formulation_equals_the_oracle(radial, envelope, sign):
         torch.set_default_dtype(old)
 
 
+def test_force_stress_output_leaves_the_callers_tensors_alone():
+    """Forces are taken against a fresh leaf per call: the caller's positions stay a plain
+    tensor (a leaf kept across calls would carry one call's gradient accumulator, and its
+    stream, into the next), and two calls on the same graph agree."""
+    import copy
+    import xnn_amd as xa
+    from xnn_amd import synthetic
+    s = synthetic.water_box(n_molecules=8, box=6.2, grid=2, seed=5)
+    g = xa.structure_to_graph(s.as_dict(), 4.0)
+    model = xa.ShEdgePotential(n_rbf=4, l_max=1, channels=4, cutoff=4.0)
+    for stress in (False, True):
+        wrapped = xa.ForceStressOutput(model, compute_stress=stress)
+        a = wrapped(copy.copy(g))
+        b = wrapped(copy.copy(g))
+        assert not g.pos.requires_grad and g.pos.grad_fn is None
+        assert not g.cell.requires_grad
+        torch.testing.assert_close(a["forces"], b["forces"], rtol=0, atol=0)
+
+
 def test_collate_offsets_and_batch():
     import xnn_amd as xa
     from xnn_amd import synthetic

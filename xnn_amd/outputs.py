@@ -45,16 +45,11 @@ class ForceStressOutput(nn.Module):
         # (``edge_virial``) gets the strain derivative from the edge-vector backward itself,
         # sym(sum_e r_e (x) dE/dr_e), the same derivative as deforming pos and cell by the
         # strain; the training step (create_graph) and the CPU keep the deformation.
-        # Under HIP graph capture the deformation is kept: the capture of this path ended
-        # in a host crash in capture_end (cause not found), so it is switched off there.
         probe = (self.compute_stress and data.cell is not None and not create_graph
-                 and data.pos.is_cuda and bool(getattr(self.model, "edge_virial", False))
-                 and not torch.cuda.is_current_stream_capturing())
+                 and data.pos.is_cuda and bool(getattr(self.model, "edge_virial", False)))
         if probe:
             strain = self._zero_strain(data)
             data.strain_probe = strain
-            if not data.pos.requires_grad:       # a fresh leaf; the caller's tensor is untouched
-                data.pos = data.pos.detach().requires_grad_(True)
         elif self.compute_stress and data.cell is not None and data.pos.is_cuda and not create_graph:
             # one HIP kernel each way instead of the broadcast products (differentiable once)
             from .ops import strain_apply_op
@@ -73,8 +68,13 @@ class ForceStressOutput(nn.Module):
             else:
                 data.pos = data.pos + (data.pos[:, :, None] * sym.index_select(0, data.batch)).sum(1)
             data.cell = data.cell + (data.cell[:, :, :, None] * sym[:, None]).sum(2)
-        if self.compute_forces:
-            data.pos.requires_grad_(True)
+        if self.compute_forces and not data.pos.requires_grad:
+            # a fresh leaf per call; the caller's tensor is left untouched. Turning the
+            # caller's positions into a leaf would keep one gradient accumulator across
+            # calls, bound to the stream of the call that made it, and autograd would sync a
+            # later call's stream with that one -- which breaks HIP graph capture (a host
+            # crash in capture_end) when the later call is captured.
+            data.pos = data.pos.detach().requires_grad_(True)
         # the double-backward of a training step needs the differentiable formulation
         if hasattr(self.model, "double_backward"):
             self.model.double_backward = bool(create_graph)
