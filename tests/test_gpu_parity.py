@@ -298,13 +298,14 @@ def test_sh_linear_message_sum_forward_backward(C, l_max, K):
     assert torch.equal(A, A2)
 
 
-@pytest.mark.parametrize("C,l_max,K,radial,envelope,sign",
-                         [(128, 3, 8, "bessel", "polynomial", 1),
-                          (64, 2, 8, "bessel", "cosine", -1),
-                          (128, 3, 8, "bessel_detuned", "polynomial", 1),
-                          (32, 1, 6, "gaussian", "polynomial", 1),
-                          (128, 3, 4, "gaussian", "cosine", 1)])
-def test_sh_radial_message_sum_forward_backward(C, l_max, K, radial, envelope, sign):
+@pytest.mark.parametrize("C,l_max,K,radial,envelope,sign,rc",
+                         [(128, 3, 8, "bessel", "polynomial", 1, 5.0),
+                          (64, 2, 8, "bessel", "cosine", -1, 5.0),
+                          (128, 3, 8, "bessel_detuned", "polynomial", 1, 5.0),
+                          (32, 1, 6, "gaussian", "polynomial", 1, 5.0),
+                          (128, 3, 4, "gaussian", "cosine", 1, 5.0),
+                          (128, 3, 8, "bessel", "polynomial", 1, 6.5)])
+def test_sh_radial_message_sum_forward_backward(C, l_max, K, radial, envelope, sign, rc):
     """Radial basis, linear layer and message in one kernel each way, against the oracle's
     radial features (radial.py / cutoff.py restated), materialized messages and float64
     autograd; also against the two-kernel composition (edge_embed + the fused linear
@@ -314,12 +315,15 @@ def test_sh_radial_message_sum_forward_backward(C, l_max, K, radial, envelope, s
     from xnn_amd import synthetic
     from xnn_amd.featurizers import SphericalHarmonicEdgeEmbedding
     from xnn_amd.ops import sh_linear_message_sum
-    _note(f"sh_radial_message_sum C={C} l_max={l_max} K={K} {radial} {envelope} sign={sign}")
+    _note(f"sh_radial_message_sum C={C} l_max={l_max} K={K} {radial} {envelope} sign={sign} rc={rc}")
     s = synthetic.water_box(n_molecules=216, box=18.6, grid=6, seed=4)
-    g = xa.structure_to_graph(s.as_dict(), 5.0, device=DEV)
+    g = xa.structure_to_graph(s.as_dict(), rc, device=DEV)
+    if rc > 6.0:
+        # receiver rows longer than one 64-edge batch
+        assert int(torch.bincount(g.edge_index[1]).max()) > 64
     g.pos = g.pos.float()
     vec = g.edge_vectors().detach().requires_grad_(True)
-    emb = SphericalHarmonicEdgeEmbedding(l_max=l_max, n_rbf=K, cutoff=5.0,
+    emb = SphericalHarmonicEdgeEmbedding(l_max=l_max, n_rbf=K, cutoff=rc,
                                          radial_type=radial.split("_")[0],
                                          envelope=envelope).to(DEV)
     freqs = None
@@ -339,11 +343,11 @@ def test_sh_radial_message_sum_forward_backward(C, l_max, K, radial, envelope, s
     Y = R.e3nn_sh(l_max, vc if sign == 1 else -vc)
     length = torch.linalg.norm(vc, dim=-1)
     if freqs is None:
-        rad = R.radial_features(length, K, 5.0, radial, envelope)
+        rad = R.radial_features(length, K, rc, radial, envelope)
     else:
-        env = (R.polynomial_envelope(length, 5.0, 6) if envelope == "polynomial"
-               else R.cosine_envelope(length, 5.0))
-        rad = R.bessel(length, K, 5.0, freqs=freqs.cpu().double()) * env[:, None]
+        env = (R.polynomial_envelope(length, rc, 6) if envelope == "polynomial"
+               else R.cosine_envelope(length, rc))
+        rad = R.bessel(length, K, rc, freqs=freqs.cpu().double()) * env[:, None]
     phi = rad @ W.cpu().double()
     msg = (phi[:, :, None] * Y[:, None, :]).reshape(vc.shape[0], -1)
     Ar = R.scatter_sum(msg, g.edge_index[1].cpu(), g.num_nodes).reshape(A.shape)

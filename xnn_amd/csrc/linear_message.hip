@@ -185,6 +185,9 @@ __global__ __launch_bounds__(256, 4) void lin_msg_fwd_kernel(
       }
       wave_sync();
       const int ntile = (cnt + 15) >> 4;
+      // the matrix-core phase runs at a raised wave priority, so that the issue arbiter
+      // keeps feeding it while other waves evaluate harmonics or wait on memory
+      __builtin_amdgcn_s_setprio(1);
 #pragma unroll 1
       for (int tau = 0; tau < ntile; ++tau) {
         if constexpr (RAD) {
@@ -225,6 +228,7 @@ __global__ __launch_bounds__(256, 4) void lin_msg_fwd_kernel(
             for (int t = 0; t < T; ++t) acc[t] = mfma_16x16x4(a[r], ph[t][r], acc[t]);
           }
       }
+      __builtin_amdgcn_s_setprio(0);
       wave_sync();  // ys is rewritten by the next batch
     }
     // lane holds A[row, channel lo T + t, lm 4 hi + r]
@@ -370,6 +374,7 @@ __global__ __launch_bounds__(256, 3) void lin_msg_bwd_kernel(
       }
       wave_sync();
       const int ntile = (cnt + 15) >> 4;
+      __builtin_amdgcn_s_setprio(1);  // the matrix-core phase (see the forward)
 #pragma unroll 1
       for (int tau = 0; tau < ntile; ++tau) {
         const int je = 16 * tau + lo;
@@ -470,6 +475,7 @@ __global__ __launch_bounds__(256, 3) void lin_msg_bwd_kernel(
           }
         }
       }
+      __builtin_amdgcn_s_setprio(0);
       wave_sync();
       if (want_vec && lane < cnt) {
         // d|r| from the radial features first, then the harmonics' share (kept apart so

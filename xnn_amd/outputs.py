@@ -48,7 +48,9 @@ class ForceStressOutput(nn.Module):
         probe = (self.compute_stress and data.cell is not None and not create_graph
                  and data.pos.is_cuda and bool(getattr(self.model, "edge_virial", False)))
         if probe:
-            strain = self._zero_strain(data)
+            # the probe's value is never read (zero by contract): no fill launch
+            strain = torch.empty((data.num_graphs, 3, 3), dtype=data.pos.dtype,
+                                 device=data.pos.device, requires_grad=True)
             data.strain_probe = strain
         elif self.compute_stress and data.cell is not None and data.pos.is_cuda and not create_graph:
             # one HIP kernel each way instead of the broadcast products (differentiable once)
