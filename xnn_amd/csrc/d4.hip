@@ -39,7 +39,29 @@ constexpr int kD4Sub = 64;      // sources per LDS stage
 constexpr int kD4MaxChunks = 128;
 constexpr int kNW = 23;         // Casimir-Polder frequencies
 constexpr double kBohr = 0.5291772109044924;
+constexpr double kInvBohr = 1.0 / kBohr;
 constexpr double kSqrtPi = 1.7724538509055160273;
+
+// 1 / x for positive normal x: the hardware estimate (v_rcp_f64) refined by two
+// Newton-Raphson steps y <- y (2 - x y), to about an ulp (the IEEE-exact division costs
+// several times more and these terms need no exact rounding)
+__device__ __forceinline__ double rcp_nr(double x) {
+  double y = __builtin_amdgcn_rcp(x);
+  double e = fma(-x, y, 1.0);
+  y = fma(y, e, y);
+  e = fma(-x, y, 1.0);
+  return fma(y, e, y);
+}
+
+// 1 / sqrt(x) for positive normal x: v_rsq_f64 refined by two Newton-Raphson steps
+// y <- y (3 - x y^2) / 2
+__device__ __forceinline__ double rsq_nr(double x) {
+  double y = __builtin_amdgcn_rsq(x);
+  const double h = 0.5 * x;
+  y = y * fma(-h * y, y, 1.5);
+  y = y * fma(-h * y, y, 1.5);
+  return y;
+}
 
 struct D4Work {
   int64_t chunk;   // source atoms per chunk (multiple of kD4Sub)
@@ -65,6 +87,7 @@ static D4Work d4_work(int64_t n_nodes, int64_t n_graphs, int64_t max_atoms) {
 // columns of the inverse cell scaled to interplanar spacings (for image pruning).
 struct Lattice {
   double a[9];
+  double ab[9];    // cell rows in bohr
   double inv[9];   // inverse cell, f = d @ inv
   double sp[3];    // interplanar spacing per axis, 1 / |inv[:, axis]|
   int n0, n1, n2;
@@ -123,13 +146,16 @@ __device__ inline void load_lattice(const double* __restrict__ cell,
                                     const int32_t* __restrict__ images, int b, Lattice& L) {
   if (cell == nullptr) {
 #pragma unroll
-    for (int k = 0; k < 9; ++k) L.a[k] = L.inv[k] = 0.0;
+    for (int k = 0; k < 9; ++k) L.a[k] = L.ab[k] = L.inv[k] = 0.0;
     L.sp[0] = L.sp[1] = L.sp[2] = 1e300;
     L.n0 = L.n1 = L.n2 = 0;
     return;
   }
 #pragma unroll
-  for (int k = 0; k < 9; ++k) L.a[k] = cell[9 * (int64_t)b + k];
+  for (int k = 0; k < 9; ++k) {
+    L.a[k] = cell[9 * (int64_t)b + k];
+    L.ab[k] = L.a[k] * kInvBohr;
+  }
   L.n0 = images[3 * b + 0];
   L.n1 = images[3 * b + 1];
   L.n2 = images[3 * b + 2];
@@ -242,32 +268,39 @@ __global__ __launch_bounds__(64) void d4_cn_kernel(
         const double den = fabs(eni - en[sj]) + prm.k5;
         enf = prm.k4 * exp(-den * den / prm.k6);
       }
+      // per pair: k0 / rc and the erf count's slope factor -k0 / (rc sqrt(pi))
+      const double k_rc = prm.kcn / rc;
+      const double dk = -k_rc / kSqrtPi;
       const double dx = xi - st.x[jj], dy = yi - st.y[jj], dz = zi - st.z[jj];
+      const double bx = dx * kInvBohr, by = dy * kInvBohr, bz = dz * kInvBohr;
       const double wsum = BACKWARD ? gi + st.w[jj] : 0.0;
       const double w2sum = BACKWARD ? g2i + st.w2[jj] : 0.0;
       int lo[3], hi[3];
       image_window(L, dx, dy, dz, cmax * kBohr, lo, hi);
       for (int n0 = lo[0]; n0 <= hi[0]; ++n0)
-        for (int n1 = lo[1]; n1 <= hi[1]; ++n1)
+        for (int n1 = lo[1]; n1 <= hi[1]; ++n1) {
+          // the image's vector in bohr, d + n @ cell
+          const double px = bx + n0 * L.ab[0] + n1 * L.ab[3];
+          const double py = by + n0 * L.ab[1] + n1 * L.ab[4];
+          const double pz = bz + n0 * L.ab[2] + n1 * L.ab[5];
           for (int n2 = lo[2]; n2 <= hi[2]; ++n2) {
-            const double vx = (dx + (n0 * L.a[0] + n1 * L.a[3] + n2 * L.a[6])) / kBohr;
-            const double vy = (dy + (n0 * L.a[1] + n1 * L.a[4] + n2 * L.a[7])) / kBohr;
-            const double vz = (dz + (n0 * L.a[2] + n1 * L.a[5] + n2 * L.a[8])) / kBohr;
+            const double vx = px + n2 * L.ab[6], vy = py + n2 * L.ab[7], vz = pz + n2 * L.ab[8];
             const double r2 = vx * vx + vy * vy + vz * vz;
             if (r2 <= 0.0 || r2 > cmax * cmax) continue;
-            const double r = sqrt(r2);
+            const double rinv = rsq_nr(r2);
+            const double r = r2 * rinv;
             const bool in_cn = r <= prm.cut_cn, in_eeq = !D3 && r <= prm.cut_eeq;
             double count, dcount;
             if (D3) {
               // 1 / (1 + exp(-k1 (rc / r - 1))) (d3.py:632-642); d/dr = -s (1 - s) k1 rc / r^2
-              const double sg = 1.0 / (1.0 + exp(-prm.kcn * (rc / r - 1.0)));
+              const double sg = rcp_nr(1.0 + exp(-prm.kcn * (rc * rinv - 1.0)));
               count = sg;
-              dcount = -sg * (1.0 - sg) * prm.kcn * rc / r2;
+              dcount = -sg * (1.0 - sg) * prm.kcn * rc * rinv * rinv;
             } else {
               // (1 + erf(-k0 (r - rc) / rc)) / 2; d/dr = -k0 exp(-x^2) / (rc sqrt(pi))
-              const double x = -prm.kcn * (r - rc) / rc;
+              const double x = k_rc * (rc - r);
               count = 0.5 * (1.0 + erf(x));
-              dcount = -prm.kcn * exp(-x * x) / (rc * kSqrtPi);
+              dcount = BACKWARD ? dk * exp(-x * x) : 0.0;
             }
             if (!BACKWARD) {
               if (in_cn) acc[0] += enf * count;
@@ -276,7 +309,7 @@ __global__ __launch_bounds__(64) void d4_cn_kernel(
               const double both = (in_cn ? wsum * enf : 0.0) + (in_eeq ? w2sum : 0.0);
               const double own = (in_cn ? gi * enf : 0.0) + (in_eeq ? g2i : 0.0);
               // per Angstrom of the edge vector: d r_bohr / d v = v_bohr / (r bohr)
-              const double s = dcount / (r * kBohr);
+              const double s = dcount * rinv * kInvBohr;
               acc[0] += both * s * vx;
               acc[1] += both * s * vy;
               acc[2] += both * s * vz;
@@ -286,6 +319,7 @@ __global__ __launch_bounds__(64) void d4_cn_kernel(
               acc[9] += n2 * ox; acc[10] += n2 * oy; acc[11] += n2 * oz;
             }
           }
+        }
     }
   }
   if (live) {
@@ -349,6 +383,10 @@ __global__ __launch_bounds__(64) void d4_pair_kernel(
     load_lattice(nullptr, nullptr, 0, L);
   }
   const double rc2 = prm.cutoff * prm.cutoff;
+  // below r = cutoff - width the switch is 1 with zero slope: r itself is not needed
+  const double wzone = prm.width > 0.0 ? fmax(prm.cutoff - fmin(prm.width, prm.cutoff), 0.0)
+                                       : prm.cutoff;
+  const double wz2 = wzone * wzone;
   for (int64_t base = j0; base < j1; base += kD4Sub) {
     const int cnt = (int)std::min<int64_t>(kD4Sub, j1 - base);
     __syncthreads();
@@ -371,38 +409,48 @@ __global__ __launch_bounds__(64) void d4_pair_kernel(
 #pragma unroll
       for (int w = 0; w < kNW; ++w) c6 += ai[w] * sa[w][jj];
       const double rr = 3.0 * qi * r4r2[st.sp[jj]];
+      const double s8rr = prm.s8 * rr;
       const double r0 = prm.a1 * sqrt(rr) + prm.a2;
       const double r02 = r0 * r0;
       const double r06 = r02 * r02 * r02, r08 = r06 * r02;
       const double dx = xi - st.x[jj], dy = yi - st.y[jj], dz = zi - st.z[jj];
+      const double bx = dx * kInvBohr, by = dy * kInvBohr, bz = dz * kInvBohr;
       const double wsum = BACKWARD ? gi + st.w[jj] : 0.0;
       double fsum = 0.0;  // sum over images of f(r): d E / d C6 of the pair
       int lo[3], hi[3];
       image_window(L, dx, dy, dz, prm.cutoff * kBohr, lo, hi);
       for (int n0 = lo[0]; n0 <= hi[0]; ++n0)
-        for (int n1 = lo[1]; n1 <= hi[1]; ++n1)
+        for (int n1 = lo[1]; n1 <= hi[1]; ++n1) {
+          // the image's vector in bohr, d + n @ cell
+          const double px = bx + n0 * L.ab[0] + n1 * L.ab[3];
+          const double py = by + n0 * L.ab[1] + n1 * L.ab[4];
+          const double pz = bz + n0 * L.ab[2] + n1 * L.ab[5];
           for (int n2 = lo[2]; n2 <= hi[2]; ++n2) {
-            const double vx = (dx + (n0 * L.a[0] + n1 * L.a[3] + n2 * L.a[6])) / kBohr;
-            const double vy = (dy + (n0 * L.a[1] + n1 * L.a[4] + n2 * L.a[7])) / kBohr;
-            const double vz = (dz + (n0 * L.a[2] + n1 * L.a[5] + n2 * L.a[8])) / kBohr;
+            const double vx = px + n2 * L.ab[6], vy = py + n2 * L.ab[7], vz = pz + n2 * L.ab[8];
             const double r2 = vx * vx + vy * vy + vz * vz;
             if (r2 <= 0.0 || r2 > rc2) continue;
-            const double r = sqrt(r2);
-            double sw, dsw;
-            switch_d(r, prm.cutoff, prm.width, sw, dsw);
-            const double r6 = r2 * r2 * r2, r8 = r6 * r2;
-            const double t6 = 1.0 / (r6 + r06), t8 = 1.0 / (r8 + r08);
-            const double g = prm.s6 * t6 + prm.s8 * rr * t8;
+            // t6 = 1 / (r^6 + r0^6), t8 = 1 / (r^8 + r0^8) from one reciprocal
+            const double r4 = r2 * r2, r6 = r4 * r2, r8 = r6 * r2;
+            const double p6 = r6 + r06, p8 = r8 + r08;
+            const double inv = rcp_nr(p6 * p8);
+            const double t6 = p8 * inv, t8 = p6 * inv;
+            const double g = prm.s6 * t6 + s8rr * t8;
+            double sw = 1.0, dsw_r = 0.0;  // the switch and its slope over r
+            if (r2 > wz2) {
+              const double rinv = rsq_nr(r2);
+              double dsw;
+              switch_d(r2 * rinv, prm.cutoff, prm.width, sw, dsw);
+              dsw_r = dsw * rinv;
+            }
             const double f = sw * g;
             if (!BACKWARD) {
               acc[0] += -0.5 * c6 * f;
             } else {
               fsum += f;
-              // d f / d r
-              const double dg = -prm.s6 * 6.0 * r * r2 * r2 * t6 * t6 -
-                                prm.s8 * rr * 8.0 * r * r6 * t8 * t8;
-              const double df = dsw * g + sw * dg;
-              const double s = -0.5 * c6 * df / (r * kBohr);
+              // (d f / d r) / r, and d r_bohr / d v_Angstrom = v_bohr / (r_bohr bohr)
+              const double dg_r = -6.0 * prm.s6 * r4 * t6 * t6 - 8.0 * s8rr * r6 * t8 * t8;
+              const double df_r = dsw_r * g + sw * dg_r;
+              const double s = -0.5 * kInvBohr * c6 * df_r;
               acc[0] += wsum * s * vx;
               acc[1] += wsum * s * vy;
               acc[2] += wsum * s * vz;
@@ -412,6 +460,7 @@ __global__ __launch_bounds__(64) void d4_pair_kernel(
               acc[9] += n2 * ox; acc[10] += n2 * oy; acc[11] += n2 * oz;
             }
           }
+        }
       if (BACKWARD && fsum != 0.0) {
         const double k = -0.5 * wsum * fsum;
 #pragma unroll
@@ -568,15 +617,19 @@ __global__ __launch_bounds__(64) void d3_pair_kernel(
       double fsum = 0.0;
       int lo[3], hi[3];
       image_window(L, dx, dy, dz, prm.cutoff * kBohr, lo, hi);
+      const double bx = dx * kInvBohr, by = dy * kInvBohr, bz = dz * kInvBohr;
       for (int n0 = lo[0]; n0 <= hi[0]; ++n0)
-        for (int n1 = lo[1]; n1 <= hi[1]; ++n1)
+        for (int n1 = lo[1]; n1 <= hi[1]; ++n1) {
+          // the image's vector in bohr, d + n @ cell
+          const double px = bx + n0 * L.ab[0] + n1 * L.ab[3];
+          const double py = by + n0 * L.ab[1] + n1 * L.ab[4];
+          const double pz = bz + n0 * L.ab[2] + n1 * L.ab[5];
           for (int n2 = lo[2]; n2 <= hi[2]; ++n2) {
-            const double vx = (dx + (n0 * L.a[0] + n1 * L.a[3] + n2 * L.a[6])) / kBohr;
-            const double vy = (dy + (n0 * L.a[1] + n1 * L.a[4] + n2 * L.a[7])) / kBohr;
-            const double vz = (dz + (n0 * L.a[2] + n1 * L.a[5] + n2 * L.a[8])) / kBohr;
+            const double vx = px + n2 * L.ab[6], vy = py + n2 * L.ab[7], vz = pz + n2 * L.ab[8];
             const double r2 = vx * vx + vy * vy + vz * vz;
             if (r2 <= 0.0 || r2 > rc2) continue;
-            const double r = sqrt(r2);
+            const double rinv = rsq_nr(r2);
+            const double r = r2 * rinv;
             double sw, dsw, t6, t8, d6, d8;
             switch_d(r, prm.cutoff, prm.width, sw, dsw);
             d3_damp(prm, r, r0, t6, t8, d6, d8);
@@ -587,7 +640,8 @@ __global__ __launch_bounds__(64) void d3_pair_kernel(
             } else {
               fsum += f;
               const double df = dsw * g + sw * (prm.s6 * d6 + prm.s8 * rr * d8);
-              const double s = -0.5 * c6 * df / (r * kBohr);
+              // d r_bohr / d v_Angstrom = v_bohr / (r_bohr bohr)
+              const double s = -0.5 * kInvBohr * c6 * df * rinv;
               acc[0] += wsum * s * vx;
               acc[1] += wsum * s * vy;
               acc[2] += wsum * s * vz;
@@ -597,6 +651,7 @@ __global__ __launch_bounds__(64) void d3_pair_kernel(
               acc[9] += n2 * ox; acc[10] += n2 * oy; acc[11] += n2 * oz;
             }
           }
+        }
       if (BACKWARD && fsum != 0.0) {
         const double k = -0.5 * wsum * fsum;
 #pragma unroll
