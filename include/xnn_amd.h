@@ -334,6 +334,40 @@ int xnn_d4_two_body_backward(const double* pos, int64_t n_nodes, const int32_t* 
                              double* cell_partial, double* grad_alpha, void* workspace,
                              size_t workspace_bytes, xnn_stream_t stream);
 
+/* D4 reference tables in the kernels' layout, indexed by atomic number (rows 0 ..
+ * n_elements-1), device memory: nref (n_el) int32, ngw / refcn / refq (n_el, 7) with
+ * ngw int32, zeff (n_el), gi = hardness x gc (n_el), refalpha (n_el, 7, 23) the
+ * charge-scaled reference polarizabilities (d4.py:444-500); ga and wf the DFTD4
+ * parameters (d4.py:419). */
+typedef struct {
+  int32_t n_elements;
+  const int32_t* nref;
+  const int32_t* ngw;
+  const double* refcn;
+  const double* refq;
+  const double* zeff;
+  const double* gi;
+  const double* refalpha;
+  double ga, wf;
+} xnn_d4_alpha_tables;
+
+/* alpha (N,23): the dynamic polarizabilities at the coordination numbers cn (N) and
+ * charges q (N) -- Gaussian reference weights normalised per atom, charge scaling zeta,
+ * contracted with refalpha. atomic_numbers (N) int64; one outside the tables gives NaN.
+ * Replaces DFTD4.weights / polarizabilities (d4.py:984-1042) and the alpha part of the
+ * reference's native d4_alpha (dispersion_fast/cpu.py:774-829). */
+int xnn_d4_polarizabilities(int64_t n_nodes, const int64_t* atomic_numbers, const double* cn,
+                            const double* q, const xnn_d4_alpha_tables* tables, double* alpha,
+                            xnn_stream_t stream);
+
+/* g_cn[i] = sum_k g_alpha[i,k] d alpha[i,k] / d cn[i] and g_q[i] the same in q[i] (either
+ * output may be NULL): the chain rule the reference's native kernel applies with its
+ * dacn / daq (dispersion_fast/cpu.py:774-829, D4CpuFunction.backward 1356-1376). */
+int xnn_d4_polarizabilities_backward(int64_t n_nodes, const int64_t* atomic_numbers,
+                                     const double* cn, const double* q,
+                                     const xnn_d4_alpha_tables* tables, const double* g_alpha,
+                                     double* g_cn, double* g_q, xnn_stream_t stream);
+
 /* D3 two-body dispersion on the same image walk (xnn_d4_workspace_bytes covers it).
  * cn[i] = sum_{r <= cutoff_cn} 1 / (1 + exp(-kcn (rc / r - 1))), rc = rcov_i + rcov_j
  * (bohr). Replaces DFTD3.coordination_numbers (d3.py:632-642). */

@@ -132,6 +132,50 @@ def test_kernels_match_oracle(tables, case):
                                    atol=1e-10 * float(ref["grad_cell"].abs().max()))
 
 
+def test_polarizabilities_kernel_matches_oracle(tables):
+    """alpha(i w) and its chain rule to cn and q from the HIP kernel against the oracle's
+    weights x charge scaling (float64 autograd): every tabulated element, CNs from 0 to
+    past the weight underflow (the largest-reference fallback), charges on both sides of
+    q + zeff = 0, and an atomic number outside the tables (NaN)."""
+    import oracle.d4 as D
+    import xnn_amd.dispersion as XD
+    _note("d4 polarizabilities kernel vs oracle")
+    model = XD.DFTD4(tables).to(DEV)
+    rng = np.random.default_rng(21)
+    elems = [int(e) for e in tables["elements"]]
+    z = np.array([elems[i % len(elems)] for i in range(60)])
+    cn = rng.uniform(0.0, 5.0, len(z))
+    cn[:5] = 40.0                                    # exp(-wf d^2) underflows: fallback
+    q = rng.normal(0.0, 0.4, len(z))
+    zeff = tables["zeff"][z]
+    q[5:9] = -zeff[5:9] - 0.5                        # q + zeff < 0: zeta = exp(ga)
+    zt = torch.as_tensor(z)
+    cn_t = torch.tensor(cn, requires_grad=True)
+    q_t = torch.tensor(q, requires_grad=True)
+    ref = D.dynamic_polarizabilities(zt, cn_t, q_t, tables)
+    g_alpha = torch.tensor(rng.normal(size=ref.shape))
+    ref_gcn, ref_gq = torch.autograd.grad((ref * g_alpha).sum(), [cn_t, q_t])
+    cg = cn_t.detach().to(DEV).requires_grad_(True)
+    qg = q_t.detach().to(DEV).requires_grad_(True)
+    alpha = model.polarizabilities(zt.to(DEV), cg, qg)
+    gcn, gq = torch.autograd.grad((alpha * g_alpha.to(DEV)).sum(), [cg, qg])
+    assert _lib_calls("xnn_d4_polarizabilities") and _lib_calls("xnn_d4_polarizabilities_backward")
+    np.testing.assert_allclose(alpha.detach().cpu(), ref.detach(), rtol=1e-13,
+                               atol=1e-13 * float(ref.abs().max()))
+    np.testing.assert_allclose(gcn.cpu(), ref_gcn, rtol=1e-12, atol=1e-12 * float(ref_gcn.abs().max()))
+    np.testing.assert_allclose(gq.cpu(), ref_gq, rtol=1e-12, atol=1e-12 * float(ref_gq.abs().max()))
+    assert float(gcn[:5].abs().max()) == 0.0          # the fallback weights are constant
+    bad = model.polarizabilities(torch.tensor([1, 200], device=DEV),
+                                 torch.tensor([1.0, 1.0], device=DEV, dtype=torch.float64),
+                                 torch.zeros(2, device=DEV, dtype=torch.float64))
+    assert torch.isfinite(bad[0]).all() and torch.isnan(bad[1]).all()
+
+
+def _lib_calls(name):
+    from xnn_amd import _lib
+    return _lib.calls.get(name, 0) > 0
+
+
 def test_full_molecule_with_eeq_matches_oracle_and_finite_differences(tables):
     """Charges from the EEQ solve on both sides; forces against central differences of
     the GPU energy (test_d4.py:202-215: h = 1e-4 A, 1e-7 eV/A)."""

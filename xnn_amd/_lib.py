@@ -58,6 +58,12 @@ class D4PairParams(ctypes.Structure):
                 ("width", dbl)]
 
 
+class D4AlphaTables(ctypes.Structure):
+    """``xnn_d4_alpha_tables`` (device pointers)."""
+    _fields_ = [("n_elements", i32), ("nref", vp), ("ngw", vp), ("refcn", vp), ("refq", vp),
+                ("zeff", vp), ("gi", vp), ("refalpha", vp), ("ga", dbl), ("wf", dbl)]
+
+
 class D3PairParams(ctypes.Structure):
     """``xnn_d3_pair_params``."""
     _fields_ = [("s6", dbl), ("s8", dbl), ("a1", dbl), ("a2", dbl), ("rs6", dbl), ("rs8", dbl),
@@ -98,6 +104,9 @@ _SIGNATURES = {
                                      ctypes.POINTER(D4CnParams), vp, vp, vp, vp, vp, sz, vp],
     "xnn_d4_two_body": [vp, i64, vp, vp, vp, i64, i64, vp, vp, vp, vp,
                         ctypes.POINTER(D4PairParams), vp, vp, sz, vp],
+    "xnn_d4_polarizabilities": [i64, vp, vp, vp, ctypes.POINTER(D4AlphaTables), vp, vp],
+    "xnn_d4_polarizabilities_backward": [i64, vp, vp, vp, ctypes.POINTER(D4AlphaTables), vp, vp,
+                                         vp, vp],
     "xnn_d4_two_body_backward": [vp, i64, vp, vp, vp, i64, i64, vp, vp, vp, vp,
                                  ctypes.POINTER(D4PairParams), vp, vp, vp, vp, vp, sz, vp],
     "xnn_d3_coordination": [vp, i64, vp, vp, vp, i64, i64, vp, vp, vp, dbl, dbl, vp, vp, sz, vp],

@@ -669,25 +669,46 @@ __global__ __launch_bounds__(64) void d3_pair_kernel(
   }
 }
 
-// out[i * nk + (k - k0)] = sum over chunk slots cy (in order) of partial[cy][k][i], for
-// the components k0 <= k < k0 + nk of a partial array of np components
-__global__ void d4_reduce_kernel(const double* __restrict__ partial, int64_t n_nodes, int np,
-                                 int k0, int nk, int64_t n_cy, double* __restrict__ out) {
-  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (idx >= n_nodes * nk) return;
-  const int64_t i = idx / nk;
-  const int k = k0 + (int)(idx - i * nk);
+// out[i * nk + (k - k0)] = sum over chunk slots cy of partial[cy][k][i], for the
+// components k0 <= k < k0 + nk of a partial array of np components. The kReduceWaves
+// waves of a block share 64 outputs: wave w sums the slots cy = w, w + kReduceWaves, ...
+// in order, and wave 0 adds the waves' sums in wave order (a fixed order, so repeated
+// calls agree bit for bit; the slot loop of one output is ~n_cy / kReduceWaves loads long
+// instead of n_cy dependent ones).
+constexpr int kReduceWaves = 8;
+
+__global__ __launch_bounds__(64 * kReduceWaves) void d4_reduce_kernel(
+    const double* __restrict__ partial, int64_t n_nodes, int np, int k0, int nk, int64_t n_cy,
+    double* __restrict__ out) {
+  __shared__ double red[kReduceWaves][64];
+  const int lane = threadIdx.x & 63;
+  const int wv = wave_in_block();
+  const int64_t idx = (int64_t)blockIdx.x * 64 + lane;
+  const bool live = idx < n_nodes * nk;
   double s = 0.0;
-  for (int64_t cy = 0; cy < n_cy; ++cy) s += partial[(cy * np + k) * n_nodes + i];
-  out[idx] = s;
+  if (live) {
+    const int64_t i = idx / nk;
+    const int k = k0 + (int)(idx - i * nk);
+    const double* src = partial + (int64_t)k * n_nodes + i;
+    const int64_t stride = (int64_t)np * n_nodes;
+    for (int64_t cy = wv; cy < n_cy; cy += kReduceWaves) s += src[cy * stride];
+  }
+  red[wv][lane] = s;
+  __syncthreads();
+  if (wv == 0 && live) {
+    double t = red[0][lane];
+#pragma unroll
+    for (int w = 1; w < kReduceWaves; ++w) t += red[w][lane];
+    out[idx] = t;
+  }
 }
 
 static void reduce_into(const double* partial, int64_t n_nodes, int np, int k0, int nk,
                         int64_t n_cy, double* out, hipStream_t s) {
   const int64_t n = n_nodes * nk;
   if (n == 0 || out == nullptr) return;
-  hipLaunchKernelGGL(d4_reduce_kernel, dim3(grid_1d(n, 256)), dim3(256), 0, s, partial, n_nodes,
-                     np, k0, nk, n_cy, out);
+  hipLaunchKernelGGL(d4_reduce_kernel, dim3(grid_1d(n, 64)), dim3(64 * kReduceWaves), 0, s,
+                     partial, n_nodes, np, k0, nk, n_cy, out);
 }
 
 static bool cp_ready[64] = {false};
@@ -707,6 +728,134 @@ static int upload_cp(hipStream_t s) {
   XNN_HIP_CHECK(hipMemcpyToSymbol(HIP_SYMBOL(c_cp3), cp3, sizeof(cp3), 0, hipMemcpyHostToDevice));
   if (dev >= 0 && dev < 64) cp_ready[dev] = true;
   return XNN_OK;
+}
+
+// ---------------------------------------------------------------- polarizabilities
+constexpr int kD4Ref = 7;                                  // reference systems per element
+constexpr double kD4NormEps = 1.4916681462400413e-154;     // smallest usable weight norm
+
+struct AlphaTables {
+  int n_el;
+  const int32_t* nref;     // (n_el,)
+  const int32_t* ngw;      // (n_el, 7)
+  const double* refcn;     // (n_el, 7)
+  const double* refq;      // (n_el, 7)
+  const double* zeff;      // (n_el,)
+  const double* gi;        // (n_el,) hardness x gc
+  const double* refalpha;  // (n_el, 7, 23)
+  double ga, wf;
+};
+
+// One thread per atom. Reference r of element z weighs
+// g_r = sum_{j=1..ngw} exp(-wf j (cn - cnref_r)^2), normalised over the element's
+// references (d4.py:984-1023; a norm below kD4NormEps puts weight 1 on the references of
+// the largest cnref), times the charge scaling zeta_r(q) = exp(ga (1 - exp(gi (1 - qref_r /
+// (q + zeff))))) with qref_r = refq_r + zeff, or exp(ga) when q + zeff < 0
+// (dispersion.py:70-121); alpha_k = sum_r w_r zeta_r refalpha[z][r][k] (d4.py:1036-1042).
+// BACKWARD contracts g_alpha with d alpha / d cn (through w) into g_cn and with
+// d alpha / d q (through zeta) into g_q, as the reference's native d4_alpha
+// (dispersion_fast/cpu.py:774-829). An atomic number outside the tables gives NaN.
+template <bool BACKWARD>
+__global__ __launch_bounds__(256) void d4_alpha_kernel(
+    int64_t n, const int64_t* __restrict__ z, const double* __restrict__ cn,
+    const double* __restrict__ q, AlphaTables T, const double* __restrict__ g_alpha,
+    double* __restrict__ alpha, double* __restrict__ g_cn, double* __restrict__ g_q) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  const int64_t zz = z[i];
+  const int nr = (zz >= 0 && zz < T.n_el) ? T.nref[zz] : -1;
+  if (nr < 0 || nr > kD4Ref) {
+    const double bad = __builtin_nan("");
+    if (!BACKWARD) {
+      for (int k = 0; k < kNW; ++k) alpha[i * kNW + k] = bad;
+    } else {
+      if (g_cn) g_cn[i] = bad;
+      if (g_q) g_q[i] = bad;
+    }
+    return;
+  }
+  const double c = cn[i];
+  double w[kD4Ref], dw[kD4Ref];
+  double norm = 0.0, dnorm = 0.0;
+#pragma unroll
+  for (int r = 0; r < kD4Ref; ++r) {
+    double g = 0.0, dg = 0.0;
+    if (r < nr) {
+      const double d = c - T.refcn[zz * kD4Ref + r];
+      const double d2 = d * d;
+      const int ng = T.ngw[zz * kD4Ref + r];
+      for (int j = 1; j <= ng; ++j) {
+        const double e = exp(-T.wf * j * d2);
+        g += e;
+        dg += e * (-2.0 * T.wf * j * d);
+      }
+    }
+    w[r] = g;
+    dw[r] = dg;
+    norm += g;
+    dnorm += dg;
+  }
+  if (norm > kD4NormEps) {
+#pragma unroll
+    for (int r = 0; r < kD4Ref; ++r) {
+      const double wr = w[r] / norm;
+      dw[r] = (dw[r] - wr * dnorm) / norm;
+      w[r] = wr;
+    }
+  } else {
+    double top = -__builtin_inf();
+    for (int r = 0; r < nr; ++r) top = fmax(top, T.refcn[zz * kD4Ref + r]);
+#pragma unroll
+    for (int r = 0; r < kD4Ref; ++r) {
+      w[r] = (r < nr && fabs(T.refcn[zz * kD4Ref + r] - top) < 1e-12) ? 1.0 : 0.0;
+      dw[r] = 0.0;
+    }
+  }
+  const double zi = T.zeff[zz], gi = T.gi[zz];
+  const double qmod = q[i] + zi;
+  double zeta[kD4Ref], dzeta[kD4Ref];
+#pragma unroll
+  for (int r = 0; r < kD4Ref; ++r) {
+    zeta[r] = 0.0;
+    dzeta[r] = 0.0;
+    if (r < nr) {
+      if (qmod < 0.0) {
+        zeta[r] = exp(T.ga);
+      } else {
+        const double qref = T.refq[zz * kD4Ref + r] + zi;
+        const double eu = exp(gi * (1.0 - qref / qmod));
+        zeta[r] = exp(T.ga * (1.0 - eu));
+        dzeta[r] = zeta[r] * (-T.ga * eu) * gi * qref / (qmod * qmod);
+      }
+    }
+  }
+  const double* ra = T.refalpha + zz * (kD4Ref * kNW);
+  if (!BACKWARD) {
+    double a[kNW];
+#pragma unroll
+    for (int k = 0; k < kNW; ++k) a[k] = 0.0;
+    for (int r = 0; r < nr; ++r) {
+      const double wz = w[r] * zeta[r];
+#pragma unroll
+      for (int k = 0; k < kNW; ++k) a[k] += wz * ra[r * kNW + k];
+    }
+#pragma unroll
+    for (int k = 0; k < kNW; ++k) alpha[i * kNW + k] = a[k];
+  } else {
+    double ga[kNW];
+#pragma unroll
+    for (int k = 0; k < kNW; ++k) ga[k] = g_alpha[i * kNW + k];
+    double gc = 0.0, gq = 0.0;
+    for (int r = 0; r < nr; ++r) {
+      double t = 0.0;  // sum_k g_alpha_k refalpha[r][k]
+#pragma unroll
+      for (int k = 0; k < kNW; ++k) t += ga[k] * ra[r * kNW + k];
+      gc += dw[r] * zeta[r] * t;
+      gq += w[r] * dzeta[r] * t;
+    }
+    if (g_cn) g_cn[i] = gc;
+    if (g_q) g_q[i] = gq;
+  }
 }
 
 static int d4_check(const double* pos, int64_t n_nodes, const int32_t* species,
@@ -977,6 +1126,49 @@ int xnn_d3_two_body_backward(const double* pos, int64_t n_nodes, const int32_t* 
   reduce_into(part, n_nodes, 12, 0, 3, w.n_cy, grad_pos, s);
   reduce_into(part, n_nodes, 12, 3, 9, w.n_cy, cell_partial, s);
   reduce_into(part_w, n_nodes, kNR, 0, kNR, w.n_cy, grad_weights, s);
+  XNN_LAUNCH_CHECK();
+  return XNN_OK;
+}
+
+static int alpha_tables(const xnn_d4_alpha_tables* t, AlphaTables& T) {
+  XNN_REQUIRE(t != nullptr, "NULL tables");
+  XNN_REQUIRE(t->n_elements >= 1, "empty tables");
+  XNN_REQUIRE(t->nref && t->ngw && t->refcn && t->refq && t->zeff && t->gi && t->refalpha,
+              "NULL table");
+  T = AlphaTables{t->n_elements, t->nref, t->ngw, t->refcn, t->refq, t->zeff, t->gi,
+                  t->refalpha, t->ga, t->wf};
+  return XNN_OK;
+}
+
+int xnn_d4_polarizabilities(int64_t n_nodes, const int64_t* atomic_numbers, const double* cn,
+                            const double* q, const xnn_d4_alpha_tables* tables, double* alpha,
+                            xnn_stream_t stream) {
+  XNN_REQUIRE(n_nodes >= 0, "negative size");
+  AlphaTables T;
+  const int st = alpha_tables(tables, T);
+  if (st != XNN_OK) return st;
+  if (n_nodes == 0) return XNN_OK;
+  XNN_REQUIRE(atomic_numbers && cn && q && alpha, "NULL input or output");
+  hipLaunchKernelGGL(d4_alpha_kernel<false>, dim3(grid_1d(n_nodes, 256)), dim3(256), 0,
+                     as_hip(stream), n_nodes, atomic_numbers, cn, q, T, nullptr, alpha, nullptr,
+                     nullptr);
+  XNN_LAUNCH_CHECK();
+  return XNN_OK;
+}
+
+int xnn_d4_polarizabilities_backward(int64_t n_nodes, const int64_t* atomic_numbers,
+                                     const double* cn, const double* q,
+                                     const xnn_d4_alpha_tables* tables, const double* g_alpha,
+                                     double* g_cn, double* g_q, xnn_stream_t stream) {
+  XNN_REQUIRE(n_nodes >= 0, "negative size");
+  AlphaTables T;
+  const int st = alpha_tables(tables, T);
+  if (st != XNN_OK) return st;
+  if (n_nodes == 0 || (g_cn == nullptr && g_q == nullptr)) return XNN_OK;
+  XNN_REQUIRE(atomic_numbers && cn && q && g_alpha, "NULL input");
+  hipLaunchKernelGGL(d4_alpha_kernel<true>, dim3(grid_1d(n_nodes, 256)), dim3(256), 0,
+                     as_hip(stream), n_nodes, atomic_numbers, cn, q, T, g_alpha, nullptr, g_cn,
+                     g_q);
   XNN_LAUNCH_CHECK();
   return XNN_OK;
 }

@@ -1,5 +1,6 @@
-"""D4 dispersion on the GPU: the coordination numbers and the two-body term as HIP
-kernels over lattice images, the charge model and the polarizabilities in PyTorch.
+"""D4 dispersion on the GPU: the coordination numbers, the polarizabilities and the
+two-body term as HIP kernels (the pair terms over lattice images), the charge model in
+PyTorch.
 
 Mirrors ``DFTD4`` / ``D4Dispersion`` (src/xnn/common/models/d4.py:266-1309,
 dispersion.py:667-878) for the two-body D4 energy:
@@ -9,7 +10,8 @@ dispersion.py:667-878) for the two-body D4 energy:
 * EEQ charges (d4.py:593-723): dense molecular and Ewald-summed periodic interaction
   matrices and the constrained linear solve, PyTorch (as in the reference);
 * charge-scaled Gaussian reference weights and alpha(i w) (d4.py:984-1042,
-  dispersion.py:70-121), PyTorch;
+  dispersion.py:70-121) -> :func:`d4_polarizabilities_op` (HIP, one kernel each way:
+  the alpha, d alpha / d cn and d alpha / d q of the reference's native d4_alpha);
 * the BJ-damped two-body energy with the quintic switch (d4.py:1044-1071,
   dispersion.py:42-67) -> :func:`d4_two_body` (HIP; gradients to positions, cell and
   alpha, the outputs of the reference's native kernel run_d4).
@@ -177,6 +179,59 @@ def _pair_backward(ctx, g_e2):
 d4_two_body_op.register_autograd(_pair_backward, setup_context=_pair_setup)
 
 
+def _alpha_tables(nref, ngw, refcn, refq, zeff, gi, refalpha, ga: float,
+                  wf: float) -> "_lib.D4AlphaTables":
+    return _lib.D4AlphaTables(nref.shape[0], _lib.ptr(nref), _lib.ptr(ngw), _lib.ptr(refcn),
+                              _lib.ptr(refq), _lib.ptr(zeff), _lib.ptr(gi), _lib.ptr(refalpha),
+                              ga, wf)
+
+
+@torch.library.custom_op(f"{_NS}::d4_polarizabilities", mutates_args=())
+def d4_polarizabilities_op(z: Tensor, cn: Tensor, q: Tensor, nref: Tensor, ngw: Tensor,
+                           refcn: Tensor, refq: Tensor, zeff: Tensor, gi: Tensor,
+                           refalpha: Tensor, ga: float, wf: float) -> Tensor:
+    """alpha(i w) (N, 23) at the coordination numbers ``cn`` and charges ``q``: the
+    charge-scaled Gaussian reference weights contracted with the reference
+    polarizabilities in one HIP kernel (d4.py:984-1042; the reference's native d4_alpha,
+    dispersion_fast/cpu.py:774-829). Tables indexed by atomic number, in the kernel's
+    layout (see ``DFTD4``); differentiable once in ``cn`` and ``q``."""
+    n = cn.shape[0]
+    alpha = torch.empty((n, N_FREQ), dtype=torch.float64, device=cn.device)
+    _lib.call("xnn_d4_polarizabilities", n, _lib.ptr(z), _lib.ptr(cn), _lib.ptr(q),
+              _alpha_tables(nref, ngw, refcn, refq, zeff, gi, refalpha, ga, wf),
+              _lib.ptr(alpha), _lib.stream(cn.device))
+    return alpha
+
+
+@d4_polarizabilities_op.register_fake
+def _(z, cn, q, nref, ngw, refcn, refq, zeff, gi, refalpha, ga, wf):
+    return cn.new_empty((cn.shape[0], N_FREQ))
+
+
+def _alpha_setup(ctx, inputs, output):
+    z, cn, q, nref, ngw, refcn, refq, zeff, gi, refalpha, ga, wf = inputs
+    ctx.save_for_backward(z, cn, q, nref, ngw, refcn, refq, zeff, gi, refalpha)
+    ctx.ga, ctx.wf = ga, wf
+
+
+def _alpha_backward(ctx, g_alpha):
+    if torch.is_grad_enabled():
+        raise RuntimeError("the D4 kernels are differentiable once (use_fast=False for more)")
+    z, cn, q, nref, ngw, refcn, refq, zeff, gi, refalpha = ctx.saved_tensors
+    n = cn.shape[0]
+    g_cn = torch.empty_like(cn) if ctx.needs_input_grad[1] else None
+    g_q = torch.empty_like(q) if ctx.needs_input_grad[2] else None
+    if g_cn is not None or g_q is not None:
+        _lib.call("xnn_d4_polarizabilities_backward", n, _lib.ptr(z), _lib.ptr(cn), _lib.ptr(q),
+                  _alpha_tables(nref, ngw, refcn, refq, zeff, gi, refalpha, ctx.ga, ctx.wf),
+                  _lib.ptr(g_alpha.contiguous()), _lib.ptr(g_cn), _lib.ptr(g_q),
+                  _lib.stream(cn.device))
+    return (None, g_cn, g_q) + (None,) * 9
+
+
+d4_polarizabilities_op.register_autograd(_alpha_backward, setup_context=_alpha_setup)
+
+
 # --------------------------------------------------------------------------- host pieces
 def image_counts(cell: Tensor, pbc: Optional[Tensor], cutoff_aa: float) -> Tensor:
     """Translations per axis that cover ``cutoff_aa`` from the interplanar spacing
@@ -263,6 +318,12 @@ class DFTD4(nn.Module):
             v = tables[k]
             dt = torch.long if np.issubdtype(v.dtype, np.integer) else torch.float64
             self.register_buffer(k, torch.as_tensor(v, dtype=dt), persistent=False)
+        # the polarizability kernel's layout: element-major rows
+        kt = {"k_nref": self.nref.to(torch.int32), "k_ngw": self.ngw.t().to(torch.int32),
+              "k_refcn": self.refcn.t(), "k_refq": self.refq.t(),
+              "k_gi": self.hardness * self.gc, "k_refalpha": self.refalpha.permute(2, 1, 0)}
+        for k, v in kt.items():
+            self.register_buffer(k, v.contiguous(), persistent=False)
 
     # ---- building blocks
     def charges(self, z: Tensor, pos_au: Tensor, cn_eeq: Tensor, total_charge: float,
@@ -361,8 +422,15 @@ class DFTD4(nn.Module):
         return w * zeta
 
     def polarizabilities(self, z: Tensor, cn: Tensor, q: Tensor) -> Tensor:
-        """alpha(i w), (N, 23) bohr^3 (d4.py:1036-1042)."""
-        return torch.einsum("nr,krn->nk", self.weights(z, cn, q), self.refalpha[:, :, z])
+        """alpha(i w), (N, 23) bohr^3 (d4.py:1036-1042): the weights above contracted
+        with the reference polarizabilities, one HIP kernel each way
+        (:func:`d4_polarizabilities_op`)."""
+        if not cn.is_cuda:
+            raise RuntimeError("xnn_amd D4 runs on the GPU (HIP kernels); there is no CPU path")
+        return d4_polarizabilities_op(z.long().contiguous(), cn.to(torch.float64).contiguous(),
+                                      q.to(torch.float64).contiguous(), self.k_nref, self.k_ngw,
+                                      self.k_refcn, self.k_refq, self.zeff, self.k_gi,
+                                      self.k_refalpha, self.ga, self.wf)
 
     # ---- evaluation
     def evaluate(self, z: Tensor, pos: Tensor, cell: Optional[Tensor], pbc: Optional[Tensor],
@@ -402,8 +470,8 @@ class DFTD4(nn.Module):
                                      species, batch32, node_ptr, images,
                                      self.rcov[uniq].contiguous(), self.en[uniq].contiguous(),
                                      [cut_cn, cut_eeq], max_atoms)
-        cn_eeq = math.log(1.0 + math.exp(EEQ_CN_MAX)) - torch.log(1.0 + torch.exp(EEQ_CN_MAX - raw))
         if charges is None:
+            cn_eeq = math.log(1.0 + math.exp(EEQ_CN_MAX)) - torch.log(1.0 + torch.exp(EEQ_CN_MAX - raw))
             qs = []
             for b in range(B):
                 s0, s1 = sum(n_atoms_h[:b]), sum(n_atoms_h[:b + 1])
