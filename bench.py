@@ -103,6 +103,13 @@ def step_bytes(E: int, N: int, C: int, L: int, K: int, msg: str) -> int:
             + kc[msg + "_backward"]["bytes"] + kc["xnn_edge_force_reduce"]["bytes"] + linear)
 
 
+def pipeline_bytes(E: int, N: int, C: int) -> int:
+    """Algorithmic bytes of the unfused featurize -> phi -> message -> readout -> backward
+    pipeline that the metric's HBM roofline is quoted on: E (124 + 12 C) + N (76 + 8 C 16)
+    (the edge streams, phi and d_phi per edge; the (C, 16) node rows and their cotangent)."""
+    return E * (124 + 12 * C) + N * (76 + 8 * C * 16)
+
+
 def message_launches(msg: str, g, model, kw: dict) -> dict:
     """The C-ABI calls of the step's message kernels, forward and backward, on the
     workload's own inputs (edge vectors, weights, a random node cotangent), as
@@ -466,6 +473,11 @@ def main() -> None:
                    "fused_linear": fused, "message_kernel": msg,
                    "step_algorithmic_bytes": sb,
                    "step_hbm_fraction": round(step_gbs / HBM_PEAK_GBS, 4),
+                   # the unfused pipeline's bytes, E (124 + 12 C) + N (76 + 8 C 16): the
+                   # "% HBM roofline" of the metric, >= 0.5 being the target
+                   "pipeline_bytes": pipeline_bytes(E, N, C),
+                   "pipeline_hbm_fraction": round(pipeline_bytes(E, N, C) / (ms * 1e-3)
+                                                  / 1e9 / HBM_PEAK_GBS, 4),
                    "kernel_mean_us": {k: round(v, 2) for k, v in replay_us.items()},
                    "eager_kernel_event_us": {k: round(v, 2) for k, v in per_kernel.items()}},
         "roofline": roofline,

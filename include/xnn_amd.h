@@ -498,6 +498,23 @@ int xnn_edge_plan(const int64_t* edge_index, const int64_t* cell_shifts, int64_t
                   int32_t* overflow, void* workspace, size_t workspace_bytes,
                   xnn_stream_t stream);
 
+/* ------------------------------------------------------------------------ */
+/* Linear per-atom readout of node rows: out[i] = bias[z[i]] + sum_f rows[i,f] w[f]
+ * (rows (N,F) row-major, w (F), out (N), all in dtype; z (N) int64 and bias (n_bias)
+ * both NULL for no bias; a z outside [0, n_bias) gives NaN). The readout
+ * E_i = <U, A_i> + atom_ref[Z_i] of the measured edge model; no counterpart in the
+ * reference's path (its models read out through their own PyTorch layers), here for
+ * callers that stream large node rows once: one wave per row, deterministic. */
+int xnn_node_readout(int dtype, const void* rows, int64_t n_rows, int64_t n_features,
+                     const void* weights, const int64_t* z, const void* bias, int64_t n_bias,
+                     void* out, xnn_stream_t stream);
+
+/* The adjoint in rows: d_rows[i,f] = g[i * g_stride] w[f] (g_stride 0: one value for
+ * every row, 1: per row). */
+int xnn_node_readout_backward(int dtype, const void* g, int64_t g_stride, int64_t n_rows,
+                              int64_t n_features, const void* weights, void* d_rows,
+                              xnn_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -424,6 +424,51 @@ def test_single_structure_reduction(F):
             assert torch.equal(out, out2)
 
 
+@pytest.mark.parametrize("F", [2048, 2050, 36, 1])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float64])
+def test_node_readout_forward_backward(F, dtype):
+    """The model's readout E_i = rows_i . w + bias[z_i] and its gradients in rows, w and
+    bias against float64 PyTorch on the CPU (float32 rtol 1e-5, float64 1e-12), the
+    vector and scalar row paths, a broadcast cotangent read as one value, a z outside the
+    bias table giving NaN, and bitwise repeatability."""
+    from xnn_amd import _lib
+    from xnn_amd.ops import node_readout_op
+    _note(f"node readout F={F} {dtype}")
+    gen = torch.Generator().manual_seed(F)
+    n = 1003
+    rows = torch.randn(n, F, generator=gen, dtype=torch.float64)
+    w = torch.randn(F, generator=gen, dtype=torch.float64)
+    bias = torch.randn(9, generator=gen, dtype=torch.float64)
+    z = torch.randint(0, 9, (n,), generator=gen)
+    g = torch.randn(n, generator=gen, dtype=torch.float64)
+    tol = dict(rtol=1e-5, atol=1e-5 * F ** 0.5) if dtype == torch.float32 else \
+        dict(rtol=1e-12, atol=1e-12 * F ** 0.5)
+    rd = rows.to(dtype).to(DEV).requires_grad_(True)
+    wd = w.to(dtype).to(DEV).requires_grad_(True)
+    bd = bias.to(dtype).to(DEV).requires_grad_(True)
+    calls = _lib.calls.get("xnn_node_readout", 0)
+    out = node_readout_op(rd, wd, z.to(DEV), bd)
+    assert _lib.calls["xnn_node_readout"] == calls + 1
+    want = rows.to(dtype).double() @ w.to(dtype).double() + bias.to(dtype).double()[z]
+    np.testing.assert_allclose(out.detach().cpu().double(), want, **tol)
+    assert torch.equal(out, node_readout_op(rd, wd, z.to(DEV), bd))
+    d_rows, d_w, d_b = torch.autograd.grad(out, [rd, wd, bd], g.to(dtype).to(DEV))
+    gq = g.to(dtype).double()
+    np.testing.assert_allclose(d_rows.cpu().double(), gq[:, None] * w.to(dtype).double()[None],
+                               rtol=tol["rtol"], atol=tol["rtol"])
+    np.testing.assert_allclose(d_w.cpu().double(), rows.to(dtype).double().t() @ gq,
+                               rtol=tol["rtol"], atol=tol["atol"] * n ** 0.5)
+    np.testing.assert_allclose(d_b.cpu().double(), torch.zeros(9, dtype=torch.float64)
+                               .index_add_(0, z, gq), rtol=tol["rtol"], atol=tol["atol"])
+    # a broadcast (stride-0) cotangent, as a force evaluation seeds it
+    seed = torch.full((1,), -1.0, dtype=dtype, device=DEV).expand(n)
+    (d_rows2,) = torch.autograd.grad(node_readout_op(rd, wd, z.to(DEV), bd), [rd], seed)
+    assert torch.equal(d_rows2, (-wd.detach())[None].expand(n, F))
+    bad = node_readout_op(rd.detach()[:2], wd.detach(), torch.tensor([0, 9], device=DEV),
+                          bd.detach())
+    assert torch.isfinite(bad[0]) and torch.isnan(bad[1])
+
+
 def test_stress_and_virial_finish_kernels():
     """sym(M + term) cast, and scale * g / |det cell| with zero stress for zero cells and
     non-periodic structures, against the PyTorch formulation."""

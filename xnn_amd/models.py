@@ -167,8 +167,18 @@ class ShEdgePotential(InteratomicPotential):
                data.num_edges, double_backward=self.double_backward)
         vec = data.edge_vectors()
         A = self.messages(data, vec)
-        # readout E_i = <U, A_i> + atom_ref[Z_i], the reference energy added by the
-        # product itself (one launch)
-        node_energy = torch.addmv(self.atom_ref.to(A.dtype)[data.atomic_numbers],
-                                  A.reshape(A.shape[0], -1), self.U.to(A.dtype).reshape(-1))
+        # readout E_i = <U, A_i> + atom_ref[Z_i]: on the fast path one HIP launch each
+        # way (the rows streamed once, the reference energy gathered in the same pass)
+        if self.edge_feat.fast_active:
+            from .ops import node_readout_op
+            U, ref = self.U.reshape(-1), self.atom_ref
+            if not self.param_grads:
+                # a custom op's backward cannot see which inputs the current backward
+                # asks for: detached parameters keep it to the rows' gradient
+                U, ref = U.detach(), ref.detach()
+            node_energy = node_readout_op(A.reshape(A.shape[0], -1), U, data.atomic_numbers,
+                                          ref)
+        else:
+            node_energy = torch.addmv(self.atom_ref.to(A.dtype)[data.atomic_numbers],
+                                      A.reshape(A.shape[0], -1), self.U.to(A.dtype).reshape(-1))
         return {"node_energy": node_energy, "energy": self.aggregate_energy(node_energy, data)}

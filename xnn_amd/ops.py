@@ -28,6 +28,8 @@ sum``                  evaluated in the kernel (spherical.py:135-138): featurize
 ``segment_sum``        ``scatter_sum`` (common/models/ops.py:403-448)
 ``gather_rows``        ``gather_rows`` (common/models/ops.py:494-528)
 ``structure_sum``      ``structure_sum`` (common/models/ops.py:531-557), float64 totals
+``node_readout``       no reference op: the measured model's linear per-atom readout
+                       ``E_i = <U, A_i> + atom_ref[Z_i]`` (one streaming pass each way)
 =====================  ==============================================================
 
 All reductions walk CSR rows in a fixed order (no float atomics), so every op
@@ -753,3 +755,57 @@ def _structure_sum_backward(ctx, grad):
 
 
 structure_sum_op.register_autograd(_structure_sum_backward, setup_context=_structure_sum_setup)
+
+
+@torch.library.custom_op(f"{_NS}::node_readout", mutates_args=())
+def node_readout_op(rows: Tensor, weight: Tensor, z: Tensor, bias: Tensor) -> Tensor:
+    """``out[i] = bias[z[i]] + rows[i] . weight`` for ``rows (N, F)``, in the rows' dtype:
+    one wave per row streams it once (``torch.addmv`` with the gathered bias, as one
+    launch). Differentiable once in every tensor input."""
+    dev = _require_gpu(rows, weight, z, bias)
+    rows = rows.contiguous()
+    weight = weight.to(rows.dtype).contiguous()
+    bias = bias.to(rows.dtype).contiguous()
+    z = z.to(torch.int64).contiguous()
+    n, F = rows.shape
+    out = torch.empty(n, dtype=rows.dtype, device=dev)
+    _lib.call("xnn_node_readout", _lib.dtype_code(rows.dtype), _lib.ptr(rows), n, F,
+              _lib.ptr(weight), _lib.ptr(z), _lib.ptr(bias), bias.shape[0], _lib.ptr(out),
+              _lib.stream(dev))
+    return out
+
+
+@node_readout_op.register_fake
+def _(rows, weight, z, bias):
+    return rows.new_empty(rows.shape[0])
+
+
+def _readout_setup(ctx, inputs, output):
+    rows, weight, z, bias = inputs
+    ctx.save_for_backward(rows if ctx.needs_input_grad[1] else None, weight, z)
+    ctx.n_bias, ctx.bias_dtype, ctx.weight_dtype = bias.shape[0], bias.dtype, weight.dtype
+
+
+def _readout_backward(ctx, grad):
+    _once_differentiable()
+    rows, weight, z = ctx.saved_tensors
+    n = grad.shape[0]
+    d_rows = d_weight = d_bias = None
+    if ctx.needs_input_grad[0]:
+        w = weight.to(grad.dtype).contiguous()
+        F = w.shape[0]
+        # a broadcast cotangent (the -1 seed of a force evaluation) is read as one value
+        g = grad if (grad.dim() == 1 and grad.stride(0) == 0) else grad.contiguous()
+        d_rows = torch.empty((n, F), dtype=grad.dtype, device=grad.device)
+        _lib.call("xnn_node_readout_backward", _lib.dtype_code(grad.dtype), _lib.ptr(g),
+                  0 if g.stride(0) == 0 else 1, n, F, _lib.ptr(w), _lib.ptr(d_rows),
+                  _lib.stream(grad.device))
+    if ctx.needs_input_grad[1]:
+        d_weight = (rows.t() @ grad).to(ctx.weight_dtype)
+    if ctx.needs_input_grad[3]:
+        d_bias = torch.zeros(ctx.n_bias, dtype=grad.dtype, device=grad.device).index_add_(
+            0, z, grad).to(ctx.bias_dtype)
+    return d_rows, d_weight, None, d_bias
+
+
+node_readout_op.register_autograd(_readout_backward, setup_context=_readout_setup)
