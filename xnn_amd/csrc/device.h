@@ -234,13 +234,14 @@ __device__ inline RadialAt<T> radial_at(const Radial<T>& R, T r) {
   return a;
 }
 
+// basis function k with its table entry tk (Bessel frequency or Gaussian center) given
 template <typename T, bool DERIV>
-__device__ inline void radial_k(const Radial<T>& R, const RadialAt<T>& a, int k, T& u, T& du) {
+__device__ inline void radial_kv(const Radial<T>& R, const RadialAt<T>& a, T tk, T& u, T& du) {
   if (R.basis == XNN_BASIS_BESSEL) {
     // prefactor * sin(freq * r / rc) / r
-    const T w = R.table[k] / R.rc;
+    const T w = tk / R.rc;
     T s, c;
-    dev_sincos(R.table[k] * a.rr / R.rc, &s, &c);
+    dev_sincos(tk * a.rr / R.rc, &s, &c);
     const T b = R.prefactor * s * a.inv;
     u = b * a.f;
     if constexpr (DERIV) {
@@ -249,11 +250,16 @@ __device__ inline void radial_k(const Radial<T>& R, const RadialAt<T>& a, int k,
     }
   } else {
     // exp(-gamma (r - mu_k)^2)  (radial.py:73-75)
-    const T dd = a.r - R.table[k];
+    const T dd = a.r - tk;
     const T b = dev_exp(-R.gamma * dd * dd);
     u = b * a.f;
     if constexpr (DERIV) du = T(-2) * R.gamma * dd * b * a.f + b * a.df;
   }
+}
+
+template <typename T, bool DERIV>
+__device__ inline void radial_k(const Radial<T>& R, const RadialAt<T>& a, int k, T& u, T& du) {
+  radial_kv<T, DERIV>(R, a, R.table[k], u, du);
 }
 
 constexpr int kMaxRbf = 32;

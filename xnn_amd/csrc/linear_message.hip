@@ -35,29 +35,45 @@ constexpr int kLinKMax = 8;  // h features: two k-steps of 4
 constexpr int kLinKK = 2;
 constexpr int kSH = 9;       // LDS row stride of per-edge radial features
 
-// Bessel frequencies in harmonic progression, f_k = (k + 1) f_0 to 4e-7 (the default
-// BesselRBF frequencies n pi, radial.py:226): then sin((k + 1) theta) and its cosine
-// follow from one sincos by the Chebyshev recurrence x_{k+1} = 2 cos(theta) x_k - x_{k-1}
-// instead of one sincos per function. Wave-uniform (the table is the same for all lanes).
-__device__ __forceinline__ bool bessel_harmonic(const Radial<float>& R) {
-  if (R.basis != XNN_BASIS_BESSEL) return false;
-  const float f0 = R.table[0];
+// The radial table (Bessel frequencies or Gaussian centers, k < kLinKMax) is read once per
+// block into LDS, and its first entry and the progression test into scalars at kernel
+// entry, before any store: there the wave-uniform loads are scalar loads (nothing the
+// kernel writes can alias them yet). Read next to the kernel's own stores they would be
+// per-lane vector loads whose latency the radial evaluation waits for on every row.
+struct RadialTab {
+  const float* f;  // the table in LDS
+  float f0;
+  // frequencies in harmonic progression, f_k = (k + 1) f_0 to 4e-7 (the default
+  // BesselRBF frequencies n pi, radial.py:226): then sin((k + 1) theta) and its cosine
+  // follow from one sincos by the Chebyshev recurrence x_{k+1} = 2 cos(theta) x_k - x_{k-1}
+  // instead of one sincos per function
+  bool harmonic;
+};
+
+// every thread of the block calls this once; the caller synchronizes the block before the
+// table is read
+__device__ __forceinline__ RadialTab load_radial_tab(const Radial<float>& R, float* sTab) {
+  RadialTab t;
+  t.f = sTab;
+  t.f0 = R.table[0];
+  t.harmonic = R.basis == XNN_BASIS_BESSEL;
   for (int k = 1; k < R.K; ++k) {
     const float fk = R.table[k];
-    if (fabsf(fk - (float)(k + 1) * f0) > 4e-7f * fabsf(fk)) return false;
+    if (fabsf(fk - (float)(k + 1) * t.f0) > 4e-7f * fabsf(fk)) t.harmonic = false;
   }
-  return true;
+  if (threadIdx.x < kLinKMax) sTab[threadIdx.x] = (int)threadIdx.x < R.K ? R.table[threadIdx.x] : 0.f;
+  return t;
 }
 
 // The lane's row of radial features h_k = rbf_k(r) envelope(r), k < kLinKMax (zeros past
 // R.K, and the whole row when the lane has no edge).
-__device__ __forceinline__ void radial_row(const Radial<float>& R, bool harmonic, bool valid,
-                                           float r, float* __restrict__ row) {
+__device__ __forceinline__ void radial_row(const Radial<float>& R, const RadialTab& tab,
+                                           bool valid, float r, float* __restrict__ row) {
   if (valid) {
     const RadialAt<float> a = radial_at(R, r);
-    if (harmonic) {
+    if (tab.harmonic) {
       float s1, c1;
-      dev_sincos(R.table[0] * a.rr / R.rc, &s1, &c1);
+      dev_sincos(tab.f0 * a.rr / R.rc, &s1, &c1);
       const float c2 = 2.f * c1, pf = R.prefactor * a.inv * a.f;
       float sp = 0.f, sk = s1;  // sin(k theta), sin((k + 1) theta)
 #pragma unroll
@@ -72,7 +88,7 @@ __device__ __forceinline__ void radial_row(const Radial<float>& R, bool harmonic
 #pragma unroll 1
     for (int k = 0; k < kLinKMax; ++k) {
       float u = 0.f, du;
-      if (k < R.K) radial_k<float, false>(R, a, k, u, du);
+      if (k < R.K) radial_kv<float, false>(R, a, tab.f[k], u, du);
       row[k] = u;
     }
   } else {
@@ -82,15 +98,15 @@ __device__ __forceinline__ void radial_row(const Radial<float>& R, bool harmonic
 }
 
 // d E / d r through the radial features of one edge: sum_k d_h[k] d h_k / d r
-__device__ __forceinline__ float radial_dot(const Radial<float>& R, bool harmonic, float r,
-                                            const float* __restrict__ d_h) {
+__device__ __forceinline__ float radial_dot(const Radial<float>& R, const RadialTab& tab,
+                                            float r, const float* __restrict__ d_h) {
   const RadialAt<float> a = radial_at(R, r);
   float dl = 0.f;
-  if (harmonic) {
+  if (tab.harmonic) {
     // d/dr [p sin((k+1) w0 r) / r] = p ((k+1) w0 cos((k+1) w0 r) - sin(..) / r) / r
-    const float w0 = R.table[0] / R.rc;
+    const float w0 = tab.f0 / R.rc;
     float s1, c1;
-    dev_sincos(R.table[0] * a.rr / R.rc, &s1, &c1);
+    dev_sincos(tab.f0 * a.rr / R.rc, &s1, &c1);
     const float c2 = 2.f * c1;
     float sp = 0.f, sk = s1, cp = 1.f, ck = c1;
 #pragma unroll 1
@@ -110,7 +126,7 @@ __device__ __forceinline__ float radial_dot(const Radial<float>& R, bool harmoni
 #pragma unroll 1
   for (int k = 0; k < R.K; ++k) {
     float u, du;
-    radial_k<float, true>(R, a, k, u, du);
+    radial_kv<float, true>(R, a, tab.f[k], u, du);
     dl += d_h[k] * du;
   }
   return dl;
@@ -133,7 +149,8 @@ __global__ __launch_bounds__(256, 4) void lin_msg_fwd_kernel(
   const int lo = lane & 15, hi = lane >> 4;
   float* ys = sY[wave];
   float* hs = sH[wave];
-  const bool harmonic = RAD && bessel_harmonic(R);
+  __shared__ float sTab[kLinKMax];
+  const RadialTab tab = RAD ? load_radial_tab(R, sTab) : RadialTab{};
   // W in LDS (rows padded to C + 4 floats, zero rows past K): the B operand of h W for
   // channel tile t, k-step q is W[4 q + hi][lo T + t], a run of T floats
   constexpr int SWS = C + 4;
@@ -181,7 +198,7 @@ __global__ __launch_bounds__(256, 4) void lin_msg_fwd_kernel(
                                  ux, uy, uz, inv, len);
       if constexpr (RAD) {
         __builtin_amdgcn_sched_barrier(0);
-        radial_row(R, harmonic, lane < cnt, len, hs + lane * kSH);
+        radial_row(R, tab, lane < cnt, len, hs + lane * kSH);
       }
       wave_sync();
       const int ntile = (cnt + 15) >> 4;
@@ -270,7 +287,8 @@ __global__ __launch_bounds__(256, 3) void lin_msg_bwd_kernel(
   // RAD: per-edge radial features, overwritten tile by tile with d_h once read
   __shared__ float sH[kWavesPerBlock][RAD ? kWave * kSH : 1];
   float* hs = sH[wave];
-  const bool harmonic = RAD && bessel_harmonic(R);
+  __shared__ float sTab[kLinKMax];
+  const RadialTab tab = RAD ? load_radial_tab(R, sTab) : RadialTab{};
   const bool want_vec = RAD || g_vec != nullptr;
   // W in LDS, zero rows past K, twice: rows padded to C + 4 floats for the A operand of
   // phi^T = W^T h^T (k-step q: W[4 q + hi][lo T + t], a run of T floats), and permuted for
@@ -370,7 +388,7 @@ __global__ __launch_bounds__(256, 3) void lin_msg_bwd_kernel(
       }
       if constexpr (RAD) {
         __builtin_amdgcn_sched_barrier(0);
-        radial_row(R, harmonic, lane < cnt, len, hs + lane * kSH);
+        radial_row(R, tab, lane < cnt, len, hs + lane * kSH);
       }
       wave_sync();
       const int ntile = (cnt + 15) >> 4;
@@ -481,7 +499,7 @@ __global__ __launch_bounds__(256, 3) void lin_msg_bwd_kernel(
         // d|r| from the radial features first, then the harmonics' share (kept apart so
         // that their temporaries are not live together)
         float dl = 0.f;
-        if constexpr (RAD) dl = radial_dot(R, harmonic, len, hs + lane * kSH);
+        if constexpr (RAD) dl = radial_dot(R, tab, len, hs + lane * kSH);
         __builtin_amdgcn_sched_barrier(0);
         float dY[L];
 #pragma unroll
