@@ -3,10 +3,10 @@
 //   out[i]    = bias[z[i]] + sum_f rows[i][f] w[f]        (xnn_node_readout)
 //   d_rows[i][f] = g[i * g_stride] w[f]                   (xnn_node_readout_backward)
 //
-// Both are streams over the (N, F) rows: one wave per row, 16-byte non-temporal
-// loads / stores (the rows are touched once), four vectors in flight per lane, and
-// the row dot product reduced by a fixed butterfly (repeated calls agree bit for bit).
-// The per-atom bias gather is folded into the forward (no separate index launch).
+// Both are streams over the (N, F) rows: one wave per row, 16-byte non-temporal loads /
+// stores (the rows are touched once), four vectors in flight per lane, and the row dot
+// product reduced by a fixed butterfly (repeated calls agree bit for bit). The per-atom
+// bias gather is folded into the forward (no separate index launch).
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -50,6 +50,13 @@ __global__ __launch_bounds__(256) void readout_fwd_kernel(
   const int lane = threadIdx.x & (kWave - 1);
   const int64_t row = (int64_t)blockIdx.x * kReadoutRows + wave_in_block();
   if (row >= n) return;
+  // the bias gather (two dependent loads) is issued first, so that its latency passes
+  // under the row's stream instead of following it
+  T b = 0;
+  if (bias != nullptr) {
+    const int64_t zz = z[row];
+    b = (zz >= 0 && zz < n_bias) ? bias[zz] : (T)__builtin_nan("");
+  }
   T acc = 0;
   if (VEC) {
     typedef typename Vec16<T>::type VT;
@@ -74,14 +81,7 @@ __global__ __launch_bounds__(256) void readout_fwd_kernel(
   }
 #pragma unroll
   for (int o = kWave / 2; o > 0; o >>= 1) acc += __shfl_xor(acc, o);
-  if (lane == 0) {
-    T b = 0;
-    if (bias != nullptr) {
-      const int64_t zz = z[row];
-      b = (zz >= 0 && zz < n_bias) ? bias[zz] : (T)__builtin_nan("");
-    }
-    out[row] = b + acc;
-  }
+  if (lane == 0) out[row] = b + acc;
 }
 
 template <typename T, bool VEC>
