@@ -674,7 +674,8 @@ __global__ __launch_bounds__(64) void d3_pair_kernel(
 // waves of a block share 64 outputs: wave w sums the slots cy = w, w + kReduceWaves, ...
 // in order, and wave 0 adds the waves' sums in wave order (a fixed order, so repeated
 // calls agree bit for bit; the slot loop of one output is ~n_cy / kReduceWaves loads long
-// instead of n_cy dependent ones).
+// instead of n_cy dependent ones). The 64 outputs of a block are 64 consecutive atoms of
+// one component, so that every load of a wave reads one contiguous run of the partials.
 constexpr int kReduceWaves = 8;
 
 __global__ __launch_bounds__(64 * kReduceWaves) void d4_reduce_kernel(
@@ -683,12 +684,11 @@ __global__ __launch_bounds__(64 * kReduceWaves) void d4_reduce_kernel(
   __shared__ double red[kReduceWaves][64];
   const int lane = threadIdx.x & 63;
   const int wv = wave_in_block();
-  const int64_t idx = (int64_t)blockIdx.x * 64 + lane;
-  const bool live = idx < n_nodes * nk;
+  const int64_t i = (int64_t)blockIdx.x * 64 + lane;
+  const int k = k0 + (int)blockIdx.y;
+  const bool live = i < n_nodes;
   double s = 0.0;
   if (live) {
-    const int64_t i = idx / nk;
-    const int k = k0 + (int)(idx - i * nk);
     const double* src = partial + (int64_t)k * n_nodes + i;
     const int64_t stride = (int64_t)np * n_nodes;
     for (int64_t cy = wv; cy < n_cy; cy += kReduceWaves) s += src[cy * stride];
@@ -699,7 +699,7 @@ __global__ __launch_bounds__(64 * kReduceWaves) void d4_reduce_kernel(
     double t = red[0][lane];
 #pragma unroll
     for (int w = 1; w < kReduceWaves; ++w) t += red[w][lane];
-    out[idx] = t;
+    out[i * nk + (k - k0)] = t;
   }
 }
 
@@ -707,8 +707,8 @@ static void reduce_into(const double* partial, int64_t n_nodes, int np, int k0, 
                         int64_t n_cy, double* out, hipStream_t s) {
   const int64_t n = n_nodes * nk;
   if (n == 0 || out == nullptr) return;
-  hipLaunchKernelGGL(d4_reduce_kernel, dim3(grid_1d(n, 64)), dim3(64 * kReduceWaves), 0, s,
-                     partial, n_nodes, np, k0, nk, n_cy, out);
+  hipLaunchKernelGGL(d4_reduce_kernel, dim3(grid_1d(n_nodes, 64), nk), dim3(64 * kReduceWaves),
+                     0, s, partial, n_nodes, np, k0, nk, n_cy, out);
 }
 
 static bool cp_ready[64] = {false};
