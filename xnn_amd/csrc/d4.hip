@@ -41,6 +41,7 @@ constexpr int kNW = 23;         // Casimir-Polder frequencies
 constexpr double kBohr = 0.5291772109044924;
 constexpr double kInvBohr = 1.0 / kBohr;
 constexpr double kSqrtPi = 1.7724538509055160273;
+constexpr double kInvSqrtPi = 1.0 / kSqrtPi;
 
 // 1 / x for positive normal x: the hardware estimate (v_rcp_f64) refined by two
 // Newton-Raphson steps y <- y (2 - x y), to about an ulp (the IEEE-exact division costs
@@ -124,22 +125,32 @@ __device__ inline void lattice_inverse(Lattice& L) {
 // Images n_c in [lo_c, hi_c] per axis that can lie within rc (Angstrom) of d: the
 // fractional component f_c + n_c of d + n @ cell bounds its length from below by
 // |f_c + n_c| sp_c, so other images are farther than rc (a small slack keeps the
-// bound conservative under rounding).
-__device__ inline void image_window(const Lattice& L, double dx, double dy, double dz, double rc,
-                                    int lo[3], int hi[3]) {
-  const int nmax[3] = {L.n0, L.n1, L.n2};
-#pragma unroll
-  for (int c = 0; c < 3; ++c) {
-    if (nmax[c] == 0) {
-      lo[c] = hi[c] = 0;
-      continue;
-    }
-    const double f = dx * L.inv[c] + dy * L.inv[3 + c] + dz * L.inv[6 + c];
-    const double w = rc / L.sp[c] + 1e-9;
-    const double m = (double)nmax[c];
-    lo[c] = (int)fmax(ceil(-w - f), -m);   // clamped as doubles, then converted
-    hi[c] = (int)fmin(floor(w - f), m);
+// bound conservative under rounding). Returned as six scalars (an indexed array here
+// lands in scratch memory, one store and one load per pair).
+struct ImageRange {
+  int lo0, hi0, lo1, hi1, lo2, hi2;
+};
+
+__device__ inline void axis_range(int nmax, double f, double w, int& lo, int& hi) {
+  if (nmax == 0) {
+    lo = hi = 0;
+    return;
   }
+  const double m = (double)nmax;
+  lo = (int)fmax(ceil(-w - f), -m);  // clamped as doubles, then converted
+  hi = (int)fmin(floor(w - f), m);
+}
+
+__device__ inline ImageRange image_window(const Lattice& L, double dx, double dy, double dz,
+                                          double rc) {
+  ImageRange r;
+  axis_range(L.n0, dx * L.inv[0] + dy * L.inv[3] + dz * L.inv[6], rc / L.sp[0] + 1e-9, r.lo0,
+             r.hi0);
+  axis_range(L.n1, dx * L.inv[1] + dy * L.inv[4] + dz * L.inv[7], rc / L.sp[1] + 1e-9, r.lo1,
+             r.hi1);
+  axis_range(L.n2, dx * L.inv[2] + dy * L.inv[5] + dz * L.inv[8], rc / L.sp[2] + 1e-9, r.lo2,
+             r.hi2);
+  return r;
 }
 
 __device__ inline void load_lattice(const double* __restrict__ cell,
@@ -189,6 +200,8 @@ struct D4Stage {
   double x[kD4Sub], y[kD4Sub], z[kD4Sub];
   double w[kD4Sub];       // backward weight of the source (its upstream gradient)
   double w2[kD4Sub];      // second weight (CN: EEQ-count gradient)
+  double p[kD4Sub], q[kD4Sub];  // per-source table values (CN: rcov, EN; pair: r4r2 and
+                                // its square root), read once per stage, not per pair
   int sp[kD4Sub];         // species
   int b[kD4Sub];          // structure
 };
@@ -242,6 +255,7 @@ __global__ __launch_bounds__(64, 3) void d4_cn_kernel(
     load_lattice(nullptr, nullptr, 0, L);
   }
   const double cmax = prm.cut_cn > prm.cut_eeq ? prm.cut_cn : prm.cut_eeq;
+  const double inv_k6 = 1.0 / prm.k6;
   for (int64_t base = j0; base < j1; base += kD4Sub) {
     const int cnt = (int)std::min<int64_t>(kD4Sub, j1 - base);
     __syncthreads();
@@ -250,8 +264,11 @@ __global__ __launch_bounds__(64, 3) void d4_cn_kernel(
       st.x[lane] = pos[3 * j];
       st.y[lane] = pos[3 * j + 1];
       st.z[lane] = pos[3 * j + 2];
-      st.sp[lane] = species[j];
+      const int sj = species[j];
+      st.sp[lane] = sj;
       st.b[lane] = batch[j];
+      st.p[lane] = rcov[sj];
+      if (!D3) st.q[lane] = en[sj];
       if (BACKWARD) {
         st.w[lane] = g_cn ? g_cn[j] : 0.0;
         st.w2[lane] = g_raw ? g_raw[j] : 0.0;
@@ -261,29 +278,27 @@ __global__ __launch_bounds__(64, 3) void d4_cn_kernel(
     if (!live) continue;
     for (int jj = 0; jj < cnt; ++jj) {
       if (st.b[jj] != bi) continue;
-      const int sj = st.sp[jj];
-      const double rc = rci + rcov[sj];
+      const double rc = rci + st.p[jj];
       double enf = 1.0;
       if (!D3) {
-        const double den = fabs(eni - en[sj]) + prm.k5;
-        enf = prm.k4 * exp(-den * den / prm.k6);
+        const double den = fabs(eni - st.q[jj]) + prm.k5;
+        enf = prm.k4 * exp(-den * den * inv_k6);
       }
       // per pair: k0 / rc and the erf count's slope factor -k0 / (rc sqrt(pi))
       const double k_rc = prm.kcn / rc;
-      const double dk = -k_rc / kSqrtPi;
+      const double dk = -k_rc * kInvSqrtPi;
       const double dx = xi - st.x[jj], dy = yi - st.y[jj], dz = zi - st.z[jj];
       const double bx = dx * kInvBohr, by = dy * kInvBohr, bz = dz * kInvBohr;
       const double wsum = BACKWARD ? gi + st.w[jj] : 0.0;
       const double w2sum = BACKWARD ? g2i + st.w2[jj] : 0.0;
-      int lo[3], hi[3];
-      image_window(L, dx, dy, dz, cmax * kBohr, lo, hi);
-      for (int n0 = lo[0]; n0 <= hi[0]; ++n0)
-        for (int n1 = lo[1]; n1 <= hi[1]; ++n1) {
+      const ImageRange win = image_window(L, dx, dy, dz, cmax * kBohr);
+      for (int n0 = win.lo0; n0 <= win.hi0; ++n0)
+        for (int n1 = win.lo1; n1 <= win.hi1; ++n1) {
           // the image's vector in bohr, d + n @ cell
           const double px = bx + n0 * L.ab[0] + n1 * L.ab[3];
           const double py = by + n0 * L.ab[1] + n1 * L.ab[4];
           const double pz = bz + n0 * L.ab[2] + n1 * L.ab[5];
-          for (int n2 = lo[2]; n2 <= hi[2]; ++n2) {
+          for (int n2 = win.lo2; n2 <= win.hi2; ++n2) {
             const double vx = px + n2 * L.ab[6], vy = py + n2 * L.ab[7], vz = pz + n2 * L.ab[8];
             const double r2 = vx * vx + vy * vy + vz * vz;
             if (r2 <= 0.0 || r2 > cmax * cmax) continue;
@@ -351,7 +366,7 @@ __global__ __launch_bounds__(64, 2) void d4_pair_kernel(
     const double* __restrict__ g_e2, int64_t chunk, int64_t n_cy, double* __restrict__ partial,
     double* __restrict__ partial_alpha) {
   __shared__ D4Stage st;
-  __shared__ double sa[kNW][kD4Sub];
+  __shared__ double sa[kNW][kD4Sub];  // the sources' alpha(i w) times the grid weights c_cp3
   const int lane = threadIdx.x;
   const int64_t t = blockIdx.x, cy = blockIdx.y;
   const int64_t i = t * kD4Tile + lane;
@@ -370,7 +385,7 @@ __global__ __launch_bounds__(64, 2) void d4_pair_kernel(
     ai[w] = 0.0;
     da[w] = 0.0;
   }
-  double xi = 0, yi = 0, zi = 0, qi = 0, gi = 0;
+  double xi = 0, yi = 0, zi = 0, qi = 0, sq3qi = 0, gi = 0;
   int bi = -1;
   Lattice L;
   if (live) {
@@ -378,10 +393,11 @@ __global__ __launch_bounds__(64, 2) void d4_pair_kernel(
     yi = pos[3 * i + 1];
     zi = pos[3 * i + 2];
     qi = r4r2[species[i]];
+    sq3qi = sqrt(3.0 * qi);
     bi = batch[i];
     if (BACKWARD) gi = g_e2[i];
 #pragma unroll
-    for (int w = 0; w < kNW; ++w) ai[w] = alpha[(int64_t)kNW * i + w] * c_cp3[w];
+    for (int w = 0; w < kNW; ++w) ai[w] = alpha[(int64_t)kNW * i + w];
     load_lattice(cell, images, bi, L);
   } else {
     load_lattice(nullptr, nullptr, 0, L);
@@ -399,11 +415,13 @@ __global__ __launch_bounds__(64, 2) void d4_pair_kernel(
       st.x[lane] = pos[3 * j];
       st.y[lane] = pos[3 * j + 1];
       st.z[lane] = pos[3 * j + 2];
-      st.sp[lane] = species[j];
+      const double qj = r4r2[species[j]];
+      st.p[lane] = qj;
+      st.q[lane] = sqrt(qj);
       st.b[lane] = batch[j];
       if (BACKWARD) st.w[lane] = g_e2[j];
 #pragma unroll
-      for (int w = 0; w < kNW; ++w) sa[w][lane] = alpha[(int64_t)kNW * j + w];
+      for (int w = 0; w < kNW; ++w) sa[w][lane] = alpha[(int64_t)kNW * j + w] * c_cp3[w];
     }
     __syncthreads();
     if (!live) continue;
@@ -412,24 +430,24 @@ __global__ __launch_bounds__(64, 2) void d4_pair_kernel(
       double c6 = 0.0;
 #pragma unroll
       for (int w = 0; w < kNW; ++w) c6 += ai[w] * sa[w][jj];
-      const double rr = 3.0 * qi * r4r2[st.sp[jj]];
+      // rr = 3 r4r2_i r4r2_j and R0 = a1 sqrt(rr) + a2, sqrt(rr) = sqrt(3 r4r2_i) sqrt(r4r2_j)
+      const double rr = 3.0 * qi * st.p[jj];
       const double s8rr = prm.s8 * rr;
-      const double r0 = prm.a1 * sqrt(rr) + prm.a2;
+      const double r0 = prm.a1 * (sq3qi * st.q[jj]) + prm.a2;
       const double r02 = r0 * r0;
       const double r06 = r02 * r02 * r02, r08 = r06 * r02;
       const double dx = xi - st.x[jj], dy = yi - st.y[jj], dz = zi - st.z[jj];
       const double bx = dx * kInvBohr, by = dy * kInvBohr, bz = dz * kInvBohr;
       const double wsum = BACKWARD ? gi + st.w[jj] : 0.0;
       double fsum = 0.0;  // sum over images of f(r): d E / d C6 of the pair
-      int lo[3], hi[3];
-      image_window(L, dx, dy, dz, prm.cutoff * kBohr, lo, hi);
-      for (int n0 = lo[0]; n0 <= hi[0]; ++n0)
-        for (int n1 = lo[1]; n1 <= hi[1]; ++n1) {
+      const ImageRange win = image_window(L, dx, dy, dz, prm.cutoff * kBohr);
+      for (int n0 = win.lo0; n0 <= win.hi0; ++n0)
+        for (int n1 = win.lo1; n1 <= win.hi1; ++n1) {
           // the image's vector in bohr, d + n @ cell
           const double px = bx + n0 * L.ab[0] + n1 * L.ab[3];
           const double py = by + n0 * L.ab[1] + n1 * L.ab[4];
           const double pz = bz + n0 * L.ab[2] + n1 * L.ab[5];
-          for (int n2 = lo[2]; n2 <= hi[2]; ++n2) {
+          for (int n2 = win.lo2; n2 <= win.hi2; ++n2) {
             const double vx = px + n2 * L.ab[6], vy = py + n2 * L.ab[7], vz = pz + n2 * L.ab[8];
             const double r2 = vx * vx + vy * vy + vz * vz;
             if (r2 <= 0.0 || r2 > rc2) continue;
@@ -468,7 +486,7 @@ __global__ __launch_bounds__(64, 2) void d4_pair_kernel(
       if (BACKWARD && fsum != 0.0) {
         const double k = -0.5 * wsum * fsum;
 #pragma unroll
-        for (int w = 0; w < kNW; ++w) da[w] += k * c_cp3[w] * sa[w][jj];
+        for (int w = 0; w < kNW; ++w) da[w] += k * sa[w][jj];
       }
     }
   }
@@ -619,16 +637,15 @@ __global__ __launch_bounds__(64) void d3_pair_kernel(
       const double dx = xi - st.x[jj], dy = yi - st.y[jj], dz = zi - st.z[jj];
       const double wsum = BACKWARD ? gi + st.w[jj] : 0.0;
       double fsum = 0.0;
-      int lo[3], hi[3];
-      image_window(L, dx, dy, dz, prm.cutoff * kBohr, lo, hi);
+      const ImageRange win = image_window(L, dx, dy, dz, prm.cutoff * kBohr);
       const double bx = dx * kInvBohr, by = dy * kInvBohr, bz = dz * kInvBohr;
-      for (int n0 = lo[0]; n0 <= hi[0]; ++n0)
-        for (int n1 = lo[1]; n1 <= hi[1]; ++n1) {
+      for (int n0 = win.lo0; n0 <= win.hi0; ++n0)
+        for (int n1 = win.lo1; n1 <= win.hi1; ++n1) {
           // the image's vector in bohr, d + n @ cell
           const double px = bx + n0 * L.ab[0] + n1 * L.ab[3];
           const double py = by + n0 * L.ab[1] + n1 * L.ab[4];
           const double pz = bz + n0 * L.ab[2] + n1 * L.ab[5];
-          for (int n2 = lo[2]; n2 <= hi[2]; ++n2) {
+          for (int n2 = win.lo2; n2 <= win.hi2; ++n2) {
             const double vx = px + n2 * L.ab[6], vy = py + n2 * L.ab[7], vz = pz + n2 * L.ab[8];
             const double r2 = vx * vx + vy * vy + vz * vz;
             if (r2 <= 0.0 || r2 > rc2) continue;
