@@ -22,6 +22,7 @@ from __future__ import annotations
 import argparse
 import copy
 import json
+import math
 import os
 import sys
 import time
@@ -260,13 +261,74 @@ def cpu_baseline(g, model, rc, kw, max_edges: int, min_seconds: float = 10.0) ->
                       f"os.cpu_count()={os.cpu_count()}"}
 
 
-def bench_d4(steps: int, warmup: int) -> dict:
+def _d4_sample_pairs(pos: np.ndarray, cell: np.ndarray, k: int, cutoff: float):
+    """Directed pair images (dst < k, any src) within ``cutoff`` Angstrom, brute force over
+    the image range that covers it: dst, src, shift arrays (the CPU baseline's sample)."""
+    inv = np.linalg.inv(cell)
+    reps = [int(math.ceil(cutoff * float(np.linalg.norm(inv[:, a])))) for a in range(3)]
+    dst, src, sh = [], [], []
+    for a in range(-reps[0], reps[0] + 1):
+        for b in range(-reps[1], reps[1] + 1):
+            for c in range(-reps[2], reps[2] + 1):
+                t = a * cell[0] + b * cell[1] + c * cell[2]
+                d = pos[:k, None, :] - pos[None, :, :] + t
+                r2 = (d * d).sum(-1)
+                ii, jj = np.nonzero((r2 <= cutoff * cutoff) & (r2 > 0))
+                dst.append(ii)
+                src.append(jj)
+                sh.append(np.repeat(np.array([[a, b, c]]), len(ii), axis=0))
+    return np.concatenate(dst), np.concatenate(src), np.concatenate(sh)
+
+
+def cpu_baseline_d4(s, tables, alpha: np.ndarray, model, k: int = 200,
+                    min_seconds: float = 10.0) -> dict:
+    """The oracle's two-body D4 (PyTorch on the CPU, float64) with its position gradient,
+    over the pair images of the first ``k`` receivers (enumeration included), repeated
+    until about ``min_seconds``; alpha(i w) given (from the GPU run of the same step)."""
+    import oracle.d4 as D
+    pos, cell = np.asarray(s.pos, dtype=np.float64), np.asarray(s.cell, dtype=np.float64)
+    z = torch.as_tensor(np.asarray(s.numbers))
+    a_t = torch.as_tensor(alpha)
+    prm = dict(D.PBE0_D4)
+    cut_aa = model.cutoff_pair
+    reps, dt, n_terms = 0, 0.0, 0
+    t0 = time.perf_counter()
+    while reps < 30 and (reps == 0 or dt < min_seconds):
+        dst, src, sh = _d4_sample_pairs(pos, cell, k, cut_aa)
+        pt = torch.tensor(pos, requires_grad=True)
+        v = D.edge_vectors_au(pt, torch.as_tensor(cell), dst, src, sh)
+        r = torch.linalg.norm(v, dim=-1)
+        e2 = D.two_body(z, dst, src, r, a_t, tables, prm, cut_aa / D.BOHR, 0.0, len(pos))
+        (g,) = torch.autograd.grad(e2.sum(), [pt])
+        n_terms = len(dst)
+        reps += 1
+        dt = time.perf_counter() - t0
+    return {"value": reps * n_terms / dt, "unit": "terms/s", "cores": torch.get_num_threads(),
+            "kind": "port", "seconds": round(dt, 2), "steps": reps,
+            "sample": f"{reps} x the two-body energy + position gradient over the {n_terms} "
+                      f"pair-image terms of the first {k} of {len(pos)} receivers (pair "
+                      f"enumeration included; alpha(i w) given), oracle PyTorch-CPU float64, "
+                      f"torch threads={torch.get_num_threads()}"}
+
+
+# algorithmic float64 flops per launch of the D4 kernels (M pair-image terms within the
+# pair cutoff, P = N (N + 1) / 2 atom pairs, M_cn CN terms): the forward pair and CN
+# counts are the survey's 60 M + 46 P and 40 M_cn; the pair backward adds per term the
+# r-derivative of the damped sum and the force and cell-gradient products (35) and per
+# pair the two atoms' d C6 / d alpha (2 x 46): 95 M + 138 P
+D4_FLOPS = {"xnn_d4_two_body": lambda M, P, Mc: 60 * M + 46 * P,
+            "xnn_d4_two_body_backward": lambda M, P, Mc: 95 * M + 138 * P,
+            "xnn_d4_coordination": lambda M, P, Mc: 40 * Mc}
+FP64_PEAK_TFLOPS = 78.6
+
+
+def bench_d4(steps: int, warmup: int, cpu: bool = True) -> dict:
     """D4 two-body energy + forces + stress of the 5,000-atom organic box (36.8 A cell,
     upstream cutoffs 60 / 30 / 25 bohr): CN kernel, polarizabilities, pair kernel and
     both backward kernels per step. The charges are fixed (zero): the dense periodic
     charge solve of 5,000 atoms is not part of this path."""
     import xnn_amd.dispersion as XD
-    from xnn_amd import synthetic
+    from xnn_amd import _lib, synthetic
     dev = torch.device("cuda:0")
     s = synthetic.organic_box(seed=0)
     tables = XD.load_d4_tables(os.path.join(ROOT, "tests", "golden", "d4_tables_hcnoar.npz"))
@@ -283,38 +345,69 @@ def bench_d4(steps: int, warmup: int) -> dict:
         cell = cell0.clone().requires_grad_(True)
         out = model.evaluate(z, pos, cell, pbc, n_atoms, charges=q)
         gp, gc = torch.autograd.grad(out["energy"].sum(), [pos, cell])
-        return out["energy"], gp, gc
+        return out, gp, gc
 
     for _ in range(warmup):
         step()
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for _ in range(steps):
-        e, gp, gc = step()
+        out, gp, gc = step()
     torch.cuda.synchronize()
     ms = (time.perf_counter() - t0) / steps * 1e3
-    # pair-image terms within the pair cutoff (for the rate), counted image by image
+    e = out["energy"].detach()
+    # per-kernel HIP events (launch stream) over a second set of steps
+    kernels = list(D4_FLOPS) + ["xnn_d4_coordination_backward", "xnn_d4_polarizabilities",
+                                "xnn_d4_polarizabilities_backward"]
+    _lib.timed.clear()
+    _lib.time_launches(*kernels)
+    for _ in range(steps):
+        step()
+    torch.cuda.synchronize()
+    kernel_us = {k: float(np.mean([a.elapsed_time(b) * 1e3 for a, b in v]))
+                 for k, v in _lib.timed.items() if v}
+    _lib.timed.clear()
+    # pair-image terms within the pair cutoff (for the rate) and CN terms, image by image
     imgs = XD.image_counts(cell0, pbc, model.cutoff_pair)[0].tolist()
-    n_terms = 0
+    n_terms, n_cn = 0, 0
     with torch.no_grad():
         d0 = pos0[:, None, :] - pos0[None, :, :]
-        rc2 = model.cutoff_pair ** 2
+        rc2, rcn2 = model.cutoff_pair ** 2, model.cutoff_cn ** 2
         for a in range(-imgs[0], imgs[0] + 1):
             for b in range(-imgs[1], imgs[1] + 1):
                 for c in range(-imgs[2], imgs[2] + 1):
                     t = a * cell0[0, 0] + b * cell0[0, 1] + c * cell0[0, 2]
                     r2 = ((d0 + t) ** 2).sum(-1)
                     n_terms += int(((r2 <= rc2) & (r2 > 0)).sum())
+                    n_cn += int(((r2 <= rcn2) & (r2 > 0)).sum())
         del d0
-    return {"metric": "D4 pair-image terms/s, energy+forces+stress, 5000-atom organic box",
-            "value": n_terms / (ms * 1e-3), "unit": "terms/s", "n_gpus": 1, "steps": steps,
-            "warmup": warmup, "ms_per_step": ms, "higher_is_better": True, "scaling": "weak",
-            "vs_baseline": None, "dtype": "f64", "data": "synthetic (seeded generator)",
-            "config": {"workload": "d4_organic_box_5000_atoms", "atoms": len(s.numbers),
-                       "pair_image_terms": n_terms, "cutoff_pair_bohr": 60.0,
-                       "cutoff_cn_bohr": 30.0, "cutoff_eeq_cn_bohr": 25.0,
-                       "charges": "fixed zero (charge model not timed)",
-                       "energy_eV": float(e[0])}}
+    N = len(s.numbers)
+    dominant = max(kernel_us, key=lambda k: kernel_us[k])
+    flops = D4_FLOPS[dominant](n_terms, N * (N + 1) // 2, n_cn) if dominant in D4_FLOPS else None
+    achieved = flops / (kernel_us[dominant] * 1e-6) / 1e12 if flops else None
+    roofline = {"bound": "fp64", "kernel": dominant,
+                "achieved": None if achieved is None else round(achieved, 2),
+                "peak": FP64_PEAK_TFLOPS, "unit": "TFLOP/s",
+                "frac": None if achieved is None else round(achieved / FP64_PEAK_TFLOPS, 4),
+                "traffic": None, "algorithmic_flops": flops,
+                "mean_launch_us": round(kernel_us[dominant], 2),
+                "timing": "eager step, HIP events on the launch stream"}
+    result = {"metric": "D4 pair-image terms/s, energy+forces+stress, 5000-atom organic box",
+              "value": n_terms / (ms * 1e-3), "unit": "terms/s", "n_gpus": 1, "steps": steps,
+              "warmup": warmup, "ms_per_step": ms, "higher_is_better": True, "scaling": "weak",
+              "vs_baseline": None, "dtype": "f64", "data": "synthetic (seeded generator)",
+              "config": {"workload": "d4_organic_box_5000_atoms", "atoms": N,
+                         "pair_image_terms": n_terms, "cn_terms": n_cn,
+                         "cutoff_pair_bohr": 60.0, "cutoff_cn_bohr": 30.0,
+                         "cutoff_eeq_cn_bohr": 25.0,
+                         "charges": "fixed zero (charge model not timed)",
+                         "energy_eV": float(e[0]),
+                         "kernel_mean_us": {k: round(v, 2) for k, v in kernel_us.items()}},
+              "roofline": roofline}
+    if cpu:
+        alpha = out["dynamic_polarizabilities"].detach().cpu().numpy()
+        result["cpu_baseline"] = cpu_baseline_d4(s, tables, alpha, model)
+    return result
 
 
 def main() -> None:
@@ -346,7 +439,7 @@ def main() -> None:
         copy_calibration()
         return
     if args.config == "d4":
-        print(json.dumps(bench_d4(args.steps, args.warmup)), flush=True)
+        print(json.dumps(bench_d4(args.steps, args.warmup, cpu=args.cpu_edges > 0)), flush=True)
         return
     device = torch.device("cuda:0")
     torch.cuda.set_device(device)
