@@ -410,12 +410,130 @@ def bench_d4(steps: int, warmup: int, cpu: bool = True) -> dict:
     return result
 
 
+def cpu_baseline_d3(s, tables, w: np.ndarray, model, k: int = 200,
+                    min_seconds: float = 10.0) -> dict:
+    """The oracle's two-body D3 (BJ, PyTorch on the CPU, float64) with its position
+    gradient over the pair images of the first ``k`` receivers (enumeration and C6 from the
+    reference weights included), repeated until about ``min_seconds``; weights given."""
+    import oracle.d3 as D3
+    pos, cell = np.asarray(s.pos, dtype=np.float64), np.asarray(s.cell, dtype=np.float64)
+    sp = D3.species_of(tables, s.numbers)
+    w_t = torch.as_tensor(w)
+    prm = dict(D3.PBE0_D3BJ)
+    cut_aa = model.cutoff_pair
+    reps, dt, n_terms = 0, 0.0, 0
+    t0 = time.perf_counter()
+    while reps < 30 and (reps == 0 or dt < min_seconds):
+        dst, src, sh = _d4_sample_pairs(pos, cell, k, cut_aa)
+        pt = torch.tensor(pos, requires_grad=True)
+        v = D3.edge_vectors_au(pt, torch.as_tensor(cell), dst, src, sh)
+        r = torch.linalg.norm(v, dim=-1)
+        c6 = D3.pair_c6(sp, w_t, torch.as_tensor(dst), torch.as_tensor(src), tables)
+        e2 = D3.two_body(sp, dst, src, r, c6, tables, prm, "bj", cut_aa / D3.BOHR, 0.0,
+                         len(pos))
+        (g,) = torch.autograd.grad(e2.sum(), [pt])
+        n_terms = len(dst)
+        reps += 1
+        dt = time.perf_counter() - t0
+    return {"value": reps * n_terms / dt, "unit": "terms/s", "cores": torch.get_num_threads(),
+            "kind": "port", "seconds": round(dt, 2), "steps": reps,
+            "sample": f"{reps} x the BJ two-body energy + position gradient over the {n_terms} "
+                      f"pair-image terms of the first {k} of {len(pos)} receivers (pair "
+                      f"enumeration and C6 included; reference weights given), oracle "
+                      f"PyTorch-CPU float64, torch threads={torch.get_num_threads()}"}
+
+
+# D3 (BJ) algorithmic float64 flops per launch: per pair-image term as D4 (60 energy, +35
+# for the backward); per atom pair C6 = W_i . C6ref . W_j (56 FMA = 112) and, backward,
+# both atoms' dC6/dW (2 x 112)
+D3_FLOPS = {"xnn_d3_two_body": lambda M, P: 60 * M + 112 * P,
+            "xnn_d3_two_body_backward": lambda M, P: 95 * M + 336 * P}
+
+
+def bench_d3(steps: int, warmup: int, cpu: bool = True) -> dict:
+    """D3(BJ) two-body energy + forces + stress of the same 5,000-atom organic box
+    (upstream cutoffs 60 / 40 bohr): CN kernel, reference weights, pair kernel and both
+    backward kernels per step (row 17 of the path; the survey's configs time D4)."""
+    import xnn_amd.dispersion as XD
+    from xnn_amd import _lib, synthetic
+    dev = torch.device("cuda:0")
+    s = synthetic.organic_box(seed=0)
+    tables = XD.load_d3_tables(os.path.join(ROOT, "tests", "golden", "d3_tables_hcnoar.npz"))
+    model = XD.DFTD3(tables).to(dev)
+    z = torch.tensor(s.numbers, device=dev)
+    pos0 = torch.tensor(s.pos, dtype=torch.float64, device=dev)
+    cell0 = torch.tensor(s.cell, dtype=torch.float64, device=dev)[None]
+    pbc = torch.ones((1, 3), dtype=torch.bool)
+    n_atoms = torch.tensor([len(s.numbers)])
+
+    def step():
+        pos = pos0.clone().requires_grad_(True)
+        cell = cell0.clone().requires_grad_(True)
+        out = model.evaluate(z, pos, cell, pbc, n_atoms)
+        gp, gc = torch.autograd.grad(out["energy"].sum(), [pos, cell])
+        return out, gp, gc
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        out, gp, gc = step()
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) / steps * 1e3
+    kernels = list(D3_FLOPS) + ["xnn_d3_coordination", "xnn_d3_coordination_backward"]
+    _lib.timed.clear()
+    _lib.time_launches(*kernels)
+    for _ in range(steps):
+        step()
+    torch.cuda.synchronize()
+    kernel_us = {k: float(np.mean([a.elapsed_time(b) * 1e3 for a, b in v]))
+                 for k, v in _lib.timed.items() if v}
+    _lib.timed.clear()
+    imgs = XD.image_counts(cell0, pbc, model.cutoff_pair)[0].tolist()
+    n_terms = 0
+    with torch.no_grad():
+        d0 = pos0[:, None, :] - pos0[None, :, :]
+        rc2 = model.cutoff_pair ** 2
+        for a in range(-imgs[0], imgs[0] + 1):
+            for b in range(-imgs[1], imgs[1] + 1):
+                for c in range(-imgs[2], imgs[2] + 1):
+                    t = a * cell0[0, 0] + b * cell0[0, 1] + c * cell0[0, 2]
+                    r2 = ((d0 + t) ** 2).sum(-1)
+                    n_terms += int(((r2 <= rc2) & (r2 > 0)).sum())
+        del d0
+    N = len(s.numbers)
+    dominant = max(kernel_us, key=lambda k: kernel_us[k])
+    flops = D3_FLOPS[dominant](n_terms, N * (N + 1) // 2) if dominant in D3_FLOPS else None
+    achieved = flops / (kernel_us[dominant] * 1e-6) / 1e12 if flops else None
+    result = {"metric": "D3(BJ) pair-image terms/s, energy+forces+stress, 5000-atom organic box",
+              "value": n_terms / (ms * 1e-3), "unit": "terms/s", "n_gpus": 1, "steps": steps,
+              "warmup": warmup, "ms_per_step": ms, "higher_is_better": True, "scaling": "weak",
+              "vs_baseline": None, "dtype": "f64", "data": "synthetic (seeded generator)",
+              "config": {"workload": "d3bj_organic_box_5000_atoms", "atoms": N,
+                         "pair_image_terms": n_terms, "cutoff_pair_bohr": 60.0,
+                         "cutoff_cn_bohr": 40.0, "energy_eV": float(out["energy"].detach()[0]),
+                         "kernel_mean_us": {k: round(v, 2) for k, v in kernel_us.items()}},
+              "roofline": {"bound": "fp64", "kernel": dominant,
+                           "achieved": None if achieved is None else round(achieved, 2),
+                           "peak": FP64_PEAK_TFLOPS, "unit": "TFLOP/s",
+                           "frac": None if achieved is None else round(achieved / FP64_PEAK_TFLOPS, 4),
+                           "traffic": None, "algorithmic_flops": flops,
+                           "mean_launch_us": round(kernel_us[dominant], 2),
+                           "timing": "eager step, HIP events on the launch stream"}}
+    if cpu:
+        result["cpu_baseline"] = cpu_baseline_d3(s, tables, out["weights"].detach().cpu().numpy(),
+                                                 model)
+    return result
+
+
 def main() -> None:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--config", default="water", choices=["water", "argon", "ragged", "d4"])
+    ap.add_argument("--config", default="water",
+                    choices=["water", "argon", "ragged", "d4", "d3"])
     ap.add_argument("--graph", action=argparse.BooleanOptionalAction, default=True,
                     help="time replays of the step captured as one HIP graph")
     ap.add_argument("--cpu-edges", type=int, default=480_000,
@@ -440,6 +558,9 @@ def main() -> None:
         return
     if args.config == "d4":
         print(json.dumps(bench_d4(args.steps, args.warmup, cpu=args.cpu_edges > 0)), flush=True)
+        return
+    if args.config == "d3":
+        print(json.dumps(bench_d3(args.steps, args.warmup, cpu=args.cpu_edges > 0)), flush=True)
         return
     device = torch.device("cuda:0")
     torch.cuda.set_device(device)

@@ -553,8 +553,15 @@ __device__ inline void d3_damp(const D3PairParams& p, double r, double r0, doubl
 // BACKWARD = true:  partial[cy][0..11][i] = grad_pos (3), cell gradient (9), and
 //                   partial_w[cy][a][i] = dE / dW_i[a] (7).
 // C6_ij = sum_ab W_i[a] W_j[b] C6ref[s_i][s_j][a][b] (d3.py:651-674).
-template <bool BACKWARD>
-__global__ __launch_bounds__(64) void d3_pair_kernel(
+// D3 reference-C6 vectors staged per receiver species (see d3_pair_kernel): species rows
+// padded by two doubles so that lanes of different species read different banks
+constexpr int kD3SvStride = kNR * kD4Sub + 2;
+constexpr int kD3MaxStaged = 16;  // 16 x 3.5 KB of LDS at most
+
+// BJ: the rational damping compiled alone (the default; the general loop with all four
+// dampings holds more registers)
+template <bool BACKWARD, bool STAGED, bool BJ>
+__global__ __launch_bounds__(64, 2) void d3_pair_kernel(
     const double* __restrict__ pos, int64_t n_nodes, const int32_t* __restrict__ species,
     const int32_t* __restrict__ batch, const int64_t* __restrict__ node_ptr,
     const double* __restrict__ cell, const int32_t* __restrict__ images,
@@ -563,7 +570,11 @@ __global__ __launch_bounds__(64) void d3_pair_kernel(
     D3PairParams prm, const double* __restrict__ g_e2, int64_t chunk, int64_t n_cy,
     double* __restrict__ partial, double* __restrict__ partial_w) {
   __shared__ D4Stage st;
-  __shared__ double sw_[kNR][kD4Sub];
+  // STAGED: for every receiver species s, v_s[a] = sum_b C6ref[s][s_j][a][b] W_j[b] of each
+  // staged source j (dynamic LDS, kD3SvStride doubles per species), so that a pair reads
+  // its seven values instead of the 7 x 7 reference block; otherwise the sources' weights
+  __shared__ double sw_[STAGED ? 1 : kNR][kD4Sub];
+  extern __shared__ double d3_sv[];
   const int lane = threadIdx.x;
   const int64_t t = blockIdx.x, cy = blockIdx.y;
   const int64_t i = t * kD4Tile + lane;
@@ -582,7 +593,7 @@ __global__ __launch_bounds__(64) void d3_pair_kernel(
     wi[a] = 0.0;
     dw[a] = 0.0;
   }
-  double xi = 0, yi = 0, zi = 0, qi = 0, gi = 0;
+  double xi = 0, yi = 0, zi = 0, qi = 0, sq3qi = 0, gi = 0;
   int bi = -1, si = 0;
   Lattice L;
   if (live) {
@@ -591,6 +602,7 @@ __global__ __launch_bounds__(64) void d3_pair_kernel(
     zi = pos[3 * i + 2];
     si = species[i];
     qi = r4r2[si];
+    sq3qi = sqrt(3.0 * qi);
     bi = batch[i];
     if (BACKWARD) gi = g_e2[i];
 #pragma unroll
@@ -600,6 +612,10 @@ __global__ __launch_bounds__(64) void d3_pair_kernel(
     load_lattice(nullptr, nullptr, 0, L);
   }
   const double rc2 = prm.cutoff * prm.cutoff;
+  // below r = cutoff - width the switch is 1 with zero slope
+  const double wzone = prm.width > 0.0 ? fmax(prm.cutoff - fmin(prm.width, prm.cutoff), 0.0)
+                                       : prm.cutoff;
+  const double wz2 = wzone * wzone;
   for (int64_t base = j0; base < j1; base += kD4Sub) {
     const int cnt = (int)std::min<int64_t>(kD4Sub, j1 - base);
     __syncthreads();
@@ -608,32 +624,60 @@ __global__ __launch_bounds__(64) void d3_pair_kernel(
       st.x[lane] = pos[3 * j];
       st.y[lane] = pos[3 * j + 1];
       st.z[lane] = pos[3 * j + 2];
-      st.sp[lane] = species[j];
+      const int sj = species[j];
+      st.sp[lane] = sj;
       st.b[lane] = batch[j];
+      st.p[lane] = r4r2[sj];
+      st.q[lane] = sqrt(st.p[lane]);
       if (BACKWARD) st.w[lane] = g_e2[j];
+      if (STAGED) {
+        double wj[kNR];
 #pragma unroll
-      for (int a = 0; a < kNR; ++a) sw_[a][lane] = wref[(int64_t)kNR * j + a];
+        for (int b = 0; b < kNR; ++b) wj[b] = wref[(int64_t)kNR * j + b];
+        for (int s2 = 0; s2 < n_species; ++s2) {
+          const double* blk = c6ref + ((int64_t)s2 * n_species + sj) * (kNR * kNR);
+#pragma unroll
+          for (int a = 0; a < kNR; ++a) {
+            double sa = 0.0;
+#pragma unroll
+            for (int b = 0; b < kNR; ++b) sa += blk[a * kNR + b] * wj[b];
+            d3_sv[s2 * kD3SvStride + a * kD4Sub + lane] = sa;
+          }
+        }
+      } else {
+#pragma unroll
+        for (int a = 0; a < kNR; ++a) sw_[a][lane] = wref[(int64_t)kNR * j + a];
+      }
     }
     __syncthreads();
     if (!live) continue;
     for (int jj = 0; jj < cnt; ++jj) {
       if (st.b[jj] != bi) continue;
       const int sj = st.sp[jj];
-      const double* blk = c6ref + ((int64_t)si * n_species + sj) * (kNR * kNR);
       double v[kNR];  // v[a] = sum_b C6ref[a][b] W_j[b]
+      if (STAGED) {
 #pragma unroll
-      for (int a = 0; a < kNR; ++a) {
-        double sa = 0.0;
+        for (int a = 0; a < kNR; ++a) v[a] = d3_sv[si * kD3SvStride + a * kD4Sub + jj];
+      } else {
+        const double* blk = c6ref + ((int64_t)si * n_species + sj) * (kNR * kNR);
 #pragma unroll
-        for (int b = 0; b < kNR; ++b) sa += blk[a * kNR + b] * sw_[b][jj];
-        v[a] = sa;
+        for (int a = 0; a < kNR; ++a) {
+          double sa = 0.0;
+#pragma unroll
+          for (int b = 0; b < kNR; ++b) sa += blk[a * kNR + b] * sw_[b][jj];
+          v[a] = sa;
+        }
       }
       double c6 = 0.0;
 #pragma unroll
       for (int a = 0; a < kNR; ++a) c6 += wi[a] * v[a];
-      const double rr = 3.0 * qi * r4r2[sj];
-      const double r0 = (prm.damping == 0 || prm.damping == 3) ? prm.a1 * sqrt(rr) + prm.a2
+      // rr = 3 r4r2_i r4r2_j; BJ and op: R0 = a1 sqrt(rr) + a2 with sqrt(rr) =
+      // sqrt(3 r4r2_i) sqrt(r4r2_j), zero and mzero: R0 from the vdW radii table
+      const double rr = 3.0 * qi * st.p[jj];
+      const double r0 = (prm.damping == 0 || prm.damping == 3) ? prm.a1 * (sq3qi * st.q[jj]) + prm.a2
                                                                : rvdw[si * n_species + sj];
+      const double s8rr = prm.s8 * rr;
+      const double r02 = r0 * r0, r06 = r02 * r02 * r02, r08 = r06 * r02;
       const double dx = xi - st.x[jj], dy = yi - st.y[jj], dz = zi - st.z[jj];
       const double wsum = BACKWARD ? gi + st.w[jj] : 0.0;
       double fsum = 0.0;
@@ -649,20 +693,43 @@ __global__ __launch_bounds__(64) void d3_pair_kernel(
             const double vx = px + n2 * L.ab[6], vy = py + n2 * L.ab[7], vz = pz + n2 * L.ab[8];
             const double r2 = vx * vx + vy * vy + vz * vz;
             if (r2 <= 0.0 || r2 > rc2) continue;
-            const double rinv = rsq_nr(r2);
-            const double r = r2 * rinv;
-            double sw, dsw, t6, t8, d6, d8;
-            switch_d(r, prm.cutoff, prm.width, sw, dsw);
-            d3_damp(prm, r, r0, t6, t8, d6, d8);
-            const double g = prm.s6 * t6 + prm.s8 * rr * t8;
-            const double f = sw * g;
+            double f, df_r;  // f(r) and (d f / d r) / r
+            if (BJ) {
+              // BJ, as the D4 pair kernel: t6 = 1 / (r^6 + R0^6), t8 = 1 / (r^8 + R0^8) from
+              // one reciprocal, r itself only inside the switching zone
+              const double r4 = r2 * r2, r6 = r4 * r2, r8 = r6 * r2;
+              const double p6 = r6 + r06, p8 = r8 + r08;
+              const double inv = rcp_nr(p6 * p8);
+              const double t6 = p8 * inv, t8 = p6 * inv;
+              const double g = prm.s6 * t6 + s8rr * t8;
+              double sw = 1.0, dsw_r = 0.0;
+              if (r2 > wz2) {
+                const double rinv = rsq_nr(r2);
+                double dsw;
+                switch_d(r2 * rinv, prm.cutoff, prm.width, sw, dsw);
+                dsw_r = dsw * rinv;
+              }
+              f = sw * g;
+              df_r = BACKWARD ? dsw_r * g + sw * (-6.0 * prm.s6 * r4 * t6 * t6 -
+                                                  8.0 * s8rr * r6 * t8 * t8)
+                              : 0.0;
+            } else {
+              // every damping (BJ included: prm.damping selects), r explicit
+              const double rinv = rsq_nr(r2);
+              const double r = r2 * rinv;
+              double sw, dsw, t6, t8, d6, d8;
+              switch_d(r, prm.cutoff, prm.width, sw, dsw);
+              d3_damp(prm, r, r0, t6, t8, d6, d8);
+              const double g = prm.s6 * t6 + s8rr * t8;
+              f = sw * g;
+              df_r = BACKWARD ? (dsw * g + sw * (prm.s6 * d6 + s8rr * d8)) * rinv : 0.0;
+            }
             if (!BACKWARD) {
               acc[0] += -0.5 * c6 * f;
             } else {
               fsum += f;
-              const double df = dsw * g + sw * (prm.s6 * d6 + prm.s8 * rr * d8);
               // d r_bohr / d v_Angstrom = v_bohr / (r_bohr bohr)
-              const double s = -0.5 * kInvBohr * c6 * df * rinv;
+              const double s = -0.5 * kInvBohr * c6 * df_r;
               acc[0] += wsum * s * vx;
               acc[1] += wsum * s * vy;
               acc[2] += wsum * s * vz;
@@ -1108,10 +1175,16 @@ int xnn_d3_two_body(const double* pos, int64_t n_nodes, const int32_t* species,
               workspace_bytes, need);
   hipStream_t s = as_hip(stream);
   double* part = static_cast<double*>(workspace);
-  hipLaunchKernelGGL(d3_pair_kernel<false>, dim3((unsigned)w.n_tiles, (unsigned)w.n_cy),
-                     dim3(kD4Tile), 0, s, pos, n_nodes, species, batch, node_ptr, cell, images,
-                     r4r2, rvdw, c6ref, n_species, weights, d3_params(prm), nullptr, w.chunk,
-                     w.n_cy, part, nullptr);
+  {
+    const size_t sv_bytes = (size_t)n_species * kD3SvStride * sizeof(double);
+    const bool staged = n_species <= kD3MaxStaged, bj = prm->damping == 0;
+    auto k = staged ? (bj ? d3_pair_kernel<false, true, true> : d3_pair_kernel<false, true, false>)
+                    : (bj ? d3_pair_kernel<false, false, true> : d3_pair_kernel<false, false, false>);
+    hipLaunchKernelGGL(k, dim3((unsigned)w.n_tiles, (unsigned)w.n_cy), dim3(kD4Tile),
+                       staged ? sv_bytes : 0, s, pos, n_nodes, species, batch, node_ptr, cell,
+                       images, r4r2, rvdw, c6ref, n_species, weights, d3_params(prm), nullptr, w.chunk, w.n_cy, part,
+                       nullptr);
+  }
   XNN_LAUNCH_CHECK();
   reduce_into(part, n_nodes, 1, 0, 1, w.n_cy, e2, s);
   XNN_LAUNCH_CHECK();
@@ -1139,10 +1212,16 @@ int xnn_d3_two_body_backward(const double* pos, int64_t n_nodes, const int32_t* 
   hipStream_t s = as_hip(stream);
   double* part = static_cast<double*>(workspace);
   double* part_w = part + w.n_cy * 12 * n_nodes;
-  hipLaunchKernelGGL(d3_pair_kernel<true>, dim3((unsigned)w.n_tiles, (unsigned)w.n_cy),
-                     dim3(kD4Tile), 0, s, pos, n_nodes, species, batch, node_ptr, cell, images,
-                     r4r2, rvdw, c6ref, n_species, weights, d3_params(prm), g_e2, w.chunk,
-                     w.n_cy, part, part_w);
+  {
+    const size_t sv_bytes = (size_t)n_species * kD3SvStride * sizeof(double);
+    const bool staged = n_species <= kD3MaxStaged, bj = prm->damping == 0;
+    auto k = staged ? (bj ? d3_pair_kernel<true, true, true> : d3_pair_kernel<true, true, false>)
+                    : (bj ? d3_pair_kernel<true, false, true> : d3_pair_kernel<true, false, false>);
+    hipLaunchKernelGGL(k, dim3((unsigned)w.n_tiles, (unsigned)w.n_cy), dim3(kD4Tile),
+                       staged ? sv_bytes : 0, s, pos, n_nodes, species, batch, node_ptr, cell,
+                       images, r4r2, rvdw, c6ref, n_species, weights, d3_params(prm), g_e2, w.chunk, w.n_cy, part,
+                       part_w);
+  }
   XNN_LAUNCH_CHECK();
   reduce_into(part, n_nodes, 12, 0, 3, w.n_cy, grad_pos, s);
   reduce_into(part, n_nodes, 12, 3, 9, w.n_cy, cell_partial, s);
