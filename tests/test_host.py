@@ -135,3 +135,33 @@ def test_collate_offsets_and_batch():
     assert b.num_graphs == 3 and b.num_nodes == 63
     assert b.num_edges == sum(g.num_edges for g in graphs)
     assert int(b.edge_index.max()) < 63 and torch.equal(b.batch.bincount(), torch.tensor([21] * 3))
+
+
+def test_d4_polarizability_tables_and_argument_checks(lib_path):
+    """DFTD4's element-major kernel tables are the reference tables transposed (refalpha
+    (23, 7, Z) -> (Z, 7, 23)), the module refuses CPU tensors, and the polarizability and
+    readout entry points reject bad arguments on the host (no launch)."""
+    import os
+    import xnn_amd.dispersion as XD
+    from xnn_amd import _lib
+    tables = XD.load_d4_tables(os.path.join(os.path.dirname(__file__), "golden",
+                                            "d4_tables_hcnoar.npz"))
+    d4 = XD.DFTD4(tables)
+    ra = torch.as_tensor(tables["refalpha"])
+    assert d4.k_refalpha.shape == (ra.shape[2], ra.shape[1], ra.shape[0])
+    assert torch.equal(d4.k_refalpha, ra.permute(2, 1, 0))
+    assert torch.equal(d4.k_refcn, torch.as_tensor(tables["refcn"]).t())
+    assert d4.k_ngw.dtype == torch.int32 and d4.k_nref.dtype == torch.int32
+    assert torch.allclose(d4.k_gi, torch.as_tensor(tables["hardness"]) * d4.gc)
+    with pytest.raises(RuntimeError, match="GPU"):
+        d4.polarizabilities(torch.tensor([1, 8]), torch.zeros(2, dtype=torch.float64),
+                            torch.zeros(2, dtype=torch.float64))
+    lib = _lib.load()
+    empty = _lib.D4AlphaTables()                     # n_elements = 0, NULL tables
+    assert lib.xnn_d4_polarizabilities(4, None, None, None, empty, None, None) == _lib.XNN_EINVAL
+    assert b"tables" in lib.xnn_last_error()
+    assert lib.xnn_node_readout(7, None, 4, 8, None, None, None, 0, None, None) == _lib.XNN_EINVAL
+    assert lib.xnn_node_readout(0, None, 4, 8, None, None, 1, 5, None, None) == _lib.XNN_EINVAL
+    assert b"bias and z" in lib.xnn_last_error()
+    assert lib.xnn_node_readout_backward(0, 1, 2, 4, 8, 1, 1, None) == _lib.XNN_EINVAL
+    assert b"g_stride" in lib.xnn_last_error()
