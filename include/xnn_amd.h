@@ -498,6 +498,21 @@ int xnn_edge_plan(const int64_t* edge_index, const int64_t* cell_shifts, int64_t
                   int32_t* overflow, void* workspace, size_t workspace_bytes,
                   xnn_stream_t stream);
 
+/* D3 reference weights (N,7): w_r = exp(-wf (cn - cnref_r)^2) normalized over the
+ * species' nref references (a zero norm: weight 1 on the largest-cnref references).
+ * species (N) int32; nref (S) int32, refcn (S,7) species-major; wf = 4 (d3.py:465).
+ * Replaces DFTD3's weights (d3.py:644-649, dispersion.py:70-121). A species outside
+ * [0, S) gives NaN. */
+int xnn_d3_weights(int64_t n_nodes, const int32_t* species, const double* cn,
+                   int32_t n_species, const int32_t* nref, const double* refcn, double wf,
+                   double* weights, xnn_stream_t stream);
+
+/* g_cn[i] = sum_r g_weights[i,r] d w_r / d cn[i]. */
+int xnn_d3_weights_backward(int64_t n_nodes, const int32_t* species, const double* cn,
+                            int32_t n_species, const int32_t* nref, const double* refcn,
+                            double wf, const double* g_weights, double* g_cn,
+                            xnn_stream_t stream);
+
 /* ------------------------------------------------------------------------ */
 /* Linear per-atom readout of node rows: out[i] = bias[z[i]] + sum_f rows[i,f] w[f]
  * (rows (N,F) row-major, w (F), out (N), all in dtype; z (N) int64 and bias (n_bias)

@@ -119,3 +119,31 @@ def test_forces_match_finite_differences(tables):
         pm[i, a] -= h
         fd = (float(_eval(model, pp, z)[0]["energy"][0]) - float(_eval(model, pm, z)[0]["energy"][0])) / (2 * h)
         assert abs(float(gp[i, a]) - fd) < 1e-7
+
+
+def test_weights_kernel_matches_oracle(tables):
+    """The D3 reference weights and their chain rule to CN from the HIP kernel against the
+    oracle (float64 autograd): every tabulated species, CNs from 0 to past the Gaussian
+    underflow (the largest-reference fallback), and a species outside the tables (NaN)."""
+    import oracle.d3 as D3
+    import xnn_amd.dispersion as XD
+    _note("d3 weights kernel vs oracle")
+    model = XD.DFTD3(tables).to(DEV)
+    rng = np.random.default_rng(31)
+    n_sp = len(tables["z"])
+    s = torch.as_tensor(np.arange(60) % n_sp)
+    cn_np = rng.uniform(0.0, 5.0, 60)
+    cn_np[:4] = 60.0                                 # exp(-4 d^2) underflows: fallback
+    cn = torch.tensor(cn_np, requires_grad=True)
+    ref = D3.weights(s, cn, tables)
+    g_w = torch.tensor(rng.normal(size=ref.shape))
+    (ref_g,) = torch.autograd.grad((ref * g_w).sum(), [cn])
+    cg = cn.detach().to(DEV).requires_grad_(True)
+    w = model.weights(s.to(DEV), cg)
+    (g,) = torch.autograd.grad((w * g_w.to(DEV)).sum(), [cg])
+    np.testing.assert_allclose(w.detach().cpu(), ref.detach(), rtol=1e-13, atol=1e-15)
+    np.testing.assert_allclose(g.cpu(), ref_g, rtol=1e-12, atol=1e-12 * float(ref_g.abs().max()))
+    assert float(g[:4].abs().max()) == 0.0
+    bad = model.weights(torch.tensor([0, n_sp], device=DEV),
+                        torch.tensor([1.0, 1.0], dtype=torch.float64, device=DEV))
+    assert torch.isfinite(bad[0]).all() and torch.isnan(bad[1]).all()

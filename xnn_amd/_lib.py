@@ -104,6 +104,8 @@ _SIGNATURES = {
                                      ctypes.POINTER(D4CnParams), vp, vp, vp, vp, vp, sz, vp],
     "xnn_d4_two_body": [vp, i64, vp, vp, vp, i64, i64, vp, vp, vp, vp,
                         ctypes.POINTER(D4PairParams), vp, vp, sz, vp],
+    "xnn_d3_weights": [i64, vp, vp, i32, vp, vp, dbl, vp, vp],
+    "xnn_d3_weights_backward": [i64, vp, vp, i32, vp, vp, dbl, vp, vp, vp],
     "xnn_node_readout": [i32, vp, i64, i64, vp, vp, vp, i64, vp, vp],
     "xnn_node_readout_backward": [i32, vp, i64, i64, i64, vp, vp, vp],
     "xnn_d4_polarizabilities": [i64, vp, vp, vp, ctypes.POINTER(D4AlphaTables), vp, vp],

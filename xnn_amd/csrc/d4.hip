@@ -946,6 +946,72 @@ __global__ __launch_bounds__(256) void d4_alpha_kernel(
   }
 }
 
+// One thread per atom: the D3 reference weights w_r = g_r / sum_r' g_r' with
+// g_r = exp(-wf (cn - cnref_r)^2) over the species' nref references (d3.py:644-649,
+// dispersion.py:70-121; a zero norm puts weight 1 on the references of the largest cnref).
+// BACKWARD: g_cn = sum_r g_w[r] d w_r / d cn. A species outside the tables gives NaN.
+template <bool BACKWARD>
+__global__ __launch_bounds__(256) void d3_weights_kernel(
+    int64_t n, const int32_t* __restrict__ species, const double* __restrict__ cn,
+    int n_species, const int32_t* __restrict__ nref, const double* __restrict__ refcn,
+    double wf, const double* __restrict__ g_w, double* __restrict__ w_out,
+    double* __restrict__ g_cn) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  const int sp = species[i];
+  const int nr = (sp >= 0 && sp < n_species) ? nref[sp] : -1;
+  if (nr < 0 || nr > kNR) {
+    const double bad = __builtin_nan("");
+    if (!BACKWARD) {
+      for (int r = 0; r < kNR; ++r) w_out[i * kNR + r] = bad;
+    } else {
+      g_cn[i] = bad;
+    }
+    return;
+  }
+  const double c = cn[i];
+  double w[kNR], dw[kNR];
+  double norm = 0.0, dnorm = 0.0;
+#pragma unroll
+  for (int r = 0; r < kNR; ++r) {
+    double g = 0.0, dg = 0.0;
+    if (r < nr) {
+      const double d = c - refcn[sp * kNR + r];
+      g = exp(-wf * (d * d));
+      dg = g * (-2.0 * wf * d);
+    }
+    w[r] = g;
+    dw[r] = dg;
+    norm += g;
+    dnorm += dg;
+  }
+  if (norm > 0.0) {
+#pragma unroll
+    for (int r = 0; r < kNR; ++r) {
+      const double wr = w[r] / norm;
+      dw[r] = (dw[r] - wr * dnorm) / norm;
+      w[r] = wr;
+    }
+  } else {
+    double top = -__builtin_inf();
+    for (int r = 0; r < nr; ++r) top = fmax(top, refcn[sp * kNR + r]);
+#pragma unroll
+    for (int r = 0; r < kNR; ++r) {
+      w[r] = (r < nr && fabs(refcn[sp * kNR + r] - top) < 1e-12) ? 1.0 : 0.0;
+      dw[r] = 0.0;
+    }
+  }
+  if (!BACKWARD) {
+#pragma unroll
+    for (int r = 0; r < kNR; ++r) w_out[i * kNR + r] = w[r];
+  } else {
+    double gc = 0.0;
+#pragma unroll
+    for (int r = 0; r < kNR; ++r) gc += g_w[i * kNR + r] * dw[r];
+    g_cn[i] = gc;
+  }
+}
+
 static int d4_check(const double* pos, int64_t n_nodes, const int32_t* species,
                     const int32_t* batch, const int64_t* node_ptr, int64_t n_graphs,
                     const double* cell, const int32_t* images, int64_t max_atoms) {
@@ -1269,6 +1335,35 @@ int xnn_d4_polarizabilities_backward(int64_t n_nodes, const int64_t* atomic_numb
   hipLaunchKernelGGL(d4_alpha_kernel<true>, dim3(grid_1d(n_nodes, 256)), dim3(256), 0,
                      as_hip(stream), n_nodes, atomic_numbers, cn, q, T, g_alpha, nullptr, g_cn,
                      g_q);
+  XNN_LAUNCH_CHECK();
+  return XNN_OK;
+}
+
+int xnn_d3_weights(int64_t n_nodes, const int32_t* species, const double* cn,
+                   int32_t n_species, const int32_t* nref, const double* refcn, double wf,
+                   double* weights, xnn_stream_t stream) {
+  XNN_REQUIRE(n_nodes >= 0 && n_species >= 1, "negative size or no species");
+  XNN_REQUIRE(nref && refcn, "NULL tables");
+  if (n_nodes == 0) return XNN_OK;
+  XNN_REQUIRE(species && cn && weights, "NULL input or output");
+  hipLaunchKernelGGL(d3_weights_kernel<false>, dim3(grid_1d(n_nodes, 256)), dim3(256), 0,
+                     as_hip(stream), n_nodes, species, cn, (int)n_species, nref, refcn, wf,
+                     nullptr, weights, nullptr);
+  XNN_LAUNCH_CHECK();
+  return XNN_OK;
+}
+
+int xnn_d3_weights_backward(int64_t n_nodes, const int32_t* species, const double* cn,
+                            int32_t n_species, const int32_t* nref, const double* refcn,
+                            double wf, const double* g_weights, double* g_cn,
+                            xnn_stream_t stream) {
+  XNN_REQUIRE(n_nodes >= 0 && n_species >= 1, "negative size or no species");
+  XNN_REQUIRE(nref && refcn, "NULL tables");
+  if (n_nodes == 0) return XNN_OK;
+  XNN_REQUIRE(species && cn && g_weights && g_cn, "NULL input or output");
+  hipLaunchKernelGGL(d3_weights_kernel<true>, dim3(grid_1d(n_nodes, 256)), dim3(256), 0,
+                     as_hip(stream), n_nodes, species, cn, (int)n_species, nref, refcn, wf,
+                     g_weights, nullptr, g_cn);
   XNN_LAUNCH_CHECK();
   return XNN_OK;
 }

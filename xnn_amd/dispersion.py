@@ -627,6 +627,42 @@ def _d3cn_backward(ctx, g_cn):
 d3_coordination_op.register_autograd(_d3cn_backward, setup_context=_d3cn_setup)
 
 
+@torch.library.custom_op(f"{_NS}::d3_weights", mutates_args=())
+def d3_weights_op(species: Tensor, cn: Tensor, nref: Tensor, refcn: Tensor) -> Tensor:
+    """D3 reference weights (N, 7): Gaussians exp(-4 (CN - CN_ref)^2) normalized per atom,
+    the largest-CN fallback where all vanish (d3.py:644-649), one HIP kernel; ``nref`` (S,)
+    int32 and ``refcn`` (S, 7) species-major. Differentiable once in ``cn``."""
+    n = cn.shape[0]
+    w = torch.empty((n, 7), dtype=torch.float64, device=cn.device)
+    _lib.call("xnn_d3_weights", n, _lib.ptr(species), _lib.ptr(cn), nref.shape[0],
+              _lib.ptr(nref), _lib.ptr(refcn), D3_WF, _lib.ptr(w), _lib.stream(cn.device))
+    return w
+
+
+@d3_weights_op.register_fake
+def _(species, cn, nref, refcn):
+    return cn.new_empty((cn.shape[0], 7))
+
+
+def _d3w_setup(ctx, inputs, output):
+    species, cn, nref, refcn = inputs
+    ctx.save_for_backward(species, cn, nref, refcn)
+
+
+def _d3w_backward(ctx, g_w):
+    if torch.is_grad_enabled():
+        raise RuntimeError("the D3 kernels are differentiable once")
+    species, cn, nref, refcn = ctx.saved_tensors
+    g_cn = torch.empty_like(cn)
+    _lib.call("xnn_d3_weights_backward", cn.shape[0], _lib.ptr(species), _lib.ptr(cn),
+              nref.shape[0], _lib.ptr(nref), _lib.ptr(refcn), D3_WF,
+              _lib.ptr(g_w.contiguous()), _lib.ptr(g_cn), _lib.stream(cn.device))
+    return None, g_cn, None, None
+
+
+d3_weights_op.register_autograd(_d3w_backward, setup_context=_d3w_setup)
+
+
 def _d3_params(p: List[float]) -> "_lib.D3PairParams":
     return _lib.D3PairParams(*p[:10], int(p[10]))
 
@@ -721,6 +757,9 @@ class DFTD3(nn.Module):
             v = tables[k]
             dt = torch.long if np.issubdtype(v.dtype, np.integer) else torch.float64
             self.register_buffer(k, torch.as_tensor(v, dtype=dt), persistent=False)
+        # species-major layouts of the reference CNs and counts for the weights kernel
+        self.register_buffer("k_refcn", self.refcn.t().contiguous(), persistent=False)
+        self.register_buffer("k_nref", self.nref.to(torch.int32), persistent=False)
         # species-pair major layout of the reference block for the kernel
         self.register_buffer("c6pair", torch.as_tensor(
             np.ascontiguousarray(np.asarray(tables["c6ref"]).transpose(2, 3, 0, 1)),
@@ -736,16 +775,12 @@ class DFTD3(nn.Module):
 
     def weights(self, s: Tensor, cn: Tensor) -> Tensor:
         """Gaussian reference weights exp(-4 (CN - CN_ref)^2), normalized, with the
-        largest-CN fallback (d3.py:644-649, dispersion.py:70-121)."""
-        refcn = self.refcn[:, s].t()
-        valid = torch.arange(refcn.shape[1], device=s.device)[None, :] < self.nref[s][:, None]
-        gw = torch.where(valid, torch.exp(-D3_WF * (cn[:, None] - refcn) ** 2), torch.zeros_like(refcn))
-        norm = gw.sum(1)
-        ok = norm > 0.0
-        w = gw / torch.where(ok, norm, torch.ones_like(norm))[:, None]
-        top = torch.where(valid, refcn, torch.full_like(refcn, -math.inf)).max(1).values
-        fb = (valid & ((refcn - top[:, None]).abs() < 1e-12)).to(cn.dtype)
-        return torch.where(ok[:, None], w, fb)
+        largest-CN fallback (d3.py:644-649, dispersion.py:70-121): one HIP kernel each
+        way (:func:`d3_weights_op`)."""
+        if not cn.is_cuda:
+            raise RuntimeError("xnn_amd D3 runs on the GPU (HIP kernels); there is no CPU path")
+        return d3_weights_op(s.to(torch.int32).contiguous(), cn.to(torch.float64).contiguous(),
+                             self.k_nref, self.k_refcn)
 
     def evaluate(self, z: Tensor, pos: Tensor, cell: Optional[Tensor], pbc: Optional[Tensor],
                  n_atoms: Tensor) -> Dict[str, Tensor]:
@@ -766,7 +801,7 @@ class DFTD3(nn.Module):
         max_atoms = max(counts) if counts else 1
         cn = d3_coordination_op(pos.contiguous(), cell64, species, batch32, node_ptr, images,
                                 self.rcov, self.cutoff_cn / BOHR, max_atoms)
-        w = self.weights(s, cn).contiguous()
+        w = self.weights(species, cn).contiguous()
         params = [self.s6, self.s8, self.a1, self.a2, self.rs6, self.rs8, self.alp, self.bet,
                   self.cutoff_pair / BOHR, self.switch_width_pair / BOHR,
                   float(D3_DAMPINGS[self.damping])]
