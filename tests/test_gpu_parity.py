@@ -125,6 +125,25 @@ def test_radius_graph_edge_cases():
         xa.build_neighbor_list(bad, 3.0)
 
 
+def test_unique_pairs_on_the_gpu_equal_the_cpu_pairs():
+    """unique_pairs from the HIP cell list: the CPU formulation's pairs, sorted by the first
+    atom (test_neighborlist_backends.py:156-174), for positions inside the cell or not."""
+    import xnn_amd as xa
+    from xnn_amd import synthetic
+    _note("unique_pairs gpu")
+    s = synthetic.water_box(n_molecules=100, box=14.4, grid=5, seed=3)
+    for offset in (0.0, -3.7):
+        pos = torch.tensor(s.pos, dtype=torch.float64) + offset * torch.diagonal(
+            torch.tensor(s.cell))
+        cell, pbc = torch.tensor(s.cell, dtype=torch.float64), torch.tensor(s.pbc)
+        i0, k0, s0 = xa.unique_pairs(pos, 3.5, cell, pbc)
+        i, k, sh = xa.unique_pairs(pos.to(DEV), 3.5, cell.to(DEV), pbc.to(DEV))
+        want = {(int(a), int(b), *map(int, v)) for a, b, v in zip(i0, k0, s0)}
+        got = {(int(a), int(b), *map(int, v)) for a, b, v in zip(i.cpu(), k.cpu(), sh.cpu())}
+        assert got == want and len(got) == i.shape[0]
+        assert bool((i[1:] >= i[:-1]).all())
+
+
 def test_batched_molecules_match_per_structure():
     import xnn_amd as xa
     from xnn_amd import synthetic

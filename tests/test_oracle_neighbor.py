@@ -116,3 +116,36 @@ def test_full_list_is_symmetric():
     fwd = canonical(ei, sh)
     rev = canonical(ei[::-1].copy(), -sh)
     assert np.array_equal(fwd, rev)
+
+
+def _unique_rows(rows):
+    """(src, dst, shift) with src < dst from independent (dst, src, shift) rows."""
+    keep = rows[:, 1] < rows[:, 0]
+    r = rows[keep][:, [1, 0, 2, 3, 4]]
+    return {tuple(int(v) for v in x) for x in r}
+
+
+@pytest.mark.parametrize("pbc", [(True, True, True), (True, True, False)])
+def test_unique_pairs_and_half_list(pbc):
+    """unique_pairs: each pair of the edge definition once as (i < k, shift) with the
+    displacement pos[k] - pos[i] + shift @ cell, sorted by i (test_grid_pairs.py:98-106);
+    half_list: every pair once, an atom's own images once; unique_pairs of the half list
+    equals unique_pairs of the full list."""
+    import xnn_amd as xa
+    pos, cell, pbc = _tiny(3, pbc=pbc)
+    rc = 4.0
+    want = _unique_rows(_independent(pos, rc, cell, pbc))
+    p, c = torch.tensor(pos), torch.tensor(cell)
+    pb = torch.tensor(pbc)
+    i, k, s = xa.unique_pairs(p, rc, c, pb)
+    got = {(int(a), int(b), *map(int, v)) for a, b, v in zip(i, k, s)}
+    assert got == want and len(got) == i.shape[0]
+    assert bool((i[1:] >= i[:-1]).all()) and bool((i < k).all())
+    d = p[k] - p[i] + s.double() @ c
+    assert float(torch.linalg.norm(d, dim=1).max()) < rc
+    (a, b), sh = xa.half_list(p, rc, c, pb)
+    rows = _independent(pos, rc, cell, pbc)
+    n_self = int((rows[:, 0] == rows[:, 1]).sum())
+    assert a.shape[0] == len(want) + n_self // 2
+    i2, k2, s2 = xa.unique_pairs(p, rc, c, pb, half=((a, b), sh))
+    assert torch.equal(i2, i) and torch.equal(k2, k) and torch.equal(s2, s)

@@ -7,7 +7,7 @@ reference's module and function interfaces.
 """
 from . import _lib
 from .data import (AtomicGraph, batched_neighbor_list, build_neighbor_list, collate,
-                   structure_to_graph)
+                   half_list, structure_to_graph, unique_pairs)
 from .fast import AutoPolicy, FastPathModule, MI355X_POLICY, select, set_use_fast
 from .featurizers import (BesselRBF, CosineCutoff, GaussianRBF, PolynomialCutoff,
                           SphericalHarmonicEdgeEmbedding, spherical_harmonics)
@@ -18,6 +18,7 @@ from .outputs import ForceStressOutput
 
 __all__ = [
     "AtomicGraph", "build_neighbor_list", "batched_neighbor_list", "structure_to_graph", "collate",
+    "half_list", "unique_pairs",
     "AutoPolicy", "FastPathModule", "MI355X_POLICY", "select", "set_use_fast",
     "BesselRBF", "GaussianRBF", "CosineCutoff", "PolynomialCutoff",
     "SphericalHarmonicEdgeEmbedding", "spherical_harmonics",

@@ -220,6 +220,46 @@ def build_neighbor_list(pos: Tensor, cutoff: float, cell: Optional[Tensor] = Non
     return _brute_force_cpu(pos, cutoff, cell, pbc, self_interaction)
 
 
+def half_list(pos: Tensor, cutoff: float, cell: Optional[Tensor] = None,
+              pbc: Optional[Tensor] = None) -> Optional[tuple]:
+    """Every pair within ``cutoff`` once, as ``((i, j), shift)`` with the displacement
+    ``pos[j] - pos[i] + shift @ cell``, an atom's own periodic images included once
+    (neighborlist.py:217-241, there vesin's half list). Here it is the full list's
+    edges ``src < dst`` plus, of an atom's two opposite images, the one whose shift is
+    lexicographically positive; never ``None``."""
+    edge_index, shifts = build_neighbor_list(pos, cutoff, cell, pbc)
+    a, b = edge_index[0], edge_index[1]
+    # of the two images (s, -s) of a self-pair: the first nonzero component positive
+    sign = torch.where(shifts[:, 0] != 0, shifts[:, 0],
+                       torch.where(shifts[:, 1] != 0, shifts[:, 1], shifts[:, 2]))
+    keep = ((a < b) | ((a == b) & (sign > 0))).nonzero()[:, 0]
+    return (a[keep], b[keep]), shifts[keep]
+
+
+def unique_pairs(pos: Tensor, cutoff: float, cell: Optional[Tensor] = None,
+                 pbc: Optional[Tensor] = None, half: Optional[tuple] = None
+                 ) -> tuple[Tensor, Tensor, Tensor]:
+    """Every pair within ``cutoff`` once, as ``(i, k, shift)`` with ``i < k``, sorted by
+    ``i`` (stable): the edges ``src < dst`` of :func:`build_neighbor_list`, with the
+    displacement ``pos[k] - pos[i] + shift @ cell``; an atom's own images are not pairs
+    (neighborlist.py:335-387). ``half``: a :func:`half_list` of these positions (each pair
+    once in either order), oriented smaller index first (the reversed displacement takes
+    the negated shift)."""
+    if half is None:
+        edge_index, shifts = build_neighbor_list(pos, cutoff, cell, pbc)
+        a, b = edge_index[0], edge_index[1]
+        keep = (a < b).nonzero()[:, 0]
+    else:
+        (i, j), shifts = half
+        swap = i > j
+        a, b = torch.where(swap, j, i), torch.where(swap, i, j)
+        shifts = torch.where(swap[:, None], -shifts, shifts)
+        keep = (a != b).nonzero()[:, 0]
+    a, b, shifts = a[keep], b[keep], shifts[keep]
+    order = torch.argsort(a.to(torch.int32), stable=True)
+    return a[order], b[order], shifts[order]
+
+
 def batched_neighbor_list(pos: Tensor, n_atoms: Tensor, cutoff: float,
                           self_interaction: bool = False) -> tuple[Tensor, Tensor]:
     """Radius graph of a batch of molecules (no cell) in one pass on the GPU:
