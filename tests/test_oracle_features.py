@@ -140,3 +140,27 @@ def test_scatter_and_structure_sums():
     vals = torch.randn(1000, generator=gen, dtype=F64) * 1e3
     assert float(R.structure_sum(vals, torch.zeros(1000, dtype=torch.long), 1)[0]) == \
         pytest.approx(math.fsum(vals.tolist()), rel=1e-15, abs=1e-9)
+
+
+def test_make_radial_basis_builds_the_path_bases():
+    """make_radial_basis (radial.py:348-401): the Gaussian basis with float64 centers on
+    [0, cutoff] and the spacing as width, the Bessel basis with trainable frequencies; the
+    bases outside this path raise, unknown names are rejected, ignored options warn."""
+    import warnings
+    from xnn_amd.featurizers import BesselRBF, GaussianRBF, make_radial_basis
+    g = make_radial_basis("gaussian", 8, 5.0)
+    assert isinstance(g, GaussianRBF) and g.centers.dtype == torch.float64
+    assert torch.equal(g.centers, torch.linspace(0.0, 5.0, 8, dtype=torch.float64))
+    assert abs(g.gamma - 0.5 * (7 / 5.0) ** 2) < 1e-15
+    r = torch.tensor([0.3, 2.0], dtype=torch.float32)
+    assert g(r).dtype == torch.float32
+    b = make_radial_basis("bessel", 8, 5.0, trainable=True)
+    assert isinstance(b, BesselRBF) and isinstance(b.freqs, torch.nn.Parameter)
+    with pytest.raises(NotImplementedError):
+        make_radial_basis("expnorm", 8, 5.0)
+    with pytest.raises(ValueError):
+        make_radial_basis("sinc", 8, 5.0)
+    with warnings.catch_warnings(record=True) as w:
+        warnings.simplefilter("always")
+        make_radial_basis("gaussian", 8, 5.0, trainable=True)
+    assert any("trainable" in str(x.message) for x in w)

@@ -1,6 +1,7 @@
 """Edge featurizers with the reference's parameters and a HIP evaluation.
 
-* :class:`BesselRBF`, :class:`GaussianRBF` -- common/featurizers/radial.py:15-75, 187-268
+* :class:`BesselRBF`, :class:`GaussianRBF` -- common/featurizers/radial.py:15-75, 187-268,
+  and :func:`make_radial_basis` (radial.py:348-401) for those two
 * :class:`CosineCutoff`, :class:`PolynomialCutoff` -- common/featurizers/cutoff.py:10-125
 * :func:`spherical_harmonics` -- e3nn ``SphericalHarmonics(normalize=True,
   normalization="component")`` for ``l <= 3`` (gnn/featurizers/spherical.py:91-93): real
@@ -36,7 +37,7 @@ class GaussianRBF(nn.Module):
         self.gamma = float(gamma) if gamma is not None else 0.5 / self.width ** 2
 
     def forward(self, r: Tensor) -> Tensor:
-        diff = r[..., None] - self.centers
+        diff = r[..., None] - self.centers.to(r.dtype)
         return torch.exp(-self.gamma * diff ** 2)
 
 
@@ -57,6 +58,37 @@ class BesselRBF(nn.Module):
     def forward(self, r: Tensor) -> Tensor:
         r = r.clamp(min=1e-8)[..., None]
         return self.norm * torch.sin(self.freqs * r / self.cutoff) / r
+
+
+RADIAL_BASES = ("gaussian", "bessel", "expnorm", "smooth_bessel")
+
+
+def make_radial_basis(name: str, n_rbf: int, cutoff: float, trainable: bool = False, *,
+                      gamma: float | None = None, prefactor: float | None = None) -> nn.Module:
+    """A radial basis by name (radial.py:348-401): ``"gaussian"`` (:class:`GaussianRBF`,
+    ``n_rbf`` centers on ``[0, cutoff]`` kept in float64, the center spacing as width
+    unless ``gamma`` is given) or ``"bessel"`` (:class:`BesselRBF`, frequencies trainable
+    with ``trainable``). The reference's ``"expnorm"`` and ``"smooth_bessel"`` bases are
+    not part of this path and raise ``NotImplementedError``; options the chosen basis does
+    not have are ignored with a warning, as there."""
+    if name not in RADIAL_BASES:
+        raise ValueError(f"radial_basis must be one of {RADIAL_BASES}, got {name!r}")
+    if name in ("expnorm", "smooth_bessel"):
+        raise NotImplementedError(f"the {name!r} radial basis is not part of this path "
+                                  "(bessel and gaussian are)")
+    ignored = [k for k, bad in (("trainable", trainable and name == "gaussian"),
+                                ("gamma", gamma is not None and name != "gaussian"),
+                                ("prefactor", prefactor is not None and name != "bessel")) if bad]
+    if ignored:
+        import warnings
+        warnings.warn(f"radial basis {name!r} ignores {ignored}", UserWarning, stacklevel=2)
+    if name == "gaussian":
+        if gamma is None and n_rbf > 1:      # the center spacing as width, in double precision
+            gamma = 0.5 * ((n_rbf - 1) / cutoff) ** 2
+        basis = GaussianRBF(n_rbf, cutoff, gamma=gamma)
+        basis.centers = torch.linspace(0.0, cutoff, n_rbf, dtype=torch.float64)
+        return basis
+    return BesselRBF(n_rbf, cutoff, trainable=trainable, prefactor=prefactor)
 
 
 class CosineCutoff(nn.Module):
