@@ -82,3 +82,19 @@ def test_tables_fixture_has_the_elements(tables):
     assert int(tables["nref"][6]) == 7 and int(tables["nref"][1]) == 2
     assert 1.9 < float(tables["r4r2"][1]) < 2.1 and 3.0 < float(tables["r4r2"][6]) < 3.2
     assert float(np.abs(tables["refalpha"][:, :, 2]).sum()) == 0.0     # outside the subset
+
+
+def test_public_switch_and_reference_weights_equal_the_oracle(tables):
+    """xnn_amd.dispersion.switching_function and gaussian_reference_weights (the reference's
+    public formulas, dispersion.py:42-121) against the oracle's switch and D4 weights."""
+    import xnn_amd.dispersion as XD
+    r = torch.linspace(0.0, 12.0, 97, dtype=torch.float64)
+    for width in (0.0, 2.5, 20.0):
+        assert torch.equal(XD.switching_function(r, 10.0, width), D.switching(r, 10.0, width))
+    z = torch.tensor([1, 6, 7, 8, 18, 6, 1])
+    cn = torch.tensor([0.9, 3.1, 2.2, 1.8, 0.0, 45.0, 1.1], dtype=torch.float64)
+    refcn = torch.as_tensor(tables["refcn"])[:, z].t()
+    ngw = torch.as_tensor(tables["ngw"])[:, z].t()
+    valid = torch.arange(refcn.shape[1])[None, :] < torch.as_tensor(tables["nref"])[z][:, None]
+    got = XD.gaussian_reference_weights(cn, refcn, valid, D.WF, ngw, 1.4916681462400413e-154)
+    np.testing.assert_allclose(got, D.gaussian_weights(z, cn, tables), rtol=1e-15, atol=1e-300)

@@ -45,7 +45,47 @@ TABLE_KEYS = ("rcov", "en", "zeff", "hardness", "r4r2", "eeq_chi", "eeq_eta", "e
 _NS = "xnn_amd"
 
 
-# --------------------------------------------------------------------------- tables
+# --------------------------------------------------------------------------- formulas
+def switching_function(r: Tensor, cutoff: float, width: float) -> Tensor:
+    """Quintic switching window (dispersion.py:42-67): 1 below ``cutoff - width``, 0 above
+    ``cutoff``, ``x^3 (10 - 15 x + 6 x^2)`` with ``x = (cutoff - r) / width`` inside;
+    ``width <= 0`` is the sharp cutoff. The pair kernels evaluate it per term (with its
+    slope); this is the tensor form of the same window."""
+    if width <= 0.0:
+        return torch.ones_like(r)
+    w = min(width, cutoff)
+    x = torch.clamp((cutoff - r) / w, 0.0, 1.0)
+    return x ** 3 * (10.0 + x * (6.0 * x - 15.0))
+
+
+def gaussian_reference_weights(cn: Tensor, refcn: Tensor, valid: Tensor, wf: float,
+                               ngw: Optional[Tensor] = None, eps_norm: float = 0.0,
+                               n_gauss: Optional[int] = None) -> Tensor:
+    """Normalized Gaussian weights of the reference systems in the coordination number
+    (dispersion.py:70-121): ``sum_{j <= ngw} exp(-wf j (CN - CN_ref)^2)`` per reference
+    (one Gaussian with ``ngw`` None, D3), normalized over the ``valid`` slots, weight one
+    on the largest-CN reference(s) where the norm is at most ``eps_norm``. The D4
+    polarizability and D3 weight kernels evaluate the same weights per atom; this is the
+    tensor form on per-atom ``(N, R)`` reference tables."""
+    dcn2 = (cn[:, None] - refcn) ** 2
+    if ngw is None:
+        gw = torch.exp(-wf * dcn2)
+    else:
+        n_max = int(ngw.max()) if n_gauss is None else int(n_gauss)
+        j = torch.arange(1, n_max + 1, device=cn.device)
+        gauss = torch.exp(-wf * j.to(cn.dtype)[None, None, :] * dcn2[:, :, None])
+        use = j[None, None, :] <= ngw[:, :, None]
+        gw = torch.where(use, gauss, torch.zeros_like(gauss)).sum(-1)
+    gw = torch.where(valid, gw, torch.zeros_like(gw))
+    norm = gw.sum(dim=1)
+    ok = norm > eps_norm
+    weights = gw / torch.where(ok, norm, torch.ones_like(norm))[:, None]
+    max_cn = torch.where(valid, refcn, torch.full_like(refcn, -math.inf)).max(dim=1).values
+    fallback = (valid & ((refcn - max_cn[:, None]).abs() < 1e-12)).to(cn.dtype)
+    return torch.where(ok[:, None], weights, fallback)
+
+
+# --------------------------------------------------------------------------- tables# --------------------------------------------------------------------------- tables
 def load_d4_tables(path: str) -> Dict[str, np.ndarray]:
     """Per-element D4 tables (index = atomic number) in the derived layout: ``rcov``
     (4/3-scaled covalent radii, bohr), ``en``, ``zeff``, ``hardness``, ``r4r2``
