@@ -530,6 +530,57 @@ int xnn_node_readout_backward(int dtype, const void* g, int64_t g_stride, int64_
                               int64_t n_features, const void* weights, void* d_rows,
                               xnn_stream_t stream);
 
+/* ------------------------------------------------------------------------ */
+/* Axilrod-Teller-Muto three-body dispersion (D4 and D3) over an edge list. Edges
+ * edge_index (2,E) int64 [src; dst] within the three-body cutoff, both directions of
+ * every pair and image; vectors edge_vec (E,3) float64 in bohr. Pair C6 of atoms x, y is
+ * <feat_a[x], feat_b[y]> over k <= 28 components (feat_a, feat_b (N,k) float64; D4:
+ * alpha(i w) sqrt(3 cp_w / pi)); the damping radius of a triangle is the product of the
+ * three table[species, species] factors (table (S,S) float64, S <= 32; species (N)
+ * int32). Energy per triangle s9 C9 (3 cos cos cos + 1) / (r r r)^3 / (1 + 6 (R0 /
+ * r r r)^alp3) times the three switches, a third to each corner (dispersion.py:124-222).
+ * Replaces the triplet plan and kernels of dispersion_fast/atm.py:297-535
+ * (plan_triplets 318-352, _energies 380-399, _gradients 413-443) and the reference's
+ * three_body_energy / three_body_energy_chunked (dispersion.py:124-222, 529-647). */
+typedef struct {
+  double s9;             /* three-body scale                                     */
+  double alp3;           /* damping exponent: alp / 3 (D4), (alp + 2) / 3 (D3)   */
+  double cutoff;         /* three-body cutoff, bohr (r_jk <= cutoff)             */
+  double width;          /* switching width, bohr (<= 0: sharp cutoff)           */
+} xnn_atm_params;
+
+/* Bytes of the plan buffer for E edges and N atoms. */
+int xnn_atm_plan_size(int64_t n_edges, int64_t n_atoms, size_t* bytes);
+
+/* Sort the edges by (center, neighbor) into the plan and lay out the work. Synchronous
+ * (one small device-to-host copy): info[0] = tiles of 64 upper edges of the busiest
+ * center, info[1] = 1 when some center has repeated-atom triangles (periodic self-images).
+ * An atom index outside [0, N) is an error. (atm.py:318-352) */
+int xnn_atm_plan(const int64_t* edge_index, int64_t n_edges, int64_t n_atoms, void* plan,
+                 size_t plan_bytes, int64_t* info, xnn_stream_t stream);
+
+/* Bytes of the workspace of xnn_atm_energy (backward = 0) or of its backward (1). */
+int xnn_atm_work_size(int64_t n_edges, int64_t n_atoms, int32_t k, int32_t backward,
+                      size_t* bytes);
+
+/* Per-atom ATM energies (N) in hartree, summed with atomics (the order of the sums is
+ * not fixed). max_tiles, has_repeats: info[0], info[1] of the plan. (atm.py:84-162) */
+int xnn_atm_energy(const void* plan, int64_t n_edges, int64_t n_atoms, int64_t max_tiles,
+                   int64_t has_repeats, const double* edge_vec, const double* feat_a,
+                   const double* feat_b, int32_t k, const int32_t* species, const double* table,
+                   int32_t n_species, const xnn_atm_params* prm, double* energy, void* work,
+                   size_t work_bytes, xnn_stream_t stream);
+
+/* Gradients of sum_i grad_energy[i] E_i: grad_vec (E,3) in the input edge order, grad_fa
+ * and grad_fb (N,k). (atm.py:165-294, 402-443) */
+int xnn_atm_energy_backward(const void* plan, int64_t n_edges, int64_t n_atoms,
+                            int64_t max_tiles, int64_t has_repeats, const double* edge_vec,
+                            const double* feat_a, const double* feat_b, int32_t k,
+                            const int32_t* species, const double* table, int32_t n_species,
+                            const xnn_atm_params* prm, const double* grad_energy,
+                            double* grad_vec, double* grad_fa, double* grad_fb, void* work,
+                            size_t work_bytes, xnn_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -12,8 +12,9 @@ Reference (molssi-ai/xnn, src/xnn/common/models/):
   d4.py:984-1042     reference_weights, gaussian_weights, charge_scaling, alpha(i w)
   d4.py:1044-1071    pair_c6, two_body_energy, pair_damping
   dispersion.py:42-121  switching_function, gaussian_reference_weights
-  dispersion.py:124-222 three-body ATM energy (restated here only to pin the total
-                        energy of the golden water values; the HIP path has no ATM)
+  dispersion.py:124-222 three-body ATM energy: atm_molecule (the direct triple loop that
+                        pins the golden water total) and atm_edges (per-atom energies over
+                        an edge list with lattice images, every corner visited)
 Golden values: tests/common/test_d4.py:110-126 (dftd4 4.2.0, PBE0-D4, water).
 """
 from __future__ import annotations
@@ -280,6 +281,68 @@ def atm_molecule(z, pos_au, alpha_neutral, tables, prm, cutoff_au):
                        / prod5 + 1.0 / prod3)
                 e = e + c9 * ang * damp
     return e
+
+
+def atm_edges(edge_index, edge_vec, feat_a, feat_b, species, r0_table, s9: float, alp3: float,
+              cutoff: float, width: float, n_atoms: int) -> Tensor:
+    """Per-atom ATM energies (hartree) from directed edges ``[src, dst]`` within the
+    three-body cutoff and their vectors (bohr), the formula of dispersion.py:183-222 with
+    the bookkeeping of dispersion.py:124-181: every pair of edges sharing a center is a
+    triangle visit, and a third of the triangle energy goes to that center. Pair C6 are
+    ``<feat_a[x], feat_b[y]>`` (dispersion_fast/atm.py:512-535 interface); the damping
+    radius is the product of the three ``r0_table[species, species]`` pair factors.
+    Differentiable (autograd) in ``edge_vec``, ``feat_a`` and ``feat_b``."""
+    src, dst = edge_index[0], edge_index[1]
+    order = torch.argsort(dst, stable=True)
+    energy = edge_vec.new_zeros(n_atoms)
+    counts = torch.bincount(dst, minlength=n_atoms).tolist()
+    start = 0
+    parts = []
+    for c in range(n_atoms):
+        m = counts[c]
+        ids = order[start:start + m]
+        start += m
+        if m < 2:
+            continue
+        ia, ib = torch.triu_indices(m, m, offset=1)
+        a, b = ids[ia], ids[ib]
+        parts.append((a, b, torch.full_like(a, c)))
+    if not parts:
+        return energy
+    a = torch.cat([p[0] for p in parts])
+    b = torch.cat([p[1] for p in parts])
+    c = torch.cat([p[2] for p in parts])
+    j, k = src[a], src[b]
+    va, vb = edge_vec[a], edge_vec[b]
+    x, y = (va * va).sum(-1), (vb * vb).sum(-1)
+    d = va - vb
+    w = (d * d).sum(-1)
+    keep = (w <= cutoff * cutoff) & (w > 2.220446049250313e-16)
+    w = torch.where(keep, w, torch.ones_like(w))
+    c6a = (feat_a[c] * feat_b[j]).sum(-1)
+    c6b = (feat_a[c] * feat_b[k]).sum(-1)
+    c6jk = (feat_a[j] * feat_b[k]).sum(-1)
+    c9 = s9 * torch.sqrt((c6a * c6b * c6jk).abs())
+    sc, sj, sk = species[c], species[j], species[k]
+    r0 = r0_table[sc, sj] * r0_table[sc, sk] * r0_table[sj, sk]
+    prod2 = x * y * w
+    prod1 = torch.sqrt(prod2)
+    prod3 = prod2 * prod1
+    prod5 = prod3 * prod2
+    damp = 1.0 / (1.0 + 6.0 * (r0 / prod1) ** alp3)
+    ang = 0.375 * (x + w - y) * (x - w + y) * (-x + w + y) / prod5 + 1.0 / prod3
+    sw = switching(torch.sqrt(x), cutoff, width) * switching(torch.sqrt(y), cutoff, width) \
+        * switching(torch.sqrt(w), cutoff, width)
+    e = torch.where(keep, c9 * ang * damp * sw / 3.0, torch.zeros_like(x))
+    return energy.index_add(0, c, e)
+
+
+def bj_radius_factors(z, tables, a1: float, a2: float):
+    """Species table of the BJ pair radii ``a1 sqrt(3 Q_A Q_B) + a2`` over the unique
+    elements of ``z`` (d4.py:970-978), and each atom's species index."""
+    uniq, species = torch.unique(torch.as_tensor(z), return_inverse=True)
+    q = _t(tables, "r4r2")[uniq]
+    return a1 * torch.sqrt(3.0 * q[:, None] * q[None, :]) + a2, species
 
 
 def d4_molecule(pos_aa: np.ndarray, numbers, tables, prm=PBE0_D4, total_charge: float = 0.0,

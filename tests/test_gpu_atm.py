@@ -1,0 +1,164 @@
+"""The ATM three-body kernels (xnn_atm_plan / xnn_atm_energy / xnn_atm_energy_backward)
+against the oracle's edge-list restatement of the reference (oracle/d4.py atm_edges,
+dispersion.py:124-222), energies and first derivatives, float64.
+
+Systems as in the reference's tests (tests/common/test_dispersion_fast.py:21-70): rigid
+water boxes on a 3.104 A grid with a 6 A three-body cutoff and a 1 A switch; the 3^3 cell
+(9.3 A) is narrower than twice the cutoff, so it has self-image triangles, the 4^3 cell
+(12.4 A) has none, and the cluster has no cell. Tolerance: 1e-11 relative to the largest
+value (the reference's fast-path tolerance for float64, test_dispersion_fast.py:102-115).
+"""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+import oracle.d4 as D
+
+pytestmark = pytest.mark.gpu
+
+WATER = np.array([[0.0, 0.0, 0.119262], [0.0, 0.763239, -0.477047],
+                  [0.0, -0.763239, -0.477047]])
+SPACING = 3.104
+TOL = 1e-11
+
+
+def _water_box(n_side, periodic, seed=3):
+    rng = np.random.default_rng(seed)
+    pos = []
+    for i in range(n_side):
+        for j in range(n_side):
+            for k in range(n_side):
+                q, _ = np.linalg.qr(rng.normal(size=(3, 3)))
+                q *= np.sign(np.linalg.det(q))
+                pos.extend((WATER - WATER[0]) @ q.T + np.array([i, j, k]) * SPACING
+                           + rng.normal(scale=0.1, size=3))
+    cell = np.eye(3) * SPACING * n_side if periodic else None
+    return np.array(pos), cell, [8, 1, 1] * n_side ** 3
+
+
+def _case(system, k=23, cutoff_aa=6.0, width_aa=1.0, seed=0):
+    n_side, periodic = {"small_cell": (3, True), "cell": (4, True), "cluster": (3, False)}[system]
+    pos, cell, z = _water_box(n_side, periodic)
+    dst, src, sh = D.pair_images(pos, cell, cutoff_aa)
+    perm = torch.randperm(len(dst), generator=torch.Generator().manual_seed(seed))
+    ei = torch.stack([torch.as_tensor(src), torch.as_tensor(dst)])[:, perm]
+    sh = torch.as_tensor(sh, dtype=torch.float64)[perm]
+    n = len(z)
+    g = torch.Generator().manual_seed(seed + 1)
+    fa = torch.rand(n, k, dtype=torch.float64, generator=g) + 0.2
+    # C6 factors as in D4 and D3: <fa[x], fb[y]> symmetric in x, y (fb = fa M, M symmetric);
+    # which edge of a pair comes first is then immaterial
+    r = torch.rand(k, k, dtype=torch.float64, generator=g)
+    mix = torch.eye(k, dtype=torch.float64) + 0.1 * (r @ r.t()) / k
+    tables = dict(np.load(D_TABLES, allow_pickle=False))
+    table, species = D.bj_radius_factors(torch.tensor(z), tables, 0.40085597, 5.02928789)
+    return dict(ei=ei, shift=sh, pos=torch.as_tensor(pos),
+                cell=None if cell is None else torch.as_tensor(cell), fa=fa, mix=mix,
+                species=species, table=table, n=n,
+                cutoff=cutoff_aa / D.BOHR, width=width_aa / D.BOHR)
+
+
+D_TABLES = __import__("os").path.join(__import__("os").path.dirname(__file__), "golden",
+                                      "d4_tables_hcnoar.npz")
+
+
+def _rel(a, b):
+    scale = float(b.abs().max())
+    return float((a.detach().cpu() - b.detach()).abs().max()) / max(scale, 1e-300)
+
+
+def _geometry(c, dev):
+    """Edge vectors (bohr) as a differentiable function of positions and cell: per-edge
+    gradients are not unique (an edge and its reverse carry the same geometry, and the
+    kernels assign each distinct triangle to one corner's edges), the forces and the
+    cell gradient are."""
+    pos = c["pos"].detach().to(dev).clone().requires_grad_(True)
+    cell = None if c["cell"] is None else c["cell"].detach().to(dev).clone().requires_grad_(True)
+    ei = c["ei"].to(dev)
+    vec = pos[ei[1]] - pos[ei[0]]
+    if cell is not None:
+        vec = vec + c["shift"].to(dev) @ cell
+    return pos, cell, vec / D.BOHR
+
+
+def _grads(e, go, pos, cell, fa):
+    (e * go).sum().backward()
+    return (e.detach(), pos.grad, fa.grad) + (() if cell is None else (cell.grad,))
+
+
+def _oracle(c, same=False, s9=1.0, alp3=16.0 / 3.0, go=None):
+    pos, cell, vec = _geometry(c, "cpu")
+    fa = c["fa"].clone().requires_grad_(True)
+    fb = fa if same else fa @ c["mix"]
+    e = D.atm_edges(c["ei"], vec, fa, fb, c["species"], c["table"], s9, alp3, c["cutoff"],
+                    c["width"], c["n"])
+    return _grads(e, go, pos, cell, fa)
+
+
+def _hip(c, same=False, s9=1.0, alp3=16.0 / 3.0, go=None):
+    from xnn_amd import dispersion as XD
+    dev = torch.device("cuda:0")
+    pos, cell, vec = _geometry(c, dev)
+    fa = c["fa"].to(dev).requires_grad_(True)
+    fb = fa if same else fa @ c["mix"].to(dev)
+    consts = XD.ATMConstants(c["species"].to(dev), c["table"].to(dev), s9, alp3, c["cutoff"],
+                             c["width"])
+    e = XD.atm_energy(c["ei"].to(dev), vec, fa, fb, consts, c["n"])
+    out = _grads(e, go.to(dev), pos, cell, fa)
+    torch.cuda.synchronize()
+    return out
+
+
+@pytest.mark.parametrize("system", ["small_cell", "cell", "cluster"])
+@pytest.mark.parametrize("k,width_aa", [(23, 1.0), (28, 0.0), (7, 1.0)])
+def test_atm_matches_the_oracle(system, k, width_aa):
+    print(f"[atm] {system} k={k} width={width_aa}", flush=True)
+    c = _case(system, k=k, width_aa=width_aa)
+    go = torch.rand(c["n"], dtype=torch.float64, generator=torch.Generator().manual_seed(9)) + 0.5
+    ref = _oracle(c, go=go)
+    out = _hip(c, go=go)
+    assert float(ref[0].abs().max()) > 0
+    for name, a, b in zip(("energy", "grad_pos", "grad_feat", "grad_cell"), out, ref):
+        assert _rel(a, b) < TOL, (name, _rel(a, b))
+
+
+def test_atm_shared_factors_and_plan_modes():
+    """feat_a is feat_b (the D4 use) sums both factor gradients; the small cell has
+    repeated-atom triangles and the 12.4 A cell none (test_dispersion_fast.py:118-131)."""
+    from xnn_amd import dispersion as XD
+    c = _case("small_cell", k=23)
+    go = torch.ones(c["n"], dtype=torch.float64)
+    ref = _oracle(c, same=True, go=go)
+    out = _hip(c, same=True, go=go)
+    for name, a, b in zip(("energy", "grad_pos", "grad_f", "grad_cell"), out, ref):
+        assert _rel(a, b) < TOL, name
+    _, info = XD.atm_plan(c["ei"].cuda(), c["n"])
+    assert info[0] >= 1 and info[1] == 1
+    big = _case("cell", k=23)
+    _, info = XD.atm_plan(big["ei"].cuda(), big["n"])
+    assert info[1] == 0
+
+
+def test_atm_edge_cases():
+    """No edges, a lone pair (no triangle), s9 = 0, and an index out of range."""
+    from xnn_amd import dispersion as XD
+    dev = torch.device("cuda:0")
+    consts = XD.ATMConstants(torch.zeros(3, dtype=torch.int32, device=dev),
+                             torch.ones(1, 1, dtype=torch.float64, device=dev), 1.0, 16 / 3, 10.0,
+                             0.0)
+    f = torch.ones(3, 23, dtype=torch.float64, device=dev)
+    e = XD.atm_energy(torch.zeros(2, 0, dtype=torch.long, device=dev),
+                      torch.zeros(0, 3, dtype=torch.float64, device=dev), f, f, consts, 3)
+    assert e.shape == (3,) and float(e.abs().sum()) == 0.0
+    ei = torch.tensor([[0, 1], [1, 0]], device=dev)
+    v = torch.tensor([[1.0, 0, 0], [-1.0, 0, 0]], dtype=torch.float64, device=dev)
+    assert float(XD.atm_energy(ei, v, f, f, consts, 3).abs().sum()) == 0.0
+    c = _case("cluster", k=23)
+    go = torch.ones(c["n"], dtype=torch.float64)
+    out = _hip(c, s9=0.0, go=go)
+    assert float(out[0].abs().max()) == 0.0 and float(out[1].abs().max()) == 0.0
+    bad = torch.tensor([[0, 5], [1, 0]], device=dev)
+    with pytest.raises(RuntimeError, match="outside"):
+        XD.atm_energy(bad, v, f, f, consts, 3)

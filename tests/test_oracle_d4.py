@@ -98,3 +98,62 @@ def test_public_switch_and_reference_weights_equal_the_oracle(tables):
     valid = torch.arange(refcn.shape[1])[None, :] < torch.as_tensor(tables["nref"])[z][:, None]
     got = XD.gaussian_reference_weights(cn, refcn, valid, D.WF, ngw, 1.4916681462400413e-154)
     np.testing.assert_allclose(got, D.gaussian_weights(z, cn, tables), rtol=1e-15, atol=1e-300)
+
+
+def _atm_inputs(pos_aa, cell_aa, z, tables, cutoff_au, feats=None):
+    dst, src, sh = D.pair_images(pos_aa, cell_aa, cutoff_au * D.BOHR)
+    pos = torch.as_tensor(pos_aa)
+    cell = None if cell_aa is None else torch.as_tensor(cell_aa)
+    vec = D.edge_vectors_au(pos, cell, dst, src, sh)
+    keep = torch.linalg.norm(vec, dim=-1) <= cutoff_au
+    ei = torch.stack([torch.as_tensor(src), torch.as_tensor(dst)])[:, keep]
+    table, species = D.bj_radius_factors(z, tables, D.PBE0_D4["a1"], D.PBE0_D4["a2"])
+    if feats is None:
+        feats = torch.rand(len(z), 23, dtype=torch.float64, generator=torch.Generator().manual_seed(1))
+    return ei, vec[keep], feats, species, table
+
+
+def test_atm_edges_total_equals_the_direct_triple_loop(tables):
+    """The edge-list ATM (every corner visited, a third each) sums to the pinned direct
+    triple loop on a molecule, with a cutoff that drops some triangles."""
+    rng = np.random.default_rng(4)
+    pos = rng.uniform(0.0, 5.0, size=(9, 3))
+    z = torch.tensor([6, 6, 8, 1, 1, 7, 1, 8, 1])
+    alpha = torch.rand(9, 23, dtype=torch.float64, generator=torch.Generator().manual_seed(2)) + 0.5
+    feats = alpha * torch.sqrt((3.0 / math.pi) * torch.as_tensor(D.cp_weights()))
+    for cut in (40.0, 7.0):
+        ei, vec, f, sp, tab = _atm_inputs(pos, None, z, tables, cut, feats)
+        e = D.atm_edges(ei, vec, f, f, sp, tab, 1.0, 16.0 / 3.0, cut, 0.0, 9)
+        ref = D.atm_molecule(z, torch.as_tensor(pos) / D.BOHR, alpha, tables, D.PBE0_D4, cut)
+        assert abs(float(e.sum()) - float(ref)) <= 1e-13 * abs(float(ref)) and float(ref) > 0
+
+
+def test_atm_edges_per_atom_is_invariant_under_replication(tables):
+    """Per-atom ATM energies of a periodic cell narrower than twice the cutoff (so with
+    self-image triangles) equal those of each copy in a 2x1x1 and a 1x2x2 supercell, and a
+    cell padded with vacuum reproduces the molecule."""
+    rng = np.random.default_rng(7)
+    cell = np.array([[5.5, 0.0, 0.0], [0.8, 5.2, 0.0], [0.3, -0.4, 5.9]])
+    frac = rng.uniform(0.0, 1.0, size=(4, 3))
+    pos = frac @ cell
+    z = torch.tensor([6, 1, 8, 1])
+    cut = 6.0 / D.BOHR
+    feats = torch.rand(4, 23, dtype=torch.float64, generator=torch.Generator().manual_seed(3)) + 0.1
+    ei, vec, f, sp, tab = _atm_inputs(pos, cell, z, tables, cut, feats)
+    assert bool((ei[0] == ei[1]).any())               # an atom sees its own image
+    e1 = D.atm_edges(ei, vec, f, f, sp, tab, 1.0, 16.0 / 3.0, cut, 1.5, 4)
+    for reps in ((2, 1, 1), (1, 2, 2)):
+        shifts = np.array([[i, j, k] for i in range(reps[0]) for j in range(reps[1])
+                           for k in range(reps[2])])
+        pos_s = np.concatenate([pos + s @ cell for s in shifts])
+        cell_s = cell * np.array(reps)[:, None]
+        n = len(shifts)
+        ei, vec, f, sp, tab = _atm_inputs(pos_s, cell_s, z.repeat(n), tables, cut, feats.repeat(n, 1))
+        es = D.atm_edges(ei, vec, f, f, sp, tab, 1.0, 16.0 / 3.0, cut, 1.5, 4 * n)
+        np.testing.assert_allclose(es.reshape(n, 4), e1.expand(n, 4), rtol=1e-12)
+    mol = pos - pos.mean(0)
+    ei, vec, f, sp, tab = _atm_inputs(mol, None, z, tables, cut, feats)
+    e_mol = D.atm_edges(ei, vec, f, f, sp, tab, 1.0, 16.0 / 3.0, cut, 1.5, 4)
+    ei, vec, f, sp, tab = _atm_inputs(mol, np.eye(3) * 30.0, z, tables, cut, feats)
+    e_pad = D.atm_edges(ei, vec, f, f, sp, tab, 1.0, 16.0 / 3.0, cut, 1.5, 4)
+    np.testing.assert_allclose(e_pad, e_mol, rtol=1e-13)

@@ -70,6 +70,11 @@ class D3PairParams(ctypes.Structure):
                 ("alp", dbl), ("bet", dbl), ("cutoff", dbl), ("width", dbl), ("damping", i32)]
 
 
+class AtmParams(ctypes.Structure):
+    """``xnn_atm_params``."""
+    _fields_ = [("s9", dbl), ("alp3", dbl), ("cutoff", dbl), ("width", dbl)]
+
+
 # name -> argtypes (restype int unless listed in _RESTYPES)
 _SIGNATURES = {
     "xnn_last_error": [],
@@ -107,6 +112,13 @@ _SIGNATURES = {
     "xnn_d3_weights": [i64, vp, vp, i32, vp, vp, dbl, vp, vp],
     "xnn_d3_weights_backward": [i64, vp, vp, i32, vp, vp, dbl, vp, vp, vp],
     "xnn_node_readout": [i32, vp, i64, i64, vp, vp, vp, i64, vp, vp],
+    "xnn_atm_plan_size": [i64, i64, ctypes.POINTER(sz)],
+    "xnn_atm_plan": [vp, i64, i64, vp, sz, ctypes.POINTER(i64), vp],
+    "xnn_atm_work_size": [i64, i64, i32, i32, ctypes.POINTER(sz)],
+    "xnn_atm_energy": [vp, i64, i64, i64, i64, vp, vp, vp, i32, vp, vp, i32,
+                       ctypes.POINTER(AtmParams), vp, vp, sz, vp],
+    "xnn_atm_energy_backward": [vp, i64, i64, i64, i64, vp, vp, vp, i32, vp, vp, i32,
+                                ctypes.POINTER(AtmParams), vp, vp, vp, vp, vp, sz, vp],
     "xnn_node_readout_backward": [i32, vp, i64, i64, i64, vp, vp, vp],
     "xnn_d4_polarizabilities": [i64, vp, vp, vp, ctypes.POINTER(D4AlphaTables), vp, vp],
     "xnn_d4_polarizabilities_backward": [i64, vp, vp, vp, ctypes.POINTER(D4AlphaTables), vp, vp,

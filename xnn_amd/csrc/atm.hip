@@ -1,0 +1,823 @@
+// The Axilrod-Teller-Muto three-body dispersion term of D4 and D3 over an edge list
+// (gfx950, wave64, float64).
+//
+// xnn_atm_plan_size, xnn_atm_plan  the triplet plan of an edge list
+//                                  (dispersion_fast/atm.py:318-352): the edges sorted by
+//                                  (center, neighbor), per-center edge ranges and the
+//                                  centers that have repeated-atom triangles
+// xnn_atm_work_size, xnn_atm_energy
+//                                  per-atom energies (atm.py:84-162, 380-399, the formula
+//                                  of dispersion.py:183-222)
+// xnn_atm_energy_backward          their gradients in the edge vectors and in both C6
+//                                  factor matrices (atm.py:165-294, 402-443)
+//
+// Bookkeeping (dispersion.py:253-270, 343-398): a triangle of three distinct atoms is
+// evaluated once, from its smallest-index corner c (the pairs among c's edges to
+// larger-index neighbors), and a third of its energy goes to each corner; a triangle with
+// a repeated atom (an atom and its own periodic image, or two images of one neighbor) is
+// evaluated at every visit, its third going to the visiting center. The per-atom
+// energies are those of visiting every corner.
+//
+// Distinct triangles: work item = one wave = a center c and a tile of 64 of its edges to
+// larger-index neighbors, a = (j -> c) one per lane; the wave walks the later edges
+// b = (k -> c) of c in lockstep. b is wave-uniform, so its 64-byte record and the C6
+// factor row of k load through the scalar unit, the per-lane sums (edge a, atom j) stay
+// in registers until the item ends, and the per-b sums (edge b, atom k) are reduced
+// across the wave once per b (in the backward a transposing butterfly that leaves each
+// lane pair holding one of up to 32 sums) and added atomically. Items run heaviest tile
+// first. Repeated-atom triangles: one wave per flagged center, lanes over its edges,
+// each lane walking the few later edges that share an atom with its own.
+//
+// Pair C6 = <fa[x], fb[y]> over K <= 28 components (held per lane for j); the damping
+// radius is the product of three species-pair factors. Energies in hartree, lengths in
+// bohr.
+#include <hipcub/hipcub.hpp>
+
+#include <algorithm>
+#include <cstdint>
+
+#include "common.h"
+#include "device.h"
+#include "fp64.h"
+
+namespace xnn {
+
+constexpr int kAtmTile = 64;          // upper edges per item, one per lane
+constexpr int kAtmWaves = 4;          // waves (centers) per block
+constexpr int kAtmMaxK = 28;          // C6 factor components
+constexpr int kAtmMaxSpecies = 32;    // side of the damping-radius factor table
+constexpr double kAtmEps = 2.220446049250313e-16;   // lower bound on r_jk^2 (dispersion.py:200)
+
+// one sorted edge (j -> c) as the triplet kernels read it (one 64-byte scalar load)
+struct __align__(16) AtmEdge {
+  double vx, vy, vz;   // edge vector, bohr
+  double c6;           // <fa[c], fb[j]>
+  double p;            // damping-radius factor of the species pair (c, j)
+  double sw;           // switch at r = |v|
+  double dsw;          // its slope in r^2: sw'(r) / (2 r)
+  int32_t nb;          // the neighbor j
+  int32_t snb;         // its species
+};
+static_assert(sizeof(AtmEdge) == 64, "AtmEdge is one 64-byte record");
+
+struct AtmConst {
+  double s9_3;         // s9 / 3: a third of every triangle per corner
+  double alp3;
+  double cut2;
+  double cutoff;
+  double width;        // <= 0: sharp cutoff
+};
+
+static size_t atm_align(size_t x) { return (x + 255) & ~(size_t)255; }
+
+struct AtmPlanLayout {
+  size_t keys, perm, nbr, lo, lo1, flag, stats, keys_in, vals_in, cub, cub_bytes, total;
+};
+
+static int atm_end_bit(int64_t n) {
+  const uint64_t top = (uint64_t)n * (uint64_t)n;   // the out-of-range sentinel key
+  int b = 1;
+  while (b < 64 && (top >> b) != 0) ++b;
+  return b;
+}
+
+static AtmPlanLayout atm_plan_layout(int64_t E, int64_t N) {
+  AtmPlanLayout L;
+  size_t at = 0;
+  L.keys = at; at += atm_align(sizeof(uint64_t) * std::max<int64_t>(E, 1));
+  L.perm = at; at += atm_align(sizeof(int32_t) * std::max<int64_t>(E, 1));
+  L.nbr = at; at += atm_align(sizeof(int32_t) * std::max<int64_t>(E, 1));
+  L.lo = at; at += atm_align(sizeof(int32_t) * (N + 1));
+  L.lo1 = at; at += atm_align(sizeof(int32_t) * std::max<int64_t>(N, 1));
+  L.flag = at; at += atm_align(sizeof(int32_t) * std::max<int64_t>(N, 1));
+  L.stats = at; at += atm_align(sizeof(int32_t) * 4);
+  L.keys_in = at; at += atm_align(sizeof(uint64_t) * std::max<int64_t>(E, 1));
+  L.vals_in = at; at += atm_align(sizeof(int32_t) * std::max<int64_t>(E, 1));
+  size_t cub_bytes = 0;
+  (void)hipcub::DeviceRadixSort::SortPairs(nullptr, cub_bytes, (uint64_t*)nullptr,
+                                           (uint64_t*)nullptr, (int32_t*)nullptr,
+                                           (int32_t*)nullptr, (int)std::max<int64_t>(E, 1), 0,
+                                           atm_end_bit(N));
+  L.cub = at;
+  L.cub_bytes = atm_align(cub_bytes + 256);
+  at += L.cub_bytes;
+  L.total = at;
+  return L;
+}
+
+struct AtmWorkLayout {
+  size_t rec, fa, fb, gs, total;
+};
+
+static AtmWorkLayout atm_work_layout(int64_t E, int64_t N, int kp, bool backward) {
+  AtmWorkLayout L;
+  size_t at = 0;
+  L.rec = at; at += atm_align(sizeof(AtmEdge) * std::max<int64_t>(E, 1));
+  L.fa = at; at += atm_align(sizeof(double) * kp * std::max<int64_t>(N, 1));
+  L.fb = at; at += atm_align(sizeof(double) * kp * std::max<int64_t>(N, 1));
+  L.gs = at;
+  if (backward) at += atm_align(sizeof(double) * 4 * std::max<int64_t>(E, 1));
+  L.total = at;
+  return L;
+}
+
+template <typename T>
+static T* at_off(void* base, size_t off) {
+  return reinterpret_cast<T*>(static_cast<char*>(base) + off);
+}
+template <typename T>
+static const T* at_off(const void* base, size_t off) {
+  return reinterpret_cast<const T*>(static_cast<const char*>(base) + off);
+}
+
+// ------------------------------------------------------------------------------ plan
+__global__ void atm_fill_i32_kernel(int32_t* __restrict__ p, int64_t n) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = 0;
+}
+
+__global__ void atm_fill_f64_kernel(double* __restrict__ p, int64_t n) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = 0.0;
+}
+
+// key = center * N + neighbor; an index out of range gets the sentinel N^2 (sorted last)
+// and raises the plan's error flag
+__global__ void atm_keys_kernel(const int64_t* __restrict__ ei, int64_t E, int64_t N,
+                                uint64_t* __restrict__ keys, int32_t* __restrict__ vals,
+                                int32_t* __restrict__ stats) {
+  const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (e >= E) return;
+  const int64_t s = ei[e], d = ei[E + e];
+  uint64_t key = (uint64_t)N * (uint64_t)N;
+  if (s >= 0 && s < N && d >= 0 && d < N)
+    key = (uint64_t)d * (uint64_t)N + (uint64_t)s;
+  else
+    stats[2] = 1;
+  keys[e] = key;
+  vals[e] = (int32_t)e;
+}
+
+__device__ inline int64_t atm_lower_bound(const uint64_t* __restrict__ keys, int64_t n,
+                                          uint64_t v) {
+  int64_t lo = 0, hi = n;
+  while (lo < hi) {
+    const int64_t mid = (lo + hi) >> 1;
+    if (keys[mid] < v)
+      lo = mid + 1;
+    else
+      hi = mid;
+  }
+  return lo;
+}
+
+// neighbor of every sorted edge; a center with two edges to images of one neighbor has
+// repeated-atom triangles
+__global__ void atm_neighbors_kernel(const uint64_t* __restrict__ keys, int64_t E, int64_t N,
+                                     int32_t* __restrict__ nbr, int32_t* __restrict__ flag,
+                                     int32_t* __restrict__ stats) {
+  const int64_t p = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (p >= E) return;
+  const uint64_t k = keys[p];
+  const uint64_t top = (uint64_t)N * (uint64_t)N;
+  nbr[p] = k < top ? (int32_t)(k % (uint64_t)N) : 0;
+  if (k < top && p + 1 < E && keys[p + 1] == k) {
+    flag[k / (uint64_t)N] = 1;
+    stats[1] = 1;
+  }
+}
+
+// per-center ranges: [lo[c], lo1[c]) neighbors <= c, [lo1[c], lo[c+1]) neighbors > c; an
+// edge to the center's own image flags it; stats[0] = most tiles of upper edges
+__global__ void atm_rows_kernel(const uint64_t* __restrict__ keys, int64_t E, int64_t N,
+                                int32_t* __restrict__ lo, int32_t* __restrict__ lo1,
+                                int32_t* __restrict__ flag, int32_t* __restrict__ stats) {
+  const int64_t c = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (c > N) return;
+  const uint64_t base = (uint64_t)c * (uint64_t)N;
+  const int64_t l = atm_lower_bound(keys, E, base);
+  lo[c] = (int32_t)l;
+  if (c == N) return;
+  const int64_t u = atm_lower_bound(keys, E, base + (uint64_t)c + 1);
+  const int64_t h = atm_lower_bound(keys, E, base + (uint64_t)N);
+  lo1[c] = (int32_t)u;
+  if (u > l && keys[u - 1] == base + (uint64_t)c) {
+    flag[c] = 1;
+    stats[1] = 1;
+  }
+  const int64_t n_up = h - u;
+  if (n_up >= 2) atomicMax(&stats[0], (int32_t)((n_up + kAtmTile - 1) / kAtmTile));
+}
+
+// ------------------------------------------------------------------------------ records
+template <int KP>
+__global__ void atm_pad_kernel(const double* __restrict__ f, int64_t N, int K,
+                               double* __restrict__ out) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= N * KP) return;
+  const int64_t n = i / KP;
+  const int w = (int)(i - n * KP);
+  out[i] = w < K ? f[n * K + w] : 0.0;
+}
+
+template <int KP>
+__global__ void atm_edges_kernel(const uint64_t* __restrict__ keys,
+                                 const int32_t* __restrict__ perm,
+                                 const int32_t* __restrict__ nbr, int64_t E, int64_t N,
+                                 const double* __restrict__ vec, const double* __restrict__ fa,
+                                 const double* __restrict__ fb,
+                                 const int32_t* __restrict__ species,
+                                 const double* __restrict__ table, int S, AtmConst kc,
+                                 AtmEdge* __restrict__ rec) {
+  const int64_t p = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (p >= E) return;
+  const int64_t e = perm[p];
+  const int64_t c = (int64_t)(keys[p] / (uint64_t)N);
+  const int32_t j = nbr[p];
+  AtmEdge r;
+  r.vx = vec[3 * e + 0];
+  r.vy = vec[3 * e + 1];
+  r.vz = vec[3 * e + 2];
+  double c6 = 0.0;
+#pragma unroll
+  for (int w = 0; w < KP; ++w) c6 = fma(fa[c * KP + w], fb[(int64_t)j * KP + w], c6);
+  r.c6 = c6;
+  // a species outside the table gives a NaN factor (and stays a valid table index)
+  const int sc = species[c], sj = species[j];
+  const bool ok = sc >= 0 && sc < S && sj >= 0 && sj < S;
+  r.p = ok ? table[sc * S + sj] : __builtin_nan("");
+  r.sw = 1.0;
+  r.dsw = 0.0;
+  if (kc.width > 0.0) {
+    const double r2 = r.vx * r.vx + r.vy * r.vy + r.vz * r.vz;
+    const double len = sqrt(r2);
+    double sw, dsw;
+    switch_d(len, kc.cutoff, kc.width, sw, dsw);
+    r.sw = sw;
+    r.dsw = len > 0.0 ? 0.5 * dsw / len : 0.0;
+  }
+  r.nb = j;
+  r.snb = sj >= 0 && sj < S ? sj : 0;
+  rec[p] = r;
+}
+
+// ------------------------------------------------------------------------------ triangle
+// The energy of one triangle visit (weight * s9/3 * C9 * angular * damping * switches)
+// and, in the backward, its derivatives in the squared sides x = r_cj^2, y = r_ck^2,
+// w = r_jk^2 (dispersion.py:183-222; closed form of dispersion.py:413-510).
+template <bool SWITCH, bool BWD>
+__device__ __forceinline__ void atm_triangle(const AtmConst& kc, double x, double y, double w,
+                                             double ix, double iy, double c6abs, double r0,
+                                             double swa, double swb, double dswa, double dswb,
+                                             double weight, double& e, double& gx, double& gy,
+                                             double& gw) {
+  const double s = rsq_nr(x * y * w);            // 1 / (r_cj r_ck r_jk)
+  const double s2 = s * s;
+  const double s3 = s2 * s;
+  const double s5 = s3 * s2;
+  const double t = exp(kc.alp3 * log(r0 * s));   // (R0 / (r_cj r_ck r_jk))^alp3
+  const double damp = rcp_nr(fma(6.0, t, 1.0));
+  const double f1 = x + w - y, f2 = x - w + y, f3 = w + y - x;
+  const double nn = f1 * f2 * f3;
+  const double ang = fma(0.375 * nn, s5, s3);
+  double swjk = 1.0, dswjk = 0.0;
+  if (SWITCH) {
+    const double r = w * rsq_nr(w);
+    double sw, dsw;
+    switch_d(r, kc.cutoff, kc.width, sw, dsw);
+    swjk = sw;
+    dswjk = 0.5 * dsw / r;
+  }
+  const double sw = swa * swb * swjk;
+  const double base = weight * kc.s9_3 * sqrt(c6abs);
+  e = base * ang * damp * sw;
+  if (BWD) {
+    const double iw = rcp_nr(w);
+    const double a23 = f2 * f3, a13 = f1 * f3, a12 = f1 * f2;
+    const double q = 0.375 * s5;
+    const double ang_x = fma(q, fma(-2.5 * nn, ix, a23 + a13 - a12), -1.5 * s3 * ix);
+    const double ang_y = fma(q, fma(-2.5 * nn, iy, a13 + a12 - a23), -1.5 * s3 * iy);
+    const double ang_w = fma(q, fma(-2.5 * nn, iw, a23 + a12 - a13), -1.5 * s3 * iw);
+    const double dc = 3.0 * kc.alp3 * t * damp * damp;   // x d(damp)/dx
+    const double bd = base * damp * sw;
+    const double ba = base * ang;
+    const double dcs = dc * sw;
+    gx = fma(bd, ang_x, ba * fma(dcs, ix, damp * dswa * swb * swjk));
+    gy = fma(bd, ang_y, ba * fma(dcs, iy, damp * swa * dswb * swjk));
+    gw = fma(bd, ang_w, ba * fma(dcs, iw, damp * swa * swb * dswjk));
+  }
+}
+
+__device__ __forceinline__ double atm_wave_sum(double v) {
+#pragma unroll
+  for (int o = kWave / 2; o > 0; o >>= 1) v += __shfl_xor(v, o);
+  return v;
+}
+
+// One level of the transposing reduction: lanes whose bit 2H is set keep the upper H of
+// their 2H partial sums and send the lower H to their partner, the others the reverse.
+template <int H>
+__device__ __forceinline__ void atm_fold(double* p, int lane) {
+  const bool up = (lane & (2 * H)) != 0;
+#pragma unroll
+  for (int i = 0; i < H; ++i) {
+    const double send = up ? p[i] : p[i + H];
+    const double keep = up ? p[i + H] : p[i];
+    p[i] = keep + __shfl_xor(send, 2 * H);
+  }
+}
+
+// The wave-wide sums of 32 per-lane values: lanes 2s and 2s + 1 return the total of slot
+// s. 31 + 1 exchanges instead of 32 separate butterflies of 6.
+__device__ __forceinline__ double atm_reduce32(double* p, int lane) {
+  atm_fold<16>(p, lane);
+  atm_fold<8>(p, lane);
+  atm_fold<4>(p, lane);
+  atm_fold<2>(p, lane);
+  atm_fold<1>(p, lane);
+  return p[0] + __shfl_xor(p[0], 1);
+}
+
+__device__ __forceinline__ void atm_stage_table(const double* __restrict__ table, int S,
+                                                double* sTab) {
+  for (int i = threadIdx.x; i < S * S; i += blockDim.x) sTab[i] = table[i];
+  __syncthreads();
+}
+
+// ------------------------------------------------------------------------------ kernels
+// Distinct triangles from their smallest corner. Forward: energy[c], energy[j],
+// energy[k] += e. Backward (weights go_c + go_j + go_k): gs[edge] += (dE/dv, dE/dC6) for
+// both edges, gfa[j] += dE/dC6_jk fb[k], gfb[k] += dE/dC6_jk fa[j].
+template <int KP, bool SWITCH, bool BWD>
+__global__ __launch_bounds__(kAtmWaves * kWave) void atm_upper_kernel(
+    const AtmEdge* __restrict__ rec, const int32_t* __restrict__ lo,
+    const int32_t* __restrict__ lo1, int64_t N, int64_t n_groups,
+    const double* __restrict__ fa, const double* __restrict__ fb,
+    const double* __restrict__ table, int S, AtmConst kc, double* __restrict__ energy,
+    const double* __restrict__ go, double* __restrict__ gs, double* __restrict__ gfa,
+    double* __restrict__ gfb, int K) {
+  __shared__ double sTab[kAtmMaxSpecies * kAtmMaxSpecies];
+  atm_stage_table(table, S, sTab);
+  const int lane = threadIdx.x & (kWave - 1);
+  const int64_t t = blockIdx.x / n_groups;
+  const int64_t c = (blockIdx.x - t * n_groups) * kAtmWaves + wave_in_block();
+  if (c >= N) return;
+  const int32_t hi = lo[c + 1];
+  const int32_t a0 = lo1[c] + (int32_t)t * kAtmTile;
+  if (a0 + 1 >= hi) return;                       // fewer than two edges left: no pair
+  const int32_t a = a0 + lane;
+  const bool va = a < hi;
+  const AtmEdge ea = rec[va ? a : a0];
+  const double ax = ea.vx, ay = ea.vy, az = ea.vz;
+  const double x = ax * ax + ay * ay + az * az;
+  const double ix = BWD ? rcp_nr(x) : 0.0;
+  const double hc6a = BWD ? 0.5 / (ea.c6 != 0.0 ? ea.c6 : 1.0) : 0.0;   // dC9/C9 per dC6_cj
+  const int32_t j = ea.nb;
+  const int sj = ea.snb;
+  double fj[KP];
+#pragma unroll
+  for (int w = 0; w < KP; ++w) fj[w] = fa[(int64_t)j * KP + w];
+  const double go_c = BWD ? go[c] : 0.0;
+  const double go_j = BWD ? go[j] : 0.0;
+  double e_row = 0.0;
+  double gax = 0.0, gay = 0.0, gaz = 0.0, gc6a = 0.0;
+  double gfj[BWD ? KP : 1];
+#pragma unroll
+  for (int w = 0; w < (BWD ? KP : 1); ++w) gfj[w] = 0.0;
+
+  for (int32_t b = a0 + 1; b < hi; ++b) {
+    const AtmEdge eb = rec[b];                      // wave-uniform
+    const int32_t k = eb.nb;
+    const double dx = ax - eb.vx, dy = ay - eb.vy, dz = az - eb.vz;
+    const double w2 = dx * dx + dy * dy + dz * dz;
+    const bool keep = va && a < b && j != k && w2 <= kc.cut2 && w2 > kAtmEps;
+    if (__ballot(keep) == 0) continue;
+    const double y = eb.vx * eb.vx + eb.vy * eb.vy + eb.vz * eb.vz;
+    const double iy = BWD ? rcp_nr(y) : 0.0;
+    const double* __restrict__ fk = fb + (int64_t)k * KP;
+    double e = 0.0, gx = 0.0, gy = 0.0, gw = 0.0, c6jk = 1.0;
+    if (keep) {
+      c6jk = 0.0;
+#pragma unroll
+      for (int w = 0; w < KP; ++w) c6jk = fma(fj[w], fk[w], c6jk);
+      const double r0 = ea.p * eb.p * sTab[sj * S + eb.snb];
+      const double weight = BWD ? go_c + go_j + go[k] : 1.0;
+      atm_triangle<SWITCH, BWD>(kc, x, y, w2, ix, iy, fabs(ea.c6 * eb.c6 * c6jk), r0, ea.sw,
+                                eb.sw, ea.dsw, eb.dsw, weight, e, gx, gy, gw);
+    }
+    if (!BWD) {
+      e_row += e;
+      const double ek = atm_wave_sum(e);
+      if (lane == 0) unsafeAtomicAdd(&energy[k], ek);
+    } else {
+      // dE/dC6 = E / (2 C6) for each of the three pair coefficients (C9 = sqrt(C6 C6 C6))
+      const double g3 = keep ? 0.5 * e * rcp_nr(c6jk != 0.0 ? c6jk : 1.0) : 0.0;
+      gax = fma(2.0, fma(gx, ax, gw * dx), gax);
+      gay = fma(2.0, fma(gx, ay, gw * dy), gay);
+      gaz = fma(2.0, fma(gx, az, gw * dz), gaz);
+      gc6a = fma(e, hc6a, gc6a);
+#pragma unroll
+      for (int w = 0; w < KP; ++w) gfj[w] = fma(g3, fk[w], gfj[w]);
+      double sl[32];
+#pragma unroll
+      for (int w = 0; w < KP; ++w) sl[w] = g3 * fj[w];
+      sl[KP + 0] = 2.0 * fma(gy, eb.vx, -gw * dx);
+      sl[KP + 1] = 2.0 * fma(gy, eb.vy, -gw * dy);
+      sl[KP + 2] = 2.0 * fma(gy, eb.vz, -gw * dz);
+      sl[KP + 3] = 0.5 * e / (eb.c6 != 0.0 ? eb.c6 : 1.0);
+#pragma unroll
+      for (int w = KP + 4; w < 32; ++w) sl[w] = 0.0;
+      const double v = atm_reduce32(sl, lane);
+      const int slot = lane >> 1;
+      if ((lane & 1) == 0) {
+        if (slot < K)
+          unsafeAtomicAdd(&gfb[(int64_t)k * K + slot], v);
+        else if (slot >= KP && slot < KP + 4)
+          unsafeAtomicAdd(&gs[(int64_t)b * 4 + (slot - KP)], v);
+      }
+    }
+  }
+  if (!BWD) {
+    if (va) unsafeAtomicAdd(&energy[j], e_row);
+    const double ec = atm_wave_sum(e_row);
+    if (lane == 0) unsafeAtomicAdd(&energy[c], ec);
+  } else if (va) {
+    unsafeAtomicAdd(&gs[(int64_t)a * 4 + 0], gax);
+    unsafeAtomicAdd(&gs[(int64_t)a * 4 + 1], gay);
+    unsafeAtomicAdd(&gs[(int64_t)a * 4 + 2], gaz);
+    unsafeAtomicAdd(&gs[(int64_t)a * 4 + 3], gc6a);
+#pragma unroll
+    for (int w = 0; w < KP; ++w)
+      if (w < K) unsafeAtomicAdd(&gfa[(int64_t)j * K + w], gfj[w]);
+  }
+}
+
+// Triangles with a repeated atom, at every visit of a flagged center c, a third to c:
+// the pairs of c's edges where one edge goes to an image of c itself (any partner) or
+// both go to images of one neighbor. Edges of c are sorted by neighbor, so the partners
+// of an edge are its run of equal neighbors and the run of self-image edges, which ends
+// the lower range [lo[c], lo1[c]).
+template <int KP, bool SWITCH, bool BWD>
+__global__ __launch_bounds__(kAtmWaves * kWave) void atm_repeat_kernel(
+    const AtmEdge* __restrict__ rec, const int32_t* __restrict__ lo,
+    const int32_t* __restrict__ lo1, const int32_t* __restrict__ flag, int64_t N,
+    const double* __restrict__ fa, const double* __restrict__ fb,
+    const double* __restrict__ table, int S, AtmConst kc, double* __restrict__ energy,
+    const double* __restrict__ go, double* __restrict__ gs, double* __restrict__ gfa,
+    double* __restrict__ gfb, int K) {
+  __shared__ double sTab[kAtmMaxSpecies * kAtmMaxSpecies];
+  atm_stage_table(table, S, sTab);
+  const int lane = threadIdx.x & (kWave - 1);
+  const int64_t c = (int64_t)blockIdx.x * kAtmWaves + wave_in_block();
+  if (c >= N || flag[c] == 0) return;
+  const int32_t l0 = lo[c], u0 = lo1[c], hi = lo[c + 1];
+  int32_t s0 = u0;                                  // self-image edges: [s0, u0)
+  while (s0 > l0 && rec[s0 - 1].nb == (int32_t)c) --s0;
+  const double go_c = BWD ? go[c] : 0.0;
+  double e_acc = 0.0;
+  for (int32_t a0 = l0; a0 < hi; a0 += kAtmTile) {
+    const int32_t a = a0 + lane;
+    if (a >= hi) break;
+    const AtmEdge ea = rec[a];
+    const double ax = ea.vx, ay = ea.vy, az = ea.vz;
+    const double x = ax * ax + ay * ay + az * az;
+    const double ix = BWD ? rcp_nr(x) : 0.0;
+    const int32_t j = ea.nb;
+    double fj[KP];
+#pragma unroll
+    for (int w = 0; w < KP; ++w) fj[w] = fa[(int64_t)j * KP + w];
+    double gax = 0.0, gay = 0.0, gaz = 0.0, gc6a = 0.0;
+    double gfj[BWD ? KP : 1];
+#pragma unroll
+    for (int w = 0; w < (BWD ? KP : 1); ++w) gfj[w] = 0.0;
+    // partner ranges: a self edge pairs with every later edge; another edge with its
+    // run of equal neighbors and with the later self edges
+    const bool self = j == (int32_t)c;
+    int32_t run_end = a + 1;
+    if (!self)
+      while (run_end < hi && rec[run_end].nb == j) ++run_end;
+    const int32_t r1_end = self ? hi : run_end;
+    const int32_t r2_beg = self ? hi : (s0 > a + 1 ? s0 : a + 1);
+    const int32_t r2_end = self ? hi : u0;
+    for (int pass = 0; pass < 2; ++pass) {
+      const int32_t b_beg = pass == 0 ? a + 1 : r2_beg;
+      const int32_t b_end = pass == 0 ? r1_end : r2_end;
+      for (int32_t b = b_beg; b < b_end; ++b) {
+        const AtmEdge eb = rec[b];
+        const double dx = ax - eb.vx, dy = ay - eb.vy, dz = az - eb.vz;
+        const double w2 = dx * dx + dy * dy + dz * dz;
+        if (!(w2 <= kc.cut2 && w2 > kAtmEps)) continue;
+        const int32_t k = eb.nb;
+        const double y = eb.vx * eb.vx + eb.vy * eb.vy + eb.vz * eb.vz;
+        const double* __restrict__ fk = fb + (int64_t)k * KP;
+        double c6jk = 0.0;
+#pragma unroll
+        for (int w = 0; w < KP; ++w) c6jk = fma(fj[w], fk[w], c6jk);
+        const double r0 = ea.p * eb.p * sTab[ea.snb * S + eb.snb];
+        double e, gx = 0.0, gy = 0.0, gw = 0.0;
+        atm_triangle<SWITCH, BWD>(kc, x, y, w2, ix, BWD ? rcp_nr(y) : 0.0,
+                                  fabs(ea.c6 * eb.c6 * c6jk), r0, ea.sw, eb.sw, ea.dsw, eb.dsw,
+                                  BWD ? go_c : 1.0, e, gx, gy, gw);
+        if (!BWD) {
+          e_acc += e;
+        } else {
+          const double g3 = 0.5 * e / (c6jk != 0.0 ? c6jk : 1.0);
+          gax = fma(2.0, fma(gx, ax, gw * dx), gax);
+          gay = fma(2.0, fma(gx, ay, gw * dy), gay);
+          gaz = fma(2.0, fma(gx, az, gw * dz), gaz);
+          gc6a += 0.5 * e / (ea.c6 != 0.0 ? ea.c6 : 1.0);
+#pragma unroll
+          for (int w = 0; w < KP; ++w) gfj[w] = fma(g3, fk[w], gfj[w]);
+          unsafeAtomicAdd(&gs[(int64_t)b * 4 + 0], 2.0 * fma(gy, eb.vx, -gw * dx));
+          unsafeAtomicAdd(&gs[(int64_t)b * 4 + 1], 2.0 * fma(gy, eb.vy, -gw * dy));
+          unsafeAtomicAdd(&gs[(int64_t)b * 4 + 2], 2.0 * fma(gy, eb.vz, -gw * dz));
+          unsafeAtomicAdd(&gs[(int64_t)b * 4 + 3], 0.5 * e / (eb.c6 != 0.0 ? eb.c6 : 1.0));
+#pragma unroll
+          for (int w = 0; w < KP; ++w)
+            if (w < K) unsafeAtomicAdd(&gfb[(int64_t)k * K + w], g3 * fj[w]);
+        }
+      }
+    }
+    if (BWD) {
+      unsafeAtomicAdd(&gs[(int64_t)a * 4 + 0], gax);
+      unsafeAtomicAdd(&gs[(int64_t)a * 4 + 1], gay);
+      unsafeAtomicAdd(&gs[(int64_t)a * 4 + 2], gaz);
+      unsafeAtomicAdd(&gs[(int64_t)a * 4 + 3], gc6a);
+#pragma unroll
+      for (int w = 0; w < KP; ++w)
+        if (w < K) unsafeAtomicAdd(&gfa[(int64_t)j * K + w], gfj[w]);
+    }
+  }
+  if (!BWD) {
+    const double ec = atm_wave_sum(e_acc);
+    if (lane == 0) unsafeAtomicAdd(&energy[c], ec);
+  }
+}
+
+// grad_vec[original edge] = the sorted edge's vector gradient
+__global__ void atm_vec_grad_kernel(const int32_t* __restrict__ perm,
+                                    const double* __restrict__ gs, int64_t E,
+                                    double* __restrict__ gvec) {
+  const int64_t p = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (p >= E) return;
+  const int64_t e = perm[p];
+  gvec[3 * e + 0] = gs[4 * p + 0];
+  gvec[3 * e + 1] = gs[4 * p + 1];
+  gvec[3 * e + 2] = gs[4 * p + 2];
+}
+
+// The center sides C6_cj = <fa[c], fb[j]> of every edge: gfa[c] += sum_row dE/dC6 fb[j]
+// (one wave per center, reduced across the wave) and gfb[j] += dE/dC6 fa[c] (atomic)
+template <int KP>
+__global__ __launch_bounds__(kAtmWaves * kWave) void atm_center_side_kernel(
+    const int32_t* __restrict__ lo, const int32_t* __restrict__ nbr,
+    const double* __restrict__ gs, const double* __restrict__ fa,
+    const double* __restrict__ fb, int64_t N, int K, double* __restrict__ gfa,
+    double* __restrict__ gfb) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int64_t c = (int64_t)blockIdx.x * kAtmWaves + wave_in_block();
+  if (c >= N) return;
+  const int32_t l0 = lo[c], hi = lo[c + 1];
+  if (l0 == hi) return;
+  double acc[32];
+#pragma unroll
+  for (int w = 0; w < 32; ++w) acc[w] = 0.0;
+  for (int32_t p = l0 + lane; p < hi; p += kWave) {
+    const double g = gs[4 * (int64_t)p + 3];
+    const int64_t j = nbr[p];
+#pragma unroll
+    for (int w = 0; w < KP; ++w) acc[w] = fma(g, fb[j * KP + w], acc[w]);
+#pragma unroll
+    for (int w = 0; w < KP; ++w)
+      if (w < K) unsafeAtomicAdd(&gfb[j * K + w], g * fa[c * KP + w]);
+  }
+  const double v = atm_reduce32(acc, lane);
+  const int slot = lane >> 1;
+  if ((lane & 1) == 0 && slot < K) gfa[c * K + slot] += v;
+}
+
+// ------------------------------------------------------------------------------ host
+static AtmConst atm_const(const xnn_atm_params* prm) {
+  AtmConst k;
+  k.s9_3 = prm->s9 / 3.0;
+  k.alp3 = prm->alp3;
+  k.cut2 = prm->cutoff * prm->cutoff;
+  k.cutoff = prm->cutoff;
+  k.width = prm->width > 0.0 ? std::min(prm->width, prm->cutoff) : 0.0;
+  return k;
+}
+
+static int atm_kp(int K) { return K <= 24 ? 24 : 28; }
+
+static void atm_zero(double* p, int64_t n, hipStream_t s) {
+  if (n > 0) hipLaunchKernelGGL(atm_fill_f64_kernel, dim3(grid_1d(n, 256)), dim3(256), 0, s, p, n);
+}
+
+struct AtmArgs {
+  const void* plan;
+  int64_t E, N, max_tiles, has_repeats;
+  const double* vec;
+  const double* fa;
+  const double* fb;
+  int K;
+  const int32_t* species;
+  const double* table;
+  int S;
+  AtmConst kc;
+  double* energy;
+  const double* go;
+  double* gvec;
+  double* gfa;
+  double* gfb;
+  void* work;
+  hipStream_t s;
+};
+
+template <int KP, bool SWITCH, bool BWD>
+static int atm_run(const AtmArgs& A) {
+  const AtmPlanLayout P = atm_plan_layout(A.E, A.N);
+  const AtmWorkLayout W = atm_work_layout(A.E, A.N, KP, BWD);
+  const uint64_t* keys = at_off<uint64_t>(A.plan, P.keys);
+  const int32_t* perm = at_off<int32_t>(A.plan, P.perm);
+  const int32_t* nbr = at_off<int32_t>(A.plan, P.nbr);
+  const int32_t* lo = at_off<int32_t>(A.plan, P.lo);
+  const int32_t* lo1 = at_off<int32_t>(A.plan, P.lo1);
+  const int32_t* flag = at_off<int32_t>(A.plan, P.flag);
+  AtmEdge* rec = at_off<AtmEdge>(A.work, W.rec);
+  double* faP = at_off<double>(A.work, W.fa);
+  double* fbP = at_off<double>(A.work, W.fb);
+  double* gs = BWD ? at_off<double>(A.work, W.gs) : nullptr;
+  const int64_t nk = A.N * (int64_t)A.K;
+  if (!BWD) {
+    atm_zero(A.energy, A.N, A.s);
+  } else {
+    atm_zero(gs, 4 * A.E, A.s);
+    atm_zero(A.gfa, nk, A.s);
+    atm_zero(A.gfb, nk, A.s);
+  }
+  XNN_LAUNCH_CHECK();
+  if (A.E == 0 || A.N == 0) return XNN_OK;
+  hipLaunchKernelGGL((atm_pad_kernel<KP>), dim3(grid_1d(A.N * KP, 256)), dim3(256), 0, A.s, A.fa,
+                     A.N, A.K, faP);
+  hipLaunchKernelGGL((atm_pad_kernel<KP>), dim3(grid_1d(A.N * KP, 256)), dim3(256), 0, A.s, A.fb,
+                     A.N, A.K, fbP);
+  hipLaunchKernelGGL((atm_edges_kernel<KP>), dim3(grid_1d(A.E, 256)), dim3(256), 0, A.s, keys,
+                     perm, nbr, A.E, A.N, A.vec, faP, fbP, A.species, A.table, A.S, A.kc, rec);
+  XNN_LAUNCH_CHECK();
+  const int64_t n_groups = (A.N + kAtmWaves - 1) / kAtmWaves;
+  if (A.max_tiles > 0) {
+    const int64_t blocks = A.max_tiles * n_groups;
+    XNN_REQUIRE(blocks <= 0x7fffffff, "ATM: too many triplet work items");
+    hipLaunchKernelGGL((atm_upper_kernel<KP, SWITCH, BWD>), dim3((unsigned)blocks),
+                       dim3(kAtmWaves * kWave), 0, A.s, rec, lo, lo1, A.N, n_groups, faP, fbP,
+                       A.table, A.S, A.kc, A.energy, A.go, gs, A.gfa, A.gfb, A.K);
+    XNN_LAUNCH_CHECK();
+  }
+  if (A.has_repeats) {
+    hipLaunchKernelGGL((atm_repeat_kernel<KP, SWITCH, BWD>), dim3((unsigned)n_groups),
+                       dim3(kAtmWaves * kWave), 0, A.s, rec, lo, lo1, flag, A.N, faP, fbP,
+                       A.table, A.S, A.kc, A.energy, A.go, gs, A.gfa, A.gfb, A.K);
+    XNN_LAUNCH_CHECK();
+  }
+  if (BWD) {
+    hipLaunchKernelGGL(atm_vec_grad_kernel, dim3(grid_1d(A.E, 256)), dim3(256), 0, A.s, perm, gs,
+                       A.E, A.gvec);
+    hipLaunchKernelGGL((atm_center_side_kernel<KP>), dim3((unsigned)n_groups),
+                       dim3(kAtmWaves * kWave), 0, A.s, lo, nbr, gs, faP, fbP, A.N, A.K, A.gfa,
+                       A.gfb);
+    XNN_LAUNCH_CHECK();
+  }
+  return XNN_OK;
+}
+
+template <bool BWD>
+static int atm_dispatch(const AtmArgs& A) {
+  const bool sw = A.kc.width > 0.0;
+  if (atm_kp(A.K) == 24)
+    return sw ? atm_run<24, true, BWD>(A) : atm_run<24, false, BWD>(A);
+  return sw ? atm_run<28, true, BWD>(A) : atm_run<28, false, BWD>(A);
+}
+
+static int atm_check(int64_t E, int64_t N, int64_t max_tiles, const double* vec, const double* fa,
+                     const double* fb, int32_t K, const int32_t* species, const double* table,
+                     int32_t S, const xnn_atm_params* prm, const void* plan, void* work,
+                     size_t work_bytes, bool bwd) {
+  XNN_REQUIRE(E >= 0 && N >= 0 && max_tiles >= 0, "negative size");
+  XNN_REQUIRE(E <= 0x7fffffff && N < 0x7fffffff, "ATM: at most 2^31 - 1 edges and atoms");
+  XNN_REQUIRE(K >= 1 && K <= kAtmMaxK, "ATM: the C6 factors need 1 to %d components (got %d)",
+              kAtmMaxK, (int)K);
+  XNN_REQUIRE(S >= 1 && S <= kAtmMaxSpecies, "ATM: 1 to %d species (got %d)", kAtmMaxSpecies,
+              (int)S);
+  XNN_REQUIRE(prm != nullptr && prm->cutoff > 0.0, "ATM: a positive cutoff is required");
+  XNN_REQUIRE(plan != nullptr && work != nullptr, "NULL plan or workspace");
+  XNN_REQUIRE(work_bytes >= atm_work_layout(E, N, atm_kp(K), bwd).total, "workspace too small");
+  XNN_REQUIRE(N == 0 || (fa && fb && species && table), "NULL input");
+  XNN_REQUIRE(E == 0 || vec, "NULL edge vectors");
+  return XNN_OK;
+}
+
+}  // namespace xnn
+
+using namespace xnn;
+
+extern "C" {
+
+int xnn_atm_plan_size(int64_t n_edges, int64_t n_atoms, size_t* bytes) {
+  XNN_REQUIRE(n_edges >= 0 && n_atoms >= 0 && bytes, "negative size or NULL output");
+  XNN_REQUIRE(n_edges <= 0x7fffffff && n_atoms < 0x7fffffff,
+              "ATM: at most 2^31 - 1 edges and atoms");
+  *bytes = atm_plan_layout(n_edges, n_atoms).total;
+  return XNN_OK;
+}
+
+int xnn_atm_plan(const int64_t* edge_index, int64_t n_edges, int64_t n_atoms, void* plan,
+                 size_t plan_bytes, int64_t* info, xnn_stream_t stream) {
+  XNN_REQUIRE(n_edges >= 0 && n_atoms >= 0, "negative size");
+  XNN_REQUIRE(n_edges <= 0x7fffffff && n_atoms < 0x7fffffff,
+              "ATM: at most 2^31 - 1 edges and atoms");
+  XNN_REQUIRE(plan != nullptr && info != nullptr, "NULL plan or info");
+  XNN_REQUIRE(n_edges == 0 || edge_index != nullptr, "NULL edge_index");
+  const AtmPlanLayout L = atm_plan_layout(n_edges, n_atoms);
+  XNN_REQUIRE(plan_bytes >= L.total, "plan buffer too small (%zu < %zu bytes)", plan_bytes,
+              L.total);
+  hipStream_t s = as_hip(stream);
+  const int64_t E = n_edges, N = n_atoms;
+  int32_t* flag = at_off<int32_t>(plan, L.flag);
+  int32_t* stats = at_off<int32_t>(plan, L.stats);
+  hipLaunchKernelGGL(atm_fill_i32_kernel, dim3(grid_1d(std::max<int64_t>(N, 1), 256)), dim3(256),
+                     0, s, flag, std::max<int64_t>(N, 1));
+  hipLaunchKernelGGL(atm_fill_i32_kernel, dim3(1), dim3(64), 0, s, stats, 4);
+  XNN_LAUNCH_CHECK();
+  if (E > 0) {
+    uint64_t* keys_in = at_off<uint64_t>(plan, L.keys_in);
+    int32_t* vals_in = at_off<int32_t>(plan, L.vals_in);
+    uint64_t* keys = at_off<uint64_t>(plan, L.keys);
+    int32_t* perm = at_off<int32_t>(plan, L.perm);
+    hipLaunchKernelGGL(atm_keys_kernel, dim3(grid_1d(E, 256)), dim3(256), 0, s, edge_index, E, N,
+                       keys_in, vals_in, stats);
+    XNN_LAUNCH_CHECK();
+    size_t cub_bytes = L.cub_bytes;
+    XNN_HIP_CHECK(hipcub::DeviceRadixSort::SortPairs(at_off<void>(plan, L.cub), cub_bytes, keys_in,
+                                                     keys, vals_in, perm, (int)E, 0,
+                                                     atm_end_bit(N), s));
+    hipLaunchKernelGGL(atm_neighbors_kernel, dim3(grid_1d(E, 256)), dim3(256), 0, s, keys, E, N,
+                       at_off<int32_t>(plan, L.nbr), flag, stats);
+    XNN_LAUNCH_CHECK();
+  }
+  hipLaunchKernelGGL(atm_rows_kernel, dim3(grid_1d(N + 1, 256)), dim3(256), 0, s,
+                     at_off<uint64_t>(plan, L.keys), E, N, at_off<int32_t>(plan, L.lo),
+                     at_off<int32_t>(plan, L.lo1), flag, stats);
+  XNN_LAUNCH_CHECK();
+  int32_t h[4];
+  XNN_HIP_CHECK(hipMemcpyAsync(h, stats, sizeof(h), hipMemcpyDeviceToHost, s));
+  XNN_HIP_CHECK(hipStreamSynchronize(s));
+  XNN_REQUIRE(h[2] == 0, "ATM: edge_index holds an atom index outside [0, %lld)",
+              (long long)N);
+  info[0] = h[0];
+  info[1] = h[1];
+  return XNN_OK;
+}
+
+int xnn_atm_work_size(int64_t n_edges, int64_t n_atoms, int32_t k, int32_t backward,
+                      size_t* bytes) {
+  XNN_REQUIRE(n_edges >= 0 && n_atoms >= 0 && bytes, "negative size or NULL output");
+  XNN_REQUIRE(k >= 1 && k <= kAtmMaxK, "ATM: the C6 factors need 1 to %d components (got %d)",
+              kAtmMaxK, (int)k);
+  *bytes = atm_work_layout(n_edges, n_atoms, atm_kp(k), backward != 0).total;
+  return XNN_OK;
+}
+
+int xnn_atm_energy(const void* plan, int64_t n_edges, int64_t n_atoms, int64_t max_tiles,
+                   int64_t has_repeats, const double* edge_vec, const double* feat_a,
+                   const double* feat_b, int32_t k, const int32_t* species, const double* table,
+                   int32_t n_species, const xnn_atm_params* prm, double* energy, void* work,
+                   size_t work_bytes, xnn_stream_t stream) {
+  const int rc = atm_check(n_edges, n_atoms, max_tiles, edge_vec, feat_a, feat_b, k, species,
+                           table, n_species, prm, plan, work, work_bytes, false);
+  if (rc != XNN_OK) return rc;
+  XNN_REQUIRE(n_atoms == 0 || energy != nullptr, "NULL output");
+  AtmArgs A{plan, n_edges, n_atoms, max_tiles, has_repeats, edge_vec, feat_a, feat_b, k,
+            species, table, n_species, atm_const(prm), energy, nullptr, nullptr, nullptr,
+            nullptr, work, as_hip(stream)};
+  return atm_dispatch<false>(A);
+}
+
+int xnn_atm_energy_backward(const void* plan, int64_t n_edges, int64_t n_atoms,
+                            int64_t max_tiles, int64_t has_repeats, const double* edge_vec,
+                            const double* feat_a, const double* feat_b, int32_t k,
+                            const int32_t* species, const double* table, int32_t n_species,
+                            const xnn_atm_params* prm, const double* grad_energy,
+                            double* grad_vec, double* grad_fa, double* grad_fb, void* work,
+                            size_t work_bytes, xnn_stream_t stream) {
+  const int rc = atm_check(n_edges, n_atoms, max_tiles, edge_vec, feat_a, feat_b, k, species,
+                           table, n_species, prm, plan, work, work_bytes, true);
+  if (rc != XNN_OK) return rc;
+  XNN_REQUIRE(n_atoms == 0 || (grad_energy && grad_fa && grad_fb), "NULL input or output");
+  XNN_REQUIRE(n_edges == 0 || grad_vec, "NULL output");
+  AtmArgs A{plan, n_edges, n_atoms, max_tiles, has_repeats, edge_vec, feat_a, feat_b, k,
+            species, table, n_species, atm_const(prm), nullptr, grad_energy, grad_vec, grad_fa,
+            grad_fb, work, as_hip(stream)};
+  return atm_dispatch<true>(A);
+}
+
+}  // extern "C"

@@ -23,7 +23,9 @@ the cutoffs, so the graph may be built at the wrapped model's own cutoff.
 """
 from __future__ import annotations
 
+import ctypes
 import math
+from dataclasses import dataclass
 from typing import Dict, List, Optional, Tuple
 
 import numpy as np
@@ -270,6 +272,123 @@ def _alpha_backward(ctx, g_alpha):
 
 
 d4_polarizabilities_op.register_autograd(_alpha_backward, setup_context=_alpha_setup)
+
+
+# --------------------------------------------------------------------------- ATM
+@dataclass
+class ATMConstants:
+    """The scalars and tables of one ATM term (dispersion_fast/atm.py:355-363): per-atom
+    ``species`` (N,) indexing the ``table`` (S, S) of damping-radius pair factors (the
+    triangle's R0 is the product of its three), ``s9``, the exponent ``alp3``, the
+    three-body ``cutoff`` and switching ``width`` (bohr; <= 0: sharp)."""
+
+    species: Tensor
+    table: Tensor
+    s9: float
+    alp3: float
+    cutoff: float
+    width: float
+
+
+def atm_plan(edge_index: Tensor, n_atoms: int) -> Tuple[Tensor, List[int]]:
+    """The triplet plan of an edge list on the GPU (dispersion_fast/atm.py:318-352): the
+    edges sorted by (center, neighbor) with the per-center ranges, as an opaque byte
+    tensor, and ``[tiles, has_repeats]`` (the busiest center's tiles of 64 edges to
+    larger-index neighbors; whether some center has repeated-atom triangles). One small
+    synchronous device-to-host copy."""
+    dev = edge_index.device
+    ei = edge_index.to(torch.long).contiguous()
+    n_edges = int(ei.shape[1])
+    nbytes = ctypes.c_size_t()
+    _lib.call("xnn_atm_plan_size", n_edges, int(n_atoms), ctypes.byref(nbytes))
+    plan = torch.empty(max(int(nbytes.value), 1), dtype=torch.uint8, device=dev)
+    info = (ctypes.c_int64 * 2)()
+    _lib.call("xnn_atm_plan", _lib.ptr(ei), n_edges, int(n_atoms), _lib.ptr(plan),
+              int(nbytes.value), info, _lib.stream(dev))
+    return plan, [int(info[0]), int(info[1])]
+
+
+def _atm_work(n_edges: int, n_atoms: int, k: int, backward: bool, dev) -> Tensor:
+    nbytes = ctypes.c_size_t()
+    _lib.call("xnn_atm_work_size", n_edges, n_atoms, k, int(backward), ctypes.byref(nbytes))
+    return torch.empty(max(int(nbytes.value), 1), dtype=torch.uint8, device=dev)
+
+
+def _atm_params(p: List[float]) -> "_lib.AtmParams":
+    return _lib.AtmParams(float(p[0]), float(p[1]), float(p[2]), float(p[3]))
+
+
+@torch.library.custom_op(f"{_NS}::atm_energy", mutates_args=())
+def atm_energy_op(plan: Tensor, edge_vec: Tensor, feat_a: Tensor, feat_b: Tensor,
+                  species: Tensor, table: Tensor, params: List[float], n_atoms: int,
+                  max_tiles: int, has_repeats: int) -> Tensor:
+    """Per-atom ATM energies (N,) in hartree over the planned edges (bohr vectors, input
+    order), pair C6 = <feat_a[x], feat_b[y]>, ``params`` = [s9, alp3, cutoff, width];
+    differentiable once in ``edge_vec``, ``feat_a`` and ``feat_b``."""
+    dev = edge_vec.device
+    n_edges, k = int(edge_vec.shape[0]), int(feat_a.shape[1])
+    energy = torch.empty(n_atoms, dtype=torch.float64, device=dev)
+    work = _atm_work(n_edges, n_atoms, k, False, dev)
+    _lib.call("xnn_atm_energy", _lib.ptr(plan), n_edges, n_atoms, max_tiles, has_repeats,
+              _lib.ptr(edge_vec), _lib.ptr(feat_a), _lib.ptr(feat_b), k, _lib.ptr(species),
+              _lib.ptr(table), int(table.shape[0]), _atm_params(params), _lib.ptr(energy),
+              _lib.ptr(work), work.numel(), _lib.stream(dev))
+    return energy
+
+
+@atm_energy_op.register_fake
+def _(plan, edge_vec, feat_a, feat_b, species, table, params, n_atoms, max_tiles, has_repeats):
+    return edge_vec.new_empty(n_atoms)
+
+
+def _atm_setup(ctx, inputs, output):
+    plan, edge_vec, feat_a, feat_b, species, table, params, n_atoms, max_tiles, has_repeats = inputs
+    ctx.save_for_backward(plan, edge_vec, feat_a, feat_b, species, table)
+    ctx.meta = (list(params), n_atoms, max_tiles, has_repeats)
+
+
+def _atm_backward(ctx, g_energy):
+    if torch.is_grad_enabled():
+        raise RuntimeError("the ATM kernels are differentiable once (use_fast=False for more)")
+    plan, vec, fa, fb, species, table = ctx.saved_tensors
+    params, n_atoms, max_tiles, has_repeats = ctx.meta
+    dev = vec.device
+    n_edges, k = int(vec.shape[0]), int(fa.shape[1])
+    g_vec = torch.empty_like(vec)
+    g_fa = torch.empty_like(fa)
+    g_fb = torch.empty_like(fb)
+    work = _atm_work(n_edges, n_atoms, k, True, dev)
+    _lib.call("xnn_atm_energy_backward", _lib.ptr(plan), n_edges, n_atoms, max_tiles,
+              has_repeats, _lib.ptr(vec), _lib.ptr(fa), _lib.ptr(fb), k, _lib.ptr(species),
+              _lib.ptr(table), int(table.shape[0]), _atm_params(params),
+              _lib.ptr(g_energy.to(torch.float64).contiguous()), _lib.ptr(g_vec), _lib.ptr(g_fa),
+              _lib.ptr(g_fb), _lib.ptr(work), work.numel(), _lib.stream(dev))
+    need = ctx.needs_input_grad
+    return (None, g_vec if need[1] else None, g_fa if need[2] else None,
+            g_fb if need[3] else None) + (None,) * 6
+
+
+atm_energy_op.register_autograd(_atm_backward, setup_context=_atm_setup)
+
+
+def atm_energy(edge_index: Tensor, edge_vec: Tensor, feat_a: Tensor, feat_b: Tensor,
+               consts: ATMConstants, n_atoms: int) -> Tensor:
+    """Per-atom ATM energies (N,) in hartree with the HIP kernels
+    (dispersion_fast/atm.py:512-535): ``edge_index`` (2, E) ``[src, dst]`` within the
+    three-body cutoff, both directions of every pair; ``edge_vec`` (E, 3) in bohr;
+    ``feat_a``, ``feat_b`` (N, K <= 28) with pair C6 = <feat_a[x], feat_b[y]> (may be the
+    same tensor). Differentiable once in ``edge_vec``, ``feat_a`` and ``feat_b``; float64
+    throughout; GPU only."""
+    if not edge_vec.is_cuda:
+        raise RuntimeError("xnn_amd ATM runs on the GPU (HIP kernels); there is no CPU path")
+    plan, info = atm_plan(edge_index, n_atoms)
+    f64 = torch.float64
+    return atm_energy_op(plan, edge_vec.to(f64).contiguous(), feat_a.to(f64).contiguous(),
+                         feat_b.to(f64).contiguous(),
+                         consts.species.to(device=edge_vec.device, dtype=torch.int32).contiguous(),
+                         consts.table.to(device=edge_vec.device, dtype=f64).contiguous(),
+                         [float(consts.s9), float(consts.alp3), float(consts.cutoff),
+                          float(consts.width)], int(n_atoms), info[0], info[1])
 
 
 # --------------------------------------------------------------------------- host pieces
