@@ -147,3 +147,47 @@ def test_weights_kernel_matches_oracle(tables):
     bad = model.weights(torch.tensor([0, n_sp], device=DEV),
                         torch.tensor([1.0, 1.0], dtype=torch.float64, device=DEV))
     assert torch.isfinite(bad[0]).all() and torch.isnan(bad[1]).all()
+
+
+@pytest.mark.parametrize("periodic", [False, True])
+def test_three_body_matches_oracle(tables, periodic):
+    """The D3 ATM term (s9 = 1, radii 4/3 R0_AB, exponent (alp + 2) / 3, a 1 A switch on a
+    6 A triple cutoff; d3.py:840-859, 916-936): its energy and its position and cell
+    gradients against the oracle's CN, weights and pair C6 (oracle/d3.py) fed as a dense C6
+    matrix to the oracle's edge-list ATM (feat_a = C6 rows, feat_b = identity), which also
+    checks the module's factorization of C6 over reference slots."""
+    import oracle.d3 as D3
+    import oracle.d4 as D4
+    import xnn_amd.dispersion as XD
+    _note(f"d3 three-body vs oracle: periodic={periodic}")
+    pos, z = _cluster(10, seed=8)
+    cell = np.diag([7.0, 7.5, 8.0]) if periodic else None
+    cut_tri, width = 6.0, 1.0
+    model = XD.DFTD3(tables, s9=1.0, cutoff_triple=cut_tri, switch_width_triple=width,
+                     **FAST).to(DEV)
+    out, p, c = _eval(model, pos, z, cell, grad=True)
+    got = torch.autograd.grad(out["energy_3body"].sum(), [p] + ([c] if c is not None else []))
+    n = len(z)
+    s = D3.species_of(tables, z)
+    dst, src, sh = D4.pair_images(pos, cell, max(FAST["cutoff_cn"], cut_tri))
+    pt = torch.tensor(pos, dtype=torch.float64, requires_grad=True)
+    ct = None if cell is None else torch.tensor(cell, dtype=torch.float64, requires_grad=True)
+    v = D4.edge_vectors_au(pt, ct, dst, src, sh)
+    r = torch.linalg.norm(v, dim=-1)
+    cn = D3.coordination_numbers(s, dst, src, r, tables, FAST["cutoff_cn"] / D4.BOHR, n)
+    w = D3.weights(s, cn, tables)
+    ii, jj = torch.meshgrid(torch.arange(n), torch.arange(n), indexing="ij")
+    c6 = D3.pair_c6(s, w, ii.reshape(-1), jj.reshape(-1), tables).reshape(n, n)
+    tri = r <= cut_tri / D4.BOHR
+    ei = torch.stack([torch.as_tensor(src), torch.as_tensor(dst)])[:, tri]
+    uniq, spec = torch.unique(s, return_inverse=True)
+    table = (4.0 / 3.0) * torch.as_tensor(tables["rvdw"])[uniq][:, uniq]
+    e3 = D4.atm_edges(ei, v[tri], c6, torch.eye(n, dtype=torch.float64), spec, table, 1.0,
+                      16.0 / 3.0, cut_tri / D4.BOHR, width / D4.BOHR, n)
+    ref = torch.autograd.grad(e3.sum(), [pt] + ([ct] if ct is not None else []))
+    assert float(e3.sum()) > 0
+    assert abs(float(out["energy_3body"][0]) / XD.HARTREE - float(e3.sum())) \
+        < 1e-12 * float(e3.sum())
+    for a, b in zip(got, ref):
+        a = a.reshape(b.shape).detach().cpu() / XD.HARTREE
+        np.testing.assert_allclose(a, b, atol=1e-11 * float(b.abs().max()))

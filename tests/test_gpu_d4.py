@@ -15,7 +15,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 TABLES = os.path.join(HERE, "golden", "d4_tables_hcnoar.npz")
 WATER = (np.array([[0.0, 0.0, 0.119262], [0.0, 0.763239, -0.477047],
                    [0.0, -0.763239, -0.477047]]), [8, 1, 1])
-FAST = dict(cutoff_pair=9.0, cutoff_cn=8.0, cutoff_eeq_cn=8.0)
+FAST = dict(cutoff_pair=9.0, cutoff_triple=7.0, cutoff_cn=8.0, cutoff_eeq_cn=8.0)
 
 
 def _note(msg):
@@ -78,8 +78,10 @@ def test_water_golden_values_on_the_gpu(tables):
                                [6.71824515, 1.35296894, 1.35296894], atol=1e-7)
     c6 = XD.c6_matrix(out["dynamic_polarizabilities"]).cpu().numpy()
     assert abs(c6[0, 0] - 24.68023585) < 1e-6 and abs(c6[0, 1] - 4.2011774) < 1e-6
-    # dftd4's total includes a 1.8e-11 Eh three-body part; the two-body term meets 1e-10
-    assert abs(float(out["energy"][0]) / XD.HARTREE - (-1.5761743e-04)) < 1e-10
+    # dftd4's total, its 1.8e-11 Eh three-body part included, to the golden's 8 printed
+    # digits (half a unit in the last: 5e-12)
+    assert abs(float(out["energy"][0]) / XD.HARTREE - (-1.5761743e-04)) < 5e-12
+    assert 1e-11 < float(out["energy_3body"][0]) / XD.HARTREE < 3e-11
 
 
 def test_argon_dimer_asymptote(tables):
@@ -114,7 +116,7 @@ def test_kernels_match_oracle(tables, case):
         pos, z = _cluster(10, seed=7)
         cell = np.array([[6.0, 0, 0], [0.8, 5.7, 0], [-0.4, 0.6, 6.2]])
         width = 2.0
-    model = XD.DFTD4(tables, switch_width_pair=width, **FAST).to(DEV)
+    model = XD.DFTD4(tables, switch_width_pair=width, s9=0.0, **FAST).to(DEV)
     q = torch.tensor(np.random.default_rng(1).normal(0, 0.2, len(z)), dtype=torch.float64)
     out, p, c = _eval(model, pos, z, cell, charges=q.to(DEV), grad=True)
     gp, *gc = torch.autograd.grad(out["energy"].sum(), [p] + ([c] if c is not None else []))
@@ -177,8 +179,10 @@ def _lib_calls(name):
 
 
 def test_full_molecule_with_eeq_matches_oracle_and_finite_differences(tables):
-    """Charges from the EEQ solve on both sides; forces against central differences of
-    the GPU energy (test_d4.py:202-215: h = 1e-4 A, 1e-7 eV/A)."""
+    """The whole D4 energy, EEQ charges and the ATM term (neutral-atom C6, 7 A triple
+    cutoff) included, against the oracle's molecule (direct triple loop); forces against
+    central differences of the GPU energy (test_d4.py:202-215: h = 1e-4 A, 1e-7 eV/A),
+    which covers the ATM force's chain through the neutral polarizabilities to the CN."""
     import oracle.d4 as D
     import xnn_amd.dispersion as XD
     _note("d4 molecule full path")
@@ -186,9 +190,12 @@ def test_full_molecule_with_eeq_matches_oracle_and_finite_differences(tables):
     model = XD.DFTD4(tables, **FAST).to(DEV)
     out, p, _ = _eval(model, pos, z, grad=True)
     (gp,) = torch.autograd.grad(out["energy"].sum(), [p])
-    ref = D.d4_molecule(pos, z, tables, prm=dict(D.PBE0_D4, s9=0.0), with_atm=False,
+    ref = D.d4_molecule(pos, z, tables, prm=D.PBE0_D4, with_atm=True,
                         cutoffs_au=(9.0 / D.BOHR, 7.0 / D.BOHR, 8.0 / D.BOHR, 8.0 / D.BOHR))
     np.testing.assert_allclose(out["charges"].detach().cpu(), ref["q"], atol=1e-12)
+    assert float(ref["energy_3body"]) > 0
+    assert abs(float(out["energy_3body"][0]) / XD.HARTREE - float(ref["energy_3body"])) \
+        < 1e-12 * float(ref["energy_3body"])
     assert abs(float(out["energy"][0]) / XD.HARTREE - float(ref["energy"])) < 1e-14
     h = 1e-4
     for i, a in [(0, 0), (3, 2), (5, 1)]:

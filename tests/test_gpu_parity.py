@@ -119,6 +119,19 @@ def test_radius_graph_edge_cases():
         ei, sh, _ = neighbor_list(pos, 4.0, cell, [True] * 3, self_interaction=si,
                                   dtype=np.float64)
         assert np.array_equal(_canon_t(e, s), canonical(ei, sh))
+    # cells narrower than a third of the cutoff (the replicated-supercell listing): a
+    # triclinic cell with every axis short, and one short axis of a slab
+    tri = np.array([[4.1, 0.0, 0.0], [0.9, 3.8, 0.0], [-0.5, 0.7, 4.4]])
+    pos = rng.uniform(0, 1, (7, 3)) @ tri
+    for cut, pb in ((13.5, [True] * 3), (12.0, [True, False, True])):
+        for si in (False, True):
+            e, s = xa.build_neighbor_list(torch.tensor(pos, device=DEV, dtype=torch.float64), cut,
+                                          torch.tensor(tri, device=DEV), torch.tensor(pb),
+                                          self_interaction=si)
+            ei, sh, _ = neighbor_list(pos, cut, tri, pb, self_interaction=si, dtype=np.float64)
+            assert e.shape[1] == ei.shape[1] > 0
+            assert np.array_equal(_canon_t(e, s), canonical(ei, sh))
+            assert bool((e[1][1:] >= e[1][:-1]).all())
     # non-finite positions raise before any kernel runs
     bad = torch.tensor([[0.0, 0.0, float("nan")], [1.0, 0, 0]], device=DEV)
     with pytest.raises(ValueError, match="finite"):

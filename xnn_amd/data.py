@@ -158,6 +158,38 @@ def _check_finite(lo_hi: list) -> None:
         raise ValueError("the positions are not finite (an unstable simulation?)")
 
 
+def _supercell_reps(cell: Tensor, cutoff: float, pbc: Tensor) -> list[int]:
+    """Replicas per axis that bring every periodic interplanar spacing to at least a third
+    of the cutoff (the cell list reaches at most three cells along an axis)."""
+    c64 = cell.reshape(3, 3).detach().double().cpu()
+    spacing = 1.0 / torch.linalg.norm(torch.linalg.inv(c64).T, dim=1)
+    flags = pbc.reshape(-1).tolist()
+    return [max(1, int(math.ceil(cutoff / (3.0 * float(spacing[a])) * (1.0 + 1e-9))))
+            if bool(flags[a]) else 1 for a in range(3)]
+
+
+def _supercell_graph(pos: Tensor, cutoff: float, cell: Tensor, pbc: Tensor,
+                     self_interaction: bool, reps: list[int]) -> tuple[Tensor, Tensor]:
+    """The radius graph of a cell narrower than a third of the cutoff: list the edges of
+    the ``reps`` supercell whose receivers are the primitive atoms (replica 0, the first
+    rows of the receiver-grouped list) and map each sender replica ``m`` back to its atom
+    and shift: ``pos_sup[i + m n] = pos[i] + o_m @ cell`` and ``cell_sup = diag(reps) cell``
+    give ``shift = S_sup * reps - o_m`` for the same edge vector."""
+    dev = pos.device
+    n = pos.shape[0]
+    c = cell.reshape(3, 3).to(device=dev, dtype=pos.dtype)
+    offs = torch.tensor(list(itertools.product(*[range(r) for r in reps])), dtype=torch.long,
+                        device=dev)
+    pos_sup = (pos[None, :, :] + (offs.to(pos.dtype) @ c)[:, None, :]).reshape(-1, 3)
+    R = torch.tensor(reps, dtype=torch.long, device=dev)
+    cell_sup = c * R.to(pos.dtype)[:, None]
+    ei, sh = _radius_graph_cuda(pos_sup, cutoff, cell_sup, pbc, self_interaction)
+    keep = (ei[1] < n).nonzero()[:, 0]
+    src_sup = ei[0][keep]
+    edge_index = torch.stack([src_sup % n, ei[1][keep]])
+    return edge_index, sh[keep] * R - offs[src_sup // n]
+
+
 def _radius_graph_cuda(pos: Tensor, cutoff: float, cell: Optional[Tensor], pbc: Optional[Tensor],
                        self_interaction: bool) -> tuple[Tensor, Tensor]:
     lib = _lib.load()
@@ -165,6 +197,10 @@ def _radius_graph_cuda(pos: Tensor, cutoff: float, cell: Optional[Tensor], pbc: 
     pos = pos.contiguous()
     n = pos.shape[0]
     molecular = cell is None or pbc is None or not bool(pbc.any())
+    if not molecular and n > 0:
+        reps = _supercell_reps(cell, cutoff, pbc)
+        if max(reps) > 1:
+            return _supercell_graph(pos, cutoff, cell, pbc, self_interaction, reps)
     plan = _lib.GridPlan()
     pbc_host = (ctypes.c_int32 * 3)(*([0, 0, 0] if molecular else [int(bool(b)) for b in pbc.reshape(-1).tolist()]))
     if n == 0:

@@ -1,9 +1,9 @@
-"""D4 dispersion on the GPU: the coordination numbers, the polarizabilities and the
-two-body term as HIP kernels (the pair terms over lattice images), the charge model in
-PyTorch.
+"""D4 and D3 dispersion on the GPU: the coordination numbers, the polarizabilities, the
+two-body term (pair terms over lattice images) and the three-body ATM term (triangles of a
+radius graph) as HIP kernels, the charge model in PyTorch.
 
 Mirrors ``DFTD4`` / ``D4Dispersion`` (src/xnn/common/models/d4.py:266-1309,
-dispersion.py:667-878) for the two-body D4 energy:
+dispersion.py:667-878) and ``DFTD3`` / ``D3Dispersion`` (d3.py:483-1011):
 
 * coordination numbers (d4.py:552-591) -> :func:`d4_coordination` (HIP,
   differentiable once in positions and cell);
@@ -14,12 +14,16 @@ dispersion.py:667-878) for the two-body D4 energy:
   the alpha, d alpha / d cn and d alpha / d q of the reference's native d4_alpha);
 * the BJ-damped two-body energy with the quintic switch (d4.py:1044-1071,
   dispersion.py:42-67) -> :func:`d4_two_body` (HIP; gradients to positions, cell and
-  alpha, the outputs of the reference's native kernel run_d4).
+  alpha, the outputs of the reference's native kernel run_d4);
+* the ATM three-body energy (dispersion.py:124-222, 529-647; the reference's Triton
+  kernels dispersion_fast/atm.py) -> :func:`atm_energy` (HIP; gradients to the edge
+  vectors and the C6 factors), with C6 from the neutral-atom polarizabilities (D4) or the
+  reference-weighted C6 rows (D3).
 
-The three-body ATM term and the tail correction are not part of this path: ``s9``
-must be 0 here. Positions in Angstrom, energies returned in eV (hartree internally).
-No neighbor list is needed: the kernels walk every atom pair and lattice image within
-the cutoffs, so the graph may be built at the wrapped model's own cutoff.
+The tail correction is not part of this path. Positions in Angstrom, energies returned in
+eV (hartree internally). The pair kernels walk every atom pair and lattice image within
+the cutoffs and the ATM term builds its own radius graph at the three-body cutoff, so the
+graph may be built at the wrapped model's own cutoff.
 """
 from __future__ import annotations
 
@@ -460,18 +464,20 @@ class DFTD4(nn.Module):
     (defaults: the upstream 60 / 30 / 25 bohr for pair / CN / EEQ CN, d4.py:121-126)."""
 
     def __init__(self, tables: Dict[str, np.ndarray], s6: float = 1.0, s8: float = 1.20065498,
-                 a1: float = 0.40085597, a2: float = 5.02928789, s9: float = 0.0,
-                 ga: float = 3.0, gc: float = 2.0, wf: float = 6.0,
-                 cutoff_pair: float = 60.0 * BOHR, cutoff_cn: float = 30.0 * BOHR,
-                 cutoff_eeq_cn: float = 25.0 * BOHR, switch_width_pair: float = 0.0):
+                 a1: float = 0.40085597, a2: float = 5.02928789, s9: float = 1.0,
+                 alp: float = 16.0, ga: float = 3.0, gc: float = 2.0, wf: float = 6.0,
+                 cutoff_pair: float = 60.0 * BOHR, cutoff_triple: float = 40.0 * BOHR,
+                 cutoff_cn: float = 30.0 * BOHR, cutoff_eeq_cn: float = 25.0 * BOHR,
+                 switch_width_pair: float = 0.0, switch_width_triple: float = 0.0):
         super().__init__()
-        if s9 != 0.0:
-            raise NotImplementedError("the three-body ATM term is not part of this path; s9 = 0")
         self.s6, self.s8, self.a1, self.a2 = float(s6), float(s8), float(a1), float(a2)
+        self.s9, self.alp = float(s9), float(alp)
         self.ga, self.gc, self.wf = float(ga), float(gc), float(wf)
         self.cutoff_pair, self.cutoff_cn = float(cutoff_pair), float(cutoff_cn)
+        self.cutoff_triple = float(cutoff_triple)
         self.cutoff_eeq_cn = float(cutoff_eeq_cn)
         self.switch_width_pair = float(switch_width_pair)
+        self.switch_width_triple = float(switch_width_triple)
         self.cutoff = max(self.cutoff_pair, self.cutoff_cn, self.cutoff_eeq_cn)
         for k in TABLE_KEYS:
             v = tables[k]
@@ -647,24 +653,81 @@ class DFTD4(nn.Module):
                             species, batch32, node_ptr, images, self.r4r2[uniq].contiguous(),
                             params, max_atoms)
         from .ops import structure_sum_op
-        energy = structure_sum_op(e2, node_ptr, batch32)        # fixed order, float64
-        return {"node_energy": e2 * HARTREE, "energy": energy * HARTREE,
-                "energy_2body": energy * HARTREE, "coordination_numbers": cn, "charges": q,
+        e3 = torch.zeros_like(e2)
+        if self.s9 != 0.0:
+            e3 = self.three_body(zc, pos, cell64, pbc, n_atoms_h, cn, species, uniq)
+        energy_2 = structure_sum_op(e2, node_ptr, batch32)        # fixed order, float64
+        energy_3 = structure_sum_op(e3, node_ptr, batch32)
+        return {"node_energy": (e2 + e3) * HARTREE, "energy": (energy_2 + energy_3) * HARTREE,
+                "energy_2body": energy_2 * HARTREE, "energy_3body": energy_3 * HARTREE,
+                "coordination_numbers": cn, "charges": q,
                 "polarizabilities": alpha[:, 0], "dynamic_polarizabilities": alpha}
+
+    def three_body(self, z: Tensor, pos: Tensor, cell64: Optional[Tensor], pbc: Optional[Tensor],
+                   counts: List[int], cn: Tensor, species: Tensor, uniq: Tensor) -> Tensor:
+        """Per-atom ATM energies (hartree, d4.py:1268-1298): C6 from the polarizabilities
+        of the neutral atoms (q = 0), damping radii ``a1 sqrt(3 Q_A Q_B) + a2``, exponent
+        ``alp / 3``, edges of the radius graph within ``cutoff_triple``; the HIP
+        triplet kernels (:func:`atm_energy`)."""
+        alpha0 = self.polarizabilities(z, cn, torch.zeros_like(cn))
+        feat = alpha0 * torch.sqrt((3.0 / math.pi) * cp_weights(alpha0))
+        edge_index, vec = triple_graph(pos, cell64, pbc, counts, self.cutoff_triple)
+        q4 = self.r4r2[uniq]
+        table = self.a1 * torch.sqrt(3.0 * q4[:, None] * q4[None, :]) + self.a2
+        consts = ATMConstants(species, table, self.s9, self.alp / 3.0, self.cutoff_triple / BOHR,
+                              self.switch_width_triple / BOHR)
+        return atm_energy(edge_index, vec, feat, feat, consts, pos.shape[0])
 
     def forward(self, data) -> Dict[str, Tensor]:
         return self.evaluate(data.atomic_numbers, data.pos, data.cell, data.pbc, data.n_atoms,
                              data.total_charge)
 
 
-def c6_matrix(alpha_iw: Tensor) -> Tensor:
-    """(3/pi) sum_w cp_w alpha_i(w) alpha_j(w) for all pairs, (N, N) (d4.py:251-266)."""
+def cp_weights(like: Tensor) -> Tensor:
+    """Casimir-Polder trapezoid weights of the 23 imaginary frequencies (d4.py:130-141)."""
     f = [0.000001, 0.05, 0.1, 0.2, 0.3, 0.4, 0.5, 0.6, 0.7, 0.8, 0.9, 1.0,
          1.2, 1.4, 1.6, 1.8, 2.0, 2.5, 3.0, 4.0, 5.0, 7.5, 10.0]
     cp = [0.5 * ((f[k] - f[k - 1] if k > 0 else 0.0) + (f[k + 1] - f[k] if k < 22 else 0.0))
           for k in range(23)]
-    w = torch.tensor(cp, dtype=alpha_iw.dtype, device=alpha_iw.device)
-    return (3.0 / math.pi) * (alpha_iw * w) @ alpha_iw.T
+    return torch.tensor(cp, dtype=like.dtype, device=like.device)
+
+
+def c6_matrix(alpha_iw: Tensor) -> Tensor:
+    """(3/pi) sum_w cp_w alpha_i(w) alpha_j(w) for all pairs, (N, N) (d4.py:251-266)."""
+    return (3.0 / math.pi) * (alpha_iw * cp_weights(alpha_iw)) @ alpha_iw.T
+
+
+def triple_graph(pos: Tensor, cell64: Optional[Tensor], pbc: Optional[Tensor], counts: List[int],
+                 cutoff_aa: float) -> Tuple[Tensor, Tensor]:
+    """Edges ``[src, dst]`` within ``cutoff_aa`` of a batch (structures contiguous, HIP
+    radius graph per structure) and their vectors in bohr,
+    ``(pos[dst] - pos[src] + shift @ cell) / bohr``, differentiable in ``pos`` and the
+    cell (d4.py:1201-1207 with the in-cutoff mask of 1277)."""
+    from .data import build_neighbor_list
+    eis, vecs = [], []
+    s0 = 0
+    for b, n in enumerate(counts):
+        p = pos[s0:s0 + n]
+        cell_b = None if cell64 is None else cell64[b]
+        pbc_b = None
+        if cell_b is not None:
+            pbc_b = (torch.ones(3, dtype=torch.bool) if pbc is None
+                     else pbc.reshape(-1, 3)[b].detach().cpu().bool())
+            if not bool(pbc_b.any()):
+                cell_b = None
+        if cell_b is None:
+            ei, _ = build_neighbor_list(p.detach(), cutoff_aa)
+            v = p[ei[1]] - p[ei[0]]
+        else:
+            ei, sh = build_neighbor_list(p.detach(), cutoff_aa, cell_b.detach(), pbc_b)
+            v = p[ei[1]] - p[ei[0]] + sh.to(pos.dtype) @ cell_b
+        eis.append(ei + s0)
+        vecs.append(v)
+        s0 += n
+    if not eis:
+        return (torch.zeros((2, 0), dtype=torch.long, device=pos.device),
+                pos.new_zeros((0, 3)))
+    return torch.cat(eis, 1), torch.cat(vecs) / BOHR
 
 
 # --------------------------------------------------------------------------- potentials
@@ -723,6 +786,7 @@ class D4Dispersion(DispersionCorrection):
 # --------------------------------------------------------------------------- D3
 D3_DAMPINGS = {"bj": 0, "zero": 1, "mzero": 2, "op": 3}
 D3_KCN, D3_WF = 16.0, 4.0                                           # d3.py:464-465
+D3_RS9 = 4.0 / 3.0                  # ATM damping radii scale (d3.py:466)
 PBE0_D3BJ = {"s6": 1.0, "s8": 1.2177, "a1": 0.4145, "a2": 4.8593}   # d3.py:477-478
 PBE0_D3ZERO = {"s6": 1.0, "s8": 0.928, "rs6": 1.287, "rs8": 1.0}
 D3_TABLE_KEYS = ("z", "rcov", "r4r2", "rvdw", "nref", "refcn", "c6ref")
@@ -886,21 +950,24 @@ def _batch_layout(n_atoms: Tensor, dev) -> Tuple[List[int], Tensor, Tensor]:
 
 
 class DFTD3(nn.Module):
-    """Two-body D3 on the GPU (d3.py:483-960 without the ATM term): ``damping`` in
-    {"bj", "zero", "mzero", "op"}, PBE0 defaults, cutoffs in Angstrom (upstream 60 / 40
-    bohr for pairs / CN)."""
+    """D3 on the GPU (d3.py:483-960): ``damping`` in {"bj", "zero", "mzero", "op"}, PBE0
+    defaults, cutoffs in Angstrom (upstream 60 / 40 / 40 bohr for pairs / triples / CN);
+    ``s9 != 0`` adds the ATM term (zero damping with radii ``4/3 R0_AB``, exponent
+    ``(alp + 2) / 3``; the upstream default is off)."""
 
     def __init__(self, tables: Dict[str, np.ndarray], damping: str = "bj", s6: float = 1.0,
                  s8: Optional[float] = None, a1: float = 0.4145, a2: float = 4.8593,
                  rs6: float = 1.287, rs8: float = 1.0, alp: float = 14.0, bet: float = 0.0,
                  s9: float = 0.0, cutoff_pair: float = 60.0 * BOHR,
-                 cutoff_cn: float = 40.0 * BOHR, switch_width_pair: float = 0.0):
+                 cutoff_triple: float = 40.0 * BOHR, cutoff_cn: float = 40.0 * BOHR,
+                 switch_width_pair: float = 0.0, switch_width_triple: float = 0.0):
         super().__init__()
         damping = {"rational": "bj", "d3bj": "bj"}.get(damping.lower(), damping.lower())
         if damping not in D3_DAMPINGS:
             raise ValueError(f"damping must be one of {tuple(D3_DAMPINGS)}, got {damping!r}")
-        if s9 != 0.0:
-            raise NotImplementedError("the three-body ATM term is not part of this path; s9 = 0")
+        self.s9 = float(s9)
+        self.cutoff_triple = float(cutoff_triple)
+        self.switch_width_triple = float(switch_width_triple)
         if s8 is None:
             s8 = PBE0_D3BJ["s8"] if damping in ("bj", "op") else PBE0_D3ZERO["s8"]
         self.damping = damping
@@ -967,9 +1034,42 @@ class DFTD3(nn.Module):
         e2 = d3_two_body_op(pos.contiguous(), cell64, w, species, batch32, node_ptr, images,
                             self.r4r2, self.rvdw.contiguous(), self.c6pair, params, max_atoms)
         from .ops import structure_sum_op
-        energy = structure_sum_op(e2, node_ptr, batch32)
-        return {"node_energy": e2 * HARTREE, "energy": energy * HARTREE,
-                "energy_2body": energy * HARTREE, "coordination_numbers": cn, "weights": w}
+        e3 = torch.zeros_like(e2)
+        if self.s9 != 0.0:
+            e3 = self.three_body(s.to(dev), w, pos, cell64, pbc, counts)
+        energy_2 = structure_sum_op(e2, node_ptr, batch32)
+        energy_3 = structure_sum_op(e3, node_ptr, batch32)
+        return {"node_energy": (e2 + e3) * HARTREE, "energy": (energy_2 + energy_3) * HARTREE,
+                "energy_2body": energy_2 * HARTREE, "energy_3body": energy_3 * HARTREE,
+                "coordination_numbers": cn, "weights": w}
+
+    def c6_factors(self, s: Tensor, w: Tensor) -> Tuple[Tensor, Tensor, Tensor, Tensor]:
+        """The pair C6 ``W_i^T C6ref[Z_i, Z_j] W_j`` (d3.py:651-674) as ``<f_i, g_j>`` over
+        the reference slots of the elements present (d3.py:840-859): ``f_i[p, b] =
+        sum_a W_i[a] C6ref[a, b, Z_i, E_p]`` and ``g_j[p, b] = W_j[b]`` at the atom's own
+        element ``E_p``; returns ``f, g`` (N, K), the present elements and each atom's
+        index among them."""
+        uniq, spec = torch.unique(s, return_inverse=True)
+        block = self.c6ref[:, :, s][:, :, :, uniq]                   # (7, 7, N, P)
+        f = torch.einsum("na,abnp->npb", w, block)                    # (N, P, 7)
+        own = torch.nn.functional.one_hot(spec, uniq.shape[0]).to(w.dtype)
+        g = own[:, :, None] * w[:, None, :]                           # (N, P, 7)
+        slots = (torch.arange(7, device=s.device)[None, :] < self.nref[uniq][:, None]).reshape(-1)
+        return f.reshape(s.shape[0], -1)[:, slots], g.reshape(s.shape[0], -1)[:, slots], uniq, spec
+
+    def three_body(self, s: Tensor, w: Tensor, pos: Tensor, cell64: Optional[Tensor],
+                   pbc: Optional[Tensor], counts: List[int]) -> Tensor:
+        """Per-atom ATM energies (hartree, d3.py:916-936) on the HIP triplet kernels."""
+        f, g, uniq, spec = self.c6_factors(s, w)
+        if f.shape[1] > 28:
+            raise NotImplementedError(
+                f"the D3 ATM term takes at most 28 reference slots over the elements present "
+                f"(these have {f.shape[1]}); set s9 = 0")
+        edge_index, vec = triple_graph(pos, cell64, pbc, counts, self.cutoff_triple)
+        table = D3_RS9 * self.rvdw[uniq][:, uniq]
+        consts = ATMConstants(spec, table, self.s9, (self.alp + 2.0) / 3.0,
+                              self.cutoff_triple / BOHR, self.switch_width_triple / BOHR)
+        return atm_energy(edge_index, vec, f.contiguous(), g.contiguous(), consts, pos.shape[0])
 
     def forward(self, data) -> Dict[str, Tensor]:
         return self.evaluate(data.atomic_numbers, data.pos, data.cell, data.pbc, data.n_atoms)
