@@ -21,6 +21,7 @@ from __future__ import annotations
 
 import argparse
 import copy
+import ctypes
 import json
 import math
 import os
@@ -31,6 +32,7 @@ import numpy as np
 import torch
 
 HBM_PEAK_GBS = 8000.0
+ctypes_i64 = ctypes.c_int64
 ROOT = os.path.dirname(os.path.abspath(__file__))
 TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "hbm_traffic_message_kernels_water_box.md")
 
@@ -527,13 +529,147 @@ def bench_d3(steps: int, warmup: int, cpu: bool = True) -> dict:
     return result
 
 
+# ATM float64 flops (FMA = 2, division = square root = exp = log = 1) per edge pair tested
+# by the distinct-triangle walk (third side: 3 differences + squared norm = 8) and per kept
+# triangle: forward 82 more (C6_jk over the 23 frequencies 46, damping radius 2, 1/r^3 and
+# powers 6, (R0/r^3)^alp3 4, damping 3, angular factor 11, C9 3, energy 5, sum 1, switch
+# off); backward 235 (forward + the three squared-side derivatives 55, vector and C6
+# gradients of both edges 16, factor gradients of both atoms 2 x 46 + the slot products)
+ATM_FLOPS = {"xnn_atm_energy": lambda P, M: 8 * P + 82 * M,
+             "xnn_atm_energy_backward": lambda P, M: 8 * P + 235 * M}
+
+
+def cpu_baseline_atm(ei: np.ndarray, vec: np.ndarray, feat: np.ndarray, species: np.ndarray,
+                     table: np.ndarray, consts, n_atoms: int, centers: int = 2,
+                     min_seconds: float = 10.0) -> dict:
+    """The oracle's ATM (every corner visited, PyTorch on the CPU, float64) with its
+    gradients in the edge vectors and the C6 factors, over the triangles at the first
+    ``centers`` atoms (all pairs of their edges), repeated until about ``min_seconds``."""
+    import oracle.d4 as D
+    sel = np.isin(ei[1], np.arange(centers))
+    e_t = torch.as_tensor(ei[:, sel])
+    v_t = torch.as_tensor(vec[sel])
+    f_t = torch.as_tensor(feat)
+    sp, tab = torch.as_tensor(species).long(), torch.as_tensor(table)
+    counts = np.bincount(ei[1][sel], minlength=centers)[:centers]
+    visits = int(sum(int(m) * (int(m) - 1) // 2 for m in counts))
+    reps, dt = 0, 0.0
+    t0 = time.perf_counter()
+    while reps < 20 and (reps == 0 or dt < min_seconds):
+        v = v_t.clone().requires_grad_(True)
+        f = f_t.clone().requires_grad_(True)
+        e = D.atm_edges(e_t, v, f, f, sp, tab, consts.s9, consts.alp3, consts.cutoff,
+                        consts.width, n_atoms)
+        torch.autograd.grad(e.sum(), [v, f])
+        reps += 1
+        dt = time.perf_counter() - t0
+    return {"value": reps * visits / dt, "unit": "triangle visits/s",
+            "cores": torch.get_num_threads(), "kind": "port", "seconds": round(dt, 2),
+            "steps": reps,
+            "sample": f"{reps} x the ATM energy + gradients (edge vectors, C6 factors) of the "
+                      f"{visits} edge pairs at the first {centers} of {n_atoms} centers "
+                      f"(every corner visited, third side tested), oracle PyTorch-CPU "
+                      f"float64, torch threads={torch.get_num_threads()}"}
+
+
+def bench_atm(steps: int, warmup: int, cpu: bool = True) -> dict:
+    """D4 ATM three-body energy + gradients on the 5,000-atom organic box (36.8 A cell) at
+    the upstream three-body cutoff (40 bohr, sharp): the triplet plan, the energy kernels
+    and the backward per step, with the edge list (HIP radius graph at 40 bohr), its
+    vectors and the neutral-atom C6 factors resident in HBM (the graph is timed apart)."""
+    import xnn_amd.dispersion as XD
+    from xnn_amd import _lib, synthetic
+    dev = torch.device("cuda:0")
+    s = synthetic.organic_box(seed=0)
+    tables = XD.load_d4_tables(os.path.join(ROOT, "tests", "golden", "d4_tables_hcnoar.npz"))
+    model = XD.DFTD4(tables).to(dev)
+    z = torch.tensor(s.numbers, device=dev)
+    pos = torch.tensor(s.pos, dtype=torch.float64, device=dev)
+    cell = torch.tensor(s.cell, dtype=torch.float64, device=dev)[None]
+    pbc = torch.ones((1, 3), dtype=torch.bool)
+    N = len(s.numbers)
+    with torch.no_grad():
+        out = model.evaluate(z, pos, cell, pbc, torch.tensor([N]),
+                             charges=torch.zeros(N, dtype=torch.float64, device=dev))
+        cn = out["coordination_numbers"]
+        uniq, species = torch.unique(z, return_inverse=True)
+        alpha0 = model.polarizabilities(z, cn, torch.zeros_like(cn))
+        feat = (alpha0 * torch.sqrt((3.0 / math.pi) * XD.cp_weights(alpha0))).contiguous()
+        q4 = model.r4r2[uniq]
+        table = model.a1 * torch.sqrt(3.0 * q4[:, None] * q4[None, :]) + model.a2
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    ei, vec = XD.triple_graph(pos, cell, pbc, [N], model.cutoff_triple)
+    torch.cuda.synchronize()
+    graph_ms = (time.perf_counter() - t0) * 1e3
+    vec = vec.contiguous()
+    consts = XD.ATMConstants(species.to(torch.int32), table, model.s9, model.alp / 3.0,
+                             model.cutoff_triple / XD.BOHR, model.switch_width_triple / XD.BOHR)
+
+    def step():
+        v = vec.detach().requires_grad_(True)
+        f = feat.detach().requires_grad_(True)
+        e = XD.atm_energy(ei, v, f, f, consts, N)
+        gv, gf = torch.autograd.grad(e.sum(), [v, f])
+        return e, gv, gf
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        e, gv, gf = step()
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) / steps * 1e3
+    kernels = ["xnn_atm_plan", "xnn_atm_energy", "xnn_atm_energy_backward"]
+    _lib.timed.clear()
+    _lib.time_launches(*kernels)
+    for _ in range(steps):
+        step()
+    torch.cuda.synchronize()
+    kernel_us = {k: float(np.mean([a.elapsed_time(b) * 1e3 for a, b in v]))
+                 for k, v in _lib.timed.items() if v}
+    _lib.timed.clear()
+    plan, info = XD.atm_plan(ei, N)
+    counts = (ctypes_i64 * 3)()
+    _lib.call("xnn_atm_count", _lib.ptr(plan), int(ei.shape[1]), N, info[0], _lib.ptr(vec),
+              consts.cutoff, counts, _lib.stream(dev))
+    tested, kept, repeated = int(counts[0]), int(counts[1]), int(counts[2])
+    triangles = kept + repeated
+    dominant = max((k for k in ATM_FLOPS if k in kernel_us), key=lambda k: kernel_us[k])
+    flops = ATM_FLOPS[dominant](tested, triangles)
+    achieved = flops / (kernel_us[dominant] * 1e-6) / 1e12
+    roofline = {"bound": "fp64", "kernel": dominant, "achieved": round(achieved, 2),
+                "peak": FP64_PEAK_TFLOPS, "unit": "TFLOP/s",
+                "frac": round(achieved / FP64_PEAK_TFLOPS, 4), "traffic": None,
+                "algorithmic_flops": flops, "mean_launch_us": round(kernel_us[dominant], 2),
+                "timing": "eager step, HIP events around the entry point on the launch stream"}
+    result = {"metric": "D4 ATM triangles/s, energy+gradients, 5000-atom organic box",
+              "value": triangles / (ms * 1e-3), "unit": "triangles/s", "n_gpus": 1,
+              "steps": steps, "warmup": warmup, "ms_per_step": ms, "higher_is_better": True,
+              "scaling": "weak", "vs_baseline": None, "dtype": "f64",
+              "data": "synthetic (seeded generator)",
+              "config": {"workload": "d4_atm_organic_box_5000_atoms", "atoms": N,
+                         "edges": int(ei.shape[1]), "cutoff_triple_bohr": 40.0,
+                         "edge_pairs_tested": tested, "distinct_triangles": kept,
+                         "repeated_atom_visits": repeated, "graph_ms": round(graph_ms, 2),
+                         "energy_3body_hartree": float(e.sum()),
+                         "kernel_mean_us": {k: round(v, 2) for k, v in kernel_us.items()}},
+              "roofline": roofline}
+    if cpu:
+        result["cpu_baseline"] = cpu_baseline_atm(
+            ei.cpu().numpy(), vec.cpu().numpy(), feat.cpu().numpy(),
+            species.cpu().numpy(), table.cpu().numpy(), consts, N)
+    return result
+
+
 def main() -> None:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--config", default="water",
-                    choices=["water", "argon", "ragged", "d4", "d3"])
+                    choices=["water", "argon", "ragged", "d4", "d3", "atm"])
     ap.add_argument("--graph", action=argparse.BooleanOptionalAction, default=True,
                     help="time replays of the step captured as one HIP graph")
     ap.add_argument("--cpu-edges", type=int, default=480_000,
@@ -561,6 +697,9 @@ def main() -> None:
         return
     if args.config == "d3":
         print(json.dumps(bench_d3(args.steps, args.warmup, cpu=args.cpu_edges > 0)), flush=True)
+        return
+    if args.config == "atm":
+        print(json.dumps(bench_atm(args.steps, args.warmup, cpu=args.cpu_edges > 0)), flush=True)
         return
     device = torch.device("cuda:0")
     torch.cuda.set_device(device)

@@ -581,6 +581,13 @@ int xnn_atm_energy_backward(const void* plan, int64_t n_edges, int64_t n_atoms,
                             double* grad_vec, double* grad_fa, double* grad_fb, void* work,
                             size_t work_bytes, xnn_stream_t stream);
 
+/* Measurement, no counterpart in the reference: counts[0] = edge pairs the distinct-
+ * triangle walk tests, counts[1] = distinct triangles it keeps (third side within the
+ * cutoff), counts[2] = repeated-atom triangle visits, for the planned edges and their
+ * vectors (bohr). Synchronous; for roofline figures (flops per triangle x triangles). */
+int xnn_atm_count(const void* plan, int64_t n_edges, int64_t n_atoms, int64_t max_tiles,
+                  const double* edge_vec, double cutoff, int64_t* counts, xnn_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

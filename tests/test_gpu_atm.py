@@ -4,8 +4,10 @@ dispersion.py:124-222), energies and first derivatives, float64.
 
 Systems as in the reference's tests (tests/common/test_dispersion_fast.py:21-70): rigid
 water boxes on a 3.104 A grid with a 6 A three-body cutoff and a 1 A switch; the 3^3 cell
-(9.3 A) is narrower than twice the cutoff, so it has self-image triangles, the 4^3 cell
-(12.4 A) has none, and the cluster has no cell. Tolerance: 1e-11 relative to the largest
+(9.3 A) is narrower than twice the cutoff, so it has repeated-atom triangles (all with a
+third side beyond the cutoff), the 4^3 cell (12.4 A) has none, and the cluster has no
+cell; the 2^3 cell (6.2 A) with a 7 A cutoff has atoms that see their own images and
+repeated-atom triangles that count. Tolerance: 1e-11 relative to the largest
 value (the reference's fast-path tolerance for float64, test_dispersion_fast.py:102-115).
 """
 import math
@@ -38,8 +40,12 @@ def _water_box(n_side, periodic, seed=3):
     return np.array(pos), cell, [8, 1, 1] * n_side ** 3
 
 
-def _case(system, k=23, cutoff_aa=6.0, width_aa=1.0, seed=0):
-    n_side, periodic = {"small_cell": (3, True), "cell": (4, True), "cluster": (3, False)}[system]
+SYSTEMS = {"small_cell": (3, True, 6.0), "cell": (4, True, 6.0), "cluster": (3, False, 6.0),
+           "tiny_cell": (2, True, 7.0)}
+
+
+def _case(system, k=23, width_aa=1.0, seed=0):
+    n_side, periodic, cutoff_aa = SYSTEMS[system]
     pos, cell, z = _water_box(n_side, periodic)
     dst, src, sh = D.pair_images(pos, cell, cutoff_aa)
     perm = torch.randperm(len(dst), generator=torch.Generator().manual_seed(seed))
@@ -111,7 +117,7 @@ def _hip(c, same=False, s9=1.0, alp3=16.0 / 3.0, go=None):
     return out
 
 
-@pytest.mark.parametrize("system", ["small_cell", "cell", "cluster"])
+@pytest.mark.parametrize("system", list(SYSTEMS))
 @pytest.mark.parametrize("k,width_aa", [(23, 1.0), (28, 0.0), (7, 1.0)])
 def test_atm_matches_the_oracle(system, k, width_aa):
     print(f"[atm] {system} k={k} width={width_aa}", flush=True)
@@ -162,3 +168,44 @@ def test_atm_edge_cases():
     bad = torch.tensor([[0, 5], [1, 0]], device=dev)
     with pytest.raises(RuntimeError, match="outside"):
         XD.atm_energy(bad, v, f, f, consts, 3)
+
+
+def test_atm_counts_match_a_direct_enumeration():
+    """xnn_atm_count (the roofline's triangle counts): pairs of edges to larger-index
+    neighbors per center, the distinct triangles among them with the third side within
+    the cutoff, and the repeated-atom visits, against a direct enumeration on the CPU."""
+    import ctypes
+    from xnn_amd import _lib
+    from xnn_amd import dispersion as XD
+    c = _case("tiny_cell", k=23)
+    pos, cell, vec = _geometry(c, "cpu")
+    vec = vec.detach()
+    n, ei = c["n"], c["ei"]
+    key = ei[1] * n + ei[0]
+    order = torch.argsort(key, stable=True)
+    src, dst, v = ei[0][order].numpy(), ei[1][order], vec[order].numpy()
+    lo = torch.searchsorted(dst, torch.arange(n + 1))
+    cut2 = c["cutoff"] ** 2
+    tested = kept = repeated = 0
+    for cc in range(n):
+        l, h = int(lo[cc]), int(lo[cc + 1])
+        row = src[l:h]
+        up = [p for p in range(l, h) if int(src[p]) > cc]
+        tested += len(up) * (len(up) - 1) // 2
+        for ia, a in enumerate(up):
+            for b in up[ia + 1:]:
+                w2 = float(((v[a] - v[b]) ** 2).sum())
+                kept += int(src[a] != src[b] and 2.220446049250313e-16 < w2 <= cut2)
+        for a in range(l, h):
+            for b in range(a + 1, h):
+                if src[a] == cc or src[b] == cc or src[a] == src[b]:
+                    w2 = float(((v[a] - v[b]) ** 2).sum())
+                    repeated += int(2.220446049250313e-16 < w2 <= cut2)
+    dev = torch.device("cuda:0")
+    plan, info = XD.atm_plan(ei.to(dev), n)
+    counts = (ctypes.c_int64 * 3)()
+    vd = vec.to(dev).contiguous()
+    _lib.call("xnn_atm_count", _lib.ptr(plan), int(ei.shape[1]), n, info[0], _lib.ptr(vd),
+              c["cutoff"], counts, _lib.stream(dev))
+    assert (counts[0], counts[1], counts[2]) == (tested, kept, repeated)
+    assert repeated > 0 and kept > 0

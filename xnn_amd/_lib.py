@@ -115,6 +115,7 @@ _SIGNATURES = {
     "xnn_atm_plan_size": [i64, i64, ctypes.POINTER(sz)],
     "xnn_atm_plan": [vp, i64, i64, vp, sz, ctypes.POINTER(i64), vp],
     "xnn_atm_work_size": [i64, i64, i32, i32, ctypes.POINTER(sz)],
+    "xnn_atm_count": [vp, i64, i64, i64, vp, dbl, ctypes.POINTER(i64), vp],
     "xnn_atm_energy": [vp, i64, i64, i64, i64, vp, vp, vp, i32, vp, vp, i32,
                        ctypes.POINTER(AtmParams), vp, vp, sz, vp],
     "xnn_atm_energy_backward": [vp, i64, i64, i64, i64, vp, vp, vp, i32, vp, vp, i32,

@@ -71,7 +71,8 @@ struct AtmConst {
 static size_t atm_align(size_t x) { return (x + 255) & ~(size_t)255; }
 
 struct AtmPlanLayout {
-  size_t keys, perm, nbr, lo, lo1, flag, stats, keys_in, vals_in, cub, cub_bytes, total;
+  size_t keys, perm, nbr, ctr, lo, lo1, flag, stats, by_src, lo_src, keys_in, vals_in, keys2,
+      cub, cub_bytes, total;
 };
 
 static int atm_end_bit(int64_t n) {
@@ -87,12 +88,16 @@ static AtmPlanLayout atm_plan_layout(int64_t E, int64_t N) {
   L.keys = at; at += atm_align(sizeof(uint64_t) * std::max<int64_t>(E, 1));
   L.perm = at; at += atm_align(sizeof(int32_t) * std::max<int64_t>(E, 1));
   L.nbr = at; at += atm_align(sizeof(int32_t) * std::max<int64_t>(E, 1));
+  L.ctr = at; at += atm_align(sizeof(int32_t) * std::max<int64_t>(E, 1));
   L.lo = at; at += atm_align(sizeof(int32_t) * (N + 1));
   L.lo1 = at; at += atm_align(sizeof(int32_t) * std::max<int64_t>(N, 1));
   L.flag = at; at += atm_align(sizeof(int32_t) * std::max<int64_t>(N, 1));
   L.stats = at; at += atm_align(sizeof(int32_t) * 4);
+  L.by_src = at; at += atm_align(sizeof(int32_t) * std::max<int64_t>(E, 1));
+  L.lo_src = at; at += atm_align(sizeof(int32_t) * (N + 1));
   L.keys_in = at; at += atm_align(sizeof(uint64_t) * std::max<int64_t>(E, 1));
   L.vals_in = at; at += atm_align(sizeof(int32_t) * std::max<int64_t>(E, 1));
+  L.keys2 = at; at += atm_align(sizeof(uint64_t) * std::max<int64_t>(E, 1));
   size_t cub_bytes = 0;
   (void)hipcub::DeviceRadixSort::SortPairs(nullptr, cub_bytes, (uint64_t*)nullptr,
                                            (uint64_t*)nullptr, (int32_t*)nullptr,
@@ -174,13 +179,19 @@ __device__ inline int64_t atm_lower_bound(const uint64_t* __restrict__ keys, int
 // neighbor of every sorted edge; a center with two edges to images of one neighbor has
 // repeated-atom triangles
 __global__ void atm_neighbors_kernel(const uint64_t* __restrict__ keys, int64_t E, int64_t N,
-                                     int32_t* __restrict__ nbr, int32_t* __restrict__ flag,
-                                     int32_t* __restrict__ stats) {
+                                     int32_t* __restrict__ nbr, int32_t* __restrict__ ctr,
+                                     uint64_t* __restrict__ keys2, int32_t* __restrict__ vals2,
+                                     int32_t* __restrict__ flag, int32_t* __restrict__ stats) {
   const int64_t p = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (p >= E) return;
   const uint64_t k = keys[p];
   const uint64_t top = (uint64_t)N * (uint64_t)N;
-  nbr[p] = k < top ? (int32_t)(k % (uint64_t)N) : 0;
+  const uint64_t cj = k < top ? k / (uint64_t)N : 0, jj = k < top ? k % (uint64_t)N : 0;
+  nbr[p] = (int32_t)jj;
+  ctr[p] = (int32_t)cj;
+  // (neighbor, center) keys: the by-source order of the backward's center sides
+  keys2[p] = k < top ? jj * (uint64_t)N + cj : top;
+  vals2[p] = (int32_t)p;
   if (k < top && p + 1 < E && keys[p + 1] == k) {
     flag[k / (uint64_t)N] = 1;
     stats[1] = 1;
@@ -207,6 +218,14 @@ __global__ void atm_rows_kernel(const uint64_t* __restrict__ keys, int64_t E, in
   }
   const int64_t n_up = h - u;
   if (n_up >= 2) atomicMax(&stats[0], (int32_t)((n_up + kAtmTile - 1) / kAtmTile));
+}
+
+// lo_src[j]: first by-source position of neighbor j
+__global__ void atm_src_rows_kernel(const uint64_t* __restrict__ keys2, int64_t E, int64_t N,
+                                    int32_t* __restrict__ lo_src) {
+  const int64_t j = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (j > N) return;
+  lo_src[j] = (int32_t)atm_lower_bound(keys2, E, (uint64_t)j * (uint64_t)N);
 }
 
 // ------------------------------------------------------------------------------ records
@@ -262,10 +281,25 @@ __global__ void atm_edges_kernel(const uint64_t* __restrict__ keys,
 }
 
 // ------------------------------------------------------------------------------ triangle
+// q^(16/3), the damping power at the upstream exponent alp / 3 = 16 / 3 (D4: alp = 16; D3:
+// (alp + 2) / 3 with alp = 14): q^6 z^2 with z = q^(-1/3) from the single-precision estimate
+// 2^(-log2(q) / 3) refined by two Newton steps z <- z (4 - q z^3) / 3 (quadratic: about
+// 2e-7, then 1e-13, then rounding); outside [1e-30, 1e30], beyond the estimate's range,
+// the general power.
+__device__ __forceinline__ double atm_pow_16_3(double q) {
+  if (!(q > 1e-30 && q < 1e30)) return exp((16.0 / 3.0) * log(q));
+  double z = (double)__builtin_amdgcn_exp2f(-0.333333343f * __builtin_amdgcn_logf((float)q));
+  z = z * fma(-q * z, z * z, 4.0) * (1.0 / 3.0);
+  z = z * fma(-q * z, z * z, 4.0) * (1.0 / 3.0);
+  const double q2 = q * q;
+  return q2 * q2 * q2 * (z * z);
+}
+
 // The energy of one triangle visit (weight * s9/3 * C9 * angular * damping * switches)
 // and, in the backward, its derivatives in the squared sides x = r_cj^2, y = r_ck^2,
-// w = r_jk^2 (dispersion.py:183-222; closed form of dispersion.py:413-510).
-template <bool SWITCH, bool BWD>
+// w = r_jk^2 (dispersion.py:183-222; closed form of dispersion.py:413-510). P16: the
+// exponent is 16/3.
+template <bool SWITCH, bool BWD, bool P16>
 __device__ __forceinline__ void atm_triangle(const AtmConst& kc, double x, double y, double w,
                                              double ix, double iy, double c6abs, double r0,
                                              double swa, double swb, double dswa, double dswb,
@@ -275,7 +309,8 @@ __device__ __forceinline__ void atm_triangle(const AtmConst& kc, double x, doubl
   const double s2 = s * s;
   const double s3 = s2 * s;
   const double s5 = s3 * s2;
-  const double t = exp(kc.alp3 * log(r0 * s));   // (R0 / (r_cj r_ck r_jk))^alp3
+  // (R0 / (r_cj r_ck r_jk))^alp3
+  const double t = P16 ? atm_pow_16_3(r0 * s) : exp(kc.alp3 * log(r0 * s));
   const double damp = rcp_nr(fma(6.0, t, 1.0));
   const double f1 = x + w - y, f2 = x - w + y, f3 = w + y - x;
   const double nn = f1 * f2 * f3;
@@ -308,34 +343,94 @@ __device__ __forceinline__ void atm_triangle(const AtmConst& kc, double x, doubl
   }
 }
 
-__device__ __forceinline__ double atm_wave_sum(double v) {
-#pragma unroll
-  for (int o = kWave / 2; o > 0; o >>= 1) v += __shfl_xor(v, o);
+// ------------------------------------------------------------------------------ exchanges
+// Cross-lane exchanges of doubles: ds_bpermute with byte addresses computed once per
+// kernel (lane ^ 32, 16, 8, 4), and DPP quad permutations for lane ^ 2 and lane ^ 1.
+struct AtmLanes {
+  int a32, a16, a8, a4;
+};
+
+__device__ __forceinline__ AtmLanes atm_lanes(int lane) {
+  return {(lane ^ 32) << 2, (lane ^ 16) << 2, (lane ^ 8) << 2, (lane ^ 4) << 2};
+}
+
+__device__ __forceinline__ double atm_bperm(double v, int addr) {
+  const int lo = __builtin_amdgcn_ds_bpermute(addr, __double2loint(v));
+  const int hi = __builtin_amdgcn_ds_bpermute(addr, __double2hiint(v));
+  return __hiloint2double(hi, lo);
+}
+
+constexpr int kDppXor1 = 0xB1;   // quad_perm [1, 0, 3, 2]
+constexpr int kDppXor2 = 0x4E;   // quad_perm [2, 3, 0, 1]
+
+template <int CTRL>
+__device__ __forceinline__ double atm_dpp(double v) {
+  const int lo = __builtin_amdgcn_mov_dpp(__double2loint(v), CTRL, 0xF, 0xF, false);
+  const int hi = __builtin_amdgcn_mov_dpp(__double2hiint(v), CTRL, 0xF, 0xF, false);
+  return __hiloint2double(hi, lo);
+}
+
+// the wave-wide sum in every lane (a fixed butterfly: every lane gets the same bits)
+__device__ __forceinline__ double atm_wave_sum(double v, const AtmLanes& L) {
+  v += atm_bperm(v, L.a32);
+  v += atm_bperm(v, L.a16);
+  v += atm_bperm(v, L.a8);
+  v += atm_bperm(v, L.a4);
+  v += atm_dpp<kDppXor2>(v);
+  v += atm_dpp<kDppXor1>(v);
   return v;
 }
 
-// One level of the transposing reduction: lanes whose bit 2H is set keep the upper H of
-// their 2H partial sums and send the lower H to their partner, the others the reverse.
-template <int H>
-__device__ __forceinline__ void atm_fold(double* p, int lane) {
-  const bool up = (lane & (2 * H)) != 0;
+// The wave-wide sums of the 32 products g * f[s] (f zero beyond its length): lanes 2s and
+// 2s + 1 return the total of slot s. Each lane holds its row permuted, fp[i] = f[i ^ (lane
+// >> 1)], so that at every halving the lane keeps its first half and receives its
+// partner's second half, which holds the same slots: 31 + 1 exchanges and no selects.
+// fp[i][lane] lives in LDS (a column per lane: conflict-free, and 64 registers fewer).
+__device__ __forceinline__ double atm_fold32(const double (*fp)[kWave], int lane, double g,
+                                             const AtmLanes& L) {
+  double p[16];
 #pragma unroll
-  for (int i = 0; i < H; ++i) {
-    const double send = up ? p[i] : p[i + H];
-    const double keep = up ? p[i + H] : p[i];
-    p[i] = keep + __shfl_xor(send, 2 * H);
-  }
+  for (int i = 0; i < 16; ++i) p[i] = g * fp[i][lane] + atm_bperm(g * fp[i + 16][lane], L.a32);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) p[i] += atm_bperm(p[i + 8], L.a16);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) p[i] += atm_bperm(p[i + 4], L.a8);
+#pragma unroll
+  for (int i = 0; i < 2; ++i) p[i] += atm_bperm(p[i + 2], L.a4);
+  p[0] += atm_dpp<kDppXor2>(p[1]);
+  return p[0] + atm_dpp<kDppXor1>(p[0]);
 }
 
-// The wave-wide sums of 32 per-lane values: lanes 2s and 2s + 1 return the total of slot
-// s. 31 + 1 exchanges instead of 32 separate butterflies of 6.
-__device__ __forceinline__ double atm_reduce32(double* p, int lane) {
-  atm_fold<16>(p, lane);
-  atm_fold<8>(p, lane);
-  atm_fold<4>(p, lane);
-  atm_fold<2>(p, lane);
-  atm_fold<1>(p, lane);
-  return p[0] + __shfl_xor(p[0], 1);
+// The wave-wide sums of four per-lane values: lanes 16 s .. 16 s + 15 return slot s.
+__device__ __forceinline__ double atm_fold4(double s0, double s1, double s2, double s3,
+                                            int lane, const AtmLanes& L) {
+  const bool u5 = (lane & 32) != 0, u4 = (lane & 16) != 0;
+  const double k0 = (u5 ? s2 : s0) + atm_bperm(u5 ? s0 : s2, L.a32);
+  const double k1 = (u5 ? s3 : s1) + atm_bperm(u5 ? s1 : s3, L.a32);
+  double v = (u4 ? k1 : k0) + atm_bperm(u4 ? k0 : k1, L.a16);
+  v += atm_bperm(v, L.a8);
+  v += atm_bperm(v, L.a4);
+  v += atm_dpp<kDppXor2>(v);
+  return v + atm_dpp<kDppXor1>(v);
+}
+
+// Per-wave ring of the energies of the last kAtmRing walked edges b (one row per b, one
+// column per lane) and their atoms k: the wave sums them 16 rows at a time, a quarter row
+// per lane, instead of one butterfly per b.
+constexpr int kAtmRing = 16;
+
+__device__ __forceinline__ void atm_ring_flush(double (*ring)[kWave + 1], const int32_t* ring_k,
+                                               int n, int lane, const AtmLanes& L,
+                                               double* __restrict__ energy) {
+  wave_sync();
+  const int r = lane & (kAtmRing - 1), q = lane >> 4;
+  double v = 0.0;
+#pragma unroll
+  for (int i = 0; i < kWave / 4; ++i) v += ring[r][q * (kWave / 4) + i];
+  v += atm_bperm(v, L.a16);
+  v += atm_bperm(v, L.a32);
+  if (q == 0 && r < n) unsafeAtomicAdd(&energy[ring_k[r]], v);
+  wave_sync();
 }
 
 __device__ __forceinline__ void atm_stage_table(const double* __restrict__ table, int S,
@@ -348,7 +443,7 @@ __device__ __forceinline__ void atm_stage_table(const double* __restrict__ table
 // Distinct triangles from their smallest corner. Forward: energy[c], energy[j],
 // energy[k] += e. Backward (weights go_c + go_j + go_k): gs[edge] += (dE/dv, dE/dC6) for
 // both edges, gfa[j] += dE/dC6_jk fb[k], gfb[k] += dE/dC6_jk fa[j].
-template <int KP, bool SWITCH, bool BWD>
+template <int KP, bool SWITCH, bool BWD, bool P16>
 __global__ __launch_bounds__(kAtmWaves * kWave) void atm_upper_kernel(
     const AtmEdge* __restrict__ rec, const int32_t* __restrict__ lo,
     const int32_t* __restrict__ lo1, int64_t N, int64_t n_groups,
@@ -357,14 +452,21 @@ __global__ __launch_bounds__(kAtmWaves * kWave) void atm_upper_kernel(
     const double* __restrict__ go, double* __restrict__ gs, double* __restrict__ gfa,
     double* __restrict__ gfb, int K) {
   __shared__ double sTab[kAtmMaxSpecies * kAtmMaxSpecies];
+  // the forward's energy ring (one per wave; a placeholder in the backward)
+  __shared__ double sRing[BWD ? 1 : kAtmWaves][BWD ? 1 : kAtmRing][kWave + 1];
+  __shared__ int32_t sRingK[BWD ? 1 : kAtmWaves][kAtmRing];
+  // the backward's permuted factor rows, fp[i][lane] = fa[j][i ^ (lane >> 1)]
+  __shared__ double sFp[BWD ? kAtmWaves : 1][BWD ? 32 : 1][kWave];
   atm_stage_table(table, S, sTab);
   const int lane = threadIdx.x & (kWave - 1);
+  const int wv = wave_in_block();
   const int64_t t = blockIdx.x / n_groups;
-  const int64_t c = (blockIdx.x - t * n_groups) * kAtmWaves + wave_in_block();
+  const int64_t c = (blockIdx.x - t * n_groups) * kAtmWaves + wv;
   if (c >= N) return;
   const int32_t hi = lo[c + 1];
   const int32_t a0 = lo1[c] + (int32_t)t * kAtmTile;
   if (a0 + 1 >= hi) return;                       // fewer than two edges left: no pair
+  const AtmLanes L = atm_lanes(lane);
   const int32_t a = a0 + lane;
   const bool va = a < hi;
   const AtmEdge ea = rec[va ? a : a0];
@@ -377,6 +479,13 @@ __global__ __launch_bounds__(kAtmWaves * kWave) void atm_upper_kernel(
   double fj[KP];
 #pragma unroll
   for (int w = 0; w < KP; ++w) fj[w] = fa[(int64_t)j * KP + w];
+  if (BWD) {
+    const int m = lane >> 1;
+#pragma unroll
+    for (int i = 0; i < 32; ++i)
+      sFp[wv][i][lane] = (i ^ m) < KP ? fa[(int64_t)j * KP + (i ^ m)] : 0.0;
+    wave_sync();
+  }
   const double go_c = BWD ? go[c] : 0.0;
   const double go_j = BWD ? go[j] : 0.0;
   double e_row = 0.0;
@@ -384,6 +493,7 @@ __global__ __launch_bounds__(kAtmWaves * kWave) void atm_upper_kernel(
   double gfj[BWD ? KP : 1];
 #pragma unroll
   for (int w = 0; w < (BWD ? KP : 1); ++w) gfj[w] = 0.0;
+  int n_ring = 0;
 
   for (int32_t b = a0 + 1; b < hi; ++b) {
     const AtmEdge eb = rec[b];                      // wave-uniform
@@ -402,13 +512,17 @@ __global__ __launch_bounds__(kAtmWaves * kWave) void atm_upper_kernel(
       for (int w = 0; w < KP; ++w) c6jk = fma(fj[w], fk[w], c6jk);
       const double r0 = ea.p * eb.p * sTab[sj * S + eb.snb];
       const double weight = BWD ? go_c + go_j + go[k] : 1.0;
-      atm_triangle<SWITCH, BWD>(kc, x, y, w2, ix, iy, fabs(ea.c6 * eb.c6 * c6jk), r0, ea.sw,
-                                eb.sw, ea.dsw, eb.dsw, weight, e, gx, gy, gw);
+      atm_triangle<SWITCH, BWD, P16>(kc, x, y, w2, ix, iy, fabs(ea.c6 * eb.c6 * c6jk), r0,
+                                     ea.sw, eb.sw, ea.dsw, eb.dsw, weight, e, gx, gy, gw);
     }
     if (!BWD) {
       e_row += e;
-      const double ek = atm_wave_sum(e);
-      if (lane == 0) unsafeAtomicAdd(&energy[k], ek);
+      sRing[wv][n_ring][lane] = e;
+      if (lane == 0) sRingK[wv][n_ring] = k;
+      if (++n_ring == kAtmRing) {
+        atm_ring_flush(sRing[wv], sRingK[wv], n_ring, lane, L, energy);
+        n_ring = 0;
+      }
     } else {
       // dE/dC6 = E / (2 C6) for each of the three pair coefficients (C9 = sqrt(C6 C6 C6))
       const double g3 = keep ? 0.5 * e * rcp_nr(c6jk != 0.0 ? c6jk : 1.0) : 0.0;
@@ -418,28 +532,21 @@ __global__ __launch_bounds__(kAtmWaves * kWave) void atm_upper_kernel(
       gc6a = fma(e, hc6a, gc6a);
 #pragma unroll
       for (int w = 0; w < KP; ++w) gfj[w] = fma(g3, fk[w], gfj[w]);
-      double sl[32];
-#pragma unroll
-      for (int w = 0; w < KP; ++w) sl[w] = g3 * fj[w];
-      sl[KP + 0] = 2.0 * fma(gy, eb.vx, -gw * dx);
-      sl[KP + 1] = 2.0 * fma(gy, eb.vy, -gw * dy);
-      sl[KP + 2] = 2.0 * fma(gy, eb.vz, -gw * dz);
-      sl[KP + 3] = 0.5 * e / (eb.c6 != 0.0 ? eb.c6 : 1.0);
-#pragma unroll
-      for (int w = KP + 4; w < 32; ++w) sl[w] = 0.0;
-      const double v = atm_reduce32(sl, lane);
+      // edge b and atom k: the wave's sums of g3 fa[j] (per component) and of the four
+      // scalars (vector gradient of edge b, dE/dC6_ck)
+      const double vf = atm_fold32(sFp[BWD ? wv : 0], lane, g3, L);
+      const double vs = atm_fold4(2.0 * fma(gy, eb.vx, -gw * dx), 2.0 * fma(gy, eb.vy, -gw * dy),
+                                  2.0 * fma(gy, eb.vz, -gw * dz),
+                                  0.5 * e / (eb.c6 != 0.0 ? eb.c6 : 1.0), lane, L);
       const int slot = lane >> 1;
-      if ((lane & 1) == 0) {
-        if (slot < K)
-          unsafeAtomicAdd(&gfb[(int64_t)k * K + slot], v);
-        else if (slot >= KP && slot < KP + 4)
-          unsafeAtomicAdd(&gs[(int64_t)b * 4 + (slot - KP)], v);
-      }
+      if ((lane & 1) == 0 && slot < K) unsafeAtomicAdd(&gfb[(int64_t)k * K + slot], vf);
+      if ((lane & 15) == 0) unsafeAtomicAdd(&gs[(int64_t)b * 4 + (lane >> 4)], vs);
     }
   }
   if (!BWD) {
+    if (n_ring > 0) atm_ring_flush(sRing[wv], sRingK[wv], n_ring, lane, L, energy);
     if (va) unsafeAtomicAdd(&energy[j], e_row);
-    const double ec = atm_wave_sum(e_row);
+    const double ec = atm_wave_sum(e_row, L);
     if (lane == 0) unsafeAtomicAdd(&energy[c], ec);
   } else if (va) {
     unsafeAtomicAdd(&gs[(int64_t)a * 4 + 0], gax);
@@ -497,6 +604,7 @@ __global__ __launch_bounds__(kAtmWaves * kWave) void atm_repeat_kernel(
     if (!self)
       while (run_end < hi && rec[run_end].nb == j) ++run_end;
     const int32_t r1_end = self ? hi : run_end;
+    bool any = false;                               // a triangle was kept for this edge
     const int32_t r2_beg = self ? hi : (s0 > a + 1 ? s0 : a + 1);
     const int32_t r2_end = self ? hi : u0;
     for (int pass = 0; pass < 2; ++pass) {
@@ -507,6 +615,7 @@ __global__ __launch_bounds__(kAtmWaves * kWave) void atm_repeat_kernel(
         const double dx = ax - eb.vx, dy = ay - eb.vy, dz = az - eb.vz;
         const double w2 = dx * dx + dy * dy + dz * dz;
         if (!(w2 <= kc.cut2 && w2 > kAtmEps)) continue;
+        any = true;
         const int32_t k = eb.nb;
         const double y = eb.vx * eb.vx + eb.vy * eb.vy + eb.vz * eb.vz;
         const double* __restrict__ fk = fb + (int64_t)k * KP;
@@ -515,7 +624,7 @@ __global__ __launch_bounds__(kAtmWaves * kWave) void atm_repeat_kernel(
         for (int w = 0; w < KP; ++w) c6jk = fma(fj[w], fk[w], c6jk);
         const double r0 = ea.p * eb.p * sTab[ea.snb * S + eb.snb];
         double e, gx = 0.0, gy = 0.0, gw = 0.0;
-        atm_triangle<SWITCH, BWD>(kc, x, y, w2, ix, BWD ? rcp_nr(y) : 0.0,
+        atm_triangle<SWITCH, BWD, false>(kc, x, y, w2, ix, BWD ? rcp_nr(y) : 0.0,
                                   fabs(ea.c6 * eb.c6 * c6jk), r0, ea.sw, eb.sw, ea.dsw, eb.dsw,
                                   BWD ? go_c : 1.0, e, gx, gy, gw);
         if (!BWD) {
@@ -538,7 +647,7 @@ __global__ __launch_bounds__(kAtmWaves * kWave) void atm_repeat_kernel(
         }
       }
     }
-    if (BWD) {
+    if (BWD && any) {
       unsafeAtomicAdd(&gs[(int64_t)a * 4 + 0], gax);
       unsafeAtomicAdd(&gs[(int64_t)a * 4 + 1], gay);
       unsafeAtomicAdd(&gs[(int64_t)a * 4 + 2], gaz);
@@ -549,7 +658,7 @@ __global__ __launch_bounds__(kAtmWaves * kWave) void atm_repeat_kernel(
     }
   }
   if (!BWD) {
-    const double ec = atm_wave_sum(e_acc);
+    const double ec = atm_wave_sum(e_acc, atm_lanes(lane));
     if (lane == 0) unsafeAtomicAdd(&energy[c], ec);
   }
 }
@@ -566,34 +675,108 @@ __global__ void atm_vec_grad_kernel(const int32_t* __restrict__ perm,
   gvec[3 * e + 2] = gs[4 * p + 2];
 }
 
-// The center sides C6_cj = <fa[c], fb[j]> of every edge: gfa[c] += sum_row dE/dC6 fb[j]
-// (one wave per center, reduced across the wave) and gfb[j] += dE/dC6 fa[c] (atomic)
+// The center sides C6_cj = <fa[c], fb[j]> of every edge, one wave per atom x, no atomics:
+// gfa[x] += sum over x's row (x the center) of dE/dC6 fb[j], gfb[x] += sum over the edges
+// whose neighbor is x (the plan's by-source order) of dE/dC6 fa[c].
 template <int KP>
 __global__ __launch_bounds__(kAtmWaves * kWave) void atm_center_side_kernel(
     const int32_t* __restrict__ lo, const int32_t* __restrict__ nbr,
-    const double* __restrict__ gs, const double* __restrict__ fa,
-    const double* __restrict__ fb, int64_t N, int K, double* __restrict__ gfa,
-    double* __restrict__ gfb) {
+    const int32_t* __restrict__ lo_src, const int32_t* __restrict__ by_src,
+    const int32_t* __restrict__ ctr, const double* __restrict__ gs,
+    const double* __restrict__ fa, const double* __restrict__ fb, int64_t N, int K,
+    double* __restrict__ gfa, double* __restrict__ gfb) {
   const int lane = threadIdx.x & (kWave - 1);
-  const int64_t c = (int64_t)blockIdx.x * kAtmWaves + wave_in_block();
-  if (c >= N) return;
-  const int32_t l0 = lo[c], hi = lo[c + 1];
-  if (l0 == hi) return;
-  double acc[32];
+  const int64_t x = (int64_t)blockIdx.x * kAtmWaves + wave_in_block();
+  if (x >= N) return;
+  const AtmLanes L = atm_lanes(lane);
+  for (int side = 0; side < 2; ++side) {
+    const int32_t p0 = side == 0 ? lo[x] : lo_src[x];
+    const int32_t p1 = side == 0 ? lo[x + 1] : lo_src[x + 1];
+    if (p0 == p1) continue;                         // uniform
+    double acc[KP];
 #pragma unroll
-  for (int w = 0; w < 32; ++w) acc[w] = 0.0;
-  for (int32_t p = l0 + lane; p < hi; p += kWave) {
-    const double g = gs[4 * (int64_t)p + 3];
-    const int64_t j = nbr[p];
+    for (int w = 0; w < KP; ++w) acc[w] = 0.0;
+    for (int32_t q = p0 + lane; q < p1; q += kWave) {
+      const int64_t p = side == 0 ? q : by_src[q];
+      const double g = gs[4 * p + 3];
+      const double* __restrict__ f = side == 0 ? fb + (int64_t)nbr[p] * KP : fa + (int64_t)ctr[p] * KP;
 #pragma unroll
-    for (int w = 0; w < KP; ++w) acc[w] = fma(g, fb[j * KP + w], acc[w]);
+      for (int w = 0; w < KP; ++w) acc[w] = fma(g, f[w], acc[w]);
+    }
+    double* __restrict__ out = side == 0 ? gfa : gfb;
 #pragma unroll
-    for (int w = 0; w < KP; ++w)
-      if (w < K) unsafeAtomicAdd(&gfb[j * K + w], g * fa[c * KP + w]);
+    for (int w = 0; w < KP; ++w) {
+      const double v = atm_wave_sum(acc[w], L);
+      if (lane == 0 && w < K) out[x * K + w] += v;
+    }
   }
-  const double v = atm_reduce32(acc, lane);
-  const int slot = lane >> 1;
-  if ((lane & 1) == 0 && slot < K) gfa[c * K + slot] += v;
+}
+
+// Diagnostics for the roofline: counts[0] += edge pairs tested by the upper kernel,
+// counts[1] += distinct triangles it keeps, counts[2] += repeated-atom triangle visits.
+// Same walk as the triangle kernels, reading the vectors through the plan's permutation.
+__global__ __launch_bounds__(kAtmWaves * kWave) void atm_count_kernel(
+    const int32_t* __restrict__ perm, const int32_t* __restrict__ nbr,
+    const int32_t* __restrict__ lo, const int32_t* __restrict__ lo1,
+    const int32_t* __restrict__ flag, int64_t N, int64_t n_groups, int64_t max_tiles,
+    const double* __restrict__ vec, double cut2, unsigned long long* __restrict__ counts) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int64_t t = blockIdx.x / n_groups;
+  const int64_t c = (blockIdx.x - t * n_groups) * kAtmWaves + wave_in_block();
+  if (c >= N) return;
+  const int32_t l0 = lo[c], u0 = lo1[c], hi = lo[c + 1];
+  unsigned long long tested = 0, kept = 0, rep = 0;
+  const int32_t a0 = u0 + (int32_t)t * kAtmTile;
+  if (t < max_tiles && a0 + 1 < hi) {
+    const int32_t a = a0 + lane;
+    const bool va = a < hi;
+    const int64_t ea = perm[va ? a : a0];
+    const double ax = vec[3 * ea], ay = vec[3 * ea + 1], az = vec[3 * ea + 2];
+    const int32_t j = nbr[va ? a : a0];
+    for (int32_t b = a0 + 1; b < hi; ++b) {
+      const int64_t eb = perm[b];
+      const double dx = ax - vec[3 * eb], dy = ay - vec[3 * eb + 1], dz = az - vec[3 * eb + 2];
+      const double w2 = dx * dx + dy * dy + dz * dz;
+      const bool live = va && a < b;
+      tested += live;
+      kept += live && j != nbr[b] && w2 <= cut2 && w2 > kAtmEps;
+    }
+  }
+  if (t == 0 && flag[c] != 0) {
+    int32_t s0 = u0;
+    while (s0 > l0 && nbr[s0 - 1] == (int32_t)c) --s0;
+    for (int32_t a = l0 + lane; a < hi; a += kWave) {
+      const int64_t ea = perm[a];
+      const double ax = vec[3 * ea], ay = vec[3 * ea + 1], az = vec[3 * ea + 2];
+      const int32_t j = nbr[a];
+      const bool self = j == (int32_t)c;
+      int32_t run_end = a + 1;
+      if (!self)
+        while (run_end < hi && nbr[run_end] == j) ++run_end;
+      for (int pass = 0; pass < 2; ++pass) {
+        const int32_t b_beg = pass == 0 ? a + 1 : (self ? hi : (s0 > a + 1 ? s0 : a + 1));
+        const int32_t b_end = pass == 0 ? (self ? hi : run_end) : (self ? hi : u0);
+        for (int32_t b = b_beg; b < b_end; ++b) {
+          const int64_t eb = perm[b];
+          const double dx = ax - vec[3 * eb], dy = ay - vec[3 * eb + 1],
+                       dz = az - vec[3 * eb + 2];
+          const double w2 = dx * dx + dy * dy + dz * dz;
+          rep += w2 <= cut2 && w2 > kAtmEps;
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int o = kWave / 2; o > 0; o >>= 1) {
+    tested += __shfl_xor(tested, o);
+    kept += __shfl_xor(kept, o);
+    rep += __shfl_xor(rep, o);
+  }
+  if (lane == 0) {
+    if (tested) atomicAdd(&counts[0], tested);
+    if (kept) atomicAdd(&counts[1], kept);
+    if (rep) atomicAdd(&counts[2], rep);
+  }
 }
 
 // ------------------------------------------------------------------------------ host
@@ -633,7 +816,7 @@ struct AtmArgs {
   hipStream_t s;
 };
 
-template <int KP, bool SWITCH, bool BWD>
+template <int KP, bool SWITCH, bool BWD, bool P16>
 static int atm_run(const AtmArgs& A) {
   const AtmPlanLayout P = atm_plan_layout(A.E, A.N);
   const AtmWorkLayout W = atm_work_layout(A.E, A.N, KP, BWD);
@@ -668,7 +851,7 @@ static int atm_run(const AtmArgs& A) {
   if (A.max_tiles > 0) {
     const int64_t blocks = A.max_tiles * n_groups;
     XNN_REQUIRE(blocks <= 0x7fffffff, "ATM: too many triplet work items");
-    hipLaunchKernelGGL((atm_upper_kernel<KP, SWITCH, BWD>), dim3((unsigned)blocks),
+    hipLaunchKernelGGL((atm_upper_kernel<KP, SWITCH, BWD, P16>), dim3((unsigned)blocks),
                        dim3(kAtmWaves * kWave), 0, A.s, rec, lo, lo1, A.N, n_groups, faP, fbP,
                        A.table, A.S, A.kc, A.energy, A.go, gs, A.gfa, A.gfb, A.K);
     XNN_LAUNCH_CHECK();
@@ -683,19 +866,26 @@ static int atm_run(const AtmArgs& A) {
     hipLaunchKernelGGL(atm_vec_grad_kernel, dim3(grid_1d(A.E, 256)), dim3(256), 0, A.s, perm, gs,
                        A.E, A.gvec);
     hipLaunchKernelGGL((atm_center_side_kernel<KP>), dim3((unsigned)n_groups),
-                       dim3(kAtmWaves * kWave), 0, A.s, lo, nbr, gs, faP, fbP, A.N, A.K, A.gfa,
-                       A.gfb);
+                       dim3(kAtmWaves * kWave), 0, A.s, lo, nbr,
+                       at_off<int32_t>(A.plan, P.lo_src), at_off<int32_t>(A.plan, P.by_src),
+                       at_off<int32_t>(A.plan, P.ctr), gs, faP, fbP, A.N, A.K, A.gfa, A.gfb);
     XNN_LAUNCH_CHECK();
   }
   return XNN_OK;
 }
 
+template <int KP, bool BWD, bool P16>
+static int atm_dispatch_sw(const AtmArgs& A) {
+  return A.kc.width > 0.0 ? atm_run<KP, true, BWD, P16>(A) : atm_run<KP, false, BWD, P16>(A);
+}
+
 template <bool BWD>
 static int atm_dispatch(const AtmArgs& A) {
-  const bool sw = A.kc.width > 0.0;
+  // the upstream exponent 16/3 takes the power without exp and log
+  const bool p16 = fabs(A.kc.alp3 - 16.0 / 3.0) < 1e-12;
   if (atm_kp(A.K) == 24)
-    return sw ? atm_run<24, true, BWD>(A) : atm_run<24, false, BWD>(A);
-  return sw ? atm_run<28, true, BWD>(A) : atm_run<28, false, BWD>(A);
+    return p16 ? atm_dispatch_sw<24, BWD, true>(A) : atm_dispatch_sw<24, BWD, false>(A);
+  return p16 ? atm_dispatch_sw<28, BWD, true>(A) : atm_dispatch_sw<28, BWD, false>(A);
 }
 
 static int atm_check(int64_t E, int64_t N, int64_t max_tiles, const double* vec, const double* fa,
@@ -761,9 +951,18 @@ int xnn_atm_plan(const int64_t* edge_index, int64_t n_edges, int64_t n_atoms, vo
                                                      keys, vals_in, perm, (int)E, 0,
                                                      atm_end_bit(N), s));
     hipLaunchKernelGGL(atm_neighbors_kernel, dim3(grid_1d(E, 256)), dim3(256), 0, s, keys, E, N,
-                       at_off<int32_t>(plan, L.nbr), flag, stats);
+                       at_off<int32_t>(plan, L.nbr), at_off<int32_t>(plan, L.ctr),
+                       at_off<uint64_t>(plan, L.keys2), vals_in, flag, stats);
     XNN_LAUNCH_CHECK();
+    // the by-source order (sorted keys into the free keys_in buffer)
+    cub_bytes = L.cub_bytes;
+    XNN_HIP_CHECK(hipcub::DeviceRadixSort::SortPairs(
+        at_off<void>(plan, L.cub), cub_bytes, at_off<uint64_t>(plan, L.keys2), keys_in, vals_in,
+        at_off<int32_t>(plan, L.by_src), (int)E, 0, atm_end_bit(N), s));
   }
+  hipLaunchKernelGGL(atm_src_rows_kernel, dim3(grid_1d(N + 1, 256)), dim3(256), 0, s,
+                     at_off<uint64_t>(plan, L.keys_in), E, N, at_off<int32_t>(plan, L.lo_src));
+  XNN_LAUNCH_CHECK();
   hipLaunchKernelGGL(atm_rows_kernel, dim3(grid_1d(N + 1, 256)), dim3(256), 0, s,
                      at_off<uint64_t>(plan, L.keys), E, N, at_off<int32_t>(plan, L.lo),
                      at_off<int32_t>(plan, L.lo1), flag, stats);
@@ -818,6 +1017,39 @@ int xnn_atm_energy_backward(const void* plan, int64_t n_edges, int64_t n_atoms,
             species, table, n_species, atm_const(prm), nullptr, grad_energy, grad_vec, grad_fa,
             grad_fb, work, as_hip(stream)};
   return atm_dispatch<true>(A);
+}
+
+int xnn_atm_count(const void* plan, int64_t n_edges, int64_t n_atoms, int64_t max_tiles,
+                  const double* edge_vec, double cutoff, int64_t* counts, xnn_stream_t stream) {
+  XNN_REQUIRE(n_edges >= 0 && n_atoms >= 0 && max_tiles >= 0, "negative size");
+  XNN_REQUIRE(n_edges <= 0x7fffffff && n_atoms < 0x7fffffff,
+              "ATM: at most 2^31 - 1 edges and atoms");
+  XNN_REQUIRE(plan != nullptr && counts != nullptr, "NULL plan or output");
+  XNN_REQUIRE(n_edges == 0 || edge_vec != nullptr, "NULL edge vectors");
+  counts[0] = counts[1] = counts[2] = 0;
+  if (n_edges == 0 || n_atoms == 0) return XNN_OK;
+  const AtmPlanLayout L = atm_plan_layout(n_edges, n_atoms);
+  hipStream_t s = as_hip(stream);
+  unsigned long long* dev = nullptr;
+  XNN_HIP_CHECK(hipMallocAsync((void**)&dev, 3 * sizeof(unsigned long long), s));
+  XNN_HIP_CHECK(hipMemsetAsync(dev, 0, 3 * sizeof(unsigned long long), s));
+  const int64_t n_groups = (n_atoms + kAtmWaves - 1) / kAtmWaves;
+  const int64_t blocks = std::max<int64_t>(max_tiles, 1) * n_groups;
+  XNN_REQUIRE(blocks <= 0x7fffffff, "ATM: too many triplet work items");
+  hipLaunchKernelGGL(atm_count_kernel, dim3((unsigned)blocks), dim3(kAtmWaves * kWave), 0, s,
+                     at_off<int32_t>(plan, L.perm), at_off<int32_t>(plan, L.nbr),
+                     at_off<int32_t>(plan, L.lo), at_off<int32_t>(plan, L.lo1),
+                     at_off<int32_t>(plan, L.flag), n_atoms, n_groups, max_tiles, edge_vec,
+                     cutoff * cutoff, dev);
+  XNN_LAUNCH_CHECK();
+  unsigned long long h[3];
+  XNN_HIP_CHECK(hipMemcpyAsync(h, dev, sizeof(h), hipMemcpyDeviceToHost, s));
+  XNN_HIP_CHECK(hipFreeAsync(dev, s));
+  XNN_HIP_CHECK(hipStreamSynchronize(s));
+  counts[0] = (int64_t)h[0];
+  counts[1] = (int64_t)h[1];
+  counts[2] = (int64_t)h[2];
+  return XNN_OK;
 }
 
 }  // extern "C"

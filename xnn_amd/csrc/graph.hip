@@ -34,6 +34,15 @@ struct GridDev {
 
 static inline size_t align_up(size_t x) { return (x + 255) & ~(size_t)255; }
 
+// blocks per receiver bin: one when bins hold a few waves' worth of atoms; with few,
+// crowded bins (a cutoff comparable to the cell) the receivers of a bin are spread over
+// up to 1024 blocks, 4 receivers per wave on average
+static inline int search_split(int64_t n_atoms, int64_t n_bins) {
+  const int64_t per_bin = (n_atoms + n_bins - 1) / (n_bins > 0 ? n_bins : 1);
+  const int64_t s = (per_bin + 15) / 16;
+  return (int)(s < 1 ? 1 : (s > 1024 ? 1024 : s));
+}
+
 // workspace layout of the cell list (offsets in bytes); the count step fills it
 // and the fill step reads it back, so both must get the same buffer.
 struct GridWs {
@@ -149,7 +158,10 @@ __global__ __launch_bounds__(256) void cell_search_kernel(
   const int bin = blockIdx.x;
   const int bx = bin % g.nb[0], by = (bin / g.nb[0]) % g.nb[1], bz = bin / (g.nb[0] * g.nb[1]);
   const int r0 = bin_start[bin], r1 = bin_start[bin + 1];
-  if (r0 == r1) return;  // uniform: no receivers
+  // the bin's receivers are dealt to gridDim.y blocks, a wave's worth at a time
+  const int split_stride = (int)gridDim.y * (int)(blockDim.x / kWave);
+  const int split_first = (int)blockIdx.y * (int)(blockDim.x / kWave);
+  if (r1 - r0 <= split_first) return;  // uniform: no receivers for this block
   const int wx = 2 * g.reach[0] + 1, wy = 2 * g.reach[1] + 1, wz = 2 * g.reach[2] + 1;
   const int n_slots = wx * wy * wz;
 
@@ -197,7 +209,6 @@ __global__ __launch_bounds__(256) void cell_search_kernel(
   const int n_cand = s_first[n_slots];
 
   const int wave = wave_in_block(), lane = threadIdx.x % kWave;
-  const int n_waves = blockDim.x / kWave;
   const int n_recv = r1 - r0;
 
   for (int c0 = 0; c0 < n_cand; c0 += kTile) {
@@ -218,7 +229,7 @@ __global__ __launch_bounds__(256) void cell_search_kernel(
       t_slot[c - c0] = s;
     }
     __syncthreads();
-    for (int r = wave; r < n_recv; r += n_waves) {
+    for (int r = split_first + wave; r < n_recv; r += split_stride) {
       const int pr = r0 + r;
       const int i = atom_sorted[pr];
       const G xi = wpos[4 * pr + 0], yi = wpos[4 * pr + 1], zi = wpos[4 * pr + 2];
@@ -455,7 +466,8 @@ static int grid_count(const void* pos_v, int64_t n, const void* cell_v, double c
                                                    end_bit_for(plan->n_bins), stream));
   hipLaunchKernelGGL((gather_sorted_kernel<G>), dim3(grid_1d(n, 256)), dim3(256), 0, stream,
                      atom_sorted, n, wpos, offs, wpos_s, offs_s);
-  hipLaunchKernelGGL((cell_search_kernel<G, false>), dim3(plan->n_bins), dim3(256), 0, stream,
+  hipLaunchKernelGGL((cell_search_kernel<G, false>),
+                     dim3(plan->n_bins, search_split(n, plan->n_bins)), dim3(256), 0, stream,
                      wpos_s, offs_s, atom_sorted, bin_start, cell, g, (G)cutoff, self_interaction,
                      counts, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, (int64_t)0,
                      overflow);
@@ -485,7 +497,8 @@ static int grid_fill(const void* pos_v, int64_t n, const void* cell_v, double cu
   hipLaunchKernelGGL(zero_i32_kernel, dim3(grid_1d(n + 1, 256)), dim3(256), 0, stream, counts,
                      n + 1);
   hipLaunchKernelGGL(zero_i32_kernel, dim3(1), dim3(64), 0, stream, overflow, (int64_t)1);
-  hipLaunchKernelGGL((cell_search_kernel<G, true>), dim3(plan->n_bins), dim3(256), 0, stream,
+  hipLaunchKernelGGL((cell_search_kernel<G, true>),
+                     dim3(plan->n_bins, search_split(n, plan->n_bins)), dim3(256), 0, stream,
                      ws_at<G>(ws, w.wpos_s), ws_at<int32_t>(ws, w.offs_s),
                      ws_at<int32_t>(ws, w.atom_sorted), ws_at<int32_t>(ws, w.bin_start), cell, g,
                      (G)cutoff, self_interaction, counts, row_ptr, src, dst, shift, ei64, sh64,
