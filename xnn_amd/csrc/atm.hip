@@ -48,17 +48,40 @@ constexpr int kAtmMaxK = 28;          // C6 factor components
 constexpr int kAtmMaxSpecies = 32;    // side of the damping-radius factor table
 constexpr double kAtmEps = 2.220446049250313e-16;   // lower bound on r_jk^2 (dispersion.py:200)
 
-// one sorted edge (j -> c) as the triplet kernels read it (one 64-byte scalar load)
+// one edge (j -> c) as the triplet kernels read it (one 64-byte scalar load)
 struct __align__(16) AtmEdge {
   double vx, vy, vz;   // edge vector, bohr
   double c6;           // <fa[c], fb[j]>
   double p;            // damping-radius factor of the species pair (c, j)
   double sw;           // switch at r = |v|
   double dsw;          // its slope in r^2: sw'(r) / (2 r)
-  int32_t nb;          // the neighbor j
-  int32_t snb;         // its species
+  uint32_t nbs;        // the neighbor j (low 26 bits) and its species (high 6)
+  int32_t pos;         // the edge's position in the (center, neighbor) order
 };
 static_assert(sizeof(AtmEdge) == 64, "AtmEdge is one 64-byte record");
+constexpr int kAtmNbBits = 26;         // atoms < 2^26
+
+__device__ __forceinline__ int32_t atm_nb(const AtmEdge& e) {
+  return (int32_t)(e.nbs & ((1u << kAtmNbBits) - 1u));
+}
+__device__ __forceinline__ int atm_snb(const AtmEdge& e) { return (int)(e.nbs >> kAtmNbBits); }
+
+// 30-bit Morton code of an edge vector inside the cutoff sphere (10 bits per axis)
+__device__ __forceinline__ uint32_t atm_spread10(uint32_t v) {
+  v &= 0x3ffu;
+  v = (v | (v << 16)) & 0x030000ffu;
+  v = (v | (v << 8)) & 0x0300f00fu;
+  v = (v | (v << 4)) & 0x030c30c3u;
+  v = (v | (v << 2)) & 0x09249249u;
+  return v;
+}
+__device__ __forceinline__ uint32_t atm_morton(double x, double y, double z, double inv_2rc) {
+  const auto q = [&](double t) {
+    const double u = (t * inv_2rc + 0.5) * 1024.0;
+    return (uint32_t)(u < 0.0 ? 0.0 : (u > 1023.0 ? 1023.0 : u));
+  };
+  return (atm_spread10(q(x)) << 2) | (atm_spread10(q(y)) << 1) | atm_spread10(q(z));
+}
 
 struct AtmConst {
   double s9_3;         // s9 / 3: a third of every triangle per corner
@@ -111,13 +134,33 @@ static AtmPlanLayout atm_plan_layout(int64_t E, int64_t N) {
 }
 
 struct AtmWorkLayout {
-  size_t rec, fa, fb, gs, total;
+  size_t rec, rec_up, fa, fb, gs, skey, sval, skey_out, sperm, cub, cub_bytes, total;
 };
+
+static int atm_bitlen(int64_t n) {
+  int b = 1;
+  while (b < 62 && (n >> b) != 0) ++b;
+  return b;
+}
 
 static AtmWorkLayout atm_work_layout(int64_t E, int64_t N, int kp, bool backward) {
   AtmWorkLayout L;
   size_t at = 0;
-  L.rec = at; at += atm_align(sizeof(AtmEdge) * std::max<int64_t>(E, 1));
+  const int64_t e1 = std::max<int64_t>(E, 1);
+  L.rec = at; at += atm_align(sizeof(AtmEdge) * e1);
+  L.rec_up = at; at += atm_align(sizeof(AtmEdge) * e1);
+  L.skey = at; at += atm_align(sizeof(uint64_t) * e1);
+  L.sval = at; at += atm_align(sizeof(int32_t) * e1);
+  L.skey_out = at; at += atm_align(sizeof(uint64_t) * e1);
+  L.sperm = at; at += atm_align(sizeof(int32_t) * e1);
+  size_t cub_bytes = 0;
+  (void)hipcub::DeviceRadixSort::SortPairs(nullptr, cub_bytes, (uint64_t*)nullptr,
+                                           (uint64_t*)nullptr, (int32_t*)nullptr,
+                                           (int32_t*)nullptr, (int)e1, 0,
+                                           33 + atm_bitlen(std::max<int64_t>(N, 1)));
+  L.cub = at;
+  L.cub_bytes = atm_align(cub_bytes + 256);
+  at += L.cub_bytes;
   L.fa = at; at += atm_align(sizeof(double) * kp * std::max<int64_t>(N, 1));
   L.fb = at; at += atm_align(sizeof(double) * kp * std::max<int64_t>(N, 1));
   L.gs = at;
@@ -247,7 +290,8 @@ __global__ void atm_edges_kernel(const uint64_t* __restrict__ keys,
                                  const double* __restrict__ fb,
                                  const int32_t* __restrict__ species,
                                  const double* __restrict__ table, int S, AtmConst kc,
-                                 AtmEdge* __restrict__ rec) {
+                                 AtmEdge* __restrict__ rec, uint64_t* __restrict__ skey,
+                                 int32_t* __restrict__ sval) {
   const int64_t p = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (p >= E) return;
   const int64_t e = perm[p];
@@ -275,9 +319,25 @@ __global__ void atm_edges_kernel(const uint64_t* __restrict__ keys,
     r.sw = sw;
     r.dsw = len > 0.0 ? 0.5 * dsw / len : 0.0;
   }
-  r.nb = j;
-  r.snb = sj >= 0 && sj < S ? sj : 0;
+  r.nbs = (uint32_t)j | ((uint32_t)(sj >= 0 && sj < S ? sj : 0) << kAtmNbBits);
+  r.pos = (int32_t)p;
   rec[p] = r;
+  // the walk order of the distinct-triangle kernel: a center's edges to smaller-index
+  // neighbors first, in the plan's order (equal keys, stable sort), then its edges to
+  // larger-index neighbors along a Morton curve of the edge vector, so that a tile of 64
+  // of them is compact in space and the walked edges far from it fail for all lanes
+  const bool up = (int64_t)j > c;
+  skey[p] = ((uint64_t)c << 33) |
+            (up ? ((1ull << 32) | atm_morton(r.vx, r.vy, r.vz, 0.5 / kc.cutoff)) : 0ull);
+  sval[p] = (int32_t)p;
+}
+
+// the walk-ordered copy of the records
+__global__ void atm_walk_order_kernel(const AtmEdge* __restrict__ rec,
+                                      const int32_t* __restrict__ sperm, int64_t E,
+                                      AtmEdge* __restrict__ rec_up) {
+  const int64_t q = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (q < E) rec_up[q] = rec[sperm[q]];
 }
 
 // ------------------------------------------------------------------------------ triangle
@@ -474,8 +534,8 @@ __global__ __launch_bounds__(kAtmWaves * kWave) void atm_upper_kernel(
   const double x = ax * ax + ay * ay + az * az;
   const double ix = BWD ? rcp_nr(x) : 0.0;
   const double hc6a = BWD ? 0.5 / (ea.c6 != 0.0 ? ea.c6 : 1.0) : 0.0;   // dC9/C9 per dC6_cj
-  const int32_t j = ea.nb;
-  const int sj = ea.snb;
+  const int32_t j = atm_nb(ea);
+  const int sj = atm_snb(ea);
   double fj[KP];
 #pragma unroll
   for (int w = 0; w < KP; ++w) fj[w] = fa[(int64_t)j * KP + w];
@@ -497,7 +557,7 @@ __global__ __launch_bounds__(kAtmWaves * kWave) void atm_upper_kernel(
 
   for (int32_t b = a0 + 1; b < hi; ++b) {
     const AtmEdge eb = rec[b];                      // wave-uniform
-    const int32_t k = eb.nb;
+    const int32_t k = atm_nb(eb);
     const double dx = ax - eb.vx, dy = ay - eb.vy, dz = az - eb.vz;
     const double w2 = dx * dx + dy * dy + dz * dz;
     const bool keep = va && a < b && j != k && w2 <= kc.cut2 && w2 > kAtmEps;
@@ -510,7 +570,7 @@ __global__ __launch_bounds__(kAtmWaves * kWave) void atm_upper_kernel(
       c6jk = 0.0;
 #pragma unroll
       for (int w = 0; w < KP; ++w) c6jk = fma(fj[w], fk[w], c6jk);
-      const double r0 = ea.p * eb.p * sTab[sj * S + eb.snb];
+      const double r0 = ea.p * eb.p * sTab[sj * S + atm_snb(eb)];
       const double weight = BWD ? go_c + go_j + go[k] : 1.0;
       atm_triangle<SWITCH, BWD, P16>(kc, x, y, w2, ix, iy, fabs(ea.c6 * eb.c6 * c6jk), r0,
                                      ea.sw, eb.sw, ea.dsw, eb.dsw, weight, e, gx, gy, gw);
@@ -540,7 +600,7 @@ __global__ __launch_bounds__(kAtmWaves * kWave) void atm_upper_kernel(
                                   0.5 * e / (eb.c6 != 0.0 ? eb.c6 : 1.0), lane, L);
       const int slot = lane >> 1;
       if ((lane & 1) == 0 && slot < K) unsafeAtomicAdd(&gfb[(int64_t)k * K + slot], vf);
-      if ((lane & 15) == 0) unsafeAtomicAdd(&gs[(int64_t)b * 4 + (lane >> 4)], vs);
+      if ((lane & 15) == 0) unsafeAtomicAdd(&gs[(int64_t)eb.pos * 4 + (lane >> 4)], vs);
     }
   }
   if (!BWD) {
@@ -549,10 +609,10 @@ __global__ __launch_bounds__(kAtmWaves * kWave) void atm_upper_kernel(
     const double ec = atm_wave_sum(e_row, L);
     if (lane == 0) unsafeAtomicAdd(&energy[c], ec);
   } else if (va) {
-    unsafeAtomicAdd(&gs[(int64_t)a * 4 + 0], gax);
-    unsafeAtomicAdd(&gs[(int64_t)a * 4 + 1], gay);
-    unsafeAtomicAdd(&gs[(int64_t)a * 4 + 2], gaz);
-    unsafeAtomicAdd(&gs[(int64_t)a * 4 + 3], gc6a);
+    unsafeAtomicAdd(&gs[(int64_t)ea.pos * 4 + 0], gax);
+    unsafeAtomicAdd(&gs[(int64_t)ea.pos * 4 + 1], gay);
+    unsafeAtomicAdd(&gs[(int64_t)ea.pos * 4 + 2], gaz);
+    unsafeAtomicAdd(&gs[(int64_t)ea.pos * 4 + 3], gc6a);
 #pragma unroll
     for (int w = 0; w < KP; ++w)
       if (w < K) unsafeAtomicAdd(&gfa[(int64_t)j * K + w], gfj[w]);
@@ -579,7 +639,7 @@ __global__ __launch_bounds__(kAtmWaves * kWave) void atm_repeat_kernel(
   if (c >= N || flag[c] == 0) return;
   const int32_t l0 = lo[c], u0 = lo1[c], hi = lo[c + 1];
   int32_t s0 = u0;                                  // self-image edges: [s0, u0)
-  while (s0 > l0 && rec[s0 - 1].nb == (int32_t)c) --s0;
+  while (s0 > l0 && atm_nb(rec[s0 - 1]) == (int32_t)c) --s0;
   const double go_c = BWD ? go[c] : 0.0;
   double e_acc = 0.0;
   for (int32_t a0 = l0; a0 < hi; a0 += kAtmTile) {
@@ -589,7 +649,7 @@ __global__ __launch_bounds__(kAtmWaves * kWave) void atm_repeat_kernel(
     const double ax = ea.vx, ay = ea.vy, az = ea.vz;
     const double x = ax * ax + ay * ay + az * az;
     const double ix = BWD ? rcp_nr(x) : 0.0;
-    const int32_t j = ea.nb;
+    const int32_t j = atm_nb(ea);
     double fj[KP];
 #pragma unroll
     for (int w = 0; w < KP; ++w) fj[w] = fa[(int64_t)j * KP + w];
@@ -602,7 +662,7 @@ __global__ __launch_bounds__(kAtmWaves * kWave) void atm_repeat_kernel(
     const bool self = j == (int32_t)c;
     int32_t run_end = a + 1;
     if (!self)
-      while (run_end < hi && rec[run_end].nb == j) ++run_end;
+      while (run_end < hi && atm_nb(rec[run_end]) == j) ++run_end;
     const int32_t r1_end = self ? hi : run_end;
     bool any = false;                               // a triangle was kept for this edge
     const int32_t r2_beg = self ? hi : (s0 > a + 1 ? s0 : a + 1);
@@ -616,13 +676,13 @@ __global__ __launch_bounds__(kAtmWaves * kWave) void atm_repeat_kernel(
         const double w2 = dx * dx + dy * dy + dz * dz;
         if (!(w2 <= kc.cut2 && w2 > kAtmEps)) continue;
         any = true;
-        const int32_t k = eb.nb;
+        const int32_t k = atm_nb(eb);
         const double y = eb.vx * eb.vx + eb.vy * eb.vy + eb.vz * eb.vz;
         const double* __restrict__ fk = fb + (int64_t)k * KP;
         double c6jk = 0.0;
 #pragma unroll
         for (int w = 0; w < KP; ++w) c6jk = fma(fj[w], fk[w], c6jk);
-        const double r0 = ea.p * eb.p * sTab[ea.snb * S + eb.snb];
+        const double r0 = ea.p * eb.p * sTab[atm_snb(ea) * S + atm_snb(eb)];
         double e, gx = 0.0, gy = 0.0, gw = 0.0;
         atm_triangle<SWITCH, BWD, false>(kc, x, y, w2, ix, BWD ? rcp_nr(y) : 0.0,
                                   fabs(ea.c6 * eb.c6 * c6jk), r0, ea.sw, eb.sw, ea.dsw, eb.dsw,
@@ -827,6 +887,10 @@ static int atm_run(const AtmArgs& A) {
   const int32_t* lo1 = at_off<int32_t>(A.plan, P.lo1);
   const int32_t* flag = at_off<int32_t>(A.plan, P.flag);
   AtmEdge* rec = at_off<AtmEdge>(A.work, W.rec);
+  AtmEdge* rec_up = at_off<AtmEdge>(A.work, W.rec_up);
+  uint64_t* skey = at_off<uint64_t>(A.work, W.skey);
+  int32_t* sval = at_off<int32_t>(A.work, W.sval);
+  int32_t* sperm = at_off<int32_t>(A.work, W.sperm);
   double* faP = at_off<double>(A.work, W.fa);
   double* fbP = at_off<double>(A.work, W.fb);
   double* gs = BWD ? at_off<double>(A.work, W.gs) : nullptr;
@@ -845,14 +909,22 @@ static int atm_run(const AtmArgs& A) {
   hipLaunchKernelGGL((atm_pad_kernel<KP>), dim3(grid_1d(A.N * KP, 256)), dim3(256), 0, A.s, A.fb,
                      A.N, A.K, fbP);
   hipLaunchKernelGGL((atm_edges_kernel<KP>), dim3(grid_1d(A.E, 256)), dim3(256), 0, A.s, keys,
-                     perm, nbr, A.E, A.N, A.vec, faP, fbP, A.species, A.table, A.S, A.kc, rec);
+                     perm, nbr, A.E, A.N, A.vec, faP, fbP, A.species, A.table, A.S, A.kc, rec,
+                     skey, sval);
+  XNN_LAUNCH_CHECK();
+  size_t cub_bytes = W.cub_bytes;
+  XNN_HIP_CHECK(hipcub::DeviceRadixSort::SortPairs(
+      at_off<void>(A.work, W.cub), cub_bytes, skey, at_off<uint64_t>(A.work, W.skey_out), sval,
+      sperm, (int)A.E, 0, 33 + atm_bitlen(A.N), A.s));
+  hipLaunchKernelGGL(atm_walk_order_kernel, dim3(grid_1d(A.E, 256)), dim3(256), 0, A.s, rec,
+                     sperm, A.E, rec_up);
   XNN_LAUNCH_CHECK();
   const int64_t n_groups = (A.N + kAtmWaves - 1) / kAtmWaves;
   if (A.max_tiles > 0) {
     const int64_t blocks = A.max_tiles * n_groups;
     XNN_REQUIRE(blocks <= 0x7fffffff, "ATM: too many triplet work items");
     hipLaunchKernelGGL((atm_upper_kernel<KP, SWITCH, BWD, P16>), dim3((unsigned)blocks),
-                       dim3(kAtmWaves * kWave), 0, A.s, rec, lo, lo1, A.N, n_groups, faP, fbP,
+                       dim3(kAtmWaves * kWave), 0, A.s, rec_up, lo, lo1, A.N, n_groups, faP, fbP,
                        A.table, A.S, A.kc, A.energy, A.go, gs, A.gfa, A.gfb, A.K);
     XNN_LAUNCH_CHECK();
   }
@@ -893,7 +965,8 @@ static int atm_check(int64_t E, int64_t N, int64_t max_tiles, const double* vec,
                      int32_t S, const xnn_atm_params* prm, const void* plan, void* work,
                      size_t work_bytes, bool bwd) {
   XNN_REQUIRE(E >= 0 && N >= 0 && max_tiles >= 0, "negative size");
-  XNN_REQUIRE(E <= 0x7fffffff && N < 0x7fffffff, "ATM: at most 2^31 - 1 edges and atoms");
+  XNN_REQUIRE(E <= 0x7fffffff && N < (1 << kAtmNbBits),
+              "ATM: at most 2^31 - 1 edges and 2^26 - 1 atoms");
   XNN_REQUIRE(K >= 1 && K <= kAtmMaxK, "ATM: the C6 factors need 1 to %d components (got %d)",
               kAtmMaxK, (int)K);
   XNN_REQUIRE(S >= 1 && S <= kAtmMaxSpecies, "ATM: 1 to %d species (got %d)", kAtmMaxSpecies,
@@ -923,8 +996,8 @@ int xnn_atm_plan_size(int64_t n_edges, int64_t n_atoms, size_t* bytes) {
 int xnn_atm_plan(const int64_t* edge_index, int64_t n_edges, int64_t n_atoms, void* plan,
                  size_t plan_bytes, int64_t* info, xnn_stream_t stream) {
   XNN_REQUIRE(n_edges >= 0 && n_atoms >= 0, "negative size");
-  XNN_REQUIRE(n_edges <= 0x7fffffff && n_atoms < 0x7fffffff,
-              "ATM: at most 2^31 - 1 edges and atoms");
+  XNN_REQUIRE(n_edges <= 0x7fffffff && n_atoms < (1 << kAtmNbBits),
+              "ATM: at most 2^31 - 1 edges and 2^26 - 1 atoms");
   XNN_REQUIRE(plan != nullptr && info != nullptr, "NULL plan or info");
   XNN_REQUIRE(n_edges == 0 || edge_index != nullptr, "NULL edge_index");
   const AtmPlanLayout L = atm_plan_layout(n_edges, n_atoms);
