@@ -138,6 +138,57 @@ def test_radius_graph_edge_cases():
         xa.build_neighbor_list(bad, 3.0)
 
 
+def test_neighbor_list_capacity_mode_eager_and_captured():
+    """The capacity mode (grid_pairs.py:414-499 semantics): the edges of the ordinary list
+    in the first n_edges entries, the rest repeating the first edge, n_edges on the device
+    and above the capacity when the list does not fit; a call captured in a HIP graph and
+    replayed on moved positions (eager work between replays) equals the ordinary list of
+    those positions, periodic and molecular (atoms moving within the planned margin)."""
+    import xnn_amd as xa
+    from xnn_amd import synthetic
+    from oracle.nl import canonical
+    _note("neighbor list capacity mode")
+    s = synthetic.water_box(n_molecules=216, box=18.6, grid=6, seed=5)
+    rng = np.random.default_rng(11)
+    for periodic in (True, False):
+        pos0 = torch.tensor(s.pos, dtype=torch.float64, device=DEV)
+        cell = torch.tensor(s.cell, dtype=torch.float64, device=DEV) if periodic else None
+        pbc = torch.tensor(s.pbc) if periodic else None
+        ei, sh = xa.build_neighbor_list(pos0, 5.0, cell, pbc)
+        E = ei.shape[1]
+        plan = xa.NeighborListPlan(pos0, 5.0, cell, pbc, margin=1.0)
+        e2, s2, m = plan(pos0, E + 37)
+        assert int(m) == E
+        assert np.array_equal(canonical(e2[:, :E].cpu().numpy(), s2[:E].cpu().numpy()),
+                              canonical(ei.cpu().numpy(), sh.cpu().numpy()))
+        assert bool((e2[:, E:] == e2[:, :1]).all()) and bool((s2[E:] == s2[:1]).all())
+        _, _, m_small = plan(pos0, E - 100)
+        assert int(m_small) == E
+        # captured: the static positions buffer is refilled before every replay
+        cap = E + 2000
+        pos_static = pos0.clone()
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            for _ in range(2):
+                plan(pos_static, cap)
+        torch.cuda.current_stream().wait_stream(side)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            out = plan(pos_static, cap)
+        for k in range(3):
+            moved = pos0 + torch.tensor(rng.normal(0.0, 0.15, s.pos.shape), device=DEV)
+            pos_static.copy_(moved)
+            graph.replay()
+            torch.cuda.synchronize()
+            ref_ei, ref_sh = xa.build_neighbor_list(moved, 5.0, cell, pbc)   # eager work
+            torch.cuda.synchronize()
+            n = int(out[2])
+            assert n == ref_ei.shape[1] <= cap, (periodic, k)
+            assert np.array_equal(canonical(out[0][:, :n].cpu().numpy(), out[1][:n].cpu().numpy()),
+                                  canonical(ref_ei.cpu().numpy(), ref_sh.cpu().numpy())), (periodic, k)
+
+
 def test_unique_pairs_on_the_gpu_equal_the_cpu_pairs():
     """unique_pairs from the HIP cell list: the CPU formulation's pairs, sorted by the first
     atom (test_neighborlist_backends.py:156-174), for positions inside the cell or not."""

@@ -6,7 +6,7 @@ CSR edge -> atom sums -> forces and virial by a CSR reduction, behind the
 reference's module and function interfaces.
 """
 from . import _lib
-from .data import (AtomicGraph, batched_neighbor_list, build_neighbor_list, collate,
+from .data import (AtomicGraph, NeighborListPlan, batched_neighbor_list, build_neighbor_list, collate,
                    half_list, structure_to_graph, unique_pairs)
 from .fast import AutoPolicy, FastPathModule, MI355X_POLICY, select, set_use_fast
 from .featurizers import (BesselRBF, CosineCutoff, GaussianRBF, PolynomialCutoff,
@@ -17,7 +17,7 @@ from .models import (InteratomicPotential, ModelConfig, ShEdgePotential, build_m
 from .outputs import ForceStressOutput
 
 __all__ = [
-    "AtomicGraph", "build_neighbor_list", "batched_neighbor_list", "structure_to_graph", "collate",
+    "AtomicGraph", "NeighborListPlan", "build_neighbor_list", "batched_neighbor_list", "structure_to_graph", "collate",
     "half_list", "unique_pairs",
     "AutoPolicy", "FastPathModule", "MI355X_POLICY", "select", "set_use_fast",
     "BesselRBF", "GaussianRBF", "CosineCutoff", "PolynomialCutoff",

@@ -241,16 +241,108 @@ def _radius_graph_cuda(pos: Tensor, cutoff: float, cell: Optional[Tensor], pbc: 
     return edge_index, cell_shifts
 
 
+class NeighborListPlan:
+    """The HIP cell list of :func:`build_neighbor_list` planned once, for positions that
+    move inside a fixed cell (or, on non-periodic axes, inside the range of ``pos`` widened
+    by ``margin``, default the cutoff; atoms beyond it are still found, in the boundary
+    bins). ``plan(pos, capacity)`` then makes no host reads: it writes the edges into
+    buffers of ``capacity`` entries and returns their number on the device, so it can run
+    behind a step or inside a captured HIP graph (the reference's capacity mode,
+    grid_pairs.py:414-499). The plan owns its workspace: calls on one plan must not
+    overlap."""
+
+    def __init__(self, pos: Tensor, cutoff: float, cell: Optional[Tensor] = None,
+                 pbc: Optional[Tensor] = None, self_interaction: bool = False,
+                 margin: Optional[float] = None):
+        if not pos.is_cuda:
+            raise RuntimeError("NeighborListPlan runs on the GPU")
+        dev = pos.device
+        n = int(pos.shape[0])
+        self.n, self.cutoff, self.dtype = n, float(cutoff), pos.dtype
+        self.self_interaction = bool(self_interaction)
+        margin = self.cutoff if margin is None else float(margin)
+        molecular = cell is None or pbc is None or not bool(pbc.any())
+        if not molecular and max(_supercell_reps(cell, cutoff, pbc)) > 1:
+            raise ValueError("capacity mode needs periodic interplanar spacings of at least a "
+                             "third of the cutoff")
+        pbc_list = [0, 0, 0] if molecular else [int(bool(b)) for b in pbc.reshape(-1).tolist()]
+        pbc_host = (ctypes.c_int32 * 3)(*pbc_list)
+        p64 = pos.detach().double()
+        if molecular:
+            lo_hi = torch.stack([p64.amin(0) - margin, p64.amax(0) + margin]).flatten().tolist()
+            cell_host, self.cell_dev = None, None
+        else:
+            cell64 = cell.reshape(3, 3).detach().double().cpu()
+            inv = torch.linalg.inv(cell64)
+            spacing = 1.0 / torch.linalg.norm(inv.T, dim=1)
+            frac = p64 @ inv.to(dev)
+            widen = (margin / spacing).to(dev)
+            lo_hi = torch.stack([frac.amin(0) - widen, frac.amax(0) + widen]).flatten().tolist()
+            cell_host = (_lib.dbl * 9)(*cell64.flatten().tolist())
+            self.cell_dev = cell.reshape(3, 3).detach().to(device=dev, dtype=pos.dtype).contiguous()
+        if n > 0:
+            _check_finite(lo_hi)
+        self.grid = _lib.GridPlan()
+        if n > 0:
+            _lib.check("xnn_radius_graph_plan",
+                       _lib.load().xnn_radius_graph_plan(n, cell_host, pbc_host, self.cutoff,
+                                                         (_lib.dbl * 3)(*lo_hi[:3]),
+                                                         (_lib.dbl * 3)(*lo_hi[3:]),
+                                                         ctypes.byref(self.grid)))
+        self.ws = torch.empty(max(1, int(self.grid.workspace_bytes)), dtype=torch.uint8, device=dev)
+        self.row_ptr = torch.zeros(n + 1, dtype=torch.int32, device=dev)
+
+    def __call__(self, pos: Tensor, capacity: int) -> tuple[Tensor, Tensor, Tensor]:
+        """``(edge_index (2, capacity), cell_shifts (capacity, 3), n_edges (1,))``: the
+        edges of :func:`build_neighbor_list` (grouped by receiver) in the first
+        ``n_edges`` entries, the rest repeating the first edge; ``n_edges`` above
+        ``capacity`` means the list did not fit (the entries hold its first
+        ``capacity`` edges)."""
+        if pos.shape[0] != self.n or pos.dtype != self.dtype or not pos.is_cuda:
+            raise ValueError(f"the plan is for {self.n} atoms in {self.dtype} on a GPU")
+        dev = pos.device
+        cap = int(capacity)
+        if cap < 1:
+            raise ValueError("capacity must be positive")
+        pos = pos.detach().contiguous()
+        edge_index = torch.zeros((2, cap), dtype=torch.long, device=dev)
+        cell_shifts = torch.zeros((cap, 3), dtype=torch.long, device=dev)
+        if self.n == 0:
+            return edge_index, cell_shifts, torch.zeros(1, dtype=torch.long, device=dev)
+        src = torch.empty(cap, dtype=torch.int32, device=dev)
+        dst = torch.empty(cap, dtype=torch.int32, device=dev)
+        shift = torch.empty(cap, dtype=torch.int32, device=dev)
+        geom = _lib.dtype_code(pos.dtype)
+        s = _lib.stream(dev)
+        si = int(self.self_interaction)
+        _lib.call("xnn_radius_graph_count", geom, _lib.ptr(pos), self.n, _lib.ptr(self.cell_dev),
+                  self.cutoff, si, ctypes.byref(self.grid), _lib.ptr(self.ws),
+                  _lib.ptr(self.row_ptr), s)
+        _lib.call("xnn_radius_graph_fill", geom, _lib.ptr(pos), self.n, _lib.ptr(self.cell_dev),
+                  self.cutoff, si, ctypes.byref(self.grid), _lib.ptr(self.ws),
+                  _lib.ptr(self.row_ptr), cap, _lib.ptr(src), _lib.ptr(dst), _lib.ptr(shift),
+                  _lib.ptr(edge_index), _lib.ptr(cell_shifts), None, s)
+        n_edges = self.row_ptr[self.n:].to(torch.long)
+        pad = torch.arange(cap, device=dev) >= n_edges
+        edge_index = torch.where(pad[None, :], edge_index[:, :1], edge_index)
+        cell_shifts = torch.where(pad[:, None], cell_shifts[:1], cell_shifts)
+        return edge_index, cell_shifts, n_edges
+
+
 def build_neighbor_list(pos: Tensor, cutoff: float, cell: Optional[Tensor] = None,
-                        pbc: Optional[Tensor] = None,
-                        self_interaction: bool = False) -> tuple[Tensor, Tensor]:
+                        pbc: Optional[Tensor] = None, self_interaction: bool = False,
+                        capacity: Optional[int] = None) -> tuple:
     """Radius graph of one structure: ``(edge_index (2, E) [src, dst], cell_shifts (E, 3))``.
 
     Same edge set and conventions as the reference (neighborlist.py:411-506): pairs with
     ``dist < cutoff`` in the positions' dtype, ``dst`` = receiver, shifts negated and
     re-expressed for unwrapped positions, self-edges only with ``self_interaction``.
-    On a GPU the edges come grouped by receiver (the order the kernels walk).
+    On a GPU the edges come grouped by receiver (the order the kernels walk). With
+    ``capacity`` (GPU): fixed-size buffers and the edge count on the device, see
+    :class:`NeighborListPlan` (keep the plan to repeat the call without host reads).
     """
+    if capacity is not None:
+        return NeighborListPlan(pos, cutoff, cell, pbc, self_interaction)(pos, capacity)
     if pos.is_cuda:
         return _radius_graph_cuda(pos, cutoff, cell, pbc, self_interaction)
     return _brute_force_cpu(pos, cutoff, cell, pbc, self_interaction)
