@@ -112,8 +112,7 @@ class ForceStressOutput(nn.Module):
             if (not create_graph and bool(getattr(self.model, "energy_is_node_sum", False))
                     and node_energy is not None and node_energy.requires_grad):
                 target = node_energy
-                seed = torch.full((1,), -1.0, dtype=node_energy.dtype,
-                                  device=node_energy.device).expand(node_energy.shape)
+                seed = _minus_one(node_energy).expand(node_energy.shape)
             else:
                 seed = torch.full_like(energy, -1.0)
             grads = torch.autograd.grad([target], inputs, grad_outputs=[seed],
@@ -126,6 +125,21 @@ class ForceStressOutput(nn.Module):
             out["stress"] = (_stress(g["strain"], data, scale=-1.0, differentiable=create_graph)
                              if g.get("strain") is not None else torch.zeros_like(strain))
         return out
+
+
+_MINUS_ONE = {}
+
+
+def _minus_one(like: Tensor) -> Tensor:
+    """A (1,) tensor of -1 on ``like``'s device and dtype, made once outside graph capture
+    (a captured step then reads it instead of launching a fill)."""
+    key = (like.device, like.dtype)
+    t = _MINUS_ONE.get(key)
+    if t is None:
+        t = torch.full((1,), -1.0, dtype=like.dtype, device=like.device)
+        if not (like.is_cuda and torch.cuda.is_current_stream_capturing()):
+            _MINUS_ONE[key] = t
+    return t
 
 
 def _layout(data):
