@@ -534,7 +534,7 @@ int xnn_node_readout_backward(int dtype, const void* g, int64_t g_stride, int64_
 /* Axilrod-Teller-Muto three-body dispersion (D4 and D3) over an edge list. Edges
  * edge_index (2,E) int64 [src; dst] within the three-body cutoff, both directions of
  * every pair and image; vectors edge_vec (E,3) float64 in bohr. Pair C6 of atoms x, y is
- * <feat_a[x], feat_b[y]> over k <= 28 components (feat_a, feat_b (N,k) float64; D4:
+ * <feat_a[x], feat_b[y]> over k <= 32 components (feat_a, feat_b (N,k) float64; D4:
  * alpha(i w) sqrt(3 cp_w / pi)); the damping radius of a triangle is the product of the
  * three table[species, species] factors (table (S,S) float64, S <= 32; species (N)
  * int32). Energy per triangle s9 C9 (3 cos cos cos + 1) / (r r r)^3 / (1 + 6 (R0 /

@@ -118,7 +118,7 @@ def _hip(c, same=False, s9=1.0, alp3=16.0 / 3.0, go=None):
 
 
 @pytest.mark.parametrize("system", list(SYSTEMS))
-@pytest.mark.parametrize("k,width_aa", [(23, 1.0), (28, 0.0), (7, 1.0)])
+@pytest.mark.parametrize("k,width_aa", [(23, 1.0), (28, 0.0), (7, 1.0), (32, 1.0)])
 def test_atm_matches_the_oracle(system, k, width_aa):
     print(f"[atm] {system} k={k} width={width_aa}", flush=True)
     c = _case(system, k=k, width_aa=width_aa)

@@ -28,7 +28,7 @@
 // first. Repeated-atom triangles: one wave per flagged center, lanes over its edges,
 // each lane walking the few later edges that share an atom with its own.
 //
-// Pair C6 = <fa[x], fb[y]> over K <= 28 components (held per lane for j); the damping
+// Pair C6 = <fa[x], fb[y]> over K <= 32 components (held per lane for j); the damping
 // radius is the product of three species-pair factors. Energies in hartree, lengths in
 // bohr.
 #include <hipcub/hipcub.hpp>
@@ -44,7 +44,7 @@ namespace xnn {
 
 constexpr int kAtmTile = 64;          // upper edges per item, one per lane
 constexpr int kAtmWaves = 4;          // waves (centers) per block
-constexpr int kAtmMaxK = 28;          // C6 factor components
+constexpr int kAtmMaxK = 32;          // C6 factor components
 constexpr int kAtmMaxSpecies = 32;    // side of the damping-radius factor table
 constexpr double kAtmEps = 2.220446049250313e-16;   // lower bound on r_jk^2 (dispersion.py:200)
 
@@ -179,19 +179,19 @@ static const T* at_off(const void* base, size_t off) {
 }
 
 // ------------------------------------------------------------------------------ plan
-__global__ void atm_fill_i32_kernel(int32_t* __restrict__ p, int64_t n) {
+__global__ __launch_bounds__(256) void atm_fill_i32_kernel(int32_t* __restrict__ p, int64_t n) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i < n) p[i] = 0;
 }
 
-__global__ void atm_fill_f64_kernel(double* __restrict__ p, int64_t n) {
+__global__ __launch_bounds__(256) void atm_fill_f64_kernel(double* __restrict__ p, int64_t n) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i < n) p[i] = 0.0;
 }
 
 // key = center * N + neighbor; an index out of range gets the sentinel N^2 (sorted last)
 // and raises the plan's error flag
-__global__ void atm_keys_kernel(const int64_t* __restrict__ ei, int64_t E, int64_t N,
+__global__ __launch_bounds__(256) void atm_keys_kernel(const int64_t* __restrict__ ei, int64_t E, int64_t N,
                                 uint64_t* __restrict__ keys, int32_t* __restrict__ vals,
                                 int32_t* __restrict__ stats) {
   const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -221,7 +221,7 @@ __device__ inline int64_t atm_lower_bound(const uint64_t* __restrict__ keys, int
 
 // neighbor of every sorted edge; a center with two edges to images of one neighbor has
 // repeated-atom triangles
-__global__ void atm_neighbors_kernel(const uint64_t* __restrict__ keys, int64_t E, int64_t N,
+__global__ __launch_bounds__(256) void atm_neighbors_kernel(const uint64_t* __restrict__ keys, int64_t E, int64_t N,
                                      int32_t* __restrict__ nbr, int32_t* __restrict__ ctr,
                                      uint64_t* __restrict__ keys2, int32_t* __restrict__ vals2,
                                      int32_t* __restrict__ flag, int32_t* __restrict__ stats) {
@@ -243,7 +243,7 @@ __global__ void atm_neighbors_kernel(const uint64_t* __restrict__ keys, int64_t 
 
 // per-center ranges: [lo[c], lo1[c]) neighbors <= c, [lo1[c], lo[c+1]) neighbors > c; an
 // edge to the center's own image flags it; stats[0] = most tiles of upper edges
-__global__ void atm_rows_kernel(const uint64_t* __restrict__ keys, int64_t E, int64_t N,
+__global__ __launch_bounds__(256) void atm_rows_kernel(const uint64_t* __restrict__ keys, int64_t E, int64_t N,
                                 int32_t* __restrict__ lo, int32_t* __restrict__ lo1,
                                 int32_t* __restrict__ flag, int32_t* __restrict__ stats) {
   const int64_t c = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -264,7 +264,7 @@ __global__ void atm_rows_kernel(const uint64_t* __restrict__ keys, int64_t E, in
 }
 
 // lo_src[j]: first by-source position of neighbor j
-__global__ void atm_src_rows_kernel(const uint64_t* __restrict__ keys2, int64_t E, int64_t N,
+__global__ __launch_bounds__(256) void atm_src_rows_kernel(const uint64_t* __restrict__ keys2, int64_t E, int64_t N,
                                     int32_t* __restrict__ lo_src) {
   const int64_t j = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (j > N) return;
@@ -273,7 +273,7 @@ __global__ void atm_src_rows_kernel(const uint64_t* __restrict__ keys2, int64_t 
 
 // ------------------------------------------------------------------------------ records
 template <int KP>
-__global__ void atm_pad_kernel(const double* __restrict__ f, int64_t N, int K,
+__global__ __launch_bounds__(256) void atm_pad_kernel(const double* __restrict__ f, int64_t N, int K,
                                double* __restrict__ out) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= N * KP) return;
@@ -283,7 +283,7 @@ __global__ void atm_pad_kernel(const double* __restrict__ f, int64_t N, int K,
 }
 
 template <int KP>
-__global__ void atm_edges_kernel(const uint64_t* __restrict__ keys,
+__global__ __launch_bounds__(256) void atm_edges_kernel(const uint64_t* __restrict__ keys,
                                  const int32_t* __restrict__ perm,
                                  const int32_t* __restrict__ nbr, int64_t E, int64_t N,
                                  const double* __restrict__ vec, const double* __restrict__ fa,
@@ -333,7 +333,7 @@ __global__ void atm_edges_kernel(const uint64_t* __restrict__ keys,
 }
 
 // the walk-ordered copy of the records
-__global__ void atm_walk_order_kernel(const AtmEdge* __restrict__ rec,
+__global__ __launch_bounds__(256) void atm_walk_order_kernel(const AtmEdge* __restrict__ rec,
                                       const int32_t* __restrict__ sperm, int64_t E,
                                       AtmEdge* __restrict__ rec_up) {
   const int64_t q = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -724,7 +724,7 @@ __global__ __launch_bounds__(kAtmWaves * kWave) void atm_repeat_kernel(
 }
 
 // grad_vec[original edge] = the sorted edge's vector gradient
-__global__ void atm_vec_grad_kernel(const int32_t* __restrict__ perm,
+__global__ __launch_bounds__(256) void atm_vec_grad_kernel(const int32_t* __restrict__ perm,
                                     const double* __restrict__ gs, int64_t E,
                                     double* __restrict__ gvec) {
   const int64_t p = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -850,7 +850,7 @@ static AtmConst atm_const(const xnn_atm_params* prm) {
   return k;
 }
 
-static int atm_kp(int K) { return K <= 24 ? 24 : 28; }
+static int atm_kp(int K) { return K <= 24 ? 24 : (K <= 28 ? 28 : 32); }
 
 static void atm_zero(double* p, int64_t n, hipStream_t s) {
   if (n > 0) hipLaunchKernelGGL(atm_fill_f64_kernel, dim3(grid_1d(n, 256)), dim3(256), 0, s, p, n);
@@ -957,7 +957,9 @@ static int atm_dispatch(const AtmArgs& A) {
   const bool p16 = fabs(A.kc.alp3 - 16.0 / 3.0) < 1e-12;
   if (atm_kp(A.K) == 24)
     return p16 ? atm_dispatch_sw<24, BWD, true>(A) : atm_dispatch_sw<24, BWD, false>(A);
-  return p16 ? atm_dispatch_sw<28, BWD, true>(A) : atm_dispatch_sw<28, BWD, false>(A);
+  if (atm_kp(A.K) == 28)
+    return p16 ? atm_dispatch_sw<28, BWD, true>(A) : atm_dispatch_sw<28, BWD, false>(A);
+  return p16 ? atm_dispatch_sw<32, BWD, true>(A) : atm_dispatch_sw<32, BWD, false>(A);
 }
 
 static int atm_check(int64_t E, int64_t N, int64_t max_tiles, const double* vec, const double* fa,

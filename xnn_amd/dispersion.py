@@ -380,7 +380,7 @@ def atm_energy(edge_index: Tensor, edge_vec: Tensor, feat_a: Tensor, feat_b: Ten
     """Per-atom ATM energies (N,) in hartree with the HIP kernels
     (dispersion_fast/atm.py:512-535): ``edge_index`` (2, E) ``[src, dst]`` within the
     three-body cutoff, both directions of every pair; ``edge_vec`` (E, 3) in bohr;
-    ``feat_a``, ``feat_b`` (N, K <= 28) with pair C6 = <feat_a[x], feat_b[y]> (may be the
+    ``feat_a``, ``feat_b`` (N, K <= 32) with pair C6 = <feat_a[x], feat_b[y]> (may be the
     same tensor). Differentiable once in ``edge_vec``, ``feat_a`` and ``feat_b``; float64
     throughout; GPU only."""
     if not edge_vec.is_cuda:
@@ -1061,9 +1061,9 @@ class DFTD3(nn.Module):
                    pbc: Optional[Tensor], counts: List[int]) -> Tensor:
         """Per-atom ATM energies (hartree, d3.py:916-936) on the HIP triplet kernels."""
         f, g, uniq, spec = self.c6_factors(s, w)
-        if f.shape[1] > 28:
+        if f.shape[1] > 32:
             raise NotImplementedError(
-                f"the D3 ATM term takes at most 28 reference slots over the elements present "
+                f"the D3 ATM term takes at most 32 reference slots over the elements present "
                 f"(these have {f.shape[1]}); set s9 = 0")
         edge_index, vec = triple_graph(pos, cell64, pbc, counts, self.cutoff_triple)
         table = D3_RS9 * self.rvdw[uniq][:, uniq]
