@@ -327,8 +327,9 @@ FP64_PEAK_TFLOPS = 78.6
 def bench_d4(steps: int, warmup: int, cpu: bool = True) -> dict:
     """D4 two-body energy + forces + stress of the 5,000-atom organic box (36.8 A cell,
     upstream cutoffs 60 / 30 / 25 bohr): CN kernel, polarizabilities, pair kernel and
-    both backward kernels per step. The charges are fixed (zero): the dense periodic
-    charge solve of 5,000 atoms is not part of this path."""
+    both backward kernels per step. The charges come from the PyTorch EEQ solve (dense
+    Ewald matrix, formed in row chunks) once, outside the timed steps, as the survey's
+    configuration specifies."""
     import xnn_amd.dispersion as XD
     from xnn_amd import _lib, synthetic
     dev = torch.device("cuda:0")
@@ -340,7 +341,12 @@ def bench_d4(steps: int, warmup: int, cpu: bool = True) -> dict:
     cell0 = torch.tensor(s.cell, dtype=torch.float64, device=dev)[None]
     pbc = torch.ones((1, 3), dtype=torch.bool)
     n_atoms = torch.tensor([len(s.numbers)])
-    q = torch.zeros(len(s.numbers), dtype=torch.float64, device=dev)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    with torch.no_grad():
+        q = model.evaluate(z, pos0, cell0, pbc, n_atoms)["charges"].detach()
+    torch.cuda.synchronize()
+    eeq_ms = (time.perf_counter() - t0) * 1e3
 
     def step():
         pos = pos0.clone().requires_grad_(True)
@@ -402,7 +408,8 @@ def bench_d4(steps: int, warmup: int, cpu: bool = True) -> dict:
                          "pair_image_terms": n_terms, "cn_terms": n_cn,
                          "cutoff_pair_bohr": 60.0, "cutoff_cn_bohr": 30.0,
                          "cutoff_eeq_cn_bohr": 25.0,
-                         "charges": "fixed zero (charge model not timed)",
+                         "charges": "EEQ (dense Ewald, PyTorch), once, outside the timed steps",
+                         "eeq_ms": round(eeq_ms, 1), "charge_abs_max": float(q.abs().max()),
                          "energy_eV": float(e[0]),
                          "kernel_mean_us": {k: round(v, 2) for k, v in kernel_us.items()}},
               "roofline": roofline}

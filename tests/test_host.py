@@ -165,3 +165,42 @@ def test_d4_polarizability_tables_and_argument_checks(lib_path):
     assert b"bias and z" in lib.xnn_last_error()
     assert lib.xnn_node_readout_backward(0, 1, 2, 4, 8, 1, 1, None) == _lib.XNN_EINVAL
     assert b"g_stride" in lib.xnn_last_error()
+
+
+def test_periodic_eeq_rows_in_chunks_equal_one_pass():
+    """The Ewald EEQ matrix formed in row chunks (bounded memory for thousands of atoms)
+    equals the one-pass matrix bit for bit, and its position and cell gradients through the
+    recomputed (checkpointed) chunks equal the direct ones. CPU, float64."""
+    import math as _m
+    import xnn_amd.dispersion as XD
+    tables = XD.load_d4_tables(os.path.join(os.path.dirname(__file__), "golden",
+                                            "d4_tables_hcnoar.npz"))
+    d4 = XD.DFTD4(tables)
+    rng = np.random.default_rng(3)
+    cell = torch.tensor([[9.0, 0.0, 0.0], [1.2, 8.5, 0.0], [-0.7, 0.9, 10.0]], dtype=torch.float64)
+    pos = torch.tensor(rng.uniform(0, 1, (11, 3)), dtype=torch.float64) @ cell
+    z = torch.tensor([8, 1, 1, 6, 1, 7, 8, 1, 6, 6, 1])
+    rad = d4.eeq_rad[z]
+    vol = torch.linalg.det(cell).abs()
+    recip = 2.0 * _m.pi * torch.linalg.inv(cell).t()
+    a = XD._ewald_alpha(float(torch.linalg.norm(recip, dim=1).min()),
+                        float(torch.linalg.norm(cell, dim=1).min()), float(vol))
+    whole = XD._ewald_rows(0, 11, a, pos, cell, vol, recip, rad)
+    split = torch.cat([XD._ewald_rows(0, 4, a, pos, cell, vol, recip, rad),
+                       XD._ewald_rows(4, 9, a, pos, cell, vol, recip, rad),
+                       XD._ewald_rows(9, 11, a, pos, cell, vol, recip, rad)])
+    assert torch.equal(whole, split)
+    assert torch.allclose(whole, whole.t(), rtol=1e-12, atol=1e-14)
+    p1, c1 = pos.clone().requires_grad_(True), cell.clone().requires_grad_(True)
+    A = d4._coulomb_periodic(z, p1, c1)                   # checkpointed chunks
+    w = torch.tensor(rng.normal(size=(11, 11)))
+    g1 = torch.autograd.grad((A * w).sum(), [p1, c1])
+    p2, c2 = pos.clone().requires_grad_(True), cell.clone().requires_grad_(True)
+    vol2 = torch.linalg.det(c2).abs()
+    recip2 = 2.0 * _m.pi * torch.linalg.inv(c2).t()
+    B = XD._ewald_rows(0, 11, a, p2, c2, vol2, recip2, rad)
+    B = B + torch.diag(d4.eeq_eta[z] + _m.sqrt(2.0 / _m.pi) / rad - 2.0 * a / _m.sqrt(_m.pi))
+    g2 = torch.autograd.grad((B * w).sum(), [p2, c2])
+    assert torch.equal(A.detach(), B.detach())
+    for x, y in zip(g1, g2):
+        assert torch.allclose(x, y, rtol=1e-12, atol=1e-15)

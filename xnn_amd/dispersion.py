@@ -395,6 +395,42 @@ def atm_energy(edge_index: Tensor, edge_vec: Tensor, feat_a: Tensor, feat_b: Ten
                           float(consts.width)], int(n_atoms), info[0], info[1])
 
 
+def _ewald_rows(i0: int, i1: int, a: float, pos: Tensor, cell: Tensor, vol: Tensor,
+                recip: Tensor, rad: Tensor) -> Tensor:
+    """Rows i0..i1 of the off-diagonal Ewald EEQ matrix (d4.py:608-680), see
+    ``DFTD4._coulomb_periodic``."""
+    n, dev, dt = pos.shape[0], pos.device, pos.dtype
+    one = torch.arange(-1, 2, device=dev)
+    t27 = torch.cartesian_prod(one, one, one).to(dt) @ cell
+    two = torch.arange(-EWALD_REP, EWALD_REP + 1, device=dev)
+    grid = torch.cartesian_prod(two, two, two)
+    t125 = grid.to(dt) @ cell
+    g = grid[(grid != 0).any(1)].to(dt) @ recip
+    g2 = (g * g).sum(-1)
+    gfac = 4.0 * math.pi / vol * torch.exp(-0.25 * g2 / (a * a)) / g2
+    m = i1 - i0
+    gamma = torch.rsqrt(rad[i0:i1, None] ** 2 + rad[None, :] ** 2)
+    d = pos[None, :, :] - pos[i0:i1, None, :]
+    d = d - torch.round(d.detach() @ torch.linalg.inv(cell.detach())) @ cell
+    dimg = d[:, :, None, :] + t27[None, None]
+    r2 = (dimg * dimg).sum(-1)
+    thr = 1.4901161193847656e-08
+    r2 = torch.where(r2 < thr, torch.full_like(r2, math.inf), r2)
+    sel = (r2 - r2.min(-1, keepdim=True).values) <= WS_TOL
+    nimg = sel.sum(-1).to(dt)
+    ii, jj, kk = torch.nonzero(sel, as_tuple=True)
+    vec = dimg[ii, jj, kk]
+    vt = vec[:, None, :] + t125[None]
+    rt2 = (vt * vt).sum(-1)
+    keep = rt2 >= thr * thr
+    rs = torch.sqrt(torch.where(keep, rt2, torch.ones_like(rt2)))
+    kern = (torch.erf(gamma[ii, jj][:, None] * rs) - torch.erf(a * rs)) / rs
+    adir = torch.where(keep, kern, torch.zeros_like(kern)).sum(-1)
+    arec = (torch.cos(vec @ g.t()) * gfac[None]).sum(-1)
+    return torch.zeros(m * n, dtype=dt, device=dev).index_add(
+        0, ii * n + jj, (adir + arec) / nimg[ii, jj]).view(m, n)
+
+
 # --------------------------------------------------------------------------- host pieces
 def image_counts(cell: Tensor, pbc: Optional[Tensor], cutoff_aa: float) -> Tensor:
     """Translations per axis that cover ``cutoff_aa`` from the interplanar spacing
@@ -521,41 +557,26 @@ class DFTD4(nn.Module):
         """Ewald-summed EEQ matrix over Wigner-Seitz images (d4.py:608-680): every pair
         vector is represented by its minimum-distance image(s) within +-1 cells (ties
         within 0.01 bohr^2 averaged), summed over +-2 cells in real space with the
-        erf(gamma r)/r - erf(a r)/r kernel and over +-2 reciprocal cells."""
+        erf(gamma r)/r - erf(a r)/r kernel and over +-2 reciprocal cells. Rows are formed in
+        chunks of bounded memory (about 1 GB of temporaries each, so thousands of atoms
+        fit), recomputed in the backward when positions or cell need gradients."""
         n, dev, dt = pos.shape[0], pos.device, pos.dtype
         vol = torch.linalg.det(cell).abs()
         recip = 2.0 * math.pi * torch.linalg.inv(cell).t()
         a = _ewald_alpha(float(torch.linalg.norm(recip, dim=1).min()),
                          float(torch.linalg.norm(cell, dim=1).min()), float(vol))
-        one = torch.arange(-1, 2, device=dev)
-        t27 = torch.cartesian_prod(one, one, one).to(dt) @ cell
-        two = torch.arange(-EWALD_REP, EWALD_REP + 1, device=dev)
-        grid = torch.cartesian_prod(two, two, two)
-        t125 = grid.to(dt) @ cell
-        g = grid[(grid != 0).any(1)].to(dt) @ recip
-        g2 = (g * g).sum(-1)
-        gfac = 4.0 * math.pi / vol * torch.exp(-0.25 * g2 / (a * a)) / g2
         rad = self.eeq_rad[z]
-        gamma = torch.rsqrt(rad[:, None] ** 2 + rad[None, :] ** 2)
-        d = pos[None, :, :] - pos[:, None, :]
-        d = d - torch.round(d.detach() @ torch.linalg.inv(cell.detach())) @ cell
-        dimg = d[:, :, None, :] + t27[None, None]
-        r2 = (dimg * dimg).sum(-1)
-        thr = 1.4901161193847656e-08
-        r2 = torch.where(r2 < thr, torch.full_like(r2, math.inf), r2)
-        sel = (r2 - r2.min(-1, keepdim=True).values) <= WS_TOL
-        nimg = sel.sum(-1).to(dt)
-        ii, jj, kk = torch.nonzero(sel, as_tuple=True)
-        vec = dimg[ii, jj, kk]
-        vt = vec[:, None, :] + t125[None]
-        rt2 = (vt * vt).sum(-1)
-        keep = rt2 >= thr * thr
-        rs = torch.sqrt(torch.where(keep, rt2, torch.ones_like(rt2)))
-        kern = (torch.erf(gamma[ii, jj][:, None] * rs) - torch.erf(a * rs)) / rs
-        adir = torch.where(keep, kern, torch.zeros_like(kern)).sum(-1)
-        arec = (torch.cos(vec @ g.t()) * gfac[None]).sum(-1)
-        A = torch.zeros(n * n, dtype=dt, device=dev).index_add(
-            0, ii * n + jj, (adir + arec) / nimg[ii, jj]).view(n, n)
+        rows = max(1, int((1 << 30) // (8 * 3 * 125 * max(n, 1))))
+        parts = []
+        for i0 in range(0, n, rows):
+            i1 = min(n, i0 + rows)
+            args = (pos, cell, vol, recip, rad)
+            if torch.is_grad_enabled() and (pos.requires_grad or cell.requires_grad):
+                from torch.utils.checkpoint import checkpoint
+                parts.append(checkpoint(_ewald_rows, i0, i1, a, *args, use_reentrant=False))
+            else:
+                parts.append(_ewald_rows(i0, i1, a, *args))
+        A = torch.cat(parts, 0) if parts else pos.new_zeros((0, 0))
         return A + torch.diag(self.eeq_eta[z] + math.sqrt(2.0 / math.pi) / rad
                               - 2.0 * a / math.sqrt(math.pi))
 
