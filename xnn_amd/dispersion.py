@@ -563,8 +563,9 @@ class DFTD4(nn.Module):
         n, dev, dt = pos.shape[0], pos.device, pos.dtype
         vol = torch.linalg.det(cell).abs()
         recip = 2.0 * math.pi * torch.linalg.inv(cell).t()
-        a = _ewald_alpha(float(torch.linalg.norm(recip, dim=1).min()),
-                         float(torch.linalg.norm(cell, dim=1).min()), float(vol))
+        # the Ewald parameter is a constant of the evaluation (a search on the host)
+        a = _ewald_alpha(float(torch.linalg.norm(recip.detach(), dim=1).min()),
+                         float(torch.linalg.norm(cell.detach(), dim=1).min()), float(vol.detach()))
         rad = self.eeq_rad[z]
         rows = max(1, int((1 << 30) // (8 * 3 * 125 * max(n, 1))))
         parts = []
