@@ -495,9 +495,10 @@ def _ewald_alpha(rlen: float, dlen: float, vol: float) -> float:
 
 
 class DFTD4(nn.Module):
-    """Two-body D4 (PBE0-D4 defaults) on the GPU; ``evaluate`` takes a batch of
-    structures, ``forward`` an :class:`~xnn_amd.data.AtomicGraph`. Cutoffs in Angstrom
-    (defaults: the upstream 60 / 30 / 25 bohr for pair / CN / EEQ CN, d4.py:121-126)."""
+    """D4 (PBE0-D4 defaults: BJ two-body and the ATM three-body term, ``s9 = 1``) on the
+    GPU; ``evaluate`` takes a batch of structures, ``forward`` an
+    :class:`~xnn_amd.data.AtomicGraph`. Cutoffs in Angstrom (defaults: the upstream
+    60 / 40 / 30 / 25 bohr for pair / triple / CN / EEQ CN, d4.py:121-127)."""
 
     def __init__(self, tables: Dict[str, np.ndarray], s6: float = 1.0, s8: float = 1.20065498,
                  a1: float = 0.40085597, a2: float = 5.02928789, s9: float = 1.0,
@@ -789,7 +790,7 @@ class DispersionCorrection(nn.Module):
 
 
 class D4Dispersion(DispersionCorrection):
-    """D4 (two-body) dispersion as a potential, standalone or wrapped around a model
+    """D4 dispersion (two- and three-body) as a potential, standalone or wrapped around a model
     (d4.py:1321-1365). ``tables``: the per-element tables (dict or a path for
     :func:`load_d4_tables`); ``d4_options``: keyword arguments of :class:`DFTD4`."""
 
@@ -1098,8 +1099,8 @@ class DFTD3(nn.Module):
 
 
 class D3Dispersion(DispersionCorrection):
-    """D3 (two-body) dispersion as a potential, standalone or wrapped around a model
-    (d3.py:965-1016); ``tables``: dict or path for :func:`load_d3_tables`."""
+    """D3 dispersion (two-body; ATM with ``s9 != 0``) as a potential, standalone or wrapped
+    around a model (d3.py:965-1016); ``tables``: dict or path for :func:`load_d3_tables`."""
 
     def __init__(self, model: Optional[nn.Module] = None, tables=None, **d3_options):
         if tables is None:
