@@ -555,8 +555,12 @@ __global__ __launch_bounds__(kAtmWaves * kWave) void atm_upper_kernel(
   for (int w = 0; w < (BWD ? KP : 1); ++w) gfj[w] = 0.0;
   int n_ring = 0;
 
+  // the forward loads the walked edge's record one step ahead (its latency under the
+  // current step; measured 3 % faster there, 3 % slower in the register-bound backward)
+  AtmEdge eb_next = rec[a0 + 1];
   for (int32_t b = a0 + 1; b < hi; ++b) {
-    const AtmEdge eb = rec[b];                      // wave-uniform
+    const AtmEdge eb = BWD ? rec[b] : eb_next;      // wave-uniform
+    if (!BWD && b + 1 < hi) eb_next = rec[b + 1];
     const int32_t k = atm_nb(eb);
     const double dx = ax - eb.vx, dy = ay - eb.vy, dz = az - eb.vz;
     const double w2 = dx * dx + dy * dy + dz * dz;
