@@ -260,3 +260,42 @@ def test_stress_matches_finite_strain(tables):
     # forces too, and the wrapper's bookkeeping
     assert out["forces"].shape == (len(z), 3)
     assert torch.equal(out["energy_disp"], out["energy"])
+
+
+def test_periodic_three_body_matches_oracle(tables):
+    """The module's ATM term in a cell narrower than a third of its 16 A triple cutoff (its
+    radius graph through the replicated supercell): energy and position and cell gradients
+    against the oracle's CN -> neutral alpha(i w) -> edge-list ATM over brute-force images
+    (d4.py:1268-1298, dispersion.py:124-222), float64."""
+    import oracle.d4 as D
+    import xnn_amd.dispersion as XD
+    _note("d4 periodic ATM vs oracle")
+    pos, z = _cluster(4, seed=9, box=5.0)
+    cell = np.diag([5.0, 5.2, 5.4])
+    model = XD.DFTD4(tables, cutoff_pair=9.0, cutoff_cn=8.0, cutoff_eeq_cn=8.0,
+                     cutoff_triple=16.0).to(DEV)
+    q = torch.tensor(np.random.default_rng(2).normal(0, 0.2, len(z)), dtype=torch.float64)
+    out, p, c = _eval(model, pos, z, cell, charges=q.to(DEV), grad=True)
+    got = torch.autograd.grad(out["energy_3body"].sum(), [p, c])
+    cut3 = model.cutoff_triple / D.BOHR
+    dst, src, sh = D.pair_images(pos, cell, model.cutoff_triple)
+    pt = torch.tensor(pos, dtype=torch.float64, requires_grad=True)
+    ct = torch.tensor(cell, dtype=torch.float64, requires_grad=True)
+    v = D.edge_vectors_au(pt, ct, dst, src, sh)
+    r = torch.linalg.norm(v, dim=-1)
+    zt = torch.as_tensor(z)
+    n = len(z)
+    cn, _, _ = D.coordination_numbers(zt, dst, src, r, tables, 8.0 / D.BOHR, 8.0 / D.BOHR, n)
+    alpha0 = D.dynamic_polarizabilities(zt, cn, torch.zeros(n, dtype=torch.float64), tables)
+    feat = alpha0 * torch.sqrt((3.0 / math.pi) * torch.as_tensor(D.cp_weights()))
+    table, species = D.bj_radius_factors(zt, tables, model.a1, model.a2)
+    tri = r <= cut3
+    ei = torch.stack([torch.as_tensor(src), torch.as_tensor(dst)])[:, tri]
+    e3 = D.atm_edges(ei, v[tri], feat, feat, species, table, 1.0, 16.0 / 3.0, cut3, 0.0, n)
+    ref = torch.autograd.grad(e3.sum(), [pt, ct])
+    assert float(e3.sum()) > 0
+    assert abs(float(out["energy_3body"][0]) / XD.HARTREE - float(e3.sum())) \
+        < 1e-11 * float(e3.sum())
+    for a, b in zip(got, ref):
+        a = a.reshape(b.shape).detach().cpu() / XD.HARTREE
+        np.testing.assert_allclose(a, b, atol=1e-10 * float(b.abs().max()))
