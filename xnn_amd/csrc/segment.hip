@@ -694,10 +694,20 @@ __global__ __launch_bounds__(BLOCK) void flat_reduce_f64_kernel(const T* __restr
   const int64_t per_s = ((e1 - e0 + chunks - 1) / chunks + S - 1) / S;
   const int64_t c0 = min(e1, e0 + (int64_t)blockIdx.x * per_s * S);
   const int64_t c1 = min(e1, c0 + per_s * S);
-  double acc = 0.0;
-  if (t < S)
-    for (int64_t i = c0 + t; i < c1; i += S) acc += (double)src[i];
-  red[t] = acc;
+  // four independent sums per thread, so that four loads are in flight at a time (a
+  // single-block launch over a short array is otherwise a chain of load latencies)
+  double a0 = 0.0, a1 = 0.0, a2 = 0.0, a3 = 0.0;
+  if (t < S) {
+    int64_t i = c0 + t;
+    for (; i + 3 * (int64_t)S < c1; i += 4 * (int64_t)S) {
+      a0 += (double)src[i];
+      a1 += (double)src[i + S];
+      a2 += (double)src[i + 2 * (int64_t)S];
+      a3 += (double)src[i + 3 * (int64_t)S];
+    }
+    for (; i < c1; i += S) a0 += (double)src[i];
+  }
+  red[t] = (a0 + a1) + (a2 + a3);
   __syncthreads();
   for (int h = S / (int)F / 2; h > 0; h >>= 1) {
     if (t < h * F) red[t] += red[t + h * F];
