@@ -97,11 +97,14 @@ def _t(tables, key, dtype=torch.float64):
 
 
 # --------------------------------------------------------------------------- geometry
-def pair_images(pos: np.ndarray, cell: Optional[np.ndarray], cutoff: float):
+def pair_images(pos: np.ndarray, cell: Optional[np.ndarray], cutoff: float,
+                receivers: Optional[np.ndarray] = None):
     """Every ordered pair (dst i, src j) and lattice translation T with
     0 < |pos_i - pos_j + T| <= cutoff (Angstrom, float64, brute force over the image
-    range that covers the cutoff): arrays dst, src, shift (E, 3) int."""
+    range that covers the cutoff): arrays dst, src, shift (E, 3) int. ``receivers``
+    restricts dst to those atom indices (a sample of a large system)."""
     n = pos.shape[0]
+    rows = np.arange(n) if receivers is None else np.asarray(receivers, dtype=np.int64)
     if cell is None:
         rng = [np.zeros((1, 3), dtype=np.int64)]
         shifts = rng[0]
@@ -114,11 +117,11 @@ def pair_images(pos: np.ndarray, cell: Optional[np.ndarray], cutoff: float):
     dst, src, sh = [], [], []
     for s in shifts:
         t = s @ cell if cell is not None else np.zeros(3)
-        d = pos[:, None, :] - pos[None, :, :] + t
+        d = pos[rows, None, :] - pos[None, :, :] + t
         r = np.sqrt((d * d).sum(-1))
         ok = (r <= cutoff) & (r > 0)
         ii, jj = np.nonzero(ok)
-        dst.append(ii)
+        dst.append(rows[ii])
         src.append(jj)
         sh.append(np.repeat(s[None, :], len(ii), axis=0))
     return (np.concatenate(dst), np.concatenate(src), np.concatenate(sh).reshape(-1, 3))

@@ -1,0 +1,82 @@
+"""The periodic EEQ charges of ``xnn_amd.dispersion.DFTD4`` (dense regime: the Ewald
+matrix over Wigner-Seitz images and fixed +-2 windows of d4.py:608-680) pinned by what
+the physics fixes, on the CPU (float64):
+
+* a water molecule in ever larger vacuum cells tends to dftd4's molecular charges
+  (tests/common/test_d4.py:110-126); the remainder is the image-dipole term, which falls
+  as 1 / L^3, so the Richardson limit of two cells must equal the golden charges;
+* charges are unchanged by replicating the cell (a supercell is the same crystal), to the
+  convergence of the fixed +-2 windows at the search's splitting parameter (matrix
+  elements to sqrt(eps) relative, d4.py:183-224);
+* the charges sum to the structure's total charge.
+"""
+import os
+
+import numpy as np
+import pytest
+import torch
+
+import oracle.d4 as D
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+WATER = np.array([[0.0, 0.0, 0.119262], [0.0, 0.763239, -0.477047], [0.0, -0.763239, -0.477047]])
+GOLDEN_Q = np.array([-0.58639069, 0.29319534, 0.29319534])
+
+
+@pytest.fixture(scope="module")
+def d4():
+    import xnn_amd.dispersion as XD
+    return XD.DFTD4(XD.load_d4_tables(os.path.join(HERE, "golden", "d4_tables_hcnoar.npz")))
+
+
+def _tables():
+    return dict(np.load(os.path.join(HERE, "golden", "d4_tables_hcnoar.npz"), allow_pickle=False))
+
+
+def _cn_eeq(pos, cell, z):
+    """The capped EEQ coordination numbers from the oracle (d4.py:552-591), 25 bohr."""
+    dst, src, sh = D.pair_images(pos, cell, 25.0 * D.BOHR)
+    v = D.edge_vectors_au(torch.tensor(pos), None if cell is None else torch.tensor(cell), dst, src, sh)
+    _, cn_eeq, _ = D.coordination_numbers(torch.as_tensor(z), dst, src, torch.linalg.norm(v, dim=-1),
+                                          _tables(), 25.0, 25.0, len(z))
+    return cn_eeq
+
+
+def _charges(d4, pos, cell, z, total=0.0):
+    return d4.charges(torch.tensor(z), torch.tensor(pos) / D.BOHR, _cn_eeq(pos, cell, z), total,
+                      torch.tensor(cell) / D.BOHR).numpy()
+
+
+def test_vacuum_cell_limit_is_the_molecular_golden(d4):
+    q = {}
+    for L in (60.0, 120.0):
+        q[L] = _charges(d4, WATER + L / 2, np.eye(3) * L, [8, 1, 1])
+    # the finite-cell charges differ from the molecule's by the image-dipole term ~ L^-3
+    ratio = (q[60.0] - GOLDEN_Q) / (q[120.0] - GOLDEN_Q)
+    np.testing.assert_allclose(ratio, 8.0, rtol=0.02)
+    limit = (8.0 * q[120.0] - q[60.0]) / 7.0
+    np.testing.assert_allclose(limit, GOLDEN_Q, atol=1e-8)
+
+
+def test_supercell_replication_keeps_the_charges(d4):
+    rng = np.random.default_rng(3)
+    cell = np.array([[9.0, 0, 0], [1.2, 8.5, 0], [-0.7, 0.9, 10.0]])
+    pos = rng.uniform(0, 1, (11, 3)) @ cell
+    z = [8, 1, 1, 6, 1, 7, 8, 1, 6, 6, 1]
+    q1 = _charges(d4, pos, cell, z)
+    for rep in ((2, 1, 1), (1, 2, 2)):
+        reps = [pos + a * cell[0] + b * cell[1] + c * cell[2]
+                for a in range(rep[0]) for b in range(rep[1]) for c in range(rep[2])]
+        big = np.concatenate(reps)
+        q2 = _charges(d4, big, cell * np.array(rep)[:, None], z * len(reps))
+        np.testing.assert_allclose(q2.reshape(len(reps), 11), np.tile(q1, (len(reps), 1)), atol=1e-6)
+
+
+@pytest.mark.parametrize("total", [0.0, 1.0, -2.0])
+def test_charges_sum_to_the_total_charge(d4, total):
+    rng = np.random.default_rng(4)
+    cell = np.diag([8.0, 9.0, 7.5])
+    pos = rng.uniform(0, 1, (9, 3)) @ cell
+    z = [6, 1, 1, 8, 7, 1, 6, 1, 8]
+    q = _charges(d4, pos, cell, z, total)
+    assert abs(q.sum() - total) < 1e-12

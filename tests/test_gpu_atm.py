@@ -209,3 +209,34 @@ def test_atm_counts_match_a_direct_enumeration():
               c["cutoff"], counts, _lib.stream(dev))
     assert (counts[0], counts[1], counts[2]) == (tested, kept, repeated)
     assert repeated > 0 and kept > 0
+
+
+@pytest.mark.parametrize("shape", ["equilateral", "right_isosceles"])
+def test_atm_kernel_triangle_closed_forms(shape):
+    """One triangle of identical atoms through the HIP kernels: each corner gets a third of
+    s9 C6^(3/2) (3 cos a cos b cos c + 1) / (r1 r2 r3)^3 / (1 + 6 (R0^3 / (r1 r2 r3))^alp3)
+    -- the equilateral angular factor 3/8 + 1, the right angle's 1 -- with C6 = <f, f>."""
+    from xnn_amd import dispersion as XD
+    dev = torch.device("cuda:0")
+    a = 6.5
+    if shape == "equilateral":
+        pos = np.array([[0.0, 0, 0], [a, 0, 0], [a / 2, a * math.sqrt(3) / 2, 0]])
+        sides = (a, a, a)
+    else:
+        pos = np.array([[0.0, 0, 0], [a, 0, 0], [0, a, 0]])
+        sides = (a, a, a * math.sqrt(2))
+    f = torch.full((3, 23), 0.7, dtype=torch.float64, device=dev)
+    c6 = float((f[0] * f[0]).sum())
+    r0 = 4.3
+    consts = XD.ATMConstants(torch.zeros(3, dtype=torch.int32, device=dev),
+                             torch.full((1, 1), r0, dtype=torch.float64, device=dev), 1.0,
+                             16.0 / 3.0, 50.0, 0.0)
+    pt = torch.tensor(pos, dtype=torch.float64, device=dev)
+    ei = torch.tensor([[j, i] for i in range(3) for j in range(3) if i != j], device=dev).t()
+    e = XD.atm_energy(ei, pt[ei[1]] - pt[ei[0]], f, f, consts, 3)
+    r1, r2, r3 = sides
+    cos = [(r2 * r2 + r3 * r3 - r1 * r1) / (2 * r2 * r3), (r1 * r1 + r3 * r3 - r2 * r2) / (2 * r1 * r3),
+           (r1 * r1 + r2 * r2 - r3 * r3) / (2 * r1 * r2)]
+    prod = r1 * r2 * r3
+    want = c6 ** 1.5 * (3 * cos[0] * cos[1] * cos[2] + 1) / prod ** 3 / (1 + 6 * (r0 ** 3 / prod) ** (16 / 3))
+    np.testing.assert_allclose(e.cpu().numpy(), want / 3.0, rtol=1e-13)

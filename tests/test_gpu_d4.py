@@ -299,3 +299,94 @@ def test_periodic_three_body_matches_oracle(tables):
     for a, b in zip(got, ref):
         a = a.reshape(b.shape).detach().cpu() / XD.HARTREE
         np.testing.assert_allclose(a, b, atol=1e-10 * float(b.abs().max()))
+
+
+def _safe_coordinates(pos, cell, cutoffs, k, h, rng):
+    """``k`` (atom, axis) pairs whose displacement by +-h moves no pair image across any of
+    the hard ``cutoffs`` (Angstrom): central differences of an unswitched energy are then
+    smooth (brute force over the images of that atom)."""
+    import oracle.d4 as D
+    out = []
+    for i in rng.permutation(len(pos)):
+        dst, src, sh = D.pair_images(pos, cell, max(cutoffs) + 1.0, receivers=[int(i)])
+        d = pos[i] - pos[src] + sh @ cell
+        r = np.sqrt((d * d).sum(-1))
+        if all(np.abs(r - c).min() > 4 * h for c in cutoffs):
+            out.append((int(i), len(out) % 3))
+        if len(out) == k:
+            return out
+    raise RuntimeError("no safe coordinates")
+
+
+def test_c5_organic_box_full_cutoffs(tables):
+    """The C5 configuration at its stated size: 5,000 atoms in the 36.8 A cell, pair cutoff
+    60 bohr (27 images per pair, ~6.7e7 pair-image terms), CN and EEQ-CN cutoffs 25 bohr,
+    s9 = 0, charges given. Against the oracle on a 200-receiver sample (brute-force pair
+    images of those receivers, d4.py:552-591, 984-1071): CN and alpha(i w) from the oracle's
+    own CN to 1e-12, per-atom two-body energies to 1e-11 of scale (alpha of the sources from
+    the GPU, pinned by the sample). Then the full-size gradients: the forces sum to zero,
+    central differences of the GPU energy on three coordinates that no pair crosses a cutoff
+    under (test_d4.py:202-215), and the strain derivative of a switched-cutoff copy against
+    a finite symmetric strain (test_d4.py:217-226)."""
+    import oracle.d4 as D
+    import xnn_amd.dispersion as XD
+    from xnn_amd import synthetic
+    _note("d4 C5 organic box, 60/25/25 bohr")
+    s = synthetic.organic_box(seed=0)
+    pos, cell, z = np.asarray(s.pos), np.asarray(s.cell), [int(v) for v in s.numbers]
+    n = len(z)
+    cuts = dict(cutoff_pair=60.0 * D.BOHR, cutoff_cn=25.0 * D.BOHR, cutoff_eeq_cn=25.0 * D.BOHR)
+    model = XD.DFTD4(tables, s9=0.0, **cuts).to(DEV)
+    rng = np.random.default_rng(31)
+    q = rng.normal(0.0, 0.15, n)
+    q = torch.tensor(q - q.mean(), dtype=torch.float64)
+    out, p, c = _eval(model, pos, z, cell, charges=q.to(DEV), grad=True)
+    gp, gc = torch.autograd.grad(out["energy"].sum(), [p, c])
+    gp, gc = gp.cpu(), gc[0].cpu()
+
+    sample = np.sort(rng.choice(n, 200, replace=False))
+    dst, src, sh = D.pair_images(pos, cell, cuts["cutoff_pair"], receivers=sample)
+    v = D.edge_vectors_au(torch.tensor(pos), torch.tensor(cell), dst, src, sh)
+    r = torch.linalg.norm(v, dim=-1)
+    zt = torch.as_tensor(z)
+    assert len(dst) > 200 * 10000                      # ~13,400 pair images per receiver
+    cn, _, _ = D.coordination_numbers(zt, dst, src, r, tables, 25.0, 25.0, n)
+    st = torch.as_tensor(sample)
+    np.testing.assert_allclose(out["coordination_numbers"].detach().cpu()[st], cn[st],
+                               rtol=1e-12, atol=1e-13)
+    alpha_gpu = out["dynamic_polarizabilities"].detach().cpu()
+    alpha_ref = D.dynamic_polarizabilities(zt[st], cn[st], q[st], tables)
+    np.testing.assert_allclose(alpha_gpu[st], alpha_ref, rtol=1e-12,
+                               atol=1e-13 * float(alpha_ref.abs().max()))
+    e2 = D.two_body(zt, dst, src, r, alpha_gpu, tables, D.PBE0_D4, 60.0, 0.0, n)[st]
+    got = out["node_energy"].detach().cpu()[st] / XD.HARTREE
+    np.testing.assert_allclose(got, e2, atol=1e-11 * float(e2.abs().max()))
+
+    # forces of a periodic system sum to zero
+    assert float(gp.sum(0).abs().max()) <= 1e-10 * float(gp.abs().max())
+    h = 1e-4
+    for i, a in _safe_coordinates(pos, cell, [cuts["cutoff_pair"]], 3, h, rng):
+        pp, pm = pos.copy(), pos.copy()
+        pp[i, a] += h
+        pm[i, a] -= h
+        ep = float(_eval(model, pp, z, cell, charges=q.to(DEV))[0]["energy"][0])
+        em = float(_eval(model, pm, z, cell, charges=q.to(DEV))[0]["energy"][0])
+        assert abs(float(gp[i, a]) - (ep - em) / (2 * h)) < 1e-7, (i, a)
+
+    # strain derivative (positions and cell deformed together) of a copy whose pair
+    # cutoff is switched over 1 A, so that the energy is smooth in the strain
+    sw = XD.DFTD4(tables, s9=0.0, switch_width_pair=1.0, **cuts).to(DEV)
+    out, p, c = _eval(sw, pos, z, cell, charges=q.to(DEV), grad=True)
+    gp, gc = torch.autograd.grad(out["energy"].sum(), [p, c])
+    D_ab = (p.detach().t() @ gp + c.detach()[0].t() @ gc[0]).cpu()
+    eps_h = 1e-5
+    for a, b in [(0, 0), (1, 2)]:
+        eps = np.zeros((3, 3))
+        eps[a, b] = eps[b, a] = eps_h
+        ep = float(_eval(sw, pos @ (np.eye(3) + eps), z, cell @ (np.eye(3) + eps),
+                         charges=q.to(DEV))[0]["energy"][0])
+        em = float(_eval(sw, pos @ (np.eye(3) - eps), z, cell @ (np.eye(3) - eps),
+                         charges=q.to(DEV))[0]["energy"][0])
+        fd = (ep - em) / (2 * eps_h)
+        want = float(D_ab[a, b]) if a == b else float(D_ab[a, b] + D_ab[b, a])
+        assert abs(fd - want) <= 1e-6 * max(1.0, abs(want)), (a, b, fd, want)

@@ -204,3 +204,150 @@ def test_periodic_eeq_rows_in_chunks_equal_one_pass():
     assert torch.equal(A.detach(), B.detach())
     for x, y in zip(g1, g2):
         assert torch.allclose(x, y, rtol=1e-12, atol=1e-15)
+
+
+class _Strict:
+    """An object with exactly the given attributes; reading any other raises (a stand-in
+    for a reference module, whose attribute names it lists)."""
+
+    def __init__(self, kind, **attrs):
+        object.__setattr__(self, "_kind", kind)
+        object.__setattr__(self, "_attrs", attrs)
+
+    def __getattr__(self, name):
+        attrs = object.__getattribute__(self, "_attrs")
+        if name in attrs:
+            return attrs[name]
+        raise AttributeError(f"{object.__getattribute__(self, '_kind')} has no attribute {name!r}")
+
+
+def test_integration_adapter_reads_reference_attributes(monkeypatch):
+    """The INTEGRATION.md adapter (``xnn_amd.featurizers.fast_embed``) reads only what the
+    reference's modules define: SphericalHarmonicEdgeEmbedding (spherical.py:86-101:
+    cutoff, l_max, irreps_sh, sph, rbf, envelope, n_rbf), BesselRBF (radial.py:225-231:
+    cutoff, freqs, norm), GaussianRBF (radial.py:56-59: centers, width, gamma) and
+    PolynomialCutoff (cutoff.py:102-103: cutoff, p); the kernel arguments it forms equal
+    those of this package's mirrored module. The HIP call is replaced by a recorder."""
+    import xnn_amd.ops as ops
+    from xnn_amd import featurizers as F
+    seen = []
+    monkeypatch.setattr(ops, "edge_embed", lambda vec, table, **kw: seen.append((table, kw)))
+    for radial_type in ("bessel", "gaussian"):
+        mine = F.SphericalHarmonicEdgeEmbedding(l_max=3, n_rbf=8, cutoff=4.5, p=5,
+                                                radial_type=radial_type, rbf_prefactor=0.7)
+        if radial_type == "bessel":
+            rbf = _Strict("BesselRBF", cutoff=4.5, freqs=mine.rbf.freqs, norm=mine.rbf.norm)
+        else:
+            rbf = _Strict("GaussianRBF", centers=mine.rbf.centers, width=mine.rbf.width,
+                          gamma=mine.rbf.gamma)
+        ref = _Strict("SphericalHarmonicEdgeEmbedding", cutoff=4.5, l_max=3, irreps_sh=None,
+                      sph=None, n_rbf=8, rbf=rbf,
+                      envelope=_Strict("PolynomialCutoff", cutoff=4.5, p=5))
+        vec = torch.randn(5, 3)
+        F.fast_embed(ref, vec)
+        mine.fast_active = True
+        mine.embed(vec)
+        (t_ref, kw_ref), (t_mine, kw_mine) = seen[-2], seen[-1]
+        assert t_ref is t_mine and kw_ref == kw_mine
+        assert kw_ref["basis"] == radial_type and kw_ref["envelope"] == "polynomial"
+        assert kw_ref["poly_p"] == 5 and kw_ref["l_max"] == 3 and kw_ref["cutoff"] == 4.5
+        if radial_type == "bessel":
+            assert kw_ref["prefactor"] == 0.7
+    # a basis the kernels do not have is an error, not a different function
+    odd = _Strict("SphericalHarmonicEdgeEmbedding", cutoff=4.5, l_max=3, n_rbf=8,
+                  rbf=_Strict("ExpNormalSmearing", means=None, betas=None),
+                  envelope=_Strict("PolynomialCutoff", cutoff=4.5, p=6))
+    with pytest.raises(TypeError, match="radial basis"):
+        F.fast_embed(odd, torch.randn(2, 3))
+
+
+def test_force_stress_output_contract_branches():
+    """The wrapper's other branches (outputs.py:136-151, 187-194): a float64 geometry for a
+    float32 model sets compute_dtype and differentiates at the float64 leaves; a model
+    without an energy is returned as is; a model that predicts forces keeps them; one that
+    forms its own forces and virial is not differentiated at all; direct forces with
+    add-on energy terms are refused."""
+    import copy
+    import xnn_amd as xa
+    from xnn_amd import synthetic
+    s = synthetic.water_box(n_molecules=8, box=6.2, grid=2, seed=5)
+    g = xa.structure_to_graph(s.as_dict(), 4.0)
+    g.pos, g.cell = g.pos.double(), g.cell.double()
+    model = xa.ShEdgePotential(n_rbf=4, l_max=1, channels=4, cutoff=4.0)   # float32
+    g64 = copy.copy(g)
+    out = xa.ForceStressOutput(model, compute_stress=True)(g64)
+    assert g64.compute_dtype == torch.float32 and g.compute_dtype is None
+    assert out["node_energy"].dtype == torch.float32 and out["forces"].dtype == torch.float64
+    # the same model in float64 agrees to float32 rounding
+    m64 = copy.deepcopy(model).double()
+    ref = xa.ForceStressOutput(m64, compute_stress=True)(copy.copy(g))
+    torch.testing.assert_close(out["forces"], ref["forces"], rtol=1e-4, atol=1e-5)
+
+    class NoEnergy(torch.nn.Module):
+        def forward(self, data):
+            return {"properties": data.pos.sum(0)}
+
+    out = xa.ForceStressOutput(NoEnergy(), compute_stress=True)(copy.copy(g))
+    assert set(out) == {"properties"}
+
+    class Direct(torch.nn.Module):
+        def __init__(self, extra=False):
+            super().__init__()
+            self.extra = extra
+
+        def forward(self, data):
+            e = (data.pos ** 2).sum().reshape(1)
+            out = {"energy": e, "forces": torch.ones_like(data.pos)}
+            if self.extra:
+                out["energy_sr"] = e
+            return out
+
+    out = xa.ForceStressOutput(Direct())(copy.copy(g))
+    assert torch.equal(out["forces"], torch.ones_like(g.pos))
+    with pytest.raises(ValueError, match="direct force"):
+        xa.ForceStressOutput(Direct(extra=True))(copy.copy(g))
+
+    class FormsForces(torch.nn.Module):
+        def forms_forces(self, data):
+            return True
+
+        def forward_direct(self, data):
+            n = data.num_nodes
+            return {"energy": torch.zeros(1, dtype=torch.float64),
+                    "forces": torch.full((n, 3), 2.0, dtype=torch.float64),
+                    "virial": torch.eye(3, dtype=torch.float64)[None]}
+
+        def forward(self, data):
+            raise AssertionError("the direct evaluation was expected")
+
+    out = xa.ForceStressOutput(FormsForces(), compute_stress=True).eval()(copy.copy(g))
+    vol = float(torch.linalg.det(g.cell[0]).abs())
+    torch.testing.assert_close(out["stress"][0], torch.eye(3, dtype=torch.float64) / vol)
+    assert "virial" not in out and float(out["forces"][0, 0]) == 2.0
+
+
+def test_atomic_graph_subset_and_label_fields():
+    """AtomicGraph carries the reference's label and mask fields, and ``subset`` keeps the
+    flagged structures with renumbered atoms and edges (atomic_data.py:284-340)."""
+    import xnn_amd as xa
+    from xnn_amd import synthetic
+    mols = synthetic.random_molecules(3, seed=1)
+    graphs = [xa.structure_to_graph(m.as_dict(), 4.0) for m in mols]
+    b = xa.collate(graphs)
+    b.energy = torch.tensor([1.0, 2.0, 3.0], dtype=torch.float64)
+    b.forces = torch.arange(b.num_nodes * 3, dtype=torch.float64).reshape(-1, 3)
+    b.energy_mask = torch.tensor([True, False, True])
+    b.charges = torch.arange(b.num_nodes, dtype=torch.float64)
+    sub = b.subset(torch.tensor([True, False, True]))
+    assert sub.num_graphs == 2 and sub.num_nodes == 42
+    assert torch.equal(sub.energy, torch.tensor([1.0, 3.0], dtype=torch.float64))
+    assert torch.equal(sub.energy_mask, torch.tensor([True, True]))
+    assert torch.equal(sub.charges, torch.cat([b.charges[:21], b.charges[42:]]))
+    assert torch.equal(sub.forces, torch.cat([b.forces[:21], b.forces[42:]]))
+    assert sub.num_edges == graphs[0].num_edges + graphs[2].num_edges
+    assert torch.equal(sub.edge_index[:, graphs[0].num_edges:],
+                       graphs[2].edge_index + 21)
+    assert torch.equal(sub.batch.bincount(), torch.tensor([21, 21]))
+    for name in ("dipole", "polarizability", "spin_multiplicity", "weight", "head", "state",
+                 "site_species", "energy_weight", "atom_force_weight", "fragment_charges"):
+        assert getattr(sub, name) is None

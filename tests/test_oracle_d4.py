@@ -90,7 +90,8 @@ def test_public_switch_and_reference_weights_equal_the_oracle(tables):
     import xnn_amd.dispersion as XD
     r = torch.linspace(0.0, 12.0, 97, dtype=torch.float64)
     for width in (0.0, 2.5, 20.0):
-        assert torch.equal(XD.switching_function(r, 10.0, width), D.switching(r, 10.0, width))
+        np.testing.assert_allclose(XD.switching_function(r, 10.0, width),
+                                   D.switching(r, 10.0, width), rtol=1e-15, atol=1e-16)
     z = torch.tensor([1, 6, 7, 8, 18, 6, 1])
     cn = torch.tensor([0.9, 3.1, 2.2, 1.8, 0.0, 45.0, 1.1], dtype=torch.float64)
     refcn = torch.as_tensor(tables["refcn"])[:, z].t()
@@ -157,3 +158,50 @@ def test_atm_edges_per_atom_is_invariant_under_replication(tables):
     ei, vec, f, sp, tab = _atm_inputs(mol, np.eye(3) * 30.0, z, tables, cut, feats)
     e_pad = D.atm_edges(ei, vec, f, f, sp, tab, 1.0, 16.0 / 3.0, cut, 1.5, 4)
     np.testing.assert_allclose(e_pad, e_mol, rtol=1e-13)
+
+
+def _triangle_closed_form(c6, r0_pair, sides, s9=1.0, alp3=16.0 / 3.0):
+    """Axilrod-Teller-Muto energy of one triangle of identical atoms from its side lengths
+    (bohr): s9 C6^(3/2) (3 cos a cos b cos c + 1) / (r1 r2 r3)^3, zero-damped by
+    1 / (1 + 6 (R0^3 / (r1 r2 r3))^alp3), the angles from the law of cosines."""
+    r1, r2, r3 = sides
+    ca = (r2 * r2 + r3 * r3 - r1 * r1) / (2 * r2 * r3)
+    cb = (r1 * r1 + r3 * r3 - r2 * r2) / (2 * r1 * r3)
+    cc = (r1 * r1 + r2 * r2 - r3 * r3) / (2 * r1 * r2)
+    prod = r1 * r2 * r3
+    damp = 1.0 / (1.0 + 6.0 * (r0_pair ** 3 / prod) ** alp3)
+    return s9 * c6 ** 1.5 * (3.0 * ca * cb * cc + 1.0) / prod ** 3 * damp
+
+
+@pytest.mark.parametrize("shape", ["equilateral", "right_isosceles"])
+def test_atm_triangle_closed_forms(tables, shape):
+    """Three argon atoms: the equilateral triangle (angular factor 3/8 + 1 over r^9) and the
+    right isosceles one (a right angle: factor 1 over (a a a sqrt 2)^3) against the oracle's
+    triple loop and its edge-list form (dispersion.py:188-222)."""
+    a = 7.0                                              # bohr
+    if shape == "equilateral":
+        pos = np.array([[0.0, 0, 0], [a, 0, 0], [a / 2, a * math.sqrt(3) / 2, 0]])
+        sides = (a, a, a)
+        factor = 1.375 / a ** 9
+    else:
+        pos = np.array([[0.0, 0, 0], [a, 0, 0], [0, a, 0]])
+        sides = (a, a, a * math.sqrt(2))
+        factor = 1.0 / (math.sqrt(2) * a ** 3) ** 3
+    z = torch.tensor([18, 18, 18])
+    alpha = D.dynamic_polarizabilities(z, torch.zeros(3, dtype=torch.float64),
+                                       torch.zeros(3, dtype=torch.float64), tables)
+    c6 = float(D.c6_pairs(alpha[0], alpha[1]))
+    q4 = float(tables["r4r2"][18])
+    r0 = D.PBE0_D4["a1"] * math.sqrt(3.0 * q4 * q4) + D.PBE0_D4["a2"]
+    want = _triangle_closed_form(c6, r0, sides)
+    prod = sides[0] * sides[1] * sides[2]
+    assert abs(want / (c6 ** 1.5 / (1 + 6 * (r0 ** 3 / prod) ** (16 / 3))) - factor) < 1e-12 * factor
+    pt = torch.tensor(pos)
+    got = float(D.atm_molecule(z, pt, alpha, tables, D.PBE0_D4, 100.0))
+    assert abs(got - want) < 1e-14 * abs(want)
+    ei = torch.tensor([[j, i] for i in range(3) for j in range(3) if i != j]).t()
+    vec = pt[ei[1]] - pt[ei[0]]
+    feat = alpha * torch.sqrt((3.0 / math.pi) * torch.as_tensor(D.cp_weights()))
+    table, species = D.bj_radius_factors(z, tables, D.PBE0_D4["a1"], D.PBE0_D4["a2"])
+    e = D.atm_edges(ei, vec, feat, feat, species, table, 1.0, 16.0 / 3.0, 100.0, 0.0, 3)
+    np.testing.assert_allclose(e.numpy(), want / 3.0, rtol=1e-13)

@@ -74,6 +74,33 @@ def test_sh_degree_two_closed_forms():
     np.testing.assert_allclose(R.e3nn_sh(2, u)[:, 4:9], want, atol=1e-13)
 
 
+def test_sh_degree_three_closed_forms():
+    """e3nn 0.4.4's l = 3 forms (e3nn/o3/_spherical_harmonics.py, the published generated
+    code), written over its component-normalized l = 2 values s20 = sqrt(15) xz and
+    s24 = sqrt(15)/2 (z^2 - x^2), y polar:
+    sqrt(42)/6 (s20 z + s24 x), sqrt(7) s20 y, sqrt(168)/8 (4y^2 - x^2 - z^2) x,
+    sqrt(7)/2 y (2y^2 - 3x^2 - 3z^2), sqrt(168)/8 z (4y^2 - x^2 - z^2), sqrt(7) s24 y,
+    sqrt(42)/6 (s24 z - s20 x). Elementwise, so a swapped or sign-flipped component fails."""
+    u = _unit(400, 11)
+    x, y, z = u[:, 0], u[:, 1], u[:, 2]
+    s20 = math.sqrt(15) * x * z
+    s24 = 0.5 * math.sqrt(15) * (z * z - x * x)
+    y2, x2z2 = y * y, x * x + z * z
+    want = torch.stack([math.sqrt(42) / 6 * (s20 * z + s24 * x),
+                        math.sqrt(7) * s20 * y,
+                        math.sqrt(168) / 8 * (4 * y2 - x2z2) * x,
+                        0.5 * math.sqrt(7) * y * (2 * y2 - 3 * x2z2),
+                        math.sqrt(168) / 8 * z * (4 * y2 - x2z2),
+                        math.sqrt(7) * s24 * y,
+                        math.sqrt(42) / 6 * (s24 * z - s20 * x)], 1)
+    # the stated forms are component-normalized by themselves (sum_m Y^2 = 7)
+    np.testing.assert_allclose((want * want).sum(1).numpy(), 7.0, atol=1e-12)
+    np.testing.assert_allclose(R.e3nn_sh(3, u)[:, 9:16], want, atol=1e-13)
+    # the package's closed forms (the kernels' polynomials) too, on unnormalized vectors
+    from xnn_amd.featurizers import spherical_harmonics
+    np.testing.assert_allclose(spherical_harmonics(3, 2.5 * u)[:, 9:16], want, atol=1e-13)
+
+
 def test_sh_odd_degrees_flip_with_the_vector():
     u = _unit(50, 7)
     Y, Ym = R.e3nn_sh(3, u), R.e3nn_sh(3, -u)

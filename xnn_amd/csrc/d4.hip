@@ -307,7 +307,23 @@ struct PairParams {
   double s6, s8, a1, a2, cutoff, width;  // cutoff, width in bohr
 };
 
-__constant__ double c_cp3[kNW];   // (3 / pi) * Casimir-Polder weights
+// The Casimir-Polder frequency grid (hartree, d4.py:130-141) and its trapezoid weights
+// times 3 / pi, folded by the compiler: (3 / pi) * (w[k+1] - w[k-1]) / 2, one-sided at the ends.
+constexpr double kCpFreq[kNW] = {0.000001, 0.05, 0.1, 0.2, 0.3, 0.4, 0.5, 0.6, 0.7, 0.8, 0.9,
+                                 1.0,      1.2,  1.4, 1.6, 1.8, 2.0, 2.5, 3.0, 4.0, 5.0, 7.5,
+                                 10.0};
+constexpr double cp3_weight(int k) {
+  return (3.0 / M_PI) * 0.5 *
+         ((k > 0 ? kCpFreq[k] - kCpFreq[k - 1] : 0.0) +
+          (k < kNW - 1 ? kCpFreq[k + 1] - kCpFreq[k] : 0.0));
+}
+__constant__ double c_cp3[kNW] = {
+    cp3_weight(0),  cp3_weight(1),  cp3_weight(2),  cp3_weight(3),  cp3_weight(4),
+    cp3_weight(5),  cp3_weight(6),  cp3_weight(7),  cp3_weight(8),  cp3_weight(9),
+    cp3_weight(10), cp3_weight(11), cp3_weight(12), cp3_weight(13), cp3_weight(14),
+    cp3_weight(15), cp3_weight(16), cp3_weight(17), cp3_weight(18), cp3_weight(19),
+    cp3_weight(20), cp3_weight(21), cp3_weight(22)};
+static_assert(sizeof(c_cp3) / sizeof(c_cp3[0]) == kNW, "one weight per frequency");
 
 // BACKWARD = false: partial[cy][0][i] = sum of -1/2 C6 f(r) over this chunk.
 // BACKWARD = true:  partial[cy][0..11][i] = grad_pos (3), cell gradient (9), and
@@ -758,25 +774,6 @@ static void reduce_into(const double* partial, int64_t n_nodes, int np, int k0, 
                      0, s, partial, n_nodes, np, k0, nk, n_cy, out);
 }
 
-static bool cp_ready[64] = {false};
-
-static int upload_cp(hipStream_t s) {
-  int dev = 0;
-  XNN_HIP_CHECK(hipGetDevice(&dev));
-  if (dev >= 0 && dev < 64 && cp_ready[dev]) return XNN_OK;
-  static const double freq[kNW] = {0.000001, 0.05, 0.1, 0.2, 0.3, 0.4, 0.5, 0.6, 0.7, 0.8, 0.9,
-                                   1.0, 1.2, 1.4, 1.6, 1.8, 2.0, 2.5, 3.0, 4.0, 5.0, 7.5, 10.0};
-  double cp3[kNW];
-  for (int k = 0; k < kNW; ++k) {
-    const double lo = k > 0 ? freq[k] - freq[k - 1] : 0.0;
-    const double hi = k < kNW - 1 ? freq[k + 1] - freq[k] : 0.0;
-    cp3[k] = (3.0 / M_PI) * 0.5 * (lo + hi);
-  }
-  XNN_HIP_CHECK(hipMemcpyToSymbol(HIP_SYMBOL(c_cp3), cp3, sizeof(cp3), 0, hipMemcpyHostToDevice));
-  if (dev >= 0 && dev < 64) cp_ready[dev] = true;
-  return XNN_OK;
-}
-
 // ---------------------------------------------------------------- polarizabilities
 constexpr int kD4Ref = 7;                                  // reference systems per element
 constexpr double kD4NormEps = 1.4916681462400413e-154;     // smallest usable weight norm
@@ -1067,8 +1064,6 @@ int xnn_d4_two_body(const double* pos, int64_t n_nodes, const int32_t* species,
   XNN_REQUIRE(workspace != nullptr && workspace_bytes >= need, "workspace too small (%zu < %zu)",
               workspace_bytes, need);
   hipStream_t s = as_hip(stream);
-  const int up = upload_cp(s);
-  if (up != XNN_OK) return up;
   const PairParams p{prm->s6, prm->s8, prm->a1, prm->a2, prm->cutoff, prm->width};
   double* part = static_cast<double*>(workspace);
   hipLaunchKernelGGL(d4_pair_kernel<false>, dim3((unsigned)w.n_tiles, (unsigned)w.n_cy),
@@ -1098,8 +1093,6 @@ int xnn_d4_two_body_backward(const double* pos, int64_t n_nodes, const int32_t* 
   XNN_REQUIRE(workspace != nullptr && workspace_bytes >= need, "workspace too small (%zu < %zu)",
               workspace_bytes, need);
   hipStream_t s = as_hip(stream);
-  const int up = upload_cp(s);
-  if (up != XNN_OK) return up;
   const PairParams p{prm->s6, prm->s8, prm->a1, prm->a2, prm->cutoff, prm->width};
   double* part = static_cast<double*>(workspace);
   double* part_a = part + w.n_cy * 12 * n_nodes;

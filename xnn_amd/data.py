@@ -44,10 +44,36 @@ class AtomicGraph:
     n_atoms: Tensor
     cell: Optional[Tensor] = None
     pbc: Optional[Tensor] = None
-    energy: Optional[Tensor] = None
-    forces: Optional[Tensor] = None
-    stress: Optional[Tensor] = None
-    total_charge: Optional[Tensor] = None
+    # labels and per-structure metadata (atomic_data.py:194-223): carried, never read by
+    # the hot path; masks are bool (B,) and say which structures carry a label
+    energy: Optional[Tensor] = None                  # (B,)
+    forces: Optional[Tensor] = None                  # (N, 3)
+    stress: Optional[Tensor] = None                  # (B, 3, 3)
+    energy_mask: Optional[Tensor] = None
+    forces_mask: Optional[Tensor] = None
+    stress_mask: Optional[Tensor] = None
+    dipole: Optional[Tensor] = None                  # (B, 3)
+    polarizability: Optional[Tensor] = None          # (B, 3, 3)
+    dipole_mask: Optional[Tensor] = None
+    polarizability_mask: Optional[Tensor] = None
+    charges: Optional[Tensor] = None                 # (N,)
+    charges_mask: Optional[Tensor] = None
+    fragment_charges: Optional[Tensor] = None        # (N,)
+    fragment_charges_mask: Optional[Tensor] = None
+    external_potential: Optional[Tensor] = None      # (N,)
+    total_charge: Optional[Tensor] = None            # (B,) read by D4 / D3 EEQ
+    spin_multiplicity: Optional[Tensor] = None       # (B,)
+    weight: Optional[Tensor] = None                  # (B,)
+    head: Optional[Tensor] = None                    # (B,)
+    properties: Optional[Tensor] = None              # (B,) or (B, k)
+    properties_mask: Optional[Tensor] = None
+    state: Optional[Tensor] = None                   # (B,) labels or (B, d)
+    site_species: Optional[Tensor] = None            # (N, K)
+    site_occupancy: Optional[Tensor] = None          # (N, K)
+    energy_weight: Optional[Tensor] = None           # (B,)
+    force_weight: Optional[Tensor] = None            # (B,)
+    stress_weight: Optional[Tensor] = None           # (B,)
+    atom_force_weight: Optional[Tensor] = None       # (N,)
     compute_dtype: Optional[torch.dtype] = None
     # (B, 3, 3) zeros set by ForceStressOutput: the strain whose gradient the edge-vector
     # backward forms directly (sym of sum_e r_e (x) dE/dr_e), in place of deforming pos and cell
@@ -75,6 +101,37 @@ class AtomicGraph:
             v = getattr(self, f.name)
             kwargs[f.name] = v.to(device) if isinstance(v, Tensor) else v
         return AtomicGraph(**kwargs)
+
+    #: per-atom optional fields (the rest of the optional tensors are per structure)
+    _PER_ATOM = ("forces", "charges", "fragment_charges", "external_potential", "site_species",
+                 "site_occupancy", "atom_force_weight")
+    _STRUCTURE = ("pos", "atomic_numbers", "edge_index", "cell_shifts", "batch", "n_atoms",
+                  "compute_dtype", "strain_probe")
+
+    def subset(self, keep: Tensor) -> "AtomicGraph":
+        """The structures flagged in the bool ``keep`` (B,) as a batch of their own, in
+        their original order, with atoms and edges renumbered and every optional field
+        restricted the same way (atomic_data.py:284-340). Positions are gathered, so
+        derivatives on the subset reach the full graph."""
+        keep = keep.to(device=self.batch.device, dtype=torch.bool)
+        atom_keep = keep.index_select(0, self.batch)
+        edge_keep = atom_keep.index_select(0, self.edge_index[0])
+        new_atom = torch.cumsum(atom_keep.to(torch.int64), 0) - 1
+        new_structure = torch.cumsum(keep.to(torch.int64), 0) - 1
+        kw = dict(pos=self.pos[atom_keep], atomic_numbers=self.atomic_numbers[atom_keep],
+                  edge_index=new_atom[self.edge_index[:, edge_keep]],
+                  cell_shifts=self.cell_shifts[edge_keep],
+                  batch=new_structure[self.batch[atom_keep]], n_atoms=self.n_atoms[keep],
+                  compute_dtype=self.compute_dtype)
+        for f in fields(self):
+            if f.name in self._STRUCTURE:
+                continue
+            v = getattr(self, f.name)
+            if v is not None:
+                mask = atom_keep if f.name in self._PER_ATOM else keep
+                v = v[mask.to(v.device)]
+            kw[f.name] = v
+        return AtomicGraph(**kw)
 
     def plan(self):
         """The cached :class:`~xnn_amd.plan.EdgePlan` of this graph (GPU only)."""

@@ -53,42 +53,45 @@ _NS = "xnn_amd"
 
 # --------------------------------------------------------------------------- formulas
 def switching_function(r: Tensor, cutoff: float, width: float) -> Tensor:
-    """Quintic switching window (dispersion.py:42-67): 1 below ``cutoff - width``, 0 above
-    ``cutoff``, ``x^3 (10 - 15 x + 6 x^2)`` with ``x = (cutoff - r) / width`` inside;
-    ``width <= 0`` is the sharp cutoff. The pair kernels evaluate it per term (with its
-    slope); this is the tensor form of the same window."""
+    """The quintic smoothstep window of the pair and triple sums (dispersion.py:42-67).
+
+    With ``t = (cutoff - r) / width`` clamped to [0, 1] the window is
+    ``10 t^3 - 15 t^4 + 6 t^5``: one at and below ``cutoff - width``, zero at and beyond
+    ``cutoff``, with vanishing first and second derivatives at both ends. A width above the
+    cutoff is taken as the cutoff; a width of zero or less means no window (all ones). The
+    pair kernels evaluate the same window per term together with its slope."""
     if width <= 0.0:
         return torch.ones_like(r)
-    w = min(width, cutoff)
-    x = torch.clamp((cutoff - r) / w, 0.0, 1.0)
-    return x ** 3 * (10.0 + x * (6.0 * x - 15.0))
+    t = ((cutoff - r) / min(width, cutoff)).clamp(0.0, 1.0)
+    return t * t * t * (t * (t * 6.0 - 15.0) + 10.0)
 
 
 def gaussian_reference_weights(cn: Tensor, refcn: Tensor, valid: Tensor, wf: float,
                                ngw: Optional[Tensor] = None, eps_norm: float = 0.0,
                                n_gauss: Optional[int] = None) -> Tensor:
-    """Normalized Gaussian weights of the reference systems in the coordination number
-    (dispersion.py:70-121): ``sum_{j <= ngw} exp(-wf j (CN - CN_ref)^2)`` per reference
-    (one Gaussian with ``ngw`` None, D3), normalized over the ``valid`` slots, weight one
-    on the largest-CN reference(s) where the norm is at most ``eps_norm``. The D4
-    polarizability and D3 weight kernels evaluate the same weights per atom; this is the
-    tensor form on per-atom ``(N, R)`` reference tables."""
-    dcn2 = (cn[:, None] - refcn) ** 2
-    if ngw is None:
-        gw = torch.exp(-wf * dcn2)
-    else:
-        n_max = int(ngw.max()) if n_gauss is None else int(n_gauss)
-        j = torch.arange(1, n_max + 1, device=cn.device)
-        gauss = torch.exp(-wf * j.to(cn.dtype)[None, None, :] * dcn2[:, :, None])
-        use = j[None, None, :] <= ngw[:, :, None]
-        gw = torch.where(use, gauss, torch.zeros_like(gauss)).sum(-1)
-    gw = torch.where(valid, gw, torch.zeros_like(gw))
-    norm = gw.sum(dim=1)
-    ok = norm > eps_norm
-    weights = gw / torch.where(ok, norm, torch.ones_like(norm))[:, None]
-    max_cn = torch.where(valid, refcn, torch.full_like(refcn, -math.inf)).max(dim=1).values
-    fallback = (valid & ((refcn - max_cn[:, None]).abs() < 1e-12)).to(cn.dtype)
-    return torch.where(ok[:, None], weights, fallback)
+    """Weights of an atom's reference systems from its coordination number (D3 paper
+    eq 16, D4 paper eq 8; dispersion.py:70-121).
+
+    Reference ``r`` of an atom carries ``g_r = sum_{j=1..n_r} exp(-wf j (CN - CN_r)^2)``
+    (``n_r = ngw[r]`` Gaussians for D4, a single one when ``ngw`` is None as in D3), and the
+    weights are ``g_r / sum_r g_r`` over the atom's ``valid`` references. When that sum is
+    at most ``eps_norm`` (the Gaussians underflow far from every reference) the weight goes
+    to the reference(s) with the largest ``CN_r`` instead, in equal parts of one each.
+    ``refcn``, ``valid`` and ``ngw`` are per-atom ``(N, R)`` tables; ``n_gauss`` bounds the
+    Gaussians per reference (default: the largest ``ngw``). The D4 polarizability and D3
+    weight kernels evaluate the same weights atom by atom."""
+    d2 = torch.square(cn.unsqueeze(1) - refcn)
+    counts = torch.ones_like(refcn, dtype=torch.long) if ngw is None else ngw
+    n_max = 1 if ngw is None else (int(ngw.max()) if n_gauss is None else int(n_gauss))
+    g = torch.zeros_like(d2)
+    for j in range(1, n_max + 1):
+        g = g + torch.exp(d2 * (-wf * j)) * (counts >= j).to(d2.dtype)
+    g = g * valid.to(d2.dtype)
+    total = g.sum(dim=1, keepdim=True)
+    usable = total > eps_norm
+    top = refcn.masked_fill(~valid, -math.inf).amax(dim=1, keepdim=True)
+    largest = (valid & ((refcn - top).abs() < 1e-12)).to(d2.dtype)
+    return torch.where(usable, g / torch.where(usable, total, torch.ones_like(total)), largest)
 
 
 # --------------------------------------------------------------------------- tables# --------------------------------------------------------------------------- tables

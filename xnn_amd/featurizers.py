@@ -150,6 +150,47 @@ def spherical_harmonics(l_max: int, vec: Tensor) -> Tensor:
     return torch.stack(out, dim=-1)
 
 
+def radial_spec(module) -> dict:
+    """The HIP featurizer's description of an embedding module's radial part, read through
+    the reference's attribute names only (spherical.py:86-101, radial.py:15-268,
+    cutoff.py:10-125): ``module.rbf`` is a Bessel basis (``freqs``, ``norm``) or a Gaussian
+    one (``centers``, ``gamma``), ``module.envelope`` a polynomial envelope (``p``) or a
+    cosine one, ``module.cutoff`` the cutoff. So a reference module and this package's
+    mirror of it give the same kernel arguments. Unknown bases or envelopes raise."""
+    rbf, env = module.rbf, module.envelope
+    if hasattr(rbf, "freqs") and hasattr(rbf, "norm"):
+        basis, table, prefactor, gamma = "bessel", rbf.freqs, float(rbf.norm), 1.0
+    elif hasattr(rbf, "centers") and hasattr(rbf, "gamma"):
+        basis, table, prefactor, gamma = "gaussian", rbf.centers, 1.0, float(rbf.gamma)
+    else:
+        raise TypeError(f"no HIP radial basis for {type(rbf).__name__} (Bessel and Gaussian "
+                        "bases are on the fast path)")
+    if hasattr(env, "p"):
+        envelope, poly_p = "polynomial", int(env.p)
+    elif type(env).__name__ == "CosineCutoff":
+        envelope, poly_p = "cosine", 1
+    else:
+        raise TypeError(f"no HIP envelope for {type(env).__name__} (polynomial and cosine "
+                        "envelopes are on the fast path)")
+    return dict(table=table, basis=basis, envelope=envelope, poly_p=poly_p,
+                cutoff=float(module.cutoff), prefactor=prefactor, gamma=gamma)
+
+
+def fast_embed(module, vec: Tensor, sh_sign: int = 1,
+               want_sh: bool = True) -> Tuple[Tensor, Tensor, Tensor]:
+    """``embed(vec)`` of a spherical-harmonic edge embedding on the HIP featurizer, for
+    this package's module or the reference's own (spherical.py:115-138): reads
+    ``module.l_max``, ``module.rbf``, ``module.envelope`` and ``module.cutoff`` and
+    returns ``(length (E,), sh (E, (l_max+1)^2), radial (E, n_rbf))``. Without the
+    harmonics (``want_sh=False``) only the radial part is evaluated."""
+    from .ops import edge_embed
+    spec = radial_spec(module)
+    table = spec.pop("table")
+    return edge_embed(vec, table, n_rbf=int(table.numel()),
+                      l_max=int(module.l_max) if want_sh else 0, sh_sign=sh_sign,
+                      want_length=want_sh, want_sh=want_sh, **spec)
+
+
 class SphericalHarmonicEdgeEmbedding(nn.Module, FastPathModule):
     """Per-edge length, SH edge attributes and enveloped radial basis
     (gnn/featurizers/spherical.py:28-171).
@@ -192,15 +233,7 @@ class SphericalHarmonicEdgeEmbedding(nn.Module, FastPathModule):
         return self.rbf.freqs if self.radial_type == "bessel" else self.rbf.centers
 
     def _embed_fast(self, vec: Tensor, sh_sign: int, want_sh: bool = True):
-        from .ops import edge_embed
-        rbf = self.rbf
-        # without harmonics, neither l_max nor the lengths are needed
-        return edge_embed(
-            vec, self._table(), n_rbf=self.n_rbf, basis=self.radial_type,
-            envelope=self.envelope_type, poly_p=getattr(self.envelope, "p", 1),
-            l_max=self.l_max if want_sh else 0, cutoff=self.cutoff,
-            prefactor=getattr(rbf, "norm", 1.0), gamma=getattr(rbf, "gamma", 1.0),
-            sh_sign=sh_sign, want_length=want_sh, want_sh=want_sh)
+        return fast_embed(self, vec, sh_sign, want_sh)
 
     @property
     def radial_trainable(self) -> bool:
@@ -211,12 +244,9 @@ class SphericalHarmonicEdgeEmbedding(nn.Module, FastPathModule):
         with this embedding's radial basis evaluated inside the HIP message kernels
         (float32, on a GPU; differentiable in ``vec`` only: forces and stress)."""
         from .ops import sh_radial_message_sum
-        rbf = self.rbf
-        return sh_radial_message_sum(
-            vec, self._table(), W, plan, basis=self.radial_type, envelope=self.envelope_type,
-            poly_p=getattr(self.envelope, "p", 1), l_max=self.l_max, cutoff=self.cutoff,
-            prefactor=getattr(rbf, "norm", 1.0), gamma=getattr(rbf, "gamma", 1.0),
-            sh_sign=sh_sign)
+        spec = radial_spec(self)
+        return sh_radial_message_sum(vec, spec.pop("table"), W, plan, l_max=self.l_max,
+                                     sh_sign=sh_sign, **spec)
 
     def embed(self, vec: Tensor, sh_sign: int = 1) -> Tuple[Tensor, Tensor, Tensor]:
         """``(edge_length (E,), edge_sh (E, (l_max+1)^2), edge_radial (E, n_rbf))``

@@ -53,18 +53,25 @@ def gather_rows(src: Tensor, index: Tensor) -> Tensor:
 
 
 def structure_sum(src: Tensor, index: Tensor, dim_size: int) -> Tensor:
-    """Per-structure totals accumulated in float64 (ops.py:531-557). ``index`` must be
-    grouped by structure (as :func:`~xnn_amd.data.collate` builds it)."""
+    """Per-structure totals accumulated in float64 (ops.py:531-557), for any ``index``.
+
+    On a GPU the rows are summed along the CSR of ``index``: an index grouped by
+    structure (as :func:`~xnn_amd.data.collate` builds it) is summed in place, any other
+    is first gathered into structure order by the CSR's stable permutation (each
+    structure's rows keep their relative order, as the CPU ``index_add`` visits them)."""
     if not src.is_cuda:
         if dim_size == 1:
             return src.to(torch.float64).sum(0, keepdim=True)
         out = torch.zeros(dim_size, dtype=torch.float64, device=src.device)
         return out.index_add(0, index, src.to(torch.float64))
     from .ops import structure_sum_op
-    counts = torch.bincount(index, minlength=dim_size)
-    node_ptr = torch.zeros(dim_size + 1, dtype=torch.int64, device=src.device)
-    node_ptr[1:] = torch.cumsum(counts, 0)
-    return structure_sum_op(src, node_ptr, index.to(torch.int32))
+    index32, ptr, perm = csr_of(index, dim_size)
+    node_ptr = ptr.to(torch.int64)
+    if perm is None:
+        return structure_sum_op(src, node_ptr, index32)
+    order = perm.to(torch.int64)
+    return structure_sum_op(src.index_select(0, order), node_ptr,
+                            index32.index_select(0, order))
 
 
 def cell_volume(cell: Tensor) -> Tensor:

@@ -29,6 +29,26 @@ class ForceStressOutput(nn.Module):
         self.compute_stress = compute_stress
         self.cutoff = getattr(model, "cutoff", None)
 
+    def _model_dtype(self) -> Optional[torch.dtype]:
+        """The wrapped model's floating dtype: that of its first floating parameter, else of
+        its first floating buffer, else ``None`` (outputs.py:73-94). Remembered per model
+        object, and re-checked against the tensor it came from (``.to()`` replaces buffers)."""
+        memo = self.__dict__.get("_dtype_memo")
+        if memo is not None and memo[0] is self.model:
+            owner, name, t = memo[1:]
+            if owner is None or owner._buffers.get(name) is t:
+                return t.dtype
+        for t in self.model.parameters():
+            if t.is_floating_point():
+                self.__dict__["_dtype_memo"] = (self.model, None, None, t)
+                return t.dtype
+        for owner in self.model.modules():
+            for name, t in owner._buffers.items():
+                if t is not None and t.is_floating_point():
+                    self.__dict__["_dtype_memo"] = (self.model, owner, name, t)
+                    return t.dtype
+        return None
+
     @staticmethod
     def _zero_strain(data) -> Tensor:
         # a fresh leaf per call: a leaf kept across calls would keep the gradient
@@ -38,8 +58,25 @@ class ForceStressOutput(nn.Module):
         return torch.zeros((data.num_graphs, 3, 3), dtype=data.pos.dtype,
                            device=data.pos.device, requires_grad=True)
 
-    def forward(self, data) -> dict:
+    def forward(self, data, plan=None) -> dict:
         create_graph = self.training
+        # a model that forms its own forces and strain derivative in evaluation: no
+        # autograd pass (outputs.py:136-143)
+        forms_forces = getattr(self.model, "forms_forces", None)
+        if (callable(forms_forces) and not self.training and self.compute_forces and plan is None
+                and forms_forces(data)):
+            out = self.model.forward_direct(data)
+            virial = out.pop("virial")
+            if self.compute_stress and data.cell is not None:
+                out["stress"] = _stress(virial, data)
+            return out
+        # a float64 geometry for a float32 model: the model computes in its own dtype
+        # through edge_vectors(), the derivatives are taken at the float64 leaves
+        # (outputs.py:146-151)
+        if data.compute_dtype is None:
+            dtype = self._model_dtype()
+            if dtype is not None and dtype != data.pos.dtype:
+                data.compute_dtype = dtype
         strain: Optional[Tensor] = None
         # A model whose energy depends on positions and cell only through the edge vectors
         # (``edge_virial``) gets the strain derivative from the edge-vector backward itself,
@@ -86,15 +123,23 @@ class ForceStressOutput(nn.Module):
         if had_param_grads is not None:
             self.model.param_grads = bool(create_graph)
         try:
-            out = self.model(data)
+            out = self.model(data) if plan is None else self.model(data, plan)
         finally:
             if had_param_grads is not None:
                 self.model.param_grads = had_param_grads
             if probe:
                 data.strain_probe = None
+        if "energy" not in out:
+            # a property model predicts no energy: no forces or stress (outputs.py:187-189)
+            return out
         energy = out["energy"]
+        # a model that predicts its forces directly returns them itself (outputs.py:191-194)
+        direct = "forces" in out
+        if direct and "energy_sr" in out:
+            raise ValueError("a model with direct force prediction cannot be combined with "
+                             "add-on energy terms (long-range, dispersion)")
         inputs, need = [], []
-        if self.compute_forces:
+        if self.compute_forces and not direct:
             inputs.append(data.pos)
             need.append("pos")
         if strain is not None:
@@ -119,7 +164,7 @@ class ForceStressOutput(nn.Module):
                                         create_graph=create_graph, retain_graph=create_graph,
                                         allow_unused=True)
             g = dict(zip(need, grads))
-        if self.compute_forces:
+        if self.compute_forces and not direct:
             out["forces"] = g["pos"] if g.get("pos") is not None else torch.zeros_like(data.pos)
         if strain is not None:
             out["stress"] = (_stress(g["strain"], data, scale=-1.0, differentiable=create_graph)
