@@ -264,6 +264,19 @@ int xnn_segment_reduce_f64(int dtype, const void* src, int64_t n_rows, int64_t n
                            const int64_t* seg_ptr, int64_t n_segments, double* out,
                            void* workspace, size_t workspace_bytes, xnn_stream_t stream);
 
+/* xnn_segment_reduce_f64 without a workspace argument and without any allocation: the
+ * partial sums live in a file-scope device array of xnn_segment_reduce_noalloc_max_bytes()
+ * bytes (1 MiB; one copy per GPU, held until the process ends; its address is looked up
+ * once per device on the first call). No counterpart in the reference: it is for callers
+ * that cannot allocate device memory (code under HIP graph capture, tight serving loops).
+ * Sizes whose partials exceed the array return XNN_EINVAL. Same kernels and results as
+ * xnn_segment_reduce_f64. Every call on a GPU shares that GPU's array: calls that overlap
+ * on one GPU (other streams, other host threads) race. */
+size_t xnn_segment_reduce_noalloc_max_bytes(void);
+int xnn_segment_reduce_f64_noalloc(int dtype, const void* src, int64_t n_rows,
+                                   int64_t n_features, const int64_t* seg_ptr,
+                                   int64_t n_segments, double* out, xnn_stream_t stream);
+
 /* ------------------------------------------------------------------------ */
 /* D4 dispersion pair terms over lattice images, float64 (no edge list: every
  * receiver i meets every source j of its structure and every translation

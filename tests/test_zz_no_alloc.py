@@ -1,0 +1,74 @@
+"""The no-allocation entry point xnn_segment_reduce_f64_noalloc (partial sums in the
+library's file-scope scratch array) against xnn_segment_reduce_f64 with a caller
+workspace, through the C ABI: two calls in a row, the second smaller, bit for bit."""
+import ctypes
+
+import numpy as np
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def _with_workspace(lib, _lib, src, seg):
+    n_rows, F = src.shape
+    n_seg = seg.numel() - 1
+    need = int(lib.xnn_segment_reduce_workspace_bytes(n_rows, F, n_seg))
+    ws = torch.empty(max(need, 1), dtype=torch.uint8, device=DEV)
+    out = torch.empty((n_seg, F), dtype=torch.float64, device=DEV)
+    _lib.call("xnn_segment_reduce_f64", _lib.dtype_code(src.dtype), _lib.ptr(src), n_rows, F,
+              _lib.ptr(seg), n_seg, _lib.ptr(out), _lib.ptr(ws), need, _lib.stream(src.device))
+    return out, need
+
+
+def _no_alloc(_lib, src, seg):
+    n_rows, F = src.shape
+    n_seg = seg.numel() - 1
+    out = torch.empty((n_seg, F), dtype=torch.float64, device=DEV)
+    _lib.call("xnn_segment_reduce_f64_noalloc", _lib.dtype_code(src.dtype), _lib.ptr(src), n_rows,
+              F, _lib.ptr(seg), n_seg, _lib.ptr(out), _lib.stream(src.device))
+    return out
+
+
+def test_no_alloc_matches_the_workspace_entry_point():
+    from xnn_amd import _lib
+    lib = _lib.load()
+    cap = int(lib.xnn_segment_reduce_noalloc_max_bytes())
+    assert cap == 1 << 20
+    gen = torch.Generator().manual_seed(11)
+    # one structure over many blocks (partials in the scratch array), then a smaller one,
+    # then several structures (no partials), in float32 and float64
+    cases = [(250_000, 9, [0, 250_000]), (60_000, 3, [0, 60_000]), (90_000, 64, [0, 90_000]),
+             (40_000, 130, [0, 40_000]), (5000, 1, [0, 1200, 1200, 5000])]
+    for dt in (torch.float32, torch.float64):
+        for n, F, bounds in cases:
+            print(f"[gpu-case] noalloc {dt} n={n} F={F} segments={len(bounds) - 1}", flush=True)
+            src = (torch.randn(n, F, generator=gen, dtype=torch.float64) * 3).to(dt).to(DEV)
+            seg = torch.tensor(bounds, dtype=torch.int64, device=DEV)
+            want, need = _with_workspace(lib, _lib, src, seg)
+            got = _no_alloc(_lib, src, seg)
+            torch.cuda.synchronize()
+            assert need <= cap
+            assert torch.equal(got, want), (n, F)
+            ref = torch.stack([src[a:b].double().sum(0).cpu() for a, b in zip(bounds, bounds[1:])])
+            np.testing.assert_allclose(got.cpu(), ref, rtol=1e-12, atol=1e-10)
+
+
+def test_no_alloc_rejects_sizes_beyond_the_scratch_array():
+    from xnn_amd import _lib
+    lib = _lib.load()
+    cap = int(lib.xnn_segment_reduce_noalloc_max_bytes())
+    # 256 chunks of 1024 features need 2 MiB of partials: refused before any launch
+    n, F = 1 << 20, 1024
+    need = int(lib.xnn_segment_reduce_workspace_bytes(n, F, 1))
+    assert need > cap
+    seg = torch.tensor([0, n], dtype=torch.int64, device=DEV)
+    out = torch.empty((1, F), dtype=torch.float64, device=DEV)
+    src = torch.empty((1, 1), dtype=torch.float32, device=DEV)   # never read: refused first
+    rc = lib.xnn_segment_reduce_f64_noalloc(_lib.XNN_F32, ctypes.c_void_p(_lib.ptr(src)), n, F,
+                                            ctypes.c_void_p(_lib.ptr(seg)), 1,
+                                            ctypes.c_void_p(_lib.ptr(out)),
+                                            ctypes.c_void_p(_lib.stream(src.device)))
+    assert rc == _lib.XNN_EINVAL
+    assert b"scratch" in lib.xnn_last_error()

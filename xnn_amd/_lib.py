@@ -139,6 +139,8 @@ _SIGNATURES = {
     "xnn_gather_rows": [c_int, vp, i64, i64, vp, i64, vp, vp],
     "xnn_segment_reduce_workspace_bytes": [i64, i64, i64],
     "xnn_segment_reduce_f64": [c_int, vp, i64, i64, vp, i64, vp, vp, sz, vp],
+    "xnn_segment_reduce_noalloc_max_bytes": [],
+    "xnn_segment_reduce_f64_noalloc": [c_int, vp, i64, i64, vp, i64, vp, vp],
     "xnn_radius_graph_plan": [i64, c_f64p, c_i32p, dbl, c_f64p, c_f64p, ctypes.POINTER(GridPlan)],
     "xnn_radius_graph_count": [c_int, vp, i64, vp, dbl, i32, ctypes.POINTER(GridPlan), vp, vp, vp],
     "xnn_radius_graph_fill": [c_int, vp, i64, vp, dbl, i32, ctypes.POINTER(GridPlan), vp, vp, i64,
@@ -153,7 +155,8 @@ _SIGNATURES = {
 }
 _RESTYPES = {"xnn_last_error": ctypes.c_char_p, "xnn_scan_workspace_bytes": sz,
              "xnn_edge_plan_workspace_bytes": sz, "xnn_segment_reduce_workspace_bytes": sz,
-             "xnn_d4_workspace_bytes": sz, "xnn_virial_reduce_workspace_bytes": sz}
+             "xnn_d4_workspace_bytes": sz, "xnn_virial_reduce_workspace_bytes": sz,
+             "xnn_segment_reduce_noalloc_max_bytes": sz}
 
 _lock = threading.Lock()
 _lib: Optional[ctypes.CDLL] = None

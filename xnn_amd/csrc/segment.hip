@@ -9,6 +9,7 @@
 #include <algorithm>
 #include <cstdint>
 #include <cstdlib>
+#include <mutex>
 
 #include "common.h"
 #include "device.h"
@@ -956,6 +957,36 @@ static int segment_sum_t(const void* src, int64_t F, const int32_t* ptr, const i
 
 using namespace xnn;
 
+// ---------------------------------------------------------------- no-allocation variant
+// The partial sums of xnn_segment_reduce_f64_noalloc live in this file-scope device
+// array (one copy per GPU, held for the life of the process). Host code never passes
+// the name itself to a kernel: in host code it is a stand-in, not a device address. Each
+// device's address is looked up once, with that device current, and kept here.
+constexpr size_t kNoAllocScratchDoubles = 131072;  // 1 MiB
+static __device__ __align__(256) double scratch[kNoAllocScratchDoubles];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mutex;
+double* g_scratch_ptr[kMaxDevices] = {};
+
+// this device's address of `scratch`, looked up on its first use (with it current)
+int scratch_for_current_device(double** out) {
+  int dev = -1;
+  XNN_HIP_CHECK(hipGetDevice(&dev));
+  XNN_REQUIRE(dev >= 0 && dev < kMaxDevices, "device %d outside the scratch table", dev);
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* p = nullptr;
+    XNN_HIP_CHECK(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+    XNN_REQUIRE(p != nullptr, "no device address for the scratch array");
+    g_scratch_ptr[dev] = static_cast<double*>(p);
+  }
+  *out = g_scratch_ptr[dev];
+  return XNN_OK;
+}
+}  // namespace
+
 extern "C" {
 
 int xnn_sh_message_sum(int geom_dtype, const float* vec_in, const void* pos, int64_t n_nodes,
@@ -1146,6 +1177,28 @@ int xnn_virial_reduce(int dtype, const double* partial, int64_t n_rows, const in
                                   ws2_bytes, stream);
   if (st != XNN_OK) return st;
   return xnn_virial_finish(dtype, M, term, n_graphs, symmetrize, out, stream);
+}
+
+size_t xnn_segment_reduce_noalloc_max_bytes(void) { return sizeof(scratch); }
+
+int xnn_segment_reduce_f64_noalloc(int dtype, const void* src, int64_t n_rows,
+                                   int64_t n_features, const int64_t* seg_ptr,
+                                   int64_t n_segments, double* out, xnn_stream_t stream) {
+  XNN_REQUIRE(n_rows >= 0 && n_features >= 0 && n_segments >= 0, "negative size");
+  if (n_segments == 0 || n_features == 0) return XNN_OK;
+  const size_t need = xnn_segment_reduce_workspace_bytes(n_rows, n_features, n_segments);
+  XNN_REQUIRE(need <= sizeof(scratch),
+              "needs %zu bytes of partial sums, more than the %zu-byte scratch array of the "
+              "no-allocation entry point (use xnn_segment_reduce_f64 with a workspace)",
+              need, sizeof(scratch));
+  double* ws = nullptr;
+  if (need > 0) {
+    const int st = scratch_for_current_device(&ws);
+    if (st != XNN_OK) return st;
+  }
+  // every partial slot the kernels read is written first in the same call: no clearing
+  return xnn_segment_reduce_f64(dtype, src, n_rows, n_features, seg_ptr, n_segments, out, ws,
+                                need, stream);
 }
 
 }  // extern "C"
