@@ -508,8 +508,10 @@ class DFTD4(nn.Module):
                  alp: float = 16.0, ga: float = 3.0, gc: float = 2.0, wf: float = 6.0,
                  cutoff_pair: float = 60.0 * BOHR, cutoff_triple: float = 40.0 * BOHR,
                  cutoff_cn: float = 30.0 * BOHR, cutoff_eeq_cn: float = 25.0 * BOHR,
-                 switch_width_pair: float = 0.0, switch_width_triple: float = 0.0):
+                 switch_width_pair: float = 0.0, switch_width_triple: float = 0.0,
+                 tail_correction: bool = False):
         super().__init__()
+        self.tail_correction = bool(tail_correction)
         self.s6, self.s8, self.a1, self.a2 = float(s6), float(s8), float(a1), float(a2)
         self.s9, self.alp = float(s9), float(alp)
         self.ga, self.gc, self.wf = float(ga), float(gc), float(wf)
@@ -682,12 +684,71 @@ class DFTD4(nn.Module):
         e3 = torch.zeros_like(e2)
         if self.s9 != 0.0:
             e3 = self.three_body(zc, pos, cell64, pbc, n_atoms_h, cn, species, uniq)
+        e_tail = torch.zeros_like(e2)
+        if self.tail_correction and cell64 is not None:
+            parts = []
+            for b in range(B):
+                s0, s1 = sum(n_atoms_h[:b]), sum(n_atoms_h[:b + 1])
+                if periodic[b]:
+                    parts.append(self.tail_energy(zc[s0:s1], alpha[s0:s1], cell64[b] / BOHR))
+                else:
+                    parts.append(torch.zeros_like(e2[s0:s1]))
+            e_tail = torch.cat(parts) if parts else e_tail
         energy_2 = structure_sum_op(e2, node_ptr, batch32)        # fixed order, float64
         energy_3 = structure_sum_op(e3, node_ptr, batch32)
-        return {"node_energy": (e2 + e3) * HARTREE, "energy": (energy_2 + energy_3) * HARTREE,
+        energy_t = structure_sum_op(e_tail, node_ptr, batch32)
+        return {"node_energy": (e2 + e3 + e_tail) * HARTREE,
+                "energy": (energy_2 + energy_3 + energy_t) * HARTREE,
                 "energy_2body": energy_2 * HARTREE, "energy_3body": energy_3 * HARTREE,
+                "energy_tail": energy_t * HARTREE,
                 "coordination_numbers": cn, "charges": q,
-                "polarizabilities": alpha[:, 0], "dynamic_polarizabilities": alpha}
+                "polarizabilities": alpha[:, 0], "dynamic_polarizabilities": alpha,
+                "node_features": torch.stack([cn, q, alpha[:, 0]], dim=1)}
+
+    # ---- homogeneous tail of the pair sum beyond its cutoff (d4.py:1073-1140)
+    def tail_integrals(self, n_points: int = 48) -> Tensor:
+        """Per element pair (A, B), the radial integral of the BJ-damped two-body kernel that
+        the pair cutoff leaves out, ``J_AB = -int (1 - sw(r)) [s6 / (r^6 + R0^6) +
+        s8 rr / (r^8 + R0^8)] r^2 dr`` from the start of the switching window (the cutoff
+        when it is sharp) to infinity, bohr^-3, with ``rr = 3 Q_A Q_B`` and
+        ``R0 = a1 sqrt(rr) + a2``. The part beyond the cutoff is integrated in ``x = 1 / r``
+        (then ``r^2 dr / (r^n + R0^n) = x^(n-4) dx / (1 + R0^n x^n)`` on ``(0, 1 / rc]``), the
+        window in ``r``, each with ``n_points``-point Gauss-Legendre quadrature. Shape
+        ``(Z, Z)`` over the tables' atomic numbers."""
+        nodes, weights = np.polynomial.legendre.leggauss(n_points)
+        t = torch.as_tensor(nodes, dtype=torch.float64, device=self.r4r2.device)
+        w = torch.as_tensor(weights, dtype=torch.float64, device=self.r4r2.device)
+        rc = self.cutoff_pair / BOHR
+        rr = 3.0 * self.r4r2[:, None] * self.r4r2[None, :]
+        r0 = self.a1 * torch.sqrt(rr) + self.a2
+        p6, p8 = (r0 ** 6).unsqueeze(-1), (r0 ** 8).unsqueeze(-1)
+        rr3 = rr.unsqueeze(-1)
+        # x = 1 / r over (0, 1 / rc]: the midpoint map of [-1, 1] onto it
+        x, wx = (t + 1.0) * (0.5 / rc), w * (0.5 / rc)
+        beyond = self.s6 * x * x / (1.0 + p6 * x ** 6) + self.s8 * rr3 * x ** 4 / (1.0 + p8 * x ** 8)
+        total = (beyond * wx).sum(-1)
+        width = min(self.switch_width_pair, self.cutoff_pair) / BOHR
+        if width > 0.0:
+            r = (rc - width) + (t + 1.0) * (0.5 * width)
+            wr = w * (0.5 * width)
+            lost = (1.0 - switching_function(r, rc, width)) * r * r
+            inside = self.s6 / (r ** 6 + p6) + self.s8 * rr3 / (r ** 8 + p8)
+            total = total + (inside * lost * wr).sum(-1)
+        return -total
+
+    def tail_energy(self, z: Tensor, alpha: Tensor, cell_au: Tensor) -> Tensor:
+        """Per-atom tail correction of one periodic structure (hartree, d4.py:1109-1140):
+        each atom's pairs with every atom beyond the cutoff in a homogeneous continuum,
+        ``E_i = (2 pi / V) sum_B J(Z_i, B) C6(i, B)`` with ``C6(i, B)`` the Casimir-Polder
+        product of ``alpha_i`` with the summed polarizabilities of the structure's atoms of
+        element ``B``. Differentiable in ``alpha`` and the cell."""
+        vol = torch.linalg.det(cell_au).abs()
+        n_z = self.r4r2.shape[0]
+        by_element = torch.zeros((n_z, alpha.shape[1]), dtype=alpha.dtype,
+                                 device=alpha.device).index_add(0, z, alpha)
+        field = self.tail_integrals() @ by_element                     # (Z, 23)
+        # (2 pi / V) (3 / pi) sum_w cp_w alpha_i(w) field(Z_i, w)
+        return (6.0 / vol) * (alpha * cp_weights(alpha) * field.index_select(0, z)).sum(-1)
 
     def three_body(self, z: Tensor, pos: Tensor, cell64: Optional[Tensor], pbc: Optional[Tensor],
                    counts: List[int], cn: Tensor, species: Tensor, uniq: Tensor) -> Tensor:
