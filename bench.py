@@ -70,6 +70,12 @@ def kernel_costs(E: int, N: int, C: int, L: int = 16, K: int = 8, grouped: bool 
     come grouped by receiver. Flops count the true dimensions (no padding)."""
     perm = 0 if grouped else 4
     return {
+        "xnn_sh_radial_message_energy": {                  # radial basis and readout in-kernel
+            "bytes": E * (12 + perm) + N * (4 + 4) + 4 * C * L,  # vec in; ptr; E_i out; U
+            "flops": E * 2 * C * (K + L) + N * 2 * C * L},
+        "xnn_sh_radial_message_energy_backward": {         # the rows' cotangent g_i U in-kernel
+            "bytes": E * (12 + perm + 12) + N * 4 + 4 * C * L,   # vec in, g_vec out; ptr; U
+            "flops": E * 2 * C * (2 * K + 2 * L)},
         "xnn_sh_radial_message_sum": {                     # radial basis evaluated in-kernel
             "bytes": E * (12 + perm) + N * (4 * C * L + 4),
             "flops": E * 2 * C * (K + L)},
@@ -97,8 +103,12 @@ def kernel_costs(E: int, N: int, C: int, L: int = 16, K: int = 8, grouped: bool 
 def step_bytes(E: int, N: int, C: int, L: int, K: int, msg: str) -> int:
     """Compulsory traffic of one whole step: edge vectors from positions, featurizer
     (unless the message kernels evaluate the radial basis), message sum, readout (reads
-    A), its backward (writes d_A), message backward, featurizer backward, force reduction."""
+    A), its backward (writes d_A), message backward, featurizer backward, force reduction.
+    With the readout in the message kernels no (N, C, L) rows exist."""
     kc = kernel_costs(E, N, C, L, K)
+    if msg == "xnn_sh_radial_message_energy":
+        return (E * 24 + N * 12 + kc[msg]["bytes"] + kc[msg + "_backward"]["bytes"]
+                + kc["xnn_edge_force_reduce"]["bytes"])
     feat = 0 if msg == "xnn_sh_radial_message_sum" else (
         kc["xnn_edge_featurize"]["bytes"] + kc["xnn_edge_featurize_backward"]["bytes"])
     linear = 2 * (E * 4 * (K + C)) if msg == "xnn_sh_message_sum" else 0  # u @ W, d_phi @ W^T
@@ -141,6 +151,17 @@ def message_launches(msg: str, g, model, kw: dict) -> dict:
     head = (_lib.XNN_F32, _lib.ptr(vec), None, N, None, 0, None, None, None, E,
             _lib.ptr(plan.ptr_dst), _lib.ptr(plan.perm_dst))
     keep = (vec, W, d_out, out, g_vec, table, plan)
+    if msg == "xnn_sh_radial_message_energy":
+        U = model.U.detach().float().reshape(-1).contiguous()
+        z = g.atomic_numbers.to(torch.int64).contiguous()
+        bias = model.atom_ref.detach().float().contiguous()
+        energy = torch.empty(N, device=vec.device)
+        g_node = torch.full((1,), -1.0, device=vec.device)          # the forces' seed
+        keep = keep + (U, z, bias, energy, g_node)
+        return {msg: (head + (prm, _lib.ptr(table), C, _lib.ptr(W), _lib.ptr(U), _lib.ptr(z),
+                              _lib.ptr(bias), bias.shape[0], _lib.ptr(energy), s), keep),
+                msg + "_backward": (head + (prm, _lib.ptr(table), C, _lib.ptr(W), _lib.ptr(U),
+                                            _lib.ptr(g_node), 0, _lib.ptr(g_vec), s), keep)}
     if msg == "xnn_sh_radial_message_sum":
         return {msg: (head + (prm, _lib.ptr(table), C, _lib.ptr(W), _lib.ptr(out), s), keep),
                 msg + "_backward": (head + (prm, _lib.ptr(table), C, _lib.ptr(W),
@@ -762,6 +783,9 @@ def main() -> None:
     ap.add_argument("--fused-radial", action=argparse.BooleanOptionalAction, default=True,
                     help="radial basis evaluated inside the message kernels (ShEdgePotential "
                          "fused_radial)")
+    ap.add_argument("--fused-readout", action=argparse.BooleanOptionalAction, default=True,
+                    help="readout inside the radial message kernels (ShEdgePotential "
+                         "fused_readout)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run the 256 MiB copy that calibrates the HBM byte counters")
     args = ap.parse_args()
@@ -792,6 +816,7 @@ def main() -> None:
     g, model, rc, kw, workload, nl_ms, structs = build_workload(args.config, device)
     model.fused_linear = bool(args.fused)
     model.fused_radial = bool(args.fused_radial)
+    model.fused_readout = bool(args.fused_readout)
     E, N = g.num_edges, g.num_nodes
     C, L = kw["channels"], (kw["l_max"] + 1) ** 2
     wrapped = xa.ForceStressOutput(model, compute_stress=g.cell is not None).eval()
@@ -806,8 +831,9 @@ def main() -> None:
         out = step()
     # the message entry point the step took (radial basis in the kernel, linear layer in
     # the kernel, or the linear layer in PyTorch)
-    msg = next(m for m in ("xnn_sh_radial_message_sum", "xnn_sh_linear_message_sum",
-                           "xnn_sh_message_sum") if _lib.calls.get(m))
+    msg = next(m for m in ("xnn_sh_radial_message_energy", "xnn_sh_radial_message_sum",
+                           "xnn_sh_linear_message_sum", "xnn_sh_message_sum")
+               if _lib.calls.get(m))
     fused = msg != "xnn_sh_message_sum"
     kernels = [msg, msg + "_backward", "xnn_edge_featurize", "xnn_edge_featurize_backward",
                "xnn_edge_force_reduce"]

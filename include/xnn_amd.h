@@ -199,6 +199,35 @@ int xnn_sh_radial_message_sum(int geom_dtype, const float* vec_in, const void* p
                               int32_t n_channels, const float* W, float* out,
                               xnn_stream_t stream);
 
+/* xnn_sh_radial_message_sum followed by the linear per-atom readout of the node rows,
+ * in the same kernel: node_energy[i] = sum_{c,lm} U[c,lm] A[i,c,lm] + bias[z[i]] (bias
+ * NULL: no bias; an index z outside [0, n_bias) gives NaN), so the (N,C,L) rows never
+ * reach memory. It fuses the aggregation (gnn/fast/conv.py:137-143, ops.py:403-448) with
+ * a model's linear energy readout before aggregate_energy (common/models/base.py:161-180);
+ * the reference has no single counterpart. U (C,L) f32, z (N) int64, bias (n_bias) f32,
+ * node_energy (N) f32. Parameter gradients are not formed. */
+int xnn_sh_radial_message_energy(int geom_dtype, const float* vec_in, const void* pos,
+                                 int64_t n_nodes, const void* cell, int64_t n_graphs,
+                                 const int32_t* batch, const int32_t* src, const int32_t* shift,
+                                 int64_t n_edges, const int32_t* ptr_dst, const int32_t* perm_dst,
+                                 const xnn_featurize_params* prm, const float* rbf_table,
+                                 int32_t n_channels, const float* W, const float* U,
+                                 const int64_t* z, const float* bias, int64_t n_bias,
+                                 float* node_energy, xnn_stream_t stream);
+
+/* Backward of xnn_sh_radial_message_energy with respect to the edge vectors for the
+ * per-atom cotangent g (N) f32 of node_energy (g_stride 1, or 0: one value for every
+ * atom): the rows' cotangent g_i U is formed in the kernel. g_vec (E,3) f32 (written). */
+int xnn_sh_radial_message_energy_backward(int geom_dtype, const float* vec_in, const void* pos,
+                                          int64_t n_nodes, const void* cell, int64_t n_graphs,
+                                          const int32_t* batch, const int32_t* src,
+                                          const int32_t* shift, int64_t n_edges,
+                                          const int32_t* ptr_dst, const int32_t* perm_dst,
+                                          const xnn_featurize_params* prm,
+                                          const float* rbf_table, int32_t n_channels,
+                                          const float* W, const float* U, const float* g,
+                                          int64_t g_stride, float* g_vec, xnn_stream_t stream);
+
 /* Backward of xnn_sh_radial_message_sum with respect to the edge vectors, through the
  * harmonics and the radial basis: g_vec (E,3) f32 = dL/dr_e (written, not added).
  * Parameter gradients (W, rbf_table) are not formed: the caller uses

@@ -453,6 +453,74 @@ def test_sh_radial_message_sum_forward_backward(C, l_max, K, radial, envelope, s
                                                    sign).sum(), (vec,))
 
 
+@pytest.mark.parametrize("C,l_max,K,radial,envelope,sign,rc",
+                         [(128, 3, 8, "bessel", "polynomial", 1, 5.0),
+                          (64, 2, 8, "bessel", "cosine", -1, 5.0),
+                          (32, 1, 6, "gaussian", "polynomial", 1, 6.5),
+                          (128, 3, 8, "bessel", "polynomial", 1, 6.5)])
+def test_sh_radial_message_energy_forward_backward(C, l_max, K, radial, envelope, sign, rc):
+    """The readout fused into the radial message kernels: E_i = <U, A_i> + bias[z_i] and the
+    edge-vector gradient of sum_i g_i E_i, against the oracle (float64 autograd through the
+    materialized messages and the readout) and against the A-row kernels followed by the
+    readout (float32 rounding); a broadcast cotangent (the -1 seed of forces) equals the
+    same cotangent spelled out per atom, bit for bit."""
+    import oracle.reference as R
+    import xnn_amd as xa
+    from xnn_amd import synthetic
+    from xnn_amd.featurizers import SphericalHarmonicEdgeEmbedding
+    from xnn_amd.ops import node_readout_op
+    _note(f"sh_radial_message_energy C={C} l_max={l_max} K={K} {radial} {envelope} sign={sign}")
+    s = synthetic.water_box(n_molecules=216, box=18.6, grid=6, seed=4)
+    g = xa.structure_to_graph(s.as_dict(), rc, device=DEV)
+    g.pos = g.pos.float()
+    vec = g.edge_vectors().detach().requires_grad_(True)
+    emb = SphericalHarmonicEdgeEmbedding(l_max=l_max, n_rbf=K, cutoff=rc, radial_type=radial,
+                                         envelope=envelope).to(DEV)
+    emb.fast_active = True
+    L = (l_max + 1) ** 2
+    gen = torch.Generator().manual_seed(11 * C + K)
+    W = (torch.randn(K, C, generator=gen) / K ** 0.5).to(DEV)
+    U = (torch.randn(C, L, generator=gen) / (C * L) ** 0.5).to(DEV)
+    bias = torch.randn(10, generator=gen).to(DEV)
+    z = g.atomic_numbers
+    E = emb.radial_message_energy(vec, W, U, z, bias, g.plan(), sign)
+    gi = torch.randn(E.shape, generator=gen).to(DEV)
+    (gvec,) = torch.autograd.grad((E * gi).sum(), (vec,))
+    # the A-row kernels and the readout kernel
+    A = emb.radial_message_sum(vec, W, g.plan(), sign)
+    E_rows = node_readout_op(A.reshape(A.shape[0], -1), U.reshape(-1), z, bias)
+    (gvec_rows,) = torch.autograd.grad((E_rows * gi).sum(), (vec,))
+    e_scale = float(E_rows.abs().max())
+    np.testing.assert_allclose(E.detach().cpu(), E_rows.detach().cpu(), atol=2e-6 * e_scale)
+    g_scale = max(1.0, float(gvec_rows.abs().max()))
+    np.testing.assert_allclose(gvec.cpu(), gvec_rows.cpu(), atol=1e-6 * g_scale)
+    # oracle, float64
+    vc = vec.detach().cpu().double().requires_grad_(True)
+    Y = R.e3nn_sh(l_max, vc if sign == 1 else -vc)
+    rad = R.radial_features(torch.linalg.norm(vc, dim=-1), K, rc, radial, envelope)
+    msg = ((rad @ W.cpu().double())[:, :, None] * Y[:, None, :]).reshape(vc.shape[0], -1)
+    Ar = R.scatter_sum(msg, g.edge_index[1].cpu(), g.num_nodes)
+    Er = Ar @ U.cpu().double().reshape(-1) + bias.cpu().double()[z.cpu()]
+    (gv_r,) = torch.autograd.grad((Er * gi.cpu().double()).sum(), (vc,))
+    np.testing.assert_allclose(E.detach().cpu().double(), Er.detach(),
+                               atol=2e-6 * float(Er.abs().max()))
+    np.testing.assert_allclose(gvec.cpu().double(), gv_r,
+                               atol=2e-5 * max(1.0, float(gv_r.abs().max())))
+    # the broadcast seed equals the spelled-out one; run to run bit for bit
+    minus = torch.full((1,), -1.0, device=DEV).expand(E.shape[0])
+    (g_b,) = torch.autograd.grad([emb.radial_message_energy(vec, W, U, z, bias, g.plan(), sign)],
+                                 [vec], grad_outputs=[minus])
+    (g_f,) = torch.autograd.grad([emb.radial_message_energy(vec, W, U, z, bias, g.plan(), sign)],
+                                 [vec], grad_outputs=[torch.full_like(E, -1.0)])
+    assert torch.equal(g_b, g_f)
+    assert torch.equal(E, emb.radial_message_energy(vec, W, U, z, bias, g.plan(), sign))
+    # no bias; an atomic number outside the bias table is NaN, not a stray read
+    E0 = emb.radial_message_energy(vec, W, U, z, None, g.plan(), sign)
+    np.testing.assert_allclose((E - E0).detach().cpu(), bias[z].cpu(), atol=1e-5)
+    E_bad = emb.radial_message_energy(vec.detach(), W, U, torch.full_like(z, 99), bias, g.plan(), sign)
+    assert torch.isnan(E_bad).all()
+
+
 def test_segment_gather_and_structure_sums():
     import oracle.reference as R
     import xnn_amd as xa
@@ -663,7 +731,8 @@ def _float32_floor(R, g, params, cpu_pos, cell, ref, err):
     assert ours <= 2.0 * floor, (ours, floor)
 
 
-@pytest.mark.parametrize("config,fused", [("water", "radial"), ("water", "linear"),
+@pytest.mark.parametrize("config,fused", [("water", "radial"), ("water", "radial_rows"),
+                                          ("water", "linear"),
                                           ("water", "unfused"), ("argon", "radial"),
                                           ("ragged", "radial"), ("ragged", "linear"),
                                           ("ragged_1024", "radial"),
@@ -706,14 +775,15 @@ def test_model_energy_forces_stress(config, fused):
     if g.cell is not None:
         g.cell = g.cell.float()
     model = xa.ShEdgePotential(cutoff=rc, species=(1, 6, 7, 8, 18),
-                               fused_linear=fused != "unfused", fused_radial=fused == "radial",
-                               **kw).to(DEV)
+                               fused_linear=fused != "unfused",
+                               fused_radial=fused in ("radial", "radial_rows"),
+                               fused_readout=fused == "radial", **kw).to(DEV)
     before = dict(_lib.calls)
     out = xa.ForceStressOutput(model, compute_stress=g.cell is not None).eval()(g)
-    msg = {"radial": "xnn_sh_radial_message_sum", "linear": "xnn_sh_linear_message_sum",
-           "unfused": "xnn_sh_message_sum"}[fused]
+    msg = {"radial": "xnn_sh_radial_message_energy", "radial_rows": "xnn_sh_radial_message_sum",
+           "linear": "xnn_sh_linear_message_sum", "unfused": "xnn_sh_message_sum"}[fused]
     ran = [msg, msg + "_backward", "xnn_edge_force_reduce", "xnn_edge_featurize"]
-    if fused != "radial":
+    if fused not in ("radial", "radial_rows"):
         ran.append("xnn_edge_featurize_backward")
     for name in ran:
         assert _lib.calls.get(name, 0) > before.get(name, 0), f"{name} did not run"

@@ -98,6 +98,12 @@ _SIGNATURES = {
     "xnn_sh_radial_message_sum_backward": [c_int, vp, vp, i64, vp, i64, vp, vp, vp, i64, vp, vp,
                                            ctypes.POINTER(FeaturizeParams), vp, i32, vp, vp, vp,
                                            vp],
+    "xnn_sh_radial_message_energy": [c_int, vp, vp, i64, vp, i64, vp, vp, vp, i64, vp, vp,
+                                     ctypes.POINTER(FeaturizeParams), vp, i32, vp, vp, vp, vp,
+                                     i64, vp, vp],
+    "xnn_sh_radial_message_energy_backward": [c_int, vp, vp, i64, vp, i64, vp, vp, vp, i64, vp,
+                                              vp, ctypes.POINTER(FeaturizeParams), vp, i32, vp,
+                                              vp, vp, i64, vp, vp],
     "xnn_stress_finish": [c_int, vp, c_int, vp, vp, i64, dbl, vp, vp],
     "xnn_virial_finish": [c_int, vp, vp, i64, i32, vp, vp],
     "xnn_virial_reduce_workspace_bytes": [i64, i64],

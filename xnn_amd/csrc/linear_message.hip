@@ -132,14 +132,18 @@ __device__ __forceinline__ float radial_dot(const Radial<float>& R, const Radial
   return dl;
 }
 
-template <typename G, int LMAX, int T, bool RAD>
+// RO (readout): instead of the (C, L) row A_i the kernel writes the atom's energy
+// E_i = sum_{c, lm} U[c, lm] A_i[c, lm] + bias[z_i] (bias may be NULL), reduced across the
+// wave in a fixed order from the accumulators: A never reaches memory.
+template <typename G, int LMAX, int T, bool RAD, bool RO>
 __global__ __launch_bounds__(256, 4) void lin_msg_fwd_kernel(
     const float* __restrict__ vec, const G* __restrict__ pos, const G* __restrict__ cell,
     int64_t n_graphs, const int32_t* __restrict__ batch, const int32_t* __restrict__ src,
     const int32_t* __restrict__ shift, const int32_t* __restrict__ ptr,
     const int32_t* __restrict__ perm, int64_t n_nodes, float sign, int K,
     const float* __restrict__ h, Radial<float> R, const float* __restrict__ W,
-    float* __restrict__ out) {
+    float* __restrict__ out, const float* __restrict__ U, const int64_t* __restrict__ z,
+    const float* __restrict__ bias, int64_t n_bias) {
   constexpr int L = ShDims<LMAX>::L;
   constexpr int C = 16 * T;
   constexpr int KK = kLinKK;
@@ -157,6 +161,10 @@ __global__ __launch_bounds__(256, 4) void lin_msg_fwd_kernel(
   __shared__ __align__(16) float sW[kLinKMax * SWS];
   for (int i = threadIdx.x; i < kLinKMax * C; i += blockDim.x)
     sW[(i / C) * SWS + i % C] = i < K * C ? W[i] : 0.f;
+  // RO: the readout weights U (C, L), read by every row's epilogue
+  __shared__ float sU[RO ? C * L : 1];
+  if constexpr (RO)
+    for (int i = threadIdx.x; i < C * L; i += blockDim.x) sU[i] = U[i];
   __syncthreads();
   // M row lo of h W stands for edge 4 (lo % 4) + lo / 4 of the tile
   const int hrow = 4 * (lo & 3) + (lo >> 2);
@@ -249,31 +257,54 @@ __global__ __launch_bounds__(256, 4) void lin_msg_fwd_kernel(
       wave_sync();  // ys is rewritten by the next batch
     }
     // lane holds A[row, channel lo T + t, lm 4 hi + r]
-    float* o = out + (int64_t)row * C * L;
+    if constexpr (RO) {
+      float part = 0.f;
 #pragma unroll
-    for (int t = 0; t < T; ++t) {
-      float* oc = o + (int64_t)(lo * T + t) * L;
-      if constexpr (L % 4 == 0) {
-        if (4 * hi < L)
-          *reinterpret_cast<float4*>(oc + 4 * hi) =
-              make_float4(acc[t][0], acc[t][1], acc[t][2], acc[t][3]);
-      } else {
+      for (int t = 0; t < T; ++t)
 #pragma unroll
         for (int r = 0; r < 4; ++r)
-          if (4 * hi + r < L) oc[4 * hi + r] = acc[t][r];
+          if (4 * hi + r < L) part += acc[t][r] * sU[(lo * T + t) * L + 4 * hi + r];
+#pragma unroll
+      for (int m = kWave / 2; m >= 1; m >>= 1) part += __shfl_xor(part, m, kWave);
+      if (lane == 0) {
+        float b = 0.f;
+        if (bias != nullptr) {
+          const int64_t zz = z[row];
+          b = (zz >= 0 && zz < n_bias) ? bias[zz] : __builtin_nanf("");
+        }
+        out[row] = part + b;
+      }
+    } else {
+      float* o = out + (int64_t)row * C * L;
+#pragma unroll
+      for (int t = 0; t < T; ++t) {
+        float* oc = o + (int64_t)(lo * T + t) * L;
+        if constexpr (L % 4 == 0) {
+          if (4 * hi < L)
+            *reinterpret_cast<float4*>(oc + 4 * hi) =
+                make_float4(acc[t][0], acc[t][1], acc[t][2], acc[t][3]);
+        } else {
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+            if (4 * hi + r < L) oc[4 * hi + r] = acc[t][r];
+        }
       }
     }
   }
 }
 
-template <typename G, int LMAX, int T, bool RAD>
+// RO (readout): the cotangent of the row is d_A_i = g_i U (the adjoint of the readout
+// E_i = <U, A_i> + bias): U's two operand layouts are loaded once per wave and kept in
+// registers, and the row's products are scaled by g_i, so no (C, L) row is read or staged.
+template <typename G, int LMAX, int T, bool RAD, bool RO>
 __global__ __launch_bounds__(256, 3) void lin_msg_bwd_kernel(
     const float* __restrict__ vec, const G* __restrict__ pos, const G* __restrict__ cell,
     int64_t n_graphs, const int32_t* __restrict__ batch, const int32_t* __restrict__ src,
     const int32_t* __restrict__ shift, const int32_t* __restrict__ ptr,
     const int32_t* __restrict__ perm, int64_t n_nodes, float sign, int K,
     const float* __restrict__ h, Radial<float> R, const float* __restrict__ W,
-    const float* __restrict__ d_out, float* __restrict__ d_h, float* __restrict__ g_vec) {
+    const float* __restrict__ d_out, float* __restrict__ d_h, float* __restrict__ g_vec,
+    const float* __restrict__ U, const float* __restrict__ g_node, int64_t g_stride) {
   constexpr int L = ShDims<LMAX>::L;
   constexpr int C = 16 * T;
   constexpr int KS = (L + 3) / 4;
@@ -315,9 +346,25 @@ __global__ __launch_bounds__(256, 3) void lin_msg_bwd_kernel(
     return SWZ ? c * 16 + ((((lm >> 2) ^ (c / T)) & 3) << 2) + (lm & 3) : c * L + lm;
   };
   const int64_t n_waves = (int64_t)gridDim.x * kWavesPerBlock;
+  // the G operands: G[lo T + t][4 s + hi] (A of d_phi) and G[(4 hi + r) T + t][lo] (B of dY)
+  float gA[T][KS], gB[T][4];
+  if constexpr (RO) {
+#pragma unroll
+    for (int t = 0; t < T; ++t) {
+#pragma unroll
+      for (int ss = 0; ss < KS; ++ss) {
+        const int lm = 4 * ss + hi;
+        gA[t][ss] = lm < L ? U[(lo * T + t) * L + lm] : 0.f;
+      }
+#pragma unroll
+      for (int r = 0; r < 4; ++r) gB[t][r] = lo < L ? U[((4 * hi + r) * T + t) * L + lo] : 0.f;
+    }
+  }
   for (int64_t row = (int64_t)blockIdx.x * kWavesPerBlock + wave; row < n_nodes; row += n_waves) {
     const int b0 = ptr[row], b1 = ptr[row + 1];
     if (b0 == b1) continue;
+    // RO: the row's cotangent scale g_i (1 otherwise)
+    const float gscale = RO ? g_node[row * g_stride] : 1.f;
     // with given edge vectors, the first batch's are loaded before G is staged, so that
     // the two loads' latencies overlap
     float cx = 0.f, cy = 0.f, cz = 0.f;
@@ -326,7 +373,7 @@ __global__ __launch_bounds__(256, 3) void lin_msg_bwd_kernel(
                                   : (n_graphs <= 1 || batch == nullptr ? cell
                                                                        : cell + 9 * (int64_t)batch[row]);
     // stage G = d_out[row] (C x L) through LDS into the two operand layouts
-    {
+    if constexpr (!RO) {
       const float4* g4 = reinterpret_cast<const float4*>(d_out + (int64_t)row * C * L);
       float4* s4 = reinterpret_cast<float4*>(sbuf[wave]);
       for (int i = lane; i < C * L / 4; i += kWave) {
@@ -346,19 +393,20 @@ __global__ __launch_bounds__(256, 3) void lin_msg_bwd_kernel(
       }
     }
     wave_sync();
-    float gA[T][KS], gB[T][4];
+    if constexpr (!RO) {
 #pragma unroll
-    for (int t = 0; t < T; ++t) {
+      for (int t = 0; t < T; ++t) {
 #pragma unroll
-      for (int s = 0; s < KS; ++s) {
-        const int lm = 4 * s + hi;
-        gA[t][s] = lm < L ? sbuf[wave][g_at(lo * T + t, lm)] : 0.f;  // G[lo T + t][4 s + hi]
+        for (int ss = 0; ss < KS; ++ss) {
+          const int lm = 4 * ss + hi;
+          gA[t][ss] = lm < L ? sbuf[wave][g_at(lo * T + t, lm)] : 0.f;  // G[lo T + t][4 s + hi]
+        }
+#pragma unroll
+        for (int r = 0; r < 4; ++r)  // G[(4 hi + r) T + t][lo]
+          gB[t][r] = lo < L ? sbuf[wave][g_at((4 * hi + r) * T + t, lo)] : 0.f;
       }
-#pragma unroll
-      for (int r = 0; r < 4; ++r)  // G[(4 hi + r) T + t][lo]
-        gB[t][r] = lo < L ? sbuf[wave][g_at((4 * hi + r) * T + t, lo)] : 0.f;
+      wave_sync();  // the staging area becomes ys / sdy
     }
-    wave_sync();  // the staging area becomes ys / sdy
 
     for (int base = b0; base < b1; base += kWave) {
       const int cnt = min(kWave, b1 - base);
@@ -429,7 +477,7 @@ __global__ __launch_bounds__(256, 3) void lin_msg_bwd_kernel(
             for (int r = 0; r < 4; ++r) dy = mfma_16x16x4(pt[t][r], gB[t][r], dy);
           // dy[r] = dY[edge 16 tau + 4 hi + r][lm lo]
 #pragma unroll
-          for (int r = 0; r < 4; ++r) sdy[(16 * tau + 4 * hi + r) * kSY + lo] = dy[r];
+          for (int r = 0; r < 4; ++r) sdy[(16 * tau + 4 * hi + r) * kSY + lo] = gscale * dy[r];
         }
         // keep phi^T and d_phi from being live together
         __builtin_amdgcn_sched_barrier(0);
@@ -477,8 +525,8 @@ __global__ __launch_bounds__(256, 3) void lin_msg_bwd_kernel(
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
               float* row_h = hs + (16 * tau + 4 * (lo >> 2) + i) * kSH + (lo & 3);
-              row_h[0] = dq0[i];
-              row_h[4] = dq1[i];
+              row_h[0] = gscale * dq0[i];
+              row_h[4] = gscale * dq1[i];
             }
           }
         } else {
@@ -487,8 +535,8 @@ __global__ __launch_bounds__(256, 3) void lin_msg_bwd_kernel(
             const int j = 16 * tau + 4 * (lo >> 2) + i;
             const int ej = __shfl(my_e, j);
             if (hi == 0 && j < cnt) {
-              if ((lo & 3) < K) d_h[(int64_t)ej * K + (lo & 3)] = dq0[i];
-              if (4 + (lo & 3) < K) d_h[(int64_t)ej * K + 4 + (lo & 3)] = dq1[i];
+              if ((lo & 3) < K) d_h[(int64_t)ej * K + (lo & 3)] = gscale * dq0[i];
+              if (4 + (lo & 3) < K) d_h[(int64_t)ej * K + 4 + (lo & 3)] = gscale * dq1[i];
             }
           }
         }
@@ -522,31 +570,41 @@ __global__ __launch_bounds__(256, 3) void lin_msg_bwd_kernel(
   }
 }
 
-template <typename G, bool RAD>
+// the readout arguments of the RO kernels (all NULL / 0 for the A-row kernels)
+struct Readout {
+  const float* U = nullptr;       // (C, L)
+  const int64_t* z = nullptr;     // forward: per-atom bias index
+  const float* bias = nullptr;    // forward: per-index bias (may be NULL)
+  int64_t n_bias = 0;
+  const float* g = nullptr;       // backward: per-atom cotangent of E_i
+  int64_t g_stride = 1;
+};
+
+template <typename G, bool RAD, bool RO>
 static void lin_msg_launch(bool backward, const float* vec, const void* pos, int64_t n_nodes,
                            const void* cell, int64_t n_graphs, const int32_t* batch,
                            const int32_t* src, const int32_t* shift, const int32_t* ptr,
                            const int32_t* perm, int l_max, int sign, int K, int C,
                            const float* h, const Radial<float>& R, const float* W,
                            const float* d_out, float* out_or_dh, float* g_vec,
-                           hipStream_t stream) {
+                           const Readout& ro, hipStream_t stream) {
   const int64_t blocks_needed = grid_1d(n_nodes, kWavesPerBlock);
   const dim3 block(kWavesPerBlock * kWave);
   const float sg = (float)sign;
 #define XNN_LIN(LM, TT)                                                                        \
   do {                                                                                         \
     if (backward) {                                                                            \
-      auto k = lin_msg_bwd_kernel<G, LM, TT, RAD>;                                             \
+      auto k = lin_msg_bwd_kernel<G, LM, TT, RAD, RO>;                                         \
       const dim3 grid((unsigned)resident_blocks((const void*)k, block.x, blocks_needed));      \
       hipLaunchKernelGGL(k, grid, block, 0, stream, vec, (const G*)pos, (const G*)cell,        \
                          n_graphs, batch, src, shift, ptr, perm, n_nodes, sg, K, h, R, W,       \
-                         d_out, out_or_dh, g_vec);                                             \
+                         d_out, out_or_dh, g_vec, ro.U, ro.g, ro.g_stride);                    \
     } else {                                                                                   \
-      auto k = lin_msg_fwd_kernel<G, LM, TT, RAD>;                                             \
+      auto k = lin_msg_fwd_kernel<G, LM, TT, RAD, RO>;                                         \
       const dim3 grid((unsigned)resident_blocks((const void*)k, block.x, blocks_needed));      \
       hipLaunchKernelGGL(k, grid, block, 0, stream, vec, (const G*)pos, (const G*)cell,        \
                          n_graphs, batch, src, shift, ptr, perm, n_nodes, sg, K, h, R, W,       \
-                         out_or_dh);                                                           \
+                         out_or_dh, ro.U, ro.z, ro.bias, ro.n_bias);                           \
     }                                                                                          \
   } while (0)
 #define XNN_LIN_L(TT)                   \
@@ -564,23 +622,28 @@ static void lin_msg_launch(bool backward, const float* vec, const void* pos, int
 #undef XNN_LIN
 }
 
-// R == nullptr: h is given (E, K); else h is evaluated in the kernels from R (K = R->K)
+// R == nullptr: h is given (E, K); else h is evaluated in the kernels from R (K = R->K).
+// ro != nullptr: the readout kernels (R must be given).
 template <typename G>
 static int lin_msg(bool backward, const float* vec, const void* pos, int64_t n_nodes,
                    const void* cell, int64_t n_graphs, const int32_t* batch, const int32_t* src,
                    const int32_t* shift, const int32_t* ptr, const int32_t* perm, int l_max,
                    int sign, int K, int C, const float* h, const Radial<float>* R,
                    const float* W, const float* d_out, float* out_or_dh, float* g_vec,
-                   hipStream_t stream) {
+                   hipStream_t stream, const Readout* ro = nullptr) {
   if (n_nodes == 0) return XNN_OK;
-  if (R != nullptr)
-    lin_msg_launch<G, true>(backward, vec, pos, n_nodes, cell, n_graphs, batch, src, shift, ptr,
-                            perm, l_max, sign, R->K, C, nullptr, *R, W, d_out, out_or_dh, g_vec,
-                            stream);
+  if (ro != nullptr)
+    lin_msg_launch<G, true, true>(backward, vec, pos, n_nodes, cell, n_graphs, batch, src,
+                                  shift, ptr, perm, l_max, sign, R->K, C, nullptr, *R, W, d_out,
+                                  out_or_dh, g_vec, *ro, stream);
+  else if (R != nullptr)
+    lin_msg_launch<G, true, false>(backward, vec, pos, n_nodes, cell, n_graphs, batch, src,
+                                   shift, ptr, perm, l_max, sign, R->K, C, nullptr, *R, W, d_out,
+                                   out_or_dh, g_vec, Readout{}, stream);
   else
-    lin_msg_launch<G, false>(backward, vec, pos, n_nodes, cell, n_graphs, batch, src, shift,
-                             ptr, perm, l_max, sign, K, C, h, Radial<float>{}, W, d_out,
-                             out_or_dh, g_vec, stream);
+    lin_msg_launch<G, false, false>(backward, vec, pos, n_nodes, cell, n_graphs, batch, src,
+                                    shift, ptr, perm, l_max, sign, K, C, h, Radial<float>{}, W,
+                                    d_out, out_or_dh, g_vec, Readout{}, stream);
   XNN_LAUNCH_CHECK();
   return XNN_OK;
 }
@@ -712,6 +775,77 @@ int xnn_sh_radial_message_sum_backward(int geom_dtype, const float* vec_in, cons
     return lin_msg<double>(true, vec_in, pos, n_nodes, cell, n_graphs, batch, src, shift,
                            ptr_dst, perm_dst, prm->l_max, prm->sh_sign, R.K, n_channels, nullptr,
                            &R, W, d_out, nullptr, g_vec, as_hip(stream));
+  set_error("unsupported geometry dtype %d", geom_dtype);
+  return XNN_EINVAL;
+}
+
+int xnn_sh_radial_message_energy(int geom_dtype, const float* vec_in, const void* pos,
+                                 int64_t n_nodes, const void* cell, int64_t n_graphs,
+                                 const int32_t* batch, const int32_t* src, const int32_t* shift,
+                                 int64_t n_edges, const int32_t* ptr_dst, const int32_t* perm_dst,
+                                 const xnn_featurize_params* prm, const float* rbf_table,
+                                 int32_t n_channels, const float* W, const float* U,
+                                 const int64_t* z, const float* bias, int64_t n_bias,
+                                 float* node_energy, xnn_stream_t stream) {
+  Radial<float> R;
+  int st = make_radial<float>(prm, rbf_table, R);
+  if (st != XNN_OK) return st;
+  st = lin_check(n_nodes, n_edges, prm->l_max, prm->sh_sign, prm->n_rbf, n_channels);
+  if (st != XNN_OK) return st;
+  XNN_REQUIRE(n_nodes == 0 || (ptr_dst && node_energy && W && U), "NULL CSR, weights or output");
+  XNN_REQUIRE(bias == nullptr || (z != nullptr && n_bias > 0), "bias needs z and n_bias > 0");
+  XNN_REQUIRE(n_edges == 0 || vec_in || (pos && src && shift), "NULL edge input");
+  XNN_REQUIRE(cell == nullptr || n_graphs <= 1 || batch != nullptr,
+              "several cells need the batch vector");
+  Readout ro;
+  ro.U = U;
+  ro.z = z;
+  ro.bias = bias;
+  ro.n_bias = n_bias;
+  if (geom_dtype == XNN_F32)
+    return lin_msg<float>(false, vec_in, pos, n_nodes, cell, n_graphs, batch, src, shift, ptr_dst,
+                          perm_dst, prm->l_max, prm->sh_sign, R.K, n_channels, nullptr, &R, W,
+                          nullptr, node_energy, nullptr, as_hip(stream), &ro);
+  if (geom_dtype == XNN_F64)
+    return lin_msg<double>(false, vec_in, pos, n_nodes, cell, n_graphs, batch, src, shift,
+                           ptr_dst, perm_dst, prm->l_max, prm->sh_sign, R.K, n_channels, nullptr,
+                           &R, W, nullptr, node_energy, nullptr, as_hip(stream), &ro);
+  set_error("unsupported geometry dtype %d", geom_dtype);
+  return XNN_EINVAL;
+}
+
+int xnn_sh_radial_message_energy_backward(int geom_dtype, const float* vec_in, const void* pos,
+                                          int64_t n_nodes, const void* cell, int64_t n_graphs,
+                                          const int32_t* batch, const int32_t* src,
+                                          const int32_t* shift, int64_t n_edges,
+                                          const int32_t* ptr_dst, const int32_t* perm_dst,
+                                          const xnn_featurize_params* prm,
+                                          const float* rbf_table, int32_t n_channels,
+                                          const float* W, const float* U, const float* g,
+                                          int64_t g_stride, float* g_vec, xnn_stream_t stream) {
+  Radial<float> R;
+  int st = make_radial<float>(prm, rbf_table, R);
+  if (st != XNN_OK) return st;
+  st = lin_check(n_nodes, n_edges, prm->l_max, prm->sh_sign, prm->n_rbf, n_channels);
+  if (st != XNN_OK) return st;
+  XNN_REQUIRE(n_nodes == 0 || (ptr_dst && g && W && U), "NULL CSR, weights or cotangent");
+  XNN_REQUIRE(g_stride == 0 || g_stride == 1, "g_stride must be 0 (broadcast) or 1");
+  XNN_REQUIRE(n_edges == 0 || ((vec_in || (pos && src && shift)) && g_vec),
+              "NULL edge input or output");
+  XNN_REQUIRE(cell == nullptr || n_graphs <= 1 || batch != nullptr,
+              "several cells need the batch vector");
+  Readout ro;
+  ro.U = U;
+  ro.g = g;
+  ro.g_stride = g_stride;
+  if (geom_dtype == XNN_F32)
+    return lin_msg<float>(true, vec_in, pos, n_nodes, cell, n_graphs, batch, src, shift, ptr_dst,
+                          perm_dst, prm->l_max, prm->sh_sign, R.K, n_channels, nullptr, &R, W,
+                          nullptr, nullptr, g_vec, as_hip(stream), &ro);
+  if (geom_dtype == XNN_F64)
+    return lin_msg<double>(true, vec_in, pos, n_nodes, cell, n_graphs, batch, src, shift,
+                           ptr_dst, perm_dst, prm->l_max, prm->sh_sign, R.K, n_channels, nullptr,
+                           &R, W, nullptr, nullptr, g_vec, as_hip(stream), &ro);
   set_error("unsupported geometry dtype %d", geom_dtype);
   return XNN_EINVAL;
 }

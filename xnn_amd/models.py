@@ -96,7 +96,9 @@ class ShEdgePotential(InteratomicPotential):
     counts the fused kernels take) the radial linear layer runs inside the message
     kernels too, so ``phi`` is never stored either, and with ``fused_radial`` (the
     default) forces and stress evaluate the radial basis inside those kernels as well
-    (one kernel each way; parameter gradients take the two-kernel path). ``use_fast=False`` or a CPU evaluates
+    (one kernel each way; parameter gradients take the two-kernel path); with
+    ``fused_readout`` (the default) those kernels also apply the readout, so the
+    (N, C, L) rows are never stored and the backward forms their cotangent g_i U itself. ``use_fast=False`` or a CPU evaluates
     the same function with the PyTorch formulation.
     """
 
@@ -108,7 +110,7 @@ class ShEdgePotential(InteratomicPotential):
                  channels: int = 128, cutoff: float = 5.0, radial_type: str = "bessel",
                  envelope: str = "polynomial", p: int = 6, sh_sign: int = 1,
                  use_fast: UseFast = "auto", seed: Optional[int] = 0, fused_linear: bool = True,
-                 fused_radial: bool = True):
+                 fused_radial: bool = True, fused_readout: bool = True):
         super().__init__()
         self.cutoff = float(cutoff)
         self.l_max = int(l_max)
@@ -116,6 +118,7 @@ class ShEdgePotential(InteratomicPotential):
         self.sh_sign = int(sh_sign)
         self.fused_linear = bool(fused_linear)
         self.fused_radial = bool(fused_radial)
+        self.fused_readout = bool(fused_readout)
         self.use_fast = resolve_use_fast(use_fast)
         self.double_backward = False
         # False while ForceStressOutput evaluates forces only (no parameter gradients)
@@ -166,6 +169,18 @@ class ShEdgePotential(InteratomicPotential):
         select(fast_modules(self), self.use_fast, MI355X_POLICY, data.pos.device, dtype,
                data.num_edges, double_backward=self.double_backward)
         vec = data.edge_vectors()
+        feat = self.edge_feat
+        if (feat.fast_active and self.fused_radial and self.fused_readout and not self.param_grads
+                and not feat.radial_trainable and vec.dtype == torch.float32):
+            from .ops import linear_message_supported
+            if linear_message_supported(self.W.shape[0], self.W.shape[1], self.l_max):
+                # forces and stress only: radial basis, linear layer, message and readout in
+                # one kernel each way (neither u, phi nor the (N, C, L) rows are stored)
+                node_energy = feat.radial_message_energy(
+                    vec, self.W.detach().float(), self.U.detach().float(), data.atomic_numbers,
+                    self.atom_ref.detach(), data.plan(), self.sh_sign)
+                return {"node_energy": node_energy,
+                        "energy": self.aggregate_energy(node_energy, data)}
         A = self.messages(data, vec)
         # readout E_i = <U, A_i> + atom_ref[Z_i]: on the fast path one HIP launch each
         # way (the rows streamed once, the reference energy gathered in the same pass)

@@ -646,6 +646,89 @@ def sh_radial_message_sum(vec: Tensor, rbf_table: Tensor, W: Tensor, plan: EdgeP
                                     plan.perm_dst, iparams, fparams)
 
 
+@torch.library.custom_op(f"{_NS}::sh_radial_message_energy", mutates_args=())
+def sh_radial_message_energy_op(vec: Tensor, rbf_table: Tensor, W: Tensor, U: Tensor,
+                                z: Tensor, bias: Optional[Tensor], ptr_dst: Tensor,
+                                perm_dst: Optional[Tensor], iparams: List[int],
+                                fparams: List[float]) -> Tensor:
+    """Per-atom energies ``E_i = <U, A_i> + bias[z_i]`` of the rows
+    ``A_i = sum_{dst(e)=i} (h_e W) (x) Y(sign vec_e)`` (float32), formed and read out in
+    one kernel: the (N, C, L) rows never reach memory."""
+    dev = _require_gpu(vec, W)
+    n_nodes = ptr_dst.shape[0] - 1
+    out = torch.empty(n_nodes, dtype=torch.float32, device=dev)
+    _lib.call("xnn_sh_radial_message_energy", _lib.XNN_F32, _lib.ptr(vec), None, n_nodes, None, 0,
+              None, None, None, vec.shape[0], _lib.ptr(ptr_dst), _lib.ptr(perm_dst),
+              _params(iparams, fparams), _lib.ptr(rbf_table), W.shape[1], _lib.ptr(W),
+              _lib.ptr(U), _lib.ptr(z), _lib.ptr(bias), 0 if bias is None else bias.shape[0],
+              _lib.ptr(out), _lib.stream(dev))
+    return out
+
+
+@sh_radial_message_energy_op.register_fake
+def _(vec, rbf_table, W, U, z, bias, ptr_dst, perm_dst, iparams, fparams):
+    return vec.new_empty(ptr_dst.shape[0] - 1)
+
+
+def _rad_energy_setup(ctx, inputs, output):
+    vec, rbf_table, W, U, z, bias, ptr_dst, perm_dst, iparams, fparams = inputs
+    ctx.save_for_backward(vec, rbf_table, W, U, ptr_dst, perm_dst)
+    ctx.iparams, ctx.fparams = list(iparams), list(fparams)
+
+
+def _rad_energy_backward(ctx, g):
+    _once_differentiable()
+    if any(ctx.needs_input_grad[1:4]) or ctx.needs_input_grad[5]:
+        raise NotImplementedError("sh_radial_message_energy differentiates the edge vectors "
+                                  "only; train the weights with the A-row kernels")
+    vec, rbf_table, W, U, ptr_dst, perm_dst = ctx.saved_tensors
+    # a broadcast cotangent (d sum_i E_i, or its -1 seed) is read as one value
+    stride = 0 if (g.dim() == 1 and g.stride(0) == 0) else 1
+    g = g.to(torch.float32)
+    if stride == 1:
+        g = g.contiguous()
+    g_vec = torch.empty_like(vec)
+    _lib.call("xnn_sh_radial_message_energy_backward", _lib.XNN_F32, _lib.ptr(vec), None,
+              ptr_dst.shape[0] - 1, None, 0, None, None, None, vec.shape[0], _lib.ptr(ptr_dst),
+              _lib.ptr(perm_dst), _params(ctx.iparams, ctx.fparams), _lib.ptr(rbf_table),
+              W.shape[1], _lib.ptr(W), _lib.ptr(U), _lib.ptr(g), stride, _lib.ptr(g_vec),
+              _lib.stream(vec.device))
+    return (g_vec,) + (None,) * 9
+
+
+sh_radial_message_energy_op.register_autograd(_rad_energy_backward,
+                                              setup_context=_rad_energy_setup)
+
+
+def sh_radial_message_energy(vec: Tensor, rbf_table: Tensor, W: Tensor, U: Tensor, z: Tensor,
+                             bias: Optional[Tensor], plan: EdgePlan, *, basis: str,
+                             envelope: str, poly_p: int, l_max: int, cutoff: float,
+                             prefactor: float = 1.0, gamma: float = 1.0,
+                             sh_sign: int = 1) -> Tensor:
+    """:func:`sh_radial_message_sum` read out in the kernel: the per-atom energies
+    ``<U, A_i> + bias[z_i]`` (U: (C, (l_max+1)^2), bias indexed by ``z``, may be None);
+    differentiable in ``vec`` only."""
+    if vec.dtype != torch.float32 or W.dtype != torch.float32 or U.dtype != torch.float32:
+        raise TypeError("sh_radial_message_energy computes in float32")
+    n_rbf, C = W.shape
+    L = (int(l_max) + 1) ** 2
+    if rbf_table.numel() != n_rbf:
+        raise ValueError("W needs one row per radial basis function")
+    if U.numel() != C * L:
+        raise ValueError(f"U needs {C} x {L} readout weights")
+    if not linear_message_supported(n_rbf, C, l_max):
+        raise ValueError(f"sh_radial_message_energy takes {LINEAR_MESSAGE_CHANNELS} channels, at "
+                         f"most {LINEAR_MESSAGE_MAX_FEATURES} basis functions and l_max in [1, 3]")
+    iparams = [int(n_rbf), _lib.BASIS[basis], _lib.ENVELOPE[envelope], int(poly_p), int(l_max),
+               int(sh_sign)]
+    fparams = [float(cutoff), float(prefactor), float(gamma)]
+    table = rbf_table.to(device=vec.device, dtype=torch.float32).contiguous()
+    b = None if bias is None else bias.to(device=vec.device, dtype=torch.float32).contiguous()
+    return sh_radial_message_energy_op(vec.contiguous(), table, W.contiguous(),
+                                       U.reshape(-1).contiguous(), z.to(torch.int64).contiguous(),
+                                       b, plan.ptr_dst, plan.perm_dst, iparams, fparams)
+
+
 # --------------------------------------------------------------------------- segment sums
 @torch.library.custom_op(f"{_NS}::segment_sum", mutates_args=())
 def segment_sum_op(src: Tensor, index32: Tensor, ptr: Tensor, perm: Optional[Tensor]) -> Tensor:
