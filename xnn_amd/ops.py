@@ -79,7 +79,8 @@ def _opt(t: Optional[Tensor]) -> Optional[Tensor]:
 @torch.library.custom_op(f"{_NS}::edge_vectors", mutates_args=())
 def edge_vectors_op(pos: Tensor, cell: Optional[Tensor], batch32: Tensor, src: Tensor, dst: Tensor,
                     shift: Tensor, ptr_dst: Tensor, perm_dst: Optional[Tensor], ptr_src: Tensor,
-                    perm_src: Tensor, node_ptr: Tensor, out_dtype: int) -> Tensor:
+                    perm_src: Tensor, visit: Optional[Tensor], node_ptr: Tensor,
+                    out_dtype: int) -> Tensor:
     """``pos[dst] - pos[src] + shift @ cell`` per edge, formed in the geometry dtype and
     returned in ``out_dtype`` (atomic_data.py:371-418)."""
     dev = _require_gpu(pos)
@@ -97,7 +98,7 @@ def edge_vectors_op(pos: Tensor, cell: Optional[Tensor], batch32: Tensor, src: T
 
 
 @edge_vectors_op.register_fake
-def _(pos, cell, batch32, src, dst, shift, ptr_dst, perm_dst, ptr_src, perm_src, node_ptr,
+def _(pos, cell, batch32, src, dst, shift, ptr_dst, perm_dst, ptr_src, perm_src, visit, node_ptr,
       out_dtype):
     odt = torch.float32 if out_dtype == _lib.XNN_F32 else torch.float64
     return pos.new_empty((src.shape[0], 3), dtype=odt)
@@ -106,8 +107,9 @@ def _(pos, cell, batch32, src, dst, shift, ptr_dst, perm_dst, ptr_src, perm_src,
 @torch.library.custom_op(f"{_NS}::force_reduce", mutates_args=())
 def force_reduce_op(g_edge: Tensor, cell_like: Optional[Tensor], batch32: Tensor, src: Tensor,
                     dst: Tensor, shift: Tensor, ptr_dst: Tensor, perm_dst: Optional[Tensor],
-                    ptr_src: Tensor, perm_src: Tensor, node_ptr: Tensor, n_nodes: int,
-                    geom_code: int, want_cell: bool) -> Tuple[Tensor, Tensor]:
+                    ptr_src: Tensor, perm_src: Tensor, visit: Optional[Tensor],
+                    node_ptr: Tensor, n_nodes: int, geom_code: int,
+                    want_cell: bool) -> Tuple[Tensor, Tensor]:
     """Adjoint of :func:`edge_vectors_op`: ``grad_pos[i] = sum_{dst=i} g - sum_{src=i} g``
     and, when ``want_cell``, ``grad_cell[b] = sum_{edges of b} shift^T g`` (float64
     accumulation, returned in the geometry dtype) (atomic_data.py:452-467)."""
@@ -120,16 +122,16 @@ def force_reduce_op(g_edge: Tensor, cell_like: Optional[Tensor], batch32: Tensor
     s = _lib.stream(dev)
     _lib.call("xnn_edge_force_reduce", geom_code, _lib.dtype_code(g_edge.dtype), _lib.ptr(g_edge),
               g_edge.shape[0], _lib.ptr(ptr_dst), _lib.ptr(perm_dst), _lib.ptr(ptr_src),
-              _lib.ptr(perm_src), _lib.ptr(shift), n_nodes, _lib.ptr(grad_pos),
-              _lib.ptr(partial), None, None, s)
+              _lib.ptr(perm_src), _lib.ptr(shift), _lib.ptr(visit), n_nodes,
+              _lib.ptr(grad_pos), _lib.ptr(partial), None, None, s)
     if not want_cell:
         return grad_pos, grad_pos.new_zeros((0,))
     return grad_pos, _lib.virial_reduce(partial, n_nodes, node_ptr, n_graphs, None, False, gdt)
 
 
 @force_reduce_op.register_fake
-def _(g_edge, cell_like, batch32, src, dst, shift, ptr_dst, perm_dst, ptr_src, perm_src, node_ptr,
-      n_nodes, geom_code, want_cell):
+def _(g_edge, cell_like, batch32, src, dst, shift, ptr_dst, perm_dst, ptr_src, perm_src, visit,
+      node_ptr, n_nodes, geom_code, want_cell):
     gdt = torch.float32 if geom_code == _lib.XNN_F32 else torch.float64
     n_graphs = node_ptr.shape[0] - 1
     return (g_edge.new_empty((n_nodes, 3), dtype=gdt),
@@ -137,38 +139,42 @@ def _(g_edge, cell_like, batch32, src, dst, shift, ptr_dst, perm_dst, ptr_src, p
 
 
 def _edge_vectors_setup(ctx, inputs, output):
-    (pos, cell, batch32, src, dst, shift, ptr_dst, perm_dst, ptr_src, perm_src, node_ptr,
-     out_dtype) = inputs
-    ctx.save_for_backward(batch32, src, dst, shift, ptr_dst, perm_dst, ptr_src, perm_src, node_ptr)
+    (pos, cell, batch32, src, dst, shift, ptr_dst, perm_dst, ptr_src, perm_src, visit,
+     node_ptr, out_dtype) = inputs
+    ctx.save_for_backward(batch32, src, dst, shift, ptr_dst, perm_dst, ptr_src, perm_src, visit,
+                          node_ptr)
     ctx.n_nodes = pos.shape[0]
     ctx.geom_code = _lib.dtype_code(pos.dtype)
     ctx.has_cell = cell is not None and cell.numel() > 0
 
 
 def _edge_vectors_backward(ctx, grad):
-    batch32, src, dst, shift, ptr_dst, perm_dst, ptr_src, perm_src, node_ptr = ctx.saved_tensors
+    (batch32, src, dst, shift, ptr_dst, perm_dst, ptr_src, perm_src, visit,
+     node_ptr) = ctx.saved_tensors
     want_cell = bool(ctx.has_cell and ctx.needs_input_grad[1])
     grad_pos, grad_cell = force_reduce_op(grad.contiguous(), None, batch32, src, dst, shift,
-                                          ptr_dst, perm_dst, ptr_src, perm_src, node_ptr,
+                                          ptr_dst, perm_dst, ptr_src, perm_src, visit, node_ptr,
                                           ctx.n_nodes, ctx.geom_code, want_cell)
     return (grad_pos if ctx.needs_input_grad[0] else None, grad_cell if want_cell else None,
-            None, None, None, None, None, None, None, None, None, None)
+            None, None, None, None, None, None, None, None, None, None, None)
 
 
 edge_vectors_op.register_autograd(_edge_vectors_backward, setup_context=_edge_vectors_setup)
 
 
 def _force_reduce_setup(ctx, inputs, output):
-    (g_edge, cell_like, batch32, src, dst, shift, ptr_dst, perm_dst, ptr_src, perm_src, node_ptr,
-     n_nodes, geom_code, want_cell) = inputs
-    ctx.save_for_backward(batch32, src, dst, shift, ptr_dst, perm_dst, ptr_src, perm_src, node_ptr)
+    (g_edge, cell_like, batch32, src, dst, shift, ptr_dst, perm_dst, ptr_src, perm_src, visit,
+     node_ptr, n_nodes, geom_code, want_cell) = inputs
+    ctx.save_for_backward(batch32, src, dst, shift, ptr_dst, perm_dst, ptr_src, perm_src, visit,
+                          node_ptr)
     ctx.out_code = _lib.dtype_code(g_edge.dtype)
     ctx.want_cell = want_cell
 
 
 def _force_reduce_backward(ctx, d_pos, d_cell):
     # the adjoint of the reduction is the edge-vector map applied to the cotangents
-    batch32, src, dst, shift, ptr_dst, perm_dst, ptr_src, perm_src, node_ptr = ctx.saved_tensors
+    (batch32, src, dst, shift, ptr_dst, perm_dst, ptr_src, perm_src, visit,
+     node_ptr) = ctx.saved_tensors
     cell = d_cell.contiguous() if (ctx.want_cell and d_cell is not None) else None
     if d_pos is None:
         d_pos = torch.zeros((ptr_dst.shape[0] - 1, 3), dtype=cell.dtype if cell is not None
@@ -176,8 +182,8 @@ def _force_reduce_backward(ctx, d_pos, d_cell):
     if cell is not None:
         cell = cell.to(d_pos.dtype)
     g = edge_vectors_op(d_pos.contiguous(), cell, batch32, src, dst, shift, ptr_dst, perm_dst,
-                        ptr_src, perm_src, node_ptr, ctx.out_code)
-    return (g, None, None, None, None, None, None, None, None, None, None, None, None, None)
+                        ptr_src, perm_src, visit, node_ptr, ctx.out_code)
+    return (g, None, None, None, None, None, None, None, None, None, None, None, None, None, None)
 
 
 force_reduce_op.register_autograd(_force_reduce_backward, setup_context=_force_reduce_setup)
@@ -221,7 +227,8 @@ def stress_finish(strain_gradient: Tensor, cell: Tensor, pbc: Optional[Tensor],
 def edge_vectors_strain_probe_op(pos: Tensor, strain_probe: Tensor, cell: Optional[Tensor],
                                  batch32: Tensor, src: Tensor, dst: Tensor, shift: Tensor,
                                  ptr_dst: Tensor, perm_dst: Optional[Tensor], ptr_src: Tensor,
-                                 perm_src: Tensor, node_ptr: Tensor, out_dtype: int) -> Tensor:
+                                 perm_src: Tensor, visit: Optional[Tensor], node_ptr: Tensor,
+                                 out_dtype: int) -> Tensor:
     """Edge vectors of the configuration deformed by the strain ``strain_probe`` (B, 3, 3)
     about zero: ``r_e (I + sym(strain))`` with ``sym(s) = (s + s^T) / 2``, the deformation
     of ForceStressOutput (outputs.py:166-180; it moves positions and cell, hence every
@@ -230,21 +237,21 @@ def edge_vectors_strain_probe_op(pos: Tensor, strain_probe: Tensor, cell: Option
     the backward forms directly: ``dE/d strain = sym(sum_e r_e (x) dE/dr_e)`` per structure,
     float64 accumulation, from the force-reduction kernel. Differentiable once."""
     return edge_vectors_op(pos, cell, batch32, src, dst, shift, ptr_dst, perm_dst, ptr_src,
-                           perm_src, node_ptr, out_dtype)
+                           perm_src, visit, node_ptr, out_dtype)
 
 
 @edge_vectors_strain_probe_op.register_fake
 def _(pos, strain_probe, cell, batch32, src, dst, shift, ptr_dst, perm_dst, ptr_src, perm_src,
-      node_ptr, out_dtype):
+      visit, node_ptr, out_dtype):
     odt = torch.float32 if out_dtype == _lib.XNN_F32 else torch.float64
     return pos.new_empty((src.shape[0], 3), dtype=odt)
 
 
 def _probe_setup(ctx, inputs, output):
     (pos, strain_probe, cell, batch32, src, dst, shift, ptr_dst, perm_dst, ptr_src, perm_src,
-     node_ptr, out_dtype) = inputs
+     visit, node_ptr, out_dtype) = inputs
     ctx.save_for_backward(output, batch32, src, dst, shift, ptr_dst, perm_dst, ptr_src, perm_src,
-                          node_ptr)
+                          visit, node_ptr)
     ctx.n_nodes = pos.shape[0]
     ctx.geom_code = _lib.dtype_code(pos.dtype)
     ctx.has_cell = cell is not None and cell.numel() > 0
@@ -253,7 +260,8 @@ def _probe_setup(ctx, inputs, output):
 
 def _probe_backward(ctx, grad):
     _once_differentiable()
-    vec, batch32, src, dst, shift, ptr_dst, perm_dst, ptr_src, perm_src, node_ptr = ctx.saved_tensors
+    (vec, batch32, src, dst, shift, ptr_dst, perm_dst, ptr_src, perm_src, visit,
+     node_ptr) = ctx.saved_tensors
     grad = grad.contiguous()
     dev = grad.device
     n_nodes = ctx.n_nodes
@@ -261,11 +269,24 @@ def _probe_backward(ctx, grad):
     gdt = torch.float32 if ctx.geom_code == _lib.XNN_F32 else torch.float64
     want_cell = bool(ctx.has_cell and ctx.needs_input_grad[2])
     grad_pos = torch.empty((n_nodes, 3), dtype=gdt, device=dev)
+    if n_graphs == 1:
+        # one structure: forces, cell gradient and strain derivative in two launches
+        grad_probe = torch.empty((1, 3, 3), dtype=ctx.probe_dtype, device=dev)
+        grad_cell = torch.empty((1, 3, 3), dtype=gdt, device=dev) if want_cell else None
+        nbytes = int(_lib.load().xnn_edge_force_virial_workspace_bytes(grad.shape[0], n_nodes))
+        ws = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+        _lib.call("xnn_edge_force_virial", ctx.geom_code, _lib.dtype_code(grad.dtype),
+                  _lib.ptr(grad), grad.shape[0], _lib.ptr(ptr_dst), _lib.ptr(perm_dst),
+                  _lib.ptr(ptr_src), _lib.ptr(perm_src), _lib.ptr(shift), _lib.ptr(visit), n_nodes,
+                  _lib.ptr(vec), _lib.ptr(grad_pos), _lib.dtype_code(ctx.probe_dtype),
+                  _lib.ptr(grad_probe), _lib.ptr(grad_cell), _lib.ptr(ws), nbytes, _lib.stream(dev))
+        return (grad_pos if ctx.needs_input_grad[0] else None, grad_probe, grad_cell,
+                None, None, None, None, None, None, None, None, None, None, None)
     cell_partial = torch.empty((n_nodes, 9), dtype=torch.float64, device=dev) if want_cell else None
     virial_partial = torch.empty((n_nodes, 9), dtype=torch.float64, device=dev)
     _lib.call("xnn_edge_force_reduce", ctx.geom_code, _lib.dtype_code(grad.dtype), _lib.ptr(grad),
               grad.shape[0], _lib.ptr(ptr_dst), _lib.ptr(perm_dst), _lib.ptr(ptr_src),
-              _lib.ptr(perm_src), _lib.ptr(shift), n_nodes, _lib.ptr(grad_pos),
+              _lib.ptr(perm_src), _lib.ptr(shift), _lib.ptr(visit), n_nodes, _lib.ptr(grad_pos),
               _lib.ptr(cell_partial), _lib.ptr(vec), _lib.ptr(virial_partial), _lib.stream(dev))
     grad_probe = _lib.virial_reduce(virial_partial, n_nodes, node_ptr, n_graphs, None, True,
                                     ctx.probe_dtype)
@@ -273,7 +294,7 @@ def _probe_backward(ctx, grad):
     if want_cell:
         grad_cell = _lib.virial_reduce(cell_partial, n_nodes, node_ptr, n_graphs, None, False, gdt)
     return (grad_pos if ctx.needs_input_grad[0] else None, grad_probe, grad_cell,
-            None, None, None, None, None, None, None, None, None, None)
+            None, None, None, None, None, None, None, None, None, None, None)
 
 
 edge_vectors_strain_probe_op.register_autograd(_probe_backward, setup_context=_probe_setup)
@@ -294,11 +315,11 @@ def edge_vectors(pos: Tensor, cell: Optional[Tensor], plan: EdgePlan,
     if strain_probe is not None:
         return edge_vectors_strain_probe_op(
             pos.contiguous(), strain_probe, cell, plan.batch32, plan.src, plan.dst, plan.shift,
-            plan.ptr_dst, plan.perm_dst, plan.ptr_src, plan.perm_src, plan.node_ptr,
+            plan.ptr_dst, plan.perm_dst, plan.ptr_src, plan.perm_src, plan.visit, plan.node_ptr,
             _lib.dtype_code(out_dtype))
     return edge_vectors_op(pos.contiguous(), cell, plan.batch32, plan.src, plan.dst, plan.shift,
                            plan.ptr_dst, plan.perm_dst, plan.ptr_src, plan.perm_src,
-                           plan.node_ptr, _lib.dtype_code(out_dtype))
+                           plan.visit, plan.node_ptr, _lib.dtype_code(out_dtype))
 
 
 # --------------------------------------------------------------------------- strain deformation

@@ -40,6 +40,9 @@ class EdgePlan:
     perm_src: Tensor
     batch32: Tensor
     node_ptr: Tensor
+    # a space-filling-curve order of the atoms (structure by structure), the order in
+    # which the force reductions take them; None: index order
+    visit: Optional[Tensor] = None
 
     @property
     def device(self) -> torch.device:
@@ -112,6 +115,33 @@ def build_plan(edge_index: Tensor, cell_shifts: Optional[Tensor], n_nodes: int,
                     node_ptr=node_ptr)
 
 
+def _spread10(q: Tensor) -> Tensor:
+    """The 10 low bits of ``q`` (int64) spread to every third bit (Morton interleave)."""
+    q = (q | (q << 16)) & 0x030000FF
+    q = (q | (q << 8)) & 0x0300F00F
+    q = (q | (q << 4)) & 0x030C30C3
+    return (q | (q << 2)) & 0x09249249
+
+
+def spatial_order(pos: Tensor, cell: Optional[Tensor], batch: Tensor, n_graphs: int) -> Tensor:
+    """The atoms sorted along a Morton (Z-order) curve of their positions, structure by
+    structure, int32: fractional coordinates of the cell for one periodic structure, else
+    the batch's bounding box, 10 bits per axis. Neighbours in space end up near one another
+    in the order; an ordering hint only (nothing computed depends on it)."""
+    p = pos.detach().to(torch.float64)
+    if cell is not None and n_graphs == 1 and bool(torch.isfinite(p).all()):
+        c = cell.detach().reshape(-1, 3, 3)[0].to(torch.float64)
+        frac = p @ torch.linalg.inv(c)
+        frac = frac - torch.floor(frac)
+    else:
+        lo, hi = p.min(0).values, p.max(0).values
+        frac = (p - lo) / (hi - lo).clamp(min=1e-9)
+    q = (frac * 1024.0).to(torch.int64).clamp(0, 1023)
+    code = _spread10(q[:, 0]) | (_spread10(q[:, 1]) << 1) | (_spread10(q[:, 2]) << 2)
+    key = (batch.to(torch.int64) << 30) | code
+    return torch.argsort(key, stable=True).to(torch.int32)
+
+
 def plan_for(graph) -> EdgePlan:
     """The cached plan of an :class:`~xnn_amd.data.AtomicGraph` (rebuilt when its edge
     list, shifts or atom count change identity)."""
@@ -122,6 +152,8 @@ def plan_for(graph) -> EdgePlan:
         return cached[3]
     plan = build_plan(graph.edge_index, graph.cell_shifts, graph.num_nodes, graph.batch,
                       graph.n_atoms)
+    if plan.n_nodes > 0:
+        plan.visit = spatial_order(graph.pos, graph.cell, plan.batch32, plan.n_graphs)
     object.__setattr__(graph, "_xnn_plan",
                        (graph.edge_index, graph.cell_shifts, graph.num_nodes, plan))
     return plan
