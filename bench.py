@@ -97,9 +97,6 @@ def kernel_costs(E: int, N: int, C: int, L: int = 16, K: int = 8, grouped: bool 
         "xnn_edge_featurize": {"bytes": E * (12 + 4 * K + 4), "flops": 0},
         "xnn_edge_featurize_backward": {"bytes": E * (12 + 4 * K + 4 + 12 + 12), "flops": 0},
         "xnn_edge_force_reduce": {"bytes": E * (12 + 4) + N * (12 + 72 + 8), "flops": 0},
-        # one structure: g and r per edge (virial), the sender index, forces, both CSR
-        # pointers and the visit order per atom; the per-block partials are negligible
-        "xnn_edge_force_virial": {"bytes": E * (12 + 12 + 4) + N * (12 + 8 + 4), "flops": 0},
     }
 
 
@@ -111,7 +108,7 @@ def step_bytes(E: int, N: int, C: int, L: int, K: int, msg: str) -> int:
     kc = kernel_costs(E, N, C, L, K)
     if msg == "xnn_sh_radial_message_energy":
         return (E * 24 + N * 12 + kc[msg]["bytes"] + kc[msg + "_backward"]["bytes"]
-                + kc["xnn_edge_force_virial"]["bytes"])
+                + kc["xnn_edge_force_reduce"]["bytes"])
     feat = 0 if msg == "xnn_sh_radial_message_sum" else (
         kc["xnn_edge_featurize"]["bytes"] + kc["xnn_edge_featurize_backward"]["bytes"])
     linear = 2 * (E * 4 * (K + C)) if msg == "xnn_sh_message_sum" else 0  # u @ W, d_phi @ W^T
@@ -839,7 +836,7 @@ def main() -> None:
                if _lib.calls.get(m))
     fused = msg != "xnn_sh_message_sum"
     kernels = [msg, msg + "_backward", "xnn_edge_featurize", "xnn_edge_featurize_backward",
-               "xnn_edge_force_reduce", "xnn_edge_force_virial"]
+               "xnn_edge_force_reduce"]
     # eager pass: per-kernel HIP events on the launch stream
     _lib.timed.clear()
     _lib.time_launches(*kernels)

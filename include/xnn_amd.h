@@ -112,22 +112,6 @@ int xnn_edge_force_reduce(int geom_dtype, int compute_dtype, const void* g_edge,
                           void* grad_pos, double* cell_partial, const void* vec,
                           double* virial_partial, xnn_stream_t stream);
 
-/* One structure's forces, cell gradient and strain derivative in two launches: as
- * xnn_edge_force_reduce, with the cell and virial sums reduced per workgroup in the same
- * kernel and finished by one more (fixed orders throughout): grad_pos (N,3) geometry
- * dtype; cell_grad (3,3) geometry dtype = sum_e shift_e (x) g_e (nullable); virial (3,3)
- * in virial_dtype = sym(sum_e r_e (x) g_e) (ForceStressOutput's strain derivative,
- * outputs.py:166-216, for an energy of the edge vectors alone; atomic_data.py:452-467 for
- * the rest). workspace: xnn_edge_force_virial_workspace_bytes. */
-size_t xnn_edge_force_virial_workspace_bytes(int64_t n_edges, int64_t n_nodes);
-int xnn_edge_force_virial(int geom_dtype, int compute_dtype, const void* g_edge, int64_t n_edges,
-                          const int32_t* ptr_dst, const int32_t* perm_dst,
-                          const int32_t* ptr_src, const int32_t* perm_src,
-                          const int32_t* shift, const int32_t* visit, int64_t n_nodes,
-                          const void* vec, void* grad_pos, int virial_dtype, void* virial,
-                          void* cell_grad, void* workspace, size_t workspace_bytes,
-                          xnn_stream_t stream);
-
 /* The strain deformation of ForceStressOutput (outputs.py:166-180): with
  * S_b = (strain_b + strain_b^T) / 2 (strain (B,3,3), geometry dtype),
  * pos_out[i] = pos[i] (I + S_batch[i]) and cell_out[b] = cell[b] (I + S_b) (cell nullable).

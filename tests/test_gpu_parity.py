@@ -521,66 +521,37 @@ def test_sh_radial_message_energy_forward_backward(C, l_max, K, radial, envelope
     assert torch.isnan(E_bad).all()
 
 
-@pytest.mark.parametrize("dtype", [torch.float32, torch.float64])
-def test_force_virial_matches_the_per_atom_partials(dtype):
-    """xnn_edge_force_virial (forces, cell gradient and sym(sum_e r_e (x) g_e) of one
-    structure, per-workgroup partials and one finish) against xnn_edge_force_reduce's
-    per-atom partials summed on the CPU in float64; the forces are bit-identical with and
-    without the spatial visit order (each atom's sum keeps its order), and the fused
-    results are reproducible run to run."""
-    import ctypes
+def test_force_reduce_visit_order_keeps_every_sum():
+    """The force reduction taken in the plan's spatial order (space-filling curve, XCD-wise
+    runs) gives the forces and the per-atom cell and virial partials bit for bit as in
+    index order (each atom's sums keep their order); the visit order is a permutation."""
     import xnn_amd as xa
     from xnn_amd import _lib, synthetic
-    _note(f"force_virial {dtype}")
-    s = synthetic.water_box(n_molecules=216, box=18.6, grid=6, seed=3)
-    g = xa.structure_to_graph(s.as_dict(), 5.0, device=DEV)
-    g.pos, g.cell = g.pos.to(dtype), g.cell.to(dtype)
-    plan = g.plan()
-    assert plan.visit is not None and torch.equal(torch.sort(plan.visit.long()).values,
-                                                  torch.arange(g.num_nodes, device=DEV))
-    vec = g.edge_vectors().detach().contiguous()
-    gen = torch.Generator().manual_seed(5)
-    ge = torch.randn(vec.shape, generator=gen, dtype=torch.float64).to(DEV, dtype)
-    E, N = vec.shape[0], g.num_nodes
-    code = _lib.dtype_code(dtype)
-    s_ = _lib.stream(vec.device)
+    _note("force reduce visit order")
+    for dtype in (torch.float32, torch.float64):
+        s = synthetic.water_box(n_molecules=216, box=18.6, grid=6, seed=3)
+        g = xa.structure_to_graph(s.as_dict(), 5.0, device=DEV)
+        g.pos, g.cell = g.pos.to(dtype), g.cell.to(dtype)
+        plan = g.plan()
+        assert torch.equal(torch.sort(plan.visit.long()).values,
+                           torch.arange(g.num_nodes, device=DEV))
+        vec = g.edge_vectors().detach().contiguous()
+        ge = torch.randn(vec.shape, generator=torch.Generator().manual_seed(5),
+                         dtype=torch.float64).to(DEV, dtype)
+        E, N, code = vec.shape[0], g.num_nodes, _lib.dtype_code(dtype)
 
-    def per_atom(visit):
-        gp = torch.empty((N, 3), dtype=dtype, device=DEV)
-        cp = torch.empty((N, 9), dtype=torch.float64, device=DEV)
-        vp = torch.empty((N, 9), dtype=torch.float64, device=DEV)
-        _lib.call("xnn_edge_force_reduce", code, code, _lib.ptr(ge), E, _lib.ptr(plan.ptr_dst),
-                  _lib.ptr(plan.perm_dst), _lib.ptr(plan.ptr_src), _lib.ptr(plan.perm_src),
-                  _lib.ptr(plan.shift), _lib.ptr(visit), N, _lib.ptr(gp), _lib.ptr(cp),
-                  _lib.ptr(vec), _lib.ptr(vp), s_)
-        return gp, cp, vp
+        def run(visit):
+            gp = torch.empty((N, 3), dtype=dtype, device=DEV)
+            cp = torch.empty((N, 9), dtype=torch.float64, device=DEV)
+            vp = torch.empty((N, 9), dtype=torch.float64, device=DEV)
+            _lib.call("xnn_edge_force_reduce", code, code, _lib.ptr(ge), E, _lib.ptr(plan.ptr_dst),
+                      _lib.ptr(plan.perm_dst), _lib.ptr(plan.ptr_src), _lib.ptr(plan.perm_src),
+                      _lib.ptr(plan.shift), _lib.ptr(visit), N, _lib.ptr(gp), _lib.ptr(cp),
+                      _lib.ptr(vec), _lib.ptr(vp), _lib.stream(vec.device))
+            return gp, cp, vp
 
-    def fused():
-        gp = torch.empty((N, 3), dtype=dtype, device=DEV)
-        vir = torch.empty((3, 3), dtype=dtype, device=DEV)
-        cg = torch.empty((3, 3), dtype=dtype, device=DEV)
-        nb = int(_lib.load().xnn_edge_force_virial_workspace_bytes(E, N))
-        ws = torch.empty(nb, dtype=torch.uint8, device=DEV)
-        _lib.call("xnn_edge_force_virial", code, code, _lib.ptr(ge), E, _lib.ptr(plan.ptr_dst),
-                  _lib.ptr(plan.perm_dst), _lib.ptr(plan.ptr_src), _lib.ptr(plan.perm_src),
-                  _lib.ptr(plan.shift), _lib.ptr(plan.visit), N, _lib.ptr(vec), _lib.ptr(gp), code,
-                  _lib.ptr(vir), _lib.ptr(cg), _lib.ptr(ws), nb, s_)
-        return gp, vir, cg
-
-    gp0, cp, vp = per_atom(None)
-    gp1, _, _ = per_atom(plan.visit)
-    assert torch.equal(gp0, gp1)
-    gp2, vir, cg = fused()
-    assert torch.equal(gp0, gp2)
-    M = vp.cpu().sum(0).reshape(3, 3)
-    want_vir = 0.5 * (M + M.t())
-    want_cg = cp.cpu().sum(0).reshape(3, 3)
-    tol = 1e-5 if dtype == torch.float32 else 1e-12
-    np.testing.assert_allclose(vir.cpu().double(), want_vir, rtol=tol, atol=tol * float(M.abs().max()))
-    np.testing.assert_allclose(cg.cpu().double(), want_cg, rtol=tol,
-                               atol=tol * float(want_cg.abs().max()))
-    gp3, vir3, cg3 = fused()
-    assert torch.equal(gp2, gp3) and torch.equal(vir, vir3) and torch.equal(cg, cg3)
+        for a, b in zip(run(None), run(plan.visit)):
+            assert torch.equal(a, b)
 
 
 def test_segment_gather_and_structure_sums():
@@ -844,12 +815,7 @@ def test_model_energy_forces_stress(config, fused):
     out = xa.ForceStressOutput(model, compute_stress=g.cell is not None).eval()(g)
     msg = {"radial": "xnn_sh_radial_message_energy", "radial_rows": "xnn_sh_radial_message_sum",
            "linear": "xnn_sh_linear_message_sum", "unfused": "xnn_sh_message_sum"}[fused]
-    ran = [msg, msg + "_backward", "xnn_edge_featurize"]
-    # one structure: forces and the strain derivative in the fused launch pair; a batch:
-    # the per-atom partials and the segmented sums
-    force = "xnn_edge_force_virial" if (g.num_graphs == 1 and g.cell is not None) \
-        else "xnn_edge_force_reduce"
-    ran.append(force)
+    ran = [msg, msg + "_backward", "xnn_edge_force_reduce", "xnn_edge_featurize"]
     if fused not in ("radial", "radial_rows"):
         ran.append("xnn_edge_featurize_backward")
     for name in ran:

@@ -157,33 +157,24 @@ __global__ __launch_bounds__(256) void featurize_bwd_kernel(
 // (b % 8) * per_xcd + b / 8 and each XCD walks one contiguous run of the visit order. The
 // sender-side gather of an atom reads the gradient rows of its neighbours; with spatially
 // compact runs those rows are shared by the XCD's other atoms and stay in its L2.
-//
-// PB (per block): the cell and virial partials of the block's atoms are summed in a fixed
-// order into one row of 18 doubles per block (9 cell, 9 virial) instead of per-atom rows
-// (one structure), for xnn_edge_force_virial's finish.
 constexpr int kXcds = 8;
 
-__global__ void zero_f64_kernel(double* p, int64_t n) {
-  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (t < n) p[t] = 0.0;
-}
-
-template <typename G, typename T, int GROUP, bool PB>
+template <typename G, typename T, int GROUP>
 __global__ __launch_bounds__(256) void force_reduce_kernel(
     const T* __restrict__ g_edge, const int32_t* __restrict__ ptr_dst,
     const int32_t* __restrict__ perm_dst, const int32_t* __restrict__ ptr_src,
     const int32_t* __restrict__ perm_src, const int32_t* __restrict__ shift,
     const int32_t* __restrict__ visit, int64_t n_nodes, G* __restrict__ grad_pos,
     double* __restrict__ cell_partial, const T* __restrict__ vec,
-    double* __restrict__ virial_partial, double* __restrict__ block_partial) {
+    double* __restrict__ virial_partial) {
   const int lane = threadIdx.x % GROUP;
   const int64_t per_xcd = ((int64_t)gridDim.x + kXcds - 1) / kXcds;
   const int64_t sb = (int64_t)(blockIdx.x % kXcds) * per_xcd + blockIdx.x / kXcds;
   const int64_t slot = (sb * blockDim.x + threadIdx.x) / GROUP;
   const bool live = slot < n_nodes;
   const int64_t i = live ? (visit ? (int64_t)visit[slot] : slot) : 0;
-  const bool want_cell = PB || cell_partial != nullptr;
-  const bool want_vir = PB ? vec != nullptr : virial_partial != nullptr;
+  const bool want_cell = cell_partial != nullptr;
+  const bool want_vir = virial_partial != nullptr;
   double fx = 0, fy = 0, fz = 0;
   double c[9] = {0, 0, 0, 0, 0, 0, 0, 0, 0};
   double v[9] = {0, 0, 0, 0, 0, 0, 0, 0, 0};
@@ -196,7 +187,7 @@ __global__ __launch_bounds__(256) void force_reduce_kernel(
       fx += x;
       fy += y;
       fz += z;
-      if (want_cell && shift != nullptr) {
+      if (want_cell) {
         int sx, sy, sz;
         unpack_shift(shift[e], sx, sy, sz);
         c[0] += sx * x; c[1] += sx * y; c[2] += sx * z;
@@ -237,60 +228,13 @@ __global__ __launch_bounds__(256) void force_reduce_kernel(
     grad_pos[3 * i + 0] = (G)fx;
     grad_pos[3 * i + 1] = (G)fy;
     grad_pos[3 * i + 2] = (G)fz;
-    if constexpr (!PB) {
-      if (cell_partial) {
+    if (cell_partial) {
 #pragma unroll
-        for (int q = 0; q < 9; ++q) cell_partial[9 * i + q] = c[q];
-      }
-      if (virial_partial) {
-#pragma unroll
-        for (int q = 0; q < 9; ++q) virial_partial[9 * i + q] = v[q];
-      }
+      for (int q = 0; q < 9; ++q) cell_partial[9 * i + q] = c[q];
     }
-  }
-  if constexpr (PB) {
-    // the block's atoms (groups) summed in group order: one row of 18 per block
-    constexpr int NG = 256 / GROUP;
-    __shared__ double rows[NG][18];
-    const int grp = threadIdx.x / GROUP;
-    if (lane == 0) {
+    if (virial_partial) {
 #pragma unroll
-      for (int q = 0; q < 9; ++q) {
-        rows[grp][q] = live ? c[q] : 0.0;
-        rows[grp][9 + q] = live ? v[q] : 0.0;
-      }
-    }
-    __syncthreads();
-    if (threadIdx.x < 18) {
-      double t = 0.0;
-      for (int g2 = 0; g2 < NG; ++g2) t += rows[g2][threadIdx.x];
-      block_partial[sb * 18 + threadIdx.x] = t;
-    }
-  }
-}
-
-// The finish of xnn_edge_force_virial: the per-block rows summed in block order (a fixed
-// order), then the cell gradient (cast to G) and sym(virial) (cast to V).
-template <typename G, typename V>
-__global__ __launch_bounds__(256) void force_virial_finish_kernel(
-    const double* __restrict__ block_partial, int64_t n_blocks, G* __restrict__ cell_grad,
-    V* __restrict__ virial) {
-  __shared__ double tot[18];
-  const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
-  for (int f = wave; f < 18; f += blockDim.x / kWave) {
-    double t = 0.0;
-    for (int64_t k = lane; k < n_blocks; k += kWave) t += block_partial[k * 18 + f];
-#pragma unroll
-    for (int m = kWave / 2; m > 0; m >>= 1) t += __shfl_xor(t, m, kWave);
-    if (lane == 0) tot[f] = t;
-  }
-  __syncthreads();
-  const int j = threadIdx.x;
-  if (j < 9) {
-    if (cell_grad != nullptr) cell_grad[j] = (G)tot[j];
-    if (virial != nullptr) {
-      const int r = j / 3, cc = j % 3;
-      virial[j] = (V)(0.5 * (tot[9 + j] + tot[9 + 3 * cc + r]));
+      for (int q = 0; q < 9; ++q) virial_partial[9 * i + q] = v[q];
     }
   }
 }
@@ -490,43 +434,16 @@ static int64_t force_blocks(int64_t n_edges, int64_t n_nodes) {
   return ((b + kXcds - 1) / kXcds) * kXcds;
 }
 
-template <typename G, typename T, int GROUP, bool PB>
+template <typename G, typename T, int GROUP>
 static void launch_force_reduce(int64_t n_blocks, const void* g_edge, const int32_t* ptr_dst,
                                 const int32_t* perm_dst, const int32_t* ptr_src,
                                 const int32_t* perm_src, const int32_t* shift,
                                 const int32_t* visit, int64_t n_nodes, void* grad_pos,
                                 double* cell_partial, const void* vec, double* virial_partial,
-                                double* block_partial, hipStream_t stream) {
-  hipLaunchKernelGGL((force_reduce_kernel<G, T, GROUP, PB>), dim3((unsigned)n_blocks), dim3(256),
-                     0, stream, (const T*)g_edge, ptr_dst, perm_dst, ptr_src, perm_src, shift,
-                     visit, n_nodes, (G*)grad_pos, cell_partial, (const T*)vec, virial_partial,
-                     block_partial);
-}
-
-template <typename G, typename T, bool PB>
-static void force_reduce_any(int64_t n_edges, const void* g_edge, const int32_t* ptr_dst,
-                             const int32_t* perm_dst, const int32_t* ptr_src,
-                             const int32_t* perm_src, const int32_t* shift, const int32_t* visit,
-                             int64_t n_nodes, void* grad_pos, double* cell_partial,
-                             const void* vec, double* virial_partial, double* block_partial,
-                             hipStream_t stream) {
-  const int64_t nb = force_blocks(n_edges, n_nodes);
-  switch (force_group(n_edges, n_nodes)) {
-    case 32:
-      launch_force_reduce<G, T, 32, PB>(nb, g_edge, ptr_dst, perm_dst, ptr_src, perm_src, shift,
-                                        visit, n_nodes, grad_pos, cell_partial, vec,
-                                        virial_partial, block_partial, stream);
-      break;
-    case 16:
-      launch_force_reduce<G, T, 16, PB>(nb, g_edge, ptr_dst, perm_dst, ptr_src, perm_src, shift,
-                                        visit, n_nodes, grad_pos, cell_partial, vec,
-                                        virial_partial, block_partial, stream);
-      break;
-    default:
-      launch_force_reduce<G, T, 4, PB>(nb, g_edge, ptr_dst, perm_dst, ptr_src, perm_src, shift,
-                                       visit, n_nodes, grad_pos, cell_partial, vec,
-                                       virial_partial, block_partial, stream);
-  }
+                                hipStream_t stream) {
+  hipLaunchKernelGGL((force_reduce_kernel<G, T, GROUP>), dim3((unsigned)n_blocks), dim3(256), 0,
+                     stream, (const T*)g_edge, ptr_dst, perm_dst, ptr_src, perm_src, shift, visit,
+                     n_nodes, (G*)grad_pos, cell_partial, (const T*)vec, virial_partial);
 }
 
 template <typename G, typename T>
@@ -536,35 +453,20 @@ static int force_reduce(const void* g_edge, int64_t n_edges, const int32_t* ptr_
                         int64_t n_nodes, void* grad_pos, double* cell_partial, const void* vec,
                         double* virial_partial, hipStream_t stream) {
   if (n_nodes == 0) return XNN_OK;
-  force_reduce_any<G, T, false>(n_edges, g_edge, ptr_dst, perm_dst, ptr_src, perm_src, shift,
-                                visit, n_nodes, grad_pos, cell_partial, vec, virial_partial,
-                                nullptr, stream);
-  XNN_LAUNCH_CHECK();
-  return XNN_OK;
-}
-
-template <typename G, typename T>
-static int force_virial(const void* g_edge, int64_t n_edges, const int32_t* ptr_dst,
-                        const int32_t* perm_dst, const int32_t* ptr_src,
-                        const int32_t* perm_src, const int32_t* shift, const int32_t* visit,
-                        int64_t n_nodes, const void* vec, void* grad_pos, int virial_dtype,
-                        void* virial, void* cell_grad, double* ws, hipStream_t stream) {
-  const int64_t nb = n_nodes == 0 ? 1 : force_blocks(n_edges, n_nodes);
-  if (n_nodes == 0) {
-    hipLaunchKernelGGL(zero_f64_kernel, dim3(1), dim3(64), 0, stream, ws, (int64_t)18);
-  } else {
-    // without a cell gradient the shifts are not read (the kernel skips the cell sums)
-    force_reduce_any<G, T, true>(n_edges, g_edge, ptr_dst, perm_dst, ptr_src, perm_src,
-                                 cell_grad ? shift : nullptr, visit, n_nodes, grad_pos, nullptr,
-                                 vec, nullptr, ws, stream);
+  const int64_t nb = force_blocks(n_edges, n_nodes);
+  switch (force_group(n_edges, n_nodes)) {
+    case 32:
+      launch_force_reduce<G, T, 32>(nb, g_edge, ptr_dst, perm_dst, ptr_src, perm_src, shift, visit,
+                                    n_nodes, grad_pos, cell_partial, vec, virial_partial, stream);
+      break;
+    case 16:
+      launch_force_reduce<G, T, 16>(nb, g_edge, ptr_dst, perm_dst, ptr_src, perm_src, shift, visit,
+                                    n_nodes, grad_pos, cell_partial, vec, virial_partial, stream);
+      break;
+    default:
+      launch_force_reduce<G, T, 4>(nb, g_edge, ptr_dst, perm_dst, ptr_src, perm_src, shift, visit,
+                                   n_nodes, grad_pos, cell_partial, vec, virial_partial, stream);
   }
-  XNN_LAUNCH_CHECK();
-  if (virial_dtype == XNN_F64)
-    hipLaunchKernelGGL((force_virial_finish_kernel<G, double>), dim3(1), dim3(256), 0, stream, ws,
-                       nb, (G*)cell_grad, (double*)virial);
-  else
-    hipLaunchKernelGGL((force_virial_finish_kernel<G, float>), dim3(1), dim3(256), 0, stream, ws,
-                       nb, (G*)cell_grad, (float*)virial);
   XNN_LAUNCH_CHECK();
   return XNN_OK;
 }
@@ -636,32 +538,6 @@ int xnn_edge_force_reduce(int geom_dtype, int compute_dtype, const void* g_edge,
   XNN_DISPATCH_GT(geom_dtype, compute_dtype, force_reduce, g_edge, n_edges, ptr_dst, perm_dst,
                   ptr_src, perm_src, shift, visit, n_nodes, grad_pos, cell_partial, vec,
                   virial_partial, as_hip(stream));
-}
-
-size_t xnn_edge_force_virial_workspace_bytes(int64_t n_edges, int64_t n_nodes) {
-  const int64_t nb = n_nodes <= 0 ? 1 : force_blocks(n_edges, n_nodes);
-  return sizeof(double) * 18 * (size_t)nb;
-}
-
-int xnn_edge_force_virial(int geom_dtype, int compute_dtype, const void* g_edge, int64_t n_edges,
-                          const int32_t* ptr_dst, const int32_t* perm_dst,
-                          const int32_t* ptr_src, const int32_t* perm_src,
-                          const int32_t* shift, const int32_t* visit, int64_t n_nodes,
-                          const void* vec, void* grad_pos, int virial_dtype, void* virial,
-                          void* cell_grad, void* workspace, size_t workspace_bytes,
-                          xnn_stream_t stream) {
-  XNN_REQUIRE(n_edges >= 0 && n_nodes >= 0, "negative size");
-  XNN_REQUIRE(n_nodes == 0 || (ptr_dst && ptr_src && grad_pos), "NULL CSR or output");
-  XNN_REQUIRE(n_edges == 0 || (g_edge && vec), "NULL g_edge or edge vectors");
-  XNN_REQUIRE(cell_grad == nullptr || shift != nullptr, "cell_grad needs the shifts");
-  XNN_REQUIRE(virial_dtype == XNN_F32 || virial_dtype == XNN_F64, "bad virial dtype %d",
-              virial_dtype);
-  const size_t need = xnn_edge_force_virial_workspace_bytes(n_edges, n_nodes);
-  XNN_REQUIRE(workspace != nullptr && workspace_bytes >= need, "workspace of %zu bytes needed",
-              need);
-  XNN_DISPATCH_GT(geom_dtype, compute_dtype, force_virial, g_edge, n_edges, ptr_dst, perm_dst,
-                  ptr_src, perm_src, shift, visit, n_nodes, vec, grad_pos, virial_dtype, virial,
-                  cell_grad, static_cast<double*>(workspace), as_hip(stream));
 }
 
 int xnn_strain_apply(int geom_dtype, const void* pos, int64_t n_nodes, const int32_t* batch,
