@@ -378,6 +378,25 @@ int xnn_d4_two_body_backward(const double* pos, int64_t n_nodes, const int32_t* 
                              double* cell_partial, double* grad_alpha, void* workspace,
                              size_t workspace_bytes, xnn_stream_t stream);
 
+/* ------------------------------------------------------------------------ */
+/* Large-system EEQ operator, real-space part (float64, bohr). Replaces the neighbor-list
+ * kernel of EEQSystem (common/models/eeq.py:170-397, the operator of eeq_charges_large,
+ * eeq.py:664; dispersion_fast/eeq.py:69 keeps it as a sparse CSR matrix):
+ * matrix (N,N) = sum over lattice images n with 0 < |d| <= cutoff of
+ * [erf(gamma_ij |d|) - erf(alpha |d|)] / |d|, d = pos_j + n cell - pos_i,
+ * gamma_ij = (rad_i^2 + rad_j^2)^(-1/2). cell (3,3) rows or NULL (a molecule: one image,
+ * alpha must be 0). Written, row-major, symmetric. */
+int xnn_eeq_real_matrix(const double* pos, int64_t n_nodes, const double* cell,
+                        const double* rad, double alpha, double cutoff, double* matrix,
+                        xnn_stream_t stream);
+
+/* Derivatives of S = sum_ij u_i matrix_ij w_j with respect to the positions, grad_pos
+ * (N,3), and the cell, as per-atom rows cell_partial (N,3,3) to be summed (nullable;
+ * NULL for a molecule). Deterministic. */
+int xnn_eeq_real_grad(const double* pos, int64_t n_nodes, const double* cell, const double* rad,
+                      double alpha, double cutoff, const double* u, const double* w,
+                      double* grad_pos, double* cell_partial, xnn_stream_t stream);
+
 /* D4 reference tables in the kernels' layout, indexed by atomic number (rows 0 ..
  * n_elements-1), device memory: nref (n_el) int32, ngw / refcn / refq (n_el, 7) with
  * ngw int32, zeff (n_el), gi = hardness x gc (n_el), refalpha (n_el, 7, 23) the

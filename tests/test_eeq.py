@@ -9,7 +9,13 @@ the physics fixes, on the CPU (float64):
   convergence of the fixed +-2 windows at the search's splitting parameter (matrix
   elements to sqrt(eps) relative, d4.py:183-224);
 * the charges sum to the structure's total charge.
+
+The large regime's checker (``oracle/eeq.py``, the converged Ewald operator of
+eeq.py:170-397 by brute force) is pinned the same way, more tightly (its sums converge to
+1e-10): the rock-salt Madelung constant for point charges at three splits, split and
+supercell invariance to 1e-9, the vacuum limit, and agreement with the dense regime.
 """
+import math
 import os
 
 import numpy as np
@@ -80,3 +86,68 @@ def test_charges_sum_to_the_total_charge(d4, total):
     z = [6, 1, 1, 8, 7, 1, 6, 1, 8]
     q = _charges(d4, pos, cell, z, total)
     assert abs(q.sum() - total) < 1e-12
+
+
+# --------------------------------------------------------------------------- large regime
+def _eeq_params(z):
+    t = _tables()
+    zz = np.asarray(z)
+    rad = t["eeq_rad"][zz]
+    diag = t["eeq_eta"][zz] + math.sqrt(2.0 / math.pi) / rad
+    return rad, diag, t
+
+
+def _large_charges(pos_aa, cell_aa, z, cutoff_au, total=0.0):
+    import oracle.eeq as Q
+    rad, diag, t = _eeq_params(z)
+    cn = _cn_eeq(pos_aa, cell_aa, z).numpy()
+    zz = np.asarray(z)
+    x = -t["eeq_chi"][zz] + t["eeq_kcnchi"][zz] * cn / np.sqrt(cn + 1e-14)
+    return Q.charges(np.asarray(pos_aa) / D.BOHR, None if cell_aa is None else np.asarray(cell_aa) / D.BOHR,
+                     rad, diag, x, total, cutoff_au)
+
+
+def test_oracle_ewald_gives_the_nacl_madelung_constant():
+    """Point charges (widths -> 0, so erf(gamma r) = 1) on the rock-salt lattice: the Ewald
+    energy 1/2 q^T A q of the conventional cell is -4 M / d with M = 1.747564594633182 (d the
+    nearest-neighbour distance), whatever the real-space cutoff (the split)."""
+    import oracle.eeq as Q
+    a0 = 10.0
+    base = np.array([[0, 0, 0], [0, .5, .5], [.5, 0, .5], [.5, .5, 0]])
+    pos = np.concatenate([base, base + [0.5, 0, 0]]) * a0
+    q = np.array([1.0] * 4 + [-1.0] * 4)
+    rad = np.full(8, 1e-9)
+    for cutoff in (12.0, 17.0, 25.0):
+        A = Q.ewald_matrix(pos, np.eye(3) * a0, rad, cutoff)
+        e = 0.5 * q @ A @ q
+        assert abs(e - (-4 * 1.747564594633182 / (a0 / 2))) < 1e-9, (cutoff, e)
+
+
+def test_oracle_large_regime_invariances():
+    """The converged Ewald charges: unchanged by the split (two real-space cutoffs), by
+    replicating the cell, neutral, and in a vacuum cell tending to dftd4's molecular
+    charges (the L^-3 image-dipole remainder extrapolated away)."""
+    rng = np.random.default_rng(3)
+    cell = np.array([[9.0, 0, 0], [1.2, 8.5, 0], [-0.7, 0.9, 10.0]])
+    pos = rng.uniform(0, 1, (11, 3)) @ cell
+    z = [8, 1, 1, 6, 1, 7, 8, 1, 6, 6, 1]
+    q20 = _large_charges(pos, cell, z, 20.0)
+    q30 = _large_charges(pos, cell, z, 30.0)
+    np.testing.assert_allclose(q20, q30, atol=1e-9)
+    assert abs(q20.sum()) < 1e-12
+    big = np.concatenate([pos, pos + cell[0]])
+    q2 = _large_charges(big, cell * np.array([[2], [1], [1]]), z * 2, 20.0)
+    np.testing.assert_allclose(q2, np.tile(q20, 2), atol=1e-9)
+    qs = {L: _large_charges(WATER + L / 2, np.eye(3) * L, [8, 1, 1], 25.0) for L in (60.0, 120.0)}
+    np.testing.assert_allclose((8 * qs[120.0] - qs[60.0]) / 7, GOLDEN_Q, atol=1e-8)
+
+
+def test_dense_and_large_regimes_agree(d4):
+    """The dense regime (dftd4's fixed +-2 windows) and the converged Ewald operator give
+    the same charges to the dense windows' convergence (matrix elements to sqrt(eps))."""
+    rng = np.random.default_rng(3)
+    cell = np.array([[9.0, 0, 0], [1.2, 8.5, 0], [-0.7, 0.9, 10.0]])
+    pos = rng.uniform(0, 1, (11, 3)) @ cell
+    z = [8, 1, 1, 6, 1, 7, 8, 1, 6, 6, 1]
+    np.testing.assert_allclose(_charges(d4, pos, cell, z), _large_charges(pos, cell, z, 25.0),
+                               atol=1e-6)

@@ -1,0 +1,188 @@
+"""GPU parity of the large-regime EEQ charges (xnn_amd.eeq: the HIP real-space matrix and
+its derivative kernel, the reciprocal sum and the device factorization) against the
+oracle's brute-force converged Ewald operator (oracle/eeq.py, eeq.py:170-397, 664), the
+rock-salt Madelung constant, finite differences of the D4 energy through the charges,
+and, at the C5 size (5,000 atoms), the split and dense-regime invariances."""
+import math
+import os
+import sys
+
+import numpy as np
+import pytest
+import torch
+
+import oracle.d4 as D
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+HERE = os.path.dirname(os.path.abspath(__file__))
+
+
+def _note(msg):
+    print(f"[gpu-case] {msg}", flush=True)
+    sys.stdout.flush()
+
+
+@pytest.fixture(scope="module")
+def tables():
+    return dict(np.load(os.path.join(HERE, "golden", "d4_tables_hcnoar.npz"), allow_pickle=False))
+
+
+def _cell_case(seed=3, n=11):
+    rng = np.random.default_rng(seed)
+    cell = np.array([[9.0, 0, 0], [1.2, 8.5, 0], [-0.7, 0.9, 10.0]])
+    pos = rng.uniform(0, 1, (n, 3)) @ cell
+    z = ([8, 1, 1, 6, 1, 7, 8, 1, 6, 6, 1] * (n // 11 + 1))[:n]
+    return pos, cell, z
+
+
+def test_operator_matches_the_oracle_and_the_madelung_constant(tables):
+    """R + A_rec - 2 alpha / sqrt(pi) (the assembled operator without J + sqrt(2/pi)/a) on a
+    triclinic cell against the brute-force oracle to 1e-12, and a molecule's erf(gamma r)/r
+    matrix; point charges on rock salt give the Madelung energy."""
+    import oracle.eeq as Q
+    from xnn_amd import eeq as E
+    _note("eeq operator vs oracle")
+    pos, cell, z = _cell_case()
+    rad = tables["eeq_rad"][np.asarray(z)]
+    for cutoff in (20.0, 27.0):
+        alpha = E.ewald_alpha(cutoff)
+        p = torch.tensor(pos / D.BOHR, device=DEV)
+        c = torch.tensor(cell / D.BOHR, device=DEV)
+        zeros = torch.zeros(len(z), dtype=torch.float64, device=DEV)
+        sysm = E.LargeEEQSystem(p, c, torch.tensor(rad, device=DEV),
+                                zeros - 2 * alpha / math.sqrt(math.pi), alpha, cutoff)
+        want = Q.ewald_matrix(pos / D.BOHR, cell / D.BOHR, rad, cutoff)
+        np.testing.assert_allclose(sysm.A.cpu().numpy(), want, atol=1e-12 * np.abs(want).max())
+    mol = pos[:7] + 3.0
+    sysm = E.LargeEEQSystem(torch.tensor(mol / D.BOHR, device=DEV), None,
+                            torch.tensor(rad[:7], device=DEV),
+                            torch.zeros(7, dtype=torch.float64, device=DEV), 0.0, math.inf)
+    want = Q.ewald_matrix(mol / D.BOHR, None, rad[:7], 1e9)
+    np.testing.assert_allclose(sysm.A.cpu().numpy(), want, atol=1e-13)
+    a0 = 10.0
+    base = np.array([[0, 0, 0], [0, .5, .5], [.5, 0, .5], [.5, .5, 0]])
+    salt = np.concatenate([base, base + [0.5, 0, 0]]) * a0
+    q = torch.tensor([1.0] * 4 + [-1.0] * 4, dtype=torch.float64, device=DEV)
+    alpha = E.ewald_alpha(17.0)
+    sysm = E.LargeEEQSystem(torch.tensor(salt, device=DEV), torch.eye(3, dtype=torch.float64,
+                                                                       device=DEV) * a0,
+                            torch.full((8,), 1e-9, dtype=torch.float64, device=DEV),
+                            torch.full((8,), -2 * alpha / math.sqrt(math.pi), dtype=torch.float64,
+                                       device=DEV), alpha, 17.0)
+    e = 0.5 * float(q @ sysm.A @ q)
+    assert abs(e - (-4 * 1.747564594633182 / (a0 / 2))) < 1e-9
+
+
+def _d4_large(tables, **kw):
+    import xnn_amd.dispersion as XD
+    return XD.DFTD4(tables, regime="large", s9=0.0, cutoff_pair=9.0, cutoff_cn=8.0,
+                    cutoff_eeq_cn=8.0, cutoff_eeq=kw.pop("cutoff_eeq", 11.0), **kw).to(DEV)
+
+
+def _eval(model, pos, z, cell, grad=False):
+    p = torch.tensor(pos, dtype=torch.float64, device=DEV, requires_grad=grad)
+    c = None if cell is None else torch.tensor(cell, dtype=torch.float64, device=DEV)[None] \
+        .requires_grad_(grad)
+    out = model.evaluate(torch.tensor(z, device=DEV), p, c,
+                         None if c is None else torch.ones((1, 3), dtype=torch.bool),
+                         torch.tensor([len(z)]))
+    return out, p, c
+
+
+def test_charges_match_the_oracle_and_finite_differences(tables):
+    """The charges of the large regime (regime="large", 11 A real-space range) against the
+    oracle's brute-force Ewald solve with the oracle's CN, 1e-10; the D4 energy through the
+    charges: forces against central differences and the strain derivative against a finite
+    strain (1e-7); a molecule too; run to run bit for bit."""
+    import oracle.eeq as Q
+    _note("eeq large regime charges and derivatives")
+    pos, cell, z = _cell_case()
+    model = _d4_large(tables)
+    out, p, c = _eval(model, pos, z, cell, grad=True)
+    q = out["charges"].detach().cpu().numpy()
+    zz = np.asarray(z)
+    dst, src, sh = D.pair_images(pos, cell, 8.0)
+    v = D.edge_vectors_au(torch.tensor(pos), torch.tensor(cell), dst, src, sh)
+    _, cn_eeq, _ = D.coordination_numbers(torch.as_tensor(zz), dst, src, torch.linalg.norm(v, dim=-1),
+                                          tables, 8.0 / D.BOHR, 8.0 / D.BOHR, len(z))
+    cn = cn_eeq.numpy()
+    rad = tables["eeq_rad"][zz]
+    x = -tables["eeq_chi"][zz] + tables["eeq_kcnchi"][zz] * cn / np.sqrt(cn + 1e-14)
+    diag = tables["eeq_eta"][zz] + math.sqrt(2 / math.pi) / rad
+    want = Q.charges(pos / D.BOHR, cell / D.BOHR, rad, diag, x, 0.0, 11.0 / D.BOHR)
+    np.testing.assert_allclose(q, want, atol=1e-10)
+    gp, gc = torch.autograd.grad(out["energy"].sum(), [p, c])
+    h = 1e-4
+    for i, a in [(0, 0), (4, 1), (9, 2)]:
+        pp, pm = pos.copy(), pos.copy()
+        pp[i, a] += h
+        pm[i, a] -= h
+        ep = float(_eval(model, pp, z, cell)[0]["energy"][0])
+        em = float(_eval(model, pm, z, cell)[0]["energy"][0])
+        assert abs(float(gp[i, a]) - (ep - em) / (2 * h)) < 1e-7, (i, a)
+    D_ab = (p.detach().t() @ gp + c.detach()[0].t() @ gc[0]).cpu()
+    for a, b in [(0, 0), (0, 2)]:
+        eps = np.zeros((3, 3))
+        eps[a, b] = eps[b, a] = h
+        ep = float(_eval(model, pos @ (np.eye(3) + eps), z, cell @ (np.eye(3) + eps))[0]["energy"][0])
+        em = float(_eval(model, pos @ (np.eye(3) - eps), z, cell @ (np.eye(3) - eps))[0]["energy"][0])
+        wantd = float(D_ab[a, b]) if a == b else float(D_ab[a, b] + D_ab[b, a])
+        assert abs((ep - em) / (2 * h) - wantd) < 1e-6, (a, b)
+    again = _eval(model, pos, z, cell)[0]["charges"]
+    assert torch.equal(again, out["charges"].detach())
+    # a molecule in the large regime: every pair, no split
+    mol, zm = pos[:9] + 2.0, z[:9]
+    outm, pm_, _ = _eval(model, mol, zm, None, grad=True)
+    dst, src, sh = D.pair_images(mol, None, 8.0)
+    v = D.edge_vectors_au(torch.tensor(mol), None, dst, src, sh)
+    zz = np.asarray(zm)
+    _, cn_eeq, _ = D.coordination_numbers(torch.as_tensor(zz), dst, src, torch.linalg.norm(v, dim=-1),
+                                          tables, 8.0 / D.BOHR, 8.0 / D.BOHR, len(zm))
+    cn = cn_eeq.numpy()
+    rad = tables["eeq_rad"][zz]
+    x = -tables["eeq_chi"][zz] + tables["eeq_kcnchi"][zz] * cn / np.sqrt(cn + 1e-14)
+    diag = tables["eeq_eta"][zz] + math.sqrt(2 / math.pi) / rad
+    want = Q.charges(mol / D.BOHR, None, rad, diag, x, 0.0, 1e9)
+    np.testing.assert_allclose(outm["charges"].detach().cpu().numpy(), want, atol=1e-11)
+    (gpm,) = torch.autograd.grad(outm["energy"].sum(), [pm_])
+    pp, pm2 = mol.copy(), mol.copy()
+    pp[2, 1] += h
+    pm2[2, 1] -= h
+    fd = (float(_eval(model, pp, zm, None)[0]["energy"][0])
+          - float(_eval(model, pm2, zm, None)[0]["energy"][0])) / (2 * h)
+    assert abs(float(gpm[2, 1]) - fd) < 1e-7
+
+
+def test_c5_charges_large_regime(tables):
+    """The C5 box (5,000 atoms, 36.8 A cell) in the large regime (the reference's default
+    there, regime="auto" above 500 periodic atoms): neutral, independent of the Ewald split
+    (real-space ranges of 31.75 and 21.2 A) to 1e-8, equal to the dense regime's charges to
+    its +-2 windows' convergence (1e-6)."""
+    import time
+    import xnn_amd.dispersion as XD
+    from xnn_amd import synthetic
+    _note("eeq C5 large regime")
+    s = synthetic.organic_box(seed=0)
+    z = [int(v) for v in s.numbers]
+    cuts = dict(cutoff_pair=60.0 * D.BOHR, cutoff_cn=25.0 * D.BOHR, cutoff_eeq_cn=25.0 * D.BOHR,
+                s9=0.0)
+    auto = XD.DFTD4(tables, **cuts).to(DEV)
+    assert auto.select_regime(5000, True) == "large"
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    with torch.no_grad():
+        q1 = _eval(auto, s.pos, z, s.cell)[0]["charges"]
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) * 1e3
+    short = XD.DFTD4(tables, cutoff_eeq=40.0 * D.BOHR, **cuts).to(DEV)
+    dense = XD.DFTD4(tables, regime="dense", **cuts).to(DEV)
+    with torch.no_grad():
+        q2 = _eval(short, s.pos, z, s.cell)[0]["charges"]
+        q3 = _eval(dense, s.pos, z, s.cell)[0]["charges"]
+    print(f"C5 large-regime EEQ evaluation {ms:.1f} ms (with CN, alpha, pair terms); "
+          f"|q(31.75 A) - q(21.2 A)| {float((q1 - q2).abs().max()):.2e}, "
+          f"|q - q_dense| {float((q1 - q3).abs().max()):.2e}", flush=True)
+    assert abs(float(q1.sum())) < 1e-10
+    np.testing.assert_allclose(q1.cpu(), q2.cpu(), atol=1e-8)
+    np.testing.assert_allclose(q1.cpu(), q3.cpu(), atol=1e-6)

@@ -1,0 +1,235 @@
+// The real-space part of the large-system EEQ operator (gfx950, float64).
+//
+// The large regime of the EEQ charges (common/models/eeq.py:170-397, the operator of
+// eeq_charges_large, eeq.py:664) splits the Coulomb interaction of the charge
+// distributions with an Ewald parameter alpha: the screened kernel
+//   K_ij(r) = [erf(gamma_ij r) - erf(alpha r)] / r,  gamma_ij = (a_i^2 + a_j^2)^(-1/2),
+// summed over every lattice image within the real-space cutoff (an atom's own images
+// included, r > 0), and a reciprocal sum that the host forms from structure factors.
+// A molecule takes alpha = 0 and the single image: K = erf(gamma r) / r.
+//
+// xnn_eeq_real_matrix forms R_ij = sum_n K_ij(|pos_j + n cell - pos_i|) as a dense (N, N)
+// float64 matrix (symmetric): one thread per (i, j), the images of the pair in a window
+// taken from its fractional coordinates and the cell's interplanar spacings (every image
+// within the cutoff lies in it). With 288 GB of HBM the dense matrix is the MI355X form up
+// to ~10^5 atoms: it is formed once per evaluation and factorized on the device.
+//
+// xnn_eeq_real_grad forms the derivatives of S = sum_ij u_i R_ij(pos, cell) w_j: with
+// d = pos_j + n cell - pos_i and K' = dK/dr,
+//   dS/dpos_k = -sum_{j,n} (u_k w_j + u_j w_k) K'(r) d / r,
+//   dS/dcell = sum_k sum_{j,n} u_k w_j K'(r) n (x) d / r   (per-atom rows, summed by the caller),
+// one wave per atom k, lanes over j, a fixed butterfly: bitwise reproducible.
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdint>
+
+#include "common.h"
+#include "device.h"
+
+namespace xnn {
+
+struct EeqCell {
+  double a[9];    // rows, bohr
+  double inv[9];  // inverse, f = d @ inv
+  double reach[3];  // cutoff / interplanar spacing per axis (0: not periodic)
+  int periodic;
+};
+
+// the window of image offsets n_a for fractional difference f_a: |f_a + n_a| <= reach_a
+__device__ inline void image_range(double f, double reach, int& lo, int& hi) {
+  lo = (int)ceil(-reach - f);
+  hi = (int)floor(reach - f);
+}
+
+__device__ inline double screened(double r, double gam, double alpha) {
+  const double k = erf(gam * r);
+  return (alpha > 0.0 ? k - erf(alpha * r) : k) / r;
+}
+
+// dK/dr of the screened kernel
+__device__ inline double screened_slope(double r, double gam, double alpha, double K) {
+  constexpr double two_over_sqrt_pi = 1.1283791670955126;
+  double g = gam * exp(-gam * gam * r * r);
+  if (alpha > 0.0) g -= alpha * exp(-alpha * alpha * r * r);
+  return (two_over_sqrt_pi * g - K) / r;
+}
+
+// calls fn(dx, dy, dz, n0, n1, n2) for every image of the pair (i -> j) within the cutoff
+template <typename Fn>
+__device__ inline void for_images(const EeqCell& C, double dx0, double dy0, double dz0,
+                                  double cut2, bool same, Fn&& fn) {
+  if (!C.periodic) {
+    const double r2 = dx0 * dx0 + dy0 * dy0 + dz0 * dz0;
+    if (!same && r2 <= cut2) fn(dx0, dy0, dz0, 0, 0, 0);
+    return;
+  }
+  // fractional difference, wrapped to [-1/2, 1/2] (the wrap is folded into n)
+  double f[3];
+#pragma unroll
+  for (int c = 0; c < 3; ++c) f[c] = dx0 * C.inv[c] + dy0 * C.inv[3 + c] + dz0 * C.inv[6 + c];
+  int w[3];
+#pragma unroll
+  for (int c = 0; c < 3; ++c) {
+    w[c] = (int)rint(f[c]);
+    f[c] -= w[c];
+  }
+  int lo[3], hi[3];
+#pragma unroll
+  for (int c = 0; c < 3; ++c) image_range(f[c], C.reach[c], lo[c], hi[c]);
+  for (int n0 = lo[0]; n0 <= hi[0]; ++n0)
+    for (int n1 = lo[1]; n1 <= hi[1]; ++n1)
+      for (int n2 = lo[2]; n2 <= hi[2]; ++n2) {
+        const double g0 = f[0] + n0, g1 = f[1] + n1, g2 = f[2] + n2;
+        const double dx = g0 * C.a[0] + g1 * C.a[3] + g2 * C.a[6];
+        const double dy = g0 * C.a[1] + g1 * C.a[4] + g2 * C.a[7];
+        const double dz = g0 * C.a[2] + g1 * C.a[5] + g2 * C.a[8];
+        const double r2 = dx * dx + dy * dy + dz * dz;
+        if (r2 <= cut2 && r2 > 1e-20) fn(dx, dy, dz, n0 - w[0], n1 - w[1], n2 - w[2]);
+      }
+}
+
+__global__ __launch_bounds__(256) void eeq_real_matrix_kernel(
+    const double* __restrict__ pos, int64_t n, EeqCell C, const double* __restrict__ rad,
+    double alpha, double cut2, double* __restrict__ R) {
+  const int64_t j = (int64_t)blockIdx.x * 16 + threadIdx.x % 16;
+  const int64_t i = (int64_t)blockIdx.y * 16 + threadIdx.x / 16;
+  if (i >= n || j >= n) return;
+  const double ai = rad[i], aj = rad[j];
+  const double gam = 1.0 / sqrt(ai * ai + aj * aj);
+  double sum = 0.0;
+  for_images(C, pos[3 * j] - pos[3 * i], pos[3 * j + 1] - pos[3 * i + 1],
+             pos[3 * j + 2] - pos[3 * i + 2], cut2, i == j,
+             [&](double dx, double dy, double dz, int, int, int) {
+               sum += screened(sqrt(dx * dx + dy * dy + dz * dz), gam, alpha);
+             });
+  R[i * n + j] = sum;
+}
+
+__global__ __launch_bounds__(256) void eeq_real_grad_kernel(
+    const double* __restrict__ pos, int64_t n, EeqCell C, const double* __restrict__ rad,
+    double alpha, double cut2, const double* __restrict__ u, const double* __restrict__ w,
+    double* __restrict__ grad_pos, double* __restrict__ cell_partial) {
+  const int lane = threadIdx.x % kWave;
+  const int64_t k = (int64_t)blockIdx.x * (blockDim.x / kWave) + threadIdx.x / kWave;
+  if (k >= n) return;
+  const double pk0 = pos[3 * k], pk1 = pos[3 * k + 1], pk2 = pos[3 * k + 2];
+  const double ak = rad[k], uk = u[k], wk = w[k];
+  double g[3] = {0.0, 0.0, 0.0};
+  double c[9] = {0, 0, 0, 0, 0, 0, 0, 0, 0};
+  const bool want_cell = cell_partial != nullptr;
+  for (int64_t j = lane; j < n; j += kWave) {
+    const double aj = rad[j];
+    const double gam = 1.0 / sqrt(ak * ak + aj * aj);
+    const double sym = uk * w[j] + u[j] * wk, own = uk * w[j];
+    for_images(C, pos[3 * j] - pk0, pos[3 * j + 1] - pk1, pos[3 * j + 2] - pk2, cut2, j == k,
+               [&](double dx, double dy, double dz, int n0, int n1, int n2) {
+                 const double r = sqrt(dx * dx + dy * dy + dz * dz);
+                 const double K = screened(r, gam, alpha);
+                 const double s = screened_slope(r, gam, alpha, K) / r;
+                 g[0] -= sym * s * dx;
+                 g[1] -= sym * s * dy;
+                 g[2] -= sym * s * dz;
+                 if (want_cell) {
+                   const double t = own * s;
+                   c[0] += t * n0 * dx; c[1] += t * n0 * dy; c[2] += t * n0 * dz;
+                   c[3] += t * n1 * dx; c[4] += t * n1 * dy; c[5] += t * n1 * dz;
+                   c[6] += t * n2 * dx; c[7] += t * n2 * dy; c[8] += t * n2 * dz;
+                 }
+               });
+  }
+#pragma unroll
+  for (int m = kWave / 2; m > 0; m >>= 1) {
+#pragma unroll
+    for (int q = 0; q < 3; ++q) g[q] += __shfl_xor(g[q], m, kWave);
+    if (want_cell) {
+#pragma unroll
+      for (int q = 0; q < 9; ++q) c[q] += __shfl_xor(c[q], m, kWave);
+    }
+  }
+  if (lane == 0) {
+#pragma unroll
+    for (int q = 0; q < 3; ++q) grad_pos[3 * k + q] = g[q];
+    if (want_cell) {
+#pragma unroll
+      for (int q = 0; q < 9; ++q) cell_partial[9 * k + q] = c[q];
+    }
+  }
+}
+
+// host: the cell's inverse and per-axis reach; false for a singular cell
+static bool eeq_cell(const double* cell, double cutoff, EeqCell& C) {
+  C.periodic = cell != nullptr;
+  for (int q = 0; q < 9; ++q) {
+    C.a[q] = cell ? cell[q] : 0.0;
+    C.inv[q] = 0.0;
+  }
+  C.reach[0] = C.reach[1] = C.reach[2] = 0.0;
+  if (!C.periodic) return true;
+  const double* a = C.a;
+  const double c00 = a[4] * a[8] - a[5] * a[7], c01 = a[2] * a[7] - a[1] * a[8],
+               c02 = a[1] * a[5] - a[2] * a[4];
+  const double det = a[0] * c00 + a[3] * c01 + a[6] * c02;
+  if (!(std::fabs(det) > 1e-12)) return false;
+  const double id = 1.0 / det;
+  C.inv[0] = c00 * id;
+  C.inv[1] = c01 * id;
+  C.inv[2] = c02 * id;
+  C.inv[3] = (a[5] * a[6] - a[3] * a[8]) * id;
+  C.inv[4] = (a[0] * a[8] - a[2] * a[6]) * id;
+  C.inv[5] = (a[2] * a[3] - a[0] * a[5]) * id;
+  C.inv[6] = (a[3] * a[7] - a[4] * a[6]) * id;
+  C.inv[7] = (a[1] * a[6] - a[0] * a[7]) * id;
+  C.inv[8] = (a[0] * a[4] - a[1] * a[3]) * id;
+  // interplanar spacing of axis c: 1 / |column c of the inverse|; a little slack so that
+  // rounding never drops an image at the cutoff (the r test decides)
+  for (int col = 0; col < 3; ++col) {
+    const double x = C.inv[col], y = C.inv[3 + col], z = C.inv[6 + col];
+    C.reach[col] = cutoff * std::sqrt(x * x + y * y + z * z) * (1.0 + 1e-12) + 1e-12;
+  }
+  return true;
+}
+
+}  // namespace xnn
+
+using namespace xnn;
+
+extern "C" {
+
+int xnn_eeq_real_matrix(const double* pos, int64_t n_nodes, const double* cell,
+                        const double* rad, double alpha, double cutoff, double* matrix,
+                        xnn_stream_t stream) {
+  XNN_REQUIRE(n_nodes >= 0, "negative size");
+  if (n_nodes == 0) return XNN_OK;
+  XNN_REQUIRE(pos && rad && matrix, "NULL input or output");
+  XNN_REQUIRE(n_nodes <= (int64_t(1) << 20), "at most 2^20 atoms");
+  XNN_REQUIRE(cutoff > 0.0 && alpha >= 0.0, "cutoff must be positive, alpha non-negative");
+  XNN_REQUIRE(cell != nullptr || alpha == 0.0, "a molecule takes alpha = 0");
+  EeqCell C;
+  XNN_REQUIRE(eeq_cell(cell, cutoff, C), "singular cell");
+  const dim3 grid((unsigned)((n_nodes + 15) / 16), (unsigned)((n_nodes + 15) / 16));
+  hipLaunchKernelGGL(eeq_real_matrix_kernel, grid, dim3(256), 0, as_hip(stream), pos, n_nodes, C,
+                     rad, alpha, cutoff * cutoff, matrix);
+  XNN_LAUNCH_CHECK();
+  return XNN_OK;
+}
+
+int xnn_eeq_real_grad(const double* pos, int64_t n_nodes, const double* cell, const double* rad,
+                      double alpha, double cutoff, const double* u, const double* w,
+                      double* grad_pos, double* cell_partial, xnn_stream_t stream) {
+  XNN_REQUIRE(n_nodes >= 0, "negative size");
+  if (n_nodes == 0) return XNN_OK;
+  XNN_REQUIRE(pos && rad && u && w && grad_pos, "NULL input or output");
+  XNN_REQUIRE(cutoff > 0.0 && alpha >= 0.0, "cutoff must be positive, alpha non-negative");
+  XNN_REQUIRE(cell != nullptr || (alpha == 0.0 && cell_partial == nullptr),
+              "a molecule takes alpha = 0 and has no cell gradient");
+  EeqCell C;
+  XNN_REQUIRE(eeq_cell(cell, cutoff, C), "singular cell");
+  hipLaunchKernelGGL(eeq_real_grad_kernel, dim3((unsigned)grid_1d(n_nodes, 4)), dim3(256), 0,
+                     as_hip(stream), pos, n_nodes, C, rad, alpha, cutoff * cutoff, u, w, grad_pos,
+                     cell_partial);
+  XNN_LAUNCH_CHECK();
+  return XNN_OK;
+}
+
+}  // extern "C"

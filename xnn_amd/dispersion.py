@@ -45,6 +45,10 @@ EEQ_CN_MAX, EEQ_CN_REG = 8.0, 1.0e-14
 WS_TOL, EWALD_REP = 0.01, 2
 PBE0_D4 = {"s6": 1.0, "s8": 1.20065498, "a1": 0.40085597, "a2": 5.02928789}
 N_FREQ = 23
+EEQ_REGIMES = ("auto", "dense", "large")
+AUTO_LARGE_PERIODIC, AUTO_LARGE_MOLECULAR = 500, 6000     # d4.py:137-139
+DEFAULT_CUTOFF_EEQ = 16.0                                 # Angstrom, d4.py:131-134
+MIN_CUTOFF_EEQ_AU = 20.0                                  # bohr, d4.py:130
 TABLE_KEYS = ("rcov", "en", "zeff", "hardness", "r4r2", "eeq_chi", "eeq_eta", "eeq_kcnchi",
               "eeq_rad", "nref", "ngw", "refcn", "refq", "refalpha")
 
@@ -509,9 +513,14 @@ class DFTD4(nn.Module):
                  cutoff_pair: float = 60.0 * BOHR, cutoff_triple: float = 40.0 * BOHR,
                  cutoff_cn: float = 30.0 * BOHR, cutoff_eeq_cn: float = 25.0 * BOHR,
                  switch_width_pair: float = 0.0, switch_width_triple: float = 0.0,
-                 tail_correction: bool = False):
+                 tail_correction: bool = False, regime: str = "auto",
+                 cutoff_eeq: Optional[float] = None):
         super().__init__()
         self.tail_correction = bool(tail_correction)
+        regime = str(regime).lower()
+        if regime not in EEQ_REGIMES:
+            raise ValueError(f"regime must be one of {EEQ_REGIMES}, got {regime!r}")
+        self.regime = regime
         self.s6, self.s8, self.a1, self.a2 = float(s6), float(s8), float(a1), float(a2)
         self.s9, self.alp = float(s9), float(alp)
         self.ga, self.gc, self.wf = float(ga), float(gc), float(wf)
@@ -521,6 +530,11 @@ class DFTD4(nn.Module):
         self.switch_width_pair = float(switch_width_pair)
         self.switch_width_triple = float(switch_width_triple)
         self.cutoff = max(self.cutoff_pair, self.cutoff_cn, self.cutoff_eeq_cn)
+        # the real-space range of the large regime's Ewald split (d4.py:461-473): at least
+        # the other terms' radius and 16 A unless given
+        base = max(self.cutoff_pair, self.cutoff_triple, self.cutoff_cn, self.cutoff_eeq_cn)
+        self.cutoff_eeq = (float(cutoff_eeq) if cutoff_eeq is not None
+                           else (base if regime == "dense" else max(base, DEFAULT_CUTOFF_EEQ)))
         for k in TABLE_KEYS:
             v = tables[k]
             dt = torch.long if np.issubdtype(v.dtype, np.integer) else torch.float64
@@ -533,10 +547,29 @@ class DFTD4(nn.Module):
             self.register_buffer(k, v.contiguous(), persistent=False)
 
     # ---- building blocks
+    def select_regime(self, n_atoms: int, periodic: bool) -> str:
+        """``"dense"`` or ``"large"`` for one structure: ``regime="auto"`` takes the large
+        regime above 500 periodic or 6000 molecular atoms (d4.py:846-851)."""
+        if self.regime != "auto":
+            return self.regime
+        return "large" if n_atoms > (AUTO_LARGE_PERIODIC if periodic else AUTO_LARGE_MOLECULAR) \
+            else "dense"
+
     def charges(self, z: Tensor, pos_au: Tensor, cn_eeq: Tensor, total_charge: float,
                 cell_au: Optional[Tensor]) -> Tensor:
-        """EEQ charges of one structure (d4.py:682-723)."""
+        """EEQ charges of one structure (d4.py:682-723): the dense restatement of dftd4, or
+        the large regime's converged Ewald operator on the GPU (:mod:`xnn_amd.eeq`)."""
         n = pos_au.shape[0]
+        if self.select_regime(n, cell_au is not None) == "large" and n > 0:
+            from .eeq import eeq_charges_large
+            if cell_au is not None and self.cutoff_eeq < MIN_CUTOFF_EEQ_AU * BOHR:
+                raise ValueError(f"the large EEQ regime needs cutoff_eeq >= {MIN_CUTOFF_EEQ_AU:.0f} "
+                                 f"bohr ({MIN_CUTOFF_EEQ_AU * BOHR:.1f} A), got {self.cutoff_eeq:.2f} A")
+            rad = self.eeq_rad[z]
+            diag = self.eeq_eta[z] + math.sqrt(2.0 / math.pi) / rad
+            x = -self.eeq_chi[z] + self.eeq_kcnchi[z] * cn_eeq / torch.sqrt(cn_eeq + EEQ_CN_REG)
+            return eeq_charges_large(pos_au, cell_au, rad, diag, x, float(total_charge),
+                                     self.cutoff_eeq / BOHR)
         A = self._coulomb_periodic(z, pos_au, cell_au) if cell_au is not None else \
             self._coulomb_molecular(z, pos_au)
         x = -self.eeq_chi[z] + self.eeq_kcnchi[z] * cn_eeq / torch.sqrt(cn_eeq + EEQ_CN_REG)
