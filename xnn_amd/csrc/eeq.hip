@@ -190,6 +190,14 @@ static bool eeq_cell(const double* cell, double cutoff, EeqCell& C) {
   return true;
 }
 
+// the image windows stay bounded: at most kMaxReach cell lengths along any axis
+constexpr double kMaxReach = 32.0;
+static bool eeq_reach_ok(const EeqCell& C, double cutoff) {
+  if (!C.periodic) return true;
+  if (!std::isfinite(cutoff)) return false;
+  return C.reach[0] <= kMaxReach && C.reach[1] <= kMaxReach && C.reach[2] <= kMaxReach;
+}
+
 }  // namespace xnn
 
 using namespace xnn;
@@ -207,6 +215,8 @@ int xnn_eeq_real_matrix(const double* pos, int64_t n_nodes, const double* cell,
   XNN_REQUIRE(cell != nullptr || alpha == 0.0, "a molecule takes alpha = 0");
   EeqCell C;
   XNN_REQUIRE(eeq_cell(cell, cutoff, C), "singular cell");
+  XNN_REQUIRE(eeq_reach_ok(C, cutoff), "the real-space range spans more than %g cells",
+              kMaxReach);
   const dim3 grid((unsigned)((n_nodes + 15) / 16), (unsigned)((n_nodes + 15) / 16));
   hipLaunchKernelGGL(eeq_real_matrix_kernel, grid, dim3(256), 0, as_hip(stream), pos, n_nodes, C,
                      rad, alpha, cutoff * cutoff, matrix);
@@ -225,6 +235,8 @@ int xnn_eeq_real_grad(const double* pos, int64_t n_nodes, const double* cell, co
               "a molecule takes alpha = 0 and has no cell gradient");
   EeqCell C;
   XNN_REQUIRE(eeq_cell(cell, cutoff, C), "singular cell");
+  XNN_REQUIRE(eeq_reach_ok(C, cutoff), "the real-space range spans more than %g cells",
+              kMaxReach);
   hipLaunchKernelGGL(eeq_real_grad_kernel, dim3((unsigned)grid_1d(n_nodes, 4)), dim3(256), 0,
                      as_hip(stream), pos, n_nodes, C, rad, alpha, cutoff * cutoff, u, w, grad_pos,
                      cell_partial);
