@@ -384,15 +384,17 @@ int xnn_d4_two_body_backward(const double* pos, int64_t n_nodes, const int32_t* 
  * eeq.py:664; dispersion_fast/eeq.py:69 keeps it as a sparse CSR matrix):
  * matrix (N,N) = sum over lattice images n with 0 < |d| <= cutoff of
  * [erf(gamma_ij |d|) - erf(alpha |d|)] / |d|, d = pos_j + n cell - pos_i,
- * gamma_ij = (rad_i^2 + rad_j^2)^(-1/2). cell (3,3) rows or NULL (a molecule: one image,
- * alpha must be 0). Written, row-major, symmetric. */
+ * gamma_ij = (rad_i^2 + rad_j^2)^(-1/2). pos, rad and matrix are device memory; cell is
+ * HOST memory, 9 doubles (rows), or NULL (a molecule: one image, alpha must be 0; the
+ * cutoff may be infinite). Written, row-major, symmetric. */
 int xnn_eeq_real_matrix(const double* pos, int64_t n_nodes, const double* cell,
                         const double* rad, double alpha, double cutoff, double* matrix,
                         xnn_stream_t stream);
 
 /* Derivatives of S = sum_ij u_i matrix_ij w_j with respect to the positions, grad_pos
  * (N,3), and the cell, as per-atom rows cell_partial (N,3,3) to be summed (nullable;
- * NULL for a molecule). Deterministic. */
+ * NULL for a molecule). cell is host memory as above, the rest device memory.
+ * Deterministic. */
 int xnn_eeq_real_grad(const double* pos, int64_t n_nodes, const double* cell, const double* rad,
                       double alpha, double cutoff, const double* u, const double* w,
                       double* grad_pos, double* cell_partial, xnn_stream_t stream);

@@ -24,6 +24,7 @@ for the reciprocal sum), so forces and stress need no second matrix. Differentia
 """
 from __future__ import annotations
 
+import ctypes
 import math
 from typing import Optional, Tuple
 
@@ -91,14 +92,21 @@ def reciprocal_apply(pos: Tensor, g: Tensor, w: Tensor, v: Tensor) -> Tensor:
 
 
 # --------------------------------------------------------------------------- real space (HIP)
+def _host_cell(cell: Optional[Tensor]):
+    """The cell rows as 9 host doubles (the kernels take the lattice by value), or None."""
+    if cell is None:
+        return None
+    vals = [float(v) for v in cell.detach().to(torch.float64).reshape(9).cpu()]
+    return (ctypes.c_double * 9)(*vals)
+
+
 def real_matrix(pos: Tensor, cell: Optional[Tensor], rad: Tensor, alpha: float,
                 cutoff_au: float) -> Tensor:
     """The dense real-space matrix R (N, N) of the screened kernel (no autograd)."""
     n = pos.shape[0]
     out = torch.empty((n, n), dtype=torch.float64, device=pos.device)
     p = pos.detach().to(torch.float64).contiguous()
-    c = None if cell is None else cell.detach().to(torch.float64).reshape(3, 3).contiguous()
-    _lib.call("xnn_eeq_real_matrix", _lib.ptr(p), n, _lib.ptr(c),
+    _lib.call("xnn_eeq_real_matrix", _lib.ptr(p), n, _host_cell(cell),
               _lib.ptr(rad.detach().to(torch.float64).contiguous()), float(alpha),
               float(cutoff_au), _lib.ptr(out), _lib.stream(pos.device))
     return out
@@ -134,9 +142,8 @@ def _real_apply_backward(ctx, grad):
     grad_pos = torch.empty((n, 3), dtype=torch.float64, device=dev)
     want_cell = cell is not None and ctx.needs_input_grad[1]
     part = torch.empty((n, 9), dtype=torch.float64, device=dev) if want_cell else None
-    c = None if cell is None else cell.detach().to(torch.float64).reshape(3, 3).contiguous()
     _lib.call("xnn_eeq_real_grad", _lib.ptr(pos.detach().to(torch.float64).contiguous()), n,
-              _lib.ptr(c), _lib.ptr(rad.detach().to(torch.float64).contiguous()), float(ctx.alpha),
+              _host_cell(cell), _lib.ptr(rad.detach().to(torch.float64).contiguous()), float(ctx.alpha),
               float(ctx.cutoff), _lib.ptr(grad.to(torch.float64).contiguous()),
               _lib.ptr(v.detach().to(torch.float64).contiguous()), _lib.ptr(grad_pos),
               _lib.ptr(part), _lib.stream(dev))
