@@ -75,9 +75,12 @@ def test_operator_matches_the_oracle_and_the_madelung_constant(tables):
 
 
 def _d4_large(tables, **kw):
+    """D4 on the large EEQ regime; the pair cutoff switched over 2 A so that the energy is
+    smooth in the positions and strain (finite differences across a sharp cutoff jump)."""
     import xnn_amd.dispersion as XD
     return XD.DFTD4(tables, regime="large", s9=0.0, cutoff_pair=9.0, cutoff_cn=8.0,
-                    cutoff_eeq_cn=8.0, cutoff_eeq=kw.pop("cutoff_eeq", 11.0), **kw).to(DEV)
+                    cutoff_eeq_cn=8.0, switch_width_pair=2.0,
+                    cutoff_eeq=kw.pop("cutoff_eeq", 11.0), **kw).to(DEV)
 
 
 def _eval(model, pos, z, cell, grad=False):
