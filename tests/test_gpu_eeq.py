@@ -163,7 +163,7 @@ def test_c5_charges_large_regime(tables):
     (real-space ranges of 31.75 and 21.2 A) to 1e-8, and close to the dense regime, whose
     Wigner-Seitz images over fixed +-2 windows are an approximation of the same Ewald sum
     (its supercell variation is ~3e-7 e on an 11-atom cell; here the two differ by ~1e-5 e):
-    charges to 5e-5 e and the D4 energy at those charges to 1e-7 relative."""
+    charges to 5e-5 e and the D4 energy at those charges to 1e-6 relative."""
     import time
     import xnn_amd.dispersion as XD
     from xnn_amd import synthetic
@@ -194,4 +194,4 @@ def test_c5_charges_large_regime(tables):
     np.testing.assert_allclose(q1.cpu(), q2.cpu(), atol=1e-8)
     np.testing.assert_allclose(q1.cpu(), q3.cpu(), atol=5e-5)
     e1, e3 = float(out1["energy"][0]), float(out3["energy"][0])
-    assert abs(e1 - e3) <= 1e-7 * abs(e3), (e1, e3)
+    assert abs(e1 - e3) <= 1e-6 * abs(e3), (e1, e3)
