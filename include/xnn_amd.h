@@ -243,6 +243,27 @@ int xnn_sh_radial_message_sum_backward(int geom_dtype, const float* vec_in, cons
                                        int32_t n_channels, const float* W, const float* d_out,
                                        float* g_vec, xnn_stream_t stream);
 
+/* Hidden layers of a per-edge radial network in one pass over the edges:
+ * s_0 = x (n_rows, n_in), s_n = silu(scales[n-1] * s_{n-1} @ W_n), out = s_{n_layers}
+ * (n_rows, widths[n_layers-1]), float32 throughout (products without reduced-precision
+ * inputs). W_n row-major (widths[n-2] or n_in, widths[n-1]); weights, widths and scales are
+ * host arrays of n_layers entries (weights holds device pointers). 1 <= n_layers <= 3,
+ * n_in <= 32, widths <= 128; x, out 16-byte aligned. Replaces FusedHidden.forward
+ * (gnn/fast/radial_kernels.py:43-58, 110-119; RadialNet._hidden_fused, gnn/models/
+ * blocks.py:289-292, with the layer factors of RadialNet._plan, blocks.py:336-365, passed
+ * as scales instead of multiplied into the matrices). */
+int xnn_radial_hidden(const float* x, int64_t n_rows, int n_in, int n_layers,
+                      const int32_t* widths, const float* const* weights, const float* scales,
+                      float* out, xnn_stream_t stream);
+
+/* Input gradient of xnn_radial_hidden, the activations recomputed: grad_x (n_rows, n_in)
+ * from grad_out (n_rows, widths[n_layers-1]). Replaces FusedHidden.backward's kernel
+ * (gnn/fast/radial_kernels.py:61-80, 121-133); the weights' gradients are the caller's
+ * (PyTorch products, as there). */
+int xnn_radial_hidden_backward(const float* x, const float* grad_out, int64_t n_rows, int n_in,
+                               int n_layers, const int32_t* widths, const float* const* weights,
+                               const float* scales, float* grad_x, xnn_stream_t stream);
+
 /* Finish of a per-structure virial: out[b] = sym(M[b] + term[b]) with sym(X) = (X + X^T)/2
  * (symmetrize != 0) or M[b] + term[b], cast to dtype. M (B,3,3) float64 (from
  * xnn_segment_reduce_f64 over the per-atom partials of xnn_edge_force_reduce or

@@ -105,6 +105,8 @@ _SIGNATURES = {
     "xnn_sh_radial_message_energy_backward": [c_int, vp, vp, i64, vp, i64, vp, vp, vp, i64, vp,
                                               vp, ctypes.POINTER(FeaturizeParams), vp, i32, vp,
                                               vp, vp, i64, vp, vp],
+    "xnn_radial_hidden": [vp, i64, c_int, c_int, vp, vp, vp, vp, vp],
+    "xnn_radial_hidden_backward": [vp, vp, i64, c_int, c_int, vp, vp, vp, vp, vp],
     "xnn_stress_finish": [c_int, vp, c_int, vp, vp, i64, dbl, vp, vp],
     "xnn_virial_finish": [c_int, vp, vp, i64, i32, vp, vp],
     "xnn_virial_reduce_workspace_bytes": [i64, i64],
@@ -293,3 +295,21 @@ def segment_reduce_f64(src: torch.Tensor, n_rows: int, n_features: int, seg_ptr:
     ws = torch.empty(max(need, 1), dtype=torch.uint8, device=out.device) if need else None
     call("xnn_segment_reduce_f64", dtype_code(src.dtype), ptr(src), n_rows, n_features,
          ptr(seg_ptr), n_segments, ptr(out), ptr(ws), need, stream(out.device))
+
+
+def radial_hidden(x: torch.Tensor, weights, scales, out: torch.Tensor,
+                  grad_out: Optional[torch.Tensor] = None) -> None:
+    """``xnn_radial_hidden`` (or its backward when ``grad_out`` is given) with the host
+    arrays of widths, weight pointers and scales built here."""
+    n = len(weights)
+    widths = (ctypes.c_int32 * n)(*[int(w.shape[1]) for w in weights])
+    wptrs = (ctypes.c_void_p * n)(*[w.data_ptr() for w in weights])
+    sc = (ctypes.c_float * n)(*[float(c) for c in scales])
+    rows, n_in = int(x.shape[0]), int(x.shape[1])
+    if grad_out is None:
+        call("xnn_radial_hidden", ptr(x), rows, n_in, n, ctypes.addressof(widths),
+             ctypes.addressof(wptrs), ctypes.addressof(sc), ptr(out), stream(x.device))
+    else:
+        call("xnn_radial_hidden_backward", ptr(x), ptr(grad_out), rows, n_in, n,
+             ctypes.addressof(widths), ctypes.addressof(wptrs), ctypes.addressof(sc), ptr(out),
+             stream(x.device))

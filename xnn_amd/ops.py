@@ -900,3 +900,34 @@ def _readout_backward(ctx, grad):
 
 
 node_readout_op.register_autograd(_readout_backward, setup_context=_readout_setup)
+
+
+# --------------------------------------------------------------------------- radial network
+@torch.library.custom_op(f"{_NS}::radial_hidden", mutates_args=())
+def radial_hidden_op(x: Tensor, weights: List[Tensor], scales: List[float]) -> Tensor:
+    """``s_n = silu(c_n s_{n-1} A_n)`` over 1-3 hidden layers (``xnn_radial_hidden``);
+    differentiable through :class:`xnn_amd.radial.FusedHidden`."""
+    _require_gpu(x, *weights)
+    out = x.new_empty((x.shape[0], weights[-1].shape[1]))
+    _lib.radial_hidden(x, weights, scales, out)
+    return out
+
+
+@radial_hidden_op.register_fake
+def _(x, weights, scales):
+    return x.new_empty((x.shape[0], weights[-1].shape[1]))
+
+
+@torch.library.custom_op(f"{_NS}::radial_hidden_backward", mutates_args=())
+def radial_hidden_backward_op(x: Tensor, grad_out: Tensor, weights: List[Tensor],
+                              scales: List[float]) -> Tensor:
+    """Input gradient of :func:`radial_hidden_op`, activations recomputed."""
+    _require_gpu(x, grad_out, *weights)
+    gx = torch.empty_like(x)
+    _lib.radial_hidden(x, weights, scales, gx, grad_out=grad_out)
+    return gx
+
+
+@radial_hidden_backward_op.register_fake
+def _(x, grad_out, weights, scales):
+    return torch.empty_like(x)
