@@ -264,6 +264,56 @@ int xnn_radial_hidden_backward(const float* x, const float* grad_out, int64_t n_
                                int n_layers, const int32_t* widths, const float* const* weights,
                                const float* scales, float* grad_x, xnn_stream_t stream);
 
+/* One uvu path of an equivariant convolution: node block of degree l1 (mul channels,
+ * offset off1 in the node rows), edge-attribute block of degree l2 (one copy, offset off2),
+ * output block of degree l3 (mul channels, offset off_out), weights off_w .. off_w + mul
+ * of the weight rows, scale coef (the path normalization over the message divisor);
+ * block: index of the node block the path reads (paths with one index share l1, mul and
+ * off1; the backward accumulates each block's gradient over its paths). */
+typedef struct {
+  int32_t l1, l2, l3;
+  int32_t mul;
+  int32_t off1, off2, off_out, off_w;
+  int32_t block;
+  float coef;
+} xnn_uvu_path;
+
+/* The message step of an equivariant convolution (uvu tensor product of the gathered
+ * sender features with the edge attributes under per-edge weights, summed onto the
+ * receivers): out[i, p, u, k] = coef_p sum_{e: dst(e)=i} w[row(e), off_w_p + u]
+ * sum_{a,b} C[a,b,k] h[src(e), off1_p + u (2 l1 + 1) + a] Y[e, off2_p + b], C the real
+ * Wigner 3j tensor of (l1, l2, l3) (e3nn convention), row(e) = weight_index[e] (nullable:
+ * e; rows outside [0, n_weight_rows) contribute nothing). Degrees <= 3, at most 48 paths
+ * with distinct output blocks, dim2 <= 16; receiver CSR (ptr_dst, perm_dst) of
+ * xnn_edge_plan. Output blocks of no path are not written. Float32, deterministic.
+ * Replaces ConvTensorProduct.conv (gnn/fast/conv.py:93-143: gather_rows + e3nn
+ * TensorProduct + scatter_sum + the message divisor) for its fast-eligible products
+ * (conv.py:35-45). */
+int xnn_uvu_conv(const float* node_feats, int64_t n_nodes, int32_t dim1, const float* edge_attrs,
+                 int32_t dim2, const float* weights, int64_t n_weight_rows, int32_t dim_w,
+                 const int32_t* weight_index, const int32_t* src, int64_t n_edges,
+                 const int32_t* ptr_dst, const int32_t* perm_dst, const xnn_uvu_path* paths,
+                 int32_t n_paths, float* out, int32_t dim_out, xnn_stream_t stream);
+
+/* Workspace of xnn_uvu_conv_backward when it forms grad_edge_attrs: one float per edge
+ * and per column of every path's edge block. */
+size_t xnn_uvu_conv_workspace_bytes(int64_t n_edges, const xnn_uvu_path* paths, int32_t n_paths);
+
+/* Gradients of xnn_uvu_conv from grad_out (N, dim_out), each output nullable:
+ * grad_node_feats (N, dim1) over the sender CSR (ptr_src, perm_src; node blocks that no
+ * path reads are not written), grad_edge_attrs (E, dim2) and grad_weights (E, dim_w), per
+ * edge, over the receiver CSR (the caller sums the rows of shared weights). */
+int xnn_uvu_conv_backward(const float* node_feats, int64_t n_nodes, int32_t dim1,
+                          const float* edge_attrs, int32_t dim2, const float* weights,
+                          int64_t n_weight_rows, int32_t dim_w, const int32_t* weight_index,
+                          const int32_t* src, const int32_t* dst, int64_t n_edges,
+                          const int32_t* ptr_dst, const int32_t* perm_dst,
+                          const int32_t* ptr_src, const int32_t* perm_src,
+                          const xnn_uvu_path* paths, int32_t n_paths, const float* grad_out,
+                          int32_t dim_out, float* grad_node_feats, float* grad_edge_attrs,
+                          float* grad_weights, void* workspace, size_t workspace_bytes,
+                          xnn_stream_t stream);
+
 /* Finish of a per-structure virial: out[b] = sym(M[b] + term[b]) with sym(X) = (X + X^T)/2
  * (symmetrize != 0) or M[b] + term[b], cast to dtype. M (B,3,3) float64 (from
  * xnn_segment_reduce_f64 over the per-atom partials of xnn_edge_force_reduce or

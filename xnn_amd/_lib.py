@@ -75,6 +75,21 @@ class AtmParams(ctypes.Structure):
     _fields_ = [("s9", dbl), ("alp3", dbl), ("cutoff", dbl), ("width", dbl)]
 
 
+class UvuPath(ctypes.Structure):
+    """``xnn_uvu_path``."""
+    _fields_ = [("l1", i32), ("l2", i32), ("l3", i32), ("mul", i32), ("off1", i32), ("off2", i32),
+                ("off_out", i32), ("off_w", i32), ("block", i32), ("coef", ctypes.c_float)]
+
+
+def uvu_paths(ints, coefs):
+    """A ctypes array of ``xnn_uvu_path`` from 9 ints per path and the coefficients."""
+    n = len(coefs)
+    arr = (UvuPath * n)()
+    for p in range(n):
+        arr[p] = UvuPath(*ints[9 * p:9 * p + 9], float(coefs[p]))
+    return arr
+
+
 # name -> argtypes (restype int unless listed in _RESTYPES)
 _SIGNATURES = {
     "xnn_last_error": [],
@@ -107,6 +122,11 @@ _SIGNATURES = {
                                               vp, vp, i64, vp, vp],
     "xnn_radial_hidden": [vp, i64, c_int, c_int, vp, vp, vp, vp, vp],
     "xnn_radial_hidden_backward": [vp, vp, i64, c_int, c_int, vp, vp, vp, vp, vp],
+    "xnn_uvu_conv": [vp, i64, i32, vp, i32, vp, i64, i32, vp, vp, i64, vp, vp, vp, i32, vp, i32,
+                     vp],
+    "xnn_uvu_conv_backward": [vp, i64, i32, vp, i32, vp, i64, i32, vp, vp, vp, i64, vp, vp, vp,
+                              vp, vp, i32, vp, i32, vp, vp, vp, vp, sz, vp],
+    "xnn_uvu_conv_workspace_bytes": [i64, vp, i32],
     "xnn_stress_finish": [c_int, vp, c_int, vp, vp, i64, dbl, vp, vp],
     "xnn_virial_finish": [c_int, vp, vp, i64, i32, vp, vp],
     "xnn_virial_reduce_workspace_bytes": [i64, i64],
@@ -167,7 +187,7 @@ _SIGNATURES = {
 _RESTYPES = {"xnn_last_error": ctypes.c_char_p, "xnn_scan_workspace_bytes": sz,
              "xnn_edge_plan_workspace_bytes": sz, "xnn_segment_reduce_workspace_bytes": sz,
              "xnn_d4_workspace_bytes": sz, "xnn_virial_reduce_workspace_bytes": sz,
-             "xnn_segment_reduce_noalloc_max_bytes": sz}
+             "xnn_segment_reduce_noalloc_max_bytes": sz, "xnn_uvu_conv_workspace_bytes": sz}
 
 _lock = threading.Lock()
 _lib: Optional[ctypes.CDLL] = None

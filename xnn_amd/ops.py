@@ -931,3 +931,90 @@ def radial_hidden_backward_op(x: Tensor, grad_out: Tensor, weights: List[Tensor]
 @radial_hidden_backward_op.register_fake
 def _(x, grad_out, weights, scales):
     return torch.empty_like(x)
+
+
+# --------------------------------------------------------------------------- uvu convolution
+def _uvu_dims(h: Tensor, y: Tensor, w: Tensor):
+    return int(h.shape[1]), int(y.shape[1]), int(w.shape[1])
+
+
+@torch.library.custom_op(f"{_NS}::uvu_conv", mutates_args=())
+def uvu_conv_op(h: Tensor, y: Tensor, w: Tensor, weight_index: Optional[Tensor], src: Tensor,
+                dst: Tensor, ptr_dst: Tensor, perm_dst: Optional[Tensor], ptr_src: Tensor,
+                perm_src: Tensor, paths: List[int], coefs: List[float], dim_out: int,
+                zero_grad_h: bool) -> Tensor:
+    """Gather + uvu tensor product + receiver sum (``xnn_uvu_conv``); ``paths`` holds 9
+    ints per path (``xnn_uvu_path``), ``coefs`` their scales (the divisor folded in)."""
+    dev = _require_gpu(h, y, w)
+    d1, d2, dw = _uvu_dims(h, y, w)
+    n, e = int(h.shape[0]), int(src.shape[0])
+    out = torch.empty((n, dim_out), dtype=torch.float32, device=dev)
+    _lib.call("xnn_uvu_conv", _lib.ptr(h), n, d1, _lib.ptr(y), d2, _lib.ptr(w), int(w.shape[0]),
+              dw, _lib.ptr(weight_index), _lib.ptr(src), e, _lib.ptr(ptr_dst), _lib.ptr(perm_dst),
+              _lib.uvu_paths(paths, coefs), len(coefs), _lib.ptr(out), dim_out, _lib.stream(dev))
+    return out
+
+
+@uvu_conv_op.register_fake
+def _(h, y, w, weight_index, src, dst, ptr_dst, perm_dst, ptr_src, perm_src, paths, coefs,
+      dim_out, zero_grad_h):
+    return h.new_empty((h.shape[0], dim_out))
+
+
+@torch.library.custom_op(f"{_NS}::uvu_conv_backward", mutates_args=())
+def uvu_conv_backward_op(g: Tensor, h: Tensor, y: Tensor, w: Tensor,
+                         weight_index: Optional[Tensor], src: Tensor, dst: Tensor,
+                         ptr_dst: Tensor, perm_dst: Optional[Tensor], ptr_src: Tensor,
+                         perm_src: Tensor, paths: List[int], coefs: List[float],
+                         zero_grad_h: bool, want_h: bool, want_y: bool,
+                         want_w: bool) -> Tuple[Tensor, Tensor, Tensor]:
+    """``(d h, d Y, d w per edge)`` of :func:`uvu_conv_op` (empty tensors where not wanted)."""
+    dev = _require_gpu(g, h, y, w)
+    d1, d2, dw = _uvu_dims(h, y, w)
+    n, e = int(h.shape[0]), int(src.shape[0])
+    f32 = dict(dtype=torch.float32, device=dev)
+    gh = ((torch.zeros if zero_grad_h else torch.empty)((n, d1), **f32) if want_h
+          else torch.empty(0, **f32))
+    gy = torch.empty((e, d2), **f32) if want_y else torch.empty(0, **f32)
+    gw = torch.empty((e, dw), **f32) if want_w else torch.empty(0, **f32)
+    table = _lib.uvu_paths(paths, coefs)
+    need = int(_lib.load().xnn_uvu_conv_workspace_bytes(e, table, len(coefs))) if want_y else 0
+    ws = torch.empty(max(need, 1), dtype=torch.uint8, device=dev) if need else None
+    _lib.call("xnn_uvu_conv_backward", _lib.ptr(h), n, d1, _lib.ptr(y), d2, _lib.ptr(w),
+              int(w.shape[0]), dw, _lib.ptr(weight_index), _lib.ptr(src), _lib.ptr(dst), e,
+              _lib.ptr(ptr_dst), _lib.ptr(perm_dst), _lib.ptr(ptr_src), _lib.ptr(perm_src),
+              table, len(coefs), _lib.ptr(g.contiguous()), int(g.shape[1]),
+              _lib.ptr(gh) if want_h else None, _lib.ptr(gy) if want_y else None,
+              _lib.ptr(gw) if want_w else None, _lib.ptr(ws), need, _lib.stream(dev))
+    return gh, gy, gw
+
+
+@uvu_conv_backward_op.register_fake
+def _(g, h, y, w, weight_index, src, dst, ptr_dst, perm_dst, ptr_src, perm_src, paths, coefs,
+      zero_grad_h, want_h, want_y, want_w):
+    e = src.shape[0]
+    return (h.new_empty(h.shape if want_h else (0,)), y.new_empty((e, y.shape[1]) if want_y else (0,)),
+            w.new_empty((e, w.shape[1]) if want_w else (0,)))
+
+
+def _uvu_setup(ctx, inputs, output):
+    (h, y, w, widx, src, dst, ptr_dst, perm_dst, ptr_src, perm_src, paths, coefs, dim_out,
+     zero_grad_h) = inputs
+    ctx.save_for_backward(h, y, w, widx, src, dst, ptr_dst, perm_dst, ptr_src, perm_src)
+    ctx.paths, ctx.coefs, ctx.zero_grad_h = paths, coefs, zero_grad_h
+
+
+def _uvu_backward(ctx, g):
+    _once_differentiable()
+    h, y, w, widx, src, dst, ptr_dst, perm_dst, ptr_src, perm_src = ctx.saved_tensors
+    need = ctx.needs_input_grad
+    gh, gy, gw = uvu_conv_backward_op(g, h, y, w, widx, src, dst, ptr_dst, perm_dst, ptr_src,
+                                      perm_src, ctx.paths, ctx.coefs, ctx.zero_grad_h,
+                                      bool(need[0]), bool(need[1]), bool(need[2]))
+    if need[2] and widx is not None:
+        gw = torch.zeros_like(w).index_add_(0, widx.to(torch.int64), gw)
+    return (gh if need[0] else None, gy if need[1] else None, gw if need[2] else None,
+            None, None, None, None, None, None, None, None, None, None, None)
+
+
+uvu_conv_op.register_autograd(_uvu_backward, setup_context=_uvu_setup)
