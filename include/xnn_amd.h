@@ -284,8 +284,9 @@ typedef struct {
  * sum_{a,b} C[a,b,k] h[src(e), off1_p + u (2 l1 + 1) + a] Y[e, off2_p + b], C the real
  * Wigner 3j tensor of (l1, l2, l3) (e3nn convention), row(e) = weight_index[e] (nullable:
  * e; rows outside [0, n_weight_rows) contribute nothing). Degrees <= 3, at most 48 paths
- * with distinct output blocks, dim2 <= 16; receiver CSR (ptr_dst, perm_dst) of
- * xnn_edge_plan. Output blocks of no path are not written. Float32, deterministic.
+ * with distinct output blocks, at most 16 node blocks, dim2 <= 16, one edge-attribute
+ * block per degree; receiver CSR (ptr_dst, perm_dst) of xnn_edge_plan. Output blocks of no
+ * path are not written. Float32, deterministic.
  * Replaces ConvTensorProduct.conv (gnn/fast/conv.py:93-143: gather_rows + e3nn
  * TensorProduct + scatter_sum + the message divisor) for its fast-eligible products
  * (conv.py:35-45). */
@@ -295,9 +296,10 @@ int xnn_uvu_conv(const float* node_feats, int64_t n_nodes, int32_t dim1, const f
                  const int32_t* ptr_dst, const int32_t* perm_dst, const xnn_uvu_path* paths,
                  int32_t n_paths, float* out, int32_t dim_out, xnn_stream_t stream);
 
-/* Workspace of xnn_uvu_conv_backward when it forms grad_edge_attrs: one float per edge
- * and per column of every path's edge block. */
-size_t xnn_uvu_conv_workspace_bytes(int64_t n_edges, const xnn_uvu_path* paths, int32_t n_paths);
+/* Workspace of xnn_uvu_conv_backward when it forms grad_edge_attrs: one float per edge,
+ * node block and edge-attribute column. */
+size_t xnn_uvu_conv_workspace_bytes(int64_t n_edges, int32_t dim2, const xnn_uvu_path* paths,
+                                    int32_t n_paths);
 
 /* Gradients of xnn_uvu_conv from grad_out (N, dim_out), each output nullable:
  * grad_node_feats (N, dim1) over the sender CSR (ptr_src, perm_src; node blocks that no

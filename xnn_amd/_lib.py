@@ -126,7 +126,7 @@ _SIGNATURES = {
                      vp],
     "xnn_uvu_conv_backward": [vp, i64, i32, vp, i32, vp, i64, i32, vp, vp, vp, i64, vp, vp, vp,
                               vp, vp, i32, vp, i32, vp, vp, vp, vp, sz, vp],
-    "xnn_uvu_conv_workspace_bytes": [i64, vp, i32],
+    "xnn_uvu_conv_workspace_bytes": [i64, i32, vp, i32],
     "xnn_stress_finish": [c_int, vp, c_int, vp, vp, i64, dbl, vp, vp],
     "xnn_virial_finish": [c_int, vp, vp, i64, i32, vp, vp],
     "xnn_virial_reduce_workspace_bytes": [i64, i64],

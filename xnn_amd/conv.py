@@ -15,7 +15,8 @@ sum over the instructions into the same output of ``in1_var in2_var mul2`` (time
 (``xnn_uvu_conv``, ``xnn_uvu_conv_backward``) that never stores a per-edge message.
 Fast-eligible products are those of the reference's fast path (conv.py:35-45): every
 instruction ``uvu``, second operand of multiplicity one, one instruction per output
-block, per-edge weights; here also degrees at most 3 and at most 48 paths.
+block, per-edge weights; here also degrees at most 3, at most 48 paths and 16 node-feature
+blocks, and one second-operand block per degree (as the harmonics have).
 """
 from __future__ import annotations
 
@@ -31,6 +32,7 @@ from .irreps import Instruction, Irreps, wigner_3j
 MAX_L = 3
 MAX_PATHS = 48
 MAX_DIM2 = 16
+MAX_BLOCKS = 16
 
 
 class ConvTensorProduct(nn.Module, FastPathModule):
@@ -105,6 +107,10 @@ class ConvTensorProduct(nn.Module, FastPathModule):
             and len({p.i_out for p in ins}) == len(ins) == len(self.irreps_out)
             and all(p.has_weight for p in ins)
             and len(ins) <= MAX_PATHS and self.irreps_in2.dim <= MAX_DIM2
+            and len(self.irreps_in1) <= MAX_BLOCKS
+            and len({m.ir.l for m in self.irreps_in2}) == len(self.irreps_in2)
+            and len({(p.i_in1, self.irreps_in2[p.i_in2].ir.l, self.irreps_out[p.i_out].ir.l)
+                     for p in ins}) == len(ins)
             and max(m.ir.l for m in list(self.irreps_in1) + list(self.irreps_in2)
                     + list(self.irreps_out)) <= MAX_L)
         self.__dict__["_w3j"] = {}

@@ -11,18 +11,21 @@
 // with C the real Wigner 3j tensor (cg_tables.h) and c_p the path's normalization
 // divided by the message divisor; row(e) = weight_index[e] or e.
 //
-// Work is split by (node, path): a wave owns one path of one node (of two nodes, one per
-// half-wave, when the path has at most 32 channels), its lanes the channels u. The path is
-// uniform over the wave, so each wave runs code specialized for its (l1, l2, l3) that keeps
-// the 2 l3 + 1 sums of a channel in registers and expands the product over the nonzero
-// entries of C only. The waves of one node are neighbours in the grid, so its rows of h,
-// Y and w are shared through the caches.
+// Work is split by (node, node-feature block): a wave owns one block of the node rows
+// (degree l1) for one node, or for two nodes (one per half-wave) when the block has at most
+// 32 channels, and its lanes the channels u. Per edge it reads the sender's block and the
+// edge's harmonics once and expands every path that reads the block: the paths of a block
+// differ only in (l2, l3), whose combinations for a given l1 are few and known at compile
+// time, so the code for each l1 (and largest l2) unrolls all of them, keeps their sums in
+// registers, expands each product over the nonzero entries of C only, and skips the
+// combinations the tensor product does not have. The second operand's blocks must have
+// distinct degrees (one block per l2, as the harmonics have).
 //
-// xnn_uvu_conv_backward, given d out:
-//   edge part, waves by (receiver, path) as in the forward: d w[e, p, u] per edge (the
-//   caller sums the rows of shared weights) and the channel sums of path p's share of
-//   d Y[e], kept per path in the workspace and added up by a last pass;
-//   node part, waves by (sender, node block): d h[s, block, u, a] =
+// xnn_uvu_conv_backward, given d out, over the same waves:
+//   edge part (receivers): d w[e, p, u] per edge (the caller sums the rows of shared
+//   weights) and the channel sums of each block's share of d Y[e], kept per block in the
+//   workspace and added up by a last pass;
+//   node part (senders): d h[s, block, u, a] =
 //     sum_{p reads block} c_p sum_{e: src(e) = s} w[row(e), p, u]
 //                         sum_{b, k} C[a, b, k] Y[e, b] d out[dst(e), p, u, k].
 #include <algorithm>
@@ -37,33 +40,70 @@ namespace xnn {
 constexpr int kConvWaves = 4;
 constexpr int kConvMaxPaths = 48;
 constexpr int kConvMaxL = 3;
-constexpr int kConvMaxDim2 = 16;  // entries of the edge attribute rows
+constexpr int kConvMaxDim2 = 16;   // entries of the edge attribute rows
+constexpr int kConvMaxBlocks = 16;  // node-feature blocks
+constexpr int kConvCombos = 12;     // (l2, l3) combinations of one l1 (at most 11)
 
-// The scalar fields of the arguments, copied into registers at kernel entry: the helpers
-// take this view, not the kernel argument (a reference to the by-value argument that
-// escapes into the specialized paths makes the compiler copy all of it, path table
-// included, to scratch memory).
-struct ConvView {
-  const float* h;
-  const float* y;
-  const float* w;
-  const int32_t* widx;
-  const int32_t* src;
-  const int32_t* dst;
-  const int32_t* ptr;
-  const int32_t* perm;
-  const float* g_out;
-  float* out;
-  float* g_w;
-  float* parts;
-  int64_t n_nodes, n_edges, n_w_rows;
-  int32_t d1, d2, dw, dout, n_paths, n_slots;
+// ------------------------------------------------------------------ (l1, l2, l3) tables
+struct Triple {
+  int a, b, c;
+};
+#define XNN_TRIPLE_ENTRY(a, b, c) Triple{a, b, c},
+constexpr Triple kTriples[] = {XNN_CG_TRIPLES(XNN_TRIPLE_ENTRY)};
+#undef XNN_TRIPLE_ENTRY
+constexpr int kNumTriples = (int)(sizeof(kTriples) / sizeof(kTriples[0]));
+
+// position of (l2, l3) among the combinations of l1 (table order), or -1
+__host__ __device__ constexpr int combo_index(int l1, int l2, int l3) {
+  int n = 0;
+  for (int t = 0; t < kNumTriples; ++t) {
+    if (kTriples[t].a != l1) continue;
+    if (kTriples[t].b == l2 && kTriples[t].c == l3) return n;
+    ++n;
+  }
+  return -1;
+}
+
+// first register of combination (l2, l3) among the 2 l3 + 1 sums of every combination of l1
+__host__ __device__ constexpr int combo_offset(int l1, int l2, int l3) {
+  int off = 0;
+  for (int t = 0; t < kNumTriples; ++t) {
+    if (kTriples[t].a != l1) continue;
+    if (kTriples[t].b == l2 && kTriples[t].c == l3) return off;
+    off += 2 * kTriples[t].c + 1;
+  }
+  return -1;
+}
+
+__host__ __device__ constexpr int combo_width(int l1) {
+  int off = 0;
+  for (int t = 0; t < kNumTriples; ++t)
+    if (kTriples[t].a == l1) off += 2 * kTriples[t].c + 1;
+  return off;
+}
+
+// ------------------------------------------------------------------ arguments
+struct ConvCombo {
+  int32_t off_w;    // < 0: the product has no such path
+  int32_t off_out;
+  float coef;
 };
 
-struct ConvArgs {
-  const float* h;     // (N, d1)
-  const float* y;     // (E, d2)
-  const float* w;     // (n_w_rows, dw)
+struct ConvBlock {
+  int32_t l1;       // < 0: no path reads the block
+  int32_t mul;
+  int32_t off1;
+  int32_t pad;
+  ConvCombo c[kConvCombos];
+};
+
+// The scalar fields, copied into registers at kernel entry and handed to the helpers (a
+// reference to the by-value kernel argument that escapes into them makes the compiler
+// copy all of it to scratch memory).
+struct ConvView {
+  const float* h;       // (N, d1)
+  const float* y;       // (E, d2)
+  const float* w;       // (n_w_rows, dw)
   const int32_t* widx;
   const int32_t* src;
   const int32_t* dst;
@@ -72,21 +112,21 @@ struct ConvArgs {
   const float* g_out;   // (N, dout) backward
   float* out;           // forward: (N, dout); node part: d h (N, d1)
   float* g_w;           // (E, dw) per edge
-  float* parts;         // (E, n_slots): per path channel sums of d Y
+  float* parts;         // (E, n_blocks, d2): per block channel sums of d Y
   int64_t n_nodes, n_edges, n_w_rows;
-  int32_t d1, d2, dw, dout, n_paths, n_slots;
-  xnn_uvu_path paths[kConvMaxPaths];
-  int32_t slot[kConvMaxPaths];  // first column of path p's d Y share in `parts`
+  int32_t d1, d2, dw, dout, n_blocks, ls;
+  int32_t off2[kConvMaxL + 1];  // column of the edge-attribute block of degree l (< 0: none)
 };
 
-__device__ __forceinline__ ConvView conv_view(const ConvArgs& A) {
-  return ConvView{A.h,     A.y,       A.w,       A.widx,     A.src, A.dst, A.ptr,
-                  A.perm,  A.g_out,   A.out,     A.g_w,      A.parts, A.n_nodes,
-                  A.n_edges, A.n_w_rows, A.d1, A.d2, A.dw,   A.dout, A.n_paths, A.n_slots};
-}
+struct ConvArgs {
+  ConvView v;
+  ConvBlock blocks[kConvMaxBlocks];
+  int32_t ids[kConvMaxBlocks];  // the blocks of one launch (one degree l1)
+  int32_t n_ids;
+};
 
-__device__ __forceinline__ int64_t conv_row(const ConvView& A, int64_t e) {
-  return A.widx ? (int64_t)A.widx[e] : e;
+__device__ __forceinline__ int64_t conv_row(const ConvView& V, int64_t e) {
+  return V.widx ? (int64_t)V.widx[e] : e;
 }
 
 // The nodes of a wave: one (channels in chunks of 64) or two (32 lanes each).
@@ -98,7 +138,7 @@ struct ConvLanes {
   int32_t trips;     // uniform: the longest range of the wave
 };
 
-__device__ __forceinline__ ConvLanes conv_lanes(const ConvView& A, int64_t group, bool pair,
+__device__ __forceinline__ ConvLanes conv_lanes(const ConvView& V, int64_t group, bool pair,
                                                 int lane) {
   ConvLanes L;
   L.width = pair ? 32 : kWave;
@@ -106,9 +146,9 @@ __device__ __forceinline__ ConvLanes conv_lanes(const ConvView& A, int64_t group
   L.node = pair ? 2 * group + (lane >> 5) : group;
   L.q0 = 0;
   L.len = 0;
-  if (L.node < A.n_nodes) {
-    L.q0 = A.ptr[L.node];
-    L.len = A.ptr[L.node + 1] - L.q0;
+  if (L.node < V.n_nodes) {
+    L.q0 = V.ptr[L.node];
+    L.len = V.ptr[L.node + 1] - L.q0;
   }
   int32_t t = L.len;
   if (pair) t = std::max(__builtin_amdgcn_readlane(L.len, 0), __builtin_amdgcn_readlane(L.len, 32));
@@ -127,250 +167,279 @@ __device__ __forceinline__ float conv_group_sum(float v, bool pair) {
   return v;
 }
 
-// ------------------------------------------------------------------ forward
-template <int L1, int L2, int L3>
-__device__ __forceinline__ void conv_fwd_path(const ConvView& A, const xnn_uvu_path& P,
-                                              const ConvLanes& L) {
-  using T = CGTable<L1, L2, L3>;
-  constexpr int D1 = 2 * L1 + 1, D2 = 2 * L2 + 1, D3 = 2 * L3 + 1;
-  for (int u0 = 0; u0 < P.mul; u0 += L.width) {
-    const int u = u0 + L.sub;
-    const bool chan = u < P.mul;
-    float acc[D3];
+// the edge's harmonics of degree <= LS into yv[l^2 + m] (zeros where absent or unused)
+template <int LS>
+__device__ __forceinline__ void conv_load_y(const ConvView& V, int64_t e, bool use, float* yv) {
 #pragma unroll
-    for (int k = 0; k < D3; ++k) acc[k] = 0.f;
-    for (int32_t it = 0; it < L.trips; ++it) {
-      const bool on = it < L.len;
-      int64_t e = 0, s = 0, row = -1;
-      if (on) {
-        const int32_t q = L.q0 + it;
-        e = A.perm ? (int64_t)A.perm[q] : (int64_t)q;
-        s = A.src[e];
-        row = conv_row(A, e);
-      }
-      const bool use = on && chan && row >= 0 && row < A.n_w_rows;
-      float yv[D2], hv[D1];
+  for (int l = 0; l <= LS; ++l) {
+    const int o = V.off2[l];
 #pragma unroll
-      for (int b = 0; b < D2; ++b) yv[b] = use ? A.y[e * A.d2 + P.off2 + b] : 0.f;
-#pragma unroll
-      for (int a = 0; a < D1; ++a) hv[a] = use ? A.h[s * A.d1 + P.off1 + u * D1 + a] : 0.f;
-      const float wv = use ? A.w[row * A.dw + P.off_w + u] : 0.f;
-      float t[D3];
-#pragma unroll
-      for (int k = 0; k < D3; ++k) t[k] = 0.f;
-#pragma unroll
-      for (int n = 0; n < T::n; ++n) t[T::e[n].k] += T::e[n].c * hv[T::e[n].i] * yv[T::e[n].j];
-#pragma unroll
-      for (int k = 0; k < D3; ++k) acc[k] += wv * t[k];
-    }
-    if (chan && L.node < A.n_nodes) {
-#pragma unroll
-      for (int k = 0; k < D3; ++k)
-        A.out[L.node * A.dout + P.off_out + u * D3 + k] = P.coef * acc[k];
-    }
+    for (int m = 0; m < 2 * l + 1; ++m) yv[l * l + m] = (use && o >= 0) ? V.y[e * V.d2 + o + m] : 0.f;
   }
 }
 
-// wave w: path w % n_paths of the node group w / n_paths
-__global__ __launch_bounds__(kConvWaves * kWave) void uvu_conv_fwd(ConvArgs K) {
-  const ConvView A = conv_view(K);
-  const int64_t w = (int64_t)blockIdx.x * kConvWaves + wave_in_block();
-  const int p = (int)(w % A.n_paths);
-  const xnn_uvu_path P = K.paths[p];
-  const bool pair = P.mul <= 32;
-  const int64_t group = w / A.n_paths;
-  if (group * (pair ? 2 : 1) >= A.n_nodes) return;
-  const ConvLanes L = conv_lanes(A, group, pair, threadIdx.x % kWave);
-  switch (P.l1 * 16 + P.l2 * 4 + P.l3) {
-#define XNN_CONV_CASE(a, b, c) \
-  case a * 16 + b * 4 + c: conv_fwd_path<a, b, c>(A, P, L); break;
-    XNN_CG_TRIPLES(XNN_CONV_CASE)
-#undef XNN_CONV_CASE
-    default: break;
+// the edge of step `it` of a lane's CSR range
+struct ConvEdge {
+  int64_t e, other, row;
+  bool on, row_ok;
+};
+
+__device__ __forceinline__ ConvEdge conv_edge(const ConvView& V, const ConvLanes& L, int32_t it,
+                                              const int32_t* other_of) {
+  ConvEdge E{0, 0, -1, it < L.len, false};
+  if (E.on) {
+    const int32_t q = L.q0 + it;
+    E.e = V.perm ? (int64_t)V.perm[q] : (int64_t)q;
+    E.other = other_of[E.e];
+    E.row = conv_row(V, E.e);
+    E.row_ok = E.row >= 0 && E.row < V.n_w_rows;
+  }
+  return E;
+}
+
+// ------------------------------------------------------------------ operand fetch
+// One edge's operands for one lane: the sender's block h[src(e), block, u, :], the edge's
+// harmonics and the weight of every path of the block. The edge loops fetch them one edge
+// ahead of the arithmetic (and the edge indices two ahead), so the gathers of the next edge
+// are in flight while this one is expanded.
+template <int L1, int LS>
+struct ConvFetch {
+  float hv[2 * L1 + 1];
+  float yv[(LS + 1) * (LS + 1)];
+  float wv[kConvCombos];
+};
+
+template <int L1, int LS>
+__device__ __forceinline__ void conv_fetch(const ConvView& V, const ConvBlock& B,
+                                           const ConvEdge& E, int u, bool chan, bool want_h,
+                                           ConvFetch<L1, LS>& F) {
+  constexpr int D1 = 2 * L1 + 1;
+  const bool use = E.row_ok && chan;
+  if (want_h) {
+#pragma unroll
+    for (int a = 0; a < D1; ++a) F.hv[a] = use ? V.h[E.other * V.d1 + B.off1 + u * D1 + a] : 0.f;
+  }
+  conv_load_y<LS>(V, E.e, use, F.yv);
+#define XNN_CONV_FETCH_W(P1_, P2_, P3_)                                               \
+  if constexpr (P1_ == L1 && P2_ <= LS) {                                             \
+    constexpr int ci = combo_index(P1_, P2_, P3_);                                    \
+    F.wv[ci] = (use && B.c[ci].off_w >= 0) ? V.w[E.row * V.dw + B.c[ci].off_w + u] : 0.f; \
+  }
+  XNN_CG_TRIPLES(XNN_CONV_FETCH_W)
+#undef XNN_CONV_FETCH_W
+}
+
+// ------------------------------------------------------------------ forward
+template <int L1, int LS>
+__device__ __forceinline__ void conv_fwd_block(const ConvView& V, const ConvBlock& B,
+                                               const ConvLanes& L) {
+  constexpr int NA = combo_width(L1);
+  for (int u0 = 0; u0 < B.mul; u0 += L.width) {
+    const int u = u0 + L.sub;
+    const bool chan = u < B.mul;
+    float acc[NA];
+#pragma unroll
+    for (int k = 0; k < NA; ++k) acc[k] = 0.f;
+    ConvFetch<L1, LS> F;
+    if (L.trips > 0) conv_fetch<L1, LS>(V, B, conv_edge(V, L, 0, V.src), u, chan, true, F);
+    ConvEdge En = conv_edge(V, L, 1, V.src);
+    for (int32_t it = 0; it < L.trips; ++it) {
+      const ConvFetch<L1, LS> C = F;
+      if (it + 1 < L.trips) conv_fetch<L1, LS>(V, B, En, u, chan, true, F);
+      En = conv_edge(V, L, it + 2, V.src);
+#define XNN_CONV_COMBO(P1_, P2_, P3_)                                                     \
+  if constexpr (P1_ == L1 && P2_ <= LS) {                                                 \
+    constexpr int ci = combo_index(P1_, P2_, P3_), ao = combo_offset(P1_, P2_, P3_);      \
+    using T = CGTable<P1_, P2_, P3_>;                                                     \
+    if (B.c[ci].off_w >= 0) {                                                             \
+      float t[2 * P3_ + 1];                                                               \
+      _Pragma("unroll") for (int k = 0; k < 2 * P3_ + 1; ++k) t[k] = 0.f;                 \
+      _Pragma("unroll") for (int n = 0; n < T::n; ++n)                                    \
+          t[T::e[n].k] += T::e[n].c * C.hv[T::e[n].i] * C.yv[P2_ * P2_ + T::e[n].j];      \
+      _Pragma("unroll") for (int k = 0; k < 2 * P3_ + 1; ++k)                             \
+          acc[ao + k] += C.wv[ci] * t[k];                                                 \
+    }                                                                                     \
+  }
+      XNN_CG_TRIPLES(XNN_CONV_COMBO)
+#undef XNN_CONV_COMBO
+    }
+    if (chan && L.node < V.n_nodes) {
+      float* o = V.out + L.node * V.dout;
+#define XNN_CONV_STORE(P1_, P2_, P3_)                                                     \
+  if constexpr (P1_ == L1 && P2_ <= LS) {                                                 \
+    constexpr int ci = combo_index(P1_, P2_, P3_), ao = combo_offset(P1_, P2_, P3_);      \
+    if (B.c[ci].off_w >= 0) {                                                             \
+      _Pragma("unroll") for (int k = 0; k < 2 * P3_ + 1; ++k)                             \
+          o[B.c[ci].off_out + u * (2 * P3_ + 1) + k] = B.c[ci].coef * acc[ao + k];        \
+    }                                                                                     \
+  }
+      XNN_CG_TRIPLES(XNN_CONV_STORE)
+#undef XNN_CONV_STORE
+    }
   }
 }
 
 // ------------------------------------------------------------------ backward, edge part
-template <int L1, int L2, int L3>
-__device__ __forceinline__ void conv_bwd_edge_path(const ConvView& A, const xnn_uvu_path& P,
-                                                   int slot, const ConvLanes& L, bool pair) {
-  using T = CGTable<L1, L2, L3>;
-  constexpr int D1 = 2 * L1 + 1, D2 = 2 * L2 + 1, D3 = 2 * L3 + 1;
-  for (int32_t it = 0; it < L.trips; ++it) {
-    const bool on = it < L.len;
-    int64_t e = 0, s = 0, row = -1;
-    if (on) {
-      const int32_t q = L.q0 + it;
-      e = A.perm ? (int64_t)A.perm[q] : (int64_t)q;
-      s = A.src[e];
-      row = conv_row(A, e);
+template <int L1, int LS>
+__device__ __forceinline__ void conv_bwd_edge_block(const ConvView& V, const ConvBlock& B,
+                                                    const ConvLanes& L, bool pair, int blk) {
+  constexpr int NA = combo_width(L1), NY = (LS + 1) * (LS + 1);
+  for (int u0 = 0; u0 < B.mul; u0 += L.width) {
+    const int u = u0 + L.sub;
+    const bool chan = u < B.mul && L.node < V.n_nodes;
+    // the receiver's output gradient of every path of the block, once per node
+    float gk[NA];
+#pragma unroll
+    for (int k = 0; k < NA; ++k) gk[k] = 0.f;
+    if (chan) {
+      const float* g = V.g_out + L.node * V.dout;
+#define XNN_CONV_LOADG(P1_, P2_, P3_)                                                     \
+  if constexpr (P1_ == L1 && P2_ <= LS) {                                                 \
+    constexpr int ci = combo_index(P1_, P2_, P3_), ao = combo_offset(P1_, P2_, P3_);      \
+    if (B.c[ci].off_w >= 0) {                                                             \
+      _Pragma("unroll") for (int k = 0; k < 2 * P3_ + 1; ++k)                             \
+          gk[ao + k] = g[B.c[ci].off_out + u * (2 * P3_ + 1) + k];                        \
+    }                                                                                     \
+  }
+      XNN_CG_TRIPLES(XNN_CONV_LOADG)
+#undef XNN_CONV_LOADG
     }
-    const bool row_ok = on && row >= 0 && row < A.n_w_rows;
-    float yv[D2], dyt[D2];
+    ConvFetch<L1, LS> F;
+    ConvEdge Ec = conv_edge(V, L, 0, V.src);
+    if (L.trips > 0) conv_fetch<L1, LS>(V, B, Ec, u, chan, true, F);
+    ConvEdge En = conv_edge(V, L, 1, V.src);
+    for (int32_t it = 0; it < L.trips; ++it) {
+      const ConvFetch<L1, LS> C = F;
+      const ConvEdge E = Ec;
+      if (it + 1 < L.trips) conv_fetch<L1, LS>(V, B, En, u, chan, true, F);
+      Ec = En;
+      En = conv_edge(V, L, it + 2, V.src);
+      float dyt[NY];
 #pragma unroll
-    for (int b = 0; b < D2; ++b) {
-      yv[b] = row_ok ? A.y[e * A.d2 + P.off2 + b] : 0.f;
-      dyt[b] = 0.f;
-    }
-    for (int u0 = 0; u0 < P.mul; u0 += L.width) {
-      const int u = u0 + L.sub;
-      const bool use = row_ok && u < P.mul;
-      float hv[D1], gk[D3];
+      for (int j = 0; j < NY; ++j) dyt[j] = 0.f;
+#define XNN_CONV_EDGE(P1_, P2_, P3_)                                                      \
+  if constexpr (P1_ == L1 && P2_ <= LS) {                                                 \
+    constexpr int ci = combo_index(P1_, P2_, P3_), ao = combo_offset(P1_, P2_, P3_);      \
+    using T = CGTable<P1_, P2_, P3_>;                                                     \
+    if (B.c[ci].off_w >= 0) {                                                             \
+      float dw = 0.f, dy[2 * P2_ + 1];                                                    \
+      _Pragma("unroll") for (int j = 0; j < 2 * P2_ + 1; ++j) dy[j] = 0.f;                \
+      _Pragma("unroll") for (int n = 0; n < T::n; ++n) {                                  \
+        const float hg = T::e[n].c * C.hv[T::e[n].i] * gk[ao + T::e[n].k];                \
+        dw += hg * C.yv[P2_ * P2_ + T::e[n].j];                                           \
+        dy[T::e[n].j] += hg;                                                              \
+      }                                                                                   \
+      if (V.g_w && E.on && u < B.mul)                                                     \
+        V.g_w[E.e * V.dw + B.c[ci].off_w + u] = B.c[ci].coef * dw;                        \
+      _Pragma("unroll") for (int j = 0; j < 2 * P2_ + 1; ++j)                             \
+          dyt[P2_ * P2_ + j] += B.c[ci].coef * C.wv[ci] * dy[j];                          \
+    }                                                                                     \
+  }
+      XNN_CG_TRIPLES(XNN_CONV_EDGE)
+#undef XNN_CONV_EDGE
+      if (V.parts) {
+        // this block's share of d Y[e], every column of the present edge blocks
+        float* row = V.parts + (E.e * V.n_blocks + blk) * V.d2;
 #pragma unroll
-      for (int a = 0; a < D1; ++a) hv[a] = use ? A.h[s * A.d1 + P.off1 + u * D1 + a] : 0.f;
+        for (int l = 0; l <= LS; ++l) {
+          const int o = V.off2[l];
+          if (o < 0) continue;
 #pragma unroll
-      for (int k = 0; k < D3; ++k)
-        gk[k] = use ? A.g_out[L.node * A.dout + P.off_out + u * D3 + k] : 0.f;
-      const float wv = use ? A.w[row * A.dw + P.off_w + u] : 0.f;
-      float dw = 0.f, dy[D2];
-#pragma unroll
-      for (int b = 0; b < D2; ++b) dy[b] = 0.f;
-#pragma unroll
-      for (int n = 0; n < T::n; ++n) {
-        const float hg = T::e[n].c * hv[T::e[n].i] * gk[T::e[n].k];
-        dw += hg * yv[T::e[n].j];
-        dy[T::e[n].j] += hg;
-      }
-      if (A.g_w && on && u < P.mul) A.g_w[e * A.dw + P.off_w + u] = P.coef * dw;
-#pragma unroll
-      for (int b = 0; b < D2; ++b) dyt[b] += P.coef * wv * dy[b];
-    }
-    if (A.parts) {
-#pragma unroll
-      for (int b = 0; b < D2; ++b) {
-        const float v = conv_group_sum(dyt[b], pair);
-        if (on && L.sub == 0) A.parts[e * A.n_slots + slot + b] = v;
+          for (int m = 0; m < 2 * l + 1; ++m) {
+            const float s = conv_group_sum(dyt[l * l + m], pair);
+            if (E.on && L.sub == 0) row[o + m] = u0 == 0 ? s : row[o + m] + s;
+          }
+        }
       }
     }
   }
 }
 
-__global__ __launch_bounds__(kConvWaves * kWave) void uvu_conv_bwd_edge(ConvArgs K) {
-  const ConvView A = conv_view(K);
-  const int64_t w = (int64_t)blockIdx.x * kConvWaves + wave_in_block();
-  const int p = (int)(w % A.n_paths);
-  const xnn_uvu_path P = K.paths[p];
-  const int slot = K.slot[p];
-  const bool pair = P.mul <= 32;
-  const int64_t group = w / A.n_paths;
-  if (group * (pair ? 2 : 1) >= A.n_nodes) return;
-  const ConvLanes L = conv_lanes(A, group, pair, threadIdx.x % kWave);
-  switch (P.l1 * 16 + P.l2 * 4 + P.l3) {
-#define XNN_CONV_CASE(a, b, c) \
-  case a * 16 + b * 4 + c: conv_bwd_edge_path<a, b, c>(A, P, slot, L, pair); break;
-    XNN_CG_TRIPLES(XNN_CONV_CASE)
-#undef XNN_CONV_CASE
-    default: break;
-  }
-}
-
-// d Y[e, j] = the sum of the paths' shares that land on column j
-__global__ void uvu_conv_dy_finish(ConvArgs A, float* __restrict__ g_y) {
+// d Y[e, j] = the sum of the blocks' shares
+__global__ void uvu_conv_dy_finish(ConvArgs K, float* __restrict__ g_y) {
+  const ConvView V = K.v;
   const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (t >= A.n_edges * A.d2) return;
-  const int64_t e = t / A.d2;
-  const int j = (int)(t % A.d2);
+  if (t >= V.n_edges * V.d2) return;
+  const int64_t e = t / V.d2;
+  const int j = (int)(t % V.d2);
   float v = 0.f;
-  for (int p = 0; p < A.n_paths; ++p) {
-    const int b = j - A.paths[p].off2;
-    if (b >= 0 && b < 2 * A.paths[p].l2 + 1) v += A.parts[e * A.n_slots + A.slot[p] + b];
-  }
+  for (int b = 0; b < V.n_blocks; ++b)
+    if (K.blocks[b].l1 >= 0) v += V.parts[(e * V.n_blocks + b) * V.d2 + j];
   g_y[t] = v;
 }
 
 // ------------------------------------------------------------------ backward, node part
-template <int L1, int L2, int L3>
-__device__ __forceinline__ void conv_bwd_node_path(const ConvView& A, const xnn_uvu_path& P,
-                                                   const ConvLanes& L, int u, float* acc) {
-  using T = CGTable<L1, L2, L3>;
-  constexpr int D1 = 2 * L1 + 1, D2 = 2 * L2 + 1, D3 = 2 * L3 + 1;
-  float part[D1];
-#pragma unroll
-  for (int a = 0; a < D1; ++a) part[a] = 0.f;
-  for (int32_t it = 0; it < L.trips; ++it) {
-    const bool on = it < L.len;
-    int64_t e = 0, d = 0, row = -1;
-    if (on) {
-      const int32_t q = L.q0 + it;
-      e = A.perm ? (int64_t)A.perm[q] : (int64_t)q;
-      d = A.dst[e];
-      row = conv_row(A, e);
-    }
-    const bool use = on && u < P.mul && row >= 0 && row < A.n_w_rows;
-    float yv[D2], gk[D3];
-#pragma unroll
-    for (int b = 0; b < D2; ++b) yv[b] = use ? A.y[e * A.d2 + P.off2 + b] : 0.f;
-#pragma unroll
-    for (int k = 0; k < D3; ++k) gk[k] = use ? A.g_out[d * A.dout + P.off_out + u * D3 + k] : 0.f;
-    const float wv = use ? A.w[row * A.dw + P.off_w + u] : 0.f;
-    float t[D1];
-#pragma unroll
-    for (int a = 0; a < D1; ++a) t[a] = 0.f;
-#pragma unroll
-    for (int n = 0; n < T::n; ++n) t[T::e[n].i] += T::e[n].c * yv[T::e[n].j] * gk[T::e[n].k];
-#pragma unroll
-    for (int a = 0; a < D1; ++a) part[a] += wv * t[a];
-  }
-#pragma unroll
-  for (int a = 0; a < D1; ++a) acc[a] += P.coef * part[a];
-}
-
-// every path that reads node block `blk` (all of degree L1), chunk by chunk of channels
-template <int L1>
-__device__ __forceinline__ void conv_bwd_node_block(const ConvArgs& K, const ConvView& A, int blk,
-                                                    const ConvLanes& L, int mul, int off1) {
+template <int L1, int LS>
+__device__ __forceinline__ void conv_bwd_node_block(const ConvView& V, const ConvBlock& B,
+                                                    const ConvLanes& L) {
   constexpr int D1 = 2 * L1 + 1;
-  for (int u0 = 0; u0 < mul; u0 += L.width) {
+  for (int u0 = 0; u0 < B.mul; u0 += L.width) {
     const int u = u0 + L.sub;
+    const bool chan = u < B.mul;
     float acc[D1];
 #pragma unroll
     for (int a = 0; a < D1; ++a) acc[a] = 0.f;
-    for (int p = 0; p < A.n_paths; ++p) {
-      const xnn_uvu_path P = K.paths[p];
-      if (P.block != blk) continue;
-      switch (P.l1 * 16 + P.l2 * 4 + P.l3) {
-#define XNN_CONV_CASE(a, b, c)                                           \
-  case a * 16 + b * 4 + c:                                               \
-    if constexpr (a == L1) conv_bwd_node_path<a, b, c>(A, P, L, u, acc); \
-    break;
-        XNN_CG_TRIPLES(XNN_CONV_CASE)
-#undef XNN_CONV_CASE
-        default: break;
-      }
+    ConvFetch<L1, LS> F;
+    ConvEdge Ec = conv_edge(V, L, 0, V.dst);
+    if (L.trips > 0) conv_fetch<L1, LS>(V, B, Ec, u, chan, false, F);
+    ConvEdge En = conv_edge(V, L, 1, V.dst);
+    for (int32_t it = 0; it < L.trips; ++it) {
+      const ConvFetch<L1, LS> C = F;
+      const ConvEdge E = Ec;
+      if (it + 1 < L.trips) conv_fetch<L1, LS>(V, B, En, u, chan, false, F);
+      Ec = En;
+      En = conv_edge(V, L, it + 2, V.dst);
+      const bool use = E.row_ok && chan;
+      const float* g = V.g_out + E.other * V.dout;
+#define XNN_CONV_NODE(P1_, P2_, P3_)                                                      \
+  if constexpr (P1_ == L1 && P2_ <= LS) {                                                 \
+    constexpr int ci = combo_index(P1_, P2_, P3_);                                        \
+    using T = CGTable<P1_, P2_, P3_>;                                                     \
+    if (B.c[ci].off_w >= 0) {                                                             \
+      float gk[2 * P3_ + 1], t[D1];                                                       \
+      _Pragma("unroll") for (int k = 0; k < 2 * P3_ + 1; ++k)                             \
+          gk[k] = use ? g[B.c[ci].off_out + u * (2 * P3_ + 1) + k] : 0.f;                 \
+      _Pragma("unroll") for (int q = 0; q < D1; ++q) t[q] = 0.f;                          \
+      _Pragma("unroll") for (int n = 0; n < T::n; ++n)                                    \
+          t[T::e[n].i] += T::e[n].c * C.yv[P2_ * P2_ + T::e[n].j] * gk[T::e[n].k];        \
+      const float wv = B.c[ci].coef * C.wv[ci];                                           \
+      _Pragma("unroll") for (int q = 0; q < D1; ++q) acc[q] += wv * t[q];                 \
+    }                                                                                     \
+  }
+      XNN_CG_TRIPLES(XNN_CONV_NODE)
+#undef XNN_CONV_NODE
     }
-    if (u < mul && L.node < A.n_nodes) {
+    if (chan && L.node < V.n_nodes) {
 #pragma unroll
-      for (int a = 0; a < D1; ++a) A.out[L.node * A.d1 + off1 + u * D1 + a] = acc[a];
+      for (int a = 0; a < D1; ++a) V.out[L.node * V.d1 + B.off1 + u * D1 + a] = acc[a];
     }
   }
 }
 
-// wave w: node block w % n_blocks of the sender group w / n_blocks
-__global__ __launch_bounds__(kConvWaves * kWave) void uvu_conv_bwd_node(ConvArgs K,
-                                                                        int32_t n_blocks) {
-  const ConvView A = conv_view(K);
+// ------------------------------------------------------------------ kernels
+enum ConvPass { kConvForward = 0, kConvEdgePart = 1, kConvNodePart = 2 };
+
+template <int PASS, int L1, int LS>
+__device__ __forceinline__ void conv_pass(const ConvView& V, const ConvBlock& B,
+                                          const ConvLanes& L, bool pair, int blk) {
+  if constexpr (PASS == kConvForward) conv_fwd_block<L1, LS>(V, B, L);
+  else if constexpr (PASS == kConvEdgePart) conv_bwd_edge_block<L1, LS>(V, B, L, pair, blk);
+  else conv_bwd_node_block<L1, LS>(V, B, L);
+}
+
+// One launch per node-block degree l1 (each specialization gets its own register budget):
+// wave w takes block ids[w % n_ids] of the node group w / n_ids.
+template <int PASS, int L1, int LS>
+__global__ __launch_bounds__(kConvWaves * kWave) void uvu_conv_kernel(ConvArgs K) {
+  const ConvView V = K.v;
   const int64_t w = (int64_t)blockIdx.x * kConvWaves + wave_in_block();
-  const int blk = (int)(w % n_blocks);
-  int first = -1;
-  for (int p = 0; p < A.n_paths; ++p) {
-    if (K.paths[p].block == blk) {
-      first = p;
-      break;
-    }
-  }
-  if (first < 0) return;
-  const xnn_uvu_path P = K.paths[first];
-  const bool pair = P.mul <= 32;
-  const int64_t group = w / n_blocks;
-  if (group * (pair ? 2 : 1) >= A.n_nodes) return;
-  const ConvLanes L = conv_lanes(A, group, pair, threadIdx.x % kWave);
-  switch (P.l1) {
-    case 0: conv_bwd_node_block<0>(K, A, blk, L, P.mul, P.off1); break;
-    case 1: conv_bwd_node_block<1>(K, A, blk, L, P.mul, P.off1); break;
-    case 2: conv_bwd_node_block<2>(K, A, blk, L, P.mul, P.off1); break;
-    case 3: conv_bwd_node_block<3>(K, A, blk, L, P.mul, P.off1); break;
-    default: break;
-  }
+  const int blk = K.ids[w % K.n_ids];
+  const ConvBlock B = K.blocks[blk];
+  const bool pair = B.mul <= 32;
+  const int64_t group = w / K.n_ids;
+  if (group * (pair ? 2 : 1) >= V.n_nodes) return;
+  const ConvLanes L = conv_lanes(V, group, pair, threadIdx.x % kWave);
+  conv_pass<PASS, L1, LS>(V, B, L, pair, blk);
 }
 
 // ------------------------------------------------------------------ host
@@ -387,21 +456,26 @@ static int conv_setup(ConvArgs& A, const float* h, int64_t n_nodes, int32_t d1, 
   XNN_REQUIRE(n_nodes < (int64_t(1) << 26) && n_edges < (int64_t(1) << 31),
               "at most 2^26 nodes and 2^31 - 1 edges");
   A = ConvArgs{};
-  A.h = h;
-  A.y = y;
-  A.w = w;
-  A.widx = widx;
-  A.src = src;
-  A.dst = dst;
-  A.n_nodes = n_nodes;
-  A.n_edges = n_edges;
-  A.n_w_rows = n_w_rows;
-  A.d1 = d1;
-  A.d2 = d2;
-  A.dw = dw;
-  A.dout = dout;
-  A.n_paths = n_paths;
-  int slots = 0;
+  ConvView& V = A.v;
+  V.h = h;
+  V.y = y;
+  V.w = w;
+  V.widx = widx;
+  V.src = src;
+  V.dst = dst;
+  V.n_nodes = n_nodes;
+  V.n_edges = n_edges;
+  V.n_w_rows = n_w_rows;
+  V.d1 = d1;
+  V.d2 = d2;
+  V.dw = dw;
+  V.dout = dout;
+  for (int l = 0; l <= kConvMaxL; ++l) V.off2[l] = -1;
+  for (int b = 0; b < kConvMaxBlocks; ++b) {
+    A.blocks[b].l1 = -1;
+    for (int c = 0; c < kConvCombos; ++c) A.blocks[b].c[c].off_w = -1;
+  }
+  int n_blocks = 0, ls = 0;
   for (int p = 0; p < n_paths; ++p) {
     const xnn_uvu_path& P = paths[p];
     XNN_REQUIRE(P.l1 >= 0 && P.l2 >= 0 && P.l3 >= 0 && P.l1 <= kConvMaxL && P.l2 <= kConvMaxL &&
@@ -416,20 +490,62 @@ static int conv_setup(ConvArgs& A, const float* h, int64_t n_nodes, int32_t d1, 
     XNN_REQUIRE(P.off_out >= 0 && (int64_t)P.off_out + (int64_t)P.mul * (2 * P.l3 + 1) <= dout,
                 "path %d: output block outside the row", p);
     XNN_REQUIRE(P.off_w >= 0 && (int64_t)P.off_w + P.mul <= dw, "path %d: weights outside the row", p);
-    XNN_REQUIRE(P.block >= 0 && P.block < kConvMaxPaths, "path %d: node block index", p);
-    for (int q = 0; q < p; ++q) {
-      if (paths[q].block == P.block)
-        XNN_REQUIRE(paths[q].l1 == P.l1 && paths[q].mul == P.mul && paths[q].off1 == P.off1,
-                    "paths %d and %d share block %d but not its degree, channels and offset", q,
-                    p, P.block);
-      XNN_REQUIRE(paths[q].off_out != P.off_out, "paths %d and %d write one output block", q, p);
+    XNN_REQUIRE(P.block >= 0 && P.block < kConvMaxBlocks, "path %d: node block index 0 to %d", p,
+                kConvMaxBlocks - 1);
+    XNN_REQUIRE(V.off2[P.l2] < 0 || V.off2[P.l2] == P.off2,
+                "path %d: the edge attributes have two blocks of degree %d", p, P.l2);
+    V.off2[P.l2] = P.off2;
+    ls = std::max(ls, (int)P.l2);
+    ConvBlock& B = A.blocks[P.block];
+    if (B.l1 < 0) {
+      B.l1 = P.l1;
+      B.mul = P.mul;
+      B.off1 = P.off1;
     }
-    A.paths[p] = P;
-    A.slot[p] = slots;
-    slots += 2 * P.l2 + 1;
+    XNN_REQUIRE(B.l1 == P.l1 && B.mul == P.mul && B.off1 == P.off1,
+                "path %d: block %d read with another degree, channel count or offset", p, P.block);
+    const int ci = combo_index(P.l1, P.l2, P.l3);
+    XNN_REQUIRE(ci >= 0 && ci < kConvCombos, "path %d: no table entry", p);
+    XNN_REQUIRE(B.c[ci].off_w < 0, "two paths read block %d with degrees (%d, %d)", P.block,
+                P.l2, P.l3);
+    for (int q = 0; q < p; ++q)
+      XNN_REQUIRE(paths[q].off_out != P.off_out, "paths %d and %d write one output block", q, p);
+    B.c[ci].off_w = P.off_w;
+    B.c[ci].off_out = P.off_out;
+    B.c[ci].coef = P.coef;
+    n_blocks = std::max(n_blocks, (int)P.block + 1);
   }
-  A.n_slots = slots;
+  V.n_blocks = n_blocks;
+  V.ls = ls;
   return XNN_OK;
+}
+
+template <int PASS, int L1>
+static int conv_launch_l1(ConvArgs& A, hipStream_t stream) {
+  A.n_ids = 0;
+  for (int b = 0; b < A.v.n_blocks; ++b)
+    if (A.blocks[b].l1 == L1) A.ids[A.n_ids++] = b;
+  if (A.n_ids == 0) return XNN_OK;
+  const int64_t waves = A.v.n_nodes * (int64_t)A.n_ids;
+  const dim3 grid((unsigned)grid_1d(waves, kConvWaves)), block(kConvWaves * kWave);
+  switch (A.v.ls) {
+    case 0: hipLaunchKernelGGL((uvu_conv_kernel<PASS, L1, 0>), grid, block, 0, stream, A); break;
+    case 1: hipLaunchKernelGGL((uvu_conv_kernel<PASS, L1, 1>), grid, block, 0, stream, A); break;
+    case 2: hipLaunchKernelGGL((uvu_conv_kernel<PASS, L1, 2>), grid, block, 0, stream, A); break;
+    default: hipLaunchKernelGGL((uvu_conv_kernel<PASS, L1, 3>), grid, block, 0, stream, A); break;
+  }
+  XNN_LAUNCH_CHECK();
+  return XNN_OK;
+}
+
+template <int PASS>
+static int conv_launch(const ConvArgs& args, hipStream_t stream) {
+  ConvArgs A = args;
+  int rc = conv_launch_l1<PASS, 0>(A, stream);
+  if (rc == XNN_OK) rc = conv_launch_l1<PASS, 1>(A, stream);
+  if (rc == XNN_OK) rc = conv_launch_l1<PASS, 2>(A, stream);
+  if (rc == XNN_OK) rc = conv_launch_l1<PASS, 3>(A, stream);
+  return rc;
 }
 
 }  // namespace xnn
@@ -438,11 +554,12 @@ using namespace xnn;
 
 extern "C" {
 
-size_t xnn_uvu_conv_workspace_bytes(int64_t n_edges, const xnn_uvu_path* paths, int32_t n_paths) {
-  if (n_edges <= 0 || paths == nullptr || n_paths <= 0) return 0;
-  int64_t slots = 0;
-  for (int p = 0; p < n_paths; ++p) slots += 2 * (int64_t)paths[p].l2 + 1;
-  return (size_t)(n_edges * slots) * sizeof(float);
+size_t xnn_uvu_conv_workspace_bytes(int64_t n_edges, int32_t dim2, const xnn_uvu_path* paths,
+                                    int32_t n_paths) {
+  if (n_edges <= 0 || dim2 <= 0 || paths == nullptr || n_paths <= 0) return 0;
+  int32_t n_blocks = 0;
+  for (int p = 0; p < n_paths; ++p) n_blocks = std::max(n_blocks, paths[p].block + 1);
+  return (size_t)n_edges * (size_t)n_blocks * (size_t)dim2 * sizeof(float);
 }
 
 int xnn_uvu_conv(const float* node_feats, int64_t n_nodes, int32_t dim1, const float* edge_attrs,
@@ -457,13 +574,10 @@ int xnn_uvu_conv(const float* node_feats, int64_t n_nodes, int32_t dim1, const f
   if (n_nodes == 0) return XNN_OK;
   XNN_REQUIRE(out && ptr_dst, "NULL output or CSR");
   XNN_REQUIRE(n_edges == 0 || (node_feats && edge_attrs && weights && src), "NULL input");
-  A.ptr = ptr_dst;
-  A.perm = perm_dst;
-  A.out = out;
-  hipLaunchKernelGGL(uvu_conv_fwd, dim3((unsigned)grid_1d(n_nodes * n_paths, kConvWaves)),
-                     dim3(kConvWaves * kWave), 0, as_hip(stream), A);
-  XNN_LAUNCH_CHECK();
-  return XNN_OK;
+  A.v.ptr = ptr_dst;
+  A.v.perm = perm_dst;
+  A.v.out = out;
+  return conv_launch<kConvForward>(A, as_hip(stream));
 }
 
 int xnn_uvu_conv_backward(const float* node_feats, int64_t n_nodes, int32_t dim1,
@@ -483,39 +597,35 @@ int xnn_uvu_conv_backward(const float* node_feats, int64_t n_nodes, int32_t dim1
   if (n_nodes == 0) return XNN_OK;
   XNN_REQUIRE(grad_out, "NULL output gradient");
   XNN_REQUIRE(n_edges == 0 || (node_feats && edge_attrs && weights && src), "NULL input");
-  A.g_out = grad_out;
+  A.v.g_out = grad_out;
+  const hipStream_t s = as_hip(stream);
   if ((grad_edge_attrs || grad_weights) && n_edges > 0) {
     XNN_REQUIRE(ptr_dst, "NULL receiver CSR");
     ConvArgs B = A;
-    B.ptr = ptr_dst;
-    B.perm = perm_dst;
-    B.g_w = grad_weights;
+    B.v.ptr = ptr_dst;
+    B.v.perm = perm_dst;
+    B.v.g_w = grad_weights;
     if (grad_edge_attrs) {
-      const size_t need = xnn_uvu_conv_workspace_bytes(n_edges, paths, n_paths);
+      const size_t need = xnn_uvu_conv_workspace_bytes(n_edges, dim2, paths, n_paths);
       XNN_REQUIRE(workspace != nullptr && workspace_bytes >= need,
                   "workspace of %zu bytes needed (xnn_uvu_conv_workspace_bytes)", need);
-      B.parts = static_cast<float*>(workspace);
+      B.v.parts = static_cast<float*>(workspace);
     }
-    hipLaunchKernelGGL(uvu_conv_bwd_edge, dim3((unsigned)grid_1d(n_nodes * n_paths, kConvWaves)),
-                       dim3(kConvWaves * kWave), 0, as_hip(stream), B);
-    XNN_LAUNCH_CHECK();
+    const int rc2 = conv_launch<kConvEdgePart>(B, s);
+    if (rc2 != XNN_OK) return rc2;
     if (grad_edge_attrs) {
       hipLaunchKernelGGL(uvu_conv_dy_finish, dim3((unsigned)grid_1d(n_edges * dim2, 256)),
-                         dim3(256), 0, as_hip(stream), B, grad_edge_attrs);
+                         dim3(256), 0, s, B, grad_edge_attrs);
       XNN_LAUNCH_CHECK();
     }
   }
   if (grad_node_feats) {
     XNN_REQUIRE(ptr_src && (n_edges == 0 || dst), "NULL sender CSR or receivers");
     ConvArgs B = A;
-    B.ptr = ptr_src;
-    B.perm = perm_src;
-    B.out = grad_node_feats;
-    int32_t n_blocks = 0;
-    for (int p = 0; p < n_paths; ++p) n_blocks = std::max(n_blocks, paths[p].block + 1);
-    hipLaunchKernelGGL(uvu_conv_bwd_node, dim3((unsigned)grid_1d(n_nodes * n_blocks, kConvWaves)),
-                       dim3(kConvWaves * kWave), 0, as_hip(stream), B, n_blocks);
-    XNN_LAUNCH_CHECK();
+    B.v.ptr = ptr_src;
+    B.v.perm = perm_src;
+    B.v.out = grad_node_feats;
+    return conv_launch<kConvNodePart>(B, s);
   }
   return XNN_OK;
 }
