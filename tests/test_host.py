@@ -2,6 +2,7 @@
 entry point of include/xnn_amd.h, the binding declares exactly those, the ops refuse
 CPU tensors (no fallback), and the PyTorch formulation of the modules equals the
 oracle (so ``use_fast=False`` is the reference function)."""
+import math
 import ctypes
 import os
 import re
@@ -351,3 +352,45 @@ def test_atomic_graph_subset_and_label_fields():
     for name in ("dipole", "polarizability", "spin_multiplicity", "weight", "head", "state",
                  "site_species", "energy_weight", "atom_force_weight", "fragment_charges"):
         assert getattr(sub, name) is None
+
+
+def test_fast_selection_warns_once_for_float32_and_skips_unsupported_modules(monkeypatch):
+    """fast.select: "auto" activates only the modules with a HIP path and warns once for
+    float32 (fast.py:171-201, 41-59); explicit True with an unsupported module raises."""
+    import warnings
+    from xnn_amd import fast
+
+    class Yes(fast.FastPathModule):
+        def fast_supported(self, device, dtype):
+            return True
+
+    class No(fast.FastPathModule):
+        def fast_supported(self, device, dtype):
+            return False
+
+    monkeypatch.setattr(fast._lib, "load", lambda: None)
+    monkeypatch.setattr(fast, "_warned_float32", [False])
+    mods = [Yes(), No()]
+    policy = fast.AutoPolicy(default_min_edges=0)
+    monkeypatch.setattr(policy, "decide", lambda device, dtype, n: True)
+    with warnings.catch_warnings(record=True) as rec:
+        warnings.simplefilter("always")
+        assert fast.select(mods, "auto", policy, torch.device("cuda"), torch.float32, 10)
+        fast.select(mods, "auto", policy, torch.device("cuda"), torch.float32, 10)
+    assert [m.fast_active for m in mods] == [True, False]
+    assert sum(issubclass(w.category, fast.FastPathPrecisionWarning) for w in rec) == 1
+    with pytest.raises(RuntimeError, match="no HIP path"):
+        fast.select(mods, True, policy, torch.device("cuda"), torch.float64, 10)
+
+
+def test_bessel_exact_constants():
+    from xnn_amd.featurizers import BesselRBF
+    rbf = BesselRBF(8, 5.0).double()
+    rbf.freqs.copy_(rbf.freqs.float().double())          # a float32 round trip
+    assert rbf.exact_constants()
+    assert torch.equal(rbf.freqs, math.pi * torch.arange(1, 9, dtype=torch.float64))
+    assert not rbf.exact_constants()
+    rbf.freqs[2] = 7.0                                     # not n pi: kept
+    assert not rbf.exact_constants() and rbf.freqs[2] == 7.0
+    assert not BesselRBF(8, 5.0).exact_constants()         # float32 buffer
+    assert not BesselRBF(8, 5.0, trainable=True).double().exact_constants()

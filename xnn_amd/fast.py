@@ -7,7 +7,8 @@ once per evaluation through :func:`select`. ``use_fast``:
 ``True``    the HIP kernels (raises if they cannot run on this device/dtype)
 ``False``   the PyTorch formulation of the reference
 ``"auto"``  the HIP kernels on a GPU (the MI355X entry of :data:`MI355X_POLICY`
-            takes them from the first edge), the PyTorch formulation elsewhere
+            takes them from the first edge) for the modules that have them, the
+            PyTorch formulation elsewhere
 
 The HIP backward is differentiable once, so a training step that needs the
 force loss's second derivative (``create_graph=True``) takes the PyTorch
@@ -18,12 +19,34 @@ from __future__ import annotations
 from dataclasses import dataclass, field
 from typing import Dict, List, Optional, Union
 
+import warnings
+
 import torch
 from torch import nn
 
 from . import _lib
 
 UseFast = Union[bool, str]
+
+
+class FastPathPrecisionWarning(UserWarning):
+    """A fast path ran in float32: results differ from the reference at ~1e-6
+    (fast.py:41-42)."""
+
+
+_warned_float32 = [False]
+
+
+def warn_float32_once() -> None:
+    """The float32 precision warning, once per process (fast.py:48-59)."""
+    if _warned_float32[0]:
+        return
+    _warned_float32[0] = True
+    warnings.warn(
+        "The HIP fast path is running in float32: it evaluates the reference's function "
+        "with another summation order, so energies and forces differ from the reference "
+        "at about 1e-6 relative (float64: about 1e-14). use_fast=False selects the "
+        "reference formulation.", FastPathPrecisionWarning, stacklevel=3)
 
 
 def resolve_use_fast(use_fast: UseFast) -> UseFast:
@@ -87,15 +110,19 @@ def select(modules: List[FastPathModule], use_fast: UseFast, policy: Optional[Au
         want = True
     else:
         want = (policy or MI355X_POLICY).decide(device, dtype, num_edges)
-    if want:
-        if device.type == "cuda":
-            _lib.load()  # raises when the HIP library is missing: no silent fallback
-        for m in modules:
-            if not m.fast_supported(device, dtype):
-                raise RuntimeError(f"{type(m).__name__} has no HIP path for {device}/{dtype}")
+    if want and device.type == "cuda":
+        _lib.load()  # raises when the HIP library is missing: no silent fallback
+    any_fast = False
     for m in modules:
-        m.fast_active = bool(want)
-    return bool(want) and bool(modules)
+        ok = m.fast_supported(device, dtype)
+        if want and not ok and use_fast is True:
+            # asked for explicitly: a module without a HIP path is an error, not a fallback
+            raise RuntimeError(f"{type(m).__name__} has no HIP path for {device}/{dtype}")
+        m.fast_active = bool(want and ok)
+        any_fast = any_fast or m.fast_active
+    if any_fast and dtype == torch.float32:
+        warn_float32_once()
+    return any_fast
 
 
 def set_use_fast(model: nn.Module, use_fast: UseFast) -> nn.Module:

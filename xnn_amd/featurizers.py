@@ -55,6 +55,27 @@ class BesselRBF(nn.Module):
             self.register_buffer("freqs", freqs)
         self.norm = math.sqrt(2.0 / cutoff) if prefactor is None else float(prefactor)
 
+    def exact_constants(self) -> bool:
+        """Rebuild fixed float64 frequencies as the exact ``n pi`` (radial.py:233-252).
+
+        A float32 build or checkpoint leaves them rounded to float32; learned (trainable)
+        frequencies, non-float64 buffers and stored values farther than rounding (1e-6
+        relative) from ``n pi`` are kept. Returns whether any value changed.
+        """
+        freqs = self.freqs
+        if isinstance(freqs, nn.Parameter) or freqs.dtype != torch.float64:
+            return False
+        exact = math.pi * torch.arange(1, freqs.numel() + 1, dtype=torch.float64,
+                                       device=freqs.device)
+        if torch.equal(freqs, exact):
+            return False
+        scale = float(exact.abs().max()) if exact.numel() else 0.0
+        if float((freqs - exact).abs().max()) > 1e-6 * max(scale, 1e-300):
+            return False
+        with torch.no_grad():
+            freqs.copy_(exact)
+        return True
+
     def forward(self, r: Tensor) -> Tensor:
         r = r.clamp(min=1e-8)[..., None]
         return self.norm * torch.sin(self.freqs * r / self.cutoff) / r
