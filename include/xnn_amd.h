@@ -618,6 +618,20 @@ int xnn_radius_graph_molecules_fill(int geom_dtype, const void* pos, int64_t n_n
                                     int32_t* dst, int32_t* shift, int64_t* edge_index64,
                                     int64_t* shifts64, xnn_stream_t stream);
 
+/* The k nearest in-edges of every receiver (max_neighbors; nearest_edges,
+ * neighborlist.py:509-552, used by structure_to_graph, dataset.py:112-120). Two steps:
+ * xnn_nearest_edges_count writes min(deg_i, k) to kept_ptr[1..N] from the receiver CSR
+ * (ptr_dst of xnn_edge_plan); xnn_scan_counts turns kept_ptr into row pointers;
+ * xnn_nearest_edges_fill writes the kept edge ids to keep[kept_ptr[i] + rank], rank the
+ * position of the edge in its row ordered by (dist, edge id): the reference's result
+ * (edges grouped by receiver, by length within each, ties in list order).
+ * dist (E) float64 or float32 (dtype), perm_dst nullable (edges grouped already). */
+int xnn_nearest_edges_count(const int32_t* ptr_dst, int64_t n_nodes, int32_t k, int32_t* kept_ptr,
+                            xnn_stream_t stream);
+int xnn_nearest_edges_fill(int dtype, const void* dist, int64_t n_edges, const int32_t* ptr_dst,
+                           const int32_t* perm_dst, int64_t n_nodes, int32_t k,
+                           const int32_t* kept_ptr, int64_t* keep, xnn_stream_t stream);
+
 /* Exclusive scan helper for the two-step protocols: row_ptr[0..n] from counts
  * already stored in row_ptr[1..n] (in place). workspace: xnn_scan_workspace_bytes(n). */
 size_t xnn_scan_workspace_bytes(int64_t n);

@@ -91,3 +91,15 @@ def canonical(edge_index: np.ndarray, shifts: np.ndarray) -> np.ndarray:
     rows = np.concatenate([edge_index[1][:, None], edge_index[0][:, None], shifts], axis=1)
     order = np.lexsort(rows.T[::-1])
     return rows[order]
+
+
+def nearest_edges(dist: np.ndarray, dst: np.ndarray, num_nodes: int, k: int):
+    """The kept edge ids of max_neighbors, by brute force: for every receiver in turn, its
+    edges sorted by (length, id), the first k (neighborlist.py:509-552, the case where some
+    receiver has more than k edges)."""
+    out = []
+    for i in range(num_nodes):
+        mine = [e for e in range(len(dst)) if dst[e] == i]
+        mine.sort(key=lambda e: (float(dist[e]), e))
+        out.extend(mine[:k])
+    return np.asarray(out, dtype=np.int64)

@@ -975,3 +975,34 @@ def test_graph_replays_match_the_eager_step(edge_virial):
         other = step()                      # eager work between replays
         torch.cuda.synchronize()
         assert torch.equal(other["forces"], eager["forces"])
+
+
+@pytest.mark.parametrize("dtype", [torch.float64, torch.float32])
+def test_nearest_edges_on_the_gpu(dtype):
+    """max_neighbors on the GPU (xnn_nearest_edges_count/_fill) against the brute-force
+    oracle: ties broken by edge id, ungrouped and grouped receivers, rows below k; and
+    structure_to_graph(max_neighbors=12) of a dense water box equal to the CPU graph."""
+    import oracle.nl as N
+    import xnn_amd as xa
+    from xnn_amd import _lib, synthetic
+    from xnn_amd.data import nearest_edges
+    _note(f"nearest edges {dtype}")
+    rng = np.random.default_rng(7)
+    for n, e, k in ((40, 2000, 7), (300, 9000, 31), (5, 400, 1)):
+        dst = rng.integers(0, n, e)
+        d = np.round(rng.uniform(0, 4, e), 1)
+        for grouped in (False, True):
+            if grouped:
+                o = np.argsort(dst, kind="stable")
+                dst, d = dst[o], d[o]
+            before = _lib.calls.get("xnn_nearest_edges_fill", 0)
+            keep, _ = nearest_edges(torch.tensor(d, dtype=dtype, device=DEV),
+                                    torch.tensor(dst, device=DEV), n, k)
+            assert _lib.calls.get("xnn_nearest_edges_fill", 0) == before + 1
+            want = N.nearest_edges(d.astype(np.float32) if dtype == torch.float32 else d, dst, n, k)
+            np.testing.assert_array_equal(keep.cpu().numpy(), want)
+    s = synthetic.water_box(n_molecules=216, box=18.6, grid=6, seed=2)
+    gpu = xa.structure_to_graph(s.as_dict(), 5.0, device=DEV, max_neighbors=12)
+    cpu = xa.structure_to_graph(s.as_dict(), 5.0, max_neighbors=12)
+    assert torch.equal(gpu.edge_index.cpu(), cpu.edge_index)
+    assert torch.equal(gpu.cell_shifts.cpu(), cpu.cell_shifts)

@@ -149,3 +149,56 @@ def test_unique_pairs_and_half_list(pbc):
     assert a.shape[0] == len(want) + n_self // 2
     i2, k2, s2 = xa.unique_pairs(p, rc, c, pb, half=((a, b), sh))
     assert torch.equal(i2, i) and torch.equal(k2, k) and torch.equal(s2, s)
+
+
+def test_nearest_edges_matches_brute_force():
+    """max_neighbors (neighborlist.py:509-552): the kept edges against a per-receiver sort by
+    (length, id), with ties, ungrouped receivers and the early exits."""
+    import torch
+    from xnn_amd.data import nearest_edges
+    import oracle.nl as N
+    rng = np.random.default_rng(0)
+    for trial in range(6):
+        n, e = 12, 300
+        dst = torch.tensor(rng.integers(0, n, e))
+        d = torch.tensor(np.round(rng.uniform(0, 4, e), 1))        # many ties
+        for k in (1, 5, 40):
+            keep, per_atom = nearest_edges(d, dst, n, k)
+            counts = np.bincount(dst.numpy(), minlength=n)
+            if counts.max() <= k:
+                assert keep is None or np.array_equal(keep.numpy(), np.argsort(dst.numpy(), kind="stable"))
+                continue
+            assert np.array_equal(keep.numpy(), N.nearest_edges(d.numpy(), dst.numpy(), n, k))
+            assert per_atom == (k if counts.min() >= k else None)
+    # every receiver with the same count <= k: grouped keeps in place, ungrouped regroups
+    dst = torch.tensor([0, 0, 1, 1, 2, 2])
+    assert nearest_edges(torch.zeros(6), dst, 3, 4) == (None, 2)
+    keep, per_atom = nearest_edges(torch.zeros(6), torch.tensor([1, 0, 2, 1, 0, 2]), 3, 4)
+    assert keep.tolist() == [1, 4, 0, 3, 2, 5] and per_atom == 2
+    assert nearest_edges(torch.zeros(3), torch.tensor([0, 0, 1]), 2, 4) == (None, None)
+    # the length function is called only when edges are dropped
+    called = []
+    nearest_edges(lambda: called.append(1), torch.tensor([0, 0, 1]), 2, 4)
+    assert not called
+
+
+def test_structure_to_graph_max_neighbors():
+    import torch
+    import xnn_amd as xa
+    from xnn_amd import synthetic
+    s = synthetic.water_box(n_molecules=64, box=12.4, grid=4, seed=1)
+    full = xa.structure_to_graph(s.as_dict(), 5.0)
+    cut = xa.structure_to_graph(s.as_dict(), 5.0, max_neighbors=10)
+    counts = torch.bincount(cut.edge_index[1], minlength=len(s.pos))
+    assert int(counts.max()) == 10
+    # the kept edges are the 10 shortest of each receiver's full list
+    p = torch.as_tensor(s.pos, dtype=torch.float64)
+    cell = torch.as_tensor(s.cell, dtype=torch.float64)
+
+    def lengths(g):
+        v = p[g.edge_index[1]] - p[g.edge_index[0]] + g.cell_shifts.double() @ cell
+        return v.norm(dim=-1)
+    lf, lc = lengths(full), lengths(cut)
+    for i in range(0, len(s.pos), 37):
+        want = np.sort(lf[full.edge_index[1] == i].numpy())[:10]
+        np.testing.assert_array_equal(np.sort(lc[cut.edge_index[1] == i].numpy()), want)

@@ -179,6 +179,8 @@ _SIGNATURES = {
     "xnn_radius_graph_molecules_count": [c_int, vp, i64, vp, vp, i64, dbl, i32, vp, vp],
     "xnn_radius_graph_molecules_fill": [c_int, vp, i64, vp, vp, i64, dbl, i32, vp, i64, vp, vp,
                                         vp, vp, vp, vp],
+    "xnn_nearest_edges_count": [vp, i64, i32, vp, vp],
+    "xnn_nearest_edges_fill": [c_int, vp, i64, vp, vp, i64, i32, vp, vp, vp],
     "xnn_scan_workspace_bytes": [i64],
     "xnn_scan_counts": [vp, i64, vp, vp],
     "xnn_edge_plan_workspace_bytes": [i64, i64],

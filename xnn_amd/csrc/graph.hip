@@ -296,6 +296,40 @@ __global__ void zero_i32_kernel(int32_t* p, int64_t n) {
   if (i < n) p[i] = 0;
 }
 
+// ---------------------------------------------------------------- nearest edges
+// max_neighbors (dataset.py:112-120, nearest_edges neighborlist.py:509-552): per receiver,
+// keep the k edges of smallest length, ties to the earlier edge; the kept edges come out
+// grouped by receiver and ordered by (length, edge index) within each, the order of the
+// reference's two stable sorts.
+__global__ void nearest_count_kernel(const int32_t* __restrict__ ptr, int64_t n_nodes, int32_t k,
+                                     int32_t* __restrict__ kept_ptr) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n_nodes) return;
+  kept_ptr[i + 1] = min(ptr[i + 1] - ptr[i], k);
+}
+
+// one wave per receiver: the rank of every edge of the row among the row's edges
+template <typename T>
+__global__ __launch_bounds__(256) void nearest_fill_kernel(
+    const T* __restrict__ dist, const int32_t* __restrict__ ptr, const int32_t* __restrict__ perm,
+    int64_t n_nodes, int32_t k, const int32_t* __restrict__ kept_ptr, int64_t* __restrict__ keep) {
+  const int64_t row = (int64_t)blockIdx.x * 4 + threadIdx.x / 64;
+  if (row >= n_nodes) return;
+  const int lane = threadIdx.x % 64;
+  const int32_t q0 = ptr[row], q1 = ptr[row + 1];
+  for (int32_t q = q0 + lane; q < q1; q += 64) {
+    const int32_t e = perm ? perm[q] : q;
+    const T d = dist[e];
+    int32_t rank = 0;
+    for (int32_t r = q0; r < q1; ++r) {
+      const int32_t f = perm ? perm[r] : r;
+      const T df = dist[f];
+      rank += (df < d || (df == d && f < e)) ? 1 : 0;
+    }
+    if (rank < k) keep[kept_ptr[row] + rank] = e;
+  }
+}
+
 __global__ void set_first_zero_kernel(int32_t* p) { p[0] = 0; }
 
 // ---------------------------------------------------------------- molecules
@@ -755,6 +789,40 @@ int xnn_edge_plan(const int64_t* edge_index, const int64_t* cell_shifts, int64_t
   XNN_HIP_CHECK(hipcub::DeviceScan::InclusiveSum(cub, cub_bytes, cnt, ptr_dst, (int)(n_nodes + 1), s));
   XNN_HIP_CHECK(hipcub::DeviceScan::InclusiveSum(cub, cub_bytes, cnt + (n_nodes + 1), ptr_src,
                                                  (int)(n_nodes + 1), s));
+  return XNN_OK;
+}
+
+
+int xnn_nearest_edges_count(const int32_t* ptr_dst, int64_t n_nodes, int32_t k, int32_t* kept_ptr,
+                            xnn_stream_t stream) {
+  XNN_REQUIRE(n_nodes >= 0 && k >= 0, "negative size");
+  XNN_REQUIRE(kept_ptr && (n_nodes == 0 || ptr_dst), "NULL CSR");
+  if (n_nodes > 0) {
+    hipLaunchKernelGGL(nearest_count_kernel, dim3(grid_1d(n_nodes, 256)), dim3(256), 0,
+                       as_hip(stream), ptr_dst, n_nodes, k, kept_ptr);
+    XNN_LAUNCH_CHECK();
+  }
+  return XNN_OK;
+}
+
+int xnn_nearest_edges_fill(int dtype, const void* dist, int64_t n_edges, const int32_t* ptr_dst,
+                           const int32_t* perm_dst, int64_t n_nodes, int32_t k,
+                           const int32_t* kept_ptr, int64_t* keep, xnn_stream_t stream) {
+  XNN_REQUIRE(n_nodes >= 0 && n_edges >= 0 && k >= 0, "negative size");
+  XNN_REQUIRE(dtype == XNN_F32 || dtype == XNN_F64, "dtype must be XNN_F32 or XNN_F64");
+  if (n_nodes == 0 || n_edges == 0 || k == 0) return XNN_OK;
+  XNN_REQUIRE(dist && ptr_dst && kept_ptr && keep, "NULL input or output");
+  XNN_REQUIRE(n_edges < (int64_t(1) << 31), "at most 2^31 - 1 edges");
+  const dim3 grid((unsigned)grid_1d(n_nodes, 4));
+  if (dtype == XNN_F64)
+    hipLaunchKernelGGL(nearest_fill_kernel<double>, grid, dim3(256), 0, as_hip(stream),
+                       static_cast<const double*>(dist), ptr_dst, perm_dst, n_nodes, k, kept_ptr,
+                       keep);
+  else
+    hipLaunchKernelGGL(nearest_fill_kernel<float>, grid, dim3(256), 0, as_hip(stream),
+                       static_cast<const float*>(dist), ptr_dst, perm_dst, n_nodes, k, kept_ptr,
+                       keep);
+  XNN_LAUNCH_CHECK();
   return XNN_OK;
 }
 

@@ -491,10 +491,63 @@ def batched_neighbor_list(pos: Tensor, n_atoms: Tensor, cutoff: float,
 
 
 # --------------------------------------------------------------------------- graphs
-def structure_to_graph(s: dict, cutoff: float, device=None) -> AtomicGraph:
+def nearest_edges(dist, dst: Tensor, num_nodes: int, k: int):
+    """The edges to the ``k`` nearest neighbors of every receiver (neighborlist.py:509-552).
+
+    ``dist``: edge lengths (E,) or a function returning them, called only when edges are
+    dropped. Returns ``(keep, per_atom)``: ``keep`` the kept edge ids grouped by receiver
+    and ordered by (length, edge id) within each, or ``None`` to keep every edge where it
+    is; ``per_atom`` the kept count of every atom when it is the same for all. One host
+    synchronization (plus one for the kept count on the GPU). On a GPU the ranks come from
+    ``xnn_nearest_edges_count`` / ``_fill`` over the receiver CSR.
+    """
+    if dst.numel() == 0:
+        return None, None
+    counts = torch.bincount(dst, minlength=num_nodes)
+    grouped = (dst[1:] >= dst[:-1]).all() if dst.numel() > 1 else torch.ones((), dtype=torch.bool,
+                                                                              device=dst.device)
+    lo, hi, grouped = torch.stack([counts.min(), counts.max(), grouped.long()]).tolist()
+    if hi <= k:
+        if lo < hi:
+            return None, None
+        return (None if grouped else torch.sort(dst, stable=True).indices), hi
+    if callable(dist):
+        dist = dist()
+    dist = dist.detach()
+    per_atom = k if lo >= k else None
+    if dst.is_cuda:
+        from .functional import csr_of
+        _, ptr, perm = csr_of(dst, num_nodes)
+        dev = dst.device
+        kept_ptr = torch.empty(num_nodes + 1, dtype=torch.int32, device=dev)
+        _lib.call("xnn_nearest_edges_count", _lib.ptr(ptr), num_nodes, int(k), _lib.ptr(kept_ptr),
+                  _lib.stream(dev))
+        need = int(_lib.load().xnn_scan_workspace_bytes(num_nodes))
+        ws = torch.empty(max(need, 1), dtype=torch.uint8, device=dev)
+        _lib.call("xnn_scan_counts", _lib.ptr(kept_ptr), num_nodes, _lib.ptr(ws), _lib.stream(dev))
+        total = int(counts.clamp(max=k).sum())
+        keep = torch.empty(total, dtype=torch.int64, device=dev)
+        d = dist.contiguous() if dist.dtype in (torch.float32, torch.float64) else \
+            dist.double().contiguous()
+        _lib.call("xnn_nearest_edges_fill", _lib.dtype_code(d.dtype), _lib.ptr(d), int(d.numel()),
+                  _lib.ptr(ptr), _lib.ptr(perm), num_nodes, int(k), _lib.ptr(kept_ptr),
+                  _lib.ptr(keep), _lib.stream(dev))
+        return keep, per_atom
+    # CPU: order the edges by (receiver, length, id), then keep the first k of each row
+    by_len = torch.sort(dist, stable=True).indices
+    order = by_len.index_select(0, torch.sort(dst.index_select(0, by_len), stable=True).indices)
+    start = torch.cumsum(counts, 0) - counts
+    rank = torch.arange(order.numel()) - start.index_select(0, dst.index_select(0, order))
+    return order[rank < k], per_atom
+
+
+def structure_to_graph(s: dict, cutoff: float, device=None,
+                       max_neighbors: Optional[int] = None) -> AtomicGraph:
     """One structure (dict of arrays) to a graph (dataset.py:21-175): ``pos``,
     ``atomic_numbers`` and optional ``cell``/``pbc`` (a cell without pbc is periodic on
-    every axis), ``energy``, ``forces``, ``stress``, ``total_charge``."""
+    every axis), ``energy``, ``forces``, ``stress``, ``total_charge``. With
+    ``max_neighbors`` every atom keeps its nearest in-edges only (lengths in float64, so
+    that the choice does not depend on the run's dtype; dataset.py:112-120)."""
     def t(x, dtype=torch.get_default_dtype()):
         out = x if isinstance(x, Tensor) else torch.as_tensor(np.asarray(x), dtype=dtype)
         return out if device is None else out.to(device)
@@ -505,6 +558,14 @@ def structure_to_graph(s: dict, cutoff: float, device=None) -> AtomicGraph:
     pbc = (torch.as_tensor(s["pbc"], dtype=torch.bool) if s.get("pbc") is not None
            else (torch.ones(3, dtype=torch.bool) if cell is not None else None))
     edge_index, cell_shifts = build_neighbor_list(pos, cutoff, cell, pbc)
+    if max_neighbors is not None and edge_index.shape[1] > 0:
+        p = pos.to(torch.float64)
+        vec = p.index_select(0, edge_index[1]) - p.index_select(0, edge_index[0])
+        if cell is not None:
+            vec = vec + cell_shifts.to(torch.float64) @ cell.to(torch.float64)
+        keep, _ = nearest_edges(vec.norm(dim=-1), edge_index[1], pos.shape[0], int(max_neighbors))
+        if keep is not None:
+            edge_index, cell_shifts = edge_index[:, keep], cell_shifts[keep]
     n = pos.shape[0]
     dev = pos.device
     charge = s.get("total_charge", s.get("charge"))
