@@ -316,6 +316,42 @@ int xnn_uvu_conv_backward(const float* node_feats, int64_t n_nodes, int32_t dim1
                           float* grad_weights, void* workspace, size_t workspace_bytes,
                           xnn_stream_t stream);
 
+/* The parameters of the measured edge potential (ShEdgePotential): the featurizer
+ * (host struct; its l_max, sh_sign, basis, envelope and cutoff), the radial table (K)
+ * device float32, the linear layer W (K, C), the readout U (C, (l_max+1)^2) and the
+ * per-element reference energies atom_ref (n_atom_ref), all device float32. */
+typedef struct {
+  const xnn_featurize_params* prm;
+  const float* rbf_table;
+  int32_t n_channels;
+  const float* W;
+  const float* U;
+  const float* atom_ref;
+  int64_t n_atom_ref;
+} xnn_sh_pair_model;
+
+/* Workspace of xnn_sh_pair_energy_forces for a step of n_nodes atoms and n_edges edges. */
+size_t xnn_sh_pair_workspace_bytes(int64_t n_nodes, int64_t n_edges);
+
+/* One MD step of the edge potential from a pair style's tensors: positions pos (N,3)
+ * (geometry dtype), atomic_numbers (N) int64, the neighbor list edge_index (2,E) int64
+ * (row 0 sender, row 1 receiver) with integer image shifts cell_shifts (E,3) int64
+ * (nullable: none), cell (3,3) geometry dtype (NULL: a molecule), all device memory.
+ * Writes the total energy to *energy_host (float64, host), node_energy (N) float32, forces
+ * (N,3) geometry dtype and, when virial is not NULL, the virial W = -sym(sum_e r_e (x)
+ * dE/dr_e) (3,3) float64 (the pair-style sign; W = -V sigma for the stress sigma of
+ * ForceStressOutput). Synchronous: the call ends by reading the energy and the edge
+ * plan's check back (invalid atom indices: XNN_EINVAL; shifts outside [-512, 511]:
+ * XNN_ECAPACITY). Replaces LAMMPSWrapper.forward (common/deploy/lammps.py:83-145) and
+ * TorchScriptPotential.forward_lammps (common/deploy/torchscript.py:883-921) for this
+ * model, without libtorch. */
+int xnn_sh_pair_energy_forces(const xnn_sh_pair_model* model, int geom_dtype, const void* pos,
+                              int64_t n_nodes, const int64_t* atomic_numbers,
+                              const int64_t* edge_index, const int64_t* cell_shifts,
+                              int64_t n_edges, const void* cell, double* energy_host,
+                              float* node_energy, void* forces, double* virial, void* workspace,
+                              size_t workspace_bytes, xnn_stream_t stream);
+
 /* Finish of a per-structure virial: out[b] = sym(M[b] + term[b]) with sym(X) = (X + X^T)/2
  * (symmetrize != 0) or M[b] + term[b], cast to dtype. M (B,3,3) float64 (from
  * xnn_segment_reduce_f64 over the per-atom partials of xnn_edge_force_reduce or

@@ -1006,3 +1006,48 @@ def test_nearest_edges_on_the_gpu(dtype):
     cpu = xa.structure_to_graph(s.as_dict(), 5.0, max_neighbors=12)
     assert torch.equal(gpu.edge_index.cpu(), cpu.edge_index)
     assert torch.equal(gpu.cell_shifts.cpu(), cpu.cell_shifts)
+
+
+@pytest.mark.parametrize("case", ["water", "molecule"])
+def test_pair_style_entry_matches_force_stress_output(case):
+    """xnn_sh_pair_energy_forces (through deploy.LAMMPSWrapper, the pair-style tensor ABI of
+    lammps.py:83-145) against ForceStressOutput on the same graph: total and per-atom
+    energies, forces, and the virial W = -V sigma; an edge index outside [0, N) is an error."""
+    import xnn_amd as xa
+    from xnn_amd import _lib, synthetic
+    from xnn_amd.deploy import LAMMPSWrapper
+    _note(f"pair-style entry {case}")
+    if case == "water":
+        s = synthetic.water_box(n_molecules=216, box=18.6, grid=6, seed=6)
+        kw = dict(l_max=3, channels=128, sh_sign=1)
+    else:
+        s = synthetic.random_molecules(1, seed=4)[0]
+        kw = dict(l_max=2, channels=32, sh_sign=-1)
+    g = xa.structure_to_graph(s.as_dict(), 5.0, device=DEV)
+    g.pos = g.pos.float()
+    if g.cell is not None:
+        g.cell = g.cell.float()
+    model = xa.ShEdgePotential(cutoff=5.0, species=(1, 6, 7, 8), **kw).to(DEV)
+    out = xa.ForceStressOutput(model, compute_stress=g.cell is not None).eval()(g)
+    cell = g.cell[0] if g.cell is not None else torch.zeros(3, 3, device=DEV)
+    before = _lib.calls.get("xnn_sh_pair_energy_forces", 0)
+    pair = LAMMPSWrapper(model)(g.pos, g.edge_index, g.cell_shifts, g.atomic_numbers, cell)
+    assert _lib.calls.get("xnn_sh_pair_energy_forces", 0) == before + 1
+    e_ref = float(out["energy"].detach().reshape(-1)[0])
+    assert abs(float(pair["total_energy"][0]) - e_ref) <= 1e-6 * max(1.0, abs(e_ref))
+    torch.testing.assert_close(pair["node_energy"], out["node_energy"].float(), atol=1e-5, rtol=0)
+    torch.testing.assert_close(pair["forces"].double(), out["forces"].double(), atol=1e-5, rtol=0)
+    if g.cell is not None:
+        vol = float(torch.det(g.cell[0].double()))
+        want = -vol * out["stress"][0].double()
+        torch.testing.assert_close(pair["virial"], want, atol=1e-4 * max(1.0, float(want.abs().max())),
+                                   rtol=0)
+    else:
+        # a molecule: sum_e r_e (x) dE/dr_e = sum_i r_i (x) dE/dr_i (translation invariance)
+        grad = -out["forces"].double()
+        M = (g.pos.double()[:, :, None] * grad[:, None, :]).sum(0)
+        torch.testing.assert_close(pair["virial"], -0.5 * (M + M.T), atol=1e-4, rtol=0)
+    bad = g.edge_index.clone()
+    bad[0, 0] = g.num_nodes + 5
+    with pytest.raises(_lib.XnnError, match="outside"):
+        LAMMPSWrapper(model)(g.pos, bad, g.cell_shifts, g.atomic_numbers, cell)

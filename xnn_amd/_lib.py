@@ -90,6 +90,12 @@ def uvu_paths(ints, coefs):
     return arr
 
 
+class ShPairModel(ctypes.Structure):
+    """``xnn_sh_pair_model``."""
+    _fields_ = [("prm", ctypes.POINTER(FeaturizeParams)), ("rbf_table", vp), ("n_channels", i32),
+                ("W", vp), ("U", vp), ("atom_ref", vp), ("n_atom_ref", i64)]
+
+
 # name -> argtypes (restype int unless listed in _RESTYPES)
 _SIGNATURES = {
     "xnn_last_error": [],
@@ -127,6 +133,9 @@ _SIGNATURES = {
     "xnn_uvu_conv_backward": [vp, i64, i32, vp, i32, vp, i64, i32, vp, vp, vp, i64, vp, vp, vp,
                               vp, vp, i32, vp, i32, vp, vp, vp, vp, sz, vp],
     "xnn_uvu_conv_workspace_bytes": [i64, i32, vp, i32],
+    "xnn_sh_pair_workspace_bytes": [i64, i64],
+    "xnn_sh_pair_energy_forces": [ctypes.POINTER(ShPairModel), c_int, vp, i64, vp, vp, vp, i64, vp,
+                                  ctypes.POINTER(dbl), vp, vp, vp, vp, sz, vp],
     "xnn_stress_finish": [c_int, vp, c_int, vp, vp, i64, dbl, vp, vp],
     "xnn_virial_finish": [c_int, vp, vp, i64, i32, vp, vp],
     "xnn_virial_reduce_workspace_bytes": [i64, i64],
@@ -189,7 +198,8 @@ _SIGNATURES = {
 _RESTYPES = {"xnn_last_error": ctypes.c_char_p, "xnn_scan_workspace_bytes": sz,
              "xnn_edge_plan_workspace_bytes": sz, "xnn_segment_reduce_workspace_bytes": sz,
              "xnn_d4_workspace_bytes": sz, "xnn_virial_reduce_workspace_bytes": sz,
-             "xnn_segment_reduce_noalloc_max_bytes": sz, "xnn_uvu_conv_workspace_bytes": sz}
+             "xnn_segment_reduce_noalloc_max_bytes": sz, "xnn_uvu_conv_workspace_bytes": sz,
+             "xnn_sh_pair_workspace_bytes": sz}
 
 _lock = threading.Lock()
 _lib: Optional[ctypes.CDLL] = None
