@@ -7,8 +7,10 @@ dispersion.py:667-878) and ``DFTD3`` / ``D3Dispersion`` (d3.py:483-1011):
 
 * coordination numbers (d4.py:552-591) -> :func:`d4_coordination` (HIP,
   differentiable once in positions and cell);
-* EEQ charges (d4.py:593-723): dense molecular and Ewald-summed periodic interaction
-  matrices and the constrained linear solve, PyTorch (as in the reference);
+* EEQ charges (d4.py:593-723): the dense regime (molecular matrix and dftd4's Ewald sum
+  over Wigner-Seitz images, PyTorch as in the reference) and the large regime of
+  eeq.py:170-397, 664 (the converged Ewald operator: its real-space part and derivative
+  as HIP kernels, :mod:`xnn_amd.eeq`), chosen as ``regime="auto"`` does (d4.py:846-851);
 * charge-scaled Gaussian reference weights and alpha(i w) (d4.py:984-1042,
   dispersion.py:70-121) -> :func:`d4_polarizabilities_op` (HIP, one kernel each way:
   the alpha, d alpha / d cn and d alpha / d q of the reference's native d4_alpha);
@@ -20,8 +22,10 @@ dispersion.py:667-878) and ``DFTD3`` / ``D3Dispersion`` (d3.py:483-1011):
   vectors and the C6 factors), with C6 from the neutral-atom polarizabilities (D4) or the
   reference-weighted C6 rows (D3).
 
-The tail correction is not part of this path. Positions in Angstrom, energies returned in
-eV (hartree internally). The pair kernels walk every atom pair and lattice image within
+* the optional tail correction (``tail_correction=True``, d4.py:1073-1140, 1259-1267): the
+  two-body energy of a homogeneous continuum beyond the pair cutoff, per atom.
+
+Positions in Angstrom, energies returned in eV (hartree internally). The pair kernels walk every atom pair and lattice image within
 the cutoffs and the ATM term builds its own radius graph at the three-body cutoff, so the
 graph may be built at the wrapped model's own cutoff.
 """
