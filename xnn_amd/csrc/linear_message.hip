@@ -360,11 +360,35 @@ __global__ __launch_bounds__(256, 3) void lin_msg_bwd_kernel(
       for (int r = 0; r < 4; ++r) gB[t][r] = lo < L ? U[((4 * hi + r) * T + t) * L + lo] : 0.f;
     }
   }
-  for (int64_t row = (int64_t)blockIdx.x * kWavesPerBlock + wave; row < n_nodes; row += n_waves) {
-    const int b0 = ptr[row], b1 = ptr[row + 1];
-    if (b0 == b1) continue;
-    // RO: the row's cotangent scale g_i (1 otherwise)
-    const float gscale = RO ? g_node[row * g_stride] : 1.f;
+  // RO: every row's cotangent is a multiple g_i U of the same U, so the tiles need not
+  // respect the rows: a wave takes 64 consecutive CSR slots (edges of several receivers),
+  // every tile is full, and each edge's gradient is scaled by its receiver's g_i at the
+  // end (everything before is linear in it). Otherwise a wave takes one receiver row.
+  const int64_t n_slots = RO ? (int64_t)ptr[n_nodes] : 0;
+  const int64_t n_items = RO ? (n_slots + kWave - 1) / kWave : n_nodes;
+  for (int64_t item = (int64_t)blockIdx.x * kWavesPerBlock + wave; item < n_items;
+       item += n_waves) {
+    int b0, b1;
+    int64_t row;    // the receiver of this lane's slot
+    if constexpr (RO) {
+      b0 = (int)(item * kWave);
+      b1 = (int)min<int64_t>(n_slots, (int64_t)b0 + kWave);
+      // the receiver of the batch's first slot (binary search, uniform), then each lane
+      // steps to its own (a batch spans a few rows)
+      int64_t lo_r = 0, hi_r = n_nodes;  // ptr[lo_r] <= b0 < ptr[hi_r]
+      while (hi_r - lo_r > 1) {
+        const int64_t mid = (lo_r + hi_r) >> 1;
+        if (ptr[mid] <= b0) lo_r = mid; else hi_r = mid;
+      }
+      row = lo_r;
+      const int q = min(b0 + lane, b1 - 1);
+      while (row + 1 < n_nodes && ptr[row + 1] <= q) ++row;
+    } else {
+      row = item;
+      b0 = ptr[row];
+      b1 = ptr[row + 1];
+      if (b0 == b1) continue;
+    }
     // with given edge vectors, the first batch's are loaded before G is staged, so that
     // the two loads' latencies overlap
     float cx = 0.f, cy = 0.f, cz = 0.f;
@@ -477,7 +501,7 @@ __global__ __launch_bounds__(256, 3) void lin_msg_bwd_kernel(
             for (int r = 0; r < 4; ++r) dy = mfma_16x16x4(pt[t][r], gB[t][r], dy);
           // dy[r] = dY[edge 16 tau + 4 hi + r][lm lo]
 #pragma unroll
-          for (int r = 0; r < 4; ++r) sdy[(16 * tau + 4 * hi + r) * kSY + lo] = gscale * dy[r];
+          for (int r = 0; r < 4; ++r) sdy[(16 * tau + 4 * hi + r) * kSY + lo] = dy[r];
         }
         // keep phi^T and d_phi from being live together
         __builtin_amdgcn_sched_barrier(0);
@@ -525,8 +549,8 @@ __global__ __launch_bounds__(256, 3) void lin_msg_bwd_kernel(
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
               float* row_h = hs + (16 * tau + 4 * (lo >> 2) + i) * kSH + (lo & 3);
-              row_h[0] = gscale * dq0[i];
-              row_h[4] = gscale * dq1[i];
+              row_h[0] = dq0[i];
+              row_h[4] = dq1[i];
             }
           }
         } else {
@@ -535,8 +559,8 @@ __global__ __launch_bounds__(256, 3) void lin_msg_bwd_kernel(
             const int j = 16 * tau + 4 * (lo >> 2) + i;
             const int ej = __shfl(my_e, j);
             if (hi == 0 && j < cnt) {
-              if ((lo & 3) < K) d_h[(int64_t)ej * K + (lo & 3)] = gscale * dq0[i];
-              if (4 + (lo & 3) < K) d_h[(int64_t)ej * K + 4 + (lo & 3)] = gscale * dq1[i];
+              if ((lo & 3) < K) d_h[(int64_t)ej * K + (lo & 3)] = dq0[i];
+              if (4 + (lo & 3) < K) d_h[(int64_t)ej * K + 4 + (lo & 3)] = dq1[i];
             }
           }
         }
@@ -560,6 +584,13 @@ __global__ __launch_bounds__(256, 3) void lin_msg_bwd_kernel(
           vx += dl * ux;
           vy += dl * uy;
           vz += dl * uz;
+        }
+        if constexpr (RO) {
+          // the lane's receiver's cotangent scale (everything above is linear in it)
+          const float gs = g_node[row * g_stride];
+          vx *= gs;
+          vy *= gs;
+          vz *= gs;
         }
         g_vec[3 * (int64_t)my_e + 0] = sign * vx;
         g_vec[3 * (int64_t)my_e + 1] = sign * vy;
