@@ -419,16 +419,20 @@ int xnn_segment_reduce_f64_noalloc(int dtype, const void* src, int64_t n_rows,
 
 /* ------------------------------------------------------------------------ */
 /* D4 dispersion pair terms over lattice images, float64 (no edge list: every
- * receiver i meets every source j of its structure and every translation
+ * atom i meets every atom j of its structure and every translation
  * n = (n0, n1, n2) with |n_a| <= images[b, a]; vectors pos_i - pos_j + n @ cell in
  * Angstrom, lengths in bohr). Atoms of a structure are contiguous: node_ptr (B+1)
- * int64 on the device, batch (N) int32, max_atoms = the largest structure.
- * species (N) int32 indexes the per-species tables. cell (B,3,3) Angstrom rows or
- * NULL (molecules). Gradients are exact derivatives of the returned sums; the cell
- * gradient comes as per-atom partials n (x) dE/dr (N,3,3) to be summed per structure
- * with xnn_segment_reduce_f64. All memory is the caller's; workspace:
- * xnn_d4_workspace_bytes(n_nodes, n_graphs, max_atoms) bytes. Deterministic (per-
- * receiver partials summed over source chunks in a fixed order). */
+ * int64 on the device, batch (N) int32, max_atoms = the largest structure (a larger
+ * one gives NaN for its atoms). species (N) int32 indexes the per-species tables.
+ * cell (B,3,3) Angstrom rows or NULL (molecules). Gradients are exact derivatives of
+ * the returned sums; the cell gradient comes as per-atom partials (N,3,3) whose sum
+ * per structure (xnn_segment_reduce_f64) is sum n (x) dE/dr. All memory is the
+ * caller's; workspace: xnn_d4_workspace_bytes(n_nodes, n_graphs, max_atoms) bytes,
+ * about 800 max_atoms n_nodes for the two-body backward (per-atom partials and the
+ * pair sums of every pair of tiles). The kernels walk 64-atom tiles of a spatial
+ * order of each structure, every pair of two tiles once; plan is that order
+ * (xnn_d4_plan on the same pos, cell and images) or NULL to build it in the call.
+ * Deterministic (per-atom partials summed in a fixed order, no atomics). */
 typedef struct {
   double cutoff_cn;      /* D4 CN cutoff, bohr (r <= cutoff counts)           */
   double cutoff_eeq_cn;  /* EEQ CN cutoff, bohr                               */
@@ -443,6 +447,16 @@ typedef struct {
 
 size_t xnn_d4_workspace_bytes(int64_t n_nodes, int64_t n_graphs, int64_t max_atoms);
 
+/* The tile plan of the D4 pair kernels for these positions and cells, built once and
+ * passed to the four entry points below (no counterpart in the reference, whose CPU
+ * kernel needs no ordering): plan = xnn_d4_plan_bytes(n_nodes, n_graphs) bytes of
+ * device memory, the Morton order of each structure's atoms over a bin grid of their
+ * (fractional, when periodic) coordinates and the first tile of each structure. */
+size_t xnn_d4_plan_bytes(int64_t n_nodes, int64_t n_graphs);
+int xnn_d4_plan(const double* pos, int64_t n_nodes, const int64_t* node_ptr, int64_t n_graphs,
+                const double* cell, const int32_t* images, int32_t* plan, size_t plan_bytes,
+                xnn_stream_t stream);
+
 /* cn_d4[i] = sum_{j,n: r <= cutoff_cn} k4 exp(-(|EN_i - EN_j| + k5)^2 / k6) c(r) and
  * cn_raw[i] = sum_{r <= cutoff_eeq_cn} c(r), c(r) = (1 + erf(-kcn (r - rc) / rc)) / 2,
  * rc = rcov_i + rcov_j (bohr). Replaces DFTD4.coordination_numbers (d4.py:552-591;
@@ -450,6 +464,7 @@ size_t xnn_d4_workspace_bytes(int64_t n_nodes, int64_t n_graphs, int64_t max_ato
 int xnn_d4_coordination(const double* pos, int64_t n_nodes, const int32_t* species,
                         const int32_t* batch, const int64_t* node_ptr, int64_t n_graphs,
                         int64_t max_atoms, const double* cell, const int32_t* images,
+                        const int32_t* plan,
                         const double* rcov, const double* en, const xnn_d4_cn_params* prm,
                         double* cn_d4, double* cn_raw, void* workspace, size_t workspace_bytes,
                         xnn_stream_t stream);
@@ -459,6 +474,7 @@ int xnn_d4_coordination(const double* pos, int64_t n_nodes, const int32_t* speci
 int xnn_d4_coordination_backward(const double* pos, int64_t n_nodes, const int32_t* species,
                                  const int32_t* batch, const int64_t* node_ptr, int64_t n_graphs,
                                  int64_t max_atoms, const double* cell, const int32_t* images,
+                                 const int32_t* plan,
                                  const double* rcov, const double* en,
                                  const xnn_d4_cn_params* prm, const double* g_cn_d4,
                                  const double* g_cn_raw, double* grad_pos, double* cell_partial,
@@ -472,6 +488,7 @@ int xnn_d4_coordination_backward(const double* pos, int64_t n_nodes, const int32
 int xnn_d4_two_body(const double* pos, int64_t n_nodes, const int32_t* species,
                     const int32_t* batch, const int64_t* node_ptr, int64_t n_graphs,
                     int64_t max_atoms, const double* cell, const int32_t* images,
+                    const int32_t* plan,
                     const double* r4r2, const double* alpha, const xnn_d4_pair_params* prm,
                     double* e2, void* workspace, size_t workspace_bytes, xnn_stream_t stream);
 
@@ -482,6 +499,7 @@ int xnn_d4_two_body(const double* pos, int64_t n_nodes, const int32_t* species,
 int xnn_d4_two_body_backward(const double* pos, int64_t n_nodes, const int32_t* species,
                              const int32_t* batch, const int64_t* node_ptr, int64_t n_graphs,
                              int64_t max_atoms, const double* cell, const int32_t* images,
+                             const int32_t* plan,
                              const double* r4r2, const double* alpha,
                              const xnn_d4_pair_params* prm, const double* g_e2, double* grad_pos,
                              double* cell_partial, double* grad_alpha, void* workspace,

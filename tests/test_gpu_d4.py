@@ -134,6 +134,130 @@ def test_kernels_match_oracle(tables, case):
                                    atol=1e-10 * float(ref["grad_cell"].abs().max()))
 
 
+TILE_CASES = {
+    # n atoms, seed, box (A), cell, switch width (A)
+    "molecule_150": (150, 21, 13.0, None, 0.0),
+    "periodic_200": (200, 22, 12.0, np.diag([12.0, 12.5, 13.0]), 0.0),
+    "triclinic_170_switched": (170, 23, 11.0,
+                               np.array([[11.0, 0, 0], [1.2, 10.6, 0], [-0.7, 0.9, 11.4]]), 2.0),
+}
+
+
+def _tile_case_check(tables, pos, z, cell, width, seed):
+    import oracle.d4 as D
+    import xnn_amd.dispersion as XD
+    model = XD.DFTD4(tables, switch_width_pair=width, s9=0.0, **FAST).to(DEV)
+    q = torch.tensor(np.random.default_rng(seed).normal(0, 0.2, len(z)), dtype=torch.float64)
+    out, p, c = _eval(model, pos, z, cell, charges=q.to(DEV), grad=True)
+    gp, *gc = torch.autograd.grad(out["energy"].sum(), [p] + ([c] if c is not None else []))
+    ref = _oracle(tables, pos, z, cell, q, (FAST["cutoff_pair"], FAST["cutoff_cn"],
+                                            FAST["cutoff_eeq_cn"]), D.PBE0_D4, width)
+    np.testing.assert_allclose(out["coordination_numbers"].detach().cpu(), ref["cn"], rtol=1e-12,
+                               atol=1e-13)
+    e2 = out["node_energy"].detach().cpu() / XD.HARTREE
+    np.testing.assert_allclose(e2, ref["e2"], atol=1e-11 * float(ref["e2"].abs().max()))
+    np.testing.assert_allclose(gp.cpu() / XD.HARTREE, ref["grad_pos"],
+                               atol=1e-10 * float(ref["grad_pos"].abs().max()))
+    if cell is not None:
+        np.testing.assert_allclose(gc[0][0].cpu() / XD.HARTREE, ref["grad_cell"],
+                                   atol=1e-10 * float(ref["grad_cell"].abs().max()))
+    return out, gp
+
+
+@pytest.mark.parametrize("case", list(TILE_CASES))
+def test_tiles_match_oracle(tables, case):
+    """Structures of several 64-atom tiles, the last one partial: the kernels order the atoms
+    spatially and evaluate every unordered pair of two tiles once (both atoms' shares), the
+    pairs inside a tile directed. CN, per-atom two-body energies and the position and cell
+    gradients against the oracle's directed brute force over all atoms (float64)."""
+    n, seed, box, cell, width = TILE_CASES[case]
+    _note(f"d4 tiles vs oracle: {case}")
+    pos, z = _cluster(n, seed=seed, box=box)
+    _tile_case_check(tables, pos, z, cell, width, seed)
+
+
+def test_tiles_are_invariant_under_atom_permutation(tables):
+    """Renumbering the atoms renumbers the per-atom results and gradients (the tile order is
+    rebuilt from the positions; sums regroup, so to rounding)."""
+    import xnn_amd.dispersion as XD
+    _note("d4 tiles permutation invariance")
+    pos, z = _cluster(200, seed=24, box=12.0)
+    cell = np.diag([12.0, 12.5, 13.0])
+    model = XD.DFTD4(tables, s9=0.0, **FAST).to(DEV)
+    q = np.random.default_rng(3).normal(0, 0.2, len(z))
+    perm = np.random.default_rng(4).permutation(len(z))
+    res = []
+    for order in (np.arange(len(z)), perm):
+        out, p, c = _eval(model, pos[order], [z[k] for k in order], cell,
+                          charges=torch.tensor(q[order], device=DEV), grad=True)
+        gp, gc = torch.autograd.grad(out["energy"].sum(), [p, c])
+        inv = np.argsort(order)
+        res.append((out["node_energy"].detach().cpu().numpy()[inv], gp.cpu().numpy()[inv],
+                    gc.cpu().numpy()))
+    for a, b in zip(*res):
+        np.testing.assert_allclose(a, b, rtol=0, atol=1e-12 * float(np.abs(a).max()))
+
+
+def test_tiles_batch_of_mixed_sizes(tables):
+    """One call over a 150-atom periodic cell (3 tiles), a 9-atom and a 70-atom molecule
+    (1 and 2 tiles): per-atom CN, energies and gradients and each structure's cell gradient
+    against the oracle run per structure (pairs never cross structures)."""
+    import oracle.d4 as D
+    import xnn_amd.dispersion as XD
+    _note("d4 tiles batch of mixed sizes")
+    model = XD.DFTD4(tables, s9=0.0, **FAST).to(DEV)
+    pc, zc = _cluster(150, seed=25, box=11.0)
+    cell = np.array([[11.0, 0, 0], [0.5, 10.8, 0], [0.0, -0.6, 11.3]])
+    m1, z1 = _cluster(9, seed=26)
+    m2, z2 = _cluster(70, seed=27, box=9.0)
+    parts = [(pc, zc, cell), (m1, z1, None), (m2, z2, None)]
+    q = [np.random.default_rng(5 + k).normal(0, 0.2, len(zz)) for k, (_, zz, _) in enumerate(parts)]
+    pos = torch.tensor(np.concatenate([a for a, _, _ in parts]), device=DEV, requires_grad=True)
+    cells = torch.tensor(np.stack([cell, np.zeros((3, 3)), np.zeros((3, 3))]), device=DEV,
+                         requires_grad=True)
+    pbc = torch.tensor([[True] * 3, [False] * 3, [False] * 3])
+    z = zc + z1 + z2
+    out = model.evaluate(torch.tensor(z, device=DEV), pos, cells, pbc,
+                         torch.tensor([150, 9, 70]),
+                         charges=torch.tensor(np.concatenate(q), device=DEV))
+    gp, gc = torch.autograd.grad(out["energy"].sum(), [pos, cells])
+    off = 0
+    for k, (pp, zz, cc) in enumerate(parts):
+        sl = slice(off, off + len(zz))
+        off += len(zz)
+        ref = _oracle(tables, pp, zz, cc, torch.tensor(q[k]), (FAST["cutoff_pair"],
+                      FAST["cutoff_cn"], FAST["cutoff_eeq_cn"]), D.PBE0_D4)
+        np.testing.assert_allclose(out["coordination_numbers"].detach().cpu()[sl], ref["cn"],
+                                   rtol=1e-12, atol=1e-13)
+        np.testing.assert_allclose(out["node_energy"].detach().cpu()[sl] / XD.HARTREE, ref["e2"],
+                                   atol=1e-11 * float(ref["e2"].abs().max()))
+        np.testing.assert_allclose(gp.cpu()[sl] / XD.HARTREE, ref["grad_pos"],
+                                   atol=1e-10 * float(ref["grad_pos"].abs().max()))
+        if cc is not None:
+            np.testing.assert_allclose(gc[k].cpu() / XD.HARTREE, ref["grad_cell"],
+                                       atol=1e-10 * float(ref["grad_cell"].abs().max()))
+
+
+def test_tiles_structure_larger_than_max_atoms_gives_nan(tables):
+    """A structure with more atoms than the max_atoms the caller promised has more tiles
+    than result slots: the kernels leave it alone and its atoms come out NaN (no write
+    outside the workspace)."""
+    import xnn_amd.dispersion as XD
+    _note("d4 tiles max_atoms guard")
+    model = XD.DFTD4(tables, **FAST).to(DEV)
+    pos, z = _cluster(150, seed=28, box=13.0)
+    zc = torch.tensor(z, device=DEV)
+    uniq, species = torch.unique(zc, return_inverse=True)
+    n = len(z)
+    cn, raw = XD.d4_coordination_op(
+        torch.tensor(pos, device=DEV), None, species.to(torch.int32).contiguous(),
+        torch.zeros(n, dtype=torch.int32, device=DEV),
+        torch.tensor([0, n], dtype=torch.int64, device=DEV),
+        torch.zeros((1, 3), dtype=torch.int32, device=DEV), None, model.rcov[uniq].contiguous(),
+        model.en[uniq].contiguous(), [8.0 / XD.BOHR, 8.0 / XD.BOHR], 64)
+    assert bool(torch.isnan(cn).all()) and bool(torch.isnan(raw).all())
+
+
 def test_polarizabilities_kernel_matches_oracle(tables):
     """alpha(i w) and its chain rule to cn and q from the HIP kernel against the oracle's
     weights x charge scaling (float64 autograd): every tabulated element, CNs from 0 to

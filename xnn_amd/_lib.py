@@ -14,7 +14,7 @@ import torch
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIBRARY = os.path.join(HERE, "libxnn_amd.so")
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 XNN_OK, XNN_EINVAL, XNN_ECAPACITY, XNN_EHIP = 0, 1, 2, 3
 XNN_F32, XNN_F64 = 0, 1
@@ -141,11 +141,13 @@ _SIGNATURES = {
     "xnn_virial_reduce_workspace_bytes": [i64, i64],
     "xnn_virial_reduce": [c_int, vp, i64, vp, i64, vp, i32, vp, vp, sz, vp],
     "xnn_d4_workspace_bytes": [i64, i64, i64],
-    "xnn_d4_coordination": [vp, i64, vp, vp, vp, i64, i64, vp, vp, vp, vp,
+    "xnn_d4_plan_bytes": [i64, i64],
+    "xnn_d4_plan": [vp, i64, vp, i64, vp, vp, vp, sz, vp],
+    "xnn_d4_coordination": [vp, i64, vp, vp, vp, i64, i64, vp, vp, vp, vp, vp,
                             ctypes.POINTER(D4CnParams), vp, vp, vp, sz, vp],
-    "xnn_d4_coordination_backward": [vp, i64, vp, vp, vp, i64, i64, vp, vp, vp, vp,
+    "xnn_d4_coordination_backward": [vp, i64, vp, vp, vp, i64, i64, vp, vp, vp, vp, vp,
                                      ctypes.POINTER(D4CnParams), vp, vp, vp, vp, vp, sz, vp],
-    "xnn_d4_two_body": [vp, i64, vp, vp, vp, i64, i64, vp, vp, vp, vp,
+    "xnn_d4_two_body": [vp, i64, vp, vp, vp, i64, i64, vp, vp, vp, vp, vp,
                         ctypes.POINTER(D4PairParams), vp, vp, sz, vp],
     "xnn_d3_weights": [i64, vp, vp, i32, vp, vp, dbl, vp, vp],
     "xnn_d3_weights_backward": [i64, vp, vp, i32, vp, vp, dbl, vp, vp, vp],
@@ -162,7 +164,7 @@ _SIGNATURES = {
     "xnn_d4_polarizabilities": [i64, vp, vp, vp, ctypes.POINTER(D4AlphaTables), vp, vp],
     "xnn_d4_polarizabilities_backward": [i64, vp, vp, vp, ctypes.POINTER(D4AlphaTables), vp, vp,
                                          vp, vp],
-    "xnn_d4_two_body_backward": [vp, i64, vp, vp, vp, i64, i64, vp, vp, vp, vp,
+    "xnn_d4_two_body_backward": [vp, i64, vp, vp, vp, i64, i64, vp, vp, vp, vp, vp,
                                  ctypes.POINTER(D4PairParams), vp, vp, vp, vp, vp, sz, vp],
     "xnn_d3_coordination": [vp, i64, vp, vp, vp, i64, i64, vp, vp, vp, dbl, dbl, vp, vp, sz, vp],
     "xnn_d3_coordination_backward": [vp, i64, vp, vp, vp, i64, i64, vp, vp, vp, dbl, dbl, vp, vp,
@@ -198,6 +200,7 @@ _SIGNATURES = {
 _RESTYPES = {"xnn_last_error": ctypes.c_char_p, "xnn_scan_workspace_bytes": sz,
              "xnn_edge_plan_workspace_bytes": sz, "xnn_segment_reduce_workspace_bytes": sz,
              "xnn_d4_workspace_bytes": sz, "xnn_virial_reduce_workspace_bytes": sz,
+             "xnn_d4_plan_bytes": sz,
              "xnn_segment_reduce_noalloc_max_bytes": sz, "xnn_uvu_conv_workspace_bytes": sz,
              "xnn_sh_pair_workspace_bytes": sz}
 

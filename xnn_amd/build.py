@@ -18,7 +18,7 @@ CSRC = os.path.join(HERE, "csrc")
 INCLUDE = os.path.join(ROOT, "include")
 LIBRARY = os.path.join(HERE, "libxnn_amd.so")
 SOURCES = ("edge.hip", "segment.hip", "linear_message.hip", "graph.hip", "d4.hip", "readout.hip",
-           "atm.hip", "eeq.hip", "radial_mlp.hip", "uvu_conv.hip", "pair.hip")
+           "atm.hip", "eeq.hip", "radial_mlp.hip", "uvu_conv.hip", "pair.hip", "d4_tiles.hip")
 ARCH = os.environ.get("XNN_AMD_ARCH", "gfx950")
 
 # packed FP32 instructions stay off (the compiler must not form v_pk_* f32 ops)

@@ -489,7 +489,7 @@ using namespace xnn;
 extern "C" {
 
 const char* xnn_last_error(void) { return g_error; }
-int xnn_abi_version(void) { return 1; }
+int xnn_abi_version(void) { return 2; }
 
 int xnn_edge_featurize(int geom_dtype, int compute_dtype, const void* vec_in, const void* pos,
                        int64_t n_nodes, const void* cell, int64_t n_graphs, const int32_t* batch,

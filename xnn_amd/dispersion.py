@@ -127,12 +127,28 @@ def _cn_params(cut_cn: float, cut_eeq: float) -> "_lib.D4CnParams":
     return _lib.D4CnParams(cut_cn, cut_eeq, KCN, K4, K5, K6)
 
 
+def d4_plan(pos: Tensor, node_ptr: Tensor, cell: Optional[Tensor], images: Tensor) -> Tensor:
+    """The tile plan of the D4 pair kernels for these positions (Angstrom, float64) and
+    cells: each structure's atoms in the Morton order of a bin grid over their
+    (fractional, when periodic) coordinates, and the first tile of each structure, as
+    int32 device memory (``xnn_d4_plan``). Built once per evaluation and shared by the
+    coordination-number and two-body kernels and their backwards."""
+    dev = pos.device
+    n, b = pos.shape[0], node_ptr.shape[0] - 1
+    nbytes = int(_lib.load().xnn_d4_plan_bytes(n, b))
+    plan = torch.empty((nbytes + 3) // 4, dtype=torch.int32, device=dev)
+    _lib.call("xnn_d4_plan", _lib.ptr(pos), n, _lib.ptr(node_ptr), b, _lib.ptr(cell),
+              _lib.ptr(images), _lib.ptr(plan), nbytes, _lib.stream(dev))
+    return plan
+
+
 @torch.library.custom_op(f"{_NS}::d4_coordination", mutates_args=())
 def d4_coordination_op(pos: Tensor, cell: Optional[Tensor], species: Tensor, batch32: Tensor,
-                       node_ptr: Tensor, images: Tensor, rcov: Tensor, en: Tensor,
-                       cutoffs: List[float], max_atoms: int) -> Tuple[Tensor, Tensor]:
+                       node_ptr: Tensor, images: Tensor, plan: Optional[Tensor], rcov: Tensor,
+                       en: Tensor, cutoffs: List[float], max_atoms: int) -> Tuple[Tensor, Tensor]:
     """``(cn_d4, cn_raw)``: the EN-weighted erf-count CN within ``cutoffs[0]`` and the
-    plain erf count within ``cutoffs[1]`` (bohr), float64 (d4.py:552-588)."""
+    plain erf count within ``cutoffs[1]`` (bohr), float64 (d4.py:552-588). ``plan`` from
+    :func:`d4_plan` (None: built in the call)."""
     dev = pos.device
     n, b = pos.shape[0], node_ptr.shape[0] - 1
     cn = torch.empty(n, dtype=torch.float64, device=dev)
@@ -140,27 +156,28 @@ def d4_coordination_op(pos: Tensor, cell: Optional[Tensor], species: Tensor, bat
     ws, need = _workspace(n, b, max_atoms, dev)
     prm = _cn_params(cutoffs[0], cutoffs[1])
     _lib.call("xnn_d4_coordination", _lib.ptr(pos), n, _lib.ptr(species), _lib.ptr(batch32),
-              _lib.ptr(node_ptr), b, max_atoms, _lib.ptr(cell), _lib.ptr(images), _lib.ptr(rcov),
-              _lib.ptr(en), prm, _lib.ptr(cn), _lib.ptr(raw), _lib.ptr(ws), need, _lib.stream(dev))
+              _lib.ptr(node_ptr), b, max_atoms, _lib.ptr(cell), _lib.ptr(images), _lib.ptr(plan),
+              _lib.ptr(rcov), _lib.ptr(en), prm, _lib.ptr(cn), _lib.ptr(raw), _lib.ptr(ws), need,
+              _lib.stream(dev))
     return cn, raw
 
 
 @d4_coordination_op.register_fake
-def _(pos, cell, species, batch32, node_ptr, images, rcov, en, cutoffs, max_atoms):
+def _(pos, cell, species, batch32, node_ptr, images, plan, rcov, en, cutoffs, max_atoms):
     n = pos.shape[0]
     return pos.new_empty(n), pos.new_empty(n)
 
 
 def _cn_setup(ctx, inputs, output):
-    pos, cell, species, batch32, node_ptr, images, rcov, en, cutoffs, max_atoms = inputs
-    ctx.save_for_backward(pos, cell, species, batch32, node_ptr, images, rcov, en)
+    pos, cell, species, batch32, node_ptr, images, plan, rcov, en, cutoffs, max_atoms = inputs
+    ctx.save_for_backward(pos, cell, species, batch32, node_ptr, images, plan, rcov, en)
     ctx.cutoffs, ctx.max_atoms = list(cutoffs), max_atoms
 
 
 def _cn_backward(ctx, g_cn, g_raw):
     if torch.is_grad_enabled():
         raise RuntimeError("the D4 kernels are differentiable once (use_fast=False for more)")
-    pos, cell, species, batch32, node_ptr, images, rcov, en = ctx.saved_tensors
+    pos, cell, species, batch32, node_ptr, images, plan, rcov, en = ctx.saved_tensors
     dev, n, b = pos.device, pos.shape[0], node_ptr.shape[0] - 1
     grad_pos = torch.empty((n, 3), dtype=torch.float64, device=dev)
     want_cell = cell is not None and ctx.needs_input_grad[1]
@@ -170,11 +187,11 @@ def _cn_backward(ctx, g_cn, g_raw):
     g_raw = None if g_raw is None else g_raw.contiguous()
     _lib.call("xnn_d4_coordination_backward", _lib.ptr(pos), n, _lib.ptr(species),
               _lib.ptr(batch32), _lib.ptr(node_ptr), b, ctx.max_atoms, _lib.ptr(cell),
-              _lib.ptr(images), _lib.ptr(rcov), _lib.ptr(en),
+              _lib.ptr(images), _lib.ptr(plan), _lib.ptr(rcov), _lib.ptr(en),
               _cn_params(ctx.cutoffs[0], ctx.cutoffs[1]), _lib.ptr(g_cn), _lib.ptr(g_raw),
               _lib.ptr(grad_pos), _lib.ptr(part), _lib.ptr(ws), need, _lib.stream(dev))
     grad_cell = _cell_grad(part, node_ptr, b) if want_cell else None
-    return grad_pos, grad_cell, None, None, None, None, None, None, None, None
+    return grad_pos, grad_cell, None, None, None, None, None, None, None, None, None
 
 
 d4_coordination_op.register_autograd(_cn_backward, setup_context=_cn_setup)
@@ -188,36 +205,37 @@ def _cell_grad(part: Tensor, node_ptr: Tensor, n_graphs: int) -> Tensor:
 
 @torch.library.custom_op(f"{_NS}::d4_two_body", mutates_args=())
 def d4_two_body_op(pos: Tensor, cell: Optional[Tensor], alpha: Tensor, species: Tensor,
-                   batch32: Tensor, node_ptr: Tensor, images: Tensor, r4r2: Tensor,
-                   params: List[float], max_atoms: int) -> Tensor:
-    """Per-atom BJ-damped two-body energy (hartree) of every directed pair image within
-    ``params[4]`` bohr, ``params = [s6, s8, a1, a2, cutoff, width]`` (d4.py:1048-1071)."""
+                   batch32: Tensor, node_ptr: Tensor, images: Tensor, plan: Optional[Tensor],
+                   r4r2: Tensor, params: List[float], max_atoms: int) -> Tensor:
+    """Per-atom BJ-damped two-body energy (hartree): half of every pair image within
+    ``params[4]`` bohr to each of its atoms, ``params = [s6, s8, a1, a2, cutoff, width]``
+    (d4.py:1048-1071). ``plan`` from :func:`d4_plan` (None: built in the call)."""
     dev = pos.device
     n, b = pos.shape[0], node_ptr.shape[0] - 1
     e2 = torch.empty(n, dtype=torch.float64, device=dev)
     ws, need = _workspace(n, b, max_atoms, dev)
     _lib.call("xnn_d4_two_body", _lib.ptr(pos), n, _lib.ptr(species), _lib.ptr(batch32),
-              _lib.ptr(node_ptr), b, max_atoms, _lib.ptr(cell), _lib.ptr(images), _lib.ptr(r4r2),
-              _lib.ptr(alpha), _lib.D4PairParams(*params), _lib.ptr(e2), _lib.ptr(ws), need,
-              _lib.stream(dev))
+              _lib.ptr(node_ptr), b, max_atoms, _lib.ptr(cell), _lib.ptr(images), _lib.ptr(plan),
+              _lib.ptr(r4r2), _lib.ptr(alpha), _lib.D4PairParams(*params), _lib.ptr(e2),
+              _lib.ptr(ws), need, _lib.stream(dev))
     return e2
 
 
 @d4_two_body_op.register_fake
-def _(pos, cell, alpha, species, batch32, node_ptr, images, r4r2, params, max_atoms):
+def _(pos, cell, alpha, species, batch32, node_ptr, images, plan, r4r2, params, max_atoms):
     return pos.new_empty(pos.shape[0])
 
 
 def _pair_setup(ctx, inputs, output):
-    pos, cell, alpha, species, batch32, node_ptr, images, r4r2, params, max_atoms = inputs
-    ctx.save_for_backward(pos, cell, alpha, species, batch32, node_ptr, images, r4r2)
+    pos, cell, alpha, species, batch32, node_ptr, images, plan, r4r2, params, max_atoms = inputs
+    ctx.save_for_backward(pos, cell, alpha, species, batch32, node_ptr, images, plan, r4r2)
     ctx.params, ctx.max_atoms = list(params), max_atoms
 
 
 def _pair_backward(ctx, g_e2):
     if torch.is_grad_enabled():
         raise RuntimeError("the D4 kernels are differentiable once (use_fast=False for more)")
-    pos, cell, alpha, species, batch32, node_ptr, images, r4r2 = ctx.saved_tensors
+    pos, cell, alpha, species, batch32, node_ptr, images, plan, r4r2 = ctx.saved_tensors
     dev, n, b = pos.device, pos.shape[0], node_ptr.shape[0] - 1
     grad_pos = torch.empty((n, 3), dtype=torch.float64, device=dev)
     want_cell = cell is not None and ctx.needs_input_grad[1]
@@ -226,11 +244,11 @@ def _pair_backward(ctx, g_e2):
     ws, need = _workspace(n, b, ctx.max_atoms, dev)
     _lib.call("xnn_d4_two_body_backward", _lib.ptr(pos), n, _lib.ptr(species), _lib.ptr(batch32),
               _lib.ptr(node_ptr), b, ctx.max_atoms, _lib.ptr(cell), _lib.ptr(images),
-              _lib.ptr(r4r2), _lib.ptr(alpha), _lib.D4PairParams(*ctx.params),
+              _lib.ptr(plan), _lib.ptr(r4r2), _lib.ptr(alpha), _lib.D4PairParams(*ctx.params),
               _lib.ptr(g_e2.contiguous()), _lib.ptr(grad_pos), _lib.ptr(part),
               _lib.ptr(grad_alpha), _lib.ptr(ws), need, _lib.stream(dev))
     grad_cell = _cell_grad(part, node_ptr, b) if want_cell else None
-    return grad_pos, grad_cell, grad_alpha, None, None, None, None, None, None, None
+    return grad_pos, grad_cell, grad_alpha, None, None, None, None, None, None, None, None
 
 
 d4_two_body_op.register_autograd(_pair_backward, setup_context=_pair_setup)
@@ -444,19 +462,41 @@ def _ewald_rows(i0: int, i1: int, a: float, pos: Tensor, cell: Tensor, vol: Tens
 
 # --------------------------------------------------------------------------- host pieces
 def image_counts(cell: Tensor, pbc: Optional[Tensor], cutoff_aa: float) -> Tensor:
-    """Translations per axis that cover ``cutoff_aa`` from the interplanar spacing
-    (the image range of neighborlist.py:74-104), (B, 3) int32; 0 on non-periodic axes."""
-    c = cell.reshape(-1, 3, 3).detach().double().cpu()
-    rows = []
-    for bi in range(c.shape[0]):
-        if float(c[bi].abs().sum()) <= 1e-8:
-            rows.append([0, 0, 0])
-            continue
-        recip = torch.linalg.inv(c[bi]).T
-        spacing = 1.0 / torch.linalg.norm(recip, dim=1)
-        per = [True] * 3 if pbc is None else [bool(x) for x in pbc.reshape(-1, 3)[bi].cpu()]
-        rows.append([int(math.ceil(cutoff_aa / float(spacing[a]))) if per[a] else 0 for a in range(3)])
-    return torch.tensor(rows, dtype=torch.int32)
+    """Translations per axis that cover ``cutoff_aa``: ceil(cutoff / interplanar spacing),
+    the spacing of axis c being the cell volume over |a_(c+1) x a_(c+2)| (the image range
+    of neighborlist.py:74-104). (B, 3) int32 on the cell's device, computed there without a
+    host synchronization; 0 on non-periodic axes and for an all-zero cell."""
+    c = cell.detach().reshape(-1, 3, 3).to(torch.float64)
+    a0, a1, a2 = c[:, 0], c[:, 1], c[:, 2]
+    x = torch.stack([torch.cross(a1, a2, dim=-1), torch.cross(a2, a0, dim=-1),
+                     torch.cross(a0, a1, dim=-1)], dim=1)
+    vol = (a0 * x[:, 0]).sum(-1).abs()
+    norm = torch.linalg.norm(x, dim=-1)
+    live = (c.abs().sum((1, 2)) > 1e-8)[:, None] & (norm > 0)
+    if pbc is not None:
+        live = live & pbc.to(c.device).reshape(-1, 3).to(torch.bool)
+    spacing = vol[:, None] / torch.where(live, norm, torch.ones_like(norm))
+    n = torch.ceil(cutoff_aa / spacing)
+    n = torch.nan_to_num(n, nan=0.0, posinf=32767.0).clamp(0.0, 32767.0)
+    return torch.where(live, n, torch.zeros_like(n)).to(torch.int32)
+
+
+_LAYOUTS: Dict[Tuple, Tuple[Tensor, Tensor]] = {}
+
+
+def _batch_tensors(counts: List[int], dev) -> Tuple[Tensor, Tensor]:
+    """node_ptr (B+1) int64 and batch (N) int32 of structures of these sizes on ``dev``,
+    built once per layout (no host synchronization after the first call)."""
+    key = (tuple(counts), str(dev))
+    hit = _LAYOUTS.get(key)
+    if hit is None:
+        node_ptr = torch.tensor(np.concatenate([[0], np.cumsum(counts)]), dtype=torch.int64)
+        batch32 = torch.repeat_interleave(torch.arange(len(counts), dtype=torch.int32),
+                                          torch.tensor(counts, dtype=torch.int64))
+        if len(_LAYOUTS) >= 64:
+            _LAYOUTS.clear()
+        hit = _LAYOUTS[key] = (node_ptr.to(dev), batch32.to(dev))
+    return hit
 
 
 def _ewald_alpha(rlen: float, dlen: float, vol: float) -> float:
@@ -678,29 +718,25 @@ class DFTD4(nn.Module):
         pos = pos.to(torch.float64)
         n_atoms_h = [int(x) for x in n_atoms.cpu()]
         B = len(n_atoms_h)
-        node_ptr = torch.tensor(np.concatenate([[0], np.cumsum(n_atoms_h)]), dtype=torch.int64,
-                                device=dev)
-        batch32 = torch.repeat_interleave(torch.arange(B, dtype=torch.int32, device=dev),
-                                          torch.tensor(n_atoms_h, device=dev))
+        node_ptr, batch32 = _batch_tensors(n_atoms_h, dev)
         zc = z.to(dev).long()
-        uniq, species = torch.unique(zc, return_inverse=True)
-        species = species.to(torch.int32).contiguous()
-        periodic = []
+        # the pair tables are indexed by atomic number; a number outside them is clamped for
+        # the lookups and its polarizabilities, hence the energies, come out NaN
+        species = zc.clamp(0, self.r4r2.shape[0] - 1).to(torch.int32).contiguous()
         cell64 = None
         images = torch.zeros((B, 3), dtype=torch.int32, device=dev)
         if cell is not None:
-            cell64 = cell.reshape(-1, 3, 3).to(dev, torch.float64)
-            images = image_counts(cell64, pbc, self.cutoff).to(dev)
-            periodic = [bool(images[b].any()) for b in range(B)]
-        else:
-            periodic = [False] * B
+            cell64 = cell.reshape(-1, 3, 3).to(dev, torch.float64).contiguous()
+            images = image_counts(cell64, pbc, self.cutoff)
         max_atoms = max(n_atoms_h) if n_atoms_h else 1
+        pos = pos.contiguous()
+        plan = d4_plan(pos.detach(), node_ptr, None if cell64 is None else cell64.detach(), images)
         cut_cn, cut_eeq = self.cutoff_cn / BOHR, self.cutoff_eeq_cn / BOHR
-        cn, raw = d4_coordination_op(pos.contiguous(), None if cell64 is None else cell64.contiguous(),
-                                     species, batch32, node_ptr, images,
-                                     self.rcov[uniq].contiguous(), self.en[uniq].contiguous(),
-                                     [cut_cn, cut_eeq], max_atoms)
+        cn, raw = d4_coordination_op(pos, cell64, species, batch32, node_ptr, images, plan,
+                                     self.rcov, self.en, [cut_cn, cut_eeq], max_atoms)
+        periodic = None  # host flags per structure, read only where needed (a synchronization)
         if charges is None:
+            periodic = [bool(x) for x in (images != 0).any(1).cpu()]
             cn_eeq = math.log(1.0 + math.exp(EEQ_CN_MAX)) - torch.log(1.0 + torch.exp(EEQ_CN_MAX - raw))
             qs = []
             for b in range(B):
@@ -714,15 +750,16 @@ class DFTD4(nn.Module):
         alpha = self.polarizabilities(zc, cn, q).contiguous()
         params = [self.s6, self.s8, self.a1, self.a2, self.cutoff_pair / BOHR,
                   self.switch_width_pair / BOHR]
-        e2 = d4_two_body_op(pos.contiguous(), None if cell64 is None else cell64.contiguous(), alpha,
-                            species, batch32, node_ptr, images, self.r4r2[uniq].contiguous(),
-                            params, max_atoms)
+        e2 = d4_two_body_op(pos, cell64, alpha, species, batch32, node_ptr, images, plan,
+                            self.r4r2, params, max_atoms)
         from .ops import structure_sum_op
         e3 = torch.zeros_like(e2)
         if self.s9 != 0.0:
-            e3 = self.three_body(zc, pos, cell64, pbc, n_atoms_h, cn, species, uniq)
+            e3 = self.three_body(zc, pos, cell64, pbc, n_atoms_h, cn)
         e_tail = torch.zeros_like(e2)
         if self.tail_correction and cell64 is not None:
+            if periodic is None:
+                periodic = [bool(x) for x in (images != 0).any(1).cpu()]
             parts = []
             for b in range(B):
                 s0, s1 = sum(n_atoms_h[:b]), sum(n_atoms_h[:b + 1])
@@ -788,11 +825,13 @@ class DFTD4(nn.Module):
         return (6.0 / vol) * (alpha * cp_weights(alpha) * field.index_select(0, z)).sum(-1)
 
     def three_body(self, z: Tensor, pos: Tensor, cell64: Optional[Tensor], pbc: Optional[Tensor],
-                   counts: List[int], cn: Tensor, species: Tensor, uniq: Tensor) -> Tensor:
+                   counts: List[int], cn: Tensor) -> Tensor:
         """Per-atom ATM energies (hartree, d4.py:1268-1298): C6 from the polarizabilities
         of the neutral atoms (q = 0), damping radii ``a1 sqrt(3 Q_A Q_B) + a2``, exponent
         ``alp / 3``, edges of the radius graph within ``cutoff_triple``; the HIP
-        triplet kernels (:func:`atm_energy`)."""
+        triplet kernels (:func:`atm_energy`), over the species present."""
+        uniq, species = torch.unique(z, return_inverse=True)
+        species = species.to(torch.int32).contiguous()
         alpha0 = self.polarizabilities(z, cn, torch.zeros_like(cn))
         feat = alpha0 * torch.sqrt((3.0 / math.pi) * cp_weights(alpha0))
         edge_index, vec = triple_graph(pos, cell64, pbc, counts, self.cutoff_triple)
@@ -1067,9 +1106,7 @@ d3_two_body_op.register_autograd(_d3pair_backward, setup_context=_d3pair_setup)
 
 def _batch_layout(n_atoms: Tensor, dev) -> Tuple[List[int], Tensor, Tensor]:
     counts = [int(x) for x in n_atoms.cpu()]
-    node_ptr = torch.tensor(np.concatenate([[0], np.cumsum(counts)]), dtype=torch.int64, device=dev)
-    batch32 = torch.repeat_interleave(torch.arange(len(counts), dtype=torch.int32, device=dev),
-                                      torch.tensor(counts, device=dev))
+    node_ptr, batch32 = _batch_tensors(counts, dev)
     return counts, node_ptr, batch32
 
 
