@@ -412,13 +412,22 @@ def cpu_baseline_d4(s, tables, alpha: np.ndarray, model, k: int = 200,
 # counts are the survey's 60 M + 46 P and 40 M_cn; the pair backward adds per term the
 # r-derivative of the damped sum and the force and cell-gradient products (35) and per
 # pair the two atoms' d C6 / d alpha (2 x 46): 95 M + 138 P
-D4_FLOPS = {"xnn_d4_two_body": lambda M, P, Mc: 60 * M + 46 * P,
-            "xnn_d4_two_body_backward": lambda M, P, Mc: 95 * M + 138 * P,
-            "xnn_d4_coordination": lambda M, P, Mc: 40 * Mc}
+# Algorithmic float64 flops of each entry point, counted on the unordered sums (each pair
+# image enters the energy once, for both of its atoms): M directed pair-image terms within the
+# cutoff are M / 2 unordered ones, P = N (N + 1) / 2 atom pairs, Mc directed CN terms.
+# Per pair-image term, the energy: the image vector and r^2 (8), r^4 r^6 r^8 (3), the two
+# BJ denominators and their common Newton-refined reciprocal (12), t6 t8 and g (5), the sum (1)
+# = 29; the backward adds df/dr / r (10) and its vector, force and cell-moment sums (18) = 57.
+# Per atom pair: C6 (46) and the damping radius, r0^6 r0^8, the pair's energy to both atoms
+# (16) = 62 forward; the backward's C6, forces to both atoms, the cell moment (51) and dE/d
+# alpha of both atoms (2 x 46 + 3) = 170. CN: 40 per unordered term.
+D4_FLOPS = {"xnn_d4_two_body": lambda M, P, Mc: 29 * M // 2 + 62 * P,
+            "xnn_d4_two_body_backward": lambda M, P, Mc: 57 * M // 2 + 170 * P,
+            "xnn_d4_coordination": lambda M, P, Mc: 40 * Mc // 2}
 FP64_PEAK_TFLOPS = 78.6
 
 
-def bench_d4(steps: int, warmup: int, cpu: bool = True) -> dict:
+def bench_d4(steps: int, warmup: int, cpu: bool = True, graph: bool = True) -> dict:
     """D4 two-body energy + forces + stress of the 5,000-atom organic box (36.8 A cell,
     cutoffs 60 / 25 / 25 bohr for pair / CN / EEQ CN): CN kernel, polarizabilities, pair kernel and
     both backward kernels per step. The charges come from the EEQ solve once, outside the
@@ -463,8 +472,42 @@ def bench_d4(steps: int, warmup: int, cpu: bool = True) -> dict:
     for _ in range(steps):
         out, gp, gc = step()
     torch.cuda.synchronize()
-    ms = (time.perf_counter() - t0) / steps * 1e3
+    eager_ms = ms = (time.perf_counter() - t0) / steps * 1e3
     e = out["energy"].detach()
+    graph_checked = None
+    if graph:
+        # the whole step (evaluation, forces and cell gradient) as one HIP graph, replayed;
+        # an MD driver copies new positions into pos0 / cell0 before each replay
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            for _ in range(3):
+                step()
+        torch.cuda.current_stream().wait_stream(side)
+        hip_graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(hip_graph):
+            s_out, s_gp, s_gc = step()
+        for _ in range(max(1, warmup)):
+            hip_graph.replay()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            hip_graph.replay()
+        torch.cuda.synchronize()
+        ms = (time.perf_counter() - t0) / steps * 1e3
+        # several replays, eager work between them, each against the eager step bit for bit
+        r_out, r_gp, r_gc = step()
+        graph_checked = True
+        for _ in range(3):
+            hip_graph.replay()
+            torch.cuda.synchronize()
+            graph_checked = graph_checked and bool(
+                torch.equal(s_gp, r_gp) and torch.equal(s_gc, r_gc)
+                and torch.equal(s_out["energy"], r_out["energy"]))
+            step()
+            torch.cuda.synchronize()
+        if not graph_checked:
+            raise SystemExit("graph replay differs from the eager D4 step")
     # per-kernel HIP events (launch stream) over a second set of steps
     kernels = list(D4_FLOPS) + ["xnn_d4_coordination_backward", "xnn_d4_polarizabilities",
                                 "xnn_d4_polarizabilities_backward"]
@@ -512,6 +555,9 @@ def bench_d4(steps: int, warmup: int, cpu: bool = True) -> dict:
                          "charges": "EEQ charges (large regime: HIP real-space Ewald matrix, "
                                     "device Cholesky), computed outside the timed steps",
                          "eeq_regime": model.select_regime(N, True),
+                         "timing": ("HIP graph replay of the step" if graph else "eager step"),
+                         "eager_ms_per_step": round(eager_ms, 4),
+                         "graph_replay_matches_eager": graph_checked,
                          "energy_with_eeq_ms": round(eeq_ms, 2),
                          "charge_abs_max": float(q.abs().max()),
                          "energy_eV": float(e[0]),
@@ -807,7 +853,8 @@ def main() -> None:
         copy_calibration()
         return
     if args.config == "d4":
-        print(json.dumps(bench_d4(args.steps, args.warmup, cpu=args.cpu_edges > 0)), flush=True)
+        print(json.dumps(bench_d4(args.steps, args.warmup, cpu=args.cpu_edges > 0,
+                                  graph=args.graph)), flush=True)
         return
     if args.config == "d3":
         print(json.dumps(bench_d3(args.steps, args.warmup, cpu=args.cpu_edges > 0)), flush=True)

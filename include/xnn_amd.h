@@ -452,6 +452,13 @@ size_t xnn_d4_workspace_bytes(int64_t n_nodes, int64_t n_graphs, int64_t max_ato
  * kernel needs no ordering): plan = xnn_d4_plan_bytes(n_nodes, n_graphs) bytes of
  * device memory, the Morton order of each structure's atoms over a bin grid of their
  * (fractional, when periodic) coordinates and the first tile of each structure. */
+/* images[b][c] = ceil(cutoff / interplanar spacing of axis c) of each structure's cell
+ * (B,3,3 Angstrom rows, device), the translations that cover cutoff (Angstrom); 0 where
+ * pbc[b][c] == 0 (pbc (B,3) uint8 or NULL: all periodic) or the cell is zero or degenerate;
+ * at most 32767. Replaces the image range of neighborlist.py:74-104 for the D4 kernels. */
+int xnn_d4_image_counts(const double* cell, const uint8_t* pbc, int64_t n_graphs, double cutoff,
+                        int32_t* images, xnn_stream_t stream);
+
 size_t xnn_d4_plan_bytes(int64_t n_nodes, int64_t n_graphs);
 int xnn_d4_plan(const double* pos, int64_t n_nodes, const int64_t* node_ptr, int64_t n_graphs,
                 const double* cell, const int32_t* images, int32_t* plan, size_t plan_bytes,

@@ -141,6 +141,7 @@ _SIGNATURES = {
     "xnn_virial_reduce_workspace_bytes": [i64, i64],
     "xnn_virial_reduce": [c_int, vp, i64, vp, i64, vp, i32, vp, vp, sz, vp],
     "xnn_d4_workspace_bytes": [i64, i64, i64],
+    "xnn_d4_image_counts": [vp, vp, i64, dbl, vp, vp],
     "xnn_d4_plan_bytes": [i64, i64],
     "xnn_d4_plan": [vp, i64, vp, i64, vp, vp, vp, sz, vp],
     "xnn_d4_coordination": [vp, i64, vp, vp, vp, i64, i64, vp, vp, vp, vp, vp,

@@ -23,8 +23,8 @@
 //    the receiver's in its lane's registers, the source's summed over the 64 lanes by a
 //    reduce-scatter tree in registers over groups of 8 lanes and the 8 group sums added
 //    through LDS every 8 sources. The backward keeps each pair's sum over images of f(r)
-//    for a second kernel that forms dE/d alpha of both atoms (small products staged
-//    through LDS).
+//    in its workspace block and ends with dE/d alpha of both atoms from them (small
+//    products staged through LDS).
 //  * d = 0: the directed pairs inside one tile, self images included, receiver side only.
 // Per-atom partial sums go to slot (the other tile) of a (slots x components x atoms)
 // array in tile order; every slot of an atom is written exactly once, and a reduce sums
@@ -440,24 +440,32 @@ __device__ __forceinline__ bool lane_finish8(double* __restrict__ buf, const dou
 // ---------------------------------------------------------------- two-body term
 
 struct PairStage {
-  double x[kT], y[kT], z[kT];  // bohr
-  double p[kT], q[kT], w[kT];  // r4r2, its square root, the upstream gradient g_e2
-  double sa[kT][kNW + 1];      // alpha(i w) times the quadrature weight c_cp3(w)
+  double w[kT];                // the sources' upstream gradient g_e2
+  double sa[kT][kNW + 1];      // alpha(i w) times the quadrature weight c_cp3(w): of the
+                               // sources, then (the backward's dE/d alpha step) the receivers
   int win[3][kT];              // packed image windows
-  double red[8 * 8 * 3];       // lane_finish8
+  union {
+    struct {
+      double x[kT], y[kT], z[kT];  // bohr
+      double p[kT], q[kT];         // r4r2, its square root
+      double red[8 * 8 * 3];       // lane_finish8
+    } s;
+    double kbuf[kFlush * kT];      // dE/dC6 of 8 sources (the dE/d alpha step)
+  } u;
 };
 
 // BACKWARD = false: partial[slot][0][p] = the atom's sum of -1/2 C6 f(r).
-// BACKWARD = true:  partial[slot][0..2][p] = grad_pos, [3..11] the cell gradient (CELL), and
-//                   fsum[jj][lane] = the pair's sum over images of f(r), the block of
-//                   d4_pair_alpha_tiles_kernel (dE/d alpha from dE/d C6 = -1/2 (g_i + g_j) fsum).
+// BACKWARD = true:  partial[slot][0..2][p] = grad_pos, [3..11] the cell gradient (CELL),
+//                   partial_alpha[slot][w][p] = dE/d alpha(i w); fsum_out[jj][lane] (this
+//                   wave's 64 x 64 block of workspace) holds the pairs' sums over images of f(r).
 template <bool BACKWARD, bool CELL, bool DIAG>
 __device__ __forceinline__ void pair_tile(
     PairStage& st, const TileItem& it, const TileGeo& G, const PairParams& prm,
     const double* __restrict__ pos, const int32_t* __restrict__ species,
     const double* __restrict__ r4r2, const double* __restrict__ alpha,
     const double* __restrict__ g_e2, const int32_t* __restrict__ order, int64_t n_nodes,
-    double* __restrict__ partial, double* __restrict__ fsum_out) {
+    double* __restrict__ partial, double* __restrict__ fsum_out,
+    double* __restrict__ partial_alpha) {
   constexpr int NV = BACKWARD ? 3 : 1;
   constexpr int NP = BACKWARD ? (CELL ? 12 : 3) : 1;
   const int lane = threadIdx.x;
@@ -476,12 +484,12 @@ __device__ __forceinline__ void pair_tile(
   if (lane < it.scnt) {
     const int j = order[it.s0 + lane];
     const double xs = pos[3 * (int64_t)j], ys = pos[3 * (int64_t)j + 1], zs = pos[3 * (int64_t)j + 2];
-    st.x[lane] = xs * kInvBohr;
-    st.y[lane] = ys * kInvBohr;
-    st.z[lane] = zs * kInvBohr;
+    st.u.s.x[lane] = xs * kInvBohr;
+    st.u.s.y[lane] = ys * kInvBohr;
+    st.u.s.z[lane] = zs * kInvBohr;
     const double pj = r4r2[species[j]];
-    st.p[lane] = pj;
-    st.q[lane] = sqrt(pj);
+    st.u.s.p[lane] = pj;
+    st.u.s.q[lane] = sqrt(pj);
     if (BACKWARD) st.w[lane] = g_e2[j];
 #pragma unroll
     for (int w = 0; w < kNW; ++w) st.sa[lane][w] = alpha[(int64_t)kNW * j + w] * c_cp3[w];
@@ -523,12 +531,12 @@ __device__ __forceinline__ void pair_tile(
       for (int w = 0; w < kNW; ++w) c6p[w & 3] += ai[w] * st.sa[jj][w];
       const double c6 = (c6p[0] + c6p[1]) + (c6p[2] + c6p[3]);
       // rr = 3 r4r2_i r4r2_j and R0 = a1 sqrt(rr) + a2, sqrt(rr) = sqrt(3 r4r2_i) sqrt(r4r2_j)
-      const double rr = 3.0 * qi * st.p[jj];
+      const double rr = 3.0 * qi * st.u.s.p[jj];
       const double s8rr = prm.s8 * rr;
-      const double r0 = prm.a1 * (sq3qi * st.q[jj]) + prm.a2;
+      const double r0 = prm.a1 * (sq3qi * st.u.s.q[jj]) + prm.a2;
       const double r02 = r0 * r0;
       const double r06 = r02 * r02 * r02, r08 = r06 * r02;
-      const double dx = xb - st.x[jj], dy = yb - st.y[jj], dz = zb - st.z[jj];
+      const double dx = xb - st.u.s.x[jj], dy = yb - st.u.s.y[jj], dz = zb - st.u.s.z[jj];
       // E = sum_i g_i e_i: the pair's energy enters with (g_i + g_j) (-1/2 C6 f); the
       // vector's gradient per Angstrom carries d r_bohr / d v = v_bohr / (r_bohr bohr)
       const double wsum = BACKWARD ? gi + st.w[jj] : 0.0;
@@ -615,7 +623,7 @@ __device__ __forceinline__ void pair_tile(
       double total;
       const int js = jj - 7 + (lane & 7);
       double* po = partial + (int64_t)it.lt * NP * n_nodes + it.s0 + js;
-      if (lane_finish8(st.red, vs, lane, total) && js < it.scnt)
+      if (lane_finish8(st.u.s.red, vs, lane, total) && js < it.scnt)
         po[(int64_t)(lane >> 3) * n_nodes] = total;
       if (BACKWARD && CELL && lane < 8 && js < it.scnt) {
 #pragma unroll
@@ -643,6 +651,58 @@ __device__ __forceinline__ void pair_tile(
       }
     }
   }
+  if (BACKWARD) {
+    // dE/d alpha(i w) of both atoms of every pair: dE/d C6_ij = -1/2 (g_i + g_j) fsum_ij
+    // (the pair sums this wave wrote, still in cache) and d C6_ij / d alpha_i(w) =
+    // cp3(w) alpha_j(w). The receivers' side in their lanes, against the sources' table.
+    double da[kNW];
+#pragma unroll
+    for (int w = 0; w < kNW; ++w) da[w] = 0.0;
+    for (int jj = 0; jj < it.scnt; ++jj) {
+      const double kk = -0.5 * (gi + st.w[jj]) * fsum_out[jj * kT + lane];
+#pragma unroll
+      for (int w = 0; w < kNW; ++w) da[w] += kk * st.sa[jj][w];
+    }
+    if (live) {
+      double* pa = partial_alpha + (int64_t)it.ls * kNW * n_nodes + pi;
+#pragma unroll
+      for (int w = 0; w < kNW; ++w) pa[(int64_t)w * n_nodes] = da[w];
+    }
+    if (!DIAG) {
+      // the sources' side: the receivers' table replaces the sources', and 8 sources at a
+      // time their dE/dC6 (skewed columns: conflict-free reads) meet lane = (source jl,
+      // frequency group wg), which sums over the receivers for w = wg, wg + 8, wg + 16
+      __syncthreads();
+#pragma unroll
+      for (int w = 0; w < kNW; ++w) st.sa[lane][w] = live ? ai[w] * c_cp3[w] : 0.0;
+      st.sa[lane][kNW] = 0.0;
+      const int jl = lane & (kFlush - 1), wg = lane / kFlush;
+      for (int j0 = 0; j0 < it.scnt; j0 += kFlush) {
+        __syncthreads();
+#pragma unroll
+        for (int q = 0; q < kFlush; ++q) {
+          const int jj = j0 + q;
+          const double kk = jj < it.scnt ? -0.5 * (gi + st.w[jj]) * fsum_out[jj * kT + lane] : 0.0;
+          st.u.kbuf[q * kT + ((lane + q) & (kT - 1))] = kk;
+        }
+        __syncthreads();
+        double o0 = 0.0, o1 = 0.0, o2 = 0.0;
+        for (int r = 0; r < it.rcnt; ++r) {
+          const double kv = st.u.kbuf[jl * kT + ((r + jl) & (kT - 1))];
+          o0 += kv * st.sa[r][wg];
+          o1 += kv * st.sa[r][wg + kFlush];
+          o2 += kv * st.sa[r][wg + 2 * kFlush];  // group 7 reads the zero padding
+        }
+        const int js = j0 + jl;
+        if (js < it.scnt) {
+          double* pa = partial_alpha + (int64_t)it.lt * kNW * n_nodes + it.s0 + js;
+          pa[(int64_t)wg * n_nodes] = o0;
+          pa[(int64_t)(wg + kFlush) * n_nodes] = o1;
+          if (wg + 2 * kFlush < kNW) pa[(int64_t)(wg + 2 * kFlush) * n_nodes] = o2;
+        }
+      }
+    }
+  }
 }
 
 // (64, 2): at most 256 registers, two waves per SIMD (20 KB of LDS: 8 waves per CU)
@@ -653,7 +713,8 @@ __global__ __launch_bounds__(kT, 2) void d4_pair_tiles_kernel(
     const int32_t* __restrict__ images, const double* __restrict__ r4r2,
     const double* __restrict__ alpha, PairParams prm, const double* __restrict__ g_e2,
     const int32_t* __restrict__ order, const int32_t* __restrict__ tile_ptr, int64_t n_nodes,
-    int max_nt, double* __restrict__ partial, double* __restrict__ fsum) {
+    int max_nt, double* __restrict__ partial, double* __restrict__ fsum,
+    double* __restrict__ partial_alpha) {
   __shared__ PairStage st;
   TileItem it;
   if (!tile_item(tile_ptr, node_ptr, n_graphs, n_nodes, max_nt, it)) return;
@@ -662,84 +723,13 @@ __global__ __launch_bounds__(kT, 2) void d4_pair_tiles_kernel(
   double* fb = BACKWARD ? fsum + ((int64_t)blockIdx.x * max_nt + blockIdx.y) * (kT * kT) : nullptr;
   if (it.ls == it.lt)
     pair_tile<BACKWARD, CELL, true>(st, it, G, prm, pos, species, r4r2, alpha, g_e2, order,
-                                    n_nodes, partial, fb);
+                                    n_nodes, partial, fb, partial_alpha);
   else
     pair_tile<BACKWARD, CELL, false>(st, it, G, prm, pos, species, r4r2, alpha, g_e2, order,
-                                     n_nodes, partial, fb);
+                                     n_nodes, partial, fb, partial_alpha);
 }
 
-// dE/d alpha(i w) of the two-body term from the pair sums fsum of the backward kernel (the
-// same work items): for the pair (i, j), dE/d C6 = -1/2 (g_i + g_j) fsum_ij and
-// d C6 / d alpha_i(w) = cp3(w) alpha_j(w). The receiver's sum runs over the sources in its
-// lane; the sources' (tiles t + d, d > 0) over the receivers, staged 8 sources at a time
-// through LDS, lane = (source, frequency group). partial_alpha[slot][w][p].
-__global__ __launch_bounds__(kT) void d4_pair_alpha_tiles_kernel(
-    const double* __restrict__ alpha, const double* __restrict__ g_e2,
-    const int64_t* __restrict__ node_ptr, int64_t n_graphs, const int32_t* __restrict__ order,
-    const int32_t* __restrict__ tile_ptr, int64_t n_nodes, int max_nt,
-    const double* __restrict__ fsum, double* __restrict__ partial_alpha) {
-  __shared__ double sr[kT][kNW + 1], ss[kT][kNW + 1];  // alpha(i w) cp3(w): receivers, sources
-  __shared__ double gr[kT], gs[kT];
-  __shared__ double kbuf[kFlush * kT];
-  TileItem it;
-  if (!tile_item(tile_ptr, node_ptr, n_graphs, n_nodes, max_nt, it)) return;
-  const bool diag = it.ls == it.lt;
-  const int lane = threadIdx.x;
-  const bool live = lane < it.rcnt;
-  {
-    const int i = order[it.r0 + (live ? lane : 0)];
-    gr[lane] = live ? g_e2[i] : 0.0;
-#pragma unroll
-    for (int w = 0; w < kNW; ++w) sr[lane][w] = alpha[(int64_t)kNW * i + w] * c_cp3[w];
-    sr[lane][kNW] = 0.0;
-    const bool src = lane < it.scnt;
-    const int j = order[it.s0 + (src ? lane : 0)];
-    gs[lane] = src ? g_e2[j] : 0.0;
-#pragma unroll
-    for (int w = 0; w < kNW; ++w) ss[lane][w] = alpha[(int64_t)kNW * j + w] * c_cp3[w];
-    ss[lane][kNW] = 0.0;
-  }
-  __syncthreads();
-  const double* fb = fsum + ((int64_t)blockIdx.x * max_nt + blockIdx.y) * (kT * kT);
-  double da[kNW];
-#pragma unroll
-  for (int w = 0; w < kNW; ++w) da[w] = 0.0;
-  const double gi = gr[lane];
-  for (int j0 = 0; j0 < kT; j0 += kFlush) {
-#pragma unroll 2
-    for (int jl = 0; jl < kFlush; ++jl) {
-      const int jj = j0 + jl;
-      const double kk = -0.5 * (gi + gs[jj]) * fb[jj * kT + lane];  // zero past the tiles
-#pragma unroll
-      for (int w = 0; w < kNW; ++w) da[w] += kk * ss[jj][w];
-      if (!diag) kbuf[jl * kT + ((lane + jl) & (kT - 1))] = kk;  // skewed: conflict-free reads
-    }
-    if (!diag) {
-      __syncthreads();
-      const int jl = lane & (kFlush - 1), wg = lane / kFlush;
-      double o0 = 0.0, o1 = 0.0, o2 = 0.0;
-      for (int r = 0; r < it.rcnt; ++r) {
-        const double kv = kbuf[jl * kT + ((r + jl) & (kT - 1))];
-        o0 += kv * sr[r][wg];
-        o1 += kv * sr[r][wg + kFlush];
-        o2 += kv * sr[r][wg + 2 * kFlush];  // group 7 reads the zero padding
-      }
-      __syncthreads();
-      const int js = j0 + jl;
-      if (js < it.scnt) {
-        double* pa = partial_alpha + (int64_t)it.lt * kNW * n_nodes + it.s0 + js;
-        pa[(int64_t)wg * n_nodes] = o0;
-        pa[(int64_t)(wg + kFlush) * n_nodes] = o1;
-        if (wg + 2 * kFlush < kNW) pa[(int64_t)(wg + 2 * kFlush) * n_nodes] = o2;
-      }
-    }
-  }
-  if (live) {
-    double* pa = partial_alpha + (int64_t)it.ls * kNW * n_nodes + it.r0 + lane;
-#pragma unroll
-    for (int w = 0; w < kNW; ++w) pa[(int64_t)w * n_nodes] = da[w];
-  }
-}
+
 
 // ---------------------------------------------------------------- coordination numbers
 
@@ -953,6 +943,40 @@ __global__ __launch_bounds__(kT, 2) void d4_cn_tiles_kernel(
   else
     cn_tile<BACKWARD, CELL, false>(st, it, G, prm, pos, species, rcov, en, g_cn, g_raw, order,
                                    n_nodes, partial);
+}
+
+// ---------------------------------------------------------------- image counts
+
+// images[b][c] = ceil(cutoff / spacing_c) for periodic axes, the interplanar spacing of axis
+// c being the cell volume over |a_(c+1) x a_(c+2)| (the image range of
+// neighborlist.py:74-104); 0 on non-periodic axes (pbc[b][c] == 0; pbc NULL: all periodic)
+// and for an all-zero or degenerate cell; at most 32767. One thread per structure.
+__global__ void d4_image_counts_kernel(const double* __restrict__ cell,
+                                       const uint8_t* __restrict__ pbc, int64_t n_graphs,
+                                       double cutoff, int32_t* __restrict__ images) {
+  const int64_t b = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (b >= n_graphs) return;
+  const double* a = cell + 9 * b;
+  double x[3][3];  // x[c] = a_(c+1) x a_(c+2)
+#pragma unroll
+  for (int c = 0; c < 3; ++c) {
+    const double* u = a + 3 * ((c + 1) % 3);
+    const double* v = a + 3 * ((c + 2) % 3);
+    x[c][0] = u[1] * v[2] - u[2] * v[1];
+    x[c][1] = u[2] * v[0] - u[0] * v[2];
+    x[c][2] = u[0] * v[1] - u[1] * v[0];
+  }
+  const double vol = fabs(a[0] * x[0][0] + a[1] * x[0][1] + a[2] * x[0][2]);
+  double total = 0.0;
+#pragma unroll
+  for (int k = 0; k < 9; ++k) total += fabs(a[k]);
+#pragma unroll
+  for (int c = 0; c < 3; ++c) {
+    const double norm = sqrt(x[c][0] * x[c][0] + x[c][1] * x[c][1] + x[c][2] * x[c][2]);
+    const bool live = total > 1e-8 && vol > 0.0 && norm > 0.0 && (pbc == nullptr || pbc[3 * b + c]);
+    const double n = live ? ceil(cutoff * norm / vol) : 0.0;
+    images[3 * b + c] = (int32_t)fmin(fmax(n, 0.0), 32767.0);
+  }
 }
 
 // ---------------------------------------------------------------- slot reduction
@@ -1185,7 +1209,7 @@ int xnn_d4_two_body(const double* pos, int64_t n_nodes, const int32_t* species,
   launch_order(pos, n_nodes, node_ptr, n_graphs, cell, images, plan, w, s);
   hipLaunchKernelGGL((d4_pair_tiles_kernel<false, false>), tiles_grid(w), dim3(kT), 0, s, pos,
                      species, node_ptr, n_graphs, cell, images, r4r2, alpha, p, nullptr, w.order,
-                     w.tile_ptr, n_nodes, w.max_nt, w.partial, nullptr);
+                     w.tile_ptr, n_nodes, w.max_nt, w.partial, nullptr, nullptr);
   launch_reduce(w.partial, n_nodes, 1, 0, 1, w, batch, node_ptr, e2, s);
   XNN_LAUNCH_CHECK();
   return XNN_OK;
@@ -1219,13 +1243,22 @@ int xnn_d4_two_body_backward(const double* pos, int64_t n_nodes, const int32_t* 
   auto k = with_cell ? d4_pair_tiles_kernel<true, true> : d4_pair_tiles_kernel<true, false>;
   hipLaunchKernelGGL(k, tiles_grid(w), dim3(kT), 0, s, pos, species, node_ptr, n_graphs, cell,
                      images, r4r2, alpha, p, g_e2, w.order, w.tile_ptr, n_nodes, w.max_nt,
-                     w.partial, w.fsum);
-  hipLaunchKernelGGL(d4_pair_alpha_tiles_kernel, tiles_grid(w), dim3(kT), 0, s, alpha, g_e2,
-                     node_ptr, n_graphs, w.order, w.tile_ptr, n_nodes, w.max_nt, w.fsum,
-                     w.partial_alpha);
+                     w.partial, w.fsum, w.partial_alpha);
   launch_reduce(w.partial, n_nodes, np, 0, 3, w, batch, node_ptr, grad_pos, s);
   if (with_cell) launch_reduce(w.partial, n_nodes, np, 3, 9, w, batch, node_ptr, cell_partial, s);
   launch_reduce(w.partial_alpha, n_nodes, kNW, 0, kNW, w, batch, node_ptr, grad_alpha, s);
+  XNN_LAUNCH_CHECK();
+  return XNN_OK;
+}
+
+int xnn_d4_image_counts(const double* cell, const uint8_t* pbc, int64_t n_graphs, double cutoff,
+                        int32_t* images, xnn_stream_t stream) {
+  XNN_REQUIRE(n_graphs >= 0, "negative size");
+  XNN_REQUIRE(cutoff >= 0.0, "negative cutoff");
+  if (n_graphs == 0) return XNN_OK;
+  XNN_REQUIRE(cell && images, "NULL cell or images");
+  hipLaunchKernelGGL(d4_image_counts_kernel, dim3((unsigned)((n_graphs + 255) / 256)), dim3(256),
+                     0, as_hip(stream), cell, pbc, n_graphs, cutoff, images);
   XNN_LAUNCH_CHECK();
   return XNN_OK;
 }
