@@ -205,3 +205,23 @@ def test_atm_triangle_closed_forms(tables, shape):
     table, species = D.bj_radius_factors(z, tables, D.PBE0_D4["a1"], D.PBE0_D4["a2"])
     e = D.atm_edges(ei, vec, feat, feat, species, table, 1.0, 16.0 / 3.0, 100.0, 0.0, 3)
     np.testing.assert_allclose(e.numpy(), want / 3.0, rtol=1e-13)
+
+
+def test_cn_count_vanishes_exactly_past_its_reach(tables):
+    """The D4 coordination kernels skip pairs farther than rc (1 + 27.5 / kcn): there the erf
+    count (d4.py:168-170) is exactly 0.0 in float64 and so is its derivative (exp(-x^2)
+    underflows for x <= -27.5), so leaving them out changes no sum. Checked with the oracle's
+    own count and autograd over every element pair of the tables, at and beyond the reach,
+    and just inside it (where the derivative must still be nonzero)."""
+    rcov = torch.as_tensor(tables["rcov"], dtype=torch.float64)
+    live = rcov[rcov > 0]
+    rc = (live[:, None] + live[None, :]).reshape(-1)
+    reach = rc * (1.0 + 27.5 / D.KCN)
+    for scale in (1.0, 1.0001, 1.5, 3.0):
+        r = (reach * scale).clone().requires_grad_(True)
+        c = D.erf_count(r, rc)
+        (g,) = torch.autograd.grad(c.sum(), [r])
+        assert bool((c == 0.0).all()) and bool((g == 0.0).all()), scale
+    r = (rc * (1.0 + 26.0 / D.KCN)).clone().requires_grad_(True)
+    (g,) = torch.autograd.grad(D.erf_count(r, rc).sum(), [r])
+    assert bool((g != 0.0).all())

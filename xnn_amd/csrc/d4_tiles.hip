@@ -291,6 +291,7 @@ __device__ inline bool tile_item(const int32_t* __restrict__ tile_ptr,
 // fractional units for cutoff rc (Angstrom), image counts
 struct TileGeo {
   double ab[9], inv[9], wf[3];
+  double isp[3];  // 1 / interplanar spacing per axis (Angstrom^-1)
   int nmax[3];
   bool periodic;
 };
@@ -319,7 +320,10 @@ __device__ inline void tile_geo(const double* __restrict__ cell,
   G.nmax[2] = L.n2;
   G.periodic = (L.n0 | L.n1 | L.n2) != 0;
 #pragma unroll
-  for (int c = 0; c < 3; ++c) G.wf[c] = wave_uniform(rc / L.sp[c] + 1e-9);
+  for (int c = 0; c < 3; ++c) {
+    G.wf[c] = wave_uniform(rc / L.sp[c] + 1e-9);
+    G.isp[c] = wave_uniform(1.0 / L.sp[c]);
+  }
 }
 
 __device__ inline double wave_min(double v) {
@@ -367,12 +371,15 @@ __device__ inline int tile_window(int nmax, double fj, double flo, double fhi, d
   return pack_window(lo, hi);
 }
 
+// rc_aa > 0: a cutoff of this source's own (Angstrom) in place of the structure's
 __device__ inline void source_windows(const TileGeo& G, double x, double y, double z,
-                                      const double* flo, const double* fhi, int* w) {
+                                      const double* flo, const double* fhi, int* w,
+                                      double rc_aa = 0.0) {
 #pragma unroll
   for (int c = 0; c < 3; ++c) {
     const double f = G.periodic ? x * G.inv[c] + y * G.inv[3 + c] + z * G.inv[6 + c] : 0.0;
-    w[c] = tile_window(G.nmax[c], f, flo[c], fhi[c], G.wf[c]);
+    const double half = rc_aa > 0.0 ? rc_aa * G.isp[c] + 1e-9 : G.wf[c];
+    w[c] = tile_window(G.nmax[c], f, flo[c], fhi[c], half);
   }
 }
 
@@ -764,6 +771,14 @@ __device__ __forceinline__ void cn_tile(
   const double g2i = BACKWARD && g_raw ? g_raw[i] : 0.0;
   double flo[3], fhi[3];
   tile_bounds(G, xa, ya, za, live, flo, fhi);
+  const double cmax = prm.cut_cn > prm.cut_eeq ? prm.cut_cn : prm.cut_eeq;
+  const double cmax2 = cmax * cmax;
+  // Beyond r = rc (1 + 27.5 / kcn) the erf argument is below -27.5: the count rounds to exactly
+  // zero and so does its slope, -kcn / (rc sqrt(pi)) exp(-x^2) (exp(-756) underflows). Such
+  // pairs are skipped: each source's window reaches only as far as its largest rc with the
+  // tile's receivers allows, and each pair as far as its own rc allows.
+  const double zfac = 1.0 + 27.5 / prm.kcn;
+  const double rc_tile = wave_max(live ? rci : 0.0);
   if (lane < it.scnt) {
     const int j = order[it.s0 + lane];
     const double xs = pos[3 * (int64_t)j], ys = pos[3 * (int64_t)j + 1], zs = pos[3 * (int64_t)j + 2];
@@ -777,8 +792,9 @@ __device__ __forceinline__ void cn_tile(
       st.w[lane] = g_cn ? g_cn[j] : 0.0;
       st.w2[lane] = g_raw ? g_raw[j] : 0.0;
     }
+    const double r_src = fmin(cmax, (rc_tile + rcov[sj]) * zfac);
     int win[3];
-    source_windows(G, xs, ys, zs, flo, fhi, win);
+    source_windows(G, xs, ys, zs, flo, fhi, win, r_src * kBohr);
 #pragma unroll
     for (int c = 0; c < 3; ++c) st.win[c][lane] = win[c];
   } else {
@@ -788,8 +804,6 @@ __device__ __forceinline__ void cn_tile(
   }
   __syncthreads();
 
-  const double cmax = prm.cut_cn > prm.cut_eeq ? prm.cut_cn : prm.cut_eeq;
-  const double cmax2 = cmax * cmax;
   const double inv_k6 = 1.0 / prm.k6;
   double acc[2] = {0.0, 0.0}, g3[3] = {0.0, 0.0, 0.0}, cacc[9];
 #pragma unroll
@@ -814,6 +828,7 @@ __device__ __forceinline__ void cn_tile(
       const double dx = xb - st.x[jj], dy = yb - st.y[jj], dz = zb - st.z[jj];
       const double wsum = BACKWARD ? gi + st.w[jj] : 0.0;
       const double w2sum = BACKWARD ? g2i + st.w2[jj] : 0.0;
+      const double reach2 = fmin(cmax2, rc * zfac * (rc * zfac));
       double c_cn = 0.0, c_eeq = 0.0;          // counts within the two cutoffs
       double sv[3] = {0.0, 0.0, 0.0};          // sum of the weighted gradients
       double sc[3] = {0.0, 0.0, 0.0};          // the same with the cell's weights (own tile)
@@ -826,7 +841,7 @@ __device__ __forceinline__ void cn_tile(
           for (int n2 = lo2; n2 <= hi2; ++n2) {
             const double vx = px + n2 * G.ab[6], vy = py + n2 * G.ab[7], vz = pz + n2 * G.ab[8];
             const double r2 = vx * vx + vy * vy + vz * vz;
-            const bool in = live && r2 > 0.0 && r2 <= cmax2;
+            const bool in = live && r2 > 0.0 && r2 <= reach2;
             if (!__any(in)) continue;
             // every lane evaluates the term and the ones outside the cutoffs discard it
             const double rinv = rsq_nr(fmax(r2, 1e-300));
