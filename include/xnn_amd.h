@@ -112,6 +112,23 @@ int xnn_edge_force_reduce(int geom_dtype, int compute_dtype, const void* g_edge,
                           void* grad_pos, double* cell_partial, const void* vec,
                           double* virial_partial, xnn_stream_t stream);
 
+/* xnn_edge_force_reduce for ONE structure with its strain derivative: grad_pos as above,
+ * and virial (3,3) of virial_dtype (XNN_F32 / XNN_F64) = sym(sum_e r_e (x) g_e), the value
+ * of xnn_edge_force_reduce's virial_partial followed by xnn_virial_reduce(symmetrize = 1) to
+ * float64 rounding (another fixed summation order; repeated calls give the same bits). Two
+ * launches: the reduction writes one 3x3 sum per block to the workspace, and a one-block
+ * kernel adds them in block order. No atomics. Workspace:
+ * xnn_edge_force_reduce_virial_workspace_bytes (0 for an empty structure). Replaces the same
+ * _EdgeVectors.backward (atomic_data.py:452-467) plus the per-structure strain sum of
+ * ForceStressOutput (outputs.py:166-216) when the batch holds one structure. */
+size_t xnn_edge_force_reduce_virial_workspace_bytes(int64_t n_edges, int64_t n_nodes);
+int xnn_edge_force_reduce_virial(int geom_dtype, int compute_dtype, const void* g_edge,
+                                 int64_t n_edges, const int32_t* ptr_dst, const int32_t* perm_dst,
+                                 const int32_t* ptr_src, const int32_t* perm_src,
+                                 const int32_t* visit, int64_t n_nodes, void* grad_pos,
+                                 const void* vec, int virial_dtype, void* virial,
+                                 void* workspace, size_t workspace_bytes, xnn_stream_t stream);
+
 /* The strain deformation of ForceStressOutput (outputs.py:166-180): with
  * S_b = (strain_b + strain_b^T) / 2 (strain (B,3,3), geometry dtype),
  * pos_out[i] = pos[i] (I + S_batch[i]) and cell_out[b] = cell[b] (I + S_b) (cell nullable).

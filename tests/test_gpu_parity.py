@@ -554,6 +554,58 @@ def test_force_reduce_visit_order_keeps_every_sum():
             assert torch.equal(a, b)
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float64])
+def test_force_reduce_with_virial_finish_matches_the_two_step_path(dtype):
+    """xnn_edge_force_reduce_virial (one structure; block sums of the strain derivative
+    added by one finishing block) gives the forces of xnn_edge_force_reduce bit for bit and
+    the virial of its per-atom partials + xnn_virial_reduce to float64 rounding; repeated
+    calls give the same bits; an empty structure gives a zero virial."""
+    import xnn_amd as xa
+    from xnn_amd import _lib, synthetic
+    _note(f"force reduce + virial finish {dtype}")
+    s = synthetic.water_box(n_molecules=216, box=18.6, grid=6, seed=3)
+    g = xa.structure_to_graph(s.as_dict(), 5.0, device=DEV)
+    g.pos, g.cell = g.pos.to(dtype), g.cell.to(dtype)
+    plan = g.plan()
+    vec = g.edge_vectors().detach().contiguous()
+    ge = torch.randn(vec.shape, generator=torch.Generator().manual_seed(7),
+                     dtype=torch.float64).to(DEV, dtype)
+    E, N, code = vec.shape[0], g.num_nodes, _lib.dtype_code(dtype)
+    gp = torch.empty((N, 3), dtype=dtype, device=DEV)
+    vp = torch.empty((N, 9), dtype=torch.float64, device=DEV)
+    _lib.call("xnn_edge_force_reduce", code, code, _lib.ptr(ge), E, _lib.ptr(plan.ptr_dst),
+              _lib.ptr(plan.perm_dst), _lib.ptr(plan.ptr_src), _lib.ptr(plan.perm_src), None,
+              _lib.ptr(plan.visit), N, _lib.ptr(gp), None, _lib.ptr(vec), _lib.ptr(vp),
+              _lib.stream(vec.device))
+    node_ptr = torch.tensor([0, N], dtype=torch.int64, device=DEV)
+    want = _lib.virial_reduce(vp, N, node_ptr, 1, None, True, torch.float64)
+
+    def fused(n_edges, n_nodes, vdt):
+        need = int(_lib.load().xnn_edge_force_reduce_virial_workspace_bytes(n_edges, n_nodes))
+        ws = torch.full((max(need, 1),), 255, dtype=torch.uint8, device=DEV)
+        out_pos = torch.full((max(n_nodes, 1), 3), float("nan"), dtype=dtype, device=DEV)
+        vir = torch.full((1, 3, 3), float("nan"), dtype=vdt, device=DEV)
+        _lib.call("xnn_edge_force_reduce_virial", code, code, _lib.ptr(ge), n_edges,
+                  _lib.ptr(plan.ptr_dst), _lib.ptr(plan.perm_dst), _lib.ptr(plan.ptr_src),
+                  _lib.ptr(plan.perm_src), _lib.ptr(plan.visit), n_nodes, _lib.ptr(out_pos),
+                  _lib.ptr(vec), _lib.dtype_code(vdt), _lib.ptr(vir), _lib.ptr(ws), need,
+                  _lib.stream(vec.device))
+        return out_pos, vir
+
+    p1, v1 = fused(E, N, torch.float64)
+    assert torch.equal(p1, gp)
+    scale = float(vp.abs().sum(0).max())
+    np.testing.assert_allclose(v1.cpu(), want.cpu(), rtol=0, atol=1e-13 * scale)
+    np.testing.assert_allclose(v1.cpu(), v1.cpu().transpose(1, 2), rtol=0, atol=0)
+    for _ in range(3):
+        p2, v2 = fused(E, N, torch.float64)
+        assert torch.equal(p2, p1) and torch.equal(v2, v1)
+    p3, v3 = fused(E, N, torch.float32)
+    assert torch.equal(p3, gp) and torch.equal(v3, v1.float())
+    _, v0 = fused(0, 0, torch.float64)
+    assert torch.equal(v0.cpu(), torch.zeros(1, 3, 3, dtype=torch.float64))
+
+
 def test_segment_gather_and_structure_sums():
     import oracle.reference as R
     import xnn_amd as xa
@@ -815,11 +867,15 @@ def test_model_energy_forces_stress(config, fused):
     out = xa.ForceStressOutput(model, compute_stress=g.cell is not None).eval()(g)
     msg = {"radial": "xnn_sh_radial_message_energy", "radial_rows": "xnn_sh_radial_message_sum",
            "linear": "xnn_sh_linear_message_sum", "unfused": "xnn_sh_message_sum"}[fused]
-    ran = [msg, msg + "_backward", "xnn_edge_force_reduce", "xnn_edge_featurize"]
+    ran = [msg, msg + "_backward", "xnn_edge_featurize"]
     if fused not in ("radial", "radial_rows"):
         ran.append("xnn_edge_featurize_backward")
     for name in ran:
         assert _lib.calls.get(name, 0) > before.get(name, 0), f"{name} did not run"
+    # one structure: the force reduction finishes the strain derivative in the same launch
+    reduce_names = ("xnn_edge_force_reduce", "xnn_edge_force_reduce_virial")
+    assert (sum(_lib.calls.get(n, 0) for n in reduce_names)
+            > sum(before.get(n, 0) for n in reduce_names)), "the force reduction did not run"
     params = dict(W=model.W.detach().cpu().double(), U=model.U.detach().cpu().double(),
                   atom_ref=model.atom_ref.detach().cpu().double(), l_max=kw["l_max"],
                   n_rbf=kw["n_rbf"], cutoff=rc, radial=kw["radial_type"],

@@ -166,7 +166,7 @@ __global__ __launch_bounds__(256) void force_reduce_kernel(
     const int32_t* __restrict__ perm_src, const int32_t* __restrict__ shift,
     const int32_t* __restrict__ visit, int64_t n_nodes, G* __restrict__ grad_pos,
     double* __restrict__ cell_partial, const T* __restrict__ vec,
-    double* __restrict__ virial_partial) {
+    double* __restrict__ virial_partial, double* __restrict__ virial_block) {
   const int lane = threadIdx.x % GROUP;
   const int64_t per_xcd = ((int64_t)gridDim.x + kXcds - 1) / kXcds;
   const int64_t sb = (int64_t)(blockIdx.x % kXcds) * per_xcd + blockIdx.x / kXcds;
@@ -174,7 +174,7 @@ __global__ __launch_bounds__(256) void force_reduce_kernel(
   const bool live = slot < n_nodes;
   const int64_t i = live ? (visit ? (int64_t)visit[slot] : slot) : 0;
   const bool want_cell = cell_partial != nullptr;
-  const bool want_vir = virial_partial != nullptr;
+  const bool want_vir = virial_partial != nullptr || virial_block != nullptr;
   double fx = 0, fy = 0, fz = 0;
   double c[9] = {0, 0, 0, 0, 0, 0, 0, 0, 0};
   double v[9] = {0, 0, 0, 0, 0, 0, 0, 0, 0};
@@ -236,6 +236,55 @@ __global__ __launch_bounds__(256) void force_reduce_kernel(
 #pragma unroll
       for (int q = 0; q < 9; ++q) virial_partial[9 * i + q] = v[q];
     }
+  }
+  if (virial_block != nullptr) {
+    // the block's atoms' r (x) g summed in group order (one structure)
+    __shared__ double gsum[256 / GROUP][9];
+    if (lane == 0) {
+#pragma unroll
+      for (int q = 0; q < 9; ++q) gsum[threadIdx.x / GROUP][q] = live ? v[q] : 0.0;
+    }
+    __syncthreads();
+    if (threadIdx.x < 9) {
+      double a = 0.0;
+      for (int g = 0; g < 256 / GROUP; ++g) a += gsum[g][threadIdx.x];
+      virial_block[9 * (int64_t)blockIdx.x + threadIdx.x] = a;
+    }
+  }
+}
+
+// One block: out (3,3) = sym(sum_b block[b]) with the rows taken in a fixed order (thread t
+// sums rows t, t + 256, ...; then each wave's butterfly and the 4 wave sums in order).
+template <typename OUT>
+__global__ __launch_bounds__(256) void virial_blocks_finish_kernel(const double* __restrict__ block,
+                                                                   int64_t n_blocks,
+                                                                   OUT* __restrict__ out) {
+  double a[9] = {0, 0, 0, 0, 0, 0, 0, 0, 0};
+  for (int64_t b = threadIdx.x; b < n_blocks; b += 256) {
+#pragma unroll
+    for (int q = 0; q < 9; ++q) a[q] += block[9 * b + q];
+  }
+#pragma unroll
+  for (int q = 0; q < 9; ++q) {
+#pragma unroll
+    for (int m = kWave / 2; m > 0; m >>= 1) a[q] += __shfl_xor(a[q], m, kWave);
+  }
+  __shared__ double wsum[256 / kWave][9];
+  __shared__ double tot[9];
+  if (threadIdx.x % kWave == 0) {
+#pragma unroll
+    for (int q = 0; q < 9; ++q) wsum[threadIdx.x / kWave][q] = a[q];
+  }
+  __syncthreads();
+  if (threadIdx.x < 9) {
+    double t = 0.0;
+    for (int w = 0; w < 256 / kWave; ++w) t += wsum[w][threadIdx.x];
+    tot[threadIdx.x] = t;
+  }
+  __syncthreads();
+  if (threadIdx.x < 9) {
+    const int r = threadIdx.x / 3, c = threadIdx.x % 3;
+    out[threadIdx.x] = (OUT)(0.5 * (tot[threadIdx.x] + tot[3 * c + r]));
   }
 }
 
@@ -440,10 +489,11 @@ static void launch_force_reduce(int64_t n_blocks, const void* g_edge, const int3
                                 const int32_t* perm_src, const int32_t* shift,
                                 const int32_t* visit, int64_t n_nodes, void* grad_pos,
                                 double* cell_partial, const void* vec, double* virial_partial,
-                                hipStream_t stream) {
+                                double* virial_block, hipStream_t stream) {
   hipLaunchKernelGGL((force_reduce_kernel<G, T, GROUP>), dim3((unsigned)n_blocks), dim3(256), 0,
                      stream, (const T*)g_edge, ptr_dst, perm_dst, ptr_src, perm_src, shift, visit,
-                     n_nodes, (G*)grad_pos, cell_partial, (const T*)vec, virial_partial);
+                     n_nodes, (G*)grad_pos, cell_partial, (const T*)vec, virial_partial,
+                     virial_block);
 }
 
 template <typename G, typename T>
@@ -451,21 +501,24 @@ static int force_reduce(const void* g_edge, int64_t n_edges, const int32_t* ptr_
                         const int32_t* perm_dst, const int32_t* ptr_src,
                         const int32_t* perm_src, const int32_t* shift, const int32_t* visit,
                         int64_t n_nodes, void* grad_pos, double* cell_partial, const void* vec,
-                        double* virial_partial, hipStream_t stream) {
+                        double* virial_partial, double* virial_block, hipStream_t stream) {
   if (n_nodes == 0) return XNN_OK;
   const int64_t nb = force_blocks(n_edges, n_nodes);
   switch (force_group(n_edges, n_nodes)) {
     case 32:
       launch_force_reduce<G, T, 32>(nb, g_edge, ptr_dst, perm_dst, ptr_src, perm_src, shift, visit,
-                                    n_nodes, grad_pos, cell_partial, vec, virial_partial, stream);
+                                    n_nodes, grad_pos, cell_partial, vec, virial_partial, virial_block,
+                                    stream);
       break;
     case 16:
       launch_force_reduce<G, T, 16>(nb, g_edge, ptr_dst, perm_dst, ptr_src, perm_src, shift, visit,
-                                    n_nodes, grad_pos, cell_partial, vec, virial_partial, stream);
+                                    n_nodes, grad_pos, cell_partial, vec, virial_partial, virial_block,
+                                    stream);
       break;
     default:
       launch_force_reduce<G, T, 4>(nb, g_edge, ptr_dst, perm_dst, ptr_src, perm_src, shift, visit,
-                                   n_nodes, grad_pos, cell_partial, vec, virial_partial, stream);
+                                   n_nodes, grad_pos, cell_partial, vec, virial_partial, virial_block,
+                                   stream);
   }
   XNN_LAUNCH_CHECK();
   return XNN_OK;
@@ -537,7 +590,59 @@ int xnn_edge_force_reduce(int geom_dtype, int compute_dtype, const void* g_edge,
               "virial_partial needs the edge vectors");
   XNN_DISPATCH_GT(geom_dtype, compute_dtype, force_reduce, g_edge, n_edges, ptr_dst, perm_dst,
                   ptr_src, perm_src, shift, visit, n_nodes, grad_pos, cell_partial, vec,
-                  virial_partial, as_hip(stream));
+                  virial_partial, nullptr, as_hip(stream));
+}
+
+size_t xnn_edge_force_reduce_virial_workspace_bytes(int64_t n_edges, int64_t n_nodes) {
+  if (n_edges < 0 || n_nodes <= 0) return 0;
+  return sizeof(double) * 9 * (size_t)force_blocks(n_edges, n_nodes);
+}
+
+int xnn_edge_force_reduce_virial(int geom_dtype, int compute_dtype, const void* g_edge,
+                                 int64_t n_edges, const int32_t* ptr_dst, const int32_t* perm_dst,
+                                 const int32_t* ptr_src, const int32_t* perm_src,
+                                 const int32_t* visit, int64_t n_nodes, void* grad_pos,
+                                 const void* vec, int virial_dtype, void* virial,
+                                 void* workspace, size_t workspace_bytes, xnn_stream_t stream) {
+  XNN_REQUIRE(n_edges >= 0 && n_nodes >= 0, "negative size");
+  XNN_REQUIRE(virial != nullptr, "NULL virial");
+  XNN_REQUIRE(virial_dtype == XNN_F32 || virial_dtype == XNN_F64,
+              "virial dtype must be XNN_F32 or XNN_F64");
+  XNN_REQUIRE(n_nodes == 0 || (ptr_dst && ptr_src && grad_pos), "NULL CSR or output");
+  XNN_REQUIRE(n_edges == 0 || (g_edge && vec), "NULL g_edge or edge vectors");
+  const size_t need = xnn_edge_force_reduce_virial_workspace_bytes(n_edges, n_nodes);
+  XNN_REQUIRE(need == 0 || (workspace != nullptr && workspace_bytes >= need),
+              "workspace of %zu bytes needed", need);
+  double* block = static_cast<double*>(workspace);
+  const int64_t nb = n_nodes > 0 ? force_blocks(n_edges, n_nodes) : 0;
+  hipStream_t st = as_hip(stream);
+  if (n_nodes > 0) {
+    int rc = XNN_OK;
+    if (geom_dtype == XNN_F32 && compute_dtype == XNN_F32)
+      rc = force_reduce<float, float>(g_edge, n_edges, ptr_dst, perm_dst, ptr_src, perm_src,
+                                      nullptr, visit, n_nodes, grad_pos, nullptr, vec, nullptr,
+                                      block, st);
+    else if (geom_dtype == XNN_F64 && compute_dtype == XNN_F64)
+      rc = force_reduce<double, double>(g_edge, n_edges, ptr_dst, perm_dst, ptr_src, perm_src,
+                                        nullptr, visit, n_nodes, grad_pos, nullptr, vec, nullptr,
+                                        block, st);
+    else if (geom_dtype == XNN_F64 && compute_dtype == XNN_F32)
+      rc = force_reduce<double, float>(g_edge, n_edges, ptr_dst, perm_dst, ptr_src, perm_src,
+                                       nullptr, visit, n_nodes, grad_pos, nullptr, vec, nullptr,
+                                       block, st);
+    else
+      XNN_REQUIRE(false, "unsupported dtype pair geometry=%d compute=%d", geom_dtype,
+                  compute_dtype);
+    if (rc != XNN_OK) return rc;
+  }
+  if (virial_dtype == XNN_F64)
+    hipLaunchKernelGGL(virial_blocks_finish_kernel<double>, dim3(1), dim3(256), 0, st, block, nb,
+                       static_cast<double*>(virial));
+  else
+    hipLaunchKernelGGL(virial_blocks_finish_kernel<float>, dim3(1), dim3(256), 0, st, block, nb,
+                       static_cast<float*>(virial));
+  XNN_LAUNCH_CHECK();
+  return XNN_OK;
 }
 
 int xnn_strain_apply(int geom_dtype, const void* pos, int64_t n_nodes, const int32_t* batch,

@@ -269,6 +269,19 @@ def _probe_backward(ctx, grad):
     gdt = torch.float32 if ctx.geom_code == _lib.XNN_F32 else torch.float64
     want_cell = bool(ctx.has_cell and ctx.needs_input_grad[2])
     grad_pos = torch.empty((n_nodes, 3), dtype=gdt, device=dev)
+    if n_graphs == 1 and not want_cell:
+        # one structure: block sums of the strain derivative, added by one finishing block
+        grad_probe = torch.empty((1, 3, 3), dtype=ctx.probe_dtype, device=dev)
+        need = int(_lib.load().xnn_edge_force_reduce_virial_workspace_bytes(grad.shape[0],
+                                                                            n_nodes))
+        ws = torch.empty(max(need, 1), dtype=torch.uint8, device=dev)
+        _lib.call("xnn_edge_force_reduce_virial", ctx.geom_code, _lib.dtype_code(grad.dtype),
+                  _lib.ptr(grad), grad.shape[0], _lib.ptr(ptr_dst), _lib.ptr(perm_dst),
+                  _lib.ptr(ptr_src), _lib.ptr(perm_src), _lib.ptr(visit), n_nodes,
+                  _lib.ptr(grad_pos), _lib.ptr(vec), _lib.dtype_code(ctx.probe_dtype),
+                  _lib.ptr(grad_probe), _lib.ptr(ws), need, _lib.stream(dev))
+        return (grad_pos if ctx.needs_input_grad[0] else None, grad_probe, None,
+                None, None, None, None, None, None, None, None, None, None, None)
     cell_partial = torch.empty((n_nodes, 9), dtype=torch.float64, device=dev) if want_cell else None
     virial_partial = torch.empty((n_nodes, 9), dtype=torch.float64, device=dev)
     _lib.call("xnn_edge_force_reduce", ctx.geom_code, _lib.dtype_code(grad.dtype), _lib.ptr(grad),
