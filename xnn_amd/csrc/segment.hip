@@ -672,6 +672,7 @@ __global__ __launch_bounds__(256) void segment_finish_kernel(const double* __res
 // of S), with coalesced loads; an LDS tree over the P threads of each feature then
 // gives the chunk's partial sums (fixed order: deterministic).
 constexpr int kFlatMaxF = 64;
+static_assert(kFlatMaxF <= kWave, "wave 0 holds the flat results");
 constexpr int kFlatPerThread = 4;
 // a single block of 1024 threads takes arrays up to this many elements (no second kernel)
 constexpr int64_t kFlatSingleMax = 16384;
@@ -710,11 +711,19 @@ __global__ __launch_bounds__(BLOCK) void flat_reduce_f64_kernel(const T* __restr
   }
   red[t] = (a0 + a1) + (a2 + a3);
   __syncthreads();
-  for (int h = S / (int)F / 2; h > 0; h >>= 1) {
+  // pairwise tree, red[t] += red[t + h F]: steps that read beyond one wave through LDS, the
+  // rest by shuffles inside wave 0 (the same pairs in the same order, without a barrier per
+  // step; F <= kFlatMaxF = kWave, so wave 0 holds every result)
+  int h = S / (int)F / 2;
+  for (; h > 0 && 2 * h * (int)F > kWave; h >>= 1) {
     if (t < h * F) red[t] += red[t + h * F];
     __syncthreads();
   }
-  if (t < F) partial[(int64_t)blockIdx.x * F + t] = red[t];
+  if (t < kWave) {
+    double x = red[t];
+    for (; h > 0; h >>= 1) x += __shfl_down(x, h * (int)F, kWave);
+    if (t < F) partial[(int64_t)blockIdx.x * F + t] = x;
+  }
 }
 
 // Totals of the 9 virial components over `chunks` partial rows (as segment_finish_kernel),
