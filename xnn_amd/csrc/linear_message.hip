@@ -365,6 +365,9 @@ __global__ __launch_bounds__(256, 3) void lin_msg_bwd_kernel(
   // every tile is full, and each edge's gradient is scaled by its receiver's g_i at the
   // end (everything before is linear in it). Otherwise a wave takes one receiver row.
   const int64_t n_slots = RO ? (int64_t)ptr[n_nodes] : 0;
+  // the lanes' receivers are needed for their cotangents (one per atom) and, without given
+  // edge vectors, for the edge geometry; a broadcast cotangent with given vectors needs none
+  const bool need_row = g_stride != 0 || vec == nullptr;
   const int64_t n_items = RO ? (n_slots + kWave - 1) / kWave : n_nodes;
   for (int64_t item = (int64_t)blockIdx.x * kWavesPerBlock + wave; item < n_items;
        item += n_waves) {
@@ -373,16 +376,19 @@ __global__ __launch_bounds__(256, 3) void lin_msg_bwd_kernel(
     if constexpr (RO) {
       b0 = (int)(item * kWave);
       b1 = (int)min<int64_t>(n_slots, (int64_t)b0 + kWave);
-      // the receiver of the batch's first slot (binary search, uniform), then each lane
-      // steps to its own (a batch spans a few rows)
-      int64_t lo_r = 0, hi_r = n_nodes;  // ptr[lo_r] <= b0 < ptr[hi_r]
-      while (hi_r - lo_r > 1) {
-        const int64_t mid = (lo_r + hi_r) >> 1;
-        if (ptr[mid] <= b0) lo_r = mid; else hi_r = mid;
+      row = 0;
+      if (need_row) {
+        // the receiver of the batch's first slot (binary search, uniform), then each lane
+        // steps to its own (a batch spans a few rows)
+        int64_t lo_r = 0, hi_r = n_nodes;  // ptr[lo_r] <= b0 < ptr[hi_r]
+        while (hi_r - lo_r > 1) {
+          const int64_t mid = (lo_r + hi_r) >> 1;
+          if (ptr[mid] <= b0) lo_r = mid; else hi_r = mid;
+        }
+        row = lo_r;
+        const int q = min(b0 + lane, b1 - 1);
+        while (row + 1 < n_nodes && ptr[row + 1] <= q) ++row;
       }
-      row = lo_r;
-      const int q = min(b0 + lane, b1 - 1);
-      while (row + 1 < n_nodes && ptr[row + 1] <= q) ++row;
     } else {
       row = item;
       b0 = ptr[row];
@@ -618,8 +624,11 @@ static void lin_msg_launch(bool backward, const float* vec, const void* pos, int
                            const int32_t* perm, int l_max, int sign, int K, int C,
                            const float* h, const Radial<float>& R, const float* W,
                            const float* d_out, float* out_or_dh, float* g_vec,
-                           const Readout& ro, hipStream_t stream) {
-  const int64_t blocks_needed = grid_1d(n_nodes, kWavesPerBlock);
+                           const Readout& ro, int64_t n_edges, hipStream_t stream) {
+  // a wave per receiver row, or (readout backward) per 64 consecutive CSR slots
+  const int64_t blocks_needed =
+      backward && RO ? grid_1d(std::max<int64_t>(1, (n_edges + kWave - 1) / kWave), kWavesPerBlock)
+                     : grid_1d(n_nodes, kWavesPerBlock);
   const dim3 block(kWavesPerBlock * kWave);
   const float sg = (float)sign;
 #define XNN_LIN(LM, TT)                                                                        \
@@ -661,20 +670,20 @@ static int lin_msg(bool backward, const float* vec, const void* pos, int64_t n_n
                    const int32_t* shift, const int32_t* ptr, const int32_t* perm, int l_max,
                    int sign, int K, int C, const float* h, const Radial<float>* R,
                    const float* W, const float* d_out, float* out_or_dh, float* g_vec,
-                   hipStream_t stream, const Readout* ro = nullptr) {
+                   hipStream_t stream, const Readout* ro = nullptr, int64_t n_edges = 0) {
   if (n_nodes == 0) return XNN_OK;
   if (ro != nullptr)
     lin_msg_launch<G, true, true>(backward, vec, pos, n_nodes, cell, n_graphs, batch, src,
                                   shift, ptr, perm, l_max, sign, R->K, C, nullptr, *R, W, d_out,
-                                  out_or_dh, g_vec, *ro, stream);
+                                  out_or_dh, g_vec, *ro, n_edges, stream);
   else if (R != nullptr)
     lin_msg_launch<G, true, false>(backward, vec, pos, n_nodes, cell, n_graphs, batch, src,
                                    shift, ptr, perm, l_max, sign, R->K, C, nullptr, *R, W, d_out,
-                                   out_or_dh, g_vec, Readout{}, stream);
+                                   out_or_dh, g_vec, Readout{}, n_edges, stream);
   else
     lin_msg_launch<G, false, false>(backward, vec, pos, n_nodes, cell, n_graphs, batch, src,
                                     shift, ptr, perm, l_max, sign, K, C, h, Radial<float>{}, W,
-                                    d_out, out_or_dh, g_vec, Readout{}, stream);
+                                    d_out, out_or_dh, g_vec, Readout{}, n_edges, stream);
   XNN_LAUNCH_CHECK();
   return XNN_OK;
 }
@@ -872,11 +881,11 @@ int xnn_sh_radial_message_energy_backward(int geom_dtype, const float* vec_in, c
   if (geom_dtype == XNN_F32)
     return lin_msg<float>(true, vec_in, pos, n_nodes, cell, n_graphs, batch, src, shift, ptr_dst,
                           perm_dst, prm->l_max, prm->sh_sign, R.K, n_channels, nullptr, &R, W,
-                          nullptr, nullptr, g_vec, as_hip(stream), &ro);
+                          nullptr, nullptr, g_vec, as_hip(stream), &ro, n_edges);
   if (geom_dtype == XNN_F64)
     return lin_msg<double>(true, vec_in, pos, n_nodes, cell, n_graphs, batch, src, shift,
                            ptr_dst, perm_dst, prm->l_max, prm->sh_sign, R.K, n_channels, nullptr,
-                           &R, W, nullptr, nullptr, g_vec, as_hip(stream), &ro);
+                           &R, W, nullptr, nullptr, g_vec, as_hip(stream), &ro, n_edges);
   set_error("unsupported geometry dtype %d", geom_dtype);
   return XNN_EINVAL;
 }
