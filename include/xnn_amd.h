@@ -397,6 +397,18 @@ int xnn_stress_finish(int dtype, const void* strain_grad, int cell_dtype, const 
                       const uint8_t* pbc, int64_t n_graphs, double scale, void* stress,
                       xnn_stream_t stream);
 
+/* One structure's energy total and stress in one launch, for a step whose energy is the sum
+ * of its node energies: energy[0] = sum_i node_energy[i] in float64 (node_dtype f32/f64; the
+ * order of xnn_segment_reduce_f64's one-block sum, equal to it bit for bit for 2,048 to
+ * 16,384 atoms) and stress (3,3) as xnn_stress_finish with n_graphs = 1. n_nodes at most
+ * xnn_energy_stress_max_nodes(). Replaces the structure sum of the energy (base.py:161-180)
+ * and the stress of ForceStressOutput (outputs.py:227-239) for one structure. */
+int64_t xnn_energy_stress_max_nodes(void);
+int xnn_energy_stress_finish(int node_dtype, const void* node_energy, int64_t n_nodes, int dtype,
+                             const void* strain_grad, int cell_dtype, const void* cell,
+                             const uint8_t* pbc, double scale, double* energy, void* stress,
+                             xnn_stream_t stream);
+
 /* ------------------------------------------------------------------------ */
 /* Segmented sum over a CSR: out[i,:] = sum_{k in [ptr[i],ptr[i+1])} src[perm[k],:].
  * Replaces scatter_sum (common/models/ops.py:403-448) without atomics; its

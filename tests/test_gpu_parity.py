@@ -777,6 +777,37 @@ def test_stress_and_virial_finish_kernels():
                                        atol=1e-7 if dt == torch.float32 else 1e-15)
 
 
+def test_energy_stress_finish_matches_the_two_kernels():
+    """One structure's energy total and stress in one launch: the energy equals the
+    structure sum bit for bit where that sum is one flat block (2,048 to 16,384 atoms) and
+    the float64 sum to rounding elsewhere; the stress equals xnn_stress_finish bit for bit
+    (a periodic cell, a zero cell, pbc all False)."""
+    import xnn_amd as xa
+    from xnn_amd.ops import energy_stress_finish, energy_stress_supported, stress_finish
+    _note("energy + stress finish")
+    gen = torch.Generator().manual_seed(12)
+    g = torch.randn(1, 3, 3, generator=gen, dtype=torch.float64)
+    cell = torch.randn(1, 3, 3, generator=gen, dtype=torch.float64) + 4 * torch.eye(3, dtype=torch.float64)
+    for n in (0, 7, 2048, 9000, 16384, 40000):
+        for edt in (torch.float32, torch.float64):
+            e = (torch.randn(n, generator=gen, dtype=torch.float64) * 3).to(DEV, edt)
+            assert energy_stress_supported(e)
+            for gdt in (torch.float32, torch.float64):
+                for c, pbc in ((cell, None), (cell, torch.zeros(1, 3, dtype=torch.bool)),
+                               (torch.zeros(1, 3, 3, dtype=torch.float64), None)):
+                    E, S = energy_stress_finish(e, g.to(DEV, gdt), c.to(DEV, gdt), pbc, -1.0)
+                    S2 = stress_finish(g.to(DEV, gdt), c.to(DEV, gdt), pbc, -1.0)
+                    assert torch.equal(S, S2)
+                    want = xa.structure_sum(e, torch.zeros(n, dtype=torch.long, device=DEV), 1)
+                    if 2048 <= n <= 16384:
+                        assert torch.equal(E, want)
+                    else:
+                        np.testing.assert_allclose(E.cpu(), e.double().sum().cpu().reshape(1),
+                                                   rtol=1e-14, atol=1e-13)
+                    E2, _ = energy_stress_finish(e, g.to(DEV, gdt), c.to(DEV, gdt), pbc, -1.0)
+                    assert torch.equal(E, E2)
+
+
 # --------------------------------------------------------------------------- full model
 def _float32_floor(R, g, params, cpu_pos, cell, ref, err):
     """The energy bar where float32 cannot give 1e-6 of E.

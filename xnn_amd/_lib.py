@@ -108,6 +108,8 @@ _SIGNATURES = {
     "xnn_edge_force_reduce": [c_int, c_int, vp, i64, vp, vp, vp, vp, vp, vp, i64, vp, vp, vp, vp,
                               vp],
     "xnn_edge_force_reduce_virial_workspace_bytes": [i64, i64],
+    "xnn_energy_stress_max_nodes": [],
+    "xnn_energy_stress_finish": [c_int, vp, i64, c_int, vp, c_int, vp, vp, dbl, vp, vp, vp],
     "xnn_edge_force_reduce_virial": [c_int, c_int, vp, i64, vp, vp, vp, vp, vp, i64, vp, vp, c_int,
                                      vp, vp, sz, vp],
     "xnn_sh_message_sum": [c_int, vp, vp, i64, vp, i64, vp, vp, vp, i64, vp, vp, i32, i32, i32,
@@ -205,6 +207,7 @@ _RESTYPES = {"xnn_last_error": ctypes.c_char_p, "xnn_scan_workspace_bytes": sz,
              "xnn_edge_plan_workspace_bytes": sz, "xnn_segment_reduce_workspace_bytes": sz,
              "xnn_d4_workspace_bytes": sz, "xnn_virial_reduce_workspace_bytes": sz,
              "xnn_d4_plan_bytes": sz, "xnn_edge_force_reduce_virial_workspace_bytes": sz,
+             "xnn_energy_stress_max_nodes": i64,
              "xnn_segment_reduce_noalloc_max_bytes": sz, "xnn_uvu_conv_workspace_bytes": sz,
              "xnn_sh_pair_workspace_bytes": sz}
 

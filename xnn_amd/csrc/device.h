@@ -158,6 +158,23 @@ __device__ inline void sh_chain(T ux, T uy, T uz, T inv_len, T gx, T gy, T gz, T
 }
 
 // ---------------------------------------------------------------- radial
+// entry j of structure b's stress, scale g[b] / V_b for a periodic structure (V_b =
+// |det cell_b| > 1e-8 and, with pbc, some periodic direction), zero otherwise
+// (outputs.py:227-239); float64 inside
+template <typename T, typename C>
+__device__ inline T stress_entry(const T* __restrict__ g, const C* __restrict__ cell,
+                                 const uint8_t* __restrict__ pbc, int64_t b, int j,
+                                 double scale) {
+  const C* c = cell + 9 * b;
+  const double a0 = c[0], a1 = c[1], a2 = c[2], b0 = c[3], b1 = c[4], b2 = c[5], c0 = c[6],
+               c1 = c[7], c2 = c[8];
+  // row 0 . (row 1 x row 2)
+  const double v = fabs(a0 * (b1 * c2 - b2 * c1) + a1 * (b2 * c0 - b0 * c2) + a2 * (b0 * c1 - b1 * c0));
+  bool periodic = v > 1e-8;
+  if (pbc != nullptr) periodic = periodic && (pbc[3 * b] | pbc[3 * b + 1] | pbc[3 * b + 2]);
+  return periodic ? (T)(scale * (double)g[9 * b + j] / v) : T(0);
+}
+
 __device__ inline void dev_sincos(float a, float* s, float* c) { sincosf(a, s, c); }
 __device__ inline void dev_sincos(double a, double* s, double* c) { sincos(a, s, c); }
 __device__ inline float dev_exp(float a) { return expf(a); }

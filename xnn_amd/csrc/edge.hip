@@ -404,15 +404,7 @@ __global__ __launch_bounds__(256) void stress_finish_kernel(const T* __restrict_
                                                             T* __restrict__ out) {
   const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (t >= 9 * n_graphs) return;
-  const int64_t b = t / 9;
-  const C* c = cell + 9 * b;
-  const double a0 = c[0], a1 = c[1], a2 = c[2], b0 = c[3], b1 = c[4], b2 = c[5], c0 = c[6],
-               c1 = c[7], c2 = c[8];
-  // row 0 . (row 1 x row 2)
-  const double v = fabs(a0 * (b1 * c2 - b2 * c1) + a1 * (b2 * c0 - b0 * c2) + a2 * (b0 * c1 - b1 * c0));
-  bool periodic = v > 1e-8;
-  if (pbc != nullptr) periodic = periodic && (pbc[3 * b] | pbc[3 * b + 1] | pbc[3 * b + 2]);
-  out[t] = periodic ? (T)(scale * (double)g[t] / v) : T(0);
+  out[t] = stress_entry(g, cell, pbc, t / 9, (int)(t % 9), scale);
 }
 
 // ---------------------------------------------------------------- dispatch helpers

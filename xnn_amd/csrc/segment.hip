@@ -676,6 +676,8 @@ static_assert(kFlatMaxF <= kWave, "wave 0 holds the flat results");
 constexpr int kFlatPerThread = 4;
 // a single block of 1024 threads takes arrays up to this many elements (no second kernel)
 constexpr int64_t kFlatSingleMax = 16384;
+// the energy-and-stress finish takes one block: structures up to this many atoms
+constexpr int64_t kEnergyStressMaxNodes = 65536;
 
 static int flat_stride(int64_t F, int block) {
   int64_t S = F;
@@ -683,19 +685,13 @@ static int flat_stride(int64_t F, int block) {
   return (int)S;
 }
 
+// The sum of src[c0, c1) over the F interleaved features by the block: thread t < S adds
+// elements c0 + t + k S (S a multiple of F), then a pairwise tree folds the S sums to F.
+// Every thread of the block calls it; lane t < F of wave 0 gets feature t's sum.
 template <typename T, int BLOCK>
-__global__ __launch_bounds__(BLOCK) void flat_reduce_f64_kernel(const T* __restrict__ src,
-                                                                int64_t F, int S,
-                                                                const int64_t* __restrict__ seg,
-                                                                int chunks,
-                                                                double* __restrict__ partial) {
-  __shared__ double red[BLOCK];
+__device__ inline double flat_block_sum(const T* __restrict__ src, int64_t F, int S, int64_t c0,
+                                        int64_t c1, double* red) {
   const int t = threadIdx.x;
-  const int64_t e0 = seg[0] * F, e1 = seg[1] * F;
-  // chunk length: a multiple of S covering the segment in `chunks` pieces
-  const int64_t per_s = ((e1 - e0 + chunks - 1) / chunks + S - 1) / S;
-  const int64_t c0 = min(e1, e0 + (int64_t)blockIdx.x * per_s * S);
-  const int64_t c1 = min(e1, c0 + per_s * S);
   // four independent sums per thread, so that four loads are in flight at a time (a
   // single-block launch over a short array is otherwise a chain of load latencies)
   double a0 = 0.0, a1 = 0.0, a2 = 0.0, a3 = 0.0;
@@ -719,11 +715,43 @@ __global__ __launch_bounds__(BLOCK) void flat_reduce_f64_kernel(const T* __restr
     if (t < h * F) red[t] += red[t + h * F];
     __syncthreads();
   }
+  double x = 0.0;
   if (t < kWave) {
-    double x = red[t];
+    x = red[t];
     for (; h > 0; h >>= 1) x += __shfl_down(x, h * (int)F, kWave);
-    if (t < F) partial[(int64_t)blockIdx.x * F + t] = x;
   }
+  return x;
+}
+
+template <typename T, int BLOCK>
+__global__ __launch_bounds__(BLOCK) void flat_reduce_f64_kernel(const T* __restrict__ src,
+                                                                int64_t F, int S,
+                                                                const int64_t* __restrict__ seg,
+                                                                int chunks,
+                                                                double* __restrict__ partial) {
+  __shared__ double red[BLOCK];
+  const int64_t e0 = seg[0] * F, e1 = seg[1] * F;
+  // chunk length: a multiple of S covering the segment in `chunks` pieces
+  const int64_t per_s = ((e1 - e0 + chunks - 1) / chunks + S - 1) / S;
+  const int64_t c0 = min(e1, e0 + (int64_t)blockIdx.x * per_s * S);
+  const int64_t c1 = min(e1, c0 + per_s * S);
+  const double x = flat_block_sum<T, BLOCK>(src, F, S, c0, c1, red);
+  if (threadIdx.x < F) partial[(int64_t)blockIdx.x * F + threadIdx.x] = x;
+}
+
+// One structure's energy total and stress in one block: energy = the flat sum of the node
+// energies (1024 threads, the same order as flat_reduce_f64_kernel<T, 1024> for one chunk
+// of one feature), and stress = scale g / V (stress_entry) by lanes of wave 1.
+template <typename T, typename G, typename C>
+__global__ __launch_bounds__(1024) void energy_stress_finish_kernel(
+    const T* __restrict__ node_energy, int64_t n, const G* __restrict__ g,
+    const C* __restrict__ cell, const uint8_t* __restrict__ pbc, double scale,
+    double* __restrict__ energy, G* __restrict__ stress) {
+  __shared__ double red[1024];
+  const double x = flat_block_sum<T, 1024>(node_energy, 1, 1024, 0, n, red);
+  if (threadIdx.x == 0) energy[0] = x;
+  const int j = (int)threadIdx.x - kWave;
+  if (j >= 0 && j < 9) stress[j] = stress_entry(g, cell, pbc, 0, j, scale);
 }
 
 // Totals of the 9 virial components over `chunks` partial rows (as segment_finish_kernel),
@@ -1186,6 +1214,45 @@ int xnn_virial_reduce(int dtype, const double* partial, int64_t n_rows, const in
                                   ws2_bytes, stream);
   if (st != XNN_OK) return st;
   return xnn_virial_finish(dtype, M, term, n_graphs, symmetrize, out, stream);
+}
+
+int64_t xnn_energy_stress_max_nodes(void) { return kEnergyStressMaxNodes; }
+
+int xnn_energy_stress_finish(int node_dtype, const void* node_energy, int64_t n_nodes, int dtype,
+                             const void* strain_grad, int cell_dtype, const void* cell,
+                             const uint8_t* pbc, double scale, double* energy, void* stress,
+                             xnn_stream_t stream) {
+  XNN_REQUIRE(n_nodes >= 0 && n_nodes <= kEnergyStressMaxNodes,
+              "n_nodes must be in [0, %lld], got %lld", (long long)kEnergyStressMaxNodes,
+              (long long)n_nodes);
+  XNN_REQUIRE(energy && strain_grad && cell && stress && (n_nodes == 0 || node_energy),
+              "NULL input or output");
+  hipStream_t s = as_hip(stream);
+#define XNN_ES(T, G, C)                                                                       \
+  hipLaunchKernelGGL((energy_stress_finish_kernel<T, G, C>), dim3(1), dim3(1024), 0, s,         \
+                     (const T*)node_energy, n_nodes, (const G*)strain_grad, (const C*)cell, pbc, \
+                     scale, energy, (G*)stress)
+#define XNN_ES_GC(T)                                                                    \
+  if (dtype == XNN_F32 && cell_dtype == XNN_F32) XNN_ES(T, float, float);               \
+  else if (dtype == XNN_F32 && cell_dtype == XNN_F64) XNN_ES(T, float, double);         \
+  else if (dtype == XNN_F64 && cell_dtype == XNN_F32) XNN_ES(T, double, float);         \
+  else if (dtype == XNN_F64 && cell_dtype == XNN_F64) XNN_ES(T, double, double);        \
+  else {                                                                                \
+    set_error("unsupported dtypes %d / %d", dtype, cell_dtype);                         \
+    return XNN_EINVAL;                                                                  \
+  }
+  if (node_dtype == XNN_F32) {
+    XNN_ES_GC(float)
+  } else if (node_dtype == XNN_F64) {
+    XNN_ES_GC(double)
+  } else {
+    set_error("unsupported node dtype %d", node_dtype);
+    return XNN_EINVAL;
+  }
+#undef XNN_ES_GC
+#undef XNN_ES
+  XNN_LAUNCH_CHECK();
+  return XNN_OK;
 }
 
 size_t xnn_segment_reduce_noalloc_max_bytes(void) { return sizeof(scratch); }

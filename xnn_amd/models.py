@@ -62,6 +62,9 @@ class InteratomicPotential(nn.Module):
     # True when ``energy`` is exactly the structure sum of ``node_energy`` (ForceStressOutput
     # then differentiates the node energies directly)
     energy_is_node_sum = False
+    # set by ForceStressOutput for one structure on a GPU: ``energy`` comes back as None
+    # and the wrapper forms the total together with the stress after the backward
+    defer_energy_sum = False
 
     def forward(self, data) -> dict:
         raise NotImplementedError
@@ -72,7 +75,10 @@ class InteratomicPotential(nn.Module):
 
     def aggregate_energy(self, node_energy: Tensor, data) -> Tensor:
         """Per-structure energies in float64 (base.py:161-180); on a GPU over the
-        plan's structure ranges (no host synchronization, so it can be graph-captured)."""
+        plan's structure ranges (no host synchronization, so it can be graph-captured).
+        None when the caller asked to form the total itself (``defer_energy_sum``)."""
+        if self.defer_energy_sum and node_energy.is_cuda:
+            return None
         if node_energy.is_cuda:
             from .ops import structure_sum_op
             plan = data.plan()

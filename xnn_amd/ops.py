@@ -198,11 +198,9 @@ def virial_finish(M: Tensor, term: Optional[Tensor], dtype: torch.dtype) -> Tens
     return out
 
 
-def stress_finish(strain_gradient: Tensor, cell: Tensor, pbc: Optional[Tensor],
-                  scale: float = 1.0) -> Tensor:
-    """``scale * strain_gradient / V`` for periodic structures, zero for molecules
-    (outputs.py:227-239), one kernel; not differentiable (forces and stress only)."""
-    g = strain_gradient.contiguous()
+def _stress_operands(g: Tensor, cell: Tensor, pbc: Optional[Tensor]):
+    """The cell as (B, 3, 3) float32/float64 and the pbc flags as uint8 (None: all periodic)
+    for the stress kernels."""
     c = cell.reshape(-1, 3, 3)
     if c.dtype not in (torch.float32, torch.float64):
         c = c.to(g.dtype)
@@ -215,6 +213,38 @@ def stress_finish(strain_gradient: Tensor, cell: Tensor, pbc: Optional[Tensor],
             # some structure is non-periodic in every direction (host check: pbc is on
             # the CPU, so this is no device sync)
             flags = pbc.reshape(-1, 3).to(device=g.device, dtype=torch.uint8)
+    return c, flags
+
+
+def energy_stress_supported(node_energy: Tensor) -> bool:
+    """Whether :func:`energy_stress_finish` takes this structure (one block of threads)."""
+    return (node_energy.is_cuda and node_energy.dim() == 1
+            and node_energy.shape[0] <= int(_lib.load().xnn_energy_stress_max_nodes()))
+
+
+def energy_stress_finish(node_energy: Tensor, strain_gradient: Tensor, cell: Tensor,
+                         pbc: Optional[Tensor], scale: float = 1.0) -> Tuple[Tensor, Tensor]:
+    """One structure's energy ``sum_i E_i`` (float64, shape (1,)) and stress
+    ``scale * strain_gradient / V`` (zero for a molecule) in one kernel: the structure sum
+    (base.py:161-180) and the stress of outputs.py:227-239; not differentiable."""
+    g = strain_gradient.contiguous()
+    c, flags = _stress_operands(g, cell, pbc)
+    e = node_energy.contiguous()
+    energy = torch.empty(1, dtype=torch.float64, device=e.device)
+    stress = torch.empty_like(g)
+    _lib.call("xnn_energy_stress_finish", _lib.dtype_code(e.dtype), _lib.ptr(e), e.shape[0],
+              _lib.dtype_code(g.dtype), _lib.ptr(g), _lib.dtype_code(c.dtype), _lib.ptr(c),
+              _lib.ptr(flags), float(scale), _lib.ptr(energy), _lib.ptr(stress),
+              _lib.stream(e.device))
+    return energy, stress
+
+
+def stress_finish(strain_gradient: Tensor, cell: Tensor, pbc: Optional[Tensor],
+                  scale: float = 1.0) -> Tensor:
+    """``scale * strain_gradient / V`` for periodic structures, zero for molecules
+    (outputs.py:227-239), one kernel; not differentiable (forces and stress only)."""
+    g = strain_gradient.contiguous()
+    c, flags = _stress_operands(g, cell, pbc)
     out = torch.empty_like(g)
     _lib.call("xnn_stress_finish", _lib.dtype_code(g.dtype), _lib.ptr(g), _lib.dtype_code(c.dtype),
               _lib.ptr(c), _lib.ptr(flags), g.shape[0], float(scale), _lib.ptr(out),

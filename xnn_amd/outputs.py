@@ -122,17 +122,30 @@ class ForceStressOutput(nn.Module):
         had_param_grads = getattr(self.model, "param_grads", None)
         if had_param_grads is not None:
             self.model.param_grads = bool(create_graph)
+        # one structure whose energy is the sum of its node energies: the model leaves the
+        # total to this wrapper, which forms it with the stress in one kernel after the
+        # backward (the backward starts from the node energies anyway)
+        defer = (probe and self.compute_forces and plan is None and data.num_graphs == 1
+                 and bool(getattr(self.model, "energy_is_node_sum", False))
+                 and hasattr(self.model, "defer_energy_sum")
+                 and data.num_nodes <= _energy_stress_max_nodes())
+        if defer:
+            self.model.defer_energy_sum = True
         try:
             out = self.model(data) if plan is None else self.model(data, plan)
         finally:
             if had_param_grads is not None:
                 self.model.param_grads = had_param_grads
+            if defer:
+                self.model.defer_energy_sum = False
             if probe:
                 data.strain_probe = None
         if "energy" not in out:
             # a property model predicts no energy: no forces or stress (outputs.py:187-189)
             return out
         energy = out["energy"]
+        if energy is None:
+            return self._deferred_energy_stress(out, data, strain)
         # a model that predicts its forces directly returns them itself (outputs.py:191-194)
         direct = "forces" in out
         if direct and "energy_sr" in out:
@@ -170,6 +183,32 @@ class ForceStressOutput(nn.Module):
             out["stress"] = (_stress(g["strain"], data, scale=-1.0, differentiable=create_graph)
                              if g.get("strain") is not None else torch.zeros_like(strain))
         return out
+
+
+    def _deferred_energy_stress(self, out: dict, data, strain: Tensor) -> dict:
+        """Forces and strain derivative from the node energies (seed -1), then the energy
+        total and the stress in one kernel (one structure, no training graph)."""
+        from .ops import energy_stress_finish
+        node_energy = out["node_energy"]
+        seed = _minus_one(node_energy).expand(node_energy.shape)
+        g_pos, g_strain = torch.autograd.grad([node_energy], [data.pos, strain],
+                                              grad_outputs=[seed], allow_unused=True)
+        out["forces"] = g_pos if g_pos is not None else torch.zeros_like(data.pos)
+        if g_strain is None:
+            g_strain = torch.zeros_like(strain)
+        out["energy"], out["stress"] = energy_stress_finish(node_energy, g_strain, data.cell,
+                                                            data.pbc, scale=-1.0)
+        return out
+
+
+_ES_MAX = []
+
+
+def _energy_stress_max_nodes() -> int:
+    if not _ES_MAX:
+        from . import _lib
+        _ES_MAX.append(int(_lib.load().xnn_energy_stress_max_nodes()))
+    return _ES_MAX[0]
 
 
 _MINUS_ONE = {}
