@@ -544,10 +544,10 @@ __global__ __launch_bounds__(256, 3) void lin_msg_bwd_kernel(
         // d_h[edge 16 tau + 4 (lo / 4) + i][k = 4 kh + lo % 4] on every hi
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          dq0[i] += __shfl_xor(dq0[i], 16, kWave);
-          dq1[i] += __shfl_xor(dq1[i], 16, kWave);
-          dq0[i] += __shfl_xor(dq0[i], 32, kWave);
-          dq1[i] += __shfl_xor(dq1[i], 32, kWave);
+          dq0[i] = add_xor16(dq0[i]);
+          dq1[i] = add_xor16(dq1[i]);
+          dq0[i] = add_xor32(dq0[i]);
+          dq1[i] = add_xor32(dq1[i]);
         }
         if constexpr (RAD) {
           wave_sync();  // d_h goes into the rows of this tile, whose h was read above
