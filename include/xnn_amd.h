@@ -676,12 +676,22 @@ int xnn_radius_graph_plan(int64_t n_nodes, const double* cell, const int32_t* pb
                           double cutoff, const double* lo, const double* hi,
                           xnn_grid_plan* plan);
 
+/* Device: the bounds xnn_radius_graph_plan takes, in one launch, so that one read gives the
+ * host all it needs: out (15 float64, device) = lo[3], hi[3] of the atoms' Cartesian
+ * coordinates (cell NULL) or fractional ones pos @ inv(cell) (float64), all six NaN when a
+ * coordinate is not finite, then the cell (3x3 row-major, geometry dtype on the device) as
+ * float64 (zeros without a cell). Replaces the host-side min/max of neighborlist.py:411-506's
+ * grid set-up. */
+int xnn_radius_graph_bounds(int geom_dtype, const void* pos, int64_t n_nodes, const void* cell,
+                            double* out, xnn_stream_t stream);
+
 int xnn_radius_graph_count(int geom_dtype, const void* pos, int64_t n_nodes, const void* cell,
                            double cutoff, int32_t self_interaction, const xnn_grid_plan* plan,
                            void* workspace, int32_t* row_ptr, xnn_stream_t stream);
 
 /* Writes E = row_ptr[n_nodes] edges. src/dst int32 (E), shift packed int32 (E);
- * edge_index64 (2,E) and shifts64 (E,3) int64 in the reference format are nullable.
+ * edge_index64 (2,E) and shifts64 (E,3) int64 in the reference format are nullable
+ * (src, dst and shift may be NULL together when both int64 outputs are given).
  * *overflow (device int32, nullable) is set non-zero when a packed shift field left
  * [-512, 511] (the int64 shifts stay exact). */
 int xnn_radius_graph_fill(int geom_dtype, const void* pos, int64_t n_nodes, const void* cell,

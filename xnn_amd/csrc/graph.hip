@@ -269,9 +269,11 @@ __global__ __launch_bounds__(256) void cell_search_kernel(
             const int sz = -s_img[s][2] + offs[4 * pj + 2] - oi2;
             if (sx < -512 || sx > 511 || sy < -512 || sy > 511 || sz < -512 || sz > 511)
               atomicOr(overflow, 1);
-            src[e] = j;
-            dst[e] = i;
-            shift_out[e] = pack_shift(sx, sy, sz);
+            if (src) {
+              src[e] = j;
+              dst[e] = i;
+              shift_out[e] = pack_shift(sx, sy, sz);
+            }
             if (ei64) {
               ei64[e] = j;
               ei64[n_edges + e] = i;
@@ -443,6 +445,83 @@ __global__ void gather_sorted_kernel(const int32_t* __restrict__ atom_sorted, in
     wpos_s[4 * p + k] = wpos[4 * i + k];
     offs_s[4 * p + k] = offs[4 * i + k];
   }
+}
+
+// The per-axis bounds the grid plan needs, in one block: lo/hi of the Cartesian coordinates
+// (cell == NULL) or of the fractional ones f = pos @ inv(cell) (float64, the inverse from
+// the adjugate), any non-finite coordinate making all six NaN; then the cell itself as
+// float64 (row-major; zeros without a cell), so that one read gives the host everything.
+template <typename G>
+__global__ __launch_bounds__(1024) void grid_bounds_kernel(const G* __restrict__ pos, int64_t n,
+                                                           const G* __restrict__ cell,
+                                                           double* __restrict__ out) {
+  double c[9], inv[9];
+  const bool frac = cell != nullptr;
+#pragma unroll
+  for (int k = 0; k < 9; ++k) c[k] = frac ? (double)cell[k] : 0.0;
+  if (frac) {
+    inv[0] = c[4] * c[8] - c[5] * c[7];
+    inv[1] = c[2] * c[7] - c[1] * c[8];
+    inv[2] = c[1] * c[5] - c[2] * c[4];
+    inv[3] = c[5] * c[6] - c[3] * c[8];
+    inv[4] = c[0] * c[8] - c[2] * c[6];
+    inv[5] = c[2] * c[3] - c[0] * c[5];
+    inv[6] = c[3] * c[7] - c[4] * c[6];
+    inv[7] = c[1] * c[6] - c[0] * c[7];
+    inv[8] = c[0] * c[4] - c[1] * c[3];
+    const double id = 1.0 / (c[0] * inv[0] + c[1] * inv[3] + c[2] * inv[6]);
+#pragma unroll
+    for (int k = 0; k < 9; ++k) inv[k] *= id;
+  }
+  double lo[3] = {INFINITY, INFINITY, INFINITY}, hi[3] = {-INFINITY, -INFINITY, -INFINITY};
+  bool bad = false;
+  for (int64_t i = threadIdx.x; i < n; i += blockDim.x) {
+    double x = (double)pos[3 * i], y = (double)pos[3 * i + 1], z = (double)pos[3 * i + 2];
+    if (frac) {
+      const double fx = x * inv[0] + y * inv[3] + z * inv[6];
+      const double fy = x * inv[1] + y * inv[4] + z * inv[7];
+      const double fz = x * inv[2] + y * inv[5] + z * inv[8];
+      x = fx;
+      y = fy;
+      z = fz;
+    }
+    bad = bad || !isfinite(x) || !isfinite(y) || !isfinite(z);
+    lo[0] = fmin(lo[0], x);
+    lo[1] = fmin(lo[1], y);
+    lo[2] = fmin(lo[2], z);
+    hi[0] = fmax(hi[0], x);
+    hi[1] = fmax(hi[1], y);
+    hi[2] = fmax(hi[2], z);
+  }
+#pragma unroll
+  for (int m = kWave / 2; m > 0; m >>= 1) {
+#pragma unroll
+    for (int a = 0; a < 3; ++a) {
+      lo[a] = fmin(lo[a], __shfl_xor(lo[a], m, kWave));
+      hi[a] = fmax(hi[a], __shfl_xor(hi[a], m, kWave));
+    }
+  }
+  __shared__ double red[1024 / kWave][6];
+  __shared__ int any_bad;
+  if (threadIdx.x == 0) any_bad = 0;
+  __syncthreads();
+  if (bad) any_bad = 1;
+  if (threadIdx.x % kWave == 0) {
+#pragma unroll
+    for (int a = 0; a < 3; ++a) {
+      red[threadIdx.x / kWave][a] = lo[a];
+      red[threadIdx.x / kWave][3 + a] = hi[a];
+    }
+  }
+  __syncthreads();
+  if (threadIdx.x < 6) {
+    const int q = threadIdx.x;
+    double v = red[0][q];
+    for (int w = 1; w < (int)(blockDim.x / kWave); ++w)
+      v = q < 3 ? fmin(v, red[w][q]) : fmax(v, red[w][q]);
+    out[q] = any_bad ? NAN : v;
+  }
+  if (threadIdx.x >= kWave && threadIdx.x < kWave + 9) out[6 + threadIdx.x - kWave] = c[threadIdx.x - kWave];
 }
 
 static GridDev grid_dev(const xnn_grid_plan* plan) {
@@ -625,6 +704,23 @@ int xnn_radius_graph_plan(int64_t n_nodes, const double* cell, const int32_t* pb
   return XNN_OK;
 }
 
+int xnn_radius_graph_bounds(int geom_dtype, const void* pos, int64_t n_nodes, const void* cell,
+                            double* out, xnn_stream_t stream) {
+  XNN_REQUIRE(n_nodes >= 0, "negative size");
+  XNN_REQUIRE(out != nullptr && (n_nodes == 0 || pos != nullptr), "NULL input or output");
+  hipStream_t st = as_hip(stream);
+  if (geom_dtype == XNN_F32)
+    hipLaunchKernelGGL(grid_bounds_kernel<float>, dim3(1), dim3(1024), 0, st, (const float*)pos,
+                       n_nodes, (const float*)cell, out);
+  else if (geom_dtype == XNN_F64)
+    hipLaunchKernelGGL(grid_bounds_kernel<double>, dim3(1), dim3(1024), 0, st,
+                       (const double*)pos, n_nodes, (const double*)cell, out);
+  else
+    XNN_REQUIRE(false, "unsupported geometry dtype %d", geom_dtype);
+  XNN_LAUNCH_CHECK();
+  return XNN_OK;
+}
+
 int xnn_radius_graph_count(int geom_dtype, const void* pos, int64_t n_nodes, const void* cell,
                            double cutoff, int32_t self_interaction, const xnn_grid_plan* plan,
                            void* workspace, int32_t* row_ptr, xnn_stream_t stream) {
@@ -653,7 +749,9 @@ int xnn_radius_graph_fill(int geom_dtype, const void* pos, int64_t n_nodes, cons
                           int32_t* overflow, xnn_stream_t stream) {
   XNN_REQUIRE(plan && row_ptr, "NULL plan or row_ptr");
   if (n_nodes == 0 || n_edges == 0) return XNN_OK;
-  XNN_REQUIRE(pos && workspace && src && dst && shift, "NULL input or output");
+  XNN_REQUIRE(pos && workspace, "NULL input");
+  XNN_REQUIRE((src && dst && shift) || (!src && !dst && !shift && edge_index64 && shifts64),
+              "src, dst and shift: all three, or none with both int64 outputs");
   XNN_REQUIRE(plan->has_cell == 0 || cell != nullptr, "the plan has a cell: pass it");
   if (geom_dtype == XNN_F32)
     return grid_fill<float>(pos, n_nodes, cell, cutoff, self_interaction, plan, workspace, row_ptr,

@@ -215,12 +215,16 @@ def _check_finite(lo_hi: list) -> None:
         raise ValueError("the positions are not finite (an unstable simulation?)")
 
 
-def _supercell_reps(cell: Tensor, cutoff: float, pbc: Tensor) -> list[int]:
+def _supercell_reps(cell, cutoff: float, pbc) -> list[int]:
     """Replicas per axis that bring every periodic interplanar spacing to at least a third
-    of the cutoff (the cell list reaches at most three cells along an axis)."""
-    c64 = cell.reshape(3, 3).detach().double().cpu()
+    of the cutoff (the cell list reaches at most three cells along an axis). ``cell``: a
+    tensor or the 9 row-major entries; ``pbc``: a tensor or 3 flags."""
+    if isinstance(cell, Tensor):
+        c64 = cell.reshape(3, 3).detach().double().cpu()
+    else:
+        c64 = torch.tensor(cell, dtype=torch.float64).reshape(3, 3)
     spacing = 1.0 / torch.linalg.norm(torch.linalg.inv(c64).T, dim=1)
-    flags = pbc.reshape(-1).tolist()
+    flags = pbc.reshape(-1).tolist() if isinstance(pbc, Tensor) else list(pbc)
     return [max(1, int(math.ceil(cutoff / (3.0 * float(spacing[a])) * (1.0 + 1e-9))))
             if bool(flags[a]) else 1 for a in range(3)]
 
@@ -254,26 +258,29 @@ def _radius_graph_cuda(pos: Tensor, cutoff: float, cell: Optional[Tensor], pbc: 
     pos = pos.contiguous()
     n = pos.shape[0]
     molecular = cell is None or pbc is None or not bool(pbc.any())
-    if not molecular and n > 0:
-        reps = _supercell_reps(cell, cutoff, pbc)
-        if max(reps) > 1:
-            return _supercell_graph(pos, cutoff, cell, pbc, self_interaction, reps)
-    plan = _lib.GridPlan()
-    pbc_host = (ctypes.c_int32 * 3)(*([0, 0, 0] if molecular else [int(bool(b)) for b in pbc.reshape(-1).tolist()]))
     if n == 0:
         return (torch.zeros((2, 0), dtype=torch.long, device=dev),
                 torch.zeros((0, 3), dtype=torch.long, device=dev))
+    pbc_list = [0, 0, 0] if molecular else [int(bool(b)) for b in pbc.reshape(-1).tolist()]
+    cell_dev = (None if molecular
+                else cell.reshape(3, 3).detach().to(device=dev, dtype=pos.dtype).contiguous())
+    # the atoms' bounds (fractional for a cell) and the cell itself in one launch and one
+    # read: the host's only look at the device before the edge count
+    bounds = torch.empty(15, dtype=torch.float64, device=dev)
+    _lib.call("xnn_radius_graph_bounds", _lib.dtype_code(pos.dtype), _lib.ptr(pos), n,
+              _lib.ptr(cell_dev), _lib.ptr(bounds), _lib.stream(dev))
+    vals = bounds.tolist()
+    lo_hi = vals[:6]
+    _check_finite(lo_hi)
     if molecular:
-        lo_hi = torch.stack([pos.detach().amin(0), pos.detach().amax(0)]).double().flatten().tolist()
-        _check_finite(lo_hi)
-        cell_host, cell_dev = None, None
+        cell_host = None
     else:
-        cell_dev = cell.reshape(3, 3).to(device=dev, dtype=pos.dtype).contiguous()
-        cell64 = cell.reshape(3, 3).detach().double().cpu()
-        frac = pos.detach().double() @ torch.linalg.inv(cell64).to(dev)
-        lo_hi = torch.stack([frac.amin(0), frac.amax(0)]).flatten().tolist()
-        _check_finite(lo_hi)
-        cell_host = (_lib.dbl * 9)(*cell64.flatten().tolist())
+        reps = _supercell_reps(vals[6:], cutoff, pbc_list)
+        if max(reps) > 1:
+            return _supercell_graph(pos, cutoff, cell, pbc, self_interaction, reps)
+        cell_host = (_lib.dbl * 9)(*vals[6:])
+    plan = _lib.GridPlan()
+    pbc_host = (ctypes.c_int32 * 3)(*pbc_list)
     lo = (_lib.dbl * 3)(*lo_hi[:3])
     hi = (_lib.dbl * 3)(*lo_hi[3:])
     _lib.check("xnn_radius_graph_plan",
@@ -288,13 +295,9 @@ def _radius_graph_cuda(pos: Tensor, cutoff: float, cell: Optional[Tensor], pbc: 
     n_edges = int(row_ptr[-1])
     edge_index = torch.empty((2, n_edges), dtype=torch.long, device=dev)
     cell_shifts = torch.empty((n_edges, 3), dtype=torch.long, device=dev)
-    src = torch.empty(n_edges, dtype=torch.int32, device=dev)
-    dst = torch.empty(n_edges, dtype=torch.int32, device=dev)
-    shift = torch.empty(n_edges, dtype=torch.int32, device=dev)
     _lib.call("xnn_radius_graph_fill", geom, _lib.ptr(pos), n, _lib.ptr(cell_dev), float(cutoff),
               int(bool(self_interaction)), ctypes.byref(plan), _lib.ptr(ws), _lib.ptr(row_ptr),
-              n_edges, _lib.ptr(src), _lib.ptr(dst), _lib.ptr(shift), _lib.ptr(edge_index),
-              _lib.ptr(cell_shifts), None, s)
+              n_edges, None, None, None, _lib.ptr(edge_index), _lib.ptr(cell_shifts), None, s)
     return edge_index, cell_shifts
 
 
@@ -366,9 +369,6 @@ class NeighborListPlan:
         cell_shifts = torch.zeros((cap, 3), dtype=torch.long, device=dev)
         if self.n == 0:
             return edge_index, cell_shifts, torch.zeros(1, dtype=torch.long, device=dev)
-        src = torch.empty(cap, dtype=torch.int32, device=dev)
-        dst = torch.empty(cap, dtype=torch.int32, device=dev)
-        shift = torch.empty(cap, dtype=torch.int32, device=dev)
         geom = _lib.dtype_code(pos.dtype)
         s = _lib.stream(dev)
         si = int(self.self_interaction)
@@ -377,8 +377,8 @@ class NeighborListPlan:
                   _lib.ptr(self.row_ptr), s)
         _lib.call("xnn_radius_graph_fill", geom, _lib.ptr(pos), self.n, _lib.ptr(self.cell_dev),
                   self.cutoff, si, ctypes.byref(self.grid), _lib.ptr(self.ws),
-                  _lib.ptr(self.row_ptr), cap, _lib.ptr(src), _lib.ptr(dst), _lib.ptr(shift),
-                  _lib.ptr(edge_index), _lib.ptr(cell_shifts), None, s)
+                  _lib.ptr(self.row_ptr), cap, None, None, None, _lib.ptr(edge_index),
+                  _lib.ptr(cell_shifts), None, s)
         n_edges = self.row_ptr[self.n:].to(torch.long)
         pad = torch.arange(cap, device=dev) >= n_edges
         edge_index = torch.where(pad[None, :], edge_index[:, :1], edge_index)
