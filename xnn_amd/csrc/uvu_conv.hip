@@ -167,14 +167,16 @@ __device__ __forceinline__ float conv_group_sum(float v, bool pair) {
   return v;
 }
 
-// the edge's harmonics of degree <= LS into yv[l^2 + m] (zeros where absent or unused)
+// the edge's harmonics of degree <= LS into yv[l^2 + m] (zeros where absent); e must be a
+// valid edge
 template <int LS>
-__device__ __forceinline__ void conv_load_y(const ConvView& V, int64_t e, bool use, float* yv) {
+__device__ __forceinline__ void conv_load_y(const ConvView& V, int64_t e, float* yv) {
+  const float* yrow = V.y + e * V.d2;
 #pragma unroll
   for (int l = 0; l <= LS; ++l) {
     const int o = V.off2[l];
 #pragma unroll
-    for (int m = 0; m < 2 * l + 1; ++m) yv[l * l + m] = (use && o >= 0) ? V.y[e * V.d2 + o + m] : 0.f;
+    for (int m = 0; m < 2 * l + 1; ++m) yv[l * l + m] = o >= 0 ? yrow[o + m] : 0.f;
   }
 }
 
@@ -201,12 +203,16 @@ __device__ __forceinline__ ConvEdge conv_edge(const ConvView& V, const ConvLanes
 // One edge's operands for one lane: the sender's block h[src(e), block, u, :], the edge's
 // harmonics and the weight of every path of the block. The edge loops fetch them one edge
 // ahead of the arithmetic (and the edge indices two ahead), so the gathers of the next edge
-// are in flight while this one is expanded.
+// are in flight while this one is expanded. Every lane loads, from a valid address (a lane
+// without an edge reads edge 0, a channel past the block channel 0, a weight row out of
+// range row 0), and `use` says whether the operands are the lane's: the arithmetic runs
+// under it, so no per-load branch or zero fill is needed.
 template <int L1, int LS>
 struct ConvFetch {
   float hv[2 * L1 + 1];
   float yv[(LS + 1) * (LS + 1)];
   float wv[kConvCombos];
+  bool use;
 };
 
 template <int L1, int LS>
@@ -214,16 +220,21 @@ __device__ __forceinline__ void conv_fetch(const ConvView& V, const ConvBlock& B
                                            const ConvEdge& E, int u, bool chan, bool want_h,
                                            ConvFetch<L1, LS>& F) {
   constexpr int D1 = 2 * L1 + 1;
-  const bool use = E.row_ok && chan;
+  F.use = E.row_ok && chan;
+  const int us = chan ? u : 0;
+  // row pointers formed once per edge (the per-path loads add uniform offsets)
   if (want_h) {
+    const float* hrow = V.h + E.other * V.d1 + B.off1 + us * D1;
 #pragma unroll
-    for (int a = 0; a < D1; ++a) F.hv[a] = use ? V.h[E.other * V.d1 + B.off1 + u * D1 + a] : 0.f;
+    for (int a = 0; a < D1; ++a) F.hv[a] = hrow[a];
   }
-  conv_load_y<LS>(V, E.e, use, F.yv);
+  conv_load_y<LS>(V, E.e, F.yv);
+  const float* wrow = V.w + (E.row_ok ? E.row : 0) * V.dw + us;
+  const bool have_w = V.n_w_rows > 0;
 #define XNN_CONV_FETCH_W(P1_, P2_, P3_)                                               \
   if constexpr (P1_ == L1 && P2_ <= LS) {                                             \
     constexpr int ci = combo_index(P1_, P2_, P3_);                                    \
-    F.wv[ci] = (use && B.c[ci].off_w >= 0) ? V.w[E.row * V.dw + B.c[ci].off_w + u] : 0.f; \
+    F.wv[ci] = (B.c[ci].off_w >= 0 && have_w) ? wrow[B.c[ci].off_w] : 0.f;            \
   }
   XNN_CG_TRIPLES(XNN_CONV_FETCH_W)
 #undef XNN_CONV_FETCH_W
@@ -247,15 +258,24 @@ __device__ __forceinline__ void conv_fwd_block(const ConvView& V, const ConvBloc
       const ConvFetch<L1, LS> C = F;
       if (it + 1 < L.trips) conv_fetch<L1, LS>(V, B, En, u, chan, true, F);
       En = conv_edge(V, L, it + 2, V.src);
+      if (!C.use) continue;
+      // the products h_a Y_b, shared by every path of the block that reads them
+      float hy[(2 * L1 + 1) * (LS + 1) * (LS + 1)];
+#pragma unroll
+      for (int a = 0; a < 2 * L1 + 1; ++a)
+#pragma unroll
+        for (int b = 0; b < (LS + 1) * (LS + 1); ++b)
+          hy[a * (LS + 1) * (LS + 1) + b] = C.hv[a] * C.yv[b];
 #define XNN_CONV_COMBO(P1_, P2_, P3_)                                                     \
   if constexpr (P1_ == L1 && P2_ <= LS) {                                                 \
     constexpr int ci = combo_index(P1_, P2_, P3_), ao = combo_offset(P1_, P2_, P3_);      \
     using T = CGTable<P1_, P2_, P3_>;                                                     \
     if (B.c[ci].off_w >= 0) {                                                             \
       float t[2 * P3_ + 1];                                                               \
-      _Pragma("unroll") for (int k = 0; k < 2 * P3_ + 1; ++k) t[k] = 0.f;                 \
+      _Pragma("unroll") for (int k = 0; k < 2 * P3_ + 1; ++k) t[k] = -0.f;                \
       _Pragma("unroll") for (int n = 0; n < T::n; ++n)                                    \
-          t[T::e[n].k] += T::e[n].c * C.hv[T::e[n].i] * C.yv[P2_ * P2_ + T::e[n].j];      \
+          t[T::e[n].k] += T::e[n].c *                                                     \
+                          hy[T::e[n].i * (LS + 1) * (LS + 1) + P2_ * P2_ + T::e[n].j];    \
       _Pragma("unroll") for (int k = 0; k < 2 * P3_ + 1; ++k)                             \
           acc[ao + k] += C.wv[ci] * t[k];                                                 \
     }                                                                                     \
@@ -316,27 +336,38 @@ __device__ __forceinline__ void conv_bwd_edge_block(const ConvView& V, const Con
       En = conv_edge(V, L, it + 2, V.src);
       float dyt[NY];
 #pragma unroll
-      for (int j = 0; j < NY; ++j) dyt[j] = 0.f;
+      for (int j = 0; j < NY; ++j) dyt[j] = -0.f;
+      // a lane whose operands are not its own (no edge, channel past the block, weight row
+      // out of range) writes zero weight gradients for an edge it has and adds nothing
+      if (C.use) {
 #define XNN_CONV_EDGE(P1_, P2_, P3_)                                                      \
   if constexpr (P1_ == L1 && P2_ <= LS) {                                                 \
     constexpr int ci = combo_index(P1_, P2_, P3_), ao = combo_offset(P1_, P2_, P3_);      \
     using T = CGTable<P1_, P2_, P3_>;                                                     \
     if (B.c[ci].off_w >= 0) {                                                             \
-      float dw = 0.f, dy[2 * P2_ + 1];                                                    \
-      _Pragma("unroll") for (int j = 0; j < 2 * P2_ + 1; ++j) dy[j] = 0.f;                \
+      float dw = -0.f, dy[2 * P2_ + 1];                                                    \
+      _Pragma("unroll") for (int j = 0; j < 2 * P2_ + 1; ++j) dy[j] = -0.f;               \
       _Pragma("unroll") for (int n = 0; n < T::n; ++n) {                                  \
         const float hg = T::e[n].c * C.hv[T::e[n].i] * gk[ao + T::e[n].k];                \
         dw += hg * C.yv[P2_ * P2_ + T::e[n].j];                                           \
         dy[T::e[n].j] += hg;                                                              \
       }                                                                                   \
-      if (V.g_w && E.on && u < B.mul)                                                     \
-        V.g_w[E.e * V.dw + B.c[ci].off_w + u] = B.c[ci].coef * dw;                        \
+      if (V.g_w) V.g_w[E.e * V.dw + B.c[ci].off_w + u] = B.c[ci].coef * dw;              \
       _Pragma("unroll") for (int j = 0; j < 2 * P2_ + 1; ++j)                             \
           dyt[P2_ * P2_ + j] += B.c[ci].coef * C.wv[ci] * dy[j];                          \
     }                                                                                     \
   }
-      XNN_CG_TRIPLES(XNN_CONV_EDGE)
+        XNN_CG_TRIPLES(XNN_CONV_EDGE)
 #undef XNN_CONV_EDGE
+      } else if (V.g_w && E.on && u < B.mul) {
+#define XNN_CONV_EDGE_ZERO(P1_, P2_, P3_)                                                 \
+  if constexpr (P1_ == L1 && P2_ <= LS) {                                                 \
+    constexpr int ci = combo_index(P1_, P2_, P3_);                                        \
+    if (B.c[ci].off_w >= 0) V.g_w[E.e * V.dw + B.c[ci].off_w + u] = 0.f;                  \
+  }
+        XNN_CG_TRIPLES(XNN_CONV_EDGE_ZERO)
+#undef XNN_CONV_EDGE_ZERO
+      }
       if (V.parts) {
         // this block's share of d Y[e], every column of the present edge blocks
         float* row = V.parts + (E.e * V.n_blocks + blk) * V.d2;
@@ -389,8 +420,11 @@ __device__ __forceinline__ void conv_bwd_node_block(const ConvView& V, const Con
       if (it + 1 < L.trips) conv_fetch<L1, LS>(V, B, En, u, chan, false, F);
       Ec = En;
       En = conv_edge(V, L, it + 2, V.dst);
-      const bool use = E.row_ok && chan;
+      // the receiver's output gradient from a valid address (channel clamped), used only
+      // by a lane whose operands are its own
+      const int us = chan ? u : 0;
       const float* g = V.g_out + E.other * V.dout;
+      if (C.use) {
 #define XNN_CONV_NODE(P1_, P2_, P3_)                                                      \
   if constexpr (P1_ == L1 && P2_ <= LS) {                                                 \
     constexpr int ci = combo_index(P1_, P2_, P3_);                                        \
@@ -398,16 +432,17 @@ __device__ __forceinline__ void conv_bwd_node_block(const ConvView& V, const Con
     if (B.c[ci].off_w >= 0) {                                                             \
       float gk[2 * P3_ + 1], t[D1];                                                       \
       _Pragma("unroll") for (int k = 0; k < 2 * P3_ + 1; ++k)                             \
-          gk[k] = use ? g[B.c[ci].off_out + u * (2 * P3_ + 1) + k] : 0.f;                 \
-      _Pragma("unroll") for (int q = 0; q < D1; ++q) t[q] = 0.f;                          \
+          gk[k] = g[B.c[ci].off_out + us * (2 * P3_ + 1) + k];                            \
+      _Pragma("unroll") for (int q = 0; q < D1; ++q) t[q] = -0.f;                         \
       _Pragma("unroll") for (int n = 0; n < T::n; ++n)                                    \
           t[T::e[n].i] += T::e[n].c * C.yv[P2_ * P2_ + T::e[n].j] * gk[T::e[n].k];        \
       const float wv = B.c[ci].coef * C.wv[ci];                                           \
       _Pragma("unroll") for (int q = 0; q < D1; ++q) acc[q] += wv * t[q];                 \
     }                                                                                     \
   }
-      XNN_CG_TRIPLES(XNN_CONV_NODE)
+        XNN_CG_TRIPLES(XNN_CONV_NODE)
 #undef XNN_CONV_NODE
+      }
     }
     if (chan && L.node < V.n_nodes) {
 #pragma unroll
