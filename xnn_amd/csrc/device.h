@@ -158,6 +158,37 @@ __device__ inline void sh_chain(T ux, T uy, T uz, T inv_len, T gx, T gy, T gz, T
 }
 
 // ---------------------------------------------------------------- radial
+// Butterfly steps across the rows of a wave (a row = 16 lanes) on gfx950's row-swap
+// permutes, vector-ALU instructions instead of an LDS round trip. With both operands x,
+// v_permlane16_swap returns (x with odd rows replaced by the even rows, x with even rows
+// replaced by the odd rows), so their sum is x + x[lane ^ 16] on every lane (the two
+// addends in either order: the same bits); v_permlane32_swap does the same for the two
+// 32-lane halves. Every lane of the wave must be active.
+__device__ __forceinline__ float add_xor16(float x) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false,
+                                                  false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float add_xor32(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false,
+                                                  false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+// Sum over the 16 lanes of a row, every lane getting it: two quad permutes and the half-row
+// and row mirrors (DPP moves, vector ALU). Every lane of the row must be active.
+template <int CTRL>
+__device__ __forceinline__ float dpp_move(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float row_sum16(float v) {
+  v += dpp_move<0xB1>(v);   // quad_perm(1, 0, 3, 2): lane ^ 1
+  v += dpp_move<0x4E>(v);   // quad_perm(2, 3, 0, 1): lane ^ 2
+  v += dpp_move<0x141>(v);  // row_half_mirror: lane i <-> 7 - i within 8
+  v += dpp_move<0x140>(v);  // row_mirror: lane i <-> 15 - i within 16
+  return v;
+}
+
 // entry j of structure b's stress, scale g[b] / V_b for a periodic structure (V_b =
 // |det cell_b| > 1e-8 and, with pbc, some periodic direction), zero otherwise
 // (outputs.py:227-239); float64 inside

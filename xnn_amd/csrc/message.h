@@ -101,23 +101,6 @@ __device__ __forceinline__ void load_first_vec(const float* __restrict__ vec,
   }
 }
 
-// Butterfly steps across the rows of a wave (a row = 16 lanes) on gfx950's row-swap
-// permutes, vector-ALU instructions instead of an LDS round trip. With both operands x,
-// v_permlane16_swap returns (x with odd rows replaced by the even rows, x with even rows
-// replaced by the odd rows), so their sum is x + x[lane ^ 16] on every lane (the two
-// addends in either order: the same bits); v_permlane32_swap does the same for the two
-// 32-lane halves. Every lane of the wave must be active.
-__device__ __forceinline__ float add_xor16(float x) {
-  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false,
-                                                  false);
-  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
-}
-__device__ __forceinline__ float add_xor32(float x) {
-  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false,
-                                                  false);
-  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
-}
-
 // ---------------------------------------------------------------- matrix-core helpers
 // v_mfma_f32_16x16x4_f32 (float32 inputs, float32 accumulation), one wave: per
 // 16 x 16 x 4 block, lane l supplies A[l % 16][l / 16] and B[l / 16][l % 16] and receives

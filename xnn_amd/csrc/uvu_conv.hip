@@ -156,15 +156,11 @@ __device__ __forceinline__ ConvLanes conv_lanes(const ConvView& V, int64_t group
   return L;
 }
 
-// sum over the lanes of one node's group (32 or 64 lanes)
+// sum over the lanes of one node's group (32 or 64 lanes), on every lane of the group: DPP
+// steps inside each 16-lane row, then the row-swap permutes (vector ALU, no LDS round trip)
 __device__ __forceinline__ float conv_group_sum(float v, bool pair) {
-  if (!pair) v += __shfl_xor(v, 32);
-  v += __shfl_xor(v, 16);
-  v += __shfl_xor(v, 8);
-  v += __shfl_xor(v, 4);
-  v += __shfl_xor(v, 2);
-  v += __shfl_xor(v, 1);
-  return v;
+  v = add_xor16(row_sum16(v));
+  return pair ? v : add_xor32(v);
 }
 
 // the edge's harmonics of degree <= LS into yv[l^2 + m] (zeros where absent); e must be a
