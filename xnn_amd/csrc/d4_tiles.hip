@@ -36,6 +36,7 @@
 
 #include "common.h"
 #include "d4_geom.h"
+#include "device.h"
 #include "fp64.h"
 
 namespace xnn {
@@ -402,7 +403,7 @@ __device__ __forceinline__ void lane_combine(const double (&a)[NV], double (&v)[
   for (int k = 0; k < NV; ++k) {
     const double send = upper ? a[k] : v[k];
     const double keep = upper ? v[k] : a[k];
-    v[k] = keep + __shfl_xor(send, 1 << LV, kT);
+    v[k] = keep + xor_lanes<1 << LV>(send);
   }
 }
 

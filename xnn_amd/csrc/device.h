@@ -189,6 +189,28 @@ __device__ __forceinline__ float row_sum16(float v) {
   return v;
 }
 
+// x of lane ^ M for M = 1, 2 (DPP quad permutes, vector ALU) or 4, 8, 16 (ds_swizzle in
+// xor mode: the LDS crossbar without an address computation or memory access), for a
+// double; every lane of the wave must be active.
+template <int M>
+__device__ __forceinline__ double xor_lanes(double v) {
+  static_assert(M == 1 || M == 2 || M == 4 || M == 8 || M == 16, "lane mask");
+  const int lo = __double2loint(v), hi = __double2hiint(v);
+  int a, b;
+  if constexpr (M == 1) {
+    a = __builtin_amdgcn_mov_dpp(lo, 0xB1, 0xF, 0xF, false);  // quad_perm(1, 0, 3, 2)
+    b = __builtin_amdgcn_mov_dpp(hi, 0xB1, 0xF, 0xF, false);
+  } else if constexpr (M == 2) {
+    a = __builtin_amdgcn_mov_dpp(lo, 0x4E, 0xF, 0xF, false);  // quad_perm(2, 3, 0, 1)
+    b = __builtin_amdgcn_mov_dpp(hi, 0x4E, 0xF, 0xF, false);
+  } else {
+    // bit mode: and_mask 0x1F, or_mask 0, xor_mask M
+    a = __builtin_amdgcn_ds_swizzle(lo, 0x1F | (M << 10));
+    b = __builtin_amdgcn_ds_swizzle(hi, 0x1F | (M << 10));
+  }
+  return __hiloint2double(b, a);
+}
+
 // entry j of structure b's stress, scale g[b] / V_b for a periodic structure (V_b =
 // |det cell_b| > 1e-8 and, with pbc, some periodic direction), zero otherwise
 // (outputs.py:227-239); float64 inside
