@@ -242,6 +242,7 @@ struct Radial {
   int envelope;
   int p;
   T rc;
+  T inv_rc;  // 1 / rc, formed on the host in float64
   T prefactor;
   T gamma;
   const T* __restrict__ table;  // Bessel frequencies or Gaussian centers
@@ -262,7 +263,7 @@ __device__ inline void envelope_eval(const Radial<T>& R, T r, T& f, T& df) {
   }
   if (R.envelope == XNN_ENV_POLYNOMIAL) {
     // 1 + ((-(p(p+1)/2) x + p(p+2)) x - (p+1)(p+2)/2) x^p  (cutoff.py:119-125)
-    const T x = r / R.rc;
+    const T x = r * R.inv_rc;
     const T pp = (T)R.p;
     const T a = -(pp * (pp + T(1)) / T(2));
     const T b = pp * (pp + T(2));
@@ -272,10 +273,10 @@ __device__ inline void envelope_eval(const Radial<T>& R, T r, T& f, T& df) {
     const T xp = xpm1 * x;
     const T tail = (a * x + b) * x + c;
     f = T(1) + tail * xp;
-    df = ((T(2) * a * x + b) * xp + pp * tail * xpm1) / R.rc;
+    df = ((T(2) * a * x + b) * xp + pp * tail * xpm1) * R.inv_rc;
   } else {
     // 0.5 (cos(pi r / rc) + 1)  (cutoff.py:40-41)
-    const T w = T(3.141592653589793) / R.rc;
+    const T w = T(3.141592653589793) * R.inv_rc;
     T s, c;
     dev_sincos(w * r, &s, &c);
     f = T(0.5) * (c + T(1));
@@ -309,9 +310,9 @@ template <typename T, bool DERIV>
 __device__ inline void radial_kv(const Radial<T>& R, const RadialAt<T>& a, T tk, T& u, T& du) {
   if (R.basis == XNN_BASIS_BESSEL) {
     // prefactor * sin(freq * r / rc) / r
-    const T w = tk / R.rc;
+    const T w = tk * R.inv_rc;
     T s, c;
-    dev_sincos(tk * a.rr / R.rc, &s, &c);
+    dev_sincos(w * a.rr, &s, &c);
     const T b = R.prefactor * s * a.inv;
     u = b * a.f;
     if constexpr (DERIV) {

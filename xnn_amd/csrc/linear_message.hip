@@ -73,7 +73,7 @@ __device__ __forceinline__ void radial_row(const Radial<float>& R, const RadialT
     const RadialAt<float> a = radial_at(R, r);
     if (tab.harmonic) {
       float s1, c1;
-      dev_sincos(tab.f0 * a.rr / R.rc, &s1, &c1);
+      dev_sincos(tab.f0 * R.inv_rc * a.rr, &s1, &c1);
       const float c2 = 2.f * c1, pf = R.prefactor * a.inv * a.f;
       float sp = 0.f, sk = s1;  // sin(k theta), sin((k + 1) theta)
 #pragma unroll
@@ -104,9 +104,9 @@ __device__ __forceinline__ float radial_dot(const Radial<float>& R, const Radial
   float dl = 0.f;
   if (tab.harmonic) {
     // d/dr [p sin((k+1) w0 r) / r] = p ((k+1) w0 cos((k+1) w0 r) - sin(..) / r) / r
-    const float w0 = tab.f0 / R.rc;
+    const float w0 = tab.f0 * R.inv_rc;
     float s1, c1;
-    dev_sincos(tab.f0 * a.rr / R.rc, &s1, &c1);
+    dev_sincos(tab.f0 * R.inv_rc * a.rr, &s1, &c1);
     const float c2 = 2.f * c1;
     float sp = 0.f, sk = s1, cp = 1.f, ck = c1;
 #pragma unroll 1

@@ -47,6 +47,7 @@ inline int make_radial(const xnn_featurize_params* prm, const void* table, Radia
   R.envelope = prm->envelope;
   R.p = prm->poly_p;
   R.rc = (T)prm->cutoff;
+  R.inv_rc = (T)(1.0 / prm->cutoff);
   R.prefactor = (T)prm->rbf_prefactor;
   R.gamma = (T)prm->gaussian_gamma;
   R.table = static_cast<const T*>(table);
