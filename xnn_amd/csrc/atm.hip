@@ -404,24 +404,39 @@ __device__ __forceinline__ void atm_triangle(const AtmConst& kc, double x, doubl
 }
 
 // ------------------------------------------------------------------------------ exchanges
-// Cross-lane exchanges of doubles: ds_bpermute with byte addresses computed once per
-// kernel (lane ^ 32, 16, 8, 4), and DPP quad permutations for lane ^ 2 and lane ^ 1.
+// Cross-lane exchanges of doubles without LDS address arithmetic: gfx950's row-swap permutes
+// for the two halves of the wave (lane ^ 32) and the two 16-lane rows of each half (lane ^
+// 16), a DPP row rotation by 8 (lane ^ 8 within a row), an xor swizzle for lane ^ 4 and DPP
+// quad permutations for lane ^ 2 and lane ^ 1. Every lane of the wave must be active.
 struct AtmLanes {
-  int a32, a16, a8, a4;
+  int unused;
 };
 
-__device__ __forceinline__ AtmLanes atm_lanes(int lane) {
-  return {(lane ^ 32) << 2, (lane ^ 16) << 2, (lane ^ 8) << 2, (lane ^ 4) << 2};
+__device__ __forceinline__ AtmLanes atm_lanes(int) { return {0}; }
+
+// v_permlane32_swap exchanges lanes 32-63 of its first operand with lanes 0-31 of its second,
+// so the sum of its two results is A_l + A_{l+32} on lanes l < 32 and B_{l-32} + B_l on the
+// others (a reduce-scatter step that needs no select); v_permlane16_swap does the same for
+// the odd and even 16-lane rows (A on rows 0 and 2, B on rows 1 and 3).
+__device__ __forceinline__ double atm_swap32_sum(double A, double B) {
+  const auto lo = __builtin_amdgcn_permlane32_swap((unsigned)__double2loint(A),
+                                                   (unsigned)__double2loint(B), false, false);
+  const auto hi = __builtin_amdgcn_permlane32_swap((unsigned)__double2hiint(A),
+                                                   (unsigned)__double2hiint(B), false, false);
+  return __hiloint2double((int)hi[0], (int)lo[0]) + __hiloint2double((int)hi[1], (int)lo[1]);
 }
 
-__device__ __forceinline__ double atm_bperm(double v, int addr) {
-  const int lo = __builtin_amdgcn_ds_bpermute(addr, __double2loint(v));
-  const int hi = __builtin_amdgcn_ds_bpermute(addr, __double2hiint(v));
-  return __hiloint2double(hi, lo);
+__device__ __forceinline__ double atm_swap16_sum(double A, double B) {
+  const auto lo = __builtin_amdgcn_permlane16_swap((unsigned)__double2loint(A),
+                                                   (unsigned)__double2loint(B), false, false);
+  const auto hi = __builtin_amdgcn_permlane16_swap((unsigned)__double2hiint(A),
+                                                   (unsigned)__double2hiint(B), false, false);
+  return __hiloint2double((int)hi[0], (int)lo[0]) + __hiloint2double((int)hi[1], (int)lo[1]);
 }
 
 constexpr int kDppXor1 = 0xB1;   // quad_perm [1, 0, 3, 2]
 constexpr int kDppXor2 = 0x4E;   // quad_perm [2, 3, 0, 1]
+constexpr int kDppRor8 = 0x128;  // row_ror:8, lane ^ 8 within a 16-lane row
 
 template <int CTRL>
 __device__ __forceinline__ double atm_dpp(double v) {
@@ -430,46 +445,55 @@ __device__ __forceinline__ double atm_dpp(double v) {
   return __hiloint2double(hi, lo);
 }
 
+// lane ^ 4: ds_swizzle in bit mode (and 0x1F, or 0, xor 4)
+__device__ __forceinline__ double atm_xor4(double v) {
+  const int lo = __builtin_amdgcn_ds_swizzle(__double2loint(v), 0x1F | (4 << 10));
+  const int hi = __builtin_amdgcn_ds_swizzle(__double2hiint(v), 0x1F | (4 << 10));
+  return __hiloint2double(hi, lo);
+}
+
 // the wave-wide sum in every lane (a fixed butterfly: every lane gets the same bits)
-__device__ __forceinline__ double atm_wave_sum(double v, const AtmLanes& L) {
-  v += atm_bperm(v, L.a32);
-  v += atm_bperm(v, L.a16);
-  v += atm_bperm(v, L.a8);
-  v += atm_bperm(v, L.a4);
+__device__ __forceinline__ double atm_wave_sum(double v, const AtmLanes&) {
+  v = atm_swap32_sum(v, v);
+  v = atm_swap16_sum(v, v);
+  v += atm_dpp<kDppRor8>(v);
+  v += atm_xor4(v);
   v += atm_dpp<kDppXor2>(v);
   v += atm_dpp<kDppXor1>(v);
   return v;
 }
 
 // The wave-wide sums of the 32 products g * f[s] (f zero beyond its length): lanes 2s and
-// 2s + 1 return the total of slot s. Each lane holds its row permuted, fp[i] = f[i ^ (lane
-// >> 1)], so that at every halving the lane keeps its first half and receives its
-// partner's second half, which holds the same slots: 31 + 1 exchanges and no selects.
+// 2s + 1 return the total of slot s. The first two halvings are row-swap sums (lanes below
+// 32 keep slots 0-15, then rows 0 and 2 keep the lower 8 of their 16), the last four
+// exchange with lane ^ 8, 4, 2, 1; for those each lane holds its row permuted, fp[i] =
+// f[i ^ ((lane >> 1) & 7)], so that at every halving the lane keeps its first half and
+// receives its partner's second half, which holds the same slots: no selects.
 // fp[i][lane] lives in LDS (a column per lane: conflict-free, and 64 registers fewer).
 __device__ __forceinline__ double atm_fold32(const double (*fp)[kWave], int lane, double g,
-                                             const AtmLanes& L) {
+                                             const AtmLanes&) {
   double p[16];
 #pragma unroll
-  for (int i = 0; i < 16; ++i) p[i] = g * fp[i][lane] + atm_bperm(g * fp[i + 16][lane], L.a32);
+  for (int i = 0; i < 16; ++i) p[i] = atm_swap32_sum(g * fp[i][lane], g * fp[i + 16][lane]);
 #pragma unroll
-  for (int i = 0; i < 8; ++i) p[i] += atm_bperm(p[i + 8], L.a16);
+  for (int i = 0; i < 8; ++i) p[i] = atm_swap16_sum(p[i], p[i + 8]);
 #pragma unroll
-  for (int i = 0; i < 4; ++i) p[i] += atm_bperm(p[i + 4], L.a8);
+  for (int i = 0; i < 4; ++i) p[i] += atm_dpp<kDppRor8>(p[i + 4]);
 #pragma unroll
-  for (int i = 0; i < 2; ++i) p[i] += atm_bperm(p[i + 2], L.a4);
+  for (int i = 0; i < 2; ++i) p[i] += atm_xor4(p[i + 2]);
   p[0] += atm_dpp<kDppXor2>(p[1]);
   return p[0] + atm_dpp<kDppXor1>(p[0]);
 }
 
 // The wave-wide sums of four per-lane values: lanes 16 s .. 16 s + 15 return slot s.
 __device__ __forceinline__ double atm_fold4(double s0, double s1, double s2, double s3,
-                                            int lane, const AtmLanes& L) {
-  const bool u5 = (lane & 32) != 0, u4 = (lane & 16) != 0;
-  const double k0 = (u5 ? s2 : s0) + atm_bperm(u5 ? s0 : s2, L.a32);
-  const double k1 = (u5 ? s3 : s1) + atm_bperm(u5 ? s1 : s3, L.a32);
-  double v = (u4 ? k1 : k0) + atm_bperm(u4 ? k0 : k1, L.a16);
-  v += atm_bperm(v, L.a8);
-  v += atm_bperm(v, L.a4);
+                                            int, const AtmLanes&) {
+  // lanes below 32 keep slots 0 and 1, the others 2 and 3; then rows 0 and 2 keep the first
+  const double k0 = atm_swap32_sum(s0, s2);
+  const double k1 = atm_swap32_sum(s1, s3);
+  double v = atm_swap16_sum(k0, k1);
+  v += atm_dpp<kDppRor8>(v);
+  v += atm_xor4(v);
   v += atm_dpp<kDppXor2>(v);
   return v + atm_dpp<kDppXor1>(v);
 }
@@ -487,8 +511,8 @@ __device__ __forceinline__ void atm_ring_flush(double (*ring)[kWave + 1], const 
   double v = 0.0;
 #pragma unroll
   for (int i = 0; i < kWave / 4; ++i) v += ring[r][q * (kWave / 4) + i];
-  v += atm_bperm(v, L.a16);
-  v += atm_bperm(v, L.a32);
+  v = atm_swap16_sum(v, v);
+  v = atm_swap32_sum(v, v);
   if (q == 0 && r < n) unsafeAtomicAdd(&energy[ring_k[r]], v);
   wave_sync();
 }
@@ -515,7 +539,7 @@ __global__ __launch_bounds__(kAtmWaves * kWave) void atm_upper_kernel(
   // the forward's energy ring (one per wave; a placeholder in the backward)
   __shared__ double sRing[BWD ? 1 : kAtmWaves][BWD ? 1 : kAtmRing][kWave + 1];
   __shared__ int32_t sRingK[BWD ? 1 : kAtmWaves][kAtmRing];
-  // the backward's permuted factor rows, fp[i][lane] = fa[j][i ^ (lane >> 1)]
+  // the backward's permuted factor rows, fp[i][lane] = fa[j][i ^ ((lane >> 1) & 7)]
   __shared__ double sFp[BWD ? kAtmWaves : 1][BWD ? 32 : 1][kWave];
   atm_stage_table(table, S, sTab);
   const int lane = threadIdx.x & (kWave - 1);
@@ -540,7 +564,7 @@ __global__ __launch_bounds__(kAtmWaves * kWave) void atm_upper_kernel(
 #pragma unroll
   for (int w = 0; w < KP; ++w) fj[w] = fa[(int64_t)j * KP + w];
   if (BWD) {
-    const int m = lane >> 1;
+    const int m = (lane >> 1) & 7;
 #pragma unroll
     for (int i = 0; i < 32; ++i)
       sFp[wv][i][lane] = (i ^ m) < KP ? fa[(int64_t)j * KP + (i ^ m)] : 0.0;
