@@ -211,6 +211,42 @@ __device__ __forceinline__ double xor_lanes(double v) {
   return __hiloint2double(b, a);
 }
 
+// v + v[lane ^ M] for a double, on the cheapest exchange for M: the row-swap permutes for 32
+// and 16, a DPP row rotation for 8, an xor swizzle for 4, DPP quad permutes for 2 and 1 (the
+// same pairs and order as __shfl_xor, so the same bits). Every lane of the wave must be
+// active.
+template <int M>
+__device__ __forceinline__ double add_xor_lanes(double v) {
+  const unsigned lo = (unsigned)__double2loint(v), hi = (unsigned)__double2hiint(v);
+  if constexpr (M == 32 || M == 16) {
+    const auto a = M == 32 ? __builtin_amdgcn_permlane32_swap(lo, lo, false, false)
+                           : __builtin_amdgcn_permlane16_swap(lo, lo, false, false);
+    const auto b = M == 32 ? __builtin_amdgcn_permlane32_swap(hi, hi, false, false)
+                           : __builtin_amdgcn_permlane16_swap(hi, hi, false, false);
+    return __hiloint2double((int)b[0], (int)a[0]) + __hiloint2double((int)b[1], (int)a[1]);
+  } else if constexpr (M == 4) {
+    return v + __hiloint2double(__builtin_amdgcn_ds_swizzle((int)hi, 0x1F | (4 << 10)),
+                                __builtin_amdgcn_ds_swizzle((int)lo, 0x1F | (4 << 10)));
+  } else {
+    static_assert(M == 8 || M == 2 || M == 1, "lane mask");
+    constexpr int ctrl = M == 8 ? 0x128 : (M == 2 ? 0x4E : 0xB1);
+    return v + __hiloint2double(__builtin_amdgcn_mov_dpp((int)hi, ctrl, 0xF, 0xF, false),
+                                __builtin_amdgcn_mov_dpp((int)lo, ctrl, 0xF, 0xF, false));
+  }
+}
+
+// the sum over aligned groups of GROUP lanes (a power of two up to 64), in every lane
+template <int GROUP>
+__device__ __forceinline__ double group_sum(double v) {
+  if constexpr (GROUP >= 64) v = add_xor_lanes<32>(v);
+  if constexpr (GROUP >= 32) v = add_xor_lanes<16>(v);
+  if constexpr (GROUP >= 16) v = add_xor_lanes<8>(v);
+  if constexpr (GROUP >= 8) v = add_xor_lanes<4>(v);
+  if constexpr (GROUP >= 4) v = add_xor_lanes<2>(v);
+  if constexpr (GROUP >= 2) v = add_xor_lanes<1>(v);
+  return v;
+}
+
 // entry j of structure b's stress, scale g[b] / V_b for a periodic structure (V_b =
 // |det cell_b| > 1e-8 and, with pbc, some periodic direction), zero otherwise
 // (outputs.py:227-239); float64 inside

@@ -210,19 +210,17 @@ __global__ __launch_bounds__(256) void force_reduce_kernel(
       fz -= g_edge[3 * (int64_t)e + 2];
     }
   }
+  // the group's sums in every lane (the butterfly of __shfl_xor, on VALU exchanges)
+  fx = group_sum<GROUP>(fx);
+  fy = group_sum<GROUP>(fy);
+  fz = group_sum<GROUP>(fz);
+  if (want_cell) {
 #pragma unroll
-  for (int m = GROUP / 2; m > 0; m >>= 1) {
-    fx += __shfl_xor(fx, m, GROUP);
-    fy += __shfl_xor(fy, m, GROUP);
-    fz += __shfl_xor(fz, m, GROUP);
-    if (want_cell) {
+    for (int q = 0; q < 9; ++q) c[q] = group_sum<GROUP>(c[q]);
+  }
+  if (want_vir) {
 #pragma unroll
-      for (int q = 0; q < 9; ++q) c[q] += __shfl_xor(c[q], m, GROUP);
-    }
-    if (want_vir) {
-#pragma unroll
-      for (int q = 0; q < 9; ++q) v[q] += __shfl_xor(v[q], m, GROUP);
-    }
+    for (int q = 0; q < 9; ++q) v[q] = group_sum<GROUP>(v[q]);
   }
   if (live && lane == 0) {
     grad_pos[3 * i + 0] = (G)fx;
