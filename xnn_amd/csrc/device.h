@@ -247,6 +247,32 @@ __device__ __forceinline__ double group_sum(double v) {
   return v;
 }
 
+// v + v[lane ^ M] and the aligned GROUP-lane sums for a float, as add_xor_lanes / group_sum
+template <int M>
+__device__ __forceinline__ float add_xor_lanes_f(float v) {
+  if constexpr (M == 32) {
+    return add_xor32(v);
+  } else if constexpr (M == 16) {
+    return add_xor16(v);
+  } else if constexpr (M == 4) {
+    return v + __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), 0x1F | (4 << 10)));
+  } else {
+    static_assert(M == 8 || M == 2 || M == 1, "lane mask");
+    return v + dpp_move<M == 8 ? 0x128 : (M == 2 ? 0x4E : 0xB1)>(v);
+  }
+}
+
+template <int GROUP>
+__device__ __forceinline__ float group_sum_f(float v) {
+  if constexpr (GROUP >= 64) v = add_xor_lanes_f<32>(v);
+  if constexpr (GROUP >= 32) v = add_xor_lanes_f<16>(v);
+  if constexpr (GROUP >= 16) v = add_xor_lanes_f<8>(v);
+  if constexpr (GROUP >= 8) v = add_xor_lanes_f<4>(v);
+  if constexpr (GROUP >= 4) v = add_xor_lanes_f<2>(v);
+  if constexpr (GROUP >= 2) v = add_xor_lanes_f<1>(v);
+  return v;
+}
+
 // entry j of structure b's stress, scale g[b] / V_b for a periodic structure (V_b =
 // |det cell_b| > 1e-8 and, with pbc, some periodic direction), zero otherwise
 // (outputs.py:227-239); float64 inside

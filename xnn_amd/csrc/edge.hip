@@ -263,10 +263,7 @@ __global__ __launch_bounds__(256) void virial_blocks_finish_kernel(const double*
     for (int q = 0; q < 9; ++q) a[q] += block[9 * b + q];
   }
 #pragma unroll
-  for (int q = 0; q < 9; ++q) {
-#pragma unroll
-    for (int m = kWave / 2; m > 0; m >>= 1) a[q] += __shfl_xor(a[q], m, kWave);
-  }
+  for (int q = 0; q < 9; ++q) a[q] = group_sum<kWave>(a[q]);
   __shared__ double wsum[256 / kWave][9];
   __shared__ double tot[9];
   if (threadIdx.x % kWave == 0) {

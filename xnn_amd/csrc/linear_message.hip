@@ -264,8 +264,7 @@ __global__ __launch_bounds__(256, 4) void lin_msg_fwd_kernel(
 #pragma unroll
         for (int r = 0; r < 4; ++r)
           if (4 * hi + r < L) part += acc[t][r] * sU[(lo * T + t) * L + 4 * hi + r];
-#pragma unroll
-      for (int m = kWave / 2; m >= 1; m >>= 1) part += __shfl_xor(part, m, kWave);
+      part = group_sum_f<kWave>(part);
       if (lane == 0) {
         float b = 0.f;
         if (bias != nullptr) {
