@@ -327,16 +327,8 @@ __device__ inline void tile_geo(const double* __restrict__ cell,
   }
 }
 
-__device__ inline double wave_min(double v) {
-#pragma unroll
-  for (int o = 1; o < kT; o <<= 1) v = fmin(v, __shfl_xor(v, o, kT));
-  return v;
-}
-__device__ inline double wave_max(double v) {
-#pragma unroll
-  for (int o = 1; o < kT; o <<= 1) v = fmax(v, __shfl_xor(v, o, kT));
-  return v;
-}
+__device__ inline double wave_min(double v) { return wave_extreme<false>(v); }
+__device__ inline double wave_max(double v) { return wave_extreme<true>(v); }
 
 // receiver tile bounds in fractional coordinates (over the live lanes)
 __device__ inline void tile_bounds(const TileGeo& G, double x, double y, double z, bool live,

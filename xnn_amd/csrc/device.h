@@ -10,6 +10,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 #include "xnn_amd.h"
 
 namespace xnn {
@@ -270,6 +272,35 @@ __device__ __forceinline__ float group_sum_f(float v) {
   if constexpr (GROUP >= 8) v = add_xor_lanes_f<4>(v);
   if constexpr (GROUP >= 4) v = add_xor_lanes_f<2>(v);
   if constexpr (GROUP >= 2) v = add_xor_lanes_f<1>(v);
+  return v;
+}
+
+// The wave-wide minimum (MAX = false) or maximum of a double in every lane: row-swap
+// permutes for lanes ^ 32 and ^ 16 (the two results of a swap of v with itself hold v and
+// its partner's value on every lane), then DPP and an xor swizzle for 8, 4, 2, 1. Every lane
+// of the wave must be active.
+template <bool MAX>
+__device__ __forceinline__ double wave_extreme(double v) {
+  auto pick = [](double a, double b) { return MAX ? fmax(a, b) : fmin(a, b); };
+#pragma unroll
+  for (int half = 0; half < 2; ++half) {
+    const unsigned lo = (unsigned)__double2loint(v), hi = (unsigned)__double2hiint(v);
+    const auto a = half == 0 ? __builtin_amdgcn_permlane32_swap(lo, lo, false, false)
+                             : __builtin_amdgcn_permlane16_swap(lo, lo, false, false);
+    const auto b = half == 0 ? __builtin_amdgcn_permlane32_swap(hi, hi, false, false)
+                             : __builtin_amdgcn_permlane16_swap(hi, hi, false, false);
+    v = pick(__hiloint2double((int)b[0], (int)a[0]), __hiloint2double((int)b[1], (int)a[1]));
+  }
+  auto dpp = [](double x, auto ctrl_tag) {
+    constexpr int ctrl = decltype(ctrl_tag)::value;
+    return __hiloint2double(__builtin_amdgcn_mov_dpp(__double2hiint(x), ctrl, 0xF, 0xF, false),
+                            __builtin_amdgcn_mov_dpp(__double2loint(x), ctrl, 0xF, 0xF, false));
+  };
+  v = pick(v, dpp(v, std::integral_constant<int, 0x128>{}));  // lane ^ 8 (row_ror:8)
+  v = pick(v, __hiloint2double(__builtin_amdgcn_ds_swizzle(__double2hiint(v), 0x1F | (4 << 10)),
+                               __builtin_amdgcn_ds_swizzle(__double2loint(v), 0x1F | (4 << 10))));
+  v = pick(v, dpp(v, std::integral_constant<int, 0x4E>{}));   // lane ^ 2
+  v = pick(v, dpp(v, std::integral_constant<int, 0xB1>{}));   // lane ^ 1
   return v;
 }
 
