@@ -65,15 +65,29 @@ __device__ __forceinline__ RadialTab load_radial_tab(const Radial<float>& R, flo
   return t;
 }
 
+// What the backward's d|r| step reuses of the radial row: the envelope state and, for the
+// harmonic Bessel frequencies, sin and cos of the first frequency.
+struct RadialCache {
+  RadialAt<float> a;
+  float s1, c1;
+};
+
 // The lane's row of radial features h_k = rbf_k(r) envelope(r), k < kLinKMax (zeros past
-// R.K, and the whole row when the lane has no edge).
+// R.K, and the whole row when the lane has no edge); the state the backward needs again goes
+// to *keep (when given).
 __device__ __forceinline__ void radial_row(const Radial<float>& R, const RadialTab& tab,
-                                           bool valid, float r, float* __restrict__ row) {
+                                           bool valid, float r, float* __restrict__ row,
+                                           RadialCache* keep = nullptr) {
   if (valid) {
     const RadialAt<float> a = radial_at(R, r);
+    if (keep) keep->a = a;
     if (tab.harmonic) {
       float s1, c1;
       dev_sincos(tab.f0 * R.inv_rc * a.rr, &s1, &c1);
+      if (keep) {
+        keep->s1 = s1;
+        keep->c1 = c1;
+      }
       const float c2 = 2.f * c1, pf = R.prefactor * a.inv * a.f;
       float sp = 0.f, sk = s1;  // sin(k theta), sin((k + 1) theta)
 #pragma unroll
@@ -97,32 +111,36 @@ __device__ __forceinline__ void radial_row(const Radial<float>& R, const RadialT
   }
 }
 
-// d E / d r through the radial features of one edge: sum_k d_h[k] d h_k / d r
+// d E / d r through the radial features of one edge, sum_k d_h[k] d h_k / d r, from the
+// state radial_row kept. Harmonic Bessel frequencies, with theta = w0 r, w0 = f0 / rc:
+// h_k = P sin((k+1) theta) f / r, so sum_k d_h[k] h_k' = P / r (f (w0 sum_k (k+1) d_h[k]
+// cos((k+1) theta) - S / r) + f' S) with S = sum_k d_h[k] sin((k+1) theta) (the sine term
+// drops at the clamped radius, where h_k does not vary with r).
 __device__ __forceinline__ float radial_dot(const Radial<float>& R, const RadialTab& tab,
-                                            float r, const float* __restrict__ d_h) {
-  const RadialAt<float> a = radial_at(R, r);
-  float dl = 0.f;
+                                            const RadialCache& rc,
+                                            const float* __restrict__ d_h) {
+  const RadialAt<float>& a = rc.a;
   if (tab.harmonic) {
-    // d/dr [p sin((k+1) w0 r) / r] = p ((k+1) w0 cos((k+1) w0 r) - sin(..) / r) / r
     const float w0 = tab.f0 * R.inv_rc;
-    float s1, c1;
-    dev_sincos(tab.f0 * R.inv_rc * a.rr, &s1, &c1);
-    const float c2 = 2.f * c1;
-    float sp = 0.f, sk = s1, cp = 1.f, ck = c1;
-#pragma unroll 1
-    for (int k = 0; k < R.K; ++k) {
-      const float b = R.prefactor * sk * a.inv;
-      const float db =
-          a.clamped ? 0.f : R.prefactor * (ck * ((float)(k + 1) * w0) - sk * a.inv) * a.inv;
-      dl += d_h[k] * (db * a.f + b * a.df);
+    const float c2 = 2.f * rc.c1;
+    float sp = 0.f, sk = rc.s1, cp = 1.f, ck = rc.c1;
+    float S = 0.f, Cw = 0.f;
+#pragma unroll
+    for (int k = 0; k < kLinKMax; ++k) {
+      if (k < R.K) {
+        S += d_h[k] * sk;
+        Cw += ((float)(k + 1) * d_h[k]) * ck;
+      }
       const float sn = c2 * sk - sp, cn = c2 * ck - cp;
       sp = sk;
       sk = sn;
       cp = ck;
       ck = cn;
     }
-    return dl;
+    const float rad = a.clamped ? 0.f : a.f * (w0 * Cw - a.inv * S);
+    return R.prefactor * a.inv * (rad + a.df * S);
   }
+  float dl = 0.f;
 #pragma unroll 1
   for (int k = 0; k < R.K; ++k) {
     float u, du;
@@ -463,9 +481,10 @@ __global__ __launch_bounds__(256, 3) void lin_msg_bwd_kernel(
         batch_harmonics<G, LMAX>(vec, pos, cl, src, shift, (int)row, sign, lane, cnt, my_e, ys,
                                  ux, uy, uz, inv, len);
       }
+      RadialCache rcache;
       if constexpr (RAD) {
         __builtin_amdgcn_sched_barrier(0);
-        radial_row(R, tab, lane < cnt, len, hs + lane * kSH);
+        radial_row(R, tab, lane < cnt, len, hs + lane * kSH, &rcache);
       }
       wave_sync();
       const int ntile = (cnt + 15) >> 4;
@@ -576,7 +595,7 @@ __global__ __launch_bounds__(256, 3) void lin_msg_bwd_kernel(
         // d|r| from the radial features first, then the harmonics' share (kept apart so
         // that their temporaries are not live together)
         float dl = 0.f;
-        if constexpr (RAD) dl = radial_dot(R, tab, len, hs + lane * kSH);
+        if constexpr (RAD) dl = radial_dot(R, tab, rcache, hs + lane * kSH);
         __builtin_amdgcn_sched_barrier(0);
         float dY[L];
 #pragma unroll
