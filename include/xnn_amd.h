@@ -562,6 +562,18 @@ int xnn_eeq_real_grad(const double* pos, int64_t n_nodes, const double* cell, co
                       double alpha, double cutoff, const double* u, const double* w,
                       double* grad_pos, double* cell_partial, xnn_stream_t stream);
 
+/* One diagonal block of the blocked Cholesky factorization of the assembled operator
+ * (replaces the factorization of EEQSystem._solve_lu, common/models/eeq.py:312-323, which
+ * LU-factors the augmented matrix; the operator is symmetric positive definite and the
+ * constraint is eliminated on the host). matrix: device, (n, n) row-major float64; the
+ * block covers rows and columns [k0, k0 + b), 1 <= b <= 128, after the host has applied
+ * the trailing updates of the blocks before it. Written in place: the block's factor L
+ * (lower; its upper triangle zeroed), and inv (b, b) = L^-1 (row-major, lower) for the
+ * panel product L21 = A21 inv^T. A pivot that is not positive and finite stores k0 + j + 1 into the
+ * device int *info when that still holds 0, and leaves the block unwritten. */
+int xnn_eeq_cholesky_block(double* matrix, int64_t n, int64_t k0, int64_t b, double* inv,
+                           int* info, xnn_stream_t stream);
+
 /* D4 reference tables in the kernels' layout, indexed by atomic number (rows 0 ..
  * n_elements-1), device memory: nref (n_el) int32, ngw / refcn / refq (n_el, 7) with
  * ngw int32, zeff (n_el), gi = hardness x gc (n_el), refalpha (n_el, 7, 23) the

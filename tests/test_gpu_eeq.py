@@ -195,3 +195,34 @@ def test_c5_charges_large_regime(tables):
     np.testing.assert_allclose(q1.cpu(), q3.cpu(), atol=5e-5)
     e1, e3 = float(out1["energy"][0]), float(out3["energy"][0])
     assert abs(e1 - e3) <= 1e-6 * abs(e3), (e1, e3)
+
+
+@pytest.mark.parametrize("n", [1, 128, 300, 700])
+def test_blocked_cholesky_matches_lapack(n):
+    """The device factorization (128-column diagonal blocks in LDS, library GEMMs for the
+    panel and trailing updates) against LAPACK's on the CPU, at sizes with a partial last
+    block; its factor reproduces the matrix."""
+    from xnn_amd.eeq import _cholesky
+    _note(f"blocked cholesky n={n}")
+    g = torch.Generator().manual_seed(n)
+    M = torch.randn((n, n), dtype=torch.float64, generator=g)
+    A = M @ M.T + n * torch.eye(n, dtype=torch.float64)
+    L, info = _cholesky(A.to(DEV))
+    assert int(info) == 0
+    L = L.cpu()
+    ref = torch.linalg.cholesky(A)
+    assert torch.equal(L, L.tril())
+    assert torch.allclose(L, ref, rtol=0, atol=1e-12 * float(ref.abs().max()))
+    assert torch.allclose(L @ L.T, A, rtol=0, atol=1e-12 * float(A.abs().max()))
+
+
+def test_blocked_cholesky_reports_the_first_bad_pivot():
+    """An indefinite matrix: LAPACK's info (the 1-based column of the first pivot that is
+    not positive), here in the second diagonal block."""
+    from xnn_amd.eeq import _cholesky
+    n = 300
+    A = torch.eye(n, dtype=torch.float64) * 2.0
+    A[200, 200] = -1.0
+    _, info = _cholesky(A.to(DEV))
+    _, ref = torch.linalg.cholesky_ex(A)
+    assert int(info) == int(ref) == 201

@@ -198,6 +198,145 @@ static bool eeq_reach_ok(const EeqCell& C, double cutoff) {
   return C.reach[0] <= kMaxReach && C.reach[1] <= kMaxReach && C.reach[2] <= kMaxReach;
 }
 
+
+// One diagonal block of the blocked Cholesky factorization of the (symmetric positive
+// definite) operator, in place: rows and columns k0 .. k0+b of the row-major matrix a
+// (leading dimension lda), whose trailing updates the host has applied. One workgroup of
+// 512 threads; thread (ty, tx) holds the 32 elements (ty + 16 p, tx + 32 q) in registers,
+// of the block and of E, which starts as the identity.
+//
+// Step j eliminates column j with unscaled columns, a_ic -= a_ij a_cj / d_j for
+// j < c <= i (pivot d_j = a_jj), and applies the same row operations to E: row i -=
+// (a_ij / d_j) row j for i > j. Afterwards L_ij = a_ij / sqrt(d_j) and E is the inverse of
+// the unit lower factor, so L^-1 = diag(d)^(-1/2) E. A step reads column j of the block
+// and row j of E, which their owners published to LDS at the end of the step before (two
+// buffers each, one barrier per step). Written: L (lower; the block's upper triangle
+// zeroed) and inv = L^-1 (b, b) row-major, which the host multiplies into the panel below
+// the block. A pivot that is not positive and finite stores k0 + j + 1 into *info if it
+// still holds 0 and leaves the block unwritten.
+constexpr int kCholBlock = 128;
+constexpr int kCholThreads = 512;
+constexpr int kCholP = kCholBlock / (kCholThreads / 32);  // row groups of 16
+constexpr int kCholQ = kCholBlock / 32;                   // column groups of 32
+
+// 1 / d for a positive normal d: the hardware estimate refined by two Newton steps
+// r <- r + r (1 - d r) (each squares the relative error), on the barrier-bound path of the
+// column steps where the full division sequence costs a large part of a step.
+__device__ inline double refined_rcp(double d) {
+  double r = __builtin_amdgcn_rcp(d);
+  r = fma(r, fma(-d, r, 1.0), r);
+  return fma(r, fma(-d, r, 1.0), r);
+}
+
+__global__ __launch_bounds__(kCholThreads) void eeq_cholesky_block_kernel(
+    double* __restrict__ a, int64_t lda, int64_t k0, int b, double* __restrict__ inv,
+    int* __restrict__ info) {
+  __shared__ double col_buf[2][kCholBlock];  // column j of the block
+  __shared__ double row_buf[2][kCholBlock];  // row j of E
+  __shared__ double piv[kCholBlock];
+  const int t = threadIdx.x, tx = t & 31, ty = t >> 5;
+  double* blk = a + k0 * lda + k0;
+  double v[kCholP][kCholQ], e[kCholP][kCholQ];
+#pragma unroll
+  for (int p = 0; p < kCholP; ++p)
+#pragma unroll
+    for (int q = 0; q < kCholQ; ++q) {
+      const int i = ty + 16 * p, c = tx + 32 * q;
+      v[p][q] = (i < b && c <= i) ? blk[i * lda + c] : 0.0;
+      e[p][q] = i == c ? 1.0 : 0.0;
+    }
+  if (t < 2 * kCholBlock) {
+    col_buf[t >> 7][t & (kCholBlock - 1)] = 0.0;
+    row_buf[t >> 7][t & (kCholBlock - 1)] = 0.0;
+  }
+  __syncthreads();
+  if (tx == 0)
+#pragma unroll
+    for (int p = 0; p < kCholP; ++p)
+      if (ty + 16 * p < b) col_buf[0][ty + 16 * p] = v[p][0];
+  if (ty == 0)
+#pragma unroll
+    for (int q = 0; q < kCholQ; ++q) row_buf[0][tx + 32 * q] = e[0][q];
+  for (int j = 0; j < b; ++j) {
+    __syncthreads();
+    const double* col = col_buf[j & 1];
+    const double* erow = row_buf[j & 1];
+    const double d = col[j];
+    double li[kCholP], lc[kCholQ], xr[kCholQ];
+#pragma unroll
+    for (int p = 0; p < kCholP; ++p) li[p] = col[ty + 16 * p];
+#pragma unroll
+    for (int q = 0; q < kCholQ; ++q) {
+      lc[q] = col[tx + 32 * q];
+      xr[q] = erow[tx + 32 * q];
+    }
+    const double r = refined_rcp(d);
+    // Columns c <= j take lc = 0 and rows i <= j take f = 0 (exact no-ops); rows i >= b,
+    // and columns c > i of the block, hold values that are never read again; row j of E
+    // vanishes right of j. So the updates run unmasked over the row groups that reach
+    // below j (uniform branches) and the column groups left of the diagonal.
+#pragma unroll
+    for (int q = 0; q < kCholQ; ++q) lc[q] = tx + 32 * q > j ? lc[q] * r : 0.0;
+#pragma unroll
+    for (int p = 0; p < kCholP; ++p) {
+      if (16 * p + 15 <= j) continue;
+      const double f = ty + 16 * p > j ? li[p] * r : 0.0;
+#pragma unroll
+      for (int q = 0; q <= (p >> 1); ++q) {
+        v[p][q] -= li[p] * lc[q];
+        e[p][q] -= f * xr[q];
+      }
+    }
+    if (!(d > 0.0 && d < INFINITY)) {  // uniform: every thread read the same pivot
+      if (t == 0 && *info == 0) *info = (int)(k0 + j + 1);
+      return;
+    }
+    if (t == 0) piv[j] = d;
+    const int jn = j + 1;
+    if (jn < b) {
+      if (tx == (jn & 31)) {
+#pragma unroll
+        for (int q = 0; q < kCholQ; ++q)
+          if (q == (jn >> 5)) {
+#pragma unroll
+            for (int p = 0; p < kCholP; ++p) {
+              const int i = ty + 16 * p;
+              if (i >= jn && i < b) col_buf[jn & 1][i] = v[p][q];
+            }
+          }
+      }
+      if (ty == (jn & 15)) {
+#pragma unroll
+        for (int p = 0; p < kCholP; ++p)
+          if (p == (jn >> 4)) {
+#pragma unroll
+            for (int q = 0; q < kCholQ; ++q) row_buf[jn & 1][tx + 32 * q] = e[p][q];
+          }
+      }
+    }
+  }
+  __syncthreads();
+#pragma unroll
+  for (int p = 0; p < kCholP; ++p) {
+    const int i = ty + 16 * p;
+    if (i >= b) continue;
+    const double rroot = 1.0 / sqrt(piv[i]);
+#pragma unroll
+    for (int q = 0; q < kCholQ; ++q) {
+      const int c = tx + 32 * q;
+      if (c >= b) continue;
+      double l = 0.0, x = 0.0;
+      if (c <= i) {
+        const double root = sqrt(piv[c]);
+        l = c == i ? root : v[p][q] / root;
+        x = e[p][q] * rroot;
+      }
+      blk[i * lda + c] = l;
+      inv[i * b + c] = x;
+    }
+  }
+}
+
 }  // namespace xnn
 
 using namespace xnn;
@@ -240,6 +379,18 @@ int xnn_eeq_real_grad(const double* pos, int64_t n_nodes, const double* cell, co
   hipLaunchKernelGGL(eeq_real_grad_kernel, dim3((unsigned)grid_1d(n_nodes, 4)), dim3(256), 0,
                      as_hip(stream), pos, n_nodes, C, rad, alpha, cutoff * cutoff, u, w, grad_pos,
                      cell_partial);
+  XNN_LAUNCH_CHECK();
+  return XNN_OK;
+}
+
+int xnn_eeq_cholesky_block(double* matrix, int64_t n, int64_t k0, int64_t b, double* inv,
+                           int* info, xnn_stream_t stream) {
+  XNN_REQUIRE(matrix && inv && info, "NULL matrix, inverse or info");
+  XNN_REQUIRE(n > 0 && k0 >= 0 && b >= 1 && b <= kCholBlock && k0 + b <= n,
+              "block [%lld, %lld) outside the matrix or wider than %d", (long long)k0,
+              (long long)(k0 + b), kCholBlock);
+  hipLaunchKernelGGL(eeq_cholesky_block_kernel, dim3(1), dim3(kCholThreads), 0, as_hip(stream), matrix,
+                     n, k0, (int)b, inv, info);
   XNN_LAUNCH_CHECK();
   return XNN_OK;
 }

@@ -184,7 +184,12 @@ class LargeEEQSystem:
 
     def _solve(self, b: Tensor) -> Tensor:
         """``A^-1 b`` for ``b`` (N, k): two triangular solves with the Cholesky factor (the
-        blocked solves; the one-column path of ``cholesky_solve`` is several times slower)."""
+        blocked solves; the one-column path of ``cholesky_solve`` is several times slower).
+        A single column is solved as two, with a zero second column: the library's
+        one-column triangular solve is about six times slower than its blocked one at
+        N = 5,000."""
+        if b.shape[1] == 1 and b.is_cuda:
+            return self._solve(torch.cat([b, torch.zeros_like(b)], 1))[:, :1]
         if self.cholesky:
             y = torch.linalg.solve_triangular(self.factor, b, upper=False)
             return torch.linalg.solve_triangular(self.factor.mT, y, upper=True)
@@ -216,20 +221,35 @@ class LargeEEQSystem:
         return out
 
 
+CHOLESKY_BLOCK = 128
+
+
 def _cholesky(A: Tensor):
-    """``cholesky_ex`` of a float64 matrix, on the MAGMA backend where the build has one
-    (measured on MI355X at N = 5000: 12.7 ms against 16.4 ms for the default)."""
+    """The Cholesky factor of the float64 operator and LAPACK's ``info`` (0, or the 1-based
+    column of the first pivot that is not positive). On the device: right-looking blocked
+    factorization, 128 columns at a time: ``xnn_eeq_cholesky_block`` factors the diagonal
+    block in LDS and forms its inverse, the panel below it is ``A21 L11^-T`` and the
+    trailing matrix takes ``- L21 L21^T`` (two library GEMMs; the trailing update
+    is applied to the full square, whose upper triangle is discarded at the end)."""
     if not A.is_cuda:
         return torch.linalg.cholesky_ex(A)
-    before = torch.backends.cuda.preferred_linalg_library()
-    try:
-        torch.backends.cuda.preferred_linalg_library("magma")
-        return torch.linalg.cholesky_ex(A)
-    except RuntimeError:
-        torch.backends.cuda.preferred_linalg_library("default")
-        return torch.linalg.cholesky_ex(A)
-    finally:
-        torch.backends.cuda.preferred_linalg_library(before)
+    n, nb = A.shape[0], CHOLESKY_BLOCK
+    L = A.contiguous().clone()
+    info = torch.zeros(1, dtype=torch.int32, device=A.device)
+    inv = torch.empty(nb * nb, dtype=torch.float64, device=A.device)
+    panel = torch.empty((max(n - nb, 0), nb), dtype=torch.float64, device=A.device)
+    stream = _lib.stream(A.device)
+    for k in range(0, n, nb):
+        b = min(nb, n - k)
+        _lib.call("xnn_eeq_cholesky_block", _lib.ptr(L), n, k, b, _lib.ptr(inv),
+                  _lib.ptr(info), stream)
+        r = k + b
+        if r < n:
+            p = panel[:n - r, :b]
+            torch.matmul(L[r:, k:r], inv[:b * b].view(b, b).t(), out=p)
+            L[r:, k:r].copy_(p)
+            L[r:, r:].addmm_(p, p.t(), alpha=-1.0)
+    return L.tril_(), info[0]
 
 
 class _ConstantSolve(torch.autograd.Function):
