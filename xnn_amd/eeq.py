@@ -229,8 +229,9 @@ def _cholesky(A: Tensor):
     column of the first pivot that is not positive). On the device: right-looking blocked
     factorization, 128 columns at a time: ``xnn_eeq_cholesky_block`` factors the diagonal
     block in LDS and forms its inverse, the panel below it is ``A21 L11^-T`` and the
-    trailing matrix takes ``- L21 L21^T`` (two library GEMMs; the trailing update
-    is applied to the full square, whose upper triangle is discarded at the end)."""
+    trailing matrix takes ``- L21 L21^T`` (library GEMMs; a large trailing update is split
+    at half height into the top rows' left square and the bottom rows, 3/4 of the square,
+    and the upper triangle is discarded at the end)."""
     if not A.is_cuda:
         return torch.linalg.cholesky_ex(A)
     n, nb = A.shape[0], CHOLESKY_BLOCK
@@ -248,7 +249,13 @@ def _cholesky(A: Tensor):
             p = panel[:n - r, :b]
             torch.matmul(L[r:, k:r], inv[:b * b].view(b, b).t(), out=p)
             L[r:, k:r].copy_(p)
-            L[r:, r:].addmm_(p, p.t(), alpha=-1.0)
+            m = n - r
+            if m >= 4 * nb:                # the lower part only: 3/4 of the square
+                h = (m // 2 + nb - 1) // nb * nb
+                L[r:r + h, r:r + h].addmm_(p[:h], p[:h].t(), alpha=-1.0)
+                L[r + h:, r:].addmm_(p[h:], p.t(), alpha=-1.0)
+            else:
+                L[r:, r:].addmm_(p, p.t(), alpha=-1.0)
     return L.tril_(), info[0]
 
 
