@@ -205,15 +205,18 @@ static bool eeq_reach_ok(const EeqCell& C, double cutoff) {
 // 512 threads; thread (ty, tx) holds the 32 elements (ty + 16 p, tx + 32 q) in registers,
 // of the block and of E, which starts as the identity.
 //
-// Step j eliminates column j with unscaled columns, a_ic -= a_ij a_cj / d_j for
-// j < c <= i (pivot d_j = a_jj), and applies the same row operations to E: row i -=
-// (a_ij / d_j) row j for i > j. Afterwards L_ij = a_ij / sqrt(d_j) and E is the inverse of
-// the unit lower factor, so L^-1 = diag(d)^(-1/2) E. A step reads column j of the block
-// and row j of E, which their owners published to LDS at the end of the step before (two
-// buffers each, one barrier per step). Written: L (lower; the block's upper triangle
-// zeroed) and inv = L^-1 (b, b) row-major, which the host multiplies into the panel below
-// the block. A pivot that is not positive and finite stores k0 + j + 1 into *info if it
-// still holds 0 and leaves the block unwritten.
+// Elimination with unscaled columns: column j's pivot d_j = a_jj, a_ic -= a_ij a_cj / d_j
+// for j < c <= i, and the same row operations on E, row i -= (a_ij / d_j) row j for i > j.
+// Afterwards L_ij = a_ij / sqrt(d_j) and E is the inverse of the unit lower factor, so
+// L^-1 = diag(d)^(-1/2) E. A step eliminates two columns: it reads columns j and j + 1 of
+// the block and rows j and j + 1 of E as their owners published them to LDS at the end of
+// the step before (two buffers, one barrier per step), column j + 1 and row j + 1 not yet
+// reduced by column j; every thread applies that reduction itself, g = a_{j+1,j} / d_j:
+// y1_i = a_{i,j+1} - a_ij g, d_{j+1} = a_{j+1,j+1} - a_{j+1,j} g, E row j+1 -= g E row j.
+// Written: L (lower; the block's upper triangle zeroed) and inv = L^-1 (b, b) row-major,
+// which the host multiplies into the panel below the block. A pivot that is not positive
+// and finite stores k0 + j + 1 into *info if it still holds 0 and leaves the block
+// unwritten. Entries of the block outside rows and columns < b stay zero throughout.
 constexpr int kCholBlock = 128;
 constexpr int kCholThreads = 512;
 constexpr int kCholP = kCholBlock / (kCholThreads / 32);  // row groups of 16
@@ -231,8 +234,8 @@ __device__ inline double refined_rcp(double d) {
 __global__ __launch_bounds__(kCholThreads) void eeq_cholesky_block_kernel(
     double* __restrict__ a, int64_t lda, int64_t k0, int b, double* __restrict__ inv,
     int* __restrict__ info) {
-  __shared__ double col_buf[2][kCholBlock];  // column j of the block
-  __shared__ double row_buf[2][kCholBlock];  // row j of E
+  __shared__ double col_buf[2][2][kCholBlock];  // columns j, j + 1 of the block
+  __shared__ double row_buf[2][2][kCholBlock];  // rows j, j + 1 of E
   __shared__ double piv[kCholBlock];
   const int t = threadIdx.x, tx = t & 31, ty = t >> 5;
   double* blk = a + k0 * lda + k0;
@@ -245,73 +248,102 @@ __global__ __launch_bounds__(kCholThreads) void eeq_cholesky_block_kernel(
       v[p][q] = (i < b && c <= i) ? blk[i * lda + c] : 0.0;
       e[p][q] = i == c ? 1.0 : 0.0;
     }
-  if (t < 2 * kCholBlock) {
-    col_buf[t >> 7][t & (kCholBlock - 1)] = 0.0;
-    row_buf[t >> 7][t & (kCholBlock - 1)] = 0.0;
+  for (int k = t; k < 4 * kCholBlock; k += kCholThreads) {
+    (&col_buf[0][0][0])[k] = 0.0;
+    (&row_buf[0][0][0])[k] = 0.0;
   }
   __syncthreads();
-  if (tx == 0)
+  if (tx < 2)
 #pragma unroll
-    for (int p = 0; p < kCholP; ++p)
-      if (ty + 16 * p < b) col_buf[0][ty + 16 * p] = v[p][0];
-  if (ty == 0)
+    for (int p = 0; p < kCholP; ++p) col_buf[0][tx][ty + 16 * p] = v[p][0];
+  if (ty < 2)
 #pragma unroll
-    for (int q = 0; q < kCholQ; ++q) row_buf[0][tx + 32 * q] = e[0][q];
-  for (int j = 0; j < b; ++j) {
+    for (int q = 0; q < kCholQ; ++q) row_buf[0][ty][tx + 32 * q] = e[0][q];
+  for (int j = 0, step = 0; j < b; j += 2, ++step) {
     __syncthreads();
-    const double* col = col_buf[j & 1];
-    const double* erow = row_buf[j & 1];
-    const double d = col[j];
-    double li[kCholP], lc[kCholQ], xr[kCholQ];
+    const double* c0 = col_buf[step & 1][0];
+    const double* c1 = col_buf[step & 1][1];
+    const double* r0w = row_buf[step & 1][0];
+    const double* r1w = row_buf[step & 1][1];
+    const double d0 = c0[j], x = c0[j + 1], e1 = c1[j + 1];
+    double l0[kCholP], l1[kCholP], m0[kCholQ], m1[kCholQ], w0[kCholQ], w1[kCholQ];
 #pragma unroll
-    for (int p = 0; p < kCholP; ++p) li[p] = col[ty + 16 * p];
+    for (int p = 0; p < kCholP; ++p) {
+      l0[p] = c0[ty + 16 * p];
+      l1[p] = c1[ty + 16 * p];
+    }
 #pragma unroll
     for (int q = 0; q < kCholQ; ++q) {
-      lc[q] = col[tx + 32 * q];
-      xr[q] = erow[tx + 32 * q];
+      m0[q] = c0[tx + 32 * q];
+      m1[q] = c1[tx + 32 * q];
+      w0[q] = r0w[tx + 32 * q];
+      w1[q] = r1w[tx + 32 * q];
     }
-    const double r = refined_rcp(d);
-    // Columns c <= j take lc = 0 and rows i <= j take f = 0 (exact no-ops); rows i >= b,
-    // and columns c > i of the block, hold values that are never read again; row j of E
-    // vanishes right of j. So the updates run unmasked over the row groups that reach
-    // below j (uniform branches) and the column groups left of the diagonal.
+    const bool pair = j + 1 < b;
+    const double r0 = refined_rcp(d0);
+    const double g = x * r0;
+    const double d1 = e1 - x * g;
+    const double r1 = pair ? refined_rcp(d1) : 0.0;
+    // Columns c <= j (c <= j + 1 for the second) take zero factors and rows i <= j
+    // (i <= j + 1) zero multipliers: exact no-ops. Rows and columns past the block's
+    // diagonal hold values that are never read again, and E's rows vanish right of their
+    // index, so the updates run unmasked over the row groups that reach below j (uniform
+    // branches) and the column groups left of the diagonal.
 #pragma unroll
-    for (int q = 0; q < kCholQ; ++q) lc[q] = tx + 32 * q > j ? lc[q] * r : 0.0;
+    for (int q = 0; q < kCholQ; ++q) {
+      const int c = tx + 32 * q;
+      const double y1 = m1[q] - m0[q] * g;
+      m0[q] = c > j ? m0[q] * r0 : 0.0;
+      m1[q] = c > j + 1 ? y1 * r1 : 0.0;
+      w1[q] -= g * w0[q];
+    }
 #pragma unroll
     for (int p = 0; p < kCholP; ++p) {
       if (16 * p + 15 <= j) continue;
-      const double f = ty + 16 * p > j ? li[p] * r : 0.0;
+      const int i = ty + 16 * p;
+      const double y0 = l0[p], y1 = l1[p] - l0[p] * g;
+      const double f0 = i > j ? y0 * r0 : 0.0;
+      const double f1 = i > j + 1 ? y1 * r1 : 0.0;
 #pragma unroll
       for (int q = 0; q <= (p >> 1); ++q) {
-        v[p][q] -= li[p] * lc[q];
-        e[p][q] -= f * xr[q];
+        v[p][q] -= y0 * m0[q] + y1 * m1[q];
+        e[p][q] -= f0 * w0[q] + f1 * w1[q];
       }
     }
-    if (!(d > 0.0 && d < INFINITY)) {  // uniform: every thread read the same pivot
-      if (t == 0 && *info == 0) *info = (int)(k0 + j + 1);
+    // uniform: every thread read the same pivots
+    const bool bad0 = !(d0 > 0.0 && d0 < INFINITY), bad1 = pair && !(d1 > 0.0 && d1 < INFINITY);
+    if (bad0 || bad1) {
+      if (t == 0 && *info == 0) *info = (int)(k0 + j + (bad0 ? 1 : 2));
       return;
     }
-    if (t == 0) piv[j] = d;
-    const int jn = j + 1;
+    if (t == 0) {
+      piv[j] = d0;
+      if (pair) piv[j + 1] = d1;
+    }
+    const int jn = j + 2;
     if (jn < b) {
-      if (tx == (jn & 31)) {
+      const int nb = (step + 1) & 1;
 #pragma unroll
-        for (int q = 0; q < kCholQ; ++q)
-          if (q == (jn >> 5)) {
+      for (int h = 0; h < 2; ++h) {
+        const int cn = jn + h;  // column and E row published in slot h
+        if (cn >= kCholBlock) continue;
+        if (tx == (cn & 31)) {
 #pragma unroll
-            for (int p = 0; p < kCholP; ++p) {
-              const int i = ty + 16 * p;
-              if (i >= jn && i < b) col_buf[jn & 1][i] = v[p][q];
+          for (int q = 0; q < kCholQ; ++q)
+            if (q == (cn >> 5)) {
+#pragma unroll
+              for (int p = 0; p < kCholP; ++p)
+                if (ty + 16 * p >= jn) col_buf[nb][h][ty + 16 * p] = v[p][q];
             }
-          }
-      }
-      if (ty == (jn & 15)) {
+        }
+        if (ty == (cn & 15)) {
 #pragma unroll
-        for (int p = 0; p < kCholP; ++p)
-          if (p == (jn >> 4)) {
+          for (int p = 0; p < kCholP; ++p)
+            if (p == (cn >> 4)) {
 #pragma unroll
-            for (int q = 0; q < kCholQ; ++q) row_buf[jn & 1][tx + 32 * q] = e[p][q];
-          }
+              for (int q = 0; q < kCholQ; ++q) row_buf[nb][h][tx + 32 * q] = e[p][q];
+            }
+        }
       }
     }
   }
@@ -325,14 +357,14 @@ __global__ __launch_bounds__(kCholThreads) void eeq_cholesky_block_kernel(
     for (int q = 0; q < kCholQ; ++q) {
       const int c = tx + 32 * q;
       if (c >= b) continue;
-      double l = 0.0, x = 0.0;
+      double l = 0.0, y = 0.0;
       if (c <= i) {
         const double root = sqrt(piv[c]);
         l = c == i ? root : v[p][q] / root;
-        x = e[p][q] * rroot;
+        y = e[p][q] * rroot;
       }
       blk[i * lda + c] = l;
-      inv[i * b + c] = x;
+      inv[i * b + c] = y;
     }
   }
 }
