@@ -461,7 +461,7 @@ def bench_d4(steps: int, warmup: int, cpu: bool = True, graph: bool = True) -> d
     def step():
         pos = pos0.clone().requires_grad_(True)
         cell = cell0.clone().requires_grad_(True)
-        out = model.evaluate(z, pos, cell, pbc, n_atoms, charges=q)
+        out = model.evaluate(z, pos, cell, pbc, n_atoms, charges=q, fused_pair=True)
         gp, gc = torch.autograd.grad(out["energy"].sum(), [pos, cell])
         return out, gp, gc
 

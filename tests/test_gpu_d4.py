@@ -564,3 +564,42 @@ def test_tail_correction_restores_the_long_range_pair_sum(tables):
                          charges=qq.to(DEV))[0]["energy"][0])
         want = float(D_ab[a, b]) if a == b else float(D_ab[a, b] + D_ab[b, a])
         assert abs((ep - em) / (2 * h) - want) < 1e-6, (a, b)
+
+
+def test_fused_pair_matches_the_two_launch_path(tables):
+    """evaluate(fused_pair=True): the two-body energies from one pair-backward launch at unit
+    seeds (e_i = 1/2 alpha_i . dE/dalpha_i, the energy being bilinear in the polarizabilities)
+    and their gradients scaled by the structure seeds, against the energy launch plus the
+    autograd backward: two periodic structures of different size, seeds 2 and -3 on their
+    energies, cutoffs with a switching window and the three-body term off."""
+    import xnn_amd.dispersion as XD
+    _note("d4 fused pair vs two launches")
+    model = XD.DFTD4(tables, s9=0.0, cutoff_pair=12.0, cutoff_cn=9.0, cutoff_eeq_cn=9.0,
+                     switch_width_pair=1.0).to(DEV)
+    rng = np.random.default_rng(11)
+    zs, ps, cs, ns = [], [], [], []
+    for n, L in ((13, 7.5), (20, 8.5)):
+        zs.append(rng.choice([1, 6, 7, 8], size=n))
+        ps.append(rng.uniform(0.0, L, size=(n, 3)))
+        cs.append(np.diag([L, L + 0.4, L - 0.3]) + rng.normal(scale=0.2, size=(3, 3)))
+        ns.append(n)
+    z = torch.tensor(np.concatenate(zs), device=DEV)
+    pos0 = torch.tensor(np.concatenate(ps), dtype=torch.float64, device=DEV)
+    cell0 = torch.tensor(np.stack(cs), dtype=torch.float64, device=DEV)
+    pbc = torch.ones((2, 3), dtype=torch.bool)
+    n_atoms = torch.tensor(ns)
+    seed = torch.tensor([2.0, -3.0], dtype=torch.float64, device=DEV)
+    res = []
+    for fused in (False, True):
+        pos = pos0.clone().requires_grad_(True)
+        cell = cell0.clone().requires_grad_(True)
+        out = model.evaluate(z, pos, cell, pbc, n_atoms, fused_pair=fused)
+        gp, gc = torch.autograd.grad((out["energy"] * seed).sum(), [pos, cell])
+        res.append((out["energy"].detach(), out["node_energy"].detach(), gp, gc,
+                    out["node_energy"].requires_grad))
+    (e0, n0, gp0, gc0, _), (e1, n1, gp1, gc1, req1) = res
+    assert not req1
+    torch.testing.assert_close(e1, e0, rtol=1e-12, atol=1e-14)
+    torch.testing.assert_close(n1, n0, rtol=1e-10, atol=1e-14)
+    torch.testing.assert_close(gp1, gp0, rtol=1e-11, atol=1e-13)
+    torch.testing.assert_close(gc1, gc0, rtol=1e-11, atol=1e-13)

@@ -254,6 +254,51 @@ def _pair_backward(ctx, g_e2):
 d4_two_body_op.register_autograd(_pair_backward, setup_context=_pair_setup)
 
 
+class TwoBodyStructureEnergy(torch.autograd.Function):
+    """The two-body energies per structure (B,) and, detached, per atom (N,), with their
+    gradients, from one launch of the pair backward at unit seeds, as the reference's native
+    kernel returns energy and gradient together (``run_d4``, dispersion_fast/cpu.py:834-935).
+
+    The energy is bilinear in the polarizabilities (C6_ij = sum_w cp3(w) alpha_i(w)
+    alpha_j(w), the damping and the switch do not depend on them), and every pair gives half
+    to each of its atoms, so an atom's share is e_i = 1/2 sum_w alpha_i(w) dE/dalpha_i(w) with
+    dE/dalpha at unit seeds: the energy-only pair kernel is not needed. The backward scales
+    the stored gradients by each structure's seed, exact for any seed on the per-structure
+    energies; the per-atom energies carry no gradient."""
+
+    @staticmethod
+    def forward(ctx, pos, cell, alpha, species, batch32, node_ptr, images, plan, r4r2, params,
+                max_atoms):
+        dev, n, b = pos.device, pos.shape[0], node_ptr.shape[0] - 1
+        grad_pos = torch.empty((n, 3), dtype=torch.float64, device=dev)
+        part = torch.empty((n, 9), dtype=torch.float64, device=dev) if cell is not None else None
+        grad_alpha = torch.empty_like(alpha)
+        ones = torch.ones(n, dtype=torch.float64, device=dev)
+        ws, need = _workspace(n, b, max_atoms, dev)
+        _lib.call("xnn_d4_two_body_backward", _lib.ptr(pos), n, _lib.ptr(species),
+                  _lib.ptr(batch32), _lib.ptr(node_ptr), b, max_atoms, _lib.ptr(cell),
+                  _lib.ptr(images), _lib.ptr(plan), _lib.ptr(r4r2), _lib.ptr(alpha),
+                  _lib.D4PairParams(*params), _lib.ptr(ones), _lib.ptr(grad_pos), _lib.ptr(part),
+                  _lib.ptr(grad_alpha), _lib.ptr(ws), need, _lib.stream(dev))
+        from .ops import structure_sum_op
+        e2 = 0.5 * (alpha * grad_alpha).sum(1)
+        e2_b = structure_sum_op(e2, node_ptr, batch32)
+        ctx.save_for_backward(batch32, node_ptr, grad_pos, part, grad_alpha)
+        ctx.mark_non_differentiable(e2)
+        return e2_b, e2
+
+    @staticmethod
+    def backward(ctx, g_b, _g_e2):
+        batch32, node_ptr, grad_pos, part, grad_alpha = ctx.saved_tensors
+        gs = g_b.index_select(0, batch32.long())[:, None]   # each atom's structure seed
+        g_pos = grad_pos * gs if ctx.needs_input_grad[0] else None
+        g_cell = None
+        if part is not None and ctx.needs_input_grad[1]:
+            g_cell = _cell_grad(part, node_ptr, g_b.shape[0]) * g_b[:, None, None]
+        g_alpha = grad_alpha * gs if ctx.needs_input_grad[2] else None
+        return g_pos, g_cell, g_alpha, None, None, None, None, None, None, None, None
+
+
 def _alpha_tables(nref, ngw, refcn, refq, zeff, gi, refalpha, ga: float,
                   wf: float) -> "_lib.D4AlphaTables":
     return _lib.D4AlphaTables(nref.shape[0], _lib.ptr(nref), _lib.ptr(ngw), _lib.ptr(refcn),
@@ -726,10 +771,17 @@ class DFTD4(nn.Module):
     # ---- evaluation
     def evaluate(self, z: Tensor, pos: Tensor, cell: Optional[Tensor], pbc: Optional[Tensor],
                  n_atoms: Tensor, total_charge: Optional[Tensor] = None,
-                 charges: Optional[Tensor] = None) -> Dict[str, Tensor]:
+                 charges: Optional[Tensor] = None, fused_pair: bool = False) -> Dict[str, Tensor]:
         """Energies and D4 properties of a batch (atoms of a structure contiguous).
         ``cell`` (B, 3, 3) Angstrom or None; ``charges`` replaces the EEQ solve when
-        given. Differentiable once in ``pos`` and ``cell``."""
+        given. Differentiable once in ``pos`` and ``cell``.
+
+        ``fused_pair``: the two-body energies and their gradients come from one pair-kernel
+        launch (:class:`TwoBodyStructureEnergy`) instead of an energy launch in the forward
+        and a gradient launch in the backward; then only the per-structure energies
+        (``"energy"``, ``"energy_2body"``, ...) carry gradients and ``"node_energy"`` is
+        returned detached. For forces and stress from the structure energies (without
+        gradients wanted, the energy-only kernel runs as usual)."""
         if not pos.is_cuda:
             raise RuntimeError("xnn_amd D4 runs on the GPU (HIP kernels); there is no CPU path")
         dev = pos.device
@@ -771,8 +823,16 @@ class DFTD4(nn.Module):
         alpha = self.polarizabilities(zc, cn, q).contiguous()
         params = [self.s6, self.s8, self.a1, self.a2, self.cutoff_pair / BOHR,
                   self.switch_width_pair / BOHR]
-        e2 = d4_two_body_op(pos, cell64, alpha, species, batch32, node_ptr, images, plan,
-                            self.r4r2, params, max_atoms)
+        e2_b = None
+        wants_grad = torch.is_grad_enabled() and (
+            pos.requires_grad or (cell64 is not None and cell64.requires_grad))
+        if fused_pair and wants_grad:
+            e2_b, e2 = TwoBodyStructureEnergy.apply(pos, cell64, alpha, species, batch32,
+                                                    node_ptr, images, plan, self.r4r2, params,
+                                                    max_atoms)
+        else:
+            e2 = d4_two_body_op(pos, cell64, alpha, species, batch32, node_ptr, images, plan,
+                                self.r4r2, params, max_atoms)
         from .ops import structure_sum_op
         e3 = None
         if self.s9 != 0.0:
@@ -796,11 +856,20 @@ class DFTD4(nn.Module):
             if extra is not None:
                 node = node + extra
         node_energy = node * HARTREE
-        energy = structure_sum_op(node_energy, node_ptr, batch32)
-        zero = None if (e3 is not None and e_tail is not None) else energy.new_zeros(B)
+        zero = None if (e3 is not None and e_tail is not None) else node_energy.new_zeros(B)
         parts_sum = {k: (zero if t is None else structure_sum_op(t, node_ptr, batch32) * HARTREE)
                      for k, t in (("energy_3body", e3), ("energy_tail", e_tail))}
-        energy_2 = energy if node is e2 else structure_sum_op(e2, node_ptr, batch32) * HARTREE
+        if e2_b is not None:
+            # the structure totals from the fused two-body sums plus the other terms' sums
+            energy_2 = e2_b * HARTREE
+            energy = energy_2
+            for extra in (e3, e_tail):
+                if extra is not None:
+                    energy = energy + structure_sum_op(extra, node_ptr, batch32) * HARTREE
+            node_energy = node_energy.detach()
+        else:
+            energy = structure_sum_op(node_energy, node_ptr, batch32)
+            energy_2 = energy if node is e2 else structure_sum_op(e2, node_ptr, batch32) * HARTREE
         return {"node_energy": node_energy, "energy": energy, "energy_2body": energy_2,
                 **parts_sum,
                 "coordination_numbers": cn, "charges": q,
