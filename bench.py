@@ -763,10 +763,14 @@ def bench_atm(steps: int, warmup: int, cpu: bool = True) -> dict:
     consts = XD.ATMConstants(species.to(torch.int32), table, model.s9, model.alp / 3.0,
                              model.cutoff_triple / XD.BOHR, model.switch_width_triple / XD.BOHR)
 
+    node_ptr = torch.tensor([0, N], dtype=torch.int64, device=dev)
+    batch32 = torch.zeros(N, dtype=torch.int32, device=dev)
+
     def step():
+        # energies and gradients from one launch of the backward kernels at unit seeds
         v = vec.detach().requires_grad_(True)
         f = feat.detach().requires_grad_(True)
-        e = XD.atm_energy(ei, v, f, f, consts, N)
+        e, _ = XD.atm_structure_energy(ei, v, f, f, consts, node_ptr, batch32)
         gv, gf = torch.autograd.grad(e.sum(), [v, f])
         return e, gv, gf
 

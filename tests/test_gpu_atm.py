@@ -240,3 +240,46 @@ def test_atm_kernel_triangle_closed_forms(shape):
     prod = r1 * r2 * r3
     want = c6 ** 1.5 * (3 * cos[0] * cos[1] * cos[2] + 1) / prod ** 3 / (1 + 6 * (r0 ** 3 / prod) ** (16 / 3))
     np.testing.assert_allclose(e.cpu().numpy(), want / 3.0, rtol=1e-13)
+
+
+@pytest.mark.parametrize("same", [True, False])
+def test_atm_structure_energy_from_the_backward_launch(same):
+    """atm_structure_energy: per-structure energies and their gradients from one launch of
+    the ATM backward at unit seeds (each triangle's energy homogeneous of degree three in the
+    features: total = 1/3 sum_i (fa_i . dE/dfa_i + fb_i . dE/dfb_i)), against the energy
+    launch plus its backward: a periodic and a molecular structure in one batch, seeds 2 and
+    -1.5 on their energies; with shared factors (the D4 form) also the per-atom energies."""
+    from xnn_amd import dispersion as XD
+    dev = torch.device("cuda:0")
+    print(f"[gpu-case] atm structure energy, same={same}", flush=True)
+    c1, c2 = _case("small_cell", seed=4), _case("cluster", seed=5)
+    n1, n2 = c1["n"], c2["n"]
+    ei = torch.cat([c1["ei"], c2["ei"] + n1], 1).to(dev)
+    node_ptr = torch.tensor([0, n1, n1 + n2], dtype=torch.int64, device=dev)
+    batch32 = torch.cat([torch.zeros(n1), torch.ones(n2)]).to(device=dev, dtype=torch.int32)
+    seed = torch.tensor([2.0, -1.5], dtype=torch.float64, device=dev)
+    fa0 = torch.cat([c1["fa"], c2["fa"]]).to(dev)
+    consts = XD.ATMConstants(torch.cat([c1["species"], c2["species"]]).to(dev),
+                             c1["table"].to(dev), 1.0, 16.0 / 3.0, c1["cutoff"], c1["width"])
+    res = []
+    for fused in (False, True):
+        pos1, cell1, v1 = _geometry(c1, dev)
+        pos2, _, v2 = _geometry(c2, dev)
+        vec = torch.cat([v1, v2])
+        fa = fa0.clone().requires_grad_(True)
+        fb = fa if same else fa @ c1["mix"].to(dev)
+        if fused:
+            e_b, e_atom = XD.atm_structure_energy(ei, vec, fa, fb, consts, node_ptr, batch32)
+            assert not e_atom.requires_grad
+        else:
+            e_atom = XD.atm_energy(ei, vec, fa, fb, consts, n1 + n2)
+            e_b = torch.stack([e_atom[:n1].sum(), e_atom[n1:].sum()])
+        (e_b * seed).sum().backward()
+        res.append((e_b.detach(), e_atom.detach(), pos1.grad, cell1.grad, pos2.grad, fa.grad))
+    torch.cuda.synchronize()
+    ref, got = res
+    assert _rel(got[0].cpu(), ref[0].cpu()) < 1e-12
+    for a, b in zip(got[2:], ref[2:]):
+        assert _rel(a.cpu(), b.cpu()) < 1e-11
+    if same:
+        assert _rel(got[1].cpu(), ref[1].cpu()) < 1e-11

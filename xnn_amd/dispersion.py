@@ -469,6 +469,71 @@ def atm_energy(edge_index: Tensor, edge_vec: Tensor, feat_a: Tensor, feat_b: Ten
                           float(consts.width)], int(n_atoms), info[0], info[1])
 
 
+class ATMStructureEnergy(torch.autograd.Function):
+    """ATM energies per structure (B,) and, detached, per atom (N,), with their gradients,
+    from one launch of the ATM backward at unit seeds (no energy launch).
+
+    A triangle's energy goes with C9 = sqrt(C6_ij C6_jk C6_ik), each pair C6 bilinear in the
+    features, so it is homogeneous of degree one in each member atom's features (both
+    operands scaled together): an atom's share is e_i = 1/3 (feat_a_i . dE/dfeat_a_i +
+    feat_b_i . dE/dfeat_b_i) at unit seeds, and the structure total is their sum. The
+    backward scales the stored gradients by the structure seeds (an edge's by the seed of
+    its structure), exact for any seed on the per-structure energies."""
+
+    @staticmethod
+    def forward(ctx, plan, edge_vec, feat_a, feat_b, species, table, params, n_atoms, max_tiles,
+                has_repeats, edge_graph, node_ptr, batch32):
+        dev = edge_vec.device
+        n_edges, k = int(edge_vec.shape[0]), int(feat_a.shape[1])
+        g_vec = torch.empty_like(edge_vec)
+        g_fa = torch.empty_like(feat_a)
+        g_fb = torch.empty_like(feat_b)
+        ones = torch.ones(n_atoms, dtype=torch.float64, device=dev)
+        work = _atm_work(n_edges, n_atoms, k, True, dev)
+        _lib.call("xnn_atm_energy_backward", _lib.ptr(plan), n_edges, n_atoms, max_tiles,
+                  has_repeats, _lib.ptr(edge_vec), _lib.ptr(feat_a), _lib.ptr(feat_b), k,
+                  _lib.ptr(species), _lib.ptr(table), int(table.shape[0]), _atm_params(params),
+                  _lib.ptr(ones), _lib.ptr(g_vec), _lib.ptr(g_fa), _lib.ptr(g_fb),
+                  _lib.ptr(work), work.numel(), _lib.stream(dev))
+        from .ops import structure_sum_op
+        e = ((feat_a * g_fa).sum(1) + (feat_b * g_fb).sum(1)) / 3.0
+        e_b = structure_sum_op(e, node_ptr, batch32)
+        ctx.save_for_backward(g_vec, g_fa, g_fb, edge_graph, batch32)
+        ctx.mark_non_differentiable(e)
+        return e_b, e
+
+    @staticmethod
+    def backward(ctx, g_b, _g_e):
+        g_vec, g_fa, g_fb, edge_graph, batch32 = ctx.saved_tensors
+        ga = g_b.index_select(0, batch32.long())[:, None]
+        need = ctx.needs_input_grad
+        gv = g_vec * g_b.index_select(0, edge_graph)[:, None] if need[1] else None
+        return (None, gv, g_fa * ga if need[2] else None, g_fb * ga if need[3] else None) + \
+            (None,) * 9
+
+
+def atm_structure_energy(edge_index: Tensor, edge_vec: Tensor, feat_a: Tensor, feat_b: Tensor,
+                         consts: ATMConstants, node_ptr: Tensor,
+                         batch32: Tensor) -> Tuple[Tensor, Tensor]:
+    """ATM energies per structure (B,) with gradients and per atom (N,) detached, from one
+    launch of the ATM backward (:class:`ATMStructureEnergy`); arguments as
+    :func:`atm_energy`, plus the structures' atom ranges ``node_ptr`` (B + 1) and each atom's
+    structure ``batch32`` (N,). For forces and stress from the structure energies."""
+    if not edge_vec.is_cuda:
+        raise RuntimeError("xnn_amd ATM runs on the GPU (HIP kernels); there is no CPU path")
+    n_atoms = int(batch32.shape[0])
+    plan, info = atm_plan(edge_index, n_atoms)
+    f64 = torch.float64
+    dev = edge_vec.device
+    edge_graph = batch32.to(dev).long().index_select(0, edge_index[0].to(dev).long())
+    return ATMStructureEnergy.apply(
+        plan, edge_vec.to(f64).contiguous(), feat_a.to(f64).contiguous(),
+        feat_b.to(f64).contiguous(), consts.species.to(device=dev, dtype=torch.int32).contiguous(),
+        consts.table.to(device=dev, dtype=f64).contiguous(),
+        [float(consts.s9), float(consts.alp3), float(consts.cutoff), float(consts.width)],
+        n_atoms, info[0], info[1], edge_graph, node_ptr, batch32)
+
+
 def _ewald_rows(i0: int, i1: int, a: float, pos: Tensor, cell: Tensor, vol: Tensor,
                 recip: Tensor, rad: Tensor) -> Tensor:
     """Rows i0..i1 of the off-diagonal Ewald EEQ matrix (d4.py:608-680), see
@@ -834,9 +899,13 @@ class DFTD4(nn.Module):
             e2 = d4_two_body_op(pos, cell64, alpha, species, batch32, node_ptr, images, plan,
                                 self.r4r2, params, max_atoms)
         from .ops import structure_sum_op
-        e3 = None
+        e3, e3_b = None, None
         if self.s9 != 0.0:
-            e3 = self.three_body(zc, pos, cell64, pbc, n_atoms_h, cn)
+            if e2_b is not None:
+                e3_b, e3 = self.three_body(zc, pos, cell64, pbc, n_atoms_h, cn,
+                                           structures=(node_ptr, batch32))
+            else:
+                e3 = self.three_body(zc, pos, cell64, pbc, n_atoms_h, cn)
         e_tail = None
         if self.tail_correction and cell64 is not None:
             if periodic is None:
@@ -860,12 +929,14 @@ class DFTD4(nn.Module):
         parts_sum = {k: (zero if t is None else structure_sum_op(t, node_ptr, batch32) * HARTREE)
                      for k, t in (("energy_3body", e3), ("energy_tail", e_tail))}
         if e2_b is not None:
-            # the structure totals from the fused two-body sums plus the other terms' sums
+            # the structure totals from the fused two- and three-body sums plus the tail's
             energy_2 = e2_b * HARTREE
             energy = energy_2
-            for extra in (e3, e_tail):
-                if extra is not None:
-                    energy = energy + structure_sum_op(extra, node_ptr, batch32) * HARTREE
+            if e3_b is not None:
+                parts_sum["energy_3body"] = e3_b * HARTREE
+                energy = energy + parts_sum["energy_3body"]
+            if e_tail is not None:
+                energy = energy + parts_sum["energy_tail"]
             node_energy = node_energy.detach()
         else:
             energy = structure_sum_op(node_energy, node_ptr, batch32)
@@ -922,11 +993,13 @@ class DFTD4(nn.Module):
         return (6.0 / vol) * (alpha * cp_weights(alpha) * field.index_select(0, z)).sum(-1)
 
     def three_body(self, z: Tensor, pos: Tensor, cell64: Optional[Tensor], pbc: Optional[Tensor],
-                   counts: List[int], cn: Tensor) -> Tensor:
+                   counts: List[int], cn: Tensor, structures: Optional[Tuple[Tensor, Tensor]] = None):
         """Per-atom ATM energies (hartree, d4.py:1268-1298): C6 from the polarizabilities
         of the neutral atoms (q = 0), damping radii ``a1 sqrt(3 Q_A Q_B) + a2``, exponent
         ``alp / 3``, edges of the radius graph within ``cutoff_triple``; the HIP
-        triplet kernels (:func:`atm_energy`), over the species present."""
+        triplet kernels (:func:`atm_energy`), over the species present. With
+        ``structures = (node_ptr, batch32)``: (per-structure energies with gradients,
+        per-atom energies detached) from :func:`atm_structure_energy`."""
         uniq, species = torch.unique(z, return_inverse=True)
         species = species.to(torch.int32).contiguous()
         alpha0 = self.polarizabilities(z, cn, torch.zeros_like(cn))
@@ -936,6 +1009,8 @@ class DFTD4(nn.Module):
         table = self.a1 * torch.sqrt(3.0 * q4[:, None] * q4[None, :]) + self.a2
         consts = ATMConstants(species, table, self.s9, self.alp / 3.0, self.cutoff_triple / BOHR,
                               self.switch_width_triple / BOHR)
+        if structures is not None:
+            return atm_structure_energy(edge_index, vec, feat, feat, consts, *structures)
         return atm_energy(edge_index, vec, feat, feat, consts, pos.shape[0])
 
     def forward(self, data) -> Dict[str, Tensor]:
