@@ -628,7 +628,7 @@ def bench_d3(steps: int, warmup: int, cpu: bool = True) -> dict:
     def step():
         pos = pos0.clone().requires_grad_(True)
         cell = cell0.clone().requires_grad_(True)
-        out = model.evaluate(z, pos, cell, pbc, n_atoms)
+        out = model.evaluate(z, pos, cell, pbc, n_atoms, fused_pair=True)
         gp, gc = torch.autograd.grad(out["energy"].sum(), [pos, cell])
         return out, gp, gc
 

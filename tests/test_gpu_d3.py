@@ -191,3 +191,42 @@ def test_three_body_matches_oracle(tables, periodic):
     for a, b in zip(got, ref):
         a = a.reshape(b.shape).detach().cpu() / XD.HARTREE
         np.testing.assert_allclose(a, b, atol=1e-11 * float(b.abs().max()))
+
+
+@pytest.mark.parametrize("damping", ["bj", "zero"])
+def test_fused_pair_matches_the_two_launch_path(tables, damping):
+    """evaluate(fused_pair=True): the two-body energies from one pair-backward launch at unit
+    seeds (e_i = 1/2 w_i . dE/dw_i, bilinear in the reference weights) and their gradients
+    scaled by the structure seeds, against the energy launch plus the autograd backward: two
+    periodic structures, seeds 2 and -3, a switching window."""
+    import xnn_amd.dispersion as XD
+    _note(f"d3 fused pair vs two launches, {damping}")
+    model = XD.DFTD3(tables, damping=damping, cutoff_pair=12.0, cutoff_cn=8.0,
+                     switch_width_pair=1.0).to(DEV)
+    rng = np.random.default_rng(12)
+    zs, ps, cs, ns = [], [], [], []
+    for n, L in ((14, 7.5), (19, 8.5)):
+        zs.append(rng.choice([1, 6, 7, 8], size=n))
+        ps.append(rng.uniform(0.0, L, size=(n, 3)))
+        cs.append(np.diag([L, L + 0.4, L - 0.3]) + rng.normal(scale=0.2, size=(3, 3)))
+        ns.append(n)
+    z = torch.tensor(np.concatenate(zs), device=DEV)
+    pos0 = torch.tensor(np.concatenate(ps), dtype=torch.float64, device=DEV)
+    cell0 = torch.tensor(np.stack(cs), dtype=torch.float64, device=DEV)
+    pbc = torch.ones((2, 3), dtype=torch.bool)
+    n_atoms = torch.tensor(ns)
+    seed = torch.tensor([2.0, -3.0], dtype=torch.float64, device=DEV)
+    res = []
+    for fused in (False, True):
+        pos = pos0.clone().requires_grad_(True)
+        cell = cell0.clone().requires_grad_(True)
+        out = model.evaluate(z, pos, cell, pbc, n_atoms, fused_pair=fused)
+        gp, gc = torch.autograd.grad((out["energy"] * seed).sum(), [pos, cell])
+        res.append((out["energy"].detach(), out["node_energy"].detach(), gp, gc,
+                    out["node_energy"].requires_grad))
+    (e0, n0, gp0, gc0, _), (e1, n1, gp1, gc1, req1) = res
+    assert not req1
+    torch.testing.assert_close(e1, e0, rtol=1e-12, atol=1e-14)
+    torch.testing.assert_close(n1, n0, rtol=1e-10, atol=1e-14)
+    torch.testing.assert_close(gp1, gp0, rtol=1e-11, atol=1e-13)
+    torch.testing.assert_close(gc1, gc0, rtol=1e-11, atol=1e-13)

@@ -1276,6 +1276,47 @@ def _d3pair_backward(ctx, g_e2):
 d3_two_body_op.register_autograd(_d3pair_backward, setup_context=_d3pair_setup)
 
 
+class D3TwoBodyStructureEnergy(torch.autograd.Function):
+    """D3 two-body energies per structure (B,) and, detached, per atom (N,), with their
+    gradients, from one launch of the pair backward at unit seeds: C6_ij = sum_ab w_ia w_jb
+    C6ref_ab is bilinear in the reference weights and the damping radii do not depend on
+    them, so an atom's share is e_i = 1/2 w_i . dE/dw_i. The backward scales the stored
+    gradients by the structure seeds (as :class:`TwoBodyStructureEnergy`)."""
+
+    @staticmethod
+    def forward(ctx, pos, cell, weights, species, batch32, node_ptr, images, r4r2, rvdw, c6ref,
+                params, max_atoms):
+        dev, n, b = pos.device, pos.shape[0], node_ptr.shape[0] - 1
+        grad_pos = torch.empty((n, 3), dtype=torch.float64, device=dev)
+        part = torch.empty((n, 9), dtype=torch.float64, device=dev) if cell is not None else None
+        grad_w = torch.empty_like(weights)
+        ones = torch.ones(n, dtype=torch.float64, device=dev)
+        ws, need = _workspace(n, b, max_atoms, dev)
+        _lib.call("xnn_d3_two_body_backward", _lib.ptr(pos), n, _lib.ptr(species),
+                  _lib.ptr(batch32), _lib.ptr(node_ptr), b, max_atoms, _lib.ptr(cell),
+                  _lib.ptr(images), _lib.ptr(r4r2), _lib.ptr(rvdw), _lib.ptr(c6ref),
+                  r4r2.shape[0], _lib.ptr(weights), _d3_params(params), _lib.ptr(ones),
+                  _lib.ptr(grad_pos), _lib.ptr(part), _lib.ptr(grad_w), _lib.ptr(ws), need,
+                  _lib.stream(dev))
+        from .ops import structure_sum_op
+        e2 = 0.5 * (weights * grad_w).sum(1)
+        e2_b = structure_sum_op(e2, node_ptr, batch32)
+        ctx.save_for_backward(batch32, node_ptr, grad_pos, part, grad_w)
+        ctx.mark_non_differentiable(e2)
+        return e2_b, e2
+
+    @staticmethod
+    def backward(ctx, g_b, _g_e2):
+        batch32, node_ptr, grad_pos, part, grad_w = ctx.saved_tensors
+        gs = g_b.index_select(0, batch32.long())[:, None]
+        g_pos = grad_pos * gs if ctx.needs_input_grad[0] else None
+        g_cell = None
+        if part is not None and ctx.needs_input_grad[1]:
+            g_cell = _cell_grad(part, node_ptr, g_b.shape[0]) * g_b[:, None, None]
+        g_w = grad_w * gs if ctx.needs_input_grad[2] else None
+        return (g_pos, g_cell, g_w) + (None,) * 9
+
+
 def _batch_layout(n_atoms: Tensor, dev) -> Tuple[List[int], Tensor, Tensor]:
     counts = [int(x) for x in n_atoms.cpu()]
     node_ptr, batch32 = _batch_tensors(counts, dev)
@@ -1342,7 +1383,9 @@ class DFTD3(nn.Module):
                              self.k_nref, self.k_refcn)
 
     def evaluate(self, z: Tensor, pos: Tensor, cell: Optional[Tensor], pbc: Optional[Tensor],
-                 n_atoms: Tensor) -> Dict[str, Tensor]:
+                 n_atoms: Tensor, fused_pair: bool = False) -> Dict[str, Tensor]:
+        """Energies of a batch; ``fused_pair`` as in :meth:`DFTD4.evaluate` (the two-body
+        energies and gradients from one launch; ``"node_energy"`` then detached)."""
         if not pos.is_cuda:
             raise RuntimeError("xnn_amd D3 runs on the GPU (HIP kernels); there is no CPU path")
         dev = pos.device
@@ -1364,15 +1407,26 @@ class DFTD3(nn.Module):
         params = [self.s6, self.s8, self.a1, self.a2, self.rs6, self.rs8, self.alp, self.bet,
                   self.cutoff_pair / BOHR, self.switch_width_pair / BOHR,
                   float(D3_DAMPINGS[self.damping])]
-        e2 = d3_two_body_op(pos.contiguous(), cell64, w, species, batch32, node_ptr, images,
-                            self.r4r2, self.rvdw.contiguous(), self.c6pair, params, max_atoms)
+        wants_grad = torch.is_grad_enabled() and (
+            pos.requires_grad or (cell64 is not None and cell64.requires_grad))
+        e2_b = None
+        if fused_pair and wants_grad:
+            e2_b, e2 = D3TwoBodyStructureEnergy.apply(
+                pos.contiguous(), cell64, w, species, batch32, node_ptr, images, self.r4r2,
+                self.rvdw.contiguous(), self.c6pair, params, max_atoms)
+        else:
+            e2 = d3_two_body_op(pos.contiguous(), cell64, w, species, batch32, node_ptr, images,
+                                self.r4r2, self.rvdw.contiguous(), self.c6pair, params, max_atoms)
         from .ops import structure_sum_op
         e3 = torch.zeros_like(e2)
         if self.s9 != 0.0:
             e3 = self.three_body(s.to(dev), w, pos, cell64, pbc, counts)
-        energy_2 = structure_sum_op(e2, node_ptr, batch32)
+        energy_2 = structure_sum_op(e2, node_ptr, batch32) if e2_b is None else e2_b
         energy_3 = structure_sum_op(e3, node_ptr, batch32)
-        return {"node_energy": (e2 + e3) * HARTREE, "energy": (energy_2 + energy_3) * HARTREE,
+        node_energy = (e2 + e3) * HARTREE
+        if e2_b is not None:
+            node_energy = node_energy.detach()
+        return {"node_energy": node_energy, "energy": (energy_2 + energy_3) * HARTREE,
                 "energy_2body": energy_2 * HARTREE, "energy_3body": energy_3 * HARTREE,
                 "coordination_numbers": cn, "weights": w}
 
