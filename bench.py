@@ -76,6 +76,9 @@ def kernel_costs(E: int, N: int, C: int, L: int = 16, K: int = 8, grouped: bool 
         "xnn_sh_radial_message_energy_backward": {         # the rows' cotangent g_i U in-kernel
             "bytes": E * (12 + perm + 12) + N * 4 + 4 * C * L,   # vec in, g_vec out; ptr; U
             "flops": E * 2 * C * (2 * K + 2 * L)},
+        "xnn_sh_radial_message_energy_forces": {           # the backward, + each edge's share
+            "bytes": E * (12 + perm + 12 + 4) + N * 4 + 4 * C * L,   # of E_i out (no forward)
+            "flops": E * 2 * C * (2 * K + 2 * L)},
         "xnn_sh_radial_message_sum": {                     # radial basis evaluated in-kernel
             "bytes": E * (12 + perm) + N * (4 * C * L + 4),
             "flops": E * 2 * C * (K + L)},
@@ -106,6 +109,9 @@ def step_bytes(E: int, N: int, C: int, L: int, K: int, msg: str) -> int:
     A), its backward (writes d_A), message backward, featurizer backward, force reduction.
     With the readout in the message kernels no (N, C, L) rows exist."""
     kc = kernel_costs(E, N, C, L, K)
+    if msg == "xnn_sh_radial_message_energy_forces":     # one launch: energies and forces
+        return (E * 24 + N * 12 + kc[msg]["bytes"] + E * 4 + N * 4
+                + kc["xnn_edge_force_reduce"]["bytes"])
     if msg == "xnn_sh_radial_message_energy":
         return (E * 24 + N * 12 + kc[msg]["bytes"] + kc[msg + "_backward"]["bytes"]
                 + kc["xnn_edge_force_reduce"]["bytes"])
@@ -151,13 +157,19 @@ def message_launches(msg: str, g, model, kw: dict) -> dict:
     head = (_lib.XNN_F32, _lib.ptr(vec), None, N, None, 0, None, None, None, E,
             _lib.ptr(plan.ptr_dst), _lib.ptr(plan.perm_dst))
     keep = (vec, W, d_out, out, g_vec, table, plan)
-    if msg == "xnn_sh_radial_message_energy":
+    if msg in ("xnn_sh_radial_message_energy", "xnn_sh_radial_message_energy_forces"):
         U = model.U.detach().float().reshape(-1).contiguous()
         z = g.atomic_numbers.to(torch.int64).contiguous()
         bias = model.atom_ref.detach().float().contiguous()
         energy = torch.empty(N, device=vec.device)
         g_node = torch.full((1,), -1.0, device=vec.device)          # the forces' seed
         keep = keep + (U, z, bias, energy, g_node)
+        if msg.endswith("_forces"):                  # the one launch of a one-pass step
+            edge_energy = torch.empty(E, device=vec.device)
+            keep = keep + (edge_energy,)
+            return {msg: (head + (prm, _lib.ptr(table), C, _lib.ptr(W), _lib.ptr(U),
+                                  _lib.ptr(g_node), 0, _lib.ptr(g_vec), _lib.ptr(edge_energy), s),
+                          keep)}
         return {msg: (head + (prm, _lib.ptr(table), C, _lib.ptr(W), _lib.ptr(U), _lib.ptr(z),
                               _lib.ptr(bias), bias.shape[0], _lib.ptr(energy), s), keep),
                 msg + "_backward": (head + (prm, _lib.ptr(table), C, _lib.ptr(W), _lib.ptr(U),
@@ -249,6 +261,8 @@ def build_workload(config: str, device):
         g = xa.AtomicGraph(pos=pos, atomic_numbers=z, edge_index=ei, cell_shifts=sh, batch=batch,
                            n_atoms=n_atoms)
     model = xa.ShEdgePotential(cutoff=rc, species=(1, 6, 7, 8, 18), seed=0, **kw).to(device)
+    # energies and gradients from one launch of the readout backward (no forward launch)
+    model.one_pass = True
     return g, model, rc, kw, workload, nl_ms, structs
 
 
@@ -890,12 +904,15 @@ def main() -> None:
         out = step()
     # the message entry point the step took (radial basis in the kernel, linear layer in
     # the kernel, or the linear layer in PyTorch)
-    msg = next(m for m in ("xnn_sh_radial_message_energy", "xnn_sh_radial_message_sum",
+    # (or, one pass: energies and forces from the readout backward alone)
+    msg = next(m for m in ("xnn_sh_radial_message_energy_forces",
+                           "xnn_sh_radial_message_energy", "xnn_sh_radial_message_sum",
                            "xnn_sh_linear_message_sum", "xnn_sh_message_sum")
                if _lib.calls.get(m))
     fused = msg != "xnn_sh_message_sum"
-    kernels = [msg, msg + "_backward", "xnn_edge_featurize", "xnn_edge_featurize_backward",
-               "xnn_edge_force_reduce"]
+    kernels = ([msg] if msg.endswith("_forces") else [msg, msg + "_backward"]) + \
+        ["xnn_edge_featurize", "xnn_edge_featurize_backward", "xnn_edge_force_reduce",
+         "xnn_edge_force_reduce_virial"]
     # eager pass: per-kernel HIP events on the launch stream
     _lib.timed.clear()
     _lib.time_launches(*kernels)

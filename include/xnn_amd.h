@@ -247,6 +247,34 @@ int xnn_sh_radial_message_energy_backward(int geom_dtype, const float* vec_in, c
                                           const float* W, const float* U, const float* g,
                                           int64_t g_stride, float* g_vec, xnn_stream_t stream);
 
+/* xnn_sh_radial_message_energy_backward that also writes each edge's share of its receiver's
+ * readout, edge_energy[e] = (phi_e U) . Y_e (E) f32 (the unscaled dY of the backward against
+ * the edge's harmonics), so that node_energy[i] = bias[z[i]] + sum_{dst(e)=i} edge_energy[e]
+ * without the forward launch: energies and forces from one pass, as the reference's fused
+ * energy-and-force evaluations return them (gnn/fast/conv.py:137-143 with the readout of
+ * common/models/base.py:161-180). g_vec is the gradient for the cotangent g as in the
+ * backward; a receiver's edges scale with its own cotangent. */
+int xnn_sh_radial_message_energy_forces(int geom_dtype, const float* vec_in, const void* pos,
+                                        int64_t n_nodes, const void* cell, int64_t n_graphs,
+                                        const int32_t* batch, const int32_t* src,
+                                        const int32_t* shift, int64_t n_edges,
+                                        const int32_t* ptr_dst, const int32_t* perm_dst,
+                                        const xnn_featurize_params* prm,
+                                        const float* rbf_table, int32_t n_channels,
+                                        const float* W, const float* U, const float* g,
+                                        int64_t g_stride, float* g_vec, float* edge_energy,
+                                        xnn_stream_t stream);
+
+/* Node energies from the edges' shares of xnn_sh_radial_message_energy_forces:
+ * node_energy[i] = bias[z[i]] + sum over the CSR row i (ptr_dst, perm_dst as for the message
+ * kernels) of edge_energy, f32; bias NULL: none; an index z outside [0, n_bias) gives NaN.
+ * The readout's aggregation of a fused energy-and-force pass (common/models/base.py:161-180);
+ * the reference forms it from the forward's rows instead. */
+int xnn_node_energy_from_edges(const float* edge_energy, const int32_t* ptr_dst,
+                               const int32_t* perm_dst, int64_t n_nodes, const int64_t* z,
+                               const float* bias, int64_t n_bias, float* node_energy,
+                               xnn_stream_t stream);
+
 /* Backward of xnn_sh_radial_message_sum with respect to the edge vectors, through the
  * harmonics and the radial basis: g_vec (E,3) f32 = dL/dr_e (written, not added).
  * Parameter gradients (W, rbf_table) are not formed: the caller uses

@@ -519,6 +519,25 @@ def test_sh_radial_message_energy_forward_backward(C, l_max, K, radial, envelope
     np.testing.assert_allclose((E - E0).detach().cpu(), bias[z].cpu(), atol=1e-5)
     E_bad = emb.radial_message_energy(vec.detach(), W, U, torch.full_like(z, 99), bias, g.plan(), sign)
     assert torch.isnan(E_bad).all()
+    # one pass (energies and gradients from the backward launch alone): the same energies
+    # to float32 rounding; gradients for a per-atom cotangent, a broadcast one and the
+    # forces' cached -1 seed, against the forward + backward launches
+    from xnn_amd.outputs import _minus_one
+    E1 = emb.radial_message_energy(vec, W, U, z, bias, g.plan(), sign, one_pass=True)
+    np.testing.assert_allclose(E1.detach().cpu(), E.detach().cpu(), atol=2e-6 * e_scale)
+    (g1,) = torch.autograd.grad((E1 * gi).sum(), (vec,))
+    np.testing.assert_allclose(g1.cpu(), gvec.cpu(), atol=1e-6 * g_scale)
+    for seed in (torch.full((1,), 2.5, device=DEV).expand(E.shape[0]),
+                 _minus_one(E).expand(E.shape[0])):
+        (g1,) = torch.autograd.grad(
+            [emb.radial_message_energy(vec, W, U, z, bias, g.plan(), sign, one_pass=True)],
+            [vec], grad_outputs=[seed])
+        (g0,) = torch.autograd.grad([emb.radial_message_energy(vec, W, U, z, bias, g.plan(), sign)],
+                                    [vec], grad_outputs=[seed])
+        np.testing.assert_allclose(g1.cpu(), g0.cpu(), atol=1e-6 * g_scale * 2.5)
+    E1_bad = emb.radial_message_energy(vec, W, U, torch.full_like(z, 99), bias, g.plan(), sign,
+                                       one_pass=True)
+    assert torch.isnan(E1_bad).all()
 
 
 def test_force_reduce_visit_order_keeps_every_sum():
@@ -854,7 +873,10 @@ def _float32_floor(R, g, params, cpu_pos, cell, ref, err):
                                           ("ragged_1024", "radial"),
                                           ("nequip_molecules", "radial"),
                                           ("nequip_molecules", "unfused"),
-                                          ("periodic_batch", "radial")])
+                                          ("periodic_batch", "radial"),
+                                          ("water", "one_pass"), ("argon", "one_pass"),
+                                          ("ragged", "one_pass"),
+                                          ("periodic_batch", "one_pass")])
 def test_model_energy_forces_stress(config, fused):
     import oracle.reference as R
     import xnn_amd as xa
@@ -890,17 +912,24 @@ def test_model_energy_forces_stress(config, fused):
     g.pos = g.pos.float()
     if g.cell is not None:
         g.cell = g.cell.float()
+    # one_pass: the readout path with energies and gradients from one backward launch
     model = xa.ShEdgePotential(cutoff=rc, species=(1, 6, 7, 8, 18),
                                fused_linear=fused != "unfused",
-                               fused_radial=fused in ("radial", "radial_rows"),
-                               fused_readout=fused == "radial", **kw).to(DEV)
+                               fused_radial=fused in ("radial", "radial_rows", "one_pass"),
+                               fused_readout=fused in ("radial", "one_pass"), **kw).to(DEV)
+    model.one_pass = fused == "one_pass"
     before = dict(_lib.calls)
     out = xa.ForceStressOutput(model, compute_stress=g.cell is not None).eval()(g)
     msg = {"radial": "xnn_sh_radial_message_energy", "radial_rows": "xnn_sh_radial_message_sum",
-           "linear": "xnn_sh_linear_message_sum", "unfused": "xnn_sh_message_sum"}[fused]
-    ran = [msg, msg + "_backward", "xnn_edge_featurize"]
-    if fused not in ("radial", "radial_rows"):
+           "linear": "xnn_sh_linear_message_sum", "unfused": "xnn_sh_message_sum",
+           "one_pass": "xnn_sh_radial_message_energy"}[fused]
+    ran = ([msg + "_forces"] if fused == "one_pass" else [msg, msg + "_backward"]) + \
+        ["xnn_edge_featurize"]
+    if fused not in ("radial", "radial_rows", "one_pass"):
         ran.append("xnn_edge_featurize_backward")
+    if fused == "one_pass":
+        for name in (msg, msg + "_backward"):
+            assert _lib.calls.get(name, 0) == before.get(name, 0), f"{name} ran"
     for name in ran:
         assert _lib.calls.get(name, 0) > before.get(name, 0), f"{name} did not run"
     # one structure: the force reduction finishes the strain derivative in the same launch

@@ -131,6 +131,10 @@ _SIGNATURES = {
     "xnn_sh_radial_message_energy_backward": [c_int, vp, vp, i64, vp, i64, vp, vp, vp, i64, vp,
                                               vp, ctypes.POINTER(FeaturizeParams), vp, i32, vp,
                                               vp, vp, i64, vp, vp],
+    "xnn_sh_radial_message_energy_forces": [c_int, vp, vp, i64, vp, i64, vp, vp, vp, i64, vp,
+                                            vp, ctypes.POINTER(FeaturizeParams), vp, i32, vp,
+                                            vp, vp, i64, vp, vp, vp],
+    "xnn_node_energy_from_edges": [vp, vp, vp, i64, vp, vp, i64, vp, vp],
     "xnn_radial_hidden": [vp, i64, c_int, c_int, vp, vp, vp, vp, vp],
     "xnn_radial_hidden_backward": [vp, vp, i64, c_int, c_int, vp, vp, vp, vp, vp],
     "xnn_uvu_conv": [vp, i64, i32, vp, i32, vp, i64, i32, vp, vp, i64, vp, vp, vp, i32, vp, i32,

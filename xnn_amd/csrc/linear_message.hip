@@ -321,7 +321,8 @@ __global__ __launch_bounds__(256, 3) void lin_msg_bwd_kernel(
     const int32_t* __restrict__ perm, int64_t n_nodes, float sign, int K,
     const float* __restrict__ h, Radial<float> R, const float* __restrict__ W,
     const float* __restrict__ d_out, float* __restrict__ d_h, float* __restrict__ g_vec,
-    const float* __restrict__ U, const float* __restrict__ g_node, int64_t g_stride) {
+    const float* __restrict__ U, const float* __restrict__ g_node, int64_t g_stride,
+    float* __restrict__ edge_energy) {
   constexpr int L = ShDims<LMAX>::L;
   constexpr int C = 16 * T;
   constexpr int KS = (L + 3) / 4;
@@ -600,6 +601,16 @@ __global__ __launch_bounds__(256, 3) void lin_msg_bwd_kernel(
         float dY[L];
 #pragma unroll
         for (int m = 0; m < L; ++m) dY[m] = sdy[lane * kSY + m];
+        if constexpr (RO) {
+          // the edge's share of its receiver's <U, A_i>: (phi_e U) . Y_e, the unscaled dY
+          // against the edge's harmonics (still in its LDS row)
+          if (edge_energy != nullptr) {
+            float se = 0.f;
+#pragma unroll
+            for (int m = 0; m < L; ++m) se = fmaf(dY[m], ys[lane * kSY + m], se);
+            edge_energy[my_e] = se;
+          }
+        }
         float Gx, Gy, Gz, vx, vy, vz;
         sh_grad<LMAX, float>(ux, uy, uz, dY, Gx, Gy, Gz);
         sh_chain<float>(ux, uy, uz, inv, Gx, Gy, Gz, vx, vy, vz);
@@ -633,6 +644,7 @@ struct Readout {
   int64_t n_bias = 0;
   const float* g = nullptr;       // backward: per-atom cotangent of E_i
   int64_t g_stride = 1;
+  float* edge_energy = nullptr;   // backward: each edge's share of <U, A_i> (may be NULL)
 };
 
 template <typename G, bool RAD, bool RO>
@@ -656,7 +668,7 @@ static void lin_msg_launch(bool backward, const float* vec, const void* pos, int
       const dim3 grid((unsigned)resident_blocks((const void*)k, block.x, blocks_needed));      \
       hipLaunchKernelGGL(k, grid, block, 0, stream, vec, (const G*)pos, (const G*)cell,        \
                          n_graphs, batch, src, shift, ptr, perm, n_nodes, sg, K, h, R, W,       \
-                         d_out, out_or_dh, g_vec, ro.U, ro.g, ro.g_stride);                    \
+                         d_out, out_or_dh, g_vec, ro.U, ro.g, ro.g_stride, ro.edge_energy);    \
     } else {                                                                                   \
       auto k = lin_msg_fwd_kernel<G, LM, TT, RAD, RO>;                                         \
       const dim3 grid((unsigned)resident_blocks((const void*)k, block.x, blocks_needed));      \
@@ -896,6 +908,44 @@ int xnn_sh_radial_message_energy_backward(int geom_dtype, const float* vec_in, c
   ro.U = U;
   ro.g = g;
   ro.g_stride = g_stride;
+  if (geom_dtype == XNN_F32)
+    return lin_msg<float>(true, vec_in, pos, n_nodes, cell, n_graphs, batch, src, shift, ptr_dst,
+                          perm_dst, prm->l_max, prm->sh_sign, R.K, n_channels, nullptr, &R, W,
+                          nullptr, nullptr, g_vec, as_hip(stream), &ro, n_edges);
+  if (geom_dtype == XNN_F64)
+    return lin_msg<double>(true, vec_in, pos, n_nodes, cell, n_graphs, batch, src, shift,
+                           ptr_dst, perm_dst, prm->l_max, prm->sh_sign, R.K, n_channels, nullptr,
+                           &R, W, nullptr, nullptr, g_vec, as_hip(stream), &ro, n_edges);
+  set_error("unsupported geometry dtype %d", geom_dtype);
+  return XNN_EINVAL;
+}
+
+int xnn_sh_radial_message_energy_forces(int geom_dtype, const float* vec_in, const void* pos,
+                                        int64_t n_nodes, const void* cell, int64_t n_graphs,
+                                        const int32_t* batch, const int32_t* src,
+                                        const int32_t* shift, int64_t n_edges,
+                                        const int32_t* ptr_dst, const int32_t* perm_dst,
+                                        const xnn_featurize_params* prm,
+                                        const float* rbf_table, int32_t n_channels,
+                                        const float* W, const float* U, const float* g,
+                                        int64_t g_stride, float* g_vec, float* edge_energy,
+                                        xnn_stream_t stream) {
+  Radial<float> R;
+  int st = make_radial<float>(prm, rbf_table, R);
+  if (st != XNN_OK) return st;
+  st = lin_check(n_nodes, n_edges, prm->l_max, prm->sh_sign, prm->n_rbf, n_channels);
+  if (st != XNN_OK) return st;
+  XNN_REQUIRE(n_nodes == 0 || (ptr_dst && g && W && U), "NULL CSR, weights or cotangent");
+  XNN_REQUIRE(g_stride == 0 || g_stride == 1, "g_stride must be 0 (broadcast) or 1");
+  XNN_REQUIRE(n_edges == 0 || ((vec_in || (pos && src && shift)) && g_vec && edge_energy),
+              "NULL edge input or output");
+  XNN_REQUIRE(cell == nullptr || n_graphs <= 1 || batch != nullptr,
+              "several cells need the batch vector");
+  Readout ro;
+  ro.U = U;
+  ro.g = g;
+  ro.g_stride = g_stride;
+  ro.edge_energy = edge_energy;
   if (geom_dtype == XNN_F32)
     return lin_msg<float>(true, vec_in, pos, n_nodes, cell, n_graphs, batch, src, shift, ptr_dst,
                           perm_dst, prm->l_max, prm->sh_sign, R.K, n_channels, nullptr, &R, W,

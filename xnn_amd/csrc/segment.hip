@@ -969,6 +969,24 @@ static int sh_msg(bool backward, const float* vec, const void* pos, int64_t n_no
   return XNN_OK;
 }
 
+// node_energy[i] = bias[z[i]] + sum over the receiver row i of edge_energy (CSR order),
+// one thread per atom; an index z outside [0, n_bias) gives NaN; no bias: 0
+__global__ __launch_bounds__(256) void node_energy_from_edges_kernel(
+    const float* __restrict__ edge_energy, const int32_t* __restrict__ ptr,
+    const int32_t* __restrict__ perm, int64_t n_nodes, const int64_t* __restrict__ z,
+    const float* __restrict__ bias, int64_t n_bias, float* __restrict__ out) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n_nodes) return;
+  float s = 0.f;
+  if (bias != nullptr) {
+    const int64_t zi = z[i];
+    s = (zi >= 0 && zi < n_bias) ? bias[zi] : __builtin_nanf("");
+  }
+  const int32_t b = ptr[i], e = ptr[i + 1];
+  for (int32_t k = b; k < e; ++k) s += edge_energy[perm ? perm[k] : k];
+  out[i] = s;
+}
+
 template <typename T>
 static int segment_sum_t(const void* src, int64_t F, const int32_t* ptr, const int32_t* perm,
                          int64_t n_seg, void* out, hipStream_t stream) {
@@ -1092,6 +1110,21 @@ int xnn_segment_sum(int dtype, const void* src, int64_t n_rows, int64_t n_featur
     return segment_sum_t<double>(src, n_features, ptr, perm, n_segments, out, as_hip(stream));
   set_error("unsupported dtype %d", dtype);
   return XNN_EINVAL;
+}
+
+int xnn_node_energy_from_edges(const float* edge_energy, const int32_t* ptr_dst,
+                               const int32_t* perm_dst, int64_t n_nodes, const int64_t* z,
+                               const float* bias, int64_t n_bias, float* node_energy,
+                               xnn_stream_t stream) {
+  XNN_REQUIRE(n_nodes >= 0 && n_bias >= 0, "negative size");
+  if (n_nodes == 0) return XNN_OK;
+  XNN_REQUIRE(ptr_dst && node_energy, "NULL CSR or output");
+  XNN_REQUIRE(bias == nullptr || z != nullptr, "a bias needs the atoms' indices");
+  hipLaunchKernelGGL(node_energy_from_edges_kernel, dim3((unsigned)grid_1d(n_nodes, 256)),
+                     dim3(256), 0, as_hip(stream), edge_energy, ptr_dst, perm_dst, n_nodes, z,
+                     bias, n_bias, node_energy);
+  XNN_LAUNCH_CHECK();
+  return XNN_OK;
 }
 
 int xnn_gather_rows(int dtype, const void* src, int64_t n_src_rows, int64_t n_features,

@@ -270,14 +270,15 @@ class SphericalHarmonicEdgeEmbedding(nn.Module, FastPathModule):
                                      sh_sign=sh_sign, **spec)
 
     def radial_message_energy(self, vec: Tensor, W: Tensor, U: Tensor, z: Tensor, bias, plan,
-                              sh_sign: int = 1) -> Tensor:
+                              sh_sign: int = 1, one_pass: bool = False) -> Tensor:
         """Per-atom ``<U, A_i> + bias[z_i]`` of the rows of :meth:`radial_message_sum`, read
         out inside the same HIP kernels (the rows never reach memory; differentiable in
         ``vec`` only)."""
         from .ops import sh_radial_message_energy
         spec = radial_spec(self)
         return sh_radial_message_energy(vec, spec.pop("table"), W, U, z, bias, plan,
-                                        l_max=self.l_max, sh_sign=sh_sign, **spec)
+                                        l_max=self.l_max, sh_sign=sh_sign, one_pass=one_pass,
+                                        **spec)
 
     def embed(self, vec: Tensor, sh_sign: int = 1) -> Tuple[Tensor, Tensor, Tensor]:
         """``(edge_length (E,), edge_sh (E, (l_max+1)^2), edge_radial (E, n_rbf))``

@@ -109,6 +109,9 @@ class ShEdgePotential(InteratomicPotential):
     """
 
     edge_virial = True
+    # forces and stress with energies and gradients from one backward launch (the readout
+    # path; node energies as CSR sums of the edges' shares, exact gradients for any seed)
+    one_pass = False
     # energy = structure_sum(node_energy), nothing added at the structure level
     energy_is_node_sum = True
 
@@ -184,7 +187,7 @@ class ShEdgePotential(InteratomicPotential):
                 # one kernel each way (neither u, phi nor the (N, C, L) rows are stored)
                 node_energy = feat.radial_message_energy(
                     vec, self.W.detach().float(), self.U.detach().float(), data.atomic_numbers,
-                    self.atom_ref.detach(), data.plan(), self.sh_sign)
+                    self.atom_ref.detach(), data.plan(), self.sh_sign, one_pass=self.one_pass)
                 return {"node_energy": node_energy,
                         "energy": self.aggregate_energy(node_energy, data)}
         A = self.messages(data, vec)

@@ -751,14 +751,58 @@ sh_radial_message_energy_op.register_autograd(_rad_energy_backward,
                                               setup_context=_rad_energy_setup)
 
 
+class MessageEnergyOnePass(torch.autograd.Function):
+    """Per-atom energies ``<U, A_i> + bias[z_i]`` and their edge-vector gradients from one
+    launch of the readout backward (``xnn_sh_radial_message_energy_forces``): each edge's
+    share ``(phi_e U) . Y_e`` of its receiver's ``<U, A_i>`` comes out of the backward's own
+    dY, the atoms' energies are their CSR sums plus the bias (``xnn_node_energy_from_edges``),
+    and no forward launch runs. The gradients are formed for the cotangent -1 of every atom
+    (the forces' seed, the tensor the force outputs pass); an edge feeds its receiver's
+    energy only, so another cotangent scales each edge's stored gradient by its receiver's
+    value: exact for any cotangent."""
+
+    @staticmethod
+    def forward(ctx, vec, rbf_table, W, U, z, bias, ptr_dst, perm_dst, dst, iparams, fparams):
+        from .outputs import _minus_one
+        dev = vec.device
+        n_nodes = ptr_dst.shape[0] - 1
+        g_vec = torch.empty_like(vec)
+        edge_energy = torch.empty(vec.shape[0], dtype=torch.float32, device=dev)
+        seed = _minus_one(edge_energy)
+        _lib.call("xnn_sh_radial_message_energy_forces", _lib.XNN_F32, _lib.ptr(vec), None,
+                  n_nodes, None, 0, None, None, None, vec.shape[0], _lib.ptr(ptr_dst),
+                  _lib.ptr(perm_dst), _params(iparams, fparams), _lib.ptr(rbf_table),
+                  W.shape[1], _lib.ptr(W), _lib.ptr(U), _lib.ptr(seed), 0,
+                  _lib.ptr(g_vec), _lib.ptr(edge_energy), _lib.stream(dev))
+        node = torch.empty(n_nodes, dtype=torch.float32, device=dev)
+        _lib.call("xnn_node_energy_from_edges", _lib.ptr(edge_energy), _lib.ptr(ptr_dst),
+                  _lib.ptr(perm_dst), n_nodes, _lib.ptr(z), _lib.ptr(bias),
+                  0 if bias is None else bias.shape[0], _lib.ptr(node), _lib.stream(dev))
+        ctx.save_for_backward(g_vec, dst, seed)
+        return node
+
+    @staticmethod
+    def backward(ctx, g):
+        _once_differentiable()
+        g_vec, dst, seed = ctx.saved_tensors
+        g = g.to(torch.float32)
+        broadcast = g.dim() == 1 and g.stride(0) == 0
+        if broadcast and g.data_ptr() == seed.data_ptr():   # the forces' own -1 seed
+            return (g_vec,) + (None,) * 10
+        if broadcast:                                       # one value for every atom
+            return (g_vec * (-g[:1]),) + (None,) * 10
+        return (g_vec * (-g).index_select(0, dst.long())[:, None],) + (None,) * 10
+
+
 def sh_radial_message_energy(vec: Tensor, rbf_table: Tensor, W: Tensor, U: Tensor, z: Tensor,
                              bias: Optional[Tensor], plan: EdgePlan, *, basis: str,
                              envelope: str, poly_p: int, l_max: int, cutoff: float,
                              prefactor: float = 1.0, gamma: float = 1.0,
-                             sh_sign: int = 1) -> Tensor:
+                             sh_sign: int = 1, one_pass: bool = False) -> Tensor:
     """:func:`sh_radial_message_sum` read out in the kernel: the per-atom energies
     ``<U, A_i> + bias[z_i]`` (U: (C, (l_max+1)^2), bias indexed by ``z``, may be None);
-    differentiable in ``vec`` only."""
+    differentiable in ``vec`` only. ``one_pass``: when ``vec`` wants gradients, energies
+    and gradients from one backward launch (:class:`MessageEnergyOnePass`)."""
     if vec.dtype != torch.float32 or W.dtype != torch.float32 or U.dtype != torch.float32:
         raise TypeError("sh_radial_message_energy computes in float32")
     n_rbf, C = W.shape
@@ -775,6 +819,11 @@ def sh_radial_message_energy(vec: Tensor, rbf_table: Tensor, W: Tensor, U: Tenso
     fparams = [float(cutoff), float(prefactor), float(gamma)]
     table = rbf_table.to(device=vec.device, dtype=torch.float32).contiguous()
     b = None if bias is None else bias.to(device=vec.device, dtype=torch.float32).contiguous()
+    if one_pass and torch.is_grad_enabled() and vec.requires_grad:
+        return MessageEnergyOnePass.apply(vec.contiguous(), table, W.contiguous(),
+                                          U.reshape(-1).contiguous(),
+                                          z.to(torch.int64).contiguous(), b, plan.ptr_dst,
+                                          plan.perm_dst, plan.dst, iparams, fparams)
     return sh_radial_message_energy_op(vec.contiguous(), table, W.contiguous(),
                                        U.reshape(-1).contiguous(), z.to(torch.int64).contiguous(),
                                        b, plan.ptr_dst, plan.perm_dst, iparams, fparams)
