@@ -972,7 +972,8 @@ def main() -> None:
     for name, (call_args, _keep) in message_launches(msg, g, model, kw).items():
         replay_us[name] = replay_launch_us(name, call_args)
         total_us[name] = replay_us[name]
-    dominant = max(total_us, key=lambda k: total_us[k])
+    # the dominant kernel among those with an algorithmic cost
+    dominant = max((k for k in total_us if k in kc), key=lambda k: total_us[k])
     launch_us = replay_us.get(dominant, per_kernel.get(dominant))
     launch_s = launch_us * 1e-6
     cost = kc[dominant]

@@ -969,22 +969,34 @@ static int sh_msg(bool backward, const float* vec, const void* pos, int64_t n_no
   return XNN_OK;
 }
 
-// node_energy[i] = bias[z[i]] + sum over the receiver row i of edge_energy (CSR order),
-// one thread per atom; an index z outside [0, n_bias) gives NaN; no bias: 0
+// node_energy[i] = bias[z[i]] + sum over the receiver row i of edge_energy: 16 lanes per
+// atom, lane k summing the row's edges k, k + 16, ... in order, then a fixed butterfly over
+// the 16 (bitwise reproducible). Every lane of a wave takes part in the exchanges (an atom
+// index past the end reads nothing). An index z outside [0, n_bias) gives NaN; no bias: 0.
+constexpr int kNodeLanes = 16;
+
 __global__ __launch_bounds__(256) void node_energy_from_edges_kernel(
     const float* __restrict__ edge_energy, const int32_t* __restrict__ ptr,
     const int32_t* __restrict__ perm, int64_t n_nodes, const int64_t* __restrict__ z,
     const float* __restrict__ bias, int64_t n_bias, float* __restrict__ out) {
-  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= n_nodes) return;
+  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t i = t / kNodeLanes;
+  const int k = (int)(t % kNodeLanes);
+  const bool live = i < n_nodes;
   float s = 0.f;
-  if (bias != nullptr) {
-    const int64_t zi = z[i];
-    s = (zi >= 0 && zi < n_bias) ? bias[zi] : __builtin_nanf("");
+  if (live) {
+    const int32_t b = ptr[i], e = ptr[i + 1];
+    for (int32_t q = b + k; q < e; q += kNodeLanes) s += edge_energy[perm ? perm[q] : q];
   }
-  const int32_t b = ptr[i], e = ptr[i + 1];
-  for (int32_t k = b; k < e; ++k) s += edge_energy[perm ? perm[k] : k];
-  out[i] = s;
+  s = group_sum_f<kNodeLanes>(s);
+  if (live && k == 0) {
+    float base = 0.f;
+    if (bias != nullptr) {
+      const int64_t zi = z[i];
+      base = (zi >= 0 && zi < n_bias) ? bias[zi] : __builtin_nanf("");
+    }
+    out[i] = base + s;
+  }
 }
 
 template <typename T>
@@ -1120,7 +1132,8 @@ int xnn_node_energy_from_edges(const float* edge_energy, const int32_t* ptr_dst,
   if (n_nodes == 0) return XNN_OK;
   XNN_REQUIRE(ptr_dst && node_energy, "NULL CSR or output");
   XNN_REQUIRE(bias == nullptr || z != nullptr, "a bias needs the atoms' indices");
-  hipLaunchKernelGGL(node_energy_from_edges_kernel, dim3((unsigned)grid_1d(n_nodes, 256)),
+  hipLaunchKernelGGL(node_energy_from_edges_kernel,
+                     dim3((unsigned)grid_1d(n_nodes * kNodeLanes, 256)),
                      dim3(256), 0, as_hip(stream), edge_energy, ptr_dst, perm_dst, n_nodes, z,
                      bias, n_bias, node_energy);
   XNN_LAUNCH_CHECK();
