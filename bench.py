@@ -3,12 +3,17 @@
 Workload (``--config water``, the default): the 9,000-atom liquid water box (3,000 rigid
 H2O at 1.0 g/cm^3, cubic periodic cell of 44.8 A), cutoff 5.0 A, 8 Bessel radial
 functions x polynomial envelope, real SH l <= 3 (16 components), 128 float32 channels.
-A step is one evaluation of ``ForceStressOutput(ShEdgePotential)``: edge vectors ->
-radial basis + radial linear + SH message sum into (N, 128, 16) in one kernel (the radial
-features u are evaluated per lane and the per-edge weights phi = u W are formed on the
-matrix cores; neither is stored) -> readout -> float64 energy -> backward to forces and
-virial stress (one kernel back through message, linear layer and radial basis), all on
-the GPU with inputs resident in HBM. The neighbor list is timed separately (``neighbor_list_ms``).
+A step is one evaluation of ``ForceStressOutput(ShEdgePotential)`` (``--variant rows``, the
+default, the metric's pipeline): edge vectors -> radial basis + radial linear + SH message
+sum into the (N, 128, 16) rows A in one kernel, written to HBM (the radial features u are
+evaluated per lane, the sum is taken as A_i = W^T sum_e u_e (x) Y_e, so phi = u W is never
+formed) -> readout as its own op (reads A) -> float64 energy -> backward: the readout's
+backward writes the rows' cotangent (N, 128, 16), the message backward reads it (a general
+cotangent, as a model whose rows feed PyTorch layers hands back) and returns the edge
+vectors' gradient -> force and virial reduction, all on the GPU with inputs resident in
+HBM. ``--variant readout`` / ``one_pass`` time the kernels that apply the readout
+themselves (no rows in memory) as labelled secondary lines. The neighbor list is timed
+separately (``neighbor_list_ms``).
 
 Prints one JSON line. ``value`` = edges / (forward + force/stress backward time).
 ``roofline`` is the dominant kernel's algorithmic work per launch (HBM bytes, or fp32
@@ -64,6 +69,26 @@ def copy_calibration() -> None:
 MFMA_F32_PEAK_TFLOPS = 157.3
 
 
+def copy_bandwidth_gbs(mib: int = 1024, reps: int = 20) -> float:
+    """Measured device-to-device copy rate (bytes read + written per second) of a plain
+    ``mib`` MiB copy between HIP events on the current stream: the attainable HBM rate
+    reported next to the fractions of the 8 TB/s vendor peak."""
+    n = mib * 1024 * 1024 // 4
+    a = torch.ones(n, device="cuda")
+    b = torch.empty_like(a)
+    for _ in range(3):
+        b.copy_(a)
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    start.record()
+    for _ in range(reps):
+        b.copy_(a)
+    end.record()
+    torch.cuda.synchronize()
+    t = start.elapsed_time(end) * 1e-3 / reps
+    return 2 * 4 * n / t / 1e9
+
+
 def kernel_costs(E: int, N: int, C: int, L: int = 16, K: int = 8, grouped: bool = True) -> dict:
     """Compulsory HBM bytes and matrix-core flops per launch of each kernel: int32
     indices, float32 features, edge vectors given (12 B per edge), no perm when the edges
@@ -79,18 +104,25 @@ def kernel_costs(E: int, N: int, C: int, L: int = 16, K: int = 8, grouped: bool 
         "xnn_sh_radial_message_energy_forces": {           # the backward, + each edge's share
             "bytes": E * (12 + perm + 12 + 4) + N * 4 + 4 * C * L,   # of E_i out (no forward)
             "flops": E * 2 * C * (2 * K + 2 * L)},
+        # the rows kernels apply the linear layer per atom, A_i = W^T sum_e u_e (x) Y_e:
+        # 2 K L flops per edge for the feature-row sums, 2 C K L per atom for W^T B_i;
+        # backward 2 C K L per atom for dB_i = W G_i and 4 K L per edge for d u_e and dY_e
         "xnn_sh_radial_message_sum": {                     # radial basis evaluated in-kernel
-            "bytes": E * (12 + perm) + N * (4 * C * L + 4),
-            "flops": E * 2 * C * (K + L)},
+            "bytes": E * (12 + perm) + N * (4 * C * L + 4),   # vec in; ptr; A out
+            "flops": E * 2 * K * L + N * 2 * C * K * L},
         "xnn_sh_radial_message_sum_backward": {
-            "bytes": E * (12 + perm + 12) + N * (4 * C * L + 4),
-            "flops": E * 2 * C * (2 * K + 2 * L)},
+            "bytes": E * (12 + perm + 12) + N * (4 * C * L + 4),  # vec in, g_vec out; G in
+            "flops": E * 4 * K * L + N * 2 * C * K * L},
         "xnn_sh_linear_message_sum": {
             "bytes": E * (12 + 4 * K + perm) + N * (4 * C * L + 4),
-            "flops": E * 2 * C * (K + L)},                 # phi = h W, then phi (x) Y
+            "flops": E * 2 * K * L + N * 2 * C * K * L},
         "xnn_sh_linear_message_sum_backward": {
             "bytes": E * (12 + 4 * K + perm + 4 * K + 12) + N * (4 * C * L + 4),
-            "flops": E * 2 * C * (2 * K + 2 * L)},         # phi, dY, d_phi, d_h
+            "flops": E * 4 * K * L + N * 2 * C * K * L},
+        "xnn_node_readout": {                              # rows in, z in, E_i out
+            "bytes": N * (4 * C * L + 8 + 4) + 4 * C * L, "flops": N * 2 * C * L},
+        "xnn_node_readout_backward": {                     # broadcast seed, d_rows out
+            "bytes": N * 4 * C * L + 4 * C * L, "flops": N * C * L},
         "xnn_sh_message_sum": {
             "bytes": E * (12 + 4 * C + perm) + N * (4 * C * L + 4),
             "flops": E * 2 * C * L},
@@ -261,8 +293,6 @@ def build_workload(config: str, device):
         g = xa.AtomicGraph(pos=pos, atomic_numbers=z, edge_index=ei, cell_shifts=sh, batch=batch,
                            n_atoms=n_atoms)
     model = xa.ShEdgePotential(cutoff=rc, species=(1, 6, 7, 8, 18), seed=0, **kw).to(device)
-    # energies and gradients from one launch of the readout backward (no forward launch)
-    model.one_pass = True
     return g, model, rc, kw, workload, nl_ms, structs
 
 
@@ -855,9 +885,12 @@ def main() -> None:
     ap.add_argument("--fused-radial", action=argparse.BooleanOptionalAction, default=True,
                     help="radial basis evaluated inside the message kernels (ShEdgePotential "
                          "fused_radial)")
-    ap.add_argument("--fused-readout", action=argparse.BooleanOptionalAction, default=True,
-                    help="readout inside the radial message kernels (ShEdgePotential "
-                         "fused_readout)")
+    ap.add_argument("--variant", default="rows", choices=["rows", "readout", "one_pass"],
+                    help="rows (the metric's pipeline): the message kernels write the (N, C, 16) "
+                         "rows and the readout is its own op, whose backward hands back a "
+                         "general cotangent; readout: the message kernels apply the readout "
+                         "(no rows in memory); one_pass: energies and forces from one backward "
+                         "launch of the readout kernels")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run the 256 MiB copy that calibrates the HBM byte counters")
     args = ap.parse_args()
@@ -889,7 +922,8 @@ def main() -> None:
     g, model, rc, kw, workload, nl_ms, structs = build_workload(args.config, device)
     model.fused_linear = bool(args.fused)
     model.fused_radial = bool(args.fused_radial)
-    model.fused_readout = bool(args.fused_readout)
+    model.fused_readout = args.variant in ("readout", "one_pass")
+    model.one_pass = args.variant == "one_pass"
     E, N = g.num_edges, g.num_nodes
     C, L = kw["channels"], (kw["l_max"] + 1) ** 2
     wrapped = xa.ForceStressOutput(model, compute_stress=g.cell is not None).eval()
@@ -912,7 +946,7 @@ def main() -> None:
     fused = msg != "xnn_sh_message_sum"
     kernels = ([msg] if msg.endswith("_forces") else [msg, msg + "_backward"]) + \
         ["xnn_edge_featurize", "xnn_edge_featurize_backward", "xnn_edge_force_reduce",
-         "xnn_edge_force_reduce_virial"]
+         "xnn_edge_force_reduce_virial", "xnn_node_readout", "xnn_node_readout_backward"]
     # eager pass: per-kernel HIP events on the launch stream
     _lib.timed.clear()
     _lib.time_launches(*kernels)
@@ -996,6 +1030,7 @@ def main() -> None:
                      "timing": ("back-to-back launches, HIP events on the launch stream"
                                 if dominant in replay_us else "eager step, HIP events")})
     sb = step_bytes(E, N, C, L, kw["n_rbf"], msg)
+    copy_gbs = copy_bandwidth_gbs()
     step_gbs = sb / (ms * 1e-3) / 1e9
     result = {
         "metric": ("edges/s fwd+force-bwd and % HBM roofline, 9k-atom water box, 1 MI355X"
@@ -1005,7 +1040,14 @@ def main() -> None:
         "vs_baseline": None, "dtype": "f32", "data": "synthetic (seeded generator, random-init weights)",
         "config": {"workload": workload, "atoms": N, "edges": E, "channels": C, "sh_components": L,
                    "n_rbf": kw["n_rbf"], "cutoff": rc, "stress": g.cell is not None,
+                   "variant": args.variant,
                    "neighbor_list_ms": round(nl_ms, 3),
+                   # the neighbor list's algorithmic bytes (positions in, the int64 edge
+                   # index and shifts out: 12 N + 40 E) over its wall time per build
+                   "neighbor_list_roofline": {
+                       "bytes": 12 * N + 40 * E,
+                       "GBs": round((12 * N + 40 * E) / (nl_ms * 1e-3) / 1e9, 1),
+                       "frac": round((12 * N + 40 * E) / (nl_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)},
                    "hip_graph": bool(args.graph), "eager_ms_per_step": round(eager_ms, 4),
                    "graph_replay_matches_eager": graph_checked,
                    "fused_linear": fused, "message_kernel": msg,
@@ -1013,6 +1055,10 @@ def main() -> None:
                    # over its time, against the 8 TB/s peak
                    "step_algorithmic_bytes": sb,
                    "step_hbm_fraction": round(step_gbs / HBM_PEAK_GBS, 4),
+                   "step_GBs": round(step_gbs, 1),
+                   # a plain 1 GiB device copy on the same GPU: the attainable rate
+                   "copy_GBs": round(copy_gbs, 1),
+                   "step_fraction_of_copy": round(step_gbs / copy_gbs, 4),
                    # an equivalent-bytes figure, not a traffic measurement: the bytes the
                    # unfused pipeline would move, E (124 + 12 C) + N (76 + 8 C 16), over
                    # the fused step's time

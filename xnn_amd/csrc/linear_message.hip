@@ -28,127 +28,9 @@
 #include "common.h"
 #include "device.h"
 #include "message.h"
+#include "radial_row.h"
 
 namespace xnn {
-
-constexpr int kLinKMax = 8;  // h features: two k-steps of 4
-constexpr int kLinKK = 2;
-constexpr int kSH = 9;       // LDS row stride of per-edge radial features
-
-// The radial table (Bessel frequencies or Gaussian centers, k < kLinKMax) is read once per
-// block into LDS, and its first entry and the progression test into scalars at kernel
-// entry, before any store: there the wave-uniform loads are scalar loads (nothing the
-// kernel writes can alias them yet). Read next to the kernel's own stores they would be
-// per-lane vector loads whose latency the radial evaluation waits for on every row.
-struct RadialTab {
-  const float* f;  // the table in LDS
-  float f0;
-  // frequencies in harmonic progression, f_k = (k + 1) f_0 to 4e-7 (the default
-  // BesselRBF frequencies n pi, radial.py:226): then sin((k + 1) theta) and its cosine
-  // follow from one sincos by the Chebyshev recurrence x_{k+1} = 2 cos(theta) x_k - x_{k-1}
-  // instead of one sincos per function
-  bool harmonic;
-};
-
-// every thread of the block calls this once; the caller synchronizes the block before the
-// table is read
-__device__ __forceinline__ RadialTab load_radial_tab(const Radial<float>& R, float* sTab) {
-  RadialTab t;
-  t.f = sTab;
-  t.f0 = R.table[0];
-  t.harmonic = R.basis == XNN_BASIS_BESSEL;
-  for (int k = 1; k < R.K; ++k) {
-    const float fk = R.table[k];
-    if (fabsf(fk - (float)(k + 1) * t.f0) > 4e-7f * fabsf(fk)) t.harmonic = false;
-  }
-  if (threadIdx.x < kLinKMax) sTab[threadIdx.x] = (int)threadIdx.x < R.K ? R.table[threadIdx.x] : 0.f;
-  return t;
-}
-
-// What the backward's d|r| step reuses of the radial row: the envelope state and, for the
-// harmonic Bessel frequencies, sin and cos of the first frequency.
-struct RadialCache {
-  RadialAt<float> a;
-  float s1, c1;
-};
-
-// The lane's row of radial features h_k = rbf_k(r) envelope(r), k < kLinKMax (zeros past
-// R.K, and the whole row when the lane has no edge); the state the backward needs again goes
-// to *keep (when given).
-__device__ __forceinline__ void radial_row(const Radial<float>& R, const RadialTab& tab,
-                                           bool valid, float r, float* __restrict__ row,
-                                           RadialCache* keep = nullptr) {
-  if (valid) {
-    const RadialAt<float> a = radial_at(R, r);
-    if (keep) keep->a = a;
-    if (tab.harmonic) {
-      float s1, c1;
-      dev_sincos(tab.f0 * R.inv_rc * a.rr, &s1, &c1);
-      if (keep) {
-        keep->s1 = s1;
-        keep->c1 = c1;
-      }
-      const float c2 = 2.f * c1, pf = R.prefactor * a.inv * a.f;
-      float sp = 0.f, sk = s1;  // sin(k theta), sin((k + 1) theta)
-#pragma unroll
-      for (int k = 0; k < kLinKMax; ++k) {
-        row[k] = k < R.K ? pf * sk : 0.f;
-        const float sn = c2 * sk - sp;
-        sp = sk;
-        sk = sn;
-      }
-      return;
-    }
-#pragma unroll 1
-    for (int k = 0; k < kLinKMax; ++k) {
-      float u = 0.f, du;
-      if (k < R.K) radial_kv<float, false>(R, a, tab.f[k], u, du);
-      row[k] = u;
-    }
-  } else {
-#pragma unroll
-    for (int k = 0; k < kLinKMax; ++k) row[k] = 0.f;
-  }
-}
-
-// d E / d r through the radial features of one edge, sum_k d_h[k] d h_k / d r, from the
-// state radial_row kept. Harmonic Bessel frequencies, with theta = w0 r, w0 = f0 / rc:
-// h_k = P sin((k+1) theta) f / r, so sum_k d_h[k] h_k' = P / r (f (w0 sum_k (k+1) d_h[k]
-// cos((k+1) theta) - S / r) + f' S) with S = sum_k d_h[k] sin((k+1) theta) (the sine term
-// drops at the clamped radius, where h_k does not vary with r).
-__device__ __forceinline__ float radial_dot(const Radial<float>& R, const RadialTab& tab,
-                                            const RadialCache& rc,
-                                            const float* __restrict__ d_h) {
-  const RadialAt<float>& a = rc.a;
-  if (tab.harmonic) {
-    const float w0 = tab.f0 * R.inv_rc;
-    const float c2 = 2.f * rc.c1;
-    float sp = 0.f, sk = rc.s1, cp = 1.f, ck = rc.c1;
-    float S = 0.f, Cw = 0.f;
-#pragma unroll
-    for (int k = 0; k < kLinKMax; ++k) {
-      if (k < R.K) {
-        S += d_h[k] * sk;
-        Cw += ((float)(k + 1) * d_h[k]) * ck;
-      }
-      const float sn = c2 * sk - sp, cn = c2 * ck - cp;
-      sp = sk;
-      sk = sn;
-      cp = ck;
-      ck = cn;
-    }
-    const float rad = a.clamped ? 0.f : a.f * (w0 * Cw - a.inv * S);
-    return R.prefactor * a.inv * (rad + a.df * S);
-  }
-  float dl = 0.f;
-#pragma unroll 1
-  for (int k = 0; k < R.K; ++k) {
-    float u, du;
-    radial_kv<float, true>(R, a, tab.f[k], u, du);
-    dl += d_h[k] * du;
-  }
-  return dl;
-}
 
 // RO (readout): instead of the (C, L) row A_i the kernel writes the atom's energy
 // E_i = sum_{c, lm} U[c, lm] A_i[c, lm] + bias[z_i] (bias may be NULL), reduced across the
@@ -692,28 +574,17 @@ static void lin_msg_launch(bool backward, const float* vec, const void* pos, int
 #undef XNN_LIN
 }
 
-// R == nullptr: h is given (E, K); else h is evaluated in the kernels from R (K = R->K).
-// ro != nullptr: the readout kernels (R must be given).
+// The readout kernels: h is evaluated in the kernels from R (K = R.K).
 template <typename G>
 static int lin_msg(bool backward, const float* vec, const void* pos, int64_t n_nodes,
                    const void* cell, int64_t n_graphs, const int32_t* batch, const int32_t* src,
                    const int32_t* shift, const int32_t* ptr, const int32_t* perm, int l_max,
-                   int sign, int K, int C, const float* h, const Radial<float>* R,
-                   const float* W, const float* d_out, float* out_or_dh, float* g_vec,
-                   hipStream_t stream, const Readout* ro = nullptr, int64_t n_edges = 0) {
+                   int sign, int C, const Radial<float>& R, const float* W, float* out,
+                   float* g_vec, hipStream_t stream, const Readout& ro, int64_t n_edges = 0) {
   if (n_nodes == 0) return XNN_OK;
-  if (ro != nullptr)
-    lin_msg_launch<G, true, true>(backward, vec, pos, n_nodes, cell, n_graphs, batch, src,
-                                  shift, ptr, perm, l_max, sign, R->K, C, nullptr, *R, W, d_out,
-                                  out_or_dh, g_vec, *ro, n_edges, stream);
-  else if (R != nullptr)
-    lin_msg_launch<G, true, false>(backward, vec, pos, n_nodes, cell, n_graphs, batch, src,
-                                   shift, ptr, perm, l_max, sign, R->K, C, nullptr, *R, W, d_out,
-                                   out_or_dh, g_vec, Readout{}, n_edges, stream);
-  else
-    lin_msg_launch<G, false, false>(backward, vec, pos, n_nodes, cell, n_graphs, batch, src,
-                                    shift, ptr, perm, l_max, sign, K, C, h, Radial<float>{}, W,
-                                    d_out, out_or_dh, g_vec, Readout{}, n_edges, stream);
+  lin_msg_launch<G, true, true>(backward, vec, pos, n_nodes, cell, n_graphs, batch, src, shift,
+                                ptr, perm, l_max, sign, R.K, C, nullptr, R, W, nullptr, out,
+                                g_vec, ro, n_edges, stream);
   XNN_LAUNCH_CHECK();
   return XNN_OK;
 }
@@ -733,121 +604,6 @@ static int lin_check(int64_t n_nodes, int64_t n_edges, int32_t l_max, int32_t sh
 using namespace xnn;
 
 extern "C" {
-
-int xnn_sh_linear_message_sum(int geom_dtype, const float* vec_in, const void* pos,
-                              int64_t n_nodes, const void* cell, int64_t n_graphs,
-                              const int32_t* batch, const int32_t* src, const int32_t* shift,
-                              int64_t n_edges, const int32_t* ptr_dst, const int32_t* perm_dst,
-                              int32_t l_max, int32_t sh_sign, int32_t n_features,
-                              int32_t n_channels, const float* h, const float* W, float* out,
-                              xnn_stream_t stream) {
-  const int st = lin_check(n_nodes, n_edges, l_max, sh_sign, n_features, n_channels);
-  if (st != XNN_OK) return st;
-  XNN_REQUIRE(n_nodes == 0 || (ptr_dst && out && W), "NULL CSR, weights or output");
-  XNN_REQUIRE(aligned16(out), "out must be 16-byte aligned");
-  XNN_REQUIRE(n_edges == 0 || ((vec_in || (pos && src && shift)) && h), "NULL edge input");
-  XNN_REQUIRE(cell == nullptr || n_graphs <= 1 || batch != nullptr,
-              "several cells need the batch vector");
-  if (geom_dtype == XNN_F32)
-    return lin_msg<float>(false, vec_in, pos, n_nodes, cell, n_graphs, batch, src, shift, ptr_dst,
-                          perm_dst, l_max, sh_sign, n_features, n_channels, h, nullptr, W, nullptr,
-                          out, nullptr, as_hip(stream));
-  if (geom_dtype == XNN_F64)
-    return lin_msg<double>(false, vec_in, pos, n_nodes, cell, n_graphs, batch, src, shift,
-                           ptr_dst, perm_dst, l_max, sh_sign, n_features, n_channels, h, nullptr,
-                           W, nullptr, out, nullptr, as_hip(stream));
-  set_error("unsupported geometry dtype %d", geom_dtype);
-  return XNN_EINVAL;
-}
-
-int xnn_sh_linear_message_sum_backward(int geom_dtype, const float* vec_in, const void* pos,
-                                       int64_t n_nodes, const void* cell, int64_t n_graphs,
-                                       const int32_t* batch, const int32_t* src,
-                                       const int32_t* shift, int64_t n_edges,
-                                       const int32_t* ptr_dst, const int32_t* perm_dst,
-                                       int32_t l_max, int32_t sh_sign, int32_t n_features,
-                                       int32_t n_channels, const float* h, const float* W,
-                                       const float* d_out, float* d_h, float* g_vec,
-                                       xnn_stream_t stream) {
-  const int st = lin_check(n_nodes, n_edges, l_max, sh_sign, n_features, n_channels);
-  if (st != XNN_OK) return st;
-  XNN_REQUIRE(n_nodes == 0 || (ptr_dst && d_out && W), "NULL CSR, weights or d_out");
-  XNN_REQUIRE(aligned16(d_out), "d_out must be 16-byte aligned");
-  XNN_REQUIRE(n_edges == 0 || ((vec_in || (pos && src && shift)) && d_h && (h || !g_vec)),
-              "NULL edge input or output");
-  XNN_REQUIRE(cell == nullptr || n_graphs <= 1 || batch != nullptr,
-              "several cells need the batch vector");
-  if (geom_dtype == XNN_F32)
-    return lin_msg<float>(true, vec_in, pos, n_nodes, cell, n_graphs, batch, src, shift, ptr_dst,
-                          perm_dst, l_max, sh_sign, n_features, n_channels, h, nullptr, W, d_out,
-                          d_h, g_vec, as_hip(stream));
-  if (geom_dtype == XNN_F64)
-    return lin_msg<double>(true, vec_in, pos, n_nodes, cell, n_graphs, batch, src, shift,
-                           ptr_dst, perm_dst, l_max, sh_sign, n_features, n_channels, h, nullptr,
-                           W, d_out, d_h, g_vec, as_hip(stream));
-  set_error("unsupported geometry dtype %d", geom_dtype);
-  return XNN_EINVAL;
-}
-
-int xnn_sh_radial_message_sum(int geom_dtype, const float* vec_in, const void* pos,
-                              int64_t n_nodes, const void* cell, int64_t n_graphs,
-                              const int32_t* batch, const int32_t* src, const int32_t* shift,
-                              int64_t n_edges, const int32_t* ptr_dst, const int32_t* perm_dst,
-                              const xnn_featurize_params* prm, const float* rbf_table,
-                              int32_t n_channels, const float* W, float* out,
-                              xnn_stream_t stream) {
-  Radial<float> R;
-  int st = make_radial<float>(prm, rbf_table, R);
-  if (st != XNN_OK) return st;
-  st = lin_check(n_nodes, n_edges, prm->l_max, prm->sh_sign, prm->n_rbf, n_channels);
-  if (st != XNN_OK) return st;
-  XNN_REQUIRE(n_nodes == 0 || (ptr_dst && out && W), "NULL CSR, weights or output");
-  XNN_REQUIRE(aligned16(out), "out must be 16-byte aligned");
-  XNN_REQUIRE(n_edges == 0 || vec_in || (pos && src && shift), "NULL edge input");
-  XNN_REQUIRE(cell == nullptr || n_graphs <= 1 || batch != nullptr,
-              "several cells need the batch vector");
-  if (geom_dtype == XNN_F32)
-    return lin_msg<float>(false, vec_in, pos, n_nodes, cell, n_graphs, batch, src, shift, ptr_dst,
-                          perm_dst, prm->l_max, prm->sh_sign, R.K, n_channels, nullptr, &R, W,
-                          nullptr, out, nullptr, as_hip(stream));
-  if (geom_dtype == XNN_F64)
-    return lin_msg<double>(false, vec_in, pos, n_nodes, cell, n_graphs, batch, src, shift,
-                           ptr_dst, perm_dst, prm->l_max, prm->sh_sign, R.K, n_channels, nullptr,
-                           &R, W, nullptr, out, nullptr, as_hip(stream));
-  set_error("unsupported geometry dtype %d", geom_dtype);
-  return XNN_EINVAL;
-}
-
-int xnn_sh_radial_message_sum_backward(int geom_dtype, const float* vec_in, const void* pos,
-                                       int64_t n_nodes, const void* cell, int64_t n_graphs,
-                                       const int32_t* batch, const int32_t* src,
-                                       const int32_t* shift, int64_t n_edges,
-                                       const int32_t* ptr_dst, const int32_t* perm_dst,
-                                       const xnn_featurize_params* prm, const float* rbf_table,
-                                       int32_t n_channels, const float* W, const float* d_out,
-                                       float* g_vec, xnn_stream_t stream) {
-  Radial<float> R;
-  int st = make_radial<float>(prm, rbf_table, R);
-  if (st != XNN_OK) return st;
-  st = lin_check(n_nodes, n_edges, prm->l_max, prm->sh_sign, prm->n_rbf, n_channels);
-  if (st != XNN_OK) return st;
-  XNN_REQUIRE(n_nodes == 0 || (ptr_dst && d_out && W), "NULL CSR, weights or d_out");
-  XNN_REQUIRE(aligned16(d_out), "d_out must be 16-byte aligned");
-  XNN_REQUIRE(n_edges == 0 || ((vec_in || (pos && src && shift)) && g_vec),
-              "NULL edge input or output");
-  XNN_REQUIRE(cell == nullptr || n_graphs <= 1 || batch != nullptr,
-              "several cells need the batch vector");
-  if (geom_dtype == XNN_F32)
-    return lin_msg<float>(true, vec_in, pos, n_nodes, cell, n_graphs, batch, src, shift, ptr_dst,
-                          perm_dst, prm->l_max, prm->sh_sign, R.K, n_channels, nullptr, &R, W,
-                          d_out, nullptr, g_vec, as_hip(stream));
-  if (geom_dtype == XNN_F64)
-    return lin_msg<double>(true, vec_in, pos, n_nodes, cell, n_graphs, batch, src, shift,
-                           ptr_dst, perm_dst, prm->l_max, prm->sh_sign, R.K, n_channels, nullptr,
-                           &R, W, d_out, nullptr, g_vec, as_hip(stream));
-  set_error("unsupported geometry dtype %d", geom_dtype);
-  return XNN_EINVAL;
-}
 
 int xnn_sh_radial_message_energy(int geom_dtype, const float* vec_in, const void* pos,
                                  int64_t n_nodes, const void* cell, int64_t n_graphs,
@@ -874,12 +630,12 @@ int xnn_sh_radial_message_energy(int geom_dtype, const float* vec_in, const void
   ro.n_bias = n_bias;
   if (geom_dtype == XNN_F32)
     return lin_msg<float>(false, vec_in, pos, n_nodes, cell, n_graphs, batch, src, shift, ptr_dst,
-                          perm_dst, prm->l_max, prm->sh_sign, R.K, n_channels, nullptr, &R, W,
-                          nullptr, node_energy, nullptr, as_hip(stream), &ro);
+                          perm_dst, prm->l_max, prm->sh_sign, n_channels, R, W, node_energy,
+                          nullptr, as_hip(stream), ro);
   if (geom_dtype == XNN_F64)
     return lin_msg<double>(false, vec_in, pos, n_nodes, cell, n_graphs, batch, src, shift,
-                           ptr_dst, perm_dst, prm->l_max, prm->sh_sign, R.K, n_channels, nullptr,
-                           &R, W, nullptr, node_energy, nullptr, as_hip(stream), &ro);
+                           ptr_dst, perm_dst, prm->l_max, prm->sh_sign, n_channels, R, W,
+                           node_energy, nullptr, as_hip(stream), ro);
   set_error("unsupported geometry dtype %d", geom_dtype);
   return XNN_EINVAL;
 }
@@ -910,12 +666,12 @@ int xnn_sh_radial_message_energy_backward(int geom_dtype, const float* vec_in, c
   ro.g_stride = g_stride;
   if (geom_dtype == XNN_F32)
     return lin_msg<float>(true, vec_in, pos, n_nodes, cell, n_graphs, batch, src, shift, ptr_dst,
-                          perm_dst, prm->l_max, prm->sh_sign, R.K, n_channels, nullptr, &R, W,
-                          nullptr, nullptr, g_vec, as_hip(stream), &ro, n_edges);
+                          perm_dst, prm->l_max, prm->sh_sign, n_channels, R, W, nullptr, g_vec,
+                          as_hip(stream), ro, n_edges);
   if (geom_dtype == XNN_F64)
     return lin_msg<double>(true, vec_in, pos, n_nodes, cell, n_graphs, batch, src, shift,
-                           ptr_dst, perm_dst, prm->l_max, prm->sh_sign, R.K, n_channels, nullptr,
-                           &R, W, nullptr, nullptr, g_vec, as_hip(stream), &ro, n_edges);
+                           ptr_dst, perm_dst, prm->l_max, prm->sh_sign, n_channels, R, W, nullptr,
+                           g_vec, as_hip(stream), ro, n_edges);
   set_error("unsupported geometry dtype %d", geom_dtype);
   return XNN_EINVAL;
 }
@@ -948,12 +704,12 @@ int xnn_sh_radial_message_energy_forces(int geom_dtype, const float* vec_in, con
   ro.edge_energy = edge_energy;
   if (geom_dtype == XNN_F32)
     return lin_msg<float>(true, vec_in, pos, n_nodes, cell, n_graphs, batch, src, shift, ptr_dst,
-                          perm_dst, prm->l_max, prm->sh_sign, R.K, n_channels, nullptr, &R, W,
-                          nullptr, nullptr, g_vec, as_hip(stream), &ro, n_edges);
+                          perm_dst, prm->l_max, prm->sh_sign, n_channels, R, W, nullptr, g_vec,
+                          as_hip(stream), ro, n_edges);
   if (geom_dtype == XNN_F64)
     return lin_msg<double>(true, vec_in, pos, n_nodes, cell, n_graphs, batch, src, shift,
-                           ptr_dst, perm_dst, prm->l_max, prm->sh_sign, R.K, n_channels, nullptr,
-                           &R, W, nullptr, nullptr, g_vec, as_hip(stream), &ro, n_edges);
+                           ptr_dst, perm_dst, prm->l_max, prm->sh_sign, n_channels, R, W, nullptr,
+                           g_vec, as_hip(stream), ro, n_edges);
   set_error("unsupported geometry dtype %d", geom_dtype);
   return XNN_EINVAL;
 }

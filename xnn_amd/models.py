@@ -99,13 +99,16 @@ class ShEdgePotential(InteratomicPotential):
     ``E_i = sum_{c,lm} U[c, lm] A_i[c, lm] + atom_ref[Z_i]`` and ``E = sum_i E_i`` in
     float64. On a GPU the featurizer and the fused message sum are HIP kernels (the
     message never exists in memory); with ``fused_linear`` (the default, for the channel
-    counts the fused kernels take) the radial linear layer runs inside the message
-    kernels too, so ``phi`` is never stored either, and with ``fused_radial`` (the
-    default) forces and stress evaluate the radial basis inside those kernels as well
-    (one kernel each way; parameter gradients take the two-kernel path); with
-    ``fused_readout`` (the default) those kernels also apply the readout, so the
-    (N, C, L) rows are never stored and the backward forms their cotangent g_i U itself. ``use_fast=False`` or a CPU evaluates
-    the same function with the PyTorch formulation.
+    counts the fused kernels take) the radial linear layer is applied inside the message
+    kernels too, per atom (``A_i = W^T sum_e u_e (x) Y_e``, the same sum reassociated), so
+    ``phi`` is never formed, and with ``fused_radial`` (the default) forces and stress
+    evaluate the radial basis inside those kernels as well (one kernel each way; parameter
+    gradients take the two-kernel path). The (N, C, L) rows A are written to memory and
+    read out by their own op, whose backward hands the message backward a general
+    (N, C, L) cotangent, as a model whose rows feed PyTorch layers needs. With
+    ``fused_readout`` the message kernels apply the readout themselves instead (no rows in
+    memory), and ``one_pass`` then takes energies and forces from one backward launch.
+    ``use_fast=False`` or a CPU evaluates the same function with the PyTorch formulation.
     """
 
     edge_virial = True
@@ -119,7 +122,7 @@ class ShEdgePotential(InteratomicPotential):
                  channels: int = 128, cutoff: float = 5.0, radial_type: str = "bessel",
                  envelope: str = "polynomial", p: int = 6, sh_sign: int = 1,
                  use_fast: UseFast = "auto", seed: Optional[int] = 0, fused_linear: bool = True,
-                 fused_radial: bool = True, fused_readout: bool = True):
+                 fused_radial: bool = True, fused_readout: bool = False):
         super().__init__()
         self.cutoff = float(cutoff)
         self.l_max = int(l_max)
