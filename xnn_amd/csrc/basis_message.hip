@@ -89,17 +89,26 @@ __global__ __launch_bounds__(256) void basis_msg_fwd_kernel(
   __syncthreads();  // the radial table
   const int feat = basis_row_feature(lo);
   const int64_t n_waves = (int64_t)gridDim.x * kWavesPerBlock;
-  for (int64_t row = (int64_t)blockIdx.x * kWavesPerBlock + wave; row < n_nodes;
-       row += n_waves) {
+  int64_t row = (int64_t)blockIdx.x * kWavesPerBlock + wave;
+  // with given edge vectors, the first batch of the wave's next row is loaded a row ahead
+  float px = 0.f, py = 0.f, pz = 0.f;
+  if (vec != nullptr && row < n_nodes) load_first_vec(vec, perm, ptr[row], ptr[row + 1], lane, px, py, pz);
+  for (; row < n_nodes; row += n_waves) {
     const G* cl = row_cell(cell, n_graphs, batch, row);
     floatx4 acc = floatx4{0.f, 0.f, 0.f, 0.f};
     const int b0 = ptr[row], b1 = ptr[row + 1];
+    const float cx = px, cy = py, cz = pz;
+    if (vec != nullptr && row + n_waves < n_nodes)
+      load_first_vec(vec, perm, ptr[row + n_waves], ptr[row + n_waves + 1], lane, px, py, pz);
     for (int base = b0; base < b1; base += kWave) {
       const int cnt = min(kWave, b1 - base);
       const int my_e = lane < cnt ? (perm ? perm[base + lane] : base + lane) : 0;
       float ux, uy, uz, inv, len;
-      batch_harmonics<G, LMAX>(vec, pos, cl, src, shift, (int)row, sign, lane, cnt, my_e, ys,
-                               ux, uy, uz, inv, len);
+      if (vec != nullptr && base == b0)
+        batch_harmonics_xyz<LMAX>(cx, cy, cz, sign, lane, cnt, ys, ux, uy, uz, inv, len);
+      else
+        batch_harmonics<G, LMAX>(vec, pos, cl, src, shift, (int)row, sign, lane, cnt, my_e, ys,
+                                 ux, uy, uz, inv, len);
       if constexpr (RAD)
         radial_row(R, tab, lane < cnt, len, hs + lane * kSH);
       else
@@ -172,11 +181,10 @@ __global__ __launch_bounds__(256) void basis_msg_bwd_kernel(
        row += n_waves) {
     const int b0 = ptr[row], b1 = ptr[row + 1];
     if (b0 == b1) continue;
-    const G* cl = row_cell(cell, n_graphs, batch, row);
-    // dB = W G with the row's cotangent in the B operand layout, G[4 s + hi][lo] (a run of
-    // 64 floats a step); two accumulators halve the dependent chain
-    const float* gr = d_out + row * (int64_t)(C * L);
     {
+      // dB = W G with the row's cotangent in the B operand layout, G[4 s + hi][lo] (a run
+      // of 64 floats a step); two accumulators halve the dependent chain
+      const float* gr = d_out + row * (int64_t)(C * L);
       float ga[NS];
 #pragma unroll
       for (int s = 0; s < NS; ++s) ga[s] = lo < L ? gr[(4 * s + hi) * L + lo] : 0.f;
@@ -190,6 +198,7 @@ __global__ __launch_bounds__(256) void basis_msg_bwd_kernel(
       sb[(2 * hi) * 16 + lo] = db0[0] + db1[0];
       sb[(2 * hi + 1) * 16 + lo] = db0[1] + db1[1];
     }
+    const G* cl = row_cell(cell, n_graphs, batch, row);
     for (int base = b0; base < b1; base += kWave) {
       const int cnt = min(kWave, b1 - base);
       const int my_e = lane < cnt ? (perm ? perm[base + lane] : base + lane) : 0;
@@ -203,30 +212,25 @@ __global__ __launch_bounds__(256) void basis_msg_bwd_kernel(
         load_h_row(h, K, lane < cnt, my_e, hs + lane * kSH);
       wave_sync();  // dB and the batch's rows
       if (lane < cnt) {
-        float Y[16], hk[kLinKMax];
+        // two passes over dB, so that few per-edge arrays are live together: d h_e first
+        // (against the harmonics), then dY_e (against the radial row)
+        float du[kLinKMax];
+        {
+          float Y[16];
 #pragma unroll
-        for (int m = 0; m < 16; ++m) Y[m] = ys[lane * kSY + m];
+          for (int m = 0; m < 16; ++m) Y[m] = ys[lane * kSY + m];
 #pragma unroll
-        for (int k = 0; k < kLinKMax; ++k) hk[k] = hs[lane * kSH + k];
-        float du[kLinKMax], dY[16];
+          for (int k = 0; k < kLinKMax; ++k) {
+            du[k] = 0.f;
+            if (k < K) {
+              const float4* bk = reinterpret_cast<const float4*>(sb + k * 16);
 #pragma unroll
-        for (int m = 0; m < 16; ++m) dY[m] = 0.f;
+              for (int q = 0; q < (L + 3) / 4; ++q) {
+                const float4 b = bk[q];
+                const float bv[4] = {b.x, b.y, b.z, b.w};
 #pragma unroll
-        for (int k = 0; k < kLinKMax; ++k) {
-          du[k] = 0.f;
-          if (k < K) {
-            const float4* bk = reinterpret_cast<const float4*>(sb + k * 16);
-#pragma unroll
-            for (int q = 0; q < (L + 3) / 4; ++q) {
-              const float4 b = bk[q];
-              const float bv[4] = {b.x, b.y, b.z, b.w};
-#pragma unroll
-              for (int j = 0; j < 4; ++j) {
-                const int m = 4 * q + j;
-                if (m < L) {
-                  du[k] = fmaf(bv[j], Y[m], du[k]);
-                  dY[m] = fmaf(hk[k], bv[j], dY[m]);
-                }
+                for (int j = 0; j < 4; ++j)
+                  if (4 * q + j < L) du[k] = fmaf(bv[j], Y[4 * q + j], du[k]);
               }
             }
           }
@@ -240,6 +244,24 @@ __global__ __launch_bounds__(256) void basis_msg_bwd_kernel(
             if (k < K) d_h[(int64_t)my_e * K + k] = du[k];
         }
         if (g_vec != nullptr) {
+          float dY[16];
+#pragma unroll
+          for (int m = 0; m < 16; ++m) dY[m] = 0.f;
+#pragma unroll
+          for (int k = 0; k < kLinKMax; ++k) {
+            if (k < K) {
+              const float hk = hs[lane * kSH + k];
+              const float4* bk = reinterpret_cast<const float4*>(sb + k * 16);
+#pragma unroll
+              for (int q = 0; q < (L + 3) / 4; ++q) {
+                const float4 b = bk[q];
+                const float bv[4] = {b.x, b.y, b.z, b.w};
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                  if (4 * q + j < L) dY[4 * q + j] = fmaf(hk, bv[j], dY[4 * q + j]);
+              }
+            }
+          }
           float Gx, Gy, Gz, vx, vy, vz;
           sh_grad<LMAX, float>(ux, uy, uz, dY, Gx, Gy, Gz);
           sh_chain<float>(ux, uy, uz, inv, Gx, Gy, Gz, vx, vy, vz);
