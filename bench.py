@@ -95,15 +95,17 @@ def kernel_costs(E: int, N: int, C: int, L: int = 16, K: int = 8, grouped: bool 
     come grouped by receiver. Flops count the true dimensions (no padding)."""
     perm = 0 if grouped else 4
     return {
+        # the readout in the kernels: each edge's share h_e^T (W U) Y_e of its receiver's
+        # energy (2 K L + 2 K flops), its gradient g_i ((W U) Y_e, (W U)^T h_e) (4 K L)
         "xnn_sh_radial_message_energy": {                  # radial basis and readout in-kernel
-            "bytes": E * (12 + perm) + N * (4 + 4) + 4 * C * L,  # vec in; ptr; E_i out; U
-            "flops": E * 2 * C * (K + L) + N * 2 * C * L},
-        "xnn_sh_radial_message_energy_backward": {         # the rows' cotangent g_i U in-kernel
+            "bytes": E * (12 + perm) + N * (4 + 4 + 8) + 4 * C * L,  # vec in; ptr, z; E_i out
+            "flops": E * (2 * K * L + 2 * K)},
+        "xnn_sh_radial_message_energy_backward": {
             "bytes": E * (12 + perm + 12) + N * 4 + 4 * C * L,   # vec in, g_vec out; ptr; U
-            "flops": E * 2 * C * (2 * K + 2 * L)},
+            "flops": E * 4 * K * L},
         "xnn_sh_radial_message_energy_forces": {           # the backward, + each edge's share
             "bytes": E * (12 + perm + 12 + 4) + N * 4 + 4 * C * L,   # of E_i out (no forward)
-            "flops": E * 2 * C * (2 * K + 2 * L)},
+            "flops": E * (4 * K * L + 2 * K)},
         # the rows kernels apply the linear layer per atom, A_i = W^T sum_e u_e (x) Y_e:
         # 2 K L flops per edge for the feature-row sums, 2 C K L per atom for W^T B_i;
         # backward 2 C K L per atom for dB_i = W G_i and 4 K L per edge for d u_e and dY_e

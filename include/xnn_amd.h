@@ -176,8 +176,10 @@ int xnn_sh_message_sum_backward(int geom_dtype, const float* vec_in, const void*
 /* The same aggregation with the edge weights formed by a linear layer in the kernel:
  * phi[e,c] = sum_k h[e,k] W[k,c], the last layer of the edge-weight network
  * (gnn/fast/conv.py:137-143 takes the weights from the radial network; the product
- * and the receiver sum as in xnn_sh_message_sum). phi is formed per 16-edge tile on
- * the matrix cores and never stored. h (E,K) f32 with K = n_features in [1, 8],
+ * and the receiver sum as in xnn_sh_message_sum). The kernel takes the same sum in the
+ * other order, A_i = W^T sum_{dst(e)=i} h_e (x) Y_e (the K x L feature rows summed per
+ * receiver, then the linear layer per atom), so phi is never formed. h (E,K) f32 with
+ * K = n_features in [1, 8],
  * W (K,C) f32 with C = n_channels in {32, 64, 128}, l_max in [1, 3]; out (N,C,L) f32,
  * 16-byte aligned. Other shapes return XNN_EINVAL (use xnn_sh_message_sum). */
 int xnn_sh_linear_message_sum(int geom_dtype, const float* vec_in, const void* pos,
@@ -223,8 +225,10 @@ int xnn_sh_radial_message_sum(int geom_dtype, const float* vec_in, const void* p
  * NULL: no bias; an index z outside [0, n_bias) gives NaN), so the (N,C,L) rows never
  * reach memory. It fuses the aggregation (gnn/fast/conv.py:137-143, ops.py:403-448) with
  * a model's linear energy readout before aggregate_energy (common/models/base.py:161-180);
- * the reference has no single counterpart. U (C,L) f32, z (N) int64, bias (n_bias) f32,
- * node_energy (N) f32. Parameter gradients are not formed. */
+ * the reference has no single counterpart. The kernels take E_i = sum_{dst(e)=i}
+ * h_e^T (W U) Y_e + bias[z_i], the same sum with W U (K x L) formed once per block.
+ * U (C,L) f32, z (N) int64, bias (n_bias) f32, node_energy (N) f32. Parameter gradients
+ * are not formed. */
 int xnn_sh_radial_message_energy(int geom_dtype, const float* vec_in, const void* pos,
                                  int64_t n_nodes, const void* cell, int64_t n_graphs,
                                  const int32_t* batch, const int32_t* src, const int32_t* shift,
@@ -236,7 +240,8 @@ int xnn_sh_radial_message_energy(int geom_dtype, const float* vec_in, const void
 
 /* Backward of xnn_sh_radial_message_energy with respect to the edge vectors for the
  * per-atom cotangent g (N) f32 of node_energy (g_stride 1, or 0: one value for every
- * atom): the rows' cotangent g_i U is formed in the kernel. g_vec (E,3) f32 (written). */
+ * atom): per edge g_i ((W U) Y_e, (W U)^T h_e) in (d h_e, dY_e), chained to the edge
+ * vector. g_vec (E,3) f32 (written). */
 int xnn_sh_radial_message_energy_backward(int geom_dtype, const float* vec_in, const void* pos,
                                           int64_t n_nodes, const void* cell, int64_t n_graphs,
                                           const int32_t* batch, const int32_t* src,
@@ -248,8 +253,7 @@ int xnn_sh_radial_message_energy_backward(int geom_dtype, const float* vec_in, c
                                           int64_t g_stride, float* g_vec, xnn_stream_t stream);
 
 /* xnn_sh_radial_message_energy_backward that also writes each edge's share of its receiver's
- * readout, edge_energy[e] = (phi_e U) . Y_e (E) f32 (the unscaled dY of the backward against
- * the edge's harmonics), so that node_energy[i] = bias[z[i]] + sum_{dst(e)=i} edge_energy[e]
+ * readout, edge_energy[e] = (phi_e U) . Y_e = h_e^T (W U) Y_e (E) f32, so that node_energy[i] = bias[z[i]] + sum_{dst(e)=i} edge_energy[e]
  * without the forward launch: energies and forces from one pass, as the reference's fused
  * energy-and-force evaluations return them (gnn/fast/conv.py:137-143 with the readout of
  * common/models/base.py:161-180). g_vec is the gradient for the cotangent g as in the

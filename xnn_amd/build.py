@@ -17,7 +17,7 @@ ROOT = os.path.dirname(HERE)
 CSRC = os.path.join(HERE, "csrc")
 INCLUDE = os.path.join(ROOT, "include")
 LIBRARY = os.path.join(HERE, "libxnn_amd.so")
-SOURCES = ("edge.hip", "segment.hip", "linear_message.hip", "basis_message.hip", "graph.hip", "d4.hip", "readout.hip",
+SOURCES = ("edge.hip", "segment.hip", "basis_message.hip", "graph.hip", "d4.hip", "readout.hip",
            "atm.hip", "eeq.hip", "radial_mlp.hip", "uvu_conv.hip", "pair.hip", "d4_tiles.hip")
 ARCH = os.environ.get("XNN_AMD_ARCH", "gfx950")
 
