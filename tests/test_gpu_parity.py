@@ -625,6 +625,25 @@ def test_force_reduce_with_virial_finish_matches_the_two_step_path(dtype):
     assert torch.equal(v0.cpu(), torch.zeros(1, 3, 3, dtype=torch.float64))
 
 
+def test_scatter_sum_sees_an_index_changed_in_place():
+    """The CSR of an index is cached while its contents stay the same: an index tensor
+    changed in place between two calls (its version moves) gets a new CSR, so the second
+    sum equals index_add over the new index, not the old one."""
+    from xnn_amd.functional import scatter_sum
+    _note("scatter_sum with an index changed in place")
+    gen = torch.Generator().manual_seed(31)
+    src = torch.randn(500, 7, generator=gen).to(DEV)
+    index = torch.randint(0, 40, (500,), generator=gen).to(DEV)
+    first = scatter_sum(src, index, 40)
+    ref = torch.zeros(40, 7, device=DEV).index_add_(0, index, src)
+    torch.testing.assert_close(first, ref, rtol=1e-6, atol=1e-6)
+    index[:250] = (index[:250] + 7) % 40          # same tensor object, new contents
+    second = scatter_sum(src, index, 40)
+    ref2 = torch.zeros(40, 7, device=DEV).index_add_(0, index, src)
+    torch.testing.assert_close(second, ref2, rtol=1e-6, atol=1e-6)
+    assert not torch.allclose(first, second)
+
+
 def test_segment_gather_and_structure_sums():
     import oracle.reference as R
     import xnn_amd as xa

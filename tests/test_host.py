@@ -305,7 +305,7 @@ def test_force_stress_output_contract_branches():
 
     out = xa.ForceStressOutput(Direct())(copy.copy(g))
     assert torch.equal(out["forces"], torch.ones_like(g.pos))
-    with pytest.raises(ValueError, match="direct force"):
+    with pytest.raises(ValueError, match="predicted by the model itself"):
         xa.ForceStressOutput(Direct(extra=True))(copy.copy(g))
 
     class FormsForces(torch.nn.Module):

@@ -431,18 +431,21 @@ def unique_pairs(pos: Tensor, cutoff: float, cell: Optional[Tensor] = None,
     once in either order), oriented smaller index first (the reversed displacement takes
     the negated shift)."""
     if half is None:
-        edge_index, shifts = build_neighbor_list(pos, cutoff, cell, pbc)
-        a, b = edge_index[0], edge_index[1]
-        keep = (a < b).nonzero()[:, 0]
+        # the full list holds every pair in both orders: take the order src < dst
+        edge_index, shift = build_neighbor_list(pos, cutoff, cell, pbc)
+        first, second = edge_index[0], edge_index[1]
+        take = first < second
     else:
-        (i, j), shifts = half
-        swap = i > j
-        a, b = torch.where(swap, j, i), torch.where(swap, i, j)
-        shifts = torch.where(swap[:, None], -shifts, shifts)
-        keep = (a != b).nonzero()[:, 0]
-    a, b, shifts = a[keep], b[keep], shifts[keep]
-    order = torch.argsort(a.to(torch.int32), stable=True)
-    return a[order], b[order], shifts[order]
+        # each pair once, in either order: every pair but an atom's own images
+        (first, second), shift = half
+        take = first != second
+    # orient smaller index first; the reversed displacement negates the shift
+    flipped = first > second
+    i, k = torch.minimum(first, second), torch.maximum(first, second)
+    shift = torch.where(flipped[:, None], -shift, shift)
+    rows = take.nonzero().squeeze(1)
+    rows = rows.index_select(0, torch.argsort(i.index_select(0, rows).to(torch.int32), stable=True))
+    return i.index_select(0, rows), k.index_select(0, rows), shift.index_select(0, rows)
 
 
 def batched_neighbor_list(pos: Tensor, n_atoms: Tensor, cutoff: float,
@@ -541,6 +544,21 @@ def nearest_edges(dist, dst: Tensor, num_nodes: int, k: int):
     return order[rank < k], per_atom
 
 
+def _nearest_in_edges(pos: Tensor, cell: Optional[Tensor], edge_index: Tensor,
+                      shifts: Tensor, k: int) -> tuple[Tensor, Tensor]:
+    """The edges of :func:`nearest_edges` (each receiver's ``k`` nearest senders), the
+    lengths taken in float64 from the positions, shifts and cell whatever their dtype."""
+    f64 = torch.float64
+    src, dst = edge_index[0], edge_index[1]
+    disp = pos.to(f64).index_select(0, dst) - pos.to(f64).index_select(0, src)
+    if cell is not None:
+        disp = disp + shifts.to(f64) @ cell.to(f64)
+    kept, _ = nearest_edges(torch.linalg.vector_norm(disp, dim=1), dst, pos.shape[0], k)
+    if kept is None:
+        return edge_index, shifts
+    return edge_index.index_select(1, kept), shifts.index_select(0, kept)
+
+
 def structure_to_graph(s: dict, cutoff: float, device=None,
                        max_neighbors: Optional[int] = None) -> AtomicGraph:
     """One structure (dict of arrays) to a graph (dataset.py:21-175): ``pos``,
@@ -558,14 +576,9 @@ def structure_to_graph(s: dict, cutoff: float, device=None,
     pbc = (torch.as_tensor(s["pbc"], dtype=torch.bool) if s.get("pbc") is not None
            else (torch.ones(3, dtype=torch.bool) if cell is not None else None))
     edge_index, cell_shifts = build_neighbor_list(pos, cutoff, cell, pbc)
-    if max_neighbors is not None and edge_index.shape[1] > 0:
-        p = pos.to(torch.float64)
-        vec = p.index_select(0, edge_index[1]) - p.index_select(0, edge_index[0])
-        if cell is not None:
-            vec = vec + cell_shifts.to(torch.float64) @ cell.to(torch.float64)
-        keep, _ = nearest_edges(vec.norm(dim=-1), edge_index[1], pos.shape[0], int(max_neighbors))
-        if keep is not None:
-            edge_index, cell_shifts = edge_index[:, keep], cell_shifts[keep]
+    if max_neighbors is not None and edge_index.numel():
+        edge_index, cell_shifts = _nearest_in_edges(pos, cell, edge_index, cell_shifts,
+                                                    int(max_neighbors))
     n = pos.shape[0]
     dev = pos.device
     charge = s.get("total_charge", s.get("charge"))
@@ -588,34 +601,31 @@ def collate(graphs: Sequence[AtomicGraph]) -> AtomicGraph:
     the running atom count, a ``batch`` vector, zero cells for molecules when any
     structure has a cell."""
     dtype, device = graphs[0].pos.dtype, graphs[0].pos.device
-    has_cell = any(g.cell is not None for g in graphs)
-    has_q = any(g.total_charge is not None for g in graphs)
-    pos, z, batch, n_atoms, ei, cs, cells, pbcs, qs = [], [], [], [], [], [], [], [], []
-    node_offset = graph_offset = 0
-    for g in graphs:
-        b = g.num_graphs
-        pos.append(g.pos)
-        z.append(g.atomic_numbers)
-        batch.append(g.batch + graph_offset)
-        n_atoms.append(g.n_atoms)
-        ei.append(g.edge_index + node_offset)
-        cs.append(g.cell_shifts)
-        node_offset += g.num_nodes
-        graph_offset += b
-        if has_cell:
-            if g.cell is not None:
-                cells.append(g.cell)
-                pbcs.append(g.pbc.to(device) if g.pbc is not None
-                            else torch.ones((b, 3), dtype=torch.bool, device=device))
-            else:
-                cells.append(torch.zeros((b, 3, 3), dtype=dtype, device=device))
-                pbcs.append(torch.zeros((b, 3), dtype=torch.bool, device=device))
-        if has_q:
-            qs.append(g.total_charge if g.total_charge is not None
-                      else torch.zeros(b, dtype=dtype, device=device))
+    # where each graph's atoms and structures start in the batch
+    node_start = np.cumsum([0] + [g.num_nodes for g in graphs])[:-1].tolist()
+    graph_start = np.cumsum([0] + [g.num_graphs for g in graphs])[:-1].tolist()
+    periodic = any(g.cell is not None for g in graphs)
+    charged = any(g.total_charge is not None for g in graphs)
+
+    def cell_and_pbc(g: AtomicGraph) -> tuple[Tensor, Tensor]:
+        # a molecule in a periodic batch: a zero cell, periodic along no axis
+        if g.cell is None:
+            return (torch.zeros((g.num_graphs, 3, 3), dtype=dtype, device=device),
+                    torch.zeros((g.num_graphs, 3), dtype=torch.bool, device=device))
+        pbc = (torch.ones((g.num_graphs, 3), dtype=torch.bool, device=device)
+               if g.pbc is None else g.pbc.to(device))
+        return g.cell, pbc
+
+    cells = [cell_and_pbc(g) for g in graphs] if periodic else None
     return AtomicGraph(
-        pos=torch.cat(pos, 0), atomic_numbers=torch.cat(z, 0), edge_index=torch.cat(ei, 1),
-        cell_shifts=torch.cat(cs, 0), batch=torch.cat(batch, 0), n_atoms=torch.cat(n_atoms, 0),
-        cell=torch.cat(cells, 0) if has_cell else None,
-        pbc=torch.cat(pbcs, 0) if has_cell else None,
-        total_charge=torch.cat(qs, 0) if has_q else None)
+        pos=torch.cat([g.pos for g in graphs], 0),
+        atomic_numbers=torch.cat([g.atomic_numbers for g in graphs], 0),
+        edge_index=torch.cat([g.edge_index + o for g, o in zip(graphs, node_start)], 1),
+        cell_shifts=torch.cat([g.cell_shifts for g in graphs], 0),
+        batch=torch.cat([g.batch + o for g, o in zip(graphs, graph_start)], 0),
+        n_atoms=torch.cat([g.n_atoms for g in graphs], 0),
+        cell=torch.cat([c for c, _ in cells], 0) if periodic else None,
+        pbc=torch.cat([p for _, p in cells], 0) if periodic else None,
+        total_charge=torch.cat([g.total_charge if g.total_charge is not None
+                                else torch.zeros(g.num_graphs, dtype=dtype, device=device)
+                                for g in graphs], 0) if charged else None)

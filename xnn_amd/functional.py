@@ -3,7 +3,8 @@
 
 On GPU tensors ``scatter_sum`` / ``gather_rows`` / ``structure_sum`` run the HIP
 segmented reductions over a CSR of ``index`` (built once per index tensor and
-cached by identity, like the reference's ``orderings``, csr.py:35-51); on CPU
+cached by identity and contents version, like the reference's ``orderings``,
+csr.py:35-51); on CPU
 tensors they are the reference's ``index_add`` formulation.
 """
 from __future__ import annotations
@@ -18,16 +19,24 @@ from . import _lib
 _last = [None]
 
 
+def _csr_key(index: Tensor, n: int) -> tuple:
+    # the same tensor object with the same storage, contents version and size: an index
+    # changed in place (its _version moves) or rebound to other memory gets a new CSR
+    return (index.data_ptr(), index._version, index.numel(), index.dtype, n)
+
+
 def csr_of(index: Tensor, n: int) -> Tuple[Tensor, Tensor, object]:
-    """``(index32, ptr (n+1), perm or None)`` of a 1-D index over ``n`` buckets."""
+    """``(index32, ptr (n+1), perm or None)`` of a 1-D index over ``n`` buckets; the last
+    one is cached for the same index tensor while its contents are unchanged."""
     hit = _last[0]
-    if hit is not None and hit[0] is index and hit[1] == n:
+    key = _csr_key(index, n)
+    if hit is not None and hit[0] is index and hit[1] == key:
         return hit[2]
     from .plan import build_plan
     pair = torch.stack([index, index]).to(torch.int64)
     plan = build_plan(pair, None, n)
     out = (plan.dst, plan.ptr_dst, plan.perm_dst)
-    _last[0] = (index, n, out)
+    _last[0] = (index, key, out)
     return out
 
 

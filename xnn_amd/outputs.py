@@ -10,6 +10,7 @@ deforms positions or cell in the forward.
 """
 from __future__ import annotations
 
+import itertools
 from typing import Optional
 
 import torch
@@ -30,24 +31,21 @@ class ForceStressOutput(nn.Module):
         self.cutoff = getattr(model, "cutoff", None)
 
     def _model_dtype(self) -> Optional[torch.dtype]:
-        """The wrapped model's floating dtype: that of its first floating parameter, else of
-        its first floating buffer, else ``None`` (outputs.py:73-94). Remembered per model
-        object, and re-checked against the tensor it came from (``.to()`` replaces buffers)."""
-        memo = self.__dict__.get("_dtype_memo")
-        if memo is not None and memo[0] is self.model:
-            owner, name, t = memo[1:]
-            if owner is None or owner._buffers.get(name) is t:
-                return t.dtype
-        for t in self.model.parameters():
-            if t.is_floating_point():
-                self.__dict__["_dtype_memo"] = (self.model, None, None, t)
-                return t.dtype
-        for owner in self.model.modules():
-            for name, t in owner._buffers.items():
-                if t is not None and t.is_floating_point():
-                    self.__dict__["_dtype_memo"] = (self.model, owner, name, t)
-                    return t.dtype
-        return None
+        """The floating dtype the wrapped model computes in: its parameters' when it has a
+        floating parameter, else its buffers', else ``None`` (outputs.py:73-94). The search
+        stops at the first floating tensor, normally the first parameter."""
+        tensors = itertools.chain(self.model.parameters(), self.model.buffers())
+        first = next((t for t in tensors if t.is_floating_point()), None)
+        return None if first is None else first.dtype
+
+    def _direct_evaluation(self, data, plan) -> bool:
+        """True in evaluation mode when the model offers to form forces and the strain
+        derivative in its own forward (``forms_forces(data)``), so that no autograd pass
+        is needed; never with a plan or when forces are not wanted."""
+        offer = getattr(self.model, "forms_forces", None)
+        if self.training or not self.compute_forces or plan is not None or not callable(offer):
+            return False
+        return bool(offer(data))
 
     @staticmethod
     def _zero_strain(data) -> Tensor:
@@ -60,11 +58,8 @@ class ForceStressOutput(nn.Module):
 
     def forward(self, data, plan=None) -> dict:
         create_graph = self.training
-        # a model that forms its own forces and strain derivative in evaluation: no
-        # autograd pass (outputs.py:136-143)
-        forms_forces = getattr(self.model, "forms_forces", None)
-        if (callable(forms_forces) and not self.training and self.compute_forces and plan is None
-                and forms_forces(data)):
+        if self._direct_evaluation(data, plan):
+            # the model returns forces and its virial itself (outputs.py:136-143)
             out = self.model.forward_direct(data)
             virial = out.pop("virial")
             if self.compute_stress and data.cell is not None:
@@ -147,10 +142,13 @@ class ForceStressOutput(nn.Module):
         if energy is None:
             return self._deferred_energy_stress(out, data, strain)
         # a model that predicts its forces directly returns them itself (outputs.py:191-194)
+        # forces the model predicts itself are returned as they are (outputs.py:191-194);
+        # an added energy term would then have no forces of its own, so that is refused
         direct = "forces" in out
         if direct and "energy_sr" in out:
-            raise ValueError("a model with direct force prediction cannot be combined with "
-                             "add-on energy terms (long-range, dispersion)")
+            raise ValueError("forces predicted by the model itself leave no gradient for the "
+                             "added energy terms (dispersion, long-range): use a conservative "
+                             "model with them")
         inputs, need = [], []
         if self.compute_forces and not direct:
             inputs.append(data.pos)

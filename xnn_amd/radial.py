@@ -21,7 +21,7 @@
 from __future__ import annotations
 
 import math
-from typing import Callable, List, Optional, Sequence, Tuple
+from typing import Callable, List, NamedTuple, Optional, Sequence, Tuple
 
 import torch
 import torch.nn.functional as F
@@ -185,18 +185,65 @@ def fused_hidden(x: Tensor, weights: Sequence[Tensor], scales: Sequence[float]) 
     return FusedHidden.apply(x, tuple(float(c) for c in scales), nodes, *weights)
 
 
+class _Stage(NamedTuple):
+    """One layer as ``post * act(gain * (x @ weight))`` (``act`` None: ``gain * (x @ weight)``,
+    the output variance already in ``gain``)."""
+    weight: Tensor
+    gain: float
+    act: Optional[Callable[[Tensor], Tensor]]
+    post: float
+
+
+def _stages(net: nn.Module) -> Optional[List[_Stage]]:
+    """The layers of a :class:`FullyConnectedNet` as stages (``None`` when a child is not
+    one of its layers). e3nn's layer is ``act(x W / sqrt(h_in var_in)) sqrt(var_out)``, and a
+    normalized activation carries its constant: both scalars are pulled out of the
+    activation so that a stage's ``post`` can be merged into the next stage's ``gain``."""
+    out: List[_Stage] = []
+    for layer in net.children():
+        if not isinstance(layer, _Layer):
+            return None
+        act, post = layer.act, math.sqrt(layer.var_out)
+        if isinstance(act, Normalize2Mom):
+            post = post if act._is_id else post * act.cst
+            act = act.f
+        gain = 1.0 / math.sqrt(layer.h_in * layer.var_in)
+        if act is None:
+            gain, post = gain * post, 1.0
+        out.append(_Stage(layer.weight, gain, act, post))
+    return out
+
+
+def _wants_checkpoint(mode: str, training: bool, x: Tensor, depth: int) -> bool:
+    """Whether the hidden activations are recomputed in the backward instead of kept:
+    never for ``"off"``, a single layer or an input that needs no gradient; always for
+    ``"on"``; for ``"auto"`` in evaluation mode from :data:`RECOMPUTE_MIN_EDGES` rows."""
+    if mode == "off" or depth < 2 or not (torch.is_grad_enabled() and x.requires_grad):
+        return False
+    return mode == "on" or (not training and x.shape[0] >= RECOMPUTE_MIN_EDGES)
+
+
+def _select_columns(y: Tensor, index: Optional[Tensor], scale: Optional[Tensor]) -> Tensor:
+    if scale is None:
+        return y
+    if index is not None:
+        y = y.index_select(-1, index)
+    return y * scale
+
+
 class RadialNet(FullyConnectedNet, FastPathModule):
     """Per-edge radial network (gnn/models/blocks.py:223-417).
 
-    A :class:`FullyConnectedNet` (same parameters and ``state_dict`` keys) whose forward
-    folds each layer's normalization and the previous activation's constant into one
-    scalar factor per product (blocks.py:336-365). With ``out_index`` / ``out_scale`` it
-    returns the output columns ``out_index`` times ``out_scale``, mapped on the last
-    matrix. On the fast path (``fast_active``, evaluation mode, float32 on the GPU, one to
-    three hidden SiLU layers of at most 128 units, at most 32 inputs) the hidden layers run
-    on :func:`fused_hidden`; otherwise, with ``recompute`` ("auto": evaluation mode from
-    :data:`RECOMPUTE_MIN_EDGES` edges; "on"; "off") they are recomputed in the backward
-    by checkpointing, or kept.
+    A :class:`FullyConnectedNet` (same parameters and ``state_dict`` keys) evaluated as
+    stages ``post * act(gain * (x @ W))`` in which each stage's ``post`` is merged into the
+    next stage's ``gain``, so that every layer costs one product and one scalar. With
+    ``out_scale`` it returns the output columns ``out_index`` (all when None) times
+    ``out_scale``; for a linear last layer the selection and scale are applied to its weight
+    before the product. On the fast path (``fast_active``, evaluation mode, float32 on the
+    GPU, one to three hidden SiLU layers of at most 128 units, at most 32 inputs) the hidden
+    layers run on :func:`fused_hidden`; otherwise, with ``recompute`` ("auto": evaluation
+    mode from :data:`RECOMPUTE_MIN_EDGES` edges; "on"; "off") they are recomputed in the
+    backward by checkpointing, or kept.
     """
 
     def __init__(self, hs, act=None, variance_in=1, variance_out=1, out_act=False):
@@ -204,102 +251,52 @@ class RadialNet(FullyConnectedNet, FastPathModule):
         self.recompute = "auto"
         self.fast_active = False
 
-    # ------------------------------------------------------------------ plan
-    @staticmethod
-    def _parts(layer: nn.Module):
-        """``(weight, activation, constant after it, h_in var_in)`` (blocks.py:303-315)."""
-        act, const = layer.act, math.sqrt(layer.var_out)
-        if isinstance(act, Normalize2Mom):
-            const *= 1.0 if act._is_id else act.cst
-            act = act.f
-        return layer.weight, act, const, layer.h_in * layer.var_in
-
-    def _plan(self):
-        """``(hidden, last)``: per hidden layer ``(layer, activation, factor)`` and for the
-        last ``(layer, activation, constant, factor)`` (blocks.py:328-365), or ``None`` for
-        layers that are not :class:`_Layer`."""
-        layers = tuple(self._modules.values())
-        key = tuple(id(m) for m in layers)
-        hit = self.__dict__.get("_plan_cache")
-        if hit is not None and hit[0] == key:
-            return hit[1]
-        plan = None
-        if all(isinstance(m, _Layer) for m in layers):
-            hidden, c = [], 1.0
-            for m in layers[:-1]:
-                _, act, const, d = self._parts(m)
-                hidden.append((m, act, c / math.sqrt(d)))
-                c = const
-            _, act, const, d = self._parts(layers[-1])
-            plan = (hidden, (layers[-1], act, const, c / math.sqrt(d)))
-        self.__dict__["_plan_cache"] = (key, plan)
-        return plan
-
     def fast_supported(self, device: torch.device, dtype: torch.dtype) -> bool:
-        if device.type != "cuda" or dtype != torch.float32:
+        stages = _stages(self)
+        if device.type != "cuda" or dtype != torch.float32 or stages is None:
             return False
-        plan = self._plan()
-        if plan is None or not 1 <= len(plan[0]) <= MAX_FUSED_LAYERS:
-            return False
-        return (self.hs[0] <= MAX_FUSED_INPUTS
-                and all(act is F.silu and m.weight.shape[1] <= MAX_FUSED_WIDTH
-                        for m, act, _ in plan[0]))
+        hidden = stages[:-1]
+        return (1 <= len(hidden) <= MAX_FUSED_LAYERS and self.hs[0] <= MAX_FUSED_INPUTS
+                and all(st.act is F.silu and st.weight.shape[1] <= MAX_FUSED_WIDTH
+                        for st in hidden))
 
-    # ------------------------------------------------------------------ forward
-    def _hidden(self, x: Tensor) -> Tensor:
-        for m, act, factor in self._plan()[0]:
-            x = x @ (m.weight * factor)
-            if act is not None:
-                x = act(x)
+    @staticmethod
+    def _run_hidden(x: Tensor, hidden: Sequence[_Stage]) -> Tensor:
+        carry = 1.0
+        for st in hidden:
+            x = x @ (st.weight * (st.gain * carry))
+            if st.act is not None:
+                x = st.act(x)
+            carry = st.post
         return x
-
-    def _recomputes(self, x: Tensor) -> bool:
-        if self.recompute == "off" or len(self) < 2:
-            return False
-        if not (torch.is_grad_enabled() and x.requires_grad):
-            return False
-        if self.recompute == "on":
-            return True
-        return not self.training and x.shape[0] >= RECOMPUTE_MIN_EDGES
 
     def forward(self, x: Tensor, out_index: Optional[Tensor] = None,
                 out_scale: Optional[Tensor] = None) -> Tensor:
-        plan = self._plan()
-        if plan is None:
-            for m in self:
-                x = m(x)
-            if out_scale is not None:
-                if out_index is not None:
-                    x = x.index_select(1, out_index)
-                x = x * out_scale
-            return x
-        lead = x.shape[:-1]
-        x = x.reshape(-1, x.shape[-1])
-        if (self.fast_active and not self.training and x.is_cuda and x.dtype == torch.float32
-                and plan[0]):
-            h = fused_hidden(x, [m.weight for m, _, _ in plan[0]], [f for _, _, f in plan[0]])
-        elif self._recomputes(x):
+        stages = _stages(self)
+        if stages is None:
+            for layer in self:
+                x = layer(x)
+            return _select_columns(x, out_index, out_scale)
+        shape = x.shape
+        x = x.reshape(-1, shape[-1])
+        hidden, last = stages[:-1], stages[-1]
+        if (self.fast_active and not self.training and x.is_cuda
+                and x.dtype == torch.float32 and hidden):
+            carried = [1.0] + [st.post for st in hidden[:-1]]
+            h = fused_hidden(x, [st.weight for st in hidden],
+                             [st.gain * c for st, c in zip(hidden, carried)])
+        elif _wants_checkpoint(self.recompute, self.training, x, len(stages)):
             from torch.utils.checkpoint import checkpoint
-            h = checkpoint(self._hidden, x, use_reentrant=False)
+            h = checkpoint(self._run_hidden, x, hidden, use_reentrant=False)
         else:
-            h = self._hidden(x)
-        m, act, const, alpha = plan[1]
-        w = m.weight
-        if act is None:
-            if out_scale is not None:
-                if out_index is not None:
-                    w = w.index_select(1, out_index)
-                w = w * out_scale
-            y = h @ (w * (alpha * const))
+            h = self._run_hidden(x, hidden)
+        scale = last.gain * (hidden[-1].post if hidden else 1.0)
+        if last.act is None:
+            y = h @ (_select_columns(last.weight, out_index, out_scale) * scale)
         else:
-            y = act(h @ (w * alpha))
-            if const != 1.0:
-                y = y * const
-            if out_scale is not None:
-                if out_index is not None:
-                    y = y.index_select(1, out_index)
-                y = y * out_scale
-        return y.reshape(lead + y.shape[-1:])
+            y = _select_columns(last.act(h @ (last.weight * scale)) * last.post, out_index,
+                                out_scale)
+        return y.reshape(shape[:-1] + y.shape[-1:])
 
 
 def set_recompute_radial(model: nn.Module, recompute: str = "auto") -> nn.Module:
