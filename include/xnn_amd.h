@@ -38,6 +38,8 @@ typedef struct ihipStream_t* xnn_stream_t; /* == hipStream_t */
 enum { XNN_OK = 0, XNN_EINVAL = 1, XNN_ECAPACITY = 2, XNN_EHIP = 3 };
 enum { XNN_F32 = 0, XNN_F64 = 1 };
 enum { XNN_BASIS_BESSEL = 0, XNN_BASIS_GAUSSIAN = 1 };
+/* Envelopes multiply the radial basis and are zero for r >= cutoff (cutoff.py:41, 125);
+ * XNN_ENV_NONE is the unit step (r < cutoff) with no smooth decay. */
 enum { XNN_ENV_POLYNOMIAL = 0, XNN_ENV_COSINE = 1, XNN_ENV_NONE = 2 };
 
 /* Last error message of the calling thread ("" if none). */

@@ -96,10 +96,12 @@ def canonical(edge_index: np.ndarray, shifts: np.ndarray) -> np.ndarray:
 def nearest_edges(dist: np.ndarray, dst: np.ndarray, num_nodes: int, k: int):
     """The kept edge ids of max_neighbors, by brute force: for every receiver in turn, its
     edges sorted by (length, id), the first k (neighborlist.py:509-552, the case where some
-    receiver has more than k edges)."""
+    receiver has more than k edges). A NaN length sorts after every number, as the
+    reference's stable ``torch.sort`` places it."""
     out = []
     for i in range(num_nodes):
         mine = [e for e in range(len(dst)) if dst[e] == i]
-        mine.sort(key=lambda e: (float(dist[e]), e))
+        mine.sort(key=lambda e: (math.isnan(float(dist[e])),
+                                 0.0 if math.isnan(float(dist[e])) else float(dist[e]), e))
         out.extend(mine[:k])
     return np.asarray(out, dtype=np.int64)

@@ -1136,6 +1136,13 @@ def test_nearest_edges_on_the_gpu(dtype):
             assert _lib.calls.get("xnn_nearest_edges_fill", 0) == before + 1
             want = N.nearest_edges(d.astype(np.float32) if dtype == torch.float32 else d, dst, n, k)
             np.testing.assert_array_equal(keep.cpu().numpy(), want)
+    # NaN lengths rank after every number (every slot of the kept rows written once)
+    dst = np.repeat(np.arange(30), 20)
+    d = np.round(rng.uniform(0, 4, dst.size), 1)
+    d[rng.random(dst.size) < 0.7] = np.nan
+    keep, _ = nearest_edges(torch.tensor(d, dtype=dtype, device=DEV), torch.tensor(dst, device=DEV),
+                            30, 9)
+    np.testing.assert_array_equal(keep.cpu().numpy(), N.nearest_edges(d, dst, 30, 9))
     s = synthetic.water_box(n_molecules=216, box=18.6, grid=6, seed=2)
     gpu = xa.structure_to_graph(s.as_dict(), 5.0, device=DEV, max_neighbors=12)
     cpu = xa.structure_to_graph(s.as_dict(), 5.0, max_neighbors=12)
@@ -1170,7 +1177,7 @@ def test_pair_style_entry_matches_force_stress_output(case):
     assert _lib.calls.get("xnn_sh_pair_energy_forces", 0) == before + 1
     e_ref = float(out["energy"].detach().reshape(-1)[0])
     assert abs(float(pair["total_energy"][0]) - e_ref) <= 1e-6 * max(1.0, abs(e_ref))
-    torch.testing.assert_close(pair["node_energy"], out["node_energy"].float(), atol=1e-5, rtol=0)
+    torch.testing.assert_close(pair["node_energy"], out["node_energy"].double(), atol=1e-5, rtol=0)
     torch.testing.assert_close(pair["forces"].double(), out["forces"].double(), atol=1e-5, rtol=0)
     if g.cell is not None:
         vol = float(torch.det(g.cell[0].double()))
@@ -1186,3 +1193,82 @@ def test_pair_style_entry_matches_force_stress_output(case):
     bad[0, 0] = g.num_nodes + 5
     with pytest.raises(_lib.XnnError, match="outside"):
         LAMMPSWrapper(model)(g.pos, bad, g.cell_shifts, g.atomic_numbers, cell)
+
+
+@pytest.mark.parametrize("case", ["d4_fused_core", "d4_other_core", "d4_alone"])
+def test_pair_style_wrapper_with_dispersion_and_other_cores(case):
+    """deploy.LAMMPSWrapper on a model wrapped in D4 (lammps.py:70-79, 128-134): the core on
+    the edges within its own cutoff of a longer pair-style list (6.5 A against the model's
+    5.0), the D4 head's per-atom energies, forces and virial added; against
+    ForceStressOutput(D4Dispersion(core)) on the core's own graph. The cores: the fused
+    pair-style kernels, a core they do not take (48 channels: the ForceStressOutput path),
+    and no core (D4 alone)."""
+    import os
+    import xnn_amd as xa
+    from xnn_amd import _lib, synthetic
+    from xnn_amd.deploy import LAMMPSWrapper
+    from xnn_amd.dispersion import D4Dispersion
+    _note(f"pair-style wrapper {case}")
+    tables = os.path.join(os.path.dirname(__file__), "golden", "d4_tables_hcnoar.npz")
+    s = synthetic.organic_box(n_atoms=300, box=14.0, seed=7)
+    g = xa.structure_to_graph(s.as_dict(), 5.0, device=DEV)
+    g.pos, g.cell = g.pos.float(), g.cell.float()
+    if case == "d4_alone":
+        model = D4Dispersion(None, tables=tables).to(DEV)
+    else:
+        kw = dict(channels=48) if case == "d4_other_core" else dict(channels=64)
+        core = xa.ShEdgePotential(cutoff=5.0, species=(1, 6, 7, 8), l_max=2, **kw).to(DEV)
+        model = D4Dispersion(core, tables=tables).to(DEV)
+    out = xa.ForceStressOutput(model, compute_stress=True).eval()(g)
+    wide = xa.structure_to_graph(s.as_dict(), 6.5, device=DEV)
+    wrapper = LAMMPSWrapper(model, cutoff=6.5)
+    assert wrapper.fused_core == (case == "d4_fused_core")
+    before = _lib.calls.get("xnn_sh_pair_energy_forces", 0)
+    pair = wrapper(wide.pos.float(), wide.edge_index, wide.cell_shifts, wide.atomic_numbers,
+                   wide.cell[0].float())
+    assert _lib.calls.get("xnn_sh_pair_energy_forces", 0) == before + int(wrapper.fused_core)
+    e_ref = float(out["energy"].detach().reshape(-1)[0])
+    assert abs(float(pair["total_energy"][0]) - e_ref) <= 1e-6 * max(1.0, abs(e_ref)), \
+        (float(pair["total_energy"][0]), e_ref)
+    torch.testing.assert_close(pair["node_energy"], out["node_energy"].detach().double(),
+                               atol=1e-5, rtol=0)
+    torch.testing.assert_close(pair["forces"].double(), out["forces"].double(), atol=1e-5, rtol=0)
+    vol = float(torch.det(g.cell[0].double()))
+    want = -vol * out["stress"][0].double()
+    torch.testing.assert_close(pair["virial"], want, atol=1e-4 * max(1.0, float(want.abs().max())),
+                               rtol=0)
+    # the list must reach the model's cutoff
+    if case != "d4_alone":
+        with pytest.raises(ValueError, match="must reach"):
+            LAMMPSWrapper(model, cutoff=4.0)
+
+
+@pytest.mark.parametrize("basis", ["bessel", "gaussian"])
+def test_every_envelope_is_zero_from_the_cutoff(basis):
+    """The envelopes of the kernels vanish for r >= rc (cutoff.py:41, 125), the unit
+    envelope (XNN_ENV_NONE) included: radial features of edges of a list longer than the
+    cutoff are zero, their gradient too; inside the cutoff the unit envelope leaves the
+    basis as it is."""
+    import oracle.reference as R
+    from xnn_amd.ops import edge_embed
+    _note(f"envelopes at the cutoff {basis}")
+    rc, K = 4.0, 6
+    r = torch.linspace(0.3, 1.6 * rc, 801, dtype=torch.float64)
+    d = torch.randn(801, 3, dtype=torch.float64, generator=torch.Generator().manual_seed(3))
+    vec = (d / d.norm(dim=1, keepdim=True) * r[:, None]).to(DEV).requires_grad_(True)
+    table = (torch.arange(1, K + 1, dtype=torch.float64) * np.pi if basis == "bessel"
+             else torch.linspace(0.0, rc, K, dtype=torch.float64))
+    gamma = 0.5 / (rc / (K - 1)) ** 2
+    inside = (r < rc).to(DEV)
+    for env in ("none", "polynomial", "cosine"):
+        _, _, rad = edge_embed(vec, table.to(DEV), n_rbf=K, basis=basis, envelope=env,
+                               poly_p=6, l_max=1, cutoff=rc, prefactor=(2.0 / rc) ** 0.5,
+                               gamma=gamma, sh_sign=1)
+        assert torch.equal(rad[~inside], torch.zeros_like(rad[~inside])), env
+        (g,) = torch.autograd.grad(rad.sum(), (vec,))
+        assert torch.equal(g[~inside], torch.zeros_like(g[~inside])), env
+        if env == "none":
+            rr = r[inside.cpu()].to(DEV)
+            want = (R.bessel(rr.cpu(), K, rc, prefactor=(2.0 / rc) ** 0.5) if basis == "bessel"
+                    else torch.exp(-gamma * (rr.cpu()[:, None] - table[None, :]) ** 2))
+            torch.testing.assert_close(rad[inside].cpu(), want, rtol=1e-12, atol=1e-12)

@@ -394,3 +394,20 @@ def test_bessel_exact_constants():
     assert not rbf.exact_constants() and rbf.freqs[2] == 7.0
     assert not BesselRBF(8, 5.0).exact_constants()         # float32 buffer
     assert not BesselRBF(8, 5.0, trainable=True).double().exact_constants()
+
+
+def test_no_alloc_entry_refuses_sizes_beyond_its_scratch_array_before_any_device_call():
+    """xnn_segment_reduce_f64_noalloc checks the partial sums' size against its file-scope
+    scratch array before it touches the device: the refusal needs no GPU and no buffers
+    (NULL pointers here), so an oversized call can never reach a kernel."""
+    import ctypes
+    from xnn_amd import _lib
+    lib = _lib.load()
+    cap = int(lib.xnn_segment_reduce_noalloc_max_bytes())
+    n, F = 1 << 20, 1024       # 256 chunks of 1024 features: 2 MiB of partials
+    assert int(lib.xnn_segment_reduce_workspace_bytes(n, F, 1)) > cap
+    rc = lib.xnn_segment_reduce_f64_noalloc(_lib.XNN_F32, None, n, F, None, 1, None, None)
+    assert rc == _lib.XNN_EINVAL
+    assert b"scratch" in lib.xnn_last_error()
+    # within the limit the same call would go on to the device: not made here
+    assert int(lib.xnn_segment_reduce_workspace_bytes(1 << 10, 8, 1)) <= cap

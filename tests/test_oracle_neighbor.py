@@ -170,6 +170,14 @@ def test_nearest_edges_matches_brute_force():
                 continue
             assert np.array_equal(keep.numpy(), N.nearest_edges(d.numpy(), dst.numpy(), n, k))
             assert per_atom == (k if counts.min() >= k else None)
+    # NaN lengths sort after every number (as torch.sort places them): a row with more
+    # than k edges but fewer than k numbers keeps its numbers first, then NaN edges by id
+    dst = torch.tensor([0] * 6 + [1] * 3)
+    d = torch.tensor([float("nan"), 2.0, float("nan"), 1.0, float("nan"), float("nan"),
+                      0.5, float("nan"), 0.25])
+    keep, _ = nearest_edges(d, dst, 2, 4)
+    assert keep.tolist() == [3, 1, 0, 2, 8, 6, 7]
+    assert keep.tolist() == N.nearest_edges(d.numpy(), dst.numpy(), 2, 4).tolist()
     # every receiver with the same count <= k: grouped keeps in place, ungrouped regroups
     dst = torch.tensor([0, 0, 1, 1, 2, 2])
     assert nearest_edges(torch.zeros(6), dst, 3, 4) == (None, 2)

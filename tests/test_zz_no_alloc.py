@@ -53,22 +53,3 @@ def test_no_alloc_matches_the_workspace_entry_point():
             assert torch.equal(got, want), (n, F)
             ref = torch.stack([src[a:b].double().sum(0).cpu() for a, b in zip(bounds, bounds[1:])])
             np.testing.assert_allclose(got.cpu(), ref, rtol=1e-12, atol=1e-10)
-
-
-def test_no_alloc_rejects_sizes_beyond_the_scratch_array():
-    from xnn_amd import _lib
-    lib = _lib.load()
-    cap = int(lib.xnn_segment_reduce_noalloc_max_bytes())
-    # 256 chunks of 1024 features need 2 MiB of partials: refused before any launch
-    n, F = 1 << 20, 1024
-    need = int(lib.xnn_segment_reduce_workspace_bytes(n, F, 1))
-    assert need > cap
-    seg = torch.tensor([0, n], dtype=torch.int64, device=DEV)
-    out = torch.empty((1, F), dtype=torch.float64, device=DEV)
-    src = torch.empty((1, 1), dtype=torch.float32, device=DEV)   # never read: refused first
-    rc = lib.xnn_segment_reduce_f64_noalloc(_lib.XNN_F32, ctypes.c_void_p(_lib.ptr(src)), n, F,
-                                            ctypes.c_void_p(_lib.ptr(seg)), 1,
-                                            ctypes.c_void_p(_lib.ptr(out)),
-                                            ctypes.c_void_p(_lib.stream(src.device)))
-    assert rc == _lib.XNN_EINVAL
-    assert b"scratch" in lib.xnn_last_error()

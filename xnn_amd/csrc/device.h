@@ -341,16 +341,18 @@ struct Radial {
   const T* __restrict__ table;  // Bessel frequencies or Gaussian centers
 };
 
-// envelope value and derivative at distance r
+// envelope value and derivative at distance r; every envelope is zero from the cutoff on
+// (the reference's multiply by (r < rc), cutoff.py:41, 125), the unit envelope included, so
+// that edges of a list longer than the cutoff contribute nothing
 template <typename T>
 __device__ inline void envelope_eval(const Radial<T>& R, T r, T& f, T& df) {
-  if (R.envelope == XNN_ENV_NONE) {
-    f = T(1);
+  if (!(r < R.rc)) {
+    f = T(0);
     df = T(0);
     return;
   }
-  if (!(r < R.rc)) {
-    f = T(0);
+  if (R.envelope == XNN_ENV_NONE) {
+    f = T(1);
     df = T(0);
     return;
   }

@@ -310,7 +310,17 @@ __global__ void nearest_count_kernel(const int32_t* __restrict__ ptr, int64_t n_
   kept_ptr[i + 1] = min(ptr[i + 1] - ptr[i], k);
 }
 
-// one wave per receiver: the rank of every edge of the row among the row's edges
+// (length, edge) of f before that of e in the order of a stable ascending sort: NaN lengths
+// after every number (as torch.sort places them), ties and NaNs by edge index
+template <typename T>
+__device__ __forceinline__ bool sorts_before(T df, int32_t f, T d, int32_t e) {
+  const bool nf = df != df, nd = d != d;
+  if (nf != nd) return nd;
+  return (!nf && df < d) || ((nf || df == d) && f < e);
+}
+
+// one wave per receiver: the rank of every edge of the row among the row's edges (every
+// rank below the row's length exactly once, NaN lengths included)
 template <typename T>
 __global__ __launch_bounds__(256) void nearest_fill_kernel(
     const T* __restrict__ dist, const int32_t* __restrict__ ptr, const int32_t* __restrict__ perm,
@@ -326,7 +336,7 @@ __global__ __launch_bounds__(256) void nearest_fill_kernel(
     for (int32_t r = q0; r < q1; ++r) {
       const int32_t f = perm ? perm[r] : r;
       const T df = dist[f];
-      rank += (df < d || (df == d && f < e)) ? 1 : 0;
+      rank += sorts_before(df, f, d, e) ? 1 : 0;
     }
     if (rank < k) keep[kept_ptr[row] + rank] = e;
   }

@@ -682,6 +682,10 @@ class DFTD4(nn.Module):
     :class:`~xnn_amd.data.AtomicGraph`. Cutoffs in Angstrom (defaults: the upstream
     60 / 40 / 30 / 25 bohr for pair / triple / CN / EEQ CN, d4.py:121-127)."""
 
+    # ``forward``'s ``fused_pair`` (see ``evaluate``); set by DispersionCorrection while only
+    # the per-structure energies are differentiated
+    fused_pair = False
+
     def __init__(self, tables: Dict[str, np.ndarray], s6: float = 1.0, s8: float = 1.20065498,
                  a1: float = 0.40085597, a2: float = 5.02928789, s9: float = 1.0,
                  alp: float = 16.0, ga: float = 3.0, gc: float = 2.0, wf: float = 6.0,
@@ -1015,7 +1019,7 @@ class DFTD4(nn.Module):
 
     def forward(self, data) -> Dict[str, Tensor]:
         return self.evaluate(data.atomic_numbers, data.pos, data.cell, data.pbc, data.n_atoms,
-                             data.total_charge)
+                             data.total_charge, fused_pair=self.fused_pair)
 
 
 def cp_weights(like: Tensor) -> Tensor:
@@ -1076,6 +1080,10 @@ class DispersionCorrection(nn.Module):
 
     _RENAME = {"charges": "eeq_charges"}
     edge_virial = False          # the term depends on the cell beyond the edge vectors
+    # False while ForceStressOutput differentiates the per-structure energies only: the
+    # term then takes its two-body energies and gradients from one pair launch and returns
+    # its per-atom energies detached
+    node_energy_grads = True
 
     def __init__(self, term: nn.Module, model: Optional[nn.Module] = None):
         super().__init__()
@@ -1084,7 +1092,14 @@ class DispersionCorrection(nn.Module):
         self.cutoff = float(getattr(model, "cutoff", 0.0)) if model is not None else 0.0
 
     def forward(self, data) -> Dict[str, Tensor]:
-        disp = dict(self.term(data))
+        fuse = not self.node_energy_grads and hasattr(self.term, "fused_pair")
+        if fuse:
+            self.term.fused_pair = True
+        try:
+            disp = dict(self.term(data))
+        finally:
+            if fuse:
+                self.term.fused_pair = False
         node_disp = disp.pop("node_energy")
         energy_disp = disp.pop("energy")
         if self.model is None:
@@ -1329,6 +1344,8 @@ class DFTD3(nn.Module):
     ``s9 != 0`` adds the ATM term (zero damping with radii ``4/3 R0_AB``, exponent
     ``(alp + 2) / 3``; the upstream default is off)."""
 
+    fused_pair = False       # as DFTD4.fused_pair
+
     def __init__(self, tables: Dict[str, np.ndarray], damping: str = "bj", s6: float = 1.0,
                  s8: Optional[float] = None, a1: float = 0.4145, a2: float = 4.8593,
                  rs6: float = 1.287, rs8: float = 1.0, alp: float = 14.0, bet: float = 0.0,
@@ -1459,7 +1476,8 @@ class DFTD3(nn.Module):
         return atm_energy(edge_index, vec, f.contiguous(), g.contiguous(), consts, pos.shape[0])
 
     def forward(self, data) -> Dict[str, Tensor]:
-        return self.evaluate(data.atomic_numbers, data.pos, data.cell, data.pbc, data.n_atoms)
+        return self.evaluate(data.atomic_numbers, data.pos, data.cell, data.pbc, data.n_atoms,
+                             fused_pair=self.fused_pair)
 
 
 class D3Dispersion(DispersionCorrection):

@@ -117,6 +117,12 @@ class ForceStressOutput(nn.Module):
         had_param_grads = getattr(self.model, "param_grads", None)
         if had_param_grads is not None:
             self.model.param_grads = bool(create_graph)
+        # a model whose total is not the sum of its returned node energies (a dispersion
+        # correction) is differentiated through its per-structure energies only: its
+        # per-atom energies need no gradient outside a training step
+        had_node_grads = getattr(self.model, "node_energy_grads", None)
+        if had_node_grads is not None and not getattr(self.model, "energy_is_node_sum", False):
+            self.model.node_energy_grads = bool(create_graph)
         # one structure whose energy is the sum of its node energies: the model leaves the
         # total to this wrapper, which forms it with the stress in one kernel after the
         # backward (the backward starts from the node energies anyway)
@@ -131,6 +137,8 @@ class ForceStressOutput(nn.Module):
         finally:
             if had_param_grads is not None:
                 self.model.param_grads = had_param_grads
+            if had_node_grads is not None:
+                self.model.node_energy_grads = had_node_grads
             if defer:
                 self.model.defer_energy_sum = False
             if probe:
