@@ -71,3 +71,22 @@ def hidden_chain(x: np.ndarray, weights: Sequence[np.ndarray], scales: Sequence[
         return g
 
     return s[-1], vjp
+
+
+def fully_connected_torch(x, weights, cst: float, f=None, variance_in: float = 1.0,
+                          variance_out: float = 1.0):
+    """:func:`fully_connected` on torch tensors (float64, SiLU by default), differentiable."""
+    import torch
+    f = torch.nn.functional.silu if f is None else f
+    var_in = variance_in
+    n = len(weights)
+    for i, w in enumerate(weights):
+        last = i == n - 1
+        var_out = variance_out if last else 1.0
+        h_in = w.shape[0]
+        if not last:
+            x = cst * f(x @ (w / math.sqrt(h_in * var_in))) * math.sqrt(var_out)
+        else:
+            x = x @ (w / math.sqrt(h_in * var_in / var_out))
+        var_in = var_out
+    return x

@@ -13,6 +13,9 @@ sender rows, e3nn ``TensorProduct``, ``scatter_sum``, divide). Float64 NumPy, ed
   (``irrep_normalization="component"``, ``path_normalization="element"``, unit variances):
   ``sqrt(dim(l_out) / sum over the instructions into that output of mul_2)``.
 * :func:`uvu_conv` -- the message step by brute force.
+* :func:`uvu_conv_torch` -- the same sums in float64 PyTorch, each instruction over all
+  edges at once, differentiable (for forces of a stacked model); pinned to
+  :func:`uvu_conv` by ``tests/test_conv.py``.
 """
 from __future__ import annotations
 
@@ -104,3 +107,35 @@ def uvu_conv(h: np.ndarray, y: np.ndarray, w: np.ndarray, src: np.ndarray, dst: 
     if divisor is not None:
         out = out / divisor
     return out
+
+
+def uvu_conv_torch(h, y, w, src, dst, n_nodes: int, irreps1: str, irreps2: str,
+                   irreps_out: str, instructions: Sequence[Tuple[int, int, int]],
+                   divisor: Optional[float] = None):
+    """:func:`uvu_conv` on torch tensors (float64), every edge of an instruction at once:
+    ``out[dst, c] += coef w[e, path] C x1[src] x2[e]`` by ``index_add``; differentiable in
+    ``h``, ``y`` and ``w``."""
+    import torch
+    i1, i2, io = parse_irreps(irreps1), parse_irreps(irreps2), parse_irreps(irreps_out)
+    o1, o2, oo = offsets(i1), offsets(i2), offsets(io)
+    coefs = path_coefficients(i1, i2, io, instructions)
+    dim_out = sum(m * (2 * l + 1) for m, l, _ in io)
+    E = y.shape[0]
+    blocks = [None] * len(io)
+    wo = 0
+    for (a, b, c), coef in zip(instructions, coefs):
+        mul, l1, _ = i1[a]
+        _, l2, _ = i2[b]
+        _, l3, _ = io[c]
+        x1 = h.index_select(0, src)[:, o1[a]:o1[a] + mul * (2 * l1 + 1)].reshape(E, mul, 2 * l1 + 1)
+        x2 = y[:, o2[b]:o2[b] + 2 * l2 + 1]
+        wp = w[:, wo:wo + mul]
+        wo += mul * i2[b][0]
+        C = torch.as_tensor(wigner_3j(l1, l2, l3), dtype=h.dtype, device=h.device)
+        msg = coef * torch.einsum("eu,ijk,eui,ej->euk", wp, C, x1, x2)
+        part = h.new_zeros(n_nodes, mul * (2 * l3 + 1)).index_add(0, dst, msg.reshape(E, -1))
+        blocks[c] = part if blocks[c] is None else blocks[c] + part
+    out = torch.cat([blk if blk is not None else h.new_zeros(n_nodes, io[k][0] * (2 * io[k][1] + 1))
+                     for k, blk in enumerate(blocks)], dim=1) if io else h.new_zeros(n_nodes, 0)
+    assert out.shape[1] == dim_out
+    return out / divisor if divisor is not None else out

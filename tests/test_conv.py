@@ -170,3 +170,26 @@ def test_fast_eligibility_follows_the_reference_conditions():
     assert not two_out.fast_eligible
     with pytest.raises(NotImplementedError):
         ConvTensorProduct("2x0e", "0e", "2x0e", [(0, 0, 0, "uvw", True)])
+
+
+def test_oracle_torch_conv_equals_the_brute_force_oracle():
+    """oracle.tp.uvu_conv_torch (every edge of an instruction at once, differentiable)
+    against the edge-by-edge oracle.tp.uvu_conv, on every path of 8x0e+8x1o+8x2e with
+    harmonics to l = 2, a divisor and a node without in-edges."""
+    import torch
+    irreps1 = I.Irreps("8x0e+8x1o+8x2e")
+    sh = I.spherical_harmonics_irreps(2)
+    mid, ins = I.tp_out_irreps_with_instructions(irreps1, sh, "8x0e+8x1o+8x2e+8x1e+8x0o",
+                                                 sort_instructions=False)
+    rng = np.random.default_rng(5)
+    n, e = 9, 60
+    src, dst = rng.integers(0, n, e), rng.integers(0, n, e)
+    dst[dst == 2] = 3
+    n_w = sum(irreps1[a].mul * sh[b].mul for a, b, _, _, _ in ins)
+    h, y, w = rng.standard_normal((n, irreps1.dim)), rng.standard_normal((e, sh.dim)), \
+        rng.standard_normal((e, n_w))
+    paths = [(a, b, c) for a, b, c, _, _ in ins]
+    want = T.uvu_conv(h, y, w, src, dst, n, repr(irreps1), repr(sh), repr(mid), paths, 1.7)
+    got = T.uvu_conv_torch(torch.tensor(h), torch.tensor(y), torch.tensor(w), torch.tensor(src),
+                           torch.tensor(dst), n, repr(irreps1), repr(sh), repr(mid), paths, 1.7)
+    np.testing.assert_allclose(got.numpy(), want, rtol=1e-12, atol=1e-12)

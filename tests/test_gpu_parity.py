@@ -894,7 +894,7 @@ def _float32_floor(R, g, params, cpu_pos, cell, ref, err):
                                           ("nequip_molecules", "unfused"),
                                           ("periodic_batch", "radial"),
                                           ("water", "one_pass"), ("argon", "one_pass"),
-                                          ("ragged", "one_pass"),
+                                          ("ragged", "one_pass"), ("ragged_1024", "one_pass"),
                                           ("periodic_batch", "one_pass")])
 def test_model_energy_forces_stress(config, fused):
     import oracle.reference as R
@@ -972,6 +972,11 @@ def test_model_energy_forces_stress(config, fused):
     print(f"energy rel err max {float(rel.max()):.3e}; err / sum|E_i| max "
           f"{float((err / scale).max()):.3e}; E={ref['energy'][:3].tolist()}", flush=True)
     if not bool((rel <= 1e-6).all()):
+        msg = (f"model {config} fused={fused}: energy bar from the float32 floor "
+               f"(rel err {float(rel.max()):.3e} > 1e-6)")
+        _note(msg)
+        import warnings
+        warnings.warn(msg)       # listed in pytest's warnings summary of the run
         _float32_floor(R, g, params, cpu_pos, cell, ref, err)
     np.testing.assert_allclose(out["forces"].detach().cpu().double(), ref["forces"], atol=1e-5)
     if cell is not None:

@@ -121,3 +121,16 @@ def test_fast_path_needs_a_gpu_and_silu_layers():
     assert not X.RadialNet([8, 64, 64, 64, 64, 10], F.silu).fast_supported(torch.device("cuda"),
                                                                            torch.float32)
     assert not X.RadialNet([40, 64, 10], F.silu).fast_supported(torch.device("cuda"), torch.float32)
+
+
+def test_oracle_torch_network_equals_the_numpy_oracle():
+    """oracle.radial.fully_connected_torch against oracle.radial.fully_connected."""
+    import oracle.radial as OR
+    rng = np.random.default_rng(2)
+    ws = [rng.standard_normal((8, 16)), rng.standard_normal((16, 16)), rng.standard_normal((16, 5))]
+    x = rng.standard_normal((40, 8))
+    cst = OR.exact_second_moment_constant(OR.silu)
+    want = OR.fully_connected(x, ws, cst, variance_in=0.7, variance_out=1.3)
+    got = OR.fully_connected_torch(torch.tensor(x), [torch.tensor(w) for w in ws], cst,
+                                   variance_in=0.7, variance_out=1.3)
+    np.testing.assert_allclose(got.numpy(), want, rtol=1e-13, atol=1e-13)
