@@ -363,6 +363,30 @@ def _cpu_stages(g, params, n_sample: int, stress: bool) -> dict:
             "total": t6 - t0}
 
 
+def cpu_neighbor_list(g, rc: float) -> dict:
+    """The neighbor list on the host: the oracle's brute-force restatement of the
+    reference's list (neighborlist.py:462-506, C, one thread) over every structure of the
+    workload, timed once (a few seconds for the water box)."""
+    import oracle.nl as N
+    pos = g.pos.detach().cpu().numpy()
+    cells = None if g.cell is None else g.cell.detach().cpu().numpy().reshape(-1, 3, 3)
+    pbcs = None if g.pbc is None else g.pbc.detach().cpu().numpy().reshape(-1, 3)
+    counts = [int(c) for c in g.n_atoms.cpu()]
+    t0 = time.perf_counter()
+    start, edges = 0, 0
+    for b, n in enumerate(counts):
+        ei, _, _ = N.neighbor_list(pos[start:start + n], rc,
+                                   None if cells is None else cells[b],
+                                   None if pbcs is None else pbcs[b], dtype=np.float32)
+        edges += ei.shape[1]
+        start += n
+    dt = time.perf_counter() - t0
+    return {"seconds": round(dt, 3), "value": edges / dt, "unit": "edges/s", "cores": 1,
+            "kind": "port", "sample": f"the whole workload's list ({edges} edges of "
+                                      f"{len(counts)} structure(s)), brute force over the "
+                                      f"image range, float32, one thread"}
+
+
 def cpu_baseline(g, model, rc, kw, max_edges: int, one_thread_edges: int = 60_000) -> dict:
     """The oracle's PyTorch-CPU restatement of one step (float32) on bounded samples of
     the workload (the edges of the first receivers in CSR order): the median of 5 timed
@@ -395,6 +419,7 @@ def cpu_baseline(g, model, rc, kw, max_edges: int, one_thread_edges: int = 60_00
             "stage_seconds": {k: round(v, 4) for k, v in many.items()},
             "one_thread": {"value": n_one / one["total"], "edges": n_one,
                            "stage_seconds": {k: round(v, 4) for k, v in one.items()}},
+            "neighbor_list": cpu_neighbor_list(g, rc),
             "os_cpu_count": os.cpu_count(), "affinity_cpus": len(os.sched_getaffinity(0)),
             "physical_cores": n_phys, "torch_threads": n_phys,
             "sample": f"float32 forward + force/stress backward of the oracle's PyTorch-CPU "

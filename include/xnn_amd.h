@@ -735,6 +735,14 @@ int xnn_radius_graph_count(int geom_dtype, const void* pos, int64_t n_nodes, con
                            double cutoff, int32_t self_interaction, const xnn_grid_plan* plan,
                            void* workspace, int32_t* row_ptr, xnn_stream_t stream);
 
+/* After xnn_radius_graph_count on the same plan and workspace: status (2 int32, device) =
+ * (E = row_ptr[n_nodes], 1 when a position was not finite else 0), so that one read gives
+ * the host the edge count and the check neighborlist.py:180-181 makes (non-finite
+ * positions raise). geom_dtype is the count step's. */
+int xnn_radius_graph_status(int geom_dtype, int64_t n_nodes, const xnn_grid_plan* plan,
+                            const void* workspace, const int32_t* row_ptr, int32_t* status,
+                            xnn_stream_t stream);
+
 /* Writes E = row_ptr[n_nodes] edges. src/dst int32 (E), shift packed int32 (E);
  * edge_index64 (2,E) and shifts64 (E,3) int64 in the reference format are nullable
  * (src, dst and shift may be NULL together when both int64 outputs are given).

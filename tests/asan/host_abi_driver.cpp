@@ -72,6 +72,9 @@ static void argument_errors() {
   double out[15];
   float virial[9];
   // every call below fails its argument checks before any device work
+  CHECK(xnn_radius_graph_status(XNN_F32, 5, nullptr, nullptr, nullptr, nullptr, nullptr) ==
+        XNN_EINVAL);
+  CHECK(xnn_radius_graph_status(7, 5, nullptr, nullptr, nullptr, nullptr, nullptr) == XNN_EINVAL);
   CHECK(xnn_segment_reduce_f64_noalloc(XNN_F32, nullptr, int64_t(1) << 20, 1024, nullptr, 1,
                                        nullptr, nullptr) == XNN_EINVAL);
   CHECK(xnn_radius_graph_bounds(XNN_F32, nullptr, 10, nullptr, out, nullptr) == XNN_EINVAL);

@@ -138,6 +138,56 @@ def test_radius_graph_edge_cases():
         xa.build_neighbor_list(bad, 3.0)
 
 
+def test_periodic_plan_reuse_keeps_the_edge_set():
+    """A fully periodic cell tensor reused unchanged reuses its grid plan (no bounds read):
+    positions that drift by whole and fractional cells (unwrapped), or a cell changed in
+    place, give the edge set of a fresh build; a non-finite position still raises."""
+    import oracle.nl as N
+    import xnn_amd as xa
+    from xnn_amd import data as D, synthetic
+    from oracle.nl import canonical
+    _note("periodic plan reuse")
+    s = synthetic.water_box(n_molecules=216, box=18.6, grid=6, seed=10)   # margin-checked
+    cell = torch.tensor(s.cell, dtype=torch.float32, device=DEV)
+    pbc = torch.tensor(s.pbc)
+    pos0 = torch.tensor(s.pos, dtype=torch.float32, device=DEV)
+    xa.build_neighbor_list(pos0, 5.0, cell, pbc)              # plans and caches the grid
+    key = (str(pos0.device), pos0.shape[0], torch.float32, 5.0, False)
+    assert D._PERIODIC_PLANS[key][0]() is cell
+    shift = torch.tensor([2.0, -1.0, 3.0], device=DEV) @ cell + 0.37
+    jitter = 0.01 * torch.randn(pos0.shape, generator=torch.Generator().manual_seed(1))
+    for pos in (pos0 + jitter.to(DEV), pos0 + shift):
+        ei, sh = xa.build_neighbor_list(pos, 5.0, cell, pbc)
+        ei_o, sh_o, near = N.neighbor_list(pos.cpu().numpy(), 5.0, s.cell, s.pbc,
+                                           dtype=np.float32, margin=1e-5)
+        assert near == 0             # no pair within 1e-5 A of the cutoff: the sets are exact
+        assert np.array_equal(canonical(ei.cpu().numpy(), sh.cpu().numpy()), canonical(ei_o, sh_o))
+    # the cell changed in place: a new plan (the version moved)
+    with torch.no_grad():
+        cell.mul_(1.05)
+    ei, sh = xa.build_neighbor_list(pos0, 5.0, cell, pbc)
+    assert D._PERIODIC_PLANS[key][1] == cell._version
+    ei_o, sh_o, near = N.neighbor_list(pos0.cpu().numpy(), 5.0, cell.cpu().double().numpy(),
+                                       s.pbc, dtype=np.float32, margin=1e-5)
+    assert near == 0
+    assert np.array_equal(canonical(ei.cpu().numpy(), sh.cpu().numpy()), canonical(ei_o, sh_o))
+    # the same atoms compressed into another cell tensor: a new plan
+    small = (cell / 1.05 * 0.8).contiguous()
+    pos_small = (pos0 * 0.8).contiguous()
+    ei, sh = xa.build_neighbor_list(pos_small, 5.0, small, pbc)
+    assert D._PERIODIC_PLANS[key][0]() is small
+    ei_o, sh_o, near = N.neighbor_list(pos_small.cpu().numpy(), 5.0, small.cpu().double().numpy(),
+                                       s.pbc, dtype=np.float32, margin=1e-5)
+    if near == 0:
+        assert np.array_equal(canonical(ei.cpu().numpy(), sh.cpu().numpy()), canonical(ei_o, sh_o))
+    else:
+        assert abs(ei.shape[1] - ei_o.shape[1]) <= near
+    bad = pos0.clone()
+    bad[7, 1] = float("nan")
+    with pytest.raises(ValueError, match="not finite"):
+        xa.build_neighbor_list(bad, 5.0, cell, pbc)
+
+
 def test_neighbor_list_capacity_mode_eager_and_captured():
     """The capacity mode (grid_pairs.py:414-499 semantics): the edges of the ordinary list
     in the first n_edges entries, the rest repeating the first edge, n_edges on the device

@@ -197,6 +197,7 @@ _SIGNATURES = {
     "xnn_radius_graph_plan": [i64, c_f64p, c_i32p, dbl, c_f64p, c_f64p, ctypes.POINTER(GridPlan)],
     "xnn_radius_graph_bounds": [c_int, vp, i64, vp, vp, vp],
     "xnn_radius_graph_count": [c_int, vp, i64, vp, dbl, i32, ctypes.POINTER(GridPlan), vp, vp, vp],
+    "xnn_radius_graph_status": [c_int, i64, ctypes.POINTER(GridPlan), vp, vp, vp, vp],
     "xnn_radius_graph_fill": [c_int, vp, i64, vp, dbl, i32, ctypes.POINTER(GridPlan), vp, vp, i64,
                               vp, vp, vp, vp, vp, vp, vp],
     "xnn_radius_graph_molecules_count": [c_int, vp, i64, vp, vp, i64, dbl, i32, vp, vp],

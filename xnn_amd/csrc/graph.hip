@@ -16,6 +16,8 @@
 #include <math.h>
 #include <string.h>
 
+#include <mutex>
+
 #include <hipcub/hipcub.hpp>
 
 #include "common.h"
@@ -47,11 +49,16 @@ static inline int search_split(int64_t n_atoms, int64_t n_bins) {
 // and the fill step reads it back, so both must get the same buffer.
 struct GridWs {
   size_t bin_key, bin_key_sorted, atom_id, atom_sorted, wpos, offs, wpos_s, offs_s, bin_cnt,
-      bin_start, counts, overflow, cub, cub_bytes, total;
+      bin_start, counts, overflow, cursor, cub, cub_bytes, total;
 };
 
+// Sizes the count step sorts and scans in one block (a 1024-thread block scans them in a few
+// microseconds, with one launch instead of the library's several); larger ones take the
+// library's radix sort and scans.
+constexpr int64_t kBlockScanMax = 65536;
+
 template <typename G>
-static GridWs grid_ws_layout(int64_t n, int64_t n_bins) {
+static GridWs grid_ws_layout_uncached(int64_t n, int64_t n_bins) {
   GridWs w;
   size_t at = 0;
   w.bin_key = at; at += align_up(sizeof(int32_t) * n);
@@ -66,6 +73,7 @@ static GridWs grid_ws_layout(int64_t n, int64_t n_bins) {
   w.bin_start = at; at += align_up(sizeof(int32_t) * (n_bins + 1));
   w.counts = at; at += align_up(sizeof(int32_t) * (n + 1));
   w.overflow = at; at += align_up(sizeof(int32_t) * 4);
+  w.cursor = at; at += align_up(sizeof(int32_t) * (n_bins + 1));
   size_t sort_bytes = 0, scan_bytes = 0, scan2 = 0;
   (void)hipcub::DeviceRadixSort::SortPairs(nullptr, sort_bytes, (int32_t*)nullptr, (int32_t*)nullptr,
                                      (int32_t*)nullptr, (int32_t*)nullptr, (int)n);
@@ -77,6 +85,31 @@ static GridWs grid_ws_layout(int64_t n, int64_t n_bins) {
   w.cub_bytes = align_up(std::max(sort_bytes, std::max(scan_bytes, scan2)) + 256);
   at += w.cub_bytes;
   w.total = at;
+  return w;
+}
+
+// The layout for (geometry size, atoms, bins), remembered for the last few shapes: the
+// temporary-storage queries of the library sort and scans cost tens of microseconds of host
+// time, and the plan, count and fill steps of every build need the same layout.
+template <typename G>
+static GridWs grid_ws_layout(int64_t n, int64_t n_bins) {
+  struct Entry {
+    int64_t n = -1, n_bins = -1;
+    GridWs w;
+  };
+  constexpr int kSlots = 8;
+  static Entry cache[kSlots];
+  static int next = 0;
+  static std::mutex mu;
+  {
+    std::lock_guard<std::mutex> lock(mu);
+    for (const Entry& e : cache)
+      if (e.n == n && e.n_bins == n_bins) return e.w;
+  }
+  const GridWs w = grid_ws_layout_uncached<G>(n, n_bins);
+  std::lock_guard<std::mutex> lock(mu);
+  cache[next] = Entry{n, n_bins, w};
+  next = (next + 1) % kSlots;
   return w;
 }
 
@@ -92,10 +125,14 @@ template <typename G>
 __global__ void bin_atoms_kernel(const G* __restrict__ pos, int64_t n, const G* __restrict__ cell,
                                  GridDev g, int32_t* __restrict__ bin_key,
                                  int32_t* __restrict__ atom_id, G* __restrict__ wpos,
-                                 int32_t* __restrict__ offs, int32_t* __restrict__ bin_count) {
+                                 int32_t* __restrict__ offs, int32_t* __restrict__ bin_count,
+                                 int32_t* __restrict__ nonfinite) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= n) return;
   const G p[3] = {pos[3 * i], pos[3 * i + 1], pos[3 * i + 2]};
+  // a non-finite coordinate is flagged for the host (xnn_radius_graph_status); the atom is
+  // binned like any other (the bin index is clamped), and finds no neighbor
+  if (!(isfinite(p[0]) && isfinite(p[1]) && isfinite(p[2]))) *nonfinite = 1;
   G w[3] = {p[0], p[1], p[2]};
   int o[3] = {0, 0, 0};
   int b[3];
@@ -344,6 +381,105 @@ __global__ __launch_bounds__(256) void nearest_fill_kernel(
 
 __global__ void set_first_zero_kernel(int32_t* p) { p[0] = 0; }
 
+// the edge count row_ptr[n] and the non-finite flag the count step left, side by side
+__global__ void grid_status_kernel(const int32_t* __restrict__ row_ptr, int64_t n,
+                                   const int32_t* __restrict__ nonfinite,
+                                   int32_t* __restrict__ status) {
+  status[0] = row_ptr[n];
+  status[1] = *nonfinite;
+}
+
+// zeroes of the fill step: per-atom counts (nc) and the overflow flag
+__global__ void zero_fill_state_kernel(int32_t* __restrict__ counts, int64_t nc,
+                                       int32_t* __restrict__ overflow) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < nc) counts[i] = 0;
+  if (i == 0) overflow[0] = 0;
+}
+
+// One block's scan of m <= kBlockScanMax ints (in and out distinct): out[i] = the sum of
+// in[0..i) (exclusive) or in[0..i] (inclusive). Each thread sums a contiguous chunk, the
+// 1024 chunk sums are scanned in LDS, and each thread writes its chunk's prefix sums.
+template <bool INCLUSIVE>
+__global__ __launch_bounds__(1024) void block_scan_kernel(const int32_t* __restrict__ in,
+                                                          int32_t* __restrict__ out, int64_t m) {
+  __shared__ int32_t part[1024];
+  const int t = threadIdx.x;
+  const int64_t chunk = (m + 1023) / 1024;
+  const int64_t a = min<int64_t>(m, (int64_t)t * chunk), b = min<int64_t>(m, a + chunk);
+  int32_t sum = 0;
+  for (int64_t i = a; i < b; ++i) sum += in[i];
+  part[t] = sum;
+  __syncthreads();
+  for (int off = 1; off < 1024; off <<= 1) {
+    const int32_t v = t >= off ? part[t - off] : 0;
+    __syncthreads();
+    part[t] += v;
+    __syncthreads();
+  }
+  int32_t run = t > 0 ? part[t - 1] : 0;
+  for (int64_t i = a; i < b; ++i) {
+    const int32_t x = in[i];
+    if (INCLUSIVE) run += x;
+    out[i] = run;
+    if (!INCLUSIVE) run += x;
+  }
+}
+
+// counting sort, step 1: every atom into its bin's range (bin_start from the exclusive scan
+// of the bin counts), in arbitrary order within the bin
+__global__ void bin_scatter_kernel(const int32_t* __restrict__ bin_key, int64_t n,
+                                   const int32_t* __restrict__ bin_start,
+                                   int32_t* __restrict__ cursor, int32_t* __restrict__ unsorted) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  const int key = bin_key[i];
+  unsorted[bin_start[key] + atomicAdd(&cursor[key], 1)] = (int32_t)i;
+}
+
+// counting sort, step 2: one wave per bin puts its atoms in index order (each atom's rank
+// among the bin's atoms: the order a stable sort by bin gives) and gathers their wrapped
+// positions and image offsets into the sorted copies
+template <typename G>
+__global__ __launch_bounds__(256) void bin_sort_gather_kernel(
+    int64_t n_bins, const int32_t* __restrict__ bin_start, const int32_t* __restrict__ unsorted,
+    int32_t* __restrict__ atom_sorted, const G* __restrict__ wpos, const int32_t* __restrict__ offs,
+    G* __restrict__ wpos_s, int32_t* __restrict__ offs_s) {
+  const int64_t bin = (int64_t)blockIdx.x * 4 + threadIdx.x / kWave;
+  if (bin >= n_bins) return;
+  const int lane = threadIdx.x % kWave;
+  const int r0 = bin_start[bin], cnt = bin_start[bin + 1] - r0;
+  for (int t = lane; t < cnt; t += kWave) {
+    const int32_t id = unsorted[r0 + t];
+    int rank = 0;
+    for (int j = 0; j < cnt; ++j) rank += unsorted[r0 + j] < id ? 1 : 0;
+    const int at = r0 + rank;
+    atom_sorted[at] = id;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      wpos_s[4 * (int64_t)at + c] = wpos[4 * (int64_t)id + c];
+      offs_s[4 * (int64_t)at + c] = offs[4 * (int64_t)id + c];
+    }
+  }
+}
+
+// zeroes of the count step: bin counts (nb), per-atom counts (nc), 4 overflow flags and
+// row_ptr[0] (the inclusive scan writes row_ptr[1..n])
+__global__ void zero_count_state_kernel(int32_t* __restrict__ bin_cnt, int64_t nb,
+                                        int32_t* __restrict__ counts, int64_t nc,
+                                        int32_t* __restrict__ overflow,
+                                        int32_t* __restrict__ row_ptr,
+                                        int32_t* __restrict__ cursor) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < nb) {
+    bin_cnt[i] = 0;
+    cursor[i] = 0;
+  }
+  if (i < nc) counts[i] = 0;
+  if (i < 4) overflow[i] = 0;
+  if (i == 0) row_ptr[0] = 0;
+}
+
 // ---------------------------------------------------------------- molecules
 template <typename G, bool FILL>
 __global__ __launch_bounds__(256) void molecule_search_kernel(
@@ -574,21 +710,34 @@ static int grid_count(const void* pos_v, int64_t n, const void* cell_v, double c
   size_t cub_bytes = w.cub_bytes;
 
   const int64_t nb1 = plan->n_bins + 1;
-  hipLaunchKernelGGL(zero_i32_kernel, dim3(grid_1d(nb1, 256)), dim3(256), 0, stream, bin_cnt, nb1);
-  hipLaunchKernelGGL(zero_i32_kernel, dim3(grid_1d(n + 1, 256)), dim3(256), 0, stream, counts,
-                     n + 1);
-  hipLaunchKernelGGL(zero_i32_kernel, dim3(1), dim3(64), 0, stream, overflow, (int64_t)4);
+  // the bin counts, the per-atom counts, the overflow flags and row_ptr[0] in one launch
+  int32_t* cursor = ws_at<int32_t>(ws, w.cursor);
+  hipLaunchKernelGGL(zero_count_state_kernel, dim3(grid_1d(std::max(nb1, n + 1), 256)), dim3(256),
+                     0, stream, bin_cnt, nb1, counts, n + 1, overflow, row_ptr, cursor);
   hipLaunchKernelGGL((bin_atoms_kernel<G>), dim3(grid_1d(n, 256)), dim3(256), 0, stream, pos, n,
-                     cell, g, bin_key, atom_id, wpos, offs, bin_cnt);
+                     cell, g, bin_key, atom_id, wpos, offs, bin_cnt, overflow + 3);
   XNN_LAUNCH_CHECK();
-  XNN_HIP_CHECK(hipcub::DeviceScan::ExclusiveSum(cub, cub_bytes, bin_cnt, bin_start, (int)nb1,
-                                                 stream));
-  // stable: atoms of one bin keep ascending index order
-  XNN_HIP_CHECK(hipcub::DeviceRadixSort::SortPairs(cub, cub_bytes, bin_key, bin_key_sorted,
-                                                   atom_id, atom_sorted, (int)n, 0,
-                                                   end_bit_for(plan->n_bins), stream));
-  hipLaunchKernelGGL((gather_sorted_kernel<G>), dim3(grid_1d(n, 256)), dim3(256), 0, stream,
-                     atom_sorted, n, wpos, offs, wpos_s, offs_s);
+  const bool small = nb1 <= kBlockScanMax && n + 1 <= kBlockScanMax;
+  if (small) {
+    // atoms of one bin in ascending index order: a counting sort by bin
+    hipLaunchKernelGGL(block_scan_kernel<false>, dim3(1), dim3(1024), 0, stream, bin_cnt,
+                       bin_start, nb1);
+    hipLaunchKernelGGL(bin_scatter_kernel, dim3(grid_1d(n, 256)), dim3(256), 0, stream, bin_key,
+                       n, bin_start, cursor, bin_key_sorted);
+    hipLaunchKernelGGL((bin_sort_gather_kernel<G>), dim3(grid_1d(plan->n_bins, 4)), dim3(256), 0,
+                       stream, plan->n_bins, bin_start, bin_key_sorted, atom_sorted, wpos, offs,
+                       wpos_s, offs_s);
+    XNN_LAUNCH_CHECK();
+  } else {
+    XNN_HIP_CHECK(hipcub::DeviceScan::ExclusiveSum(cub, cub_bytes, bin_cnt, bin_start, (int)nb1,
+                                                   stream));
+    // stable: atoms of one bin keep ascending index order
+    XNN_HIP_CHECK(hipcub::DeviceRadixSort::SortPairs(cub, cub_bytes, bin_key, bin_key_sorted,
+                                                     atom_id, atom_sorted, (int)n, 0,
+                                                     end_bit_for(plan->n_bins), stream));
+    hipLaunchKernelGGL((gather_sorted_kernel<G>), dim3(grid_1d(n, 256)), dim3(256), 0, stream,
+                       atom_sorted, n, wpos, offs, wpos_s, offs_s);
+  }
   hipLaunchKernelGGL((cell_search_kernel<G, false>),
                      dim3(plan->n_bins, search_split(n, plan->n_bins)), dim3(256), 0, stream,
                      wpos_s, offs_s, atom_sorted, bin_start, cell, g, (G)cutoff, self_interaction,
@@ -596,10 +745,14 @@ static int grid_count(const void* pos_v, int64_t n, const void* cell_v, double c
                      overflow);
   XNN_LAUNCH_CHECK();
   // row_ptr[1..n] = inclusive scan of the per-atom counts; row_ptr[0] = 0
-  XNN_HIP_CHECK(hipcub::DeviceScan::InclusiveSum(cub, cub_bytes, counts, row_ptr + 1, (int)n,
-                                                 stream));
-  hipLaunchKernelGGL(set_first_zero_kernel, dim3(1), dim3(1), 0, stream, row_ptr);
-  XNN_LAUNCH_CHECK();
+  if (small) {
+    hipLaunchKernelGGL(block_scan_kernel<true>, dim3(1), dim3(1024), 0, stream, counts,
+                       row_ptr + 1, n);
+    XNN_LAUNCH_CHECK();
+  } else {
+    XNN_HIP_CHECK(hipcub::DeviceScan::InclusiveSum(cub, cub_bytes, counts, row_ptr + 1, (int)n,
+                                                   stream));
+  }
   return XNN_OK;
 }
 
@@ -617,9 +770,8 @@ static int grid_fill(const void* pos_v, int64_t n, const void* cell_v, double cu
   XNN_REQUIRE(w.total <= plan->workspace_bytes, "workspace smaller than the plan's");
   int32_t* counts = ws_at<int32_t>(ws, w.counts);
   int32_t* overflow = overflow_out ? overflow_out : ws_at<int32_t>(ws, w.overflow);
-  hipLaunchKernelGGL(zero_i32_kernel, dim3(grid_1d(n + 1, 256)), dim3(256), 0, stream, counts,
-                     n + 1);
-  hipLaunchKernelGGL(zero_i32_kernel, dim3(1), dim3(64), 0, stream, overflow, (int64_t)1);
+  hipLaunchKernelGGL(zero_fill_state_kernel, dim3(grid_1d(n + 1, 256)), dim3(256), 0, stream,
+                     counts, n + 1, overflow);
   hipLaunchKernelGGL((cell_search_kernel<G, true>),
                      dim3(plan->n_bins, search_split(n, plan->n_bins)), dim3(256), 0, stream,
                      ws_at<G>(ws, w.wpos_s), ws_at<int32_t>(ws, w.offs_s),
@@ -750,6 +902,29 @@ int xnn_radius_graph_count(int geom_dtype, const void* pos, int64_t n_nodes, con
                               row_ptr, as_hip(stream));
   set_error("unsupported geometry dtype %d", geom_dtype);
   return XNN_EINVAL;
+}
+
+int xnn_radius_graph_status(int geom_dtype, int64_t n_nodes, const xnn_grid_plan* plan,
+                            const void* workspace, const int32_t* row_ptr, int32_t* status,
+                            xnn_stream_t stream) {
+  XNN_REQUIRE(plan && row_ptr && status, "NULL plan, row_ptr or status");
+  XNN_REQUIRE(n_nodes >= 0, "negative size");
+  XNN_REQUIRE(geom_dtype == XNN_F32 || geom_dtype == XNN_F64, "unsupported geometry dtype %d",
+              geom_dtype);
+  if (n_nodes == 0) {
+    hipLaunchKernelGGL(zero_i32_kernel, dim3(1), dim3(64), 0, as_hip(stream), status, (int64_t)2);
+    XNN_LAUNCH_CHECK();
+    return XNN_OK;
+  }
+  XNN_REQUIRE(workspace != nullptr, "NULL workspace");
+  const GridWs w = geom_dtype == XNN_F32 ? grid_ws_layout<float>(n_nodes, plan->n_bins)
+                                         : grid_ws_layout<double>(n_nodes, plan->n_bins);
+  XNN_REQUIRE(w.total <= plan->workspace_bytes, "workspace smaller than the plan's");
+  const int32_t* overflow = ws_at<const int32_t>(const_cast<void*>(workspace), w.overflow);
+  hipLaunchKernelGGL(grid_status_kernel, dim3(1), dim3(1), 0, as_hip(stream), row_ptr, n_nodes,
+                     overflow + 3, status);
+  XNN_LAUNCH_CHECK();
+  return XNN_OK;
 }
 
 int xnn_radius_graph_fill(int geom_dtype, const void* pos, int64_t n_nodes, const void* cell,

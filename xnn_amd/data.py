@@ -17,6 +17,7 @@ from __future__ import annotations
 import ctypes
 import itertools
 import math
+import weakref
 from dataclasses import dataclass, fields
 from typing import Optional, Sequence
 
@@ -215,17 +216,27 @@ def _check_finite(lo_hi: list) -> None:
         raise ValueError("the positions are not finite (an unstable simulation?)")
 
 
+def _spacings(c: Sequence[float]) -> list[float]:
+    """Interplanar spacings of a cell given as its 9 row-major entries (rows a, b, c): the
+    volume over the area spanned by the other two rows, |det| / |a_j x a_k|."""
+    a, b, c3 = c[0:3], c[3:6], c[6:9]
+
+    def cross(u, v):
+        return (u[1] * v[2] - u[2] * v[1], u[2] * v[0] - u[0] * v[2], u[0] * v[1] - u[1] * v[0])
+
+    bc, ca, ab = cross(b, c3), cross(c3, a), cross(a, b)
+    vol = abs(a[0] * bc[0] + a[1] * bc[1] + a[2] * bc[2])
+    return [vol / math.sqrt(x[0] * x[0] + x[1] * x[1] + x[2] * x[2]) for x in (bc, ca, ab)]
+
+
 def _supercell_reps(cell, cutoff: float, pbc) -> list[int]:
     """Replicas per axis that bring every periodic interplanar spacing to at least a third
     of the cutoff (the cell list reaches at most three cells along an axis). ``cell``: a
     tensor or the 9 row-major entries; ``pbc``: a tensor or 3 flags."""
-    if isinstance(cell, Tensor):
-        c64 = cell.reshape(3, 3).detach().double().cpu()
-    else:
-        c64 = torch.tensor(cell, dtype=torch.float64).reshape(3, 3)
-    spacing = 1.0 / torch.linalg.norm(torch.linalg.inv(c64).T, dim=1)
+    entries = cell.reshape(-1).tolist() if isinstance(cell, Tensor) else list(cell)
+    spacing = _spacings([float(v) for v in entries])
     flags = pbc.reshape(-1).tolist() if isinstance(pbc, Tensor) else list(pbc)
-    return [max(1, int(math.ceil(cutoff / (3.0 * float(spacing[a])) * (1.0 + 1e-9))))
+    return [max(1, int(math.ceil(cutoff / (3.0 * spacing[a]) * (1.0 + 1e-9))))
             if bool(flags[a]) else 1 for a in range(3)]
 
 
@@ -251,8 +262,18 @@ def _supercell_graph(pos: Tensor, cutoff: float, cell: Tensor, pbc: Tensor,
     return edge_index, sh[keep] * R - offs[src_sup // n]
 
 
+#: grid plans of fully periodic cells, one per (device, atoms, dtype, cutoff, self-edges):
+#: (weak reference to the cell tensor, its version, plan, device cell, workspace). A plan
+#: owns its workspace: builds with one key must not run concurrently on different streams.
+_PERIODIC_PLANS: dict = {}
+
+
 def _radius_graph_cuda(pos: Tensor, cutoff: float, cell: Optional[Tensor], pbc: Optional[Tensor],
                        self_interaction: bool) -> tuple[Tensor, Tensor]:
+    """The HIP cell list. The host reads the device twice at most: the atoms' bounds and the
+    cell (to plan the grid), then the edge count (to size the outputs). A fully periodic
+    cell's grid depends on the cell alone (positions are wrapped into it), so for the same,
+    unchanged cell tensor the plan is reused and the edge count is the only read."""
     lib = _lib.load()
     dev = pos.device
     pos = pos.contiguous()
@@ -262,42 +283,58 @@ def _radius_graph_cuda(pos: Tensor, cutoff: float, cell: Optional[Tensor], pbc: 
         return (torch.zeros((2, 0), dtype=torch.long, device=dev),
                 torch.zeros((0, 3), dtype=torch.long, device=dev))
     pbc_list = [0, 0, 0] if molecular else [int(bool(b)) for b in pbc.reshape(-1).tolist()]
-    cell_dev = (None if molecular
-                else cell.reshape(3, 3).detach().to(device=dev, dtype=pos.dtype).contiguous())
-    # the atoms' bounds (fractional for a cell) and the cell itself in one launch and one
-    # read: the host's only look at the device before the edge count
-    bounds = torch.empty(15, dtype=torch.float64, device=dev)
-    _lib.call("xnn_radius_graph_bounds", _lib.dtype_code(pos.dtype), _lib.ptr(pos), n,
-              _lib.ptr(cell_dev), _lib.ptr(bounds), _lib.stream(dev))
-    vals = bounds.tolist()
-    lo_hi = vals[:6]
-    _check_finite(lo_hi)
-    if molecular:
-        cell_host = None
+    key = (str(dev), n, pos.dtype, float(cutoff), bool(self_interaction))
+    hit = None
+    if not molecular and all(pbc_list) and isinstance(cell, Tensor):
+        hit = _PERIODIC_PLANS.get(key)
+        if hit is not None and not (hit[0]() is cell and hit[1] == cell._version):
+            hit = None
+    if hit is not None:
+        _, _, plan, cell_dev, ws = hit
     else:
-        reps = _supercell_reps(vals[6:], cutoff, pbc_list)
-        if max(reps) > 1:
-            return _supercell_graph(pos, cutoff, cell, pbc, self_interaction, reps)
-        cell_host = (_lib.dbl * 9)(*vals[6:])
-    plan = _lib.GridPlan()
-    pbc_host = (ctypes.c_int32 * 3)(*pbc_list)
-    lo = (_lib.dbl * 3)(*lo_hi[:3])
-    hi = (_lib.dbl * 3)(*lo_hi[3:])
-    _lib.check("xnn_radius_graph_plan",
-               lib.xnn_radius_graph_plan(n, cell_host, pbc_host, float(cutoff), lo, hi,
-                                         ctypes.byref(plan)))
-    ws = torch.empty(max(1, int(plan.workspace_bytes)), dtype=torch.uint8, device=dev)
+        cell_dev = (None if molecular
+                    else cell.reshape(3, 3).detach().to(device=dev, dtype=pos.dtype).contiguous())
+        # the atoms' bounds (fractional for a cell) and the cell itself in one launch and
+        # one read
+        bounds = torch.empty(15, dtype=torch.float64, device=dev)
+        _lib.call("xnn_radius_graph_bounds", _lib.dtype_code(pos.dtype), _lib.ptr(pos), n,
+                  _lib.ptr(cell_dev), _lib.ptr(bounds), _lib.stream(dev))
+        vals = bounds.tolist()
+        lo_hi = vals[:6]
+        _check_finite(lo_hi)
+        if molecular:
+            cell_host = None
+        else:
+            reps = _supercell_reps(vals[6:], cutoff, pbc_list)
+            if max(reps) > 1:
+                return _supercell_graph(pos, cutoff, cell, pbc, self_interaction, reps)
+            cell_host = (_lib.dbl * 9)(*vals[6:])
+        plan = _lib.GridPlan()
+        _lib.check("xnn_radius_graph_plan",
+                   lib.xnn_radius_graph_plan(n, cell_host, (ctypes.c_int32 * 3)(*pbc_list),
+                                             float(cutoff), (_lib.dbl * 3)(*lo_hi[:3]),
+                                             (_lib.dbl * 3)(*lo_hi[3:]), ctypes.byref(plan)))
+        ws = torch.empty(max(1, int(plan.workspace_bytes)), dtype=torch.uint8, device=dev)
+        if not molecular and all(pbc_list) and isinstance(cell, Tensor):
+            _PERIODIC_PLANS[key] = (weakref.ref(cell), cell._version, plan, cell_dev, ws)
     row_ptr = torch.empty(n + 1, dtype=torch.int32, device=dev)
+    status = torch.empty(2, dtype=torch.int32, device=dev)
     geom = _lib.dtype_code(pos.dtype)
     s = _lib.stream(dev)
+    si = int(bool(self_interaction))
+
     _lib.call("xnn_radius_graph_count", geom, _lib.ptr(pos), n, _lib.ptr(cell_dev), float(cutoff),
-              int(bool(self_interaction)), ctypes.byref(plan), _lib.ptr(ws), _lib.ptr(row_ptr), s)
-    n_edges = int(row_ptr[-1])
+              si, ctypes.byref(plan), _lib.ptr(ws), _lib.ptr(row_ptr), s)
+    _lib.call("xnn_radius_graph_status", geom, n, ctypes.byref(plan), _lib.ptr(ws),
+              _lib.ptr(row_ptr), _lib.ptr(status), s)
+    n_edges, nonfinite = status.tolist()
+    if nonfinite:
+        raise ValueError("the positions are not finite (an unstable simulation?)")
     edge_index = torch.empty((2, n_edges), dtype=torch.long, device=dev)
     cell_shifts = torch.empty((n_edges, 3), dtype=torch.long, device=dev)
     _lib.call("xnn_radius_graph_fill", geom, _lib.ptr(pos), n, _lib.ptr(cell_dev), float(cutoff),
-              int(bool(self_interaction)), ctypes.byref(plan), _lib.ptr(ws), _lib.ptr(row_ptr),
-              n_edges, None, None, None, _lib.ptr(edge_index), _lib.ptr(cell_shifts), None, s)
+              si, ctypes.byref(plan), _lib.ptr(ws), _lib.ptr(row_ptr), n_edges, None, None, None,
+              _lib.ptr(edge_index), _lib.ptr(cell_shifts), None, s)
     return edge_index, cell_shifts
 
 
