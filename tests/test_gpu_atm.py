@@ -283,3 +283,25 @@ def test_atm_structure_energy_from_the_backward_launch(same):
         assert _rel(a.cpu(), b.cpu()) < 1e-11
     if same:
         assert _rel(got[1].cpu(), ref[1].cpu()) < 1e-11
+
+
+@pytest.mark.parametrize("system", ["tiny_cell", "large_cell"])
+def test_atm_is_reproducible_bit_for_bit(system):
+    """Two evaluations of the energies and of every gradient give the same bits: the kernels'
+    atomic sums are exact sums of fixed-quantum parts (a head of multiples of 2^-40 and a
+    tail of multiples of 2^-70), whose value does not depend on the order of the atomics.
+    The tiny cell has repeated-atom triangles; the 6^3 cell with an 8 A cutoff (648 atoms)
+    gives every factor-gradient row thousands of atomic contributions."""
+    print(f"[gpu-case] atm run twice, {system}", flush=True)
+    if system == "large_cell":
+        SYSTEMS["large_cell"] = (6, True, 8.0)
+    try:
+        c = _case(system, k=23)
+    finally:
+        SYSTEMS.pop("large_cell", None)
+    go = torch.rand(c["n"], dtype=torch.float64, generator=torch.Generator().manual_seed(9)) + 0.5
+    first = _hip(c, go=go)
+    second = _hip(c, go=go)
+    assert float(first[0].abs().max()) > 0
+    for name, a, b in zip(("energy", "grad_pos", "grad_feat", "grad_cell"), first, second):
+        assert torch.equal(a, b), name

@@ -24,9 +24,11 @@
 // factor row of k load through the scalar unit, the per-lane sums (edge a, atom j) stay
 // in registers until the item ends, and the per-b sums (edge b, atom k) are reduced
 // across the wave once per b (in the backward a transposing butterfly that leaves each
-// lane pair holding one of up to 32 sums) and added atomically. Items run heaviest tile
-// first. Repeated-atom triangles: one wave per flagged center, lanes over its edges,
-// each lane walking the few later edges that share an atom with its own.
+// lane pair holding one of up to 32 sums) and added atomically as reproducible sums: a
+// head and a tail of fixed quanta whose float64 sums are exact in any order (atm_acc), so
+// the results do not depend on the order of the atomics. Items run heaviest tile first.
+// Repeated-atom triangles: one wave per flagged center, lanes over its edges, each lane
+// walking the few later edges that share an atom with its own.
 //
 // Pair C6 = <fa[x], fb[y]> over K <= 32 components (held per lane for j); the damping
 // radius is the product of three species-pair factors. Energies in hartree, lengths in
@@ -134,7 +136,8 @@ static AtmPlanLayout atm_plan_layout(int64_t E, int64_t N) {
 }
 
 struct AtmWorkLayout {
-  size_t rec, rec_up, fa, fb, gs, skey, sval, skey_out, sperm, cub, cub_bytes, total;
+  size_t rec, rec_up, fa, fb, gs, skey, sval, skey_out, sperm, cub, cub_bytes, tail,
+      tail_count, total;
 };
 
 static int atm_bitlen(int64_t n) {
@@ -165,6 +168,10 @@ static AtmWorkLayout atm_work_layout(int64_t E, int64_t N, int kp, bool backward
   L.fb = at; at += atm_align(sizeof(double) * kp * std::max<int64_t>(N, 1));
   L.gs = at;
   if (backward) at += atm_align(sizeof(double) * 4 * std::max<int64_t>(E, 1));
+  // the tails of the reproducible sums: energies (forward); or gs, gfa and gfb (backward)
+  L.tail = at;
+  L.tail_count = backward ? 4 * E + 2 * N * (int64_t)kp : N;
+  at += atm_align(sizeof(double) * std::max<int64_t>((int64_t)L.tail_count, 1));
   L.total = at;
   return L;
 }
@@ -187,6 +194,14 @@ __global__ __launch_bounds__(256) void atm_fill_i32_kernel(int32_t* __restrict__
 __global__ __launch_bounds__(256) void atm_fill_f64_kernel(double* __restrict__ p, int64_t n) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i < n) p[i] = 0.0;
+}
+
+// head[i] += tail[i]: the one rounding of a reproducible sum
+__global__ __launch_bounds__(256) void atm_add_tail_kernel(double* __restrict__ head,
+                                                           const double* __restrict__ tail,
+                                                           int64_t n) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) head[i] += tail[i];
 }
 
 // key = center * N + neighbor; an index out of range gets the sentinel N^2 (sorted last)
@@ -498,6 +513,29 @@ __device__ __forceinline__ double atm_fold4(double s0, double s1, double s2, dou
   return v + atm_dpp<kDppXor1>(v);
 }
 
+// Reproducible sums. Every addend v is split into a head, v rounded to a multiple of
+// 2^-40, and a tail, the rest rounded to a multiple of 2^-70 (both splits exact: v - head
+// is exact since |v - head| <= 2^-41 and both are multiples of the ulp of v), and the two
+// are added atomically to two arrays. Sums of multiples of 2^-40 below 2^13 in magnitude
+// and of multiples of 2^-70 below 2^-17 (fewer than 2^24 tails per target) are exact in
+// float64, so every order of the atomics gives the same bits: the totals head + tail are
+// reproducible run to run, within 2^-71 per addend of the exact sum. Non-finite addends
+// give NaN.
+struct AtmTail {
+  double* energy;   // (N)
+  double* gs;       // (E, 4)
+  double* gfa;      // (N, K)
+  double* gfb;      // (N, K)
+};
+
+__device__ __forceinline__ void atm_acc(double* __restrict__ head, double* __restrict__ tail,
+                                        int64_t i, double v) {
+  const double h = __builtin_rint(v * 0x1p40) * 0x1p-40;
+  const double t = __builtin_rint((v - h) * 0x1p70) * 0x1p-70;
+  unsafeAtomicAdd(head + i, h);
+  unsafeAtomicAdd(tail + i, t);
+}
+
 // Per-wave ring of the energies of the last kAtmRing walked edges b (one row per b, one
 // column per lane) and their atoms k: the wave sums them 16 rows at a time, a quarter row
 // per lane, instead of one butterfly per b.
@@ -505,7 +543,8 @@ constexpr int kAtmRing = 16;
 
 __device__ __forceinline__ void atm_ring_flush(double (*ring)[kWave + 1], const int32_t* ring_k,
                                                int n, int lane, const AtmLanes& L,
-                                               double* __restrict__ energy) {
+                                               double* __restrict__ energy,
+                                               double* __restrict__ energy_tail) {
   wave_sync();
   const int r = lane & (kAtmRing - 1), q = lane >> 4;
   double v = 0.0;
@@ -513,7 +552,7 @@ __device__ __forceinline__ void atm_ring_flush(double (*ring)[kWave + 1], const 
   for (int i = 0; i < kWave / 4; ++i) v += ring[r][q * (kWave / 4) + i];
   v = atm_swap16_sum(v, v);
   v = atm_swap32_sum(v, v);
-  if (q == 0 && r < n) unsafeAtomicAdd(&energy[ring_k[r]], v);
+  if (q == 0 && r < n) atm_acc(energy, energy_tail, ring_k[r], v);
   wave_sync();
 }
 
@@ -534,7 +573,7 @@ __global__ __launch_bounds__(kAtmWaves * kWave) void atm_upper_kernel(
     const double* __restrict__ fa, const double* __restrict__ fb,
     const double* __restrict__ table, int S, AtmConst kc, double* __restrict__ energy,
     const double* __restrict__ go, double* __restrict__ gs, double* __restrict__ gfa,
-    double* __restrict__ gfb, int K) {
+    double* __restrict__ gfb, int K, AtmTail tail) {
   __shared__ double sTab[kAtmMaxSpecies * kAtmMaxSpecies];
   // the forward's energy ring (one per wave; a placeholder in the backward)
   __shared__ double sRing[BWD ? 1 : kAtmWaves][BWD ? 1 : kAtmRing][kWave + 1];
@@ -608,7 +647,7 @@ __global__ __launch_bounds__(kAtmWaves * kWave) void atm_upper_kernel(
       sRing[wv][n_ring][lane] = e;
       if (lane == 0) sRingK[wv][n_ring] = k;
       if (++n_ring == kAtmRing) {
-        atm_ring_flush(sRing[wv], sRingK[wv], n_ring, lane, L, energy);
+        atm_ring_flush(sRing[wv], sRingK[wv], n_ring, lane, L, energy, tail.energy);
         n_ring = 0;
       }
     } else {
@@ -627,23 +666,23 @@ __global__ __launch_bounds__(kAtmWaves * kWave) void atm_upper_kernel(
                                   2.0 * fma(gy, eb.vz, -gw * dz),
                                   0.5 * e / (eb.c6 != 0.0 ? eb.c6 : 1.0), lane, L);
       const int slot = lane >> 1;
-      if ((lane & 1) == 0 && slot < K) unsafeAtomicAdd(&gfb[(int64_t)k * K + slot], vf);
-      if ((lane & 15) == 0) unsafeAtomicAdd(&gs[(int64_t)eb.pos * 4 + (lane >> 4)], vs);
+      if ((lane & 1) == 0 && slot < K) atm_acc(gfb, tail.gfb, (int64_t)k * K + slot, vf);
+      if ((lane & 15) == 0) atm_acc(gs, tail.gs, (int64_t)eb.pos * 4 + (lane >> 4), vs);
     }
   }
   if (!BWD) {
-    if (n_ring > 0) atm_ring_flush(sRing[wv], sRingK[wv], n_ring, lane, L, energy);
-    if (va) unsafeAtomicAdd(&energy[j], e_row);
+    if (n_ring > 0) atm_ring_flush(sRing[wv], sRingK[wv], n_ring, lane, L, energy, tail.energy);
+    if (va) atm_acc(energy, tail.energy, j, e_row);
     const double ec = atm_wave_sum(e_row, L);
-    if (lane == 0) unsafeAtomicAdd(&energy[c], ec);
+    if (lane == 0) atm_acc(energy, tail.energy, c, ec);
   } else if (va) {
-    unsafeAtomicAdd(&gs[(int64_t)ea.pos * 4 + 0], gax);
-    unsafeAtomicAdd(&gs[(int64_t)ea.pos * 4 + 1], gay);
-    unsafeAtomicAdd(&gs[(int64_t)ea.pos * 4 + 2], gaz);
-    unsafeAtomicAdd(&gs[(int64_t)ea.pos * 4 + 3], gc6a);
+    atm_acc(gs, tail.gs, (int64_t)ea.pos * 4 + 0, gax);
+    atm_acc(gs, tail.gs, (int64_t)ea.pos * 4 + 1, gay);
+    atm_acc(gs, tail.gs, (int64_t)ea.pos * 4 + 2, gaz);
+    atm_acc(gs, tail.gs, (int64_t)ea.pos * 4 + 3, gc6a);
 #pragma unroll
     for (int w = 0; w < KP; ++w)
-      if (w < K) unsafeAtomicAdd(&gfa[(int64_t)j * K + w], gfj[w]);
+      if (w < K) atm_acc(gfa, tail.gfa, (int64_t)j * K + w, gfj[w]);
   }
 }
 
@@ -659,7 +698,7 @@ __global__ __launch_bounds__(kAtmWaves * kWave) void atm_repeat_kernel(
     const double* __restrict__ fa, const double* __restrict__ fb,
     const double* __restrict__ table, int S, AtmConst kc, double* __restrict__ energy,
     const double* __restrict__ go, double* __restrict__ gs, double* __restrict__ gfa,
-    double* __restrict__ gfb, int K) {
+    double* __restrict__ gfb, int K, AtmTail tail) {
   __shared__ double sTab[kAtmMaxSpecies * kAtmMaxSpecies];
   atm_stage_table(table, S, sTab);
   const int lane = threadIdx.x & (kWave - 1);
@@ -725,29 +764,29 @@ __global__ __launch_bounds__(kAtmWaves * kWave) void atm_repeat_kernel(
           gc6a += 0.5 * e / (ea.c6 != 0.0 ? ea.c6 : 1.0);
 #pragma unroll
           for (int w = 0; w < KP; ++w) gfj[w] = fma(g3, fk[w], gfj[w]);
-          unsafeAtomicAdd(&gs[(int64_t)b * 4 + 0], 2.0 * fma(gy, eb.vx, -gw * dx));
-          unsafeAtomicAdd(&gs[(int64_t)b * 4 + 1], 2.0 * fma(gy, eb.vy, -gw * dy));
-          unsafeAtomicAdd(&gs[(int64_t)b * 4 + 2], 2.0 * fma(gy, eb.vz, -gw * dz));
-          unsafeAtomicAdd(&gs[(int64_t)b * 4 + 3], 0.5 * e / (eb.c6 != 0.0 ? eb.c6 : 1.0));
+          atm_acc(gs, tail.gs, (int64_t)b * 4 + 0, 2.0 * fma(gy, eb.vx, -gw * dx));
+          atm_acc(gs, tail.gs, (int64_t)b * 4 + 1, 2.0 * fma(gy, eb.vy, -gw * dy));
+          atm_acc(gs, tail.gs, (int64_t)b * 4 + 2, 2.0 * fma(gy, eb.vz, -gw * dz));
+          atm_acc(gs, tail.gs, (int64_t)b * 4 + 3, 0.5 * e / (eb.c6 != 0.0 ? eb.c6 : 1.0));
 #pragma unroll
           for (int w = 0; w < KP; ++w)
-            if (w < K) unsafeAtomicAdd(&gfb[(int64_t)k * K + w], g3 * fj[w]);
+            if (w < K) atm_acc(gfb, tail.gfb, (int64_t)k * K + w, g3 * fj[w]);
         }
       }
     }
     if (BWD && any) {
-      unsafeAtomicAdd(&gs[(int64_t)a * 4 + 0], gax);
-      unsafeAtomicAdd(&gs[(int64_t)a * 4 + 1], gay);
-      unsafeAtomicAdd(&gs[(int64_t)a * 4 + 2], gaz);
-      unsafeAtomicAdd(&gs[(int64_t)a * 4 + 3], gc6a);
+      atm_acc(gs, tail.gs, (int64_t)a * 4 + 0, gax);
+      atm_acc(gs, tail.gs, (int64_t)a * 4 + 1, gay);
+      atm_acc(gs, tail.gs, (int64_t)a * 4 + 2, gaz);
+      atm_acc(gs, tail.gs, (int64_t)a * 4 + 3, gc6a);
 #pragma unroll
       for (int w = 0; w < KP; ++w)
-        if (w < K) unsafeAtomicAdd(&gfa[(int64_t)j * K + w], gfj[w]);
+        if (w < K) atm_acc(gfa, tail.gfa, (int64_t)j * K + w, gfj[w]);
     }
   }
   if (!BWD) {
     const double ec = atm_wave_sum(e_acc, atm_lanes(lane));
-    if (lane == 0) unsafeAtomicAdd(&energy[c], ec);
+    if (lane == 0) atm_acc(energy, tail.energy, c, ec);
   }
 }
 
@@ -884,6 +923,11 @@ static void atm_zero(double* p, int64_t n, hipStream_t s) {
   if (n > 0) hipLaunchKernelGGL(atm_fill_f64_kernel, dim3(grid_1d(n, 256)), dim3(256), 0, s, p, n);
 }
 
+static void atm_add_tail(double* head, const double* tail, int64_t n, hipStream_t s) {
+  if (n > 0)
+    hipLaunchKernelGGL(atm_add_tail_kernel, dim3(grid_1d(n, 256)), dim3(256), 0, s, head, tail, n);
+}
+
 struct AtmArgs {
   const void* plan;
   int64_t E, N, max_tiles, has_repeats;
@@ -923,12 +967,20 @@ static int atm_run(const AtmArgs& A) {
   double* fbP = at_off<double>(A.work, W.fb);
   double* gs = BWD ? at_off<double>(A.work, W.gs) : nullptr;
   const int64_t nk = A.N * (int64_t)A.K;
+  double* tails = at_off<double>(A.work, W.tail);
+  AtmTail tail{nullptr, nullptr, nullptr, nullptr};
   if (!BWD) {
+    tail.energy = tails;
     atm_zero(A.energy, A.N, A.s);
+    atm_zero(tail.energy, A.N, A.s);
   } else {
+    tail.gs = tails;
+    tail.gfa = tail.gs + 4 * A.E;
+    tail.gfb = tail.gfa + nk;
     atm_zero(gs, 4 * A.E, A.s);
     atm_zero(A.gfa, nk, A.s);
     atm_zero(A.gfb, nk, A.s);
+    atm_zero(tails, 4 * A.E + 2 * nk, A.s);
   }
   XNN_LAUNCH_CHECK();
   if (A.E == 0 || A.N == 0) return XNN_OK;
@@ -953,14 +1005,21 @@ static int atm_run(const AtmArgs& A) {
     XNN_REQUIRE(blocks <= 0x7fffffff, "ATM: too many triplet work items");
     hipLaunchKernelGGL((atm_upper_kernel<KP, SWITCH, BWD, P16>), dim3((unsigned)blocks),
                        dim3(kAtmWaves * kWave), 0, A.s, rec_up, lo, lo1, A.N, n_groups, faP, fbP,
-                       A.table, A.S, A.kc, A.energy, A.go, gs, A.gfa, A.gfb, A.K);
+                       A.table, A.S, A.kc, A.energy, A.go, gs, A.gfa, A.gfb, A.K, tail);
     XNN_LAUNCH_CHECK();
   }
   if (A.has_repeats) {
     hipLaunchKernelGGL((atm_repeat_kernel<KP, SWITCH, BWD>), dim3((unsigned)n_groups),
                        dim3(kAtmWaves * kWave), 0, A.s, rec, lo, lo1, flag, A.N, faP, fbP,
-                       A.table, A.S, A.kc, A.energy, A.go, gs, A.gfa, A.gfb, A.K);
+                       A.table, A.S, A.kc, A.energy, A.go, gs, A.gfa, A.gfb, A.K, tail);
     XNN_LAUNCH_CHECK();
+  }
+  if (!BWD) {
+    atm_add_tail(A.energy, tail.energy, A.N, A.s);
+  } else {
+    atm_add_tail(gs, tail.gs, 4 * A.E, A.s);
+    atm_add_tail(A.gfa, tail.gfa, nk, A.s);
+    atm_add_tail(A.gfb, tail.gfb, nk, A.s);
   }
   if (BWD) {
     hipLaunchKernelGGL(atm_vec_grad_kernel, dim3(grid_1d(A.E, 256)), dim3(256), 0, A.s, perm, gs,
