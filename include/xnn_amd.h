@@ -596,6 +596,25 @@ int xnn_eeq_real_grad(const double* pos, int64_t n_nodes, const double* cell, co
                       double alpha, double cutoff, const double* u, const double* w,
                       double* grad_pos, double* cell_partial, xnn_stream_t stream);
 
+/* Bytes of the workspace of xnn_eeq_real_apply for n_nodes atoms and nrhs (1 or 2)
+ * right-hand sides. */
+int xnn_eeq_real_apply_work_size(int64_t n_nodes, int32_t nrhs, size_t* bytes);
+
+/* out (N, nrhs) = matrix v for v (N, nrhs) row-major, nrhs 1 or 2, without forming the
+ * matrix of xnn_eeq_real_matrix (the conjugate-gradient regime above LU_MAX_ATOMS,
+ * common/models/eeq.py:70, 226, 325-360; dispersion_fast/eeq.py keeps the real-space
+ * kernel as a sparse CSR matrix instead). Memory O(N): the screened kernel is evaluated for
+ * every pair and image at every product. tiles: NULL, or (ceil(N / 256), 4) doubles, per
+ * tile of 256 consecutive atoms the center and radius of a sphere holding them (in the
+ * coordinates of pos); a tile pair with no lattice image within the cutoff is skipped,
+ * so atoms ordered along space (a cell list's order) make a large cell's product
+ * O(N x neighbors). pos, rad, tiles, v, out and work device memory, cell host memory as
+ * above. Deterministic (fixed-order partial sums). */
+int xnn_eeq_real_apply(const double* pos, int64_t n_nodes, const double* cell, const double* rad,
+                       double alpha, double cutoff, const double* tiles, const double* v,
+                       int32_t nrhs, double* out, void* work, size_t work_bytes,
+                       xnn_stream_t stream);
+
 /* One diagonal block of the blocked Cholesky factorization of the assembled operator
  * (replaces the factorization of EEQSystem._solve_lu, common/models/eeq.py:312-323, which
  * LU-factors the augmented matrix; the operator is symmetric positive definite and the

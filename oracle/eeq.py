@@ -87,3 +87,55 @@ def charges(pos: np.ndarray, cell: Optional[np.ndarray], rad: np.ndarray, diag: 
     M[:n, n] = M[n, :n] = 1.0
     rhs = np.concatenate([x, [total]])
     return np.linalg.solve(M, rhs)[:n]
+
+
+def _full_reciprocal_set(cell: np.ndarray, alpha: float, eps: float):
+    """Every G != 0 (G and -G both) with exp(-G^2 / 4 alpha^2) >= eps and its weight
+    4 pi / V exp(-G^2 / 4 alpha^2) / G^2, as in ewald_matrix."""
+    vol = abs(np.linalg.det(cell))
+    recip = 2.0 * math.pi * np.linalg.inv(cell).T
+    g_max = 2.0 * alpha * math.sqrt(-math.log(eps))
+    span = [int(g_max * np.linalg.norm(cell[k]) / (2 * math.pi)) + 1 for k in range(3)]
+    m = np.stack(np.meshgrid(*[np.arange(-s, s + 1) for s in span], indexing="ij"), -1).reshape(-1, 3)
+    g = m @ recip
+    g2 = (g * g).sum(1)
+    keep = (g2 <= g_max * g_max) & (g2 > 0)
+    g, g2 = g[keep], g2[keep]
+    return g, 4 * math.pi / vol * np.exp(-g2 / (4 * alpha * alpha)) / g2
+
+
+def operator_rows(pos: np.ndarray, cell: np.ndarray, rad: np.ndarray, diag: np.ndarray,
+                  q: np.ndarray, rows, cutoff: float, eps: float = EPS) -> np.ndarray:
+    """``(A q)[rows]`` for the periodic operator of :func:`charges` (ewald_matrix plus
+    diag(J + sqrt(2/pi)/a)) without forming A, for systems too large for it: the real-space
+    part over every image of every pair of the sampled rows, the reciprocal part from the
+    structure factors of q on the full set, sum_G w_G [cos(G r_i) C_G + sin(G r_i) S_G]
+    with C_G, S_G = sum_j q_j cos, sin(G r_j). O(N_G N + len(rows) N images)."""
+    from scipy.special import erf
+    alpha = erfc_inverse(eps) / cutoff
+    inv = np.linalg.inv(cell)
+    spacing = 1.0 / np.linalg.norm(inv, axis=0)
+    reps = [int(math.ceil(cutoff / s)) + 1 for s in spacing]
+    shifts = np.stack(np.meshgrid(*[np.arange(-r, r + 1) for r in reps], indexing="ij"),
+                      -1).reshape(-1, 3) @ cell
+    g, w = _full_reciprocal_set(cell, alpha, eps)
+    cs = np.zeros(len(g))
+    sn = np.zeros(len(g))
+    for k0 in range(0, len(g), 256):
+        ph = pos @ g[k0:k0 + 256].T
+        cs[k0:k0 + 256] = q @ np.cos(ph)
+        sn[k0:k0 + 256] = q @ np.sin(ph)
+    out = []
+    for i in rows:
+        gam = 1.0 / np.sqrt(rad[i] ** 2 + rad ** 2)
+        acc = 0.0
+        for t in shifts:
+            d = pos + t - pos[i]
+            r = np.sqrt((d * d).sum(1))
+            use = (r <= cutoff) & (r > 1e-10)
+            acc += float(((erf(gam[use] * r[use]) - erf(alpha * r[use])) / r[use]) @ q[use])
+        ph = g @ pos[i]
+        acc += float(w @ (np.cos(ph) * cs + np.sin(ph) * sn))
+        acc += (diag[i] - 2.0 * alpha / math.sqrt(math.pi)) * q[i]
+        out.append(acc)
+    return np.array(out)

@@ -151,3 +151,21 @@ def test_dense_and_large_regimes_agree(d4):
     z = [8, 1, 1, 6, 1, 7, 8, 1, 6, 6, 1]
     np.testing.assert_allclose(_charges(d4, pos, cell, z), _large_charges(pos, cell, z, 25.0),
                                atol=1e-6)
+
+
+def test_oracle_operator_rows_equal_the_assembled_operator():
+    """oracle/eeq.py operator_rows (the matrix-free rows the 24,000-atom GPU test checks its
+    charges with) against rows of the assembled ewald_matrix + diag, on a triclinic cell with
+    atoms outside the cell and a real-space range wider than the cell."""
+    import oracle.eeq as Q
+    rng = np.random.default_rng(4)
+    cell = np.array([[9.0, 0, 0], [1.2, 8.5, 0], [-0.7, 0.9, 10.0]]) / D.BOHR
+    pos = rng.uniform(-0.2, 1.2, (17, 3)) @ cell
+    rad = rng.uniform(0.8, 2.5, 17)
+    diag = rng.uniform(0.3, 1.0, 17)
+    q = rng.normal(size=17)
+    cutoff = 24.0
+    A = Q.ewald_matrix(pos, cell, rad, cutoff) + np.diag(diag)
+    rows = [0, 5, 16]
+    got = Q.operator_rows(pos, cell, rad, diag, q, rows, cutoff)
+    np.testing.assert_allclose(got, (A @ q)[rows], rtol=0, atol=1e-12 * np.abs(A).max())

@@ -93,15 +93,18 @@ def _eval(model, pos, z, cell, grad=False):
     return out, p, c
 
 
-def test_charges_match_the_oracle_and_finite_differences(tables):
+@pytest.mark.parametrize("solver", ["lu", "cg"])
+def test_charges_match_the_oracle_and_finite_differences(tables, solver):
     """The charges of the large regime (regime="large", 11 A real-space range) against the
     oracle's brute-force Ewald solve with the oracle's CN, 1e-10; the D4 energy through the
     charges: forces against central differences and the strain derivative against a finite
-    strain (1e-7); a molecule too; run to run bit for bit."""
+    strain (1e-7); a molecule too; run to run bit for bit. Both solvers: the factorized
+    operator and the conjugate gradients of the matrix-free one (the regime above
+    LU_MAX_ATOMS atoms, forced here)."""
     import oracle.eeq as Q
-    _note("eeq large regime charges and derivatives")
+    _note(f"eeq large regime charges and derivatives, solver={solver}")
     pos, cell, z = _cell_case()
-    model = _d4_large(tables)
+    model = _d4_large(tables, eeq_solver=solver)
     out, p, c = _eval(model, pos, z, cell, grad=True)
     q = out["charges"].detach().cpu().numpy()
     zz = np.asarray(z)
@@ -147,7 +150,8 @@ def test_charges_match_the_oracle_and_finite_differences(tables):
     x = -tables["eeq_chi"][zz] + tables["eeq_kcnchi"][zz] * cn / np.sqrt(cn + 1e-14)
     diag = tables["eeq_eta"][zz] + math.sqrt(2 / math.pi) / rad
     want = Q.charges(mol / D.BOHR, None, rad, diag, x, 0.0, 1e9)
-    np.testing.assert_allclose(outm["charges"].detach().cpu().numpy(), want, atol=1e-11)
+    np.testing.assert_allclose(outm["charges"].detach().cpu().numpy(), want,
+                               atol=1e-11 if solver == "lu" else 1e-10)
     (gpm,) = torch.autograd.grad(outm["energy"].sum(), [pm_])
     pp, pm2 = mol.copy(), mol.copy()
     pp[2, 1] += h
@@ -226,3 +230,113 @@ def test_blocked_cholesky_reports_the_first_bad_pivot():
     _, info = _cholesky(A.to(DEV))
     _, ref = torch.linalg.cholesky_ex(A)
     assert int(info) == int(ref) == 201
+
+
+def _box(n, seed):
+    """An organic box of n atoms at the C5 density (bohr), its elements and cell."""
+    from xnn_amd import synthetic
+    s = synthetic.organic_box(n, box=36.8 * (n / 5000) ** (1.0 / 3.0), seed=seed)
+    return s.pos / D.BOHR, s.cell / D.BOHR, np.asarray([int(v) for v in s.numbers])
+
+
+@pytest.mark.parametrize("case", ["triclinic_11", "box_2000", "molecule_300"])
+def test_matrix_free_real_product_matches_the_matrix(tables, case):
+    """xnn_eeq_real_apply (no matrix; 256-atom tiles, far tiles skipped) against the formed
+    matrix of xnn_eeq_real_matrix times v, one and two right-hand sides: the triclinic
+    11-atom cell with an 11 A range (many images per pair), a 2,000-atom box ordered along
+    a Morton curve with an 8 A range (most tile pairs skipped), a 300-atom molecule (every
+    pair). With and without tile bounds the same bits (a skipped tile adds only zeros), and
+    run to run the same bits."""
+    from xnn_amd import eeq as E
+    _note(f"eeq matrix-free real-space product, {case}")
+    if case == "triclinic_11":
+        pos, cell, z = _cell_case()
+        pos, cell, z, cutoff = pos / D.BOHR, cell / D.BOHR, np.asarray(z), 11.0 / D.BOHR
+    elif case == "box_2000":
+        pos, cell, z = _box(2000, 5)
+        cutoff = 8.0 / D.BOHR
+    else:
+        rng = np.random.default_rng(2)
+        pos, cell = rng.uniform(0, 30.0, (300, 3)), None
+        z, cutoff = np.asarray(([6, 1, 8] * 100)), math.inf
+    alpha = E.ewald_alpha(cutoff) if cell is not None else 0.0
+    rad = torch.tensor(tables["eeq_rad"][z], device=DEV)
+    p = torch.tensor(pos, device=DEV)
+    c = None if cell is None else torch.tensor(cell, device=DEV)
+    if c is not None:                              # wrapped, along a Morton curve
+        frac = p @ torch.linalg.inv(c)
+        frac = frac - torch.floor(frac)
+        order = E.morton_order(frac)
+        p = (frac[order] @ c).contiguous()
+        rad = rad[order].contiguous()
+    R = E.real_matrix(p, c, rad, alpha, cutoff)
+    tiles = E.tile_bounds(p) if c is not None else None
+    g = torch.Generator().manual_seed(1)
+    v = torch.randn(len(z), 2, dtype=torch.float64, generator=g).to(DEV)
+    for nrhs in (1, 2):
+        vv = v[:, :nrhs].contiguous()
+        want = R @ vv
+        got = E.real_apply(p, c, rad, alpha, cutoff, vv, tiles)
+        scale = float(want.abs().max())
+        err = float((got - want).abs().max())
+        print(f"{case} nrhs={nrhs}: max |R v| {scale:.3e}, err {err:.2e}", flush=True)
+        assert err <= 1e-13 * scale
+        assert torch.equal(E.real_apply(p, c, rad, alpha, cutoff, vv, tiles), got)
+        assert torch.equal(E.real_apply(p, c, rad, alpha, cutoff, vv, None), got)
+
+
+def test_cg_regime_24000_atoms(tables):
+    """The conjugate-gradient regime at 24,000 atoms (a 62 A organic box, the default
+    60-bohr real-space range of D4, 5.3e3 reciprocal vectors of the half set): the charges
+    against the factorized operator's to 1e-8; the operator the GPU applies against the
+    oracle's matrix-free rows (oracle/eeq.py operator_rows) on a sample of 12 atoms, and
+    the charges solve those rows (x - A q the same Lagrange multiplier on every sampled row,
+    1e-9); memory: no (N, N) array (the conjugate-gradient solve's peak well below the
+    4.6 GB of one such matrix)."""
+    import time
+    import oracle.eeq as Q
+    from xnn_amd import eeq as E
+    n = 24000
+    _note(f"eeq conjugate-gradient regime, {n} atoms")
+    pos, cell, z = _box(n, 1)
+    rng = np.random.default_rng(7)
+    cn = rng.uniform(0.0, 4.0, n)
+    rad_h = tables["eeq_rad"][z]
+    x_h = -tables["eeq_chi"][z] + tables["eeq_kcnchi"][z] * cn / np.sqrt(cn + 1e-14)
+    diag_h = tables["eeq_eta"][z] + math.sqrt(2 / math.pi) / rad_h
+    p, c = torch.tensor(pos, device=DEV), torch.tensor(cell, device=DEV)
+    rad, x, diag = (torch.tensor(a, device=DEV) for a in (rad_h, x_h, diag_h))
+    cutoff = 60.0
+    torch.cuda.synchronize()
+    base = torch.cuda.memory_allocated()
+    torch.cuda.reset_peak_memory_stats()
+    t0 = time.perf_counter()
+    q_cg = E.eeq_charges_large(p, c, rad, diag, x, 0.0, cutoff, solver="cg")
+    torch.cuda.synchronize()
+    t_cg = time.perf_counter() - t0
+    peak_cg = torch.cuda.max_memory_allocated() - base
+    alpha = E.ewald_alpha(cutoff)
+    system = E.IterativeEEQSystem(p, c, rad, diag - 2 * alpha / math.sqrt(math.pi), alpha, cutoff)
+    y, mu = system.solve_augmented(x, torch.zeros((), dtype=torch.float64, device=DEV))
+    print(f"CG regime, {n} atoms: {t_cg:.2f} s for the charges (solve + correction), peak "
+          f"{peak_cg / 2**30:.2f} GiB above the inputs; {system.recip.C} columns x "
+          f"{system.recip.K} of the reciprocal table; iterations {system.iterations}", flush=True)
+    assert peak_cg < 0.5 * n * n * 8
+    t0 = time.perf_counter()
+    q_lu = E.eeq_charges_large(p, c, rad, diag, x, 0.0, cutoff, solver="lu")
+    torch.cuda.synchronize()
+    print(f"factorized operator: {time.perf_counter() - t0:.2f} s; |q_cg - q_lu| "
+          f"{float((q_cg - q_lu).abs().max()):.2e}", flush=True)
+    np.testing.assert_allclose(q_cg.cpu(), q_lu.cpu(), rtol=0, atol=1e-8)
+    assert abs(float(q_cg.sum())) < 1e-9
+    rows = np.sort(rng.choice(n, 12, replace=False))
+    q_h = q_cg.cpu().numpy()
+    t0 = time.perf_counter()
+    want = Q.operator_rows(pos, cell, rad_h, diag_h, q_h, rows, cutoff)
+    got = system.apply(q_cg).cpu().numpy()[rows]
+    lam = x_h[rows] - want
+    print(f"oracle rows: {time.perf_counter() - t0:.1f} s; |A q (GPU) - A q (oracle)| "
+          f"{np.abs(got - want).max():.2e} of {np.abs(want).max():.2e}; multiplier spread "
+          f"{np.ptp(lam):.2e}", flush=True)
+    np.testing.assert_allclose(got, want, rtol=0, atol=1e-11 * np.abs(want).max())
+    assert np.ptp(lam) < 1e-9

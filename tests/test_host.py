@@ -411,3 +411,66 @@ def test_no_alloc_entry_refuses_sizes_beyond_its_scratch_array_before_any_device
     assert b"scratch" in lib.xnn_last_error()
     # within the limit the same call would go on to the device: not made here
     assert int(lib.xnn_segment_reduce_workspace_bytes(1 << 10, 8, 1)) <= cap
+
+
+def test_factorized_reciprocal_product_equals_the_direct_sum():
+    """The conjugate-gradient regime's reciprocal product (xnn_amd.eeq.FactorizedReciprocal:
+    per-axis phase tables, columns of fixed (m1, m2), two stacked real GEMMs) against the
+    direct cos / sin sum over the half set, for two right-hand sides, with the column table
+    kept and formed again in blocks; its diagonal is sum_G w_G. Also the own-image diagonal
+    against a direct sum and the Morton order (a permutation)."""
+    from scipy.special import erf
+    from xnn_amd import eeq as E
+    g0 = torch.Generator().manual_seed(0)
+    cell = torch.tensor([[9.0, 0, 0], [1.2, 8.5, 0], [-0.7, 0.9, 10.0]], dtype=torch.float64) / 0.5291772109
+    pos = torch.rand(40, 3, dtype=torch.float64, generator=g0) @ cell * 1.3 - 2.0
+    alpha = E.ewald_alpha(20.0)
+    m = E.reciprocal_half_set(cell, alpha)
+    g, w = E.reciprocal_weights(m, cell, alpha)
+    v = torch.randn(40, 2, dtype=torch.float64, generator=g0)
+    want = torch.stack([E.reciprocal_apply(pos, g, w, v[:, k]) for k in range(2)], 1)
+    fr = E.FactorizedReciprocal(pos, cell, m, alpha)
+    assert fr.table is not None
+    torch.testing.assert_close(fr.apply(v), want, rtol=0, atol=1e-13)
+    fr.block, fr.table = 7, None                  # the blocked form of a large system
+    torch.testing.assert_close(fr.apply(v), want, rtol=0, atol=1e-13)
+    assert abs(fr.diagonal - float(w.sum())) < 1e-15
+    # own images within 25 bohr of a 9 A cell
+    rad = torch.tensor([0.9, 2.1], dtype=torch.float64)
+    got = E.own_image_diagonal(cell, rad, alpha, 25.0)
+    want = np.zeros(2)
+    c = cell.numpy()
+    for a in range(-4, 5):
+        for b in range(-4, 5):
+            for k in range(-4, 5):
+                r = float(np.linalg.norm(a * c[0] + b * c[1] + k * c[2]))
+                if 0 < r <= 25.0:
+                    gam = 1 / (math.sqrt(2) * rad.numpy())
+                    want += (erf(gam * r) - erf(alpha * r)) / r
+    assert want[0] != 0.0
+    np.testing.assert_allclose(got.numpy(), want, rtol=1e-13)
+    order = E.morton_order(torch.rand(1000, 3, dtype=torch.float64, generator=g0))
+    assert torch.equal(torch.sort(order).values, torch.arange(1000))
+
+
+def test_low_rank_preconditioner_inverts_its_matrix():
+    """The conjugate-gradient regime's preconditioner M = D + U W U^T (U the cos / sin of the
+    smallest reciprocal vectors at the ordered positions, D the full diagonal less their
+    part) applied through the Woodbury identity: M (M^-1 r) = r for two columns, with M
+    formed explicitly; the set-up runs no device code."""
+    from xnn_amd import eeq as E
+    g0 = torch.Generator().manual_seed(3)
+    cell = torch.tensor([[9.0, 0, 0], [1.2, 8.5, 0], [-0.7, 0.9, 10.0]], dtype=torch.float64) / 0.5291772109
+    n = 60
+    pos = torch.rand(n, 3, dtype=torch.float64, generator=g0) @ cell
+    rad = torch.rand(n, dtype=torch.float64, generator=g0) + 1.0
+    diag = torch.rand(n, dtype=torch.float64, generator=g0) + 0.5
+    alpha = E.ewald_alpha(20.0)
+    system = E.IterativeEEQSystem(pos, cell, rad, diag - 2 * alpha / math.sqrt(math.pi), alpha, 20.0)
+    assert system.U is not None and system.U.shape == (n, 2 * min(E.LOW_K_VECTORS, len(system.m)))
+    g, w = E.reciprocal_weights(system.m, cell, alpha)
+    L = system.U.shape[1] // 2
+    wl = w[torch.argsort((g * g).sum(1))[:L]]
+    M = torch.diag(1.0 / system.inv_d) + system.U @ torch.diag(torch.cat([wl, wl])) @ system.U.t()
+    r = torch.randn(n, 2, dtype=torch.float64, generator=g0)
+    torch.testing.assert_close(M @ system.precondition(r), r, rtol=0, atol=1e-11)

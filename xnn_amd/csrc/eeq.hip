@@ -21,11 +21,13 @@
 // one wave per atom k, lanes over j, a fixed butterfly: bitwise reproducible.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cmath>
 #include <cstdint>
 
 #include "common.h"
 #include "device.h"
+#include "fp64.h"
 
 namespace xnn {
 
@@ -42,9 +44,25 @@ __device__ inline void image_range(double f, double reach, int& lo, int& hi) {
   hi = (int)floor(reach - f);
 }
 
+// erf(gam r) - erf(alpha r) is evaluated as erfc(alpha r) - erfc(gam r), without the
+// cancellation of two values near one; erfc(gam r) < 4e-20 for gam r >= 6.5, where it is
+// dropped (most pairs of a long real-space range: one error function instead of two).
 __device__ inline double screened(double r, double gam, double alpha) {
-  const double k = erf(gam * r);
-  return (alpha > 0.0 ? k - erf(alpha * r) : k) / r;
+  if (alpha > 0.0) {
+    const double x = gam * r;
+    return (erfc(alpha * r) - (x < 6.5 ? erfc(x) : 0.0)) / r;
+  }
+  return erf(gam * r) / r;
+}
+
+// the same from r^2 and 1 / r
+__device__ inline double screened_inv(double r2, double ir, double gam, double alpha) {
+  const double r = r2 * ir;
+  if (alpha > 0.0) {
+    const double x = gam * r;
+    return (erfc(alpha * r) - (x < 6.5 ? erfc(x) : 0.0)) * ir;
+  }
+  return erf(gam * r) * ir;
 }
 
 // dK/dr of the screened kernel
@@ -53,6 +71,41 @@ __device__ inline double screened_slope(double r, double gam, double alpha, doub
   double g = gam * exp(-gam * gam * r * r);
   if (alpha > 0.0) g -= alpha * exp(-alpha * alpha * r * r);
   return (two_over_sqrt_pi * g - K) / r;
+}
+
+// calls fn(dx, dy, dz, n0, n1, n2) for every image n of a pair within distance^2 cut2,
+// given the fractional difference f of its two atoms and the per-axis window reach (the
+// image offsets with |f_a + n_a| <= reach_a hold every image within the range): f is
+// wrapped to [-1/2, 1/2] first and the wrap folded into n. The zero vector (an atom and
+// itself) is skipped.
+template <typename Fn>
+__device__ inline void for_images_frac(const EeqCell& C, const double* reach, double f0,
+                                       double f1, double f2, double cut2, Fn&& fn) {
+  double f[3] = {f0, f1, f2};
+  int w[3];
+#pragma unroll
+  for (int c = 0; c < 3; ++c) {
+    w[c] = (int)rint(f[c]);
+    f[c] -= w[c];
+  }
+  int lo[3], hi[3];
+#pragma unroll
+  for (int c = 0; c < 3; ++c) image_range(f[c], reach[c], lo[c], hi[c]);
+  for (int n0 = lo[0]; n0 <= hi[0]; ++n0)
+    for (int n1 = lo[1]; n1 <= hi[1]; ++n1)
+      for (int n2 = lo[2]; n2 <= hi[2]; ++n2) {
+        const double g0 = f[0] + n0, g1 = f[1] + n1, g2 = f[2] + n2;
+        const double dx = g0 * C.a[0] + g1 * C.a[3] + g2 * C.a[6];
+        const double dy = g0 * C.a[1] + g1 * C.a[4] + g2 * C.a[7];
+        const double dz = g0 * C.a[2] + g1 * C.a[5] + g2 * C.a[8];
+        const double r2 = dx * dx + dy * dy + dz * dz;
+        if (r2 <= cut2 && r2 > 1e-20) fn(dx, dy, dz, n0 - w[0], n1 - w[1], n2 - w[2]);
+      }
+}
+
+__device__ inline void to_frac(const EeqCell& C, double dx, double dy, double dz, double* f) {
+#pragma unroll
+  for (int c = 0; c < 3; ++c) f[c] = dx * C.inv[c] + dy * C.inv[3 + c] + dz * C.inv[6 + c];
 }
 
 // calls fn(dx, dy, dz, n0, n1, n2) for every image of the pair (i -> j) within the cutoff
@@ -64,29 +117,9 @@ __device__ inline void for_images(const EeqCell& C, double dx0, double dy0, doub
     if (!same && r2 <= cut2) fn(dx0, dy0, dz0, 0, 0, 0);
     return;
   }
-  // fractional difference, wrapped to [-1/2, 1/2] (the wrap is folded into n)
   double f[3];
-#pragma unroll
-  for (int c = 0; c < 3; ++c) f[c] = dx0 * C.inv[c] + dy0 * C.inv[3 + c] + dz0 * C.inv[6 + c];
-  int w[3];
-#pragma unroll
-  for (int c = 0; c < 3; ++c) {
-    w[c] = (int)rint(f[c]);
-    f[c] -= w[c];
-  }
-  int lo[3], hi[3];
-#pragma unroll
-  for (int c = 0; c < 3; ++c) image_range(f[c], C.reach[c], lo[c], hi[c]);
-  for (int n0 = lo[0]; n0 <= hi[0]; ++n0)
-    for (int n1 = lo[1]; n1 <= hi[1]; ++n1)
-      for (int n2 = lo[2]; n2 <= hi[2]; ++n2) {
-        const double g0 = f[0] + n0, g1 = f[1] + n1, g2 = f[2] + n2;
-        const double dx = g0 * C.a[0] + g1 * C.a[3] + g2 * C.a[6];
-        const double dy = g0 * C.a[1] + g1 * C.a[4] + g2 * C.a[7];
-        const double dz = g0 * C.a[2] + g1 * C.a[5] + g2 * C.a[8];
-        const double r2 = dx * dx + dy * dy + dz * dz;
-        if (r2 <= cut2 && r2 > 1e-20) fn(dx, dy, dz, n0 - w[0], n1 - w[1], n2 - w[2]);
-      }
+  to_frac(C, dx0, dy0, dz0, f);
+  for_images_frac(C, C.reach, f[0], f[1], f[2], cut2, fn);
 }
 
 __global__ __launch_bounds__(256) void eeq_real_matrix_kernel(
@@ -155,6 +188,126 @@ __global__ __launch_bounds__(256) void eeq_real_grad_kernel(
       for (int q = 0; q < 9; ++q) cell_partial[9 * k + q] = c[q];
     }
   }
+}
+
+// ------------------------------------------------------------------ matrix-free product
+// out = R v for one or two right-hand sides (the conjugate-gradient regime): R is never
+// stored. Atoms come in tiles of kApplyTile consecutive indices; block (i tile, split)
+// takes the i tile, one atom per thread, against the j tiles of its split, staged in LDS
+// (fractional coordinates, width, v), and writes its partial sums; the splits are added
+// in a fixed order afterwards (bitwise reproducible). With tile bounds (center, radius of
+// a sphere holding the tile's atoms, in the coordinates of pos), a j tile is skipped when
+// no lattice image of it comes within the cutoff of the i tile: ordered along space (the
+// cell list of the caller), most tiles of a large cell are skipped.
+constexpr int kApplyTile = 256;
+constexpr int kApplyBlocks = 2048;   // target blocks per launch (8 per CU)
+
+__device__ inline bool eeq_tiles_meet(const EeqCell& C, const double* __restrict__ tiles,
+                                      int64_t ti, int64_t tj, double cutoff) {
+  const double* a = tiles + 4 * ti;
+  const double* b = tiles + 4 * tj;
+  const double R = cutoff + a[3] + b[3];
+  const double dx = b[0] - a[0], dy = b[1] - a[1], dz = b[2] - a[2];
+  if (!C.periodic) return dx * dx + dy * dy + dz * dz <= R * R;
+  double f[3], reach[3];
+  to_frac(C, dx, dy, dz, f);
+#pragma unroll
+  for (int c = 0; c < 3; ++c) reach[c] = C.reach[c] * (R / cutoff) + 1e-12;
+  bool hit = dx * dx + dy * dy + dz * dz <= R * R;   // the zero image, which the walk skips
+  for_images_frac(C, reach, f[0], f[1], f[2], R * R,
+                  [&](double, double, double, int, int, int) { hit = true; });
+  return hit;
+}
+
+template <int NRHS>
+__global__ __launch_bounds__(kApplyTile) void eeq_real_apply_kernel(
+    const double* __restrict__ pos, int64_t n, EeqCell C, const double* __restrict__ rad,
+    double alpha, double cutoff, const double* __restrict__ tiles,
+    const double* __restrict__ v, int64_t tiles_per_split, double* __restrict__ part) {
+  __shared__ double sp[3][kApplyTile], sa[kApplyTile], sv[NRHS][kApplyTile];
+  const int64_t ti = blockIdx.x, split = blockIdx.y;
+  const int64_t n_tiles = (n + kApplyTile - 1) / kApplyTile;
+  const int64_t i = ti * kApplyTile + threadIdx.x;
+  const bool vi = i < n;
+  const int64_t ic = vi ? i : 0;
+  double pi[3];
+  if (C.periodic) {
+    to_frac(C, pos[3 * ic], pos[3 * ic + 1], pos[3 * ic + 2], pi);
+  } else {
+#pragma unroll
+    for (int c = 0; c < 3; ++c) pi[c] = pos[3 * ic + c];
+  }
+  const double ai2 = rad[ic] * rad[ic];
+  const double cut2 = cutoff * cutoff;
+  double acc[NRHS];
+#pragma unroll
+  for (int r = 0; r < NRHS; ++r) acc[r] = 0.0;
+  const int64_t t0 = split * tiles_per_split;
+  const int64_t t1 = t0 + tiles_per_split < n_tiles ? t0 + tiles_per_split : n_tiles;
+  for (int64_t tj = t0; tj < t1; ++tj) {
+    if (tiles != nullptr && !eeq_tiles_meet(C, tiles, ti, tj, cutoff)) continue;  // uniform
+    const int64_t j0 = tj * kApplyTile;
+    const int cnt = (int)(n - j0 < kApplyTile ? n - j0 : kApplyTile);
+    __syncthreads();
+    if ((int)threadIdx.x < cnt) {
+      const int64_t j = j0 + threadIdx.x;
+      double pj[3];
+      if (C.periodic) {
+        to_frac(C, pos[3 * j], pos[3 * j + 1], pos[3 * j + 2], pj);
+      } else {
+#pragma unroll
+        for (int c = 0; c < 3; ++c) pj[c] = pos[3 * j + c];
+      }
+#pragma unroll
+      for (int c = 0; c < 3; ++c) sp[c][threadIdx.x] = pj[c];
+      sa[threadIdx.x] = rad[j] * rad[j];
+#pragma unroll
+      for (int r = 0; r < NRHS; ++r) sv[r][threadIdx.x] = v[j * NRHS + r];
+    }
+    __syncthreads();
+    if (!vi) continue;
+    for (int q = 0; q < cnt; ++q) {
+      // refined hardware reciprocal square roots (about an ulp) instead of the IEEE square
+      // roots and divisions: the kernel value only needs float64 accuracy, not rounding
+      const double gam = rsq_nr(ai2 + sa[q]);
+      double k = 0.0;
+      const auto add = [&](double dx, double dy, double dz, int, int, int) {
+        const double r2 = dx * dx + dy * dy + dz * dz;
+        k += screened_inv(r2, rsq_nr(r2), gam, alpha);
+      };
+      if (C.periodic) {
+        for_images_frac(C, C.reach, sp[0][q] - pi[0], sp[1][q] - pi[1], sp[2][q] - pi[2], cut2,
+                        add);
+      } else if (j0 + q != i) {
+        const double dx = sp[0][q] - pi[0], dy = sp[1][q] - pi[1], dz = sp[2][q] - pi[2];
+        if (dx * dx + dy * dy + dz * dz <= cut2) add(dx, dy, dz, 0, 0, 0);
+      }
+#pragma unroll
+      for (int r = 0; r < NRHS; ++r) acc[r] = fma(k, sv[r][q], acc[r]);
+    }
+  }
+  if (vi) {
+#pragma unroll
+    for (int r = 0; r < NRHS; ++r) part[(split * n + i) * NRHS + r] = acc[r];
+  }
+}
+
+// out[k] = sum over the splits of part[s][k], in split order
+__global__ __launch_bounds__(256) void eeq_sum_splits_kernel(const double* __restrict__ part,
+                                                             int64_t splits, int64_t m,
+                                                             double* __restrict__ out) {
+  const int64_t k = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (k >= m) return;
+  double s = 0.0;
+  for (int64_t q = 0; q < splits; ++q) s += part[q * m + k];
+  out[k] = s;
+}
+
+static int64_t eeq_apply_splits(int64_t n) {
+  const int64_t tiles = (n + kApplyTile - 1) / kApplyTile;
+  if (tiles == 0) return 1;
+  const int64_t want = (kApplyBlocks + tiles - 1) / tiles;
+  return std::max<int64_t>(1, std::min<int64_t>(want, tiles));
 }
 
 // host: the cell's inverse and per-axis reach; false for a singular cell
@@ -411,6 +564,50 @@ int xnn_eeq_real_grad(const double* pos, int64_t n_nodes, const double* cell, co
   hipLaunchKernelGGL(eeq_real_grad_kernel, dim3((unsigned)grid_1d(n_nodes, 4)), dim3(256), 0,
                      as_hip(stream), pos, n_nodes, C, rad, alpha, cutoff * cutoff, u, w, grad_pos,
                      cell_partial);
+  XNN_LAUNCH_CHECK();
+  return XNN_OK;
+}
+
+int xnn_eeq_real_apply_work_size(int64_t n_nodes, int32_t nrhs, size_t* bytes) {
+  XNN_REQUIRE(n_nodes >= 0 && bytes != nullptr, "negative size or NULL output");
+  XNN_REQUIRE(nrhs == 1 || nrhs == 2, "one or two right-hand sides (got %d)", (int)nrhs);
+  *bytes = sizeof(double) * (size_t)std::max<int64_t>(eeq_apply_splits(n_nodes) * n_nodes * nrhs, 1);
+  return XNN_OK;
+}
+
+int xnn_eeq_real_apply(const double* pos, int64_t n_nodes, const double* cell, const double* rad,
+                       double alpha, double cutoff, const double* tiles, const double* v,
+                       int32_t nrhs, double* out, void* work, size_t work_bytes,
+                       xnn_stream_t stream) {
+  XNN_REQUIRE(n_nodes >= 0, "negative size");
+  XNN_REQUIRE(nrhs == 1 || nrhs == 2, "one or two right-hand sides (got %d)", (int)nrhs);
+  if (n_nodes == 0) return XNN_OK;
+  XNN_REQUIRE(pos && rad && v && out && work, "NULL input, output or workspace");
+  XNN_REQUIRE(n_nodes <= (int64_t(1) << 26), "at most 2^26 atoms");
+  XNN_REQUIRE(cutoff > 0.0 && alpha >= 0.0, "cutoff must be positive, alpha non-negative");
+  XNN_REQUIRE(cell != nullptr || alpha == 0.0, "a molecule takes alpha = 0");
+  const int64_t splits = eeq_apply_splits(n_nodes);
+  XNN_REQUIRE(work_bytes >= sizeof(double) * (size_t)(splits * n_nodes * nrhs),
+              "workspace too small");
+  EeqCell C;
+  XNN_REQUIRE(eeq_cell(cell, cutoff, C), "singular cell");
+  XNN_REQUIRE(eeq_reach_ok(C, cutoff), "the real-space range spans more than %g cells",
+              kMaxReach);
+  const int64_t n_tiles = (n_nodes + kApplyTile - 1) / kApplyTile;
+  const int64_t per = (n_tiles + splits - 1) / splits;
+  const dim3 grid((unsigned)n_tiles, (unsigned)splits);
+  hipStream_t s = as_hip(stream);
+  double* part = static_cast<double*>(work);
+  if (nrhs == 1)
+    hipLaunchKernelGGL(eeq_real_apply_kernel<1>, grid, dim3(kApplyTile), 0, s, pos, n_nodes, C,
+                       rad, alpha, cutoff, tiles, v, per, part);
+  else
+    hipLaunchKernelGGL(eeq_real_apply_kernel<2>, grid, dim3(kApplyTile), 0, s, pos, n_nodes, C,
+                       rad, alpha, cutoff, tiles, v, per, part);
+  XNN_LAUNCH_CHECK();
+  const int64_t m = n_nodes * nrhs;
+  hipLaunchKernelGGL(eeq_sum_splits_kernel, dim3((unsigned)grid_1d(m, 256)), dim3(256), 0, s, part,
+                     splits, m, out);
   XNN_LAUNCH_CHECK();
   return XNN_OK;
 }

@@ -693,9 +693,14 @@ class DFTD4(nn.Module):
                  cutoff_cn: float = 30.0 * BOHR, cutoff_eeq_cn: float = 25.0 * BOHR,
                  switch_width_pair: float = 0.0, switch_width_triple: float = 0.0,
                  tail_correction: bool = False, regime: str = "auto",
-                 cutoff_eeq: Optional[float] = None):
+                 cutoff_eeq: Optional[float] = None, eeq_solver: str = "auto"):
         super().__init__()
         self.tail_correction = bool(tail_correction)
+        if eeq_solver not in ("auto", "lu", "cg"):
+            raise ValueError(f"eeq_solver must be 'auto', 'lu' or 'cg', got {eeq_solver!r}")
+        # the large regime's solve: the factorized operator up to LU_MAX_ATOMS atoms,
+        # conjugate gradients above (eeq.py:194, 226)
+        self.eeq_solver = eeq_solver
         regime = str(regime).lower()
         if regime not in EEQ_REGIMES:
             raise ValueError(f"regime must be one of {EEQ_REGIMES}, got {regime!r}")
@@ -748,7 +753,7 @@ class DFTD4(nn.Module):
             diag = self.eeq_eta[z] + math.sqrt(2.0 / math.pi) / rad
             x = -self.eeq_chi[z] + self.eeq_kcnchi[z] * cn_eeq / torch.sqrt(cn_eeq + EEQ_CN_REG)
             return eeq_charges_large(pos_au, cell_au, rad, diag, x, float(total_charge),
-                                     self.cutoff_eeq / BOHR)
+                                     self.cutoff_eeq / BOHR, solver=self.eeq_solver)
         A = self._coulomb_periodic(z, pos_au, cell_au) if cell_au is not None else \
             self._coulomb_molecular(z, pos_au)
         x = -self.eeq_chi[z] + self.eeq_kcnchi[z] * cn_eeq / torch.sqrt(cn_eeq + EEQ_CN_REG)

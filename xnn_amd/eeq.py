@@ -35,6 +35,22 @@ from . import _lib
 
 #: relative truncation of the real- and reciprocal-space Ewald tails
 EWALD_EPS = 1e-10
+#: atoms up to which the assembled operator is factorized; conjugate gradients above
+#: (eeq.py:70, 226: two (N, N) float64 matrices, 2.3 GB at 12,000 atoms)
+LU_MAX_ATOMS = 12000
+#: conjugate-gradient stopping rule |r| <= tol |b| per right-hand side, and its cap
+#: (eeq.py:63-67)
+CG_TOL = 1e-12
+CG_MAXITER = 1000
+#: float64 entries of the (N, 2C) column table of the factorized reciprocal product kept
+#: between products (2 GB); above it the table is formed again in blocks at every product
+TABLE_BUDGET = 1 << 28
+#: (N, G) entries per block of the differentiable reciprocal sum (recomputed in the
+#: backward)
+LIVE_BUDGET = 1 << 23
+#: reciprocal vectors (smallest |G|, largest weights) in the low-rank part of the
+#: conjugate-gradient preconditioner (dispersion_fast/eeq.py:60-66); 0 for plain Jacobi
+LOW_K_VECTORS = 256
 _NS = "xnn_amd"
 
 
@@ -84,11 +100,32 @@ def reciprocal_weights(m: Tensor, cell_au: Tensor, alpha: float) -> Tuple[Tensor
     return g, w
 
 
-def reciprocal_apply(pos: Tensor, g: Tensor, w: Tensor, v: Tensor) -> Tensor:
-    """``A_rec v = C diag(w) C^T v + S diag(w) S^T v`` with ``C, S = cos, sin(pos G^T)``."""
+def _reciprocal_block(pos: Tensor, g: Tensor, w: Tensor, v: Tensor) -> Tensor:
     phase = pos @ g.t()
     c, s = torch.cos(phase), torch.sin(phase)
     return c @ (w * (c.t() @ v)) + s @ (w * (s.t() @ v))
+
+
+def reciprocal_apply(pos: Tensor, g: Tensor, w: Tensor, v: Tensor) -> Tensor:
+    """``A_rec v = C diag(w) C^T v + S diag(w) S^T v`` with ``C, S = cos, sin(pos G^T)``,
+    over blocks of reciprocal vectors of at most :data:`LIVE_BUDGET` phases each; a block
+    that carries gradients is recomputed in the backward instead of kept (memory
+    ``O(LIVE_BUDGET)`` at any size)."""
+    n = max(int(pos.shape[0]), 1)
+    step = max(1, LIVE_BUDGET // n)
+    if g.shape[0] <= step:
+        return _reciprocal_block(pos, g, w, v)
+    live = torch.is_grad_enabled() and any(t.requires_grad for t in (pos, g, w, v))
+    out = None
+    for k0 in range(0, int(g.shape[0]), step):
+        args = (pos, g[k0:k0 + step], w[k0:k0 + step], v)
+        if live:
+            from torch.utils.checkpoint import checkpoint
+            part = checkpoint(_reciprocal_block, *args, use_reentrant=False)
+        else:
+            part = _reciprocal_block(*args)
+        out = part if out is None else out + part
+    return out
 
 
 # --------------------------------------------------------------------------- real space (HIP)
@@ -112,12 +149,39 @@ def real_matrix(pos: Tensor, cell: Optional[Tensor], rad: Tensor, alpha: float,
     return out
 
 
+def real_apply(pos: Tensor, cell, rad: Tensor, alpha: float, cutoff_au: float,
+               v: Tensor, tiles: Optional[Tensor] = None, work: Optional[Tensor] = None) -> Tensor:
+    """``R v`` for ``v`` (N, 1 or 2) without the matrix (``xnn_eeq_real_apply``, HIP):
+    every pair and image evaluated at every product, memory O(N). ``cell``: the (3, 3)
+    tensor, its 9 host doubles (:func:`_host_cell`) or None. ``tiles``: bounding
+    spheres of 256-atom tiles of ``pos`` (:func:`tile_bounds`) to skip distant tiles;
+    ``work``: a reusable workspace of at least the queried size (uint8)."""
+    n, r = int(pos.shape[0]), int(v.shape[1])
+    out = torch.empty((n, r), dtype=torch.float64, device=pos.device)
+    if n == 0:
+        return out
+    need = ctypes.c_size_t(0)
+    _lib.call("xnn_eeq_real_apply_work_size", n, r, ctypes.byref(need))
+    if work is None or work.numel() < need.value:
+        work = torch.empty(need.value, dtype=torch.uint8, device=pos.device)
+    vv = v.detach().to(torch.float64).contiguous()
+    host = cell if isinstance(cell, ctypes.Array) else _host_cell(cell)
+    _lib.call("xnn_eeq_real_apply", _lib.ptr(pos.detach().to(torch.float64).contiguous()), n,
+              host, _lib.ptr(rad.detach().to(torch.float64).contiguous()),
+              float(alpha), float(cutoff_au), _lib.ptr(tiles), _lib.ptr(vv), r, _lib.ptr(out),
+              _lib.ptr(work), int(work.numel()), _lib.stream(pos.device))
+    return out
+
+
 @torch.library.custom_op(f"{_NS}::eeq_real_apply", mutates_args=())
-def real_apply_op(pos: Tensor, cell: Optional[Tensor], rad: Tensor, v: Tensor, matrix: Tensor,
-                  alpha: float, cutoff_au: float) -> Tensor:
-    """``R(pos, cell) v`` with the matrix formed at these positions; differentiable in
-    ``pos`` and ``cell`` through ``xnn_eeq_real_grad`` (``v`` is held constant)."""
-    return matrix @ v
+def real_apply_op(pos: Tensor, cell: Optional[Tensor], rad: Tensor, v: Tensor,
+                  matrix: Optional[Tensor], alpha: float, cutoff_au: float) -> Tensor:
+    """``R(pos, cell) v`` with the matrix formed at these positions, or without a matrix
+    (``matrix`` None: the matrix-free HIP product); differentiable in ``pos`` and ``cell``
+    through ``xnn_eeq_real_grad`` (``v`` is held constant)."""
+    if matrix is not None:
+        return matrix @ v
+    return real_apply(pos, cell, rad, alpha, cutoff_au, v.reshape(-1, 1)).reshape(v.shape)
 
 
 @real_apply_op.register_fake
@@ -195,9 +259,11 @@ class LargeEEQSystem:
             return torch.linalg.solve_triangular(self.factor.mT, y, upper=True)
         return torch.linalg.lu_solve(*self.lu, b)
 
-    def solve_augmented(self, top: Tensor, bottom: Tensor) -> Tuple[Tensor, Tensor]:
+    def solve_augmented(self, top: Tensor, bottom: Tensor,
+                        tol_abs: Optional[float] = None) -> Tuple[Tensor, Tensor]:
         """``[[A, 1], [1^T, 0]] [y; mu] = [top; bottom]`` by eliminating the constraint:
-        ``y = A^-1 top - mu A^-1 1`` with ``mu = (1^T A^-1 top - bottom) / 1^T A^-1 1``."""
+        ``y = A^-1 top - mu A^-1 1`` with ``mu = (1^T A^-1 top - bottom) / 1^T A^-1 1``
+        (direct: ``tol_abs`` is not used)."""
         b = top.to(torch.float64).reshape(-1, 1)
         if self.y_ones is None:                # the constraint's A^-1 1, with the first solve
             y = self._solve(torch.cat([b, torch.ones_like(b)], 1))
@@ -215,6 +281,291 @@ class LargeEEQSystem:
         """``A(pos, cell) v`` with derivatives in ``pos`` and ``cell`` (``v`` constant)."""
         out = self.diag * v + real_apply_op(pos, cell, self.rad, v, self.R, self.alpha,
                                             self.cutoff)
+        if cell is not None:
+            g, w = reciprocal_weights(self.m, cell, self.alpha)
+            out = out + reciprocal_apply(pos, g, w, v)
+        return out
+
+
+# --------------------------------------------------------------------------- CG regime
+def morton_order(unit: Tensor) -> Tensor:
+    """The permutation that orders points of the unit cube (N, 3) along a Morton curve
+    (10 bits per axis): consecutive points are close in space."""
+    q = (unit.clamp(0.0, 1.0 - 1e-12) * 1024.0).to(torch.int64)
+    code = torch.zeros(unit.shape[0], dtype=torch.int64, device=unit.device)
+    for bit in range(10):
+        for a in range(3):
+            code |= ((q[:, a] >> bit) & 1) << (3 * bit + a)
+    return torch.argsort(code, stable=True)
+
+
+def tile_bounds(pos: Tensor, tile: int = 256) -> Tensor:
+    """Per tile of ``tile`` consecutive atoms, the center and radius of a sphere holding them,
+    ``(ceil(N / tile), 4)`` (the radius rounded up: the kernels' tile test stays
+    conservative)."""
+    n = int(pos.shape[0])
+    t = (n + tile - 1) // tile
+    p = pos.to(torch.float64)
+    if t * tile > n:                      # the last tile padded with copies of its last atom
+        p = torch.cat([p, p[-1:].expand(t * tile - n, 3)])
+    p = p.view(t, tile, 3)
+    center = p.mean(1)
+    radius = torch.linalg.vector_norm(p - center[:, None], dim=-1).amax(1)
+    return torch.cat([center, (radius * (1.0 + 1e-12) + 1e-9)[:, None]], 1).contiguous()
+
+
+def own_image_diagonal(cell: Tensor, rad: Tensor, alpha: float, cutoff_au: float) -> Tensor:
+    """``R_ii``: the screened kernel summed over the atom's own lattice images ``n cell``
+    (``n != 0``) within the cutoff, ``(N,)`` (zero when the cell is wider than the cutoff)."""
+    c = cell.to(torch.float64)
+    inv = torch.linalg.inv(c)
+    reach = [int(math.floor(cutoff_au * float(torch.linalg.norm(inv[:, a])))) for a in range(3)]
+    axes = [torch.arange(-k, k + 1, dtype=torch.float64, device=c.device) for k in reach]
+    t = torch.cartesian_prod(*axes).reshape(-1, 3) @ c
+    r = torch.linalg.vector_norm(t, dim=-1)
+    r = r[(r > 1e-10) & (r <= cutoff_au)]
+    if r.numel() == 0:
+        return torch.zeros_like(rad, dtype=torch.float64)
+    gam = 1.0 / (math.sqrt(2.0) * rad.to(torch.float64))
+    k = (torch.erf(gam[:, None] * r[None]) - torch.erf(alpha * r)[None]) / r[None]
+    return k.sum(1)
+
+
+def _tn_product(b: Tensor, v: Tensor, chunks: int = 32) -> Tensor:
+    """``b^T v`` for tall ``b`` (N, P) and ``v`` (N, Q) with a long reduction over N: split
+    into ``chunks`` batched products that are summed afterwards (one library GEMM of a small
+    output would run on a handful of workgroups)."""
+    n = int(b.shape[0])
+    m = n // chunks
+    if m < 256:
+        return b.t() @ v
+    k = m * chunks
+    out = torch.bmm(b[:k].view(chunks, m, -1).transpose(1, 2), v[:k].view(chunks, m, -1)).sum(0)
+    if k < n:
+        out += b[k:].t() @ v[k:]
+    return out
+
+
+class FactorizedReciprocal:
+    """``A_rec v`` at fixed positions through factorized structure-factor phases
+    (dispersion_fast/eeq.py:1-33): with ``G = m B``, ``exp(i G . r) = exp(2 pi i (m_1 f_1 +
+    m_2 f_2)) exp(2 pi i m_3 f_3)`` for the fractional coordinates ``f``; the vectors of
+    the half set are grouped in columns of fixed ``(m_1, m_2)``, whose phases ``Bc (N, C)``
+    are products of two per-axis tables, and the third axis is ``P (N, 2 M_3 + 1)``. Then
+    ``S = Bc^T (P * v)`` is the structure factor of ``v`` on every vector and ``A_rec v =
+    Re[sum_k conj(P_k) (conj(Bc) (W S))_k]``: two real GEMMs per product (library GEMMs,
+    real and imaginary parts stacked), no trigonometry. ``Bc`` is kept while it fits
+    :data:`TABLE_BUDGET` and formed again in column blocks otherwise."""
+
+    def __init__(self, pos: Tensor, cell: Tensor, m: Tensor, alpha: float):
+        c = cell.to(torch.float64)
+        f = pos.to(torch.float64) @ torch.linalg.inv(c)
+        g, w = reciprocal_weights(m, c, alpha)
+        mi = m.round().to(torch.int64)
+        span = [int(mi[:, a].abs().max()) if mi.shape[0] else 0 for a in range(3)]
+        self.tables = []
+        for a in range(3):
+            ms = torch.arange(-span[a], span[a] + 1, dtype=torch.float64, device=f.device)
+            ph = (2.0 * math.pi) * f[:, a:a + 1] * ms[None]
+            self.tables.append((torch.cos(ph), torch.sin(ph)))
+        w2 = 2 * span[1] + 1
+        key = (mi[:, 0] + span[0]) * w2 + (mi[:, 1] + span[1])
+        cols, col_of = torch.unique(key, return_inverse=True)
+        self.c1, self.c2 = cols // w2, cols % w2
+        self.K = 2 * span[2] + 1
+        self.C = int(cols.numel())
+        W = torch.zeros((self.C, self.K), dtype=torch.float64, device=f.device)
+        W[col_of, mi[:, 2] + span[2]] = w
+        self.W = W
+        self.n = int(f.shape[0])
+        self.diagonal = float(w.sum())     # A_rec,ii = sum_G w_G
+        self.block = max(1, TABLE_BUDGET // max(2 * self.n, 1))
+        self.table = self._columns(0, self.C) if self.C <= self.block else None
+
+    def _columns(self, c0: int, c1: int) -> Tensor:
+        (ar, ai), (br, bi) = self.tables[0], self.tables[1]
+        ar, ai = ar[:, self.c1[c0:c1]], ai[:, self.c1[c0:c1]]
+        br, bi = br[:, self.c2[c0:c1]], bi[:, self.c2[c0:c1]]
+        return torch.cat([ar * br - ai * bi, ar * bi + ai * br], 1)
+
+    def apply(self, v: Tensor) -> Tensor:
+        """``A_rec v`` for ``v`` (N, R)."""
+        n, R = v.shape
+        K, KR = self.K, self.K * v.shape[1]
+        pr, pi = self.tables[2]
+        vp = torch.cat([(pr[:, :, None] * v[:, None, :]).reshape(n, KR),
+                        (pi[:, :, None] * v[:, None, :]).reshape(n, KR)], 1)
+        ur = v.new_zeros((n, KR))
+        ui = v.new_zeros((n, KR))
+        for c0 in range(0, self.C, self.block):
+            c1 = min(self.C, c0 + self.block)
+            b = self.table if self.table is not None else self._columns(c0, c1)
+            cb = c1 - c0
+            x = _tn_product(b, vp)                           # (2 cb, 2 KR)
+            sr = x[:cb, :KR] - x[cb:, KR:]
+            si = x[:cb, KR:] + x[cb:, :KR]
+            wb = self.W[c0:c1].repeat_interleave(R, dim=1)
+            gr, gi = wb * sr, wb * si
+            y = b @ torch.cat([torch.cat([gr, gi], 1), torch.cat([gi, -gr], 1)], 0)
+            ur += y[:, :KR]
+            ui += y[:, KR:]
+        return (pr[:, :, None] * ur.view(n, K, R) + pi[:, :, None] * ui.view(n, K, R)).sum(1)
+
+
+class IterativeEEQSystem:
+    """The EEQ operator of one structure at fixed (detached) geometry, never assembled: the
+    conjugate-gradient regime above :data:`LU_MAX_ATOMS` (eeq.py:226, 325-360;
+    dispersion_fast/eeq.py:1-33). A product is ``diag v`` plus the matrix-free real-space
+    product (``xnn_eeq_real_apply``, HIP, atoms ordered along a Morton curve of the wrapped
+    fractional coordinates so that 256-atom tiles are compact and far tiles are skipped)
+    plus the factorized reciprocal product (:class:`FactorizedReciprocal`). Memory O(N) in
+    the real-space part and O(N C) in the reciprocal tables. Solves: preconditioned
+    conjugate gradients, the preconditioner the full diagonal (``J + sqrt(2/pi)/a - 2
+    alpha/sqrt(pi)``, the own images and ``sum_G w_G``) with the long-range modes of the
+    smallest reciprocal vectors as a low-rank part (:meth:`_low_rank`; Jacobi for a
+    molecule), the charge and the constraint right-hand sides in lockstep as two columns
+    of one product. Same interface as :class:`LargeEEQSystem`."""
+
+    def __init__(self, pos: Tensor, cell: Optional[Tensor], rad: Tensor, diag: Tensor,
+                 alpha: float, cutoff_au: float, eps: float = EWALD_EPS, tol: float = CG_TOL,
+                 maxiter: int = CG_MAXITER):
+        self.pos = pos.detach().to(torch.float64)
+        self.cell = None if cell is None else cell.detach().to(torch.float64)
+        self.rad, self.alpha, self.cutoff = rad.detach().to(torch.float64), float(alpha), float(cutoff_au)
+        self.diag = diag.detach().to(torch.float64)
+        self.tol, self.maxiter = float(tol), int(maxiter)
+        self.n = int(self.pos.shape[0])
+        if self.cell is not None:
+            frac = self.pos @ torch.linalg.inv(self.cell)
+            frac = frac - torch.floor(frac)
+            self.order = morton_order(frac)
+            self.pos_s = (frac[self.order] @ self.cell).contiguous()
+            self.tiles = tile_bounds(self.pos_s)
+            self.m = reciprocal_half_set(self.cell, self.alpha, eps)
+            self.recip = FactorizedReciprocal(self.pos_s, self.cell, self.m, self.alpha)
+            own = own_image_diagonal(self.cell, self.rad, self.alpha, self.cutoff)
+            full = self.diag + own + self.recip.diagonal
+            self._low_rank(full[self.order])
+        else:
+            lo = self.pos.amin(0)
+            span = (self.pos.amax(0) - lo).clamp_min(1e-12)
+            self.order = morton_order((self.pos - lo) / span)
+            self.pos_s = self.pos[self.order].contiguous()
+            self.tiles = None                  # every pair: nothing to skip
+            self.m, self.recip = None, None
+            full = self.diag
+        self.cell_host = _host_cell(self.cell)
+        self.rad_s = self.rad[self.order].contiguous()
+        self.diag_s = self.diag[self.order].contiguous()
+        if self.cell is None:
+            self.U = None
+            self.inv_d = (1.0 / full[self.order]).contiguous()
+        self.y_ones = None
+        self.iterations = []                   # per conjugate-gradient solve
+        self._work = None
+
+    def _low_rank(self, full_s: Tensor) -> None:
+        """The preconditioner ``M = D + U W U^T`` (dispersion_fast/eeq.py:72-86): ``U = [cos,
+        sin]`` of the :data:`LOW_K_VECTORS` smallest reciprocal vectors at the (ordered)
+        positions, ``W`` their weights, ``D`` the full diagonal of ``A`` less that part's
+        (``sum_l w_l``); ``M^-1`` through the Woodbury identity with the Cholesky factor of
+        ``W^-1 + U^T D^-1 U``. It changes how fast the iteration converges, not its limit."""
+        g, w = reciprocal_weights(self.m, self.cell, self.alpha)
+        L = min(LOW_K_VECTORS, int(g.shape[0]))
+        if L == 0:
+            self.U = None
+            self.inv_d = (1.0 / full_s).contiguous()
+            return
+        idx = torch.argsort((g * g).sum(1))[:L]
+        ph = self.pos_s @ g[idx].t()
+        self.U = torch.cat([torch.cos(ph), torch.sin(ph)], 1).contiguous()
+        wl = torch.cat([w[idx], w[idx]])
+        self.inv_d = (1.0 / (full_s - w[idx].sum())).contiguous()
+        core = torch.diag(1.0 / wl) + self.U.t() @ (self.inv_d[:, None] * self.U)
+        self.core = torch.linalg.cholesky(core)
+
+    def precondition(self, r: Tensor) -> Tensor:
+        """``M^-1 r`` for the columns of ``r``."""
+        z = self.inv_d[:, None] * r
+        if self.U is None:
+            return z
+        t = torch.cholesky_solve(_tn_product(self.U, z), self.core)
+        return z - self.inv_d[:, None] * (self.U @ t)
+
+    def _matvec(self, v: Tensor) -> Tensor:
+        """``A v`` in the spatial order, ``v`` (N, 1 or 2)."""
+        need = ctypes.c_size_t(0)
+        _lib.call("xnn_eeq_real_apply_work_size", self.n, int(v.shape[1]), ctypes.byref(need))
+        if self._work is None or self._work.numel() < need.value:
+            self._work = torch.empty(need.value, dtype=torch.uint8, device=v.device)
+        out = real_apply(self.pos_s, self.cell_host, self.rad_s, self.alpha, self.cutoff, v,
+                         self.tiles, self._work)
+        out += self.diag_s[:, None] * v
+        if self.recip is not None:
+            out += self.recip.apply(v)
+        return out
+
+    def conjugate_gradient(self, b: Tensor, tol_abs: Tensor) -> Tensor:
+        """``A^-1 b`` for the columns of ``b`` (N, 1 or 2) in the spatial order, each column
+        to ``|r| <= tol_abs`` (a column that meets it is frozen while the other runs)."""
+        x = self.precondition(b)
+        r = b - self._matvec(x)
+        z = self.precondition(r)
+        p = z.clone()
+        rz = (r * z).sum(0)
+        for it in range(self.maxiter + 1):
+            done = torch.linalg.vector_norm(r, dim=0) <= tol_abs
+            if bool(done.all()):
+                self.iterations.append(it)
+                return x
+            if it == self.maxiter:
+                break
+            ap = self._matvec(p)
+            a = torch.where(done, torch.zeros_like(rz), rz / (p * ap).sum(0))
+            x += a * p
+            r -= a * ap
+            z = self.precondition(r)
+            rz_new = (r * z).sum(0)
+            p = z + torch.where(done, torch.zeros_like(rz), rz_new / rz) * p
+            rz = rz_new
+        res = torch.linalg.vector_norm(r, dim=0) / torch.linalg.vector_norm(b, dim=0)
+        raise RuntimeError(f"EEQ conjugate gradients did not converge in {self.maxiter} "
+                           f"iterations (relative residuals {res.tolist()})")
+
+    def solve_augmented(self, top: Tensor, bottom: Tensor,
+                        tol_abs: Optional[float] = None) -> Tuple[Tensor, Tensor]:
+        """``[[A, 1], [1^T, 0]] [y; mu] = [top; bottom]`` by eliminating the constraint
+        (eeq.py:325-331): ``y = A^-1 top - mu A^-1 1``; ``A^-1 1`` is solved with the first
+        right-hand side, as a second column of the same iteration. ``tol_abs``: an absolute
+        tolerance for ``top``'s solve (default ``tol |top|``)."""
+        b = top.detach().to(torch.float64).reshape(-1)[self.order]
+        tb = self.tol * float(torch.linalg.vector_norm(b)) if tol_abs is None else float(tol_abs)
+        if self.y_ones is None:
+            ones = torch.ones_like(b)
+            tols = torch.tensor([tb, self.tol * math.sqrt(self.n)], dtype=torch.float64,
+                                device=b.device)
+            y = self.conjugate_gradient(torch.stack([b, ones], 1), tols)
+            y1, self.y_ones = y[:, 0], y[:, 1].contiguous()
+        else:
+            y1 = self.conjugate_gradient(b[:, None], torch.tensor([tb], dtype=torch.float64,
+                                                                   device=b.device))[:, 0]
+        mu = (y1.sum() - bottom) / self.y_ones.sum()
+        y = y1 - mu * self.y_ones
+        out = torch.empty_like(y)
+        out[self.order] = y
+        return out, mu
+
+    def apply(self, v: Tensor) -> Tensor:
+        """``A v`` at the detached geometry, in the atoms' order."""
+        y = self._matvec(v.detach().to(torch.float64)[self.order][:, None])[:, 0]
+        out = torch.empty_like(y)
+        out[self.order] = y
+        return out
+
+    def apply_live(self, pos: Tensor, cell: Optional[Tensor], v: Tensor) -> Tensor:
+        """``A(pos, cell) v`` with derivatives in ``pos`` and ``cell`` (``v`` constant): the
+        matrix-free real-space product and the reciprocal sum in recomputed blocks."""
+        out = self.diag * v + real_apply_op(pos, cell, self.rad, v, None, self.alpha, self.cutoff)
         if cell is not None:
             g, w = reciprocal_weights(self.m, cell, self.alpha)
             out = out + reciprocal_apply(pos, g, w, v)
@@ -278,24 +629,33 @@ class _ConstantSolve(torch.autograd.Function):
 
 def eeq_charges_large(pos: Tensor, cell: Optional[Tensor], rad: Tensor, diag: Tensor,
                       x: Tensor, total_charge: float, cutoff_au: float,
-                      eps: float = EWALD_EPS) -> Tensor:
+                      eps: float = EWALD_EPS, solver: str = "auto") -> Tensor:
     """EEQ charges of one structure in the large regime (eeq.py:664-700): positions and
     cell in bohr (``cell`` None: a molecule), the charge widths ``rad``, the diagonal
     ``J + sqrt(2/pi) / a`` (the ``- 2 alpha / sqrt(pi)`` of a cell is added here), the
     right-hand side ``x`` and the total charge; ``cutoff_au`` the real-space range.
-    Differentiable once in ``pos``, ``cell`` and ``x``."""
+    ``solver``: ``"auto"`` (the factorized operator up to :data:`LU_MAX_ATOMS` atoms,
+    conjugate gradients above, eeq.py:226), ``"lu"`` or ``"cg"``. Differentiable once in
+    ``pos``, ``cell`` and ``x``."""
+    if solver not in ("auto", "lu", "cg"):
+        raise ValueError(f"solver must be 'auto', 'lu' or 'cg', got {solver!r}")
     periodic = cell is not None
     alpha = ewald_alpha(cutoff_au, eps) if periodic else 0.0
     if periodic:
         diag = diag - 2.0 * alpha / math.sqrt(math.pi)
     else:
         cutoff_au = math.inf            # a molecule: every pair (eeq.py:346-360), no split
-    system = LargeEEQSystem(pos, cell, rad, diag, alpha, cutoff_au, eps)
+    n = int(pos.shape[0])
+    iterative = solver == "cg" or (solver == "auto" and n > LU_MAX_ATOMS)
+    kind = IterativeEEQSystem if iterative else LargeEEQSystem
+    system = kind(pos, cell, rad, diag, alpha, cutoff_au, eps)
     total = torch.as_tensor(float(total_charge), dtype=torch.float64, device=pos.device)
     with torch.no_grad():
         xd = x.detach().to(torch.float64)
         q0, mu0 = system.solve_augmented(xd, total)
-        dq, dmu = system.solve_augmented(xd - system.apply(q0) - mu0, total - q0.sum())
+        # the residual correction (zero at convergence) to the first solve's tolerance
+        tol_abs = CG_TOL * float(torch.linalg.vector_norm(xd)) if iterative else None
+        dq, dmu = system.solve_augmented(xd - system.apply(q0) - mu0, total - q0.sum(), tol_abs)
         q1, mu1 = q0 + dq, mu0 + dmu
     live = x.requires_grad or pos.requires_grad or (periodic and cell.requires_grad)
     if not (live and torch.is_grad_enabled()):
