@@ -268,7 +268,7 @@ def build_workload(config: str, device):
         ei, sh = xa.build_neighbor_list(pos, rc, cell, pbc)        # warm-up build
         torch.cuda.synchronize()
         t0 = time.perf_counter()
-        reps = 5
+        reps = 20
         for _ in range(reps):
             ei, sh = xa.build_neighbor_list(pos, rc, cell, pbc)
         torch.cuda.synchronize()

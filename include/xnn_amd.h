@@ -774,6 +774,23 @@ int xnn_radius_graph_fill(int geom_dtype, const void* pos, int64_t n_nodes, cons
                           int64_t* edge_index64, int64_t* shifts64, int32_t* overflow,
                           xnn_stream_t stream);
 
+/* The fill without the host knowing the edge count (replaces the same step of
+ * build_neighbor_list, neighborlist.py:462-506, for a caller that sizes its outputs from
+ * an earlier list, e.g. the last step of an MD run): after xnn_radius_graph_count, the
+ * count E = row_ptr[n_nodes] is read on the device and, when E <= capacity, edge_index64 is
+ * written as (2, E) and shifts64 as (E, 3) at the front of buffers of 2 capacity and
+ * 3 capacity entries; when E > capacity nothing is written and the fill may be run again
+ * with room (xnn_radius_graph_fill with n_edges = E). status (nullable, 2 int32, device)
+ * receives what xnn_radius_graph_status gives: E and the non-finite flag. No host
+ * synchronization. Either fill runs once per count (it counts the count step's totals
+ * down), except after a capacity fill that had no room. */
+int xnn_radius_graph_fill_capacity(int geom_dtype, const void* pos, int64_t n_nodes,
+                                   const void* cell, double cutoff, int32_t self_interaction,
+                                   const xnn_grid_plan* plan, void* workspace,
+                                   const int32_t* row_ptr, int64_t capacity,
+                                   int64_t* edge_index64, int64_t* shifts64, int32_t* status,
+                                   xnn_stream_t stream);
+
 /* Radius graph of a batch of small molecules (no cell): structure b owns atoms
  * [node_ptr[b], node_ptr[b+1]); every atom tests every atom of its structure.
  * Same two-step protocol as above (count -> row_ptr, then fill). Structures of

@@ -186,6 +186,25 @@ def test_periodic_plan_reuse_keeps_the_edge_set():
     bad[7, 1] = float("nan")
     with pytest.raises(ValueError, match="not finite"):
         xa.build_neighbor_list(bad, 5.0, cell, pbc)
+    # a reused plan sizes its outputs from the last list (+5 %): a list that outgrows that
+    # room (the atoms packed into half the cell, four times the edges) is filled again
+    # exactly, and the next, smaller list fits the room of the larger one
+    fresh = torch.tensor(s.cell, dtype=torch.float32, device=DEV)
+    e0 = xa.build_neighbor_list(pos0, 5.0, fresh, pbc)[0].shape[1]
+    packed = (pos0 * 0.5).contiguous()
+    for pos in (packed, pos0):
+        ei, sh = xa.build_neighbor_list(pos, 5.0, fresh, pbc)
+        assert ei.is_contiguous() and sh.is_contiguous()
+        ei_o, sh_o, near = N.neighbor_list(pos.cpu().numpy(), 5.0, s.cell, s.pbc,
+                                           dtype=np.float32, margin=1e-5)
+        print(f"capacity room: {ei.shape[1]} edges after {e0}; {near} pairs near the cutoff",
+              flush=True)
+        if near == 0:
+            assert np.array_equal(canonical(ei.cpu().numpy(), sh.cpu().numpy()),
+                                  canonical(ei_o, sh_o))
+        else:
+            assert abs(ei.shape[1] - ei_o.shape[1]) <= near
+    assert ei.shape[1] == e0 and D._PERIODIC_PLANS[key][5][0] == e0
 
 
 def test_neighbor_list_capacity_mode_eager_and_captured():

@@ -202,6 +202,8 @@ _SIGNATURES = {
     "xnn_radius_graph_status": [c_int, i64, ctypes.POINTER(GridPlan), vp, vp, vp, vp],
     "xnn_radius_graph_fill": [c_int, vp, i64, vp, dbl, i32, ctypes.POINTER(GridPlan), vp, vp, i64,
                               vp, vp, vp, vp, vp, vp, vp],
+    "xnn_radius_graph_fill_capacity": [c_int, vp, i64, vp, dbl, i32, ctypes.POINTER(GridPlan), vp,
+                                       vp, i64, vp, vp, vp, vp],
     "xnn_radius_graph_molecules_count": [c_int, vp, i64, vp, vp, i64, dbl, i32, vp, vp],
     "xnn_radius_graph_molecules_fill": [c_int, vp, i64, vp, vp, i64, dbl, i32, vp, i64, vp, vp,
                                         vp, vp, vp, vp],

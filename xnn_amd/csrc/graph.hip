@@ -182,7 +182,9 @@ __global__ __launch_bounds__(256) void cell_search_kernel(
     const G* __restrict__ cell, GridDev g, G cutoff, int self_interaction,
     int32_t* __restrict__ counts, const int32_t* __restrict__ row_ptr, int32_t* __restrict__ src,
     int32_t* __restrict__ dst, int32_t* __restrict__ shift_out, int64_t* __restrict__ ei64,
-    int64_t* __restrict__ sh64, int64_t n_edges, int32_t* __restrict__ overflow) {
+    int64_t* __restrict__ sh64, int64_t n_edges, int32_t* __restrict__ overflow,
+    const int32_t* __restrict__ e_total, int32_t* __restrict__ status,
+    const int32_t* __restrict__ nonfinite) {
   constexpr int kMaxSlots = 343;  // reach <= 3 per axis
   __shared__ int s_bin[kMaxSlots];
   __shared__ int s_img[kMaxSlots][3];
@@ -193,6 +195,11 @@ __global__ __launch_bounds__(256) void cell_search_kernel(
   __shared__ int t_slot[kTile];
 
   const int bin = blockIdx.x;
+  // the fill's status for the host: the number of edges and the non-finite flag
+  if (FILL && status != nullptr && blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x == 0) {
+    status[0] = e_total != nullptr ? *e_total : (int32_t)n_edges;
+    status[1] = *nonfinite;
+  }
   const int bx = bin % g.nb[0], by = (bin / g.nb[0]) % g.nb[1], bz = bin / (g.nb[0] * g.nb[1]);
   const int r0 = bin_start[bin], r1 = bin_start[bin + 1];
   // the bin's receivers are dealt to gridDim.y blocks, a wave's worth at a time
@@ -221,6 +228,8 @@ __global__ __launch_bounds__(256) void cell_search_kernel(
       }
     }
     s_bin[s] = ok ? (idx[2] * g.nb[1] + idx[1]) * g.nb[0] + idx[0] : -1;
+    // the slot's candidate count (its bin's atoms), loaded by all threads at once
+    s_first[s + 1] = ok ? bin_start[s_bin[s] + 1] - bin_start[s_bin[s]] : 0;
     s_img[s][0] = img[0];
     s_img[s][1] = img[1];
     s_img[s][2] = img[2];
@@ -233,20 +242,37 @@ __global__ __launch_bounds__(256) void cell_search_kernel(
     }
   }
   __syncthreads();
-  if (threadIdx.x == 0) {
-    int acc = 0;
-    for (int s = 0; s < n_slots; ++s) {
-      s_first[s] = acc;
-      const int b = s_bin[s];
-      if (b >= 0) acc += bin_start[b + 1] - bin_start[b];
+  // s_first = exclusive prefix sums of the slot counts (held in s_first[1..n_slots]): the
+  // first wave scans them, each lane a run of consecutive slots
+  if (threadIdx.x < kWave) {
+    const int lane0 = threadIdx.x;
+    const int per = (n_slots + kWave - 1) / kWave;
+    const int a0 = min(n_slots, lane0 * per), a1 = min(n_slots, a0 + per);
+    int sum = 0;
+    for (int q = a0; q < a1; ++q) sum += s_first[q + 1];
+    int x = sum;
+#pragma unroll
+    for (int o = 1; o < kWave; o <<= 1) {
+      const int y = __shfl_up(x, o, kWave);
+      if (lane0 >= o) x += y;
     }
-    s_first[n_slots] = acc;
+    int run = x - sum;
+    for (int q = a0; q < a1; ++q) {
+      const int c = s_first[q + 1];
+      s_first[q + 1] = run + c;
+      run += c;
+    }
+    if (lane0 == 0) s_first[0] = 0;
   }
   __syncthreads();
   const int n_cand = s_first[n_slots];
 
   const int wave = wave_in_block(), lane = threadIdx.x % kWave;
   const int n_recv = r1 - r0;
+  // the number of edges: given, or (capacity mode, e_total) the count pass's total on the
+  // device, written only when it fits the n_edges entries the outputs hold
+  const int64_t n_out = (FILL && e_total != nullptr) ? (int64_t)*e_total : n_edges;
+  const bool fits = n_out <= n_edges;
 
   for (int c0 = 0; c0 < n_cand; c0 += kTile) {
     const int c1 = min(n_cand, c0 + kTile);
@@ -270,8 +296,11 @@ __global__ __launch_bounds__(256) void cell_search_kernel(
       const int pr = r0 + r;
       const int i = atom_sorted[pr];
       const G xi = wpos[4 * pr + 0], yi = wpos[4 * pr + 1], zi = wpos[4 * pr + 2];
-      // edges of receiver i found in earlier tiles (a receiver stays with its wave)
-      const int base = counts[i];
+      // edges of receiver i found in earlier tiles (a receiver stays with its wave): the
+      // count pass adds them up from zero; the fill counts the count pass's totals down,
+      // so it needs no zeroing and leaves them in place when its outputs have no room
+      const int rem = counts[i];
+      const int base = FILL ? (row_ptr[i + 1] - row_ptr[i]) - rem : rem;
       int local = 0;
       for (int c = 0; c < c1 - c0; c += kWave) {
         const int t = c + lane;
@@ -297,7 +326,7 @@ __global__ __launch_bounds__(256) void cell_search_kernel(
         if (FILL && hit) {
           const int rank = __popcll(mask & ((1ull << lane) - 1ull));
           const int64_t e = (int64_t)row_ptr[i] + base + local + rank;
-          if (e < n_edges) {
+          if (fits && e < n_out) {
             const int oi0 = offs[4 * pr + 0], oi1 = offs[4 * pr + 1], oi2 = offs[4 * pr + 2];
             // sender offsets live with the sorted copy; find j's through its own slot
             const int pj = bin_start[s_bin[s]] + (t + c0 - s_first[s]);
@@ -313,7 +342,7 @@ __global__ __launch_bounds__(256) void cell_search_kernel(
             }
             if (ei64) {
               ei64[e] = j;
-              ei64[n_edges + e] = i;
+              ei64[n_out + e] = i;
             }
             if (sh64) {
               sh64[3 * e + 0] = sx;
@@ -324,7 +353,7 @@ __global__ __launch_bounds__(256) void cell_search_kernel(
         }
         local += __popcll(mask);
       }
-      if (lane == 0) counts[i] = base + local;
+      if (lane == 0) counts[i] = FILL ? (fits ? rem - local : rem) : base + local;
     }
     __syncthreads();
   }
@@ -398,31 +427,69 @@ __global__ void zero_fill_state_kernel(int32_t* __restrict__ counts, int64_t nc,
 }
 
 // One block's scan of m <= kBlockScanMax ints (in and out distinct): out[i] = the sum of
-// in[0..i) (exclusive) or in[0..i] (inclusive). Each thread sums a contiguous chunk, the
-// 1024 chunk sums are scanned in LDS, and each thread writes its chunk's prefix sums.
+// in[0..i) (exclusive) or in[0..i] (inclusive). Tiles of 8192 values are loaded coalesced
+// into LDS (padded: value i at i + i / 32, so that a thread's 8 consecutive values sit in
+// distinct banks across the wave), each thread sums its 8, the 1024 sums are scanned by
+// wave shuffles and one wave over the 16 wave totals, and the prefix sums go back through
+// LDS to coalesced stores; a carry runs across tiles.
 template <bool INCLUSIVE>
 __global__ __launch_bounds__(1024) void block_scan_kernel(const int32_t* __restrict__ in,
                                                           int32_t* __restrict__ out, int64_t m) {
-  __shared__ int32_t part[1024];
-  const int t = threadIdx.x;
-  const int64_t chunk = (m + 1023) / 1024;
-  const int64_t a = min<int64_t>(m, (int64_t)t * chunk), b = min<int64_t>(m, a + chunk);
-  int32_t sum = 0;
-  for (int64_t i = a; i < b; ++i) sum += in[i];
-  part[t] = sum;
-  __syncthreads();
-  for (int off = 1; off < 1024; off <<= 1) {
-    const int32_t v = t >= off ? part[t - off] : 0;
+  constexpr int kPer = 8, kTileN = 1024 * kPer;
+  __shared__ int32_t tile[kTileN + kTileN / 32];
+  __shared__ int32_t wsum[16];
+  const int t = threadIdx.x, lane = t & (kWave - 1), wv = t / kWave;
+  int32_t carry = 0;
+  for (int64_t base = 0; base < m; base += kTileN) {
+    const int cnt = (int)min<int64_t>(kTileN, m - base);
+#pragma unroll
+    for (int k = 0; k < kPer; ++k) {
+      const int i = k * 1024 + t;
+      tile[i + (i >> 5)] = i < cnt ? in[base + i] : 0;
+    }
     __syncthreads();
-    part[t] += v;
+    int32_t v[kPer];
+    int32_t sum = 0;
+#pragma unroll
+    for (int k = 0; k < kPer; ++k) {
+      const int i = t * kPer + k;
+      v[k] = tile[i + (i >> 5)];
+      sum += v[k];
+    }
+    int32_t x = sum;  // inclusive scan of the thread sums within the wave
+#pragma unroll
+    for (int o = 1; o < kWave; o <<= 1) {
+      const int32_t y = __shfl_up(x, o, kWave);
+      if (lane >= o) x += y;
+    }
+    if (lane == kWave - 1) wsum[wv] = x;
     __syncthreads();
-  }
-  int32_t run = t > 0 ? part[t - 1] : 0;
-  for (int64_t i = a; i < b; ++i) {
-    const int32_t x = in[i];
-    if (INCLUSIVE) run += x;
-    out[i] = run;
-    if (!INCLUSIVE) run += x;
+    if (wv == 0) {
+      int32_t w = lane < 16 ? wsum[lane] : 0;
+#pragma unroll
+      for (int o = 1; o < 16; o <<= 1) {
+        const int32_t y = __shfl_up(w, o, kWave);
+        if (lane >= o) w += y;
+      }
+      if (lane < 16) wsum[lane] = w;
+    }
+    __syncthreads();
+    int32_t run = carry + (wv > 0 ? wsum[wv - 1] : 0) + x - sum;
+#pragma unroll
+    for (int k = 0; k < kPer; ++k) {
+      const int i = t * kPer + k;
+      if (INCLUSIVE) run += v[k];
+      tile[i + (i >> 5)] = run;
+      if (!INCLUSIVE) run += v[k];
+    }
+    carry += wsum[15];
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < kPer; ++k) {
+      const int i = k * 1024 + t;
+      if (i < cnt) out[base + i] = tile[i + (i >> 5)];
+    }
+    __syncthreads();
   }
 }
 
@@ -742,7 +809,7 @@ static int grid_count(const void* pos_v, int64_t n, const void* cell_v, double c
                      dim3(plan->n_bins, search_split(n, plan->n_bins)), dim3(256), 0, stream,
                      wpos_s, offs_s, atom_sorted, bin_start, cell, g, (G)cutoff, self_interaction,
                      counts, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, (int64_t)0,
-                     overflow);
+                     overflow, nullptr, nullptr, nullptr);
   XNN_LAUNCH_CHECK();
   // row_ptr[1..n] = inclusive scan of the per-atom counts; row_ptr[0] = 0
   if (small) {
@@ -762,22 +829,27 @@ static int grid_fill(const void* pos_v, int64_t n, const void* cell_v, double cu
                      int self_interaction, const xnn_grid_plan* plan, void* ws,
                      const int32_t* row_ptr, int64_t n_edges, int32_t* src, int32_t* dst,
                      int32_t* shift, int64_t* ei64, int64_t* sh64, int32_t* overflow_out,
-                     hipStream_t stream) {
+                     hipStream_t stream, const int32_t* e_total = nullptr,
+                     int32_t* status = nullptr) {
   (void)pos_v;
   const G* cell = (const G*)cell_v;
   const GridDev g = grid_dev(plan);
   const GridWs w = grid_ws_layout<G>(n, plan->n_bins);
   XNN_REQUIRE(w.total <= plan->workspace_bytes, "workspace smaller than the plan's");
   int32_t* counts = ws_at<int32_t>(ws, w.counts);
-  int32_t* overflow = overflow_out ? overflow_out : ws_at<int32_t>(ws, w.overflow);
-  hipLaunchKernelGGL(zero_fill_state_kernel, dim3(grid_1d(n + 1, 256)), dim3(256), 0, stream,
-                     counts, n + 1, overflow);
+  int32_t* ws_overflow = ws_at<int32_t>(ws, w.overflow);
+  int32_t* overflow = overflow_out ? overflow_out : ws_overflow;
+  // the workspace's shift-overflow flag was cleared by the count step; a caller's flag is
+  // cleared here
+  if (overflow_out != nullptr)
+    hipLaunchKernelGGL(zero_fill_state_kernel, dim3(1), dim3(64), 0, stream, counts, (int64_t)0,
+                       overflow_out);
   hipLaunchKernelGGL((cell_search_kernel<G, true>),
                      dim3(plan->n_bins, search_split(n, plan->n_bins)), dim3(256), 0, stream,
                      ws_at<G>(ws, w.wpos_s), ws_at<int32_t>(ws, w.offs_s),
                      ws_at<int32_t>(ws, w.atom_sorted), ws_at<int32_t>(ws, w.bin_start), cell, g,
                      (G)cutoff, self_interaction, counts, row_ptr, src, dst, shift, ei64, sh64,
-                     n_edges, overflow);
+                     n_edges, overflow, e_total, status, ws_overflow + 3);
   XNN_LAUNCH_CHECK();
   return XNN_OK;
 }
@@ -946,6 +1018,37 @@ int xnn_radius_graph_fill(int geom_dtype, const void* pos, int64_t n_nodes, cons
     return grid_fill<double>(pos, n_nodes, cell, cutoff, self_interaction, plan, workspace,
                              row_ptr, n_edges, src, dst, shift, edge_index64, shifts64, overflow,
                              as_hip(stream));
+  set_error("unsupported geometry dtype %d", geom_dtype);
+  return XNN_EINVAL;
+}
+
+int xnn_radius_graph_fill_capacity(int geom_dtype, const void* pos, int64_t n_nodes,
+                                   const void* cell, double cutoff, int32_t self_interaction,
+                                   const xnn_grid_plan* plan, void* workspace,
+                                   const int32_t* row_ptr, int64_t capacity,
+                                   int64_t* edge_index64, int64_t* shifts64, int32_t* status,
+                                   xnn_stream_t stream) {
+  XNN_REQUIRE(plan && row_ptr, "NULL plan or row_ptr");
+  XNN_REQUIRE(capacity >= 0, "negative capacity");
+  if (n_nodes == 0) {
+    if (status != nullptr) {
+      hipLaunchKernelGGL(zero_i32_kernel, dim3(1), dim3(64), 0, as_hip(stream), status,
+                         (int64_t)2);
+      XNN_LAUNCH_CHECK();
+    }
+    return XNN_OK;
+  }
+  XNN_REQUIRE(pos && workspace, "NULL input");
+  XNN_REQUIRE(capacity == 0 || (edge_index64 && shifts64), "NULL output");
+  XNN_REQUIRE(plan->has_cell == 0 || cell != nullptr, "the plan has a cell: pass it");
+  if (geom_dtype == XNN_F32)
+    return grid_fill<float>(pos, n_nodes, cell, cutoff, self_interaction, plan, workspace, row_ptr,
+                            capacity, nullptr, nullptr, nullptr, edge_index64, shifts64, nullptr,
+                            as_hip(stream), row_ptr + n_nodes, status);
+  if (geom_dtype == XNN_F64)
+    return grid_fill<double>(pos, n_nodes, cell, cutoff, self_interaction, plan, workspace,
+                             row_ptr, capacity, nullptr, nullptr, nullptr, edge_index64, shifts64,
+                             nullptr, as_hip(stream), row_ptr + n_nodes, status);
   set_error("unsupported geometry dtype %d", geom_dtype);
   return XNN_EINVAL;
 }

@@ -273,7 +273,10 @@ def _radius_graph_cuda(pos: Tensor, cutoff: float, cell: Optional[Tensor], pbc: 
     """The HIP cell list. The host reads the device twice at most: the atoms' bounds and the
     cell (to plan the grid), then the edge count (to size the outputs). A fully periodic
     cell's grid depends on the cell alone (positions are wrapped into it), so for the same,
-    unchanged cell tensor the plan is reused and the edge count is the only read."""
+    unchanged cell tensor the plan is reused and the outputs are sized from the last list
+    of that plan with some room: the count pass, the fill (which reads the count on the
+    device) and one read of the count and the non-finite flag run back to back, and only a
+    list that outgrew the room is filled again."""
     lib = _lib.load()
     dev = pos.device
     pos = pos.contiguous()
@@ -290,8 +293,9 @@ def _radius_graph_cuda(pos: Tensor, cutoff: float, cell: Optional[Tensor], pbc: 
         if hit is not None and not (hit[0]() is cell and hit[1] == cell._version):
             hit = None
     if hit is not None:
-        _, _, plan, cell_dev, ws = hit
+        _, _, plan, cell_dev, ws, last = hit
     else:
+        last = None
         cell_dev = (None if molecular
                     else cell.reshape(3, 3).detach().to(device=dev, dtype=pos.dtype).contiguous())
         # the atoms' bounds (fractional for a cell) and the cell itself in one launch and
@@ -316,7 +320,8 @@ def _radius_graph_cuda(pos: Tensor, cutoff: float, cell: Optional[Tensor], pbc: 
                                              (_lib.dbl * 3)(*lo_hi[3:]), ctypes.byref(plan)))
         ws = torch.empty(max(1, int(plan.workspace_bytes)), dtype=torch.uint8, device=dev)
         if not molecular and all(pbc_list) and isinstance(cell, Tensor):
-            _PERIODIC_PLANS[key] = (weakref.ref(cell), cell._version, plan, cell_dev, ws)
+            last = [-1]
+            _PERIODIC_PLANS[key] = (weakref.ref(cell), cell._version, plan, cell_dev, ws, last)
     row_ptr = torch.empty(n + 1, dtype=torch.int32, device=dev)
     status = torch.empty(2, dtype=torch.int32, device=dev)
     geom = _lib.dtype_code(pos.dtype)
@@ -325,11 +330,25 @@ def _radius_graph_cuda(pos: Tensor, cutoff: float, cell: Optional[Tensor], pbc: 
 
     _lib.call("xnn_radius_graph_count", geom, _lib.ptr(pos), n, _lib.ptr(cell_dev), float(cutoff),
               si, ctypes.byref(plan), _lib.ptr(ws), _lib.ptr(row_ptr), s)
-    _lib.call("xnn_radius_graph_status", geom, n, ctypes.byref(plan), _lib.ptr(ws),
-              _lib.ptr(row_ptr), _lib.ptr(status), s)
+    cap = -1
+    if last is not None and last[0] >= 0:
+        # room for the last list of this plan plus 5 % (atoms drift between MD steps)
+        cap = last[0] + last[0] // 20 + 64
+        ei_buf = torch.empty(2 * cap, dtype=torch.long, device=dev)
+        sh_buf = torch.empty(3 * cap, dtype=torch.long, device=dev)
+        _lib.call("xnn_radius_graph_fill_capacity", geom, _lib.ptr(pos), n, _lib.ptr(cell_dev),
+                  float(cutoff), si, ctypes.byref(plan), _lib.ptr(ws), _lib.ptr(row_ptr), cap,
+                  _lib.ptr(ei_buf), _lib.ptr(sh_buf), _lib.ptr(status), s)
+    else:
+        _lib.call("xnn_radius_graph_status", geom, n, ctypes.byref(plan), _lib.ptr(ws),
+                  _lib.ptr(row_ptr), _lib.ptr(status), s)
     n_edges, nonfinite = status.tolist()
     if nonfinite:
         raise ValueError("the positions are not finite (an unstable simulation?)")
+    if last is not None:
+        last[0] = n_edges
+    if 0 <= n_edges <= cap:
+        return ei_buf[:2 * n_edges].view(2, n_edges), sh_buf[:3 * n_edges].view(n_edges, 3)
     edge_index = torch.empty((2, n_edges), dtype=torch.long, device=dev)
     cell_shifts = torch.empty((n_edges, 3), dtype=torch.long, device=dev)
     _lib.call("xnn_radius_graph_fill", geom, _lib.ptr(pos), n, _lib.ptr(cell_dev), float(cutoff),
