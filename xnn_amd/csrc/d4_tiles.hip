@@ -31,6 +31,7 @@
 // them in slot order, so a call repeats bit for bit (no atomics). Positions and cells in
 // Angstrom, lengths inside the kernels in bohr, all float64.
 #include <algorithm>
+#include <initializer_list>
 #include <cmath>
 #include <cstdint>
 
@@ -994,15 +995,31 @@ __global__ void d4_image_counts_kernel(const double* __restrict__ cell,
 // components. The 8 waves of a block share 64 outputs (64 consecutive places of one
 // component): wave w sums the slots w, w + 8, ... in order and wave 0 adds the waves' sums
 // in wave order. A structure larger than max_atoms (more tiles than slots) gives NaN.
+// The slot sums of up to three partial arrays in one launch: grid row y belongs to target q
+// with y0[q] <= y < y0[q + 1], component k = k0 + (y - y0[q]) of its partial array (np
+// components) into out[i * nk + (k - k0)]. Per atom the slots are added in slot order.
+struct ReduceTarget {
+  const double* partial;
+  double* out;
+  int np, k0, nk;
+};
+struct ReduceTargets {
+  ReduceTarget t[3];
+  int y0[4];
+  int n;
+};
+
 __global__ __launch_bounds__(kT * kRedWaves) void d4_tiles_reduce_kernel(
-    const double* __restrict__ partial, int64_t n_nodes, int np, int k0, int nk,
-    const int32_t* __restrict__ order, const int32_t* __restrict__ batch,
-    const int64_t* __restrict__ node_ptr, int max_nt, double* __restrict__ out) {
+    ReduceTargets R, int64_t n_nodes, const int32_t* __restrict__ order,
+    const int32_t* __restrict__ batch, const int64_t* __restrict__ node_ptr, int max_nt) {
   __shared__ double red[kRedWaves][kT];
   const int lane = threadIdx.x % kT;
   const int wv = __builtin_amdgcn_readfirstlane((int)(threadIdx.x / kT));
+  const int y = (int)blockIdx.y;
+  const int q = y < R.y0[1] ? 0 : (y < R.y0[2] ? 1 : 2);   // uniform
+  const ReduceTarget T = R.t[q];
   const int64_t p = (int64_t)blockIdx.x * kT + lane;
-  const int k = k0 + (int)blockIdx.y;
+  const int k = T.k0 + (y - R.y0[q]);
   const bool live = p < n_nodes;
   double s = 0.0;
   int nt = 0;
@@ -1011,8 +1028,8 @@ __global__ __launch_bounds__(kT * kRedWaves) void d4_tiles_reduce_kernel(
     i = std::min<int64_t>(std::max<int64_t>(order[p], 0), n_nodes - 1);
     const int b = batch[i];
     nt = (int)((node_ptr[b + 1] - node_ptr[b] + kT - 1) / kT);
-    const double* src = partial + (int64_t)k * n_nodes + p;
-    const int64_t stride = (int64_t)np * n_nodes;
+    const double* src = T.partial + (int64_t)k * n_nodes + p;
+    const int64_t stride = (int64_t)T.np * n_nodes;
     const int ns = std::min(nt, max_nt);
     for (int slot = wv; slot < ns; slot += kRedWaves) s += src[slot * stride];
   }
@@ -1022,7 +1039,7 @@ __global__ __launch_bounds__(kT * kRedWaves) void d4_tiles_reduce_kernel(
     double t = red[0][lane];
 #pragma unroll
     for (int w = 1; w < kRedWaves; ++w) t += red[w][lane];
-    out[i * nk + (k - k0)] = nt > max_nt ? __builtin_nan("") : t;
+    T.out[i * T.nk + (k - T.k0)] = nt > max_nt ? __builtin_nan("") : t;
   }
 }
 
@@ -1108,12 +1125,22 @@ void launch_order(const double* pos, int64_t n_nodes, const int64_t* node_ptr, i
   build_plan(pos, n_nodes, node_ptr, n_graphs, cell, images, w.order, w.tile_ptr, s);
 }
 
-void launch_reduce(const double* partial, int64_t n_nodes, int np, int k0, int nk, const TilesWs& w,
-                   const int32_t* batch, const int64_t* node_ptr, double* out, hipStream_t s) {
-  if (out == nullptr) return;
-  hipLaunchKernelGGL(d4_tiles_reduce_kernel, dim3((unsigned)((n_nodes + kT - 1) / kT), nk),
-                     dim3(kT * kRedWaves), 0, s, partial, n_nodes, np, k0, nk, w.order, batch,
-                     node_ptr, w.max_nt, out);
+// the targets with an output, in one launch
+void launch_reduce(std::initializer_list<ReduceTarget> targets, int64_t n_nodes, const TilesWs& w,
+                   const int32_t* batch, const int64_t* node_ptr, hipStream_t s) {
+  ReduceTargets R{};
+  int rows = 0;
+  for (const ReduceTarget& t : targets) {
+    if (t.out == nullptr) continue;
+    R.t[R.n] = t;
+    R.y0[R.n] = rows;
+    rows += t.nk;
+    ++R.n;
+  }
+  for (int q = R.n; q < 4; ++q) R.y0[q] = rows;
+  if (rows == 0) return;
+  hipLaunchKernelGGL(d4_tiles_reduce_kernel, dim3((unsigned)((n_nodes + kT - 1) / kT), rows),
+                     dim3(kT * kRedWaves), 0, s, R, n_nodes, w.order, batch, node_ptr, w.max_nt);
 }
 
 dim3 tiles_grid(const TilesWs& w) { return dim3((unsigned)w.grid_tiles, (unsigned)w.max_nt); }
@@ -1155,8 +1182,8 @@ int xnn_d4_coordination(const double* pos, int64_t n_nodes, const int32_t* speci
   hipLaunchKernelGGL((d4_cn_tiles_kernel<false, false>), tiles_grid(w), dim3(kT), 0, s, pos,
                      species, node_ptr, n_graphs, cell, images, rcov, en, p, nullptr, nullptr,
                      w.order, w.tile_ptr, n_nodes, w.max_nt, w.partial);
-  launch_reduce(w.partial, n_nodes, 2, 0, 1, w, batch, node_ptr, cn_d4, s);
-  launch_reduce(w.partial, n_nodes, 2, 1, 1, w, batch, node_ptr, cn_raw, s);
+  launch_reduce({{w.partial, cn_d4, 2, 0, 1}, {w.partial, cn_raw, 2, 1, 1}}, n_nodes, w, batch,
+                node_ptr, s);
   XNN_LAUNCH_CHECK();
   return XNN_OK;
 }
@@ -1189,8 +1216,8 @@ int xnn_d4_coordination_backward(const double* pos, int64_t n_nodes, const int32
   hipLaunchKernelGGL(k, tiles_grid(w), dim3(kT), 0, s, pos, species, node_ptr, n_graphs, cell,
                      images, rcov, en, p, g_cn_d4, g_cn_raw, w.order, w.tile_ptr, n_nodes,
                      w.max_nt, w.partial);
-  launch_reduce(w.partial, n_nodes, np, 0, 3, w, batch, node_ptr, grad_pos, s);
-  if (with_cell) launch_reduce(w.partial, n_nodes, np, 3, 9, w, batch, node_ptr, cell_partial, s);
+  launch_reduce({{w.partial, grad_pos, np, 0, 3}, {w.partial, cell_partial, np, 3, 9}}, n_nodes, w,
+                batch, node_ptr, s);
   XNN_LAUNCH_CHECK();
   return XNN_OK;
 }
@@ -1218,7 +1245,7 @@ int xnn_d4_two_body(const double* pos, int64_t n_nodes, const int32_t* species,
   hipLaunchKernelGGL((d4_pair_tiles_kernel<false, false>), tiles_grid(w), dim3(kT), 0, s, pos,
                      species, node_ptr, n_graphs, cell, images, r4r2, alpha, p, nullptr, w.order,
                      w.tile_ptr, n_nodes, w.max_nt, w.partial, nullptr, nullptr);
-  launch_reduce(w.partial, n_nodes, 1, 0, 1, w, batch, node_ptr, e2, s);
+  launch_reduce({{w.partial, e2, 1, 0, 1}}, n_nodes, w, batch, node_ptr, s);
   XNN_LAUNCH_CHECK();
   return XNN_OK;
 }
@@ -1252,9 +1279,9 @@ int xnn_d4_two_body_backward(const double* pos, int64_t n_nodes, const int32_t* 
   hipLaunchKernelGGL(k, tiles_grid(w), dim3(kT), 0, s, pos, species, node_ptr, n_graphs, cell,
                      images, r4r2, alpha, p, g_e2, w.order, w.tile_ptr, n_nodes, w.max_nt,
                      w.partial, w.fsum, w.partial_alpha);
-  launch_reduce(w.partial, n_nodes, np, 0, 3, w, batch, node_ptr, grad_pos, s);
-  if (with_cell) launch_reduce(w.partial, n_nodes, np, 3, 9, w, batch, node_ptr, cell_partial, s);
-  launch_reduce(w.partial_alpha, n_nodes, kNW, 0, kNW, w, batch, node_ptr, grad_alpha, s);
+  launch_reduce({{w.partial, grad_pos, np, 0, 3}, {w.partial, cell_partial, np, 3, 9},
+                 {w.partial_alpha, grad_alpha, kNW, 0, kNW}},
+                n_nodes, w, batch, node_ptr, s);
   XNN_LAUNCH_CHECK();
   return XNN_OK;
 }

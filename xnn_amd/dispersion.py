@@ -176,7 +176,8 @@ def _cn_setup(ctx, inputs, output):
 
 def _cn_backward(ctx, g_cn, g_raw):
     if torch.is_grad_enabled():
-        raise RuntimeError("the D4 kernels are differentiable once (use_fast=False for more)")
+        raise RuntimeError("the D4 kernels are differentiable once (forces and stress); a "
+                           "second derivative through the dispersion term has no GPU path")
     pos, cell, species, batch32, node_ptr, images, plan, rcov, en = ctx.saved_tensors
     dev, n, b = pos.device, pos.shape[0], node_ptr.shape[0] - 1
     grad_pos = torch.empty((n, 3), dtype=torch.float64, device=dev)
@@ -234,7 +235,8 @@ def _pair_setup(ctx, inputs, output):
 
 def _pair_backward(ctx, g_e2):
     if torch.is_grad_enabled():
-        raise RuntimeError("the D4 kernels are differentiable once (use_fast=False for more)")
+        raise RuntimeError("the D4 kernels are differentiable once (forces and stress); a "
+                           "second derivative through the dispersion term has no GPU path")
     pos, cell, alpha, species, batch32, node_ptr, images, plan, r4r2 = ctx.saved_tensors
     dev, n, b = pos.device, pos.shape[0], node_ptr.shape[0] - 1
     grad_pos = torch.empty((n, 3), dtype=torch.float64, device=dev)
@@ -336,7 +338,8 @@ def _alpha_setup(ctx, inputs, output):
 
 def _alpha_backward(ctx, g_alpha):
     if torch.is_grad_enabled():
-        raise RuntimeError("the D4 kernels are differentiable once (use_fast=False for more)")
+        raise RuntimeError("the D4 kernels are differentiable once (forces and stress); a "
+                           "second derivative through the dispersion term has no GPU path")
     z, cn, q, nref, ngw, refcn, refq, zeff, gi, refalpha = ctx.saved_tensors
     n = cn.shape[0]
     g_cn = torch.empty_like(cn) if ctx.needs_input_grad[1] else None
@@ -427,7 +430,8 @@ def _atm_setup(ctx, inputs, output):
 
 def _atm_backward(ctx, g_energy):
     if torch.is_grad_enabled():
-        raise RuntimeError("the ATM kernels are differentiable once (use_fast=False for more)")
+        raise RuntimeError("the ATM kernels are differentiable once (forces and stress); a "
+                           "second derivative through the dispersion term has no GPU path")
     plan, vec, fa, fb, species, table = ctx.saved_tensors
     params, n_atoms, max_tiles, has_repeats = ctx.meta
     dev = vec.device
