@@ -12,8 +12,9 @@
 // divided by the message divisor; row(e) = weight_index[e] or e.
 //
 // Work is split by (node, node-feature block): a wave owns one block of the node rows
-// (degree l1) for one node, or for two nodes (one per half-wave) when the block has at most
-// 32 channels, and its lanes the channels u. Per edge it reads the sender's block and the
+// (degree l1) for one node, its lanes the channels u; when the block has at most 32
+// channels, each half-wave takes every other edge of the node's row and the halves' sums
+// are added at the end. Per edge it reads the sender's block and the
 // edge's harmonics once and expands every path that reads the block: the paths of a block
 // differ only in (l2, l3), whose combinations for a given l1 are few and known at compile
 // time, so the code for each l1 (and largest l2) unrolls all of them, keeps their sums in
@@ -34,6 +35,7 @@
 #include "cg_tables.h"
 #include "common.h"
 #include "device.h"
+#include "fork_join.h"
 
 namespace xnn {
 
@@ -129,31 +131,41 @@ __device__ __forceinline__ int64_t conv_row(const ConvView& V, int64_t e) {
   return V.widx ? (int64_t)V.widx[e] : e;
 }
 
-// The nodes of a wave: one (channels in chunks of 64) or two (32 lanes each).
+// The lanes of a wave on its node: all 64 over the channels (in chunks of 64), or, for a
+// block of at most 32 channels, two halves of 32 over the channels, each half walking every
+// other edge of the node's row (twice the independent gathers in flight per wave; the two
+// halves' sums are added once per node).
 struct ConvLanes {
-  int64_t node;      // this lane's node (>= n_nodes: no work)
-  int sub;           // lane within its node's group
+  int64_t node;      // the wave's node (>= n_nodes: no work)
+  int sub;           // lane within its half (split) or the wave
   int width;         // channels per chunk (64 or 32)
-  int32_t q0, len;   // this lane's node's CSR range
-  int32_t trips;     // uniform: the longest range of the wave
+  int half;          // split: the half (0 or 1) whose edges are 2 it + half; else 0
+  int step;          // edges per trip: 2 (split) or 1
+  int32_t q0, len;   // the node's CSR range
+  int32_t trips;     // uniform: trips over the row
 };
 
-__device__ __forceinline__ ConvLanes conv_lanes(const ConvView& V, int64_t group, bool pair,
+__device__ __forceinline__ ConvLanes conv_lanes(const ConvView& V, int64_t group, bool split,
                                                 int lane) {
   ConvLanes L;
-  L.width = pair ? 32 : kWave;
-  L.sub = pair ? (lane & 31) : lane;
-  L.node = pair ? 2 * group + (lane >> 5) : group;
+  L.width = split ? 32 : kWave;
+  L.sub = split ? (lane & 31) : lane;
+  L.half = split ? (lane >> 5) : 0;
+  L.step = split ? 2 : 1;
+  L.node = group;
   L.q0 = 0;
   L.len = 0;
   if (L.node < V.n_nodes) {
     L.q0 = V.ptr[L.node];
     L.len = V.ptr[L.node + 1] - L.q0;
   }
-  int32_t t = L.len;
-  if (pair) t = std::max(__builtin_amdgcn_readlane(L.len, 0), __builtin_amdgcn_readlane(L.len, 32));
-  L.trips = __builtin_amdgcn_readfirstlane(t);
+  L.trips = __builtin_amdgcn_readfirstlane((L.len + L.step - 1) / L.step);
   return L;
+}
+
+// a split wave's two halves added (every lane gets the node's total); unchanged otherwise
+__device__ __forceinline__ float conv_halves_sum(float v, bool split) {
+  return split ? add_xor32(v) : v;
 }
 
 // sum over the lanes of one node's group (32 or 64 lanes), on every lane of the group: DPP
@@ -184,9 +196,10 @@ struct ConvEdge {
 
 __device__ __forceinline__ ConvEdge conv_edge(const ConvView& V, const ConvLanes& L, int32_t it,
                                               const int32_t* other_of) {
-  ConvEdge E{0, 0, -1, it < L.len, false};
+  const int32_t k = it * L.step + L.half;
+  ConvEdge E{0, 0, -1, k < L.len, false};
   if (E.on) {
-    const int32_t q = L.q0 + it;
+    const int32_t q = L.q0 + k;
     E.e = V.perm ? (int64_t)V.perm[q] : (int64_t)q;
     E.other = other_of[E.e];
     E.row = conv_row(V, E.e);
@@ -279,7 +292,9 @@ __device__ __forceinline__ void conv_fwd_block(const ConvView& V, const ConvBloc
       XNN_CG_TRIPLES(XNN_CONV_COMBO)
 #undef XNN_CONV_COMBO
     }
-    if (chan && L.node < V.n_nodes) {
+#pragma unroll
+    for (int k = 0; k < NA; ++k) acc[k] = conv_halves_sum(acc[k], L.step == 2);
+    if (chan && L.half == 0 && L.node < V.n_nodes) {
       float* o = V.out + L.node * V.dout;
 #define XNN_CONV_STORE(P1_, P2_, P3_)                                                     \
   if constexpr (P1_ == L1 && P2_ <= LS) {                                                 \
@@ -440,7 +455,9 @@ __device__ __forceinline__ void conv_bwd_node_block(const ConvView& V, const Con
 #undef XNN_CONV_NODE
       }
     }
-    if (chan && L.node < V.n_nodes) {
+#pragma unroll
+    for (int a = 0; a < D1; ++a) acc[a] = conv_halves_sum(acc[a], L.step == 2);
+    if (chan && L.half == 0 && L.node < V.n_nodes) {
 #pragma unroll
       for (int a = 0; a < D1; ++a) V.out[L.node * V.d1 + B.off1 + u * D1 + a] = acc[a];
     }
@@ -466,11 +483,11 @@ __global__ __launch_bounds__(kConvWaves * kWave) void uvu_conv_kernel(ConvArgs K
   const int64_t w = (int64_t)blockIdx.x * kConvWaves + wave_in_block();
   const int blk = K.ids[w % K.n_ids];
   const ConvBlock B = K.blocks[blk];
-  const bool pair = B.mul <= 32;
+  const bool split = B.mul <= 32;
   const int64_t group = w / K.n_ids;
-  if (group * (pair ? 2 : 1) >= V.n_nodes) return;
-  const ConvLanes L = conv_lanes(V, group, pair, threadIdx.x % kWave);
-  conv_pass<PASS, L1, LS>(V, B, L, pair, blk);
+  if (group >= V.n_nodes) return;
+  const ConvLanes L = conv_lanes(V, group, split, threadIdx.x % kWave);
+  conv_pass<PASS, L1, LS>(V, B, L, split, blk);
 }
 
 // ------------------------------------------------------------------ host
@@ -570,12 +587,25 @@ static int conv_launch_l1(ConvArgs& A, hipStream_t stream) {
 }
 
 template <int PASS>
-static int conv_launch(const ConvArgs& args, hipStream_t stream) {
+static int conv_launch_serial(const ConvArgs& args, hipStream_t stream) {
   ConvArgs A = args;
   int rc = conv_launch_l1<PASS, 0>(A, stream);
   if (rc == XNN_OK) rc = conv_launch_l1<PASS, 1>(A, stream);
   if (rc == XNN_OK) rc = conv_launch_l1<PASS, 2>(A, stream);
   if (rc == XNN_OK) rc = conv_launch_l1<PASS, 3>(A, stream);
+  return rc;
+}
+
+// The launches of the node-block degrees are independent (distinct blocks of the node
+// rows, distinct output columns and weight columns): degree l goes to stream si[l] of the
+// fork.
+template <int PASS>
+static int conv_launch(const ConvArgs& args, ForkJoin& fj, const int (&si)[4]) {
+  ConvArgs A = args;
+  int rc = conv_launch_l1<PASS, 0>(A, fj.stream(si[0]));
+  if (rc == XNN_OK) rc = conv_launch_l1<PASS, 1>(A, fj.stream(si[1]));
+  if (rc == XNN_OK) rc = conv_launch_l1<PASS, 2>(A, fj.stream(si[2]));
+  if (rc == XNN_OK) rc = conv_launch_l1<PASS, 3>(A, fj.stream(si[3]));
   return rc;
 }
 
@@ -608,7 +638,10 @@ int xnn_uvu_conv(const float* node_feats, int64_t n_nodes, int32_t dim1, const f
   A.v.ptr = ptr_dst;
   A.v.perm = perm_dst;
   A.v.out = out;
-  return conv_launch<kConvForward>(A, as_hip(stream));
+  ForkJoin fj(as_hip(stream));
+  const int rc2 = conv_launch<kConvForward>(A, fj, {0, 1, 2, 3});
+  XNN_HIP_CHECK(fj.join());
+  return rc2;
 }
 
 int xnn_uvu_conv_backward(const float* node_feats, int64_t n_nodes, int32_t dim1,
@@ -630,6 +663,9 @@ int xnn_uvu_conv_backward(const float* node_feats, int64_t n_nodes, int32_t dim1
   XNN_REQUIRE(n_edges == 0 || (node_feats && edge_attrs && weights && src), "NULL input");
   A.v.g_out = grad_out;
   const hipStream_t s = as_hip(stream);
+  // the edge part (receivers) and the node part (senders) write different outputs: all of
+  // their launches run side by side; the d Y finish follows the edge part on its stream
+  ForkJoin fj(s);
   if ((grad_edge_attrs || grad_weights) && n_edges > 0) {
     XNN_REQUIRE(ptr_dst, "NULL receiver CSR");
     ConvArgs B = A;
@@ -642,11 +678,12 @@ int xnn_uvu_conv_backward(const float* node_feats, int64_t n_nodes, int32_t dim1
                   "workspace of %zu bytes needed (xnn_uvu_conv_workspace_bytes)", need);
       B.v.parts = static_cast<float*>(workspace);
     }
-    const int rc2 = conv_launch<kConvEdgePart>(B, s);
+    // the edge part in order on one side stream (the d Y finish reads every block's share)
+    const int rc2 = conv_launch_serial<kConvEdgePart>(B, fj.stream(1));
     if (rc2 != XNN_OK) return rc2;
     if (grad_edge_attrs) {
       hipLaunchKernelGGL(uvu_conv_dy_finish, dim3((unsigned)grid_1d(n_edges * dim2, 256)),
-                         dim3(256), 0, s, B, grad_edge_attrs);
+                         dim3(256), 0, fj.stream(1), B, grad_edge_attrs);
       XNN_LAUNCH_CHECK();
     }
   }
@@ -656,8 +693,10 @@ int xnn_uvu_conv_backward(const float* node_feats, int64_t n_nodes, int32_t dim1
     B.v.ptr = ptr_src;
     B.v.perm = perm_src;
     B.v.out = grad_node_feats;
-    return conv_launch<kConvNodePart>(B, s);
+    const int rc3 = conv_launch<kConvNodePart>(B, fj, {0, 2, 3, 0});
+    if (rc3 != XNN_OK) return rc3;
   }
+  XNN_HIP_CHECK(fj.join());
   return XNN_OK;
 }
 
