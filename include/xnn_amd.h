@@ -347,15 +347,19 @@ int xnn_uvu_conv(const float* node_feats, int64_t n_nodes, int32_t dim1, const f
                  const int32_t* ptr_dst, const int32_t* perm_dst, const xnn_uvu_path* paths,
                  int32_t n_paths, float* out, int32_t dim_out, xnn_stream_t stream);
 
-/* Workspace of xnn_uvu_conv_backward when it forms grad_edge_attrs: one float per edge,
- * node block and edge-attribute column. */
+/* Workspace of xnn_uvu_conv_backward when it forms grad_edge_attrs or grad_node_feats:
+ * one float per edge, node block and edge-attribute column (the blocks' shares of d Y),
+ * then one float per edge and node-row column up to the last column a path reads (each
+ * edge's share of d h at its sender). */
 size_t xnn_uvu_conv_workspace_bytes(int64_t n_edges, int32_t dim2, const xnn_uvu_path* paths,
                                     int32_t n_paths);
 
-/* Gradients of xnn_uvu_conv from grad_out (N, dim_out), each output nullable:
- * grad_node_feats (N, dim1) over the sender CSR (ptr_src, perm_src; node blocks that no
- * path reads are not written), grad_edge_attrs (E, dim2) and grad_weights (E, dim_w), per
- * edge, over the receiver CSR (the caller sums the rows of shared weights). */
+/* Gradients of xnn_uvu_conv from grad_out (N, dim_out), each output nullable. One walk
+ * over the receiver CSR gives grad_edge_attrs (E, dim2), grad_weights (E, dim_w) per edge
+ * (the caller sums the rows of shared weights) and each edge's share of d h; grad_node_feats
+ * (N, dim1) is then the sum of those shares over the sender CSR (ptr_src, perm_src), in row
+ * order (columns past the last one a path reads are not written; gaps between the path-read
+ * blocks get zeros). */
 int xnn_uvu_conv_backward(const float* node_feats, int64_t n_nodes, int32_t dim1,
                           const float* edge_attrs, int32_t dim2, const float* weights,
                           int64_t n_weight_rows, int32_t dim_w, const int32_t* weight_index,

@@ -22,13 +22,15 @@
 // combinations the tensor product does not have. The second operand's blocks must have
 // distinct degrees (one block per l2, as the harmonics have).
 //
-// xnn_uvu_conv_backward, given d out, over the same waves:
-//   edge part (receivers): d w[e, p, u] per edge (the caller sums the rows of shared
-//   weights) and the channel sums of each block's share of d Y[e], kept per block in the
-//   workspace and added up by a last pass;
-//   node part (senders): d h[s, block, u, a] =
-//     sum_{p reads block} c_p sum_{e: src(e) = s} w[row(e), p, u]
-//                         sum_{b, k} C[a, b, k] Y[e, b] d out[dst(e), p, u, k].
+// xnn_uvu_conv_backward, given d out, over the same waves and the receivers' rows (each
+// receiver's d out read once):
+//   d w[e, p, u] per edge (the caller sums the rows of shared weights);
+//   the channel sums of each block's share of d Y[e], kept per block in the workspace and
+//   added up by a last pass;
+//   each edge's share of d h at its sender, d h_e[block, u, a] =
+//     sum_{p reads block} c_p w[row(e), p, u] sum_{b, k} C[a, b, k] Y[e, b] d out[dst(e), p, u, k],
+//   in the workspace in node-row layout, summed over each sender's row by a last pass
+//   (deterministic; a walk over the senders' rows would gather d out once per edge).
 #include <algorithm>
 #include <cstdint>
 
@@ -109,12 +111,15 @@ struct ConvView {
   const int32_t* widx;
   const int32_t* src;
   const int32_t* dst;
-  const int32_t* ptr;   // CSR of the walk: receivers (forward, edge part) or senders
+  const int32_t* ptr;   // CSR of the walk: the receivers
   const int32_t* perm;
   const float* g_out;   // (N, dout) backward
-  float* out;           // forward: (N, dout); node part: d h (N, d1)
+  float* out;           // forward: (N, dout)
   float* g_w;           // (E, dw) per edge
   float* parts;         // (E, n_blocks, d2): per block channel sums of d Y
+  float* dh_edge;       // (E, dh_stride): each edge's share of d h at its sender, node-row
+                        // layout (summed over the senders' rows afterwards)
+  int64_t dh_stride;
   int64_t n_nodes, n_edges, n_w_rows;
   int32_t d1, d2, dw, dout, n_blocks, ls;
   int32_t off2[kConvMaxL + 1];  // column of the edge-attribute block of degree l (< 0: none)
@@ -311,10 +316,14 @@ __device__ __forceinline__ void conv_fwd_block(const ConvView& V, const ConvBloc
 }
 
 // ------------------------------------------------------------------ backward, edge part
-template <int L1, int LS>
+// With DH, also each edge's share of d h at its sender,
+//   d h_e[u, a] = sum_p c_p w[e, p, u] sum_{b, k} C[a, b, k] Y[e, b] d out[dst(e), p, u, k],
+// from the receiver's output gradient already in registers (the receiver walk reads it once
+// per node, where a walk over the senders' rows would gather it once per edge).
+template <int L1, int LS, bool DH>
 __device__ __forceinline__ void conv_bwd_edge_block(const ConvView& V, const ConvBlock& B,
                                                     const ConvLanes& L, bool pair, int blk) {
-  constexpr int NA = combo_width(L1), NY = (LS + 1) * (LS + 1);
+  constexpr int NA = combo_width(L1), NY = (LS + 1) * (LS + 1), D1 = 2 * L1 + 1;
   for (int u0 = 0; u0 < B.mul; u0 += L.width) {
     const int u = u0 + L.sub;
     const bool chan = u < B.mul && L.node < V.n_nodes;
@@ -345,9 +354,11 @@ __device__ __forceinline__ void conv_bwd_edge_block(const ConvView& V, const Con
       if (it + 1 < L.trips) conv_fetch<L1, LS>(V, B, En, u, chan, true, F);
       Ec = En;
       En = conv_edge(V, L, it + 2, V.src);
-      float dyt[NY];
+      float dyt[NY], dh[D1];
 #pragma unroll
       for (int j = 0; j < NY; ++j) dyt[j] = -0.f;
+#pragma unroll
+      for (int a = 0; a < D1; ++a) dh[a] = 0.f;
       // a lane whose operands are not its own (no edge, channel past the block, weight row
       // out of range) writes zero weight gradients for an edge it has and adds nothing
       if (C.use) {
@@ -356,16 +367,23 @@ __device__ __forceinline__ void conv_bwd_edge_block(const ConvView& V, const Con
     constexpr int ci = combo_index(P1_, P2_, P3_), ao = combo_offset(P1_, P2_, P3_);      \
     using T = CGTable<P1_, P2_, P3_>;                                                     \
     if (B.c[ci].off_w >= 0) {                                                             \
-      float dw = -0.f, dy[2 * P2_ + 1];                                                    \
+      float dw = -0.f, dy[2 * P2_ + 1], dhp[D1];                                          \
       _Pragma("unroll") for (int j = 0; j < 2 * P2_ + 1; ++j) dy[j] = -0.f;               \
+      _Pragma("unroll") for (int a = 0; a < D1; ++a) dhp[a] = -0.f;                       \
       _Pragma("unroll") for (int n = 0; n < T::n; ++n) {                                  \
-        const float hg = T::e[n].c * C.hv[T::e[n].i] * gk[ao + T::e[n].k];                \
+        const float cg = T::e[n].c * gk[ao + T::e[n].k];                                  \
+        const float hg = cg * C.hv[T::e[n].i];                                            \
         dw += hg * C.yv[P2_ * P2_ + T::e[n].j];                                           \
         dy[T::e[n].j] += hg;                                                              \
+        if (DH) dhp[T::e[n].i] += cg * C.yv[P2_ * P2_ + T::e[n].j];                       \
       }                                                                                   \
       if (V.g_w) V.g_w[E.e * V.dw + B.c[ci].off_w + u] = B.c[ci].coef * dw;              \
+      const float sc = B.c[ci].coef * C.wv[ci];                                           \
       _Pragma("unroll") for (int j = 0; j < 2 * P2_ + 1; ++j)                             \
-          dyt[P2_ * P2_ + j] += B.c[ci].coef * C.wv[ci] * dy[j];                          \
+          dyt[P2_ * P2_ + j] += sc * dy[j];                                               \
+      if (DH) {                                                                           \
+        _Pragma("unroll") for (int a = 0; a < D1; ++a) dh[a] = fmaf(sc, dhp[a], dh[a]);   \
+      }                                                                                   \
     }                                                                                     \
   }
         XNN_CG_TRIPLES(XNN_CONV_EDGE)
@@ -378,6 +396,12 @@ __device__ __forceinline__ void conv_bwd_edge_block(const ConvView& V, const Con
   }
         XNN_CG_TRIPLES(XNN_CONV_EDGE_ZERO)
 #undef XNN_CONV_EDGE_ZERO
+      }
+      if (DH && E.on && u < B.mul) {
+        // zeros from a lane whose operands are not its own (dh stays 0)
+        float* hr = V.dh_edge + E.e * V.dh_stride + B.off1 + (int64_t)u * D1;
+#pragma unroll
+        for (int a = 0; a < D1; ++a) hr[a] = dh[a];
       }
       if (V.parts) {
         // this block's share of d Y[e], every column of the present edge blocks
@@ -410,69 +434,69 @@ __global__ void uvu_conv_dy_finish(ConvArgs K, float* __restrict__ g_y) {
   g_y[t] = v;
 }
 
-// ------------------------------------------------------------------ backward, node part
-template <int L1, int LS>
-__device__ __forceinline__ void conv_bwd_node_block(const ConvView& V, const ConvBlock& B,
-                                                    const ConvLanes& L) {
-  constexpr int D1 = 2 * L1 + 1;
-  for (int u0 = 0; u0 < B.mul; u0 += L.width) {
-    const int u = u0 + L.sub;
-    const bool chan = u < B.mul;
-    float acc[D1];
+// d h[s] = the sum of the edge shares over the sender's row, in row order; one wave per
+// node, lanes over the columns, NC chunks of 64 columns per pass: each edge's index loaded
+// once per pass and its NC loads independent, two edges in flight.
+template <int NC>
+__global__ __launch_bounds__(256) void uvu_conv_dh_sum(const float* __restrict__ dh_edge,
+                                                       int64_t stride, const int32_t* __restrict__ ptr,
+                                                       const int32_t* __restrict__ perm,
+                                                       int64_t n_nodes, float* __restrict__ out,
+                                                       int64_t out_stride) {
+  const int lane = threadIdx.x % kWave;
+  const int64_t node = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) / kWave;
+  if (node >= n_nodes) return;
+  const int32_t q0 = ptr[node], q1 = ptr[node + 1];
+  for (int64_t f0 = 0; f0 < stride; f0 += NC * kWave) {
+    float acc[NC];
+    bool in[NC];
 #pragma unroll
-    for (int a = 0; a < D1; ++a) acc[a] = 0.f;
-    ConvFetch<L1, LS> F;
-    ConvEdge Ec = conv_edge(V, L, 0, V.dst);
-    if (L.trips > 0) conv_fetch<L1, LS>(V, B, Ec, u, chan, false, F);
-    ConvEdge En = conv_edge(V, L, 1, V.dst);
-    for (int32_t it = 0; it < L.trips; ++it) {
-      const ConvFetch<L1, LS> C = F;
-      const ConvEdge E = Ec;
-      if (it + 1 < L.trips) conv_fetch<L1, LS>(V, B, En, u, chan, false, F);
-      Ec = En;
-      En = conv_edge(V, L, it + 2, V.dst);
-      // the receiver's output gradient from a valid address (channel clamped), used only
-      // by a lane whose operands are its own
-      const int us = chan ? u : 0;
-      const float* g = V.g_out + E.other * V.dout;
-      if (C.use) {
-#define XNN_CONV_NODE(P1_, P2_, P3_)                                                      \
-  if constexpr (P1_ == L1 && P2_ <= LS) {                                                 \
-    constexpr int ci = combo_index(P1_, P2_, P3_);                                        \
-    using T = CGTable<P1_, P2_, P3_>;                                                     \
-    if (B.c[ci].off_w >= 0) {                                                             \
-      float gk[2 * P3_ + 1], t[D1];                                                       \
-      _Pragma("unroll") for (int k = 0; k < 2 * P3_ + 1; ++k)                             \
-          gk[k] = g[B.c[ci].off_out + us * (2 * P3_ + 1) + k];                            \
-      _Pragma("unroll") for (int q = 0; q < D1; ++q) t[q] = -0.f;                         \
-      _Pragma("unroll") for (int n = 0; n < T::n; ++n)                                    \
-          t[T::e[n].i] += T::e[n].c * C.yv[P2_ * P2_ + T::e[n].j] * gk[T::e[n].k];        \
-      const float wv = B.c[ci].coef * C.wv[ci];                                           \
-      _Pragma("unroll") for (int q = 0; q < D1; ++q) acc[q] += wv * t[q];                 \
-    }                                                                                     \
-  }
-        XNN_CG_TRIPLES(XNN_CONV_NODE)
-#undef XNN_CONV_NODE
+    for (int c = 0; c < NC; ++c) {
+      acc[c] = 0.f;
+      in[c] = f0 + c * kWave + lane < stride;
+    }
+    int32_t q = q0;
+    for (; q + 1 < q1; q += 2) {
+      const int64_t e0 = perm ? (int64_t)perm[q] : (int64_t)q;
+      const int64_t e1 = perm ? (int64_t)perm[q + 1] : (int64_t)(q + 1);
+      const float* r0 = dh_edge + e0 * stride + f0 + lane;
+      const float* r1 = dh_edge + e1 * stride + f0 + lane;
+      float v0[NC], v1[NC];
+#pragma unroll
+      for (int c = 0; c < NC; ++c) {
+        v0[c] = in[c] ? r0[c * kWave] : 0.f;
+        v1[c] = in[c] ? r1[c * kWave] : 0.f;
       }
-    }
 #pragma unroll
-    for (int a = 0; a < D1; ++a) acc[a] = conv_halves_sum(acc[a], L.step == 2);
-    if (chan && L.half == 0 && L.node < V.n_nodes) {
-#pragma unroll
-      for (int a = 0; a < D1; ++a) V.out[L.node * V.d1 + B.off1 + u * D1 + a] = acc[a];
+      for (int c = 0; c < NC; ++c) acc[c] = (acc[c] + v0[c]) + v1[c];
     }
+    if (q < q1) {
+      const int64_t e0 = perm ? (int64_t)perm[q] : (int64_t)q;
+      const float* r0 = dh_edge + e0 * stride + f0 + lane;
+#pragma unroll
+      for (int c = 0; c < NC; ++c) acc[c] += in[c] ? r0[c * kWave] : 0.f;
+    }
+    float* o = out + node * out_stride + f0 + lane;
+#pragma unroll
+    for (int c = 0; c < NC; ++c)
+      if (in[c]) o[c * kWave] = acc[c];
   }
 }
 
+__global__ __launch_bounds__(256) void uvu_conv_zero(float* __restrict__ p, int64_t n) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = 0.f;
+}
+
 // ------------------------------------------------------------------ kernels
-enum ConvPass { kConvForward = 0, kConvEdgePart = 1, kConvNodePart = 2 };
+// the backward's edge part without (1) or with (2) the edges' shares of d h
+enum ConvPass { kConvForward = 0, kConvEdgePart = 1, kConvEdgePartDh = 2 };
 
 template <int PASS, int L1, int LS>
 __device__ __forceinline__ void conv_pass(const ConvView& V, const ConvBlock& B,
                                           const ConvLanes& L, bool pair, int blk) {
   if constexpr (PASS == kConvForward) conv_fwd_block<L1, LS>(V, B, L);
-  else if constexpr (PASS == kConvEdgePart) conv_bwd_edge_block<L1, LS>(V, B, L, pair, blk);
-  else conv_bwd_node_block<L1, LS>(V, B, L);
+  else conv_bwd_edge_block<L1, LS, PASS == kConvEdgePartDh>(V, B, L, pair, blk);
 }
 
 // One launch per node-block degree l1 (each specialization gets its own register budget):
@@ -586,16 +610,6 @@ static int conv_launch_l1(ConvArgs& A, hipStream_t stream) {
   return XNN_OK;
 }
 
-template <int PASS>
-static int conv_launch_serial(const ConvArgs& args, hipStream_t stream) {
-  ConvArgs A = args;
-  int rc = conv_launch_l1<PASS, 0>(A, stream);
-  if (rc == XNN_OK) rc = conv_launch_l1<PASS, 1>(A, stream);
-  if (rc == XNN_OK) rc = conv_launch_l1<PASS, 2>(A, stream);
-  if (rc == XNN_OK) rc = conv_launch_l1<PASS, 3>(A, stream);
-  return rc;
-}
-
 // The launches of the node-block degrees are independent (distinct blocks of the node
 // rows, distinct output columns and weight columns): degree l goes to stream si[l] of the
 // fork.
@@ -609,6 +623,42 @@ static int conv_launch(const ConvArgs& args, ForkJoin& fj, const int (&si)[4]) {
   return rc;
 }
 
+// The backward's workspace: the per-block d Y shares (E, n_blocks, d2), then the edges'
+// d h shares (E, dh_stride) with dh_stride the last node-row column a path reads.
+struct ConvWsLayout {
+  size_t parts, dh, total;
+  int64_t dh_stride;
+  bool dh_gaps;  // some columns below dh_stride are read by no path (zeroed before use)
+};
+
+static ConvWsLayout conv_ws_layout(int64_t n_edges, int32_t dim2, const xnn_uvu_path* paths,
+                                   int32_t n_paths) {
+  ConvWsLayout L{};
+  int32_t n_blocks = 0;
+  int64_t stride = 0;
+  for (int p = 0; p < n_paths; ++p) {
+    n_blocks = std::max(n_blocks, paths[p].block + 1);
+    stride = std::max<int64_t>(stride, (int64_t)paths[p].off1 +
+                                           (int64_t)paths[p].mul * (2 * paths[p].l1 + 1));
+  }
+  // columns read by some path (the blocks may leave gaps)
+  int64_t covered = 0;
+  for (int b = 0; b < n_blocks; ++b) {
+    for (int p = 0; p < n_paths; ++p) {
+      if (paths[p].block != b) continue;
+      covered += (int64_t)paths[p].mul * (2 * paths[p].l1 + 1);
+      break;
+    }
+  }
+  L.dh_stride = stride;
+  L.dh_gaps = covered != stride;
+  const auto align = [](size_t x) { return (x + 255) & ~(size_t)255; };
+  L.parts = 0;
+  L.dh = align((size_t)n_edges * (size_t)n_blocks * (size_t)dim2 * sizeof(float));
+  L.total = L.dh + (size_t)n_edges * (size_t)stride * sizeof(float);
+  return L;
+}
+
 }  // namespace xnn
 
 using namespace xnn;
@@ -618,9 +668,8 @@ extern "C" {
 size_t xnn_uvu_conv_workspace_bytes(int64_t n_edges, int32_t dim2, const xnn_uvu_path* paths,
                                     int32_t n_paths) {
   if (n_edges <= 0 || dim2 <= 0 || paths == nullptr || n_paths <= 0) return 0;
-  int32_t n_blocks = 0;
-  for (int p = 0; p < n_paths; ++p) n_blocks = std::max(n_blocks, paths[p].block + 1);
-  return (size_t)n_edges * (size_t)n_blocks * (size_t)dim2 * sizeof(float);
+  const ConvWsLayout L = conv_ws_layout(n_edges, dim2, paths, n_paths);
+  return L.total;
 }
 
 int xnn_uvu_conv(const float* node_feats, int64_t n_nodes, int32_t dim1, const float* edge_attrs,
@@ -663,40 +712,60 @@ int xnn_uvu_conv_backward(const float* node_feats, int64_t n_nodes, int32_t dim1
   XNN_REQUIRE(n_edges == 0 || (node_feats && edge_attrs && weights && src), "NULL input");
   A.v.g_out = grad_out;
   const hipStream_t s = as_hip(stream);
-  // the edge part (receivers) and the node part (senders) write different outputs: all of
-  // their launches run side by side; the d Y finish follows the edge part on its stream
-  ForkJoin fj(s);
-  if ((grad_edge_attrs || grad_weights) && n_edges > 0) {
-    XNN_REQUIRE(ptr_dst, "NULL receiver CSR");
-    ConvArgs B = A;
-    B.v.ptr = ptr_dst;
-    B.v.perm = perm_dst;
-    B.v.g_w = grad_weights;
-    if (grad_edge_attrs) {
-      const size_t need = xnn_uvu_conv_workspace_bytes(n_edges, dim2, paths, n_paths);
-      XNN_REQUIRE(workspace != nullptr && workspace_bytes >= need,
-                  "workspace of %zu bytes needed (xnn_uvu_conv_workspace_bytes)", need);
-      B.v.parts = static_cast<float*>(workspace);
+  const ConvWsLayout W = conv_ws_layout(n_edges, dim2, paths, n_paths);
+  if (grad_node_feats) {
+    XNN_REQUIRE(ptr_src && (n_edges == 0 || dst), "NULL sender CSR or receivers");
+    if (n_edges == 0) {
+      // no edge: every column of the path-read blocks is zero
+      hipLaunchKernelGGL(uvu_conv_zero, dim3((unsigned)grid_1d(n_nodes * dim1, 256)), dim3(256), 0,
+                         s, grad_node_feats, n_nodes * (int64_t)dim1);
+      XNN_LAUNCH_CHECK();
+      return XNN_OK;
     }
-    // the edge part in order on one side stream (the d Y finish reads every block's share)
-    const int rc2 = conv_launch_serial<kConvEdgePart>(B, fj.stream(1));
-    if (rc2 != XNN_OK) return rc2;
-    if (grad_edge_attrs) {
-      hipLaunchKernelGGL(uvu_conv_dy_finish, dim3((unsigned)grid_1d(n_edges * dim2, 256)),
-                         dim3(256), 0, fj.stream(1), B, grad_edge_attrs);
+  }
+  if (n_edges == 0 || !(grad_edge_attrs || grad_weights || grad_node_feats)) return XNN_OK;
+  XNN_REQUIRE(ptr_dst, "NULL receiver CSR");
+  const bool need_ws = grad_edge_attrs || grad_node_feats;
+  XNN_REQUIRE(!need_ws || (workspace != nullptr && workspace_bytes >= W.total),
+              "workspace of %zu bytes needed (xnn_uvu_conv_workspace_bytes)", W.total);
+  ConvArgs B = A;
+  B.v.ptr = ptr_dst;
+  B.v.perm = perm_dst;
+  B.v.g_w = grad_weights;
+  if (grad_edge_attrs) B.v.parts = reinterpret_cast<float*>(static_cast<char*>(workspace) + W.parts);
+  if (grad_node_feats) {
+    B.v.dh_edge = reinterpret_cast<float*>(static_cast<char*>(workspace) + W.dh);
+    B.v.dh_stride = W.dh_stride;
+    if (W.dh_gaps) {
+      hipLaunchKernelGGL(uvu_conv_zero, dim3((unsigned)grid_1d(n_edges * W.dh_stride, 256)),
+                         dim3(256), 0, s, B.v.dh_edge, n_edges * W.dh_stride);
       XNN_LAUNCH_CHECK();
     }
   }
-  if (grad_node_feats) {
-    XNN_REQUIRE(ptr_src && (n_edges == 0 || dst), "NULL sender CSR or receivers");
-    ConvArgs B = A;
-    B.v.ptr = ptr_src;
-    B.v.perm = perm_src;
-    B.v.out = grad_node_feats;
-    const int rc3 = conv_launch<kConvNodePart>(B, fj, {0, 2, 3, 0});
-    if (rc3 != XNN_OK) return rc3;
+  {
+    // one edge part over the receivers' rows (the node-block degrees side by side), then the
+    // finishes: d Y from the blocks' shares, d h from the edges' shares over the senders
+    ForkJoin fj(s);
+    const int rc2 = grad_node_feats ? conv_launch<kConvEdgePartDh>(B, fj, {0, 1, 2, 3})
+                                    : conv_launch<kConvEdgePart>(B, fj, {0, 1, 2, 3});
+    if (rc2 != XNN_OK) return rc2;
+    XNN_HIP_CHECK(fj.join());
   }
-  XNN_HIP_CHECK(fj.join());
+  if (grad_edge_attrs) {
+    hipLaunchKernelGGL(uvu_conv_dy_finish, dim3((unsigned)grid_1d(n_edges * dim2, 256)),
+                       dim3(256), 0, s, B, grad_edge_attrs);
+    XNN_LAUNCH_CHECK();
+  }
+  if (grad_node_feats) {
+    const dim3 grid((unsigned)grid_1d(n_nodes * kWave, 256));
+    if (W.dh_stride <= 4 * kWave)
+      hipLaunchKernelGGL(uvu_conv_dh_sum<4>, grid, dim3(256), 0, s, B.v.dh_edge, W.dh_stride,
+                         ptr_src, perm_src, n_nodes, grad_node_feats, (int64_t)dim1);
+    else
+      hipLaunchKernelGGL(uvu_conv_dh_sum<8>, grid, dim3(256), 0, s, B.v.dh_edge, W.dh_stride,
+                         ptr_src, perm_src, n_nodes, grad_node_feats, (int64_t)dim1);
+    XNN_LAUNCH_CHECK();
+  }
   return XNN_OK;
 }
 

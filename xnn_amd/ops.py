@@ -1070,7 +1070,8 @@ def uvu_conv_backward_op(g: Tensor, h: Tensor, y: Tensor, w: Tensor,
     gy = torch.empty((e, d2), **f32) if want_y else torch.empty(0, **f32)
     gw = torch.empty((e, dw), **f32) if want_w else torch.empty(0, **f32)
     table = _lib.uvu_paths(paths, coefs)
-    need = int(_lib.load().xnn_uvu_conv_workspace_bytes(e, d2, table, len(coefs))) if want_y else 0
+    need = (int(_lib.load().xnn_uvu_conv_workspace_bytes(e, d2, table, len(coefs)))
+            if (want_y or want_h) else 0)
     ws = torch.empty(max(need, 1), dtype=torch.uint8, device=dev) if need else None
     _lib.call("xnn_uvu_conv_backward", _lib.ptr(h), n, d1, _lib.ptr(y), d2, _lib.ptr(w),
               int(w.shape[0]), dw, _lib.ptr(weight_index), _lib.ptr(src), _lib.ptr(dst), e,
