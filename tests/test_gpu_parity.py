@@ -1346,3 +1346,29 @@ def test_every_envelope_is_zero_from_the_cutoff(basis):
             want = (R.bessel(rr.cpu(), K, rc, prefactor=(2.0 / rc) ** 0.5) if basis == "bessel"
                     else torch.exp(-gamma * (rr.cpu()[:, None] - table[None, :]) ** 2))
             torch.testing.assert_close(rad[inside].cpu(), want, rtol=1e-12, atol=1e-12)
+
+
+def test_deployment_neighbor_list_matches_the_reference_semantics():
+    """deploy.build_neighbor_list_ts (the exported artifact's neighbor list,
+    torchscript.py:124-212) on the GPU: a zero cell or no periodic flag is a molecule; a
+    cell with partial periodicity; the edge sets equal the oracle's."""
+    import oracle.nl as N
+    from oracle.nl import canonical
+    from xnn_amd import synthetic
+    from xnn_amd.deploy import build_neighbor_list_ts
+    _note("deployment neighbor list")
+    s = synthetic.water_box(n_molecules=64, box=12.4, grid=4, seed=10)
+    pos = torch.tensor(s.pos, dtype=torch.float64, device=DEV)
+    cell = torch.tensor(s.cell, dtype=torch.float64, device=DEV)
+    for pbc in ([True, True, True], [True, False, True]):
+        ei, sh = build_neighbor_list_ts(pos, 4.0, cell, torch.tensor(pbc, device=DEV))
+        ei_o, sh_o, near = N.neighbor_list(s.pos, 4.0, s.cell, np.array(pbc), dtype=np.float64,
+                                           margin=1e-7)
+        assert near == 0
+        assert np.array_equal(canonical(ei.cpu().numpy(), sh.cpu().numpy()), canonical(ei_o, sh_o))
+    for cl, pbc in ((torch.zeros(3, 3, dtype=torch.float64, device=DEV), [True, True, True]),
+                    (cell, [False, False, False])):
+        ei, sh = build_neighbor_list_ts(pos, 4.0, cl, torch.tensor(pbc, device=DEV))
+        ei_o, sh_o, near = N.neighbor_list(s.pos, 4.0, None, None, dtype=np.float64, margin=1e-7)
+        assert near == 0 and int(sh.abs().sum()) == 0
+        assert np.array_equal(canonical(ei.cpu().numpy(), sh.cpu().numpy()), canonical(ei_o, sh_o))

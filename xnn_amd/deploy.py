@@ -29,6 +29,24 @@ from .featurizers import radial_spec
 from .ops import linear_message_supported
 
 
+def build_neighbor_list_ts(pos: Tensor, cutoff: float, cell: Tensor,
+                           pbc: Tensor) -> Tuple[Tensor, Tensor]:
+    """The deployment form of the neighbor list (torchscript.py:124-212): the same arguments
+    as the exported artifact's, ``cell`` (3, 3) all zeros and / or no periodic flag for a
+    molecule, ``pbc`` (3,); returns ``(edge_index [src, dst], cell_shifts)`` with the same
+    conventions. On the GPU it is the HIP cell list (:func:`~xnn_amd.data.
+    build_neighbor_list`), O(N x neighbors) instead of the exported artifact's brute force
+    over (images, N, N), so it serves large cells too; it is a Python function, not a
+    TorchScript one (the HIP path is reached through the C ABI in a C++ engine)."""
+    from .data import build_neighbor_list
+    cell = cell.reshape(3, 3)
+    pbc = pbc.reshape(3).to(torch.bool)
+    periodic = bool(pbc.any()) and bool(torch.linalg.norm(cell.to(torch.float64), dim=1).sum() > 1e-8)
+    if not periodic:
+        return build_neighbor_list(pos, cutoff)
+    return build_neighbor_list(pos, cutoff, cell.to(pos.dtype), pbc.cpu())
+
+
 def split_dispersion(model: nn.Module) -> Tuple[Optional[nn.Module], List[nn.Module]]:
     """``(core, terms)``: the innermost model (``None`` for a standalone dispersion model)
     and the dispersion terms of every :class:`~xnn_amd.dispersion.DispersionCorrection`
