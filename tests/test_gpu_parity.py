@@ -95,6 +95,40 @@ def test_radius_graph_full_water_box_bit_exact():
     assert np.array_equal(_canon_t(e2, s2), canonical(ei, sh))
 
 
+@pytest.mark.parametrize("case", ["cluster_16384", "cluster_16385", "cluster_20000_f64",
+                                  "dilute_box_many_bins"])
+def test_radius_graph_binning_paths(case):
+    """The count step bins up to 16,384 atoms over at most 8,191 bins in one workgroup and
+    larger systems through the general scatter and sort: both, at and past the boundary,
+    against the oracle. Coordinates lie on a 1/8 A grid and the cutoff is 4.03 A, so every
+    squared distance is a multiple of 1/64 at least 0.0066 from the cutoff's square: no pair
+    lies near the cutoff."""
+    import xnn_amd as xa
+    from oracle.nl import canonical, neighbor_list
+    rng = np.random.default_rng(7)
+    rc, dtype = 4.03, (np.float64 if case.endswith("f64") else np.float32)
+    if case.startswith("cluster"):
+        n = int(case.split("_")[1])
+        side = (n / 0.1) ** (1.0 / 3.0)
+        pos, cell, pbc = np.round(rng.uniform(0, side, (n, 3)) * 8) / 8, None, None
+    else:
+        n, side = 1500, 100.0                  # 24^3 = 13,824 bins
+        pos = np.round(rng.uniform(0, side, (n, 3)) * 8) / 8
+        cell, pbc = np.eye(3) * side, [True] * 3
+    _note(f"radius_graph binning path {case} N={n}")
+    ei, sh, near = neighbor_list(pos, rc, cell, pbc, dtype=dtype, margin=1e-5)
+    assert near == 0 and ei.shape[1] > 0
+    tdt = torch.float32 if dtype == np.float32 else torch.float64
+    args = (torch.tensor(pos, dtype=tdt, device=DEV), rc)
+    kw = {} if cell is None else {"cell": torch.tensor(cell, dtype=tdt, device=DEV),
+                                  "pbc": torch.tensor(pbc)}
+    e2, s2 = xa.build_neighbor_list(*args, **kw)
+    assert np.array_equal(_canon_t(e2, s2), canonical(ei, sh))
+    assert bool((e2[1][1:] >= e2[1][:-1]).all())
+    e3, s3 = xa.build_neighbor_list(*args, **kw)
+    assert torch.equal(e2, e3) and torch.equal(s2, s3)
+
+
 def test_radius_graph_edge_cases():
     import xnn_amd as xa
     from oracle.nl import canonical, neighbor_list

@@ -31,7 +31,7 @@ constexpr int kTile = 1024;             // candidates staged in LDS per pass
 
 struct GridDev {
   int nb[3], reach[3], periodic[3], has_cell;
-  double lo[3], width[3], inv[9];
+  double lo[3], width[3], iwidth[3], inv[9];
 };
 
 static inline size_t align_up(size_t x) { return (x + 255) & ~(size_t)255; }
@@ -120,21 +120,17 @@ __device__ __host__ inline T* ws_at(void* ws, size_t off) {
 
 // ---------------------------------------------------------------- binning
 // frac = pos @ inv(cell); wrap offsets o = floor(frac) on periodic axes; wrapped
-// position wpos = pos - o @ cell (geometry dtype, as neighborlist.py:472-475).
+// position w = pos - o @ cell (geometry dtype, as neighborlist.py:472-475); the bin key from
+// the unwrapped fractional coordinate minus the offset (Cartesian without a cell), in
+// double times the inverse bin width (the bins' slack absorbs its rounding), clamped to the
+// grid.
 template <typename G>
-__global__ void bin_atoms_kernel(const G* __restrict__ pos, int64_t n, const G* __restrict__ cell,
-                                 GridDev g, int32_t* __restrict__ bin_key,
-                                 int32_t* __restrict__ atom_id, G* __restrict__ wpos,
-                                 int32_t* __restrict__ offs, int32_t* __restrict__ bin_count,
-                                 int32_t* __restrict__ nonfinite) {
-  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= n) return;
-  const G p[3] = {pos[3 * i], pos[3 * i + 1], pos[3 * i + 2]};
-  // a non-finite coordinate is flagged for the host (xnn_radius_graph_status); the atom is
-  // binned like any other (the bin index is clamped), and finds no neighbor
-  if (!(isfinite(p[0]) && isfinite(p[1]) && isfinite(p[2]))) *nonfinite = 1;
-  G w[3] = {p[0], p[1], p[2]};
-  int o[3] = {0, 0, 0};
+__device__ __forceinline__ int wrap_and_bin(const G p[3], const G* __restrict__ cell,
+                                            const GridDev& g, G w[3], int o[3]) {
+  w[0] = p[0];
+  w[1] = p[1];
+  w[2] = p[2];
+  o[0] = o[1] = o[2] = 0;
   int b[3];
   if (g.has_cell) {
     G f[3];
@@ -147,18 +143,34 @@ __global__ void bin_atoms_kernel(const G* __restrict__ pos, int64_t n, const G* 
       for (int a = 0; a < 3; ++a) w[a] = p[a] - (ox * cell[a] + oy * cell[3 + a] + oz * cell[6 + a]);
     }
     for (int a = 0; a < 3; ++a) {
-      // bin from the unwrapped fractional coordinate minus the offset, in double
       const double fa = (double)f[a] - (double)o[a];
-      int k = (int)floor((fa - g.lo[a]) / g.width[a]);
+      int k = (int)floor((fa - g.lo[a]) * g.iwidth[a]);
       b[a] = min(max(k, 0), g.nb[a] - 1);
     }
   } else {
     for (int a = 0; a < 3; ++a) {
-      int k = (int)floor(((double)p[a] - g.lo[a]) / g.width[a]);
+      int k = (int)floor(((double)p[a] - g.lo[a]) * g.iwidth[a]);
       b[a] = min(max(k, 0), g.nb[a] - 1);
     }
   }
-  const int key = (b[2] * g.nb[1] + b[1]) * g.nb[0] + b[0];
+  return (b[2] * g.nb[1] + b[1]) * g.nb[0] + b[0];
+}
+
+template <typename G>
+__global__ void bin_atoms_kernel(const G* __restrict__ pos, int64_t n, const G* __restrict__ cell,
+                                 GridDev g, int32_t* __restrict__ bin_key,
+                                 int32_t* __restrict__ atom_id, G* __restrict__ wpos,
+                                 int32_t* __restrict__ offs, int32_t* __restrict__ bin_count,
+                                 int32_t* __restrict__ nonfinite) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  const G p[3] = {pos[3 * i], pos[3 * i + 1], pos[3 * i + 2]};
+  // a non-finite coordinate is flagged for the host (xnn_radius_graph_status); the atom is
+  // binned like any other (the bin index is clamped), and finds no neighbor
+  if (!(isfinite(p[0]) && isfinite(p[1]) && isfinite(p[2]))) *nonfinite = 1;
+  G w[3];
+  int o[3];
+  const int key = wrap_and_bin(p, cell, g, w, o);
   bin_key[i] = key;
   atom_id[i] = (int32_t)i;
   wpos[4 * i + 0] = w[0];
@@ -170,6 +182,173 @@ __global__ void bin_atoms_kernel(const G* __restrict__ pos, int64_t n, const G* 
   offs[4 * i + 2] = o[2];
   offs[4 * i + 3] = key;
   atomicAdd(&bin_count[key], 1);
+}
+
+// one row of 4 (16- or 32-byte aligned) in 16-byte stores
+__device__ __forceinline__ void store_row4(float* p, float a, float b, float c, float d) {
+  *reinterpret_cast<float4*>(p) = make_float4(a, b, c, d);
+}
+__device__ __forceinline__ void store_row4(double* p, double a, double b, double c, double d) {
+  reinterpret_cast<double2*>(p)[0] = make_double2(a, b);
+  reinterpret_cast<double2*>(p)[1] = make_double2(c, d);
+}
+
+// positions of atoms (c + k) * THREADS + t, k < CHUNK, loaded together (indices past the
+// last atom clamped to it, n >= 1), so that their round trips overlap
+template <typename G, int CHUNK, int THREADS>
+__device__ __forceinline__ void load_chunk(const G* __restrict__ pos, int n, int c, int t,
+                                           G (&p)[CHUNK][3]) {
+#pragma unroll
+  for (int k = 0; k < CHUNK; ++k) {
+    const int i = min((c + k) * THREADS + t, n - 1);
+    p[k][0] = pos[3 * i];
+    p[k][1] = pos[3 * i + 1];
+    p[k][2] = pos[3 * i + 2];
+  }
+}
+
+// Sizes the count step bins in one workgroup: the bins' counts and starts and the atoms'
+// bin lists held in LDS, 4 (bins + 1) + 4 atoms bytes <= 96 KiB.
+constexpr int kOneBlockAtoms = 16384, kOneBlockBins = 8191;
+
+// The count step's whole binning in one workgroup of 1024 threads, for up to kOneBlockAtoms
+// atoms and kOneBlockBins bins (one launch where the general path takes five): the count
+// step's zeroes; every atom's wrap and bin, counted into its bin by an LDS atomic whose old
+// value is the atom's arrival in the bin; the bins' starts (exclusive scan in LDS); the bins'
+// atoms listed in arrival order; then, per list position, the atom's rank among its bin's
+// atoms of lower index (the order a stable sort by bin gives) and its sorted copies written
+// at its bin's start plus that rank. The wrap is computed again for the copies rather than
+// kept; positions are loaded 8 (float64: 4) atoms at a time so that their round trips
+// overlap.
+template <typename G>
+__global__ __launch_bounds__(1024) void bin_one_block_kernel(
+    const G* __restrict__ pos, int n, const G* __restrict__ cell, GridDev g, int nb,
+    int32_t* __restrict__ bin_start, int32_t* __restrict__ atom_sorted, G* __restrict__ wpos_s,
+    int32_t* __restrict__ offs_s, int32_t* __restrict__ counts, int32_t* __restrict__ overflow,
+    int32_t* __restrict__ row_ptr) {
+  constexpr int kThreads = 1024, kPer = kOneBlockAtoms / kThreads;
+  constexpr int kScanPer = (kOneBlockBins + 1) / kThreads;
+  constexpr int kIdBits = 14, kIdMask = (1 << kIdBits) - 1;  // atoms < 2^14, bins < 2^13
+  static_assert(kOneBlockAtoms <= (1 << kIdBits) && kOneBlockBins < (1 << (31 - kIdBits)), "packed list entries");
+  // atoms per thread whose positions are loaded together
+  constexpr int kChunk = sizeof(G) == 4 ? 8 : 4;
+  __shared__ int32_t s_start[kOneBlockBins + 1];
+  __shared__ int32_t s_list[kOneBlockAtoms];
+  __shared__ int32_t s_wsum[kThreads / kWave];
+  __shared__ int32_t s_bad;
+  const int t = threadIdx.x, lane = t % kWave, wv = t / kWave;
+  for (int b = t; b <= nb; b += kThreads) s_start[b] = 0;
+  for (int i = t; i <= n; i += kThreads) counts[i] = 0;
+  if (t == 0) {
+    s_bad = 0;
+    row_ptr[0] = 0;
+  }
+  __syncthreads();
+  // key -1: no atom (past the last one, or in a chunk the loop skips)
+  int key[kPer], arrival[kPer];
+#pragma unroll
+  for (int k = 0; k < kPer; ++k) {
+    key[k] = -1;
+    arrival[k] = 0;
+  }
+  bool bad = false;
+#pragma unroll
+  for (int c = 0; c < kPer; c += kChunk) {
+    if (c * kThreads >= n) break;
+    G p[kChunk][3];
+    load_chunk<G, kChunk, kThreads>(pos, n, c, t, p);
+#pragma unroll
+    for (int k = 0; k < kChunk; ++k) {
+      const int i = (c + k) * kThreads + t;
+      if (i < n) {
+        bad = bad || !(isfinite(p[k][0]) && isfinite(p[k][1]) && isfinite(p[k][2]));
+        G w[3];
+        int o[3];
+        key[c + k] = wrap_and_bin(p[k], cell, g, w, o);
+        arrival[c + k] = atomicAdd(&s_start[key[c + k]], 1);
+      }
+    }
+  }
+  if (bad) s_bad = 1;
+  __syncthreads();
+  // exclusive scan of the nb + 1 counts (the last one zero): thread t sums a run of
+  // kScanPer, the runs are scanned by wave shuffles and one wave over the wave totals
+  int32_t v[kScanPer];
+  int32_t sum = 0;
+#pragma unroll
+  for (int k = 0; k < kScanPer; ++k) {
+    const int b = t * kScanPer + k;
+    v[k] = b <= nb ? s_start[b] : 0;
+    sum += v[k];
+  }
+  int32_t x = sum;
+#pragma unroll
+  for (int o = 1; o < kWave; o <<= 1) {
+    const int32_t y = __shfl_up(x, o, kWave);
+    if (lane >= o) x += y;
+  }
+  if (lane == kWave - 1) s_wsum[wv] = x;
+  __syncthreads();
+  if (wv == 0) {
+    int32_t w = lane < kThreads / kWave ? s_wsum[lane] : 0;
+#pragma unroll
+    for (int o = 1; o < kThreads / kWave; o <<= 1) {
+      const int32_t y = __shfl_up(w, o, kWave);
+      if (lane >= o) w += y;
+    }
+    if (lane < kThreads / kWave) s_wsum[lane] = w;
+  }
+  __syncthreads();
+  int32_t run = (wv > 0 ? s_wsum[wv - 1] : 0) + x - sum;
+#pragma unroll
+  for (int k = 0; k < kScanPer; ++k) {
+    const int b = t * kScanPer + k;
+    if (b <= nb) {
+      s_start[b] = run;
+      bin_start[b] = run;
+    }
+    run += v[k];
+  }
+  __syncthreads();
+  // the bins' lists in arrival order, each entry (bin key << kIdBits) | atom
+#pragma unroll
+  for (int k = 0; k < kPer; ++k)
+    if (key[k] >= 0) s_list[s_start[key[k]] + arrival[k]] = (key[k] << kIdBits) | (k * kThreads + t);
+  __syncthreads();
+  // position q of the lists: its atom's rank among the bin's atoms of lower index (the
+  // entries of one bin compare as their atoms do); the lanes of a wave take consecutive
+  // positions, a few bins' worth, so that their reads of a bin's list are LDS broadcasts
+#pragma unroll
+  for (int c = 0; c < kPer; c += kChunk) {
+    if (c * kThreads >= n) break;
+    int ent[kChunk];
+    G p[kChunk][3];
+#pragma unroll
+    for (int k = 0; k < kChunk; ++k) {
+      ent[k] = s_list[min((c + k) * kThreads + t, n - 1)];
+      const int i = ent[k] & kIdMask;
+      p[k][0] = pos[3 * i];
+      p[k][1] = pos[3 * i + 1];
+      p[k][2] = pos[3 * i + 2];
+    }
+#pragma unroll
+    for (int k = 0; k < kChunk; ++k) {
+      if ((c + k) * kThreads + t >= n) continue;
+      const int b = ent[k] >> kIdBits, i = ent[k] & kIdMask;
+      const int b0 = s_start[b], cnt = s_start[b + 1] - b0;
+      int rank = 0;
+#pragma unroll 4
+      for (int j = 0; j < cnt; ++j) rank += s_list[b0 + j] < ent[k] ? 1 : 0;
+      const int at = b0 + rank;
+      G w[3];
+      int o[3];
+      (void)wrap_and_bin(p[k], cell, g, w, o);
+      atom_sorted[at] = i;
+      store_row4(wpos_s + 4 * (int64_t)at, w[0], w[1], w[2], G(0));
+      *reinterpret_cast<int4*>(offs_s + 4 * (int64_t)at) = make_int4(o[0], o[1], o[2], b);
+    }
+  }
+  if (t < 4) overflow[t] = t == 3 ? s_bad : 0;
 }
 
 // ---------------------------------------------------------------- search
@@ -745,6 +924,7 @@ static GridDev grid_dev(const xnn_grid_plan* plan) {
     g.periodic[a] = plan->periodic[a];
     g.lo[a] = plan->lo[a];
     g.width[a] = plan->width[a];
+    g.iwidth[a] = 1.0 / plan->width[a];
   }
   g.has_cell = plan->has_cell;
   for (int k = 0; k < 9; ++k) g.inv[k] = plan->inv_cell[k];
@@ -777,33 +957,42 @@ static int grid_count(const void* pos_v, int64_t n, const void* cell_v, double c
   size_t cub_bytes = w.cub_bytes;
 
   const int64_t nb1 = plan->n_bins + 1;
-  // the bin counts, the per-atom counts, the overflow flags and row_ptr[0] in one launch
-  int32_t* cursor = ws_at<int32_t>(ws, w.cursor);
-  hipLaunchKernelGGL(zero_count_state_kernel, dim3(grid_1d(std::max(nb1, n + 1), 256)), dim3(256),
-                     0, stream, bin_cnt, nb1, counts, n + 1, overflow, row_ptr, cursor);
-  hipLaunchKernelGGL((bin_atoms_kernel<G>), dim3(grid_1d(n, 256)), dim3(256), 0, stream, pos, n,
-                     cell, g, bin_key, atom_id, wpos, offs, bin_cnt, overflow + 3);
-  XNN_LAUNCH_CHECK();
   const bool small = nb1 <= kBlockScanMax && n + 1 <= kBlockScanMax;
-  if (small) {
-    // atoms of one bin in ascending index order: a counting sort by bin
-    hipLaunchKernelGGL(block_scan_kernel<false>, dim3(1), dim3(1024), 0, stream, bin_cnt,
-                       bin_start, nb1);
-    hipLaunchKernelGGL(bin_scatter_kernel, dim3(grid_1d(n, 256)), dim3(256), 0, stream, bin_key,
-                       n, bin_start, cursor, bin_key_sorted);
-    hipLaunchKernelGGL((bin_sort_gather_kernel<G>), dim3(grid_1d(plan->n_bins, 4)), dim3(256), 0,
-                       stream, plan->n_bins, bin_start, bin_key_sorted, atom_sorted, wpos, offs,
-                       wpos_s, offs_s);
+  if (n <= kOneBlockAtoms && plan->n_bins <= kOneBlockBins) {
+    // the zeroes, the wrap, the bins and the stable sort by bin in one workgroup
+    hipLaunchKernelGGL((bin_one_block_kernel<G>), dim3(1), dim3(1024), 0, stream, pos, (int)n,
+                       cell, g, (int)plan->n_bins, bin_start, atom_sorted, wpos_s, offs_s, counts,
+                       overflow, row_ptr);
     XNN_LAUNCH_CHECK();
   } else {
-    XNN_HIP_CHECK(hipcub::DeviceScan::ExclusiveSum(cub, cub_bytes, bin_cnt, bin_start, (int)nb1,
-                                                   stream));
-    // stable: atoms of one bin keep ascending index order
-    XNN_HIP_CHECK(hipcub::DeviceRadixSort::SortPairs(cub, cub_bytes, bin_key, bin_key_sorted,
-                                                     atom_id, atom_sorted, (int)n, 0,
-                                                     end_bit_for(plan->n_bins), stream));
-    hipLaunchKernelGGL((gather_sorted_kernel<G>), dim3(grid_1d(n, 256)), dim3(256), 0, stream,
-                       atom_sorted, n, wpos, offs, wpos_s, offs_s);
+    // the bin counts, the per-atom counts, the overflow flags and row_ptr[0] in one launch
+    int32_t* cursor = ws_at<int32_t>(ws, w.cursor);
+    hipLaunchKernelGGL(zero_count_state_kernel, dim3(grid_1d(std::max(nb1, n + 1), 256)),
+                       dim3(256), 0, stream, bin_cnt, nb1, counts, n + 1, overflow, row_ptr,
+                       cursor);
+    hipLaunchKernelGGL((bin_atoms_kernel<G>), dim3(grid_1d(n, 256)), dim3(256), 0, stream, pos,
+                       n, cell, g, bin_key, atom_id, wpos, offs, bin_cnt, overflow + 3);
+    XNN_LAUNCH_CHECK();
+    if (small) {
+      // atoms of one bin in ascending index order: a counting sort by bin
+      hipLaunchKernelGGL(block_scan_kernel<false>, dim3(1), dim3(1024), 0, stream, bin_cnt,
+                         bin_start, nb1);
+      hipLaunchKernelGGL(bin_scatter_kernel, dim3(grid_1d(n, 256)), dim3(256), 0, stream,
+                         bin_key, n, bin_start, cursor, bin_key_sorted);
+      hipLaunchKernelGGL((bin_sort_gather_kernel<G>), dim3(grid_1d(plan->n_bins, 4)), dim3(256),
+                         0, stream, plan->n_bins, bin_start, bin_key_sorted, atom_sorted, wpos,
+                         offs, wpos_s, offs_s);
+      XNN_LAUNCH_CHECK();
+    } else {
+      XNN_HIP_CHECK(hipcub::DeviceScan::ExclusiveSum(cub, cub_bytes, bin_cnt, bin_start,
+                                                     (int)nb1, stream));
+      // stable: atoms of one bin keep ascending index order
+      XNN_HIP_CHECK(hipcub::DeviceRadixSort::SortPairs(cub, cub_bytes, bin_key, bin_key_sorted,
+                                                       atom_id, atom_sorted, (int)n, 0,
+                                                       end_bit_for(plan->n_bins), stream));
+      hipLaunchKernelGGL((gather_sorted_kernel<G>), dim3(grid_1d(n, 256)), dim3(256), 0, stream,
+                         atom_sorted, n, wpos, offs, wpos_s, offs_s);
+    }
   }
   hipLaunchKernelGGL((cell_search_kernel<G, false>),
                      dim3(plan->n_bins, search_split(n, plan->n_bins)), dim3(256), 0, stream,
