@@ -94,6 +94,54 @@ def test_conv_matches_the_oracle_and_the_pytorch_gradients(mul, lsh, n, e, seed,
     assert torch.equal(again, out)
 
 
+def test_conv_water_box_graph_timing():
+    """The same layer on the water box's own neighbor list (9,000 atoms, 477,698 edges, 5 A
+    cutoff, receivers in CSR order, atoms in the generator's spatial order), where the
+    senders of nearby receivers are shared: forward against the oracle on a sample of nodes,
+    and the time per launch."""
+    import xnn_amd as xa
+    from xnn_amd import synthetic
+    from xnn_amd.conv import plan_of
+    _note("uvu conv on the water box's neighbor list")
+    s = synthetic.water_box(seed=0)
+    n = len(s.pos)
+    ei, _ = xa.build_neighbor_list(torch.tensor(s.pos, dtype=torch.float32, device=DEV), 5.0,
+                                   torch.tensor(s.cell, dtype=torch.float32, device=DEV),
+                                   torch.tensor(s.pbc))
+    e = ei.shape[1]
+    src, dst = (a.cpu().numpy() for a in ei)
+    assert bool((dst[1:] >= dst[:-1]).all())
+    tp, irreps1, sh, mid, ins, _, _, h, y, w, _ = _setup(32, 2, n, e, 7)
+    hd, yd, wd = (torch.tensor(a, device=DEV) for a in (h, y, w))
+    tp.fast_active = True
+    plan = plan_of(ei, n)
+    out = tp.conv(hd, yd, wd, ei, n, plan=plan)
+    torch.cuda.synchronize()
+    pick = np.arange(0, n, 97)
+    sel = np.isin(dst, pick)
+    want = T.uvu_conv(h.astype(np.float64), y[sel].astype(np.float64), w[sel].astype(np.float64),
+                      src[sel], dst[sel], n, repr(irreps1), repr(sh), repr(mid),
+                      [(a, b, c) for a, b, c, _, _ in ins])
+    _close(out.cpu().numpy()[pick], want[pick])
+    hr, yr, wr = (t.clone().requires_grad_() for t in (hd, yd, wd))
+    g = torch.randn_like(out)
+    times = {}
+    for name in ("forward", "backward"):
+        for rep in range(6):
+            if rep == 1:
+                torch.cuda.synchronize()
+                t0 = time.perf_counter()
+            if name == "forward":
+                tp.conv(hd, yd, wd, ei, n, plan=plan)
+            else:
+                o = tp.conv(hr, yr, wr, ei, n, plan=plan)
+                torch.autograd.grad(o, [hr, yr, wr], g)
+        torch.cuda.synchronize()
+        times[name] = (time.perf_counter() - t0) / 5 * 1e6
+    print(f"uvu conv water box graph {n} nodes / {e} edges: forward {times['forward']:.0f} us, "
+          f"forward+backward {times['backward']:.0f} us", flush=True)
+
+
 def test_conv_water_size_timing():
     """A NequIP-sized layer on the water box's graph shape (9,000 nodes, 450k edges, 32
     channels of 0e + 1o + 2e, harmonics to l = 2): forward and backward against the

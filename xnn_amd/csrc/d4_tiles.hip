@@ -797,6 +797,29 @@ __device__ __forceinline__ void cn_tile(
     st.win[2][lane] = pack_window(0, 0);
   }
   __syncthreads();
+  // a tile pair none of whose sources reaches the receivers' box (most of them, the CN's
+  // reach being a few Angstrom): its slots hold zeros, written without the source loop
+  if (!DIAG) {
+    bool reach = false;
+    if (lane < it.scnt) {
+      const int w0 = st.win[0][lane], w1 = st.win[1][lane], w2 = st.win[2][lane];
+      reach = window_lo(w0) <= window_hi(w0) && window_lo(w1) <= window_hi(w1) &&
+              window_lo(w2) <= window_hi(w2);
+    }
+    if (!__any(reach)) {
+      if (live) {
+        double* po = partial + (int64_t)it.ls * NP * n_nodes + pi;
+#pragma unroll
+        for (int k = 0; k < NP; ++k) po[(int64_t)k * n_nodes] = 0.0;
+      }
+      if (lane < it.scnt) {
+        double* po = partial + (int64_t)it.lt * NP * n_nodes + it.s0 + lane;
+#pragma unroll
+        for (int k = 0; k < NP; ++k) po[(int64_t)k * n_nodes] = 0.0;
+      }
+      return;
+    }
+  }
 
   const double inv_k6 = 1.0 / prm.k6;
   double acc[2] = {0.0, 0.0}, g3[3] = {0.0, 0.0, 0.0}, cacc[9];

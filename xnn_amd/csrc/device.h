@@ -18,6 +18,21 @@ namespace xnn {
 
 constexpr int kWave = 64;
 
+// MI355X's accelerator dies: workgroups are dispatched to the 8 XCDs in turn (block b to XCD
+// b % 8), each XCD with its own L2. A launch of a multiple of 8 blocks that gives block b
+// the slot xcd_slot(b) = (b % 8) * (blocks / 8) + b / 8 has each XCD walk one contiguous run
+// of slots: with work laid out in a spatial order, the rows a run gathers are shared by the
+// XCD's other waves and stay in its L2.
+constexpr int kXcds = 8;
+
+__device__ __forceinline__ int64_t xcd_slot() {
+  const int64_t per_xcd = ((int64_t)gridDim.x + kXcds - 1) / kXcds;
+  return (int64_t)(blockIdx.x % kXcds) * per_xcd + blockIdx.x / kXcds;
+}
+
+// a block count rounded up to whole XCD rounds (xcd_slot is then a permutation)
+inline int64_t xcd_blocks(int64_t blocks) { return ((blocks + kXcds - 1) / kXcds) * kXcds; }
+
 // Wave index within the block, as a wave-uniform (scalar) value: the compiler cannot
 // infer that threadIdx.x / 64 is the same on every lane, and values derived from a
 // divergent-looking index turn uniform loops and branches into vector control flow.

@@ -157,7 +157,6 @@ __global__ __launch_bounds__(256) void featurize_bwd_kernel(
 // (b % 8) * per_xcd + b / 8 and each XCD walks one contiguous run of the visit order. The
 // sender-side gather of an atom reads the gradient rows of its neighbours; with spatially
 // compact runs those rows are shared by the XCD's other atoms and stay in its L2.
-constexpr int kXcds = 8;
 
 template <typename G, typename T, int GROUP>
 __global__ __launch_bounds__(256) void force_reduce_kernel(
@@ -168,8 +167,7 @@ __global__ __launch_bounds__(256) void force_reduce_kernel(
     double* __restrict__ cell_partial, const T* __restrict__ vec,
     double* __restrict__ virial_partial, double* __restrict__ virial_block) {
   const int lane = threadIdx.x % GROUP;
-  const int64_t per_xcd = ((int64_t)gridDim.x + kXcds - 1) / kXcds;
-  const int64_t sb = (int64_t)(blockIdx.x % kXcds) * per_xcd + blockIdx.x / kXcds;
+  const int64_t sb = xcd_slot();
   const int64_t slot = (sb * blockDim.x + threadIdx.x) / GROUP;
   const bool live = slot < n_nodes;
   const int64_t i = live ? (visit ? (int64_t)visit[slot] : slot) : 0;
@@ -466,8 +464,7 @@ static int force_group(int64_t n_edges, int64_t n_nodes) {
 
 // blocks of the force reduction: enough for every atom, rounded up to whole XCD rounds
 static int64_t force_blocks(int64_t n_edges, int64_t n_nodes) {
-  const int64_t b = grid_1d(n_nodes * force_group(n_edges, n_nodes), 256);
-  return ((b + kXcds - 1) / kXcds) * kXcds;
+  return xcd_blocks(grid_1d(n_nodes * force_group(n_edges, n_nodes), 256));
 }
 
 template <typename G, typename T, int GROUP>

@@ -500,11 +500,13 @@ __device__ __forceinline__ void conv_pass(const ConvView& V, const ConvBlock& B,
 }
 
 // One launch per node-block degree l1 (each specialization gets its own register budget):
-// wave w takes block ids[w % n_ids] of the node group w / n_ids.
+// wave w takes block ids[w % n_ids] of the node group w / n_ids, the blocks laid out over the
+// XCDs (xcd_slot): each XCD walks one contiguous run of receivers, whose senders (their
+// neighbours, in a spatial atom order) it gathers from its own L2.
 template <int PASS, int L1, int LS>
 __global__ __launch_bounds__(kConvWaves * kWave) void uvu_conv_kernel(ConvArgs K) {
   const ConvView V = K.v;
-  const int64_t w = (int64_t)blockIdx.x * kConvWaves + wave_in_block();
+  const int64_t w = xcd_slot() * kConvWaves + wave_in_block();
   const int blk = K.ids[w % K.n_ids];
   const ConvBlock B = K.blocks[blk];
   const bool split = B.mul <= 32;
@@ -599,7 +601,7 @@ static int conv_launch_l1(ConvArgs& A, hipStream_t stream) {
     if (A.blocks[b].l1 == L1) A.ids[A.n_ids++] = b;
   if (A.n_ids == 0) return XNN_OK;
   const int64_t waves = A.v.n_nodes * (int64_t)A.n_ids;
-  const dim3 grid((unsigned)grid_1d(waves, kConvWaves)), block(kConvWaves * kWave);
+  const dim3 grid((unsigned)xcd_blocks(grid_1d(waves, kConvWaves))), block(kConvWaves * kWave);
   switch (A.v.ls) {
     case 0: hipLaunchKernelGGL((uvu_conv_kernel<PASS, L1, 0>), grid, block, 0, stream, A); break;
     case 1: hipLaunchKernelGGL((uvu_conv_kernel<PASS, L1, 1>), grid, block, 0, stream, A); break;
