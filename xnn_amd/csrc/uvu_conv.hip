@@ -188,8 +188,13 @@ __device__ __forceinline__ void conv_load_y(const ConvView& V, int64_t e, float*
 #pragma unroll
   for (int l = 0; l <= LS; ++l) {
     const int o = V.off2[l];
+    // an absent degree loads the row's first value (a valid address) and uses zero: every
+    // load is issued unconditionally, so the wait counts of the edge loops stay exact
 #pragma unroll
-    for (int m = 0; m < 2 * l + 1; ++m) yv[l * l + m] = o >= 0 ? yrow[o + m] : 0.f;
+    for (int m = 0; m < 2 * l + 1; ++m) {
+      const float v = yrow[o >= 0 ? o + m : 0];
+      yv[l * l + m] = o >= 0 ? v : 0.f;
+    }
   }
 }
 
@@ -199,28 +204,52 @@ struct ConvEdge {
   bool on, row_ok;
 };
 
-__device__ __forceinline__ ConvEdge conv_edge(const ConvView& V, const ConvLanes& L, int32_t it,
-                                              const int32_t* other_of) {
+// The indices of up to 64 edges of a wave's node row, one edge per lane (lane j: the
+// chunk's edge j; past the row's end, its last edge), loaded once per chunk: in the edge
+// loops an edge's indices come from a lane exchange, so the loops issue no index loads and
+// one edge's operand loads stay in flight across the previous edge's arithmetic.
+struct ConvChunk {
+  int32_t e, other, row;  // this lane's edge of the chunk
+  int32_t cnt, trips;     // the chunk's edges and trips over them (uniform)
+};
+
+__device__ __forceinline__ ConvChunk conv_chunk(const ConvView& V, const ConvLanes& L,
+                                                int32_t base, int lane,
+                                                const int32_t* __restrict__ other_of) {
+  ConvChunk K;
+  K.cnt = min(kWave, L.len - base);
+  K.trips = (K.cnt + L.step - 1) / L.step;
+  const int32_t q = L.q0 + base + min(lane, K.cnt - 1);
+  K.e = V.perm ? V.perm[q] : q;
+  K.other = other_of[K.e];
+  K.row = V.widx ? V.widx[K.e] : K.e;
+  return K;
+}
+
+// the edge of trip `it` of chunk K for a lane: position it * step + half of the chunk (a
+// position past the chunk gives its last edge, `on` false)
+__device__ __forceinline__ ConvEdge conv_edge_at(const ConvView& V, const ConvChunk& K,
+                                                 const ConvLanes& L, int32_t it) {
   const int32_t k = it * L.step + L.half;
-  ConvEdge E{0, 0, -1, k < L.len, false};
-  if (E.on) {
-    const int32_t q = L.q0 + k;
-    E.e = V.perm ? (int64_t)V.perm[q] : (int64_t)q;
-    E.other = other_of[E.e];
-    E.row = conv_row(V, E.e);
-    E.row_ok = E.row >= 0 && E.row < V.n_w_rows;
-  }
+  const int src_lane = min(k, K.cnt - 1);
+  ConvEdge E;
+  E.e = __shfl(K.e, src_lane, kWave);
+  E.other = __shfl(K.other, src_lane, kWave);
+  E.row = __shfl(K.row, src_lane, kWave);
+  E.on = k < K.cnt;
+  E.row_ok = E.on && E.row >= 0 && E.row < V.n_w_rows;
   return E;
 }
 
 // ------------------------------------------------------------------ operand fetch
 // One edge's operands for one lane: the sender's block h[src(e), block, u, :], the edge's
-// harmonics and the weight of every path of the block. The edge loops fetch them one edge
-// ahead of the arithmetic (and the edge indices two ahead), so the gathers of the next edge
-// are in flight while this one is expanded. Every lane loads, from a valid address (a lane
-// without an edge reads edge 0, a channel past the block channel 0, a weight row out of
-// range row 0), and `use` says whether the operands are the lane's: the arithmetic runs
-// under it, so no per-load branch or zero fill is needed.
+// harmonics and the weight of every path of the block. The edge loops keep two of them,
+// fetched one trip ahead of the arithmetic in alternation (no copies between them), so the
+// gathers of the next edge are in flight while this one is expanded. Every lane loads, from
+// a valid address (a lane without an edge reads the chunk's last edge, a channel past the
+// block channel 0, a weight row out of range row 0, an absent path the row's first weight),
+// and `use` says whether the operands are the lane's: the arithmetic runs under it, and
+// with no branch around a load the wait before each use counts exactly the loads after it.
 template <int L1, int LS>
 struct ConvFetch {
   float hv[2 * L1 + 1];
@@ -243,12 +272,13 @@ __device__ __forceinline__ void conv_fetch(const ConvView& V, const ConvBlock& B
     for (int a = 0; a < D1; ++a) F.hv[a] = hrow[a];
   }
   conv_load_y<LS>(V, E.e, F.yv);
-  const float* wrow = V.w + (E.row_ok ? E.row : 0) * V.dw + us;
   const bool have_w = V.n_w_rows > 0;
+  // without weight rows any valid address (no lane uses the values: row_ok is false)
+  const float* wrow = have_w ? V.w + (E.row_ok ? E.row : 0) * V.dw + us : V.y;
 #define XNN_CONV_FETCH_W(P1_, P2_, P3_)                                               \
   if constexpr (P1_ == L1 && P2_ <= LS) {                                             \
     constexpr int ci = combo_index(P1_, P2_, P3_);                                    \
-    F.wv[ci] = (B.c[ci].off_w >= 0 && have_w) ? wrow[B.c[ci].off_w] : 0.f;            \
+    F.wv[ci] = wrow[(B.c[ci].off_w >= 0 && have_w) ? B.c[ci].off_w : 0];              \
   }
   XNN_CG_TRIPLES(XNN_CONV_FETCH_W)
 #undef XNN_CONV_FETCH_W
@@ -259,20 +289,15 @@ template <int L1, int LS>
 __device__ __forceinline__ void conv_fwd_block(const ConvView& V, const ConvBlock& B,
                                                const ConvLanes& L) {
   constexpr int NA = combo_width(L1);
+  const int lane = threadIdx.x % kWave;
   for (int u0 = 0; u0 < B.mul; u0 += L.width) {
     const int u = u0 + L.sub;
     const bool chan = u < B.mul;
     float acc[NA];
 #pragma unroll
     for (int k = 0; k < NA; ++k) acc[k] = 0.f;
-    ConvFetch<L1, LS> F;
-    if (L.trips > 0) conv_fetch<L1, LS>(V, B, conv_edge(V, L, 0, V.src), u, chan, true, F);
-    ConvEdge En = conv_edge(V, L, 1, V.src);
-    for (int32_t it = 0; it < L.trips; ++it) {
-      const ConvFetch<L1, LS> C = F;
-      if (it + 1 < L.trips) conv_fetch<L1, LS>(V, B, En, u, chan, true, F);
-      En = conv_edge(V, L, it + 2, V.src);
-      if (!C.use) continue;
+    auto edge = [&](const ConvFetch<L1, LS>& C) {
+      if (!C.use) return;
       // the products h_a Y_b, shared by every path of the block that reads them
       float hy[(2 * L1 + 1) * (LS + 1) * (LS + 1)];
 #pragma unroll
@@ -296,6 +321,18 @@ __device__ __forceinline__ void conv_fwd_block(const ConvView& V, const ConvBloc
   }
       XNN_CG_TRIPLES(XNN_CONV_COMBO)
 #undef XNN_CONV_COMBO
+    };
+    for (int32_t base = 0; base < L.len; base += kWave) {
+      const ConvChunk K = conv_chunk(V, L, base, lane, V.src);
+      ConvFetch<L1, LS> F0, F1;
+      conv_fetch<L1, LS>(V, B, conv_edge_at(V, K, L, 0), u, chan, true, F0);
+      conv_fetch<L1, LS>(V, B, conv_edge_at(V, K, L, 1), u, chan, true, F1);
+      for (int32_t it = 0; it < K.trips; it += 2) {
+        edge(F0);
+        conv_fetch<L1, LS>(V, B, conv_edge_at(V, K, L, it + 2), u, chan, true, F0);
+        if (it + 1 < K.trips) edge(F1);
+        conv_fetch<L1, LS>(V, B, conv_edge_at(V, K, L, it + 3), u, chan, true, F1);
+      }
     }
 #pragma unroll
     for (int k = 0; k < NA; ++k) acc[k] = conv_halves_sum(acc[k], L.step == 2);
@@ -324,6 +361,7 @@ template <int L1, int LS, bool DH>
 __device__ __forceinline__ void conv_bwd_edge_block(const ConvView& V, const ConvBlock& B,
                                                     const ConvLanes& L, bool pair, int blk) {
   constexpr int NA = combo_width(L1), NY = (LS + 1) * (LS + 1), D1 = 2 * L1 + 1;
+  const int lane = threadIdx.x % kWave;
   for (int u0 = 0; u0 < B.mul; u0 += L.width) {
     const int u = u0 + L.sub;
     const bool chan = u < B.mul && L.node < V.n_nodes;
@@ -344,16 +382,7 @@ __device__ __forceinline__ void conv_bwd_edge_block(const ConvView& V, const Con
       XNN_CG_TRIPLES(XNN_CONV_LOADG)
 #undef XNN_CONV_LOADG
     }
-    ConvFetch<L1, LS> F;
-    ConvEdge Ec = conv_edge(V, L, 0, V.src);
-    if (L.trips > 0) conv_fetch<L1, LS>(V, B, Ec, u, chan, true, F);
-    ConvEdge En = conv_edge(V, L, 1, V.src);
-    for (int32_t it = 0; it < L.trips; ++it) {
-      const ConvFetch<L1, LS> C = F;
-      const ConvEdge E = Ec;
-      if (it + 1 < L.trips) conv_fetch<L1, LS>(V, B, En, u, chan, true, F);
-      Ec = En;
-      En = conv_edge(V, L, it + 2, V.src);
+    auto edge = [&](const ConvFetch<L1, LS>& C, const ConvEdge& E) {
       float dyt[NY], dh[D1];
 #pragma unroll
       for (int j = 0; j < NY; ++j) dyt[j] = -0.f;
@@ -416,6 +445,21 @@ __device__ __forceinline__ void conv_bwd_edge_block(const ConvView& V, const Con
             if (E.on && L.sub == 0) row[o + m] = u0 == 0 ? s : row[o + m] + s;
           }
         }
+      }
+    };
+    for (int32_t base = 0; base < L.len; base += kWave) {
+      const ConvChunk K = conv_chunk(V, L, base, lane, V.src);
+      ConvEdge E0 = conv_edge_at(V, K, L, 0), E1 = conv_edge_at(V, K, L, 1);
+      ConvFetch<L1, LS> F0, F1;
+      conv_fetch<L1, LS>(V, B, E0, u, chan, true, F0);
+      conv_fetch<L1, LS>(V, B, E1, u, chan, true, F1);
+      for (int32_t it = 0; it < K.trips; it += 2) {
+        edge(F0, E0);
+        E0 = conv_edge_at(V, K, L, it + 2);
+        conv_fetch<L1, LS>(V, B, E0, u, chan, true, F0);
+        if (it + 1 < K.trips) edge(F1, E1);
+        E1 = conv_edge_at(V, K, L, it + 3);
+        conv_fetch<L1, LS>(V, B, E1, u, chan, true, F1);
       }
     }
   }
