@@ -47,7 +47,6 @@ constexpr int kT = 64;                 // atoms per tile (lanes of a wave)
 constexpr int kOrderThreads = 1024;    // one workgroup orders one structure
 constexpr int kOrderBits = 4;          // at most 16 bins per axis
 constexpr int kOrderBins = 1 << (3 * kOrderBits);
-constexpr int kFlush = 8;              // sources per dE/d alpha flush (pair backward)
 constexpr int kRedWaves = 8;           // waves of a slot-reduction block
 
 __constant__ double c_cp3[kNW] = {
@@ -440,28 +439,104 @@ __device__ __forceinline__ bool lane_finish8(double* __restrict__ buf, const dou
 
 // ---------------------------------------------------------------- two-body term
 
+template <bool BACKWARD>
 struct PairStage {
-  double w[kT];                // the sources' upstream gradient g_e2
-  double sa[kT][kNW + 1];      // alpha(i w) times the quadrature weight c_cp3(w): of the
-                               // sources, then (the backward's dE/d alpha step) the receivers
-  int win[3][kT];              // packed image windows
-  union {
-    struct {
-      double x[kT], y[kT], z[kT];  // bohr
-      double p[kT], q[kT];         // r4r2, its square root
-      double red[8 * 8 * 3];       // lane_finish8
-    } s;
-    double kbuf[kFlush * kT];      // dE/dC6 of 8 sources (the dE/d alpha step)
-  } u;
+  double w[kT];                        // the sources' upstream gradient g_e2
+  double gr[BACKWARD ? kT : 1];        // the receivers' (the dE/d alpha products)
+  int id[BACKWARD ? 2 : 1][kT];        // atom ids of the receivers, the sources
+  double sa[BACKWARD ? 1 : kT][kNW + 1];  // the energy kernel: the sources' alpha(i w) times
+                                          // the quadrature weight c_cp3(w)
+  int win[3][kT];                      // packed image windows
+  double x[kT], y[kT], z[kT];          // bohr
+  double p[kT], q[kT];                 // r4r2, its square root
+  double red[8 * 8 * 3];               // lane_finish8
 };
+
+// dE/d alpha(i w) of both atoms of every pair of the work item, from the pairs' image sums
+// of f(r) this wave left in its block: dE/d C6_ij = -1/2 (g_i + g_j) fsum_ij =: K_ij and
+// d C6_ij / d alpha_i(w) = cp3(w) alpha_j(w), so
+//   receivers: D_r[r][w] = sum_s K[s][r] cp3(w) alpha_s(w)   (64 x 23, K = 64 sources)
+//   sources:   D_s[s][w] = sum_r K[s][r] cp3(w) alpha_r(w)   (tile pairs d > 0 only)
+// two 64 x 64 x 24 products on the float64 matrix cores (v_mfma_f64_16x16x4: lane l gives
+// A[l % 16][l / 16] and B[l / 16][l % 16] and gets D[4 v + l / 16][l % 16] in register v --
+// not the float32 form's row 4 (l / 16) + v; checked on gfx950 with one-hot operands). The
+// A operand is read from the block (still in cache), the B operand from the alpha table.
+typedef double doublex4 __attribute__((ext_vector_type(4)));
+
+template <bool DIAG>
+__device__ __forceinline__ void pair_alpha_products(
+    const PairStage<true>& st, const TileItem& it, const double* __restrict__ alpha,
+    const int32_t* __restrict__ order, int64_t n_nodes, const double* __restrict__ fb,
+    double* __restrict__ partial_alpha) {
+  __syncthreads();  // the block's rows, written by every lane, read across lanes
+  const int lane = threadIdx.x, lo = lane & 15, hi = lane >> 4;
+#pragma unroll 1
+  for (int side = 0; side < (DIAG ? 1 : 2); ++side) {
+    // side 0: output rows the receivers, contracted over the sources (K read down a row);
+    // side 1: output rows the sources, contracted over the receivers (K read across)
+    const int out_cnt = side == 0 ? it.rcnt : it.scnt;
+    const int b_cnt = side == 0 ? it.scnt : it.rcnt;
+    const int* __restrict__ bid = st.id[1 - side];
+    // every B element of the side, then the A elements of one 16-row tile at a time: the
+    // loads of a batch are in flight together, the products wait once per batch
+    double b[kT / 4][2];
+#pragma unroll
+    for (int ks = 0; ks < kT / 4; ++ks) {
+      const int kk = 4 * ks + hi;  // the contracted atom of this lane's B elements
+#pragma unroll
+      for (int nt = 0; nt < 2; ++nt) {
+        const int w = 16 * nt + lo;
+        b[ks][nt] = (kk < b_cnt && w < kNW)
+                        ? alpha[(int64_t)kNW * bid[kk] + w] * c_cp3[w < kNW ? w : 0]
+                        : 0.0;
+      }
+    }
+    const int slot = side == 0 ? it.ls : it.lt;
+    const int64_t p0 = side == 0 ? it.r0 : it.s0;
+    double* __restrict__ pa = partial_alpha + (int64_t)slot * kNW * n_nodes + p0;
+#pragma unroll 1
+    for (int mt = 0; mt < 4; ++mt) {
+      const int m = 16 * mt + lo;  // output row of this lane's A elements
+      double a[kT / 4];
+#pragma unroll
+      for (int ks = 0; ks < kT / 4; ++ks) {
+        const int kk = 4 * ks + hi;
+        const int s = side == 0 ? kk : m, r = side == 0 ? m : kk;
+        a[ks] = (s < it.scnt && r < it.rcnt) ? -0.5 * (st.gr[r] + st.w[s]) * fb[s * kT + r]
+                                             : 0.0;
+      }
+      doublex4 acc[2] = {doublex4{0.0, 0.0, 0.0, 0.0}, doublex4{0.0, 0.0, 0.0, 0.0}};
+#pragma unroll
+      for (int ks = 0; ks < kT / 4; ++ks)
+#pragma unroll
+        for (int nt = 0; nt < 2; ++nt)
+          acc[nt] = __builtin_amdgcn_mfma_f64_16x16x4f64(a[ks], b[ks][nt], acc[nt], 0, 0, 0);
+#pragma unroll
+      for (int nt = 0; nt < 2; ++nt) {
+        const int w = 16 * nt + lo;
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          const int mo = 16 * mt + 4 * v + hi;
+          if (w < kNW && mo < out_cnt) pa[(int64_t)w * n_nodes + mo] = acc[nt][v];
+        }
+      }
+    }
+  }
+}
 
 // BACKWARD = false: partial[slot][0][p] = the atom's sum of -1/2 C6 f(r).
 // BACKWARD = true:  partial[slot][0..2][p] = grad_pos, [3..11] the cell gradient (CELL),
 //                   partial_alpha[slot][w][p] = dE/d alpha(i w); fsum_out[jj][lane] (this
-//                   wave's 64 x 64 block of workspace) holds the pairs' sums over images of f(r).
+//                   wave's 64 x 64 block of workspace) holds the pairs' sums over images of
+//                   f(r), from which pair_alpha_products forms dE/d alpha at the end. The
+//                   block first holds the pairs' C6, which the lane writes
+//                   before the source loop (its receiver's alpha then leaves the registers)
+//                   and reads back one source at a time, just before that source's row takes
+//                   the image sum: no alpha table in LDS and no 23 alpha registers in the
+//                   loop, so three waves fit on a SIMD.
 template <bool BACKWARD, bool CELL, bool DIAG>
 __device__ __forceinline__ void pair_tile(
-    PairStage& st, const TileItem& it, const TileGeo& G, const PairParams& prm,
+    PairStage<BACKWARD>& st, const TileItem& it, const TileGeo& G, const PairParams& prm,
     const double* __restrict__ pos, const int32_t* __restrict__ species,
     const double* __restrict__ r4r2, const double* __restrict__ alpha,
     const double* __restrict__ g_e2, const int32_t* __restrict__ order, int64_t n_nodes,
@@ -480,20 +555,36 @@ __device__ __forceinline__ void pair_tile(
   double ai[kNW];
 #pragma unroll
   for (int w = 0; w < kNW; ++w) ai[w] = alpha[(int64_t)kNW * i + w];
+  if constexpr (BACKWARD) {
+    // C6 of this lane's pair with every source, into the block's rows; the source's
+    // alpha is wave-uniform (scalar loads)
+    for (int jj = 0; jj < it.scnt; ++jj) {
+      const int j = __builtin_amdgcn_readfirstlane(order[it.s0 + jj]);
+      const double* __restrict__ aj = alpha + (int64_t)kNW * j;
+      double c6p[4] = {0.0, 0.0, 0.0, 0.0};
+#pragma unroll
+      for (int w = 0; w < kNW; ++w) c6p[w & 3] += ai[w] * (aj[w] * c_cp3[w]);
+      fsum_out[jj * kT + lane] = (c6p[0] + c6p[1]) + (c6p[2] + c6p[3]);
+    }
+  }
   double flo[3], fhi[3];
   tile_bounds(G, xa, ya, za, live, flo, fhi);
   if (lane < it.scnt) {
     const int j = order[it.s0 + lane];
     const double xs = pos[3 * (int64_t)j], ys = pos[3 * (int64_t)j + 1], zs = pos[3 * (int64_t)j + 2];
-    st.u.s.x[lane] = xs * kInvBohr;
-    st.u.s.y[lane] = ys * kInvBohr;
-    st.u.s.z[lane] = zs * kInvBohr;
+    st.x[lane] = xs * kInvBohr;
+    st.y[lane] = ys * kInvBohr;
+    st.z[lane] = zs * kInvBohr;
     const double pj = r4r2[species[j]];
-    st.u.s.p[lane] = pj;
-    st.u.s.q[lane] = sqrt(pj);
-    if (BACKWARD) st.w[lane] = g_e2[j];
+    st.p[lane] = pj;
+    st.q[lane] = sqrt(pj);
+    if constexpr (BACKWARD) {
+      st.w[lane] = g_e2[j];
+      st.id[1][lane] = j;
+    } else {
 #pragma unroll
-    for (int w = 0; w < kNW; ++w) st.sa[lane][w] = alpha[(int64_t)kNW * j + w] * c_cp3[w];
+      for (int w = 0; w < kNW; ++w) st.sa[lane][w] = alpha[(int64_t)kNW * j + w] * c_cp3[w];
+    }
     int win[3];
     source_windows(G, xs, ys, zs, flo, fhi, win);
 #pragma unroll
@@ -502,6 +593,14 @@ __device__ __forceinline__ void pair_tile(
     st.win[0][lane] = pack_window(1, 0);  // empty
     st.win[1][lane] = pack_window(0, 0);
     st.win[2][lane] = pack_window(0, 0);
+    if constexpr (BACKWARD) {
+      st.w[lane] = 0.0;
+      st.id[1][lane] = i;
+    }
+  }
+  if constexpr (BACKWARD) {
+    st.gr[lane] = live ? gi : 0.0;
+    st.id[0][lane] = i;
   }
   __syncthreads();
 
@@ -526,18 +625,23 @@ __device__ __forceinline__ void pair_tile(
               lo2 = window_lo(w2), hi2 = window_hi(w2);
     double fs = 0.0;  // the pair's sum over images of f(r)
     if (lo0 <= hi0 && lo1 <= hi1 && lo2 <= hi2) {
-      // four partial sums: four short dependency chains instead of one of 23
-      double c6p[4] = {0.0, 0.0, 0.0, 0.0};
+      double c6;
+      if constexpr (BACKWARD) {
+        c6 = fsum_out[jj * kT + lane];
+      } else {
+        // four partial sums: four short dependency chains instead of one of 23
+        double c6p[4] = {0.0, 0.0, 0.0, 0.0};
 #pragma unroll
-      for (int w = 0; w < kNW; ++w) c6p[w & 3] += ai[w] * st.sa[jj][w];
-      const double c6 = (c6p[0] + c6p[1]) + (c6p[2] + c6p[3]);
+        for (int w = 0; w < kNW; ++w) c6p[w & 3] += ai[w] * st.sa[jj][w];
+        c6 = (c6p[0] + c6p[1]) + (c6p[2] + c6p[3]);
+      }
       // rr = 3 r4r2_i r4r2_j and R0 = a1 sqrt(rr) + a2, sqrt(rr) = sqrt(3 r4r2_i) sqrt(r4r2_j)
-      const double rr = 3.0 * qi * st.u.s.p[jj];
+      const double rr = 3.0 * qi * st.p[jj];
       const double s8rr = prm.s8 * rr;
-      const double r0 = prm.a1 * (sq3qi * st.u.s.q[jj]) + prm.a2;
+      const double r0 = prm.a1 * (sq3qi * st.q[jj]) + prm.a2;
       const double r02 = r0 * r0;
       const double r06 = r02 * r02 * r02, r08 = r06 * r02;
-      const double dx = xb - st.u.s.x[jj], dy = yb - st.u.s.y[jj], dz = zb - st.u.s.z[jj];
+      const double dx = xb - st.x[jj], dy = yb - st.y[jj], dz = zb - st.z[jj];
       // E = sum_i g_i e_i: the pair's energy enters with (g_i + g_j) (-1/2 C6 f); the
       // vector's gradient per Angstrom carries d r_bohr / d v = v_bohr / (r_bohr bohr)
       const double wsum = BACKWARD ? gi + st.w[jj] : 0.0;
@@ -624,7 +728,7 @@ __device__ __forceinline__ void pair_tile(
       double total;
       const int js = jj - 7 + (lane & 7);
       double* po = partial + (int64_t)it.lt * NP * n_nodes + it.s0 + js;
-      if (lane_finish8(st.u.s.red, vs, lane, total) && js < it.scnt)
+      if (lane_finish8(st.red, vs, lane, total) && js < it.scnt)
         po[(int64_t)(lane >> 3) * n_nodes] = total;
       if (BACKWARD && CELL && lane < 8 && js < it.scnt) {
 #pragma unroll
@@ -652,63 +756,14 @@ __device__ __forceinline__ void pair_tile(
       }
     }
   }
-  if (BACKWARD) {
-    // dE/d alpha(i w) of both atoms of every pair: dE/d C6_ij = -1/2 (g_i + g_j) fsum_ij
-    // (the pair sums this wave wrote, still in cache) and d C6_ij / d alpha_i(w) =
-    // cp3(w) alpha_j(w). The receivers' side in their lanes, against the sources' table.
-    double da[kNW];
-#pragma unroll
-    for (int w = 0; w < kNW; ++w) da[w] = 0.0;
-    for (int jj = 0; jj < it.scnt; ++jj) {
-      const double kk = -0.5 * (gi + st.w[jj]) * fsum_out[jj * kT + lane];
-#pragma unroll
-      for (int w = 0; w < kNW; ++w) da[w] += kk * st.sa[jj][w];
-    }
-    if (live) {
-      double* pa = partial_alpha + (int64_t)it.ls * kNW * n_nodes + pi;
-#pragma unroll
-      for (int w = 0; w < kNW; ++w) pa[(int64_t)w * n_nodes] = da[w];
-    }
-    if (!DIAG) {
-      // the sources' side: the receivers' table replaces the sources', and 8 sources at a
-      // time their dE/dC6 (skewed columns: conflict-free reads) meet lane = (source jl,
-      // frequency group wg), which sums over the receivers for w = wg, wg + 8, wg + 16
-      __syncthreads();
-#pragma unroll
-      for (int w = 0; w < kNW; ++w) st.sa[lane][w] = live ? ai[w] * c_cp3[w] : 0.0;
-      st.sa[lane][kNW] = 0.0;
-      const int jl = lane & (kFlush - 1), wg = lane / kFlush;
-      for (int j0 = 0; j0 < it.scnt; j0 += kFlush) {
-        __syncthreads();
-#pragma unroll
-        for (int q = 0; q < kFlush; ++q) {
-          const int jj = j0 + q;
-          const double kk = jj < it.scnt ? -0.5 * (gi + st.w[jj]) * fsum_out[jj * kT + lane] : 0.0;
-          st.u.kbuf[q * kT + ((lane + q) & (kT - 1))] = kk;
-        }
-        __syncthreads();
-        double o0 = 0.0, o1 = 0.0, o2 = 0.0;
-        for (int r = 0; r < it.rcnt; ++r) {
-          const double kv = st.u.kbuf[jl * kT + ((r + jl) & (kT - 1))];
-          o0 += kv * st.sa[r][wg];
-          o1 += kv * st.sa[r][wg + kFlush];
-          o2 += kv * st.sa[r][wg + 2 * kFlush];  // group 7 reads the zero padding
-        }
-        const int js = j0 + jl;
-        if (js < it.scnt) {
-          double* pa = partial_alpha + (int64_t)it.lt * kNW * n_nodes + it.s0 + js;
-          pa[(int64_t)wg * n_nodes] = o0;
-          pa[(int64_t)(wg + kFlush) * n_nodes] = o1;
-          if (wg + 2 * kFlush < kNW) pa[(int64_t)(wg + 2 * kFlush) * n_nodes] = o2;
-        }
-      }
-    }
-  }
+  if constexpr (BACKWARD) pair_alpha_products<DIAG>(st, it, alpha, order, n_nodes, fsum_out,
+                                                     partial_alpha);
 }
 
-// (64, 2): at most 256 registers, two waves per SIMD (20 KB of LDS: 8 waves per CU)
+// The energy kernel (64, 2): at most 256 registers, two waves per SIMD (18 KB of LDS). The
+// backward (64, 3): at most 168 registers, three waves per SIMD (5.5 KB of LDS).
 template <bool BACKWARD, bool CELL>
-__global__ __launch_bounds__(kT, 2) void d4_pair_tiles_kernel(
+__global__ __launch_bounds__(kT, BACKWARD ? 3 : 2) void d4_pair_tiles_kernel(
     const double* __restrict__ pos, const int32_t* __restrict__ species,
     const int64_t* __restrict__ node_ptr, int64_t n_graphs, const double* __restrict__ cell,
     const int32_t* __restrict__ images, const double* __restrict__ r4r2,
@@ -716,7 +771,7 @@ __global__ __launch_bounds__(kT, 2) void d4_pair_tiles_kernel(
     const int32_t* __restrict__ order, const int32_t* __restrict__ tile_ptr, int64_t n_nodes,
     int max_nt, double* __restrict__ partial, double* __restrict__ fsum,
     double* __restrict__ partial_alpha) {
-  __shared__ PairStage st;
+  __shared__ PairStage<BACKWARD> st;
   TileItem it;
   if (!tile_item(tile_ptr, node_ptr, n_graphs, n_nodes, max_nt, it)) return;
   TileGeo G;
@@ -729,8 +784,6 @@ __global__ __launch_bounds__(kT, 2) void d4_pair_tiles_kernel(
     pair_tile<BACKWARD, CELL, false>(st, it, G, prm, pos, species, r4r2, alpha, g_e2, order,
                                      n_nodes, partial, fb, partial_alpha);
 }
-
-
 
 // ---------------------------------------------------------------- coordination numbers
 
@@ -955,7 +1008,7 @@ __device__ __forceinline__ void cn_tile(
 }
 
 template <bool BACKWARD, bool CELL>
-__global__ __launch_bounds__(kT, 2) void d4_cn_tiles_kernel(
+__global__ __launch_bounds__(kT, 3) void d4_cn_tiles_kernel(
     const double* __restrict__ pos, const int32_t* __restrict__ species,
     const int64_t* __restrict__ node_ptr, int64_t n_graphs, const double* __restrict__ cell,
     const int32_t* __restrict__ images, const double* __restrict__ rcov,
