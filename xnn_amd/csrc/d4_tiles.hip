@@ -439,7 +439,13 @@ __device__ __forceinline__ bool lane_finish8(double* __restrict__ buf, const dou
 
 // ---------------------------------------------------------------- two-body term
 
-template <bool BACKWARD>
+// The backward deals a work item's 64 sources over the W waves of its block, kT / W
+// consecutive sources to a wave (whole 8-source flushes), every wave holding all 64
+// receivers: three waves per SIMD hold about as many waves as there are tile pairs, so one
+// wave per item would leave the kernel as long as its slowest items; finer items keep the
+// SIMDs filled to the end. The sources are staged once per block; the receiver-side sums
+// of the waves meet in LDS in wave order (the same order on every run).
+template <bool BACKWARD, int W>
 struct PairStage {
   double w[kT];                        // the sources' upstream gradient g_e2
   double gr[BACKWARD ? kT : 1];        // the receivers' (the dE/d alpha products)
@@ -447,10 +453,41 @@ struct PairStage {
   double sa[BACKWARD ? 1 : kT][kNW + 1];  // the energy kernel: the sources' alpha(i w) times
                                           // the quadrature weight c_cp3(w)
   int win[3][kT];                      // packed image windows
-  double x[kT], y[kT], z[kT];          // bohr
-  double p[kT], q[kT];                 // r4r2, its square root
-  double red[8 * 8 * 3];               // lane_finish8
+  union {
+    struct {
+      double x[kT], y[kT], z[kT];      // bohr
+      double p[kT], q[kT];             // r4r2, its square root
+      double red[W][8 * 8 * 3];        // lane_finish8, one buffer per wave
+    } s;
+    double comb[W > 1 ? 12 * kT : 1];  // receiver-side sums on their way across waves
+  } u;
 };
+
+// The receiver-side sums v of the block's W waves, added in wave order through comb (NC x 64
+// doubles); true in the last wave, whose v then holds the totals. Every wave of the block
+// calls it; comb is free again when it returns.
+template <int W, int NC>
+__device__ __forceinline__ bool waves_combine(double* __restrict__ comb, double (&v)[NC], int wv,
+                                              int lane) {
+  if constexpr (W == 1) {
+    return true;
+  } else {
+    for (int k = 0; k < W; ++k) {
+      if (wv == k) {
+        if (k > 0) {
+#pragma unroll
+          for (int c = 0; c < NC; ++c) v[c] = comb[c * kT + lane] + v[c];
+        }
+        if (k < W - 1) {
+#pragma unroll
+          for (int c = 0; c < NC; ++c) comb[c * kT + lane] = v[c];
+        }
+      }
+      __syncthreads();
+    }
+    return wv == W - 1;
+  }
+}
 
 // dE/d alpha(i w) of both atoms of every pair of the work item, from the pairs' image sums
 // of f(r) this wave left in its block: dE/d C6_ij = -1/2 (g_i + g_j) fsum_ij =: K_ij and
@@ -463,13 +500,13 @@ struct PairStage {
 // A operand is read from the block (still in cache), the B operand from the alpha table.
 typedef double doublex4 __attribute__((ext_vector_type(4)));
 
-template <bool DIAG>
+template <bool DIAG, int W>
 __device__ __forceinline__ void pair_alpha_products(
-    const PairStage<true>& st, const TileItem& it, const double* __restrict__ alpha,
+    const PairStage<true, W>& st, const TileItem& it, const double* __restrict__ alpha,
     const int32_t* __restrict__ order, int64_t n_nodes, const double* __restrict__ fb,
     double* __restrict__ partial_alpha) {
-  __syncthreads();  // the block's rows, written by every lane, read across lanes
-  const int lane = threadIdx.x, lo = lane & 15, hi = lane >> 4;
+  __syncthreads();  // the block's rows, written by every lane, read across lanes and waves
+  const int lane = threadIdx.x % kT, lo = lane & 15, hi = lane >> 4, wv = wave_in_block();
 #pragma unroll 1
   for (int side = 0; side < (DIAG ? 1 : 2); ++side) {
     // side 0: output rows the receivers, contracted over the sources (K read down a row);
@@ -495,7 +532,7 @@ __device__ __forceinline__ void pair_alpha_products(
     const int64_t p0 = side == 0 ? it.r0 : it.s0;
     double* __restrict__ pa = partial_alpha + (int64_t)slot * kNW * n_nodes + p0;
 #pragma unroll 1
-    for (int mt = 0; mt < 4; ++mt) {
+    for (int mt = wv % 4; mt < 4; mt += W) {  // the wave's 16-row tiles
       const int m = 16 * mt + lo;  // output row of this lane's A elements
       double a[kT / 4];
 #pragma unroll
@@ -534,9 +571,9 @@ __device__ __forceinline__ void pair_alpha_products(
 //                   and reads back one source at a time, just before that source's row takes
 //                   the image sum: no alpha table in LDS and no 23 alpha registers in the
 //                   loop, so three waves fit on a SIMD.
-template <bool BACKWARD, bool CELL, bool DIAG>
+template <bool BACKWARD, bool CELL, bool DIAG, int W>
 __device__ __forceinline__ void pair_tile(
-    PairStage<BACKWARD>& st, const TileItem& it, const TileGeo& G, const PairParams& prm,
+    PairStage<BACKWARD, W>& st, const TileItem& it, const TileGeo& G, const PairParams& prm,
     const double* __restrict__ pos, const int32_t* __restrict__ species,
     const double* __restrict__ r4r2, const double* __restrict__ alpha,
     const double* __restrict__ g_e2, const int32_t* __restrict__ order, int64_t n_nodes,
@@ -544,7 +581,10 @@ __device__ __forceinline__ void pair_tile(
     double* __restrict__ partial_alpha) {
   constexpr int NV = BACKWARD ? 3 : 1;
   constexpr int NP = BACKWARD ? (CELL ? 12 : 3) : 1;
-  const int lane = threadIdx.x;
+  constexpr int S = kT / W;  // sources of a wave
+  static_assert(S % 8 == 0 && (BACKWARD || W == 1), "whole 8-source flushes per wave");
+  const int lane = threadIdx.x % kT, wv = wave_in_block();
+  const int j_lo = wv * S, j_end = std::min(j_lo + S, it.scnt);
   const bool live = lane < it.rcnt;
   const int64_t pi = it.r0 + (live ? lane : 0);
   const int i = order[pi];
@@ -556,9 +596,9 @@ __device__ __forceinline__ void pair_tile(
 #pragma unroll
   for (int w = 0; w < kNW; ++w) ai[w] = alpha[(int64_t)kNW * i + w];
   if constexpr (BACKWARD) {
-    // C6 of this lane's pair with every source, into the block's rows; the source's
-    // alpha is wave-uniform (scalar loads)
-    for (int jj = 0; jj < it.scnt; ++jj) {
+    // C6 of this lane's pair with each of the wave's sources, into the block's rows; the
+    // source's alpha is wave-uniform (scalar loads)
+    for (int jj = j_lo; jj < j_end; ++jj) {
       const int j = __builtin_amdgcn_readfirstlane(order[it.s0 + jj]);
       const double* __restrict__ aj = alpha + (int64_t)kNW * j;
       double c6p[4] = {0.0, 0.0, 0.0, 0.0};
@@ -567,17 +607,18 @@ __device__ __forceinline__ void pair_tile(
       fsum_out[jj * kT + lane] = (c6p[0] + c6p[1]) + (c6p[2] + c6p[3]);
     }
   }
-  double flo[3], fhi[3];
-  tile_bounds(G, xa, ya, za, live, flo, fhi);
-  if (lane < it.scnt) {
+  if (wv == 0) {  // the sources, staged by the first wave
+    double flo[3], fhi[3];
+    tile_bounds(G, xa, ya, za, live, flo, fhi);
+    if (lane < it.scnt) {
     const int j = order[it.s0 + lane];
     const double xs = pos[3 * (int64_t)j], ys = pos[3 * (int64_t)j + 1], zs = pos[3 * (int64_t)j + 2];
-    st.x[lane] = xs * kInvBohr;
-    st.y[lane] = ys * kInvBohr;
-    st.z[lane] = zs * kInvBohr;
+    st.u.s.x[lane] = xs * kInvBohr;
+    st.u.s.y[lane] = ys * kInvBohr;
+    st.u.s.z[lane] = zs * kInvBohr;
     const double pj = r4r2[species[j]];
-    st.p[lane] = pj;
-    st.q[lane] = sqrt(pj);
+    st.u.s.p[lane] = pj;
+    st.u.s.q[lane] = sqrt(pj);
     if constexpr (BACKWARD) {
       st.w[lane] = g_e2[j];
       st.id[1][lane] = j;
@@ -598,9 +639,10 @@ __device__ __forceinline__ void pair_tile(
       st.id[1][lane] = i;
     }
   }
-  if constexpr (BACKWARD) {
-    st.gr[lane] = live ? gi : 0.0;
-    st.id[0][lane] = i;
+    if constexpr (BACKWARD) {
+      st.gr[lane] = live ? gi : 0.0;
+      st.id[0][lane] = i;
+    }
   }
   __syncthreads();
 
@@ -614,7 +656,7 @@ __device__ __forceinline__ void pair_tile(
 #pragma unroll
   for (int m = 0; m < 9; ++m) cacc[m] = 0.0;
   LaneTree8<NV> tree;
-  for (int jj = 0; jj < kT; ++jj) {
+  for (int jj = j_lo; jj < j_lo + S; ++jj) {
     double vs[NV];  // this source's share from this lane's pair
 #pragma unroll
     for (int k = 0; k < NV; ++k) vs[k] = 0.0;
@@ -636,12 +678,12 @@ __device__ __forceinline__ void pair_tile(
         c6 = (c6p[0] + c6p[1]) + (c6p[2] + c6p[3]);
       }
       // rr = 3 r4r2_i r4r2_j and R0 = a1 sqrt(rr) + a2, sqrt(rr) = sqrt(3 r4r2_i) sqrt(r4r2_j)
-      const double rr = 3.0 * qi * st.p[jj];
+      const double rr = 3.0 * qi * st.u.s.p[jj];
       const double s8rr = prm.s8 * rr;
-      const double r0 = prm.a1 * (sq3qi * st.q[jj]) + prm.a2;
+      const double r0 = prm.a1 * (sq3qi * st.u.s.q[jj]) + prm.a2;
       const double r02 = r0 * r0;
       const double r06 = r02 * r02 * r02, r08 = r06 * r02;
-      const double dx = xb - st.x[jj], dy = yb - st.y[jj], dz = zb - st.z[jj];
+      const double dx = xb - st.u.s.x[jj], dy = yb - st.u.s.y[jj], dz = zb - st.u.s.z[jj];
       // E = sum_i g_i e_i: the pair's energy enters with (g_i + g_j) (-1/2 C6 f); the
       // vector's gradient per Angstrom carries d r_bohr / d v = v_bohr / (r_bohr bohr)
       const double wsum = BACKWARD ? gi + st.w[jj] : 0.0;
@@ -728,7 +770,7 @@ __device__ __forceinline__ void pair_tile(
       double total;
       const int js = jj - 7 + (lane & 7);
       double* po = partial + (int64_t)it.lt * NP * n_nodes + it.s0 + js;
-      if (lane_finish8(st.red, vs, lane, total) && js < it.scnt)
+      if (lane_finish8(st.u.s.red[wv], vs, lane, total) && js < it.scnt)
         po[(int64_t)(lane >> 3) * n_nodes] = total;
       if (BACKWARD && CELL && lane < 8 && js < it.scnt) {
 #pragma unroll
@@ -736,34 +778,43 @@ __device__ __forceinline__ void pair_tile(
       }
     }
   }
-  if (live) {
-    double* po = partial + (int64_t)it.ls * NP * n_nodes + pi;
-    if (!BACKWARD) {
-      po[0] = e_acc;
-    } else {
+  // the receivers' side, summed over the waves (the staging area is reused for it)
+  if constexpr (W > 1) __syncthreads();
+  double v[NP];
+  if constexpr (!BACKWARD) {
+    v[0] = e_acc;
+  } else {
 #pragma unroll
-      for (int k = 0; k < 3; ++k) po[(int64_t)k * n_nodes] = g3[k];
-      if (CELL) {
-        // n_c = sum_m (v - d)_m inverse(cell in bohr)_mc, the inverse in bohr being bohr
-        // times that in Angstrom
+    for (int k = 0; k < 3; ++k) v[k] = g3[k];
+    if constexpr (CELL) {
 #pragma unroll
-        for (int c = 0; c < 3; ++c)
-#pragma unroll
-          for (int k = 0; k < 3; ++k) {
-            const double t = G.inv[c] * cacc[k] + G.inv[3 + c] * cacc[3 + k] + G.inv[6 + c] * cacc[6 + k];
-            po[(int64_t)(3 + 3 * c + k) * n_nodes] = kBohr * t;
-          }
-      }
+      for (int m = 0; m < 9; ++m) v[3 + m] = cacc[m];
     }
   }
-  if constexpr (BACKWARD) pair_alpha_products<DIAG>(st, it, alpha, order, n_nodes, fsum_out,
-                                                     partial_alpha);
+  if (waves_combine<W>(st.u.comb, v, wv, lane) && live) {
+    double* po = partial + (int64_t)it.ls * NP * n_nodes + pi;
+#pragma unroll
+    for (int k = 0; k < (BACKWARD ? 3 : 1); ++k) po[(int64_t)k * n_nodes] = v[k];
+    if constexpr (BACKWARD && CELL) {
+      // n_c = sum_m (v - d)_m inverse(cell in bohr)_mc, the inverse in bohr being bohr
+      // times that in Angstrom
+#pragma unroll
+      for (int c = 0; c < 3; ++c)
+#pragma unroll
+        for (int k = 0; k < 3; ++k) {
+          const double t = G.inv[c] * v[3 + k] + G.inv[3 + c] * v[6 + k] + G.inv[6 + c] * v[9 + k];
+          po[(int64_t)(3 + 3 * c + k) * n_nodes] = kBohr * t;
+        }
+    }
+  }
+  if constexpr (BACKWARD) pair_alpha_products<DIAG, W>(st, it, alpha, order, n_nodes, fsum_out,
+                                                        partial_alpha);
 }
 
 // The energy kernel (64, 2): at most 256 registers, two waves per SIMD (18 KB of LDS). The
-// backward (64, 3): at most 168 registers, three waves per SIMD (5.5 KB of LDS).
-template <bool BACKWARD, bool CELL>
-__global__ __launch_bounds__(kT, BACKWARD ? 3 : 2) void d4_pair_tiles_kernel(
+// backward (64 W, 3): at most 168 registers, three waves per SIMD.
+template <bool BACKWARD, bool CELL, int W>
+__global__ __launch_bounds__(kT * W, BACKWARD ? 3 : 2) void d4_pair_tiles_kernel(
     const double* __restrict__ pos, const int32_t* __restrict__ species,
     const int64_t* __restrict__ node_ptr, int64_t n_graphs, const double* __restrict__ cell,
     const int32_t* __restrict__ images, const double* __restrict__ r4r2,
@@ -771,42 +822,52 @@ __global__ __launch_bounds__(kT, BACKWARD ? 3 : 2) void d4_pair_tiles_kernel(
     const int32_t* __restrict__ order, const int32_t* __restrict__ tile_ptr, int64_t n_nodes,
     int max_nt, double* __restrict__ partial, double* __restrict__ fsum,
     double* __restrict__ partial_alpha) {
-  __shared__ PairStage<BACKWARD> st;
+  __shared__ PairStage<BACKWARD, W> st;
   TileItem it;
   if (!tile_item(tile_ptr, node_ptr, n_graphs, n_nodes, max_nt, it)) return;
   TileGeo G;
   tile_geo(cell, images, it.b, prm.cutoff * kBohr, G);
   double* fb = BACKWARD ? fsum + ((int64_t)blockIdx.x * max_nt + blockIdx.y) * (kT * kT) : nullptr;
   if (it.ls == it.lt)
-    pair_tile<BACKWARD, CELL, true>(st, it, G, prm, pos, species, r4r2, alpha, g_e2, order,
-                                    n_nodes, partial, fb, partial_alpha);
+    pair_tile<BACKWARD, CELL, true, W>(st, it, G, prm, pos, species, r4r2, alpha, g_e2, order,
+                                       n_nodes, partial, fb, partial_alpha);
   else
-    pair_tile<BACKWARD, CELL, false>(st, it, G, prm, pos, species, r4r2, alpha, g_e2, order,
-                                     n_nodes, partial, fb, partial_alpha);
+    pair_tile<BACKWARD, CELL, false, W>(st, it, G, prm, pos, species, r4r2, alpha, g_e2, order,
+                                        n_nodes, partial, fb, partial_alpha);
 }
 
 // ---------------------------------------------------------------- coordination numbers
 
+// As the pair backward, a work item's sources dealt over the W waves of its block.
+template <int W>
 struct CnStage {
-  double x[kT], y[kT], z[kT];  // bohr
-  double rc[kT], en[kT];       // covalent radius (bohr), electronegativity
-  double w[kT], w2[kT];        // upstream gradients of cn_d4 and cn_raw
   int win[3][kT];
-  double red[8 * 8 * 3];       // lane_finish8
+  union {
+    struct {
+      double x[kT], y[kT], z[kT];  // bohr
+      double rc[kT], en[kT];       // covalent radius (bohr), electronegativity
+      double w[kT], w2[kT];        // upstream gradients of cn_d4 and cn_raw
+      double red[W][8 * 8 * 3];    // lane_finish8, one buffer per wave
+    } s;
+    double comb[W > 1 ? 12 * kT : 1];  // receiver-side sums on their way across waves
+  } u;
 };
 
 // BACKWARD = false: partial[slot][0/1][p] = (cn_d4, cn_raw) sums.
 // BACKWARD = true:  partial[slot][0..2][p] = grad_pos, [3..11] the cell gradient (CELL).
-template <bool BACKWARD, bool CELL, bool DIAG>
+template <bool BACKWARD, bool CELL, bool DIAG, int W>
 __device__ __forceinline__ void cn_tile(
-    CnStage& st, const TileItem& it, const TileGeo& G, const CnParams& prm,
+    CnStage<W>& st, const TileItem& it, const TileGeo& G, const CnParams& prm,
     const double* __restrict__ pos, const int32_t* __restrict__ species,
     const double* __restrict__ rcov, const double* __restrict__ en,
     const double* __restrict__ g_cn, const double* __restrict__ g_raw,
     const int32_t* __restrict__ order, int64_t n_nodes, double* __restrict__ partial) {
   constexpr int NV = BACKWARD ? 3 : 2;
   constexpr int NP = BACKWARD ? (CELL ? 12 : 3) : 2;
-  const int lane = threadIdx.x;
+  constexpr int S = kT / W;  // sources of a wave
+  static_assert(S % 8 == 0, "whole 8-source flushes per wave");
+  const int lane = threadIdx.x % kT, wv = wave_in_block();
+  const int j_lo = wv * S;
   const bool live = lane < it.rcnt;
   const int64_t pi = it.r0 + (live ? lane : 0);
   const int i = order[pi];
@@ -816,8 +877,6 @@ __device__ __forceinline__ void cn_tile(
   const double rci = rcov[si], eni = en[si];
   const double gi = BACKWARD && g_cn ? g_cn[i] : 0.0;
   const double g2i = BACKWARD && g_raw ? g_raw[i] : 0.0;
-  double flo[3], fhi[3];
-  tile_bounds(G, xa, ya, za, live, flo, fhi);
   const double cmax = prm.cut_cn > prm.cut_eeq ? prm.cut_cn : prm.cut_eeq;
   const double cmax2 = cmax * cmax;
   // Beyond r = rc (1 + 27.5 / kcn) the erf argument is below -27.5: the count rounds to exactly
@@ -825,29 +884,34 @@ __device__ __forceinline__ void cn_tile(
   // pairs are skipped: each source's window reaches only as far as its largest rc with the
   // tile's receivers allows, and each pair as far as its own rc allows.
   const double zfac = 1.0 + 27.5 / prm.kcn;
-  const double rc_tile = wave_max(live ? rci : 0.0);
-  if (lane < it.scnt) {
-    const int j = order[it.s0 + lane];
-    const double xs = pos[3 * (int64_t)j], ys = pos[3 * (int64_t)j + 1], zs = pos[3 * (int64_t)j + 2];
-    st.x[lane] = xs * kInvBohr;
-    st.y[lane] = ys * kInvBohr;
-    st.z[lane] = zs * kInvBohr;
-    const int sj = species[j];
-    st.rc[lane] = rcov[sj];
-    st.en[lane] = en[sj];
-    if (BACKWARD) {
-      st.w[lane] = g_cn ? g_cn[j] : 0.0;
-      st.w2[lane] = g_raw ? g_raw[j] : 0.0;
-    }
-    const double r_src = fmin(cmax, (rc_tile + rcov[sj]) * zfac);
-    int win[3];
-    source_windows(G, xs, ys, zs, flo, fhi, win, r_src * kBohr);
+  if (wv == 0) {  // the sources, staged by the first wave
+    double flo[3], fhi[3];
+    tile_bounds(G, xa, ya, za, live, flo, fhi);
+    const double rc_tile = wave_max(live ? rci : 0.0);
+    if (lane < it.scnt) {
+      const int j = order[it.s0 + lane];
+      const double xs = pos[3 * (int64_t)j], ys = pos[3 * (int64_t)j + 1],
+                   zs = pos[3 * (int64_t)j + 2];
+      st.u.s.x[lane] = xs * kInvBohr;
+      st.u.s.y[lane] = ys * kInvBohr;
+      st.u.s.z[lane] = zs * kInvBohr;
+      const int sj = species[j];
+      st.u.s.rc[lane] = rcov[sj];
+      st.u.s.en[lane] = en[sj];
+      if (BACKWARD) {
+        st.u.s.w[lane] = g_cn ? g_cn[j] : 0.0;
+        st.u.s.w2[lane] = g_raw ? g_raw[j] : 0.0;
+      }
+      const double r_src = fmin(cmax, (rc_tile + rcov[sj]) * zfac);
+      int win[3];
+      source_windows(G, xs, ys, zs, flo, fhi, win, r_src * kBohr);
 #pragma unroll
-    for (int c = 0; c < 3; ++c) st.win[c][lane] = win[c];
-  } else {
-    st.win[0][lane] = pack_window(1, 0);
-    st.win[1][lane] = pack_window(0, 0);
-    st.win[2][lane] = pack_window(0, 0);
+      for (int c = 0; c < 3; ++c) st.win[c][lane] = win[c];
+    } else {
+      st.win[0][lane] = pack_window(1, 0);
+      st.win[1][lane] = pack_window(0, 0);
+      st.win[2][lane] = pack_window(0, 0);
+    }
   }
   __syncthreads();
   // a tile pair none of whose sources reaches the receivers' box (most of them, the CN's
@@ -859,13 +923,13 @@ __device__ __forceinline__ void cn_tile(
       reach = window_lo(w0) <= window_hi(w0) && window_lo(w1) <= window_hi(w1) &&
               window_lo(w2) <= window_hi(w2);
     }
-    if (!__any(reach)) {
-      if (live) {
+    if (!__any(reach)) {  // the same answer in every wave of the block
+      if (live && wv == 0) {
         double* po = partial + (int64_t)it.ls * NP * n_nodes + pi;
 #pragma unroll
         for (int k = 0; k < NP; ++k) po[(int64_t)k * n_nodes] = 0.0;
       }
-      if (lane < it.scnt) {
+      if (lane < it.scnt && wv == 0) {
         double* po = partial + (int64_t)it.lt * NP * n_nodes + it.s0 + lane;
 #pragma unroll
         for (int k = 0; k < NP; ++k) po[(int64_t)k * n_nodes] = 0.0;
@@ -879,7 +943,7 @@ __device__ __forceinline__ void cn_tile(
 #pragma unroll
   for (int m = 0; m < 9; ++m) cacc[m] = 0.0;
   LaneTree8<NV> tree;
-  for (int jj = 0; jj < kT; ++jj) {
+  for (int jj = j_lo; jj < j_lo + S; ++jj) {
     double vs[NV];
 #pragma unroll
     for (int k = 0; k < NV; ++k) vs[k] = 0.0;
@@ -889,15 +953,15 @@ __device__ __forceinline__ void cn_tile(
     const int lo0 = window_lo(w0), hi0 = window_hi(w0), lo1 = window_lo(w1), hi1 = window_hi(w1),
               lo2 = window_lo(w2), hi2 = window_hi(w2);
     if (lo0 <= hi0 && lo1 <= hi1 && lo2 <= hi2) {
-      const double rc = rci + st.rc[jj];
-      const double den = fabs(eni - st.en[jj]) + prm.k5;
+      const double rc = rci + st.u.s.rc[jj];
+      const double den = fabs(eni - st.u.s.en[jj]) + prm.k5;
       const double enf = prm.k4 * exp(-den * den * inv_k6);
       // per pair: k0 / rc and the erf count's slope factor -k0 / (rc sqrt(pi))
       const double k_rc = prm.kcn / rc;
       const double dk = -k_rc * kInvSqrtPi;
-      const double dx = xb - st.x[jj], dy = yb - st.y[jj], dz = zb - st.z[jj];
-      const double wsum = BACKWARD ? gi + st.w[jj] : 0.0;
-      const double w2sum = BACKWARD ? g2i + st.w2[jj] : 0.0;
+      const double dx = xb - st.u.s.x[jj], dy = yb - st.u.s.y[jj], dz = zb - st.u.s.z[jj];
+      const double wsum = BACKWARD ? gi + st.u.s.w[jj] : 0.0;
+      const double w2sum = BACKWARD ? g2i + st.u.s.w2[jj] : 0.0;
       const double reach2 = fmin(cmax2, rc * zfac * (rc * zfac));
       double c_cn = 0.0, c_eeq = 0.0;          // counts within the two cutoffs
       double sv[3] = {0.0, 0.0, 0.0};          // sum of the weighted gradients
@@ -978,7 +1042,7 @@ __device__ __forceinline__ void cn_tile(
       double total;
       const int js = jj - 7 + (lane & 7);
       double* po = partial + (int64_t)it.lt * NP * n_nodes + it.s0 + js;
-      if (lane_finish8(st.red, vs, lane, total) && js < it.scnt)
+      if (lane_finish8(st.u.s.red[wv], vs, lane, total) && js < it.scnt)
         po[(int64_t)(lane >> 3) * n_nodes] = total;
       if (BACKWARD && CELL && lane < 8 && js < it.scnt) {
 #pragma unroll
@@ -986,29 +1050,38 @@ __device__ __forceinline__ void cn_tile(
       }
     }
   }
-  if (live) {
+  // the receivers' side, summed over the waves (the staging area is reused for it)
+  if constexpr (W > 1) __syncthreads();
+  double v[NP];
+  if constexpr (!BACKWARD) {
+    v[0] = acc[0];
+    v[1] = acc[1];
+  } else {
+#pragma unroll
+    for (int k = 0; k < 3; ++k) v[k] = g3[k];
+    if constexpr (CELL) {
+#pragma unroll
+      for (int m = 0; m < 9; ++m) v[3 + m] = cacc[m];
+    }
+  }
+  if (waves_combine<W>(st.u.comb, v, wv, lane) && live) {
     double* po = partial + (int64_t)it.ls * NP * n_nodes + pi;
-    if (!BACKWARD) {
-      po[0] = acc[0];
-      po[n_nodes] = acc[1];
-    } else {
 #pragma unroll
-      for (int k = 0; k < 3; ++k) po[(int64_t)k * n_nodes] = g3[k];
-      if (CELL) {
+    for (int k = 0; k < (BACKWARD ? 3 : 2); ++k) po[(int64_t)k * n_nodes] = v[k];
+    if constexpr (BACKWARD && CELL) {
 #pragma unroll
-        for (int c = 0; c < 3; ++c)
+      for (int c = 0; c < 3; ++c)
 #pragma unroll
-          for (int k = 0; k < 3; ++k) {
-            const double t = G.inv[c] * cacc[k] + G.inv[3 + c] * cacc[3 + k] + G.inv[6 + c] * cacc[6 + k];
-            po[(int64_t)(3 + 3 * c + k) * n_nodes] = kBohr * t;
-          }
-      }
+        for (int k = 0; k < 3; ++k) {
+          const double t = G.inv[c] * v[3 + k] + G.inv[3 + c] * v[6 + k] + G.inv[6 + c] * v[9 + k];
+          po[(int64_t)(3 + 3 * c + k) * n_nodes] = kBohr * t;
+        }
     }
   }
 }
 
-template <bool BACKWARD, bool CELL>
-__global__ __launch_bounds__(kT, 3) void d4_cn_tiles_kernel(
+template <bool BACKWARD, bool CELL, int W>
+__global__ __launch_bounds__(kT * W, 3) void d4_cn_tiles_kernel(
     const double* __restrict__ pos, const int32_t* __restrict__ species,
     const int64_t* __restrict__ node_ptr, int64_t n_graphs, const double* __restrict__ cell,
     const int32_t* __restrict__ images, const double* __restrict__ rcov,
@@ -1016,18 +1089,18 @@ __global__ __launch_bounds__(kT, 3) void d4_cn_tiles_kernel(
     const double* __restrict__ g_raw, const int32_t* __restrict__ order,
     const int32_t* __restrict__ tile_ptr, int64_t n_nodes, int max_nt,
     double* __restrict__ partial) {
-  __shared__ CnStage st;
+  __shared__ CnStage<W> st;
   TileItem it;
   if (!tile_item(tile_ptr, node_ptr, n_graphs, n_nodes, max_nt, it)) return;
   TileGeo G;
   const double cmax = prm.cut_cn > prm.cut_eeq ? prm.cut_cn : prm.cut_eeq;
   tile_geo(cell, images, it.b, cmax * kBohr, G);
   if (it.ls == it.lt)
-    cn_tile<BACKWARD, CELL, true>(st, it, G, prm, pos, species, rcov, en, g_cn, g_raw, order,
-                                  n_nodes, partial);
+    cn_tile<BACKWARD, CELL, true, W>(st, it, G, prm, pos, species, rcov, en, g_cn, g_raw, order,
+                                     n_nodes, partial);
   else
-    cn_tile<BACKWARD, CELL, false>(st, it, G, prm, pos, species, rcov, en, g_cn, g_raw, order,
-                                   n_nodes, partial);
+    cn_tile<BACKWARD, CELL, false, W>(st, it, G, prm, pos, species, rcov, en, g_cn, g_raw, order,
+                                      n_nodes, partial);
 }
 
 // ---------------------------------------------------------------- image counts
@@ -1221,6 +1294,24 @@ void launch_reduce(std::initializer_list<ReduceTarget> targets, int64_t n_nodes,
 
 dim3 tiles_grid(const TilesWs& w) { return dim3((unsigned)w.grid_tiles, (unsigned)w.max_nt); }
 
+// waves per block of the pair backward: two (measured on the C5 box against one and four:
+// 396 us, 436 us, 399 us)
+constexpr int kPairWaves = 2;
+constexpr int kCnWaves = 2;   // the same for the coordination-number kernels
+
+void launch_pair_backward(bool with_cell, dim3 grid, hipStream_t s, const double* pos,
+                          const int32_t* species, const int64_t* node_ptr, int64_t n_graphs,
+                          const double* cell, const int32_t* images, const double* r4r2,
+                          const double* alpha, const PairParams& p, const double* g_e2,
+                          const int32_t* order, const int32_t* tile_ptr, int64_t n_nodes,
+                          int max_nt, double* partial, double* fsum, double* partial_alpha) {
+  auto k = with_cell ? d4_pair_tiles_kernel<true, true, kPairWaves>
+                     : d4_pair_tiles_kernel<true, false, kPairWaves>;
+  hipLaunchKernelGGL(k, grid, dim3(kT * kPairWaves), 0, s, pos, species, node_ptr, n_graphs, cell,
+                     images, r4r2, alpha, p, g_e2, order, tile_ptr, n_nodes, max_nt, partial, fsum,
+                     partial_alpha);
+}
+
 }  // namespace
 
 size_t d4_tiles_workspace_bytes(int64_t n_nodes, int64_t n_graphs, int64_t max_atoms) {
@@ -1255,7 +1346,8 @@ int xnn_d4_coordination(const double* pos, int64_t n_nodes, const int32_t* speci
   const CnParams p{prm->cutoff_cn, prm->cutoff_eeq_cn, prm->kcn, prm->k4, prm->k5, prm->k6};
   hipStream_t s = as_hip(stream);
   launch_order(pos, n_nodes, node_ptr, n_graphs, cell, images, plan, w, s);
-  hipLaunchKernelGGL((d4_cn_tiles_kernel<false, false>), tiles_grid(w), dim3(kT), 0, s, pos,
+  hipLaunchKernelGGL((d4_cn_tiles_kernel<false, false, kCnWaves>), tiles_grid(w),
+                     dim3(kT * kCnWaves), 0, s, pos,
                      species, node_ptr, n_graphs, cell, images, rcov, en, p, nullptr, nullptr,
                      w.order, w.tile_ptr, n_nodes, w.max_nt, w.partial);
   launch_reduce({{w.partial, cn_d4, 2, 0, 1}, {w.partial, cn_raw, 2, 1, 1}}, n_nodes, w, batch,
@@ -1288,8 +1380,10 @@ int xnn_d4_coordination_backward(const double* pos, int64_t n_nodes, const int32
   const CnParams p{prm->cutoff_cn, prm->cutoff_eeq_cn, prm->kcn, prm->k4, prm->k5, prm->k6};
   hipStream_t s = as_hip(stream);
   launch_order(pos, n_nodes, node_ptr, n_graphs, cell, images, plan, w, s);
-  auto k = with_cell ? d4_cn_tiles_kernel<true, true> : d4_cn_tiles_kernel<true, false>;
-  hipLaunchKernelGGL(k, tiles_grid(w), dim3(kT), 0, s, pos, species, node_ptr, n_graphs, cell,
+  auto k = with_cell ? d4_cn_tiles_kernel<true, true, kCnWaves>
+                     : d4_cn_tiles_kernel<true, false, kCnWaves>;
+  hipLaunchKernelGGL(k, tiles_grid(w), dim3(kT * kCnWaves), 0, s, pos, species, node_ptr, n_graphs,
+                     cell,
                      images, rcov, en, p, g_cn_d4, g_cn_raw, w.order, w.tile_ptr, n_nodes,
                      w.max_nt, w.partial);
   launch_reduce({{w.partial, grad_pos, np, 0, 3}, {w.partial, cell_partial, np, 3, 9}}, n_nodes, w,
@@ -1318,7 +1412,7 @@ int xnn_d4_two_body(const double* pos, int64_t n_nodes, const int32_t* species,
   const PairParams p{prm->s6, prm->s8, prm->a1, prm->a2, prm->cutoff, prm->width};
   hipStream_t s = as_hip(stream);
   launch_order(pos, n_nodes, node_ptr, n_graphs, cell, images, plan, w, s);
-  hipLaunchKernelGGL((d4_pair_tiles_kernel<false, false>), tiles_grid(w), dim3(kT), 0, s, pos,
+  hipLaunchKernelGGL((d4_pair_tiles_kernel<false, false, 1>), tiles_grid(w), dim3(kT), 0, s, pos,
                      species, node_ptr, n_graphs, cell, images, r4r2, alpha, p, nullptr, w.order,
                      w.tile_ptr, n_nodes, w.max_nt, w.partial, nullptr, nullptr);
   launch_reduce({{w.partial, e2, 1, 0, 1}}, n_nodes, w, batch, node_ptr, s);
@@ -1351,10 +1445,9 @@ int xnn_d4_two_body_backward(const double* pos, int64_t n_nodes, const int32_t* 
   const PairParams p{prm->s6, prm->s8, prm->a1, prm->a2, prm->cutoff, prm->width};
   hipStream_t s = as_hip(stream);
   launch_order(pos, n_nodes, node_ptr, n_graphs, cell, images, plan, w, s);
-  auto k = with_cell ? d4_pair_tiles_kernel<true, true> : d4_pair_tiles_kernel<true, false>;
-  hipLaunchKernelGGL(k, tiles_grid(w), dim3(kT), 0, s, pos, species, node_ptr, n_graphs, cell,
-                     images, r4r2, alpha, p, g_e2, w.order, w.tile_ptr, n_nodes, w.max_nt,
-                     w.partial, w.fsum, w.partial_alpha);
+  launch_pair_backward(with_cell, tiles_grid(w), s, pos, species, node_ptr, n_graphs, cell, images,
+                       r4r2, alpha, p, g_e2, w.order, w.tile_ptr, n_nodes, w.max_nt, w.partial,
+                       w.fsum, w.partial_alpha);
   launch_reduce({{w.partial, grad_pos, np, 0, 3}, {w.partial, cell_partial, np, 3, 9},
                  {w.partial_alpha, grad_alpha, kNW, 0, kNW}},
                 n_nodes, w, batch, node_ptr, s);
