@@ -201,7 +201,7 @@ def test_c5_charges_large_regime(tables):
     assert abs(e1 - e3) <= 1e-6 * abs(e3), (e1, e3)
 
 
-@pytest.mark.parametrize("n", [1, 128, 300, 700])
+@pytest.mark.parametrize("n", [1, 128, 300, 700, 1100])
 def test_blocked_cholesky_matches_lapack(n):
     """The device factorization (128-column diagonal blocks in LDS, library GEMMs for the
     panel and trailing updates) against LAPACK's on the CPU, at sizes with a partial last
