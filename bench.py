@@ -624,6 +624,9 @@ def bench_d4(steps: int, warmup: int, cpu: bool = True, graph: bool = True) -> d
               "vs_baseline": None, "dtype": "f64", "data": "synthetic (seeded generator)",
               "config": {"workload": "d4_organic_box_5000_atoms", "atoms": N,
                          "pair_image_terms": n_terms, "cn_terms": n_cn,
+                         # within-cutoff pair-image terms over the 27 N^2 candidates of the
+                         # 3 x 3 x 3 image block (the kernels test per-source image windows)
+                         "candidate_test_efficiency": round(n_terms / (27.0 * N * N), 4),
                          "cutoff_pair_bohr": 60.0, "cutoff_cn_bohr": 25.0,
                          "cutoff_eeq_cn_bohr": 25.0,
                          "charges": "EEQ charges (large regime: HIP real-space Ewald matrix, "
