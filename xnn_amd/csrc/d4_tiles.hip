@@ -490,7 +490,7 @@ __device__ __forceinline__ bool waves_combine(double* __restrict__ comb, double 
 }
 
 // dE/d alpha(i w) of both atoms of every pair of the work item, from the pairs' image sums
-// of f(r) this wave left in its block: dE/d C6_ij = -1/2 (g_i + g_j) fsum_ij =: K_ij and
+// of f(r) the block's waves left in its workspace block: dE/d C6_ij = -1/2 (g_i + g_j) fsum_ij =: K_ij and
 // d C6_ij / d alpha_i(w) = cp3(w) alpha_j(w), so
 //   receivers: D_r[r][w] = sum_s K[s][r] cp3(w) alpha_s(w)   (64 x 23, K = 64 sources)
 //   sources:   D_s[s][w] = sum_r K[s][r] cp3(w) alpha_r(w)   (tile pairs d > 0 only)
@@ -503,14 +503,14 @@ typedef double doublex4 __attribute__((ext_vector_type(4)));
 template <bool DIAG, int W>
 __device__ __forceinline__ void pair_alpha_products(
     const PairStage<true, W>& st, const TileItem& it, const double* __restrict__ alpha,
-    const int32_t* __restrict__ order, int64_t n_nodes, const double* __restrict__ fb,
-    double* __restrict__ partial_alpha) {
+    int64_t n_nodes, const double* __restrict__ fb, double* __restrict__ partial_alpha) {
   __syncthreads();  // the block's rows, written by every lane, read across lanes and waves
   const int lane = threadIdx.x % kT, lo = lane & 15, hi = lane >> 4, wv = wave_in_block();
 #pragma unroll 1
   for (int side = 0; side < (DIAG ? 1 : 2); ++side) {
-    // side 0: output rows the receivers, contracted over the sources (K read down a row);
-    // side 1: output rows the sources, contracted over the receivers (K read across)
+    // side 0: output rows the receivers, contracted over the sources (an A load reads 16
+    // consecutive doubles of four rows of K); side 1: output rows the sources, contracted
+    // over the receivers (an A load reads four consecutive doubles of 16 rows)
     const int out_cnt = side == 0 ? it.rcnt : it.scnt;
     const int b_cnt = side == 0 ? it.scnt : it.rcnt;
     const int* __restrict__ bid = st.id[1 - side];
@@ -807,7 +807,7 @@ __device__ __forceinline__ void pair_tile(
         }
     }
   }
-  if constexpr (BACKWARD) pair_alpha_products<DIAG, W>(st, it, alpha, order, n_nodes, fsum_out,
+  if constexpr (BACKWARD) pair_alpha_products<DIAG, W>(st, it, alpha, n_nodes, fsum_out,
                                                         partial_alpha);
 }
 
