@@ -374,6 +374,7 @@ constexpr int kCholBlock = 128;
 constexpr int kCholThreads = 512;
 constexpr int kCholP = kCholBlock / (kCholThreads / 32);  // row groups of 16
 constexpr int kCholQ = kCholBlock / 32;                   // column groups of 32
+static_assert(kCholP == 8 && kCholQ == 4, "the pivot publish switches list 8 and 4 groups");
 
 // 1 / d for a positive normal d: the hardware estimate refined by two Newton steps
 // r <- r + r (1 - d r) (each squares the relative error), on the barrier-bound path of the
@@ -476,27 +477,51 @@ __global__ __launch_bounds__(kCholThreads) void eeq_cholesky_block_kernel(
     const int jn = j + 2;
     if (jn < b) {
       const int nb = (step + 1) & 1;
+      // jn is even, so columns jn and jn + 1 lie in one register column group and E rows jn
+      // and jn + 1 in one row group: a uniform switch picks the registers, two lanes of each
+      // 32 write the columns and two thread rows the E rows. The columns' rows above jn go
+      // out too: every later update takes them with zero column factors.
+      const int qs = __builtin_amdgcn_readfirstlane(jn >> 5);
+      const int ps = __builtin_amdgcn_readfirstlane(jn >> 4);
+      double vc[kCholP], er[kCholQ];
+      switch (qs) {
+#define XNN_CHOL_COL(Q)                                          \
+  case Q:                                                        \
+    _Pragma("unroll") for (int p = 0; p < kCholP; ++p) vc[p] = v[p][Q]; \
+    break;
+        XNN_CHOL_COL(0)
+        XNN_CHOL_COL(1)
+        XNN_CHOL_COL(2)
+        default:
 #pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        const int cn = jn + h;  // column and E row published in slot h
-        if (cn >= kCholBlock) continue;
-        if (tx == (cn & 31)) {
+          for (int p = 0; p < kCholP; ++p) vc[p] = v[p][kCholQ - 1];
+      }
+#undef XNN_CHOL_COL
+      switch (ps) {
+#define XNN_CHOL_ROW(P)                                          \
+  case P:                                                        \
+    _Pragma("unroll") for (int q = 0; q < kCholQ; ++q) er[q] = e[P][q]; \
+    break;
+        XNN_CHOL_ROW(0)
+        XNN_CHOL_ROW(1)
+        XNN_CHOL_ROW(2)
+        XNN_CHOL_ROW(3)
+        XNN_CHOL_ROW(4)
+        XNN_CHOL_ROW(5)
+        XNN_CHOL_ROW(6)
+        default:
 #pragma unroll
-          for (int q = 0; q < kCholQ; ++q)
-            if (q == (cn >> 5)) {
+          for (int q = 0; q < kCholQ; ++q) er[q] = e[kCholP - 1][q];
+      }
+#undef XNN_CHOL_ROW
+      const int hc = tx - (jn & 31), hr = ty - (jn & 15);
+      if (hc == 0 || hc == 1) {
 #pragma unroll
-              for (int p = 0; p < kCholP; ++p)
-                if (ty + 16 * p >= jn) col_buf[nb][h][ty + 16 * p] = v[p][q];
-            }
-        }
-        if (ty == (cn & 15)) {
+        for (int p = 0; p < kCholP; ++p) col_buf[nb][hc][ty + 16 * p] = vc[p];
+      }
+      if (hr == 0 || hr == 1) {
 #pragma unroll
-          for (int p = 0; p < kCholP; ++p)
-            if (p == (cn >> 4)) {
-#pragma unroll
-              for (int q = 0; q < kCholQ; ++q) row_buf[nb][h][tx + 32 * q] = e[p][q];
-            }
-        }
+        for (int q = 0; q < kCholQ; ++q) row_buf[nb][hr][tx + 32 * q] = er[q];
       }
     }
   }
