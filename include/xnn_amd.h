@@ -909,8 +909,9 @@ int xnn_atm_plan(const int64_t* edge_index, int64_t n_edges, int64_t n_atoms, vo
 int xnn_atm_work_size(int64_t n_edges, int64_t n_atoms, int32_t k, int32_t backward,
                       size_t* bytes);
 
-/* Per-atom ATM energies (N) in hartree, summed with atomics (the order of the sums is
- * not fixed). max_tiles, has_repeats: info[0], info[1] of the plan. (atm.py:84-162) */
+/* Per-atom ATM energies (N) in hartree, summed with atomics as reproducible head/tail
+ * sums (the same bits in any order). max_tiles, has_repeats: info[0], info[1] of the plan.
+ * (atm.py:84-162) */
 int xnn_atm_energy(const void* plan, int64_t n_edges, int64_t n_atoms, int64_t max_tiles,
                    int64_t has_repeats, const double* edge_vec, const double* feat_a,
                    const double* feat_b, int32_t k, const int32_t* species, const double* table,
@@ -926,6 +927,24 @@ int xnn_atm_energy_backward(const void* plan, int64_t n_edges, int64_t n_atoms,
                             const xnn_atm_params* prm, const double* grad_energy,
                             double* grad_vec, double* grad_fa, double* grad_fb, void* work,
                             size_t work_bytes, xnn_stream_t stream);
+
+/* Bytes of the workspace of xnn_atm_energy_backward_tangent. */
+int xnn_atm_tangent_work_size(int64_t n_edges, int64_t n_atoms, int32_t k, size_t* bytes);
+
+/* Second derivatives along a direction (edge_vec_t (E,3) in the input edge order,
+ * feat_a_t, feat_b_t (N,k)): energy_t (N) = the derivative of the per-atom energies along
+ * it, and grad_vec_t (E,3), grad_fa_t, grad_fb_t (N,k) = the derivatives of the gradients
+ * of sum_i grad_energy[i] E_i (xnn_atm_energy_backward) along it at fixed grad_energy, a
+ * Hessian-vector product. Reproducible sums. Replaces the tangent kernels of
+ * dispersion_fast/atm_tangents.py (_atm_forward_t, _atm_backward_t) as _ATMGrad.backward
+ * calls them (dispersion_fast/atm.py:475-509). */
+int xnn_atm_energy_backward_tangent(
+    const void* plan, int64_t n_edges, int64_t n_atoms, int64_t max_tiles, int64_t has_repeats,
+    const double* edge_vec, const double* feat_a, const double* feat_b, int32_t k,
+    const int32_t* species, const double* table, int32_t n_species, const xnn_atm_params* prm,
+    const double* grad_energy, const double* edge_vec_t, const double* feat_a_t,
+    const double* feat_b_t, double* energy_t, double* grad_vec_t, double* grad_fa_t,
+    double* grad_fb_t, void* work, size_t work_bytes, xnn_stream_t stream);
 
 /* Measurement, no counterpart in the reference: counts[0] = edge pairs the distinct-
  * triangle walk tests, counts[1] = distinct triangles it keeps (third side within the

@@ -305,3 +305,75 @@ def test_atm_is_reproducible_bit_for_bit(system):
     assert float(first[0].abs().max()) > 0
     for name, a, b in zip(("energy", "grad_pos", "grad_feat", "grad_cell"), first, second):
         assert torch.equal(a, b), name
+
+
+def _second(c, dev, same, width_aa, seed=11):
+    """Second derivatives of a force-loss-like scalar through the ATM energies: with
+    L1 = sum_i go_i E_i and g = dL1/d(pos, feat[, cell]) formed with create_graph,
+    L2 = <g, (U, V[, C])>, the gradients of L2 in pos, feat, go[, cell] (the Hessian of L1
+    times the direction, and the energies' derivative along it)."""
+    from xnn_amd import dispersion as XD
+    g = torch.Generator().manual_seed(seed)
+    n, k = c["fa"].shape
+    go = (torch.rand(n, dtype=torch.float64, generator=g) + 0.5).to(dev).requires_grad_(True)
+    U = torch.randn(n, 3, dtype=torch.float64, generator=g).to(dev)
+    V = torch.randn(n, k, dtype=torch.float64, generator=g).to(dev)
+    C = torch.randn(3, 3, dtype=torch.float64, generator=g).to(dev)
+    pos, cell, vec = _geometry(c, dev)
+    fa = c["fa"].to(dev).clone().requires_grad_(True)
+    fb = fa if same else fa @ c["mix"].to(dev)
+    if dev == "cpu":
+        e = D.atm_edges(c["ei"], vec, fa, fb, c["species"], c["table"], 1.0, 16.0 / 3.0,
+                        c["cutoff"], c["width"], c["n"])
+    else:
+        consts = XD.ATMConstants(c["species"].to(dev), c["table"].to(dev), 1.0, 16.0 / 3.0,
+                                 c["cutoff"], c["width"])
+        e = XD.atm_energy(c["ei"].to(dev), vec, fa, fb, consts, c["n"])
+    wrt = [pos, fa] + ([] if cell is None else [cell])
+    first = torch.autograd.grad((e * go).sum(), wrt, create_graph=True)
+    l2 = (first[0] * U).sum() + (first[1] * V).sum()
+    if cell is not None:
+        l2 = l2 + (first[2] * C).sum()
+    out = torch.autograd.grad(l2, wrt + [go])
+    if dev != "cpu":
+        torch.cuda.synchronize()
+    return [x.detach().cpu() for x in out]
+
+
+@pytest.mark.parametrize("system", list(SYSTEMS))
+@pytest.mark.parametrize("same,width_aa", [(False, 1.0), (True, 0.0)])
+def test_atm_second_derivatives_match_the_oracle(system, same, width_aa):
+    """The ATM gradient is itself differentiable (dispersion_fast/atm.py:446-509): the
+    Hessian-vector products in positions, factors and cell and the derivative in the
+    energy cotangents, against autograd's second derivatives of the oracle's edge-list
+    formula; every plan mode (repeated-atom triangles in the 2^3 and 3^3 cells), both
+    switches, shared and separate factor matrices. Tolerance 1e-10 of the largest value
+    (forward-mode numbers through the closed-form gradient vs. autograd's reverse-over-
+    reverse: different rounding paths)."""
+    print(f"[atm second] {system} same={same} width={width_aa}", flush=True)
+    c = _case(system, k=23, width_aa=width_aa)
+    ref = _second(c, "cpu", same, width_aa)
+    out = _second(c, "cuda:0", same, width_aa)
+    names = ["pos", "feat"] + (["cell"] if c["cell"] is not None else []) + ["go"]
+    for name, a, b in zip(names, out, ref):
+        assert float(b.abs().max()) > 0, name
+        assert _rel(a, b) < 1e-10, (name, _rel(a, b))
+    again = _second(c, "cuda:0", same, width_aa)
+    for name, a, b in zip(names, out, again):
+        assert torch.equal(a, b), f"{name}: the second derivatives differ run to run"
+
+
+def test_atm_third_derivative_is_refused():
+    """Second derivatives with a graph of their own (a third derivative) are refused, as
+    the reference's once_differentiable tangent backward does (atm.py:494)."""
+    from xnn_amd import dispersion as XD
+    c = _case("cluster", k=23)
+    dev = "cuda:0"
+    pos, _, vec = _geometry(c, dev)
+    fa = c["fa"].to(dev)
+    consts = XD.ATMConstants(c["species"].to(dev), c["table"].to(dev), 1.0, 16.0 / 3.0,
+                             c["cutoff"], c["width"])
+    e = XD.atm_energy(c["ei"].to(dev), vec, fa, fa, consts, c["n"])
+    (g,) = torch.autograd.grad(e.sum(), [pos], create_graph=True)
+    with pytest.raises(RuntimeError, match="differentiable twice"):
+        torch.autograd.grad((g * g).sum(), [pos], create_graph=True)

@@ -170,6 +170,10 @@ _SIGNATURES = {
                        ctypes.POINTER(AtmParams), vp, vp, sz, vp],
     "xnn_atm_energy_backward": [vp, i64, i64, i64, i64, vp, vp, vp, i32, vp, vp, i32,
                                 ctypes.POINTER(AtmParams), vp, vp, vp, vp, vp, sz, vp],
+    "xnn_atm_tangent_work_size": [i64, i64, i32, ctypes.POINTER(sz)],
+    "xnn_atm_energy_backward_tangent": [vp, i64, i64, i64, i64, vp, vp, vp, i32, vp, vp, i32,
+                                        ctypes.POINTER(AtmParams), vp, vp, vp, vp, vp, vp, vp,
+                                        vp, vp, sz, vp],
     "xnn_node_readout_backward": [i32, vp, i64, i64, i64, vp, vp, vp],
     "xnn_d4_polarizabilities": [i64, vp, vp, vp, ctypes.POINTER(D4AlphaTables), vp, vp],
     "xnn_d4_polarizabilities_backward": [i64, vp, vp, vp, ctypes.POINTER(D4AlphaTables), vp, vp,

@@ -10,6 +10,10 @@
 //                                  of dispersion.py:183-222)
 // xnn_atm_energy_backward          their gradients in the edge vectors and in both C6
 //                                  factor matrices (atm.py:165-294, 402-443)
+// xnn_atm_tangent_work_size, xnn_atm_energy_backward_tangent
+//                                  second derivatives: the tangents of the energies and
+//                                  of those gradients along a direction (atm.py:475-509,
+//                                  atm_tangents.py)
 //
 // Bookkeeping (dispersion.py:253-270, 343-398): a triangle of three distinct atoms is
 // evaluated once, from its smallest-index corner c (the pairs among c's edges to
@@ -485,11 +489,8 @@ __device__ __forceinline__ double atm_wave_sum(double v, const AtmLanes&) {
 // f[i ^ ((lane >> 1) & 7)], so that at every halving the lane keeps its first half and
 // receives its partner's second half, which holds the same slots: no selects.
 // fp[i][lane] lives in LDS (a column per lane: conflict-free, and 64 registers fewer).
-__device__ __forceinline__ double atm_fold32(const double (*fp)[kWave], int lane, double g,
-                                             const AtmLanes&) {
-  double p[16];
-#pragma unroll
-  for (int i = 0; i < 16; ++i) p[i] = atm_swap32_sum(g * fp[i][lane], g * fp[i + 16][lane]);
+// atm_fold16 is every halving after the first, atm_fold32 the whole fold.
+__device__ __forceinline__ double atm_fold16(double (&p)[16]) {
 #pragma unroll
   for (int i = 0; i < 8; ++i) p[i] = atm_swap16_sum(p[i], p[i + 8]);
 #pragma unroll
@@ -498,6 +499,26 @@ __device__ __forceinline__ double atm_fold32(const double (*fp)[kWave], int lane
   for (int i = 0; i < 2; ++i) p[i] += atm_xor4(p[i + 2]);
   p[0] += atm_dpp<kDppXor2>(p[1]);
   return p[0] + atm_dpp<kDppXor1>(p[0]);
+}
+
+__device__ __forceinline__ double atm_fold32(const double (*fp)[kWave], int lane, double g,
+                                             const AtmLanes&) {
+  double p[16];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) p[i] = atm_swap32_sum(g * fp[i][lane], g * fp[i + 16][lane]);
+  return atm_fold16(p);
+}
+
+// The same sums of g * f[s] + h * u[s] (two permuted tables, one fold).
+__device__ __forceinline__ double atm_fold32x2(const double (*fp)[kWave],
+                                               const double (*up)[kWave], int lane, double g,
+                                               double h) {
+  double p[16];
+#pragma unroll
+  for (int i = 0; i < 16; ++i)
+    p[i] = atm_swap32_sum(fma(h, up[i][lane], g * fp[i][lane]),
+                          fma(h, up[i + 16][lane], g * fp[i + 16][lane]));
+  return atm_fold16(p);
 }
 
 // The wave-wide sums of four per-lane values: lanes 16 s .. 16 s + 15 return slot s.
@@ -906,6 +927,383 @@ __global__ __launch_bounds__(kAtmWaves * kWave) void atm_count_kernel(
   }
 }
 
+// ------------------------------------------------------------------------------ tangents
+// Second derivatives (dispersion_fast/atm.py:475-509, atm_tangents.py): along a direction
+// (edge vectors, both factor matrices), the derivative of the per-atom energies and of the
+// gradient of sum_i go_i E_i at fixed go, i.e. the Hessian of that sum times the direction.
+// Every quantity of a triangle's energy and of its closed-form gradient (atm_triangle)
+// carries its derivative along the direction as a forward-mode number, so those formulas
+// are differentiated exactly as written. Sums are the reproducible head/tail sums.
+
+struct AtmDual {
+  double v, t;   // value, derivative along the direction
+};
+using Dl = AtmDual;
+__device__ __forceinline__ Dl operator+(Dl a, Dl b) { return {a.v + b.v, a.t + b.t}; }
+__device__ __forceinline__ Dl operator-(Dl a, Dl b) { return {a.v - b.v, a.t - b.t}; }
+__device__ __forceinline__ Dl operator-(Dl a) { return {-a.v, -a.t}; }
+__device__ __forceinline__ Dl operator*(Dl a, Dl b) { return {a.v * b.v, fma(a.v, b.t, a.t * b.v)}; }
+__device__ __forceinline__ Dl operator*(double s, Dl a) { return {s * a.v, s * a.t}; }
+__device__ __forceinline__ Dl operator+(Dl a, double s) { return {a.v + s, a.t}; }
+__device__ __forceinline__ Dl operator/(Dl a, Dl b) {
+  const double r = 1.0 / b.v, q = a.v * r;
+  return {q, (a.t - q * b.t) * r};
+}
+__device__ __forceinline__ Dl dl_rcp(Dl a) {
+  const double r = 1.0 / a.v;
+  return {r, -a.t * r * r};
+}
+__device__ __forceinline__ Dl dl_sqrt(Dl a) {
+  const double s = sqrt(a.v);
+  return {s, a.v > 0.0 ? 0.5 * a.t / s : 0.0};
+}
+__device__ __forceinline__ Dl dl_rsqrt(Dl a) {
+  const double r = 1.0 / sqrt(a.v);
+  return {r, -0.5 * a.t * r / a.v};
+}
+// a^p, a > 0
+__device__ __forceinline__ Dl dl_pow(Dl a, double p) {
+  const double v = exp(p * log(a.v));
+  return {v, p * v * a.t / a.v};
+}
+// a / b with the kernels' guard: b = 0 divides by one
+__device__ __forceinline__ Dl dl_over(Dl a, Dl b) {
+  return b.v != 0.0 ? a / b : a;
+}
+
+// the switch of one side and its slope in r^2 (switch_d, width > 0), from r^2
+__device__ __forceinline__ void atm_switch_t(Dl r2, const AtmConst& kc, Dl& sw, Dl& dsw2) {
+  const Dl r = dl_sqrt(r2);
+  const Dl u = (1.0 / kc.width) * (Dl{kc.cutoff, 0.0} - r);
+  if (u.v >= 1.0 || u.v <= 0.0) {
+    sw = {u.v >= 1.0 ? 1.0 : 0.0, 0.0};
+    dsw2 = {0.0, 0.0};
+    return;
+  }
+  sw = u * u * u * ((6.0 * u + (-15.0)) * u + 10.0);
+  const Dl om = Dl{1.0, 0.0} - u;
+  const Dl dsw = (-30.0 / kc.width) * (u * u * om * om);
+  dsw2 = 0.5 * (r.v > 0.0 ? dsw / r : Dl{0.0, 0.0});
+}
+
+// atm_triangle's energy and derivatives in x, y, w at unit weight, as forward-mode numbers;
+// c9sq = |C6_cj C6_ck C6_jk|, the three switches and their slopes in the squared sides
+// given for the two walked sides (the third from w).
+template <bool SWITCH>
+__device__ __forceinline__ void atm_triangle_t(const AtmConst& kc, Dl x, Dl y, Dl w, Dl c9sq,
+                                               double r0, Dl swa, Dl swb, Dl dswa, Dl dswb,
+                                               Dl& e, Dl& gx, Dl& gy, Dl& gw) {
+  const Dl s = dl_rsqrt(x * y * w);
+  const Dl s2 = s * s;
+  const Dl s3 = s2 * s;
+  const Dl s5 = s3 * s2;
+  const Dl t = dl_pow(r0 * s, kc.alp3);
+  const Dl damp = dl_rcp(6.0 * t + 1.0);
+  const Dl f1 = x + w - y, f2 = x - w + y, f3 = w + y - x;
+  const Dl nn = f1 * f2 * f3;
+  const Dl ang = 0.375 * nn * s5 + s3;
+  Dl swjk{1.0, 0.0}, dswjk{0.0, 0.0};
+  if (SWITCH) atm_switch_t(w, kc, swjk, dswjk);
+  const Dl sw = swa * swb * swjk;
+  const Dl base = kc.s9_3 * dl_sqrt(c9sq);
+  e = base * ang * damp * sw;
+  const Dl ix = dl_rcp(x), iy = dl_rcp(y), iw = dl_rcp(w);
+  const Dl a23 = f2 * f3, a13 = f1 * f3, a12 = f1 * f2;
+  const Dl q = 0.375 * s5;
+  const Dl ang_x = q * (-2.5 * nn * ix + a23 + a13 - a12) - 1.5 * s3 * ix;
+  const Dl ang_y = q * (-2.5 * nn * iy + a13 + a12 - a23) - 1.5 * s3 * iy;
+  const Dl ang_w = q * (-2.5 * nn * iw + a23 + a12 - a13) - 1.5 * s3 * iw;
+  const Dl dc = 3.0 * kc.alp3 * t * damp * damp;
+  const Dl bd = base * damp * sw;
+  const Dl ba = base * ang;
+  const Dl dcs = dc * sw;
+  gx = bd * ang_x + ba * (dcs * ix + damp * dswa * swb * swjk);
+  gy = bd * ang_y + ba * (dcs * iy + damp * swa * dswb * swjk);
+  gw = bd * ang_w + ba * (dcs * iw + damp * swa * swb * dswjk);
+}
+
+// one edge's tangents: the vector's and that of C6_cj = <fa[c], fb[j]>
+struct __align__(32) AtmEdgeT {
+  double vx, vy, vz, c6;
+};
+
+// the tangent kernels' sums (heads, or their tails)
+struct AtmTanSums {
+  double* energy_t;   // (N)   tangents of the per-atom energies
+  double* gs;         // (E,4) column 3: dE/dC6_cj (the value, for the center sides)
+  double* gs_t;       // (E,4) tangents of the edge gradients (vector, C6_cj)
+  double* gfa_t;      // (N,K)
+  double* gfb_t;      // (N,K)
+};
+
+// one wave (center) per block: the two permuted factor tables take 32 KB of LDS per wave
+constexpr int kAtmTanWaves = 1;
+
+template <int KP>
+__global__ __launch_bounds__(256) void atm_edges_tangent_kernel(
+    const uint64_t* __restrict__ keys, const int32_t* __restrict__ perm,
+    const int32_t* __restrict__ nbr, int64_t E, int64_t N, const double* __restrict__ vec_t,
+    const double* __restrict__ fa, const double* __restrict__ fb,
+    const double* __restrict__ fa_t, const double* __restrict__ fb_t,
+    AtmEdgeT* __restrict__ rec_t) {
+  const int64_t p = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (p >= E) return;
+  const int64_t e = perm[p];
+  const int64_t c = (int64_t)(keys[p] / (uint64_t)N);
+  const int64_t j = nbr[p];
+  double c6 = 0.0;
+#pragma unroll
+  for (int w = 0; w < KP; ++w)
+    c6 = fma(fa_t[c * KP + w], fb[j * KP + w], fma(fa[c * KP + w], fb_t[j * KP + w], c6));
+  rec_t[p] = AtmEdgeT{vec_t[3 * e + 0], vec_t[3 * e + 1], vec_t[3 * e + 2], c6};
+}
+
+// The distinct-triangle walk of atm_upper_kernel (same items, same order of b) with
+// forward-mode numbers: per triangle the energy tangent to c, j and k, and the tangents of
+// both edges' gradients and of the jk side's factor gradients at weight go_c + go_j + go_k,
+// with the value of dE/dC6 of both edges for the center sides. The walked edge's sums go
+// through the fold (fa[j] and its tangent permuted in LDS) and atm_fold4.
+template <int KP, bool SWITCH>
+__global__ __launch_bounds__(kAtmTanWaves * kWave) void atm_upper_tangent_kernel(
+    const AtmEdge* __restrict__ rec, const AtmEdgeT* __restrict__ rec_t,
+    const int32_t* __restrict__ lo, const int32_t* __restrict__ lo1, int64_t N,
+    int64_t n_groups, const double* __restrict__ fa, const double* __restrict__ fb,
+    const double* __restrict__ fa_t, const double* __restrict__ fb_t,
+    const double* __restrict__ table, int S, AtmConst kc, const double* __restrict__ go, int K,
+    AtmTanSums out, AtmTanSums tail) {
+  __shared__ double sTab[kAtmMaxSpecies * kAtmMaxSpecies];
+  __shared__ double sFp[kAtmTanWaves][32][kWave];   // fa[j][i ^ ((lane >> 1) & 7)]
+  __shared__ double sFq[kAtmTanWaves][32][kWave];   // fa_t[j], same permutation
+  atm_stage_table(table, S, sTab);
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wv = wave_in_block();
+  const int64_t t = blockIdx.x / n_groups;
+  const int64_t c = (blockIdx.x - t * n_groups) * kAtmTanWaves + wv;
+  if (c >= N) return;
+  const int32_t hi = lo[c + 1];
+  const int32_t a0 = lo1[c] + (int32_t)t * kAtmTile;
+  if (a0 + 1 >= hi) return;
+  const AtmLanes L = atm_lanes(lane);
+  const int32_t a = a0 + lane;
+  const bool va = a < hi;
+  const AtmEdge ea = rec[va ? a : a0];
+  const AtmEdgeT eat = rec_t[ea.pos];
+  const Dl avx{ea.vx, eat.vx}, avy{ea.vy, eat.vy}, avz{ea.vz, eat.vz};
+  const Dl x = avx * avx + avy * avy + avz * avz;
+  Dl swa{ea.sw, 0.0}, dswa{ea.dsw, 0.0};
+  if (SWITCH) atm_switch_t(x, kc, swa, dswa);
+  const Dl c6a{ea.c6, eat.c6};
+  const int32_t j = atm_nb(ea);
+  const int sj = atm_snb(ea);
+  const int m = (lane >> 1) & 7;
+  double fj[KP];
+#pragma unroll
+  for (int w = 0; w < KP; ++w) fj[w] = fa[(int64_t)j * KP + w];
+#pragma unroll
+  for (int i = 0; i < 32; ++i) {
+    sFp[wv][i][lane] = (i ^ m) < KP ? fa[(int64_t)j * KP + (i ^ m)] : 0.0;
+    sFq[wv][i][lane] = (i ^ m) < KP ? fa_t[(int64_t)j * KP + (i ^ m)] : 0.0;
+  }
+  wave_sync();
+  const double go_cj = go[c] + go[j];
+  double e_row_t = 0.0, gax_t = 0.0, gay_t = 0.0, gaz_t = 0.0, gc6a = 0.0, gc6a_t = 0.0;
+  double gfj_t[KP];
+#pragma unroll
+  for (int w = 0; w < KP; ++w) gfj_t[w] = 0.0;
+
+  for (int32_t b = a0 + 1; b < hi; ++b) {
+    const AtmEdge eb = rec[b];                      // wave-uniform
+    const int32_t k = atm_nb(eb);
+    const double dx = ea.vx - eb.vx, dy = ea.vy - eb.vy, dz = ea.vz - eb.vz;
+    const double w2 = dx * dx + dy * dy + dz * dz;
+    const bool keep = va && a < b && j != k && w2 <= kc.cut2 && w2 > kAtmEps;
+    if (__ballot(keep) == 0) continue;
+    const AtmEdgeT ebt = rec_t[eb.pos];
+    const double* __restrict__ fk = fb + (int64_t)k * KP;
+    const double* __restrict__ fkt = fb_t + (int64_t)k * KP;
+    double bx_t = 0.0, by_t = 0.0, bz_t = 0.0, bc6 = 0.0, bc6_t = 0.0, ek_t = 0.0;
+    double g3 = 0.0, g3_t = 0.0;
+    if (keep) {
+      const Dl bvx{eb.vx, ebt.vx}, bvy{eb.vy, ebt.vy}, bvz{eb.vz, ebt.vz};
+      const Dl y = bvx * bvx + bvy * bvy + bvz * bvz;
+      Dl swb{eb.sw, 0.0}, dswb{eb.dsw, 0.0};
+      if (SWITCH) atm_switch_t(y, kc, swb, dswb);
+      const Dl ddx = avx - bvx, ddy = avy - bvy, ddz = avz - bvz;
+      const Dl w = ddx * ddx + ddy * ddy + ddz * ddz;
+      double c6jk = 0.0, c6jk_t = 0.0;
+#pragma unroll
+      for (int q = 0; q < KP; ++q) {
+        c6jk = fma(fj[q], fk[q], c6jk);
+        c6jk_t = fma(fj[q], fkt[q], fma(sFq[wv][q ^ m][lane], fk[q], c6jk_t));
+      }
+      const Dl cjk{c6jk, c6jk_t}, c6b{eb.c6, ebt.c6};
+      const Dl pr = c6a * c6b * cjk;
+      const double r0 = ea.p * eb.p * sTab[sj * S + atm_snb(eb)];
+      Dl e, gx, gy, gw;
+      atm_triangle_t<SWITCH>(kc, x, y, w, pr.v < 0.0 ? -pr : pr, r0, swa, swb, dswa, dswb, e,
+                             gx, gy, gw);
+      const double W = go_cj + go[k];
+      e_row_t += e.t;
+      ek_t = e.t;
+      const Dl eW = W * e, gxW = W * gx, gyW = W * gy, gwW = W * gw;
+      // edge a's vector gradient 2 (gx v_a + gw d), edge b's 2 (gy v_b - gw d)
+      gax_t = fma(2.0, (gxW * avx + gwW * ddx).t, gax_t);
+      gay_t = fma(2.0, (gxW * avy + gwW * ddy).t, gay_t);
+      gaz_t = fma(2.0, (gxW * avz + gwW * ddz).t, gaz_t);
+      bx_t = 2.0 * (gyW * bvx - gwW * ddx).t;
+      by_t = 2.0 * (gyW * bvy - gwW * ddy).t;
+      bz_t = 2.0 * (gyW * bvz - gwW * ddz).t;
+      // dE/dC6 = E / (2 C6) for each of the three pair coefficients
+      const Dl ha = 0.5 * dl_over(eW, c6a), hb = 0.5 * dl_over(eW, c6b);
+      const Dl h3 = 0.5 * dl_over(eW, cjk);
+      gc6a += ha.v;
+      gc6a_t += ha.t;
+      bc6 = hb.v;
+      bc6_t = hb.t;
+      g3 = h3.v;
+      g3_t = h3.t;
+#pragma unroll
+      for (int q = 0; q < KP; ++q) gfj_t[q] = fma(g3_t, fk[q], fma(g3, fkt[q], gfj_t[q]));
+    }
+    // edge b and atom k: the wave's sums
+    const double vf = atm_fold32x2(sFp[wv], sFq[wv], lane, g3_t, g3);
+    const double vs = atm_fold4(bx_t, by_t, bz_t, bc6_t, lane, L);
+    const double vp = atm_fold4(bc6, ek_t, 0.0, 0.0, lane, L);
+    const int slot = lane >> 1;
+    if ((lane & 1) == 0 && slot < K) atm_acc(out.gfb_t, tail.gfb_t, (int64_t)k * K + slot, vf);
+    if ((lane & 15) == 0) atm_acc(out.gs_t, tail.gs_t, (int64_t)eb.pos * 4 + (lane >> 4), vs);
+    if (lane == 0) atm_acc(out.gs, tail.gs, (int64_t)eb.pos * 4 + 3, vp);
+    if (lane == 16) atm_acc(out.energy_t, tail.energy_t, k, vp);
+  }
+  if (va) {
+    atm_acc(out.gs_t, tail.gs_t, (int64_t)ea.pos * 4 + 0, gax_t);
+    atm_acc(out.gs_t, tail.gs_t, (int64_t)ea.pos * 4 + 1, gay_t);
+    atm_acc(out.gs_t, tail.gs_t, (int64_t)ea.pos * 4 + 2, gaz_t);
+    atm_acc(out.gs_t, tail.gs_t, (int64_t)ea.pos * 4 + 3, gc6a_t);
+    atm_acc(out.gs, tail.gs, (int64_t)ea.pos * 4 + 3, gc6a);
+    atm_acc(out.energy_t, tail.energy_t, j, e_row_t);
+#pragma unroll
+    for (int w = 0; w < KP; ++w)
+      if (w < K) atm_acc(out.gfa_t, tail.gfa_t, (int64_t)j * K + w, gfj_t[w]);
+  }
+  const double ec = atm_wave_sum(e_row_t, L);
+  if (lane == 0) atm_acc(out.energy_t, tail.energy_t, c, ec);
+}
+
+// atm_repeat_kernel's walk with forward-mode numbers (weight go_c, energy tangent to c).
+template <int KP, bool SWITCH>
+__global__ __launch_bounds__(kAtmWaves * kWave) void atm_repeat_tangent_kernel(
+    const AtmEdge* __restrict__ rec, const AtmEdgeT* __restrict__ rec_t,
+    const int32_t* __restrict__ lo, const int32_t* __restrict__ lo1,
+    const int32_t* __restrict__ flag, int64_t N, const double* __restrict__ fa,
+    const double* __restrict__ fb, const double* __restrict__ fa_t,
+    const double* __restrict__ fb_t, const double* __restrict__ table, int S, AtmConst kc,
+    const double* __restrict__ go, int K, AtmTanSums out, AtmTanSums tail) {
+  __shared__ double sTab[kAtmMaxSpecies * kAtmMaxSpecies];
+  atm_stage_table(table, S, sTab);
+  const int lane = threadIdx.x & (kWave - 1);
+  const int64_t c = (int64_t)blockIdx.x * kAtmWaves + wave_in_block();
+  if (c >= N || flag[c] == 0) return;
+  const int32_t l0 = lo[c], u0 = lo1[c], hi = lo[c + 1];
+  int32_t s0 = u0;                                  // self-image edges: [s0, u0)
+  while (s0 > l0 && atm_nb(rec[s0 - 1]) == (int32_t)c) --s0;
+  const double go_c = go[c];
+  double e_acc_t = 0.0;
+  for (int32_t a0 = l0; a0 < hi; a0 += kAtmTile) {
+    const int32_t a = a0 + lane;
+    if (a >= hi) break;
+    const AtmEdge ea = rec[a];
+    const AtmEdgeT eat = rec_t[a];
+    const Dl avx{ea.vx, eat.vx}, avy{ea.vy, eat.vy}, avz{ea.vz, eat.vz};
+    const Dl x = avx * avx + avy * avy + avz * avz;
+    Dl swa{ea.sw, 0.0}, dswa{ea.dsw, 0.0};
+    if (SWITCH) atm_switch_t(x, kc, swa, dswa);
+    const Dl c6a{ea.c6, eat.c6};
+    const int32_t j = atm_nb(ea);
+    double fj[KP], fjt[KP], gfj_t[KP];
+#pragma unroll
+    for (int w = 0; w < KP; ++w) {
+      fj[w] = fa[(int64_t)j * KP + w];
+      fjt[w] = fa_t[(int64_t)j * KP + w];
+      gfj_t[w] = 0.0;
+    }
+    double gax_t = 0.0, gay_t = 0.0, gaz_t = 0.0, gc6a = 0.0, gc6a_t = 0.0;
+    const bool self = j == (int32_t)c;
+    int32_t run_end = a + 1;
+    if (!self)
+      while (run_end < hi && atm_nb(rec[run_end]) == j) ++run_end;
+    const int32_t r1_end = self ? hi : run_end;
+    bool any = false;
+    const int32_t r2_beg = self ? hi : (s0 > a + 1 ? s0 : a + 1);
+    const int32_t r2_end = self ? hi : u0;
+    for (int pass = 0; pass < 2; ++pass) {
+      const int32_t b_beg = pass == 0 ? a + 1 : r2_beg;
+      const int32_t b_end = pass == 0 ? r1_end : r2_end;
+      for (int32_t b = b_beg; b < b_end; ++b) {
+        const AtmEdge eb = rec[b];
+        const double dx = ea.vx - eb.vx, dy = ea.vy - eb.vy, dz = ea.vz - eb.vz;
+        const double w2 = dx * dx + dy * dy + dz * dz;
+        if (!(w2 <= kc.cut2 && w2 > kAtmEps)) continue;
+        any = true;
+        const AtmEdgeT ebt = rec_t[b];
+        const int32_t k = atm_nb(eb);
+        const Dl bvx{eb.vx, ebt.vx}, bvy{eb.vy, ebt.vy}, bvz{eb.vz, ebt.vz};
+        const Dl y = bvx * bvx + bvy * bvy + bvz * bvz;
+        Dl swb{eb.sw, 0.0}, dswb{eb.dsw, 0.0};
+        if (SWITCH) atm_switch_t(y, kc, swb, dswb);
+        const Dl ddx = avx - bvx, ddy = avy - bvy, ddz = avz - bvz;
+        const Dl w = ddx * ddx + ddy * ddy + ddz * ddz;
+        const double* __restrict__ fk = fb + (int64_t)k * KP;
+        const double* __restrict__ fkt = fb_t + (int64_t)k * KP;
+        double c6jk = 0.0, c6jk_t = 0.0;
+#pragma unroll
+        for (int q = 0; q < KP; ++q) {
+          c6jk = fma(fj[q], fk[q], c6jk);
+          c6jk_t = fma(fj[q], fkt[q], fma(fjt[q], fk[q], c6jk_t));
+        }
+        const Dl cjk{c6jk, c6jk_t}, c6b{eb.c6, ebt.c6};
+        const Dl pr = c6a * c6b * cjk;
+        const double r0 = ea.p * eb.p * sTab[atm_snb(ea) * S + atm_snb(eb)];
+        Dl e, gx, gy, gw;
+        atm_triangle_t<SWITCH>(kc, x, y, w, pr.v < 0.0 ? -pr : pr, r0, swa, swb, dswa, dswb,
+                               e, gx, gy, gw);
+        e_acc_t += e.t;
+        const Dl eW = go_c * e, gxW = go_c * gx, gyW = go_c * gy, gwW = go_c * gw;
+        gax_t = fma(2.0, (gxW * avx + gwW * ddx).t, gax_t);
+        gay_t = fma(2.0, (gxW * avy + gwW * ddy).t, gay_t);
+        gaz_t = fma(2.0, (gxW * avz + gwW * ddz).t, gaz_t);
+        const Dl ha = 0.5 * dl_over(eW, c6a), hb = 0.5 * dl_over(eW, c6b);
+        const Dl h3 = 0.5 * dl_over(eW, cjk);
+        gc6a += ha.v;
+        gc6a_t += ha.t;
+#pragma unroll
+        for (int q = 0; q < KP; ++q) gfj_t[q] = fma(h3.t, fk[q], fma(h3.v, fkt[q], gfj_t[q]));
+        atm_acc(out.gs_t, tail.gs_t, (int64_t)b * 4 + 0, 2.0 * (gyW * bvx - gwW * ddx).t);
+        atm_acc(out.gs_t, tail.gs_t, (int64_t)b * 4 + 1, 2.0 * (gyW * bvy - gwW * ddy).t);
+        atm_acc(out.gs_t, tail.gs_t, (int64_t)b * 4 + 2, 2.0 * (gyW * bvz - gwW * ddz).t);
+        atm_acc(out.gs_t, tail.gs_t, (int64_t)b * 4 + 3, hb.t);
+        atm_acc(out.gs, tail.gs, (int64_t)b * 4 + 3, hb.v);
+#pragma unroll
+        for (int q = 0; q < KP; ++q)
+          if (q < K)
+            atm_acc(out.gfb_t, tail.gfb_t, (int64_t)k * K + q, fma(h3.t, fj[q], h3.v * fjt[q]));
+      }
+    }
+    if (any) {
+      atm_acc(out.gs_t, tail.gs_t, (int64_t)a * 4 + 0, gax_t);
+      atm_acc(out.gs_t, tail.gs_t, (int64_t)a * 4 + 1, gay_t);
+      atm_acc(out.gs_t, tail.gs_t, (int64_t)a * 4 + 2, gaz_t);
+      atm_acc(out.gs_t, tail.gs_t, (int64_t)a * 4 + 3, gc6a_t);
+      atm_acc(out.gs, tail.gs, (int64_t)a * 4 + 3, gc6a);
+#pragma unroll
+      for (int w = 0; w < KP; ++w)
+        if (w < K) atm_acc(out.gfa_t, tail.gfa_t, (int64_t)j * K + w, gfj_t[w]);
+    }
+  }
+  const double ec = atm_wave_sum(e_acc_t, atm_lanes(lane));
+  if (lane == 0) atm_acc(out.energy_t, tail.energy_t, c, ec);
+}
+
 // ------------------------------------------------------------------------------ host
 static AtmConst atm_const(const xnn_atm_params* prm) {
   AtmConst k;
@@ -1049,6 +1447,139 @@ static int atm_dispatch(const AtmArgs& A) {
   return p16 ? atm_dispatch_sw<32, BWD, true>(A) : atm_dispatch_sw<32, BWD, false>(A);
 }
 
+// The tangent workspace: the backward's layout, then the padded directions of both factor
+// matrices, the edges' tangent records, the tangents of the edge gradients and the tails of
+// the energy and edge-gradient tangents.
+struct AtmTanLayout {
+  AtmWorkLayout base;
+  size_t fa_t, fb_t, rec_t, gs_t, tail2, total;
+};
+
+static AtmTanLayout atm_tangent_layout(int64_t E, int64_t N, int kp) {
+  AtmTanLayout T;
+  T.base = atm_work_layout(E, N, kp, true);
+  size_t at = T.base.total;
+  const int64_t e1 = std::max<int64_t>(E, 1), n1 = std::max<int64_t>(N, 1);
+  T.fa_t = at; at += atm_align(sizeof(double) * kp * n1);
+  T.fb_t = at; at += atm_align(sizeof(double) * kp * n1);
+  T.rec_t = at; at += atm_align(sizeof(AtmEdgeT) * e1);
+  T.gs_t = at; at += atm_align(sizeof(double) * 4 * e1);
+  T.tail2 = at; at += atm_align(sizeof(double) * (n1 + 4 * e1));
+  T.total = at;
+  return T;
+}
+
+struct AtmTanArgs {
+  const double* vec_t;
+  const double* fa_t;
+  const double* fb_t;
+  double* energy_t;
+  double* gvec_t;
+  double* gfa_t;
+  double* gfb_t;
+};
+
+template <int KP, bool SWITCH>
+static int atm_tangent_run(const AtmArgs& A, const AtmTanArgs& D) {
+  const AtmPlanLayout P = atm_plan_layout(A.E, A.N);
+  const AtmTanLayout T = atm_tangent_layout(A.E, A.N, KP);
+  const AtmWorkLayout& W = T.base;
+  const uint64_t* keys = at_off<uint64_t>(A.plan, P.keys);
+  const int32_t* perm = at_off<int32_t>(A.plan, P.perm);
+  const int32_t* nbr = at_off<int32_t>(A.plan, P.nbr);
+  const int32_t* lo = at_off<int32_t>(A.plan, P.lo);
+  const int32_t* lo1 = at_off<int32_t>(A.plan, P.lo1);
+  const int32_t* flag = at_off<int32_t>(A.plan, P.flag);
+  AtmEdge* rec = at_off<AtmEdge>(A.work, W.rec);
+  AtmEdge* rec_up = at_off<AtmEdge>(A.work, W.rec_up);
+  AtmEdgeT* rec_t = at_off<AtmEdgeT>(A.work, T.rec_t);
+  uint64_t* skey = at_off<uint64_t>(A.work, W.skey);
+  int32_t* sval = at_off<int32_t>(A.work, W.sval);
+  int32_t* sperm = at_off<int32_t>(A.work, W.sperm);
+  double* faP = at_off<double>(A.work, W.fa);
+  double* fbP = at_off<double>(A.work, W.fb);
+  double* fatP = at_off<double>(A.work, T.fa_t);
+  double* fbtP = at_off<double>(A.work, T.fb_t);
+  const int64_t nk = A.N * (int64_t)A.K;
+  AtmTanSums out{D.energy_t, at_off<double>(A.work, W.gs), at_off<double>(A.work, T.gs_t),
+                 D.gfa_t, D.gfb_t};
+  double* tails = at_off<double>(A.work, W.tail);     // gs, gfa_t, gfb_t
+  double* tails2 = at_off<double>(A.work, T.tail2);   // energy_t, gs_t
+  AtmTanSums tail{tails2, tails, tails2 + A.N, tails + 4 * A.E, tails + 4 * A.E + nk};
+  atm_zero(out.energy_t, A.N, A.s);
+  atm_zero(out.gs, 4 * A.E, A.s);
+  atm_zero(out.gs_t, 4 * A.E, A.s);
+  atm_zero(out.gfa_t, nk, A.s);
+  atm_zero(out.gfb_t, nk, A.s);
+  atm_zero(tails, 4 * A.E + 2 * nk, A.s);
+  atm_zero(tails2, A.N + 4 * A.E, A.s);
+  if (A.E > 0) atm_zero(D.gvec_t, 3 * A.E, A.s);
+  XNN_LAUNCH_CHECK();
+  if (A.E == 0 || A.N == 0) return XNN_OK;
+  const double* f4[4] = {A.fa, A.fb, D.fa_t, D.fb_t};
+  double* p4[4] = {faP, fbP, fatP, fbtP};
+  for (int i = 0; i < 4; ++i)
+    hipLaunchKernelGGL((atm_pad_kernel<KP>), dim3(grid_1d(A.N * KP, 256)), dim3(256), 0, A.s,
+                       f4[i], A.N, A.K, p4[i]);
+  hipLaunchKernelGGL((atm_edges_kernel<KP>), dim3(grid_1d(A.E, 256)), dim3(256), 0, A.s, keys,
+                     perm, nbr, A.E, A.N, A.vec, faP, fbP, A.species, A.table, A.S, A.kc, rec,
+                     skey, sval);
+  hipLaunchKernelGGL((atm_edges_tangent_kernel<KP>), dim3(grid_1d(A.E, 256)), dim3(256), 0, A.s,
+                     keys, perm, nbr, A.E, A.N, D.vec_t, faP, fbP, fatP, fbtP, rec_t);
+  XNN_LAUNCH_CHECK();
+  size_t cub_bytes = W.cub_bytes;
+  XNN_HIP_CHECK(hipcub::DeviceRadixSort::SortPairs(
+      at_off<void>(A.work, W.cub), cub_bytes, skey, at_off<uint64_t>(A.work, W.skey_out), sval,
+      sperm, (int)A.E, 0, 33 + atm_bitlen(A.N), A.s));
+  hipLaunchKernelGGL(atm_walk_order_kernel, dim3(grid_1d(A.E, 256)), dim3(256), 0, A.s, rec,
+                     sperm, A.E, rec_up);
+  XNN_LAUNCH_CHECK();
+  if (A.max_tiles > 0) {
+    const int64_t n_groups = (A.N + kAtmTanWaves - 1) / kAtmTanWaves;
+    const int64_t blocks = A.max_tiles * n_groups;
+    XNN_REQUIRE(blocks <= 0x7fffffff, "ATM: too many triplet work items");
+    hipLaunchKernelGGL((atm_upper_tangent_kernel<KP, SWITCH>), dim3((unsigned)blocks),
+                       dim3(kAtmTanWaves * kWave), 0, A.s, rec_up, rec_t, lo, lo1, A.N, n_groups,
+                       faP, fbP, fatP, fbtP, A.table, A.S, A.kc, A.go, A.K, out, tail);
+    XNN_LAUNCH_CHECK();
+  }
+  if (A.has_repeats) {
+    const int64_t n_groups = (A.N + kAtmWaves - 1) / kAtmWaves;
+    hipLaunchKernelGGL((atm_repeat_tangent_kernel<KP, SWITCH>), dim3((unsigned)n_groups),
+                       dim3(kAtmWaves * kWave), 0, A.s, rec, rec_t, lo, lo1, flag, A.N, faP, fbP,
+                       fatP, fbtP, A.table, A.S, A.kc, A.go, A.K, out, tail);
+    XNN_LAUNCH_CHECK();
+  }
+  atm_add_tail(out.energy_t, tail.energy_t, A.N, A.s);
+  atm_add_tail(out.gs, tail.gs, 4 * A.E, A.s);
+  atm_add_tail(out.gs_t, tail.gs_t, 4 * A.E, A.s);
+  atm_add_tail(out.gfa_t, tail.gfa_t, nk, A.s);
+  atm_add_tail(out.gfb_t, tail.gfb_t, nk, A.s);
+  hipLaunchKernelGGL(atm_vec_grad_kernel, dim3(grid_1d(A.E, 256)), dim3(256), 0, A.s, perm,
+                     out.gs_t, A.E, D.gvec_t);
+  // the center sides C6_cj = <fa[c], fb[j]>: tangents of their gradients with the values of
+  // the factors, then their gradients with the factors' directions
+  const int64_t n_groups = (A.N + kAtmWaves - 1) / kAtmWaves;
+  for (int pass = 0; pass < 2; ++pass)
+    hipLaunchKernelGGL((atm_center_side_kernel<KP>), dim3((unsigned)n_groups),
+                       dim3(kAtmWaves * kWave), 0, A.s, lo, nbr,
+                       at_off<int32_t>(A.plan, P.lo_src), at_off<int32_t>(A.plan, P.by_src),
+                       at_off<int32_t>(A.plan, P.ctr), pass == 0 ? out.gs_t : out.gs,
+                       pass == 0 ? faP : fatP, pass == 0 ? fbP : fbtP, A.N, A.K, D.gfa_t,
+                       D.gfb_t);
+  XNN_LAUNCH_CHECK();
+  return XNN_OK;
+}
+
+static int atm_tangent_dispatch(const AtmArgs& A, const AtmTanArgs& D) {
+  const bool sw = A.kc.width > 0.0;
+  switch (atm_kp(A.K)) {
+    case 24: return sw ? atm_tangent_run<24, true>(A, D) : atm_tangent_run<24, false>(A, D);
+    case 28: return sw ? atm_tangent_run<28, true>(A, D) : atm_tangent_run<28, false>(A, D);
+    default: return sw ? atm_tangent_run<32, true>(A, D) : atm_tangent_run<32, false>(A, D);
+  }
+}
+
 static int atm_check(int64_t E, int64_t N, int64_t max_tiles, const double* vec, const double* fa,
                      const double* fb, int32_t K, const int32_t* species, const double* table,
                      int32_t S, const xnn_atm_params* prm, const void* plan, void* work,
@@ -1179,6 +1710,37 @@ int xnn_atm_energy_backward(const void* plan, int64_t n_edges, int64_t n_atoms,
             species, table, n_species, atm_const(prm), nullptr, grad_energy, grad_vec, grad_fa,
             grad_fb, work, as_hip(stream)};
   return atm_dispatch<true>(A);
+}
+
+int xnn_atm_tangent_work_size(int64_t n_edges, int64_t n_atoms, int32_t k, size_t* bytes) {
+  XNN_REQUIRE(n_edges >= 0 && n_atoms >= 0 && bytes, "negative size or NULL output");
+  XNN_REQUIRE(k >= 1 && k <= kAtmMaxK, "ATM: the C6 factors need 1 to %d components (got %d)",
+              kAtmMaxK, (int)k);
+  *bytes = atm_tangent_layout(n_edges, n_atoms, atm_kp(k)).total;
+  return XNN_OK;
+}
+
+int xnn_atm_energy_backward_tangent(
+    const void* plan, int64_t n_edges, int64_t n_atoms, int64_t max_tiles, int64_t has_repeats,
+    const double* edge_vec, const double* feat_a, const double* feat_b, int32_t k,
+    const int32_t* species, const double* table, int32_t n_species, const xnn_atm_params* prm,
+    const double* grad_energy, const double* edge_vec_t, const double* feat_a_t,
+    const double* feat_b_t, double* energy_t, double* grad_vec_t, double* grad_fa_t,
+    double* grad_fb_t, void* work, size_t work_bytes, xnn_stream_t stream) {
+  const int rc = atm_check(n_edges, n_atoms, max_tiles, edge_vec, feat_a, feat_b, k, species,
+                           table, n_species, prm, plan, work, work_bytes, true);
+  if (rc != XNN_OK) return rc;
+  XNN_REQUIRE(work_bytes >= atm_tangent_layout(n_edges, n_atoms, atm_kp(k)).total,
+              "workspace too small");
+  XNN_REQUIRE(n_atoms == 0 || (grad_energy && feat_a_t && feat_b_t && energy_t && grad_fa_t &&
+                               grad_fb_t),
+              "NULL input or output");
+  XNN_REQUIRE(n_edges == 0 || (edge_vec_t && grad_vec_t), "NULL edge tangents or output");
+  AtmArgs A{plan, n_edges, n_atoms, max_tiles, has_repeats, edge_vec, feat_a, feat_b, k,
+            species, table, n_species, atm_const(prm), nullptr, grad_energy, nullptr, nullptr,
+            nullptr, work, as_hip(stream)};
+  AtmTanArgs D{edge_vec_t, feat_a_t, feat_b_t, energy_t, grad_vec_t, grad_fa_t, grad_fb_t};
+  return atm_tangent_dispatch(A, D);
 }
 
 int xnn_atm_count(const void* plan, int64_t n_edges, int64_t n_atoms, int64_t max_tiles,

@@ -256,6 +256,14 @@ def _pair_backward(ctx, g_e2):
 d4_two_body_op.register_autograd(_pair_backward, setup_context=_pair_setup)
 
 
+def _structure_once() -> None:
+    """The one-launch structure energies hold their gradients as constants: a backward
+    recorded for a second derivative would drop the Hessian, so it is refused."""
+    if torch.is_grad_enabled():
+        raise RuntimeError("the per-structure dispersion energies of one backward launch are "
+                           "differentiable once (forces and stress)")
+
+
 class TwoBodyStructureEnergy(torch.autograd.Function):
     """The two-body energies per structure (B,) and, detached, per atom (N,), with their
     gradients, from one launch of the pair backward at unit seeds, as the reference's native
@@ -291,6 +299,7 @@ class TwoBodyStructureEnergy(torch.autograd.Function):
 
     @staticmethod
     def backward(ctx, g_b, _g_e2):
+        _structure_once()
         batch32, node_ptr, grad_pos, part, grad_alpha = ctx.saved_tensors
         gs = g_b.index_select(0, batch32.long())[:, None]   # each atom's structure seed
         g_pos = grad_pos * gs if ctx.needs_input_grad[0] else None
@@ -405,7 +414,8 @@ def atm_energy_op(plan: Tensor, edge_vec: Tensor, feat_a: Tensor, feat_b: Tensor
                   max_tiles: int, has_repeats: int) -> Tensor:
     """Per-atom ATM energies (N,) in hartree over the planned edges (bohr vectors, input
     order), pair C6 = <feat_a[x], feat_b[y]>, ``params`` = [s9, alp3, cutoff, width];
-    differentiable once in ``edge_vec``, ``feat_a`` and ``feat_b``."""
+    differentiable twice in ``edge_vec``, ``feat_a`` and ``feat_b`` (the gradient is
+    :func:`atm_energy_grad_op`, itself differentiable)."""
     dev = edge_vec.device
     n_edges, k = int(edge_vec.shape[0]), int(feat_a.shape[1])
     energy = torch.empty(n_atoms, dtype=torch.float64, device=dev)
@@ -429,25 +439,80 @@ def _atm_setup(ctx, inputs, output):
 
 
 def _atm_backward(ctx, g_energy):
-    if torch.is_grad_enabled():
-        raise RuntimeError("the ATM kernels are differentiable once (forces and stress); a "
-                           "second derivative through the dispersion term has no GPU path")
     plan, vec, fa, fb, species, table = ctx.saved_tensors
     params, n_atoms, max_tiles, has_repeats = ctx.meta
-    dev = vec.device
-    n_edges, k = int(vec.shape[0]), int(fa.shape[1])
-    g_vec = torch.empty_like(vec)
-    g_fa = torch.empty_like(fa)
-    g_fb = torch.empty_like(fb)
-    work = _atm_work(n_edges, n_atoms, k, True, dev)
-    _lib.call("xnn_atm_energy_backward", _lib.ptr(plan), n_edges, n_atoms, max_tiles,
-              has_repeats, _lib.ptr(vec), _lib.ptr(fa), _lib.ptr(fb), k, _lib.ptr(species),
-              _lib.ptr(table), int(table.shape[0]), _atm_params(params),
-              _lib.ptr(g_energy.to(torch.float64).contiguous()), _lib.ptr(g_vec), _lib.ptr(g_fa),
-              _lib.ptr(g_fb), _lib.ptr(work), work.numel(), _lib.stream(dev))
+    g_vec, g_fa, g_fb = atm_energy_grad_op(plan, vec, fa, fb, g_energy.to(torch.float64),
+                                           species, table, params, n_atoms, max_tiles,
+                                           has_repeats)
     need = ctx.needs_input_grad
     return (None, g_vec if need[1] else None, g_fa if need[2] else None,
             g_fb if need[3] else None) + (None,) * 6
+
+
+@torch.library.custom_op(f"{_NS}::atm_energy_grad", mutates_args=())
+def atm_energy_grad_op(plan: Tensor, edge_vec: Tensor, feat_a: Tensor, feat_b: Tensor,
+                       grad_energy: Tensor, species: Tensor, table: Tensor, params: List[float],
+                       n_atoms: int, max_tiles: int,
+                       has_repeats: int) -> Tuple[Tensor, Tensor, Tensor]:
+    """The gradients of ``sum_i grad_energy[i] E_i`` in the edge vectors and both factor
+    matrices (dispersion_fast/atm.py:413-443). Differentiable once more: its Jacobian in
+    the first three inputs is the (symmetric) Hessian of that sum, so its backward is the
+    Hessian times the incoming cotangents, and in ``grad_energy`` the energies' derivative
+    along them (xnn_atm_energy_backward_tangent, atm.py:475-509)."""
+    dev = edge_vec.device
+    n_edges, k = int(edge_vec.shape[0]), int(feat_a.shape[1])
+    g_vec = torch.empty_like(edge_vec)
+    g_fa = torch.empty_like(feat_a)
+    g_fb = torch.empty_like(feat_b)
+    work = _atm_work(n_edges, n_atoms, k, True, dev)
+    _lib.call("xnn_atm_energy_backward", _lib.ptr(plan), n_edges, n_atoms, max_tiles,
+              has_repeats, _lib.ptr(edge_vec), _lib.ptr(feat_a), _lib.ptr(feat_b), k,
+              _lib.ptr(species), _lib.ptr(table), int(table.shape[0]), _atm_params(params),
+              _lib.ptr(grad_energy.contiguous()), _lib.ptr(g_vec), _lib.ptr(g_fa),
+              _lib.ptr(g_fb), _lib.ptr(work), work.numel(), _lib.stream(dev))
+    return g_vec, g_fa, g_fb
+
+
+@atm_energy_grad_op.register_fake
+def _(plan, edge_vec, feat_a, feat_b, grad_energy, species, table, params, n_atoms, max_tiles,
+      has_repeats):
+    return torch.empty_like(edge_vec), torch.empty_like(feat_a), torch.empty_like(feat_b)
+
+
+def _atm_grad_setup(ctx, inputs, output):
+    plan, vec, fa, fb, go, species, table, params, n_atoms, max_tiles, has_repeats = inputs
+    ctx.save_for_backward(plan, vec, fa, fb, go, species, table)
+    ctx.meta = (list(params), n_atoms, max_tiles, has_repeats)
+
+
+def _atm_grad_backward(ctx, u_vec, u_fa, u_fb):
+    if torch.is_grad_enabled():
+        raise RuntimeError("the ATM kernels are differentiable twice (forces, stress and their "
+                           "derivatives); a third derivative has no GPU path")
+    plan, vec, fa, fb, go, species, table = ctx.saved_tensors
+    params, n_atoms, max_tiles, has_repeats = ctx.meta
+    dev = vec.device
+    n_edges, k = int(vec.shape[0]), int(fa.shape[1])
+    # an output that reached no loss has no cotangent: a zero direction
+    dirs = [torch.zeros_like(x) if u is None else u.to(torch.float64).contiguous()
+            for x, u in ((vec, u_vec), (fa, u_fa), (fb, u_fb))]
+    energy_t = torch.empty(n_atoms, dtype=torch.float64, device=dev)
+    h_vec, h_fa, h_fb = (torch.empty_like(x) for x in (vec, fa, fb))
+    nbytes = ctypes.c_size_t()
+    _lib.call("xnn_atm_tangent_work_size", n_edges, n_atoms, k, ctypes.byref(nbytes))
+    work = torch.empty(max(int(nbytes.value), 1), dtype=torch.uint8, device=dev)
+    _lib.call("xnn_atm_energy_backward_tangent", _lib.ptr(plan), n_edges, n_atoms, max_tiles,
+              has_repeats, _lib.ptr(vec), _lib.ptr(fa), _lib.ptr(fb), k, _lib.ptr(species),
+              _lib.ptr(table), int(table.shape[0]), _atm_params(params),
+              _lib.ptr(go.contiguous()), _lib.ptr(dirs[0]), _lib.ptr(dirs[1]),
+              _lib.ptr(dirs[2]), _lib.ptr(energy_t), _lib.ptr(h_vec), _lib.ptr(h_fa),
+              _lib.ptr(h_fb), _lib.ptr(work), work.numel(), _lib.stream(dev))
+    need = ctx.needs_input_grad
+    return (None, h_vec if need[1] else None, h_fa if need[2] else None,
+            h_fb if need[3] else None, energy_t.to(go.dtype) if need[4] else None) + (None,) * 6
+
+
+atm_energy_grad_op.register_autograd(_atm_grad_backward, setup_context=_atm_grad_setup)
 
 
 atm_energy_op.register_autograd(_atm_backward, setup_context=_atm_setup)
@@ -459,8 +524,8 @@ def atm_energy(edge_index: Tensor, edge_vec: Tensor, feat_a: Tensor, feat_b: Ten
     (dispersion_fast/atm.py:512-535): ``edge_index`` (2, E) ``[src, dst]`` within the
     three-body cutoff, both directions of every pair; ``edge_vec`` (E, 3) in bohr;
     ``feat_a``, ``feat_b`` (N, K <= 32) with pair C6 = <feat_a[x], feat_b[y]> (may be the
-    same tensor). Differentiable once in ``edge_vec``, ``feat_a`` and ``feat_b``; float64
-    throughout; GPU only."""
+    same tensor). Differentiable twice in ``edge_vec``, ``feat_a`` and ``feat_b`` (forces,
+    stress, and the second derivatives of a force loss); float64 throughout; GPU only."""
     if not edge_vec.is_cuda:
         raise RuntimeError("xnn_amd ATM runs on the GPU (HIP kernels); there is no CPU path")
     plan, info = atm_plan(edge_index, n_atoms)
@@ -508,6 +573,7 @@ class ATMStructureEnergy(torch.autograd.Function):
 
     @staticmethod
     def backward(ctx, g_b, _g_e):
+        _structure_once()
         g_vec, g_fa, g_fb, edge_graph, batch32 = ctx.saved_tensors
         ga = g_b.index_select(0, batch32.long())[:, None]
         need = ctx.needs_input_grad
@@ -1331,6 +1397,7 @@ class D3TwoBodyStructureEnergy(torch.autograd.Function):
 
     @staticmethod
     def backward(ctx, g_b, _g_e2):
+        _structure_once()
         batch32, node_ptr, grad_pos, part, grad_w = ctx.saved_tensors
         gs = g_b.index_select(0, batch32.long())[:, None]
         g_pos = grad_pos * gs if ctx.needs_input_grad[0] else None
