@@ -868,6 +868,29 @@ def bench_atm(steps: int, warmup: int, cpu: bool = True) -> dict:
     kernel_us = {k: float(np.mean([a.elapsed_time(b) * 1e3 for a, b in v]))
                  for k, v in _lib.timed.items() if v}
     _lib.timed.clear()
+
+    # one second-derivative step (a force-training loss through the ATM term): the
+    # energies, their gradient with a graph, and the gradient of <gradient, direction>
+    # (the Hessian-vector product of xnn_atm_energy_backward_tangent)
+    u_vec, u_feat = torch.randn_like(vec), torch.randn_like(feat)
+
+    def second_step():
+        v = vec.detach().requires_grad_(True)
+        f = feat.detach().requires_grad_(True)
+        e3 = XD.atm_energy(ei, v, f, f, consts, N)
+        gv, gf = torch.autograd.grad(e3.sum(), [v, f], create_graph=True)
+        return torch.autograd.grad((gv * u_vec).sum() + (gf * u_feat).sum(), [v, f])
+
+    second_step()
+    torch.cuda.synchronize()
+    _lib.time_launches("xnn_atm_energy_backward_tangent")
+    t0 = time.perf_counter()
+    second_step()
+    torch.cuda.synchronize()
+    second_ms = (time.perf_counter() - t0) * 1e3
+    tangent_us = float(np.mean([a.elapsed_time(b) * 1e3
+                                for a, b in _lib.timed["xnn_atm_energy_backward_tangent"]]))
+    _lib.timed.clear()
     plan, info = XD.atm_plan(ei, N)
     counts = (ctypes_i64 * 3)()
     _lib.call("xnn_atm_count", _lib.ptr(plan), int(ei.shape[1]), N, info[0], _lib.ptr(vec),
@@ -892,7 +915,9 @@ def bench_atm(steps: int, warmup: int, cpu: bool = True) -> dict:
                          "edge_pairs_tested": tested, "distinct_triangles": kept,
                          "repeated_atom_visits": repeated, "graph_ms": round(graph_ms, 2),
                          "energy_3body_hartree": float(e.sum()),
-                         "kernel_mean_us": {k: round(v, 2) for k, v in kernel_us.items()}},
+                         "kernel_mean_us": {k: round(v, 2) for k, v in kernel_us.items()},
+                         "second_derivative_step_ms": round(second_ms, 2),
+                         "tangent_kernel_us": round(tangent_us, 2)},
               "roofline": roofline}
     if cpu:
         result["cpu_baseline"] = cpu_baseline_atm(
