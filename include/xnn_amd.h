@@ -631,6 +631,17 @@ int xnn_eeq_real_apply(const double* pos, int64_t n_nodes, const double* cell, c
 int xnn_eeq_cholesky_block(double* matrix, int64_t n, int64_t k0, int64_t b, double* inv,
                            int* info, xnn_stream_t stream);
 
+/* (L L^T) X = B in place: X (n, nrhs) row-major float64 on entry B, nrhs 1 or 2; L the
+ * factor that xnn_eeq_cholesky_block left in the matrix (row-major, lower), inv_blocks the
+ * inverses of its diagonal blocks (block j of rows [128 j, 128 j + b_j) at inv_blocks +
+ * 128 * 128 j, row stride b_j, as xnn_eeq_cholesky_block wrote them); work: n * nrhs
+ * doubles. Blocked forward and backward substitution, one launch per block and direction;
+ * sums in a fixed order. Stands in for the factorized solves of the large regime
+ * (eeq.py:117-140: torch.linalg.lu_solve on the LU factors), here with the Cholesky factor
+ * of the symmetric operator. */
+int xnn_eeq_cholesky_solve(const double* factor, int64_t n, const double* inv_blocks, double* x,
+                           int32_t nrhs, double* work, xnn_stream_t stream);
+
 /* D4 reference tables in the kernels' layout, indexed by atomic number (rows 0 ..
  * n_elements-1), device memory: nref (n_el) int32, ngw / refcn / refq (n_el, 7) with
  * ngw int32, zeff (n_el), gi = hardness x gc (n_el), refalpha (n_el, 7, 23) the

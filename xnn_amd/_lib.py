@@ -197,6 +197,7 @@ _SIGNATURES = {
     "xnn_eeq_real_matrix": [vp, i64, vp, vp, dbl, dbl, vp, vp],
     "xnn_eeq_real_grad": [vp, i64, vp, vp, dbl, dbl, vp, vp, vp, vp, vp],
     "xnn_eeq_cholesky_block": [vp, i64, i64, i64, vp, vp, vp],
+    "xnn_eeq_cholesky_solve": [vp, i64, vp, vp, i32, vp, vp],
     "xnn_eeq_real_apply_work_size": [i64, c_int, ctypes.POINTER(ctypes.c_size_t)],
     "xnn_eeq_real_apply": [vp, i64, vp, vp, dbl, dbl, vp, vp, c_int, vp, vp, ctypes.c_size_t, vp],
     "xnn_segment_reduce_f64_noalloc": [c_int, vp, i64, i64, vp, i64, vp, vp],

@@ -547,6 +547,130 @@ __global__ __launch_bounds__(kCholThreads) void eeq_cholesky_block_kernel(
   }
 }
 
+// ---------------------------------------------------------------- solves with the factor
+// (L L^T) X = B with L from eeq_cholesky_block_kernel and the inverses of its diagonal
+// blocks (block j: rows [128 j, 128 j + b_j), inverse at inv + 128 * 128 j, row stride
+// b_j), X (n, NRHS) row-major. Forward L Y = B walks the blocks down, backward L^T X = Y
+// up, one launch per block. Launch k: every workgroup solves block k from its residual
+// rows with the block's inverse (forward y = inv r, backward x = inv^T r; a 128 x 128
+// product, repeated per workgroup rather than waiting for one), workgroup 0 stores it,
+// and every row still to come takes away the block's contribution (forward: r_i -= L[i,
+// k0:k0 + b_k] y_k, a wave per row over its contiguous entries, 8 rows' loads in flight at
+// once; backward: r_i -= L[k0:k0 + b_k, i]^T x_k for i < k0, a thread per row, the block
+// row read across threads). The solution goes to another array than the residual rows
+// the launch reads (forward: residual in X, solution in the work array; backward the
+// reverse), so no workgroup reads a row another one rewrites. Sums in a fixed order.
+constexpr int kTrsvBlock = kCholBlock;
+constexpr int kTrsvFwdRows = 32;      // rows per workgroup (forward)
+constexpr int kTrsvBwdRows = 256;     // rows per workgroup (backward)
+
+__device__ __forceinline__ double wave_sum_xor(double v) {
+#pragma unroll
+  for (int m = kWave / 2; m > 0; m >>= 1) v += __shfl_xor(v, m, kWave);
+  return v;
+}
+
+// out = inv rb (TRANS: inv^T rb) over one block of size b <= 128 with its lower-triangular
+// inverse (row stride b), rb and out in LDS: two threads per entry, each over half of the
+// columns (the loads independent of the sums, so they are in flight together), the halves
+// added by one exchange.
+template <int NRHS, bool TRANS>
+__device__ __forceinline__ void trsv_block_inverse(const double* __restrict__ ib, int b,
+                                                   const double (*rb)[NRHS],
+                                                   double (*out)[NRHS]) {
+  const int t = threadIdx.x, i = t >> 1, h = t & 1;
+  const int ii = i < b ? i : 0;
+  double s[NRHS];
+#pragma unroll
+  for (int r = 0; r < NRHS; ++r) s[r] = 0.0;
+#pragma unroll 16
+  for (int q = 0; q < kTrsvBlock / 2; ++q) {
+    const int c = h * (kTrsvBlock / 2) + q;
+    // forward: inv[i][c], c <= i; backward: inv[c][i], c >= i
+    const bool use = c < b && (TRANS ? c >= ii : c <= ii);
+    const double l = use ? (TRANS ? ib[(int64_t)c * b + ii] : ib[(int64_t)ii * b + c]) : 0.0;
+#pragma unroll
+    for (int r = 0; r < NRHS; ++r) s[r] = fma(l, rb[use ? c : 0][r], s[r]);
+  }
+#pragma unroll
+  for (int r = 0; r < NRHS; ++r) s[r] += __shfl_xor(s[r], 1, kWave);
+  if (h == 0 && i < b) {
+#pragma unroll
+    for (int r = 0; r < NRHS; ++r) out[i][r] = s[r];
+  }
+}
+
+template <int NRHS, bool TRANS>
+__global__ __launch_bounds__(256) void eeq_trsv_step_kernel(const double* __restrict__ L,
+                                                            int64_t n,
+                                                            const double* __restrict__ inv,
+                                                            int k, double* __restrict__ res,
+                                                            double* __restrict__ sol) {
+  __shared__ double rs[kTrsvBlock][NRHS];     // block k's residual
+  __shared__ double xs[kTrsvBlock][NRHS];     // its solution
+  const int t = threadIdx.x, lane = t & (kWave - 1), wv = t >> 6;
+  const int64_t k0 = (int64_t)k * kTrsvBlock;
+  const int bk = (int)(n - k0 < kTrsvBlock ? n - k0 : kTrsvBlock);
+  for (int i = t; i < bk * NRHS; i += blockDim.x) (&rs[0][0])[i] = res[k0 * NRHS + i];
+  __syncthreads();
+  trsv_block_inverse<NRHS, TRANS>(inv + (int64_t)k * kTrsvBlock * kTrsvBlock, bk, rs, xs);
+  __syncthreads();
+  if (blockIdx.x == 0)
+    for (int i = t; i < bk * NRHS; i += blockDim.x) sol[k0 * NRHS + i] = (&xs[0][0])[i];
+  if (!TRANS) {
+    // rows after the block, kTrsvFwdRows per workgroup; a wave takes 8 rows at a time
+    constexpr int kBatch = 8;
+    const int64_t r0 = k0 + bk + (int64_t)blockIdx.x * kTrsvFwdRows;
+    const int64_t r1 = r0 + kTrsvFwdRows < n ? r0 + kTrsvFwdRows : n;
+    const int ca = lane < bk ? lane : 0, cb = lane + kWave < bk ? lane + kWave : 0;
+    for (int64_t base = r0 + (int64_t)wv * kBatch; base < r1;
+         base += (int64_t)(blockDim.x / kWave) * kBatch) {
+      double v0[kBatch], v1[kBatch], old[kBatch][NRHS];
+#pragma unroll
+      for (int q = 0; q < kBatch; ++q) {
+        const int64_t i = base + q;
+        const bool ok = i < r1;
+        const double* row = L + (ok ? i : k0) * n + k0;
+        v0[q] = ok && lane < bk ? row[lane] : 0.0;
+        v1[q] = ok && lane + kWave < bk ? row[lane + kWave] : 0.0;
+#pragma unroll
+        for (int r = 0; r < NRHS; ++r) old[q][r] = ok ? res[i * NRHS + r] : 0.0;
+      }
+#pragma unroll
+      for (int q = 0; q < kBatch; ++q) {
+        const int64_t i = base + q;
+        if (i >= r1) break;                       // uniform in the wave
+#pragma unroll
+        for (int r = 0; r < NRHS; ++r) {
+          const double sr = wave_sum_xor(fma(v0[q], xs[ca][r], v1[q] * xs[cb][r]));
+          if (lane == 0) res[i * NRHS + r] = old[q][r] - sr;
+        }
+      }
+    }
+  } else {
+    // rows before the block, kTrsvBwdRows per workgroup, a thread per row
+    const int64_t r0 = (int64_t)blockIdx.x * kTrsvBwdRows;
+    const int64_t r1 = r0 + kTrsvBwdRows < k0 ? r0 + kTrsvBwdRows : k0;
+    for (int64_t i = r0 + t; i < r1; i += blockDim.x) {
+      double s[NRHS], old[NRHS];
+#pragma unroll
+      for (int r = 0; r < NRHS; ++r) {
+        s[r] = 0.0;
+        old[r] = res[i * NRHS + r];
+      }
+#pragma unroll 16
+      for (int c = 0; c < kTrsvBlock; ++c) {
+        const bool use = c < bk;
+        const double l = use ? L[(k0 + c) * n + i] : 0.0;
+#pragma unroll
+        for (int r = 0; r < NRHS; ++r) s[r] = fma(l, xs[use ? c : 0][r], s[r]);
+      }
+#pragma unroll
+      for (int r = 0; r < NRHS; ++r) res[i * NRHS + r] = old[r] - s[r];
+    }
+  }
+}
+
 }  // namespace xnn
 
 using namespace xnn;
@@ -633,6 +757,39 @@ int xnn_eeq_real_apply(const double* pos, int64_t n_nodes, const double* cell, c
   const int64_t m = n_nodes * nrhs;
   hipLaunchKernelGGL(eeq_sum_splits_kernel, dim3((unsigned)grid_1d(m, 256)), dim3(256), 0, s, part,
                      splits, m, out);
+  XNN_LAUNCH_CHECK();
+  return XNN_OK;
+}
+
+int xnn_eeq_cholesky_solve(const double* factor, int64_t n, const double* inv_blocks, double* x,
+                           int32_t nrhs, double* work, xnn_stream_t stream) {
+  XNN_REQUIRE(n >= 0, "negative size");
+  XNN_REQUIRE(nrhs == 1 || nrhs == 2, "one or two right-hand sides (got %d)", (int)nrhs);
+  if (n == 0) return XNN_OK;
+  XNN_REQUIRE(factor && inv_blocks && x && work, "NULL factor, inverses, right-hand side or work");
+  XNN_REQUIRE(n <= (int64_t(1) << 20), "at most 2^20 rows");
+  const int nb = (int)((n + kTrsvBlock - 1) / kTrsvBlock);
+  hipStream_t s = as_hip(stream);
+  for (int k = 0; k < nb; ++k) {          // forward: residual in x, solution into work
+    const int64_t after = n - std::min<int64_t>(n, (int64_t)(k + 1) * kTrsvBlock);
+    const unsigned grid = (unsigned)std::max<int64_t>(1, (after + kTrsvFwdRows - 1) / kTrsvFwdRows);
+    if (nrhs == 1)
+      hipLaunchKernelGGL((eeq_trsv_step_kernel<1, false>), dim3(grid), dim3(256), 0, s, factor, n,
+                         inv_blocks, k, x, work);
+    else
+      hipLaunchKernelGGL((eeq_trsv_step_kernel<2, false>), dim3(grid), dim3(256), 0, s, factor, n,
+                         inv_blocks, k, x, work);
+  }
+  for (int k = nb - 1; k >= 0; --k) {     // backward: residual in work, solution into x
+    const int64_t before = (int64_t)k * kTrsvBlock;
+    const unsigned grid = (unsigned)std::max<int64_t>(1, (before + kTrsvBwdRows - 1) / kTrsvBwdRows);
+    if (nrhs == 1)
+      hipLaunchKernelGGL((eeq_trsv_step_kernel<1, true>), dim3(grid), dim3(256), 0, s, factor, n,
+                         inv_blocks, k, work, x);
+    else
+      hipLaunchKernelGGL((eeq_trsv_step_kernel<2, true>), dim3(grid), dim3(256), 0, s, factor, n,
+                         inv_blocks, k, work, x);
+  }
   XNN_LAUNCH_CHECK();
   return XNN_OK;
 }

@@ -240,21 +240,20 @@ class LargeEEQSystem:
             del c, s, phase
         A.diagonal().add_(self.diag.to(torch.float64))
         self.A = A
-        self.factor, info = _cholesky(A)
+        self.factor, info, self.inv_blocks = _cholesky(A, keep_inverses=True)
         self.cholesky = bool(int(info) == 0)
         if not self.cholesky:                  # not numerically positive definite: LU
             self.lu = torch.linalg.lu_factor(A)
         self.y_ones = None
 
     def _solve(self, b: Tensor) -> Tensor:
-        """``A^-1 b`` for ``b`` (N, k): two triangular solves with the Cholesky factor (the
-        blocked solves; the one-column path of ``cholesky_solve`` is several times slower).
-        A single column is solved as two, with a zero second column: the library's
-        one-column triangular solve is about six times slower than its blocked one at
-        N = 5,000."""
-        if b.shape[1] == 1 and b.is_cuda:
-            return self._solve(torch.cat([b, torch.zeros_like(b)], 1))[:, :1]
+        """``A^-1 b`` for ``b`` (N, k): forward and backward substitution with the Cholesky
+        factor on the device (:func:`_cholesky_solve`: one launch per 128-row block, where
+        the library's blocked triangular solves launch several small products per block);
+        LAPACK's triangular solves on the CPU; the LU solve when the factorization failed."""
         if self.cholesky:
+            if self.inv_blocks is not None:
+                return _cholesky_solve(self.factor, self.inv_blocks, b)
             y = torch.linalg.solve_triangular(self.factor, b, upper=False)
             return torch.linalg.solve_triangular(self.factor.mT, y, upper=True)
         return torch.linalg.lu_solve(*self.lu, b)
@@ -575,24 +574,29 @@ class IterativeEEQSystem:
 CHOLESKY_BLOCK = 128
 
 
-def _cholesky(A: Tensor):
+def _cholesky(A: Tensor, keep_inverses: bool = False):
     """The Cholesky factor of the float64 operator and LAPACK's ``info`` (0, or the 1-based
     column of the first pivot that is not positive). On the device: right-looking blocked
     factorization, 128 columns at a time: ``xnn_eeq_cholesky_block`` factors the diagonal
     block in LDS and forms its inverse, the panel below it is ``A21 L11^-T`` and the
     trailing matrix takes ``- L21 L21^T`` (library GEMMs; a large trailing update is split
     at half height into the top rows' left square and the bottom rows, 3/4 of the square,
-    and the upper triangle is discarded at the end)."""
+    and the upper triangle is discarded at the end). ``keep_inverses``: also return the
+    diagonal blocks' inverses (block j at ``128 * 128 j``, row stride its size; None off
+    the device) for :func:`_cholesky_solve`."""
     if not A.is_cuda:
-        return torch.linalg.cholesky_ex(A)
+        L, info = torch.linalg.cholesky_ex(A)
+        return (L, info, None) if keep_inverses else (L, info)
     n, nb = A.shape[0], CHOLESKY_BLOCK
     L = A.contiguous().clone()
     info = torch.zeros(1, dtype=torch.int32, device=A.device)
-    inv = torch.empty(nb * nb, dtype=torch.float64, device=A.device)
+    inv_all = torch.empty(max((n + nb - 1) // nb, 1) * nb * nb, dtype=torch.float64,
+                          device=A.device)
     panel = torch.empty((max(n - nb, 0), nb), dtype=torch.float64, device=A.device)
     stream = _lib.stream(A.device)
     for k in range(0, n, nb):
         b = min(nb, n - k)
+        inv = inv_all[(k // nb) * nb * nb:]
         _lib.call("xnn_eeq_cholesky_block", _lib.ptr(L), n, k, b, _lib.ptr(inv),
                   _lib.ptr(info), stream)
         r = k + b
@@ -607,7 +611,23 @@ def _cholesky(A: Tensor):
                 L[r + h:, r:].addmm_(p[h:], p.t(), alpha=-1.0)
             else:
                 L[r:, r:].addmm_(p, p.t(), alpha=-1.0)
-    return L.tril_(), info[0]
+    return (L.tril_(), info[0], inv_all) if keep_inverses else (L.tril_(), info[0])
+
+
+def _cholesky_solve(L: Tensor, inv_all: Tensor, b: Tensor) -> Tensor:
+    """``(L L^T)^-1 b`` for ``b`` (N, k) on the device: forward and backward blocked
+    substitution with the factor and its diagonal blocks' inverses, one launch per block
+    and direction (``xnn_eeq_cholesky_solve``), two columns per pass."""
+    n = L.shape[0]
+    x = b.to(torch.float64).contiguous().clone()
+    work = torch.empty((n, min(x.shape[1], 2)), dtype=torch.float64, device=L.device)
+    stream = _lib.stream(L.device)
+    for c in range(0, x.shape[1], 2):
+        part = x[:, c:c + 2].contiguous()
+        _lib.call("xnn_eeq_cholesky_solve", _lib.ptr(L), n, _lib.ptr(inv_all), _lib.ptr(part),
+                  int(part.shape[1]), _lib.ptr(work), stream)
+        x[:, c:c + 2] = part
+    return x
 
 
 class _ConstantSolve(torch.autograd.Function):
