@@ -169,3 +169,19 @@ def test_oracle_operator_rows_equal_the_assembled_operator():
     rows = [0, 5, 16]
     got = Q.operator_rows(pos, cell, rad, diag, q, rows, cutoff)
     np.testing.assert_allclose(got, (A @ q)[rows], rtol=0, atol=1e-12 * np.abs(A).max())
+
+
+@pytest.mark.parametrize("n,parts", [(300, 4), (1000, 4), (1001, 3), (2048, 4)])
+def test_gram_update_over_the_lower_block_triangle(n, parts):
+    """xnn_amd.eeq._add_gram (A += X X^T from the block rows' lower parts and mirrored upper
+    blocks) equals the full product for a symmetric A, sizes with and without a partial
+    last block and the small-size full product."""
+    from xnn_amd.eeq import _add_gram
+    g = torch.Generator().manual_seed(n)
+    M = torch.randn((n, n), dtype=torch.float64, generator=g)
+    A = M + M.T
+    X = torch.randn((n, 37), dtype=torch.float64, generator=g)
+    ref = A + X @ X.T
+    _add_gram(A, X, parts)
+    assert torch.allclose(A, ref, rtol=0, atol=1e-12 * float(ref.abs().max()))
+    assert torch.equal(A, A.T)

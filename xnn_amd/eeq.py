@@ -235,9 +235,17 @@ class LargeEEQSystem:
             self.m = reciprocal_half_set(self.cell, self.alpha, eps)
             g, w = reciprocal_weights(self.m, self.cell.to(torch.float64), self.alpha)
             phase = self.pos.to(torch.float64) @ g.t()
-            c, s = torch.cos(phase), torch.sin(phase)
-            A.addmm_(c * w, c.t()).addmm_(s * w, s.t())
-            del c, s, phase
+            # A_rec = C W C^T + S W S^T = X X^T with X = [C W^1/2, S W^1/2] (w_G > 0)
+            m = phase.shape[1]
+            X = torch.empty((phase.shape[0], 2 * m), dtype=torch.float64, device=phase.device)
+            sw = torch.sqrt(w)
+            torch.cos(phase, out=X[:, :m])
+            torch.sin(phase, out=X[:, m:])
+            del phase
+            X[:, :m].mul_(sw)
+            X[:, m:].mul_(sw)
+            _add_gram(A, X)
+            del X
         A.diagonal().add_(self.diag.to(torch.float64))
         self.A = A
         self.factor, info, self.inv_blocks = _cholesky(A, keep_inverses=True)
@@ -572,6 +580,27 @@ class IterativeEEQSystem:
 
 
 CHOLESKY_BLOCK = 128
+#: row blocks of :func:`_add_gram` (the lower block triangle: 5/8 of the square at 4)
+GRAM_PARTS = 4
+
+
+def _add_gram(A: Tensor, X: Tensor, parts: int = GRAM_PARTS) -> None:
+    """``A += X X^T`` for a symmetric ``A`` (N, N): each of ``parts`` block rows takes the
+    product up to its diagonal block (library GEMMs over the lower block triangle), then
+    the blocks above the diagonal are copied from their transposes below it."""
+    n = A.shape[0]
+    if n < 512 or parts <= 1:
+        A.addmm_(X, X.t())
+        return
+    step = -(-n // parts)
+    cuts = list(range(0, n, step)) + [n]
+    for i in range(len(cuts) - 1):
+        r0, r1 = cuts[i], cuts[i + 1]
+        A[r0:r1, :r1].addmm_(X[r0:r1], X[:r1].t())
+    for i in range(len(cuts) - 1):
+        for j in range(i + 1, len(cuts) - 1):
+            A[cuts[i]:cuts[i + 1], cuts[j]:cuts[j + 1]].copy_(
+                A[cuts[j]:cuts[j + 1], cuts[i]:cuts[i + 1]].t())
 
 
 def _cholesky(A: Tensor, keep_inverses: bool = False):
