@@ -122,21 +122,33 @@ __device__ inline void for_images(const EeqCell& C, double dx0, double dy0, doub
   for_images_frac(C, C.reach, f[0], f[1], f[2], cut2, fn);
 }
 
+// 16 x 16 tiles of the lower block triangle (the upper tiles return at once): each entry
+// summed over its images, a tile below the diagonal also stored transposed through LDS, so
+// the matrix is symmetric to the bit and half of its entries are summed.
 __global__ __launch_bounds__(256) void eeq_real_matrix_kernel(
     const double* __restrict__ pos, int64_t n, EeqCell C, const double* __restrict__ rad,
     double alpha, double cut2, double* __restrict__ R) {
-  const int64_t j = (int64_t)blockIdx.x * 16 + threadIdx.x % 16;
-  const int64_t i = (int64_t)blockIdx.y * 16 + threadIdx.x / 16;
-  if (i >= n || j >= n) return;
-  const double ai = rad[i], aj = rad[j];
-  const double gam = 1.0 / sqrt(ai * ai + aj * aj);
+  __shared__ double tile[16][17];
+  if (blockIdx.x > blockIdx.y) return;            // uniform: mirrored from below
+  const int tx = threadIdx.x % 16, ty = threadIdx.x / 16;
+  const int64_t j = (int64_t)blockIdx.x * 16 + tx;
+  const int64_t i = (int64_t)blockIdx.y * 16 + ty;
   double sum = 0.0;
-  for_images(C, pos[3 * j] - pos[3 * i], pos[3 * j + 1] - pos[3 * i + 1],
-             pos[3 * j + 2] - pos[3 * i + 2], cut2, i == j,
-             [&](double dx, double dy, double dz, int, int, int) {
-               sum += screened(sqrt(dx * dx + dy * dy + dz * dz), gam, alpha);
-             });
-  R[i * n + j] = sum;
+  if (i < n && j < n) {
+    const double ai = rad[i], aj = rad[j];
+    const double gam = 1.0 / sqrt(ai * ai + aj * aj);
+    for_images(C, pos[3 * j] - pos[3 * i], pos[3 * j + 1] - pos[3 * i + 1],
+               pos[3 * j + 2] - pos[3 * i + 2], cut2, i == j,
+               [&](double dx, double dy, double dz, int, int, int) {
+                 sum += screened(sqrt(dx * dx + dy * dy + dz * dz), gam, alpha);
+               });
+    R[i * n + j] = sum;
+  }
+  if (blockIdx.x == blockIdx.y) return;           // uniform: a diagonal tile is whole
+  tile[ty][tx] = sum;
+  __syncthreads();
+  const int64_t it = (int64_t)blockIdx.x * 16 + ty, jt = (int64_t)blockIdx.y * 16 + tx;
+  if (it < n && jt < n) R[it * n + jt] = tile[tx][ty];
 }
 
 __global__ __launch_bounds__(256) void eeq_real_grad_kernel(
