@@ -138,12 +138,14 @@ def _host_cell(cell: Optional[Tensor]):
 
 
 def real_matrix(pos: Tensor, cell: Optional[Tensor], rad: Tensor, alpha: float,
-                cutoff_au: float) -> Tensor:
-    """The dense real-space matrix R (N, N) of the screened kernel (no autograd)."""
+                cutoff_au: float, host_cell=None) -> Tensor:
+    """The dense real-space matrix R (N, N) of the screened kernel (no autograd);
+    ``host_cell``: the cell as :func:`_host_cell` returns it, when the caller has it."""
     n = pos.shape[0]
     out = torch.empty((n, n), dtype=torch.float64, device=pos.device)
     p = pos.detach().to(torch.float64).contiguous()
-    _lib.call("xnn_eeq_real_matrix", _lib.ptr(p), n, _host_cell(cell),
+    _lib.call("xnn_eeq_real_matrix", _lib.ptr(p), n,
+              host_cell if host_cell is not None else _host_cell(cell),
               _lib.ptr(rad.detach().to(torch.float64).contiguous()), float(alpha),
               float(cutoff_au), _lib.ptr(out), _lib.stream(pos.device))
     return out
@@ -228,12 +230,21 @@ class LargeEEQSystem:
         self.pos, self.cell = pos.detach(), None if cell is None else cell.detach()
         self.rad, self.alpha, self.cutoff = rad.detach(), float(alpha), float(cutoff_au)
         self.diag = diag.detach()
-        self.R = real_matrix(self.pos, self.cell, self.rad, self.alpha, self.cutoff)
+        # one read of the cell to the host; the real-space kernel runs while the host forms
+        # the reciprocal vectors and weights, which go up by asynchronous copies (no drain
+        # of the queue between the two parts)
+        cell_h = None if self.cell is None else self.cell.to(torch.float64).cpu()
+        host = None if cell_h is None else _host_cell(cell_h)
+        self.R = real_matrix(self.pos, self.cell, self.rad, self.alpha, self.cutoff, host)
         A = self.R.clone()
         self.m = None
         if self.cell is not None:
-            self.m = reciprocal_half_set(self.cell, self.alpha, eps)
-            g, w = reciprocal_weights(self.m, self.cell.to(torch.float64), self.alpha)
+            dev = self.pos.device
+            m_h = reciprocal_half_set(cell_h, self.alpha, eps)
+            g_h, w_h = reciprocal_weights(m_h, cell_h, self.alpha)
+            up = (lambda t: t.pin_memory().to(dev, non_blocking=True)) if dev.type == "cuda" \
+                else (lambda t: t)
+            self.m, g, w = up(m_h), up(g_h), up(w_h)
             phase = self.pos.to(torch.float64) @ g.t()
             # A_rec = C W C^T + S W S^T = X X^T with X = [C W^1/2, S W^1/2] (w_G > 0)
             m = phase.shape[1]
