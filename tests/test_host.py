@@ -61,6 +61,24 @@ def test_argument_errors_come_back_as_status_codes(lib_path):
     cell = (ctypes.c_double * 9)(20, 0, 0, 0, 20, 0, 0, 0, 20)
     assert lib.xnn_radius_graph_plan(10, cell, pbc, 5.0, None, None, ctypes.byref(plan)) == 0
     assert list(plan.nbins) == [3, 3, 3] and list(plan.reach) == [1, 1, 1]
+    # the factor solve takes one or two right-hand sides and a work array
+    assert lib.xnn_eeq_cholesky_solve(None, 10, None, None, 3, None, None) == _lib.XNN_EINVAL
+    assert b"right-hand sides" in lib.xnn_last_error()
+    assert lib.xnn_eeq_cholesky_solve(None, 10, None, None, 2, None, None) == _lib.XNN_EINVAL
+    assert lib.xnn_eeq_cholesky_solve(None, 0, None, None, 1, None, None) == 0
+    # the ATM tangents check their workspace size before anything runs
+    size = ctypes.c_size_t()
+    assert lib.xnn_atm_tangent_work_size(100, 10, 23, ctypes.byref(size)) == 0
+    base = ctypes.c_size_t()
+    assert lib.xnn_atm_work_size(100, 10, 23, 1, ctypes.byref(base)) == 0
+    assert size.value > base.value
+    assert lib.xnn_atm_tangent_work_size(100, 10, 33, ctypes.byref(size)) == _lib.XNN_EINVAL
+    prm = _lib.AtmParams(1.0, 16.0 / 3.0, 10.0, 0.0)
+    buf = (ctypes.c_double * 8)()
+    code = lib.xnn_atm_energy_backward_tangent(
+        buf, 100, 10, 1, 0, buf, buf, buf, 23, buf, buf, 1, ctypes.byref(prm), buf, buf, buf,
+        buf, buf, buf, buf, buf, buf, base.value, None)
+    assert code == _lib.XNN_EINVAL and b"workspace too small" in lib.xnn_last_error()
 
 
 def test_ops_refuse_cpu_tensors():
