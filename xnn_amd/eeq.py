@@ -591,8 +591,8 @@ class IterativeEEQSystem:
 
 
 CHOLESKY_BLOCK = 128
-#: row blocks of :func:`_add_gram` (the lower block triangle: 5/8 of the square at 4)
-GRAM_PARTS = 4
+#: row blocks of :func:`_add_gram` (the lower block triangle: 9/16 of the square at 8)
+GRAM_PARTS = 8
 
 
 def _add_gram(A: Tensor, X: Tensor, parts: int = GRAM_PARTS) -> None:
